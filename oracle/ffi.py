@@ -1,0 +1,201 @@
+"""ctypes binding of the CPU oracle (oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, as the checker or the timed CPU baseline. The product (spindle_amd/)
+never imports it.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "liboracle.so")
+
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4K, Q5K, Q6K, BF16 = 0, 1, 2, 3, 6, 7, 8, 12, 13, 14, 30
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22),
+         Q5_1: (32, 24), Q8_0: (32, 34), Q4K: (256, 144), Q5K: (256, 176), Q6K: (256, 210)}
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        build()
+    return C.CDLL(LIB_PATH)
+
+
+lib = _load()
+P = C.c_void_p
+fp = C.POINTER(C.c_float)
+
+
+class Mat(C.Structure):
+    _fields_ = [("dtype", C.c_int), ("cols", C.c_size_t), ("rows", C.c_size_t), ("data", P)]
+
+
+class Config(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("dim", "n_heads", "n_kv_heads", "head_dim", "n_layers", "vocab", "max_seq")] + \
+        [("rope_theta", C.c_float), ("rms_eps", C.c_float), ("rope_neox", C.c_int),
+         ("n_expert", C.c_int), ("n_expert_used", C.c_int), ("expert_norm", C.c_int), ("moe_prune", C.c_float),
+         ("embedding_scale", C.c_float), ("residual_scale", C.c_float), ("logit_scale", C.c_float),
+         ("attn_scale", C.c_float)]
+
+
+class Layer(C.Structure):
+    _fields_ = [("attn_norm", P), ("ffn_norm", P), ("wq", Mat), ("wk", Mat), ("wv", Mat), ("wo", Mat),
+                ("q_bias", P), ("k_bias", P), ("v_bias", P), ("q_norm", P), ("k_norm", P),
+                ("qk_norm_full", C.c_int), ("is_moe", C.c_int),
+                ("gate", Mat), ("up", Mat), ("down", Mat), ("router", Mat)]
+
+
+class Model(C.Structure):
+    _fields_ = [("c", Config), ("layers", C.POINTER(Layer)), ("embed", Mat), ("lm_head", Mat),
+                ("output_norm", P), ("k_cache", P), ("v_cache", P), ("inv_freq", P),
+                ("last_chosen", C.c_int * (16 * 32))]
+
+
+class SpecModel(C.Structure):
+    _fields_ = [("acc", C.c_double * 4), ("fail", C.c_double * 4), ("t1_us", C.c_double), ("extra_us", C.c_double),
+                ("have_t1", C.c_int), ("have_extra", C.c_int), ("since_try", C.c_int), ("fixed", C.c_int)]
+
+
+class GenParams(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("draft_len", "min_ngram", "max_ngram", "fixed", "speculate", "adaptive_k", "prefill_chunk")]
+
+
+class GenStats(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("accepted", "drafted", "verifies", "steps")]
+
+
+def _sig(name, res, *args):
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+    return f
+
+
+_sig("or_row_bytes", C.c_size_t, C.c_int, C.c_size_t)
+_sig("or_f16_to_f32", C.c_float, C.c_uint16)
+_sig("or_f32_to_f16", C.c_uint16, C.c_float)
+_sig("or_unpack_q4k_scales", None, P, P, P)
+_sig("or_dequant_row", C.c_int, C.c_int, P, C.c_size_t, P)
+_sig("or_q8k_quantize", None, P, C.c_size_t, P, P, P)
+_sig("or_q8k_matmul_rows", None, P, C.c_int, C.c_size_t, C.c_int, P, P, P, P, C.c_size_t, C.c_size_t)
+_sig("or_q8k_block_sums", None, P, C.c_int, C.c_size_t, P, P, P, P, P)
+_sig("or_matvec_rows", C.c_int, P, C.c_int, C.c_size_t, P, P, C.c_size_t, C.c_size_t)
+_sig("or_matmul_rows_multi", C.c_int, P, C.c_int, C.c_size_t, C.c_int, P, P, C.c_size_t, C.c_size_t)
+_sig("or_matvec", C.c_int, C.POINTER(Mat), P, P)
+_sig("or_matvec_multi", C.c_int, C.POINTER(Mat), C.c_int, P, P)
+_sig("or_rmsnorm", None, P, P, P, C.c_size_t, C.c_float)
+_sig("or_rmsnorm_heads", None, P, P, C.c_size_t, C.c_size_t, C.c_float)
+_sig("or_silu", C.c_float, C.c_float)
+_sig("or_rope_inv_freq", None, C.c_size_t, C.c_float, P)
+_sig("or_rope_rotate", None, P, C.c_int, P, C.c_size_t, C.c_size_t, C.c_float)
+_sig("or_model_init", None, C.POINTER(Model))
+_sig("or_forward_slice", C.c_int, C.POINTER(Model), C.c_int, C.c_int, P)
+_sig("or_forward_batch", C.c_int, C.POINTER(Model), P, C.c_int, C.c_int, P)
+_sig("or_logits", C.c_int, C.POINTER(Model), P, C.c_int, P)
+_sig("or_argmax", C.c_int, P, C.c_int, C.c_float)
+_sig("or_moe_forward", C.c_int, C.POINTER(Config), C.POINTER(Layer), C.c_int, P, P, P, P)
+_sig("or_ffns_fused", C.c_int, C.POINTER(Mat), C.POINTER(Mat), C.POINTER(Mat), C.c_int, P, P, P, P)
+_sig("or_lookup_draft", C.c_int, P, C.c_int, C.c_int, P, C.c_int, C.c_int, C.c_int, P, P)
+_sig("or_spec_init", None, C.POINTER(SpecModel), C.c_int)
+_sig("or_spec_class", C.c_int, C.c_int)
+_sig("or_spec_accept_rate", C.c_double, C.POINTER(SpecModel), C.c_int)
+_sig("or_spec_best_len", C.c_int, C.POINTER(SpecModel), C.c_int, C.c_int)
+_sig("or_spec_reset_rates", None, C.POINTER(SpecModel))
+_sig("or_spec_record_draft", None, C.POINTER(SpecModel), C.c_int, C.c_int, C.c_int)
+_sig("or_spec_record_step", None, C.POINTER(SpecModel), C.c_uint64)
+_sig("or_spec_record_verify", None, C.POINTER(SpecModel), C.c_int, C.c_uint64)
+_sig("or_generate", C.c_int, C.POINTER(Model), P, C.c_int, C.c_int, C.POINTER(GenParams), P, C.POINTER(GenStats))
+_sig("or_set_threads", None, C.c_int)
+_sig("or_get_threads", C.c_int)
+
+
+def ptr(a):
+    return a.ctypes.data_as(P) if a is not None else None
+
+
+def row_bytes(dtype, cols):
+    return lib.or_row_bytes(dtype, cols)
+
+
+def dequant_row(dtype, row, cols):
+    out = np.empty(cols, np.float32)
+    assert lib.or_dequant_row(dtype, ptr(row), cols, ptr(out)) == 0
+    return out
+
+
+def dequant(dtype, data, rows, cols):
+    rb = row_bytes(dtype, cols)
+    return np.stack([dequant_row(dtype, data[r * rb:(r + 1) * rb], cols) for r in range(rows)])
+
+
+def q8k_quantize(x):
+    x = np.ascontiguousarray(x, np.float32)
+    n = x.size
+    d = np.empty(n // 256, np.float32)
+    qs = np.empty(n, np.int8)
+    bs = np.empty(n // 16, np.int16)
+    lib.or_q8k_quantize(ptr(x), n, ptr(d), ptr(qs), ptr(bs))
+    return d, qs, bs
+
+
+def _parr(arrs):
+    return (P * len(arrs))(*[a.ctypes.data for a in arrs])
+
+
+def q8k_matmul_rows(data, dtype, cols, qs_list, rows, r0=0, r1=None, outs=None):
+    r1 = rows if r1 is None else r1
+    if outs is None:
+        outs = [np.full(rows, np.nan, np.float32) for _ in qs_list]
+    lib.or_q8k_matmul_rows(ptr(data), dtype, cols, len(qs_list), _parr([q[0] for q in qs_list]),
+                           _parr([q[1] for q in qs_list]), _parr([q[2] for q in qs_list]), _parr(outs), r0, r1)
+    return outs
+
+
+def q8k_block_sums(row, dtype, cols, q):
+    nb = cols // 256
+    s = np.empty(nb, np.int32)
+    c = np.empty(nb, np.int32)
+    lanes = np.empty(nb * 8, np.int32)
+    lib.or_q8k_block_sums(ptr(row), dtype, cols, ptr(q[1]), ptr(q[2]), ptr(s), ptr(c), ptr(lanes))
+    return s, c, lanes.reshape(nb, 8)
+
+
+def matvec_rows(data, dtype, cols, x, r0, nrows):
+    out = np.empty(nrows, np.float32)
+    assert lib.or_matvec_rows(ptr(data), dtype, cols, ptr(x), ptr(out), r0, nrows) == 0
+    return out
+
+
+def matmul_rows_multi(data, dtype, cols, xs, rows, r0=0, r1=None, outs=None):
+    r1 = rows if r1 is None else r1
+    if outs is None:
+        outs = [np.full(rows, np.nan, np.float32) for _ in xs]
+    assert lib.or_matmul_rows_multi(ptr(data), dtype, cols, len(xs), _parr(xs), _parr(outs), r0, r1) == 0
+    return outs
+
+
+def mat(dtype, data, rows, cols):
+    return Mat(dtype, cols, rows, data.ctypes.data)
+
+
+def matvec(m, x):
+    out = np.empty(m.rows, np.float32)
+    assert lib.or_matvec(C.byref(m), ptr(x), ptr(out)) == 0
+    return out
+
+
+def matvec_multi(m, xs):
+    outs = [np.empty(m.rows, np.float32) for _ in xs]
+    assert lib.or_matvec_multi(C.byref(m), len(xs), _parr(xs), _parr(outs)) == 0
+    return outs
+
+
+def set_threads(n):
+    lib.or_set_threads(n)

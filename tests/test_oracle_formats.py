@@ -1,0 +1,107 @@
+"""Pins the oracle's formats: f16 conversions, the 6-bit scale unpack, dequantization and
+Q8_K quantization. Reference: quant.rs:876-899, 1504-1660; q4k_gemv.rs:70-85;
+quant_q8k.rs:84-121 (and its property test :342-362)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import ffi
+from tests import refdata as R
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def test_f16_to_f32_exhaustive():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([ffi.lib.or_f16_to_f32(int(v)) for v in h], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_round_to_nearest_even():
+    rng = np.random.default_rng(5)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32),
+        (rng.standard_normal(20000) * 1e-5).astype(np.float32),   # subnormal halfs
+        (rng.standard_normal(5000) * 3e4).astype(np.float32),     # near overflow
+        np.array([0.0, -0.0, 65504.0, 65520.0, 65519.996, 2 ** -25, 2 ** -24, 3 * 2 ** -26, np.inf, -np.inf], np.float32),
+    ])
+    # midpoints between adjacent halfs round to even
+    hs = np.arange(0, 0x7BFF, 7, dtype=np.uint16)
+    a = hs.view(np.float16).astype(np.float64)
+    b = (hs + 1).view(np.float16).astype(np.float64)
+    vals = np.concatenate([vals, ((a + b) / 2).astype(np.float32)])
+    want = vals.astype(np.float16).view(np.uint16)
+    got = np.array([ffi.lib.or_f32_to_f16(float(v)) for v in vals], np.uint16)
+    assert np.array_equal(got, want)
+
+
+def _q4k_block(d, dmin, scales, rule):
+    qs = [eval(rule, {"i": i}) for i in range(128)]
+    return np.frombuffer(int(d).to_bytes(2, "little") + int(dmin).to_bytes(2, "little") + bytes(scales) + bytes(qs), np.uint8).copy()
+
+
+@pytest.mark.parametrize("case", range(2))
+def test_q4k_known_answer_block(case):
+    g = json.load(open(os.path.join(GOLD, "known_blocks.json")))["q4k"][case]
+    blk = _q4k_block(g["d"], g["dmin"], g["scales"], g["qs_rule"])
+    s = np.empty(8, np.uint8)
+    m = np.empty(8, np.uint8)
+    ffi.lib.or_unpack_q4k_scales(ffi.ptr(blk[4:16].copy()), ffi.ptr(s), ffi.ptr(m))
+    assert s.tolist() == g["sc"] and m.tolist() == g["mn"]
+    y = ffi.dequant_row(ffi.Q4K, blk, 256)
+    for e, v in g["elements"].items():
+        assert y[int(e)] == np.float32(v), (e, y[int(e)], v)
+
+
+def test_q6k_known_answer_block():
+    g = json.load(open(os.path.join(GOLD, "known_blocks.json")))["q6k"]
+    ql = bytes((i * 37 + 11) & 255 for i in range(128))
+    qh = bytes((i * 53 + 7) & 255 for i in range(64))
+    sc = bytes((i * 9 - 70) & 255 for i in range(16))
+    blk = np.frombuffer(ql + qh + sc + int(g["d"]).to_bytes(2, "little"), np.uint8).copy()
+    y = ffi.dequant_row(ffi.Q6K, blk, 256)
+    for e, v in g["elements"].items():
+        assert y[int(e)] == np.float32(v), (e, y[int(e)], v)
+
+
+def test_q5_0_and_q8_0_known_answer():
+    g = json.load(open(os.path.join(GOLD, "known_blocks.json")))["q5_0"]
+    blk = np.frombuffer(int(g["d"]).to_bytes(2, "little") + int(g["qh"]).to_bytes(4, "little") +
+                        bytes((j * 17) & 255 for j in range(16)), np.uint8).copy()
+    y = ffi.dequant_row(ffi.Q5_0, blk, 32)
+    for e, v in g["elements"].items():
+        assert y[int(e)] == np.float32(v)
+    codes = np.arange(-128, 128, 8, dtype=np.int8)
+    blk = np.frombuffer((0x3800).to_bytes(2, "little") + codes.tobytes(), np.uint8).copy()
+    assert np.array_equal(ffi.dequant_row(ffi.Q8_0, blk, 32), codes.astype(np.float32) * 0.5)
+
+
+def test_q8k_quantize_reference_property():
+    """quant_q8k.rs:342-362 (same seed), plus the closed form d = amax/127, q = rint(x*127/amax)."""
+    rng = R.Rng(11)
+    x = rng.floats(768, -3.0, 3.0)
+    d, qs, bs = ffi.q8k_quantize(x)
+    for b in range(3):
+        chunk = x[b * 256:(b + 1) * 256]
+        amax = np.float32(np.abs(chunk).max())
+        back = d[b] * qs[b * 256:(b + 1) * 256].astype(np.float32)
+        assert np.all(np.abs(back - chunk) <= amax / np.float32(127.0) * np.float32(0.5) + np.float32(1e-6))
+        assert d[b] == amax / np.float32(127.0)
+        iscale = np.float32(127.0) / amax
+        assert np.array_equal(qs[b * 256:(b + 1) * 256], np.rint(chunk * iscale).astype(np.int8))
+    assert np.array_equal(bs.astype(np.int32), qs.astype(np.int32).reshape(-1, 16).sum(1))
+    d, qs, bs = ffi.q8k_quantize(np.zeros(256, np.float32))
+    assert d[0] == 0 and not qs.any() and not bs.any()
+
+
+def test_q8k_quantize_nonfinite_block_is_zero():
+    x = np.ones(512, np.float32)
+    x[300] = np.inf
+    d, qs, bs = ffi.q8k_quantize(x)
+    assert d[1] == 0 and not qs[256:].any() and not bs[16:].any()
+    assert d[0] == np.float32(1.0) / np.float32(127.0) and np.all(qs[:256] == 127)

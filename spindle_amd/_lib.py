@@ -1,0 +1,62 @@
+"""ctypes binding of libspx.so (include/spx.h)."""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libspx.so")
+
+
+class SpxError(RuntimeError):
+    pass
+
+
+P = C.c_void_p
+I64 = C.c_int64
+_lib = None
+
+SIGNATURES = {
+    "spx_last_error": (C.c_char_p, []),
+    "spx_create": (C.c_int, [C.c_int, C.POINTER(P)]),
+    "spx_destroy": (C.c_int, [P]),
+    "spx_sync": (C.c_int, [P]),
+    "spx_get_stream": (P, [P]),
+    "spx_row_bytes": (I64, [C.c_int, I64]),
+    "spx_tensor_upload": (C.c_int, [P, C.c_int, I64, I64, C.c_int, P, C.POINTER(P)]),
+    "spx_tensor_download": (C.c_int, [P, P, P]),
+    "spx_tensor_free": (C.c_int, [P, P]),
+    "spx_q8k_quantize": (C.c_int, [P, P, I64, I64, C.c_int, P, P, P]),
+    "spx_matmul_rows_q8k": (C.c_int, [P, P, C.c_int, P, P, P, C.c_int, P, I64, I64, I64]),
+    "spx_block_sums_q8k": (C.c_int, [P, P, C.c_int, I64, P, P, P]),
+    "spx_matvec": (C.c_int, [P, P, C.c_int, P, I64, C.c_int, P, I64]),
+}
+
+
+def load():
+    """Loads libspx.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise SpxError(f"{LIB_PATH} is missing: run `python -m spindle_amd.build` (or __graft_entry__.build())")
+    lib_ = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        f = getattr(lib_, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = lib_
+    return _lib
+
+
+class _Lazy:
+    def __getattr__(self, name):
+        return getattr(load(), name)
+
+
+lib = _Lazy()
+
+
+def check(rc):
+    if rc != 0:
+        msg = load().spx_last_error()
+        raise SpxError(msg.decode() if msg else f"spx error {rc}")
+    return rc

@@ -1,0 +1,274 @@
+// C ABI: context, weight tensors (planar re-layout), Q8_K quantization and matvec entry points.
+#include <string.h>
+
+#include <algorithm>
+#include <functional>
+#include <thread>
+
+#include "../../include/spx.h"
+#include "internal.h"
+
+namespace spx {
+
+static thread_local std::string g_err;
+
+void set_error(const std::string &msg) { g_err = msg; }
+int fail(const std::string &msg) { g_err = msg; return -1; }
+int hip_fail(hipError_t e, const char *what) {
+  g_err = std::string(what) + ": " + hipGetErrorString(e);
+  return -2;
+}
+
+int64_t block_elems(int dtype) {
+  switch (dtype) {
+  case T_F32: case T_F16: return 1;
+  case T_Q5_0: case T_Q8_0: return 32;
+  case T_Q4K: case T_Q6K: return 256;
+  default: return 0;
+  }
+}
+
+int64_t row_bytes(int dtype, int64_t cols) {
+  int64_t be = block_elems(dtype), bb;
+  switch (dtype) {
+  case T_F32: bb = 4; break;
+  case T_F16: bb = 2; break;
+  case T_Q5_0: bb = 22; break;
+  case T_Q8_0: bb = 34; break;
+  case T_Q4K: bb = 144; break;
+  case T_Q6K: bb = 210; break;
+  default: return 0;
+  }
+  if (cols <= 0 || cols % be) return 0;
+  return cols / be * bb;
+}
+
+void *ws_get(spx_ctx *ctx, size_t bytes) {
+  if (bytes <= ctx->ws_bytes) return ctx->ws;
+  if (ctx->ws) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(ctx->ws); }
+  ctx->ws = nullptr;
+  ctx->ws_bytes = 0;
+  size_t want = std::max(bytes, (size_t)1 << 20);
+  if (hipMalloc(&ctx->ws, want) != hipSuccess) return nullptr;
+  ctx->ws_bytes = want;
+  return ctx->ws;
+}
+
+// Field records of one GGUF block: (offset in block, length, plane).
+struct Field { int off, len, plane; };
+static int fields_of(int dtype, Field *f) {
+  switch (dtype) {
+  case T_Q4K: f[0] = {16, 128, 0}; f[1] = {0, 16, 1}; return 2;
+  case T_Q6K: f[0] = {0, 128, 0}; f[1] = {128, 64, 1}; f[2] = {192, 16, 2}; f[3] = {208, 2, 3}; return 4;
+  case T_Q8_0: f[0] = {2, 32, 0}; f[1] = {0, 2, 3}; return 2;
+  case T_Q5_0: f[0] = {6, 16, 0}; f[1] = {2, 4, 1}; f[2] = {0, 2, 3}; return 3;
+  default: return 0;
+  }
+}
+static int block_bytes(int dtype) {
+  switch (dtype) { case T_Q4K: return 144; case T_Q6K: return 210; case T_Q8_0: return 34; case T_Q5_0: return 22; default: return 0; }
+}
+
+// GGUF <-> planar, over block range [g0, g1).
+static void relayout(int dtype, const uint8_t *ggml, uint8_t *planar, const size_t *poff, int64_t g0, int64_t g1, bool to_planar) {
+  Field f[4];
+  const int nf = fields_of(dtype, f), bb = block_bytes(dtype);
+  for (int64_t g = g0; g < g1; g++)
+    for (int k = 0; k < nf; k++) {
+      uint8_t *p = planar + poff[f[k].plane] + (size_t)g * f[k].len;
+      const uint8_t *q = ggml + (size_t)g * bb + f[k].off;
+      if (to_planar) memcpy(p, q, f[k].len); else memcpy(const_cast<uint8_t *>(q), p, f[k].len);
+    }
+}
+
+static void parallel_blocks(int64_t nblk, const std::function<void(int64_t, int64_t)> &fn) {
+  const int64_t min_per = 1 << 16;
+  int nt = (int)std::min<int64_t>(std::max(1u, std::thread::hardware_concurrency()), std::max<int64_t>(1, nblk / min_per));
+  nt = std::min(nt, 16);
+  if (nt <= 1) { fn(0, nblk); return; }
+  std::vector<std::thread> th;
+  for (int t = 0; t < nt; t++) th.emplace_back([&, t] { fn(nblk * t / nt, nblk * (t + 1) / nt); });
+  for (auto &x : th) x.join();
+}
+
+}  // namespace spx
+
+using namespace spx;
+
+extern "C" {
+
+const char *spx_last_error(void) { return g_err.c_str(); }
+
+int spx_create(int device, spx_ctx **out) {
+  if (!out) return fail("spx_create: out is null");
+  int n = 0;
+  SPX_HIP(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail("spx_create: no such device");
+  SPX_HIP(hipSetDevice(device));
+  spx_ctx *c = new spx_ctx();
+  c->device = device;
+  hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) { delete c; return hip_fail(e, "hipStreamCreate"); }
+  *out = c;
+  return 0;
+}
+
+int spx_destroy(spx_ctx *ctx) {
+  if (!ctx) return 0;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return 0;
+}
+
+int spx_sync(spx_ctx *ctx) {
+  if (!ctx) return fail("spx_sync: null context");
+  SPX_HIP(hipStreamSynchronize(ctx->stream));
+  return 0;
+}
+
+void *spx_get_stream(spx_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int64_t spx_row_bytes(int dtype, int64_t cols) { return row_bytes(dtype, cols); }
+
+int spx_tensor_upload(spx_ctx *ctx, int dtype, int64_t cols, int64_t rows, int n_expert, const void *ggml, spx_tensor **out) {
+  if (!ctx || !out || !ggml) return fail("spx_tensor_upload: null argument");
+  const int64_t rb = row_bytes(dtype, cols);
+  if (!rb || rows <= 0 || n_expert <= 0) return fail("spx_tensor_upload: unsupported dtype or shape (dtype " + std::to_string(dtype) + ", cols " + std::to_string(cols) + ")");
+  SPX_HIP(hipSetDevice(ctx->device));
+  spx_tensor *t = new spx_tensor();
+  t->v.dtype = dtype;
+  t->v.cols = cols;
+  t->v.rows = rows;
+  t->v.n_expert = n_expert;
+  t->v.nb = cols / block_elems(dtype);
+  const int64_t total_rows = rows * n_expert, nblk = total_rows * t->v.nb;
+  std::vector<uint8_t> img;
+  size_t bytes = 0;
+  if (dtype == T_F32 || dtype == T_F16) {
+    bytes = (size_t)rb * total_rows;
+    t->plane_off[0] = 0;
+  } else {
+    Field f[4];
+    const int nf = fields_of(dtype, f);
+    for (int k = 0; k < nf; k++) {
+      t->plane_off[f[k].plane] = bytes;
+      bytes += ((size_t)nblk * f[k].len + 255) & ~(size_t)255;
+    }
+  }
+  hipError_t e = hipMalloc(&t->dev, std::max<size_t>(bytes, 256));
+  if (e != hipSuccess) { delete t; return hip_fail(e, "hipMalloc(tensor)"); }
+  t->bytes = bytes;
+  const uint8_t *src = static_cast<const uint8_t *>(ggml);
+  if (dtype == T_F32 || dtype == T_F16) {
+    e = hipMemcpy(t->dev, src, bytes, hipMemcpyHostToDevice);
+  } else {
+    img.resize(bytes);
+    parallel_blocks(nblk, [&](int64_t a, int64_t b) { relayout(dtype, src, img.data(), t->plane_off, a, b, true); });
+    e = hipMemcpy(t->dev, img.data(), bytes, hipMemcpyHostToDevice);
+  }
+  if (e != hipSuccess) { (void)hipFree(t->dev); delete t; return hip_fail(e, "hipMemcpy(tensor)"); }
+  uint8_t *base = static_cast<uint8_t *>(t->dev);
+  t->v.pl.p0 = base + t->plane_off[0];
+  t->v.pl.p1 = base + t->plane_off[1];
+  t->v.pl.p2 = base + t->plane_off[2];
+  t->v.pl.p3 = base + t->plane_off[3];
+  *out = t;
+  return 0;
+}
+
+int spx_tensor_download(spx_ctx *ctx, const spx_tensor *t, void *ggml) {
+  if (!ctx || !t || !ggml) return fail("spx_tensor_download: null argument");
+  SPX_HIP(hipSetDevice(ctx->device));
+  SPX_HIP(hipStreamSynchronize(ctx->stream));
+  const int dtype = t->v.dtype;
+  const int64_t nblk = t->v.rows * t->v.n_expert * t->v.nb;
+  if (dtype == T_F32 || dtype == T_F16) {
+    SPX_HIP(hipMemcpy(ggml, t->dev, t->bytes, hipMemcpyDeviceToHost));
+    return 0;
+  }
+  std::vector<uint8_t> img(t->bytes);
+  SPX_HIP(hipMemcpy(img.data(), t->dev, t->bytes, hipMemcpyDeviceToHost));
+  parallel_blocks(nblk, [&](int64_t a, int64_t b) { relayout(dtype, static_cast<uint8_t *>(ggml), img.data(), t->plane_off, a, b, false); });
+  return 0;
+}
+
+int spx_tensor_free(spx_ctx *ctx, spx_tensor *t) {
+  if (!t) return 0;
+  if (ctx) { (void)hipSetDevice(ctx->device); (void)hipStreamSynchronize(ctx->stream); }
+  if (t->dev) (void)hipFree(t->dev);
+  delete t;
+  return 0;
+}
+
+int spx_q8k_quantize(spx_ctx *ctx, const float *x, int64_t n, int64_t ld_x, int m, float *d, int8_t *qs, int16_t *bsums) {
+  if (!ctx || !x || !d || !qs || !bsums) return fail("spx_q8k_quantize: null argument");
+  if (n <= 0 || n % 256 || m <= 0 || ld_x < n || ld_x % 4) return fail("spx_q8k_quantize: n must be a positive multiple of 256, ld_x >= n and a multiple of 4");
+  SPX_HIP(launch_q8k_quantize(x, n, ld_x, m, d, qs, bsums, ctx->stream));
+  return 0;
+}
+
+static int check_kq(const spx_tensor *w, int expert, int m) {
+  if (!w) return fail("null tensor");
+  if (w->v.dtype != T_Q4K && w->v.dtype != T_Q6K) return fail("integer kernel needs a Q4_K or Q6_K tensor");
+  if (expert < 0 || expert >= w->v.n_expert) return fail("expert index out of range");
+  if (m < 1 || m > 16) return fail("m must be in 1..16");
+  return 0;
+}
+
+int spx_matmul_rows_q8k(spx_ctx *ctx, const spx_tensor *w, int expert, const float *xd, const int8_t *xs, const int16_t *xb, int m, float *out, int64_t ld_out, int64_t r0, int64_t r1) {
+  if (!ctx || !xd || !xs || !xb || !out) return fail("spx_matmul_rows_q8k: null argument");
+  if (int r = check_kq(w, expert, m)) return r;
+  if (r0 < 0 || r1 > w->v.rows || r0 > r1) return fail("spx_matmul_rows_q8k: bad row range");
+  if (m > 1 && ld_out < r1) return fail("spx_matmul_rows_q8k: ld_out smaller than the row range");
+  if (r1 == r0) return 0;
+  KQArgs a{};
+  a.w = w->v; a.xd = xd; a.xq = xs; a.xb = xb; a.out = out; a.ld_out = ld_out; a.r0 = r0; a.r1 = r1;
+  a.expert = expert; a.m = m;
+  SPX_HIP(launch_gemv_kq(a, m, false, 1, ctx->stream));
+  return 0;
+}
+
+int spx_block_sums_q8k(spx_ctx *ctx, const spx_tensor *w, int expert, int64_t row, const int8_t *xs, const int16_t *xb, int32_t *sums) {
+  if (!ctx || !xs || !xb || !sums) return fail("spx_block_sums_q8k: null argument");
+  if (int r = check_kq(w, expert, 1)) return r;
+  if (row < 0 || row >= w->v.rows) return fail("spx_block_sums_q8k: row out of range");
+  KQArgs a{};
+  a.w = w->v; a.xq = xs; a.xb = xb; a.r0 = row; a.r1 = row + 1; a.expert = expert; a.m = 1; a.dbg = sums;
+  SPX_HIP(launch_kq_block_sums(a, ctx->stream));
+  return 0;
+}
+
+int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, int64_t ld_x, int m, float *out, int64_t ld_out) {
+  if (!ctx || !w || !x || !out) return fail("spx_matvec: null argument");
+  if (m < 1 || m > 16) return fail("spx_matvec: m must be in 1..16");
+  if (expert < 0 || expert >= w->v.n_expert) return fail("spx_matvec: expert index out of range");
+  const int64_t cols = w->v.cols, rows = w->v.rows;
+  if (ld_x < cols || (m > 1 && ld_out < rows)) return fail("spx_matvec: leading dimension too small");
+  if (ld_x % 4) return fail("spx_matvec: ld_x must be a multiple of 4 (16-byte rows)");
+  if (w->v.dtype == T_Q4K || w->v.dtype == T_Q6K) {
+    const int64_t nb = w->v.nb;
+    const size_t need = (size_t)m * (cols + nb * 4 + nb * 32) + 256;
+    uint8_t *wsp = static_cast<uint8_t *>(ws_get(ctx, need));
+    if (!wsp) return fail("spx_matvec: workspace allocation failed");
+    int8_t *qs = reinterpret_cast<int8_t *>(wsp);
+    float *d = reinterpret_cast<float *>(wsp + (((size_t)m * cols + 15) & ~(size_t)15));
+    int16_t *bs = reinterpret_cast<int16_t *>(reinterpret_cast<uint8_t *>(d) + (((size_t)m * nb * 4 + 15) & ~(size_t)15));
+    SPX_HIP(launch_q8k_quantize(x, cols, ld_x, m, d, qs, bs, ctx->stream));
+    KQArgs a{};
+    a.w = w->v; a.xd = d; a.xq = qs; a.xb = bs; a.out = out; a.ld_out = ld_out; a.r0 = 0; a.r1 = rows;
+    a.expert = expert; a.m = m;
+    SPX_HIP(launch_gemv_kq(a, m, false, 1, ctx->stream));
+    return 0;
+  }
+  if (w->v.dtype == T_F32 && cols % 16) return fail("spx_matvec: F32 needs cols % 16 == 0");
+  if (w->v.dtype != T_Q8_0 && w->v.dtype != T_Q5_0 && w->v.dtype != T_F32) return fail("spx_matvec: unsupported dtype " + std::to_string(w->v.dtype));
+  FArgs a{};
+  a.w = w->v; a.x = x; a.ld_x = ld_x; a.out = out; a.ld_out = ld_out; a.r0 = 0; a.r1 = rows; a.expert = expert; a.m = m;
+  SPX_HIP(launch_gemv_f(a, m, false, 1, ctx->stream));
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,125 @@
+"""Operator-level mirror of the reference's kernel interface over the C ABI.
+
+Names follow the reference: `matvec` / `matvec_multi` (smollm_chat.rs:309, 447),
+`q8k_quantize` (Q8K::quantize, quant_q8k.rs:73), `matmul_rows_q8k` (quant_q8k::matmul_rows,
+:255). Device memory comes from torch (cuda == HIP on ROCm); torch is plumbing only.
+"""
+import ctypes as C
+
+import numpy as np
+import torch
+
+from ._lib import P, check, lib
+
+F32, F16, Q5_0, Q8_0, Q4K, Q6K = 0, 1, 6, 8, 12, 14
+
+
+class Context:
+    """A device + HIP stream (replaces the reference's WorkerPool as the execution resource)."""
+
+    def __init__(self, device=0):
+        if not torch.cuda.is_available():
+            raise RuntimeError("spindle_amd needs a visible AMD GPU (torch.cuda.is_available() is False)")
+        self.device = device
+        torch.cuda.set_device(device)
+        h = P()
+        check(lib.spx_create(device, C.byref(h)))
+        self.h = h
+
+    def sync(self):
+        check(lib.spx_sync(self.h))
+
+    def close(self):
+        if self.h:
+            lib.spx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Tensor:
+    """An uploaded weight tensor: n_expert slabs of rows x cols in GGUF block layout (Mat)."""
+
+    def __init__(self, ctx, dtype, cols, rows, ggml_bytes, n_expert=1):
+        self.ctx, self.dtype, self.cols, self.rows, self.n_expert = ctx, dtype, cols, rows, n_expert
+        data = np.ascontiguousarray(ggml_bytes, dtype=np.uint8)
+        rb = lib.spx_row_bytes(dtype, cols)
+        if rb <= 0 or data.size != rb * rows * n_expert:
+            raise ValueError(f"expected {rb * rows * n_expert} bytes for dtype {dtype} {rows}x{cols}x{n_expert}, got {data.size}")
+        h = P()
+        check(lib.spx_tensor_upload(ctx.h, dtype, cols, rows, n_expert, data.ctypes.data_as(P), C.byref(h)))
+        self.h = h
+        self.nbytes = data.size
+
+    def download(self):
+        out = np.empty(self.nbytes, np.uint8)
+        check(lib.spx_tensor_download(self.ctx.h, self.h, out.ctypes.data_as(P)))
+        return out
+
+    def free(self):
+        if self.h:
+            lib.spx_tensor_free(self.ctx.h, self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _p(t):
+    return C.c_void_p(t.data_ptr())
+
+
+def q8k_quantize(ctx, x):
+    """x: [m, n] float32 cuda tensor -> (d [m, n/256] f32, qs [m, n] i8, bsums [m, n/16] i16)."""
+    x = x.contiguous()
+    m, n = x.shape
+    d = torch.empty((m, n // 256), dtype=torch.float32, device=x.device)
+    qs = torch.empty((m, n), dtype=torch.int8, device=x.device)
+    bs = torch.empty((m, n // 16), dtype=torch.int16, device=x.device)
+    torch.cuda.synchronize()
+    check(lib.spx_q8k_quantize(ctx.h, _p(x), n, n, m, _p(d), _p(qs), _p(bs)))
+    ctx.sync()
+    return d, qs, bs
+
+
+def matmul_rows_q8k(ctx, w, q, expert=0, r0=0, r1=None, out=None):
+    d, qs, bs = q
+    m = qs.shape[0]
+    r1 = w.rows if r1 is None else r1
+    if out is None:
+        out = torch.full((m, w.rows), float("nan"), dtype=torch.float32, device=qs.device)
+    torch.cuda.synchronize()
+    check(lib.spx_matmul_rows_q8k(ctx.h, w.h, expert, _p(d), _p(qs), _p(bs), m, _p(out), out.shape[1], r0, r1))
+    ctx.sync()
+    return out
+
+
+def block_sums_q8k(ctx, w, row, q, expert=0):
+    d, qs, bs = q
+    nb = w.cols // 256
+    out = torch.empty((nb, 2), dtype=torch.int32, device=qs.device)
+    torch.cuda.synchronize()
+    check(lib.spx_block_sums_q8k(ctx.h, w.h, expert, row, _p(qs), _p(bs), _p(out)))
+    ctx.sync()
+    return out
+
+
+def matvec(ctx, w, x, expert=0):
+    """x: [m, cols] float32 cuda (m <= 16) -> [m, rows] (matvec for m == 1, matvec_multi above)."""
+    x = x.contiguous()
+    m = x.shape[0]
+    out = torch.empty((m, w.rows), dtype=torch.float32, device=x.device)
+    torch.cuda.synchronize()
+    check(lib.spx_matvec(ctx.h, w.h, expert, _p(x), x.shape[1], m, _p(out), w.rows))
+    ctx.sync()
+    return out
+
+
+matvec_multi = matvec

@@ -72,6 +72,81 @@ int spx_block_sums_q8k(spx_ctx *ctx, const spx_tensor *w, int expert, int64_t ro
 int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, int64_t ld_x, int m,
                float *out, int64_t ld_out);
 
+/* ------------------------------------------------------------------ synthetic weights */
+/* Seeded synthetic tensor in GGUF block layout (n_expert slabs of rows x cols). kind 0:
+ * quantized weights (Q4_K/Q6_K/Q8_0/Q5_0) whose dequantised values have std sigma; kind 1:
+ * F32 uniform with std sigma; kind 2: F32 1 + sigma*U(-1,1) (norm weights). Host memory;
+ * needs no GPU. No reference counterpart: the reference loads GGUF files only. */
+int spx_synth_tensor(int dtype, int64_t cols, int64_t rows, int n_expert, uint64_t seed, float sigma,
+                     int kind, void *out);
+
+/* ------------------------------------------------------------------ engine */
+/* Model hyperparameters (ModelConfig, smollm_chat.rs:38-120). attn_scale <= 0 means
+ * 1/sqrt(head_dim); embedding/residual/logit scales of 0 mean 1 (the non-Granite default). */
+typedef struct {
+  int dim, n_heads, n_kv_heads, head_dim, n_layers, vocab, max_seq;
+  float rope_theta, rms_eps;
+  int rope_neox;
+  int n_expert, n_expert_used, expert_norm;
+  float moe_prune;
+  float embedding_scale, residual_scale, logit_scale, attn_scale;
+} spx_model_config;
+
+typedef struct spx_engine spx_engine;
+
+/* SmolLm2Engine::load_with_index (smollm_chat.rs:1905-2154), split in three: create with the
+ * config, set every tensor by its GGUF name (resolve_layers :214-284: token_embd.weight,
+ * output.weight (optional, tied otherwise), output_norm.weight, blk.N.{attn_norm, attn_q,
+ * attn_k, attn_v, attn_output, attn_q_norm, attn_k_norm, ffn_norm, ffn_gate, ffn_up, ffn_down,
+ * ffn_gate_inp, ffn_gate_exps, ffn_up_exps, ffn_down_exps}.weight, attn_{q,k,v}.bias), then
+ * prepare (validates shapes, allocates the f16 KV cache [n_layers][max_seq][kv_dim]). */
+int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **out);
+int spx_engine_set_tensor(spx_engine *e, const char *name, int dtype, int64_t cols, int64_t rows,
+                          int n_expert, const void *ggml_bytes);
+int spx_engine_prepare(spx_engine *e);
+/* 1 (default): each pass length m is captured once into a HIP graph and replayed. */
+int spx_engine_set_graphs(spx_engine *e, int on);
+
+/* One pass of m <= 16 tokens at positions start_pos.. (forward_slice :3364-3552 for m == 1,
+ * forward_batch_slice :3142-3362 for m > 1, then compute_logits_batch :3588-3602 and the
+ * greedy pick of sample_from_logits :3624-3671). K/V of every row are written before any
+ * row attends, row b sees positions <= start_pos + b. Optional host outputs: hidden [m][dim]
+ * (after output_norm), logits [m][vocab], argmax [m]. Synchronous. */
+int spx_engine_forward(spx_engine *e, const int32_t *ids, int m, int start_pos, float *hidden,
+                       float *logits, int32_t *argmax);
+/* Number of distinct experts each MoE layer ran in the last pass (0 for dense layers). */
+int spx_engine_last_experts(spx_engine *e, int32_t *njobs_per_layer);
+/* Per layer and expert: passes that selected the expert since prepare ([n_layers][n_expert]). */
+int spx_engine_expert_counts(spx_engine *e, int32_t *counts);
+/* Copies the f16 K and V caches ([n_layers][max_seq][kv_dim] each) to host memory. */
+int spx_engine_kv_download(spx_engine *e, void *k_host, void *v_host);
+int spx_engine_destroy(spx_engine *e);
+
+/* Prompt-lookup drafting (lookup_draft, smollm_chat.rs:2982-3015) with the n-gram range as a
+ * parameter: the reference uses min_ngram 2, max_ngram 4. Returns the draft length. */
+int spx_lookup_draft(const int32_t *corpus, int n, int k, const int32_t *stop_ids, int n_stop,
+                     int min_ngram, int max_ngram, int32_t *draft, int *ngram);
+
+typedef struct {
+  int draft_len;     /* k: tokens proposed per verify (draft_len, :1952) */
+  int min_ngram, max_ngram;
+  int fixed;         /* SPINDLE_SPEC_FIXED: always verify the whole draft (:1703) */
+  int speculate;     /* 0: plain one-token decoding */
+  int adaptive_k;    /* grow k after a fully accepted draft (:4343) */
+  int prefill_chunk; /* prompt rows per pass, <= 16 */
+} spx_gen_params;
+
+typedef struct {
+  int accepted, drafted, verifies, steps; /* spec_stats (:1642-1643) plus one-token steps */
+  double prefill_us, step_us, verify_us;  /* host wall time of the passes */
+} spx_gen_stats;
+
+/* Greedy generation with prompt-lookup speculation (generate_reply's loop :4205-4348 minus
+ * chat framing, stop tokens ignored, repeat penalty 1): feeds the prompt from position 0,
+ * writes up to max_new tokens to out and returns how many. */
+int spx_engine_generate(spx_engine *e, const int32_t *prompt, int n_prompt, int max_new,
+                        const spx_gen_params *params, int32_t *out, spx_gen_stats *stats);
+
 #ifdef __cplusplus
 }
 #endif

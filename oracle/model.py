@@ -1,0 +1,88 @@
+"""Builds the oracle's CPU model (or_model) from the same tensors the GPU engine gets.
+
+TEST INFRASTRUCTURE ONLY (tests/, smoke() and bench.py's cpu_baseline leg)."""
+import ctypes as C
+
+import numpy as np
+
+from . import ffi
+
+
+class OracleModel:
+    def __init__(self, cfg, tensors):
+        self.cfg = cfg
+        self.keep = []
+        self.tensors = tensors
+        oc = ffi.Config(cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.n_layers, cfg.vocab, cfg.max_seq,
+                        cfg.rope_theta, cfg.rms_eps, int(cfg.rope_neox), cfg.n_expert, cfg.n_expert_used,
+                        int(cfg.expert_norm), cfg.moe_prune, cfg.embedding_scale, cfg.residual_scale,
+                        cfg.logit_scale, cfg.attn_scale)
+        layers = (ffi.Layer * cfg.n_layers)()
+        for l in range(cfg.n_layers):
+            p = f"blk.{l}."
+            ly = layers[l]
+            ly.attn_norm = self._vec(p + "attn_norm.weight")
+            ly.ffn_norm = self._vec(p + "ffn_norm.weight")
+            ly.wq, ly.wk, ly.wv, ly.wo = (self._mat(p + n) for n in ("attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight"))
+            ly.q_norm = self._vec(p + "attn_q_norm.weight")
+            ly.k_norm = self._vec(p + "attn_k_norm.weight")
+            ly.q_bias = self._vec(p + "attn_q.bias")
+            ly.k_bias = self._vec(p + "attn_k.bias")
+            ly.v_bias = self._vec(p + "attn_v.bias")
+            if (p + "ffn_gate_inp.weight") in tensors:
+                ly.is_moe = 1
+                ly.router = self._mat(p + "ffn_gate_inp.weight")
+                ly.gate, ly.up, ly.down = (self._mat(p + n) for n in ("ffn_gate_exps.weight", "ffn_up_exps.weight", "ffn_down_exps.weight"))
+            else:
+                ly.gate, ly.up, ly.down = (self._mat(p + n) for n in ("ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"))
+        self.layers = layers
+        n = cfg.n_layers * cfg.max_seq * cfg.kv_dim
+        self.k_cache = np.zeros(n, np.uint16)
+        self.v_cache = np.zeros(n, np.uint16)
+        m = ffi.Model()
+        m.c = oc
+        m.layers = C.cast(layers, C.POINTER(ffi.Layer))
+        m.embed = self._mat("token_embd.weight")
+        m.lm_head = self._mat("output.weight") if "output.weight" in tensors else m.embed
+        m.output_norm = self._vec("output_norm.weight")
+        m.k_cache = self.k_cache.ctypes.data
+        m.v_cache = self.v_cache.ctypes.data
+        self.m = m
+        ffi.lib.or_model_init(C.byref(m))
+
+    def _vec(self, name):
+        if name not in self.tensors:
+            return None
+        return self.tensors[name][1].ctypes.data
+
+    def _mat(self, name):
+        spec, data = self.tensors[name]
+        return ffi.Mat(spec.dtype, spec.cols, spec.rows, data.ctypes.data)
+
+    def forward(self, ids, start_pos):
+        ids = np.ascontiguousarray(ids, np.int32)
+        h = np.empty((ids.size, self.cfg.dim), np.float32)
+        rc = ffi.lib.or_forward_batch(C.byref(self.m), ids.ctypes.data_as(C.c_void_p), ids.size, start_pos, h.ctypes.data_as(C.c_void_p))
+        assert rc == 0
+        return h
+
+    def logits(self, hidden):
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        out = np.empty((hidden.shape[0], self.cfg.vocab), np.float32)
+        assert ffi.lib.or_logits(C.byref(self.m), hidden.ctypes.data_as(C.c_void_p), hidden.shape[0], out.ctypes.data_as(C.c_void_p)) == 0
+        return out
+
+    def argmax(self, logits):
+        lg = np.ascontiguousarray(logits, np.float32)
+        return ffi.lib.or_argmax(lg.ctypes.data_as(C.c_void_p), lg.size, self.cfg.logit_scale)
+
+    def generate(self, prompt, max_new, draft_len=8, min_ngram=2, max_ngram=4, fixed=False, speculate=True,
+                 adaptive_k=True, prefill_chunk=16):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(max_new, np.int32)
+        gp = ffi.GenParams(draft_len, min_ngram, max_ngram, int(fixed), int(speculate), int(adaptive_k), prefill_chunk)
+        st = ffi.GenStats()
+        n = ffi.lib.or_generate(C.byref(self.m), prompt.ctypes.data_as(C.c_void_p), prompt.size, max_new, C.byref(gp),
+                                out.ctypes.data_as(C.c_void_p), C.byref(st))
+        assert n >= 0
+        return out[:n], {k: getattr(st, k) for k, _ in ffi.GenStats._fields_}

@@ -28,6 +28,18 @@ SIGNATURES = {
     "spx_matmul_rows_q8k": (C.c_int, [P, P, C.c_int, P, P, P, C.c_int, P, I64, I64, I64]),
     "spx_block_sums_q8k": (C.c_int, [P, P, C.c_int, I64, P, P, P]),
     "spx_matvec": (C.c_int, [P, P, C.c_int, P, I64, C.c_int, P, I64]),
+    "spx_synth_tensor": (C.c_int, [C.c_int, I64, I64, C.c_int, C.c_uint64, C.c_float, C.c_int, P]),
+    "spx_engine_create": (C.c_int, [P, P, C.POINTER(P)]),
+    "spx_engine_set_tensor": (C.c_int, [P, C.c_char_p, C.c_int, I64, I64, C.c_int, P]),
+    "spx_engine_prepare": (C.c_int, [P]),
+    "spx_engine_set_graphs": (C.c_int, [P, C.c_int]),
+    "spx_engine_forward": (C.c_int, [P, P, C.c_int, C.c_int, P, P, P]),
+    "spx_engine_last_experts": (C.c_int, [P, P]),
+    "spx_engine_expert_counts": (C.c_int, [P, P]),
+    "spx_engine_kv_download": (C.c_int, [P, P, P]),
+    "spx_engine_destroy": (C.c_int, [P]),
+    "spx_lookup_draft": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int, C.c_int, C.c_int, P, P]),
+    "spx_engine_generate": (C.c_int, [P, P, C.c_int, C.c_int, P, P, P]),
 }
 
 

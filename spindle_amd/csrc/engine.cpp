@@ -1,0 +1,598 @@
+// The decode / verify engine: a C++ restatement of SmolLm2Engine's hot API
+// (smollm_chat.rs:1574-1668, forward_slice :3364-3552, forward_batch_slice :3142-3362,
+// compute_logits_batch :3588-3602, the greedy speculative loop of generate_reply :4205-4348)
+// over one GPU. The whole model and the f16 KV cache stay resident in HBM; one forward pass
+// of m <= 16 rows is a fixed launch sequence, captured once per m into a HIP graph and
+// replayed with the step record (token ids, start position) in device memory.
+#include <string.h>
+
+#include <chrono>
+#include <cmath>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/spx.h"
+#include "internal.h"
+#include "layer_kernels.h"
+
+using namespace spx;
+
+namespace {
+
+struct Q8Buf {
+  float *d = nullptr;
+  int8_t *q = nullptr;
+  int16_t *b = nullptr;
+};
+
+struct LayerW {
+  const float *attn_norm = nullptr, *ffn_norm = nullptr;
+  const float *q_bias = nullptr, *k_bias = nullptr, *v_bias = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+  spx_tensor *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
+  bool moe = false;
+  spx_tensor *gate = nullptr, *up = nullptr, *down = nullptr, *router = nullptr;
+  int *njobs = nullptr;  // device: jobs of this layer's last pass (union of chosen experts)
+};
+
+bool is_kq(const spx_tensor *t) { return t && (t->v.dtype == T_Q4K || t->v.dtype == T_Q6K); }
+
+int64_t now_us() {
+  return std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+}  // namespace
+
+struct spx_engine {
+  spx_ctx *ctx = nullptr;
+  spx_model_config c{};
+  int q_dim = 0, kv_dim = 0, n_ff = 0, max_chunks = 0;
+  std::map<std::string, spx_tensor *> mats;
+  std::map<std::string, float *> vecs;
+  std::map<std::string, int64_t> vec_len;
+  std::vector<LayerW> L;
+  spx_tensor *embed = nullptr, *lm_head = nullptr;
+  const float *out_norm = nullptr;
+  bool prepared = false, use_graphs = true;
+  std::vector<void *> allocs;
+  // device state
+  __half *kc = nullptr, *vc = nullptr;
+  float2 *rope = nullptr;
+  StepRec *st_dev = nullptr, *st_host = nullptr;
+  float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *proj = nullptr;
+  Q8Buf xq, aq, hq;
+  float *h = nullptr, *u = nullptr, *y = nullptr, *rlog = nullptr, *logits = nullptr;
+  int *amax = nullptr;
+  float *part_m = nullptr, *part_l = nullptr, *part_o = nullptr;
+  int *chosen = nullptr, *nkeep = nullptr, *expert_count = nullptr;
+  float *weights = nullptr;
+  Job *jobs_gu = nullptr, *jobs_dn = nullptr;
+  hipGraphExec_t graph[MAX_M + 1] = {};
+  int n_used = 0;
+
+  template <class T>
+  T *dalloc(size_t n) {
+    void *p = nullptr;
+    if (hipMalloc(&p, std::max<size_t>(n * sizeof(T), 16)) != hipSuccess) return nullptr;
+    (void)hipMemset(p, 0, std::max<size_t>(n * sizeof(T), 16));
+    allocs.push_back(p);
+    return static_cast<T *>(p);
+  }
+};
+
+namespace {
+
+// ---------------------------------------------------------------- matrix launches
+int gemv(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld_x, const Q8Buf *xq, float *out, int64_t ld_out,
+         const Job *jobs = nullptr, const int *njobs = nullptr, int max_jobs = 0, int expert = 0) {
+  const bool grouped = jobs != nullptr;
+  if (is_kq(w)) {
+    KQArgs a{};
+    a.w = w->v; a.xd = xq->d; a.xq = xq->q; a.xb = xq->b; a.out = out; a.ld_out = ld_out;
+    a.r0 = 0; a.r1 = w->v.rows; a.expert = expert; a.m = m; a.jobs = jobs; a.njobs = njobs;
+    SPX_HIP(launch_gemv_kq(a, m, grouped, max_jobs, E->ctx->stream));
+  } else {
+    FArgs a{};
+    a.w = w->v; a.x = x; a.ld_x = ld_x; a.out = out; a.ld_out = ld_out; a.r0 = 0; a.r1 = w->v.rows;
+    a.expert = expert; a.m = m; a.jobs = jobs; a.njobs = njobs;
+    SPX_HIP(launch_gemv_f(a, m, grouped, max_jobs, E->ctx->stream));
+  }
+  return 0;
+}
+
+// One forward pass of m rows at the step record's start position: embeddings through the
+// LM head and the greedy argmax (forward_slice / forward_batch_slice + compute_logits_batch).
+int enqueue_forward(spx_engine *E, int m) {
+  const auto &c = E->c;
+  hipStream_t s = E->ctx->stream;
+  const int dim = c.dim, hd = c.head_dim;
+  SPX_HIP(launch_embed(E->embed->v, E->st_dev, E->x, dim, c.embedding_scale, m, s));
+  const float *pending = nullptr;  // residual to add before the next norm
+  for (int l = 0; l < c.n_layers; l++) {
+    const LayerW &ly = E->L[l];
+    const bool q_int = is_kq(ly.wq) || is_kq(ly.wk) || is_kq(ly.wv);
+    SPX_HIP(launch_res_norm(E->x, dim, pending, dim, c.residual_scale, ly.attn_norm, dim, c.rms_eps, E->xn, dim,
+                            q_int ? E->xq.d : nullptr, q_int ? E->xq.q : nullptr, q_int ? E->xq.b : nullptr, E->st_dev, m, s));
+    if (int r = gemv(E, ly.wq, m, E->xn, dim, &E->xq, E->q, E->q_dim)) return r;
+    if (int r = gemv(E, ly.wk, m, E->xn, dim, &E->xq, E->k, E->kv_dim)) return r;
+    if (int r = gemv(E, ly.wv, m, E->xn, dim, &E->xq, E->v, E->kv_dim)) return r;
+    QKArgs qa{};
+    qa.q = E->q; qa.k = E->k; qa.v = E->v; qa.ld_q = E->q_dim; qa.ld_kv = E->kv_dim;
+    qa.q_bias = ly.q_bias; qa.k_bias = ly.k_bias; qa.v_bias = ly.v_bias; qa.q_norm = ly.q_norm; qa.k_norm = ly.k_norm;
+    qa.rope = E->rope; qa.k_cache = E->kc; qa.v_cache = E->vc; qa.layer = l; qa.max_seq = c.max_seq; qa.kv_dim = E->kv_dim;
+    qa.head_dim = hd; qa.n_heads = c.n_heads; qa.n_kv = c.n_kv_heads; qa.neox = c.rope_neox; qa.eps = c.rms_eps;
+    SPX_HIP(launch_qk_rope_kv(qa, E->st_dev, m, s));
+    AttnArgs aa{};
+    aa.q = E->q; aa.ld_q = E->q_dim; aa.k_cache = E->kc; aa.v_cache = E->vc; aa.part_m = E->part_m; aa.part_l = E->part_l;
+    aa.part_o = E->part_o; aa.out = E->att; aa.ld_out = E->q_dim; aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim;
+    aa.head_dim = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads; aa.max_chunks = E->max_chunks;
+    aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
+    SPX_HIP(launch_attention(aa, E->st_dev, m, s));
+    if (is_kq(ly.wo)) SPX_HIP(launch_q8k_quantize(E->att, E->q_dim, E->q_dim, m, E->aq.d, E->aq.q, E->aq.b, s));
+    if (int r = gemv(E, ly.wo, m, E->att, E->q_dim, &E->aq, E->proj, dim)) return r;
+    const bool f_int = is_kq(ly.gate) || is_kq(ly.up);
+    SPX_HIP(launch_res_norm(E->x, dim, E->proj, dim, c.residual_scale, ly.ffn_norm, dim, c.rms_eps, E->xn, dim,
+                            f_int ? E->xq.d : nullptr, f_int ? E->xq.q : nullptr, f_int ? E->xq.b : nullptr, E->st_dev, m, s));
+    const int nff = (int)ly.gate->v.rows;
+    const bool d_int = is_kq(ly.down);
+    if (!ly.moe) {  // ffn_forward / ffn_forward_multi (:590-646)
+      if (int r = gemv(E, ly.gate, m, E->xn, dim, &E->xq, E->h, nff)) return r;
+      if (int r = gemv(E, ly.up, m, E->xn, dim, &E->xq, E->u, nff)) return r;
+      SwigluArgs sa{};
+      sa.g = E->h; sa.u = E->u; sa.ld = nff; sa.n = nff;
+      if (d_int) { sa.qd = E->hq.d; sa.qq = E->hq.q; sa.qb = E->hq.b; }
+      SPX_HIP(launch_swiglu(sa, E->st_dev, m, s));
+      if (int r = gemv(E, ly.down, m, E->h, nff, &E->hq, E->proj, dim)) return r;
+    } else {  // moe_forward / moe_forward_batch (:925-1392)
+      const int nu = c.n_expert_used, ne = c.n_expert;
+      if (int r = gemv(E, ly.router, m, E->xn, dim, nullptr, E->rlog, ne)) return r;
+      RouteArgs ra{};
+      ra.logits = E->rlog; ra.ld_logits = ne; ra.n_expert = ne; ra.n_used = nu; ra.norm = c.expert_norm; ra.moe_prune = c.moe_prune;
+      ra.chosen = E->chosen; ra.weights = E->weights; ra.nkeep = E->nkeep; ra.jobs_gu = E->jobs_gu; ra.jobs_dn = E->jobs_dn;
+      ra.njobs = ly.njobs; ra.expert_count = E->expert_count + (size_t)l * ne;
+      SPX_HIP(launch_moe_route(ra, E->st_dev, s));
+      const int max_jobs = std::min(ne, m * nu);
+      if (int r = gemv(E, ly.gate, m, E->xn, dim, &E->xq, E->h, nff, E->jobs_gu, ly.njobs, max_jobs)) return r;
+      if (int r = gemv(E, ly.up, m, E->xn, dim, &E->xq, E->u, nff, E->jobs_gu, ly.njobs, max_jobs)) return r;
+      SwigluArgs sa{};
+      sa.g = E->h; sa.u = E->u; sa.ld = nff; sa.n = nff; sa.jobs = E->jobs_gu; sa.njobs = ly.njobs;
+      if (d_int) { sa.qd = E->hq.d; sa.qq = E->hq.q; sa.qb = E->hq.b; }
+      SPX_HIP(launch_swiglu(sa, E->st_dev, m * nu, s));
+      if (int r = gemv(E, ly.down, m, E->h, nff, &E->hq, E->y, dim, E->jobs_dn, ly.njobs, max_jobs)) return r;
+      CombineArgs ca{};
+      ca.y = E->y; ca.ld_y = dim; ca.weights = E->weights; ca.nkeep = E->nkeep; ca.n_used = nu; ca.dim = dim; ca.out = E->proj; ca.ld_out = dim;
+      SPX_HIP(launch_moe_combine(ca, E->st_dev, m, s));
+    }
+    pending = E->proj;
+  }
+  const bool h_int = is_kq(E->lm_head);
+  SPX_HIP(launch_res_norm(E->x, dim, pending, dim, c.residual_scale, E->out_norm, dim, c.rms_eps, E->xn, dim,
+                          h_int ? E->xq.d : nullptr, h_int ? E->xq.q : nullptr, h_int ? E->xq.b : nullptr, E->st_dev, m, s));
+  if (int r = gemv(E, E->lm_head, m, E->xn, dim, &E->xq, E->logits, c.vocab)) return r;
+  SPX_HIP(launch_argmax(E->logits, c.vocab, c.vocab, c.logit_scale, E->amax, E->st_dev, m, s));
+  return 0;
+}
+
+int run_forward(spx_engine *E, int m) {
+  hipStream_t s = E->ctx->stream;
+  if (!E->use_graphs) return enqueue_forward(E, m);
+  if (!E->graph[m]) {
+    SPX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int r = enqueue_forward(E, m);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (r) { if (g) (void)hipGraphDestroy(g); return r; }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    e = hipGraphInstantiate(&E->graph[m], g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) { E->graph[m] = nullptr; return hip_fail(e, "hipGraphInstantiate"); }
+  }
+  SPX_HIP(hipGraphLaunch(E->graph[m], s));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **out) {
+  if (!ctx || !cfg || !out) return fail("spx_engine_create: null argument");
+  const spx_model_config &c = *cfg;
+  if (c.dim <= 0 || c.dim > 4096 || c.dim % 16) return fail("spx_engine_create: dim must be a positive multiple of 16, at most 4096");
+  if (c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads) return fail("spx_engine_create: n_heads must be a multiple of n_kv_heads");
+  if (c.head_dim <= 0 || c.head_dim > 128 || c.head_dim % 8) return fail("spx_engine_create: head_dim must be a multiple of 8, at most 128");
+  if (16 * (c.n_heads / c.n_kv_heads) > 4096) return fail("spx_engine_create: too many query heads per kv head");
+  if (c.n_layers <= 0 || c.vocab <= 0 || c.max_seq <= 0) return fail("spx_engine_create: bad layer count, vocab or max_seq");
+  if (c.n_expert < 0 || c.n_expert > 256 || c.n_expert_used < 0 || c.n_expert_used > 32 || (c.n_expert && !c.n_expert_used))
+    return fail("spx_engine_create: unsupported expert counts (n_expert <= 256, n_expert_used in 1..32)");
+  spx_engine *E = new spx_engine();
+  E->ctx = ctx;
+  E->c = c;
+  if (E->c.embedding_scale == 0.0f) E->c.embedding_scale = 1.0f;
+  if (E->c.residual_scale == 0.0f) E->c.residual_scale = 1.0f;
+  if (E->c.logit_scale == 0.0f) E->c.logit_scale = 1.0f;
+  E->q_dim = c.n_heads * c.head_dim;
+  E->kv_dim = c.n_kv_heads * c.head_dim;
+  E->L.resize(c.n_layers);
+  *out = E;
+  return 0;
+}
+
+int spx_engine_set_tensor(spx_engine *E, const char *name, int dtype, int64_t cols, int64_t rows, int n_expert, const void *data) {
+  if (!E || !name || !data) return fail("spx_engine_set_tensor: null argument");
+  if (E->prepared) return fail("spx_engine_set_tensor: engine already prepared");
+  const std::string n(name);
+  SPX_HIP(hipSetDevice(E->ctx->device));
+  const bool is_vec = n.find("_norm.weight") != std::string::npos || n.find(".bias") != std::string::npos;
+  if (is_vec) {
+    if (dtype != T_F32) return fail(n + ": norms and biases must be F32 (resolve_layers, smollm_chat.rs:220-226)");
+    const int64_t len = cols * rows * n_expert;
+    float *d = E->dalloc<float>((size_t)len);
+    if (!d) return fail("out of device memory for " + n);
+    SPX_HIP(hipMemcpy(d, data, sizeof(float) * len, hipMemcpyHostToDevice));
+    E->vecs[n] = d;
+    E->vec_len[n] = len;
+    return 0;
+  }
+  spx_tensor *t = nullptr;
+  if (int r = spx_tensor_upload(E->ctx, dtype, cols, rows, n_expert, data, &t)) return r;
+  auto it = E->mats.find(n);
+  if (it != E->mats.end()) spx_tensor_free(E->ctx, it->second);
+  E->mats[n] = t;
+  return 0;
+}
+
+int spx_engine_prepare(spx_engine *E) {
+  if (!E) return fail("spx_engine_prepare: null engine");
+  if (E->prepared) return 0;
+  auto &c = E->c;
+  auto mat = [&](const std::string &n) -> spx_tensor * { auto it = E->mats.find(n); return it == E->mats.end() ? nullptr : it->second; };
+  auto vec = [&](const std::string &n, int64_t len) -> const float * {
+    auto it = E->vecs.find(n);
+    if (it == E->vecs.end() || E->vec_len[n] != len) return nullptr;
+    return it->second;
+  };
+  auto need_mat = [&](const std::string &n, int64_t cols, int64_t rows, int ne, spx_tensor **dst) -> int {
+    spx_tensor *t = mat(n);
+    if (!t) return fail("missing tensor " + n);
+    if (t->v.cols != cols || t->v.rows != rows || t->v.n_expert != ne)
+      return fail(n + ": expected " + std::to_string(rows) + "x" + std::to_string(cols) + "x" + std::to_string(ne) + ", got " +
+                  std::to_string(t->v.rows) + "x" + std::to_string(t->v.cols) + "x" + std::to_string(t->v.n_expert));
+    if (t->v.dtype == T_F16) return fail(n + ": F16 weight matrices are not supported by the GPU kernels");
+    *dst = t;
+    return 0;
+  };
+  E->embed = mat("token_embd.weight");
+  if (!E->embed || E->embed->v.cols != c.dim || E->embed->v.rows != c.vocab) return fail("missing or misshaped token_embd.weight");
+  E->lm_head = mat("output.weight") ? mat("output.weight") : E->embed;  // tied embeddings (:1921)
+  if (E->lm_head->v.cols != c.dim || E->lm_head->v.rows != c.vocab) return fail("misshaped output.weight");
+  if (!(E->out_norm = vec("output_norm.weight", c.dim))) return fail("missing output_norm.weight");
+  int nff_max = 0;
+  for (int l = 0; l < c.n_layers; l++) {
+    LayerW &ly = E->L[l];
+    const std::string p = "blk." + std::to_string(l) + ".";
+    if (!(ly.attn_norm = vec(p + "attn_norm.weight", c.dim))) return fail("missing " + p + "attn_norm.weight");
+    if (!(ly.ffn_norm = vec(p + "ffn_norm.weight", c.dim))) return fail("missing " + p + "ffn_norm.weight");
+    if (int r = need_mat(p + "attn_q.weight", c.dim, E->q_dim, 1, &ly.wq)) return r;
+    if (int r = need_mat(p + "attn_k.weight", c.dim, E->kv_dim, 1, &ly.wk)) return r;
+    if (int r = need_mat(p + "attn_v.weight", c.dim, E->kv_dim, 1, &ly.wv)) return r;
+    if (int r = need_mat(p + "attn_output.weight", E->q_dim, c.dim, 1, &ly.wo)) return r;
+    ly.q_bias = vec(p + "attn_q.bias", E->q_dim);
+    ly.k_bias = vec(p + "attn_k.bias", E->kv_dim);
+    ly.v_bias = vec(p + "attn_v.bias", E->kv_dim);
+    ly.q_norm = vec(p + "attn_q_norm.weight", c.head_dim);
+    ly.k_norm = vec(p + "attn_k_norm.weight", c.head_dim);
+    if ((E->vecs.count(p + "attn_q_norm.weight") && !ly.q_norm) || (E->vecs.count(p + "attn_k_norm.weight") && !ly.k_norm))
+      return fail(p + "attn_q_norm/attn_k_norm: only per-head norms (head_dim entries) are supported");
+    if (mat(p + "ffn_gate_inp.weight")) {
+      if (!c.n_expert) return fail("MoE tensors present but expert_count is 0");
+      ly.moe = true;
+      spx_tensor *r = mat(p + "ffn_gate_inp.weight");
+      if (r->v.dtype != T_F32 || r->v.cols != c.dim || r->v.rows != c.n_expert) return fail(p + "ffn_gate_inp.weight: expected F32 " + std::to_string(c.n_expert) + "x" + std::to_string(c.dim));
+      ly.router = r;
+      spx_tensor *g = mat(p + "ffn_gate_exps.weight");
+      if (!g) return fail("missing " + p + "ffn_gate_exps.weight");
+      const int64_t nff = g->v.rows;
+      if (int rr = need_mat(p + "ffn_gate_exps.weight", c.dim, nff, c.n_expert, &ly.gate)) return rr;
+      if (int rr = need_mat(p + "ffn_up_exps.weight", c.dim, nff, c.n_expert, &ly.up)) return rr;
+      if (int rr = need_mat(p + "ffn_down_exps.weight", nff, c.dim, c.n_expert, &ly.down)) return rr;
+      nff_max = std::max<int>(nff_max, (int)nff);
+    } else {
+      spx_tensor *g = mat(p + "ffn_gate.weight");
+      if (!g) return fail("missing " + p + "ffn_gate.weight");
+      const int64_t nff = g->v.rows;
+      if (int rr = need_mat(p + "ffn_gate.weight", c.dim, nff, 1, &ly.gate)) return rr;
+      if (int rr = need_mat(p + "ffn_up.weight", c.dim, nff, 1, &ly.up)) return rr;
+      if (int rr = need_mat(p + "ffn_down.weight", nff, c.dim, 1, &ly.down)) return rr;
+      nff_max = std::max<int>(nff_max, (int)nff);
+    }
+    if (ly.wq->v.dtype == T_F32 || ly.wo->v.dtype == T_F32) {
+      if (c.dim % 16 || E->q_dim % 16) return fail("F32 projections need 16-multiple widths");
+    }
+  }
+  if (nff_max > 4096 || nff_max % 16) return fail("feed-forward width must be a multiple of 16, at most 4096");
+  E->n_ff = nff_max;
+  for (auto &ly : E->L)
+    for (spx_tensor *t : {ly.wq, ly.wk, ly.wv, ly.wo, ly.gate, ly.up, ly.down, E->lm_head})
+      if (t && is_kq(t) && t->v.cols % 256) return fail("K-quant tensors need cols % 256 == 0");
+  // device buffers
+  const int M = MAX_M, nu = std::max(1, c.n_expert_used), nv = M * nu;
+  const int64_t kvn = (int64_t)c.n_layers * c.max_seq * E->kv_dim;
+  E->max_chunks = (c.max_seq + ATT_CHUNK - 1) / ATT_CHUNK;
+  const int g = c.n_heads / c.n_kv_heads;
+  const int64_t prow = (int64_t)c.n_kv_heads * 16 * g * E->max_chunks;
+  const int qmax = std::max({c.dim, E->q_dim, E->n_ff});
+  bool ok = (E->kc = E->dalloc<__half>(kvn)) && (E->vc = E->dalloc<__half>(kvn)) &&
+            (E->rope = E->dalloc<float2>((size_t)c.max_seq * (c.head_dim / 2))) && (E->st_dev = E->dalloc<StepRec>(1)) &&
+            (E->x = E->dalloc<float>((size_t)M * c.dim)) && (E->xn = E->dalloc<float>((size_t)M * c.dim)) &&
+            (E->q = E->dalloc<float>((size_t)M * E->q_dim)) && (E->k = E->dalloc<float>((size_t)M * E->kv_dim)) &&
+            (E->v = E->dalloc<float>((size_t)M * E->kv_dim)) && (E->att = E->dalloc<float>((size_t)M * E->q_dim)) &&
+            (E->proj = E->dalloc<float>((size_t)M * c.dim)) && (E->xq.d = E->dalloc<float>((size_t)M * qmax / 256 + 16)) &&
+            (E->xq.q = E->dalloc<int8_t>((size_t)M * qmax)) && (E->xq.b = E->dalloc<int16_t>((size_t)M * qmax / 16 + 16)) &&
+            (E->aq.d = E->dalloc<float>((size_t)M * E->q_dim / 256 + 16)) && (E->aq.q = E->dalloc<int8_t>((size_t)M * E->q_dim)) &&
+            (E->aq.b = E->dalloc<int16_t>((size_t)M * E->q_dim / 16 + 16)) && (E->hq.d = E->dalloc<float>((size_t)nv * E->n_ff / 256 + 16)) &&
+            (E->hq.q = E->dalloc<int8_t>((size_t)nv * E->n_ff)) && (E->hq.b = E->dalloc<int16_t>((size_t)nv * E->n_ff / 16 + 16)) &&
+            (E->h = E->dalloc<float>((size_t)nv * E->n_ff)) && (E->u = E->dalloc<float>((size_t)nv * E->n_ff)) &&
+            (E->y = E->dalloc<float>((size_t)nv * c.dim)) && (E->rlog = E->dalloc<float>((size_t)M * std::max(1, c.n_expert))) &&
+            (E->logits = E->dalloc<float>((size_t)M * c.vocab)) && (E->amax = E->dalloc<int>(M)) &&
+            (E->part_m = E->dalloc<float>(prow)) && (E->part_l = E->dalloc<float>(prow)) &&
+            (E->part_o = E->dalloc<float>(prow * c.head_dim)) && (E->chosen = E->dalloc<int>(16 * 32)) &&
+            (E->nkeep = E->dalloc<int>(16)) && (E->weights = E->dalloc<float>(16 * 32)) &&
+            (E->jobs_gu = E->dalloc<Job>(256)) && (E->jobs_dn = E->dalloc<Job>(256)) &&
+            (E->expert_count = E->dalloc<int>((size_t)c.n_layers * std::max(1, c.n_expert)));
+  if (!ok) return fail("spx_engine_prepare: out of device memory");
+  for (auto &ly : E->L)
+    if (ly.moe && !(ly.njobs = E->dalloc<int>(1))) return fail("out of device memory");
+  SPX_HIP(hipHostMalloc(&E->st_host, sizeof(StepRec)));
+  // RoPE table: inv_freq = 1/theta^(2i/hd) (Rope::new :1399-1402); angle = pos * inv_freq.
+  const int half = c.head_dim / 2;
+  std::vector<float2> tab((size_t)c.max_seq * half);
+  std::vector<float> inv(half);
+  for (int i = 0; i < half; i++) inv[i] = 1.0f / powf(c.rope_theta, 2.0f * (float)i / (float)c.head_dim);
+  for (int p = 0; p < c.max_seq; p++)
+    for (int i = 0; i < half; i++) {
+      const float ang = (float)p * inv[i];
+      tab[(size_t)p * half + i] = make_float2(cosf(ang), sinf(ang));
+    }
+  SPX_HIP(hipMemcpy(E->rope, tab.data(), sizeof(float2) * tab.size(), hipMemcpyHostToDevice));
+  E->n_used = nu;
+  E->prepared = true;
+  return 0;
+}
+
+int spx_engine_set_graphs(spx_engine *E, int on) {
+  if (!E) return fail("null engine");
+  E->use_graphs = on != 0;
+  return 0;
+}
+
+int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, float *hidden, float *logits, int32_t *argmax) {
+  if (!E || !ids) return fail("spx_engine_forward: null argument");
+  if (!E->prepared) return fail("spx_engine_forward: call spx_engine_prepare first");
+  if (m < 1 || m > MAX_M) return fail("spx_engine_forward: m must be in 1..16");
+  if (start_pos < 0 || start_pos + m > E->c.max_seq) return fail("spx_engine_forward: positions beyond max_seq (the KV window is full)");
+  for (int i = 0; i < m; i++)
+    if (ids[i] < 0 || ids[i] >= E->c.vocab) return fail("spx_engine_forward: token id out of range");
+  hipStream_t s = E->ctx->stream;
+  SPX_HIP(hipSetDevice(E->ctx->device));
+  SPX_HIP(hipStreamSynchronize(s));
+  E->st_host->m = m;
+  E->st_host->start = start_pos;
+  for (int i = 0; i < m; i++) E->st_host->ids[i] = ids[i];
+  SPX_HIP(hipMemcpyAsync(E->st_dev, E->st_host, sizeof(StepRec), hipMemcpyHostToDevice, s));
+  if (int r = run_forward(E, m)) return r;
+  if (hidden) SPX_HIP(hipMemcpyAsync(hidden, E->xn, sizeof(float) * m * E->c.dim, hipMemcpyDeviceToHost, s));
+  if (logits) SPX_HIP(hipMemcpyAsync(logits, E->logits, sizeof(float) * m * E->c.vocab, hipMemcpyDeviceToHost, s));
+  if (argmax) SPX_HIP(hipMemcpyAsync(argmax, E->amax, sizeof(int) * m, hipMemcpyDeviceToHost, s));
+  SPX_HIP(hipStreamSynchronize(s));
+  return 0;
+}
+
+int spx_engine_last_experts(spx_engine *E, int32_t *njobs_per_layer) {
+  if (!E || !njobs_per_layer) return fail("null argument");
+  SPX_HIP(hipStreamSynchronize(E->ctx->stream));
+  for (int l = 0; l < E->c.n_layers; l++) {
+    njobs_per_layer[l] = 0;
+    if (E->L[l].moe) SPX_HIP(hipMemcpy(&njobs_per_layer[l], E->L[l].njobs, sizeof(int), hipMemcpyDeviceToHost));
+  }
+  return 0;
+}
+
+int spx_engine_expert_counts(spx_engine *E, int32_t *counts) {
+  if (!E || !counts) return fail("null argument");
+  SPX_HIP(hipStreamSynchronize(E->ctx->stream));
+  SPX_HIP(hipMemcpy(counts, E->expert_count, sizeof(int) * E->c.n_layers * std::max(1, E->c.n_expert), hipMemcpyDeviceToHost));
+  return 0;
+}
+
+int spx_engine_kv_download(spx_engine *E, void *k_host, void *v_host) {
+  if (!E || !k_host || !v_host) return fail("null argument");
+  const size_t n = (size_t)E->c.n_layers * E->c.max_seq * E->kv_dim * sizeof(__half);
+  SPX_HIP(hipStreamSynchronize(E->ctx->stream));
+  SPX_HIP(hipMemcpy(k_host, E->kc, n, hipMemcpyDeviceToHost));
+  SPX_HIP(hipMemcpy(v_host, E->vc, n, hipMemcpyDeviceToHost));
+  return 0;
+}
+
+// ---------------------------------------------------------------- speculation
+// lookup_draft (:2982-3015): latest earlier occurrence of the corpus's last n tokens, n from
+// max_ngram down to min_ngram; a 2-token match proposes at most 2; drafts stop at stop ids.
+int spx_lookup_draft(const int32_t *c, int n, int k, const int32_t *stop, int n_stop, int min_ng, int max_ng, int32_t *draft, int *ngram) {
+  *ngram = 0;
+  if (k <= 0) return 0;
+  for (int ng = max_ng; ng >= min_ng; ng--) {
+    if (n <= ng) continue;
+    const int32_t *pat = c + n - ng;
+    for (int i = n - ng - 1; i >= 0; i--) {
+      if (c[i + ng - 1] != pat[ng - 1] || memcmp(c + i, pat, sizeof(int32_t) * ng) != 0) continue;
+      const int s = i + ng, kk = ng == 2 ? std::min(k, 2) : k, e = std::min(s + kk, n);
+      int len = 0;
+      for (int j = s; j < e; j++) {
+        bool is_stop = false;
+        for (int q = 0; q < n_stop; q++) is_stop |= stop[q] == c[j];
+        if (is_stop) break;
+        draft[len++] = c[j];
+      }
+      if (len > 0) { *ngram = ng; return len; }
+    }
+  }
+  return 0;
+}
+
+}  // extern "C"
+
+namespace {
+
+// SpecModel (:1670-1809): measured accept rates and pass costs choose each draft's length.
+struct SpecModel {
+  double acc[4] = {1, 1, 1, 1}, fail_[4] = {1, 1, 1, 1}, t1_us = 100000.0, extra_us = 30000.0;
+  bool have_t1 = false, have_extra = false, fixed = false;
+  int since_try = 0;
+  static int cls(int ng) { return ng == 0 ? 3 : ng <= 2 ? 0 : ng == 3 ? 1 : 2; }
+  double rate(int c) const { return acc[c] / (acc[c] + fail_[c]); }
+  double cost(int b) const { return t1_us + extra_us * (double)(b > 1 ? b - 1 : 0); }
+  int best_len(int c, int avail) {
+    if (fixed || avail == 0) return avail;
+    const double p = rate(c);
+    double best_rate = 1.0 / cost(1), gain = 1.0, pk = 1.0;
+    int best = 0;
+    for (int k = 1; k <= avail; k++) {
+      pk *= p;
+      gain += pk;
+      const double r = gain / cost(k + 1);
+      if (r > best_rate) { best_rate = r; best = k; }
+    }
+    if (best == 0 && ++since_try >= 24) { since_try = 0; return std::min(avail, 2); }
+    return best;
+  }
+  void record_draft(int c, int drafted, int accepted) {
+    for (int i = 0; i < 4; i++) { acc[i] = std::max(acc[i] * 0.97, 0.5); fail_[i] = std::max(fail_[i] * 0.97, 0.5); }
+    acc[c] += accepted;
+    if (accepted < drafted) fail_[c] += 1.0;
+  }
+  void record_step(double us) {
+    t1_us = have_t1 ? 0.9 * t1_us + 0.1 * us : us;
+    if (!have_extra) extra_us = 0.3 * t1_us;
+    have_t1 = true;
+  }
+  void record_verify(int b, double us) {
+    if (b < 2 || !have_t1) return;
+    const double m = std::min(std::max((us - t1_us) / (double)(b - 1), 0.0), 1.5 * t1_us);
+    extra_us = have_extra ? 0.85 * extra_us + 0.15 * m : m;
+    have_extra = true;
+  }
+};
+
+constexpr int CORPUS_MAX = 16 * 1024;  // LOOKUP_CORPUS_MAX (:28)
+
+void remember(std::vector<int32_t> &corpus, const int32_t *ids, int n) {
+  corpus.insert(corpus.end(), ids, ids + n);
+  if ((int)corpus.size() > CORPUS_MAX) corpus.erase(corpus.begin(), corpus.begin() + (corpus.size() - CORPUS_MAX / 2));
+}
+
+}  // namespace
+
+extern "C" {
+
+// generate_reply's speculative loop (:4205-4348) without chat framing: greedy decoding of up
+// to max_new tokens after the prompt. Invariant at the top of the loop: `tok` is sampled but
+// not yet in the KV cache; a verify pass feeds [tok, drafts...], the longest matching prefix
+// of drafts is accepted, and the first mismatch (or the bonus token) becomes the next tok.
+int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int max_new, const spx_gen_params *p, int32_t *out,
+                        spx_gen_stats *st) {
+  if (!E || !prompt || !p || !out || !st) return fail("spx_engine_generate: null argument");
+  if (n_prompt < 1 || max_new < 1) return fail("spx_engine_generate: empty prompt or max_new < 1");
+  if (n_prompt + max_new + MAX_M > E->c.max_seq) return fail("spx_engine_generate: prompt + max_new exceeds max_seq");
+  if (p->speculate && (p->draft_len < 1 || p->draft_len > MAX_M - 1)) return fail("spx_engine_generate: draft_len must be in 1..15");
+  memset(st, 0, sizeof(*st));
+  std::vector<int32_t> corpus;
+  remember(corpus, prompt, n_prompt);
+  const int chunk = std::min(MAX_M, p->prefill_chunk > 0 ? p->prefill_chunk : MAX_M);
+  int pos = 0;
+  int32_t am[MAX_M];
+  int64_t t0 = now_us();
+  for (int s = 0; s < n_prompt; s += chunk) {  // feed (:3041-3104)
+    const int cnt = std::min(chunk, n_prompt - s);
+    if (int r = spx_engine_forward(E, prompt + s, cnt, pos, nullptr, nullptr, am)) return r;
+    pos += cnt;
+  }
+  st->prefill_us = (double)(now_us() - t0);
+  const int last_rows = n_prompt - ((n_prompt - 1) / chunk) * chunk;  // rows in the last chunk
+  int tok = am[last_rows - 1];
+  int gen = 0, backoff = 0, skip = 0, k_dyn = p->draft_len;
+  SpecModel sm;
+  sm.fixed = p->fixed != 0;
+  for (;;) {
+    out[gen++] = tok;  // emit!
+    remember(corpus, &tok, 1);
+    if (gen >= max_new) break;
+    const int budget = max_new - gen, k = std::min(k_dyn, budget - 1);
+    int32_t draft[MAX_M];
+    int nd = 0, cls = 3;
+    if (p->speculate && k > 0) {
+      int32_t d[MAX_M];
+      int ng = 0;
+      const int len = spx_lookup_draft(corpus.data(), (int)corpus.size(), std::min(k, MAX_M - 1), nullptr, 0, p->min_ngram, p->max_ngram, d, &ng);
+      if (skip == 0 || ng > 2) { memcpy(draft, d, sizeof(int32_t) * len); nd = len; cls = SpecModel::cls(ng); }
+    }
+    nd = sm.best_len(cls, nd);
+    if (skip > 0) skip--;
+    if (nd == 0) {
+      const int64_t ts = now_us();
+      if (int r = spx_engine_forward(E, &tok, 1, pos, nullptr, nullptr, am)) return r;
+      const double us = (double)(now_us() - ts);
+      pos++;
+      tok = am[0];
+      sm.record_step(us);
+      st->steps++;
+      st->step_us += us;
+      continue;
+    }
+    int32_t batch[MAX_M];
+    batch[0] = tok;
+    memcpy(batch + 1, draft, sizeof(int32_t) * nd);
+    const int start = pos;
+    const int64_t tv = now_us();
+    if (int r = spx_engine_forward(E, batch, nd + 1, start, nullptr, nullptr, am)) return r;
+    const double us = (double)(now_us() - tv);
+    sm.record_verify(nd + 1, us);
+    st->verify_us += us;
+    st->drafted += nd;
+    st->verifies++;
+    int accepted = 0, correction = -1;
+    bool done = false;
+    for (int i = 0; i < nd; i++) {
+      const int s = am[i];
+      if (s != draft[i]) { correction = s; break; }
+      accepted++;
+      out[gen++] = s;
+      remember(corpus, &s, 1);
+      if (gen >= max_new) { done = true; break; }
+    }
+    st->accepted += accepted;
+    sm.record_draft(cls, nd, accepted);
+    pos = start + 1 + accepted;
+    if (done) break;
+    if (accepted == 0) { backoff = std::min(std::max(backoff * 2, 1), 16); skip = backoff; }
+    else backoff = 0;
+    if (p->adaptive_k) k_dyn = accepted == nd ? std::max(std::min(k_dyn + 2, 7), p->draft_len) : p->draft_len;
+    tok = correction >= 0 ? correction : am[nd];
+  }
+  return gen;
+}
+
+int spx_engine_destroy(spx_engine *E) {
+  if (!E) return 0;
+  (void)hipSetDevice(E->ctx->device);
+  (void)hipStreamSynchronize(E->ctx->stream);
+  for (auto &g : E->graph)
+    if (g) (void)hipGraphExecDestroy(g);
+  for (auto &kv : E->mats) spx_tensor_free(E->ctx, kv.second);
+  for (void *p : E->allocs) (void)hipFree(p);
+  if (E->st_host) (void)hipHostFree(E->st_host);
+  delete E;
+  return 0;
+}
+
+}  // extern "C"

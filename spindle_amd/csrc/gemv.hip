@@ -300,8 +300,8 @@ __global__ __launch_bounds__(256) void k_gemv_f(FArgs a) {
           for (int j = 0; j < 4; j++) {
             const int e = 4 * k + j;
             const int byte = (cw[k] >> (8 * j)) & 0xff;
-            q[e] = (float)(((byte & 0xF) | (((qh >> e) & 1) << 4)) - 16);
-            q[e + 16] = (float)(((byte >> 4) | (((qh >> (e + 16)) & 1) << 4)) - 16);
+            q[e] = (float)((int)((byte & 0xF) | (((qh >> e) & 1u) << 4)) - 16);
+            q[e + 16] = (float)((int)((byte >> 4) | (((qh >> (e + 16)) & 1u) << 4)) - 16);
           }
       }
 #pragma unroll

@@ -220,6 +220,7 @@ class Engine:
                                             data.ctypes.data_as(P)))
         check(lib.spx_engine_prepare(h))
         check(lib.spx_engine_set_graphs(h, int(graphs)))
+        ctx.adopt(self)
 
     def forward(self, ids, start_pos, hidden=False, logits=False):
         """One pass; returns (argmax [m], hidden [m, dim] or None, logits [m, vocab] or None)."""
@@ -264,9 +265,9 @@ class Engine:
         return k, v
 
     def close(self):
-        if self.h:
+        if self.h and self.ctx.h:
             lib.spx_engine_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:

@@ -5,6 +5,7 @@ Names follow the reference: `matvec` / `matvec_multi` (smollm_chat.rs:309, 447),
 :255). Device memory comes from torch (cuda == HIP on ROCm); torch is plumbing only.
 """
 import ctypes as C
+import weakref
 
 import numpy as np
 import torch
@@ -25,12 +26,18 @@ class Context:
         h = P()
         check(lib.spx_create(device, C.byref(h)))
         self.h = h
+        self._children = weakref.WeakSet()   # engines / tensors to release before the context
+
+    def adopt(self, obj):
+        self._children.add(obj)
 
     def sync(self):
         check(lib.spx_sync(self.h))
 
     def close(self):
         if self.h:
+            for ch in list(self._children):
+                ch.close()
             lib.spx_destroy(self.h)
             self.h = None
 
@@ -54,6 +61,7 @@ class Tensor:
         check(lib.spx_tensor_upload(ctx.h, dtype, cols, rows, n_expert, data.ctypes.data_as(P), C.byref(h)))
         self.h = h
         self.nbytes = data.size
+        ctx.adopt(self)
 
     def download(self):
         out = np.empty(self.nbytes, np.uint8)
@@ -61,9 +69,11 @@ class Tensor:
         return out
 
     def free(self):
-        if self.h:
+        if self.h and self.ctx.h:
             lib.spx_tensor_free(self.ctx.h, self.h)
-            self.h = None
+        self.h = None
+
+    close = free
 
     def __del__(self):
         try:

@@ -1,0 +1,213 @@
+#!/usr/bin/env python3
+"""Benchmark of the decode / verify hot path on one MI355X (BASELINE.json's metric).
+
+Workload: Qwen3-30B-A3B-shaped Q4_K_M model (random-init, GGUF block layout, ~17 GiB,
+resident in HBM), a 4096-token repeated-span synthetic prompt, then
+  * decode: K greedy one-token passes (M=1) at context ~4.1K -> value = decode tok/s;
+  * verify: greedy generation with prompt-lookup drafts (n-gram 3, k=8, fixed length), M=9
+    verify passes -> verify-pass us, mean accepted tokens per pass, end-to-end tok/s;
+  * kernel profile: HIP events around every launch of a few eager decode passes; the kernel
+    class with the most time is the roofline line (algorithmic bytes per launch / average
+    launch time vs the 8 TB/s HBM peak);
+  * cpu_baseline: the C oracle (the reference's AVX2 arithmetic restated in C, pthreads over
+    rows like the reference's worker pool) decoding a few tokens from the same KV state.
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def spec_prompt(vocab, n, seed):
+    """BASELINE.json config 3's construction at length n: n/2 random tokens, then copied spans
+    of 16..64 tokens from the first half, each token replaced by a random one with p = 0.1."""
+    rng = np.random.default_rng(seed)
+    half = n // 2
+    head = rng.integers(0, vocab, half)
+    tail = []
+    while len(tail) < n - half:
+        ln = int(rng.integers(16, 65))
+        s = int(rng.integers(0, half - 16))
+        for t in head[s:s + ln]:
+            tail.append(int(rng.integers(0, vocab)) if rng.random() < 0.1 else int(t))
+    return np.concatenate([head, np.array(tail[:n - half])]).astype(np.int32)
+
+
+def decode_bytes(cfg, specs, pos, experts_per_layer):
+    """Algorithmic HBM bytes of one decode pass at position pos (weights read once, the
+    experts actually selected, K and V of positions 0..pos)."""
+    from spindle_amd.model import row_bytes
+    by = 0.0
+    for s in specs:
+        b = row_bytes(s.dtype, s.cols) * s.rows
+        if s.name == "token_embd.weight":
+            by += row_bytes(s.dtype, s.cols) if not cfg.tied else b  # one row, or the tied LM head
+        elif "_exps" in s.name:
+            layer = int(s.name.split(".")[1])
+            by += b * experts_per_layer[layer]
+        else:
+            by += b * s.n_expert
+    by += cfg.n_layers * (pos + 1) * cfg.kv_dim * 2 * 2
+    return by
+
+
+def cpu_baseline(cfg, w, eng, tok, pos, seconds, threads):
+    from oracle import ffi
+    from oracle.model import OracleModel
+    ffi.set_threads(threads)
+    om = OracleModel(cfg, w)
+    k, v = eng.kv_cache()
+    om.k_cache[:] = k
+    om.v_cache[:] = v
+    n, t0 = 0, time.perf_counter()
+    while True:
+        h = om.forward([tok], pos + n)
+        tok = om.argmax(om.logits(h)[0])
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 64:
+            break
+    return n / el, n, el
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128, help="timed decode passes")
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", default="qwen3-30b-a3b")
+    ap.add_argument("--prompt-len", type=int, default=4096)
+    ap.add_argument("--spec-tokens", type=int, default=256)
+    ap.add_argument("--profile-passes", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=1)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the whole model fits in one MI355X's HBM and this build "
+              "has no multi-GPU path (see DESIGN.md, 'How the path would shard'). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from spindle_amd import model as M
+    from spindle_amd import ops
+
+    cfg = M.get_config(args.config)
+    need = args.prompt_len + args.warmup + args.steps + args.profile_passes + 32
+    if cfg.max_seq < need:
+        cfg = cfg.replace(max_seq=need)
+    specs = M.tensor_specs(cfg)
+    t0 = time.perf_counter()
+    w = M.synth_model(cfg, args.seed)
+    gib = sum(d.size for _, d in w.values()) / 2**30
+    log(f"synthetic {cfg.name}: {gib:.2f} GiB in {time.perf_counter() - t0:.1f}s")
+    ctx = ops.Context(0)
+    t0 = time.perf_counter()
+    eng = M.Engine(ctx, cfg, w)
+    log(f"uploaded in {time.perf_counter() - t0:.1f}s")
+
+    prompt = spec_prompt(cfg.vocab, args.prompt_len, args.seed)
+    t0 = time.perf_counter()
+    pos = 0
+    for s in range(0, len(prompt), 16):
+        am, _, _ = eng.forward(prompt[s:s + 16], s)
+        pos = s + len(prompt[s:s + 16])
+    prefill_s = time.perf_counter() - t0
+    tok = int(am[-1])
+    log(f"prefill {len(prompt)} tokens in {prefill_s:.2f}s ({len(prompt) / prefill_s:.0f} tok/s, 16-row passes)")
+
+    # warmup, then the timed decode passes (each pass synchronises: the next token is its argmax)
+    out = eng.decode(tok, pos, args.warmup)
+    tok, pos = int(out[-1]), pos + args.warmup
+    ctx.sync()
+    t0 = time.perf_counter()
+    out = eng.decode(tok, pos, args.steps)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+    tok_s = args.steps / dt
+    experts = eng.last_experts()
+    dec_bytes = decode_bytes(cfg, specs, pos + args.steps // 2, experts)
+    log(f"decode: {args.steps} passes in {dt * 1e3:.1f} ms = {tok_s:.1f} tok/s, "
+        f"{dec_bytes / 1e9:.3f} GB/pass -> {dec_bytes * tok_s / 1e9:.0f} GB/s end to end")
+    tok, pos = int(out[-1]), pos + args.steps
+
+    # per-kernel profile of eager decode passes (HIP events on the engine's stream)
+    eng.profile(True)
+    out = eng.decode(tok, pos, args.profile_passes)
+    eng.profile(False)
+    prof = eng.profile_read()
+    tok, pos = int(out[-1]), pos + args.profile_passes
+    tot = sum(v[1] for v in prof.values())
+    for name, (n, us, by) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        if n:
+            log(f"  {name:22s} {n:6d} launches {us / args.profile_passes:9.1f} us/pass ({100 * us / tot:4.1f}%)"
+                + (f"  {by / us / 1e3:8.1f} GB/s" if by > 0 else ""))
+    dom = max((k for k in prof if prof[k][2] > 0), key=lambda k: prof[k][1])
+    n, us, by = prof[dom]
+    achieved = by / us / 1e3
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+            "bytes_per_launch": round(by / n), "avg_launch_us": round(us / n, 3)}
+
+    # verify: prompt-lookup speculation, benchmark mode (n-gram 3, k = 8, fixed length)
+    toks, st = eng.generate(prompt, args.spec_tokens, draft_len=8, min_ngram=3, max_ngram=3, fixed=True,
+                            adaptive_k=False, prefill_chunk=16)
+    ver_us = st["verify_us"] / max(1, st["verifies"])
+    acc = st["accepted"] / max(1, st["verifies"])
+    spec_tok_s = len(toks) / ((st["verify_us"] + st["step_us"]) / 1e6)
+    log(f"verify: {st['verifies']} passes of M<=9, {ver_us:.0f} us/pass, {acc:.2f} accepted/pass, "
+        f"{st['steps']} plain steps, {spec_tok_s:.1f} tok/s end to end")
+    # one M=9 pass timed alone (fixed draft of 8 copied tokens)
+    ids = prompt[100:109]
+    for _ in range(3):
+        eng.forward(ids, 1000)
+    t0 = time.perf_counter()
+    for _ in range(10):
+        eng.forward(ids, 1000)
+    m9_us = (time.perf_counter() - t0) / 10 * 1e6
+    ver_experts = eng.last_experts()
+    ver_bytes = decode_bytes(cfg, specs, 1008, ver_experts)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = min(args.cpu_threads, os.cpu_count() or 1)
+        cpu_tok_s, n_cpu, el = cpu_baseline(cfg, w, eng, tok, pos, args.cpu_seconds, threads)
+        log(f"cpu baseline (oracle, {threads} threads): {n_cpu} tokens in {el:.1f}s = {cpu_tok_s:.3f} tok/s")
+        cpu = {"value": round(cpu_tok_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"{n_cpu} greedy decode passes at positions {pos}..{pos + n_cpu - 1} from the GPU's KV cache "
+                         f"(same weights, C restatement of the reference's AVX2 kernels, {threads} threads)"}
+
+    res = {
+        "metric": "decode tok/s (Qwen3-30B-A3B Q4_K_M-shaped, 1 GPU); k=8 verify-pass us; HBM GB/s",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(1e3 / tok_s, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "i8 dot (int32) + f32", "data": "synthetic (random-init weights, seed %d)" % args.seed,
+        "config": {"workload": f"{cfg.name} greedy decode, M=1, context {args.prompt_len}+ of {cfg.max_seq}",
+                   "prompt_tokens": args.prompt_len, "weights_gib": round(gib, 2)},
+        "decode_gb_per_pass": round(dec_bytes / 1e9, 4), "decode_hbm_gbs": round(dec_bytes * tok_s / 1e9, 1),
+        "decode_roofline_frac": round(dec_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+        "verify_pass_us": round(ver_us, 1), "verify_m9_pass_us": round(m9_us, 1),
+        "verify_gb_per_pass": round(ver_bytes / 1e9, 4), "verify_unique_experts_per_layer": round(float(np.mean(ver_experts)), 1),
+        "accepted_per_pass": round(acc, 3), "spec_tok_s": round(spec_tok_s, 2), "prefill_tok_s": round(len(prompt) / prefill_s, 1),
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    eng.close()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -114,6 +114,17 @@ int spx_engine_set_graphs(spx_engine *e, int on);
  * (after output_norm), logits [m][vocab], argmax [m]. Synchronous. */
 int spx_engine_forward(spx_engine *e, const int32_t *ids, int m, int start_pos, float *hidden,
                        float *logits, int32_t *argmax);
+/* Greedy decoding of n tokens, one pass each (step_token :3106-3132 + the greedy pick):
+ * feeds `token` at start_pos, then each pass's argmax at the next position; out[i] is the
+ * token chosen by pass i. */
+int spx_engine_decode(spx_engine *e, int32_t token, int start_pos, int n, int32_t *out);
+/* Kernel timing: while on, passes run eagerly with a HIP event pair on the engine's stream
+ * around every launch; totals per kernel class accumulate until the next spx_engine_profile(e,1).
+ * bytes = algorithmic bytes (weights of the experts actually selected; KV for attention).
+ * No reference counterpart (the reference keeps StepTiming per phase, smollm_chat.rs:1811-1858). */
+int spx_engine_profile(spx_engine *e, int on);
+int spx_engine_profile_read(spx_engine *e, int cls, const char **name, int64_t *launches,
+                            double *total_us, double *bytes);
 /* Number of distinct experts each MoE layer ran in the last pass (0 for dense layers). */
 int spx_engine_last_experts(spx_engine *e, int32_t *njobs_per_layer);
 /* Per layer and expert: passes that selected the expert since prepare ([n_layers][n_expert]). */

@@ -21,6 +21,15 @@ using namespace spx;
 
 namespace {
 
+// kernel classes of the profile (spx_engine_profile_read)
+enum {
+  PC_EMBED, PC_NORM, PC_QKV, PC_QKROPE, PC_ATTN, PC_QUANT, PC_WO, PC_FFN_DENSE, PC_ROUTER, PC_ROUTE,
+  PC_MOE_GATEUP, PC_SWIGLU, PC_MOE_DOWN, PC_COMBINE, PC_LMHEAD, PC_ARGMAX, PROF_NCLS
+};
+const char *PROF_NAMES[PROF_NCLS] = {"embed", "residual_rmsnorm_q8k", "attn_qkv_matvec", "qk_norm_rope_kv", "attention",
+                                     "q8k_quantize", "attn_output_matvec", "dense_ffn_matvec", "router_matvec", "moe_route",
+                                     "moe_gate_up_grouped", "swiglu_q8k", "moe_down_grouped", "moe_combine", "lm_head_matvec", "argmax"};
+
 struct Q8Buf {
   float *d = nullptr;
   int8_t *q = nullptr;
@@ -70,6 +79,14 @@ struct spx_engine {
   Job *jobs_gu = nullptr, *jobs_dn = nullptr;
   hipGraphExec_t graph[MAX_M + 1] = {};
   int n_used = 0;
+  // kernel-class timing (eager passes only): event pairs recorded around each launch
+  struct ProfRec { int cls, layer; double bytes; bool per_expert; hipEvent_t a, b; };
+  bool profiling = false;
+  std::vector<ProfRec> prof;
+  std::vector<hipEvent_t> ev_pool;
+  size_t ev_next = 0;
+  double prof_us[PROF_NCLS] = {}, prof_bytes[PROF_NCLS] = {};
+  int64_t prof_n[PROF_NCLS] = {};
 
   template <class T>
   T *dalloc(size_t n) {
@@ -82,6 +99,29 @@ struct spx_engine {
 };
 
 namespace {
+
+// ---------------------------------------------------------------- profiling
+struct ProfScope {
+  spx_engine *E;
+  int idx = -1;
+  ProfScope(spx_engine *e, int cls, double bytes, int layer = -1, bool per_expert = false) : E(e) {
+    if (!E->profiling) return;
+    if (E->ev_next + 2 > E->ev_pool.size()) {
+      for (int i = 0; i < 256; i++) { hipEvent_t ev; if (hipEventCreate(&ev) == hipSuccess) E->ev_pool.push_back(ev); }
+    }
+    if (E->ev_next + 2 > E->ev_pool.size()) return;
+    spx_engine::ProfRec r{cls, layer, bytes, per_expert, E->ev_pool[E->ev_next], E->ev_pool[E->ev_next + 1]};
+    E->ev_next += 2;
+    (void)hipEventRecord(r.a, E->ctx->stream);
+    E->prof.push_back(r);
+    idx = (int)E->prof.size() - 1;
+  }
+  ~ProfScope() {
+    if (idx >= 0) (void)hipEventRecord(E->prof[idx].b, E->ctx->stream);
+  }
+};
+
+double wbytes(const spx_tensor *t) { return (double)row_bytes(t->v.dtype, t->v.cols) * (double)t->v.rows; }
 
 // ---------------------------------------------------------------- matrix launches
 int gemv(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld_x, const Q8Buf *xq, float *out, int64_t ld_out,
@@ -107,76 +147,79 @@ int enqueue_forward(spx_engine *E, int m) {
   const auto &c = E->c;
   hipStream_t s = E->ctx->stream;
   const int dim = c.dim, hd = c.head_dim;
-  SPX_HIP(launch_embed(E->embed->v, E->st_dev, E->x, dim, c.embedding_scale, m, s));
+  { ProfScope ps(E, PC_EMBED, 0); SPX_HIP(launch_embed(E->embed->v, E->st_dev, E->x, dim, c.embedding_scale, m, s)); }
   const float *pending = nullptr;  // residual to add before the next norm
   for (int l = 0; l < c.n_layers; l++) {
     const LayerW &ly = E->L[l];
     const bool q_int = is_kq(ly.wq) || is_kq(ly.wk) || is_kq(ly.wv);
-    SPX_HIP(launch_res_norm(E->x, dim, pending, dim, c.residual_scale, ly.attn_norm, dim, c.rms_eps, E->xn, dim,
-                            q_int ? E->xq.d : nullptr, q_int ? E->xq.q : nullptr, q_int ? E->xq.b : nullptr, E->st_dev, m, s));
-    if (int r = gemv(E, ly.wq, m, E->xn, dim, &E->xq, E->q, E->q_dim)) return r;
-    if (int r = gemv(E, ly.wk, m, E->xn, dim, &E->xq, E->k, E->kv_dim)) return r;
-    if (int r = gemv(E, ly.wv, m, E->xn, dim, &E->xq, E->v, E->kv_dim)) return r;
+    { ProfScope ps(E, PC_NORM, 0);
+      SPX_HIP(launch_res_norm(E->x, dim, pending, dim, c.residual_scale, ly.attn_norm, dim, c.rms_eps, E->xn, dim,
+                              q_int ? E->xq.d : nullptr, q_int ? E->xq.q : nullptr, q_int ? E->xq.b : nullptr, E->st_dev, m, s)); }
+    { ProfScope ps(E, PC_QKV, wbytes(ly.wq)); if (int r = gemv(E, ly.wq, m, E->xn, dim, &E->xq, E->q, E->q_dim)) return r; }
+    { ProfScope ps(E, PC_QKV, wbytes(ly.wk)); if (int r = gemv(E, ly.wk, m, E->xn, dim, &E->xq, E->k, E->kv_dim)) return r; }
+    { ProfScope ps(E, PC_QKV, wbytes(ly.wv)); if (int r = gemv(E, ly.wv, m, E->xn, dim, &E->xq, E->v, E->kv_dim)) return r; }
     QKArgs qa{};
     qa.q = E->q; qa.k = E->k; qa.v = E->v; qa.ld_q = E->q_dim; qa.ld_kv = E->kv_dim;
     qa.q_bias = ly.q_bias; qa.k_bias = ly.k_bias; qa.v_bias = ly.v_bias; qa.q_norm = ly.q_norm; qa.k_norm = ly.k_norm;
     qa.rope = E->rope; qa.k_cache = E->kc; qa.v_cache = E->vc; qa.layer = l; qa.max_seq = c.max_seq; qa.kv_dim = E->kv_dim;
     qa.head_dim = hd; qa.n_heads = c.n_heads; qa.n_kv = c.n_kv_heads; qa.neox = c.rope_neox; qa.eps = c.rms_eps;
-    SPX_HIP(launch_qk_rope_kv(qa, E->st_dev, m, s));
+    { ProfScope ps(E, PC_QKROPE, 0); SPX_HIP(launch_qk_rope_kv(qa, E->st_dev, m, s)); }
     AttnArgs aa{};
     aa.q = E->q; aa.ld_q = E->q_dim; aa.k_cache = E->kc; aa.v_cache = E->vc; aa.part_m = E->part_m; aa.part_l = E->part_l;
     aa.part_o = E->part_o; aa.out = E->att; aa.ld_out = E->q_dim; aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim;
     aa.head_dim = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads; aa.max_chunks = E->max_chunks;
     aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
-    SPX_HIP(launch_attention(aa, E->st_dev, m, s));
-    if (is_kq(ly.wo)) SPX_HIP(launch_q8k_quantize(E->att, E->q_dim, E->q_dim, m, E->aq.d, E->aq.q, E->aq.b, s));
-    if (int r = gemv(E, ly.wo, m, E->att, E->q_dim, &E->aq, E->proj, dim)) return r;
+    { ProfScope ps(E, PC_ATTN, -1.0 - l); SPX_HIP(launch_attention(aa, E->st_dev, m, s)); }
+    if (is_kq(ly.wo)) { ProfScope ps(E, PC_QUANT, 0); SPX_HIP(launch_q8k_quantize(E->att, E->q_dim, E->q_dim, m, E->aq.d, E->aq.q, E->aq.b, s)); }
+    { ProfScope ps(E, PC_WO, wbytes(ly.wo)); if (int r = gemv(E, ly.wo, m, E->att, E->q_dim, &E->aq, E->proj, dim)) return r; }
     const bool f_int = is_kq(ly.gate) || is_kq(ly.up);
-    SPX_HIP(launch_res_norm(E->x, dim, E->proj, dim, c.residual_scale, ly.ffn_norm, dim, c.rms_eps, E->xn, dim,
-                            f_int ? E->xq.d : nullptr, f_int ? E->xq.q : nullptr, f_int ? E->xq.b : nullptr, E->st_dev, m, s));
+    { ProfScope ps(E, PC_NORM, 0);
+      SPX_HIP(launch_res_norm(E->x, dim, E->proj, dim, c.residual_scale, ly.ffn_norm, dim, c.rms_eps, E->xn, dim,
+                              f_int ? E->xq.d : nullptr, f_int ? E->xq.q : nullptr, f_int ? E->xq.b : nullptr, E->st_dev, m, s)); }
     const int nff = (int)ly.gate->v.rows;
     const bool d_int = is_kq(ly.down);
     if (!ly.moe) {  // ffn_forward / ffn_forward_multi (:590-646)
-      if (int r = gemv(E, ly.gate, m, E->xn, dim, &E->xq, E->h, nff)) return r;
-      if (int r = gemv(E, ly.up, m, E->xn, dim, &E->xq, E->u, nff)) return r;
+      { ProfScope ps(E, PC_FFN_DENSE, wbytes(ly.gate)); if (int r = gemv(E, ly.gate, m, E->xn, dim, &E->xq, E->h, nff)) return r; }
+      { ProfScope ps(E, PC_FFN_DENSE, wbytes(ly.up)); if (int r = gemv(E, ly.up, m, E->xn, dim, &E->xq, E->u, nff)) return r; }
       SwigluArgs sa{};
       sa.g = E->h; sa.u = E->u; sa.ld = nff; sa.n = nff;
       if (d_int) { sa.qd = E->hq.d; sa.qq = E->hq.q; sa.qb = E->hq.b; }
-      SPX_HIP(launch_swiglu(sa, E->st_dev, m, s));
-      if (int r = gemv(E, ly.down, m, E->h, nff, &E->hq, E->proj, dim)) return r;
+      { ProfScope ps(E, PC_SWIGLU, 0); SPX_HIP(launch_swiglu(sa, E->st_dev, m, s)); }
+      { ProfScope ps(E, PC_FFN_DENSE, wbytes(ly.down)); if (int r = gemv(E, ly.down, m, E->h, nff, &E->hq, E->proj, dim)) return r; }
     } else {  // moe_forward / moe_forward_batch (:925-1392)
       const int nu = c.n_expert_used, ne = c.n_expert;
-      if (int r = gemv(E, ly.router, m, E->xn, dim, nullptr, E->rlog, ne)) return r;
+      { ProfScope ps(E, PC_ROUTER, wbytes(ly.router)); if (int r = gemv(E, ly.router, m, E->xn, dim, nullptr, E->rlog, ne)) return r; }
       RouteArgs ra{};
       ra.logits = E->rlog; ra.ld_logits = ne; ra.n_expert = ne; ra.n_used = nu; ra.norm = c.expert_norm; ra.moe_prune = c.moe_prune;
       ra.chosen = E->chosen; ra.weights = E->weights; ra.nkeep = E->nkeep; ra.jobs_gu = E->jobs_gu; ra.jobs_dn = E->jobs_dn;
       ra.njobs = ly.njobs; ra.expert_count = E->expert_count + (size_t)l * ne;
-      SPX_HIP(launch_moe_route(ra, E->st_dev, s));
+      { ProfScope ps(E, PC_ROUTE, 0); SPX_HIP(launch_moe_route(ra, E->st_dev, s)); }
       const int max_jobs = std::min(ne, m * nu);
-      if (int r = gemv(E, ly.gate, m, E->xn, dim, &E->xq, E->h, nff, E->jobs_gu, ly.njobs, max_jobs)) return r;
-      if (int r = gemv(E, ly.up, m, E->xn, dim, &E->xq, E->u, nff, E->jobs_gu, ly.njobs, max_jobs)) return r;
+      { ProfScope ps(E, PC_MOE_GATEUP, wbytes(ly.gate), l, true); if (int r = gemv(E, ly.gate, m, E->xn, dim, &E->xq, E->h, nff, E->jobs_gu, ly.njobs, max_jobs)) return r; }
+      { ProfScope ps(E, PC_MOE_GATEUP, wbytes(ly.up), l, true); if (int r = gemv(E, ly.up, m, E->xn, dim, &E->xq, E->u, nff, E->jobs_gu, ly.njobs, max_jobs)) return r; }
       SwigluArgs sa{};
       sa.g = E->h; sa.u = E->u; sa.ld = nff; sa.n = nff; sa.jobs = E->jobs_gu; sa.njobs = ly.njobs;
       if (d_int) { sa.qd = E->hq.d; sa.qq = E->hq.q; sa.qb = E->hq.b; }
-      SPX_HIP(launch_swiglu(sa, E->st_dev, m * nu, s));
-      if (int r = gemv(E, ly.down, m, E->h, nff, &E->hq, E->y, dim, E->jobs_dn, ly.njobs, max_jobs)) return r;
+      { ProfScope ps(E, PC_SWIGLU, 0); SPX_HIP(launch_swiglu(sa, E->st_dev, m * nu, s)); }
+      { ProfScope ps(E, PC_MOE_DOWN, wbytes(ly.down), l, true); if (int r = gemv(E, ly.down, m, E->h, nff, &E->hq, E->y, dim, E->jobs_dn, ly.njobs, max_jobs)) return r; }
       CombineArgs ca{};
       ca.y = E->y; ca.ld_y = dim; ca.weights = E->weights; ca.nkeep = E->nkeep; ca.n_used = nu; ca.dim = dim; ca.out = E->proj; ca.ld_out = dim;
-      SPX_HIP(launch_moe_combine(ca, E->st_dev, m, s));
+      { ProfScope ps(E, PC_COMBINE, 0); SPX_HIP(launch_moe_combine(ca, E->st_dev, m, s)); }
     }
     pending = E->proj;
   }
   const bool h_int = is_kq(E->lm_head);
-  SPX_HIP(launch_res_norm(E->x, dim, pending, dim, c.residual_scale, E->out_norm, dim, c.rms_eps, E->xn, dim,
-                          h_int ? E->xq.d : nullptr, h_int ? E->xq.q : nullptr, h_int ? E->xq.b : nullptr, E->st_dev, m, s));
-  if (int r = gemv(E, E->lm_head, m, E->xn, dim, &E->xq, E->logits, c.vocab)) return r;
-  SPX_HIP(launch_argmax(E->logits, c.vocab, c.vocab, c.logit_scale, E->amax, E->st_dev, m, s));
+  { ProfScope ps(E, PC_NORM, 0);
+    SPX_HIP(launch_res_norm(E->x, dim, pending, dim, c.residual_scale, E->out_norm, dim, c.rms_eps, E->xn, dim,
+                            h_int ? E->xq.d : nullptr, h_int ? E->xq.q : nullptr, h_int ? E->xq.b : nullptr, E->st_dev, m, s)); }
+  { ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head)); if (int r = gemv(E, E->lm_head, m, E->xn, dim, &E->xq, E->logits, c.vocab)) return r; }
+  { ProfScope ps(E, PC_ARGMAX, 0); SPX_HIP(launch_argmax(E->logits, c.vocab, c.vocab, c.logit_scale, E->amax, E->st_dev, m, s)); }
   return 0;
 }
 
 int run_forward(spx_engine *E, int m) {
   hipStream_t s = E->ctx->stream;
-  if (!E->use_graphs) return enqueue_forward(E, m);
+  if (!E->use_graphs || E->profiling) return enqueue_forward(E, m);
   if (!E->graph[m]) {
     SPX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     int r = enqueue_forward(E, m);
@@ -386,6 +429,52 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
   if (logits) SPX_HIP(hipMemcpyAsync(logits, E->logits, sizeof(float) * m * E->c.vocab, hipMemcpyDeviceToHost, s));
   if (argmax) SPX_HIP(hipMemcpyAsync(argmax, E->amax, sizeof(int) * m, hipMemcpyDeviceToHost, s));
   SPX_HIP(hipStreamSynchronize(s));
+  if (E->profiling && !E->prof.empty()) {
+    std::vector<int32_t> nj(E->c.n_layers, 0);
+    for (int l = 0; l < E->c.n_layers; l++)
+      if (E->L[l].moe) SPX_HIP(hipMemcpy(&nj[l], E->L[l].njobs, sizeof(int), hipMemcpyDeviceToHost));
+    const int64_t kv_pos_bytes = (int64_t)E->kv_dim * 2 * 2;  // K and V, f16
+    for (auto &r : E->prof) {
+      float ms = 0.0f;
+      SPX_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+      double bytes = r.bytes;
+      if (r.per_expert) bytes = r.bytes / E->c.n_expert * nj[r.layer];
+      if (r.cls == PC_ATTN) bytes = (double)kv_pos_bytes * (start_pos + m);  // KV bytes read once per pass
+      E->prof_us[r.cls] += 1000.0 * ms;
+      E->prof_bytes[r.cls] += bytes;
+      E->prof_n[r.cls] += 1;
+    }
+    E->prof.clear();
+    E->ev_next = 0;
+  }
+  return 0;
+}
+
+int spx_engine_profile(spx_engine *E, int on) {
+  if (!E) return fail("null engine");
+  E->profiling = on != 0;
+  if (on) { for (int i = 0; i < PROF_NCLS; i++) { E->prof_us[i] = 0; E->prof_bytes[i] = 0; E->prof_n[i] = 0; } }
+  return 0;
+}
+
+int spx_engine_profile_read(spx_engine *E, int cls, const char **name, int64_t *launches, double *total_us, double *bytes) {
+  if (!E || cls < 0 || cls >= PROF_NCLS) return fail("spx_engine_profile_read: bad class");
+  if (name) *name = PROF_NAMES[cls];
+  if (launches) *launches = E->prof_n[cls];
+  if (total_us) *total_us = E->prof_us[cls];
+  if (bytes) *bytes = E->prof_bytes[cls];
+  return 0;
+}
+
+int spx_engine_decode(spx_engine *E, int32_t token, int start_pos, int n, int32_t *out) {
+  if (!E || !out || n < 0) return fail("spx_engine_decode: bad argument");
+  int32_t tok = token;
+  for (int i = 0; i < n; i++) {  // step_token (:3106-3132) + greedy sample, one token per pass
+    int32_t am = 0;
+    if (int r = spx_engine_forward(E, &tok, 1, start_pos + i, nullptr, nullptr, &am)) return r;
+    out[i] = am;
+    tok = am;
+  }
   return 0;
 }
 
@@ -588,6 +677,7 @@ int spx_engine_destroy(spx_engine *E) {
   (void)hipStreamSynchronize(E->ctx->stream);
   for (auto &g : E->graph)
     if (g) (void)hipGraphExecDestroy(g);
+  for (auto ev : E->ev_pool) (void)hipEventDestroy(ev);
   for (auto &kv : E->mats) spx_tensor_free(E->ctx, kv.second);
   for (void *p : E->allocs) (void)hipFree(p);
   if (E->st_host) (void)hipHostFree(E->st_host);

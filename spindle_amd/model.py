@@ -252,6 +252,28 @@ class Engine:
             check(n)
         return out[:n], {k: getattr(st, k) for k, _ in GenStats._fields_}
 
+    def decode(self, token, start_pos, n):
+        """n greedy one-token passes starting with `token` at start_pos; returns the n picks."""
+        out = np.empty(n, np.int32)
+        check(lib.spx_engine_decode(self.h, int(token), start_pos, n, out.ctypes.data_as(P)))
+        return out
+
+    def profile(self, on):
+        check(lib.spx_engine_profile(self.h, int(on)))
+
+    def profile_read(self):
+        """{kernel class: (launches, total_us, algorithmic bytes)} accumulated while profiling."""
+        res = {}
+        for cls in range(64):
+            name = C.c_char_p()
+            n = C.c_int64()
+            us = C.c_double()
+            by = C.c_double()
+            if lib.spx_engine_profile_read(self.h, cls, C.byref(name), C.byref(n), C.byref(us), C.byref(by)) != 0:
+                break
+            res[name.value.decode()] = (n.value, us.value, by.value)
+        return res
+
     def last_experts(self):
         out = np.empty(self.cfg.n_layers, np.int32)
         check(lib.spx_engine_last_experts(self.h, out.ctypes.data_as(P)))

@@ -55,7 +55,8 @@ class Layer(C.Structure):
 class Model(C.Structure):
     _fields_ = [("c", Config), ("layers", C.POINTER(Layer)), ("embed", Mat), ("lm_head", Mat),
                 ("output_norm", P), ("k_cache", P), ("v_cache", P), ("inv_freq", P),
-                ("last_chosen", C.c_int * (16 * 32))]
+                ("last_chosen", C.c_int * (16 * 32)),
+                ("dbg_q", P), ("dbg_att", P), ("dbg_proj", P), ("dbg_ffn", P)]
 
 
 class SpecModel(C.Structure):

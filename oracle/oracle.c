@@ -763,6 +763,7 @@ int or_forward_slice(or_model *m, int token, int pos, float *hidden) {
     qkv_post(m, ly, l, pos, q, k, v);
     attention(m, l, pos, q, ao);
     or_matvec(&ly->wo, ao, proj);
+    if (m->dbg_q) { memcpy(m->dbg_q, q, 4 * q_dim); memcpy(m->dbg_att, ao, 4 * q_dim); memcpy(m->dbg_proj, proj, 4 * dim); }
     for (int i = 0; i < dim; i++) x[i] += c->residual_scale * proj[i];
     or_rmsnorm(x, ly->ffn_norm, xn, dim, c->rms_eps);
     if (ly->is_moe) {
@@ -773,6 +774,7 @@ int or_forward_slice(or_model *m, int token, int pos, float *hidden) {
       memset(proj, 0, 4 * dim);
       or_ffns_fused(&ly->gate, &ly->up, &ly->down, 1, &e0, &w1, xn, proj);
     }
+    if (m->dbg_ffn) memcpy(m->dbg_ffn, proj, 4 * dim);
     for (int i = 0; i < dim; i++) x[i] += c->residual_scale * proj[i];
   }
   or_rmsnorm(x, m->output_norm, hidden, dim, c->rms_eps);

@@ -125,6 +125,9 @@ typedef struct {
   float *inv_freq;             /* head_dim/2, filled by or_model_init */
   /* statistics of the last MoE layer evaluation (tests) */
   int last_chosen[16 * 32];
+  /* optional debug capture (tests): forward_slice copies the last layer's q (after RoPE),
+   * attention output, attention projection and FFN output here when non-null */
+  float *dbg_q, *dbg_att, *dbg_proj, *dbg_ffn;
 } or_model;
 
 void or_model_init(or_model *m);

@@ -57,6 +57,7 @@ struct KQArgs {
   const Job *jobs;      // grouped launch: job per blockIdx.y
   const int *njobs;
   int32_t *dbg;         // block-sums probe: [nb][2] for (row r0, vector 0)
+  int passes;           // row passes per workgroup (set by the launcher)
 };
 
 // Arguments of the fp32-activation matrix-vector kernels.

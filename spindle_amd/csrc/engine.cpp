@@ -247,6 +247,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   if (c.head_dim <= 0 || c.head_dim > 128 || c.head_dim % 8) return fail("spx_engine_create: head_dim must be a multiple of 8, at most 128");
   if (16 * (c.n_heads / c.n_kv_heads) > 4096) return fail("spx_engine_create: too many query heads per kv head");
   if (c.n_layers <= 0 || c.vocab <= 0 || c.max_seq <= 0) return fail("spx_engine_create: bad layer count, vocab or max_seq");
+  if (c.max_seq > MAX_CHUNKS * ATT_CHUNK) return fail("spx_engine_create: max_seq above " + std::to_string(MAX_CHUNKS * ATT_CHUNK));
   if (c.n_expert < 0 || c.n_expert > 256 || c.n_expert_used < 0 || c.n_expert_used > 32 || (c.n_expert && !c.n_expert_used))
     return fail("spx_engine_create: unsupported expert counts (n_expert <= 256, n_expert_used in 1..32)");
   spx_engine *E = new spx_engine();
@@ -438,7 +439,7 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
       float ms = 0.0f;
       SPX_HIP(hipEventElapsedTime(&ms, r.a, r.b));
       double bytes = r.bytes;
-      if (r.per_expert) bytes = r.bytes / E->c.n_expert * nj[r.layer];
+      if (r.per_expert) bytes = r.bytes * nj[r.layer];  // wbytes() is one expert's slab
       if (r.cls == PC_ATTN) bytes = (double)kv_pos_bytes * (start_pos + m);  // KV bytes read once per pass
       E->prof_us[r.cls] += 1000.0 * ms;
       E->prof_bytes[r.cls] += bytes;
@@ -475,6 +476,19 @@ int spx_engine_decode(spx_engine *E, int32_t token, int start_pos, int n, int32_
     out[i] = am;
     tok = am;
   }
+  return 0;
+}
+
+int spx_engine_debug_read(spx_engine *E, const char *what, void *host, int64_t bytes) {
+  if (!E || !what || !host) return fail("null argument");
+  const std::string w(what);
+  const void *src = w == "x" ? (const void *)E->x : w == "xn" ? (const void *)E->xn : w == "q" ? (const void *)E->q
+                  : w == "att" ? (const void *)E->att : w == "proj" ? (const void *)E->proj : w == "rlog" ? (const void *)E->rlog
+                  : w == "chosen" ? (const void *)E->chosen : w == "weights" ? (const void *)E->weights
+                  : w == "nkeep" ? (const void *)E->nkeep : w == "h" ? (const void *)E->h : w == "y" ? (const void *)E->y : nullptr;
+  if (!src) return fail("spx_engine_debug_read: unknown buffer " + w);
+  SPX_HIP(hipStreamSynchronize(E->ctx->stream));
+  SPX_HIP(hipMemcpy(host, src, (size_t)bytes, hipMemcpyDeviceToHost));
   return 0;
 }
 

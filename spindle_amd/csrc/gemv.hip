@@ -5,15 +5,13 @@
 //     S_i = sum_e scale(e) * w_e * y_e            (Q4_K: 6-bit scale per 32, codes 0..15;
 //                                                  Q6_K: int8 scale per 16, codes 0..63)
 //     s_i = Q4_K: sum_j min_j * (bsum_2j + bsum_2j+1);  Q6_K: 32 * sum_g scale_g * bsum_g
-//   with v_dot4_i32_i8 (codes are non-negative, so the signed dot is exact), then
-//     acc = fma(d*xd_i, float(S_i), acc)            (one chain over blocks, block order)
-//     corr = corr + (dmin*xd_i) * float(s_i)        (Q6_K: (d*xd_i) * float(32 s); the
-//                                                    reference's own expression, :204/:232)
-//     out = acc - corr
-//   S_i and s_i equal the reference's per-block integers bit for bit; the fp32 result
-//   differs from the reference's eight-lane accumulation (:243-247) only in rounding. The
-//   same per-vector code runs for every batch size, so a vector's result is bitwise
-//   independent of the batch it is in (the property quant_q8k.rs:413-442 tests).
+//   with v_dot4_i32_i8 (codes are non-negative, so the signed dot is exact), split exactly
+//   like the reference's 8 x int32 lanes of sumi (element e in lane (e % 32) / 4), then the
+//   reference's fp32 epilogue: eight chains acc_l = fma(d*xd_i, float(P_il), acc_l) in block
+//   order, corr = corr + (dmin*xd_i) * float(s_i) (Q6_K: (d*xd_i) * float(32 s)), and
+//   out = hsum(acc) - corr with the tree of quant_q8k.rs:151-158. Given the same Q8_K input
+//   the output is bit-identical to the reference's rows<B,T>, for every batch size (the
+//   property quant_q8k.rs:413-442 tests).
 //
 // Float path (Q8_0, Q5_0, F32 weights x fp32 activations), restating quant.rs:48-161 and
 // quant_multi.rs:168-190: per block s = sum q_e * x_e, acc = fma(d, s, acc); the reduction
@@ -24,6 +22,8 @@
 // [32c, 32c+32) of a Q4_K block (scale groups 2c, 2c+1) or the (half c>>1, l-range c&1) slice
 // of a Q6_K block; the quad sums its four int32 partials with DPP quad permutes (exact).
 // Float path: lane c owns blocks c, c+4, c+8, ... of the row.
+#include <algorithm>
+
 #include "common.h"
 
 namespace spx {
@@ -38,6 +38,13 @@ struct VecSet {
 };
 
 // ---------------------------------------------------------------- Q4_K block decode
+// The activation slice a lane needs for one block: four 16-byte pieces of Q8_K codes and the
+// bsums its sub-blocks use.
+struct YSlice {
+  uint4 y[4];
+  int bs[4];
+};
+
 struct Q4KBlock {
   uint32_t lo[8], hi[8];
   int sc0, sc1, mn0, mn1;
@@ -68,24 +75,30 @@ struct Q4KBlock {
       mn1 = ((S2 >> (8 * k1 + 4)) & 0xF) | (((S1 >> (8 * k1 + 6)) & 3) << 4);
     }
   }
-  // y: this vector's 256 codes of the block; bs: its 16 bsums. Returns the lane partials.
-  __device__ __forceinline__ void dot(const int8_t *y, const int16_t *bs, int c, int &p, int &s) const {
+  // y: the vector's 256 codes of this block; bs: its 16 bsums. Lane c: codes [64c, 64c+64).
+  static __device__ __forceinline__ void load_y(const int8_t *y, const int16_t *bs, int c, YSlice &ys) {
     const uint4 *yl = reinterpret_cast<const uint4 *>(y + c * 64);
-    const uint4 a0 = yl[0], a1 = yl[1], b0 = yl[2], b1 = yl[3];
-    const int ya[8] = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-    const int yb[8] = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-    int slo = 0, shi = 0;
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-      slo = sdot4((int)lo[t], ya[t], slo);
-      shi = sdot4((int)hi[t], yb[t], shi);
-    }
-    p = sc0 * slo + sc1 * shi;
+    ys.y[0] = yl[0]; ys.y[1] = yl[1]; ys.y[2] = yl[2]; ys.y[3] = yl[3];
     const int2 bb = *reinterpret_cast<const int2 *>(bs + 4 * c);
-    const int b0s = (int)(int16_t)(bb.x & 0xffff), b1s = (int)(int16_t)(bb.x >> 16);
-    const int b2s = (int)(int16_t)(bb.y & 0xffff), b3s = (int)(int16_t)(bb.y >> 16);
-    s = mn0 * (b0s + b1s) + mn1 * (b2s + b3s);
+    ys.bs[0] = (int)(int16_t)(bb.x & 0xffff); ys.bs[1] = (int)(int16_t)(bb.x >> 16);
+    ys.bs[2] = (int)(int16_t)(bb.y & 0xffff); ys.bs[3] = (int)(int16_t)(bb.y >> 16);
   }
+  // Lane c's contribution to the eight 32-bit lanes of the reference's sumi (element e goes to
+  // lane (e % 32) / 4): dword t of this lane's codes holds elements 64c + 4t.. (low nibbles, scale
+  // 2c) and 64c + 32 + 4t.. (high nibbles, scale 2c+1), both in lane t.
+  __device__ __forceinline__ void dot8(const YSlice &ys, int c, int P[8], int &s) const {
+    const int ya[8] = {(int)ys.y[0].x, (int)ys.y[0].y, (int)ys.y[0].z, (int)ys.y[0].w, (int)ys.y[1].x, (int)ys.y[1].y, (int)ys.y[1].z, (int)ys.y[1].w};
+    const int yb[8] = {(int)ys.y[2].x, (int)ys.y[2].y, (int)ys.y[2].z, (int)ys.y[2].w, (int)ys.y[3].x, (int)ys.y[3].y, (int)ys.y[3].z, (int)ys.y[3].w};
+#pragma unroll
+    for (int t = 0; t < 8; t++) P[t] = sc0 * sdot4((int)lo[t], ya[t], 0) + sc1 * sdot4((int)hi[t], yb[t], 0);
+    s = mn0 * (ys.bs[0] + ys.bs[1]) + mn1 * (ys.bs[2] + ys.bs[3]);
+  }
+  __device__ __forceinline__ void dot(const YSlice &ys, int c, int &p, int &s) const {
+    int P[8];
+    dot8(ys, c, P, s);
+    p = ((P[0] + P[1]) + (P[2] + P[3])) + ((P[4] + P[5]) + (P[6] + P[7]));
+  }
+  __device__ __forceinline__ float dm() const { return dmin; }
 };
 
 // ---------------------------------------------------------------- Q6_K block decode
@@ -115,21 +128,41 @@ struct Q6KBlock {
     sc[2] = (int)(int8_t)(w1 >> (8 * half));
     sc[3] = (int)(int8_t)(w1 >> (8 * (2 + half)));
   }
-  __device__ __forceinline__ void dot(const int8_t *y, const int16_t *bs, int c, int &p, int &s) const {
+  // Lane c = (h, half): codes 128h + 32m + 16half + [0, 16) for m = 0..3, bsums 8h + 2m + half.
+  static __device__ __forceinline__ void load_y(const int8_t *y, const int16_t *bs, int c, YSlice &ys) {
     const int h = c >> 1, half = c & 1;
-    p = 0;
+#pragma unroll
+    for (int m = 0; m < 4; m++) ys.y[m] = *reinterpret_cast<const uint4 *>(y + 128 * h + 32 * m + 16 * half);
+    const int4 bb = *reinterpret_cast<const int4 *>(bs + 8 * h);  // bsums 8h .. 8h+7
+    const int w[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+    for (int m = 0; m < 4; m++) ys.bs[m] = (int)(int16_t)((w[m] >> (16 * half)) & 0xffff);
+  }
+  // Lane c = (h, half) holds elements 128h + 32m + 16half + 4t.. for m = 0..3: reference lane
+  // 4*half + t (scale per 16 elements, so one scale per (m, half)).
+  __device__ __forceinline__ void dot8(const YSlice &ys, int c, int P[8], int &s) const {
+    const int half = c & 1;
+    int L[4];
+    const uint32_t *yw[4] = {&ys.y[0].x, &ys.y[1].x, &ys.y[2].x, &ys.y[3].x};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      int acc = 0;
+#pragma unroll
+      for (int m = 0; m < 4; m++) acc += sc[m] * sdot4((int)q[m][t], (int)yw[m][t], 0);
+      L[t] = acc;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) { P[t] = half ? 0 : L[t]; P[4 + t] = half ? L[t] : 0; }
     s = 0;
 #pragma unroll
-    for (int m = 0; m < 4; m++) {
-      const uint4 yv = *reinterpret_cast<const uint4 *>(y + 128 * h + 32 * m + 16 * half);
-      int t = sdot4((int)q[m][0], (int)yv.x, 0);
-      t = sdot4((int)q[m][1], (int)yv.y, t);
-      t = sdot4((int)q[m][2], (int)yv.z, t);
-      t = sdot4((int)q[m][3], (int)yv.w, t);
-      p += sc[m] * t;
-      s += sc[m] * (int)bs[8 * h + 2 * m + half];
-    }
+    for (int m = 0; m < 4; m++) s += sc[m] * ys.bs[m];
   }
+  __device__ __forceinline__ void dot(const YSlice &ys, int c, int &p, int &s) const {
+    int P[8];
+    dot8(ys, c, P, s);
+    p = ((P[0] + P[1]) + (P[2] + P[3])) + ((P[4] + P[5]) + (P[6] + P[7]));
+  }
+  __device__ __forceinline__ float dm() const { return d; }
 };
 
 template <int T>
@@ -137,21 +170,27 @@ struct KQBlock;
 template <> struct KQBlock<T_Q4K> { using type = Q4KBlock; };
 template <> struct KQBlock<T_Q6K> { using type = Q6KBlock; };
 
-// Accumulates one block's exact integers into the fp32 chain (quant_q8k.rs:204/:232/:243).
+// The fp32 epilogue of rows<B,T> (quant_q8k.rs:204/:232/:243-247), bit for bit: eight lane
+// accumulators acc_l = fma(d*xd, float(P_l), acc_l) over the blocks in order, the correction
+// chain corr = corr + (dmin*xd)*float(s) (Q6_K: (d*xd)*float(32 s)), and out =
+// hsum(acc) - corr with the tree ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) of quant_q8k.rs:151-158.
 template <int T>
-__device__ __forceinline__ void kq_accum(const typename KQBlock<T>::type &B, float xdv, int p, int s, float &acc, float &corr) {
-  if (T == T_Q4K) {
-    const Q4KBlock &b = reinterpret_cast<const Q4KBlock &>(B);
-    acc = fmaf(b.d * xdv, (float)p, acc);
-    corr = corr + (b.dmin * xdv) * (float)s;
-  } else {
-    const Q6KBlock &b = reinterpret_cast<const Q6KBlock &>(B);
-    acc = fmaf(b.d * xdv, (float)p, acc);
-    corr = corr + (b.d * xdv) * (float)(32 * s);
-  }
+__device__ __forceinline__ void kq_accum8(float d, float dm, float xdv, const int *P, int s, float acc[8], float &corr) {
+  if (T == T_Q4K) corr = corr + (dm * xdv) * (float)s;
+  else corr = corr + (dm * xdv) * (float)(32 * s);
+  const float dd = d * xdv;
+#pragma unroll
+  for (int l = 0; l < 8; l++) acc[l] = fmaf(dd, (float)P[l], acc[l]);
+}
+__device__ __forceinline__ float hsum8(const float a[8]) {
+  const float x0 = a[0] + a[4], x1 = a[1] + a[5], x2 = a[2] + a[6], x3 = a[3] + a[7];
+  return (x0 + x2) + (x1 + x3);
 }
 
-template <int T, int MT, bool GROUPED>
+// Block-parallel integer matvec. A pass covers R = (64/nb)*RR rows: quad q takes block q%nb of
+// row group q/nb (RR rows), forms the exact int32 partials for every vector and leaves them in
+// LDS; then one thread per (row, vector) runs the fp32 chain over the blocks in order.
+template <int T, int MT, int RR, bool GROUPED>
 __global__ __launch_bounds__(256) void k_gemv_kq(KQArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   VecSet<MT> vs;
@@ -169,46 +208,74 @@ __global__ __launch_bounds__(256) void k_gemv_kq(KQArgs a) {
 #pragma unroll
     for (int v = 0; v < MT; v++) { vs.src[v] = v; vs.dst[v] = v; }
   }
-  const int64_t cols = a.w.cols, nb = a.w.nb;
-  // LDS holds the job's Q8_K vectors: codes, then scales, then bsums (16-byte aligned parts).
-  const int64_t mcap = GROUPED ? MT : a.m;
-  int8_t *sy = reinterpret_cast<int8_t *>(smem);
-  float *sd = reinterpret_cast<float *>(smem + mcap * cols);
-  int16_t *sb = reinterpret_cast<int16_t *>(smem + mcap * cols + ((mcap * nb * 4 + 15) & ~(int64_t)15));
-  for (int v = 0; v < vs.m; v++) {
-    const int64_t src = vs.src[v];
-    const uint4 *s4 = reinterpret_cast<const uint4 *>(a.xq + src * cols);
-    uint4 *d4 = reinterpret_cast<uint4 *>(sy + v * cols);
-    for (int i = threadIdx.x; i < cols / 16; i += 256) d4[i] = s4[i];
-    for (int i = threadIdx.x; i < nb; i += 256) sd[v * nb + i] = a.xd[src * nb + i];
-    for (int i = threadIdx.x; i < nb * 16; i += 256) sb[v * nb * 16 + i] = a.xb[src * nb * 16 + i];
-  }
-  __syncthreads();
+  const int nb = (int)a.w.nb, cols = (int)a.w.cols;
+  const int gpp = 64 / nb, R = gpp * RR;            // row groups and rows per pass
+  int *sP = reinterpret_cast<int *>(smem);          // [R][nb][MT][8] lane partials
+  int *sS = sP + R * nb * MT * 8;                    // [R][nb][MT]
+  float *sD = reinterpret_cast<float *>(sS + R * nb * MT);  // [R][nb]
+  float *sM = sD + R * nb;                           // [R][nb]
   const int quad = threadIdx.x >> 2, c = threadIdx.x & 3;
-  const int64_t r = a.r0 + (int64_t)blockIdx.x * 64 + quad;
-  if (r >= a.r1) return;
-  const int64_t g0 = ((int64_t)expert * a.w.rows + r) * nb;
-  float acc[MT], corr[MT];
+  const int grp = quad / nb, blk = quad % nb;
+  const bool active = grp < gpp;
+  const int64_t rows_per_wg = (int64_t)R * a.passes;
+  const int64_t wg_r0 = a.r0 + (int64_t)blockIdx.x * rows_per_wg;
+  for (int pass = 0; pass < a.passes; pass++) {
+    const int64_t pr0 = wg_r0 + (int64_t)pass * R;
+    if (pr0 >= a.r1) break;
+    if (active) {
+      typename KQBlock<T>::type B[RR];
+      bool ok[RR];
 #pragma unroll
-  for (int v = 0; v < MT; v++) { acc[v] = 0.0f; corr[v] = 0.0f; }
-  typename KQBlock<T>::type B;
-  for (int64_t i = 0; i < nb; i++) {
-    B.load(a.w.pl, g0 + i, c);
+      for (int rr = 0; rr < RR; rr++) {
+        const int64_t row = pr0 + grp * RR + rr;
+        ok[rr] = row < a.r1;
+        if (ok[rr]) B[rr].load(a.w.pl, ((int64_t)expert * a.w.rows + row) * nb + blk, c);
+      }
 #pragma unroll
-    for (int v = 0; v < MT; v++) {
-      if (v < vs.m) {
-        int p, s;
-        B.dot(sy + v * cols + i * 256, sb + (v * nb + i) * 16, c, p, s);
-        p = quad_sum(p);
-        s = quad_sum(s);
-        kq_accum<T>(B, sd[v * nb + i], p, s, acc[v], corr[v]);
+      for (int v = 0; v < MT; v++) {
+        if (v < vs.m) {
+          YSlice ys;
+          KQBlock<T>::type::load_y(a.xq + (int64_t)vs.src[v] * cols + blk * 256, a.xb + ((int64_t)vs.src[v] * nb + blk) * 16, c, ys);
+#pragma unroll
+          for (int rr = 0; rr < RR; rr++) {
+            int P[8] = {0, 0, 0, 0, 0, 0, 0, 0}, s = 0;
+            if (ok[rr]) B[rr].dot8(ys, c, P, s);
+#pragma unroll
+            for (int l = 0; l < 8; l++) P[l] = quad_sum(P[l]);
+            s = quad_sum(s);
+            if (c == 0) {
+              const int o = ((grp * RR + rr) * nb + blk) * MT + v;
+              int4 *pp = reinterpret_cast<int4 *>(sP + 8 * o);
+              pp[0] = make_int4(P[0], P[1], P[2], P[3]);
+              pp[1] = make_int4(P[4], P[5], P[6], P[7]);
+              sS[o] = s;
+            }
+          }
+        }
+      }
+      if (c == 0) {
+#pragma unroll
+        for (int rr = 0; rr < RR; rr++) {
+          sD[(grp * RR + rr) * nb + blk] = ok[rr] ? B[rr].d : 0.0f;
+          sM[(grp * RR + rr) * nb + blk] = ok[rr] ? B[rr].dm() : 0.0f;
+        }
       }
     }
-  }
-  if (c == 0) {
-#pragma unroll
-    for (int v = 0; v < MT; v++)
-      if (v < vs.m) a.out[(int64_t)vs.dst[v] * a.ld_out + r] = acc[v] - corr[v];
+    __syncthreads();
+    for (int t = threadIdx.x; t < R * vs.m; t += 256) {
+      const int r = t / vs.m, v = t % vs.m;
+      const int64_t row = pr0 + r;
+      if (row < a.r1) {
+        const float *xd = a.xd + (int64_t)vs.src[v] * nb;
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, corr = 0.0f;
+        for (int i = 0; i < nb; i++) {
+          const int o = (r * nb + i) * MT + v;
+          kq_accum8<T>(sD[r * nb + i], sM[r * nb + i], xd[i], sP + 8 * o, sS[o], acc, corr);
+        }
+        a.out[(int64_t)vs.dst[v] * a.ld_out + row] = hsum8(acc) - corr;
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -221,8 +288,10 @@ __global__ __launch_bounds__(64) void k_kq_block_sums(KQArgs a) {
   const int64_t g = ((int64_t)a.expert * a.w.rows + a.r0) * a.w.nb + i;
   typename KQBlock<T>::type B;
   B.load(a.w.pl, g, c);
+  YSlice ys;
+  KQBlock<T>::type::load_y(a.xq + i * 256, a.xb + i * 16, c, ys);
   int p, s;
-  B.dot(a.xq + i * 256, a.xb + i * 16, c, p, s);
+  B.dot(ys, c, p, s);
   p = quad_sum(p);
   s = quad_sum(s);
   if (c == 0) { a.dbg[2 * i] = p; a.dbg[2 * i + 1] = T == T_Q6K ? 32 * s : s; }
@@ -338,26 +407,40 @@ __global__ __launch_bounds__(256) void k_gemv_f(FArgs a) {
 // ---------------------------------------------------------------- launchers
 static inline int mt_bucket(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
 
+static int kq_rr(int mt) { return mt <= 1 ? 1 : mt <= 4 ? 2 : 4; }
+
 size_t kq_smem_bytes(const TensorView &w, int mt) {
-  return (size_t)mt * w.cols + (((size_t)mt * w.nb * 4 + 15) & ~(size_t)15) + (size_t)mt * w.nb * 32;
+  const int nb = (int)w.nb, R = (64 / nb) * kq_rr(mt);
+  return (size_t)R * nb * (9 * mt * 4 + 8);
+}
+
+template <int T, int MT, bool G>
+static hipError_t launch_kq_mt(KQArgs a, int grid_y, hipStream_t st) {
+  constexpr int RR = MT <= 1 ? 1 : MT <= 4 ? 2 : 4;
+  const int nb = (int)a.w.nb, R = (64 / nb) * RR;
+  const int64_t rows = a.r1 - a.r0, groups = (rows + R - 1) / R;
+  // enough passes per workgroup to amortise its set-up, while keeping >= ~2048 workgroups
+  const int64_t per_y = std::max<int64_t>(1, 2048 / std::max(1, grid_y));
+  a.passes = (int)std::max<int64_t>(1, std::min<int64_t>(16, groups / per_y));
+  dim3 grid((unsigned)((groups + a.passes - 1) / a.passes), (unsigned)grid_y);
+  const size_t sm = (size_t)R * nb * (9 * MT * 4 + 8);
+  hipLaunchKernelGGL((k_gemv_kq<T, MT, RR, G>), grid, dim3(256), sm, st, a);
+  return hipGetLastError();
 }
 
 template <int T, bool G>
 static hipError_t launch_kq_t(const KQArgs &a, int mt, int grid_y, hipStream_t st) {
-  const int64_t rows = a.r1 - a.r0;
-  dim3 grid((unsigned)((rows + 63) / 64), (unsigned)grid_y);
-  const size_t sm = kq_smem_bytes(a.w, G ? mt : a.m);
   switch (mt) {
-  case 1: hipLaunchKernelGGL((k_gemv_kq<T, 1, G>), grid, dim3(256), sm, st, a); break;
-  case 2: hipLaunchKernelGGL((k_gemv_kq<T, 2, G>), grid, dim3(256), sm, st, a); break;
-  case 4: hipLaunchKernelGGL((k_gemv_kq<T, 4, G>), grid, dim3(256), sm, st, a); break;
-  case 8: hipLaunchKernelGGL((k_gemv_kq<T, 8, G>), grid, dim3(256), sm, st, a); break;
-  default: hipLaunchKernelGGL((k_gemv_kq<T, 16, G>), grid, dim3(256), sm, st, a); break;
+  case 1: return launch_kq_mt<T, 1, G>(a, grid_y, st);
+  case 2: return launch_kq_mt<T, 2, G>(a, grid_y, st);
+  case 4: return launch_kq_mt<T, 4, G>(a, grid_y, st);
+  case 8: return launch_kq_mt<T, 8, G>(a, grid_y, st);
+  default: return launch_kq_mt<T, 16, G>(a, grid_y, st);
   }
-  return hipGetLastError();
 }
 
 hipError_t launch_gemv_kq(const KQArgs &a, int mt, bool grouped, int grid_y, hipStream_t st) {
+  if (a.w.nb > 64) return hipErrorInvalidValue;
   mt = mt_bucket(mt);
   if (a.w.dtype == T_Q4K) return grouped ? launch_kq_t<T_Q4K, true>(a, mt, grid_y, st) : launch_kq_t<T_Q4K, false>(a, mt, 1, st);
   return grouped ? launch_kq_t<T_Q6K, true>(a, mt, grid_y, st) : launch_kq_t<T_Q6K, false>(a, mt, 1, st);
@@ -367,6 +450,69 @@ hipError_t launch_kq_block_sums(const KQArgs &a, hipStream_t st) {
   dim3 grid((unsigned)((a.w.nb + 15) / 16));
   if (a.w.dtype == T_Q4K) hipLaunchKernelGGL((k_kq_block_sums<T_Q4K>), grid, dim3(64), 0, st, a);
   else hipLaunchKernelGGL((k_kq_block_sums<T_Q6K>), grid, dim3(64), 0, st, a);
+  return hipGetLastError();
+}
+
+// F32 weights (MoE routers): one wavefront per row, lane l takes float4 chunks l, l+64, ...;
+// the lane partials are reduced with a fixed butterfly and lane 0's sum is written, so the
+// order is the same for every batch size (matvec_multi runs F32 per vector, :455-464).
+template <int MT, bool GROUPED>
+__global__ __launch_bounds__(256) void k_gemv_f32(FArgs a) {
+  VecSet<MT> vs;
+  int expert;
+  if (GROUPED) {
+    if ((int)blockIdx.y >= *a.njobs) return;
+    const Job &J = a.jobs[blockIdx.y];
+    expert = J.expert;
+    vs.m = J.nvec;
+#pragma unroll
+    for (int v = 0; v < MT; v++) { vs.src[v] = v < J.nvec ? J.vec[v] : 0; vs.dst[v] = v < J.nvec ? J.out[v] : 0; }
+  } else {
+    expert = a.expert;
+    vs.m = a.m;
+#pragma unroll
+    for (int v = 0; v < MT; v++) { vs.src[v] = v; vs.dst[v] = v; }
+  }
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t r = a.r0 + (int64_t)blockIdx.x * 4 + wv;
+  if (r >= a.r1) return;
+  const float4 *wr = reinterpret_cast<const float4 *>(a.w.pl.p0 + ((int64_t)expert * a.w.rows + r) * a.w.cols * 4);
+  const int64_t n4 = a.w.cols / 4;
+  float part[MT][4];
+#pragma unroll
+  for (int v = 0; v < MT; v++) part[v][0] = part[v][1] = part[v][2] = part[v][3] = 0.0f;
+  for (int64_t k = lane; k < n4; k += 64) {
+    const float4 w = wr[k];
+#pragma unroll
+    for (int v = 0; v < MT; v++) {
+      if (v < vs.m) {
+        const float4 xv = reinterpret_cast<const float4 *>(a.x + (int64_t)vs.src[v] * a.ld_x)[k];
+        part[v][0] = fmaf(w.x, xv.x, part[v][0]);
+        part[v][1] = fmaf(w.y, xv.y, part[v][1]);
+        part[v][2] = fmaf(w.z, xv.z, part[v][2]);
+        part[v][3] = fmaf(w.w, xv.w, part[v][3]);
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < MT; v++) {
+    float t = (part[v][0] + part[v][1]) + (part[v][2] + part[v][3]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+    if (lane == 0 && v < vs.m) a.out[(int64_t)vs.dst[v] * a.ld_out + r] = t;
+  }
+}
+
+template <bool G>
+static hipError_t launch_f32(const FArgs &a, int mt, int grid_y, hipStream_t st) {
+  dim3 grid((unsigned)((a.r1 - a.r0 + 3) / 4), (unsigned)grid_y);
+  switch (mt) {
+  case 1: hipLaunchKernelGGL((k_gemv_f32<1, G>), grid, dim3(256), 0, st, a); break;
+  case 2: hipLaunchKernelGGL((k_gemv_f32<2, G>), grid, dim3(256), 0, st, a); break;
+  case 4: hipLaunchKernelGGL((k_gemv_f32<4, G>), grid, dim3(256), 0, st, a); break;
+  case 8: hipLaunchKernelGGL((k_gemv_f32<8, G>), grid, dim3(256), 0, st, a); break;
+  default: hipLaunchKernelGGL((k_gemv_f32<16, G>), grid, dim3(256), 0, st, a); break;
+  }
   return hipGetLastError();
 }
 
@@ -390,7 +536,7 @@ hipError_t launch_gemv_f(const FArgs &a, int mt, bool grouped, int grid_y, hipSt
   switch (a.w.dtype) {
   case T_Q8_0: return grouped ? launch_f_t<T_Q8_0, true>(a, mt, gy, st) : launch_f_t<T_Q8_0, false>(a, mt, gy, st);
   case T_Q5_0: return grouped ? launch_f_t<T_Q5_0, true>(a, mt, gy, st) : launch_f_t<T_Q5_0, false>(a, mt, gy, st);
-  case T_F32: return grouped ? launch_f_t<T_F32, true>(a, mt, gy, st) : launch_f_t<T_F32, false>(a, mt, gy, st);
+  case T_F32: return grouped ? launch_f32<true>(a, mt, gy, st) : launch_f32<false>(a, mt, gy, st);
   default: return hipErrorInvalidValue;
   }
 }

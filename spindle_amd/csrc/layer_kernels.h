@@ -7,6 +7,7 @@ namespace spx {
 constexpr int ATT_CHUNK = 64;  // positions per attention workgroup (one per lane)
 constexpr int ATT_QG = 16;     // query vectors per pass inside an attention workgroup
 constexpr int MAX_M = 16;      // rows per verify / prefill pass
+constexpr int MAX_CHUNKS = 512; // attention chunks: max_seq <= MAX_CHUNKS * ATT_CHUNK
 
 // Device-side step record: the token rows of this pass and where they go in the KV cache.
 struct StepRec {

@@ -205,22 +205,25 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs a, const Step
   if (t0 > last) return;
   const int hd = a.head_dim, g = a.n_heads / a.n_kv, nq = m * g;
   const int tn = min(ATT_CHUNK, last + 1 - t0);
-  const int kst = hd + 2;                       // padded K row (halves): conflict-free columns
+  const int kst = hd + 2;                       // padded K row (halves): 65-dword stride, conflict-free
   __shared__ __align__(16) __half ks[ATT_CHUNK * (128 + 2)];
   __shared__ __align__(16) __half vs[ATT_CHUNK * 128];
   __shared__ __align__(16) float qs[ATT_QG * 128];
   __shared__ float ps[ATT_QG * ATT_CHUNK];
   const int64_t base = (int64_t)a.layer * a.max_seq * a.kv_dim + kvh * hd;
-  for (int i = threadIdx.x; i < ATT_CHUNK * hd; i += 256) {
-    const int t = i / hd, dd = i % hd;
-    __half kv = __float2half(0.0f), vv = __float2half(0.0f);
+  const int n8 = hd / 8;                        // 16-byte pieces per K/V row
+#pragma unroll 4
+  for (int i = threadIdx.x; i < ATT_CHUNK * n8; i += 256) {
+    const int t = i / n8, j = i % n8;
+    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
     if (t < tn) {
-      const int64_t off = base + (int64_t)(t0 + t) * a.kv_dim + dd;
-      kv = a.k_cache[off];
-      vv = a.v_cache[off];
+      const int64_t off = base + (int64_t)(t0 + t) * a.kv_dim + 8 * j;
+      kv = *reinterpret_cast<const uint4 *>(a.k_cache + off);
+      vv = *reinterpret_cast<const uint4 *>(a.v_cache + off);
     }
-    ks[t * kst + dd] = kv;
-    vs[t * hd + dd] = vv;
+    uint32_t *kd = reinterpret_cast<uint32_t *>(ks + t * kst + 8 * j);
+    kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
+    *reinterpret_cast<uint4 *>(vs + t * hd + 8 * j) = vv;
   }
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int q0 = 0; q0 < nq; q0 += ATT_QG) {
@@ -277,20 +280,27 @@ __global__ __launch_bounds__(128) void k_attn_merge(const AttnArgs a, const Step
   const int b = qi / g, h = kvh * g + qi % g, hd = a.head_dim;
   const int nch = (st->start + b) / ATT_CHUNK + 1;  // chunks row b sees
   const int64_t row = (int64_t)(kvh * (16 * g)) + qi;
+  __shared__ float wsm[MAX_CHUNKS];
+  __shared__ float red[2];
+  // chunk weights exp(m_c - max) and the normaliser, computed once
   float mx = -INFINITY;
-  for (int c = 0; c < nch; c++) mx = fmaxf(mx, a.part_m[row * a.max_chunks + c]);
-  float l = 0.0f;
-  for (int c = 0; c < nch; c++) {
+  for (int c = threadIdx.x; c < nch; c += 128) mx = fmaxf(mx, a.part_m[row * a.max_chunks + c]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(red[0], red[1]);
+  for (int c = threadIdx.x; c < nch; c += 128) {
     const float mc = a.part_m[row * a.max_chunks + c];
-    if (mc != -INFINITY) l += a.part_l[row * a.max_chunks + c] * expf(mc - mx);
+    wsm[c] = mc == -INFINITY ? 0.0f : expf(mc - mx);
   }
+  __syncthreads();
+  float l = 0.0f;
+  for (int c = 0; c < nch; c++) l = fmaf(a.part_l[row * a.max_chunks + c], wsm[c], l);
   const float invl = __fdiv_rn(1.0f, fmaxf(l, 1e-9f));
   for (int dd = threadIdx.x; dd < hd; dd += 128) {
     float acc = 0.0f;
-    for (int c = 0; c < nch; c++) {
-      const float mc = a.part_m[row * a.max_chunks + c];
-      if (mc != -INFINITY) acc = fmaf(a.part_o[(row * a.max_chunks + c) * hd + dd], expf(mc - mx), acc);
-    }
+    for (int c = 0; c < nch; c++) acc = fmaf(a.part_o[(row * a.max_chunks + c) * hd + dd], wsm[c], acc);
     a.out[b * a.ld_out + h * hd + dd] = acc * invl;
   }
 }
@@ -298,7 +308,7 @@ __global__ __launch_bounds__(128) void k_attn_merge(const AttnArgs a, const Step
 // ------------------------------------------------------------------ MoE routing
 // Router softmax, top-n_used by probability (ties: lower expert index), pruning and weight
 // normalisation (:1199-1239, :959-997), then the grouped job lists over the union of chosen
-// experts in first-seen order (:982-986, :648-700). One workgroup.
+// experts (:982-986, :648-700). One workgroup.
 __global__ __launch_bounds__(256) void k_moe_route(const RouteArgs a, const StepRec *st) {
   __shared__ float probs[16][256];
   __shared__ int chosen[16][32];

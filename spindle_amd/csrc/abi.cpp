@@ -6,6 +6,7 @@
 #include <thread>
 
 #include "../../include/spx.h"
+#include "fused.h"
 #include "internal.h"
 
 namespace spx {
@@ -69,15 +70,41 @@ static int block_bytes(int dtype) {
   switch (dtype) { case T_Q4K: return 144; case T_Q6K: return 210; case T_Q8_0: return 34; case T_Q5_0: return 22; default: return 0; }
 }
 
+// Byte order inside one plane record: device position of GGUF byte b of the field, so that
+// the eight lanes of a row group each load one contiguous piece (16 B of codes):
+//   Q4_K codes  qs[32c + 4l + j]        -> 16l + 4c + j      (lane l: dword c, c = 0..3)
+//   Q6_K ql     ql[64h + 32mm + 4l + j] -> 16l + 8h + 4mm + j
+//   Q6_K qh     qh[32h + 4l + j]        -> 8l + 4h + j
+// Every other field keeps the GGUF order.
+static int perm_of(int dtype, int plane, int b) {
+  if (dtype == T_Q4K && plane == 0) { const int c = b >> 5, l = (b >> 2) & 7, j = b & 3; return 16 * l + 4 * c + j; }
+  if (dtype == T_Q6K && plane == 0) { const int h = b >> 6, mm = (b >> 5) & 1, l = (b >> 2) & 7, j = b & 3; return 16 * l + 8 * h + 4 * mm + j; }
+  if (dtype == T_Q6K && plane == 1) { const int h = b >> 5, l = (b >> 2) & 7, j = b & 3; return 8 * l + 4 * h + j; }
+  return b;
+}
+
 // GGUF <-> planar, over block range [g0, g1).
 static void relayout(int dtype, const uint8_t *ggml, uint8_t *planar, const size_t *poff, int64_t g0, int64_t g1, bool to_planar) {
   Field f[4];
   const int nf = fields_of(dtype, f), bb = block_bytes(dtype);
+  int perm[4][128];
+  bool permuted[4] = {false, false, false, false};
+  for (int k = 0; k < nf; k++)
+    for (int b = 0; b < f[k].len && b < 128; b++) {
+      perm[k][b] = perm_of(dtype, f[k].plane, b);
+      permuted[k] |= perm[k][b] != b;
+    }
   for (int64_t g = g0; g < g1; g++)
     for (int k = 0; k < nf; k++) {
       uint8_t *p = planar + poff[f[k].plane] + (size_t)g * f[k].len;
-      const uint8_t *q = ggml + (size_t)g * bb + f[k].off;
-      if (to_planar) memcpy(p, q, f[k].len); else memcpy(const_cast<uint8_t *>(q), p, f[k].len);
+      uint8_t *q = const_cast<uint8_t *>(ggml) + (size_t)g * bb + f[k].off;
+      if (!permuted[k]) {
+        if (to_planar) memcpy(p, q, f[k].len); else memcpy(q, p, f[k].len);
+      } else if (to_planar) {
+        for (int b = 0; b < f[k].len; b++) p[perm[k][b]] = q[b];
+      } else {
+        for (int b = 0; b < f[k].len; b++) q[b] = p[perm[k][b]];
+      }
     }
 }
 
@@ -155,7 +182,7 @@ int spx_tensor_upload(spx_ctx *ctx, int dtype, int64_t cols, int64_t rows, int n
     const int nf = fields_of(dtype, f);
     for (int k = 0; k < nf; k++) {
       t->plane_off[f[k].plane] = bytes;
-      bytes += ((size_t)nblk * f[k].len + 255) & ~(size_t)255;
+      bytes += (((size_t)nblk * f[k].len + 255) & ~(size_t)255) + 256;  // slack: 16-byte loads may run past a plane's end
     }
   }
   hipError_t e = hipMalloc(&t->dev, std::max<size_t>(bytes, 256));
@@ -218,26 +245,61 @@ static int check_kq(const spx_tensor *w, int expert, int m) {
   return 0;
 }
 
+// Workspace image of m permuted Q8_K vectors of n columns.
+static Q8KP ws_q8kp(spx_ctx *ctx, int m, int64_t n, bool *ok) {
+  const int64_t nb = n / 256;
+  const size_t qb = ((size_t)m * n + 255) & ~(size_t)255, db = ((size_t)m * nb * 4 + 255) & ~(size_t)255;
+  uint8_t *w = static_cast<uint8_t *>(ws_get(ctx, qb + db + (size_t)m * nb * 64));
+  Q8KP r{};
+  *ok = w != nullptr;
+  if (!w) return r;
+  r.q = reinterpret_cast<uint32_t *>(w);
+  r.d = reinterpret_cast<float *>(w + qb);
+  r.bs = reinterpret_cast<int2 *>(w + qb + db);
+  return r;
+}
+
+static int mv_launch(spx_ctx *ctx, const spx_tensor *w, int expert, int m, const float *x, int64_t ld_x, Q8KP y, float *out,
+                     int64_t ld_out, int64_t r0, int64_t r1) {
+  MVArgs a{};
+  a.seg[0].w = w->v;
+  a.seg[0].out = out;
+  a.seg[0].ld_out = ld_out;
+  a.seg[0].r0 = r0;
+  a.seg[0].r1 = r1;
+  a.seg[0].expert = expert;
+  a.seg[0].wgs = mv_wgs(r1 - r0, m, false, w->v.dtype);
+  a.nseg = 1;
+  a.x = x;
+  a.ld_x = ld_x;
+  a.y = y;
+  a.m = m;
+  SPX_HIP(launch_mv(a, m, false, nullptr, a.seg[0].wgs, ctx->stream));
+  return 0;
+}
+
 int spx_matmul_rows_q8k(spx_ctx *ctx, const spx_tensor *w, int expert, const float *xd, const int8_t *xs, const int16_t *xb, int m, float *out, int64_t ld_out, int64_t r0, int64_t r1) {
   if (!ctx || !xd || !xs || !xb || !out) return fail("spx_matmul_rows_q8k: null argument");
   if (int r = check_kq(w, expert, m)) return r;
   if (r0 < 0 || r1 > w->v.rows || r0 > r1) return fail("spx_matmul_rows_q8k: bad row range");
   if (m > 1 && ld_out < r1) return fail("spx_matmul_rows_q8k: ld_out smaller than the row range");
   if (r1 == r0) return 0;
-  KQArgs a{};
-  a.w = w->v; a.xd = xd; a.xq = xs; a.xb = xb; a.out = out; a.ld_out = ld_out; a.r0 = r0; a.r1 = r1;
-  a.expert = expert; a.m = m;
-  SPX_HIP(launch_gemv_kq(a, m, false, 1, ctx->stream));
-  return 0;
+  bool ok = false;
+  Q8KP y = ws_q8kp(ctx, m, w->v.cols, &ok);
+  if (!ok) return fail("spx_matmul_rows_q8k: workspace allocation failed");
+  SPX_HIP(launch_q8kp_from_ref(xd, xs, xb, w->v.cols, m, y, ctx->stream));
+  return mv_launch(ctx, w, expert, m, nullptr, 0, y, out, ld_out, r0, r1);
 }
 
 int spx_block_sums_q8k(spx_ctx *ctx, const spx_tensor *w, int expert, int64_t row, const int8_t *xs, const int16_t *xb, int32_t *sums) {
   if (!ctx || !xs || !xb || !sums) return fail("spx_block_sums_q8k: null argument");
   if (int r = check_kq(w, expert, 1)) return r;
   if (row < 0 || row >= w->v.rows) return fail("spx_block_sums_q8k: row out of range");
-  KQArgs a{};
-  a.w = w->v; a.xq = xs; a.xb = xb; a.r0 = row; a.r1 = row + 1; a.expert = expert; a.m = 1; a.dbg = sums;
-  SPX_HIP(launch_kq_block_sums(a, ctx->stream));
+  bool ok = false;
+  Q8KP y = ws_q8kp(ctx, 1, w->v.cols, &ok);
+  if (!ok) return fail("spx_block_sums_q8k: workspace allocation failed");
+  SPX_HIP(launch_q8kp_from_ref(nullptr, xs, xb, w->v.cols, 1, y, ctx->stream));
+  SPX_HIP(launch_kq_block_sums(w->v, expert, row, y, sums, ctx->stream));
   return 0;
 }
 
@@ -249,26 +311,15 @@ int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, in
   if (ld_x < cols || (m > 1 && ld_out < rows)) return fail("spx_matvec: leading dimension too small");
   if (ld_x % 4) return fail("spx_matvec: ld_x must be a multiple of 4 (16-byte rows)");
   if (w->v.dtype == T_Q4K || w->v.dtype == T_Q6K) {
-    const int64_t nb = w->v.nb;
-    const size_t need = (size_t)m * (cols + nb * 4 + nb * 32) + 256;
-    uint8_t *wsp = static_cast<uint8_t *>(ws_get(ctx, need));
-    if (!wsp) return fail("spx_matvec: workspace allocation failed");
-    int8_t *qs = reinterpret_cast<int8_t *>(wsp);
-    float *d = reinterpret_cast<float *>(wsp + (((size_t)m * cols + 15) & ~(size_t)15));
-    int16_t *bs = reinterpret_cast<int16_t *>(reinterpret_cast<uint8_t *>(d) + (((size_t)m * nb * 4 + 15) & ~(size_t)15));
-    SPX_HIP(launch_q8k_quantize(x, cols, ld_x, m, d, qs, bs, ctx->stream));
-    KQArgs a{};
-    a.w = w->v; a.xd = d; a.xq = qs; a.xb = bs; a.out = out; a.ld_out = ld_out; a.r0 = 0; a.r1 = rows;
-    a.expert = expert; a.m = m;
-    SPX_HIP(launch_gemv_kq(a, m, false, 1, ctx->stream));
-    return 0;
+    bool ok = false;
+    Q8KP y = ws_q8kp(ctx, m, cols, &ok);
+    if (!ok) return fail("spx_matvec: workspace allocation failed");
+    SPX_HIP(launch_q8kp_quantize(x, cols, ld_x, m, y, ctx->stream));
+    return mv_launch(ctx, w, expert, m, nullptr, 0, y, out, ld_out, 0, rows);
   }
   if (w->v.dtype == T_F32 && cols % 16) return fail("spx_matvec: F32 needs cols % 16 == 0");
   if (w->v.dtype != T_Q8_0 && w->v.dtype != T_Q5_0 && w->v.dtype != T_F32) return fail("spx_matvec: unsupported dtype " + std::to_string(w->v.dtype));
-  FArgs a{};
-  a.w = w->v; a.x = x; a.ld_x = ld_x; a.out = out; a.ld_out = ld_out; a.r0 = 0; a.r1 = rows; a.expert = expert; a.m = m;
-  SPX_HIP(launch_gemv_f(a, m, false, 1, ctx->stream));
-  return 0;
+  return mv_launch(ctx, w, expert, m, x, ld_x, Q8KP{}, out, ld_out, 0, rows);
 }
 
 }  // extern "C"

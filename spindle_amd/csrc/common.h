@@ -19,8 +19,9 @@ enum DType : int {
 };
 
 // Device view of one uploaded tensor (all experts). Plane pointers by dtype:
-//   Q4_K: p0 = codes (128 B/blk), p1 = header (16 B/blk: d, dmin, scales[12])
-//   Q6_K: p0 = ql (128), p1 = qh (64), p2 = scales (16), p3 = d (2)
+//   Q4_K: p0 = codes (128 B/blk, lane-permuted, see kq.h), p1 = header (16 B/blk: d, dmin,
+//         scales[12])
+//   Q6_K: p0 = ql (128, lane-permuted), p1 = qh (64, lane-permuted), p2 = scales (16), p3 = d (2)
 //   Q8_0: p0 = codes (32), p3 = d (2)
 //   Q5_0: p0 = low nibbles (16), p1 = high bits (4), p3 = d (2)
 //   F32 / F16: p0 = row-major values
@@ -34,43 +35,6 @@ struct TensorView {
   int64_t cols, rows;   // rows per expert
   int n_expert;
   int64_t nb;           // blocks per row
-};
-
-// One grouped job of the MoE kernels: an expert, its user vectors and where results go.
-struct Job {
-  int expert;
-  int nvec;
-  int vec[16];  // index of each user's input vector (into the job's activation buffer)
-  int out[16];  // index of each user's output vector
-};
-
-// Arguments of the integer (Q8_K activation) matrix-vector kernels.
-struct KQArgs {
-  TensorView w;
-  const float *xd;      // Q8_K scales  [vec][nb]
-  const int8_t *xq;     // Q8_K codes   [vec][cols]
-  const int16_t *xb;    // Q8_K bsums   [vec][nb*16]
-  float *out;           // [out_vec][ld_out]
-  int64_t ld_out;
-  int64_t r0, r1;       // rows within the expert
-  int expert, m;        // plain launch
-  const Job *jobs;      // grouped launch: job per blockIdx.y
-  const int *njobs;
-  int32_t *dbg;         // block-sums probe: [nb][2] for (row r0, vector 0)
-  int passes;           // row passes per workgroup (set by the launcher)
-};
-
-// Arguments of the fp32-activation matrix-vector kernels.
-struct FArgs {
-  TensorView w;
-  const float *x;       // [vec][ld_x]
-  int64_t ld_x;
-  float *out;
-  int64_t ld_out;
-  int64_t r0, r1;
-  int expert, m;
-  const Job *jobs;
-  const int *njobs;
 };
 
 __device__ __forceinline__ float h2f(uint32_t h) {

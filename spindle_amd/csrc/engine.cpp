@@ -2,20 +2,26 @@
 // (smollm_chat.rs:1574-1668, forward_slice :3364-3552, forward_batch_slice :3142-3362,
 // compute_logits_batch :3588-3602, the greedy speculative loop of generate_reply :4205-4348)
 // over one GPU. The whole model and the f16 KV cache stay resident in HBM; one forward pass
-// of m <= 16 rows is a fixed launch sequence, captured once per m into a HIP graph and
-// replayed with the step record (token ids, start position) in device memory.
+// of m <= 16 rows is a fixed launch sequence of fused kernels (fused.hip), captured once per
+// m into a HIP graph and replayed with the step record (token ids, start position) in device
+// memory.
+//
+// Residual stream: two buffers alternate so that no kernel reads what it writes. The q/k/v
+// kernel reads xA (+ the previous layer's FFN output) and writes the sum to xB; the router
+// (or the dense gate/up kernel) reads xB (+ the attention output) and writes the sum to xA.
 #include <string.h>
 
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <map>
 #include <memory>
 #include <string>
 #include <vector>
 
 #include "../../include/spx.h"
+#include "fused.h"
 #include "internal.h"
-#include "layer_kernels.h"
 
 using namespace spx;
 
@@ -23,18 +29,10 @@ namespace {
 
 // kernel classes of the profile (spx_engine_profile_read)
 enum {
-  PC_EMBED, PC_NORM, PC_QKV, PC_QKROPE, PC_ATTN, PC_QUANT, PC_WO, PC_FFN_DENSE, PC_ROUTER, PC_ROUTE,
-  PC_MOE_GATEUP, PC_SWIGLU, PC_MOE_DOWN, PC_COMBINE, PC_LMHEAD, PC_ARGMAX, PROF_NCLS
+  PC_EMBED, PC_QKV, PC_ATTN, PC_QUANT, PC_WO, PC_ROUTER, PC_GATEUP, PC_DOWN, PC_NORM, PC_LMHEAD, PC_ARGMAX, PROF_NCLS
 };
-const char *PROF_NAMES[PROF_NCLS] = {"embed", "residual_rmsnorm_q8k", "attn_qkv_matvec", "qk_norm_rope_kv", "attention",
-                                     "q8k_quantize", "attn_output_matvec", "dense_ffn_matvec", "router_matvec", "moe_route",
-                                     "moe_gate_up_grouped", "swiglu_q8k", "moe_down_grouped", "moe_combine", "lm_head_matvec", "argmax"};
-
-struct Q8Buf {
-  float *d = nullptr;
-  int8_t *q = nullptr;
-  int16_t *b = nullptr;
-};
+const char *PROF_NAMES[PROF_NCLS] = {"embed", "qkv_matvec", "attention", "q8k_quantize", "attn_output_matvec", "router_route",
+                                     "gate_up_swiglu", "down_combine", "final_norm", "lm_head_matvec", "argmax"};
 
 struct LayerW {
   const float *attn_norm = nullptr, *ffn_norm = nullptr;
@@ -46,6 +44,8 @@ struct LayerW {
 };
 
 bool is_kq(const spx_tensor *t) { return t && (t->v.dtype == T_Q4K || t->v.dtype == T_Q6K); }
+bool is_fq(const spx_tensor *t) { return t && (t->v.dtype == T_Q8_0 || t->v.dtype == T_Q5_0); }
+int bucket(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
 
 int64_t now_us() {
   return std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now().time_since_epoch()).count();
@@ -56,7 +56,7 @@ int64_t now_us() {
 struct spx_engine {
   spx_ctx *ctx = nullptr;
   spx_model_config c{};
-  int q_dim = 0, kv_dim = 0, n_ff = 0, max_chunks = 0;
+  int q_dim = 0, kv_dim = 0, n_ff = 0, nch = 64, lm_grid = 2048;
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
   std::map<std::string, int64_t> vec_len;
@@ -69,14 +69,14 @@ struct spx_engine {
   __half *kc = nullptr, *vc = nullptr;
   float2 *rope = nullptr;
   StepRec *st_dev = nullptr, *st_host = nullptr;
-  float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *proj = nullptr;
-  Q8Buf xq, aq, hq;
-  float *h = nullptr, *u = nullptr, *y = nullptr, *rlog = nullptr, *logits = nullptr;
-  int *amax = nullptr;
-  float *part_m = nullptr, *part_l = nullptr, *part_o = nullptr;
+  float *xA = nullptr, *xB = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *proj = nullptr, *ffn = nullptr;
+  float *xn2 = nullptr, *h = nullptr, *rlog = nullptr, *logits = nullptr, *xn = nullptr, *part_ml = nullptr, *part_o = nullptr;
+  Q8KP aq{}, xq2{}, hq{}, xq{};
+  int *amax = nullptr, *att_cnt = nullptr, *rt_cnt = nullptr, *gu_cnt = nullptr;
+  unsigned long long *best = nullptr;
   int *chosen = nullptr, *nkeep = nullptr, *expert_count = nullptr;
   float *weights = nullptr;
-  Job *jobs_gu = nullptr, *jobs_dn = nullptr;
+  Job *jobs = nullptr;
   hipGraphExec_t graph[MAX_M + 1] = {};
   int n_used = 0;
   // kernel-class timing (eager passes only): event pairs recorded around each launch
@@ -95,6 +95,14 @@ struct spx_engine {
     (void)hipMemset(p, 0, std::max<size_t>(n * sizeof(T), 16));
     allocs.push_back(p);
     return static_cast<T *>(p);
+  }
+  // permuted Q8_K buffer for nv vectors of cols columns
+  bool q8alloc(Q8KP &b, int nv, int64_t cols) {
+    const int64_t nb = cols / 256;
+    b.q = dalloc<uint32_t>((size_t)nv * cols / 4 + 16);
+    b.d = dalloc<float>((size_t)nv * nb + 16);
+    b.bs = dalloc<int2>((size_t)nv * nb * 8 + 16);
+    return b.q && b.d && b.bs;
   }
 };
 
@@ -123,97 +131,182 @@ struct ProfScope {
 
 double wbytes(const spx_tensor *t) { return (double)row_bytes(t->v.dtype, t->v.cols) * (double)t->v.rows; }
 
-// ---------------------------------------------------------------- matrix launches
-int gemv(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld_x, const Q8Buf *xq, float *out, int64_t ld_out,
-         const Job *jobs = nullptr, const int *njobs = nullptr, int max_jobs = 0, int expert = 0) {
-  const bool grouped = jobs != nullptr;
-  if (is_kq(w)) {
-    KQArgs a{};
-    a.w = w->v; a.xd = xq->d; a.xq = xq->q; a.xb = xq->b; a.out = out; a.ld_out = ld_out;
-    a.r0 = 0; a.r1 = w->v.rows; a.expert = expert; a.m = m; a.jobs = jobs; a.njobs = njobs;
-    SPX_HIP(launch_gemv_kq(a, m, grouped, max_jobs, E->ctx->stream));
-  } else {
-    FArgs a{};
-    a.w = w->v; a.x = x; a.ld_x = ld_x; a.out = out; a.ld_out = ld_out; a.r0 = 0; a.r1 = w->v.rows;
-    a.expert = expert; a.m = m; a.jobs = jobs; a.njobs = njobs;
-    SPX_HIP(launch_gemv_f(a, m, grouped, max_jobs, E->ctx->stream));
+Seg seg_of(const spx_tensor *t, float *out, int64_t ld_out, int m, bool pro) {
+  Seg s{};
+  s.w = t->v;
+  s.out = out;
+  s.ld_out = ld_out;
+  s.r0 = 0;
+  s.r1 = t->v.rows;
+  s.expert = 0;
+  s.wgs = mv_wgs(t->v.rows, m, pro, t->v.dtype);
+  return s;
+}
+
+// residual + norm prologue record
+Pro pro_of(spx_engine *E, const float *xa, const float *pa, const float *nw, float *xb) {
+  Pro p{};
+  p.xa = xa;
+  p.pa = pa;
+  p.rscale = E->c.residual_scale;
+  p.nw = nw;
+  p.eps = E->c.rms_eps;
+  p.xb = xb;
+  p.dim = E->c.dim;
+  return p;
+}
+
+// Matrix launch with the residual + norm prologue when it fits in LDS, else a norm kernel
+// (writing xn_tmp, and its Q8_K for integer weights) and a plain launch.
+int mv_pro(spx_engine *E, MVArgs &a, int m, float *xn_tmp, Q8KP q_tmp) {
+  hipStream_t s = E->ctx->stream;
+  const bool kq = a.seg[0].w.dtype == T_Q4K || a.seg[0].w.dtype == T_Q6K;
+  const size_t lds = kq ? 0 : (size_t)bucket(m) * a.pro.dim * 4;
+  if (lds <= 65536 && a.pro.dim <= 256 * PRO_NT) {
+    int total = 0;
+    for (int i = 0; i < a.nseg; i++) total += a.seg[i].wgs;
+    SPX_HIP(launch_mv(a, m, true, E->st_dev, total, s));
+    return 0;
   }
+  Pro p = a.pro;
+  p.xn_out = xn_tmp;
+  if (kq) p.q_out = q_tmp;
+  SPX_HIP(launch_norm(p, E->st_dev, m, s));
+  int total = 0;
+  for (int i = 0; i < a.nseg; i++) { a.seg[i].wgs = mv_wgs(a.seg[i].r1 - a.seg[i].r0, m, false, a.seg[i].w.dtype); total += a.seg[i].wgs; }
+  a.x = xn_tmp;
+  a.ld_x = a.pro.dim;
+  a.y = q_tmp;
+  SPX_HIP(launch_mv(a, m, false, E->st_dev, total, s));
+  return 0;
+}
+
+// Plain matrix launch: activations y (integer weights) or x (float weights).
+int mv_plain(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld_x, Q8KP y, float *out, int64_t ld_out,
+             unsigned long long *best = nullptr, int grid_cap = 0) {
+  MVArgs a{};
+  a.seg[0] = seg_of(w, out, ld_out, m, false);
+  a.nseg = 1;
+  a.x = x;
+  a.ld_x = ld_x;
+  a.y = y;
+  a.m = m;
+  a.best = best;
+  a.lscale = E->c.logit_scale;
+  int grid = a.seg[0].wgs;
+  if (grid_cap > 0 && grid > grid_cap) grid = grid_cap;
+  a.nbest = grid;
+  SPX_HIP(launch_mv(a, m, false, E->st_dev, grid, E->ctx->stream));
   return 0;
 }
 
 // One forward pass of m rows at the step record's start position: embeddings through the
-// LM head and the greedy argmax (forward_slice / forward_batch_slice + compute_logits_batch).
+// LM head and the greedy pick (forward_slice / forward_batch_slice + compute_logits_batch).
 int enqueue_forward(spx_engine *E, int m) {
   const auto &c = E->c;
   hipStream_t s = E->ctx->stream;
   const int dim = c.dim, hd = c.head_dim;
-  { ProfScope ps(E, PC_EMBED, 0); SPX_HIP(launch_embed(E->embed->v, E->st_dev, E->x, dim, c.embedding_scale, m, s)); }
-  const float *pending = nullptr;  // residual to add before the next norm
+  { ProfScope ps(E, PC_EMBED, 0); SPX_HIP(launch_embed(E->embed->v, E->st_dev, E->xA, dim, c.embedding_scale, m, s)); }
   for (int l = 0; l < c.n_layers; l++) {
     const LayerW &ly = E->L[l];
-    const bool q_int = is_kq(ly.wq) || is_kq(ly.wk) || is_kq(ly.wv);
-    { ProfScope ps(E, PC_NORM, 0);
-      SPX_HIP(launch_res_norm(E->x, dim, pending, dim, c.residual_scale, ly.attn_norm, dim, c.rms_eps, E->xn, dim,
-                              q_int ? E->xq.d : nullptr, q_int ? E->xq.q : nullptr, q_int ? E->xq.b : nullptr, E->st_dev, m, s)); }
-    { ProfScope ps(E, PC_QKV, wbytes(ly.wq)); if (int r = gemv(E, ly.wq, m, E->xn, dim, &E->xq, E->q, E->q_dim)) return r; }
-    { ProfScope ps(E, PC_QKV, wbytes(ly.wk)); if (int r = gemv(E, ly.wk, m, E->xn, dim, &E->xq, E->k, E->kv_dim)) return r; }
-    { ProfScope ps(E, PC_QKV, wbytes(ly.wv)); if (int r = gemv(E, ly.wv, m, E->xn, dim, &E->xq, E->v, E->kv_dim)) return r; }
-    QKArgs qa{};
-    qa.q = E->q; qa.k = E->k; qa.v = E->v; qa.ld_q = E->q_dim; qa.ld_kv = E->kv_dim;
-    qa.q_bias = ly.q_bias; qa.k_bias = ly.k_bias; qa.v_bias = ly.v_bias; qa.q_norm = ly.q_norm; qa.k_norm = ly.k_norm;
-    qa.rope = E->rope; qa.k_cache = E->kc; qa.v_cache = E->vc; qa.layer = l; qa.max_seq = c.max_seq; qa.kv_dim = E->kv_dim;
-    qa.head_dim = hd; qa.n_heads = c.n_heads; qa.n_kv = c.n_kv_heads; qa.neox = c.rope_neox; qa.eps = c.rms_eps;
-    { ProfScope ps(E, PC_QKROPE, 0); SPX_HIP(launch_qk_rope_kv(qa, E->st_dev, m, s)); }
-    AttnArgs aa{};
-    aa.q = E->q; aa.ld_q = E->q_dim; aa.k_cache = E->kc; aa.v_cache = E->vc; aa.part_m = E->part_m; aa.part_l = E->part_l;
-    aa.part_o = E->part_o; aa.out = E->att; aa.ld_out = E->q_dim; aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim;
-    aa.head_dim = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads; aa.max_chunks = E->max_chunks;
-    aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
-    { ProfScope ps(E, PC_ATTN, -1.0 - l); SPX_HIP(launch_attention(aa, E->st_dev, m, s)); }
-    if (is_kq(ly.wo)) { ProfScope ps(E, PC_QUANT, 0); SPX_HIP(launch_q8k_quantize(E->att, E->q_dim, E->q_dim, m, E->aq.d, E->aq.q, E->aq.b, s)); }
-    { ProfScope ps(E, PC_WO, wbytes(ly.wo)); if (int r = gemv(E, ly.wo, m, E->att, E->q_dim, &E->aq, E->proj, dim)) return r; }
-    const bool f_int = is_kq(ly.gate) || is_kq(ly.up);
-    { ProfScope ps(E, PC_NORM, 0);
-      SPX_HIP(launch_res_norm(E->x, dim, E->proj, dim, c.residual_scale, ly.ffn_norm, dim, c.rms_eps, E->xn, dim,
-                              f_int ? E->xq.d : nullptr, f_int ? E->xq.q : nullptr, f_int ? E->xq.b : nullptr, E->st_dev, m, s)); }
-    const int nff = (int)ly.gate->v.rows;
-    const bool d_int = is_kq(ly.down);
-    if (!ly.moe) {  // ffn_forward / ffn_forward_multi (:590-646)
-      { ProfScope ps(E, PC_FFN_DENSE, wbytes(ly.gate)); if (int r = gemv(E, ly.gate, m, E->xn, dim, &E->xq, E->h, nff)) return r; }
-      { ProfScope ps(E, PC_FFN_DENSE, wbytes(ly.up)); if (int r = gemv(E, ly.up, m, E->xn, dim, &E->xq, E->u, nff)) return r; }
-      SwigluArgs sa{};
-      sa.g = E->h; sa.u = E->u; sa.ld = nff; sa.n = nff;
-      if (d_int) { sa.qd = E->hq.d; sa.qq = E->hq.q; sa.qb = E->hq.b; }
-      { ProfScope ps(E, PC_SWIGLU, 0); SPX_HIP(launch_swiglu(sa, E->st_dev, m, s)); }
-      { ProfScope ps(E, PC_FFN_DENSE, wbytes(ly.down)); if (int r = gemv(E, ly.down, m, E->h, nff, &E->hq, E->proj, dim)) return r; }
-    } else {  // moe_forward / moe_forward_batch (:925-1392)
-      const int nu = c.n_expert_used, ne = c.n_expert;
-      { ProfScope ps(E, PC_ROUTER, wbytes(ly.router)); if (int r = gemv(E, ly.router, m, E->xn, dim, nullptr, E->rlog, ne)) return r; }
-      RouteArgs ra{};
-      ra.logits = E->rlog; ra.ld_logits = ne; ra.n_expert = ne; ra.n_used = nu; ra.norm = c.expert_norm; ra.moe_prune = c.moe_prune;
-      ra.chosen = E->chosen; ra.weights = E->weights; ra.nkeep = E->nkeep; ra.jobs_gu = E->jobs_gu; ra.jobs_dn = E->jobs_dn;
-      ra.njobs = ly.njobs; ra.expert_count = E->expert_count + (size_t)l * ne;
-      { ProfScope ps(E, PC_ROUTE, 0); SPX_HIP(launch_moe_route(ra, E->st_dev, s)); }
-      const int max_jobs = std::min(ne, m * nu);
-      { ProfScope ps(E, PC_MOE_GATEUP, wbytes(ly.gate), l, true); if (int r = gemv(E, ly.gate, m, E->xn, dim, &E->xq, E->h, nff, E->jobs_gu, ly.njobs, max_jobs)) return r; }
-      { ProfScope ps(E, PC_MOE_GATEUP, wbytes(ly.up), l, true); if (int r = gemv(E, ly.up, m, E->xn, dim, &E->xq, E->u, nff, E->jobs_gu, ly.njobs, max_jobs)) return r; }
-      SwigluArgs sa{};
-      sa.g = E->h; sa.u = E->u; sa.ld = nff; sa.n = nff; sa.jobs = E->jobs_gu; sa.njobs = ly.njobs;
-      if (d_int) { sa.qd = E->hq.d; sa.qq = E->hq.q; sa.qb = E->hq.b; }
-      { ProfScope ps(E, PC_SWIGLU, 0); SPX_HIP(launch_swiglu(sa, E->st_dev, m * nu, s)); }
-      { ProfScope ps(E, PC_MOE_DOWN, wbytes(ly.down), l, true); if (int r = gemv(E, ly.down, m, E->h, nff, &E->hq, E->y, dim, E->jobs_dn, ly.njobs, max_jobs)) return r; }
-      CombineArgs ca{};
-      ca.y = E->y; ca.ld_y = dim; ca.weights = E->weights; ca.nkeep = E->nkeep; ca.n_used = nu; ca.dim = dim; ca.out = E->proj; ca.ld_out = dim;
-      { ProfScope ps(E, PC_COMBINE, 0); SPX_HIP(launch_moe_combine(ca, E->st_dev, m, s)); }
+    const float *pend = l == 0 ? nullptr : E->ffn;
+    // q, k, v with the attn_norm prologue (xA + ffn -> xB)
+    {
+      ProfScope ps(E, PC_QKV, wbytes(ly.wq) + wbytes(ly.wk) + wbytes(ly.wv));
+      MVArgs a{};
+      a.seg[0] = seg_of(ly.wq, E->q, E->q_dim, m, true);
+      a.seg[1] = seg_of(ly.wk, E->k, E->kv_dim, m, true);
+      a.seg[2] = seg_of(ly.wv, E->v, E->kv_dim, m, true);
+      a.nseg = 3;
+      a.pro = pro_of(E, E->xA, pend, ly.attn_norm, E->xB);
+      if (int r = mv_pro(E, a, m, E->xn2, E->xq2)) return r;
     }
-    pending = E->proj;
+    // attention (+ Q8_K of its output for an integer attn_output)
+    const bool wo_int = is_kq(ly.wo);
+    const bool att_q_fused = wo_int && ((c.n_heads / c.n_kv_heads) * hd) % 256 == 0;
+    {
+      ProfScope ps(E, PC_ATTN, -1.0 - l);
+      AttnArgs aa{};
+      aa.q = E->q; aa.k = E->k; aa.v = E->v;
+      aa.q_bias = ly.q_bias; aa.k_bias = ly.k_bias; aa.v_bias = ly.v_bias; aa.q_norm = ly.q_norm; aa.k_norm = ly.k_norm;
+      aa.rope = E->rope; aa.kc = E->kc; aa.vc = E->vc; aa.part_ml = E->part_ml; aa.part_o = E->part_o; aa.counter = E->att_cnt; aa.att = E->att;
+      if (att_q_fused) aa.aq = E->aq;
+      aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
+      aa.neox = c.rope_neox; aa.nch = E->nch; aa.eps = c.rms_eps;
+      aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
+      SPX_HIP(launch_attention(aa, m, E->st_dev, s));
+    }
+    if (wo_int && !att_q_fused) { ProfScope ps(E, PC_QUANT, 0); SPX_HIP(launch_q8kp_quantize(E->att, E->q_dim, E->q_dim, m, E->aq, s)); }
+    { ProfScope ps(E, PC_WO, wbytes(ly.wo)); if (int r = mv_plain(E, ly.wo, m, E->att, E->q_dim, E->aq, E->proj, dim)) return r; }
+    const int nff = (int)ly.gate->v.rows;
+    const bool f_int = is_kq(ly.gate), d_int = is_kq(ly.down);
+    if (ly.moe) {  // moe_forward / moe_forward_batch (:925-1392)
+      const int nu = c.n_expert_used, ne = c.n_expert;
+      {
+        ProfScope ps(E, PC_ROUTER, wbytes(ly.router));
+        RouterArgs ra{};
+        ra.w = ly.router->v; ra.logits = E->rlog;
+        ra.pro = pro_of(E, E->xB, E->proj, ly.ffn_norm, E->xA);
+        if (f_int) ra.pro.q_out = E->xq2; else ra.pro.xn_out = E->xn2;
+        ra.n_expert = ne; ra.n_used = nu; ra.norm = c.expert_norm; ra.moe_prune = c.moe_prune; ra.counter = E->rt_cnt;
+        ra.chosen = E->chosen; ra.weights = E->weights; ra.nkeep = E->nkeep; ra.jobs = E->jobs; ra.njobs = ly.njobs;
+        ra.expert_count = E->expert_count + (size_t)l * ne; ra.rows_per_wg = 2;
+        SPX_HIP(launch_router(ra, m, E->st_dev, s));
+      }
+      const int max_jobs = std::min(ne, m * nu);
+      {
+        ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up), l, true);  // one expert's slabs
+        GUArgs ga{};
+        ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.x = E->xn2; ga.use_pro = false;
+        ga.jobs = E->jobs; ga.njobs = ly.njobs; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
+        if (d_int) ga.hq = E->hq;
+        SPX_HIP(launch_gateup(ga, m, E->st_dev, max_jobs, s));
+      }
+      {
+        ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
+        DownArgs da{};
+        da.w = ly.down->v; da.y = E->hq; da.x = E->h; da.jobs = E->jobs + 256; da.njobs = ly.njobs; da.weights = E->weights;
+        da.nkeep = E->nkeep; da.n_used = nu; da.out = E->ffn;
+        SPX_HIP(launch_down(da, m, E->st_dev, max_jobs, s));
+      }
+    } else {  // ffn_forward / ffn_forward_multi (:590-646): k = 1, w = 1
+      {
+        ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
+        GUArgs ga{};
+        ga.gate = ly.gate->v; ga.up = ly.up->v; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
+        if (d_int) ga.hq = E->hq;
+        ga.pro = pro_of(E, E->xB, E->proj, ly.ffn_norm, E->xA);
+        const size_t lds = f_int ? 0 : (size_t)bucket(m) * dim * 4;
+        if (lds <= 65536 && dim <= 256 * PRO_NT) {
+          ga.use_pro = true;
+        } else {
+          Pro p = ga.pro;
+          p.xn_out = E->xn2;
+          if (f_int) p.q_out = E->xq2;
+          SPX_HIP(launch_norm(p, E->st_dev, m, s));
+          ga.use_pro = false;
+          ga.x = E->xn2;
+          ga.y = E->xq2;
+        }
+        SPX_HIP(launch_gateup(ga, m, E->st_dev, 1, s));
+      }
+      { ProfScope ps(E, PC_DOWN, wbytes(ly.down)); if (int r = mv_plain(E, ly.down, m, E->h, nff, E->hq, E->ffn, dim)) return r; }
+    }
   }
   const bool h_int = is_kq(E->lm_head);
-  { ProfScope ps(E, PC_NORM, 0);
-    SPX_HIP(launch_res_norm(E->x, dim, pending, dim, c.residual_scale, E->out_norm, dim, c.rms_eps, E->xn, dim,
-                            h_int ? E->xq.d : nullptr, h_int ? E->xq.q : nullptr, h_int ? E->xq.b : nullptr, E->st_dev, m, s)); }
-  { ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head)); if (int r = gemv(E, E->lm_head, m, E->xn, dim, &E->xq, E->logits, c.vocab)) return r; }
-  { ProfScope ps(E, PC_ARGMAX, 0); SPX_HIP(launch_argmax(E->logits, c.vocab, c.vocab, c.logit_scale, E->amax, E->st_dev, m, s)); }
+  {
+    ProfScope ps(E, PC_NORM, 0);
+    Pro p = pro_of(E, E->xA, E->ffn, E->out_norm, nullptr);
+    p.xn_out = E->xn;
+    if (h_int) p.q_out = E->xq;
+    SPX_HIP(launch_norm(p, E->st_dev, m, s));
+  }
+  { ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head)); if (int r = mv_plain(E, E->lm_head, m, E->xn, dim, E->xq, E->logits, c.vocab, E->best, E->lm_grid)) return r; }
+  {
+    ProfScope ps(E, PC_ARGMAX, 0);
+    const int nbest = std::min(mv_wgs(E->lm_head->v.rows, m, false, E->lm_head->v.dtype), E->lm_grid);
+    SPX_HIP(launch_argmax_final(E->best, nbest, E->amax, E->st_dev, m, s));
+  }
   return 0;
 }
 
@@ -242,12 +335,12 @@ extern "C" {
 int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **out) {
   if (!ctx || !cfg || !out) return fail("spx_engine_create: null argument");
   const spx_model_config &c = *cfg;
-  if (c.dim <= 0 || c.dim > 4096 || c.dim % 16) return fail("spx_engine_create: dim must be a positive multiple of 16, at most 4096");
+  if (c.dim <= 0 || c.dim > 256 * PRO_NT || c.dim % 16)
+    return fail("spx_engine_create: dim must be a positive multiple of 16, at most " + std::to_string(256 * PRO_NT));
   if (c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads) return fail("spx_engine_create: n_heads must be a multiple of n_kv_heads");
-  if (c.head_dim <= 0 || c.head_dim > 128 || c.head_dim % 8) return fail("spx_engine_create: head_dim must be a multiple of 8, at most 128");
-  if (16 * (c.n_heads / c.n_kv_heads) > 4096) return fail("spx_engine_create: too many query heads per kv head");
+  if (c.head_dim != 64 && c.head_dim != 128) return fail("spx_engine_create: the attention kernel supports head_dim 64 or 128");
+  if (16 * (c.n_heads / c.n_kv_heads) > ATT_QMAX) return fail("spx_engine_create: at most 8 query heads per kv head");
   if (c.n_layers <= 0 || c.vocab <= 0 || c.max_seq <= 0) return fail("spx_engine_create: bad layer count, vocab or max_seq");
-  if (c.max_seq > MAX_CHUNKS * ATT_CHUNK) return fail("spx_engine_create: max_seq above " + std::to_string(MAX_CHUNKS * ATT_CHUNK));
   if (c.n_expert < 0 || c.n_expert > 256 || c.n_expert_used < 0 || c.n_expert_used > 32 || (c.n_expert && !c.n_expert_used))
     return fail("spx_engine_create: unsupported expert counts (n_expert <= 256, n_expert_used in 1..32)");
   spx_engine *E = new spx_engine();
@@ -259,6 +352,8 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   E->q_dim = c.n_heads * c.head_dim;
   E->kv_dim = c.n_kv_heads * c.head_dim;
   E->L.resize(c.n_layers);
+  if (const char *v = std::getenv("SPX_ATT_CHUNKS")) E->nch = std::max(1, std::min(64, atoi(v)));
+  if (const char *v = std::getenv("SPX_LM_GRID")) E->lm_grid = std::max(1, atoi(v));
   *out = E;
   return 0;
 }
@@ -303,7 +398,7 @@ int spx_engine_prepare(spx_engine *E) {
     if (t->v.cols != cols || t->v.rows != rows || t->v.n_expert != ne)
       return fail(n + ": expected " + std::to_string(rows) + "x" + std::to_string(cols) + "x" + std::to_string(ne) + ", got " +
                   std::to_string(t->v.rows) + "x" + std::to_string(t->v.cols) + "x" + std::to_string(t->v.n_expert));
-    if (t->v.dtype == T_F16) return fail(n + ": F16 weight matrices are not supported by the GPU kernels");
+    if (!is_kq(t) && !is_fq(t)) return fail(n + ": weight matrices must be Q4_K, Q6_K, Q8_0 or Q5_0 for the GPU kernels");
     *dst = t;
     return 0;
   };
@@ -311,6 +406,7 @@ int spx_engine_prepare(spx_engine *E) {
   if (!E->embed || E->embed->v.cols != c.dim || E->embed->v.rows != c.vocab) return fail("missing or misshaped token_embd.weight");
   E->lm_head = mat("output.weight") ? mat("output.weight") : E->embed;  // tied embeddings (:1921)
   if (E->lm_head->v.cols != c.dim || E->lm_head->v.rows != c.vocab) return fail("misshaped output.weight");
+  if (!is_kq(E->lm_head) && !is_fq(E->lm_head)) return fail("the LM head must be Q4_K, Q6_K, Q8_0 or Q5_0");
   if (!(E->out_norm = vec("output_norm.weight", c.dim))) return fail("missing output_norm.weight");
   int nff_max = 0;
   for (int l = 0; l < c.n_layers; l++) {
@@ -322,6 +418,8 @@ int spx_engine_prepare(spx_engine *E) {
     if (int r = need_mat(p + "attn_k.weight", c.dim, E->kv_dim, 1, &ly.wk)) return r;
     if (int r = need_mat(p + "attn_v.weight", c.dim, E->kv_dim, 1, &ly.wv)) return r;
     if (int r = need_mat(p + "attn_output.weight", E->q_dim, c.dim, 1, &ly.wo)) return r;
+    if (is_kq(ly.wq) != is_kq(ly.wk) || is_kq(ly.wq) != is_kq(ly.wv))
+      return fail(p + "attn_q/k/v: integer (Q4_K/Q6_K) and float-activation (Q8_0/Q5_0) formats cannot be mixed");
     ly.q_bias = vec(p + "attn_q.bias", E->q_dim);
     ly.k_bias = vec(p + "attn_k.bias", E->kv_dim);
     ly.v_bias = vec(p + "attn_v.bias", E->kv_dim);
@@ -351,11 +449,11 @@ int spx_engine_prepare(spx_engine *E) {
       if (int rr = need_mat(p + "ffn_down.weight", nff, c.dim, 1, &ly.down)) return rr;
       nff_max = std::max<int>(nff_max, (int)nff);
     }
-    if (ly.wq->v.dtype == T_F32 || ly.wo->v.dtype == T_F32) {
-      if (c.dim % 16 || E->q_dim % 16) return fail("F32 projections need 16-multiple widths");
-    }
+    if (ly.gate->v.dtype != ly.up->v.dtype) return fail(p + "ffn_gate and ffn_up must share a format");
+    if (is_kq(ly.down) && ly.gate->v.rows % 256) return fail(p + "a Q4_K/Q6_K ffn_down needs a feed-forward width that is a multiple of 256");
+    if (ly.gate->v.rows % 16) return fail(p + "the feed-forward width must be a multiple of 16");
   }
-  if (nff_max > 4096 || nff_max % 16) return fail("feed-forward width must be a multiple of 16, at most 4096");
+  if (nff_max > 4096) return fail("feed-forward width above 4096");
   E->n_ff = nff_max;
   for (auto &ly : E->L)
     for (spx_tensor *t : {ly.wq, ly.wk, ly.wv, ly.wo, ly.gate, ly.up, ly.down, E->lm_head})
@@ -363,28 +461,26 @@ int spx_engine_prepare(spx_engine *E) {
   // device buffers
   const int M = MAX_M, nu = std::max(1, c.n_expert_used), nv = M * nu;
   const int64_t kvn = (int64_t)c.n_layers * c.max_seq * E->kv_dim;
-  E->max_chunks = (c.max_seq + ATT_CHUNK - 1) / ATT_CHUNK;
-  const int g = c.n_heads / c.n_kv_heads;
-  const int64_t prow = (int64_t)c.n_kv_heads * 16 * g * E->max_chunks;
-  const int qmax = std::max({c.dim, E->q_dim, E->n_ff});
+  const int qmax = std::max({c.dim, E->q_dim});
+  const int nff = std::max(256, E->n_ff);
   bool ok = (E->kc = E->dalloc<__half>(kvn)) && (E->vc = E->dalloc<__half>(kvn)) &&
             (E->rope = E->dalloc<float2>((size_t)c.max_seq * (c.head_dim / 2))) && (E->st_dev = E->dalloc<StepRec>(1)) &&
-            (E->x = E->dalloc<float>((size_t)M * c.dim)) && (E->xn = E->dalloc<float>((size_t)M * c.dim)) &&
+            (E->xA = E->dalloc<float>((size_t)M * c.dim)) && (E->xB = E->dalloc<float>((size_t)M * c.dim)) &&
             (E->q = E->dalloc<float>((size_t)M * E->q_dim)) && (E->k = E->dalloc<float>((size_t)M * E->kv_dim)) &&
             (E->v = E->dalloc<float>((size_t)M * E->kv_dim)) && (E->att = E->dalloc<float>((size_t)M * E->q_dim)) &&
-            (E->proj = E->dalloc<float>((size_t)M * c.dim)) && (E->xq.d = E->dalloc<float>((size_t)M * qmax / 256 + 16)) &&
-            (E->xq.q = E->dalloc<int8_t>((size_t)M * qmax)) && (E->xq.b = E->dalloc<int16_t>((size_t)M * qmax / 16 + 16)) &&
-            (E->aq.d = E->dalloc<float>((size_t)M * E->q_dim / 256 + 16)) && (E->aq.q = E->dalloc<int8_t>((size_t)M * E->q_dim)) &&
-            (E->aq.b = E->dalloc<int16_t>((size_t)M * E->q_dim / 16 + 16)) && (E->hq.d = E->dalloc<float>((size_t)nv * E->n_ff / 256 + 16)) &&
-            (E->hq.q = E->dalloc<int8_t>((size_t)nv * E->n_ff)) && (E->hq.b = E->dalloc<int16_t>((size_t)nv * E->n_ff / 16 + 16)) &&
-            (E->h = E->dalloc<float>((size_t)nv * E->n_ff)) && (E->u = E->dalloc<float>((size_t)nv * E->n_ff)) &&
-            (E->y = E->dalloc<float>((size_t)nv * c.dim)) && (E->rlog = E->dalloc<float>((size_t)M * std::max(1, c.n_expert))) &&
+            (E->proj = E->dalloc<float>((size_t)M * c.dim)) && (E->ffn = E->dalloc<float>((size_t)M * c.dim)) &&
+            (E->xn2 = E->dalloc<float>((size_t)M * qmax)) && (E->xn = E->dalloc<float>((size_t)M * c.dim)) &&
+            (E->h = E->dalloc<float>((size_t)nv * nff)) && (E->rlog = E->dalloc<float>((size_t)M * std::max(1, c.n_expert))) &&
             (E->logits = E->dalloc<float>((size_t)M * c.vocab)) && (E->amax = E->dalloc<int>(M)) &&
-            (E->part_m = E->dalloc<float>(prow)) && (E->part_l = E->dalloc<float>(prow)) &&
-            (E->part_o = E->dalloc<float>(prow * c.head_dim)) && (E->chosen = E->dalloc<int>(16 * 32)) &&
-            (E->nkeep = E->dalloc<int>(16)) && (E->weights = E->dalloc<float>(16 * 32)) &&
-            (E->jobs_gu = E->dalloc<Job>(256)) && (E->jobs_dn = E->dalloc<Job>(256)) &&
-            (E->expert_count = E->dalloc<int>((size_t)c.n_layers * std::max(1, c.n_expert)));
+            (E->best = E->dalloc<unsigned long long>((size_t)M * E->lm_grid)) &&
+            (E->part_ml = E->dalloc<float>((size_t)c.n_kv_heads * E->nch * ATT_QMAX * 2)) &&
+            (E->part_o = E->dalloc<float>((size_t)c.n_kv_heads * E->nch * ATT_QMAX * c.head_dim)) &&
+            (E->att_cnt = E->dalloc<int>(c.n_kv_heads)) && (E->rt_cnt = E->dalloc<int>(1)) &&
+            (E->gu_cnt = E->dalloc<int>((size_t)nv * (nff / 256 + 1))) && (E->chosen = E->dalloc<int>(16 * 32)) &&
+            (E->nkeep = E->dalloc<int>(16)) && (E->weights = E->dalloc<float>(16 * 32)) && (E->jobs = E->dalloc<Job>(512)) &&
+            (E->expert_count = E->dalloc<int>((size_t)c.n_layers * std::max(1, c.n_expert))) &&
+            E->q8alloc(E->aq, M, ((E->q_dim + 255) / 256) * 256) && E->q8alloc(E->xq2, M, ((c.dim + 255) / 256) * 256) &&
+            E->q8alloc(E->xq, M, ((c.dim + 255) / 256) * 256) && E->q8alloc(E->hq, nv, nff);
   if (!ok) return fail("spx_engine_prepare: out of device memory");
   for (auto &ly : E->L)
     if (ly.moe && !(ly.njobs = E->dalloc<int>(1))) return fail("out of device memory");
@@ -400,6 +496,7 @@ int spx_engine_prepare(spx_engine *E) {
       tab[(size_t)p * half + i] = make_float2(cosf(ang), sinf(ang));
     }
   SPX_HIP(hipMemcpy(E->rope, tab.data(), sizeof(float2) * tab.size(), hipMemcpyHostToDevice));
+  SPX_HIP(hipDeviceSynchronize());
   E->n_used = nu;
   E->prepared = true;
   return 0;
@@ -439,7 +536,7 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
       float ms = 0.0f;
       SPX_HIP(hipEventElapsedTime(&ms, r.a, r.b));
       double bytes = r.bytes;
-      if (r.per_expert) bytes = r.bytes * nj[r.layer];  // wbytes() is one expert's slab
+      if (r.per_expert) bytes = r.bytes * nj[r.layer];  // one expert's slab per selected expert
       if (r.cls == PC_ATTN) bytes = (double)kv_pos_bytes * (start_pos + m);  // KV bytes read once per pass
       E->prof_us[r.cls] += 1000.0 * ms;
       E->prof_bytes[r.cls] += bytes;
@@ -482,10 +579,10 @@ int spx_engine_decode(spx_engine *E, int32_t token, int start_pos, int n, int32_
 int spx_engine_debug_read(spx_engine *E, const char *what, void *host, int64_t bytes) {
   if (!E || !what || !host) return fail("null argument");
   const std::string w(what);
-  const void *src = w == "x" ? (const void *)E->x : w == "xn" ? (const void *)E->xn : w == "q" ? (const void *)E->q
+  const void *src = w == "x" ? (const void *)E->xA : w == "xn" ? (const void *)E->xn : w == "q" ? (const void *)E->q
                   : w == "att" ? (const void *)E->att : w == "proj" ? (const void *)E->proj : w == "rlog" ? (const void *)E->rlog
                   : w == "chosen" ? (const void *)E->chosen : w == "weights" ? (const void *)E->weights
-                  : w == "nkeep" ? (const void *)E->nkeep : w == "h" ? (const void *)E->h : w == "y" ? (const void *)E->y : nullptr;
+                  : w == "nkeep" ? (const void *)E->nkeep : w == "h" ? (const void *)E->h : w == "y" ? (const void *)E->ffn : nullptr;
   if (!src) return fail("spx_engine_debug_read: unknown buffer " + w);
   SPX_HIP(hipStreamSynchronize(E->ctx->stream));
   SPX_HIP(hipMemcpy(host, src, (size_t)bytes, hipMemcpyDeviceToHost));

@@ -1,0 +1,1639 @@
+// Fused decode / verify kernels for gfx950 (wave64). One forward pass of m <= 16 token rows
+// is, per layer, six launches:
+//   k_mv_kq / k_mv_f  (attn_norm prologue) q, k, v projections in one launch
+//   k_attn            q/k norm, RoPE, K/V cache write, split-K attention, last-workgroup merge
+//                     (+ Q8_K of the output)
+//   k_mv_*            attn_output projection
+//   k_router          (ffn_norm prologue) F32 router + last-workgroup routing and job lists
+//   k_gateup          grouped gate/up + SwiGLU (+ Q8_K of h by the last workgroup per block)
+//   k_down            grouped down projection + weighted combine in chosen order
+// (dense FFN layers: k_gateup with the ffn_norm prologue, then k_mv_* for ffn_down).
+// Positions and row counts come from the device-side step record, so a captured HIP graph
+// replays at any position. References are to smollm_chat.rs unless a file is named.
+#include <float.h>
+
+#include "fused.h"
+
+namespace spx {
+
+// ------------------------------------------------------------------ wave reductions
+#define SPX_DPPF(v, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), (ctrl), 0xF, 0xF, true))
+
+// Butterfly sum / max over the 64 lanes; every lane gets the same bits (each step combines
+// a value with its partner's, and fp add / max are commutative).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = v + SPX_DPPF(v, 0xB1);
+  v = v + SPX_DPPF(v, 0x4E);
+  v = v + SPX_DPPF(v, 0x141);
+  v = v + SPX_DPPF(v, 0x140);
+  v = v + __shfl_xor(v, 16);
+  v = v + __shfl_xor(v, 32);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, SPX_DPPF(v, 0xB1));
+  v = fmaxf(v, SPX_DPPF(v, 0x4E));
+  v = fmaxf(v, SPX_DPPF(v, 0x141));
+  v = fmaxf(v, SPX_DPPF(v, 0x140));
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+#define SPX_DPP64(v, ctrl)                                                                              \
+  (((unsigned long long)(uint32_t)__builtin_amdgcn_mov_dpp((int)((v) >> 32), (ctrl), 0xF, 0xF, true) << 32) | \
+   (unsigned long long)(uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v), (ctrl), 0xF, 0xF, true))
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+  unsigned long long w;
+  w = SPX_DPP64(v, 0xB1); v = w > v ? w : v;
+  w = SPX_DPP64(v, 0x4E); v = w > v ? w : v;
+  w = SPX_DPP64(v, 0x141); v = w > v ? w : v;
+  w = SPX_DPP64(v, 0x140); v = w > v ? w : v;
+  w = __shfl_xor(v, 16); v = w > v ? w : v;
+  w = __shfl_xor(v, 32); v = w > v ? w : v;
+  return v;
+}
+
+// ------------------------------------------------------------------ cross-workgroup hand-off
+// Values one workgroup leaves for the last workgroup of a kernel go through relaxed
+// agent-scope atomic stores and loads (global_store / global_load with sc1: coherent across
+// the XCDs' L2s per location), so no workgroup has to write back or invalidate a whole L2.
+// arrive(): every store of this workgroup has completed (s_waitcnt 0 + barrier) before one
+// thread bumps the counter; returns the counter's previous value to every thread.
+__device__ __forceinline__ void st_dev(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ float ld_dev(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i2v __attribute__((ext_vector_type(2)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Raw buffer view of [base, base + 2 GB) for agent-coherent (sc1) vector loads and stores that
+// the compiler can batch (unlike atomic loads).
+__device__ __forceinline__ rsrc_t rsrc_of(const void *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ f4v ld_coh4(rsrc_t r, int off) { return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16)); }
+__device__ __forceinline__ f2v ld_coh2(rsrc_t r, int off) { return __builtin_bit_cast(f2v, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 16)); }
+__device__ __forceinline__ void st_coh4(rsrc_t r, int off, f4v v) { __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, v), r, off, 0, 16); }
+__device__ __forceinline__ void st_coh2(rsrc_t r, int off, f2v v) { __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2v, v), r, off, 0, 16); }
+__device__ __forceinline__ int arrive(int *counter) {
+  __shared__ int prev;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) prev = atomicAdd(counter, 1);
+  __syncthreads();
+  return prev;
+}
+
+// ------------------------------------------------------------------ Q8_K of one block
+// quantize_avx2 (quant_q8k.rs:84-121) of 256 values, lane j holding values 4j..4j+3:
+// amax (exact), iscale = 127/amax and d = amax/127 correctly rounded, q = rint(x*iscale)
+// saturated to int8, bsums = sums of 16 codes; zero or non-finite amax -> zeros. Writes the
+// permuted layout (lane j's dword goes to [l = j % 8][k = j / 8]).
+__device__ __forceinline__ void q8k_block_store(float4 x, float amax, uint32_t *q, float *d, int *bs) {
+  const int lane = threadIdx.x & 63;
+  int qv[4] = {0, 0, 0, 0};
+  float dv = 0.0f;
+  if (amax > 0.0f && !isinf(amax)) {
+    const float iscale = __fdiv_rn(127.0f, amax);
+    dv = __fdiv_rn(amax, 127.0f);
+    const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) qv[j] = (int)fminf(fmaxf(rintf(__fmul_rn(xs[j], iscale)), -128.0f), 127.0f);
+  }
+  q[(lane & 7) * 8 + (lane >> 3)] = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
+                                    ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
+  const int s = quad_sum(qv[0] + qv[1] + qv[2] + qv[3]);
+  if ((lane & 3) == 0) bs[lane >> 2] = s;
+  if (lane == 0) *d = dv;
+}
+
+__device__ __forceinline__ float amax4(float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); }
+
+// ------------------------------------------------------------------ prologue
+// Residual add + RMSNorm of row b by one wavefront (lane j holds float4 chunks j + 64t,
+// t < PRO_NT, so dim <= 256 * PRO_NT).
+// Outputs (each optional): xs = normalised fp32 row, (yq, yd, ybs) = its permuted Q8_K;
+// the writer also stores the sum to p.xb and the outputs to p.xn_out / p.q_out.
+__device__ __forceinline__ void pro_row(const Pro &p, int b, bool writer, float *xs, uint32_t *yq, float *yd, int *ybs) {
+  const int lane = threadIdx.x & 63;
+  const int dim = p.dim, n4 = dim >> 2, nt = (n4 + 63) >> 6;
+  const float4 *xa4 = reinterpret_cast<const float4 *>(p.xa + (int64_t)b * dim);
+  const float4 *pa4 = p.pa ? reinterpret_cast<const float4 *>(p.pa + (int64_t)b * dim) : nullptr;
+  const float4 *w4 = reinterpret_cast<const float4 *>(p.nw);
+  float4 xr[PRO_NT];
+  float ss = 0.0f;
+#pragma unroll
+  for (int t = 0; t < PRO_NT; t++) {
+    xr[t] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (t < nt) {
+      const int f = lane + 64 * t;
+      if (f < n4) {
+        float4 v = xa4[f];
+        if (pa4) {
+          const float4 q = pa4[f];
+          v.x = v.x + p.rscale * q.x; v.y = v.y + p.rscale * q.y;
+          v.z = v.z + p.rscale * q.z; v.w = v.w + p.rscale * q.w;
+        }
+        xr[t] = v;
+      }
+      ss = fmaf(xr[t].x, xr[t].x, ss); ss = fmaf(xr[t].y, xr[t].y, ss);
+      ss = fmaf(xr[t].z, xr[t].z, ss); ss = fmaf(xr[t].w, xr[t].w, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)dim) + p.eps));
+  float am[PRO_NT];
+#pragma unroll
+  for (int t = 0; t < PRO_NT; t++) {
+    am[t] = 0.0f;
+    if (t < nt) {
+      const int f = lane + 64 * t;
+      if (f < n4) {
+        if (writer && p.xb) reinterpret_cast<float4 *>(p.xb + (int64_t)b * dim)[f] = xr[t];
+        const float4 w = w4[f];
+        float4 v = xr[t];
+        v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
+        xr[t] = v;
+        if (xs) reinterpret_cast<float4 *>(xs)[f] = v;
+        if (writer && p.xn_out) reinterpret_cast<float4 *>(p.xn_out + (int64_t)b * dim)[f] = v;
+        am[t] = amax4(v);
+      }
+    }
+  }
+  if (!yq && !(writer && p.q_out.q)) return;
+  // Q8_K (dim % 256 == 0 here): block t = chunks 64t .. 64t+63
+#pragma unroll
+  for (int t = 0; t < PRO_NT; t++)
+    if (t < nt) am[t] = wave_max(am[t]);
+  const int nb = dim >> 8;
+#pragma unroll
+  for (int t = 0; t < PRO_NT; t++) {
+    if (t < nt) {
+      if (yq) q8k_block_store(xr[t], am[t], yq + t * 64, yd + t, ybs + t * 16);
+      if (writer && p.q_out.q) {
+        const int64_t vb = (int64_t)b * nb + t;
+        q8k_block_store(xr[t], am[t], p.q_out.q + vb * 64, p.q_out.d + vb, reinterpret_cast<int *>(p.q_out.bs + vb * 8));
+      }
+    }
+  }
+}
+
+// LDS image of m permuted Q8_K vectors of `dim` columns: q [m][dim/4], d [m][nb], bs [m][nb][8].
+__host__ __device__ inline size_t ldsq_dbytes(int mt, int dim) { return ((size_t)mt * (dim / 256) * 4 + 15) & ~(size_t)15; }
+__device__ __forceinline__ Q8KP ldsq_of(uint8_t *smem, int mt, int dim) {
+  Q8KP r;
+  r.q = reinterpret_cast<uint32_t *>(smem);
+  r.d = reinterpret_cast<float *>(smem + (size_t)mt * dim);
+  r.bs = reinterpret_cast<int2 *>(smem + (size_t)mt * dim + ldsq_dbytes(mt, dim));
+  return r;
+}
+__host__ __device__ inline size_t ldsq_bytes(int mt, int dim) { return (size_t)mt * dim + ldsq_dbytes(mt, dim) + (size_t)mt * (dim / 256) * 64; }
+
+// All waves of the workgroup: prologue of rows 0..m-1 into LDS as permuted Q8_K.
+template <int NW>
+__device__ __forceinline__ void pro_q8k(const Pro &p, int m, const Q8KP &lq, bool writer) {
+  const int wave = threadIdx.x >> 6, nb = p.dim >> 8;
+  for (int v = wave; v < m; v += NW)
+    pro_row(p, v, writer, nullptr, lq.q + (int64_t)v * (p.dim >> 2), lq.d + v * nb, reinterpret_cast<int *>(lq.bs + v * nb * 8));
+  __syncthreads();
+}
+// ... or as fp32 rows [m][dim].
+template <int NW>
+__device__ __forceinline__ void pro_f32(const Pro &p, int v0, int nv, float *xs, bool writer) {
+  const int wave = threadIdx.x >> 6;
+  for (int v = wave; v < nv; v += NW) pro_row(p, v0 + v, writer, xs + (int64_t)v * p.dim, nullptr, nullptr, nullptr);
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------ integer row walker
+template <int T, int D>
+__device__ __forceinline__ void kq_preload(KQRaw<T> *buf, const Planes &pl, int64_t g0, int nb, int l) {
+#pragma unroll
+  for (int j = 0; j < D; j++)
+    if (j < nb) buf[j].load(pl, g0 + j, l);
+}
+
+// Continues kq_preload: blocks in order, D in flight. Vector v of this row group is
+// activation vector vidx[v] of y (cols columns); mv = the row group's vector count.
+template <int T, int MT, int D>
+__device__ __forceinline__ void kq_walk(KQRaw<T> *buf, const Planes &pl, int64_t g0, int nb, const Q8KP &y, const int *vidx, int mv, int l,
+                                        float *res) {
+  float acc[MT], corr[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) { acc[v] = 0.0f; corr[v] = 0.0f; }
+  for (int i0 = 0; i0 < nb; i0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; j++) {
+      const int i = i0 + j;
+      if (i < nb) {
+        KQDec<T> dec;
+        dec.decode(buf[j], l);
+        if (i + D < nb) buf[j].load(pl, g0 + i + D, l);
+#pragma unroll
+        for (int v = 0; v < MT; v++) {
+          if (v < mv) {
+            const int64_t vb = (int64_t)vidx[v] * nb + i;
+            const uint4 *yq = reinterpret_cast<const uint4 *>(y.q + vb * 64 + 8 * l);
+            const uint4 y0 = yq[0], y1 = yq[1];
+            const float xd = y.d[vb];
+            const int2 bs = y.bs[vb * 8 + l];
+            int P, s;
+            dec.dot(y0, y1, bs, P, s);
+            s = sum8(s);
+            corr[v] = corr[v] + dec.corr_term(xd, s);
+            acc[v] = fmaf(dec.d * xd, (float)P, acc[v]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < MT; v++) res[v] = hsum_rows8(acc[v]) - corr[v];
+}
+
+template <int MT>
+constexpr int kq_depth() { return MT <= 2 ? 8 : MT <= 8 ? 4 : 2; }
+
+// ------------------------------------------------------------------ float row walker
+// Q8_0 / Q5_0 weights x fp32 activations (quant.rs:48-161, quant_multi.rs:168-190): lane l
+// of the row group takes blocks l, l+8, ...; per block s = sum q*x in four fixed chains,
+// acc = fma(d, s, acc); the row is the 8-lane tree. The order is this kernel's own (fixed
+// for every batch size), within 1e-4 of the reference's.
+template <int T> struct FRaw;
+template <> struct FRaw<T_Q8_0> {
+  uint4 c0, c1;
+  uint32_t d;
+  __device__ __forceinline__ void load(const Planes &pl, int64_t g) {
+    c0 = ld16(pl.p0 + g * 32);
+    c1 = ld16(pl.p0 + g * 32 + 16);
+    d = *reinterpret_cast<const uint16_t *>(pl.p3 + g * 2);
+  }
+  __device__ __forceinline__ void decode(float q[32]) const {
+    const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) q[4 * k + j] = (float)(int8_t)(cw[k] >> (8 * j));
+  }
+};
+template <> struct FRaw<T_Q5_0> {
+  uint4 c;
+  uint32_t qh, d;
+  __device__ __forceinline__ void load(const Planes &pl, int64_t g) {
+    c = ld16(pl.p0 + g * 16);
+    qh = *reinterpret_cast<const uint32_t *>(pl.p1 + g * 4);
+    d = *reinterpret_cast<const uint16_t *>(pl.p3 + g * 2);
+  }
+  __device__ __forceinline__ void decode(float q[32]) const {  // j<16: low nibble | bit j; j>=16: high nibble | bit j
+    const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int e = 4 * k + j;
+        const uint32_t byte = (cw[k] >> (8 * j)) & 0xffu;
+        q[e] = (float)((int)((byte & 0xFu) | (((qh >> e) & 1u) << 4)) - 16);
+        q[e + 16] = (float)((int)((byte >> 4) | (((qh >> (e + 16)) & 1u) << 4)) - 16);
+      }
+  }
+};
+
+template <int T, int MT, int D>
+__device__ __forceinline__ void f_walk(const Planes &pl, int64_t grow, int nb, const float *x, int64_t ld_x, const int *vidx, int mv, int l,
+                                       float *res) {
+  float acc[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) acc[v] = 0.0f;
+  const int64_t g0 = grow * nb;
+  const int nmine = nb > l ? (nb - l + 7) >> 3 : 0;
+  FRaw<T> buf[D];
+#pragma unroll
+  for (int j = 0; j < D; j++)
+    if (j < nmine) buf[j].load(pl, g0 + l + 8 * j);
+  for (int k0 = 0; k0 < nmine; k0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; j++) {
+      const int k = k0 + j;
+      if (k < nmine) {
+        const int i = l + 8 * k;
+        float q[32];
+        buf[j].decode(q);
+        const float d = h2f(buf[j].d);
+        if (k + D < nmine) buf[j].load(pl, g0 + l + 8 * (k + D));
+#pragma unroll
+        for (int v = 0; v < MT; v++) {
+          if (v < mv) {
+            const float4 *xv = reinterpret_cast<const float4 *>(x + (int64_t)vidx[v] * ld_x + (int64_t)i * 32);
+            float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) {
+              const float4 xx = xv[kk];
+              s0 = fmaf(q[4 * kk + 0], xx.x, s0);
+              s1 = fmaf(q[4 * kk + 1], xx.y, s1);
+              s2 = fmaf(q[4 * kk + 2], xx.z, s2);
+              s3 = fmaf(q[4 * kk + 3], xx.w, s3);
+            }
+            acc[v] = fmaf(d, (s0 + s1) + (s2 + s3), acc[v]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < MT; v++) res[v] = hsum_rows8(acc[v]);
+}
+
+// F32 weights (quant.rs:1409-1502 semantics): lane l of the row group takes float4 chunks
+// l, l+8, ... in one fma chain per vector; the row is the 8-lane tree.
+template <int MT>
+__device__ __forceinline__ void f32_walk(const Planes &pl, int64_t grow, int64_t cols, const float *x, int64_t ld_x, const int *vidx, int mv,
+                                         int l, float *res) {
+  float acc[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) acc[v] = 0.0f;
+  const float4 *wr = reinterpret_cast<const float4 *>(pl.p0 + grow * cols * 4);
+  const int64_t n4 = cols / 4;
+  for (int64_t k = l; k < n4; k += 8) {
+    const float4 w = wr[k];
+#pragma unroll
+    for (int v = 0; v < MT; v++) {
+      if (v < mv) {
+        const float4 xx = reinterpret_cast<const float4 *>(x + (int64_t)vidx[v] * ld_x)[k];
+        acc[v] = fmaf(w.x, xx.x, acc[v]);
+        acc[v] = fmaf(w.y, xx.y, acc[v]);
+        acc[v] = fmaf(w.z, xx.z, acc[v]);
+        acc[v] = fmaf(w.w, xx.w, acc[v]);
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < MT; v++) res[v] = hsum_rows8(acc[v]);
+}
+
+template <int MT>
+constexpr int f_depth() { return MT <= 2 ? 4 : 2; }
+
+// ------------------------------------------------------------------ greedy-pick keys
+// logits / logit_scale, then the last maximum under f32 total order (max_by(total_cmp),
+// :3661-3671): key = total-order bits as unsigned, packed above the row index so that the
+// larger packed value is the larger logit and, on ties, the higher index.
+__device__ __forceinline__ unsigned long long pick_key(float v, float lscale, int64_t row) {
+  const float x = lscale != 1.0f ? v / lscale : v;
+  const int i = __float_as_int(x);
+  const int k = i ^ (int)(((unsigned)(i >> 31)) >> 1);
+  return ((unsigned long long)((unsigned)k ^ 0x80000000u) << 32) | (unsigned long long)(uint32_t)row;
+}
+
+template <int MT, int NW>
+__device__ __forceinline__ void best_flush(const MVArgs &a, unsigned long long (&bestv)[MT], int m) {
+  __shared__ unsigned long long sb[NW][MT];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int v = 0; v < MT; v++) {
+    const unsigned long long w = wave_max_u64(bestv[v]);
+    if (lane == 0) sb[wave][v] = w;
+  }
+  __syncthreads();
+  if (threadIdx.x < MT && (int)threadIdx.x < m) {
+    unsigned long long b = 0;
+    for (int w = 0; w < NW; w++) b = sb[w][threadIdx.x] > b ? sb[w][threadIdx.x] : b;
+    a.best[(int64_t)threadIdx.x * a.nbest + blockIdx.x] = b;
+  }
+}
+
+// ------------------------------------------------------------------ integer tiles in LDS
+// A wavefront's 8 row slots x nb blocks of a K-quant tensor are copied into LDS with direct
+// global->LDS loads (global_load_lds_dwordx4: lane i's 16 bytes land at M0 + 16 i), then the
+// blocks are walked from LDS in a compact loop. LDS tile layout, plane by plane, slot-major:
+//   Q4_K: codes [8][nb][128], headers [8][nb][16]
+//   Q6_K: ql [8][nb][128], qh [8][nb][64], scales [8][nb][16], d [8][nb] as the dword that
+//         holds the 2-byte d (the dword at the record's address rounded down to 4)
+typedef __attribute__((address_space(3))) void *lds_ptr;
+template <int T> struct KQPlanes;
+template <> struct KQPlanes<T_Q4K> {
+  static constexpr int NP = 2;
+  __host__ __device__ static constexpr int rec(int k) { return k == 0 ? 128 : 16; }   // global bytes per block
+  __host__ __device__ static constexpr int lrec(int k) { return rec(k); }             // LDS bytes per block
+};
+template <> struct KQPlanes<T_Q6K> {
+  static constexpr int NP = 4;
+  __host__ __device__ static constexpr int rec(int k) { return k == 0 ? 128 : k == 1 ? 64 : k == 2 ? 16 : 2; }
+  __host__ __device__ static constexpr int lrec(int k) { return k == 3 ? 4 : rec(k); }
+};
+__host__ __device__ constexpr int tile_bytes_per_block() { return 128 + 64 + 16 + 4; }  // the larger of Q4_K (144) and Q6_K (212)
+
+// src(s) = global row index (expert * rows + row) of slot s, or -1 for an empty slot.
+template <int T, class F>
+__device__ __forceinline__ void tile_fetch(uint8_t *tile, const Planes &pl, int nb, F src) {
+  const int lane = threadIdx.x & 63;
+  const uint8_t *planes[4] = {pl.p0, pl.p1, pl.p2, pl.p3};
+  int off = 0;
+#pragma unroll
+  for (int k = 0; k < KQPlanes<T>::NP; k++) {
+    const int R = KQPlanes<T>::rec(k);
+    if (R >= 16) {
+      const int per = nb * R / 16, total = 8 * per;
+      for (int p0 = 0; p0 < total; p0 += 64) {
+        const int p = p0 + lane, sl = p / per, w = p - sl * per;
+        const int64_t grow = p < total ? src(sl) : -1;
+        if (grow >= 0) __builtin_amdgcn_global_load_lds(planes[k] + grow * nb * R + 16 * w, (lds_ptr)(tile + off + 16 * p0), 16, 0, 0);
+      }
+    } else {  // 2-byte records: the dword holding each
+      const int total = 8 * nb;
+      for (int p0 = 0; p0 < total; p0 += 64) {
+        const int p = p0 + lane, sl = p / nb, w = p - sl * nb;
+        const int64_t grow = p < total ? src(sl) : -1;
+        if (grow >= 0) {
+          const uintptr_t a = reinterpret_cast<uintptr_t>(planes[k] + (grow * nb + w) * 2) & ~(uintptr_t)3;
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(a), (lds_ptr)(tile + off + 4 * p0), 4, 0, 0);
+        }
+      }
+    }
+    off += 8 * nb * KQPlanes<T>::lrec(k);
+  }
+}
+
+// Block i of slot s as lane l needs it. odd = the block's global index is odd (Q6_K d half).
+__device__ __forceinline__ void tile_block(const uint8_t *tile, int nb, int s, int i, int l, bool odd, KQRaw<T_Q4K> &r) {
+  const int rec = s * nb + i;
+  r.c = *reinterpret_cast<const uint4 *>(tile + rec * 128 + 16 * l);
+  r.h = *reinterpret_cast<const uint4 *>(tile + 8 * nb * 128 + rec * 16);
+}
+__device__ __forceinline__ void tile_block(const uint8_t *tile, int nb, int s, int i, int l, bool odd, KQRaw<T_Q6K> &r) {
+  const int rec = s * nb + i;
+  r.ql = *reinterpret_cast<const uint4 *>(tile + rec * 128 + 16 * l);
+  r.qh = *reinterpret_cast<const uint2 *>(tile + 8 * nb * 128 + rec * 64 + 8 * l);
+  r.sc = *reinterpret_cast<const uint4 *>(tile + 8 * nb * 192 + rec * 16);
+  r.d = (*reinterpret_cast<const uint32_t *>(tile + 8 * nb * 208 + rec * 4) >> (odd ? 16 : 0)) & 0xffffu;
+}
+
+// The row of slot s (global row index grow) against vectors vidx[0..mv) of y (LDS or global).
+template <int T, int MT>
+__device__ __forceinline__ void kq_walk_tile(const uint8_t *tile, int nb, int s, int64_t grow, const Q8KP &y, const int *vidx, int mv, int l,
+                                             float *res) {
+  float acc[MT], corr[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) { acc[v] = 0.0f; corr[v] = 0.0f; }
+  const bool odd0 = ((grow * nb) & 1) != 0;
+#pragma unroll 2
+  for (int i = 0; i < nb; i++) {
+    KQRaw<T> r;
+    tile_block(tile, nb, s, i, l, odd0 ^ ((i & 1) != 0), r);
+    KQDec<T> dec;
+    dec.decode(r, l);
+#pragma unroll
+    for (int v = 0; v < MT; v++) {
+      if (v < mv) {
+        const int64_t vb = (int64_t)vidx[v] * nb + i;
+        const uint4 *yq = reinterpret_cast<const uint4 *>(y.q + vb * 64 + 8 * l);
+        const uint4 y0 = yq[0], y1 = yq[1];
+        const float xd = y.d[vb];
+        const int2 bs = y.bs[vb * 8 + l];
+        int P, sc;
+        dec.dot(y0, y1, bs, P, sc);
+        sc = sum8(sc);
+        corr[v] = corr[v] + dec.corr_term(xd, sc);
+        acc[v] = fmaf(dec.d * xd, (float)P, acc[v]);
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < MT; v++) res[v] = hsum_rows8(acc[v]) - corr[v];
+}
+
+// Copies permuted Q8_K vectors vsrc(u), u < nv, of `cols` columns from global y into the LDS
+// image ly (vector u at slot u) with direct loads spread over the workgroup's nw waves. Each
+// region (codes, d, bsums) is contiguous in LDS across vectors, so a wave's destinations are
+// consecutive: 16-byte pieces for codes and bsums, 4-byte pieces for d.
+template <class F>
+__device__ __forceinline__ void stage_q8kp(const Q8KP &ly, const Q8KP &y, int cols, int nv, int nw, F vsrc) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nb = cols >> 8;
+  const int pq = cols / 16, pb = nb * 4;  // 16-byte pieces per vector: codes, bsums (nb * 64 bytes)
+  for (int p0 = wave * 64; p0 < nv * pq; p0 += nw * 64) {
+    const int p = p0 + lane, u = p / pq, w = p - u * pq;
+    if (p < nv * pq)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(y.q) + (int64_t)vsrc(u) * cols + 16 * w,
+                                       (lds_ptr)(reinterpret_cast<uint8_t *>(ly.q) + 16 * p0), 16, 0, 0);
+  }
+  for (int p0 = wave * 64; p0 < nv * pb; p0 += nw * 64) {
+    const int p = p0 + lane, u = p / pb, w = p - u * pb;
+    if (p < nv * pb)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(y.bs + (int64_t)vsrc(u) * nb * 8) + 16 * w,
+                                       (lds_ptr)(reinterpret_cast<uint8_t *>(ly.bs) + 16 * p0), 16, 0, 0);
+  }
+  for (int p0 = wave * 64; p0 < nv * nb; p0 += nw * 64) {
+    const int p = p0 + lane, u = p / nb, w = p - u * nb;
+    if (p < nv * nb)
+      __builtin_amdgcn_global_load_lds(y.d + (int64_t)vsrc(u) * nb + w, (lds_ptr)(reinterpret_cast<uint8_t *>(ly.d) + 4 * p0), 4, 0, 0);
+  }
+}
+
+// ------------------------------------------------------------------ matvec kernels
+// Workgroups of NW wavefronts, 8 rows per wavefront; a workgroup belongs to one segment
+// (all its rows share a dtype). Without a prologue the grid may be smaller than the work:
+// workgroups then stride over it.
+template <int T, int NW>
+__device__ __forceinline__ void mvt_fetch(const Seg &sg, int wg, uint8_t *tiles) {
+  const int wave = threadIdx.x >> 6;
+  const int nb = (int)sg.w.nb;
+  const int64_t ebase = (int64_t)sg.expert * sg.w.rows, rbase = sg.r0 + ((int64_t)wg * NW + wave) * 8;
+  tile_fetch<T>(tiles + (size_t)wave * 8 * nb * tile_bytes_per_block(), sg.w.pl, nb,
+                [&](int sl) -> int64_t { const int64_t r = rbase + sl; return r < sg.r1 ? ebase + r : -1; });
+}
+
+template <int T, int MT, int NW>
+__device__ __forceinline__ void mvt_walk(const MVArgs &a, const Seg &sg, int wg, int m, const uint8_t *tiles, const Q8KP &ly, bool want_best,
+                                         unsigned long long (&bestv)[MT]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int nb = (int)sg.w.nb;
+  const int64_t ebase = (int64_t)sg.expert * sg.w.rows, row = sg.r0 + ((int64_t)wg * NW + wave) * 8 + slot;
+  const bool valid = row < sg.r1;
+  int vidx[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) vidx[v] = v;
+  float res[MT];
+  kq_walk_tile<T, MT>(tiles + (size_t)wave * 8 * nb * tile_bytes_per_block(), nb, slot, ebase + (valid ? row : sg.r1 - 1), ly, vidx, m, l, res);
+  if (valid && l == 0) {
+#pragma unroll
+    for (int v = 0; v < MT; v++)
+      if (v < m) sg.out[(int64_t)v * sg.ld_out + row] = res[v];
+  }
+  if (want_best) {
+#pragma unroll
+    for (int v = 0; v < MT; v++)
+      if (valid && l == 0 && v < m) {
+        const unsigned long long k = pick_key(res[v], a.lscale, row);
+        bestv[v] = k > bestv[v] ? k : bestv[v];
+      }
+  }
+}
+
+// Integer matvec: workgroups of NW wavefronts, 8 rows per wavefront, one segment per
+// workgroup (all its rows share a dtype). Without a prologue the grid may be smaller than the
+// work: workgroups then stride over it. LDS: activations (permuted Q8_K), then one tile per
+// wave; the tile's direct loads are in flight while the prologue or activation copy runs.
+template <int MT, int NW, bool PRO>
+__global__ __launch_bounds__(NW * 64) void k_mvt(const MVArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int m = st ? st->m : a.m;
+  const int cols = (int)a.seg[0].w.cols;
+  const Q8KP ly = ldsq_of(smem, MT, cols);
+  uint8_t *tiles = smem + ((ldsq_bytes(MT, cols) + 15) & ~(size_t)15);
+  unsigned long long bestv[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) bestv[v] = 0;
+  const int total = a.seg[0].wgs + (a.nseg > 1 ? a.seg[1].wgs : 0) + (a.nseg > 2 ? a.seg[2].wgs : 0);
+  bool first = true;
+  for (int t = blockIdx.x; t < total; t += gridDim.x) {
+    int s = 0, wg = t;
+    if (a.nseg > 1 && wg >= a.seg[0].wgs) { wg -= a.seg[0].wgs; s = 1; if (a.nseg > 2 && wg >= a.seg[1].wgs) { wg -= a.seg[1].wgs; s = 2; } }
+    const Seg sg = s == 0 ? a.seg[0] : s == 1 ? a.seg[1] : a.seg[2];
+    const bool q4 = sg.w.dtype == T_Q4K;
+    if (q4) mvt_fetch<T_Q4K, NW>(sg, wg, tiles); else mvt_fetch<T_Q6K, NW>(sg, wg, tiles);
+    if (first) {
+      if (PRO) pro_q8k<NW>(a.pro, m, ly, blockIdx.x == 0);
+      else stage_q8kp(ly, a.y, cols, m, NW, [](int u) { return u; });
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (q4) mvt_walk<T_Q4K, MT, NW>(a, sg, wg, m, tiles, ly, a.best != nullptr, bestv);
+    else mvt_walk<T_Q6K, MT, NW>(a, sg, wg, m, tiles, ly, a.best != nullptr, bestv);
+    __syncthreads();  // the tiles may be refilled by the next task
+    first = false;
+    if (PRO) break;
+  }
+  if (a.best) best_flush<MT, NW>(a, bestv, m);
+}
+
+template <int T, int MT, int NW, bool PRO>
+__device__ __forceinline__ void mv_f_task(const MVArgs &a, const Seg &sg, int wg, int m, uint8_t *smem, bool want_best,
+                                          unsigned long long (&bestv)[MT]) {
+  constexpr int D = f_depth<MT>();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int nb = (int)sg.w.nb;
+  const int64_t rows = sg.w.rows;
+  const int64_t row = sg.r0 + ((int64_t)wg * NW + wave) * 8 + slot;
+  const bool valid = row < sg.r1;
+  const int64_t grow = (int64_t)sg.expert * rows + (valid ? row : sg.r1 - 1);
+  int vidx[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) vidx[v] = v;
+  float res[MT];
+  if constexpr (T == T_F32) {
+    f32_walk<MT>(sg.w.pl, grow, sg.w.cols, a.x, a.ld_x, vidx, m, l, res);
+  } else if (PRO) {
+    float *xl = reinterpret_cast<float *>(smem);
+    pro_f32<NW>(a.pro, 0, m, xl, blockIdx.x == 0);
+    f_walk<T, MT, D>(sg.w.pl, grow, nb, xl, a.pro.dim, vidx, m, l, res);
+  } else {
+    f_walk<T, MT, D>(sg.w.pl, grow, nb, a.x, a.ld_x, vidx, m, l, res);
+  }
+  if (valid && l == 0) {
+#pragma unroll
+    for (int v = 0; v < MT; v++)
+      if (v < m) sg.out[(int64_t)v * sg.ld_out + row] = res[v];
+  }
+  if (want_best) {
+#pragma unroll
+    for (int v = 0; v < MT; v++)
+      if (valid && l == 0 && v < m) {
+        const unsigned long long k = pick_key(res[v], a.lscale, row);
+        bestv[v] = k > bestv[v] ? k : bestv[v];
+      }
+  }
+}
+
+template <int MT, int NW, bool PRO>
+__global__ __launch_bounds__(NW * 64) void k_mv_f(const MVArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int m = st ? st->m : a.m;
+  unsigned long long bestv[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) bestv[v] = 0;
+  const int total = a.seg[0].wgs + (a.nseg > 1 ? a.seg[1].wgs : 0) + (a.nseg > 2 ? a.seg[2].wgs : 0);
+  for (int t = blockIdx.x; t < total; t += gridDim.x) {
+    int s = 0, wg = t;
+    if (a.nseg > 1 && wg >= a.seg[0].wgs) { wg -= a.seg[0].wgs; s = 1; if (a.nseg > 2 && wg >= a.seg[1].wgs) { wg -= a.seg[1].wgs; s = 2; } }
+    const Seg sg = s == 0 ? a.seg[0] : s == 1 ? a.seg[1] : a.seg[2];
+    if (sg.w.dtype == T_Q8_0) mv_f_task<T_Q8_0, MT, NW, PRO>(a, sg, wg, m, smem, a.best != nullptr, bestv);
+    else if (sg.w.dtype == T_Q5_0) mv_f_task<T_Q5_0, MT, NW, PRO>(a, sg, wg, m, smem, a.best != nullptr, bestv);
+    else if (!PRO) mv_f_task<T_F32, MT, NW, false>(a, sg, wg, m, smem, a.best != nullptr, bestv);
+    if (PRO) break;
+  }
+  if (a.best) best_flush<MT, NW>(a, bestv, m);
+}
+
+// ------------------------------------------------------------------ standalone norm / quantize
+// Residual + RMSNorm of each row (one wavefront per row): writes xb, xn_out, q_out.
+__global__ __launch_bounds__(64) void k_norm(const Pro p, const StepRec *st) {
+  const int b = blockIdx.x;
+  if (st && b >= st->m) return;
+  pro_row(p, b, true, nullptr, nullptr, nullptr, nullptr);
+}
+
+// fp32 rows -> permuted Q8_K, one wavefront per 256-block.
+__global__ __launch_bounds__(256) void k_q8kp_quantize(const float *x, int64_t n, int64_t ld_x, int m, Q8KP out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nb = n / 256, gb = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gb >= nb * m) return;
+  const int64_t v = gb / nb, b = gb % nb;
+  const float4 xv = reinterpret_cast<const float4 *>(x + v * ld_x + b * 256)[lane];
+  const float am = wave_max(amax4(xv));
+  const int64_t vb = v * nb + b;
+  q8k_block_store(xv, am, out.q + vb * 64, out.d + vb, reinterpret_cast<int *>(out.bs + vb * 8));
+}
+
+// Reference-layout Q8_K (d, qs, bsums) -> permuted layout.
+__global__ __launch_bounds__(64) void k_q8kp_from_ref(const float *d, const int8_t *qs, const int16_t *bs, int64_t n, Q8KP out) {
+  const int lane = threadIdx.x;
+  const int64_t vb = blockIdx.x;  // (vector, block)
+  const uint32_t w = reinterpret_cast<const uint32_t *>(qs + vb * 256)[lane];
+  out.q[vb * 64 + (lane & 7) * 8 + (lane >> 3)] = w;
+  if (lane < 16) reinterpret_cast<int *>(out.bs + vb * 8)[lane] = (int)bs[vb * 16 + lane];
+  if (lane == 0 && d) out.d[vb] = d[vb];
+}
+
+// Per-block integers of one row against one vector (probe): sums[2i] = sum over the 8 lanes
+// of P (the block's scaled dot), sums[2i+1] = the correction integer (Q6_K: 32 * s).
+template <int T>
+__global__ __launch_bounds__(64) void k_kq_block_sums(TensorView w, int expert, int64_t row, Q8KP y, int32_t *sums) {
+  const int lane = threadIdx.x, l = lane & 7;
+  const int64_t i = (int64_t)blockIdx.x * 8 + (lane >> 3);
+  const bool ok = i < w.nb;
+  const int64_t g = ((int64_t)expert * w.rows + row) * w.nb + (ok ? i : 0);
+  KQRaw<T> r;
+  r.load(w.pl, g, l);
+  KQDec<T> dec;
+  dec.decode(r, l);
+  const int64_t ib = ok ? i : 0;
+  const uint4 *yq = reinterpret_cast<const uint4 *>(y.q + ib * 64 + 8 * l);
+  int P, s;
+  dec.dot(yq[0], yq[1], y.bs[ib * 8 + l], P, s);
+  P = sum8(P);
+  s = sum8(s);
+  if (ok && l == 0) { sums[2 * i] = P; sums[2 * i + 1] = T == T_Q6K ? 32 * s : s; }
+}
+
+// ------------------------------------------------------------------ embedding
+// dequant_row (quant.rs:1548-1660) of token rows, times embedding_scale (:3381-3388).
+__global__ __launch_bounds__(256) void k_embed(TensorView e, const StepRec *st, float *x, int64_t ld_x, float escale) {
+  const int b = blockIdx.x;
+  if (b >= st->m) return;
+  const int64_t tok = st->ids[b];
+  const int64_t cols = e.cols;
+  float *out = x + b * ld_x;
+  for (int64_t j = threadIdx.x; j < cols; j += 256) {
+    float v = 0.0f;
+    if (e.dtype == T_F32) {
+      v = reinterpret_cast<const float *>(e.pl.p0)[tok * cols + j];
+    } else if (e.dtype == T_Q8_0) {
+      const int64_t g = tok * e.nb + j / 32;
+      const float dd = h2f(*reinterpret_cast<const uint16_t *>(e.pl.p3 + g * 2));
+      v = (float)(int8_t)e.pl.p0[g * 32 + j % 32] * dd;
+    } else if (e.dtype == T_Q5_0) {
+      const int64_t g = tok * e.nb + j / 32;
+      const int k = (int)(j % 32), l = k & 15;
+      const float dd = h2f(*reinterpret_cast<const uint16_t *>(e.pl.p3 + g * 2));
+      const uint32_t qh = *reinterpret_cast<const uint32_t *>(e.pl.p1 + g * 4);
+      const int byte = e.pl.p0[g * 16 + l];
+      const int nib = k < 16 ? (byte & 0xF) : (byte >> 4);
+      const int q = nib | (int)(((qh >> k) & 1u) << 4);
+      v = (float)(q - 16) * dd + 0.0f;
+    } else if (e.dtype == T_Q4K) {  // element 64c + 32hi + t: byte qs[32c + t] (device offset 16(t/4) + 4c + t%4)
+      const int64_t g = tok * e.nb + j / 256;
+      const int k = (int)(j % 256), c = k / 64, t = k % 32, hi = (k % 64) >= 32;
+      const uint8_t *hd = e.pl.p1 + g * 16;
+      const float dd = h2f(hd[0] | (hd[1] << 8)), dm = h2f(hd[2] | (hd[3] << 8));
+      const uint8_t *s = hd + 4;
+      const int jj = 2 * c + hi;
+      int sc, mn;
+      if (jj < 4) { sc = s[jj] & 63; mn = s[jj + 4] & 63; }
+      else { sc = (s[jj + 4] & 0xF) | ((s[jj - 4] >> 6) << 4); mn = (s[jj + 4] >> 4) | ((s[jj] >> 6) << 4); }
+      const int byte = e.pl.p0[g * 128 + 16 * (t >> 2) + 4 * c + (t & 3)];
+      const int q = hi ? (byte >> 4) : (byte & 0xF);
+      v = dd * (float)sc * (float)q - dm * (float)mn;
+    } else if (e.dtype == T_Q6K) {  // element 128h + 32mq + t
+      const int64_t g = tok * e.nb + j / 256;
+      const int k = (int)(j % 256), h = k / 128, r = k % 128, mq = r / 32, t = r % 32;
+      const int lb = 16 * (t >> 2) + 8 * h + 4 * (mq & 1) + (t & 3);
+      const int hb = 8 * (t >> 2) + 4 * h + (t & 3);
+      const int qlb = e.pl.p0[g * 128 + lb], qhb = e.pl.p1[g * 64 + hb];
+      const int8_t *sc = reinterpret_cast<const int8_t *>(e.pl.p2 + g * 16);
+      const float dd = h2f(*reinterpret_cast<const uint16_t *>(e.pl.p3 + g * 2));
+      const int q = ((mq >> 1) ? (qlb >> 4) : (qlb & 0xF)) | (((qhb >> (2 * mq)) & 3) << 4);
+      v = dd * (float)sc[h * 8 + t / 16 + 2 * mq] * (float)(q - 32);
+    }
+    if (escale != 1.0f) v *= escale;
+    out[j] = v;
+  }
+}
+
+// ------------------------------------------------------------------ attention
+// One workgroup per (position chunk, kv head): every row's query heads of the group (after
+// bias, per-head RMSNorm and RoPE, :3226-3248 / :3432-3448) against the chunk's K/V (f16
+// cache), causal per row (row b sees positions <= start + b), online softmax per 64-position
+// sub-chunk; the new K/V rows that fall in the chunk are normed/rotated and written to the
+// cache first. Each workgroup leaves (max, sum, unnormalised output) per query; the last one
+// to finish merges the chunks (flash-decoding) and writes the output, optionally as Q8_K.
+__device__ __forceinline__ void head_prep(const float *src, const float *bias, const float *nw, const float2 *rope_row, int hd, int neox,
+                                          float eps, float &e0, float &e1) {
+  const int lane = threadIdx.x & 63, half = hd >> 1;
+  const bool act = lane < half;
+  const int da = neox ? lane : 2 * lane, db = neox ? lane + half : 2 * lane + 1;
+  float x0 = act ? src[da] : 0.0f, x1 = act ? src[db] : 0.0f;
+  if (bias && act) { x0 += bias[da]; x1 += bias[db]; }
+  if (nw) {
+    const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)hd) + eps));
+    if (act) { x0 = x0 * inv * nw[da]; x1 = x1 * inv * nw[db]; }
+  }
+  if (rope_row && act) {  // Rope::rotate (:1404-1419)
+    const float c = rope_row[lane].x, s = rope_row[lane].y;
+    const float r0 = x0 * c - x1 * s, r1 = x0 * s + x1 * c;
+    x0 = r0;
+    x1 = r1;
+  }
+  e0 = x0;
+  e1 = x1;
+}
+
+template <int NU>
+__device__ __forceinline__ void attn_load_kv(const AttnArgs &a, int64_t cache0, int s0, int p_hi, int pp, int d0, uint32_t (&kr)[4 * NU],
+                                             uint32_t (&vr)[4 * NU]) {
+  const int pos = min(s0 + pp, p_hi - 1);
+  const uint4 *kp = reinterpret_cast<const uint4 *>(a.kc + cache0 + (int64_t)pos * a.kv_dim + d0);
+  const uint4 *vp = reinterpret_cast<const uint4 *>(a.vc + cache0 + (int64_t)pos * a.kv_dim + d0);
+#pragma unroll
+  for (int u = 0; u < NU; u++) {
+    const uint4 k4 = kp[u], v4 = vp[u];
+    kr[4 * u] = k4.x; kr[4 * u + 1] = k4.y; kr[4 * u + 2] = k4.z; kr[4 * u + 3] = k4.w;
+    vr[4 * u] = v4.x; vr[4 * u + 1] = v4.y; vr[4 * u + 2] = v4.z; vr[4 * u + 3] = v4.w;
+  }
+}
+
+template <int HD, int NGM>
+__global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int KS = HD + 8;          // padded K/V row (halves) in LDS
+  constexpr int DQ = HD / 4;          // dims per quarter (score phase)
+  constexpr int NU = DQ / 8;          // 16-byte pieces per quarter
+  constexpr int DP = HD / 32;         // dims per thread (PV phase)
+  const int h = blockIdx.y, c = blockIdx.x;
+  const int m = st->m, start = st->start, total = start + m;
+  const int g = a.n_heads / a.n_kv, NQ = m * g, NG = (NQ + 7) >> 3;
+  int span = (total + a.nch - 1) / a.nch;
+  span = (span + 15) & ~15;
+  const int nch = (total + span - 1) / span;
+  if (c >= nch) return;
+  const int p_lo = c * span, p_hi = min(p_lo + span, total);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  float *qs = reinterpret_cast<float *>(smem);                // [NQ][HD] queries, later the merged output
+  __half *ks = reinterpret_cast<__half *>(qs + NQ * HD);      // [64][KS]
+  __half *vs = ks + 64 * KS;                                  // [64][KS]
+  float *ps = reinterpret_cast<float *>(vs + 64 * KS);        // [8][64]
+  float *sm = ps + 8 * 64, *sl = sm + ATT_QMAX, *sa = sl + ATT_QMAX;  // running max, sum; group alpha [8]
+  float *wsm = sa + 8;                                        // merge weights [NQ][64]
+  const int64_t cache0 = (int64_t)a.layer * a.max_seq * a.kv_dim + (int64_t)h * HD;
+  const int half = HD / 2;
+
+  // 1. queries -> LDS; new K/V rows of this chunk -> cache
+  const int da = a.neox ? lane : 2 * lane, db = a.neox ? lane + half : 2 * lane + 1;
+  for (int qi = wave; qi < NQ; qi += 4) {
+    const int b = qi / g, head = h * g + qi % g;
+    float e0, e1;
+    head_prep(a.q + (int64_t)b * a.n_heads * HD + head * HD, a.q_bias ? a.q_bias + head * HD : nullptr, a.q_norm,
+              a.rope + (int64_t)(start + b) * half, HD, a.neox, a.eps, e0, e1);
+    if (lane < half) { qs[qi * HD + da] = e0; qs[qi * HD + db] = e1; }
+  }
+  for (int b = wave; b < m; b += 4) {
+    const int pos = start + b;
+    if (pos < p_lo || pos >= p_hi) continue;
+    float e0, e1;
+    head_prep(a.k + (int64_t)b * a.kv_dim + h * HD, a.k_bias ? a.k_bias + h * HD : nullptr, a.k_norm,
+              a.rope + (int64_t)pos * half, HD, a.neox, a.eps, e0, e1);
+    __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim;
+    if (lane < half) { kd[da] = __float2half_rn(e0); kd[db] = __float2half_rn(e1); }
+    head_prep(a.v + (int64_t)b * a.kv_dim + h * HD, a.v_bias ? a.v_bias + h * HD : nullptr, nullptr, nullptr, HD, a.neox, a.eps, e0, e1);
+    __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim;
+    if (lane < half) { vd[da] = __float2half_rn(e0); vd[db] = __float2half_rn(e1); }
+  }
+  for (int i = tid; i < NQ; i += 256) { sm[i] = -INFINITY; sl[i] = 0.0f; }
+  __syncthreads();  // the new K/V rows are visible to this workgroup's loads
+
+  // 2. sub-chunks of 64 positions. Loader: position lp = tid / 4, quarter lq = tid % 4.
+  // Scores: query jq = tid / 32, position group sg = (tid / 4) % 8 (positions sg + 8k), quarter qq.
+  // PV: query jq, dims dd0 .. dd0 + DP.
+  const int lp = tid >> 2, lq = tid & 3;
+  const int jq = tid >> 5, sg = (tid >> 2) & 7, qq = tid & 3, dd0 = (tid & 31) * DP;
+  uint32_t kr[4 * NU], vr[4 * NU];
+  attn_load_kv<NU>(a, cache0, p_lo, p_hi, lp, lq * DQ, kr, vr);
+  float o[NGM][DP];
+#pragma unroll
+  for (int G = 0; G < NGM; G++)
+#pragma unroll
+    for (int d = 0; d < DP; d++) o[G][d] = 0.0f;
+  for (int s0 = p_lo; s0 < p_hi; s0 += 64) {
+    __syncthreads();  // previous sub-chunk is done with ks / vs / ps
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+      reinterpret_cast<uint4 *>(ks + lp * KS + lq * DQ)[u] = make_uint4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
+      reinterpret_cast<uint4 *>(vs + lp * KS + lq * DQ)[u] = make_uint4(vr[4 * u], vr[4 * u + 1], vr[4 * u + 2], vr[4 * u + 3]);
+    }
+    attn_load_kv<NU>(a, cache0, s0 + 64, p_hi, lp, lq * DQ, kr, vr);  // next sub-chunk (clamped rows past the end)
+    __syncthreads();
+#pragma unroll
+    for (int G = 0; G < NGM; G++) {
+      if (G < NG) {
+        // scores: this thread's query quarter in registers against 8 positions' K quarters
+        const int qi = 8 * G + jq;
+        float qv[DQ];
+#pragma unroll
+        for (int u = 0; u < DQ / 4; u++) {
+          const float4 x = qi < NQ ? reinterpret_cast<const float4 *>(qs + qi * HD + qq * DQ)[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+          qv[4 * u] = x.x; qv[4 * u + 1] = x.y; qv[4 * u + 2] = x.z; qv[4 * u + 3] = x.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const int pp = sg + 8 * k;
+          const uint4 *kp = reinterpret_cast<const uint4 *>(ks + pp * KS + qq * DQ);
+          float sdot = 0.0f;
+#pragma unroll
+          for (int u = 0; u < NU; u++) {
+            const uint4 w = kp[u];
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+              sdot = fmaf(qv[8 * u + 2 * t], h2f(ww[t]), sdot);
+              sdot = fmaf(qv[8 * u + 2 * t + 1], h2f(ww[t] >> 16), sdot);
+            }
+          }
+          sdot = sdot + quad_xor1f(sdot);
+          sdot = sdot + quad_xor2f(sdot);
+          const int pos = s0 + pp;
+          if (qq == 0) {
+            const bool ok = qi < NQ && pos < p_hi && pos <= start + qi / g;
+            ps[jq * 64 + pp] = ok ? sdot * a.scale : -INFINITY;
+          }
+        }
+        __syncthreads();
+        // online-softmax update: wave w takes queries w and w + 4 of the group; lane = position
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+          const int j = wave + 4 * r, qj = 8 * G + j;
+          if (qj < NQ) {
+            const float sv = ps[j * 64 + lane];
+            const float mx = wave_max(sv);
+            const float m_old = sm[qj];
+            const float m_new = fmaxf(m_old, mx);
+            const float p = (sv == -INFINITY || m_new == -INFINITY) ? 0.0f : expf(sv - m_new);
+            const float lsum = wave_sum(p);
+            const float alpha = m_new == -INFINITY ? 1.0f : (m_old == -INFINITY ? 0.0f : expf(m_old - m_new));
+            ps[j * 64 + lane] = p;
+            if (lane == 0) { sm[qj] = m_new; sl[qj] = sl[qj] * alpha + lsum; sa[j] = alpha; }
+          }
+        }
+        __syncthreads();
+        // o = o * alpha + sum_p p * v
+        if (qi < NQ) {
+          const float al = sa[jq];
+#pragma unroll
+          for (int d = 0; d < DP; d++) o[G][d] *= al;
+          const float *pr = ps + jq * 64;
+#pragma unroll 8
+          for (int t = 0; t < 64; t++) {
+            const float pv = pr[t];
+            if (DP == 4) {
+              const uint2 vv = *reinterpret_cast<const uint2 *>(vs + t * KS + dd0);
+              o[G][0] = fmaf(pv, h2f(vv.x), o[G][0]);
+              o[G][1] = fmaf(pv, h2f(vv.x >> 16), o[G][1]);
+              o[G][2] = fmaf(pv, h2f(vv.y), o[G][2]);
+              o[G][3] = fmaf(pv, h2f(vv.y >> 16), o[G][3]);
+            } else {
+              const uint32_t vv = *reinterpret_cast<const uint32_t *>(vs + t * KS + dd0);
+              o[G][0] = fmaf(pv, h2f(vv), o[G][0]);
+              o[G][1] = fmaf(pv, h2f(vv >> 16), o[G][1]);
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  // 3. partials (coherent stores), then the last workgroup of this kv head merges
+  const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nch) * ATT_QMAX * 2);
+  const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nch) * ATT_QMAX * HD);
+#pragma unroll
+  for (int G = 0; G < NGM; G++) {
+    const int qi = 8 * G + jq;
+    if (G < NG && qi < NQ) {
+      const int off = ((c * ATT_QMAX + qi) * HD + dd0) * 4;
+      if (DP == 4) st_coh4(r_o, off, f4v{o[G][0], o[G][1], o[G][2], o[G][3]});
+      else st_coh2(r_o, off, f2v{o[G][0], o[G][1]});
+      if ((tid & 31) == 0) st_coh2(r_ml, (c * ATT_QMAX + qi) * 8, f2v{sm[qi], sl[qi]});
+    }
+  }
+  if (arrive(&a.counter[h]) != nch - 1) return;
+  // chunk weights exp(m_c - max) and 1 / sum_c l_c w_c per query (wave per query, lane per chunk)
+  for (int qi = wave; qi < NQ; qi += 4) {
+    const f2v ml = lane < nch ? ld_coh2(r_ml, (lane * ATT_QMAX + qi) * 8) : f2v{-INFINITY, 0.0f};
+    const float mx = wave_max(ml.x);
+    const float w = ml.x == -INFINITY ? 0.0f : expf(ml.x - mx);
+    const float l = wave_sum(ml.y * w);
+    wsm[qi * 64 + lane] = w;
+    if (lane == 0) sl[qi] = __fdiv_rn(1.0f, fmaxf(l, 1e-30f));
+  }
+  __syncthreads();
+  float *ol = qs;  // merged output [NQ][HD] = rows b, then this group's heads
+  for (int q0 = 0; q0 < NQ; q0 += 8) {
+    const int qi = q0 + jq;
+    if (qi < NQ) {
+      float acc[DP];
+#pragma unroll
+      for (int d = 0; d < DP; d++) acc[d] = 0.0f;
+      for (int c0 = 0; c0 < nch; c0 += 8) {
+        f4v ov[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const int cc = min(c0 + k, nch - 1);
+          const int off = ((cc * ATT_QMAX + qi) * HD + dd0) * 4;
+          if (DP == 4) ov[k] = ld_coh4(r_o, off);
+          else { const f2v t2 = ld_coh2(r_o, off); ov[k] = f4v{t2.x, t2.y, 0.0f, 0.0f}; }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          if (c0 + k < nch) {
+            const float w = wsm[qi * 64 + c0 + k];
+            acc[0] = fmaf(ov[k].x, w, acc[0]);
+            acc[1] = fmaf(ov[k].y, w, acc[1]);
+            if (DP == 4) { acc[2] = fmaf(ov[k].z, w, acc[2]); acc[3] = fmaf(ov[k].w, w, acc[3]); }
+          }
+        }
+      }
+      const float il = sl[qi];
+      const int b = qi / g, head = h * g + qi % g;
+#pragma unroll
+      for (int d = 0; d < DP; d++) {
+        const float ov = acc[d] * il;
+        ol[qi * HD + dd0 + d] = ov;
+        a.att[(int64_t)b * a.n_heads * HD + head * HD + dd0 + d] = ov;
+      }
+    }
+  }
+  if (a.aq.q) {
+    __syncthreads();
+    const int gw = g * HD, nbq = gw / 256, qdim = a.n_heads * HD, nbr = qdim / 256;
+    for (int it = wave; it < m * nbq; it += 4) {
+      const int b = it / nbq, kb = it % nbq;
+      const float4 xv = reinterpret_cast<const float4 *>(ol + b * gw + kb * 256)[lane];
+      const float am = wave_max(amax4(xv));
+      const int64_t vb = (int64_t)b * nbr + (h * gw) / 256 + kb;
+      q8k_block_store(xv, am, a.aq.q + vb * 64, a.aq.d + vb, reinterpret_cast<int *>(a.aq.bs + vb * 8));
+    }
+  }
+  if (tid == 0) a.counter[h] = 0;
+}
+
+// ------------------------------------------------------------------ MoE router + routing
+// F32 router rows (two per wavefront, 32 lanes each; fixed per-row order, so batch
+// independent like matvec_multi's per-vector F32 path :455-464), then the last workgroup
+// routes: softmax (max, exp, sum, divide), top-n_used by probability (ties to the lower
+// expert index), pruning (moe_prune >= 1: keep clamp(x, max(2, n/2), n); < 1: mass rule),
+// weights p / sum(kept) when normalised (:1199-1239, :959-997), and the grouped job lists
+// over the union of chosen experts in expert order, users in (row, slot) order (:982-986).
+template <int MT>
+__global__ __launch_bounds__(64) void k_router(const RouterArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int m = st->m, lane = threadIdx.x;
+  const int dim = a.pro.dim, n4 = dim >> 2;
+  const int hl = lane & 31;
+  float *xl = reinterpret_cast<float *>(smem);  // [G][dim]
+  constexpr int G = MT < 8 ? MT : 8;
+  // one row per half-wavefront; its weights are loaded before the prologue
+  const int row = blockIdx.x * 2 + (lane >> 5);
+  const bool valid = row < a.n_expert;
+  const float4 *wr = reinterpret_cast<const float4 *>(a.w.pl.p0 + (int64_t)(valid ? row : 0) * dim * 4);
+  float4 wreg[PRO_NT * 2];
+#pragma unroll
+  for (int t = 0; t < PRO_NT * 2; t++) {
+    const int f = hl + 32 * t;
+    wreg[t] = f < n4 ? wr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int v0 = 0; v0 < m; v0 += G) {
+    const int nv = min(G, m - v0);
+    if (v0 > 0) __syncthreads();
+    pro_f32<1>(a.pro, v0, nv, xl, blockIdx.x == 0);
+    float part[G];
+#pragma unroll
+    for (int v = 0; v < G; v++) part[v] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < PRO_NT * 2; t++) {
+      const int f = hl + 32 * t;
+      if (f < n4) {
+#pragma unroll
+        for (int v = 0; v < G; v++) {
+          if (v < nv) {
+            const float4 x = reinterpret_cast<const float4 *>(xl + v * dim)[f];
+            part[v] = fmaf(wreg[t].x, x.x, part[v]);
+            part[v] = fmaf(wreg[t].y, x.y, part[v]);
+            part[v] = fmaf(wreg[t].z, x.z, part[v]);
+            part[v] = fmaf(wreg[t].w, x.w, part[v]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < G; v++) {
+      float t = part[v];
+      t = t + SPX_DPPF(t, 0xB1);
+      t = t + SPX_DPPF(t, 0x4E);
+      t = t + SPX_DPPF(t, 0x141);
+      t = t + SPX_DPPF(t, 0x140);
+      t = t + __shfl_xor(t, 16);
+      if (hl == 0 && valid && v < nv) st_dev(a.logits + (int64_t)(v0 + v) * a.n_expert + row, t);
+    }
+  }
+  if (arrive(a.counter) != (int)gridDim.x - 1) return;
+  // routing (one wavefront)
+  __shared__ float probs[256];
+  __shared__ int chosen[MAX_M][32];
+  __shared__ int nkeep[MAX_M];
+  const int ne = a.n_expert, nu = a.n_used;
+  for (int b = 0; b < m; b++) {
+    const float *lg = a.logits + (int64_t)b * ne;
+    float lv[4], mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 4; k++) { const int e = lane + 64 * k; lv[k] = e < ne ? ld_dev(lg + e) : -INFINITY; mx = fmaxf(mx, lv[k]); }
+    mx = wave_max(mx);
+    float pv[4], sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) { const int e = lane + 64 * k; pv[k] = e < ne ? expf(lv[k] - mx) : 0.0f; sum += pv[k]; }
+    sum = wave_sum(sum);
+    // top-n_used by probability, ties to the lower expert index: repeated wave argmax over
+    // keys (probability bits, ~index); a probability is >= 0, so its bits order as unsigned
+    unsigned long long key[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int e = lane + 64 * k;
+      if (e < ne) { pv[k] = pv[k] / sum; probs[e] = pv[k]; }
+      key[k] = e < ne ? ((unsigned long long)__float_as_uint(pv[k]) << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)e) : 0ull;
+    }
+    for (int i = 0; i < nu; i++) {
+      unsigned long long bk = key[0];
+#pragma unroll
+      for (int k = 1; k < 4; k++) bk = key[k] > bk ? key[k] : bk;
+      bk = wave_max_u64(bk);
+      const int e = (int)(0xFFFFFFFFu - (unsigned)(bk & 0xFFFFFFFFull));
+      if (lane == 0) chosen[b][i] = e;
+      if ((e & 63) == lane) key[e >> 6] = 0ull;
+    }
+    __syncthreads();
+    if (lane == 0) {
+      int keep = nu;
+      if (a.moe_prune > 0.0f && nu > 2) {
+        const int min_keep = max(2, nu / 2);
+        if (a.moe_prune >= 1.0f) keep = min(max((int)a.moe_prune, min_keep), nu);
+        else {
+          float top = 0.0f;
+          for (int i = 0; i < nu; i++) top += probs[chosen[b][i]];
+          const float target = top * (1.0f - a.moe_prune);
+          float cum = 0.0f;
+          int k = 0;
+          while (k < nu && (k < min_keep || cum < target)) { cum += probs[chosen[b][k]]; k++; }
+          keep = k;
+        }
+      }
+      float wsum = 0.0f;
+      for (int i = 0; i < keep; i++) wsum += probs[chosen[b][i]];
+      for (int i = 0; i < keep; i++) {
+        a.chosen[b * 32 + i] = chosen[b][i];
+        a.weights[b * 32 + i] = a.norm ? probs[chosen[b][i]] / wsum : probs[chosen[b][i]];
+      }
+      nkeep[b] = keep;
+      a.nkeep[b] = keep;
+    }
+    __syncthreads();
+  }
+  // jobs: experts with at least one user, in expert order
+  int base = 0;
+  for (int e0 = 0; e0 < ne; e0 += 64) {
+    const int e = e0 + lane;
+    int cnt = 0;
+    if (e < ne)
+      for (int b = 0; b < m; b++)
+        for (int i = 0; i < nkeep[b]; i++) cnt += chosen[b][i] == e;
+    const unsigned long long bal = __ballot(cnt > 0);
+    if (cnt > 0) {
+      const int j = base + __popcll(bal & ((1ull << lane) - 1ull));
+      Job &J = a.jobs[j];
+      Job &Jd = a.jobs[256 + j];
+      int k = 0;
+      for (int b = 0; b < m; b++)
+        for (int i = 0; i < nkeep[b]; i++)
+          if (chosen[b][i] == e) {
+            J.vec[k] = b;
+            J.out[k] = b * nu + i;
+            Jd.vec[k] = b * nu + i;
+            Jd.out[k] = b * nu + i;
+            k++;
+          }
+      J.expert = e;
+      Jd.expert = e;
+      J.nvec = k;
+      Jd.nvec = k;
+      if (a.expert_count) a.expert_count[e] += 1;
+    }
+    base += __popcll(bal);
+  }
+  if (lane == 0) { *a.njobs = base; *a.counter = 0; }
+}
+
+// ------------------------------------------------------------------ gate / up + SwiGLU
+// Workgroup of 4 wavefronts = 16 rows of one job: in each wavefront row slots 0-3 are gate
+// rows r..r+3 and slots 4-7 the same rows of up; h = silu(g) * u (silu :586-588, ffns_fused
+// :407-417). With hq, the last of the 16 workgroups that cover a 256-row block of h
+// quantizes it (Q8_K for the integer down projection, :420-424).
+// The last of the 16 workgroups that cover a 256-row block of h quantizes it (Q8_K for an
+// integer down projection, :420-424) and clears the block's counter for the next pass.
+__device__ __forceinline__ void gateup_quant_tail(const GUArgs &a, int nvec, const int *jo) {
+  __shared__ int quant_u[MAX_M];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n_ff = a.n_ff, nbh = n_ff / 256, blk = (blockIdx.x * 16) / 256;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if ((int)threadIdx.x < nvec) {
+    const int vo = jo ? jo[threadIdx.x] : threadIdx.x;
+    quant_u[threadIdx.x] = atomicAdd(&a.counter[vo * nbh + blk], 1) == 15;
+  }
+  __syncthreads();
+  for (int u = wave; u < nvec; u += 4) {
+    if (!quant_u[u]) continue;
+    const int vo = jo ? jo[u] : u;
+    const float *hp = a.h + (int64_t)vo * n_ff + blk * 256 + 4 * lane;
+    const float4 xv = make_float4(ld_dev(hp), ld_dev(hp + 1), ld_dev(hp + 2), ld_dev(hp + 3));
+    const float am = wave_max(amax4(xv));
+    const int64_t vb = (int64_t)vo * nbh + blk;
+    q8k_block_store(xv, am, a.hq.q + vb * 64, a.hq.d + vb, reinterpret_cast<int *>(a.hq.bs + vb * 8));
+    if (lane == 0) a.counter[vo * nbh + blk] = 0;
+  }
+}
+
+template <int T, int MT, bool PRO>
+__global__ __launch_bounds__(256) void k_gateup_kq(const GUArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int m = st->m;
+  int expert = 0, nvec = m;
+  const int *jv = nullptr, *jo = nullptr;
+  if (a.jobs) {
+    if ((int)blockIdx.y >= *a.njobs) return;
+    const Job &J = a.jobs[blockIdx.y];
+    expert = J.expert;
+    nvec = J.nvec;
+    jv = J.vec;
+    jo = J.out;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int nb = (int)a.gate.nb, n_ff = a.n_ff, dim = (int)a.gate.cols;
+  const int rb = blockIdx.x * 16 + wave * 4;           // this wave's first row
+  const int64_t eb = (int64_t)expert * a.gate.rows;
+  const Q8KP ly = ldsq_of(smem, MT, dim);
+  uint8_t *tile = smem + ((ldsq_bytes(MT, dim) + 15) & ~(size_t)15) + (size_t)wave * 8 * nb * tile_bytes_per_block();
+  tile_fetch<T>(tile, a.gate.pl, nb, [&](int sl) -> int64_t { return sl < 4 && rb + sl < n_ff ? eb + rb + sl : -1; });
+  tile_fetch<T>(tile, a.up.pl, nb, [&](int sl) -> int64_t { return sl >= 4 && rb + sl - 4 < n_ff ? eb + rb + sl - 4 : -1; });
+  if (PRO) pro_q8k<4>(a.pro, m, ly, blockIdx.x == 0 && blockIdx.y == 0);
+  else stage_q8kp(ly, a.y, dim, nvec, 4, [&](int u) { return jv ? jv[u] : u; });
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const int r = rb + (slot & 3);
+  const bool valid = r < n_ff;
+  int vidx[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) vidx[v] = v;
+  float res[MT];
+  kq_walk_tile<T, MT>(tile, nb, slot, eb + (valid ? r : n_ff - 1), ly, vidx, nvec, l, res);
+#pragma unroll
+  for (int v = 0; v < MT; v++) {
+    const float u = __shfl_down(res[v], 32);
+    if (slot < 4 && l == 0 && valid && v < nvec) {
+      const float x = res[v];
+      st_dev(a.h + (int64_t)(jo ? jo[v] : v) * n_ff + r, x / (1.0f + expf(-x)) * u);
+    }
+  }
+  if (a.hq.q) gateup_quant_tail(a, nvec, jo);
+}
+
+template <int T, int MT, bool PRO>
+__global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int m = st->m;
+  int expert = 0, nvec = m;
+  const int *jv = nullptr, *jo = nullptr;
+  if (a.jobs) {
+    if ((int)blockIdx.y >= *a.njobs) return;
+    const Job &J = a.jobs[blockIdx.y];
+    expert = J.expert;
+    nvec = J.nvec;
+    jv = J.vec;
+    jo = J.out;
+  }
+  constexpr int D = f_depth<MT>();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const TensorView &w = slot < 4 ? a.gate : a.up;
+  const int nb = (int)w.nb, n_ff = a.n_ff;
+  const int r = blockIdx.x * 16 + wave * 4 + (slot & 3);
+  const bool valid = r < n_ff;
+  const int64_t grow = (int64_t)expert * w.rows + (valid ? r : n_ff - 1);
+  const Planes pl = slot < 4 ? a.gate.pl : a.up.pl;
+  int vidx[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) vidx[v] = jv && v < nvec ? jv[v] : v;
+  float res[MT];
+  if (PRO) {
+    float *xl = reinterpret_cast<float *>(smem);
+    pro_f32<4>(a.pro, 0, m, xl, blockIdx.x == 0 && blockIdx.y == 0);
+    f_walk<T, MT, D>(pl, grow, nb, xl, a.pro.dim, vidx, nvec, l, res);
+  } else {
+    f_walk<T, MT, D>(pl, grow, nb, a.x, w.cols, vidx, nvec, l, res);
+  }
+#pragma unroll
+  for (int v = 0; v < MT; v++) {
+    const float u = __shfl_down(res[v], 32);
+    if (slot < 4 && l == 0 && valid && v < nvec) {
+      const float x = res[v];
+      st_dev(a.h + (int64_t)(jo ? jo[v] : v) * n_ff + r, x / (1.0f + expf(-x)) * u);
+    }
+  }
+  if (a.hq.q) gateup_quant_tail(a, nvec, jo);
+}
+
+// ------------------------------------------------------------------ down + combine
+// One output row per wavefront; row slots take jobs eight at a time; each job's users get
+// y_e[r] in LDS, then out[b][r] = sum over b's chosen slots, in chosen order, of w * y
+// (non-fused multiply and add, ffns_fused :432-437, moe_forward_batch :1133-1140).
+template <int T, int MT>
+__global__ __launch_bounds__(256) void k_down_kq(const DownArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float yb[4][MAX_M * 32];
+  constexpr bool STAGE = MT <= 2;  // every row's h vectors fit in LDS
+  const int m = st->m, nj = *a.njobs;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int64_t r = (int64_t)blockIdx.x * 4 + wave;
+  const int dim = (int)a.w.rows, nb = (int)a.w.nb, n_ff = (int)a.w.cols;
+  const bool valid = r < dim;
+  const int npairs = m * a.n_used;
+  const int nst = STAGE ? MT * a.n_used : 0;
+  const Q8KP ly = ldsq_of(smem, nst, n_ff);
+  uint8_t *tile = smem + ((ldsq_bytes(nst, n_ff) + 15) & ~(size_t)15) + (size_t)wave * 8 * nb * tile_bytes_per_block();
+  for (int j0 = 0; j0 < nj; j0 += 8) {
+    const int j = j0 + slot;
+    const bool has = j < nj;
+    const Job &J = a.jobs[has ? j : 0];
+    tile_fetch<T>(tile, a.w.pl, nb, [&](int sl) -> int64_t {
+      return j0 + sl < nj && valid ? (int64_t)a.jobs[j0 + sl].expert * dim + r : -1;
+    });
+    if (STAGE && j0 == 0) stage_q8kp(ly, a.y, n_ff, npairs, 4, [](int u) { return u; });
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const int nvec = has ? J.nvec : 0;
+    int vidx[MT];
+#pragma unroll
+    for (int v = 0; v < MT; v++) vidx[v] = v < nvec ? J.vec[v] : 0;
+    float res[MT];
+    kq_walk_tile<T, MT>(tile, nb, slot, (int64_t)J.expert * dim + (valid ? r : 0), STAGE ? ly : a.y, vidx, nvec, l, res);
+    if (l == 0) {
+#pragma unroll
+      for (int v = 0; v < MT; v++)
+        if (v < nvec) yb[wave][J.out[v]] = res[v];
+    }
+    __syncthreads();
+  }
+  if (valid && lane < m) {
+    const int b = lane, nk = a.nkeep[b];
+    float acc = 0.0f;
+    for (int i = 0; i < nk; i++) acc = acc + a.weights[b * 32 + i] * yb[wave][b * a.n_used + i];
+    a.out[(int64_t)b * dim + r] = acc;
+  }
+}
+
+template <int T, int MT>
+__global__ __launch_bounds__(256) void k_down_f(const DownArgs a, const StepRec *st) {
+  __shared__ float yb[4][MAX_M * 32];
+  const int m = st->m, nj = *a.njobs;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int64_t r = (int64_t)blockIdx.x * 4 + wave;
+  const int dim = (int)a.w.rows, nb = (int)a.w.nb;
+  const bool valid = r < dim;
+  constexpr int D = f_depth<MT>();
+  for (int j0 = 0; j0 < nj; j0 += 8) {
+    const int j = j0 + slot;
+    const bool has = j < nj;
+    const Job &J = a.jobs[has ? j : 0];
+    const int nvec = has ? J.nvec : 0;
+    const int64_t grow = (int64_t)J.expert * dim + (valid ? r : 0);
+    int vidx[MT];
+#pragma unroll
+    for (int v = 0; v < MT; v++) vidx[v] = v < nvec ? J.vec[v] : 0;
+    float res[MT];
+    f_walk<T, MT, D>(a.w.pl, grow, nb, a.x, a.w.cols, vidx, nvec, l, res);
+    if (l == 0) {
+#pragma unroll
+      for (int v = 0; v < MT; v++)
+        if (v < nvec) yb[wave][J.out[v]] = res[v];
+    }
+  }
+  __syncthreads();
+  if (valid && lane < m) {
+    const int b = lane, nk = a.nkeep[b];
+    float acc = 0.0f;
+    for (int i = 0; i < nk; i++) acc = acc + a.weights[b * 32 + i] * yb[wave][b * a.n_used + i];
+    a.out[(int64_t)b * dim + r] = acc;
+  }
+}
+
+// ------------------------------------------------------------------ final greedy pick
+__global__ __launch_bounds__(256) void k_argmax_final(const unsigned long long *best, int nbest, int *out, const StepRec *st) {
+  const int b = blockIdx.x;
+  if (st && b >= st->m) return;
+  unsigned long long v = 0;
+  for (int i = threadIdx.x; i < nbest; i += 256) { const unsigned long long w = best[(int64_t)b * nbest + i]; v = w > v ? w : v; }
+  v = wave_max_u64(v);
+  __shared__ unsigned long long sb[4];
+  if ((threadIdx.x & 63) == 0) sb[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long r = sb[0];
+    for (int w = 1; w < 4; w++) r = sb[w] > r ? sb[w] : r;
+    out[b] = (int)(uint32_t)(r & 0xffffffffull);
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+static inline int bucket(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
+// Waves per workgroup: one for a decode pass (spreads a small matrix over the most CUs), four
+// for a fused prologue over several rows; integer launches without a prologue use one.
+static inline int mv_nw(int mt, bool pro, bool kq) { return pro ? (mt == 1 ? 1 : 4) : (kq ? 1 : 4); }
+
+int mv_wgs(int64_t rows, int mt, bool pro, int dtype) {
+  const bool kq = dtype == T_Q4K || dtype == T_Q6K;
+  const int64_t rows_per_wg = 8 * mv_nw(bucket(mt), pro, kq);
+  return (int)((rows + rows_per_wg - 1) / rows_per_wg);
+}
+
+size_t mv_smem(const MVArgs &a, int mt, bool pro, int dtype) {
+  mt = bucket(mt);
+  const bool kq = dtype == T_Q4K || dtype == T_Q6K;
+  const int cols = (int)a.seg[0].w.cols;
+  if (kq) return ((ldsq_bytes(mt, cols) + 15) & ~(size_t)15) + (size_t)mv_nw(mt, pro, kq) * 8 * (cols / 256) * tile_bytes_per_block();
+  if (!pro) return 0;
+  return (size_t)mt * a.pro.dim * 4;
+}
+
+template <int MT, int NW, bool PRO>
+static hipError_t launch_mv_t(const MVArgs &a, const StepRec *st, int grid, size_t sm, hipStream_t s) {
+  const int dt = a.seg[0].w.dtype;
+  if (dt == T_Q4K || dt == T_Q6K) {
+    if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_mvt<MT, NW, PRO>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+    hipLaunchKernelGGL((k_mvt<MT, NW, PRO>), dim3(grid), dim3(NW * 64), sm, s, a, st);
+  } else {
+    if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_mv_f<MT, NW, PRO>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+    hipLaunchKernelGGL((k_mv_f<MT, NW, PRO>), dim3(grid), dim3(NW * 64), sm, s, a, st);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_mv(const MVArgs &a, int mt, bool pro, const StepRec *st, int grid, hipStream_t s) {
+  mt = bucket(mt);
+  const int dt = a.seg[0].w.dtype;
+  const bool kq = dt == T_Q4K || dt == T_Q6K;
+  const int nw = mv_nw(mt, pro, kq);
+  const size_t sm = mv_smem(a, mt, pro, dt);
+  if (pro) {
+    switch (mt) {
+    case 1: return launch_mv_t<1, 1, true>(a, st, grid, sm, s);
+    case 2: return launch_mv_t<2, 4, true>(a, st, grid, sm, s);
+    case 4: return launch_mv_t<4, 4, true>(a, st, grid, sm, s);
+    case 8: return launch_mv_t<8, 4, true>(a, st, grid, sm, s);
+    default: return launch_mv_t<16, 4, true>(a, st, grid, sm, s);
+    }
+  }
+  if (nw == 1) {
+    switch (mt) {
+    case 1: return launch_mv_t<1, 1, false>(a, st, grid, sm, s);
+    case 2: return launch_mv_t<2, 1, false>(a, st, grid, sm, s);
+    case 4: return launch_mv_t<4, 1, false>(a, st, grid, sm, s);
+    case 8: return launch_mv_t<8, 1, false>(a, st, grid, sm, s);
+    default: return launch_mv_t<16, 1, false>(a, st, grid, sm, s);
+    }
+  }
+  switch (mt) {
+  case 1: return launch_mv_t<1, 4, false>(a, st, grid, sm, s);
+  case 2: return launch_mv_t<2, 4, false>(a, st, grid, sm, s);
+  case 4: return launch_mv_t<4, 4, false>(a, st, grid, sm, s);
+  case 8: return launch_mv_t<8, 4, false>(a, st, grid, sm, s);
+  default: return launch_mv_t<16, 4, false>(a, st, grid, sm, s);
+  }
+}
+
+static size_t attn_smem(const AttnArgs &a, int m) {
+  const int g = a.n_heads / a.n_kv, nq = m * g;
+  return (size_t)nq * a.hd * 4 + 2 * 64 * (a.hd + 8) * 2 + 8 * 64 * 4 + (2 * ATT_QMAX + 8) * 4 + (size_t)nq * 64 * 4 + 16;
+}
+
+template <int HD, int NGM>
+static void launch_attn_t(const AttnArgs &a, const StepRec *st, size_t sm, hipStream_t s) {
+  if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_attn<HD, NGM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+  hipLaunchKernelGGL((k_attn<HD, NGM>), dim3(a.nch, a.n_kv), dim3(256), sm, s, a, st);
+}
+
+hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
+  const size_t sm = attn_smem(a, m);
+  const int nq = m * (a.n_heads / a.n_kv);
+  if (a.hd == 128) {
+    if (nq <= 8) launch_attn_t<128, 1>(a, st, sm, s); else launch_attn_t<128, ATT_QMAX / 8>(a, st, sm, s);
+  } else if (a.hd == 64) {
+    if (nq <= 8) launch_attn_t<64, 1>(a, st, sm, s); else launch_attn_t<64, ATT_QMAX / 8>(a, st, sm, s);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStream_t s) {
+  mt = bucket(mt);
+  const int g = mt < 8 ? mt : 8;
+  const size_t sm = (size_t)g * a.pro.dim * 4;
+  const int grid = (a.n_expert + a.rows_per_wg - 1) / a.rows_per_wg;
+#define SPX_RT(MTV)                                                                                                          \
+  do {                                                                                                                       \
+    if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_router<MTV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); \
+    hipLaunchKernelGGL(k_router<MTV>, dim3(grid), dim3(64), sm, s, a, st);                                                   \
+  } while (0)
+  switch (mt) {
+  case 1: SPX_RT(1); break;
+  case 2: SPX_RT(2); break;
+  case 4: SPX_RT(4); break;
+  case 8: SPX_RT(8); break;
+  default: SPX_RT(16); break;
+  }
+#undef SPX_RT
+  return hipGetLastError();
+}
+
+template <int T, int MT>
+static hipError_t launch_gu_t(const GUArgs &a, const StepRec *st, dim3 grid, hipStream_t s) {
+  constexpr bool kq = T == T_Q4K || T == T_Q6K;
+  size_t sm = 0;
+  if (kq) sm = ((ldsq_bytes(MT, (int)a.gate.cols) + 15) & ~(size_t)15) + (size_t)4 * 8 * a.gate.nb * tile_bytes_per_block();
+  else if (a.use_pro) sm = (size_t)MT * a.pro.dim * 4;
+  if constexpr (kq) {
+    if (a.use_pro) {
+      if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_gateup_kq<T, MT, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+      hipLaunchKernelGGL((k_gateup_kq<T, MT, true>), grid, dim3(256), sm, s, a, st);
+    } else {
+      if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_gateup_kq<T, MT, false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+      hipLaunchKernelGGL((k_gateup_kq<T, MT, false>), grid, dim3(256), sm, s, a, st);
+    }
+  } else {
+    if (a.use_pro) {
+      if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_gateup_f<T, MT, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+      hipLaunchKernelGGL((k_gateup_f<T, MT, true>), grid, dim3(256), sm, s, a, st);
+    } else {
+      hipLaunchKernelGGL((k_gateup_f<T, MT, false>), grid, dim3(256), 0, s, a, st);
+    }
+  }
+  return hipGetLastError();
+}
+
+template <int T>
+static hipError_t launch_gu_dt(const GUArgs &a, int mt, const StepRec *st, dim3 grid, hipStream_t s) {
+  switch (mt) {
+  case 1: return launch_gu_t<T, 1>(a, st, grid, s);
+  case 2: return launch_gu_t<T, 2>(a, st, grid, s);
+  case 4: return launch_gu_t<T, 4>(a, st, grid, s);
+  case 8: return launch_gu_t<T, 8>(a, st, grid, s);
+  default: return launch_gu_t<T, 16>(a, st, grid, s);
+  }
+}
+
+hipError_t launch_gateup(const GUArgs &a, int mt, const StepRec *st, int max_jobs, hipStream_t s) {
+  mt = bucket(mt);
+  dim3 grid((unsigned)((a.n_ff + 15) / 16), (unsigned)std::max(1, max_jobs));
+  switch (a.gate.dtype) {
+  case T_Q4K: return launch_gu_dt<T_Q4K>(a, mt, st, grid, s);
+  case T_Q6K: return launch_gu_dt<T_Q6K>(a, mt, st, grid, s);
+  case T_Q8_0: return launch_gu_dt<T_Q8_0>(a, mt, st, grid, s);
+  case T_Q5_0: return launch_gu_dt<T_Q5_0>(a, mt, st, grid, s);
+  default: return hipErrorInvalidValue;
+  }
+}
+
+template <int T>
+static hipError_t launch_down_dt(const DownArgs &a, int mt, const StepRec *st, hipStream_t s) {
+  dim3 grid((unsigned)((a.w.rows + 3) / 4));
+  constexpr bool kq = T == T_Q4K || T == T_Q6K;
+  const int nst = mt <= 2 ? mt * a.n_used : 0;
+  const size_t sm = kq ? ((ldsq_bytes(nst, (int)a.w.cols) + 15) & ~(size_t)15) + (size_t)4 * 8 * a.w.nb * tile_bytes_per_block() : 0;
+#define SPX_DN(MTV)                                                                     \
+  do {                                                                                  \
+    if constexpr (kq) {                                                                 \
+      if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_down_kq<T, MTV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); \
+      hipLaunchKernelGGL((k_down_kq<T, MTV>), grid, dim3(256), sm, s, a, st);          \
+    } else hipLaunchKernelGGL((k_down_f<T, MTV>), grid, dim3(256), 0, s, a, st);        \
+  } while (0)
+  switch (mt) {
+  case 1: SPX_DN(1); break;
+  case 2: SPX_DN(2); break;
+  case 4: SPX_DN(4); break;
+  case 8: SPX_DN(8); break;
+  default: SPX_DN(16); break;
+  }
+#undef SPX_DN
+  return hipGetLastError();
+}
+
+hipError_t launch_down(const DownArgs &a, int mt, const StepRec *st, int njob_max, hipStream_t s) {
+  (void)njob_max;
+  mt = bucket(mt);
+  switch (a.w.dtype) {
+  case T_Q4K: return launch_down_dt<T_Q4K>(a, mt, st, s);
+  case T_Q6K: return launch_down_dt<T_Q6K>(a, mt, st, s);
+  case T_Q8_0: return launch_down_dt<T_Q8_0>(a, mt, st, s);
+  case T_Q5_0: return launch_down_dt<T_Q5_0>(a, mt, st, s);
+  default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_embed(const TensorView &e, const StepRec *st, float *x, int64_t ld_x, float escale, int m, hipStream_t s) {
+  hipLaunchKernelGGL(k_embed, dim3(m), dim3(256), 0, s, e, st, x, ld_x, escale);
+  return hipGetLastError();
+}
+
+hipError_t launch_norm(const Pro &p, const StepRec *st, int m, hipStream_t s) {
+  hipLaunchKernelGGL(k_norm, dim3(m), dim3(64), 0, s, p, st);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax_final(const unsigned long long *best, int nbest, int *out, const StepRec *st, int m, hipStream_t s) {
+  hipLaunchKernelGGL(k_argmax_final, dim3(m), dim3(256), 0, s, best, nbest, out, st);
+  return hipGetLastError();
+}
+
+hipError_t launch_q8kp_quantize(const float *x, int64_t n, int64_t ld_x, int m, Q8KP out, hipStream_t s) {
+  const int64_t blocks = (n / 256) * m;
+  hipLaunchKernelGGL(k_q8kp_quantize, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, s, x, n, ld_x, m, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_q8kp_from_ref(const float *d, const int8_t *qs, const int16_t *bs, int64_t n, int m, Q8KP out, hipStream_t s) {
+  hipLaunchKernelGGL(k_q8kp_from_ref, dim3((unsigned)((n / 256) * m)), dim3(64), 0, s, d, qs, bs, n, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_kq_block_sums(const TensorView &w, int expert, int64_t row, Q8KP y, int32_t *sums, hipStream_t s) {
+  dim3 grid((unsigned)((w.nb + 7) / 8));
+  if (w.dtype == T_Q4K) hipLaunchKernelGGL(k_kq_block_sums<T_Q4K>, grid, dim3(64), 0, s, w, expert, row, y, sums);
+  else hipLaunchKernelGGL(k_kq_block_sums<T_Q6K>, grid, dim3(64), 0, s, w, expert, row, y, sums);
+  return hipGetLastError();
+}
+
+}  // namespace spx

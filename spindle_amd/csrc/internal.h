@@ -29,12 +29,6 @@ int64_t row_bytes(int dtype, int64_t cols);
 int64_t block_elems(int dtype);
 void *ws_get(spx_ctx *ctx, size_t bytes);
 
-struct KQArgs;
-struct FArgs;
-size_t kq_smem_bytes(const TensorView &w, int mt);
-hipError_t launch_gemv_kq(const KQArgs &a, int mt, bool grouped, int grid_y, hipStream_t st);
-hipError_t launch_kq_block_sums(const KQArgs &a, hipStream_t st);
-hipError_t launch_gemv_f(const FArgs &a, int mt, bool grouped, int grid_y, hipStream_t st);
 hipError_t launch_q8k_quantize(const float *x, int64_t n, int64_t ld_x, int m, float *d, int8_t *qs,
                                int16_t *bsums, hipStream_t st);
 }  // namespace spx

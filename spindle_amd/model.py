@@ -102,7 +102,7 @@ CONFIGS = {
 
 # Small models of the same families for parity tests against the CPU oracle.
 TINY = {
-    "tiny-llama": ModelConfig("tiny-llama", "llama", 192, 2, 6, 2, 32, 512, 512, max_seq=256,
+    "tiny-llama": ModelConfig("tiny-llama", "llama", 192, 2, 3, 1, 64, 512, 512, max_seq=256,
                               t_embd=Q8_0, t_q=Q5_0, t_k=Q5_0, t_v=Q5_0, t_o=Q5_0, t_gate=Q5_0, t_up=Q5_0,
                               t_down=Q6K, t_out=Q8_0),
     "tiny-qwen3": ModelConfig("tiny-qwen3", "qwen3", 256, 2, 4, 2, 64, 768, 1000, max_seq=256, rope_theta=1e6,

@@ -2,6 +2,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <functional>
 #include <thread>
 
@@ -259,8 +260,15 @@ static Q8KP ws_q8kp(spx_ctx *ctx, int m, int64_t n, bool *ok) {
   return r;
 }
 
+// Launch mode: row-parallel for integer weights at m <= 2, else eight rows per wavefront;
+// SPX_MV_MODE=0/1 forces one (tests cover both).
 static int mv_launch(spx_ctx *ctx, const spx_tensor *w, int expert, int m, const float *x, int64_t ld_x, Q8KP y, float *out,
                      int64_t ld_out, int64_t r0, int64_t r1) {
+  const bool kq = w->v.dtype == T_Q4K || w->v.dtype == T_Q6K;
+  int mode = kq && m <= 2 ? 1 : 0;
+  if (const char *v = std::getenv("SPX_MV_MODE")) mode = kq && m <= 2 && atoi(v) == 1 ? 1 : 0;
+  int G = 8, R = 1;
+  rp_shape(w->v.nb, G, R);
   MVArgs a{};
   a.seg[0].w = w->v;
   a.seg[0].out = out;
@@ -268,13 +276,15 @@ static int mv_launch(spx_ctx *ctx, const spx_tensor *w, int expert, int m, const
   a.seg[0].r0 = r0;
   a.seg[0].r1 = r1;
   a.seg[0].expert = expert;
-  a.seg[0].wgs = mv_wgs(r1 - r0, m, false, w->v.dtype);
+  a.seg[0].wgs = mv_wgs(r1 - r0, m, mode, w->v.dtype, R);
   a.nseg = 1;
   a.x = x;
   a.ld_x = ld_x;
   a.y = y;
   a.m = m;
-  SPX_HIP(launch_mv(a, m, false, nullptr, a.seg[0].wgs, ctx->stream));
+  a.G = G;
+  a.R = R;
+  SPX_HIP(launch_mv(a, m, mode, nullptr, a.seg[0].wgs, ctx->stream));
   return 0;
 }
 

@@ -56,7 +56,8 @@ int64_t now_us() {
 struct spx_engine {
   spx_ctx *ctx = nullptr;
   spx_model_config c{};
-  int q_dim = 0, kv_dim = 0, n_ff = 0, nch = 64, lm_grid = 2048;
+  int q_dim = 0, kv_dim = 0, n_ff = 0, nch = 64, lm_grid = 2048, nbest = 1;
+  int mv_mode = -1, lm_mode = -1, tail_max = 2;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX)
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
   std::map<std::string, int64_t> vec_len;
@@ -72,7 +73,7 @@ struct spx_engine {
   float *xA = nullptr, *xB = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *proj = nullptr, *ffn = nullptr;
   float *xn2 = nullptr, *h = nullptr, *rlog = nullptr, *logits = nullptr, *xn = nullptr, *part_ml = nullptr, *part_o = nullptr;
   Q8KP aq{}, xq2{}, hq{}, xq{};
-  int *amax = nullptr, *att_cnt = nullptr, *rt_cnt = nullptr, *gu_cnt = nullptr;
+  int *amax = nullptr, *att_cnt = nullptr, *rt_cnt = nullptr, *gu_cnt = nullptr, *tail_cnt = nullptr;
   unsigned long long *best = nullptr;
   int *chosen = nullptr, *nkeep = nullptr, *expert_count = nullptr;
   float *weights = nullptr;
@@ -131,7 +132,7 @@ struct ProfScope {
 
 double wbytes(const spx_tensor *t) { return (double)row_bytes(t->v.dtype, t->v.cols) * (double)t->v.rows; }
 
-Seg seg_of(const spx_tensor *t, float *out, int64_t ld_out, int m, bool pro) {
+Seg seg_of(const spx_tensor *t, float *out, int64_t ld_out, int m, int mode, int R) {
   Seg s{};
   s.w = t->v;
   s.out = out;
@@ -139,87 +140,126 @@ Seg seg_of(const spx_tensor *t, float *out, int64_t ld_out, int m, bool pro) {
   s.r0 = 0;
   s.r1 = t->v.rows;
   s.expert = 0;
-  s.wgs = mv_wgs(t->v.rows, m, pro, t->v.dtype);
+  s.wgs = mv_wgs(t->v.rows, m, mode, t->v.dtype, R);
   return s;
 }
 
-// residual + norm prologue record
-Pro pro_of(spx_engine *E, const float *xa, const float *pa, const float *nw, float *xb) {
-  Pro p{};
-  p.xa = xa;
-  p.pa = pa;
-  p.rscale = E->c.residual_scale;
-  p.nw = nw;
-  p.eps = E->c.rms_eps;
-  p.xb = xb;
-  p.dim = E->c.dim;
-  return p;
+// Launch mode of a matrix pass: row-parallel for integer weights at m <= 2 (decode), else
+// eight rows per wavefront.
+int mode_of(const spx_engine *E, const spx_tensor *t, int m) {
+  if (!is_kq(t) || m > 2) return 0;
+  return E->mv_mode >= 0 ? E->mv_mode : 1;
 }
 
-// Matrix launch with the residual + norm prologue when it fits in LDS, else a norm kernel
-// (writing xn_tmp, and its Q8_K for integer weights) and a plain launch.
-int mv_pro(spx_engine *E, MVArgs &a, int m, float *xn_tmp, Q8KP q_tmp) {
-  hipStream_t s = E->ctx->stream;
-  const bool kq = a.seg[0].w.dtype == T_Q4K || a.seg[0].w.dtype == T_Q6K;
-  const size_t lds = kq ? 0 : (size_t)bucket(m) * a.pro.dim * 4;
-  if (lds <= 65536 && a.pro.dim <= 256 * PRO_NT) {
-    int total = 0;
-    for (int i = 0; i < a.nseg; i++) total += a.seg[i].wgs;
-    SPX_HIP(launch_mv(a, m, true, E->st_dev, total, s));
-    return 0;
+// Residual add + RMSNorm feeding the next consumer: the attn_norm of layer l's q/k/v (fp32
+// for float-activation weights, Q8_K for integer ones), or for l == n_layers the
+// output_norm (fp32 hidden state, and Q8_K for an integer LM head).
+NormTail norm_next(spx_engine *E, int l, const float *x, const float *add, float *x_out) {
+  NormTail t{};
+  t.x = x;
+  t.add = add;
+  t.rscale = E->c.residual_scale;
+  t.eps = E->c.rms_eps;
+  t.x_out = x_out;
+  t.dim = E->c.dim;
+  t.counter = E->tail_cnt;
+  if (l < E->c.n_layers) {
+    const LayerW &ly = E->L[l];
+    t.nw = ly.attn_norm;
+    if (is_kq(ly.wq)) t.q_out = E->xq2; else t.xn_out = E->xn2;
+  } else {
+    t.nw = E->out_norm;
+    t.xn_out = E->xn;
+    if (is_kq(E->lm_head)) t.q_out = E->xq;
   }
-  Pro p = a.pro;
-  p.xn_out = xn_tmp;
-  if (kq) p.q_out = q_tmp;
-  SPX_HIP(launch_norm(p, E->st_dev, m, s));
+  return t;
+}
+
+// ffn_norm of layer l: fp32 for the router or float gate/up, Q8_K for integer gate/up.
+NormTail norm_ffn(spx_engine *E, int l, const float *x, const float *add, float *x_out) {
+  const LayerW &ly = E->L[l];
+  NormTail t{};
+  t.x = x;
+  t.add = add;
+  t.rscale = E->c.residual_scale;
+  t.eps = E->c.rms_eps;
+  t.x_out = x_out;
+  t.dim = E->c.dim;
+  t.counter = E->tail_cnt;
+  t.nw = ly.ffn_norm;
+  if (ly.moe || !is_kq(ly.gate)) t.xn_out = E->xn2;
+  if (is_kq(ly.gate)) t.q_out = E->xq2;
+  return t;
+}
+
+int mv_run(spx_engine *E, MVArgs &a, int m, int mode, int grid_cap = 0) {
   int total = 0;
-  for (int i = 0; i < a.nseg; i++) { a.seg[i].wgs = mv_wgs(a.seg[i].r1 - a.seg[i].r0, m, false, a.seg[i].w.dtype); total += a.seg[i].wgs; }
-  a.x = xn_tmp;
-  a.ld_x = a.pro.dim;
-  a.y = q_tmp;
-  SPX_HIP(launch_mv(a, m, false, E->st_dev, total, s));
+  for (int i = 0; i < a.nseg; i++) total += a.seg[i].wgs;
+  int grid = total;
+  if (grid_cap > 0 && grid > grid_cap) grid = grid_cap;
+  a.m = m;
+  a.nbest = grid;
+  SPX_HIP(launch_mv(a, m, mode, E->st_dev, grid, E->ctx->stream));
   return 0;
 }
 
-// Plain matrix launch: activations y (integer weights) or x (float weights).
-int mv_plain(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld_x, Q8KP y, float *out, int64_t ld_out,
-             unsigned long long *best = nullptr, int grid_cap = 0) {
+// Matrix pass over one tensor; with a norm tail when `tail` has weights and tails are on for
+// this pass, else followed by a standalone norm launch.
+int mv_one(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld_x, Q8KP y, float *out, int64_t ld_out,
+           const NormTail *tail, bool tails, int cls_norm) {
+  const int mode = mode_of(E, w, m);
+  int G = 8, R = 1;
+  rp_shape(w->v.nb, G, R);
   MVArgs a{};
-  a.seg[0] = seg_of(w, out, ld_out, m, false);
+  a.seg[0] = seg_of(w, out, ld_out, m, mode, R);
   a.nseg = 1;
   a.x = x;
   a.ld_x = ld_x;
   a.y = y;
-  a.m = m;
-  a.best = best;
+  a.G = G;
+  a.R = R;
   a.lscale = E->c.logit_scale;
-  int grid = a.seg[0].wgs;
-  if (grid_cap > 0 && grid > grid_cap) grid = grid_cap;
-  a.nbest = grid;
-  SPX_HIP(launch_mv(a, m, false, E->st_dev, grid, E->ctx->stream));
+  if (tail && tails) a.tail = *tail;
+  if (int r = mv_run(E, a, m, mode)) return r;
+  if (tail && !tails) {
+    ProfScope ps(E, cls_norm, 0);
+    SPX_HIP(launch_norm(*tail, E->st_dev, m, E->ctx->stream));
+  }
   return 0;
 }
 
 // One forward pass of m rows at the step record's start position: embeddings through the
 // LM head and the greedy pick (forward_slice / forward_batch_slice + compute_logits_batch).
+// Residual stream: the embedding writes xA; attn_output's norm tail adds its output to xA
+// and writes xB; the FFN's tail adds its output to xB and writes xA.
 int enqueue_forward(spx_engine *E, int m) {
   const auto &c = E->c;
   hipStream_t s = E->ctx->stream;
   const int dim = c.dim, hd = c.head_dim;
-  { ProfScope ps(E, PC_EMBED, 0); SPX_HIP(launch_embed(E->embed->v, E->st_dev, E->xA, dim, c.embedding_scale, m, s)); }
+  const bool tails = m <= E->tail_max;
+  {
+    ProfScope ps(E, PC_EMBED, 0);
+    NormTail t = norm_next(E, 0, E->xA, nullptr, nullptr);
+    SPX_HIP(launch_embed(E->embed->v, E->st_dev, c.embedding_scale, t, m, s));
+  }
   for (int l = 0; l < c.n_layers; l++) {
     const LayerW &ly = E->L[l];
-    const float *pend = l == 0 ? nullptr : E->ffn;
-    // q, k, v with the attn_norm prologue (xA + ffn -> xB)
-    {
+    {  // q, k, v in one launch
       ProfScope ps(E, PC_QKV, wbytes(ly.wq) + wbytes(ly.wk) + wbytes(ly.wv));
+      const int mode = mode_of(E, ly.wq, m);
+      int G = 8, R = 1;
+      rp_shape(ly.wq->v.nb, G, R);
       MVArgs a{};
-      a.seg[0] = seg_of(ly.wq, E->q, E->q_dim, m, true);
-      a.seg[1] = seg_of(ly.wk, E->k, E->kv_dim, m, true);
-      a.seg[2] = seg_of(ly.wv, E->v, E->kv_dim, m, true);
+      a.seg[0] = seg_of(ly.wq, E->q, E->q_dim, m, mode, R);
+      a.seg[1] = seg_of(ly.wk, E->k, E->kv_dim, m, mode, R);
+      a.seg[2] = seg_of(ly.wv, E->v, E->kv_dim, m, mode, R);
       a.nseg = 3;
-      a.pro = pro_of(E, E->xA, pend, ly.attn_norm, E->xB);
-      if (int r = mv_pro(E, a, m, E->xn2, E->xq2)) return r;
+      a.y = E->xq2;
+      a.x = E->xn2;
+      a.ld_x = dim;
+      a.G = G;
+      a.R = R;
+      if (int r = mv_run(E, a, m, mode)) return r;
     }
     // attention (+ Q8_K of its output for an integer attn_output)
     const bool wo_int = is_kq(ly.wo);
@@ -237,75 +277,79 @@ int enqueue_forward(spx_engine *E, int m) {
       SPX_HIP(launch_attention(aa, m, E->st_dev, s));
     }
     if (wo_int && !att_q_fused) { ProfScope ps(E, PC_QUANT, 0); SPX_HIP(launch_q8kp_quantize(E->att, E->q_dim, E->q_dim, m, E->aq, s)); }
-    { ProfScope ps(E, PC_WO, wbytes(ly.wo)); if (int r = mv_plain(E, ly.wo, m, E->att, E->q_dim, E->aq, E->proj, dim)) return r; }
+    {  // attn_output + residual + ffn_norm
+      ProfScope ps(E, PC_WO, wbytes(ly.wo));
+      const NormTail t = norm_ffn(E, l, E->xA, E->proj, E->xB);
+      if (int r = mv_one(E, ly.wo, m, E->att, E->q_dim, E->aq, E->proj, dim, &t, tails, PC_NORM)) return r;
+    }
     const int nff = (int)ly.gate->v.rows;
-    const bool f_int = is_kq(ly.gate), d_int = is_kq(ly.down);
+    const bool d_int = is_kq(ly.down);
+    const NormTail tn = norm_next(E, l + 1, E->xB, E->ffn, E->xA);
+    const int gmode = mode_of(E, ly.gate, m);
     if (ly.moe) {  // moe_forward / moe_forward_batch (:925-1392)
       const int nu = c.n_expert_used, ne = c.n_expert;
       {
         ProfScope ps(E, PC_ROUTER, wbytes(ly.router));
         RouterArgs ra{};
-        ra.w = ly.router->v; ra.logits = E->rlog;
-        ra.pro = pro_of(E, E->xB, E->proj, ly.ffn_norm, E->xA);
-        if (f_int) ra.pro.q_out = E->xq2; else ra.pro.xn_out = E->xn2;
+        ra.w = ly.router->v; ra.x = E->xn2; ra.logits = E->rlog; ra.dim = dim;
         ra.n_expert = ne; ra.n_used = nu; ra.norm = c.expert_norm; ra.moe_prune = c.moe_prune; ra.counter = E->rt_cnt;
         ra.chosen = E->chosen; ra.weights = E->weights; ra.nkeep = E->nkeep; ra.jobs = E->jobs; ra.njobs = ly.njobs;
-        ra.expert_count = E->expert_count + (size_t)l * ne; ra.rows_per_wg = 2;
+        ra.expert_count = E->expert_count + (size_t)l * ne;
         SPX_HIP(launch_router(ra, m, E->st_dev, s));
       }
       const int max_jobs = std::min(ne, m * nu);
       {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up), l, true);  // one expert's slabs
         GUArgs ga{};
-        ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.x = E->xn2; ga.use_pro = false;
+        ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.x = E->xn2;
         ga.jobs = E->jobs; ga.njobs = ly.njobs; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
         if (d_int) ga.hq = E->hq;
-        SPX_HIP(launch_gateup(ga, m, E->st_dev, max_jobs, s));
+        SPX_HIP(launch_gateup(ga, m, gmode, E->st_dev, max_jobs, s));
       }
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
         DownArgs da{};
         da.w = ly.down->v; da.y = E->hq; da.x = E->h; da.jobs = E->jobs + 256; da.njobs = ly.njobs; da.weights = E->weights;
         da.nkeep = E->nkeep; da.n_used = nu; da.out = E->ffn;
-        SPX_HIP(launch_down(da, m, E->st_dev, max_jobs, s));
+        if (tails) da.tail = tn;
+        SPX_HIP(launch_down(da, m, 0, E->st_dev, s));
       }
+      if (!tails) { ProfScope ps(E, PC_NORM, 0); SPX_HIP(launch_norm(tn, E->st_dev, m, s)); }
     } else {  // ffn_forward / ffn_forward_multi (:590-646): k = 1, w = 1
       {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
         GUArgs ga{};
-        ga.gate = ly.gate->v; ga.up = ly.up->v; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
+        ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.x = E->xn2; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
         if (d_int) ga.hq = E->hq;
-        ga.pro = pro_of(E, E->xB, E->proj, ly.ffn_norm, E->xA);
-        const size_t lds = f_int ? 0 : (size_t)bucket(m) * dim * 4;
-        if (lds <= 65536 && dim <= 256 * PRO_NT) {
-          ga.use_pro = true;
-        } else {
-          Pro p = ga.pro;
-          p.xn_out = E->xn2;
-          if (f_int) p.q_out = E->xq2;
-          SPX_HIP(launch_norm(p, E->st_dev, m, s));
-          ga.use_pro = false;
-          ga.x = E->xn2;
-          ga.y = E->xq2;
-        }
-        SPX_HIP(launch_gateup(ga, m, E->st_dev, 1, s));
+        SPX_HIP(launch_gateup(ga, m, gmode, E->st_dev, 1, s));
       }
-      { ProfScope ps(E, PC_DOWN, wbytes(ly.down)); if (int r = mv_plain(E, ly.down, m, E->h, nff, E->hq, E->ffn, dim)) return r; }
+      {
+        ProfScope ps(E, PC_DOWN, wbytes(ly.down));
+        if (int r = mv_one(E, ly.down, m, E->h, nff, E->hq, E->ffn, dim, &tn, tails, PC_NORM)) return r;
+      }
     }
   }
-  const bool h_int = is_kq(E->lm_head);
   {
-    ProfScope ps(E, PC_NORM, 0);
-    Pro p = pro_of(E, E->xA, E->ffn, E->out_norm, nullptr);
-    p.xn_out = E->xn;
-    if (h_int) p.q_out = E->xq;
-    SPX_HIP(launch_norm(p, E->st_dev, m, s));
+    ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
+    const int mode = E->lm_mode >= 0 && m <= 2 && is_kq(E->lm_head) ? E->lm_mode : 0;
+    int G = 8, R = 1;
+    rp_shape(E->lm_head->v.nb, G, R);
+    MVArgs a{};
+    a.seg[0] = seg_of(E->lm_head, E->logits, c.vocab, m, mode, R);
+    a.nseg = 1;
+    a.x = E->xn;
+    a.ld_x = dim;
+    a.y = E->xq;
+    a.G = G;
+    a.R = R;
+    a.best = E->best;
+    a.lscale = c.logit_scale;
+    if (int r = mv_run(E, a, m, mode, mode == 0 ? E->lm_grid : 0)) return r;
+    E->nbest = a.nbest;
   }
-  { ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head)); if (int r = mv_plain(E, E->lm_head, m, E->xn, dim, E->xq, E->logits, c.vocab, E->best, E->lm_grid)) return r; }
   {
     ProfScope ps(E, PC_ARGMAX, 0);
-    const int nbest = std::min(mv_wgs(E->lm_head->v.rows, m, false, E->lm_head->v.dtype), E->lm_grid);
-    SPX_HIP(launch_argmax_final(E->best, nbest, E->amax, E->st_dev, m, s));
+    SPX_HIP(launch_argmax_final(E->best, E->nbest, E->amax, E->st_dev, m, s));
   }
   return 0;
 }
@@ -335,8 +379,8 @@ extern "C" {
 int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **out) {
   if (!ctx || !cfg || !out) return fail("spx_engine_create: null argument");
   const spx_model_config &c = *cfg;
-  if (c.dim <= 0 || c.dim > 256 * PRO_NT || c.dim % 16)
-    return fail("spx_engine_create: dim must be a positive multiple of 16, at most " + std::to_string(256 * PRO_NT));
+  if (c.dim <= 0 || c.dim > 256 * NORM_NT || c.dim % 16)
+    return fail("spx_engine_create: dim must be a positive multiple of 16, at most " + std::to_string(256 * NORM_NT));
   if (c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads) return fail("spx_engine_create: n_heads must be a multiple of n_kv_heads");
   if (c.head_dim != 64 && c.head_dim != 128) return fail("spx_engine_create: the attention kernel supports head_dim 64 or 128");
   if (16 * (c.n_heads / c.n_kv_heads) > ATT_QMAX) return fail("spx_engine_create: at most 8 query heads per kv head");
@@ -354,6 +398,9 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   E->L.resize(c.n_layers);
   if (const char *v = std::getenv("SPX_ATT_CHUNKS")) E->nch = std::max(1, std::min(64, atoi(v)));
   if (const char *v = std::getenv("SPX_LM_GRID")) E->lm_grid = std::max(1, atoi(v));
+  if (const char *v = std::getenv("SPX_MV_MODE")) E->mv_mode = std::max(0, std::min(1, atoi(v)));
+  if (const char *v = std::getenv("SPX_LM_MODE")) E->lm_mode = std::max(0, std::min(1, atoi(v)));
+  if (const char *v = std::getenv("SPX_TAIL_MAX")) E->tail_max = std::max(0, std::min(MAX_M, atoi(v)));
   *out = E;
   return 0;
 }
@@ -472,7 +519,8 @@ int spx_engine_prepare(spx_engine *E) {
             (E->xn2 = E->dalloc<float>((size_t)M * qmax)) && (E->xn = E->dalloc<float>((size_t)M * c.dim)) &&
             (E->h = E->dalloc<float>((size_t)nv * nff)) && (E->rlog = E->dalloc<float>((size_t)M * std::max(1, c.n_expert))) &&
             (E->logits = E->dalloc<float>((size_t)M * c.vocab)) && (E->amax = E->dalloc<int>(M)) &&
-            (E->best = E->dalloc<unsigned long long>((size_t)M * E->lm_grid)) &&
+            (E->best = E->dalloc<unsigned long long>((size_t)M * std::max<int64_t>(E->lm_grid, c.vocab / 4 + 1))) &&
+            (E->tail_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) &&
             (E->part_ml = E->dalloc<float>((size_t)c.n_kv_heads * E->nch * ATT_QMAX * 2)) &&
             (E->part_o = E->dalloc<float>((size_t)c.n_kv_heads * E->nch * ATT_QMAX * c.head_dim)) &&
             (E->att_cnt = E->dalloc<int>(c.n_kv_heads)) && (E->rt_cnt = E->dalloc<int>(1)) &&
@@ -579,7 +627,7 @@ int spx_engine_decode(spx_engine *E, int32_t token, int start_pos, int n, int32_
 int spx_engine_debug_read(spx_engine *E, const char *what, void *host, int64_t bytes) {
   if (!E || !what || !host) return fail("null argument");
   const std::string w(what);
-  const void *src = w == "x" ? (const void *)E->xA : w == "xn" ? (const void *)E->xn : w == "q" ? (const void *)E->q
+  const void *src = w == "x" ? (const void *)E->xA : w == "xn" ? (const void *)E->xn : w == "q" ? (const void *)E->q : w == "k" ? (const void *)E->k : w == "v" ? (const void *)E->v
                   : w == "att" ? (const void *)E->att : w == "proj" ? (const void *)E->proj : w == "rlog" ? (const void *)E->rlog
                   : w == "chosen" ? (const void *)E->chosen : w == "weights" ? (const void *)E->weights
                   : w == "nkeep" ? (const void *)E->nkeep : w == "h" ? (const void *)E->h : w == "y" ? (const void *)E->ffn : nullptr;

@@ -7,7 +7,9 @@ namespace spx {
 
 constexpr int MAX_M = 16;       // rows per verify / prefill pass
 constexpr int ATT_QMAX = 128;   // query heads x rows per kv head in one pass (16 rows x 8)
-constexpr int PRO_NT = 8;       // fused prologues handle dim <= 256 * PRO_NT
+constexpr int NORM_NT = 16;     // norm tails handle dim <= 256 * NORM_NT
+constexpr int CNT_SUB = 64;     // first-level arrival counters of a two-level count
+constexpr int CNT_STRIDE = 32;  // ints between counters (own 128-byte line each)
 
 // Device-side step record: the token rows of this pass and where they go in the KV cache.
 struct StepRec {
@@ -16,20 +18,24 @@ struct StepRec {
   int ids[MAX_M];
 };
 
-// Residual + RMSNorm prologue of a kernel (rmsnorm smollm_chat.rs:569-575 after the residual
-// add :3518-3520 / :3538-3540): row b's input is xa[b] + rscale * pa[b] (pa may be null),
-// normalised with weight nw. The normalised row stays in the workgroup (LDS), as fp32 or as
-// permuted Q8_K; workgroup 0 also writes the un-normalised sum to xb and, optionally, the
-// normalised row (xn_out, fp32) and its Q8_K (q_out) for later kernels.
-struct Pro {
-  const float *xa, *pa;
+// Residual add + RMSNorm (+ Q8_K) of the pass's rows, run once by the last workgroup of the
+// kernel that produced `add` (rmsnorm smollm_chat.rs:569-575 after the residual add
+// :3518-3520 / :3538-3540): x_out = x + rscale * add, then xn = x_out * inv * nw with
+// inv = 1/sqrt(sum(x_out^2)/dim + eps), written as fp32 (xn_out) and / or permuted Q8_K
+// (q_out). The sum is taken in a fixed order: per 256-value block a wavefront tree, then the
+// blocks in order, so a row's result does not depend on how many rows the pass has.
+// nw == null: no tail.
+struct NormTail {
+  const float *x;     // residual input [m][dim]
+  const float *add;   // this kernel's output [m][dim] (null: none), read coherently
   float rscale;
   const float *nw;
   float eps;
-  float *xb;
-  float *xn_out;
-  Q8KP q_out;
+  float *x_out;       // [m][dim] (null: not written)
+  float *xn_out;      // [m][dim] (null: not written)
+  Q8KP q_out;         // q null: not written (needs dim % 256 == 0)
   int dim;
+  int *counter;       // (1 + CNT_SUB) * CNT_STRIDE ints, zero between passes
 };
 
 // One weight tensor's rows as a matvec segment.
@@ -45,16 +51,17 @@ struct Seg {
 struct MVArgs {
   Seg seg[3];
   int nseg;
-  Q8KP y;             // integer path without prologue: activations (cols of the segments)
-  const float *x;     // float path without prologue: fp32 activations [m][ld_x]
+  Q8KP y;             // integer path: activations (permuted Q8_K, cols of the segments)
+  const float *x;     // float path: fp32 activations [m][ld_x]
   int64_t ld_x;
-  Pro pro;
   int m;              // rows of activations when no step record is given
+  int G, R;           // row-parallel launches: lane groups per row, rows per wavefront
   // optional greedy-pick partials (LM head): per vector, the best packed (key, index) of
   // each workgroup -> best[v * nbest + blockIdx.x]
   unsigned long long *best;
   int nbest;
   float lscale;
+  NormTail tail;
 };
 
 struct AttnArgs {
@@ -81,34 +88,32 @@ struct Job {
 
 struct RouterArgs {
   TensorView w;                       // F32 [n_expert][dim]
+  const float *x;                     // normalised rows [m][dim]
   float *logits;                      // [m][n_expert]
-  Pro pro;
-  int n_expert, n_used, norm;
+  int n_expert, n_used, norm, dim;
   float moe_prune;
   int *counter;                       // zero between passes
   int *chosen;                        // [16][32]
   float *weights;                     // [16][32]
   int *nkeep;                         // [16]
-  Job *jobs;                          // union of chosen experts, expert order
+  Job *jobs;                          // gate/up jobs [256], then down jobs [256]
   int *njobs;
   int *expert_count;                  // optional [n_expert] selection counter
-  int rows_per_wg;
 };
 
-// Gate/up (+ SwiGLU, + Q8_K of the result) over jobs; a dense FFN is one job whose users are
-// the pass's rows (with the residual + RMSNorm prologue).
+// Gate/up + SwiGLU (+ Q8_K of h by the last workgroup covering each 256-row block) over
+// jobs; a dense FFN is one job whose users are the pass's rows.
 struct GUArgs {
   TensorView gate, up;
-  Q8KP y;                             // integer path input (no prologue)
-  const float *x;                     // float path input (no prologue), ld = dim
-  Pro pro;
-  bool use_pro;
+  Q8KP y;                             // integer path input
+  const float *x;                     // float path input, ld = dim
   const Job *jobs;                    // null: dense, users = rows 0..m-1
   const int *njobs;
   float *h;                           // [vec][n_ff]
   Q8KP hq;                            // q null: no quantization
   int *counter;                       // [16*32][n_ff/256], zero between passes
   int n_ff;
+  int G;                              // row-parallel launch: lane groups per row
 };
 
 struct DownArgs {
@@ -121,21 +126,31 @@ struct DownArgs {
   const int *nkeep;
   int n_used;
   float *out;                         // [m][dim]
+  int G;                              // row-parallel launch: lane groups per row
+  NormTail tail;
 };
 
-hipError_t launch_embed(const TensorView &e, const StepRec *st, float *x, int64_t ld_x, float escale, int m, hipStream_t s);
-hipError_t launch_mv(const MVArgs &a, int mt, bool pro, const StepRec *st, int total_wgs, hipStream_t s);
+hipError_t launch_embed(const TensorView &e, const StepRec *st, float escale, const NormTail &t, int m, hipStream_t s);
+// mode 0: eight rows per wavefront (tiles); 1: row-parallel (integer only)
+hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int grid, hipStream_t s);
 hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);
 hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStream_t s);
-hipError_t launch_gateup(const GUArgs &a, int mt, const StepRec *st, int max_jobs, hipStream_t s);
-hipError_t launch_down(const DownArgs &a, int mt, const StepRec *st, int njob_max, hipStream_t s);
-hipError_t launch_norm(const Pro &p, const StepRec *st, int m, hipStream_t s);
+hipError_t launch_gateup(const GUArgs &a, int mt, int mode, const StepRec *st, int max_jobs, hipStream_t s);
+hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, hipStream_t s);
+hipError_t launch_norm(const NormTail &t, const StepRec *st, int m, hipStream_t s);
 hipError_t launch_argmax_final(const unsigned long long *best, int nbest, int *out, const StepRec *st, int m, hipStream_t s);
 hipError_t launch_q8kp_quantize(const float *x, int64_t n, int64_t ld_x, int m, Q8KP out, hipStream_t s);
 hipError_t launch_q8kp_from_ref(const float *d, const int8_t *qs, const int16_t *bs, int64_t n, int m, Q8KP out, hipStream_t s);
 hipError_t launch_kq_block_sums(const TensorView &w, int expert, int64_t row, Q8KP y, int32_t *sums, hipStream_t s);
-// workgroups a matvec segment needs (8 rows per wavefront, waves per workgroup as launched)
-int mv_wgs(int64_t rows, int mt, bool pro, int dtype);
-size_t mv_smem(const MVArgs &a, int mt, bool pro, int dtype);
+// workgroups a matvec segment needs for the launch mode (rows per workgroup as launched)
+int mv_wgs(int64_t rows, int mt, int mode, int dtype, int R);
+
+// Row-parallel shape for rows of nb blocks: G lane groups per row (the smallest power of two
+// >= nb, at most 8), R = 8 / G rows per wavefront.
+inline void rp_shape(int64_t nb, int &G, int &R) {
+  G = 1;
+  while (G < nb && G < 8) G *= 2;
+  R = 8 / G;
+}
 
 }  // namespace spx

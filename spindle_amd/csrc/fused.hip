@@ -1,13 +1,20 @@
 // Fused decode / verify kernels for gfx950 (wave64). One forward pass of m <= 16 token rows
-// is, per layer, six launches:
-//   k_mv_kq / k_mv_f  (attn_norm prologue) q, k, v projections in one launch
-//   k_attn            q/k norm, RoPE, K/V cache write, split-K attention, last-workgroup merge
-//                     (+ Q8_K of the output)
-//   k_mv_*            attn_output projection
-//   k_router          (ffn_norm prologue) F32 router + last-workgroup routing and job lists
-//   k_gateup          grouped gate/up + SwiGLU (+ Q8_K of h by the last workgroup per block)
-//   k_down            grouped down projection + weighted combine in chosen order
-// (dense FFN layers: k_gateup with the ffn_norm prologue, then k_mv_* for ffn_down).
+// is, per layer:
+//   q/k/v projections     one launch over the three tensors (segments)
+//   attention             q/k norm, RoPE, K/V cache write, split-K attention, last-workgroup
+//                         merge (+ Q8_K of the output)
+//   attn_output           + the residual add, ffn_norm and Q8_K of the next input, computed
+//                         once by the launch's last workgroup ("norm tail")
+//   router + routing      F32 router rows, then the last workgroup routes and builds the
+//                         grouped job lists (MoE layers)
+//   gate/up + SwiGLU      grouped over the selected experts (+ Q8_K of h by the last
+//                         workgroup covering each 256-row block)
+//   down + combine        grouped, weighted sum in chosen order, + the residual add and the
+//                         next layer's attn_norm (or output_norm) as a norm tail
+// Decode (m <= 2) runs the integer projections row-parallel: the 8-lane groups of a
+// wavefront each take one block of a row, and the reference's per-lane fp32 chain then runs
+// over the per-block results in LDS, in block order. Larger passes run eight rows per
+// wavefront, each lane walking its row's blocks in order; both give the same bits.
 // Positions and row counts come from the device-side step record, so a captured HIP graph
 // replays at any position. References are to smollm_chat.rs unless a file is named.
 #include <float.h>
@@ -39,7 +46,7 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, __shfl_xor(v, 32));
   return v;
 }
-#define SPX_DPP64(v, ctrl)                                                                              \
+#define SPX_DPP64(v, ctrl)                                                                                         \
   (((unsigned long long)(uint32_t)__builtin_amdgcn_mov_dpp((int)((v) >> 32), (ctrl), 0xF, 0xF, true) << 32) | \
    (unsigned long long)(uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v), (ctrl), 0xF, 0xF, true))
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
@@ -54,20 +61,16 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
 }
 
 // ------------------------------------------------------------------ cross-workgroup hand-off
-// Values one workgroup leaves for the last workgroup of a kernel go through relaxed
-// agent-scope atomic stores and loads (global_store / global_load with sc1: coherent across
-// the XCDs' L2s per location), so no workgroup has to write back or invalidate a whole L2.
-// arrive(): every store of this workgroup has completed (s_waitcnt 0 + barrier) before one
-// thread bumps the counter; returns the counter's previous value to every thread.
-__device__ __forceinline__ void st_dev(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ float ld_dev(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// Values one workgroup leaves for the last workgroup of a launch go through agent-coherent
+// (sc1) stores and loads: relaxed agent-scope atomics for scalars, raw buffer operations with
+// the sc1 bit for vectors (these the compiler can batch). No workgroup writes back or
+// invalidates a whole L2. Before a workgroup counts itself in, all its stores have completed
+// (s_waitcnt 0) and its waves have met at a barrier.
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef float f2v __attribute__((ext_vector_type(2)));
 typedef int i4v __attribute__((ext_vector_type(4)));
 typedef int i2v __attribute__((ext_vector_type(2)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
-// Raw buffer view of [base, base + 2 GB) for agent-coherent (sc1) vector loads and stores that
-// the compiler can batch (unlike atomic loads).
 __device__ __forceinline__ rsrc_t rsrc_of(const void *base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
 }
@@ -75,6 +78,10 @@ __device__ __forceinline__ f4v ld_coh4(rsrc_t r, int off) { return __builtin_bit
 __device__ __forceinline__ f2v ld_coh2(rsrc_t r, int off) { return __builtin_bit_cast(f2v, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 16)); }
 __device__ __forceinline__ void st_coh4(rsrc_t r, int off, f4v v) { __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, v), r, off, 0, 16); }
 __device__ __forceinline__ void st_coh2(rsrc_t r, int off, f2v v) { __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2v, v), r, off, 0, 16); }
+__device__ __forceinline__ void st_dev(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ float ld_dev(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// Single counter: returns the counter's previous value to every thread.
 __device__ __forceinline__ int arrive(int *counter) {
   __shared__ int prev;
   __builtin_amdgcn_s_waitcnt(0);
@@ -82,6 +89,28 @@ __device__ __forceinline__ int arrive(int *counter) {
   if (threadIdx.x == 0) prev = atomicAdd(counter, 1);
   __syncthreads();
   return prev;
+}
+// Two-level count for launches with many workgroups (no hot counter): workgroup w counts
+// into sub-counter w % CNT_SUB; the last of each sub-counter counts into the top counter.
+// True in every thread of the last of the n workgroups. Counters are left at zero.
+__device__ __forceinline__ bool arrive_last(int *cnt, int n) {
+  __shared__ int last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int wg = blockIdx.x + blockIdx.y * gridDim.x, sub = wg % CNT_SUB;
+    const int expect = (n - sub + CNT_SUB - 1) / CNT_SUB, nsub = n < CNT_SUB ? n : CNT_SUB;
+    int l = 0;
+    int *sc = cnt + (1 + sub) * CNT_STRIDE;
+    if (atomicAdd(sc, 1) == expect - 1) {
+      *sc = 0;
+      l = atomicAdd(cnt, 1) == nsub - 1;
+      if (l) *cnt = 0;
+    }
+    last = l;
+  }
+  __syncthreads();
+  return last;
 }
 
 // ------------------------------------------------------------------ Q8_K of one block
@@ -109,77 +138,72 @@ __device__ __forceinline__ void q8k_block_store(float4 x, float amax, uint32_t *
 
 __device__ __forceinline__ float amax4(float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); }
 
-// ------------------------------------------------------------------ prologue
-// Residual add + RMSNorm of row b by one wavefront (lane j holds float4 chunks j + 64t,
-// t < PRO_NT, so dim <= 256 * PRO_NT).
-// Outputs (each optional): xs = normalised fp32 row, (yq, yd, ybs) = its permuted Q8_K;
-// the writer also stores the sum to p.xb and the outputs to p.xn_out / p.q_out.
-__device__ __forceinline__ void pro_row(const Pro &p, int b, bool writer, float *xs, uint32_t *yq, float *yd, int *ybs) {
-  const int lane = threadIdx.x & 63;
-  const int dim = p.dim, n4 = dim >> 2, nt = (n4 + 63) >> 6;
-  const float4 *xa4 = reinterpret_cast<const float4 *>(p.xa + (int64_t)b * dim);
-  const float4 *pa4 = p.pa ? reinterpret_cast<const float4 *>(p.pa + (int64_t)b * dim) : nullptr;
-  const float4 *w4 = reinterpret_cast<const float4 *>(p.nw);
-  float4 xr[PRO_NT];
-  float ss = 0.0f;
+// ------------------------------------------------------------------ norm tail
+// Rows [b0, b1) of a NormTail by all NW wavefronts of the workgroup. Wave w takes the
+// 256-value blocks w, w+NW, ...; lane j holds values 4j..4j+3 of a block.
+template <int NW>
+__device__ __forceinline__ void norm_rows(const NormTail &t, int b0, int b1) {
+  __shared__ float bsum[NORM_NT];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int dim = t.dim, n4 = dim >> 2, nblk = (n4 + 63) >> 6, nbq = dim >> 8;
+  const rsrc_t ra = rsrc_of(t.add ? t.add : t.x);
+  const float4 *x4 = reinterpret_cast<const float4 *>(t.x);
+  const float4 *w4 = reinterpret_cast<const float4 *>(t.nw);
+  for (int b = b0; b < b1; b++) {
+    float4 r[NORM_NT / NW];
 #pragma unroll
-  for (int t = 0; t < PRO_NT; t++) {
-    xr[t] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (t < nt) {
-      const int f = lane + 64 * t;
-      if (f < n4) {
-        float4 v = xa4[f];
-        if (pa4) {
-          const float4 q = pa4[f];
-          v.x = v.x + p.rscale * q.x; v.y = v.y + p.rscale * q.y;
-          v.z = v.z + p.rscale * q.z; v.w = v.w + p.rscale * q.w;
+    for (int k = 0; k < NORM_NT / NW; k++) {
+      const int tb = wave + NW * k, f = tb * 64 + lane;
+      r[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (tb < nblk) {
+        if (f < n4) {
+          float4 v = x4[(int64_t)b * n4 + f];
+          if (t.add) {
+            const f4v a = ld_coh4(ra, (b * n4 + f) * 16);
+            v.x = v.x + t.rscale * a.x; v.y = v.y + t.rscale * a.y; v.z = v.z + t.rscale * a.z; v.w = v.w + t.rscale * a.w;
+          }
+          r[k] = v;
         }
-        xr[t] = v;
-      }
-      ss = fmaf(xr[t].x, xr[t].x, ss); ss = fmaf(xr[t].y, xr[t].y, ss);
-      ss = fmaf(xr[t].z, xr[t].z, ss); ss = fmaf(xr[t].w, xr[t].w, ss);
-    }
-  }
-  ss = wave_sum(ss);
-  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)dim) + p.eps));
-  float am[PRO_NT];
-#pragma unroll
-  for (int t = 0; t < PRO_NT; t++) {
-    am[t] = 0.0f;
-    if (t < nt) {
-      const int f = lane + 64 * t;
-      if (f < n4) {
-        if (writer && p.xb) reinterpret_cast<float4 *>(p.xb + (int64_t)b * dim)[f] = xr[t];
-        const float4 w = w4[f];
-        float4 v = xr[t];
-        v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
-        xr[t] = v;
-        if (xs) reinterpret_cast<float4 *>(xs)[f] = v;
-        if (writer && p.xn_out) reinterpret_cast<float4 *>(p.xn_out + (int64_t)b * dim)[f] = v;
-        am[t] = amax4(v);
+        float p = r[k].x * r[k].x;
+        p = fmaf(r[k].y, r[k].y, p);
+        p = fmaf(r[k].z, r[k].z, p);
+        p = fmaf(r[k].w, r[k].w, p);
+        p = wave_sum(p);
+        if (lane == 0) bsum[tb] = p;
       }
     }
-  }
-  if (!yq && !(writer && p.q_out.q)) return;
-  // Q8_K (dim % 256 == 0 here): block t = chunks 64t .. 64t+63
+    __syncthreads();
+    float S = 0.0f;
+    for (int k = 0; k < nblk; k++) S = S + bsum[k];
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(S, (float)dim) + t.eps));
 #pragma unroll
-  for (int t = 0; t < PRO_NT; t++)
-    if (t < nt) am[t] = wave_max(am[t]);
-  const int nb = dim >> 8;
-#pragma unroll
-  for (int t = 0; t < PRO_NT; t++) {
-    if (t < nt) {
-      if (yq) q8k_block_store(xr[t], am[t], yq + t * 64, yd + t, ybs + t * 16);
-      if (writer && p.q_out.q) {
-        const int64_t vb = (int64_t)b * nb + t;
-        q8k_block_store(xr[t], am[t], p.q_out.q + vb * 64, p.q_out.d + vb, reinterpret_cast<int *>(p.q_out.bs + vb * 8));
+    for (int k = 0; k < NORM_NT / NW; k++) {
+      const int tb = wave + NW * k, f = tb * 64 + lane;
+      if (tb < nblk) {
+        float4 v = r[k];
+        if (f < n4) {
+          if (t.x_out) reinterpret_cast<float4 *>(t.x_out)[(int64_t)b * n4 + f] = v;
+          const float4 w = w4[f];
+          v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
+          if (t.xn_out) reinterpret_cast<float4 *>(t.xn_out)[(int64_t)b * n4 + f] = v;
+        }
+        if (t.q_out.q) {
+          const float am = wave_max(amax4(v));
+          const int64_t vb = (int64_t)b * nbq + tb;
+          q8k_block_store(v, am, t.q_out.q + vb * 64, t.q_out.d + vb, reinterpret_cast<int *>(t.q_out.bs + vb * 8));
+        }
       }
     }
+    __syncthreads();
   }
 }
 
-// LDS image of m permuted Q8_K vectors of `dim` columns: q [m][dim/4], d [m][nb], bs [m][nb][8].
+// ------------------------------------------------------------------ activations in LDS
 __host__ __device__ inline size_t ldsq_dbytes(int mt, int dim) { return ((size_t)mt * (dim / 256) * 4 + 15) & ~(size_t)15; }
+__host__ __device__ inline size_t ldsq_bytes(int mt, int dim) {
+  return ((size_t)mt * dim + ldsq_dbytes(mt, dim) + (size_t)mt * (dim / 256) * 64 + 15) & ~(size_t)15;
+}
+// LDS image of mt permuted Q8_K vectors of dim columns: q [mt][dim/4], d [mt][nb], bs [mt][nb][8].
 __device__ __forceinline__ Q8KP ldsq_of(uint8_t *smem, int mt, int dim) {
   Q8KP r;
   r.q = reinterpret_cast<uint32_t *>(smem);
@@ -187,63 +211,132 @@ __device__ __forceinline__ Q8KP ldsq_of(uint8_t *smem, int mt, int dim) {
   r.bs = reinterpret_cast<int2 *>(smem + (size_t)mt * dim + ldsq_dbytes(mt, dim));
   return r;
 }
-__host__ __device__ inline size_t ldsq_bytes(int mt, int dim) { return (size_t)mt * dim + ldsq_dbytes(mt, dim) + (size_t)mt * (dim / 256) * 64; }
 
-// All waves of the workgroup: prologue of rows 0..m-1 into LDS as permuted Q8_K.
-template <int NW>
-__device__ __forceinline__ void pro_q8k(const Pro &p, int m, const Q8KP &lq, bool writer) {
-  const int wave = threadIdx.x >> 6, nb = p.dim >> 8;
-  for (int v = wave; v < m; v += NW)
-    pro_row(p, v, writer, nullptr, lq.q + (int64_t)v * (p.dim >> 2), lq.d + v * nb, reinterpret_cast<int *>(lq.bs + v * nb * 8));
-  __syncthreads();
-}
-// ... or as fp32 rows [m][dim].
-template <int NW>
-__device__ __forceinline__ void pro_f32(const Pro &p, int v0, int nv, float *xs, bool writer) {
-  const int wave = threadIdx.x >> 6;
-  for (int v = wave; v < nv; v += NW) pro_row(p, v0 + v, writer, xs + (int64_t)v * p.dim, nullptr, nullptr, nullptr);
-  __syncthreads();
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+// Copies permuted Q8_K vectors vsrc(u), u < nv, of `cols` columns from global y into the LDS
+// image ly (vector u at slot u) with direct global->LDS loads (lane i's piece lands at
+// M0 + size * i) spread over the workgroup's nw waves. Each region (codes, d, bsums) is
+// contiguous in LDS across vectors, so a wave's destinations are consecutive.
+template <class F>
+__device__ __forceinline__ void stage_q8kp(const Q8KP &ly, const Q8KP &y, int cols, int nv, int nw, F vsrc) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nb = cols >> 8;
+  const int pq = cols / 16, pb = nb * 4;  // 16-byte pieces per vector: codes, bsums (nb * 64 bytes)
+  for (int p0 = wave * 64; p0 < nv * pq; p0 += nw * 64) {
+    const int p = p0 + lane, u = p / pq, w = p - u * pq;
+    if (p < nv * pq)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(y.q) + (int64_t)vsrc(u) * cols + 16 * w,
+                                       (lds_ptr)(reinterpret_cast<uint8_t *>(ly.q) + 16 * p0), 16, 0, 0);
+  }
+  for (int p0 = wave * 64; p0 < nv * pb; p0 += nw * 64) {
+    const int p = p0 + lane, u = p / pb, w = p - u * pb;
+    if (p < nv * pb)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(y.bs + (int64_t)vsrc(u) * nb * 8) + 16 * w,
+                                       (lds_ptr)(reinterpret_cast<uint8_t *>(ly.bs) + 16 * p0), 16, 0, 0);
+  }
+  for (int p0 = wave * 64; p0 < nv * nb; p0 += nw * 64) {
+    const int p = p0 + lane, u = p / nb, w = p - u * nb;
+    if (p < nv * nb)
+      __builtin_amdgcn_global_load_lds(y.d + (int64_t)vsrc(u) * nb + w, (lds_ptr)(reinterpret_cast<uint8_t *>(ly.d) + 4 * p0), 4, 0, 0);
+  }
 }
 
-// ------------------------------------------------------------------ integer row walker
-template <int T, int D>
-__device__ __forceinline__ void kq_preload(KQRaw<T> *buf, const Planes &pl, int64_t g0, int nb, int l) {
+// ------------------------------------------------------------------ integer tiles in LDS
+// A wavefront's slots (rows) x nb blocks of a K-quant tensor are copied into LDS with direct
+// loads, then the blocks are read from LDS. Tile layout, plane by plane, slot-major:
+//   Q4_K: codes [ns][nb][128], headers [ns][nb][16]
+//   Q6_K: ql [ns][nb][128], qh [ns][nb][64], scales [ns][nb][16], d [ns][nb] as the dword
+//         that holds the 2-byte d (the dword at the record's address rounded down to 4)
+template <int T> struct KQPlanes;
+template <> struct KQPlanes<T_Q4K> {
+  static constexpr int NP = 2;
+  __host__ __device__ static constexpr int rec(int k) { return k == 0 ? 128 : 16; }
+  __host__ __device__ static constexpr int lrec(int k) { return rec(k); }
+};
+template <> struct KQPlanes<T_Q6K> {
+  static constexpr int NP = 4;
+  __host__ __device__ static constexpr int rec(int k) { return k == 0 ? 128 : k == 1 ? 64 : k == 2 ? 16 : 2; }
+  __host__ __device__ static constexpr int lrec(int k) { return k == 3 ? 4 : rec(k); }
+};
+__host__ __device__ constexpr int tile_bpb() { return 128 + 64 + 16 + 4; }  // LDS bytes per block, the larger of Q4_K and Q6_K
+
+// src(s) = global row index (expert * rows + row) of slot s < ns, or -1 for an empty slot.
+template <int T, class F>
+__device__ __forceinline__ void tile_fetch(uint8_t *tile, const Planes &pl, int ns, int nb, F src) {
+  const int lane = threadIdx.x & 63;
+  const uint8_t *planes[4] = {pl.p0, pl.p1, pl.p2, pl.p3};
+  int off = 0;
 #pragma unroll
-  for (int j = 0; j < D; j++)
-    if (j < nb) buf[j].load(pl, g0 + j, l);
+  for (int k = 0; k < KQPlanes<T>::NP; k++) {
+    const int R = KQPlanes<T>::rec(k);
+    if (R >= 16) {
+      const int per = nb * R / 16, total = ns * per;
+      for (int p0 = 0; p0 < total; p0 += 64) {
+        const int p = p0 + lane, sl = p / per, w = p - sl * per;
+        const int64_t grow = p < total ? src(sl) : -1;
+        if (grow >= 0) __builtin_amdgcn_global_load_lds(planes[k] + grow * nb * R + 16 * w, (lds_ptr)(tile + off + 16 * p0), 16, 0, 0);
+      }
+    } else {  // 2-byte records: the dword holding each
+      const int total = ns * nb;
+      for (int p0 = 0; p0 < total; p0 += 64) {
+        const int p = p0 + lane, sl = p / nb, w = p - sl * nb;
+        const int64_t grow = p < total ? src(sl) : -1;
+        if (grow >= 0) {
+          const uintptr_t a = reinterpret_cast<uintptr_t>(planes[k] + (grow * nb + w) * 2) & ~(uintptr_t)3;
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(a), (lds_ptr)(tile + off + 4 * p0), 4, 0, 0);
+        }
+      }
+    }
+    off += ns * nb * KQPlanes<T>::lrec(k);
+  }
 }
 
-// Continues kq_preload: blocks in order, D in flight. Vector v of this row group is
-// activation vector vidx[v] of y (cols columns); mv = the row group's vector count.
-template <int T, int MT, int D>
-__device__ __forceinline__ void kq_walk(KQRaw<T> *buf, const Planes &pl, int64_t g0, int nb, const Q8KP &y, const int *vidx, int mv, int l,
-                                        float *res) {
+// Block i of slot s as lane l needs it. odd = the block's global index is odd (Q6_K d half).
+__device__ __forceinline__ void tile_block(const uint8_t *tile, int ns, int nb, int s, int i, int l, bool odd, KQRaw<T_Q4K> &r) {
+  const int rec = s * nb + i;
+  r.c = *reinterpret_cast<const uint4 *>(tile + rec * 128 + 16 * l);
+  r.h = *reinterpret_cast<const uint4 *>(tile + ns * nb * 128 + rec * 16);
+}
+__device__ __forceinline__ void tile_block(const uint8_t *tile, int ns, int nb, int s, int i, int l, bool odd, KQRaw<T_Q6K> &r) {
+  const int rec = s * nb + i;
+  r.ql = *reinterpret_cast<const uint4 *>(tile + rec * 128 + 16 * l);
+  r.qh = *reinterpret_cast<const uint2 *>(tile + ns * nb * 128 + rec * 64 + 8 * l);
+  r.sc = *reinterpret_cast<const uint4 *>(tile + ns * nb * 192 + rec * 16);
+  r.d = (*reinterpret_cast<const uint32_t *>(tile + ns * nb * 208 + rec * 4) >> (odd ? 16 : 0)) & 0xffffu;
+}
+
+// One block of one row against one vector (lane l's part): P = the lane's scaled dot,
+// s = the correction integer summed over the row group's 8 lanes.
+template <int T>
+__device__ __forceinline__ void kq_block_dot(const KQDec<T> &dec, const Q8KP &y, int64_t vb, int l, int &P, int &s) {
+  const uint4 *yq = reinterpret_cast<const uint4 *>(y.q + vb * 64 + 8 * l);
+  dec.dot(yq[0], yq[1], y.bs[vb * 8 + l], P, s);
+  s = sum8(s);
+}
+
+// Eight-rows-per-wavefront walker: slot s's row (global row index grow) against vectors
+// vidx[0..mv) of y, blocks in order, the reference's per-lane chain kept in registers.
+template <int T, int MT>
+__device__ __forceinline__ void kq_walk_tile(const uint8_t *tile, int ns, int nb, int s, int64_t grow, const Q8KP &y, const int *vidx, int mv,
+                                             int l, float *res) {
   float acc[MT], corr[MT];
 #pragma unroll
   for (int v = 0; v < MT; v++) { acc[v] = 0.0f; corr[v] = 0.0f; }
-  for (int i0 = 0; i0 < nb; i0 += D) {
+  const bool odd0 = ((grow * nb) & 1) != 0;
+  for (int i = 0; i < nb; i++) {
+    KQRaw<T> r;
+    tile_block(tile, ns, nb, s, i, l, odd0 ^ ((i & 1) != 0), r);
+    KQDec<T> dec;
+    dec.decode(r, l);
 #pragma unroll
-    for (int j = 0; j < D; j++) {
-      const int i = i0 + j;
-      if (i < nb) {
-        KQDec<T> dec;
-        dec.decode(buf[j], l);
-        if (i + D < nb) buf[j].load(pl, g0 + i + D, l);
-#pragma unroll
-        for (int v = 0; v < MT; v++) {
-          if (v < mv) {
-            const int64_t vb = (int64_t)vidx[v] * nb + i;
-            const uint4 *yq = reinterpret_cast<const uint4 *>(y.q + vb * 64 + 8 * l);
-            const uint4 y0 = yq[0], y1 = yq[1];
-            const float xd = y.d[vb];
-            const int2 bs = y.bs[vb * 8 + l];
-            int P, s;
-            dec.dot(y0, y1, bs, P, s);
-            s = sum8(s);
-            corr[v] = corr[v] + dec.corr_term(xd, s);
-            acc[v] = fmaf(dec.d * xd, (float)P, acc[v]);
-          }
-        }
+    for (int v = 0; v < MT; v++) {
+      if (v < mv) {
+        const int64_t vb = (int64_t)vidx[v] * nb + i;
+        int P, sc;
+        kq_block_dot<T>(dec, y, vb, l, P, sc);
+        const float xd = y.d[vb];
+        corr[v] = corr[v] + dec.corr_term(xd, sc);
+        acc[v] = fmaf(dec.d * xd, (float)P, acc[v]);
       }
     }
   }
@@ -251,8 +344,65 @@ __device__ __forceinline__ void kq_walk(KQRaw<T> *buf, const Planes &pl, int64_t
   for (int v = 0; v < MT; v++) res[v] = hsum_rows8(acc[v]) - corr[v];
 }
 
-template <int MT>
-constexpr int kq_depth() { return MT <= 2 ? 8 : MT <= 8 ? 4 : 2; }
+// Row-parallel walker: the wavefront's R slots (rows) x G lane groups; group gi of row r
+// computes blocks gi, gi+G, ... and leaves, per block and vector, d*xd, the 8 lane dots as
+// floats and the correction term in the chain buffer cb (LDS); then group 0 of each row runs
+// the reference's chain acc_l = fma(d*xd_i, float(P_il), acc_l), corr = corr + term_i over
+// the blocks in order. res[v] is valid in lane 0 of group 0 of each row.
+// cb: [R][nb][MT] x {8 lane dots, d*xd, term} floats.
+template <int T, int MT, class GROW, class VID, class MV>
+__device__ __forceinline__ void kq_rows_par(const uint8_t *tile, int ns, int nb, int G, int R, GROW grow_of, VID vid, MV mv_of, const Q8KP &y,
+                                            float *cb, float *res) {
+  const int lane = threadIdx.x & 63, l = lane & 7, grp = lane >> 3;
+  const int r = grp / G, gi = grp - r * G;
+  if (r < R) {
+    const int64_t grow = grow_of(r);
+    const int mv = mv_of(r);
+    const bool odd0 = ((grow * nb) & 1) != 0;
+    for (int i = gi; i < nb; i += G) {
+      KQRaw<T> raw;
+      tile_block(tile, ns, nb, r, i, l, odd0 ^ ((i & 1) != 0), raw);
+      KQDec<T> dec;
+      dec.decode(raw, l);
+#pragma unroll
+      for (int v = 0; v < MT; v++) {
+        if (v < mv) {
+          const int64_t vb = (int64_t)vid(r, v) * nb + i;
+          int P, sc;
+          kq_block_dot<T>(dec, y, vb, l, P, sc);
+          const float xd = y.d[vb];
+          float *e = cb + (((int64_t)r * nb + i) * MT + v) * 10;
+          e[l] = (float)P;
+          if (l == 0) { e[8] = dec.d * xd; e[9] = dec.corr_term(xd, sc); }
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  float corr[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) { res[v] = 0.0f; corr[v] = 0.0f; }
+  const bool chain = r < R && gi == 0;
+  const int mvc = chain ? mv_of(r) : 0;
+  if (chain) {
+#pragma unroll
+    for (int v = 0; v < MT; v++) {
+      if (v < mvc) {
+        float acc = 0.0f, cr = 0.0f;
+        for (int i = 0; i < nb; i++) {
+          const float *e = cb + (((int64_t)r * nb + i) * MT + v) * 10;
+          acc = fmaf(e[8], e[l], acc);
+          cr = cr + e[9];
+        }
+        res[v] = acc;
+        corr[v] = cr;
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < MT; v++) res[v] = hsum_rows8(res[v]) - corr[v];
+}
 
 // ------------------------------------------------------------------ float row walker
 // Q8_0 / Q5_0 weights x fp32 activations (quant.rs:48-161, quant_multi.rs:168-190): lane l
@@ -374,6 +524,7 @@ template <int MT>
 constexpr int f_depth() { return MT <= 2 ? 4 : 2; }
 
 // ------------------------------------------------------------------ greedy-pick keys
+// ------------------------------------------------------------------ greedy-pick keys
 // logits / logit_scale, then the last maximum under f32 total order (max_by(total_cmp),
 // :3661-3671): key = total-order bits as unsigned, packed above the row index so that the
 // larger packed value is the larger logit and, on ties, the higher index.
@@ -401,274 +552,169 @@ __device__ __forceinline__ void best_flush(const MVArgs &a, unsigned long long (
   }
 }
 
-// ------------------------------------------------------------------ integer tiles in LDS
-// A wavefront's 8 row slots x nb blocks of a K-quant tensor are copied into LDS with direct
-// global->LDS loads (global_load_lds_dwordx4: lane i's 16 bytes land at M0 + 16 i), then the
-// blocks are walked from LDS in a compact loop. LDS tile layout, plane by plane, slot-major:
-//   Q4_K: codes [8][nb][128], headers [8][nb][16]
-//   Q6_K: ql [8][nb][128], qh [8][nb][64], scales [8][nb][16], d [8][nb] as the dword that
-//         holds the 2-byte d (the dword at the record's address rounded down to 4)
-typedef __attribute__((address_space(3))) void *lds_ptr;
-template <int T> struct KQPlanes;
-template <> struct KQPlanes<T_Q4K> {
-  static constexpr int NP = 2;
-  __host__ __device__ static constexpr int rec(int k) { return k == 0 ? 128 : 16; }   // global bytes per block
-  __host__ __device__ static constexpr int lrec(int k) { return rec(k); }             // LDS bytes per block
-};
-template <> struct KQPlanes<T_Q6K> {
-  static constexpr int NP = 4;
-  __host__ __device__ static constexpr int rec(int k) { return k == 0 ? 128 : k == 1 ? 64 : k == 2 ? 16 : 2; }
-  __host__ __device__ static constexpr int lrec(int k) { return k == 3 ? 4 : rec(k); }
-};
-__host__ __device__ constexpr int tile_bytes_per_block() { return 128 + 64 + 16 + 4; }  // the larger of Q4_K (144) and Q6_K (212)
-
-// src(s) = global row index (expert * rows + row) of slot s, or -1 for an empty slot.
-template <int T, class F>
-__device__ __forceinline__ void tile_fetch(uint8_t *tile, const Planes &pl, int nb, F src) {
-  const int lane = threadIdx.x & 63;
-  const uint8_t *planes[4] = {pl.p0, pl.p1, pl.p2, pl.p3};
-  int off = 0;
-#pragma unroll
-  for (int k = 0; k < KQPlanes<T>::NP; k++) {
-    const int R = KQPlanes<T>::rec(k);
-    if (R >= 16) {
-      const int per = nb * R / 16, total = 8 * per;
-      for (int p0 = 0; p0 < total; p0 += 64) {
-        const int p = p0 + lane, sl = p / per, w = p - sl * per;
-        const int64_t grow = p < total ? src(sl) : -1;
-        if (grow >= 0) __builtin_amdgcn_global_load_lds(planes[k] + grow * nb * R + 16 * w, (lds_ptr)(tile + off + 16 * p0), 16, 0, 0);
-      }
-    } else {  // 2-byte records: the dword holding each
-      const int total = 8 * nb;
-      for (int p0 = 0; p0 < total; p0 += 64) {
-        const int p = p0 + lane, sl = p / nb, w = p - sl * nb;
-        const int64_t grow = p < total ? src(sl) : -1;
-        if (grow >= 0) {
-          const uintptr_t a = reinterpret_cast<uintptr_t>(planes[k] + (grow * nb + w) * 2) & ~(uintptr_t)3;
-          __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(a), (lds_ptr)(tile + off + 4 * p0), 4, 0, 0);
-        }
-      }
-    }
-    off += 8 * nb * KQPlanes<T>::lrec(k);
-  }
+// A launch output a norm tail will read is stored coherently.
+__device__ __forceinline__ void out_store(float *p, float v, bool coh) {
+  if (coh) st_dev(p, v);
+  else *p = v;
 }
 
-// Block i of slot s as lane l needs it. odd = the block's global index is odd (Q6_K d half).
-__device__ __forceinline__ void tile_block(const uint8_t *tile, int nb, int s, int i, int l, bool odd, KQRaw<T_Q4K> &r) {
-  const int rec = s * nb + i;
-  r.c = *reinterpret_cast<const uint4 *>(tile + rec * 128 + 16 * l);
-  r.h = *reinterpret_cast<const uint4 *>(tile + 8 * nb * 128 + rec * 16);
-}
-__device__ __forceinline__ void tile_block(const uint8_t *tile, int nb, int s, int i, int l, bool odd, KQRaw<T_Q6K> &r) {
-  const int rec = s * nb + i;
-  r.ql = *reinterpret_cast<const uint4 *>(tile + rec * 128 + 16 * l);
-  r.qh = *reinterpret_cast<const uint2 *>(tile + 8 * nb * 128 + rec * 64 + 8 * l);
-  r.sc = *reinterpret_cast<const uint4 *>(tile + 8 * nb * 192 + rec * 16);
-  r.d = (*reinterpret_cast<const uint32_t *>(tile + 8 * nb * 208 + rec * 4) >> (odd ? 16 : 0)) & 0xffffu;
+// Segment of workgroup task t and the task's index within it. The index is computed with
+// selects and made wave-uniform, so the segment's fields are read from the kernel arguments
+// directly (no branchy selection between argument sub-objects).
+__device__ __forceinline__ int seg_index(const MVArgs &a, int t, int &wg) {
+  const int w0 = a.seg[0].wgs, w1 = a.nseg > 1 ? a.seg[1].wgs : 0;
+  const int i = a.nseg > 1 && t >= w0 ? (a.nseg > 2 && t >= w0 + w1 ? 2 : 1) : 0;
+  wg = t - (i > 0 ? w0 : 0) - (i > 1 ? w1 : 0);
+  return __builtin_amdgcn_readfirstlane(i);
 }
 
-// The row of slot s (global row index grow) against vectors vidx[0..mv) of y (LDS or global).
-template <int T, int MT>
-__device__ __forceinline__ void kq_walk_tile(const uint8_t *tile, int nb, int s, int64_t grow, const Q8KP &y, const int *vidx, int mv, int l,
-                                             float *res) {
-  float acc[MT], corr[MT];
-#pragma unroll
-  for (int v = 0; v < MT; v++) { acc[v] = 0.0f; corr[v] = 0.0f; }
-  const bool odd0 = ((grow * nb) & 1) != 0;
-#pragma unroll 2
-  for (int i = 0; i < nb; i++) {
-    KQRaw<T> r;
-    tile_block(tile, nb, s, i, l, odd0 ^ ((i & 1) != 0), r);
-    KQDec<T> dec;
-    dec.decode(r, l);
-#pragma unroll
-    for (int v = 0; v < MT; v++) {
-      if (v < mv) {
-        const int64_t vb = (int64_t)vidx[v] * nb + i;
-        const uint4 *yq = reinterpret_cast<const uint4 *>(y.q + vb * 64 + 8 * l);
-        const uint4 y0 = yq[0], y1 = yq[1];
-        const float xd = y.d[vb];
-        const int2 bs = y.bs[vb * 8 + l];
-        int P, sc;
-        dec.dot(y0, y1, bs, P, sc);
-        sc = sum8(sc);
-        corr[v] = corr[v] + dec.corr_term(xd, sc);
-        acc[v] = fmaf(dec.d * xd, (float)P, acc[v]);
-      }
-    }
-  }
-#pragma unroll
-  for (int v = 0; v < MT; v++) res[v] = hsum_rows8(acc[v]) - corr[v];
-}
-
-// Copies permuted Q8_K vectors vsrc(u), u < nv, of `cols` columns from global y into the LDS
-// image ly (vector u at slot u) with direct loads spread over the workgroup's nw waves. Each
-// region (codes, d, bsums) is contiguous in LDS across vectors, so a wave's destinations are
-// consecutive: 16-byte pieces for codes and bsums, 4-byte pieces for d.
-template <class F>
-__device__ __forceinline__ void stage_q8kp(const Q8KP &ly, const Q8KP &y, int cols, int nv, int nw, F vsrc) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nb = cols >> 8;
-  const int pq = cols / 16, pb = nb * 4;  // 16-byte pieces per vector: codes, bsums (nb * 64 bytes)
-  for (int p0 = wave * 64; p0 < nv * pq; p0 += nw * 64) {
-    const int p = p0 + lane, u = p / pq, w = p - u * pq;
-    if (p < nv * pq)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(y.q) + (int64_t)vsrc(u) * cols + 16 * w,
-                                       (lds_ptr)(reinterpret_cast<uint8_t *>(ly.q) + 16 * p0), 16, 0, 0);
-  }
-  for (int p0 = wave * 64; p0 < nv * pb; p0 += nw * 64) {
-    const int p = p0 + lane, u = p / pb, w = p - u * pb;
-    if (p < nv * pb)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(y.bs + (int64_t)vsrc(u) * nb * 8) + 16 * w,
-                                       (lds_ptr)(reinterpret_cast<uint8_t *>(ly.bs) + 16 * p0), 16, 0, 0);
-  }
-  for (int p0 = wave * 64; p0 < nv * nb; p0 += nw * 64) {
-    const int p = p0 + lane, u = p / nb, w = p - u * nb;
-    if (p < nv * nb)
-      __builtin_amdgcn_global_load_lds(y.d + (int64_t)vsrc(u) * nb + w, (lds_ptr)(reinterpret_cast<uint8_t *>(ly.d) + 4 * p0), 4, 0, 0);
-  }
-}
-
-// ------------------------------------------------------------------ matvec kernels
-// Workgroups of NW wavefronts, 8 rows per wavefront; a workgroup belongs to one segment
-// (all its rows share a dtype). Without a prologue the grid may be smaller than the work:
-// workgroups then stride over it.
-template <int T, int NW>
-__device__ __forceinline__ void mvt_fetch(const Seg &sg, int wg, uint8_t *tiles) {
-  const int wave = threadIdx.x >> 6;
-  const int nb = (int)sg.w.nb;
-  const int64_t ebase = (int64_t)sg.expert * sg.w.rows, rbase = sg.r0 + ((int64_t)wg * NW + wave) * 8;
-  tile_fetch<T>(tiles + (size_t)wave * 8 * nb * tile_bytes_per_block(), sg.w.pl, nb,
-                [&](int sl) -> int64_t { const int64_t r = rbase + sl; return r < sg.r1 ? ebase + r : -1; });
-}
-
-template <int T, int MT, int NW>
-__device__ __forceinline__ void mvt_walk(const MVArgs &a, const Seg &sg, int wg, int m, const uint8_t *tiles, const Q8KP &ly, bool want_best,
-                                         unsigned long long (&bestv)[MT]) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
-  const int nb = (int)sg.w.nb;
-  const int64_t ebase = (int64_t)sg.expert * sg.w.rows, row = sg.r0 + ((int64_t)wg * NW + wave) * 8 + slot;
-  const bool valid = row < sg.r1;
-  int vidx[MT];
-#pragma unroll
-  for (int v = 0; v < MT; v++) vidx[v] = v;
-  float res[MT];
-  kq_walk_tile<T, MT>(tiles + (size_t)wave * 8 * nb * tile_bytes_per_block(), nb, slot, ebase + (valid ? row : sg.r1 - 1), ly, vidx, m, l, res);
-  if (valid && l == 0) {
-#pragma unroll
-    for (int v = 0; v < MT; v++)
-      if (v < m) sg.out[(int64_t)v * sg.ld_out + row] = res[v];
-  }
-  if (want_best) {
-#pragma unroll
-    for (int v = 0; v < MT; v++)
-      if (valid && l == 0 && v < m) {
-        const unsigned long long k = pick_key(res[v], a.lscale, row);
-        bestv[v] = k > bestv[v] ? k : bestv[v];
-      }
-  }
-}
-
-// Integer matvec: workgroups of NW wavefronts, 8 rows per wavefront, one segment per
-// workgroup (all its rows share a dtype). Without a prologue the grid may be smaller than the
-// work: workgroups then stride over it. LDS: activations (permuted Q8_K), then one tile per
-// wave; the tile's direct loads are in flight while the prologue or activation copy runs.
-template <int MT, int NW, bool PRO>
-__global__ __launch_bounds__(NW * 64) void k_mvt(const MVArgs a, const StepRec *st) {
+// ------------------------------------------------------------------ integer matvec, 8 rows per wavefront
+// One wavefront per workgroup, eight rows per task; tasks stride over the grid (the LM head
+// runs on a few thousand workgroups). LDS: the activations (staged once), then the tile.
+template <int MT>
+__global__ __launch_bounds__(64) void k_mvt(const MVArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int m = st ? st->m : a.m;
-  const int cols = (int)a.seg[0].w.cols;
+  const int lane = threadIdx.x, slot = lane >> 3, l = lane & 7;
+  const int cols = (int)a.seg[0].w.cols, nb = cols >> 8;
   const Q8KP ly = ldsq_of(smem, MT, cols);
-  uint8_t *tiles = smem + ((ldsq_bytes(MT, cols) + 15) & ~(size_t)15);
+  uint8_t *tile = smem + ldsq_bytes(MT, cols);
+  const bool coh = a.tail.nw != nullptr;
   unsigned long long bestv[MT];
 #pragma unroll
   for (int v = 0; v < MT; v++) bestv[v] = 0;
   const int total = a.seg[0].wgs + (a.nseg > 1 ? a.seg[1].wgs : 0) + (a.nseg > 2 ? a.seg[2].wgs : 0);
   bool first = true;
   for (int t = blockIdx.x; t < total; t += gridDim.x) {
-    int s = 0, wg = t;
-    if (a.nseg > 1 && wg >= a.seg[0].wgs) { wg -= a.seg[0].wgs; s = 1; if (a.nseg > 2 && wg >= a.seg[1].wgs) { wg -= a.seg[1].wgs; s = 2; } }
-    const Seg sg = s == 0 ? a.seg[0] : s == 1 ? a.seg[1] : a.seg[2];
+    int wg;
+    const Seg &sg = a.seg[seg_index(a, t, wg)];
+    const int64_t ebase = (int64_t)sg.expert * sg.w.rows, rbase = sg.r0 + (int64_t)wg * 8, r1 = sg.r1;
     const bool q4 = sg.w.dtype == T_Q4K;
-    if (q4) mvt_fetch<T_Q4K, NW>(sg, wg, tiles); else mvt_fetch<T_Q6K, NW>(sg, wg, tiles);
-    if (first) {
-      if (PRO) pro_q8k<NW>(a.pro, m, ly, blockIdx.x == 0);
-      else stage_q8kp(ly, a.y, cols, m, NW, [](int u) { return u; });
-    }
+    auto src = [&](int s) -> int64_t { return rbase + s < r1 ? ebase + rbase + s : -1; };
+    if (q4) tile_fetch<T_Q4K>(tile, sg.w.pl, 8, nb, src); else tile_fetch<T_Q6K>(tile, sg.w.pl, 8, nb, src);
+    if (first) stage_q8kp(ly, a.y, cols, m, 1, [](int u) { return u; });
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (q4) mvt_walk<T_Q4K, MT, NW>(a, sg, wg, m, tiles, ly, a.best != nullptr, bestv);
-    else mvt_walk<T_Q6K, MT, NW>(a, sg, wg, m, tiles, ly, a.best != nullptr, bestv);
-    __syncthreads();  // the tiles may be refilled by the next task
+    const int64_t row = rbase + slot;
+    const bool valid = row < r1;
+    int vidx[MT];
+#pragma unroll
+    for (int v = 0; v < MT; v++) vidx[v] = v;
+    float res[MT];
+    const int64_t grow = ebase + (valid ? row : r1 - 1);
+    if (q4) kq_walk_tile<T_Q4K, MT>(tile, 8, nb, slot, grow, ly, vidx, m, l, res);
+    else kq_walk_tile<T_Q6K, MT>(tile, 8, nb, slot, grow, ly, vidx, m, l, res);
+    if (valid && l == 0) {
+#pragma unroll
+      for (int v = 0; v < MT; v++)
+        if (v < m) {
+          out_store(sg.out + (int64_t)v * sg.ld_out + row, res[v], coh);
+          if (a.best) { const unsigned long long k = pick_key(res[v], a.lscale, row); bestv[v] = k > bestv[v] ? k : bestv[v]; }
+        }
+    }
+    __syncthreads();  // the tile may be refilled by the next task
     first = false;
-    if (PRO) break;
   }
-  if (a.best) best_flush<MT, NW>(a, bestv, m);
+  if (a.best) best_flush<MT, 1>(a, bestv, m);
+  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<1>(a.tail, 0, m);
 }
 
-template <int T, int MT, int NW, bool PRO>
-__device__ __forceinline__ void mv_f_task(const MVArgs &a, const Seg &sg, int wg, int m, uint8_t *smem, bool want_best,
-                                          unsigned long long (&bestv)[MT]) {
-  constexpr int D = f_depth<MT>();
+// ------------------------------------------------------------------ integer matvec, row-parallel
+// Four wavefronts per workgroup, R rows per wavefront, G lane groups per row (decode).
+__host__ __device__ inline size_t rp_wave_bytes(int R, int nb, int mt) {
+  return ((size_t)R * nb * tile_bpb() + (size_t)R * nb * mt * 10 * 4 + 15) & ~(size_t)15;
+}
+
+template <int MT>
+__global__ __launch_bounds__(256) void k_mvr(const MVArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int m = st ? st->m : a.m;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l = lane & 7, grp = lane >> 3;
+  const int cols = (int)a.seg[0].w.cols, nb = cols >> 8, G = a.G, R = a.R;
+  const Q8KP ly = ldsq_of(smem, MT, cols);
+  uint8_t *tile = smem + ldsq_bytes(MT, cols) + (size_t)wave * rp_wave_bytes(R, nb, MT);
+  float *cb = reinterpret_cast<float *>(tile + (size_t)R * nb * tile_bpb());
+  const bool coh = a.tail.nw != nullptr;
+  int wg;
+  const Seg &sg = a.seg[seg_index(a, blockIdx.x, wg)];
+  const int64_t ebase = (int64_t)sg.expert * sg.w.rows, rbase = sg.r0 + ((int64_t)wg * 4 + wave) * R, r1 = sg.r1;
+  const bool q4 = sg.w.dtype == T_Q4K;
+  auto src = [&](int s) -> int64_t { return s < R && rbase + s < r1 ? ebase + rbase + s : -1; };
+  if (q4) tile_fetch<T_Q4K>(tile, sg.w.pl, R, nb, src); else tile_fetch<T_Q6K>(tile, sg.w.pl, R, nb, src);
+  stage_q8kp(ly, a.y, cols, m, 4, [](int u) { return u; });
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  float res[MT];
+  auto grow = [&](int r) -> int64_t { return ebase + (rbase + r < r1 ? rbase + r : r1 - 1); };
+  auto vid = [](int r, int v) { return v; };
+  auto mvf = [&](int r) { return m; };
+  if (q4) kq_rows_par<T_Q4K, MT>(tile, R, nb, G, R, grow, vid, mvf, ly, cb, res);
+  else kq_rows_par<T_Q6K, MT>(tile, R, nb, G, R, grow, vid, mvf, ly, cb, res);
+  const int r = grp / G;
+  unsigned long long bestv[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) bestv[v] = 0;
+  if (r < R && grp == r * G && l == 0 && rbase + r < r1) {
+#pragma unroll
+    for (int v = 0; v < MT; v++)
+      if (v < m) {
+        out_store(sg.out + (int64_t)v * sg.ld_out + rbase + r, res[v], coh);
+        if (a.best) bestv[v] = pick_key(res[v], a.lscale, rbase + r);
+      }
+  }
+  if (a.best) best_flush<MT, 4>(a, bestv, m);
+  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
+}
+
+// ------------------------------------------------------------------ float matvec
+// Q8_0 / Q5_0 / F32 weights x fp32 activations; four wavefronts per workgroup, eight rows per
+// wavefront; tasks stride over the grid.
+template <int T, int MT>
+__device__ __forceinline__ void mv_f_task(const MVArgs &a, const Seg &sg, int wg, int m, bool coh, unsigned long long (&bestv)[MT]) {
+  constexpr int D = MT <= 2 ? 4 : 2;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
-  const int nb = (int)sg.w.nb;
-  const int64_t rows = sg.w.rows;
-  const int64_t row = sg.r0 + ((int64_t)wg * NW + wave) * 8 + slot;
+  const int64_t row = sg.r0 + ((int64_t)wg * 4 + wave) * 8 + slot;
   const bool valid = row < sg.r1;
-  const int64_t grow = (int64_t)sg.expert * rows + (valid ? row : sg.r1 - 1);
+  const int64_t grow = (int64_t)sg.expert * sg.w.rows + (valid ? row : sg.r1 - 1);
   int vidx[MT];
 #pragma unroll
   for (int v = 0; v < MT; v++) vidx[v] = v;
   float res[MT];
-  if constexpr (T == T_F32) {
-    f32_walk<MT>(sg.w.pl, grow, sg.w.cols, a.x, a.ld_x, vidx, m, l, res);
-  } else if (PRO) {
-    float *xl = reinterpret_cast<float *>(smem);
-    pro_f32<NW>(a.pro, 0, m, xl, blockIdx.x == 0);
-    f_walk<T, MT, D>(sg.w.pl, grow, nb, xl, a.pro.dim, vidx, m, l, res);
-  } else {
-    f_walk<T, MT, D>(sg.w.pl, grow, nb, a.x, a.ld_x, vidx, m, l, res);
-  }
+  if constexpr (T == T_F32) f32_walk<MT>(sg.w.pl, grow, sg.w.cols, a.x, a.ld_x, vidx, m, l, res);
+  else f_walk<T, MT, D>(sg.w.pl, grow, (int)sg.w.nb, a.x, a.ld_x, vidx, m, l, res);
   if (valid && l == 0) {
 #pragma unroll
     for (int v = 0; v < MT; v++)
-      if (v < m) sg.out[(int64_t)v * sg.ld_out + row] = res[v];
-  }
-  if (want_best) {
-#pragma unroll
-    for (int v = 0; v < MT; v++)
-      if (valid && l == 0 && v < m) {
-        const unsigned long long k = pick_key(res[v], a.lscale, row);
-        bestv[v] = k > bestv[v] ? k : bestv[v];
+      if (v < m) {
+        out_store(sg.out + (int64_t)v * sg.ld_out + row, res[v], coh);
+        if (a.best) { const unsigned long long k = pick_key(res[v], a.lscale, row); bestv[v] = k > bestv[v] ? k : bestv[v]; }
       }
   }
 }
 
-template <int MT, int NW, bool PRO>
-__global__ __launch_bounds__(NW * 64) void k_mv_f(const MVArgs a, const StepRec *st) {
-  extern __shared__ __align__(16) uint8_t smem[];
+template <int MT>
+__global__ __launch_bounds__(256) void k_mv_f(const MVArgs a, const StepRec *st) {
   const int m = st ? st->m : a.m;
+  const bool coh = a.tail.nw != nullptr;
   unsigned long long bestv[MT];
 #pragma unroll
   for (int v = 0; v < MT; v++) bestv[v] = 0;
   const int total = a.seg[0].wgs + (a.nseg > 1 ? a.seg[1].wgs : 0) + (a.nseg > 2 ? a.seg[2].wgs : 0);
   for (int t = blockIdx.x; t < total; t += gridDim.x) {
-    int s = 0, wg = t;
-    if (a.nseg > 1 && wg >= a.seg[0].wgs) { wg -= a.seg[0].wgs; s = 1; if (a.nseg > 2 && wg >= a.seg[1].wgs) { wg -= a.seg[1].wgs; s = 2; } }
-    const Seg sg = s == 0 ? a.seg[0] : s == 1 ? a.seg[1] : a.seg[2];
-    if (sg.w.dtype == T_Q8_0) mv_f_task<T_Q8_0, MT, NW, PRO>(a, sg, wg, m, smem, a.best != nullptr, bestv);
-    else if (sg.w.dtype == T_Q5_0) mv_f_task<T_Q5_0, MT, NW, PRO>(a, sg, wg, m, smem, a.best != nullptr, bestv);
-    else if (!PRO) mv_f_task<T_F32, MT, NW, false>(a, sg, wg, m, smem, a.best != nullptr, bestv);
-    if (PRO) break;
+    int wg;
+    const Seg &sg = a.seg[seg_index(a, t, wg)];
+    if (sg.w.dtype == T_Q8_0) mv_f_task<T_Q8_0, MT>(a, sg, wg, m, coh, bestv);
+    else if (sg.w.dtype == T_Q5_0) mv_f_task<T_Q5_0, MT>(a, sg, wg, m, coh, bestv);
+    else mv_f_task<T_F32, MT>(a, sg, wg, m, coh, bestv);
   }
-  if (a.best) best_flush<MT, NW>(a, bestv, m);
+  if (a.best) best_flush<MT, 4>(a, bestv, m);
+  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
 }
 
-// ------------------------------------------------------------------ standalone norm / quantize
-// Residual + RMSNorm of each row (one wavefront per row): writes xb, xn_out, q_out.
-__global__ __launch_bounds__(64) void k_norm(const Pro p, const StepRec *st) {
-  const int b = blockIdx.x;
-  if (st && b >= st->m) return;
-  pro_row(p, b, true, nullptr, nullptr, nullptr, nullptr);
+// ------------------------------------------------------------------ standalone kernels
+// Standalone norm: one workgroup per row.
+__global__ __launch_bounds__(256) void k_norm(const NormTail t, const StepRec *st) {
+  if ((int)blockIdx.x < st->m) norm_rows<4>(t, blockIdx.x, blockIdx.x + 1);
 }
 
 // fp32 rows -> permuted Q8_K, one wavefront per 256-block.
@@ -715,13 +761,14 @@ __global__ __launch_bounds__(64) void k_kq_block_sums(TensorView w, int expert, 
 }
 
 // ------------------------------------------------------------------ embedding
-// dequant_row (quant.rs:1548-1660) of token rows, times embedding_scale (:3381-3388).
-__global__ __launch_bounds__(256) void k_embed(TensorView e, const StepRec *st, float *x, int64_t ld_x, float escale) {
+// dequant_row (quant.rs:1548-1660) of token rows, times embedding_scale (:3381-3388), into
+// t.x; then the row's norm tail (layer 0's attn_norm). One workgroup per row.
+__global__ __launch_bounds__(256) void k_embed(TensorView e, const StepRec *st, float escale, const NormTail t) {
   const int b = blockIdx.x;
   if (b >= st->m) return;
   const int64_t tok = st->ids[b];
   const int64_t cols = e.cols;
-  float *out = x + b * ld_x;
+  float *out = const_cast<float *>(t.x) + b * cols;
   for (int64_t j = threadIdx.x; j < cols; j += 256) {
     float v = 0.0f;
     if (e.dtype == T_F32) {
@@ -741,7 +788,7 @@ __global__ __launch_bounds__(256) void k_embed(TensorView e, const StepRec *st, 
       v = (float)(q - 16) * dd + 0.0f;
     } else if (e.dtype == T_Q4K) {  // element 64c + 32hi + t: byte qs[32c + t] (device offset 16(t/4) + 4c + t%4)
       const int64_t g = tok * e.nb + j / 256;
-      const int k = (int)(j % 256), c = k / 64, t = k % 32, hi = (k % 64) >= 32;
+      const int k = (int)(j % 256), c = k / 64, tt = k % 32, hi = (k % 64) >= 32;
       const uint8_t *hd = e.pl.p1 + g * 16;
       const float dd = h2f(hd[0] | (hd[1] << 8)), dm = h2f(hd[2] | (hd[3] << 8));
       const uint8_t *s = hd + 4;
@@ -749,23 +796,26 @@ __global__ __launch_bounds__(256) void k_embed(TensorView e, const StepRec *st, 
       int sc, mn;
       if (jj < 4) { sc = s[jj] & 63; mn = s[jj + 4] & 63; }
       else { sc = (s[jj + 4] & 0xF) | ((s[jj - 4] >> 6) << 4); mn = (s[jj + 4] >> 4) | ((s[jj] >> 6) << 4); }
-      const int byte = e.pl.p0[g * 128 + 16 * (t >> 2) + 4 * c + (t & 3)];
+      const int byte = e.pl.p0[g * 128 + 16 * (tt >> 2) + 4 * c + (tt & 3)];
       const int q = hi ? (byte >> 4) : (byte & 0xF);
       v = dd * (float)sc * (float)q - dm * (float)mn;
     } else if (e.dtype == T_Q6K) {  // element 128h + 32mq + t
       const int64_t g = tok * e.nb + j / 256;
-      const int k = (int)(j % 256), h = k / 128, r = k % 128, mq = r / 32, t = r % 32;
-      const int lb = 16 * (t >> 2) + 8 * h + 4 * (mq & 1) + (t & 3);
-      const int hb = 8 * (t >> 2) + 4 * h + (t & 3);
+      const int k = (int)(j % 256), h = k / 128, r = k % 128, mq = r / 32, tt = r % 32;
+      const int lb = 16 * (tt >> 2) + 8 * h + 4 * (mq & 1) + (tt & 3);
+      const int hb = 8 * (tt >> 2) + 4 * h + (tt & 3);
       const int qlb = e.pl.p0[g * 128 + lb], qhb = e.pl.p1[g * 64 + hb];
       const int8_t *sc = reinterpret_cast<const int8_t *>(e.pl.p2 + g * 16);
       const float dd = h2f(*reinterpret_cast<const uint16_t *>(e.pl.p3 + g * 2));
       const int q = ((mq >> 1) ? (qlb >> 4) : (qlb & 0xF)) | (((qhb >> (2 * mq)) & 3) << 4);
-      v = dd * (float)sc[h * 8 + t / 16 + 2 * mq] * (float)(q - 32);
+      v = dd * (float)sc[h * 8 + tt / 16 + 2 * mq] * (float)(q - 32);
     }
     if (escale != 1.0f) v *= escale;
     out[j] = v;
   }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  norm_rows<4>(t, b, b + 1);
 }
 
 // ------------------------------------------------------------------ attention
@@ -942,7 +992,7 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
 #pragma unroll 8
           for (int t = 0; t < 64; t++) {
             const float pv = pr[t];
-            if (DP == 4) {
+            if constexpr (DP == 4) {
               const uint2 vv = *reinterpret_cast<const uint2 *>(vs + t * KS + dd0);
               o[G][0] = fmaf(pv, h2f(vv.x), o[G][0]);
               o[G][1] = fmaf(pv, h2f(vv.x >> 16), o[G][1]);
@@ -1006,7 +1056,7 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
             const float w = wsm[qi * 64 + c0 + k];
             acc[0] = fmaf(ov[k].x, w, acc[0]);
             acc[1] = fmaf(ov[k].y, w, acc[1]);
-            if (DP == 4) { acc[2] = fmaf(ov[k].z, w, acc[2]); acc[3] = fmaf(ov[k].w, w, acc[3]); }
+            if constexpr (DP == 4) { acc[2] = fmaf(ov[k].z, w, acc[2]); acc[3] = fmaf(ov[k].w, w, acc[3]); }
           }
         }
       }
@@ -1035,6 +1085,7 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
 }
 
 // ------------------------------------------------------------------ MoE router + routing
+// ------------------------------------------------------------------ MoE router + routing
 // F32 router rows (two per wavefront, 32 lanes each; fixed per-row order, so batch
 // independent like matvec_multi's per-vector F32 path :455-464), then the last workgroup
 // routes: softmax (max, exp, sum, divide), top-n_used by probability (ties to the lower
@@ -1043,42 +1094,29 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
 // over the union of chosen experts in expert order, users in (row, slot) order (:982-986).
 template <int MT>
 __global__ __launch_bounds__(64) void k_router(const RouterArgs a, const StepRec *st) {
-  extern __shared__ __align__(16) uint8_t smem[];
   const int m = st->m, lane = threadIdx.x;
-  const int dim = a.pro.dim, n4 = dim >> 2;
+  const int dim = a.dim, n4 = dim >> 2;
   const int hl = lane & 31;
-  float *xl = reinterpret_cast<float *>(smem);  // [G][dim]
   constexpr int G = MT < 8 ? MT : 8;
-  // one row per half-wavefront; its weights are loaded before the prologue
   const int row = blockIdx.x * 2 + (lane >> 5);
   const bool valid = row < a.n_expert;
   const float4 *wr = reinterpret_cast<const float4 *>(a.w.pl.p0 + (int64_t)(valid ? row : 0) * dim * 4);
-  float4 wreg[PRO_NT * 2];
-#pragma unroll
-  for (int t = 0; t < PRO_NT * 2; t++) {
-    const int f = hl + 32 * t;
-    wreg[t] = f < n4 ? wr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
   for (int v0 = 0; v0 < m; v0 += G) {
     const int nv = min(G, m - v0);
-    if (v0 > 0) __syncthreads();
-    pro_f32<1>(a.pro, v0, nv, xl, blockIdx.x == 0);
     float part[G];
 #pragma unroll
     for (int v = 0; v < G; v++) part[v] = 0.0f;
+    for (int f = hl; f < n4; f += 32) {
+      const float4 w = wr[f];
 #pragma unroll
-    for (int t = 0; t < PRO_NT * 2; t++) {
-      const int f = hl + 32 * t;
-      if (f < n4) {
-#pragma unroll
-        for (int v = 0; v < G; v++) {
-          if (v < nv) {
-            const float4 x = reinterpret_cast<const float4 *>(xl + v * dim)[f];
-            part[v] = fmaf(wreg[t].x, x.x, part[v]);
-            part[v] = fmaf(wreg[t].y, x.y, part[v]);
-            part[v] = fmaf(wreg[t].z, x.z, part[v]);
-            part[v] = fmaf(wreg[t].w, x.w, part[v]);
-          }
+      for (int v = 0; v < G; v++) {
+        if (v < nv) {
+          const float4 x = x4[(int64_t)(v0 + v) * n4 + f];
+          part[v] = fmaf(w.x, x.x, part[v]);
+          part[v] = fmaf(w.y, x.y, part[v]);
+          part[v] = fmaf(w.z, x.z, part[v]);
+          part[v] = fmaf(w.w, x.w, part[v]);
         }
       }
     }
@@ -1189,21 +1227,19 @@ __global__ __launch_bounds__(64) void k_router(const RouterArgs a, const StepRec
 }
 
 // ------------------------------------------------------------------ gate / up + SwiGLU
-// Workgroup of 4 wavefronts = 16 rows of one job: in each wavefront row slots 0-3 are gate
-// rows r..r+3 and slots 4-7 the same rows of up; h = silu(g) * u (silu :586-588, ffns_fused
-// :407-417). With hq, the last of the 16 workgroups that cover a 256-row block of h
-// quantizes it (Q8_K for the integer down projection, :420-424).
-// The last of the 16 workgroups that cover a 256-row block of h quantizes it (Q8_K for an
-// integer down projection, :420-424) and clears the block's counter for the next pass.
-__device__ __forceinline__ void gateup_quant_tail(const GUArgs &a, int nvec, const int *jo) {
+// h = silu(g) * u (silu :586-588, ffns_fused :407-417) for the rows of one job. With hq, the
+// last of the workgroups that cover a 256-row block of h quantizes it (Q8_K for an integer
+// down projection, :420-424) and clears the block's counter for the next pass. rpw = rows of
+// h per workgroup.
+__device__ __forceinline__ void gateup_quant_tail(const GUArgs &a, int nvec, const int *jo, int rpw) {
   __shared__ int quant_u[MAX_M];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n_ff = a.n_ff, nbh = n_ff / 256, blk = (blockIdx.x * 16) / 256;
+  const int n_ff = a.n_ff, nbh = n_ff / 256, blk = (blockIdx.x * rpw) / 256, expect = 256 / rpw;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if ((int)threadIdx.x < nvec) {
     const int vo = jo ? jo[threadIdx.x] : threadIdx.x;
-    quant_u[threadIdx.x] = atomicAdd(&a.counter[vo * nbh + blk], 1) == 15;
+    quant_u[threadIdx.x] = atomicAdd(&a.counter[vo * nbh + blk], 1) == expect - 1;
   }
   __syncthreads();
   for (int u = wave; u < nvec; u += 4) {
@@ -1218,30 +1254,35 @@ __device__ __forceinline__ void gateup_quant_tail(const GUArgs &a, int nvec, con
   }
 }
 
-template <int T, int MT, bool PRO>
+struct GUJob {
+  int expert, nvec;
+  const int *jv, *jo;
+};
+__device__ __forceinline__ bool gu_job(const GUArgs &a, int m, GUJob &j) {
+  j.expert = 0; j.nvec = m; j.jv = nullptr; j.jo = nullptr;
+  if (!a.jobs) return true;
+  if ((int)blockIdx.y >= *a.njobs) return false;
+  const Job &J = a.jobs[blockIdx.y];
+  j.expert = J.expert; j.nvec = J.nvec; j.jv = J.vec; j.jo = J.out;
+  return true;
+}
+
+// Integer, eight rows per wavefront: 16 rows of h per workgroup; in each wavefront slots 0-3
+// are gate rows r..r+3 and slots 4-7 the same rows of up.
+template <int T, int MT>
 __global__ __launch_bounds__(256) void k_gateup_kq(const GUArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
-  const int m = st->m;
-  int expert = 0, nvec = m;
-  const int *jv = nullptr, *jo = nullptr;
-  if (a.jobs) {
-    if ((int)blockIdx.y >= *a.njobs) return;
-    const Job &J = a.jobs[blockIdx.y];
-    expert = J.expert;
-    nvec = J.nvec;
-    jv = J.vec;
-    jo = J.out;
-  }
+  GUJob J;
+  if (!gu_job(a, st->m, J)) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
   const int nb = (int)a.gate.nb, n_ff = a.n_ff, dim = (int)a.gate.cols;
-  const int rb = blockIdx.x * 16 + wave * 4;           // this wave's first row
-  const int64_t eb = (int64_t)expert * a.gate.rows;
+  const int rb = blockIdx.x * 16 + wave * 4;
+  const int64_t eb = (int64_t)J.expert * a.gate.rows;
   const Q8KP ly = ldsq_of(smem, MT, dim);
-  uint8_t *tile = smem + ((ldsq_bytes(MT, dim) + 15) & ~(size_t)15) + (size_t)wave * 8 * nb * tile_bytes_per_block();
-  tile_fetch<T>(tile, a.gate.pl, nb, [&](int sl) -> int64_t { return sl < 4 && rb + sl < n_ff ? eb + rb + sl : -1; });
-  tile_fetch<T>(tile, a.up.pl, nb, [&](int sl) -> int64_t { return sl >= 4 && rb + sl - 4 < n_ff ? eb + rb + sl - 4 : -1; });
-  if (PRO) pro_q8k<4>(a.pro, m, ly, blockIdx.x == 0 && blockIdx.y == 0);
-  else stage_q8kp(ly, a.y, dim, nvec, 4, [&](int u) { return jv ? jv[u] : u; });
+  uint8_t *tile = smem + ldsq_bytes(MT, dim) + (size_t)wave * 8 * nb * tile_bpb();
+  tile_fetch<T>(tile, a.gate.pl, 8, nb, [&](int sl) -> int64_t { return sl < 4 && rb + sl < n_ff ? eb + rb + sl : -1; });
+  tile_fetch<T>(tile, a.up.pl, 8, nb, [&](int sl) -> int64_t { return sl >= 4 && rb + sl - 4 < n_ff ? eb + rb + sl - 4 : -1; });
+  stage_q8kp(ly, a.y, dim, J.nvec, 4, [&](int u) { return J.jv ? J.jv[u] : u; });
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   const int r = rb + (slot & 3);
@@ -1250,85 +1291,114 @@ __global__ __launch_bounds__(256) void k_gateup_kq(const GUArgs a, const StepRec
 #pragma unroll
   for (int v = 0; v < MT; v++) vidx[v] = v;
   float res[MT];
-  kq_walk_tile<T, MT>(tile, nb, slot, eb + (valid ? r : n_ff - 1), ly, vidx, nvec, l, res);
+  kq_walk_tile<T, MT>(tile, 8, nb, slot, eb + (valid ? r : n_ff - 1), ly, vidx, J.nvec, l, res);
 #pragma unroll
   for (int v = 0; v < MT; v++) {
     const float u = __shfl_down(res[v], 32);
-    if (slot < 4 && l == 0 && valid && v < nvec) {
+    if (slot < 4 && l == 0 && valid && v < J.nvec) {
       const float x = res[v];
-      st_dev(a.h + (int64_t)(jo ? jo[v] : v) * n_ff + r, x / (1.0f + expf(-x)) * u);
+      st_dev(a.h + (int64_t)(J.jo ? J.jo[v] : v) * n_ff + r, x / (1.0f + expf(-x)) * u);
     }
   }
-  if (a.hq.q) gateup_quant_tail(a, nvec, jo);
+  if (a.hq.q) gateup_quant_tail(a, J.nvec, J.jo, 16);
 }
 
-template <int T, int MT, bool PRO>
-__global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec *st) {
+// Integer, row-parallel (decode): one row of h per wavefront, four per workgroup; slot 0 is
+// the gate row, slot 1 the up row, four lane groups each.
+template <int T, int MT>
+__global__ __launch_bounds__(256) void k_gateup_rp(const GUArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
-  const int m = st->m;
-  int expert = 0, nvec = m;
-  const int *jv = nullptr, *jo = nullptr;
-  if (a.jobs) {
-    if ((int)blockIdx.y >= *a.njobs) return;
-    const Job &J = a.jobs[blockIdx.y];
-    expert = J.expert;
-    nvec = J.nvec;
-    jv = J.vec;
-    jo = J.out;
+  GUJob J;
+  if (!gu_job(a, st->m, J)) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nb = (int)a.gate.nb, n_ff = a.n_ff, dim = (int)a.gate.cols;
+  const int r = blockIdx.x * 4 + wave;
+  const bool valid = r < n_ff;
+  const int64_t grow = (int64_t)J.expert * a.gate.rows + (valid ? r : n_ff - 1);
+  const Q8KP ly = ldsq_of(smem, MT, dim);
+  uint8_t *tile = smem + ldsq_bytes(MT, dim) + (size_t)wave * rp_wave_bytes(2, nb, MT);
+  float *cb = reinterpret_cast<float *>(tile + (size_t)2 * nb * tile_bpb());
+  tile_fetch<T>(tile, a.gate.pl, 2, nb, [&](int sl) -> int64_t { return sl == 0 ? grow : -1; });
+  tile_fetch<T>(tile, a.up.pl, 2, nb, [&](int sl) -> int64_t { return sl == 1 ? grow : -1; });
+  stage_q8kp(ly, a.y, dim, J.nvec, 4, [&](int u) { return J.jv ? J.jv[u] : u; });
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  float res[MT];
+  const int nv = J.nvec;
+  kq_rows_par<T, MT>(tile, 2, nb, 4, 2, [&](int) { return grow; }, [](int, int v) { return v; }, [&](int) { return nv; }, ly, cb, res);
+#pragma unroll
+  for (int v = 0; v < MT; v++) {
+    const float u = __shfl_down(res[v], 32);
+    if (lane == 0 && valid && v < nv) {
+      const float x = res[v];
+      st_dev(a.h + (int64_t)(J.jo ? J.jo[v] : v) * n_ff + r, x / (1.0f + expf(-x)) * u);
+    }
   }
+  if (a.hq.q) gateup_quant_tail(a, nv, J.jo, 4);
+}
+
+// Float weights (Q8_0 / Q5_0) x fp32 activations: 16 rows of h per workgroup.
+template <int T, int MT>
+__global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec *st) {
+  GUJob J;
+  if (!gu_job(a, st->m, J)) return;
   constexpr int D = f_depth<MT>();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
   const TensorView &w = slot < 4 ? a.gate : a.up;
   const int nb = (int)w.nb, n_ff = a.n_ff;
   const int r = blockIdx.x * 16 + wave * 4 + (slot & 3);
   const bool valid = r < n_ff;
-  const int64_t grow = (int64_t)expert * w.rows + (valid ? r : n_ff - 1);
+  const int64_t grow = (int64_t)J.expert * w.rows + (valid ? r : n_ff - 1);
   const Planes pl = slot < 4 ? a.gate.pl : a.up.pl;
   int vidx[MT];
 #pragma unroll
-  for (int v = 0; v < MT; v++) vidx[v] = jv && v < nvec ? jv[v] : v;
+  for (int v = 0; v < MT; v++) vidx[v] = J.jv && v < J.nvec ? J.jv[v] : v;
   float res[MT];
-  if (PRO) {
-    float *xl = reinterpret_cast<float *>(smem);
-    pro_f32<4>(a.pro, 0, m, xl, blockIdx.x == 0 && blockIdx.y == 0);
-    f_walk<T, MT, D>(pl, grow, nb, xl, a.pro.dim, vidx, nvec, l, res);
-  } else {
-    f_walk<T, MT, D>(pl, grow, nb, a.x, w.cols, vidx, nvec, l, res);
-  }
+  f_walk<T, MT, D>(pl, grow, nb, a.x, w.cols, vidx, J.nvec, l, res);
 #pragma unroll
   for (int v = 0; v < MT; v++) {
     const float u = __shfl_down(res[v], 32);
-    if (slot < 4 && l == 0 && valid && v < nvec) {
+    if (slot < 4 && l == 0 && valid && v < J.nvec) {
       const float x = res[v];
-      st_dev(a.h + (int64_t)(jo ? jo[v] : v) * n_ff + r, x / (1.0f + expf(-x)) * u);
+      st_dev(a.h + (int64_t)(J.jo ? J.jo[v] : v) * n_ff + r, x / (1.0f + expf(-x)) * u);
     }
   }
-  if (a.hq.q) gateup_quant_tail(a, nvec, jo);
+  if (a.hq.q) gateup_quant_tail(a, J.nvec, J.jo, 16);
 }
 
 // ------------------------------------------------------------------ down + combine
 // One output row per wavefront; row slots take jobs eight at a time; each job's users get
 // y_e[r] in LDS, then out[b][r] = sum over b's chosen slots, in chosen order, of w * y
-// (non-fused multiply and add, ffns_fused :432-437, moe_forward_batch :1133-1140).
-template <int T, int MT>
+// (non-fused multiply and add, ffns_fused :432-437, moe_forward_batch :1133-1140). With a
+// tail, the outputs are stored coherently and the last workgroup runs it.
+__device__ __forceinline__ void down_combine(const DownArgs &a, int m, float (*yb)[MAX_M * 32], int64_t r, int dim, bool coh) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (r < dim && lane < m) {
+    const int b = lane, nk = a.nkeep[b];
+    float acc = 0.0f;
+    for (int i = 0; i < nk; i++) acc = acc + a.weights[b * 32 + i] * yb[wave][b * a.n_used + i];
+    out_store(a.out + (int64_t)b * dim + r, acc, coh);
+  }
+}
+
+template <int T, int MT, bool STAGE>
 __global__ __launch_bounds__(256) void k_down_kq(const DownArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float yb[4][MAX_M * 32];
-  constexpr bool STAGE = MT <= 2;  // every row's h vectors fit in LDS
   const int m = st->m, nj = *a.njobs;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
   const int64_t r = (int64_t)blockIdx.x * 4 + wave;
   const int dim = (int)a.w.rows, nb = (int)a.w.nb, n_ff = (int)a.w.cols;
   const bool valid = r < dim;
+  const bool coh = a.tail.nw != nullptr;
   const int npairs = m * a.n_used;
-  const int nst = STAGE ? MT * a.n_used : 0;
-  const Q8KP ly = ldsq_of(smem, nst, n_ff);
-  uint8_t *tile = smem + ((ldsq_bytes(nst, n_ff) + 15) & ~(size_t)15) + (size_t)wave * 8 * nb * tile_bytes_per_block();
+  const Q8KP ly = ldsq_of(smem, STAGE ? MT * a.n_used : 0, n_ff);
+  uint8_t *tile = smem + (STAGE ? ldsq_bytes(MT * a.n_used, n_ff) : 0) + (size_t)wave * 8 * nb * tile_bpb();
   for (int j0 = 0; j0 < nj; j0 += 8) {
     const int j = j0 + slot;
     const bool has = j < nj;
     const Job &J = a.jobs[has ? j : 0];
-    tile_fetch<T>(tile, a.w.pl, nb, [&](int sl) -> int64_t {
+    tile_fetch<T>(tile, a.w.pl, 8, nb, [&](int sl) -> int64_t {
       return j0 + sl < nj && valid ? (int64_t)a.jobs[j0 + sl].expert * dim + r : -1;
     });
     if (STAGE && j0 == 0) stage_q8kp(ly, a.y, n_ff, npairs, 4, [](int u) { return u; });
@@ -1339,7 +1409,7 @@ __global__ __launch_bounds__(256) void k_down_kq(const DownArgs a, const StepRec
 #pragma unroll
     for (int v = 0; v < MT; v++) vidx[v] = v < nvec ? J.vec[v] : 0;
     float res[MT];
-    kq_walk_tile<T, MT>(tile, nb, slot, (int64_t)J.expert * dim + (valid ? r : 0), STAGE ? ly : a.y, vidx, nvec, l, res);
+    kq_walk_tile<T, MT>(tile, 8, nb, slot, (int64_t)J.expert * dim + (valid ? r : 0), STAGE ? ly : a.y, vidx, nvec, l, res);
     if (l == 0) {
 #pragma unroll
       for (int v = 0; v < MT; v++)
@@ -1347,12 +1417,8 @@ __global__ __launch_bounds__(256) void k_down_kq(const DownArgs a, const StepRec
     }
     __syncthreads();
   }
-  if (valid && lane < m) {
-    const int b = lane, nk = a.nkeep[b];
-    float acc = 0.0f;
-    for (int i = 0; i < nk; i++) acc = acc + a.weights[b * 32 + i] * yb[wave][b * a.n_used + i];
-    a.out[(int64_t)b * dim + r] = acc;
-  }
+  down_combine(a, m, yb, r, dim, coh);
+  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
 }
 
 template <int T, int MT>
@@ -1363,6 +1429,7 @@ __global__ __launch_bounds__(256) void k_down_f(const DownArgs a, const StepRec 
   const int64_t r = (int64_t)blockIdx.x * 4 + wave;
   const int dim = (int)a.w.rows, nb = (int)a.w.nb;
   const bool valid = r < dim;
+  const bool coh = a.tail.nw != nullptr;
   constexpr int D = f_depth<MT>();
   for (int j0 = 0; j0 < nj; j0 += 8) {
     const int j = j0 + slot;
@@ -1382,12 +1449,8 @@ __global__ __launch_bounds__(256) void k_down_f(const DownArgs a, const StepRec 
     }
   }
   __syncthreads();
-  if (valid && lane < m) {
-    const int b = lane, nk = a.nkeep[b];
-    float acc = 0.0f;
-    for (int i = 0; i < nk; i++) acc = acc + a.weights[b * 32 + i] * yb[wave][b * a.n_used + i];
-    a.out[(int64_t)b * dim + r] = acc;
-  }
+  down_combine(a, m, yb, r, dim, coh);
+  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
 }
 
 // ------------------------------------------------------------------ final greedy pick
@@ -1409,69 +1472,52 @@ __global__ __launch_bounds__(256) void k_argmax_final(const unsigned long long *
 
 // ------------------------------------------------------------------ launchers
 static inline int bucket(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
-// Waves per workgroup: one for a decode pass (spreads a small matrix over the most CUs), four
-// for a fused prologue over several rows; integer launches without a prologue use one.
-static inline int mv_nw(int mt, bool pro, bool kq) { return pro ? (mt == 1 ? 1 : 4) : (kq ? 1 : 4); }
+static inline bool kq_type(int dt) { return dt == T_Q4K || dt == T_Q6K; }
 
-int mv_wgs(int64_t rows, int mt, bool pro, int dtype) {
-  const bool kq = dtype == T_Q4K || dtype == T_Q6K;
-  const int64_t rows_per_wg = 8 * mv_nw(bucket(mt), pro, kq);
-  return (int)((rows + rows_per_wg - 1) / rows_per_wg);
+// Rows per workgroup: float 32 (4 waves x 8), tiles 8 (1 wave), row-parallel 4R.
+int mv_wgs(int64_t rows, int mt, int mode, int dtype, int R) {
+  (void)mt;
+  const int64_t per = !kq_type(dtype) ? 32 : mode == 1 ? 4 * R : 8;
+  return (int)((rows + per - 1) / per);
 }
 
-size_t mv_smem(const MVArgs &a, int mt, bool pro, int dtype) {
+#define SPX_LDS(kern, sm) \
+  if ((sm) > 65536) (void)hipFuncSetAttribute((const void *)(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)(sm))
+
+hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int grid, hipStream_t s) {
   mt = bucket(mt);
-  const bool kq = dtype == T_Q4K || dtype == T_Q6K;
-  const int cols = (int)a.seg[0].w.cols;
-  if (kq) return ((ldsq_bytes(mt, cols) + 15) & ~(size_t)15) + (size_t)mv_nw(mt, pro, kq) * 8 * (cols / 256) * tile_bytes_per_block();
-  if (!pro) return 0;
-  return (size_t)mt * a.pro.dim * 4;
-}
-
-template <int MT, int NW, bool PRO>
-static hipError_t launch_mv_t(const MVArgs &a, const StepRec *st, int grid, size_t sm, hipStream_t s) {
-  const int dt = a.seg[0].w.dtype;
-  if (dt == T_Q4K || dt == T_Q6K) {
-    if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_mvt<MT, NW, PRO>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
-    hipLaunchKernelGGL((k_mvt<MT, NW, PRO>), dim3(grid), dim3(NW * 64), sm, s, a, st);
-  } else {
-    if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_mv_f<MT, NW, PRO>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
-    hipLaunchKernelGGL((k_mv_f<MT, NW, PRO>), dim3(grid), dim3(NW * 64), sm, s, a, st);
-  }
-  return hipGetLastError();
-}
-
-hipError_t launch_mv(const MVArgs &a, int mt, bool pro, const StepRec *st, int grid, hipStream_t s) {
-  mt = bucket(mt);
-  const int dt = a.seg[0].w.dtype;
-  const bool kq = dt == T_Q4K || dt == T_Q6K;
-  const int nw = mv_nw(mt, pro, kq);
-  const size_t sm = mv_smem(a, mt, pro, dt);
-  if (pro) {
+  const int dt = a.seg[0].w.dtype, cols = (int)a.seg[0].w.cols, nb = cols / 256;
+  if (grid < 1) return hipErrorInvalidValue;
+  if (!kq_type(dt)) {
+#define SPX_MVF(MTV) hipLaunchKernelGGL(k_mv_f<MTV>, dim3(grid), dim3(256), 0, s, a, st)
     switch (mt) {
-    case 1: return launch_mv_t<1, 1, true>(a, st, grid, sm, s);
-    case 2: return launch_mv_t<2, 4, true>(a, st, grid, sm, s);
-    case 4: return launch_mv_t<4, 4, true>(a, st, grid, sm, s);
-    case 8: return launch_mv_t<8, 4, true>(a, st, grid, sm, s);
-    default: return launch_mv_t<16, 4, true>(a, st, grid, sm, s);
+    case 1: SPX_MVF(1); break;
+    case 2: SPX_MVF(2); break;
+    case 4: SPX_MVF(4); break;
+    case 8: SPX_MVF(8); break;
+    default: SPX_MVF(16); break;
     }
+#undef SPX_MVF
+    return hipGetLastError();
   }
-  if (nw == 1) {
-    switch (mt) {
-    case 1: return launch_mv_t<1, 1, false>(a, st, grid, sm, s);
-    case 2: return launch_mv_t<2, 1, false>(a, st, grid, sm, s);
-    case 4: return launch_mv_t<4, 1, false>(a, st, grid, sm, s);
-    case 8: return launch_mv_t<8, 1, false>(a, st, grid, sm, s);
-    default: return launch_mv_t<16, 1, false>(a, st, grid, sm, s);
-    }
+  if (mode == 1) {
+    if (mt > 2 || a.G < 1 || a.R < 1 || a.G * a.R > 8) return hipErrorInvalidValue;
+    const size_t sm = ldsq_bytes(mt, cols) + 4 * rp_wave_bytes(a.R, nb, mt);
+    if (mt == 1) { SPX_LDS(k_mvr<1>, sm); hipLaunchKernelGGL(k_mvr<1>, dim3(grid), dim3(256), sm, s, a, st); }
+    else { SPX_LDS(k_mvr<2>, sm); hipLaunchKernelGGL(k_mvr<2>, dim3(grid), dim3(256), sm, s, a, st); }
+    return hipGetLastError();
   }
+  const size_t sm = ldsq_bytes(mt, cols) + (size_t)8 * nb * tile_bpb();
+#define SPX_MVT(MTV) do { SPX_LDS(k_mvt<MTV>, sm); hipLaunchKernelGGL(k_mvt<MTV>, dim3(grid), dim3(64), sm, s, a, st); } while (0)
   switch (mt) {
-  case 1: return launch_mv_t<1, 4, false>(a, st, grid, sm, s);
-  case 2: return launch_mv_t<2, 4, false>(a, st, grid, sm, s);
-  case 4: return launch_mv_t<4, 4, false>(a, st, grid, sm, s);
-  case 8: return launch_mv_t<8, 4, false>(a, st, grid, sm, s);
-  default: return launch_mv_t<16, 4, false>(a, st, grid, sm, s);
+  case 1: SPX_MVT(1); break;
+  case 2: SPX_MVT(2); break;
+  case 4: SPX_MVT(4); break;
+  case 8: SPX_MVT(8); break;
+  default: SPX_MVT(16); break;
   }
+#undef SPX_MVT
+  return hipGetLastError();
 }
 
 static size_t attn_smem(const AttnArgs &a, int m) {
@@ -1481,7 +1527,7 @@ static size_t attn_smem(const AttnArgs &a, int m) {
 
 template <int HD, int NGM>
 static void launch_attn_t(const AttnArgs &a, const StepRec *st, size_t sm, hipStream_t s) {
-  if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_attn<HD, NGM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+  SPX_LDS((k_attn<HD, NGM>), sm);
   hipLaunchKernelGGL((k_attn<HD, NGM>), dim3(a.nch, a.n_kv), dim3(256), sm, s, a, st);
 }
 
@@ -1500,99 +1546,93 @@ hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStre
 
 hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStream_t s) {
   mt = bucket(mt);
-  const int g = mt < 8 ? mt : 8;
-  const size_t sm = (size_t)g * a.pro.dim * 4;
-  const int grid = (a.n_expert + a.rows_per_wg - 1) / a.rows_per_wg;
-#define SPX_RT(MTV)                                                                                                          \
-  do {                                                                                                                       \
-    if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_router<MTV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); \
-    hipLaunchKernelGGL(k_router<MTV>, dim3(grid), dim3(64), sm, s, a, st);                                                   \
-  } while (0)
+  const int grid = (a.n_expert + 1) / 2;
   switch (mt) {
-  case 1: SPX_RT(1); break;
-  case 2: SPX_RT(2); break;
-  case 4: SPX_RT(4); break;
-  case 8: SPX_RT(8); break;
-  default: SPX_RT(16); break;
+  case 1: hipLaunchKernelGGL(k_router<1>, dim3(grid), dim3(64), 0, s, a, st); break;
+  case 2: hipLaunchKernelGGL(k_router<2>, dim3(grid), dim3(64), 0, s, a, st); break;
+  case 4: hipLaunchKernelGGL(k_router<4>, dim3(grid), dim3(64), 0, s, a, st); break;
+  case 8: hipLaunchKernelGGL(k_router<8>, dim3(grid), dim3(64), 0, s, a, st); break;
+  default: hipLaunchKernelGGL(k_router<16>, dim3(grid), dim3(64), 0, s, a, st); break;
   }
-#undef SPX_RT
   return hipGetLastError();
 }
 
 template <int T, int MT>
-static hipError_t launch_gu_t(const GUArgs &a, const StepRec *st, dim3 grid, hipStream_t s) {
-  constexpr bool kq = T == T_Q4K || T == T_Q6K;
-  size_t sm = 0;
-  if (kq) sm = ((ldsq_bytes(MT, (int)a.gate.cols) + 15) & ~(size_t)15) + (size_t)4 * 8 * a.gate.nb * tile_bytes_per_block();
-  else if (a.use_pro) sm = (size_t)MT * a.pro.dim * 4;
-  if constexpr (kq) {
-    if (a.use_pro) {
-      if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_gateup_kq<T, MT, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
-      hipLaunchKernelGGL((k_gateup_kq<T, MT, true>), grid, dim3(256), sm, s, a, st);
-    } else {
-      if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_gateup_kq<T, MT, false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
-      hipLaunchKernelGGL((k_gateup_kq<T, MT, false>), grid, dim3(256), sm, s, a, st);
+static hipError_t launch_gu_t(const GUArgs &a, int mode, const StepRec *st, int max_jobs, hipStream_t s) {
+  const unsigned jobs = (unsigned)std::max(1, max_jobs);
+  if constexpr (T == T_Q4K || T == T_Q6K) {
+    const int dim = (int)a.gate.cols, nb = (int)a.gate.nb;
+    if constexpr (MT <= 2) {
+      if (mode == 1) {
+        const size_t sm = ldsq_bytes(MT, dim) + 4 * rp_wave_bytes(2, nb, MT);
+        SPX_LDS((k_gateup_rp<T, MT>), sm);
+        hipLaunchKernelGGL((k_gateup_rp<T, MT>), dim3((unsigned)((a.n_ff + 3) / 4), jobs), dim3(256), sm, s, a, st);
+        return hipGetLastError();
+      }
     }
+    const size_t sm = ldsq_bytes(MT, dim) + (size_t)4 * 8 * nb * tile_bpb();
+    SPX_LDS((k_gateup_kq<T, MT>), sm);
+    hipLaunchKernelGGL((k_gateup_kq<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), sm, s, a, st);
   } else {
-    if (a.use_pro) {
-      if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_gateup_f<T, MT, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
-      hipLaunchKernelGGL((k_gateup_f<T, MT, true>), grid, dim3(256), sm, s, a, st);
-    } else {
-      hipLaunchKernelGGL((k_gateup_f<T, MT, false>), grid, dim3(256), 0, s, a, st);
-    }
+    hipLaunchKernelGGL((k_gateup_f<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), 0, s, a, st);
   }
   return hipGetLastError();
 }
 
 template <int T>
-static hipError_t launch_gu_dt(const GUArgs &a, int mt, const StepRec *st, dim3 grid, hipStream_t s) {
+static hipError_t launch_gu_dt(const GUArgs &a, int mt, int mode, const StepRec *st, int max_jobs, hipStream_t s) {
   switch (mt) {
-  case 1: return launch_gu_t<T, 1>(a, st, grid, s);
-  case 2: return launch_gu_t<T, 2>(a, st, grid, s);
-  case 4: return launch_gu_t<T, 4>(a, st, grid, s);
-  case 8: return launch_gu_t<T, 8>(a, st, grid, s);
-  default: return launch_gu_t<T, 16>(a, st, grid, s);
+  case 1: return launch_gu_t<T, 1>(a, mode, st, max_jobs, s);
+  case 2: return launch_gu_t<T, 2>(a, mode, st, max_jobs, s);
+  case 4: return launch_gu_t<T, 4>(a, mode, st, max_jobs, s);
+  case 8: return launch_gu_t<T, 8>(a, mode, st, max_jobs, s);
+  default: return launch_gu_t<T, 16>(a, mode, st, max_jobs, s);
   }
 }
 
-hipError_t launch_gateup(const GUArgs &a, int mt, const StepRec *st, int max_jobs, hipStream_t s) {
+hipError_t launch_gateup(const GUArgs &a, int mt, int mode, const StepRec *st, int max_jobs, hipStream_t s) {
   mt = bucket(mt);
-  dim3 grid((unsigned)((a.n_ff + 15) / 16), (unsigned)std::max(1, max_jobs));
   switch (a.gate.dtype) {
-  case T_Q4K: return launch_gu_dt<T_Q4K>(a, mt, st, grid, s);
-  case T_Q6K: return launch_gu_dt<T_Q6K>(a, mt, st, grid, s);
-  case T_Q8_0: return launch_gu_dt<T_Q8_0>(a, mt, st, grid, s);
-  case T_Q5_0: return launch_gu_dt<T_Q5_0>(a, mt, st, grid, s);
+  case T_Q4K: return launch_gu_dt<T_Q4K>(a, mt, mode, st, max_jobs, s);
+  case T_Q6K: return launch_gu_dt<T_Q6K>(a, mt, mode, st, max_jobs, s);
+  case T_Q8_0: return launch_gu_dt<T_Q8_0>(a, mt, mode, st, max_jobs, s);
+  case T_Q5_0: return launch_gu_dt<T_Q5_0>(a, mt, mode, st, max_jobs, s);
   default: return hipErrorInvalidValue;
   }
 }
 
-template <int T>
-static hipError_t launch_down_dt(const DownArgs &a, int mt, const StepRec *st, hipStream_t s) {
-  dim3 grid((unsigned)((a.w.rows + 3) / 4));
-  constexpr bool kq = T == T_Q4K || T == T_Q6K;
-  const int nst = mt <= 2 ? mt * a.n_used : 0;
-  const size_t sm = kq ? ((ldsq_bytes(nst, (int)a.w.cols) + 15) & ~(size_t)15) + (size_t)4 * 8 * a.w.nb * tile_bytes_per_block() : 0;
-#define SPX_DN(MTV)                                                                     \
-  do {                                                                                  \
-    if constexpr (kq) {                                                                 \
-      if (sm > 65536) (void)hipFuncSetAttribute((const void *)k_down_kq<T, MTV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); \
-      hipLaunchKernelGGL((k_down_kq<T, MTV>), grid, dim3(256), sm, s, a, st);          \
-    } else hipLaunchKernelGGL((k_down_f<T, MTV>), grid, dim3(256), 0, s, a, st);        \
-  } while (0)
-  switch (mt) {
-  case 1: SPX_DN(1); break;
-  case 2: SPX_DN(2); break;
-  case 4: SPX_DN(4); break;
-  case 8: SPX_DN(8); break;
-  default: SPX_DN(16); break;
+template <int T, int MT>
+static hipError_t launch_down_t(const DownArgs &a, const StepRec *st, hipStream_t s) {
+  const dim3 grid((unsigned)((a.w.rows + 3) / 4));
+  if constexpr (T == T_Q4K || T == T_Q6K) {
+    const int n_ff = (int)a.w.cols, nb = (int)a.w.nb;
+    const size_t tiles = (size_t)4 * 8 * nb * tile_bpb();
+    const size_t staged = ldsq_bytes(MT * a.n_used, n_ff) + tiles;
+    if (MT <= 2 && staged <= 65536) {
+      hipLaunchKernelGGL((k_down_kq<T, MT, true>), grid, dim3(256), staged, s, a, st);
+    } else {
+      SPX_LDS((k_down_kq<T, MT, false>), tiles);
+      hipLaunchKernelGGL((k_down_kq<T, MT, false>), grid, dim3(256), tiles, s, a, st);
+    }
+  } else {
+    hipLaunchKernelGGL((k_down_f<T, MT>), grid, dim3(256), 0, s, a, st);
   }
-#undef SPX_DN
   return hipGetLastError();
 }
 
-hipError_t launch_down(const DownArgs &a, int mt, const StepRec *st, int njob_max, hipStream_t s) {
-  (void)njob_max;
+template <int T>
+static hipError_t launch_down_dt(const DownArgs &a, int mt, const StepRec *st, hipStream_t s) {
+  switch (mt) {
+  case 1: return launch_down_t<T, 1>(a, st, s);
+  case 2: return launch_down_t<T, 2>(a, st, s);
+  case 4: return launch_down_t<T, 4>(a, st, s);
+  case 8: return launch_down_t<T, 8>(a, st, s);
+  default: return launch_down_t<T, 16>(a, st, s);
+  }
+}
+
+hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, hipStream_t s) {
+  (void)mode;
   mt = bucket(mt);
   switch (a.w.dtype) {
   case T_Q4K: return launch_down_dt<T_Q4K>(a, mt, st, s);
@@ -1603,13 +1643,13 @@ hipError_t launch_down(const DownArgs &a, int mt, const StepRec *st, int njob_ma
   }
 }
 
-hipError_t launch_embed(const TensorView &e, const StepRec *st, float *x, int64_t ld_x, float escale, int m, hipStream_t s) {
-  hipLaunchKernelGGL(k_embed, dim3(m), dim3(256), 0, s, e, st, x, ld_x, escale);
+hipError_t launch_embed(const TensorView &e, const StepRec *st, float escale, const NormTail &t, int m, hipStream_t s) {
+  hipLaunchKernelGGL(k_embed, dim3(m), dim3(256), 0, s, e, st, escale, t);
   return hipGetLastError();
 }
 
-hipError_t launch_norm(const Pro &p, const StepRec *st, int m, hipStream_t s) {
-  hipLaunchKernelGGL(k_norm, dim3(m), dim3(64), 0, s, p, st);
+hipError_t launch_norm(const NormTail &t, const StepRec *st, int m, hipStream_t s) {
+  hipLaunchKernelGGL(k_norm, dim3(m), dim3(256), 0, s, t, st);
   return hipGetLastError();
 }
 

@@ -93,6 +93,36 @@ def test_batch_equals_sequential_bitwise(ctx, name):
         assert np.array_equal(ls[0].view(np.uint32), lb[i].view(np.uint32)), (name, i)
 
 
+SHAPES = {"tiles at decode": {"SPX_MV_MODE": "0"}, "standalone norms": {"SPX_TAIL_MAX": "0"},
+          "tails at every m": {"SPX_TAIL_MAX": "16"}, "row-parallel LM head": {"SPX_LM_MODE": "1"}}
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-qwen3moe"])
+def test_launch_shapes_bitwise(ctx, name, shape, monkeypatch):
+    """Every launch shape (row-parallel or tiled matvecs, norm tails or standalone norm
+    launches, LM head shape) gives the same bits for the same pass."""
+    cfg = M.TINY[name].replace(sigma=0.05)
+    w = M.synth_model(cfg, seed=14)
+    ref = M.Engine(ctx, cfg, w)
+    for k, v in SHAPES[shape].items():
+        monkeypatch.setenv(k, v)
+    eng = M.Engine(ctx, cfg, w)
+    for k in SHAPES[shape]:
+        monkeypatch.delenv(k)
+    ids = np.arange(30) * 5 % cfg.vocab
+    pos = 0
+    for m in (5, 1, 2, 1, 9, 2):
+        a0, h0, l0 = ref.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        a1, h1, l1 = eng.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        assert np.array_equal(h0.view(np.uint32), h1.view(np.uint32)), (shape, m)
+        assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32)), (shape, m)
+        assert np.array_equal(a0, a1), (shape, m)
+        pos += m
+    ref.close()
+    eng.close()
+
+
 @pytest.mark.parametrize("graphs", [True, False])
 def test_graph_replay_matches_eager(ctx, graphs):
     cfg = M.TINY["tiny-qwen3moe"]

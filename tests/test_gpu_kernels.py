@@ -26,6 +26,17 @@ def ctx():
     c.close()
 
 
+@pytest.fixture(params=["auto", "tiles"])
+def mv_mode(request, monkeypatch):
+    """Integer matvec launch shape: the default (row-parallel at m <= 2) or forced
+    eight-rows-per-wavefront tiles; both must give the reference's bits."""
+    if request.param == "tiles":
+        monkeypatch.setenv("SPX_MV_MODE", "0")
+    else:
+        monkeypatch.delenv("SPX_MV_MODE", raising=False)
+    return request.param
+
+
 def _cuda(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
@@ -81,12 +92,12 @@ def test_block_sums_bitwise(ctx, dtype, n):
         assert np.array_equal(got[:, 0], sumi) and np.array_equal(got[:, 1], corr), (r,)
 
 
-def test_int_kernel_reference_seed(ctx):
+def test_int_kernel_reference_seed(ctx, mv_mode):
     """The data of quant_q8k.rs:364-411 (seed 0x51ED): GPU vs oracle and vs the f64 dot."""
     from spindle_amd import ops
     rng = R.Rng(0x51ED)
     for dtype in (R.Q4K, R.Q6K):
-        for n in (256, 768, 2048):
+        for n in (256, 512, 768, 1024, 1536, 2048):
             rows = 37
             mat = R.random_matrix(dtype, n, rows, rng)
             w = ops.Tensor(ctx, dtype, n, rows, mat)
@@ -108,7 +119,7 @@ def test_int_kernel_reference_seed(ctx):
 
 
 @pytest.mark.parametrize("dtype", [R.Q4K, R.Q6K])
-def test_int_kernel_batch_bitwise(ctx, dtype):
+def test_int_kernel_batch_bitwise(ctx, dtype, mv_mode):
     from spindle_amd import ops
     rng = np.random.default_rng(7)
     n, rows = 2048, 300
@@ -124,7 +135,7 @@ def test_int_kernel_batch_bitwise(ctx, dtype):
 
 @pytest.mark.parametrize("dtype,n,rows,ne", [(R.Q4K, 2048, 768, 8), (R.Q6K, 768, 2048, 8), (R.Q4K, 4096, 2048, 1),
                                               (R.Q6K, 2048, 151936, 1)])
-def test_int_matvec_real_shapes(ctx, dtype, n, rows, ne):
+def test_int_matvec_real_shapes(ctx, dtype, n, rows, ne, mv_mode):
     """Qwen3-30B-A3B shapes: expert gate/up, expert down, attn_output, LM head."""
     from spindle_amd import ops
     rng = np.random.default_rng(rows)

@@ -125,8 +125,8 @@ int spx_engine_decode(spx_engine *e, int32_t token, int start_pos, int n, int32_
 int spx_engine_profile(spx_engine *e, int on);
 int spx_engine_profile_read(spx_engine *e, int cls, const char **name, int64_t *launches,
                             double *total_us, double *bytes);
-/* Copies `bytes` of an internal buffer of the last pass (x, xn, q, att, proj, rlog, chosen,
- * weights, nkeep, h, y: the last layer's values) to host memory; for tests. */
+/* Copies `bytes` of an internal buffer of the last pass (x, xn, q, k, v, att, proj, rlog,
+ * chosen, weights, nkeep, h, y: the last layer's values) to host memory; for tests. */
 int spx_engine_debug_read(spx_engine *e, const char *what, void *host, int64_t bytes);
 /* Number of distinct experts each MoE layer ran in the last pass (0 for dense layers). */
 int spx_engine_last_experts(spx_engine *e, int32_t *njobs_per_layer);

@@ -56,7 +56,7 @@ int64_t now_us() {
 struct spx_engine {
   spx_ctx *ctx = nullptr;
   spx_model_config c{};
-  int q_dim = 0, kv_dim = 0, n_ff = 0, nch = 64, lm_grid = 2048, nbest = 1;
+  int q_dim = 0, kv_dim = 0, n_ff = 0, nch = 1, lm_grid = 2048, nbest = 1;
   int mv_mode = -1, lm_mode = -1, tail_max = 2;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX)
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
@@ -272,7 +272,7 @@ int enqueue_forward(spx_engine *E, int m) {
       aa.rope = E->rope; aa.kc = E->kc; aa.vc = E->vc; aa.part_ml = E->part_ml; aa.part_o = E->part_o; aa.counter = E->att_cnt; aa.att = E->att;
       if (att_q_fused) aa.aq = E->aq;
       aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
-      aa.neox = c.rope_neox; aa.nch = E->nch; aa.eps = c.rms_eps;
+      aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
       aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
       SPX_HIP(launch_attention(aa, m, E->st_dev, s));
     }
@@ -385,6 +385,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   if (c.head_dim != 64 && c.head_dim != 128) return fail("spx_engine_create: the attention kernel supports head_dim 64 or 128");
   if (16 * (c.n_heads / c.n_kv_heads) > ATT_QMAX) return fail("spx_engine_create: at most 8 query heads per kv head");
   if (c.n_layers <= 0 || c.vocab <= 0 || c.max_seq <= 0) return fail("spx_engine_create: bad layer count, vocab or max_seq");
+  if (c.max_seq > 64 * ATT_GRP * ATT_GMAX) return fail("spx_engine_create: max_seq above " + std::to_string(64 * ATT_GRP * ATT_GMAX));
   if (c.n_expert < 0 || c.n_expert > 256 || c.n_expert_used < 0 || c.n_expert_used > 32 || (c.n_expert && !c.n_expert_used))
     return fail("spx_engine_create: unsupported expert counts (n_expert <= 256, n_expert_used in 1..32)");
   spx_engine *E = new spx_engine();
@@ -396,7 +397,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   E->q_dim = c.n_heads * c.head_dim;
   E->kv_dim = c.n_kv_heads * c.head_dim;
   E->L.resize(c.n_layers);
-  if (const char *v = std::getenv("SPX_ATT_CHUNKS")) E->nch = std::max(1, std::min(64, atoi(v)));
+  E->nch = (c.max_seq + 63) / 64;
   if (const char *v = std::getenv("SPX_LM_GRID")) E->lm_grid = std::max(1, atoi(v));
   if (const char *v = std::getenv("SPX_MV_MODE")) E->mv_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_LM_MODE")) E->lm_mode = std::max(0, std::min(1, atoi(v)));
@@ -521,10 +522,10 @@ int spx_engine_prepare(spx_engine *E) {
             (E->logits = E->dalloc<float>((size_t)M * c.vocab)) && (E->amax = E->dalloc<int>(M)) &&
             (E->best = E->dalloc<unsigned long long>((size_t)M * std::max<int64_t>(E->lm_grid, c.vocab / 4 + 1))) &&
             (E->tail_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) &&
-            (E->part_ml = E->dalloc<float>((size_t)c.n_kv_heads * E->nch * ATT_QMAX * 2)) &&
-            (E->part_o = E->dalloc<float>((size_t)c.n_kv_heads * E->nch * ATT_QMAX * c.head_dim)) &&
-            (E->att_cnt = E->dalloc<int>(c.n_kv_heads)) && (E->rt_cnt = E->dalloc<int>(1)) &&
-            (E->gu_cnt = E->dalloc<int>((size_t)nv * (nff / 256 + 1))) && (E->chosen = E->dalloc<int>(16 * 32)) &&
+            (E->part_ml = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * 2)) &&
+            (E->part_o = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * c.head_dim)) &&
+            (E->att_cnt = E->dalloc<int>((size_t)c.n_kv_heads * (1 + ATT_GMAX) * CNT_STRIDE)) && (E->rt_cnt = E->dalloc<int>(1)) &&
+            (E->gu_cnt = E->dalloc<int>((size_t)nv * (nff / 256 + 1) * (1 + GU_SUB) * CNT_STRIDE)) && (E->chosen = E->dalloc<int>(16 * 32)) &&
             (E->nkeep = E->dalloc<int>(16)) && (E->weights = E->dalloc<float>(16 * 32)) && (E->jobs = E->dalloc<Job>(512)) &&
             (E->expert_count = E->dalloc<int>((size_t)c.n_layers * std::max(1, c.n_expert))) &&
             E->q8alloc(E->aq, M, ((E->q_dim + 255) / 256) * 256) && E->q8alloc(E->xq2, M, ((c.dim + 255) / 256) * 256) &&

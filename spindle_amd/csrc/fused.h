@@ -7,9 +7,12 @@ namespace spx {
 
 constexpr int MAX_M = 16;       // rows per verify / prefill pass
 constexpr int ATT_QMAX = 128;   // query heads x rows per kv head in one pass (16 rows x 8)
+constexpr int ATT_GRP = 16;     // attention: 64-position chunks merged per group
+constexpr int ATT_GMAX = 16;    // attention: groups per kv head (max_seq <= 64 * 16 * 16)
 constexpr int NORM_NT = 16;     // norm tails handle dim <= 256 * NORM_NT
 constexpr int CNT_SUB = 64;     // first-level arrival counters of a two-level count
 constexpr int CNT_STRIDE = 32;  // ints between counters (own 128-byte line each)
+constexpr int GU_SUB = 8;       // first-level counters per 256-row block of h (gate/up Q8_K tail)
 
 // Device-side step record: the token rows of this pass and where they go in the KV cache.
 struct StepRec {
@@ -69,12 +72,14 @@ struct AttnArgs {
   const float *q_bias, *k_bias, *v_bias, *q_norm, *k_norm;
   const float2 *rope;                 // [max_seq][head_dim/2] (cos, sin)
   __half *kc, *vc;                    // [n_layers][max_seq][kv_dim]
-  float *part_ml;                     // [n_kv][nch][ATT_QMAX][2] (running max, sum)
-  float *part_o;                      // [n_kv][nch][ATT_QMAX][hd] (unnormalised output)
-  int *counter;                       // [n_kv], zero between passes
+  float *part_ml;                     // [n_kv][nslot][ATT_QMAX][2] (running max, sum)
+  float *part_o;                      // [n_kv][nslot][ATT_QMAX][hd] (unnormalised output)
+  int *counter;                       // [n_kv][1 + ATT_GMAX][CNT_STRIDE], zero between passes
   float *att;                         // [m][q_dim]
   Q8KP aq;                            // permuted Q8_K of att (q null: not produced)
-  int layer, max_seq, kv_dim, hd, n_heads, n_kv, neox, nch;
+  int layer, max_seq, kv_dim, hd, n_heads, n_kv, neox;
+  int nch;                            // 64-position chunks launched per kv head (>= max_seq / 64)
+  int nslot;                          // partial slots per kv head: nch chunks, then group partials
   float eps, scale;
 };
 
@@ -111,7 +116,7 @@ struct GUArgs {
   const int *njobs;
   float *h;                           // [vec][n_ff]
   Q8KP hq;                            // q null: no quantization
-  int *counter;                       // [16*32][n_ff/256], zero between passes
+  int *counter;                       // [vectors][n_ff/256][1 + GU_SUB][CNT_STRIDE], zero between passes
   int n_ff;
   int G;                              // row-parallel launch: lane groups per row
 };

@@ -149,6 +149,12 @@ __device__ __forceinline__ void norm_rows(const NormTail &t, int b0, int b1) {
   const rsrc_t ra = rsrc_of(t.add ? t.add : t.x);
   const float4 *x4 = reinterpret_cast<const float4 *>(t.x);
   const float4 *w4 = reinterpret_cast<const float4 *>(t.nw);
+  float4 wn[NORM_NT / NW];  // the norm weights, loaded once with the first row's inputs
+#pragma unroll
+  for (int k = 0; k < NORM_NT / NW; k++) {
+    const int f = (wave + NW * k) * 64 + lane;
+    wn[k] = f < n4 ? w4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   for (int b = b0; b < b1; b++) {
     float4 r[NORM_NT / NW];
 #pragma unroll
@@ -183,7 +189,7 @@ __device__ __forceinline__ void norm_rows(const NormTail &t, int b0, int b1) {
         float4 v = r[k];
         if (f < n4) {
           if (t.x_out) reinterpret_cast<float4 *>(t.x_out)[(int64_t)b * n4 + f] = v;
-          const float4 w = w4[f];
+          const float4 w = wn[k];
           v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
           if (t.xn_out) reinterpret_cast<float4 *>(t.xn_out)[(int64_t)b * n4 + f] = v;
         }
@@ -390,6 +396,7 @@ __device__ __forceinline__ void kq_rows_par(const uint8_t *tile, int ns, int nb,
     for (int v = 0; v < MT; v++) {
       if (v < mvc) {
         float acc = 0.0f, cr = 0.0f;
+#pragma unroll 8
         for (int i = 0; i < nb; i++) {
           const float *e = cb + (((int64_t)r * nb + i) * MT + v) * 10;
           acc = fmaf(e[8], e[l], acc);
@@ -577,8 +584,9 @@ __global__ __launch_bounds__(64) void k_mvt(const MVArgs a, const StepRec *st) {
   const int m = st ? st->m : a.m;
   const int lane = threadIdx.x, slot = lane >> 3, l = lane & 7;
   const int cols = (int)a.seg[0].w.cols, nb = cols >> 8;
-  const Q8KP ly = ldsq_of(smem, MT, cols);
-  uint8_t *tile = smem + ldsq_bytes(MT, cols);
+  constexpr bool ST = MT <= 2;  // activations staged in LDS (small m); else read through the caches
+  const Q8KP ly = ST ? ldsq_of(smem, MT, cols) : a.y;
+  uint8_t *tile = smem + (ST ? ldsq_bytes(MT, cols) : 0);
   const bool coh = a.tail.nw != nullptr;
   unsigned long long bestv[MT];
 #pragma unroll
@@ -592,7 +600,7 @@ __global__ __launch_bounds__(64) void k_mvt(const MVArgs a, const StepRec *st) {
     const bool q4 = sg.w.dtype == T_Q4K;
     auto src = [&](int s) -> int64_t { return rbase + s < r1 ? ebase + rbase + s : -1; };
     if (q4) tile_fetch<T_Q4K>(tile, sg.w.pl, 8, nb, src); else tile_fetch<T_Q6K>(tile, sg.w.pl, 8, nb, src);
-    if (first) stage_q8kp(ly, a.y, cols, m, 1, [](int u) { return u; });
+    if (ST && first) stage_q8kp(ly, a.y, cols, m, 1, [](int u) { return u; });
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     const int64_t row = rbase + slot;
@@ -861,6 +869,54 @@ __device__ __forceinline__ void attn_load_kv(const AttnArgs &a, int64_t cache0, 
   }
 }
 
+// Merges n online-softmax partials (running max m, sum l, unnormalised output o) in slots
+// s0 .. s0+n-1 for NQ queries: M = max m_c, w_c = exp(m_c - M), L = sum l_c w_c, O = sum w_c o_c
+// in slot order. Thread (query jq of each group of 8, dims dd0..dd0+DP-1) loads its own
+// inputs (one round of coherent loads). Writes either the normalised output O / L to LDS
+// (ol) or the merged partial (M, L, O) to slot `dst`.
+template <int HD, int DP, int NMAX>
+__device__ __forceinline__ void attn_merge(rsrc_t r_ml, rsrc_t r_o, int s0, int n, int NQ, int jq, int dd0, float *ol,
+                                           const rsrc_t *d_ml, const rsrc_t *d_o, int dst) {
+  for (int q0 = 0; q0 < NQ; q0 += 8) {
+    const int qi = q0 + jq;
+    if (qi >= NQ) continue;
+    f2v ml[NMAX];
+    f4v ov[NMAX];
+#pragma unroll
+    for (int k = 0; k < NMAX; k++) {
+      const int sc = s0 + min(k, n - 1);
+      ml[k] = ld_coh2(r_ml, (sc * ATT_QMAX + qi) * 8);
+      const int off = ((sc * ATT_QMAX + qi) * HD + dd0) * 4;
+      if constexpr (DP == 4) ov[k] = ld_coh4(r_o, off);
+      else { const f2v t2 = ld_coh2(r_o, off); ov[k] = f4v{t2.x, t2.y, 0.0f, 0.0f}; }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < NMAX; k++) if (k < n) M = fmaxf(M, ml[k].x);
+    float L = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < NMAX; k++) {
+      if (k < n) {
+        const float w = ml[k].x == -INFINITY ? 0.0f : expf(ml[k].x - M);
+        L = fmaf(ml[k].y, w, L);
+        acc[0] = fmaf(ov[k].x, w, acc[0]);
+        acc[1] = fmaf(ov[k].y, w, acc[1]);
+        if constexpr (DP == 4) { acc[2] = fmaf(ov[k].z, w, acc[2]); acc[3] = fmaf(ov[k].w, w, acc[3]); }
+      }
+    }
+    if (ol) {
+      const float il = __fdiv_rn(1.0f, fmaxf(L, 1e-30f));
+#pragma unroll
+      for (int d = 0; d < DP; d++) ol[qi * HD + dd0 + d] = acc[d] * il;
+    } else {
+      const int off = ((dst * ATT_QMAX + qi) * HD + dd0) * 4;
+      if constexpr (DP == 4) st_coh4(*d_o, off, f4v{acc[0], acc[1], acc[2], acc[3]});
+      else st_coh2(*d_o, off, f2v{acc[0], acc[1]});
+      if ((threadIdx.x & 31) == 0) st_coh2(*d_ml, (dst * ATT_QMAX + qi) * 8, f2v{M, L});
+    }
+  }
+}
+
 template <int HD, int NGM>
 __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -871,18 +927,17 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
   const int h = blockIdx.y, c = blockIdx.x;
   const int m = st->m, start = st->start, total = start + m;
   const int g = a.n_heads / a.n_kv, NQ = m * g, NG = (NQ + 7) >> 3;
-  int span = (total + a.nch - 1) / a.nch;
-  span = (span + 15) & ~15;
-  const int nch = (total + span - 1) / span;
+  // chunk c = positions [64c, 64c + 64): fixed boundaries, so a row's partials (and the merge
+  // below) do not depend on how many rows the pass has or where it starts
+  const int nch = (total + 63) >> 6;
   if (c >= nch) return;
-  const int p_lo = c * span, p_hi = min(p_lo + span, total);
+  const int p_lo = c * 64, p_hi = min(p_lo + 64, total);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   float *qs = reinterpret_cast<float *>(smem);                // [NQ][HD] queries, later the merged output
   __half *ks = reinterpret_cast<__half *>(qs + NQ * HD);      // [64][KS]
   __half *vs = ks + 64 * KS;                                  // [64][KS]
   float *ps = reinterpret_cast<float *>(vs + 64 * KS);        // [8][64]
   float *sm = ps + 8 * 64, *sl = sm + ATT_QMAX, *sa = sl + ATT_QMAX;  // running max, sum; group alpha [8]
-  float *wsm = sa + 8;                                        // merge weights [NQ][64]
   const int64_t cache0 = (int64_t)a.layer * a.max_seq * a.kv_dim + (int64_t)h * HD;
   const int half = HD / 2;
 
@@ -1010,9 +1065,10 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
     }
   }
 
-  // 3. partials (coherent stores), then the last workgroup of this kv head merges
-  const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nch) * ATT_QMAX * 2);
-  const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nch) * ATT_QMAX * HD);
+  // 3. partials (coherent stores); the last chunk of each group of ATT_GRP chunks merges the
+  // group, the last group merger of the kv head merges the groups (chunk / group order)
+  const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nslot) * ATT_QMAX * 2);
+  const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nslot) * ATT_QMAX * HD);
 #pragma unroll
   for (int G = 0; G < NGM; G++) {
     const int qi = 8 * G + jq;
@@ -1023,55 +1079,26 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
       if ((tid & 31) == 0) st_coh2(r_ml, (c * ATT_QMAX + qi) * 8, f2v{sm[qi], sl[qi]});
     }
   }
-  if (arrive(&a.counter[h]) != nch - 1) return;
-  // chunk weights exp(m_c - max) and 1 / sum_c l_c w_c per query (wave per query, lane per chunk)
-  for (int qi = wave; qi < NQ; qi += 4) {
-    const f2v ml = lane < nch ? ld_coh2(r_ml, (lane * ATT_QMAX + qi) * 8) : f2v{-INFINITY, 0.0f};
-    const float mx = wave_max(ml.x);
-    const float w = ml.x == -INFINITY ? 0.0f : expf(ml.x - mx);
-    const float l = wave_sum(ml.y * w);
-    wsm[qi * 64 + lane] = w;
-    if (lane == 0) sl[qi] = __fdiv_rn(1.0f, fmaxf(l, 1e-30f));
+  const int grp = c / ATT_GRP, ngrp = (nch + ATT_GRP - 1) / ATT_GRP, gcnt = min(ATT_GRP, nch - grp * ATT_GRP);
+  int *hcnt = a.counter + (int64_t)h * (1 + ATT_GMAX) * CNT_STRIDE;
+  if (arrive(hcnt + (1 + grp) * CNT_STRIDE) != gcnt - 1) return;
+  if (tid == 0) hcnt[(1 + grp) * CNT_STRIDE] = 0;
+  float *ol = qs;  // merged output [NQ][HD] = rows b, then this group's heads
+  if (ngrp == 1) {
+    attn_merge<HD, DP, ATT_GRP>(r_ml, r_o, 0, gcnt, NQ, jq, dd0, ol, nullptr, nullptr, 0);
+  } else {
+    // group partial -> slot a.nch + grp
+    attn_merge<HD, DP, ATT_GRP>(r_ml, r_o, grp * ATT_GRP, gcnt, NQ, jq, dd0, nullptr, &r_ml, &r_o, a.nch + grp);
+    if (arrive(hcnt) != ngrp - 1) return;
+    if (tid == 0) hcnt[0] = 0;
+    attn_merge<HD, DP, ATT_GMAX>(r_ml, r_o, a.nch, ngrp, NQ, jq, dd0, ol, nullptr, nullptr, 0);
   }
   __syncthreads();
-  float *ol = qs;  // merged output [NQ][HD] = rows b, then this group's heads
-  for (int q0 = 0; q0 < NQ; q0 += 8) {
-    const int qi = q0 + jq;
-    if (qi < NQ) {
-      float acc[DP];
-#pragma unroll
-      for (int d = 0; d < DP; d++) acc[d] = 0.0f;
-      for (int c0 = 0; c0 < nch; c0 += 8) {
-        f4v ov[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-          const int cc = min(c0 + k, nch - 1);
-          const int off = ((cc * ATT_QMAX + qi) * HD + dd0) * 4;
-          if (DP == 4) ov[k] = ld_coh4(r_o, off);
-          else { const f2v t2 = ld_coh2(r_o, off); ov[k] = f4v{t2.x, t2.y, 0.0f, 0.0f}; }
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-          if (c0 + k < nch) {
-            const float w = wsm[qi * 64 + c0 + k];
-            acc[0] = fmaf(ov[k].x, w, acc[0]);
-            acc[1] = fmaf(ov[k].y, w, acc[1]);
-            if constexpr (DP == 4) { acc[2] = fmaf(ov[k].z, w, acc[2]); acc[3] = fmaf(ov[k].w, w, acc[3]); }
-          }
-        }
-      }
-      const float il = sl[qi];
-      const int b = qi / g, head = h * g + qi % g;
-#pragma unroll
-      for (int d = 0; d < DP; d++) {
-        const float ov = acc[d] * il;
-        ol[qi * HD + dd0 + d] = ov;
-        a.att[(int64_t)b * a.n_heads * HD + head * HD + dd0 + d] = ov;
-      }
-    }
+  for (int i = tid; i < NQ * HD; i += 256) {
+    const int qi = i / HD, d = i - qi * HD, b = qi / g, head = h * g + qi % g;
+    a.att[(int64_t)b * a.n_heads * HD + head * HD + d] = ol[i];
   }
   if (a.aq.q) {
-    __syncthreads();
     const int gw = g * HD, nbq = gw / 256, qdim = a.n_heads * HD, nbr = qdim / 256;
     for (int it = wave; it < m * nbq; it += 4) {
       const int b = it / nbq, kb = it % nbq;
@@ -1081,63 +1108,68 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
       q8k_block_store(xv, am, a.aq.q + vb * 64, a.aq.d + vb, reinterpret_cast<int *>(a.aq.bs + vb * 8));
     }
   }
-  if (tid == 0) a.counter[h] = 0;
 }
 
 // ------------------------------------------------------------------ MoE router + routing
-// ------------------------------------------------------------------ MoE router + routing
-// F32 router rows (two per wavefront, 32 lanes each; fixed per-row order, so batch
-// independent like matvec_multi's per-vector F32 path :455-464), then the last workgroup
-// routes: softmax (max, exp, sum, divide), top-n_used by probability (ties to the lower
-// expert index), pruning (moe_prune >= 1: keep clamp(x, max(2, n/2), n); < 1: mass rule),
-// weights p / sum(kept) when normalised (:1199-1239, :959-997), and the grouped job lists
-// over the union of chosen experts in expert order, users in (row, slot) order (:982-986).
+// F32 router rows (one per wavefront; lane j holds float4s j, j+64, ... of the row in
+// registers, each vector's dot is the lane's fma chain then the wave tree: a fixed order
+// for every batch size, like matvec_multi's per-vector F32 path :455-464), then the last
+// workgroup routes, a wavefront per row: softmax (max, exp, sum, divide), top-n_used by
+// probability (ties to the lower expert index), pruning (moe_prune >= 1: keep
+// clamp(x, max(2, n/2), n); < 1: mass rule), weights p / sum(kept) when normalised
+// (:1199-1239, :959-997), and the grouped job lists over the union of chosen experts in
+// expert order, users in (row, slot) order (:982-986).
 template <int MT>
-__global__ __launch_bounds__(64) void k_router(const RouterArgs a, const StepRec *st) {
-  const int m = st->m, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void k_router(const RouterArgs a, const StepRec *st) {
+  const int m = st->m, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int dim = a.dim, n4 = dim >> 2;
-  const int hl = lane & 31;
-  constexpr int G = MT < 8 ? MT : 8;
-  const int row = blockIdx.x * 2 + (lane >> 5);
+  constexpr int G = MT < 4 ? MT : 4;
+  const int row = blockIdx.x * 4 + wave;
   const bool valid = row < a.n_expert;
   const float4 *wr = reinterpret_cast<const float4 *>(a.w.pl.p0 + (int64_t)(valid ? row : 0) * dim * 4);
   const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
+  float4 wv[NORM_NT];
+#pragma unroll
+  for (int k = 0; k < NORM_NT; k++) {
+    const int f = lane + 64 * k;
+    wv[k] = f < n4 ? wr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   for (int v0 = 0; v0 < m; v0 += G) {
     const int nv = min(G, m - v0);
     float part[G];
 #pragma unroll
     for (int v = 0; v < G; v++) part[v] = 0.0f;
-    for (int f = hl; f < n4; f += 32) {
-      const float4 w = wr[f];
 #pragma unroll
-      for (int v = 0; v < G; v++) {
-        if (v < nv) {
-          const float4 x = x4[(int64_t)(v0 + v) * n4 + f];
-          part[v] = fmaf(w.x, x.x, part[v]);
-          part[v] = fmaf(w.y, x.y, part[v]);
-          part[v] = fmaf(w.z, x.z, part[v]);
-          part[v] = fmaf(w.w, x.w, part[v]);
+    for (int k = 0; k < NORM_NT; k++) {
+      const int f = lane + 64 * k;
+      if (f < n4) {
+#pragma unroll
+        for (int v = 0; v < G; v++) {
+          if (v < nv) {
+            const float4 x = x4[(int64_t)(v0 + v) * n4 + f];
+            part[v] = fmaf(wv[k].x, x.x, part[v]);
+            part[v] = fmaf(wv[k].y, x.y, part[v]);
+            part[v] = fmaf(wv[k].z, x.z, part[v]);
+            part[v] = fmaf(wv[k].w, x.w, part[v]);
+          }
         }
       }
     }
 #pragma unroll
     for (int v = 0; v < G; v++) {
-      float t = part[v];
-      t = t + SPX_DPPF(t, 0xB1);
-      t = t + SPX_DPPF(t, 0x4E);
-      t = t + SPX_DPPF(t, 0x141);
-      t = t + SPX_DPPF(t, 0x140);
-      t = t + __shfl_xor(t, 16);
-      if (hl == 0 && valid && v < nv) st_dev(a.logits + (int64_t)(v0 + v) * a.n_expert + row, t);
+      const float t = wave_sum(part[v]);
+      if (lane == 0 && valid && v < nv) st_dev(a.logits + (int64_t)(v0 + v) * a.n_expert + row, t);
     }
   }
   if (arrive(a.counter) != (int)gridDim.x - 1) return;
-  // routing (one wavefront)
-  __shared__ float probs[256];
-  __shared__ int chosen[MAX_M][32];
-  __shared__ int nkeep[MAX_M];
+  // routing: wave w takes rows w, w+4, ...; lane i < n_used ends up holding the row's i-th
+  // choice (expert, probability)
+  __shared__ signed char slot_of[MAX_M][256];  // slot of expert e among row b's kept choices, -1: none
+  __shared__ int wcount[4];
   const int ne = a.n_expert, nu = a.n_used;
-  for (int b = 0; b < m; b++) {
+  for (int i = threadIdx.x; i < MAX_M * 256; i += 256) (&slot_of[0][0])[i] = -1;
+  __syncthreads();
+  for (int b = wave; b < m; b += 4) {
     const float *lg = a.logits + (int64_t)b * ne;
     float lv[4], mx = -INFINITY;
 #pragma unroll
@@ -1153,93 +1185,104 @@ __global__ __launch_bounds__(64) void k_router(const RouterArgs a, const StepRec
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int e = lane + 64 * k;
-      if (e < ne) { pv[k] = pv[k] / sum; probs[e] = pv[k]; }
+      if (e < ne) pv[k] = pv[k] / sum;
       key[k] = e < ne ? ((unsigned long long)__float_as_uint(pv[k]) << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)e) : 0ull;
     }
+    int my_e = 0;
+    float my_p = 0.0f;
     for (int i = 0; i < nu; i++) {
       unsigned long long bk = key[0];
 #pragma unroll
       for (int k = 1; k < 4; k++) bk = key[k] > bk ? key[k] : bk;
       bk = wave_max_u64(bk);
       const int e = (int)(0xFFFFFFFFu - (unsigned)(bk & 0xFFFFFFFFull));
-      if (lane == 0) chosen[b][i] = e;
+      if (lane == i) { my_e = e; my_p = __uint_as_float((uint32_t)(bk >> 32)); }
       if ((e & 63) == lane) key[e >> 6] = 0ull;
     }
-    __syncthreads();
-    if (lane == 0) {
-      int keep = nu;
-      if (a.moe_prune > 0.0f && nu > 2) {
-        const int min_keep = max(2, nu / 2);
-        if (a.moe_prune >= 1.0f) keep = min(max((int)a.moe_prune, min_keep), nu);
-        else {
-          float top = 0.0f;
-          for (int i = 0; i < nu; i++) top += probs[chosen[b][i]];
-          const float target = top * (1.0f - a.moe_prune);
-          float cum = 0.0f;
-          int k = 0;
-          while (k < nu && (k < min_keep || cum < target)) { cum += probs[chosen[b][k]]; k++; }
-          keep = k;
-        }
+    // pruning and the normalising sum, in choice order (the reference's sequential sums)
+    int keep = nu;
+    if (a.moe_prune > 0.0f && nu > 2) {
+      const int min_keep = max(2, nu / 2);
+      if (a.moe_prune >= 1.0f) keep = min(max((int)a.moe_prune, min_keep), nu);
+      else {
+        float top = 0.0f;
+        for (int i = 0; i < nu; i++) top += __shfl(my_p, i);
+        const float target = top * (1.0f - a.moe_prune);
+        float cum = 0.0f;
+        int k = 0;
+        while (k < nu && (k < min_keep || cum < target)) { cum += __shfl(my_p, k); k++; }
+        keep = k;
       }
-      float wsum = 0.0f;
-      for (int i = 0; i < keep; i++) wsum += probs[chosen[b][i]];
-      for (int i = 0; i < keep; i++) {
-        a.chosen[b * 32 + i] = chosen[b][i];
-        a.weights[b * 32 + i] = a.norm ? probs[chosen[b][i]] / wsum : probs[chosen[b][i]];
-      }
-      nkeep[b] = keep;
-      a.nkeep[b] = keep;
     }
-    __syncthreads();
+    float wsum = 0.0f;
+    for (int i = 0; i < keep; i++) wsum += __shfl(my_p, i);
+    if (lane < keep) {
+      a.chosen[b * 32 + lane] = my_e;
+      a.weights[b * 32 + lane] = a.norm ? my_p / wsum : my_p;
+      slot_of[b][my_e] = (signed char)lane;
+    }
+    if (lane == 0) a.nkeep[b] = keep;
   }
-  // jobs: experts with at least one user, in expert order
+  __syncthreads();
+  // jobs: experts with at least one user, in expert order (thread e = expert e); users in
+  // row order (a row chooses an expert at most once)
+  const int e = threadIdx.x;
+  int cnt = 0;
+  if (e < ne)
+    for (int b = 0; b < m; b++) cnt += slot_of[b][e] >= 0;
+  const unsigned long long bal = __ballot(cnt > 0);
+  if (lane == 0) wcount[wave] = __popcll(bal);
+  __syncthreads();
   int base = 0;
-  for (int e0 = 0; e0 < ne; e0 += 64) {
-    const int e = e0 + lane;
-    int cnt = 0;
-    if (e < ne)
-      for (int b = 0; b < m; b++)
-        for (int i = 0; i < nkeep[b]; i++) cnt += chosen[b][i] == e;
-    const unsigned long long bal = __ballot(cnt > 0);
-    if (cnt > 0) {
-      const int j = base + __popcll(bal & ((1ull << lane) - 1ull));
-      Job &J = a.jobs[j];
-      Job &Jd = a.jobs[256 + j];
-      int k = 0;
-      for (int b = 0; b < m; b++)
-        for (int i = 0; i < nkeep[b]; i++)
-          if (chosen[b][i] == e) {
-            J.vec[k] = b;
-            J.out[k] = b * nu + i;
-            Jd.vec[k] = b * nu + i;
-            Jd.out[k] = b * nu + i;
-            k++;
-          }
-      J.expert = e;
-      Jd.expert = e;
-      J.nvec = k;
-      Jd.nvec = k;
-      if (a.expert_count) a.expert_count[e] += 1;
+  for (int w = 0; w < wave; w++) base += wcount[w];
+  if (cnt > 0) {
+    const int j = base + __popcll(bal & ((1ull << lane) - 1ull));
+    Job &J = a.jobs[j];
+    Job &Jd = a.jobs[256 + j];
+    int k = 0;
+    for (int b = 0; b < m; b++) {
+      const int s = slot_of[b][e];
+      if (s >= 0) {
+        J.vec[k] = b;
+        J.out[k] = b * nu + s;
+        Jd.vec[k] = b * nu + s;
+        Jd.out[k] = b * nu + s;
+        k++;
+      }
     }
-    base += __popcll(bal);
+    J.expert = e;
+    Jd.expert = e;
+    J.nvec = k;
+    Jd.nvec = k;
+    if (a.expert_count) a.expert_count[e] += 1;
   }
-  if (lane == 0) { *a.njobs = base; *a.counter = 0; }
+  if (threadIdx.x == 0) { *a.njobs = wcount[0] + wcount[1] + wcount[2] + wcount[3]; *a.counter = 0; }
 }
 
 // ------------------------------------------------------------------ gate / up + SwiGLU
 // h = silu(g) * u (silu :586-588, ffns_fused :407-417) for the rows of one job. With hq, the
 // last of the workgroups that cover a 256-row block of h quantizes it (Q8_K for an integer
-// down projection, :420-424) and clears the block's counter for the next pass. rpw = rows of
-// h per workgroup.
+// down projection, :420-424). rpw = rows of h per workgroup. The arrivals of a block's
+// workgroups are counted in two levels (GU_SUB sub-counters, then one top counter, each on
+// its own 128-byte line) so that no counter takes more than a few atomics; the counters are
+// left at zero for the next pass.
 __device__ __forceinline__ void gateup_quant_tail(const GUArgs &a, int nvec, const int *jo, int rpw) {
   __shared__ int quant_u[MAX_M];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n_ff = a.n_ff, nbh = n_ff / 256, blk = (blockIdx.x * rpw) / 256, expect = 256 / rpw;
+  const int n_ff = a.n_ff, nbh = n_ff / 256, per = 256 / rpw, blk = blockIdx.x / per, sub = (blockIdx.x % per) % GU_SUB;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if ((int)threadIdx.x < nvec) {
     const int vo = jo ? jo[threadIdx.x] : threadIdx.x;
-    quant_u[threadIdx.x] = atomicAdd(&a.counter[vo * nbh + blk], 1) == expect - 1;
+    int *base = a.counter + (int64_t)(vo * nbh + blk) * (1 + GU_SUB) * CNT_STRIDE;
+    int *sc = base + (1 + sub) * CNT_STRIDE;
+    int last = 0;
+    if (atomicAdd(sc, 1) == per / GU_SUB - 1) {
+      *sc = 0;
+      last = atomicAdd(base, 1) == GU_SUB - 1;
+      if (last) *base = 0;
+    }
+    quant_u[threadIdx.x] = last;
   }
   __syncthreads();
   for (int u = wave; u < nvec; u += 4) {
@@ -1250,7 +1293,6 @@ __device__ __forceinline__ void gateup_quant_tail(const GUArgs &a, int nvec, con
     const float am = wave_max(amax4(xv));
     const int64_t vb = (int64_t)vo * nbh + blk;
     q8k_block_store(xv, am, a.hq.q + vb * 64, a.hq.d + vb, reinterpret_cast<int *>(a.hq.bs + vb * 8));
-    if (lane == 0) a.counter[vo * nbh + blk] = 0;
   }
 }
 
@@ -1261,10 +1303,9 @@ struct GUJob {
 __device__ __forceinline__ bool gu_job(const GUArgs &a, int m, GUJob &j) {
   j.expert = 0; j.nvec = m; j.jv = nullptr; j.jo = nullptr;
   if (!a.jobs) return true;
-  if ((int)blockIdx.y >= *a.njobs) return false;
-  const Job &J = a.jobs[blockIdx.y];
+  const Job &J = a.jobs[blockIdx.y];  // always addressable: loaded together with the job count
   j.expert = J.expert; j.nvec = J.nvec; j.jv = J.vec; j.jo = J.out;
-  return true;
+  return (int)blockIdx.y < *a.njobs;
 }
 
 // Integer, eight rows per wavefront: 16 rows of h per workgroup; in each wavefront slots 0-3
@@ -1278,18 +1319,19 @@ __global__ __launch_bounds__(256) void k_gateup_kq(const GUArgs a, const StepRec
   const int nb = (int)a.gate.nb, n_ff = a.n_ff, dim = (int)a.gate.cols;
   const int rb = blockIdx.x * 16 + wave * 4;
   const int64_t eb = (int64_t)J.expert * a.gate.rows;
-  const Q8KP ly = ldsq_of(smem, MT, dim);
-  uint8_t *tile = smem + ldsq_bytes(MT, dim) + (size_t)wave * 8 * nb * tile_bpb();
+  constexpr bool ST = MT <= 2;  // activations staged in LDS (small m); else read through the caches
+  const Q8KP ly = ST ? ldsq_of(smem, MT, dim) : a.y;
+  uint8_t *tile = smem + (ST ? ldsq_bytes(MT, dim) : 0) + (size_t)wave * 8 * nb * tile_bpb();
   tile_fetch<T>(tile, a.gate.pl, 8, nb, [&](int sl) -> int64_t { return sl < 4 && rb + sl < n_ff ? eb + rb + sl : -1; });
   tile_fetch<T>(tile, a.up.pl, 8, nb, [&](int sl) -> int64_t { return sl >= 4 && rb + sl - 4 < n_ff ? eb + rb + sl - 4 : -1; });
-  stage_q8kp(ly, a.y, dim, J.nvec, 4, [&](int u) { return J.jv ? J.jv[u] : u; });
+  if (ST) stage_q8kp(ly, a.y, dim, J.nvec, 4, [&](int u) { return J.jv ? J.jv[u] : u; });
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   const int r = rb + (slot & 3);
   const bool valid = r < n_ff;
   int vidx[MT];
 #pragma unroll
-  for (int v = 0; v < MT; v++) vidx[v] = v;
+  for (int v = 0; v < MT; v++) vidx[v] = ST ? v : (J.jv && v < J.nvec ? J.jv[v] : v);
   float res[MT];
   kq_walk_tile<T, MT>(tile, 8, nb, slot, eb + (valid ? r : n_ff - 1), ly, vidx, J.nvec, l, res);
 #pragma unroll
@@ -1398,8 +1440,12 @@ __global__ __launch_bounds__(256) void k_down_kq(const DownArgs a, const StepRec
     const int j = j0 + slot;
     const bool has = j < nj;
     const Job &J = a.jobs[has ? j : 0];
+    // lane s < 8 holds slot s's expert (the job array is always addressable, so this load
+    // need not wait for the job count)
+    const int ex = a.jobs[j0 + (lane & 7)].expert;
     tile_fetch<T>(tile, a.w.pl, 8, nb, [&](int sl) -> int64_t {
-      return j0 + sl < nj && valid ? (int64_t)a.jobs[j0 + sl].expert * dim + r : -1;
+      const int e = __shfl(ex, sl);
+      return j0 + sl < nj && valid ? (int64_t)e * dim + r : -1;
     });
     if (STAGE && j0 == 0) stage_q8kp(ly, a.y, n_ff, npairs, 4, [](int u) { return u; });
     __builtin_amdgcn_s_waitcnt(0);
@@ -1507,7 +1553,7 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
     else { SPX_LDS(k_mvr<2>, sm); hipLaunchKernelGGL(k_mvr<2>, dim3(grid), dim3(256), sm, s, a, st); }
     return hipGetLastError();
   }
-  const size_t sm = ldsq_bytes(mt, cols) + (size_t)8 * nb * tile_bpb();
+  const size_t sm = (mt <= 2 ? ldsq_bytes(mt, cols) : 0) + (size_t)8 * nb * tile_bpb();
 #define SPX_MVT(MTV) do { SPX_LDS(k_mvt<MTV>, sm); hipLaunchKernelGGL(k_mvt<MTV>, dim3(grid), dim3(64), sm, s, a, st); } while (0)
   switch (mt) {
   case 1: SPX_MVT(1); break;
@@ -1522,7 +1568,7 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
 
 static size_t attn_smem(const AttnArgs &a, int m) {
   const int g = a.n_heads / a.n_kv, nq = m * g;
-  return (size_t)nq * a.hd * 4 + 2 * 64 * (a.hd + 8) * 2 + 8 * 64 * 4 + (2 * ATT_QMAX + 8) * 4 + (size_t)nq * 64 * 4 + 16;
+  return (size_t)nq * a.hd * 4 + 2 * 64 * (a.hd + 8) * 2 + 8 * 64 * 4 + (2 * ATT_QMAX + 8) * 4 + 16;
 }
 
 template <int HD, int NGM>
@@ -1546,13 +1592,11 @@ hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStre
 
 hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStream_t s) {
   mt = bucket(mt);
-  const int grid = (a.n_expert + 1) / 2;
+  const int grid = (a.n_expert + 3) / 4;
   switch (mt) {
-  case 1: hipLaunchKernelGGL(k_router<1>, dim3(grid), dim3(64), 0, s, a, st); break;
-  case 2: hipLaunchKernelGGL(k_router<2>, dim3(grid), dim3(64), 0, s, a, st); break;
-  case 4: hipLaunchKernelGGL(k_router<4>, dim3(grid), dim3(64), 0, s, a, st); break;
-  case 8: hipLaunchKernelGGL(k_router<8>, dim3(grid), dim3(64), 0, s, a, st); break;
-  default: hipLaunchKernelGGL(k_router<16>, dim3(grid), dim3(64), 0, s, a, st); break;
+  case 1: hipLaunchKernelGGL(k_router<1>, dim3(grid), dim3(256), 0, s, a, st); break;
+  case 2: hipLaunchKernelGGL(k_router<2>, dim3(grid), dim3(256), 0, s, a, st); break;
+  default: hipLaunchKernelGGL(k_router<4>, dim3(grid), dim3(256), 0, s, a, st); break;
   }
   return hipGetLastError();
 }
@@ -1570,7 +1614,7 @@ static hipError_t launch_gu_t(const GUArgs &a, int mode, const StepRec *st, int 
         return hipGetLastError();
       }
     }
-    const size_t sm = ldsq_bytes(MT, dim) + (size_t)4 * 8 * nb * tile_bpb();
+    const size_t sm = (MT <= 2 ? ldsq_bytes(MT, dim) : 0) + (size_t)4 * 8 * nb * tile_bpb();
     SPX_LDS((k_gateup_kq<T, MT>), sm);
     hipLaunchKernelGGL((k_gateup_kq<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), sm, s, a, st);
   } else {

@@ -260,13 +260,13 @@ static Q8KP ws_q8kp(spx_ctx *ctx, int m, int64_t n, bool *ok) {
   return r;
 }
 
-// Launch mode: row-parallel for integer weights at m <= 2, else eight rows per wavefront;
-// SPX_MV_MODE=0/1 forces one (tests cover both).
+// Launch mode: row-parallel for integer weights, eight rows per wavefront for the float
+// formats; SPX_MV_MODE=0 forces the eight-row tiles for integer weights too (tests cover both).
 static int mv_launch(spx_ctx *ctx, const spx_tensor *w, int expert, int m, const float *x, int64_t ld_x, Q8KP y, float *out,
                      int64_t ld_out, int64_t r0, int64_t r1) {
   const bool kq = w->v.dtype == T_Q4K || w->v.dtype == T_Q6K;
-  int mode = kq && m <= 2 ? 1 : 0;
-  if (const char *v = std::getenv("SPX_MV_MODE")) mode = kq && m <= 2 && atoi(v) == 1 ? 1 : 0;
+  int mode = kq ? 1 : 0;
+  if (const char *v = std::getenv("SPX_MV_MODE")) mode = kq && atoi(v) == 1 ? 1 : 0;
   int G = 8, R = 1;
   rp_shape(w->v.nb, G, R);
   MVArgs a{};

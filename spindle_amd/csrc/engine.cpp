@@ -144,10 +144,11 @@ Seg seg_of(const spx_tensor *t, float *out, int64_t ld_out, int m, int mode, int
   return s;
 }
 
-// Launch mode of a matrix pass: row-parallel for integer weights at m <= 2 (decode), else
-// eight rows per wavefront.
+// Launch mode of a matrix pass: row-parallel for integer weights (all m), unless forced to
+// eight rows per wavefront (SPX_MV_MODE=0).
 int mode_of(const spx_engine *E, const spx_tensor *t, int m) {
-  if (!is_kq(t) || m > 2) return 0;
+  (void)m;
+  if (!is_kq(t)) return 0;
   return E->mv_mode >= 0 ? E->mv_mode : 1;
 }
 
@@ -219,9 +220,10 @@ int mv_one(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld
   a.G = G;
   a.R = R;
   a.lscale = E->c.logit_scale;
-  if (tail && tails) a.tail = *tail;
+  const bool fused = tail && tails && (mode == 1 || !is_kq(w));  // the tile kernel takes no tail
+  if (fused) a.tail = *tail;
   if (int r = mv_run(E, a, m, mode)) return r;
-  if (tail && !tails) {
+  if (tail && !fused) {
     ProfScope ps(E, cls_norm, 0);
     SPX_HIP(launch_norm(*tail, E->st_dev, m, E->ctx->stream));
   }
@@ -285,7 +287,7 @@ int enqueue_forward(spx_engine *E, int m) {
     const int nff = (int)ly.gate->v.rows;
     const bool d_int = is_kq(ly.down);
     const NormTail tn = norm_next(E, l + 1, E->xB, E->ffn, E->xA);
-    const int gmode = mode_of(E, ly.gate, m);
+    const int gmode = m <= 2 ? mode_of(E, ly.gate, m) : 0;  // grouped experts: row-parallel at decode, tiles for verify
     if (ly.moe) {  // moe_forward / moe_forward_batch (:925-1392)
       const int nu = c.n_expert_used, ne = c.n_expert;
       {
@@ -331,7 +333,7 @@ int enqueue_forward(spx_engine *E, int m) {
   }
   {
     ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
-    const int mode = E->lm_mode >= 0 && m <= 2 && is_kq(E->lm_head) ? E->lm_mode : 0;
+    const int mode = E->lm_mode >= 0 && is_kq(E->lm_head) ? E->lm_mode : 0;
     int G = 8, R = 1;
     rp_shape(E->lm_head->v.nb, G, R);
     MVArgs a{};

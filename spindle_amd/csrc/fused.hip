@@ -350,15 +350,16 @@ __device__ __forceinline__ void kq_walk_tile(const uint8_t *tile, int ns, int nb
   for (int v = 0; v < MT; v++) res[v] = hsum_rows8(acc[v]) - corr[v];
 }
 
-// Row-parallel walker: the wavefront's R slots (rows) x G lane groups; group gi of row r
-// computes blocks gi, gi+G, ... and leaves, per block and vector, d*xd, the 8 lane dots as
-// floats and the correction term in the chain buffer cb (LDS); then group 0 of each row runs
-// the reference's chain acc_l = fma(d*xd_i, float(P_il), acc_l), corr = corr + term_i over
-// the blocks in order. res[v] is valid in lane 0 of group 0 of each row.
+// Row-parallel walker: the wavefront's R slots (rows) x G lane groups (G a power of two);
+// group gi of row r computes blocks gi, gi+G, ... and leaves, per block and vector, d*xd, the
+// 8 lane dots as floats and the correction term in the chain buffer cb (LDS); then, for
+// vector v, group v % G of each row runs the reference's chain acc_l = fma(d*xd_i, float(P_il),
+// acc_l), corr = corr + term_i over the blocks in order and its lane 0 writes the row's result
+// to ov[r * MT + v] (LDS). The caller reads ov after the call.
 // cb: [R][nb][MT] x {8 lane dots, d*xd, term} floats.
 template <int T, int MT, class GROW, class VID, class MV>
 __device__ __forceinline__ void kq_rows_par(const uint8_t *tile, int ns, int nb, int G, int R, GROW grow_of, VID vid, MV mv_of, const Q8KP &y,
-                                            float *cb, float *res) {
+                                            float *cb, float *ov) {
   const int lane = threadIdx.x & 63, l = lane & 7, grp = lane >> 3;
   const int r = grp / G, gi = grp - r * G;
   if (r < R) {
@@ -370,7 +371,7 @@ __device__ __forceinline__ void kq_rows_par(const uint8_t *tile, int ns, int nb,
       tile_block(tile, ns, nb, r, i, l, odd0 ^ ((i & 1) != 0), raw);
       KQDec<T> dec;
       dec.decode(raw, l);
-#pragma unroll
+#pragma unroll 4
       for (int v = 0; v < MT; v++) {
         if (v < mv) {
           const int64_t vb = (int64_t)vid(r, v) * nb + i;
@@ -386,15 +387,11 @@ __device__ __forceinline__ void kq_rows_par(const uint8_t *tile, int ns, int nb,
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
-  float corr[MT];
-#pragma unroll
-  for (int v = 0; v < MT; v++) { res[v] = 0.0f; corr[v] = 0.0f; }
-  const bool chain = r < R && gi == 0;
-  const int mvc = chain ? mv_of(r) : 0;
-  if (chain) {
+  if (r < R) {
+    const int mvc = mv_of(r);
 #pragma unroll
     for (int v = 0; v < MT; v++) {
-      if (v < mvc) {
+      if ((v & (G - 1)) == gi && v < mvc) {
         float acc = 0.0f, cr = 0.0f;
 #pragma unroll 8
         for (int i = 0; i < nb; i++) {
@@ -402,13 +399,13 @@ __device__ __forceinline__ void kq_rows_par(const uint8_t *tile, int ns, int nb,
           acc = fmaf(e[8], e[l], acc);
           cr = cr + e[9];
         }
-        res[v] = acc;
-        corr[v] = cr;
+        const float res = hsum_rows8(acc) - cr;
+        if (l == 0) ov[r * MT + v] = res;
       }
     }
   }
-#pragma unroll
-  for (int v = 0; v < MT; v++) res[v] = hsum_rows8(res[v]) - corr[v];
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
 }
 
 // ------------------------------------------------------------------ float row walker
@@ -577,7 +574,8 @@ __device__ __forceinline__ int seg_index(const MVArgs &a, int t, int &wg) {
 
 // ------------------------------------------------------------------ integer matvec, 8 rows per wavefront
 // One wavefront per workgroup, eight rows per task; tasks stride over the grid (the LM head
-// runs on a few thousand workgroups). LDS: the activations (staged once), then the tile.
+// runs on a few thousand workgroups). LDS: the activations (staged once), then the tile. No
+// norm tail (a pass that needs one runs the row-parallel kernel or a standalone norm).
 template <int MT>
 __global__ __launch_bounds__(64) void k_mvt(const MVArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -587,7 +585,6 @@ __global__ __launch_bounds__(64) void k_mvt(const MVArgs a, const StepRec *st) {
   constexpr bool ST = MT <= 2;  // activations staged in LDS (small m); else read through the caches
   const Q8KP ly = ST ? ldsq_of(smem, MT, cols) : a.y;
   uint8_t *tile = smem + (ST ? ldsq_bytes(MT, cols) : 0);
-  const bool coh = a.tail.nw != nullptr;
   unsigned long long bestv[MT];
 #pragma unroll
   for (int v = 0; v < MT; v++) bestv[v] = 0;
@@ -616,7 +613,7 @@ __global__ __launch_bounds__(64) void k_mvt(const MVArgs a, const StepRec *st) {
 #pragma unroll
       for (int v = 0; v < MT; v++)
         if (v < m) {
-          out_store(sg.out + (int64_t)v * sg.ld_out + row, res[v], coh);
+          sg.out[(int64_t)v * sg.ld_out + row] = res[v];
           if (a.best) { const unsigned long long k = pick_key(res[v], a.lscale, row); bestv[v] = k > bestv[v] ? k : bestv[v]; }
         }
     }
@@ -624,24 +621,27 @@ __global__ __launch_bounds__(64) void k_mvt(const MVArgs a, const StepRec *st) {
     first = false;
   }
   if (a.best) best_flush<MT, 1>(a, bestv, m);
-  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<1>(a.tail, 0, m);
 }
 
 // ------------------------------------------------------------------ integer matvec, row-parallel
-// Four wavefronts per workgroup, R rows per wavefront, G lane groups per row (decode).
+// Four wavefronts per workgroup, R rows per wavefront, G lane groups per row. m <= 2: the
+// activations are staged in LDS; larger m reads them through the caches.
 __host__ __device__ inline size_t rp_wave_bytes(int R, int nb, int mt) {
-  return ((size_t)R * nb * tile_bpb() + (size_t)R * nb * mt * 10 * 4 + 15) & ~(size_t)15;
+  return ((size_t)R * nb * tile_bpb() + (size_t)R * nb * mt * 10 * 4 + (size_t)R * mt * 4 + 15) & ~(size_t)15;
 }
+__host__ __device__ inline size_t rp_act_bytes(int mt, int cols) { return mt <= 2 ? ldsq_bytes(mt, cols) : 0; }
 
 template <int MT>
 __global__ __launch_bounds__(256) void k_mvr(const MVArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
+  constexpr bool ST = MT <= 2;
   const int m = st ? st->m : a.m;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l = lane & 7, grp = lane >> 3;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int cols = (int)a.seg[0].w.cols, nb = cols >> 8, G = a.G, R = a.R;
-  const Q8KP ly = ldsq_of(smem, MT, cols);
-  uint8_t *tile = smem + ldsq_bytes(MT, cols) + (size_t)wave * rp_wave_bytes(R, nb, MT);
+  const Q8KP ly = ST ? ldsq_of(smem, MT, cols) : a.y;
+  uint8_t *tile = smem + rp_act_bytes(MT, cols) + (size_t)wave * rp_wave_bytes(R, nb, MT);
   float *cb = reinterpret_cast<float *>(tile + (size_t)R * nb * tile_bpb());
+  float *ov = cb + (size_t)R * nb * MT * 10;
   const bool coh = a.tail.nw != nullptr;
   int wg;
   const Seg &sg = a.seg[seg_index(a, blockIdx.x, wg)];
@@ -649,28 +649,37 @@ __global__ __launch_bounds__(256) void k_mvr(const MVArgs a, const StepRec *st) 
   const bool q4 = sg.w.dtype == T_Q4K;
   auto src = [&](int s) -> int64_t { return s < R && rbase + s < r1 ? ebase + rbase + s : -1; };
   if (q4) tile_fetch<T_Q4K>(tile, sg.w.pl, R, nb, src); else tile_fetch<T_Q6K>(tile, sg.w.pl, R, nb, src);
-  stage_q8kp(ly, a.y, cols, m, 4, [](int u) { return u; });
+  if (ST) stage_q8kp(ly, a.y, cols, m, 4, [](int u) { return u; });
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  float res[MT];
   auto grow = [&](int r) -> int64_t { return ebase + (rbase + r < r1 ? rbase + r : r1 - 1); };
   auto vid = [](int r, int v) { return v; };
   auto mvf = [&](int r) { return m; };
-  if (q4) kq_rows_par<T_Q4K, MT>(tile, R, nb, G, R, grow, vid, mvf, ly, cb, res);
-  else kq_rows_par<T_Q6K, MT>(tile, R, nb, G, R, grow, vid, mvf, ly, cb, res);
-  const int r = grp / G;
-  unsigned long long bestv[MT];
-#pragma unroll
-  for (int v = 0; v < MT; v++) bestv[v] = 0;
-  if (r < R && grp == r * G && l == 0 && rbase + r < r1) {
-#pragma unroll
-    for (int v = 0; v < MT; v++)
-      if (v < m) {
-        out_store(sg.out + (int64_t)v * sg.ld_out + rbase + r, res[v], coh);
-        if (a.best) bestv[v] = pick_key(res[v], a.lscale, rbase + r);
-      }
+  if (q4) kq_rows_par<T_Q4K, MT>(tile, R, nb, G, R, grow, vid, mvf, ly, cb, ov);
+  else kq_rows_par<T_Q6K, MT>(tile, R, nb, G, R, grow, vid, mvf, ly, cb, ov);
+  for (int idx = lane; idx < R * MT; idx += 64) {
+    const int r = idx / MT, v = idx - r * MT;
+    if (v < m && rbase + r < r1) out_store(sg.out + (int64_t)v * sg.ld_out + rbase + r, ov[idx], coh);
   }
-  if (a.best) best_flush<MT, 4>(a, bestv, m);
+  if (a.best) {  // lane v: the wavefront's best key of vector v, then the workgroup's
+    __shared__ unsigned long long sbest[4][MAX_M];
+    if (lane < MT) {
+      unsigned long long b = 0;
+      if (lane < m)
+        for (int r = 0; r < R; r++)
+          if (rbase + r < r1) {
+            const unsigned long long k = pick_key(ov[r * MT + lane], a.lscale, rbase + r);
+            b = k > b ? k : b;
+          }
+      sbest[wave][lane] = b;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < m) {
+      unsigned long long b = sbest[0][threadIdx.x];
+      for (int w = 1; w < 4; w++) b = sbest[w][threadIdx.x] > b ? sbest[w][threadIdx.x] : b;
+      a.best[(int64_t)threadIdx.x * a.nbest + blockIdx.x] = b;
+    }
+  }
   if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
 }
 
@@ -1345,11 +1354,12 @@ __global__ __launch_bounds__(256) void k_gateup_kq(const GUArgs a, const StepRec
   if (a.hq.q) gateup_quant_tail(a, J.nvec, J.jo, 16);
 }
 
-// Integer, row-parallel (decode): one row of h per wavefront, four per workgroup; slot 0 is
-// the gate row, slot 1 the up row, four lane groups each.
+// Integer, row-parallel: one row of h per wavefront, four per workgroup; slot 0 is the gate
+// row, slot 1 the up row, four lane groups each. m <= 2 stages the job's vectors in LDS.
 template <int T, int MT>
 __global__ __launch_bounds__(256) void k_gateup_rp(const GUArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
+  constexpr bool ST = MT <= 2;
   GUJob J;
   if (!gu_job(a, st->m, J)) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1357,24 +1367,22 @@ __global__ __launch_bounds__(256) void k_gateup_rp(const GUArgs a, const StepRec
   const int r = blockIdx.x * 4 + wave;
   const bool valid = r < n_ff;
   const int64_t grow = (int64_t)J.expert * a.gate.rows + (valid ? r : n_ff - 1);
-  const Q8KP ly = ldsq_of(smem, MT, dim);
-  uint8_t *tile = smem + ldsq_bytes(MT, dim) + (size_t)wave * rp_wave_bytes(2, nb, MT);
+  const Q8KP ly = ST ? ldsq_of(smem, MT, dim) : a.y;
+  uint8_t *tile = smem + rp_act_bytes(MT, dim) + (size_t)wave * rp_wave_bytes(2, nb, MT);
   float *cb = reinterpret_cast<float *>(tile + (size_t)2 * nb * tile_bpb());
+  float *ov = cb + (size_t)2 * nb * MT * 10;
   tile_fetch<T>(tile, a.gate.pl, 2, nb, [&](int sl) -> int64_t { return sl == 0 ? grow : -1; });
   tile_fetch<T>(tile, a.up.pl, 2, nb, [&](int sl) -> int64_t { return sl == 1 ? grow : -1; });
-  stage_q8kp(ly, a.y, dim, J.nvec, 4, [&](int u) { return J.jv ? J.jv[u] : u; });
+  if (ST) stage_q8kp(ly, a.y, dim, J.nvec, 4, [&](int u) { return J.jv ? J.jv[u] : u; });
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  float res[MT];
   const int nv = J.nvec;
-  kq_rows_par<T, MT>(tile, 2, nb, 4, 2, [&](int) { return grow; }, [](int, int v) { return v; }, [&](int) { return nv; }, ly, cb, res);
-#pragma unroll
-  for (int v = 0; v < MT; v++) {
-    const float u = __shfl_down(res[v], 32);
-    if (lane == 0 && valid && v < nv) {
-      const float x = res[v];
-      st_dev(a.h + (int64_t)(J.jo ? J.jo[v] : v) * n_ff + r, x / (1.0f + expf(-x)) * u);
-    }
+  const int *jv = J.jv;
+  auto vid = [&](int, int v) { return ST || !jv ? v : jv[v]; };
+  kq_rows_par<T, MT>(tile, 2, nb, 4, 2, [&](int) { return grow; }, vid, [&](int) { return nv; }, ly, cb, ov);
+  if (lane < nv && valid) {
+    const float x = ov[lane], u = ov[MT + lane];
+    st_dev(a.h + (int64_t)(J.jo ? J.jo[lane] : lane) * n_ff + r, x / (1.0f + expf(-x)) * u);
   }
   if (a.hq.q) gateup_quant_tail(a, nv, J.jo, 4);
 }
@@ -1547,12 +1555,20 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
     return hipGetLastError();
   }
   if (mode == 1) {
-    if (mt > 2 || a.G < 1 || a.R < 1 || a.G * a.R > 8) return hipErrorInvalidValue;
-    const size_t sm = ldsq_bytes(mt, cols) + 4 * rp_wave_bytes(a.R, nb, mt);
-    if (mt == 1) { SPX_LDS(k_mvr<1>, sm); hipLaunchKernelGGL(k_mvr<1>, dim3(grid), dim3(256), sm, s, a, st); }
-    else { SPX_LDS(k_mvr<2>, sm); hipLaunchKernelGGL(k_mvr<2>, dim3(grid), dim3(256), sm, s, a, st); }
+    if (a.G < 1 || a.R < 1 || a.G * a.R > 8 || (a.G & (a.G - 1))) return hipErrorInvalidValue;
+    const size_t sm = rp_act_bytes(mt, cols) + 4 * rp_wave_bytes(a.R, nb, mt);
+#define SPX_MVR(MTV) do { SPX_LDS(k_mvr<MTV>, sm); hipLaunchKernelGGL(k_mvr<MTV>, dim3(grid), dim3(256), sm, s, a, st); } while (0)
+    switch (mt) {
+    case 1: SPX_MVR(1); break;
+    case 2: SPX_MVR(2); break;
+    case 4: SPX_MVR(4); break;
+    case 8: SPX_MVR(8); break;
+    default: SPX_MVR(16); break;
+    }
+#undef SPX_MVR
     return hipGetLastError();
   }
+  if (a.tail.nw) return hipErrorInvalidValue;  // tiles take no norm tail
   const size_t sm = (mt <= 2 ? ldsq_bytes(mt, cols) : 0) + (size_t)8 * nb * tile_bpb();
 #define SPX_MVT(MTV) do { SPX_LDS(k_mvt<MTV>, sm); hipLaunchKernelGGL(k_mvt<MTV>, dim3(grid), dim3(64), sm, s, a, st); } while (0)
   switch (mt) {
@@ -1606,13 +1622,11 @@ static hipError_t launch_gu_t(const GUArgs &a, int mode, const StepRec *st, int 
   const unsigned jobs = (unsigned)std::max(1, max_jobs);
   if constexpr (T == T_Q4K || T == T_Q6K) {
     const int dim = (int)a.gate.cols, nb = (int)a.gate.nb;
-    if constexpr (MT <= 2) {
-      if (mode == 1) {
-        const size_t sm = ldsq_bytes(MT, dim) + 4 * rp_wave_bytes(2, nb, MT);
-        SPX_LDS((k_gateup_rp<T, MT>), sm);
-        hipLaunchKernelGGL((k_gateup_rp<T, MT>), dim3((unsigned)((a.n_ff + 3) / 4), jobs), dim3(256), sm, s, a, st);
-        return hipGetLastError();
-      }
+    if (mode == 1) {
+      const size_t sm = rp_act_bytes(MT, dim) + 4 * rp_wave_bytes(2, nb, MT);
+      SPX_LDS((k_gateup_rp<T, MT>), sm);
+      hipLaunchKernelGGL((k_gateup_rp<T, MT>), dim3((unsigned)((a.n_ff + 3) / 4), jobs), dim3(256), sm, s, a, st);
+      return hipGetLastError();
     }
     const size_t sm = (MT <= 2 ? ldsq_bytes(MT, dim) : 0) + (size_t)4 * 8 * nb * tile_bpb();
     SPX_LDS((k_gateup_kq<T, MT>), sm);

@@ -526,7 +526,7 @@ int spx_engine_prepare(spx_engine *E) {
             (E->tail_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) &&
             (E->part_ml = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * 2)) &&
             (E->part_o = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * c.head_dim)) &&
-            (E->att_cnt = E->dalloc<int>((size_t)c.n_kv_heads * (1 + ATT_GMAX) * CNT_STRIDE)) && (E->rt_cnt = E->dalloc<int>(1)) &&
+            (E->att_cnt = E->dalloc<int>((size_t)c.n_kv_heads * ATT_QT * (1 + ATT_GMAX) * CNT_STRIDE)) && (E->rt_cnt = E->dalloc<int>(1)) &&
             (E->gu_cnt = E->dalloc<int>((size_t)nv * (nff / 256 + 1) * (1 + GU_SUB) * CNT_STRIDE)) && (E->chosen = E->dalloc<int>(16 * 32)) &&
             (E->nkeep = E->dalloc<int>(16)) && (E->weights = E->dalloc<float>(16 * 32)) && (E->jobs = E->dalloc<Job>(512)) &&
             (E->expert_count = E->dalloc<int>((size_t)c.n_layers * std::max(1, c.n_expert))) &&

@@ -7,7 +7,8 @@ namespace spx {
 
 constexpr int MAX_M = 16;       // rows per verify / prefill pass
 constexpr int ATT_QMAX = 128;   // query heads x rows per kv head in one pass (16 rows x 8)
-constexpr int ATT_GRP = 16;     // attention: 64-position chunks merged per group
+constexpr int ATT_QT = ATT_QMAX / 16;  // attention: 16-query tiles per kv head
+constexpr int ATT_GRP = 16;     // attention: chunks merged per group
 constexpr int ATT_GMAX = 16;    // attention: groups per kv head (max_seq <= 64 * 16 * 16)
 constexpr int NORM_NT = 16;     // norm tails handle dim <= 256 * NORM_NT
 constexpr int CNT_SUB = 64;     // first-level arrival counters of a two-level count
@@ -74,11 +75,11 @@ struct AttnArgs {
   __half *kc, *vc;                    // [n_layers][max_seq][kv_dim]
   float *part_ml;                     // [n_kv][nslot][ATT_QMAX][2] (running max, sum)
   float *part_o;                      // [n_kv][nslot][ATT_QMAX][hd] (unnormalised output)
-  int *counter;                       // [n_kv][1 + ATT_GMAX][CNT_STRIDE], zero between passes
+  int *counter;                       // [n_kv][ATT_QT][1 + ATT_GMAX][CNT_STRIDE], zero between passes
   float *att;                         // [m][q_dim]
   Q8KP aq;                            // permuted Q8_K of att (q null: not produced)
   int layer, max_seq, kv_dim, hd, n_heads, n_kv, neox;
-  int nch;                            // 64-position chunks launched per kv head (>= max_seq / 64)
+  int nch;                            // chunks launched per kv head (>= max_seq / 64)
   int nslot;                          // partial slots per kv head: nch chunks, then group partials
   float eps, scale;
 };

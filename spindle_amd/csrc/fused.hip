@@ -836,12 +836,17 @@ __global__ __launch_bounds__(256) void k_embed(TensorView e, const StepRec *st, 
 }
 
 // ------------------------------------------------------------------ attention
-// One workgroup per (position chunk, kv head): every row's query heads of the group (after
-// bias, per-head RMSNorm and RoPE, :3226-3248 / :3432-3448) against the chunk's K/V (f16
-// cache), causal per row (row b sees positions <= start + b), online softmax per 64-position
-// sub-chunk; the new K/V rows that fall in the chunk are normed/rotated and written to the
-// cache first. Each workgroup leaves (max, sum, unnormalised output) per query; the last one
-// to finish merges the chunks (flash-decoding) and writes the output, optionally as Q8_K.
+// One workgroup per (position chunk, kv head, tile of 16 query rows): the tile's query heads
+// (rows b of the pass x the kv group's heads, after bias, per-head RMSNorm and RoPE,
+// :3226-3248 / :3432-3448) against the chunk's K/V (f16 cache), causal per row (row b sees
+// positions <= start + b), online softmax over the chunk's 64-position sub-chunks. The new
+// K/V rows (positions start..start+m-1) are normed / rotated by every workgroup that needs
+// them (straight into its LDS tile) and written to the cache by the first query tile's.
+// Scores and P.V run on the matrix cores (v_mfma_f32_16x16x16_f16): K and V are f16 already;
+// queries and probabilities are split into two f16 parts (x = hi + lo, ~22 significant bits)
+// whose products accumulate in fp32. Each workgroup leaves (max, sum, unnormalised output) per
+// query; chunks are merged in two levels (flash-decoding, chunk order), the last merger of a
+// query tile writes its output, optionally as Q8_K.
 __device__ __forceinline__ void head_prep(const float *src, const float *bias, const float *nw, const float2 *rope_row, int hd, int neox,
                                           float eps, float &e0, float &e1) {
   const int lane = threadIdx.x & 63, half = hd >> 1;
@@ -864,256 +869,281 @@ __device__ __forceinline__ void head_prep(const float *src, const float *bias, c
   e1 = x1;
 }
 
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4v mfma16(h4v a, h4v b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+
+// x = hi + lo in f16 (hi = x rounded, lo = the rounded remainder)
+__device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo) {
+  hi = (_Float16)x;
+  lo = (_Float16)(x - (float)hi);
+}
+
+// Merges n <= 16 partials (running max m, sum l, unnormalised output o) in slots s0 .. s0+n-1
+// for the 16 queries qa .. qa+15 (< NQ): M = max m_c, w_c = exp(m_c - M), L = sum l_c w_c,
+// O = sum w_c o_c in slot order. Thread: query qa + tid / 16, dims (tid % 16) * HD/16 ... .
+// Writes the normalised O / L to LDS (ol, rows from qa) or the merged partial to slot dst.
+template <int HD>
+__device__ __forceinline__ void attn_merge16(rsrc_t r_ml, rsrc_t r_o, int s0, int n, int qa, int NQ, float *ol, const rsrc_t *d_ml,
+                                             const rsrc_t *d_o, int dst) {
+  constexpr int DW = HD / 16, NV = DW / 4;
+  const int tid = threadIdx.x, qi = qa + (tid >> 4), d0 = (tid & 15) * DW;
+  if (qi >= NQ) return;
+  f2v ml[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) ml[k] = k < n ? ld_coh2(r_ml, ((s0 + k) * ATT_QMAX + qi) * 8) : f2v{-INFINITY, 0.0f};
+  float M = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 16; k++) M = fmaxf(M, ml[k].x);
+  float w[16], L = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    w[k] = ml[k].x == -INFINITY ? 0.0f : expf(ml[k].x - M);
+    if (k < n) L = fmaf(ml[k].y, w[k], L);
+  }
+  float acc[DW];
+#pragma unroll
+  for (int j = 0; j < DW; j++) acc[j] = 0.0f;
+#pragma unroll
+  for (int k0 = 0; k0 < 16; k0 += 8) {
+    if (k0 < n) {
+      f4v ov[8][NV];
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+#pragma unroll
+        for (int v = 0; v < NV; v++)
+          ov[k][v] = ld_coh4(r_o, (((s0 + min(k0 + k, n - 1)) * ATT_QMAX + qi) * HD + d0 + 4 * v) * 4);
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        if (k0 + k < n) {
+#pragma unroll
+          for (int v = 0; v < NV; v++) {
+            acc[4 * v] = fmaf(ov[k][v].x, w[k0 + k], acc[4 * v]);
+            acc[4 * v + 1] = fmaf(ov[k][v].y, w[k0 + k], acc[4 * v + 1]);
+            acc[4 * v + 2] = fmaf(ov[k][v].z, w[k0 + k], acc[4 * v + 2]);
+            acc[4 * v + 3] = fmaf(ov[k][v].w, w[k0 + k], acc[4 * v + 3]);
+          }
+        }
+      }
+    }
+  }
+  if (ol) {
+    const float il = __fdiv_rn(1.0f, fmaxf(L, 1e-30f));
+#pragma unroll
+    for (int j = 0; j < DW; j++) ol[(qi - qa) * HD + d0 + j] = acc[j] * il;
+  } else {
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+      st_coh4(*d_o, ((dst * ATT_QMAX + qi) * HD + d0 + 4 * v) * 4, f4v{acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]});
+    if ((threadIdx.x & 15) == 0) st_coh2(*d_ml, (dst * ATT_QMAX + qi) * 8, f2v{M, L});
+  }
+}
+
 template <int NU>
-__device__ __forceinline__ void attn_load_kv(const AttnArgs &a, int64_t cache0, int s0, int p_hi, int pp, int d0, uint32_t (&kr)[4 * NU],
-                                             uint32_t (&vr)[4 * NU]) {
-  const int pos = min(s0 + pp, p_hi - 1);
-  const uint4 *kp = reinterpret_cast<const uint4 *>(a.kc + cache0 + (int64_t)pos * a.kv_dim + d0);
-  const uint4 *vp = reinterpret_cast<const uint4 *>(a.vc + cache0 + (int64_t)pos * a.kv_dim + d0);
+__device__ __forceinline__ void attn_kv_load(const AttnArgs &a, int64_t off, uint32_t (&kr)[4 * NU], uint32_t (&vr)[4 * NU]) {
+  const uint4 *kp = reinterpret_cast<const uint4 *>(a.kc + off), *vp = reinterpret_cast<const uint4 *>(a.vc + off);
 #pragma unroll
   for (int u = 0; u < NU; u++) {
-    const uint4 k4 = kp[u], v4 = vp[u];
-    kr[4 * u] = k4.x; kr[4 * u + 1] = k4.y; kr[4 * u + 2] = k4.z; kr[4 * u + 3] = k4.w;
-    vr[4 * u] = v4.x; vr[4 * u + 1] = v4.y; vr[4 * u + 2] = v4.z; vr[4 * u + 3] = v4.w;
+    const uint4 k = kp[u], v = vp[u];
+    kr[4 * u] = k.x; kr[4 * u + 1] = k.y; kr[4 * u + 2] = k.z; kr[4 * u + 3] = k.w;
+    vr[4 * u] = v.x; vr[4 * u + 1] = v.y; vr[4 * u + 2] = v.z; vr[4 * u + 3] = v.w;
   }
 }
 
-// Merges n online-softmax partials (running max m, sum l, unnormalised output o) in slots
-// s0 .. s0+n-1 for NQ queries: M = max m_c, w_c = exp(m_c - M), L = sum l_c w_c, O = sum w_c o_c
-// in slot order. Thread (query jq of each group of 8, dims dd0..dd0+DP-1) loads its own
-// inputs (one round of coherent loads). Writes either the normalised output O / L to LDS
-// (ol) or the merged partial (M, L, O) to slot `dst`.
-template <int HD, int DP, int NMAX>
-__device__ __forceinline__ void attn_merge(rsrc_t r_ml, rsrc_t r_o, int s0, int n, int NQ, int jq, int dd0, float *ol,
-                                           const rsrc_t *d_ml, const rsrc_t *d_o, int dst) {
-  for (int q0 = 0; q0 < NQ; q0 += 8) {
-    const int qi = q0 + jq;
-    if (qi >= NQ) continue;
-    f2v ml[NMAX];
-    f4v ov[NMAX];
-#pragma unroll
-    for (int k = 0; k < NMAX; k++) {
-      const int sc = s0 + min(k, n - 1);
-      ml[k] = ld_coh2(r_ml, (sc * ATT_QMAX + qi) * 8);
-      const int off = ((sc * ATT_QMAX + qi) * HD + dd0) * 4;
-      if constexpr (DP == 4) ov[k] = ld_coh4(r_o, off);
-      else { const f2v t2 = ld_coh2(r_o, off); ov[k] = f4v{t2.x, t2.y, 0.0f, 0.0f}; }
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < NMAX; k++) if (k < n) M = fmaxf(M, ml[k].x);
-    float L = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int k = 0; k < NMAX; k++) {
-      if (k < n) {
-        const float w = ml[k].x == -INFINITY ? 0.0f : expf(ml[k].x - M);
-        L = fmaf(ml[k].y, w, L);
-        acc[0] = fmaf(ov[k].x, w, acc[0]);
-        acc[1] = fmaf(ov[k].y, w, acc[1]);
-        if constexpr (DP == 4) { acc[2] = fmaf(ov[k].z, w, acc[2]); acc[3] = fmaf(ov[k].w, w, acc[3]); }
-      }
-    }
-    if (ol) {
-      const float il = __fdiv_rn(1.0f, fmaxf(L, 1e-30f));
-#pragma unroll
-      for (int d = 0; d < DP; d++) ol[qi * HD + dd0 + d] = acc[d] * il;
-    } else {
-      const int off = ((dst * ATT_QMAX + qi) * HD + dd0) * 4;
-      if constexpr (DP == 4) st_coh4(*d_o, off, f4v{acc[0], acc[1], acc[2], acc[3]});
-      else st_coh2(*d_o, off, f2v{acc[0], acc[1]});
-      if ((threadIdx.x & 31) == 0) st_coh2(*d_ml, (dst * ATT_QMAX + qi) * 8, f2v{M, L});
-    }
-  }
+// LDS of k_attn (strides in halves / floats, padded against bank conflicts)
+template <int HD> struct AttnLds {
+  static constexpr int QS = HD + 16, KS = HD + 16, VS = 64 + 16, PS = 64 + 16, SS = 64 + 4;
+  static constexpr size_t QB = (size_t)2 * 16 * QS * 2;  // qh, ql; later the merged output [16][HD] f32
+  static constexpr size_t BYTES = QB + (size_t)64 * KS * 2 + (size_t)HD * VS * 2 + (size_t)16 * SS * 4 + (size_t)2 * 16 * PS * 2 + 3 * 16 * 4;
+  static_assert(QB >= (size_t)16 * HD * 4, "merged output fits over the queries");
+};
+
+// Sub-chunks per chunk: one when one query tile covers the pass (decode: most chunks, most
+// parallelism); otherwise enough that a kv head has at most 16 chunks (one merge level).
+__host__ __device__ inline int attn_sub(int nq, int total) {
+  const int nsc = (total + 63) >> 6;
+  return nq <= 16 ? 1 : (nsc + 15) / 16;
 }
 
-template <int HD, int NGM>
+template <int HD>
 __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
-  constexpr int KS = HD + 8;          // padded K/V row (halves) in LDS
-  constexpr int DQ = HD / 4;          // dims per quarter (score phase)
-  constexpr int NU = DQ / 8;          // 16-byte pieces per quarter
-  constexpr int DP = HD / 32;         // dims per thread (PV phase)
-  const int h = blockIdx.y, c = blockIdx.x;
+  using LY = AttnLds<HD>;
+  constexpr int QS = LY::QS, KS = LY::KS, VS = LY::VS, PS = LY::PS, SS = LY::SS;
+  constexpr int DT = HD / 16, TPW = DT / 4;  // 16-dim output tiles, per wavefront
+  constexpr int DQ = HD / 4, NU = DQ / 8;    // K/V loader: dims per thread, 16-byte pieces
+  const int h = blockIdx.y, c = blockIdx.x, qt = blockIdx.z;
   const int m = st->m, start = st->start, total = start + m;
-  const int g = a.n_heads / a.n_kv, NQ = m * g, NG = (NQ + 7) >> 3;
-  // chunk c = positions [64c, 64c + 64): fixed boundaries, so a row's partials (and the merge
-  // below) do not depend on how many rows the pass has or where it starts
-  const int nch = (total + 63) >> 6;
+  const int g = a.n_heads / a.n_kv, NQ = m * g, qa = qt * 16;
+  if (qa >= NQ) return;
+  const int SUB = attn_sub(NQ, total), CS = 64 * SUB, nch = (total + CS - 1) / CS;
   if (c >= nch) return;
-  const int p_lo = c * 64, p_hi = min(p_lo + 64, total);
+  const int p_lo = c * CS, p_hi = min(p_lo + CS, total);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  float *qs = reinterpret_cast<float *>(smem);                // [NQ][HD] queries, later the merged output
-  __half *ks = reinterpret_cast<__half *>(qs + NQ * HD);      // [64][KS]
-  __half *vs = ks + 64 * KS;                                  // [64][KS]
-  float *ps = reinterpret_cast<float *>(vs + 64 * KS);        // [8][64]
-  float *sm = ps + 8 * 64, *sl = sm + ATT_QMAX, *sa = sl + ATT_QMAX;  // running max, sum; group alpha [8]
+  _Float16 *qh = reinterpret_cast<_Float16 *>(smem);            // [16][QS]
+  _Float16 *ql = qh + 16 * QS;                                   // [16][QS]
+  _Float16 *ks = reinterpret_cast<_Float16 *>(smem + LY::QB);    // [64][KS]
+  _Float16 *vt = ks + 64 * KS;                                   // [HD][VS] (V transposed)
+  float *ss = reinterpret_cast<float *>(vt + HD * VS);           // [16][SS] scores
+  _Float16 *ph = reinterpret_cast<_Float16 *>(ss + 16 * SS);     // [16][PS]
+  _Float16 *pl = ph + 16 * PS;                                   // [16][PS]
+  float *rm = reinterpret_cast<float *>(pl + 16 * PS), *rl = rm + 16, *sa = rl + 16;  // running max, sum; rescale
   const int64_t cache0 = (int64_t)a.layer * a.max_seq * a.kv_dim + (int64_t)h * HD;
   const int half = HD / 2;
-
-  // 1. queries -> LDS; new K/V rows of this chunk -> cache
   const int da = a.neox ? lane : 2 * lane, db = a.neox ? lane + half : 2 * lane + 1;
-  for (int qi = wave; qi < NQ; qi += 4) {
-    const int b = qi / g, head = h * g + qi % g;
-    float e0, e1;
-    head_prep(a.q + (int64_t)b * a.n_heads * HD + head * HD, a.q_bias ? a.q_bias + head * HD : nullptr, a.q_norm,
-              a.rope + (int64_t)(start + b) * half, HD, a.neox, a.eps, e0, e1);
-    if (lane < half) { qs[qi * HD + da] = e0; qs[qi * HD + db] = e1; }
-  }
-  for (int b = wave; b < m; b += 4) {
-    const int pos = start + b;
-    if (pos < p_lo || pos >= p_hi) continue;
-    float e0, e1;
-    head_prep(a.k + (int64_t)b * a.kv_dim + h * HD, a.k_bias ? a.k_bias + h * HD : nullptr, a.k_norm,
-              a.rope + (int64_t)pos * half, HD, a.neox, a.eps, e0, e1);
-    __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim;
-    if (lane < half) { kd[da] = __float2half_rn(e0); kd[db] = __float2half_rn(e1); }
-    head_prep(a.v + (int64_t)b * a.kv_dim + h * HD, a.v_bias ? a.v_bias + h * HD : nullptr, nullptr, nullptr, HD, a.neox, a.eps, e0, e1);
-    __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim;
-    if (lane < half) { vd[da] = __float2half_rn(e0); vd[db] = __float2half_rn(e1); }
-  }
-  for (int i = tid; i < NQ; i += 256) { sm[i] = -INFINITY; sl[i] = 0.0f; }
-  __syncthreads();  // the new K/V rows are visible to this workgroup's loads
+  const int ar = lane & 15, kg = (lane >> 4) * 4;  // MFMA operand row / column, k offset
 
-  // 2. sub-chunks of 64 positions. Loader: position lp = tid / 4, quarter lq = tid % 4.
-  // Scores: query jq = tid / 32, position group sg = (tid / 4) % 8 (positions sg + 8k), quarter qq.
-  // PV: query jq, dims dd0 .. dd0 + DP.
+  // K/V of the first sub-chunk in flight while the queries are prepared
   const int lp = tid >> 2, lq = tid & 3;
-  const int jq = tid >> 5, sg = (tid >> 2) & 7, qq = tid & 3, dd0 = (tid & 31) * DP;
   uint32_t kr[4 * NU], vr[4 * NU];
-  attn_load_kv<NU>(a, cache0, p_lo, p_hi, lp, lq * DQ, kr, vr);
-  float o[NGM][DP];
-#pragma unroll
-  for (int G = 0; G < NGM; G++)
-#pragma unroll
-    for (int d = 0; d < DP; d++) o[G][d] = 0.0f;
-  for (int s0 = p_lo; s0 < p_hi; s0 += 64) {
-    __syncthreads();  // previous sub-chunk is done with ks / vs / ps
-#pragma unroll
-    for (int u = 0; u < NU; u++) {
-      reinterpret_cast<uint4 *>(ks + lp * KS + lq * DQ)[u] = make_uint4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
-      reinterpret_cast<uint4 *>(vs + lp * KS + lq * DQ)[u] = make_uint4(vr[4 * u], vr[4 * u + 1], vr[4 * u + 2], vr[4 * u + 3]);
+  attn_kv_load<NU>(a, cache0 + (int64_t)min(p_lo + lp, p_hi - 1) * a.kv_dim + lq * DQ, kr, vr);
+  // queries of this tile -> LDS as hi / lo f16 (rows past NQ are zero)
+  for (int r = wave; r < 16; r += 4) {
+    const int qi = qa + r;
+    float e0 = 0.0f, e1 = 0.0f;
+    if (qi < NQ) {
+      const int b = qi / g, head = h * g + qi % g;
+      head_prep(a.q + (int64_t)b * a.n_heads * HD + head * HD, a.q_bias ? a.q_bias + head * HD : nullptr, a.q_norm,
+                a.rope + (int64_t)(start + b) * half, HD, a.neox, a.eps, e0, e1);
     }
-    attn_load_kv<NU>(a, cache0, s0 + 64, p_hi, lp, lq * DQ, kr, vr);  // next sub-chunk (clamped rows past the end)
+    if (lane < half) {
+      split_f16(e0, qh[r * QS + da], ql[r * QS + da]);
+      split_f16(e1, qh[r * QS + db], ql[r * QS + db]);
+    }
+  }
+  if (tid < 16) { rm[tid] = -INFINITY; rl[tid] = 0.0f; }
+  f4v acc[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; j++) acc[j] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int s0 = p_lo; s0 < p_hi; s0 += 64) {
+    __syncthreads();  // the previous sub-chunk is done with ks / vt / ph / pl
+    // cached rows -> LDS (K row-major, V transposed); rows of this pass come from below; rows
+    // past the pass are zero (their probabilities are zero, and 0 * V must stay 0)
+    if (s0 + lp >= total) {
+#pragma unroll
+      for (int t = 0; t < 4 * NU; t++) { kr[t] = 0u; vr[t] = 0u; }
+    }
+    if (s0 + lp < start || s0 + lp >= total) {
+      uint16_t *vt16 = reinterpret_cast<uint16_t *>(vt);
+#pragma unroll
+      for (int u = 0; u < NU; u++) reinterpret_cast<uint4 *>(ks + lp * KS + lq * DQ)[u] = make_uint4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
+#pragma unroll
+      for (int t = 0; t < 4 * NU; t++) {
+        vt16[(lq * DQ + 2 * t) * VS + lp] = (uint16_t)(vr[t] & 0xffffu);
+        vt16[(lq * DQ + 2 * t + 1) * VS + lp] = (uint16_t)(vr[t] >> 16);
+      }
+    }
+    if (s0 + 64 < p_hi) attn_kv_load<NU>(a, cache0 + (int64_t)min(s0 + 64 + lp, p_hi - 1) * a.kv_dim + lq * DQ, kr, vr);
+    // this pass's K/V rows in the sub-chunk: normed / rotated here, to the cache by tile 0
+    for (int b = wave; b < m; b += 4) {
+      const int pos = start + b, pp = pos - s0;
+      if (pp < 0 || pp >= 64 || pos >= p_hi) continue;
+      float e0, e1;
+      head_prep(a.k + (int64_t)b * a.kv_dim + h * HD, a.k_bias ? a.k_bias + h * HD : nullptr, a.k_norm,
+                a.rope + (int64_t)pos * half, HD, a.neox, a.eps, e0, e1);
+      if (lane < half) {
+        const __half k0 = __float2half_rn(e0), k1 = __float2half_rn(e1);
+        ks[pp * KS + da] = (_Float16)__half2float(k0);
+        ks[pp * KS + db] = (_Float16)__half2float(k1);
+        if (qt == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
+      }
+      head_prep(a.v + (int64_t)b * a.kv_dim + h * HD, a.v_bias ? a.v_bias + h * HD : nullptr, nullptr, nullptr, HD, a.neox, a.eps, e0, e1);
+      if (lane < half) {
+        const __half v0 = __float2half_rn(e0), v1 = __float2half_rn(e1);
+        vt[da * VS + pp] = (_Float16)__half2float(v0);
+        vt[db * VS + pp] = (_Float16)__half2float(v1);
+        if (qt == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
+      }
+    }
     __syncthreads();
+    // scores S = Q K^T, wavefront w: positions 16w .. 16w+15
+    {
+      f4v sacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int G = 0; G < NGM; G++) {
-      if (G < NG) {
-        // scores: this thread's query quarter in registers against 8 positions' K quarters
-        const int qi = 8 * G + jq;
-        float qv[DQ];
+      for (int kt = 0; kt < DT; kt++) {
+        const h4v bk = *reinterpret_cast<const h4v *>(ks + (wave * 16 + ar) * KS + kt * 16 + kg);
+        const h4v ahi = *reinterpret_cast<const h4v *>(qh + ar * QS + kt * 16 + kg);
+        const h4v alo = *reinterpret_cast<const h4v *>(ql + ar * QS + kt * 16 + kg);
+        sacc = mfma16(ahi, bk, sacc);
+        sacc = mfma16(alo, bk, sacc);
+      }
 #pragma unroll
-        for (int u = 0; u < DQ / 4; u++) {
-          const float4 x = qi < NQ ? reinterpret_cast<const float4 *>(qs + qi * HD + qq * DQ)[u] : make_float4(0.f, 0.f, 0.f, 0.f);
-          qv[4 * u] = x.x; qv[4 * u + 1] = x.y; qv[4 * u + 2] = x.z; qv[4 * u + 3] = x.w;
-        }
+      for (int r = 0; r < 4; r++) ss[(kg + r) * SS + wave * 16 + ar] = sacc[r];
+    }
+    __syncthreads();
+    // online softmax, wavefront w: query rows 4w .. 4w+3, lane = position
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-          const int pp = sg + 8 * k;
-          const uint4 *kp = reinterpret_cast<const uint4 *>(ks + pp * KS + qq * DQ);
-          float sdot = 0.0f;
+    for (int r4 = 0; r4 < 4; r4++) {
+      const int row = wave * 4 + r4, qi = qa + row, pos = s0 + lane;
+      const float sv = qi < NQ && pos < p_hi && pos <= start + qi / g ? ss[row * SS + lane] * a.scale : -INFINITY;
+      const float mx = wave_max(sv);
+      const float m_old = rm[row], m_new = fmaxf(m_old, mx);
+      const float pv = (sv == -INFINITY || m_new == -INFINITY) ? 0.0f : expf(sv - m_new);
+      const float ls = wave_sum(pv);
+      const float alpha = m_new == -INFINITY ? 1.0f : (m_old == -INFINITY ? 0.0f : expf(m_old - m_new));
+      split_f16(pv, ph[row * PS + lane], pl[row * PS + lane]);
+      if (lane == 0) { rm[row] = m_new; rl[row] = rl[row] * alpha + ls; sa[row] = alpha; }
+    }
+    __syncthreads();
+    // O = O * alpha + P V, wavefront w: dim tiles w*TPW .. w*TPW + TPW-1
 #pragma unroll
-          for (int u = 0; u < NU; u++) {
-            const uint4 w = kp[u];
-            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    for (int j = 0; j < TPW; j++) {
+      const int dt = wave * TPW + j;
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-              sdot = fmaf(qv[8 * u + 2 * t], h2f(ww[t]), sdot);
-              sdot = fmaf(qv[8 * u + 2 * t + 1], h2f(ww[t] >> 16), sdot);
-            }
-          }
-          sdot = sdot + quad_xor1f(sdot);
-          sdot = sdot + quad_xor2f(sdot);
-          const int pos = s0 + pp;
-          if (qq == 0) {
-            const bool ok = qi < NQ && pos < p_hi && pos <= start + qi / g;
-            ps[jq * 64 + pp] = ok ? sdot * a.scale : -INFINITY;
-          }
-        }
-        __syncthreads();
-        // online-softmax update: wave w takes queries w and w + 4 of the group; lane = position
+      for (int r = 0; r < 4; r++) acc[j][r] *= sa[kg + r];
 #pragma unroll
-        for (int r = 0; r < 2; r++) {
-          const int j = wave + 4 * r, qj = 8 * G + j;
-          if (qj < NQ) {
-            const float sv = ps[j * 64 + lane];
-            const float mx = wave_max(sv);
-            const float m_old = sm[qj];
-            const float m_new = fmaxf(m_old, mx);
-            const float p = (sv == -INFINITY || m_new == -INFINITY) ? 0.0f : expf(sv - m_new);
-            const float lsum = wave_sum(p);
-            const float alpha = m_new == -INFINITY ? 1.0f : (m_old == -INFINITY ? 0.0f : expf(m_old - m_new));
-            ps[j * 64 + lane] = p;
-            if (lane == 0) { sm[qj] = m_new; sl[qj] = sl[qj] * alpha + lsum; sa[j] = alpha; }
-          }
-        }
-        __syncthreads();
-        // o = o * alpha + sum_p p * v
-        if (qi < NQ) {
-          const float al = sa[jq];
-#pragma unroll
-          for (int d = 0; d < DP; d++) o[G][d] *= al;
-          const float *pr = ps + jq * 64;
-#pragma unroll 8
-          for (int t = 0; t < 64; t++) {
-            const float pv = pr[t];
-            if constexpr (DP == 4) {
-              const uint2 vv = *reinterpret_cast<const uint2 *>(vs + t * KS + dd0);
-              o[G][0] = fmaf(pv, h2f(vv.x), o[G][0]);
-              o[G][1] = fmaf(pv, h2f(vv.x >> 16), o[G][1]);
-              o[G][2] = fmaf(pv, h2f(vv.y), o[G][2]);
-              o[G][3] = fmaf(pv, h2f(vv.y >> 16), o[G][3]);
-            } else {
-              const uint32_t vv = *reinterpret_cast<const uint32_t *>(vs + t * KS + dd0);
-              o[G][0] = fmaf(pv, h2f(vv), o[G][0]);
-              o[G][1] = fmaf(pv, h2f(vv >> 16), o[G][1]);
-            }
-          }
-        }
-        __syncthreads();
+      for (int kt = 0; kt < 4; kt++) {
+        const h4v bv = *reinterpret_cast<const h4v *>(vt + (dt * 16 + ar) * VS + kt * 16 + kg);
+        const h4v ahi = *reinterpret_cast<const h4v *>(ph + ar * PS + kt * 16 + kg);
+        const h4v alo = *reinterpret_cast<const h4v *>(pl + ar * PS + kt * 16 + kg);
+        acc[j] = mfma16(ahi, bv, acc[j]);
+        acc[j] = mfma16(alo, bv, acc[j]);
       }
     }
   }
+  __syncthreads();
 
-  // 3. partials (coherent stores); the last chunk of each group of ATT_GRP chunks merges the
-  // group, the last group merger of the kv head merges the groups (chunk / group order)
+  // partials (coherent stores): O from the accumulators, (max, sum) per query
   const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nslot) * ATT_QMAX * 2);
   const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nslot) * ATT_QMAX * HD);
 #pragma unroll
-  for (int G = 0; G < NGM; G++) {
-    const int qi = 8 * G + jq;
-    if (G < NG && qi < NQ) {
-      const int off = ((c * ATT_QMAX + qi) * HD + dd0) * 4;
-      if (DP == 4) st_coh4(r_o, off, f4v{o[G][0], o[G][1], o[G][2], o[G][3]});
-      else st_coh2(r_o, off, f2v{o[G][0], o[G][1]});
-      if ((tid & 31) == 0) st_coh2(r_ml, (c * ATT_QMAX + qi) * 8, f2v{sm[qi], sl[qi]});
+  for (int j = 0; j < TPW; j++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int qi = qa + kg + r;
+      if (qi < NQ) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(acc[j][r]), r_o, ((c * ATT_QMAX + qi) * HD + (wave * TPW + j) * 16 + ar) * 4, 0, 16);
     }
-  }
+  if (tid < 16 && qa + tid < NQ) st_coh2(r_ml, (c * ATT_QMAX + qa + tid) * 8, f2v{rm[tid], rl[tid]});
+
+  // merges of this query tile: the last chunk of each group of ATT_GRP chunks merges the
+  // group, the last group merger merges the groups (chunk / group order)
   const int grp = c / ATT_GRP, ngrp = (nch + ATT_GRP - 1) / ATT_GRP, gcnt = min(ATT_GRP, nch - grp * ATT_GRP);
-  int *hcnt = a.counter + (int64_t)h * (1 + ATT_GMAX) * CNT_STRIDE;
+  int *hcnt = a.counter + ((int64_t)h * ATT_QT + qt) * (1 + ATT_GMAX) * CNT_STRIDE;
   if (arrive(hcnt + (1 + grp) * CNT_STRIDE) != gcnt - 1) return;
   if (tid == 0) hcnt[(1 + grp) * CNT_STRIDE] = 0;
-  float *ol = qs;  // merged output [NQ][HD] = rows b, then this group's heads
+  float *ol = reinterpret_cast<float *>(smem);  // merged output [16][HD] of the tile's queries
   if (ngrp == 1) {
-    attn_merge<HD, DP, ATT_GRP>(r_ml, r_o, 0, gcnt, NQ, jq, dd0, ol, nullptr, nullptr, 0);
+    attn_merge16<HD>(r_ml, r_o, 0, gcnt, qa, NQ, ol, nullptr, nullptr, 0);
   } else {
-    // group partial -> slot a.nch + grp
-    attn_merge<HD, DP, ATT_GRP>(r_ml, r_o, grp * ATT_GRP, gcnt, NQ, jq, dd0, nullptr, &r_ml, &r_o, a.nch + grp);
+    attn_merge16<HD>(r_ml, r_o, grp * ATT_GRP, gcnt, qa, NQ, nullptr, &r_ml, &r_o, a.nch + grp);  // -> slot a.nch + grp
     if (arrive(hcnt) != ngrp - 1) return;
     if (tid == 0) hcnt[0] = 0;
-    attn_merge<HD, DP, ATT_GMAX>(r_ml, r_o, a.nch, ngrp, NQ, jq, dd0, ol, nullptr, nullptr, 0);
+    attn_merge16<HD>(r_ml, r_o, a.nch, ngrp, qa, NQ, ol, nullptr, nullptr, 0);
   }
   __syncthreads();
-  for (int i = tid; i < NQ * HD; i += 256) {
-    const int qi = i / HD, d = i - qi * HD, b = qi / g, head = h * g + qi % g;
+  const int nrow = min(16, NQ - qa);
+  for (int i = tid; i < nrow * HD; i += 256) {
+    const int qi = qa + i / HD, d = i % HD, b = qi / g, head = h * g + qi % g;
     a.att[(int64_t)b * a.n_heads * HD + head * HD + d] = ol[i];
   }
-  if (a.aq.q) {
-    const int gw = g * HD, nbq = gw / 256, qdim = a.n_heads * HD, nbr = qdim / 256;
-    for (int it = wave; it < m * nbq; it += 4) {
-      const int b = it / nbq, kb = it % nbq;
-      const float4 xv = reinterpret_cast<const float4 *>(ol + b * gw + kb * 256)[lane];
+  if (a.aq.q) {  // 256-value blocks of att rows: (256 / HD) consecutive queries of the tile
+    const int qpb = 256 / HD, nbr = a.n_heads * HD / 256;
+    for (int j = wave; j < nrow / qpb; j += 4) {
+      const int q0 = qa + j * qpb, b = q0 / g, head = h * g + q0 % g;
+      const float4 xv = reinterpret_cast<const float4 *>(ol + j * 256)[lane];
       const float am = wave_max(amax4(xv));
-      const int64_t vb = (int64_t)b * nbr + (h * gw) / 256 + kb;
+      const int64_t vb = (int64_t)b * nbr + head * HD / 256;
       q8k_block_store(xv, am, a.aq.q + vb * 64, a.aq.d + vb, reinterpret_cast<int *>(a.aq.bs + vb * 8));
     }
   }
@@ -1582,27 +1612,19 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
   return hipGetLastError();
 }
 
-static size_t attn_smem(const AttnArgs &a, int m) {
-  const int g = a.n_heads / a.n_kv, nq = m * g;
-  return (size_t)nq * a.hd * 4 + 2 * 64 * (a.hd + 8) * 2 + 8 * 64 * 4 + (2 * ATT_QMAX + 8) * 4 + 16;
-}
-
-template <int HD, int NGM>
-static void launch_attn_t(const AttnArgs &a, const StepRec *st, size_t sm, hipStream_t s) {
-  SPX_LDS((k_attn<HD, NGM>), sm);
-  hipLaunchKernelGGL((k_attn<HD, NGM>), dim3(a.nch, a.n_kv), dim3(256), sm, s, a, st);
+template <int HD>
+static void launch_attn_t(const AttnArgs &a, int nqt, const StepRec *st, hipStream_t s) {
+  const size_t sm = AttnLds<HD>::BYTES;
+  SPX_LDS((k_attn<HD>), sm);
+  hipLaunchKernelGGL((k_attn<HD>), dim3(a.nch, a.n_kv, nqt), dim3(256), sm, s, a, st);
 }
 
 hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
-  const size_t sm = attn_smem(a, m);
-  const int nq = m * (a.n_heads / a.n_kv);
-  if (a.hd == 128) {
-    if (nq <= 8) launch_attn_t<128, 1>(a, st, sm, s); else launch_attn_t<128, ATT_QMAX / 8>(a, st, sm, s);
-  } else if (a.hd == 64) {
-    if (nq <= 8) launch_attn_t<64, 1>(a, st, sm, s); else launch_attn_t<64, ATT_QMAX / 8>(a, st, sm, s);
-  } else {
-    return hipErrorInvalidValue;
-  }
+  const int nqt = (m * (a.n_heads / a.n_kv) + 15) / 16;
+  if (nqt > ATT_QT) return hipErrorInvalidValue;
+  if (a.hd == 128) launch_attn_t<128>(a, nqt, st, s);
+  else if (a.hd == 64) launch_attn_t<64>(a, nqt, st, s);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

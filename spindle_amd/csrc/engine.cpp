@@ -57,7 +57,7 @@ struct spx_engine {
   spx_ctx *ctx = nullptr;
   spx_model_config c{};
   int q_dim = 0, kv_dim = 0, n_ff = 0, nch = 1, lm_grid = 2048, nbest = 1;
-  int mv_mode = -1, lm_mode = -1, tail_max = 2;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX)
+  int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
   std::map<std::string, int64_t> vec_len;
@@ -299,14 +299,14 @@ int enqueue_forward(spx_engine *E, int m) {
         ra.expert_count = E->expert_count + (size_t)l * ne;
         SPX_HIP(launch_router(ra, m, E->st_dev, s));
       }
-      const int max_jobs = std::min(ne, m * nu);
+      const int max_gu_jobs = std::min(256, m * nu);  // jobs of at most GU_USERS users
       {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up), l, true);  // one expert's slabs
         GUArgs ga{};
         ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.x = E->xn2;
-        ga.jobs = E->jobs; ga.njobs = ly.njobs; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
+        ga.jobs = E->jobs; ga.njobs = ly.njobs + 1; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
         if (d_int) ga.hq = E->hq;
-        SPX_HIP(launch_gateup(ga, m, gmode, E->st_dev, max_jobs, s));
+        SPX_HIP(launch_gateup(ga, std::min(m, GU_USERS), mode_of(E, ly.gate, m), E->st_dev, max_gu_jobs, s));
       }
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
@@ -314,7 +314,7 @@ int enqueue_forward(spx_engine *E, int m) {
         da.w = ly.down->v; da.y = E->hq; da.x = E->h; da.jobs = E->jobs + 256; da.njobs = ly.njobs; da.weights = E->weights;
         da.nkeep = E->nkeep; da.n_used = nu; da.out = E->ffn;
         if (tails) da.tail = tn;
-        SPX_HIP(launch_down(da, m, 0, E->st_dev, s));
+        SPX_HIP(launch_down(da, m, m > 2 && d_int && E->down_mode == 1 ? 1 : 0, E->st_dev, s));
       }
       if (!tails) { ProfScope ps(E, PC_NORM, 0); SPX_HIP(launch_norm(tn, E->st_dev, m, s)); }
     } else {  // ffn_forward / ffn_forward_multi (:590-646): k = 1, w = 1
@@ -404,6 +404,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   if (const char *v = std::getenv("SPX_MV_MODE")) E->mv_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_LM_MODE")) E->lm_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_TAIL_MAX")) E->tail_max = std::max(0, std::min(MAX_M, atoi(v)));
+  if (const char *v = std::getenv("SPX_DOWN_MODE")) E->down_mode = std::max(0, std::min(1, atoi(v)));
   *out = E;
   return 0;
 }
@@ -526,7 +527,7 @@ int spx_engine_prepare(spx_engine *E) {
             (E->tail_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) &&
             (E->part_ml = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * 2)) &&
             (E->part_o = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * c.head_dim)) &&
-            (E->att_cnt = E->dalloc<int>((size_t)c.n_kv_heads * ATT_QT * (1 + ATT_GMAX) * CNT_STRIDE)) && (E->rt_cnt = E->dalloc<int>(1)) &&
+            (E->att_cnt = E->dalloc<int>((size_t)c.n_kv_heads * ATT_QT * (1 + ATT_GMAX) * CNT_STRIDE)) && (E->rt_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) &&
             (E->gu_cnt = E->dalloc<int>((size_t)nv * (nff / 256 + 1) * (1 + GU_SUB) * CNT_STRIDE)) && (E->chosen = E->dalloc<int>(16 * 32)) &&
             (E->nkeep = E->dalloc<int>(16)) && (E->weights = E->dalloc<float>(16 * 32)) && (E->jobs = E->dalloc<Job>(512)) &&
             (E->expert_count = E->dalloc<int>((size_t)c.n_layers * std::max(1, c.n_expert))) &&
@@ -534,7 +535,7 @@ int spx_engine_prepare(spx_engine *E) {
             E->q8alloc(E->xq, M, ((c.dim + 255) / 256) * 256) && E->q8alloc(E->hq, nv, nff);
   if (!ok) return fail("spx_engine_prepare: out of device memory");
   for (auto &ly : E->L)
-    if (ly.moe && !(ly.njobs = E->dalloc<int>(1))) return fail("out of device memory");
+    if (ly.moe && !(ly.njobs = E->dalloc<int>(2))) return fail("out of device memory");
   SPX_HIP(hipHostMalloc(&E->st_host, sizeof(StepRec)));
   // RoPE table: inv_freq = 1/theta^(2i/hd) (Rope::new :1399-1402); angle = pos * inv_freq.
   const int half = c.head_dim / 2;

@@ -14,6 +14,7 @@ constexpr int NORM_NT = 16;     // norm tails handle dim <= 256 * NORM_NT
 constexpr int CNT_SUB = 64;     // first-level arrival counters of a two-level count
 constexpr int CNT_STRIDE = 32;  // ints between counters (own 128-byte line each)
 constexpr int GU_SUB = 8;       // first-level counters per 256-row block of h (gate/up Q8_K tail)
+constexpr int GU_USERS = 2;     // users per gate/up job (an expert's users split over jobs)
 
 // Device-side step record: the token rows of this pass and where they go in the KV cache.
 struct StepRec {
@@ -98,12 +99,12 @@ struct RouterArgs {
   float *logits;                      // [m][n_expert]
   int n_expert, n_used, norm, dim;
   float moe_prune;
-  int *counter;                       // zero between passes
+  int *counter;                       // (1 + CNT_SUB) * CNT_STRIDE ints, zero between passes
   int *chosen;                        // [16][32]
   float *weights;                     // [16][32]
   int *nkeep;                         // [16]
-  Job *jobs;                          // gate/up jobs [256], then down jobs [256]
-  int *njobs;
+  Job *jobs;                          // gate/up jobs [256] (<= GU_USERS users), then down jobs [256]
+  int *njobs;                         // [2]: down jobs (= distinct experts), gate/up jobs
   int *expert_count;                  // optional [n_expert] selection counter
 };
 

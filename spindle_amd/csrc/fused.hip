@@ -1150,69 +1150,81 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
 }
 
 // ------------------------------------------------------------------ MoE router + routing
-// F32 router rows (one per wavefront; lane j holds float4s j, j+64, ... of the row in
-// registers, each vector's dot is the lane's fma chain then the wave tree: a fixed order
-// for every batch size, like matvec_multi's per-vector F32 path :455-464), then the last
-// workgroup routes, a wavefront per row: softmax (max, exp, sum, divide), top-n_used by
+// F32 router rows (one per workgroup; wavefront w, lane j hold float4s w*64 + j + 256k of the
+// row in registers; each vector's dot is the lane's fma chain, the wave tree, then the four
+// wavefronts in order: a fixed order for every batch size, like matvec_multi's per-vector F32
+// path :455-464), then the last workgroup routes, a wavefront per row: softmax (max, exp, sum, divide), top-n_used by
 // probability (ties to the lower expert index), pruning (moe_prune >= 1: keep
 // clamp(x, max(2, n/2), n); < 1: mass rule), weights p / sum(kept) when normalised
 // (:1199-1239, :959-997), and the grouped job lists over the union of chosen experts in
 // expert order, users in (row, slot) order (:982-986).
 template <int MT>
 __global__ __launch_bounds__(256) void k_router(const RouterArgs a, const StepRec *st) {
+  __shared__ float part[4][MAX_M];
   const int m = st->m, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int dim = a.dim, n4 = dim >> 2;
-  constexpr int G = MT < 4 ? MT : 4;
-  const int row = blockIdx.x * 4 + wave;
-  const bool valid = row < a.n_expert;
-  const float4 *wr = reinterpret_cast<const float4 *>(a.w.pl.p0 + (int64_t)(valid ? row : 0) * dim * 4);
+  const int dim = a.dim, n4 = dim >> 2, row = blockIdx.x;
+  constexpr int NK = NORM_NT / 4;  // float4s per lane: wave w, lane j take float4s w*64 + j + 256k
+  const float4 *wr = reinterpret_cast<const float4 *>(a.w.pl.p0 + (int64_t)row * dim * 4);
   const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
-  float4 wv[NORM_NT];
+  float4 wv[NK];
 #pragma unroll
-  for (int k = 0; k < NORM_NT; k++) {
-    const int f = lane + 64 * k;
+  for (int k = 0; k < NK; k++) {
+    const int f = wave * 64 + lane + 256 * k;
     wv[k] = f < n4 ? wr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  for (int v0 = 0; v0 < m; v0 += G) {
-    const int nv = min(G, m - v0);
-    float part[G];
+  for (int v0 = 0; v0 < m; v0 += MT) {
+    float pv[MT];
 #pragma unroll
-    for (int v = 0; v < G; v++) part[v] = 0.0f;
+    for (int v = 0; v < MT; v++) {
+      pv[v] = 0.0f;
+      if (v0 + v < m) {
 #pragma unroll
-    for (int k = 0; k < NORM_NT; k++) {
-      const int f = lane + 64 * k;
-      if (f < n4) {
-#pragma unroll
-        for (int v = 0; v < G; v++) {
-          if (v < nv) {
+        for (int k = 0; k < NK; k++) {
+          const int f = wave * 64 + lane + 256 * k;
+          if (f < n4) {
             const float4 x = x4[(int64_t)(v0 + v) * n4 + f];
-            part[v] = fmaf(wv[k].x, x.x, part[v]);
-            part[v] = fmaf(wv[k].y, x.y, part[v]);
-            part[v] = fmaf(wv[k].z, x.z, part[v]);
-            part[v] = fmaf(wv[k].w, x.w, part[v]);
+            pv[v] = fmaf(wv[k].x, x.x, pv[v]);
+            pv[v] = fmaf(wv[k].y, x.y, pv[v]);
+            pv[v] = fmaf(wv[k].z, x.z, pv[v]);
+            pv[v] = fmaf(wv[k].w, x.w, pv[v]);
           }
         }
       }
     }
 #pragma unroll
-    for (int v = 0; v < G; v++) {
-      const float t = wave_sum(part[v]);
-      if (lane == 0 && valid && v < nv) st_dev(a.logits + (int64_t)(v0 + v) * a.n_expert + row, t);
+    for (int v = 0; v < MT; v++) {
+      const float t = wave_sum(pv[v]);
+      if (lane == 0 && v0 + v < m) part[wave][v0 + v] = t;
     }
   }
-  if (arrive(a.counter) != (int)gridDim.x - 1) return;
+  __syncthreads();
+  if ((int)threadIdx.x < m) {
+    const int v = threadIdx.x;
+    st_dev(a.logits + (int64_t)v * a.n_expert + row, ((part[0][v] + part[1][v]) + part[2][v]) + part[3][v]);
+  }
+  if (!arrive_last(a.counter, gridDim.x)) return;
   // routing: wave w takes rows w, w+4, ...; lane i < n_used ends up holding the row's i-th
   // choice (expert, probability)
   __shared__ signed char slot_of[MAX_M][256];  // slot of expert e among row b's kept choices, -1: none
   __shared__ int wcount[4];
   const int ne = a.n_expert, nu = a.n_used;
   for (int i = threadIdx.x; i < MAX_M * 256; i += 256) (&slot_of[0][0])[i] = -1;
+  float lall[MAX_M / 4][4];  // logits of this wavefront's rows, all loaded in one round
+#pragma unroll
+  for (int rr = 0; rr < MAX_M / 4; rr++)
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int b = wave + 4 * rr, e = lane + 64 * k;
+      lall[rr][k] = b < m && e < ne ? ld_dev(a.logits + (int64_t)b * ne + e) : -INFINITY;
+    }
   __syncthreads();
-  for (int b = wave; b < m; b += 4) {
-    const float *lg = a.logits + (int64_t)b * ne;
+#pragma unroll
+  for (int rr = 0; rr < MAX_M / 4; rr++) {
+    const int b = wave + 4 * rr;
+    if (b >= m) break;
     float lv[4], mx = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < 4; k++) { const int e = lane + 64 * k; lv[k] = e < ne ? ld_dev(lg + e) : -INFINITY; mx = fmaxf(mx, lv[k]); }
+    for (int k = 0; k < 4; k++) { lv[k] = lall[rr][k]; mx = fmaxf(mx, lv[k]); }
     mx = wave_max(mx);
     float pv[4], sum = 0.0f;
 #pragma unroll
@@ -1264,38 +1276,51 @@ __global__ __launch_bounds__(256) void k_router(const RouterArgs a, const StepRe
   }
   __syncthreads();
   // jobs: experts with at least one user, in expert order (thread e = expert e); users in
-  // row order (a row chooses an expert at most once)
+  // row order (a row chooses an expert at most once). Down jobs (jobs[256 + j]) hold all of
+  // an expert's users; gate/up jobs (jobs[0 ..]) at most GU_USERS each, an expert's users in
+  // consecutive jobs.
+  __shared__ int ssub[4];
   const int e = threadIdx.x;
   int cnt = 0;
   if (e < ne)
     for (int b = 0; b < m; b++) cnt += slot_of[b][e] >= 0;
+  const int nsj = (cnt + GU_USERS - 1) / GU_USERS;
+  int incl = nsj;  // inclusive scan of the gate/up job counts over the wavefront
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(incl, d);
+    if (lane >= d) incl += t;
+  }
   const unsigned long long bal = __ballot(cnt > 0);
   if (lane == 0) wcount[wave] = __popcll(bal);
+  if (lane == 63) ssub[wave] = incl;
   __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; w++) base += wcount[w];
+  int base = 0, sbase = 0;
+  for (int w = 0; w < wave; w++) { base += wcount[w]; sbase += ssub[w]; }
   if (cnt > 0) {
     const int j = base + __popcll(bal & ((1ull << lane) - 1ull));
-    Job &J = a.jobs[j];
     Job &Jd = a.jobs[256 + j];
-    int k = 0;
+    int k = 0, sj = sbase + incl - nsj, ks = 0;
     for (int b = 0; b < m; b++) {
       const int s = slot_of[b][e];
       if (s >= 0) {
-        J.vec[k] = b;
-        J.out[k] = b * nu + s;
         Jd.vec[k] = b * nu + s;
         Jd.out[k] = b * nu + s;
         k++;
+        Job &J = a.jobs[sj];
+        J.vec[ks] = b;
+        J.out[ks] = b * nu + s;
+        if (++ks == GU_USERS) { J.expert = e; J.nvec = ks; sj++; ks = 0; }
       }
     }
-    J.expert = e;
+    if (ks > 0) { a.jobs[sj].expert = e; a.jobs[sj].nvec = ks; }
     Jd.expert = e;
-    J.nvec = k;
     Jd.nvec = k;
     if (a.expert_count) a.expert_count[e] += 1;
   }
-  if (threadIdx.x == 0) { *a.njobs = wcount[0] + wcount[1] + wcount[2] + wcount[3]; *a.counter = 0; }
+  if (threadIdx.x == 0) {
+    a.njobs[0] = wcount[0] + wcount[1] + wcount[2] + wcount[3];
+    a.njobs[1] = ssub[0] + ssub[1] + ssub[2] + ssub[3];
+  }
 }
 
 // ------------------------------------------------------------------ gate / up + SwiGLU
@@ -1505,6 +1530,53 @@ __global__ __launch_bounds__(256) void k_down_kq(const DownArgs a, const StepRec
   if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
 }
 
+// Verify / prefill passes: one output row per workgroup; its four wavefronts take the jobs in
+// rounds of eight (slot = job), then the row's combine as above.
+template <int T, int MT>
+__global__ __launch_bounds__(256) void k_down_rj(const DownArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float yb[MAX_M * 32];
+  const int m = st->m, nj = *a.njobs;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int64_t r = blockIdx.x;
+  const int dim = (int)a.w.rows, nb = (int)a.w.nb;
+  const bool coh = a.tail.nw != nullptr;
+  uint8_t *tile = smem + (size_t)wave * 8 * nb * tile_bpb();
+  for (int j0 = wave * 8; j0 < nj; j0 += 32) {
+    const int j = j0 + slot;
+    const bool has = j < nj;
+    const Job &J = a.jobs[has ? j : 0];
+    const int ex = a.jobs[min(j0 + (lane & 7), 255)].expert;
+    tile_fetch<T>(tile, a.w.pl, 8, nb, [&](int sl) -> int64_t {
+      const int e = __shfl(ex, sl);
+      return j0 + sl < nj ? (int64_t)e * dim + r : -1;
+    });
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    const int nvec = has ? J.nvec : 0;
+    int vidx[MT];
+#pragma unroll
+    for (int v = 0; v < MT; v++) vidx[v] = v < nvec ? J.vec[v] : 0;
+    float res[MT];
+    kq_walk_tile<T, MT>(tile, 8, nb, slot, (int64_t)J.expert * dim + r, a.y, vidx, nvec, l, res);
+    if (l == 0) {
+#pragma unroll
+      for (int v = 0; v < MT; v++)
+        if (v < nvec) yb[J.out[v]] = res[v];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();  // the tile is refilled next round
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < m) {
+    const int b = threadIdx.x, nk = a.nkeep[b];
+    float acc = 0.0f;
+    for (int i = 0; i < nk; i++) acc = acc + a.weights[b * 32 + i] * yb[b * a.n_used + i];
+    out_store(a.out + (int64_t)b * dim + r, acc, coh);
+  }
+  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
+}
+
 template <int T, int MT>
 __global__ __launch_bounds__(256) void k_down_f(const DownArgs a, const StepRec *st) {
   __shared__ float yb[4][MAX_M * 32];
@@ -1630,11 +1702,12 @@ hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStre
 
 hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStream_t s) {
   mt = bucket(mt);
-  const int grid = (a.n_expert + 3) / 4;
+  const int grid = a.n_expert;
   switch (mt) {
   case 1: hipLaunchKernelGGL(k_router<1>, dim3(grid), dim3(256), 0, s, a, st); break;
   case 2: hipLaunchKernelGGL(k_router<2>, dim3(grid), dim3(256), 0, s, a, st); break;
-  default: hipLaunchKernelGGL(k_router<4>, dim3(grid), dim3(256), 0, s, a, st); break;
+  case 4: hipLaunchKernelGGL(k_router<4>, dim3(grid), dim3(256), 0, s, a, st); break;
+  default: hipLaunchKernelGGL(k_router<8>, dim3(grid), dim3(256), 0, s, a, st); break;
   }
   return hipGetLastError();
 }
@@ -1682,11 +1755,16 @@ hipError_t launch_gateup(const GUArgs &a, int mt, int mode, const StepRec *st, i
 }
 
 template <int T, int MT>
-static hipError_t launch_down_t(const DownArgs &a, const StepRec *st, hipStream_t s) {
+static hipError_t launch_down_t(const DownArgs &a, int mode, const StepRec *st, hipStream_t s) {
   const dim3 grid((unsigned)((a.w.rows + 3) / 4));
   if constexpr (T == T_Q4K || T == T_Q6K) {
     const int n_ff = (int)a.w.cols, nb = (int)a.w.nb;
     const size_t tiles = (size_t)4 * 8 * nb * tile_bpb();
+    if (mode == 1) {
+      SPX_LDS((k_down_rj<T, MT>), tiles);
+      hipLaunchKernelGGL((k_down_rj<T, MT>), dim3((unsigned)a.w.rows), dim3(256), tiles, s, a, st);
+      return hipGetLastError();
+    }
     const size_t staged = ldsq_bytes(MT * a.n_used, n_ff) + tiles;
     if (MT <= 2 && staged <= 65536) {
       hipLaunchKernelGGL((k_down_kq<T, MT, true>), grid, dim3(256), staged, s, a, st);
@@ -1701,24 +1779,25 @@ static hipError_t launch_down_t(const DownArgs &a, const StepRec *st, hipStream_
 }
 
 template <int T>
-static hipError_t launch_down_dt(const DownArgs &a, int mt, const StepRec *st, hipStream_t s) {
+static hipError_t launch_down_dt(const DownArgs &a, int mt, int mode, const StepRec *st, hipStream_t s) {
   switch (mt) {
-  case 1: return launch_down_t<T, 1>(a, st, s);
-  case 2: return launch_down_t<T, 2>(a, st, s);
-  case 4: return launch_down_t<T, 4>(a, st, s);
-  case 8: return launch_down_t<T, 8>(a, st, s);
-  default: return launch_down_t<T, 16>(a, st, s);
+  case 1: return launch_down_t<T, 1>(a, mode, st, s);
+  case 2: return launch_down_t<T, 2>(a, mode, st, s);
+  case 4: return launch_down_t<T, 4>(a, mode, st, s);
+  case 8: return launch_down_t<T, 8>(a, mode, st, s);
+  default: return launch_down_t<T, 16>(a, mode, st, s);
   }
 }
 
+// mode 0: four output rows per workgroup, a wavefront per row over the jobs; 1 (integer):
+// one row per workgroup, the wavefronts split the jobs
 hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, hipStream_t s) {
-  (void)mode;
   mt = bucket(mt);
   switch (a.w.dtype) {
-  case T_Q4K: return launch_down_dt<T_Q4K>(a, mt, st, s);
-  case T_Q6K: return launch_down_dt<T_Q6K>(a, mt, st, s);
-  case T_Q8_0: return launch_down_dt<T_Q8_0>(a, mt, st, s);
-  case T_Q5_0: return launch_down_dt<T_Q5_0>(a, mt, st, s);
+  case T_Q4K: return launch_down_dt<T_Q4K>(a, mt, mode, st, s);
+  case T_Q6K: return launch_down_dt<T_Q6K>(a, mt, mode, st, s);
+  case T_Q8_0: return launch_down_dt<T_Q8_0>(a, mt, mode, st, s);
+  case T_Q5_0: return launch_down_dt<T_Q5_0>(a, mt, mode, st, s);
   default: return hipErrorInvalidValue;
   }
 }

@@ -75,6 +75,7 @@ struct spx_engine {
   Q8KP aq{}, xq2{}, hq{}, xq{};
   int *amax = nullptr, *att_cnt = nullptr, *rt_cnt = nullptr, *gu_cnt = nullptr, *tail_cnt = nullptr;
   unsigned long long *best = nullptr;
+  int *hist = nullptr;  // token history of back-to-back decode passes [max_seq]
   int *chosen = nullptr, *nkeep = nullptr, *expert_count = nullptr;
   float *weights = nullptr;
   Job *jobs = nullptr;
@@ -234,7 +235,7 @@ int mv_one(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld
 // LM head and the greedy pick (forward_slice / forward_batch_slice + compute_logits_batch).
 // Residual stream: the embedding writes xA; attn_output's norm tail adds its output to xA
 // and writes xB; the FFN's tail adds its output to xB and writes xA.
-int enqueue_forward(spx_engine *E, int m) {
+int enqueue_forward(spx_engine *E, int m, bool advance = false) {
   const auto &c = E->c;
   hipStream_t s = E->ctx->stream;
   const int dim = c.dim, hd = c.head_dim;
@@ -351,26 +352,29 @@ int enqueue_forward(spx_engine *E, int m) {
   }
   {
     ProfScope ps(E, PC_ARGMAX, 0);
-    SPX_HIP(launch_argmax_final(E->best, E->nbest, E->amax, E->st_dev, m, s));
+    SPX_HIP(launch_argmax_final(E->best, E->nbest, E->amax, E->st_dev, advance ? E->hist : nullptr, m, s));
   }
   return 0;
 }
 
-int run_forward(spx_engine *E, int m) {
+// Graph slot m (1..16): a pass of m rows; slot 0: a one-row decode pass that advances the
+// step record itself (back-to-back greedy decoding without host round trips).
+int run_forward(spx_engine *E, int m, bool advance = false) {
   hipStream_t s = E->ctx->stream;
-  if (!E->use_graphs || E->profiling) return enqueue_forward(E, m);
-  if (!E->graph[m]) {
+  if (!E->use_graphs || E->profiling) return enqueue_forward(E, m, advance);
+  const int slot = advance ? 0 : m;
+  if (!E->graph[slot]) {
     SPX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    int r = enqueue_forward(E, m);
+    int r = enqueue_forward(E, m, advance);
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(s, &g);
     if (r) { if (g) (void)hipGraphDestroy(g); return r; }
     if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
-    e = hipGraphInstantiate(&E->graph[m], g, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(&E->graph[slot], g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
-    if (e != hipSuccess) { E->graph[m] = nullptr; return hip_fail(e, "hipGraphInstantiate"); }
+    if (e != hipSuccess) { E->graph[slot] = nullptr; return hip_fail(e, "hipGraphInstantiate"); }
   }
-  SPX_HIP(hipGraphLaunch(E->graph[m], s));
+  SPX_HIP(hipGraphLaunch(E->graph[slot], s));
   return 0;
 }
 
@@ -524,7 +528,7 @@ int spx_engine_prepare(spx_engine *E) {
             (E->h = E->dalloc<float>((size_t)nv * nff)) && (E->rlog = E->dalloc<float>((size_t)M * std::max(1, c.n_expert))) &&
             (E->logits = E->dalloc<float>((size_t)M * c.vocab)) && (E->amax = E->dalloc<int>(M)) &&
             (E->best = E->dalloc<unsigned long long>((size_t)M * std::max<int64_t>(E->lm_grid, c.vocab / 4 + 1))) &&
-            (E->tail_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) &&
+            (E->tail_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) && (E->hist = E->dalloc<int>((size_t)c.max_seq)) &&
             (E->part_ml = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * 2)) &&
             (E->part_o = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * c.head_dim)) &&
             (E->att_cnt = E->dalloc<int>((size_t)c.n_kv_heads * ATT_QT * (1 + ATT_GMAX) * CNT_STRIDE)) && (E->rt_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) &&
@@ -572,6 +576,7 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
   SPX_HIP(hipStreamSynchronize(s));
   E->st_host->m = m;
   E->st_host->start = start_pos;
+  E->st_host->step = 0;
   for (int i = 0; i < m; i++) E->st_host->ids[i] = ids[i];
   SPX_HIP(hipMemcpyAsync(E->st_dev, E->st_host, sizeof(StepRec), hipMemcpyHostToDevice, s));
   if (int r = run_forward(E, m)) return r;
@@ -618,13 +623,34 @@ int spx_engine_profile_read(spx_engine *E, int cls, const char **name, int64_t *
 
 int spx_engine_decode(spx_engine *E, int32_t token, int start_pos, int n, int32_t *out) {
   if (!E || !out || n < 0) return fail("spx_engine_decode: bad argument");
-  int32_t tok = token;
-  for (int i = 0; i < n; i++) {  // step_token (:3106-3132) + greedy sample, one token per pass
-    int32_t am = 0;
-    if (int r = spx_engine_forward(E, &tok, 1, start_pos + i, nullptr, nullptr, &am)) return r;
-    out[i] = am;
-    tok = am;
+  if (!E->use_graphs || E->profiling) {
+    int32_t tok = token;
+    for (int i = 0; i < n; i++) {  // step_token (:3106-3132) + greedy sample, one token per pass
+      int32_t am = 0;
+      if (int r = spx_engine_forward(E, &tok, 1, start_pos + i, nullptr, nullptr, &am)) return r;
+      out[i] = am;
+      tok = am;
+    }
+    return 0;
   }
+  // the same passes replayed back to back: each pass's pick becomes the next pass's token on
+  // the device (the step record advances), the picks are copied out once at the end
+  if (!E->prepared) return fail("spx_engine_decode: call spx_engine_prepare first");
+  if (token < 0 || token >= E->c.vocab) return fail("spx_engine_decode: token id out of range");
+  if (start_pos < 0 || start_pos + n > E->c.max_seq) return fail("spx_engine_decode: positions beyond max_seq (the KV window is full)");
+  if (n == 0) return 0;
+  hipStream_t s = E->ctx->stream;
+  SPX_HIP(hipSetDevice(E->ctx->device));
+  SPX_HIP(hipStreamSynchronize(s));
+  E->st_host->m = 1;
+  E->st_host->start = start_pos;
+  E->st_host->ids[0] = token;
+  E->st_host->step = 0;
+  SPX_HIP(hipMemcpyAsync(E->st_dev, E->st_host, sizeof(StepRec), hipMemcpyHostToDevice, s));
+  for (int i = 0; i < n; i++)
+    if (int r = run_forward(E, 1, true)) return r;
+  SPX_HIP(hipMemcpyAsync(out, E->hist, sizeof(int32_t) * n, hipMemcpyDeviceToHost, s));
+  SPX_HIP(hipStreamSynchronize(s));
   return 0;
 }
 

@@ -21,6 +21,7 @@ struct StepRec {
   int m;
   int start;
   int ids[MAX_M];
+  int step;           // back-to-back decode: passes done (index into the token history)
 };
 
 // Residual add + RMSNorm (+ Q8_K) of the pass's rows, run once by the last workgroup of the
@@ -145,7 +146,9 @@ hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStre
 hipError_t launch_gateup(const GUArgs &a, int mt, int mode, const StepRec *st, int max_jobs, hipStream_t s);
 hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, hipStream_t s);
 hipError_t launch_norm(const NormTail &t, const StepRec *st, int m, hipStream_t s);
-hipError_t launch_argmax_final(const unsigned long long *best, int nbest, int *out, const StepRec *st, int m, hipStream_t s);
+// hist non-null (m == 1): the pick advances the step record (next token and position) and is
+// appended to hist[step]
+hipError_t launch_argmax_final(const unsigned long long *best, int nbest, int *out, StepRec *st, int *hist, int m, hipStream_t s);
 hipError_t launch_q8kp_quantize(const float *x, int64_t n, int64_t ld_x, int m, Q8KP out, hipStream_t s);
 hipError_t launch_q8kp_from_ref(const float *d, const int8_t *qs, const int16_t *bs, int64_t n, int m, Q8KP out, hipStream_t s);
 hipError_t launch_kq_block_sums(const TensorView &w, int expert, int64_t row, Q8KP y, int32_t *sums, hipStream_t s);

@@ -1610,7 +1610,9 @@ __global__ __launch_bounds__(256) void k_down_f(const DownArgs a, const StepRec 
 }
 
 // ------------------------------------------------------------------ final greedy pick
-__global__ __launch_bounds__(256) void k_argmax_final(const unsigned long long *best, int nbest, int *out, const StepRec *st) {
+// With hist (one-row decode passes replayed back to back): the pick also becomes the next
+// pass's token at the next position, and is appended to hist.
+__global__ __launch_bounds__(256) void k_argmax_final(const unsigned long long *best, int nbest, int *out, StepRec *st, int *hist) {
   const int b = blockIdx.x;
   if (st && b >= st->m) return;
   unsigned long long v = 0;
@@ -1622,7 +1624,14 @@ __global__ __launch_bounds__(256) void k_argmax_final(const unsigned long long *
   if (threadIdx.x == 0) {
     unsigned long long r = sb[0];
     for (int w = 1; w < 4; w++) r = sb[w] > r ? sb[w] : r;
-    out[b] = (int)(uint32_t)(r & 0xffffffffull);
+    const int tok = (int)(uint32_t)(r & 0xffffffffull);
+    out[b] = tok;
+    if (hist) {
+      hist[st->step] = tok;
+      st->step += 1;
+      st->ids[0] = tok;
+      st->start += 1;
+    }
   }
 }
 
@@ -1812,8 +1821,9 @@ hipError_t launch_norm(const NormTail &t, const StepRec *st, int m, hipStream_t 
   return hipGetLastError();
 }
 
-hipError_t launch_argmax_final(const unsigned long long *best, int nbest, int *out, const StepRec *st, int m, hipStream_t s) {
-  hipLaunchKernelGGL(k_argmax_final, dim3(m), dim3(256), 0, s, best, nbest, out, st);
+hipError_t launch_argmax_final(const unsigned long long *best, int nbest, int *out, StepRec *st, int *hist, int m, hipStream_t s) {
+  if (hist && m != 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_argmax_final, dim3(m), dim3(256), 0, s, best, nbest, out, st, hist);
   return hipGetLastError();
 }
 

@@ -137,6 +137,31 @@ def test_graph_replay_matches_eager(ctx, graphs):
             assert np.array_equal(h0.view(np.uint32), h1.view(np.uint32)), (s, rep)
 
 
+@pytest.mark.parametrize("name", ["tiny-qwen3moe", "tiny-llama"])
+def test_decode_back_to_back_matches_single_passes(ctx, name):
+    """spx_engine_decode replays one-row passes back to back with the pick fed forward on the
+    device; it must pick what separate one-token passes pick."""
+    cfg = M.TINY[name].replace(sigma=0.05)
+    w = M.synth_model(cfg, seed=15)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    ids = np.arange(12) * 11 % cfg.vocab
+    a.forward(ids, 0)
+    b.forward(ids, 0)
+    got = a.decode(int(ids[-1]), 12, 20)
+    tok, want = int(ids[-1]), []
+    for i in range(20):
+        am, _, _ = b.forward([tok], 12 + i)
+        tok = int(am[0])
+        want.append(tok)
+    assert got.tolist() == want
+    # and the caches agree afterwards
+    ka, va = a.kv_cache()
+    kb, vb = b.kv_cache()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    a.close()
+    b.close()
+
+
 def _spec_prompt(vocab, seed):
     """BASELINE.json config 3's construction at small size: random tokens, then copied spans
     of 16..64 tokens from the first half interleaved with 10% random tokens."""

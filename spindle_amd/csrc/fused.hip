@@ -880,14 +880,15 @@ __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo) {
 }
 
 // Merges n <= 16 partials (running max m, sum l, unnormalised output o) in slots s0 .. s0+n-1
-// for the 16 queries qa .. qa+15 (< NQ): M = max m_c, w_c = exp(m_c - M), L = sum l_c w_c,
-// O = sum w_c o_c in slot order. Thread: query qa + tid / 16, dims (tid % 16) * HD/16 ... .
-// Writes the normalised O / L to LDS (ol, rows from qa) or the merged partial to slot dst.
-template <int HD>
-__device__ __forceinline__ void attn_merge16(rsrc_t r_ml, rsrc_t r_o, int s0, int n, int qa, int NQ, float *ol, const rsrc_t *d_ml,
+// for the QPT queries qa .. qa+QPT-1 (< NQ): M = max m_c, w_c = exp(m_c - M),
+// L = sum l_c w_c, O = sum w_c o_c in slot order. Thread: query qa + tid / (256 / QPT), a
+// slice of its dims. Writes the normalised O / L to LDS (ol, rows from qa) or the merged
+// partial to slot dst.
+template <int HD, int QPT>
+__device__ __forceinline__ void attn_merge_q(rsrc_t r_ml, rsrc_t r_o, int s0, int n, int qa, int NQ, float *ol, const rsrc_t *d_ml,
                                              const rsrc_t *d_o, int dst) {
-  constexpr int DW = HD / 16, NV = DW / 4;
-  const int tid = threadIdx.x, qi = qa + (tid >> 4), d0 = (tid & 15) * DW;
+  constexpr int TPQ = 256 / QPT, DW = HD / TPQ, NV = DW / 4;  // threads per query, dims per thread
+  const int tid = threadIdx.x, qi = qa + tid / TPQ, d0 = (tid % TPQ) * DW;
   if (qi >= NQ) return;
   f2v ml[16];
 #pragma unroll
@@ -935,8 +936,17 @@ __device__ __forceinline__ void attn_merge16(rsrc_t r_ml, rsrc_t r_o, int s0, in
 #pragma unroll
     for (int v = 0; v < NV; v++)
       st_coh4(*d_o, ((dst * ATT_QMAX + qi) * HD + d0 + 4 * v) * 4, f4v{acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]});
-    if ((threadIdx.x & 15) == 0) st_coh2(*d_ml, (dst * ATT_QMAX + qi) * 8, f2v{M, L});
+    if (tid % TPQ == 0) st_coh2(*d_ml, (dst * ATT_QMAX + qi) * 8, f2v{M, L});
   }
+}
+
+// The tile's merge with all 256 threads: 8 queries (32 threads each) when the tile has at
+// most 8, else 16 (16 threads each).
+template <int HD>
+__device__ __forceinline__ void attn_merge16(rsrc_t r_ml, rsrc_t r_o, int s0, int n, int qa, int NQ, float *ol, const rsrc_t *d_ml,
+                                             const rsrc_t *d_o, int dst) {
+  if (NQ - qa <= 8 && HD / 32 >= 4) attn_merge_q<HD, 8>(r_ml, r_o, s0, n, qa, NQ, ol, d_ml, d_o, dst);
+  else attn_merge_q<HD, 16>(r_ml, r_o, s0, n, qa, NQ, ol, d_ml, d_o, dst);
 }
 
 template <int NU>
@@ -1072,18 +1082,36 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
       for (int r = 0; r < 4; r++) ss[(kg + r) * SS + wave * 16 + ar] = sacc[r];
     }
     __syncthreads();
-    // online softmax, wavefront w: query rows 4w .. 4w+3, lane = position
+    // online softmax, wavefront w: query rows w, w+4, w+8, w+12 (rows past the pass: their
+    // probabilities are zero), lane = position; the rows' reductions are interleaved
+    {
+      float sv[4], mx[4];
 #pragma unroll
-    for (int r4 = 0; r4 < 4; r4++) {
-      const int row = wave * 4 + r4, qi = qa + row, pos = s0 + lane;
-      const float sv = qi < NQ && pos < p_hi && pos <= start + qi / g ? ss[row * SS + lane] * a.scale : -INFINITY;
-      const float mx = wave_max(sv);
-      const float m_old = rm[row], m_new = fmaxf(m_old, mx);
-      const float pv = (sv == -INFINITY || m_new == -INFINITY) ? 0.0f : expf(sv - m_new);
-      const float ls = wave_sum(pv);
-      const float alpha = m_new == -INFINITY ? 1.0f : (m_old == -INFINITY ? 0.0f : expf(m_old - m_new));
-      split_f16(pv, ph[row * PS + lane], pl[row * PS + lane]);
-      if (lane == 0) { rm[row] = m_new; rl[row] = rl[row] * alpha + ls; sa[row] = alpha; }
+      for (int r4 = 0; r4 < 4; r4++) {
+        const int row = wave + 4 * r4, qi = qa + row, pos = s0 + lane;
+        sv[r4] = qi < NQ && pos < p_hi && pos <= start + qi / g ? ss[row * SS + lane] * a.scale : -INFINITY;
+        mx[r4] = sv[r4];
+      }
+#pragma unroll
+      for (int r4 = 0; r4 < 4; r4++) mx[r4] = wave_max(mx[r4]);
+      float pv[4], ls[4], mn[4], al[4];
+#pragma unroll
+      for (int r4 = 0; r4 < 4; r4++) {
+        const int row = wave + 4 * r4;
+        const float m_old = rm[row];
+        mn[r4] = fmaxf(m_old, mx[r4]);
+        pv[r4] = (sv[r4] == -INFINITY || mn[r4] == -INFINITY) ? 0.0f : expf(sv[r4] - mn[r4]);
+        al[r4] = mn[r4] == -INFINITY ? 1.0f : (m_old == -INFINITY ? 0.0f : expf(m_old - mn[r4]));
+        ls[r4] = pv[r4];
+      }
+#pragma unroll
+      for (int r4 = 0; r4 < 4; r4++) ls[r4] = wave_sum(ls[r4]);
+#pragma unroll
+      for (int r4 = 0; r4 < 4; r4++) {
+        const int row = wave + 4 * r4;
+        split_f16(pv[r4], ph[row * PS + lane], pl[row * PS + lane]);
+        if (lane == 0) { rm[row] = mn[r4]; rl[row] = rl[row] * al[r4] + ls[r4]; sa[row] = al[r4]; }
+      }
     }
     __syncthreads();
     // O = O * alpha + P V, wavefront w: dim tiles w*TPW .. w*TPW + TPW-1

@@ -1,0 +1,57 @@
+"""Summarises a rocprofv3 kernel trace of the engine per forward pass.
+
+A pass is the kernels from k_embed to k_argmax_final; passes are grouped by kernel count and
+their first matrix kernel (k_mvr<M> / k_mvt<M> / k_mv_f<M>: M = the pass's row bucket). For each
+group: pass span vs busy time, and the median per-pass time of every kernel.
+
+  python3 -m spindle_amd.trace_summary <run_kernel_trace.csv> <summary.txt>
+"""
+import csv, sys, collections, statistics as S
+if len(sys.argv) != 3:
+    sys.exit(__doc__)
+path, out = sys.argv[1], sys.argv[2]
+rows = []
+with open(path) as f:
+    for r in csv.DictReader(f):
+        rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"], int(r.get("Grid_Size_X", r.get("Grid_Size", 0)) or 0), int(r.get("Workgroup_Size_X", 0) or 0)))
+rows.sort()
+def short(n):
+    n = n.split("(")[0]
+    return n.replace("void ", "").replace("spx::", "")[:60]
+passes, cur = [], None
+for r in rows:
+    nm = short(r[2])
+    if nm.startswith("k_embed"):
+        cur = [r]
+    elif cur is not None:
+        cur.append(r)
+        if nm.startswith("k_argmax"):
+            passes.append(cur); cur = None
+lines = []
+lines.append(f"kernels in trace: {len(rows)}; forward passes found: {len(passes)}")
+# classify by kernel count
+groups = collections.defaultdict(list)
+for p in passes:
+    sig = next((short(r[2]) for r in p if short(r[2]).startswith(("k_mvr", "k_mvt", "k_mv_f"))), "none")
+    groups[(len(p), sig)].append(p)
+for n, ps in sorted(groups.items()):
+    spans = [(p[-1][1] - p[0][0]) / 1e3 for p in ps]
+    busy = [sum(r[1] - r[0] for r in p) / 1e3 for p in ps]
+    lines.append(f"passes {n}: {len(ps)}; span median {S.median(spans):.1f} us, busy median {S.median(busy):.1f} us, gap median {(S.median(spans)-S.median(busy)):.1f} us")
+# per-kernel breakdown in the most common pass type(s): take the last 20 passes of each group
+for n, ps in sorted(groups.items(), key=lambda kv: -len(kv[1]))[:3]:
+    sel = ps[-20:]
+    agg = collections.defaultdict(list)
+    for p in sel:
+        per = collections.defaultdict(float); cnt = collections.Counter()
+        for r in p:
+            per[short(r[2])] += (r[1] - r[0]) / 1e3; cnt[short(r[2])] += 1
+        for k in per: agg[k].append((per[k], cnt[k]))
+    lines.append(f"-- per-pass kernel time, passes {n} (median over {len(sel)} passes)")
+    tot = 0
+    for k, v in sorted(agg.items(), key=lambda kv: -S.median([x[0] for x in kv[1]])):
+        t = S.median([x[0] for x in v]); c = v[0][1]; tot += t
+        lines.append(f"  {t:9.1f} us  {c:5d} launches  {t / c:7.2f} us/launch  {k}")
+    lines.append(f"  {tot:9.1f} us  total")
+open(out, "w").write("\n".join(lines) + "\n")
+print("\n".join(lines))

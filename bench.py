@@ -26,6 +26,16 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 
+# HBM bytes per M=1 decode launch at context ~4.1K, measured with rocprofv3 hardware counters
+# (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, factors from a 512 MiB copy measured the same way) by
+# spindle_amd.traffic_probe; profiles/decode_qwen3_30b_a3b_hbm_traffic.txt holds the runs.
+# Counters cannot be read inside a timed run, so the bench reports this measurement.
+MEASURED_TRAFFIC = {
+    "attention": 11_235_328, "qkv_matvec": 6_455_296, "attn_output_matvec": 5_064_499,
+    "router_route": 1_191_629, "gate_up_swiglu": 14_630_502, "down_combine": 11_404_902,
+    "lm_head_matvec": 256_084_480,
+}
+
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
@@ -125,6 +135,8 @@ def main():
     for s in range(0, len(prompt), 16):
         am, _, _ = eng.forward(prompt[s:s + 16], s)
         pos = s + len(prompt[s:s + 16])
+        if s % 1024 == 0:
+            log(f"prefill {pos}/{len(prompt)}")
     prefill_s = time.perf_counter() - t0
     tok = int(am[-1])
     log(f"prefill {len(prompt)} tokens in {prefill_s:.2f}s ({len(prompt) / prefill_s:.0f} tok/s, 16-row passes)")
@@ -159,7 +171,7 @@ def main():
     n, us, by = prof[dom]
     achieved = by / us / 1e3
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(dom), "kernel": dom,
             "bytes_per_launch": round(by / n), "avg_launch_us": round(us / n, 3)}
 
     # verify: prompt-lookup speculation, benchmark mode (n-gram 3, k = 8, fixed length)

@@ -33,6 +33,8 @@ SIGNATURES = {
     "spx_engine_set_tensor": (C.c_int, [P, C.c_char_p, C.c_int, I64, I64, C.c_int, P]),
     "spx_engine_prepare": (C.c_int, [P]),
     "spx_engine_set_graphs": (C.c_int, [P, C.c_int]),
+    "spx_engine_set_decode": (C.c_int, [P, C.c_int]),
+    "spx_engine_decode_pipeline": (C.c_int, [P, C.POINTER(C.c_int)]),
     "spx_engine_forward": (C.c_int, [P, P, C.c_int, C.c_int, P, P, P]),
     "spx_engine_last_experts": (C.c_int, [P, P]),
     "spx_engine_debug_read": (C.c_int, [P, C.c_char_p, P, I64]),

@@ -1,0 +1,99 @@
+// Argument records and launchers of the one-row decode pipeline (decode.hip).
+//
+// A decode pass (M = 1, forward_slice smollm_chat.rs:3364-3552) is a chain of kernels that
+// hand their results to each other only through kernel boundaries: no arrival counters and
+// no last-workgroup tails. A producer writes the residual add itself (x + rscale * y, row by
+// row), and every workgroup of a consumer recomputes the RMSNorm and Q8_K of the row it
+// needs (a few KB, read while its weights are already in flight). The arithmetic is the same
+// as the fused kernels' (fused.hip) operation for operation, so both pipelines give the same
+// bits.
+#pragma once
+#include "fused.h"
+
+namespace spx {
+
+// Activation prologue: the fp32 row x (cols values) read by every workgroup, RMS-normalised
+// with nw unless nw is null, and quantized to permuted Q8_K in LDS.
+struct DecIn {
+  const float *x;
+  const float *nw;
+  float eps;
+  int cols;
+};
+
+// Integer matvec of one row over up to three tensors (segments) sharing the input.
+struct DecMVArgs {
+  TensorView w[3];
+  float *out[3];      // segment outputs (null: not written)
+  int tiles[3];       // row tiles (NW * 8 rows) of each segment
+  int nseg;
+  DecIn in;
+  // residual epilogue (one segment): res_out[r] = res_in[r] + rscale * y[r]
+  const float *res_in;
+  float *res_out;
+  float rscale;
+  // greedy pick (LM head): best key of each workgroup -> best[blockIdx.x]
+  unsigned long long *best;
+  float lscale;
+  float *xn_out;      // the normalised input row, written by workgroup 0 (null: not written)
+};
+
+// Merge of the attention partials of one pass row: one workgroup per 256 values of the
+// output (256 / head_dim query heads), written as fp32.
+struct DecMergeArgs {
+  const float *part_ml, *part_o;  // as AttnArgs
+  float *att;
+  int nslot, hd, n_heads, n_kv;
+};
+
+// F32 router rows (one per workgroup) of the ffn_norm'd row.
+struct DecRouterArgs {
+  TensorView w;
+  DecIn in;
+  float *logits;
+  int n_expert;
+};
+
+// Routing (MoE) and gate/up + SwiGLU of the chosen experts; a dense FFN is expert 0 with no
+// routing (logits null).
+struct DecGateUpArgs {
+  TensorView gate, up;
+  DecIn in;
+  const float *logits;  // null: dense
+  int n_expert, n_used, norm;
+  float moe_prune;
+  float *h;             // [n_used][n_ff]
+  int *chosen;          // [n_used] kept experts in choice order
+  float *weights;       // [n_used]
+  int *nkeep;           // [1]
+  int *njobs;           // [1]: distinct experts of the pass (kept choices)
+  int *expert_count;    // [n_expert] selection counter (null: none)
+  int n_ff;
+};
+
+// Down projection of the chosen experts + weighted combine + residual add.
+struct DecDownArgs {
+  TensorView w;
+  const float *h;
+  const int *chosen;
+  const float *weights;
+  const int *nkeep;
+  int n_used;
+  const float *res_in;
+  float *res_out;
+  float rscale;
+};
+
+constexpr int DEC_NW = 4;       // wavefronts per matvec workgroup
+constexpr int DEC_MAXNB = 16;   // blocks per row (cols <= 4096) of the decode kernels
+constexpr int DEC_DOWN_Q = 16384;  // n_used * n_ff values of h quantized in LDS by the down kernel
+
+hipError_t launch_dec_mv(const DecMVArgs &a, int grid, hipStream_t s);
+hipError_t launch_dec_merge(const DecMergeArgs &a, const StepRec *st, hipStream_t s);
+hipError_t launch_dec_router(const DecRouterArgs &a, hipStream_t s);
+hipError_t launch_dec_gateup(const DecGateUpArgs &a, hipStream_t s);
+hipError_t launch_dec_down(const DecDownArgs &a, hipStream_t s);
+// partials only (no merge): one-row decode passes, merged by launch_dec_merge
+hipError_t launch_attention_partials(const AttnArgs &a, const StepRec *st, hipStream_t s);
+
+}  // namespace spx

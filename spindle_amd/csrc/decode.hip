@@ -1,0 +1,654 @@
+// One-row decode pipeline for gfx950 (wave64): forward_slice (smollm_chat.rs:3364-3552) of a
+// single token as a chain of kernels that meet only at kernel boundaries. Per layer:
+//   kd_mv (q|k|v)     attn_norm + Q8_K of the residual row in every workgroup's LDS, then
+//                     the three integer projections (eight rows per wavefront)
+//   attention         split-K partials (k_attn without its merge, fused.hip), then kd_merge
+//   kd_mv (wo)        Q8_K of the attention row, attn_output, + the residual add
+//   kd_router         ffn_norm in every workgroup, one F32 router row per workgroup
+//   kd_gateup         every wavefront routes the row (softmax, top-k, pruning, weights), then
+//                     gate/up + SwiGLU of the chosen experts (or the dense FFN)
+//   kd_down           Q8_K of h in every workgroup's LDS, the chosen experts' down rows, the
+//                     weighted combine and the residual add (a dense down is kd_mv)
+// and at the end kd_mv over the LM head (output_norm in every workgroup) with greedy keys.
+// A workgroup first issues the loads of its input row, then its weight loads, then computes
+// the norm / Q8_K while the weights are in flight. Every result is the same fp32 value, bit
+// for bit, as the fused pipeline's (same operations in the same order: the norm's fixed-order
+// sum, quantize_avx2, the reference's per-lane integer-dot chain, the router's lane chains
+// and wave tree, the combine's chosen-order sum); only where the work is done changes.
+#include "decode.h"
+#include "dev.h"
+
+namespace spx {
+
+// Address spaces are spelled out: pointers picked with selects (segments, gate / up) would
+// otherwise become flat accesses, which also count against the LDS / scalar wait counter.
+#define SPX_G __attribute__((address_space(1)))
+#define SPX_L __attribute__((address_space(3)))
+typedef int spx_i4 __attribute__((ext_vector_type(4)));
+typedef int spx_i2 __attribute__((ext_vector_type(2)));
+template <int N> struct GWord;
+template <> struct GWord<16> { typedef spx_i4 type; };
+template <> struct GWord<8> { typedef spx_i2 type; };
+template <> struct GWord<4> { typedef int type; };
+template <> struct GWord<2> { typedef unsigned short type; };
+template <class T>
+__device__ __forceinline__ T gld(const void *p) {
+  typedef typename GWord<sizeof(T)>::type W;
+  return __builtin_bit_cast(T, *(const SPX_G W *)p);
+}
+template <class T>
+__device__ __forceinline__ T lld(const SPX_L void *p) {
+  typedef typename GWord<sizeof(T)>::type W;
+  return __builtin_bit_cast(T, *(const SPX_L W *)p);
+}
+template <class T>
+__device__ __forceinline__ void gst(void *p, T v) {
+  typedef typename GWord<sizeof(T)>::type W;
+  *(SPX_G W *)p = __builtin_bit_cast(W, v);
+}
+
+// ------------------------------------------------------------------ weight blocks in registers
+// Raw bytes of one K-quant block as lane l of its row group loads them (the planar layout of
+// kq.h): Q4_K a = codes, b = header; Q6_K a = ql, b = scales, c = qh, d = d.
+struct DRaw {
+  uint4 a, b;
+  uint2 c;
+  uint32_t d;
+};
+
+template <int T>
+__device__ __forceinline__ void draw_load(DRaw &r, const Planes &pl, int64_t g, int l) {
+  if constexpr (T == T_Q4K) {
+    r.a = gld<uint4>(pl.p0 + g * 128 + 16 * l);
+    r.b = gld<uint4>(pl.p1 + g * 16);
+  } else {
+    r.a = gld<uint4>(pl.p0 + g * 128 + 16 * l);
+    r.c = gld<uint2>(pl.p1 + g * 64 + 8 * l);
+    r.b = gld<uint4>(pl.p2 + g * 16);
+    r.d = gld<uint16_t>(pl.p3 + g * 2);
+  }
+}
+
+// All NB blocks of global row grow (blocks past nb re-load the last one: every lane issues
+// the same number of loads, so the input row's wait never waits for the weights).
+template <int T, int NB>
+__device__ __forceinline__ void draw_row(DRaw (&raw)[NB], const Planes &pl, int64_t grow, int nb, int l) {
+#pragma unroll
+  for (int i = 0; i < NB; i++) draw_load<T>(raw[i], pl, grow * nb + min(i, nb - 1), l);
+}
+
+template <int T>
+__device__ __forceinline__ KQRaw<T> draw_kq(const DRaw &r) {
+  KQRaw<T> k;
+  if constexpr (T == T_Q4K) {
+    k.c = r.a;
+    k.h = r.b;
+  } else {
+    k.ql = r.a;
+    k.qh = r.c;
+    k.sc = r.b;
+    k.d = r.d;
+  }
+  return k;
+}
+
+// One row against the Q8_K row in LDS (blocks 0..nb-1): the reference's chain of rows<B,T>
+// (quant_q8k.rs:198-243) exactly as kq_walk_tile runs it: per block the lane's scaled integer
+// dot P and the group's correction integer, acc = fma(d * xd, float(P), acc), corr += term;
+// the row is hsum(acc) - corr, valid in lane 0 of the row group.
+template <int T, int NB>
+__device__ __forceinline__ float dot_row(const DRaw (&raw)[NB], int nb, int l, const SPX_L uint32_t *lq, const SPX_L float *ld,
+                                        const SPX_L int2 *lbs) {
+  float acc = 0.0f, corr = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NB; i++) {
+    if (i < nb) {
+      KQDec<T> dec;
+      dec.decode(draw_kq<T>(raw[i]), l);
+      const uint4 y0 = lld<uint4>(lq + i * 64 + 8 * l), y1 = lld<uint4>(lq + i * 64 + 8 * l + 4);
+      int P, s;
+      dec.dot(y0, y1, lld<int2>(lbs + i * 8 + l), P, s);
+      s = sum8(s);
+      const float xd = ld[i];
+      corr = corr + dec.corr_term(xd, s);
+      acc = fmaf(dec.d * xd, (float)P, acc);
+    }
+  }
+  return hsum_rows8(acc) - corr;
+}
+
+// ------------------------------------------------------------------ input row prologue
+// Wave w, lane j hold float4 j of the 256-value blocks w, w + NW, ... (KB of them).
+template <int KB>
+struct InRow {
+  float4 v[KB], w[KB];
+};
+
+template <int NW, int KB>
+__device__ __forceinline__ void in_load(const DecIn &in, InRow<KB> &r) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nbq = in.cols >> 8;
+#pragma unroll
+  for (int k = 0; k < KB; k++) {
+    const int tb = wave + NW * k;
+    r.v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    r.w[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tb < nbq) {
+      r.v[k] = gld<float4>(in.x + 4 * (tb * 64 + lane));
+      if (in.nw) r.w[k] = gld<float4>(in.nw + 4 * (tb * 64 + lane));
+    }
+  }
+}
+
+// rmsnorm (:569-575) as the norm tails compute it (per 256 block a wavefront tree, then the
+// blocks in order; inv = 1 / sqrt(S / cols + eps) correctly rounded; x * inv * w), then
+// quantize_avx2 of each block into the LDS image (lq, ld, lbs). xn_out: the normalised row.
+template <int NW, int KB>
+__device__ __forceinline__ void in_quant(const DecIn &in, InRow<KB> &r, SPX_L uint32_t *lq, SPX_L float *ld, SPX_L int2 *lbs, SPX_L float *bsum,
+                                         float *xn_out) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nbq = in.cols >> 8;
+  if (in.nw) {
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+      const int tb = wave + NW * k;
+      if (tb < nbq) {
+        float p = r.v[k].x * r.v[k].x;
+        p = fmaf(r.v[k].y, r.v[k].y, p);
+        p = fmaf(r.v[k].z, r.v[k].z, p);
+        p = fmaf(r.v[k].w, r.v[k].w, p);
+        p = wave_sum(p);
+        if (lane == 0) bsum[tb] = p;
+      }
+    }
+    __syncthreads();
+    float S = 0.0f;
+    for (int k = 0; k < nbq; k++) S = S + bsum[k];
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(S, (float)in.cols) + in.eps));
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+      const int tb = wave + NW * k;
+      if (tb < nbq) {
+        float4 v = r.v[k];
+        const float4 w = r.w[k];
+        v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
+        r.v[k] = v;
+        if (xn_out) gst<float4>(xn_out + 4 * (tb * 64 + lane), v);
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < KB; k++) {
+    const int tb = wave + NW * k;
+    if (tb < nbq) {
+      const float am = wave_max(amax4(r.v[k]));
+      q8k_block_store(r.v[k], am, lq + tb * 64, ld + tb, (SPX_L int *)(lbs + tb * 8));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ integer matvec, one row
+// Four wavefronts per workgroup, eight rows per wavefront (row group = 8 lanes, lane l = the
+// reference's lane l), every block of a row in registers. Tiles of 32 rows stride over the
+// grid (the LM head runs on fewer workgroups than tiles). TT = the segments' format, or 0
+// when they differ (then per segment).
+template <int TT, int NB>
+__global__ __launch_bounds__(DEC_NW * 64) void kd_mv(const DecMVArgs a) {
+  constexpr int NW = DEC_NW, KB = DEC_MAXNB / NW;
+  __shared__ __align__(16) uint32_t lq_[DEC_MAXNB * 64];
+  __shared__ float ld_[DEC_MAXNB];
+  __shared__ __align__(16) int2 lbs_[DEC_MAXNB * 8];
+  __shared__ float bsum_[DEC_MAXNB];
+  __shared__ unsigned long long sbest[NW];
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)lq_;
+  SPX_L float *ld = (SPX_L float *)ld_, *bsum = (SPX_L float *)bsum_;
+  SPX_L int2 *lbs = (SPX_L int2 *)lbs_;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int nb = a.in.cols >> 8;
+  const int t0 = a.tiles[0], t1 = a.nseg > 1 ? a.tiles[1] : 0, t2 = a.nseg > 2 ? a.tiles[2] : 0;
+  const int total = t0 + t1 + t2;
+  // segment and row of tile t; the segments' fields are all read from the kernel arguments
+  // up front and picked with wave-uniform selects (an indexed argument access would chain
+  // dependent scalar loads ahead of the weight loads)
+  const Planes pl0 = a.w[0].pl, pl1 = a.w[1].pl, pl2 = a.w[2].pl;
+  const int64_t rw0 = a.w[0].rows, rw1 = a.w[1].rows, rw2 = a.w[2].rows;
+  const int dt0 = a.w[0].dtype, dt1 = a.w[1].dtype, dt2 = a.w[2].dtype;
+  float *const o0 = a.out[0], *const o1 = a.out[1], *const o2 = a.out[2];
+  InRow<KB> in;
+  in_load<NW, KB>(a.in, in);  // the input row's loads go first
+  DRaw raw[NB];
+  int t = min((int)blockIdx.x, total - 1), si, dt;
+  int64_t row, rows;
+  Planes pl;
+  float *out;
+#define SPX_LOCATE_ISSUE()                                                        \
+  do {                                                                            \
+    si = __builtin_amdgcn_readfirstlane(t >= t0 ? (t >= t0 + t1 ? 2 : 1) : 0);    \
+    const int tt = t - (si > 0 ? t0 : 0) - (si > 1 ? t1 : 0);                     \
+    row = ((int64_t)tt * NW + wave) * 8 + slot;                                   \
+    rows = si == 0 ? rw0 : si == 1 ? rw1 : rw2;                                   \
+    dt = si == 0 ? dt0 : si == 1 ? dt1 : dt2;                                     \
+    out = si == 0 ? o0 : si == 1 ? o1 : o2;                                       \
+    pl.p0 = si == 0 ? pl0.p0 : si == 1 ? pl1.p0 : pl2.p0;                         \
+    pl.p1 = si == 0 ? pl0.p1 : si == 1 ? pl1.p1 : pl2.p1;                         \
+    pl.p2 = si == 0 ? pl0.p2 : si == 1 ? pl1.p2 : pl2.p2;                         \
+    pl.p3 = si == 0 ? pl0.p3 : si == 1 ? pl1.p3 : pl2.p3;                         \
+    const int64_t grow = row < rows ? row : rows - 1;                             \
+    if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) draw_row<T_Q4K, NB>(raw, pl, grow, nb, l); \
+    else draw_row<T_Q6K, NB>(raw, pl, grow, nb, l);                               \
+  } while (0)
+  SPX_LOCATE_ISSUE();
+  in_quant<NW, KB>(a.in, in, lq, ld, lbs, bsum, blockIdx.x == 0 ? a.xn_out : nullptr);
+  __syncthreads();
+  unsigned long long bestk = 0;
+  const bool live = (int)blockIdx.x < total;
+  while (live) {
+    float res;
+    if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) res = dot_row<T_Q4K, NB>(raw, nb, l, lq, ld, lbs);
+    else res = dot_row<T_Q6K, NB>(raw, nb, l, lq, ld, lbs);
+    if (l == 0 && row < rows) {
+      if (out) gst<float>(out + row, res);
+      if (a.res_out) gst<float>(a.res_out + row, gld<float>(a.res_in + row) + a.rscale * res);
+      if (a.best) {
+        const unsigned long long k = pick_key(res, a.lscale, row);
+        bestk = k > bestk ? k : bestk;
+      }
+    }
+    t += gridDim.x;
+    if (t >= total) break;
+    SPX_LOCATE_ISSUE();
+  }
+#undef SPX_LOCATE_ISSUE
+  if (a.best) {
+    const unsigned long long b = wave_max_u64(bestk);
+    if (lane == 0) sbest[wave] = b;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned long long r = sbest[0];
+      for (int w = 1; w < NW; w++) r = sbest[w] > r ? sbest[w] : r;
+      gst<unsigned long long>(a.best + blockIdx.x, r);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ attention merge
+// One workgroup per 256 output values (256 / HD query heads of the row). Thread (d, gs):
+// output value d, chunk groups gs, gs + 4, ...: each group of ATT_GRP chunks is merged as the
+// fused kernel's first level does (M = max m_c, w_c = exp(m_c - M), L = sum l_c w_c,
+// O = sum w_c o_c in chunk order), then the groups in group order; O / L is the output.
+template <int HD>
+__global__ __launch_bounds__(1024) void kd_merge(const DecMergeArgs a, const StepRec *st) {
+  constexpr int QPB = 256 / HD;
+  __shared__ float sO[ATT_GMAX][256];
+  __shared__ float sM[ATT_GMAX][QPB], sL[ATT_GMAX][QPB];
+  const int total = st->start + 1, nch = (total + 63) >> 6, ngrp = (nch + ATT_GRP - 1) / ATT_GRP;
+  const int t = threadIdx.x, d = t & 255, gs = t >> 8;
+  const int hq = d / HD, dim = d % HD, head = blockIdx.x * QPB + hq;
+  const int g = a.n_heads / a.n_kv, h = head / g, qi = head % g;
+  const float2 *pml = reinterpret_cast<const float2 *>(a.part_ml) + ((int64_t)h * a.nslot) * ATT_QMAX + qi;
+  const float *po = a.part_o + ((int64_t)h * a.nslot * ATT_QMAX + qi) * HD + dim;
+  for (int gi = gs; gi < ngrp; gi += 4) {
+    const int s0 = gi * ATT_GRP, n = min(ATT_GRP, nch - s0);
+    float2 ml[ATT_GRP];
+    float ov[ATT_GRP];
+#pragma unroll
+    for (int k = 0; k < ATT_GRP; k++) {
+      const int c = s0 + min(k, n - 1);
+      ml[k] = k < n ? pml[(int64_t)c * ATT_QMAX] : make_float2(-INFINITY, 0.0f);
+      ov[k] = po[(int64_t)c * ATT_QMAX * HD];
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < ATT_GRP; k++) M = fmaxf(M, ml[k].x);
+    float w[ATT_GRP], L = 0.0f;
+#pragma unroll
+    for (int k = 0; k < ATT_GRP; k++) {
+      w[k] = ml[k].x == -INFINITY ? 0.0f : expf(ml[k].x - M);
+      if (k < n) L = fmaf(ml[k].y, w[k], L);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < ATT_GRP; k++)
+      if (k < n) acc = fmaf(ov[k], w[k], acc);
+    sO[gi][d] = acc;
+    if (dim == 0) { sM[gi][hq] = M; sL[gi][hq] = L; }
+  }
+  __syncthreads();
+  if (gs != 0) return;
+  float out;
+  if (ngrp == 1) {
+    out = sO[0][d] * __fdiv_rn(1.0f, fmaxf(sL[0][hq], 1e-30f));
+  } else {
+    float mg[ATT_GMAX];
+#pragma unroll
+    for (int k = 0; k < ATT_GMAX; k++) mg[k] = k < ngrp ? sM[k][hq] : -INFINITY;
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < ATT_GMAX; k++) M = fmaxf(M, mg[k]);
+    float L = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < ATT_GMAX; k++) {
+      const float w = mg[k] == -INFINITY ? 0.0f : expf(mg[k] - M);
+      if (k < ngrp) {
+        L = fmaf(sL[k][hq], w, L);
+        acc = fmaf(sO[k][d], w, acc);
+      }
+    }
+    out = acc * __fdiv_rn(1.0f, fmaxf(L, 1e-30f));
+  }
+  a.att[(int64_t)head * HD + dim] = out;
+}
+
+// ------------------------------------------------------------------ router
+// One F32 router row per workgroup (k_router's arithmetic: wavefront w, lane j hold float4s
+// w*64 + j + 256k; the lane's fma chain, the wave tree, the four wavefronts in order) against
+// the ffn_norm'd row, which every workgroup computes for itself.
+__global__ __launch_bounds__(256) void kd_router(const DecRouterArgs a) {
+  constexpr int NK = DEC_MAXNB / 4;
+  __shared__ float bsum[DEC_MAXNB];
+  __shared__ float part[4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, row = blockIdx.x;
+  const int dim = a.in.cols, n4 = dim >> 2;
+  InRow<NK> in;
+  in_load<4, NK>(a.in, in);
+  const float4 *wr = reinterpret_cast<const float4 *>(a.w.pl.p0 + (int64_t)row * dim * 4);
+  float4 wv[NK];
+#pragma unroll
+  for (int k = 0; k < NK; k++) {
+    const int f = wave * 64 + lane + 256 * k;
+    wv[k] = f < n4 ? wr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // normalise in registers (block tb = wave + 4k holds float4 f = tb * 64 + lane)
+  const int nbq = dim >> 8;
+#pragma unroll
+  for (int k = 0; k < NK; k++) {
+    const int tb = wave + 4 * k;
+    if (tb < nbq) {
+      float p = in.v[k].x * in.v[k].x;
+      p = fmaf(in.v[k].y, in.v[k].y, p);
+      p = fmaf(in.v[k].z, in.v[k].z, p);
+      p = fmaf(in.v[k].w, in.v[k].w, p);
+      p = wave_sum(p);
+      if (lane == 0) bsum[tb] = p;
+    }
+  }
+  __syncthreads();
+  float S = 0.0f;
+  for (int k = 0; k < nbq; k++) S = S + bsum[k];
+  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(S, (float)dim) + a.in.eps));
+  float pv = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NK; k++) {
+    const int f = wave * 64 + lane + 256 * k;
+    if (f < n4) {
+      float4 x = in.v[k];
+      const float4 w = in.w[k];
+      x.x = x.x * inv * w.x; x.y = x.y * inv * w.y; x.z = x.z * inv * w.z; x.w = x.w * inv * w.w;
+      pv = fmaf(wv[k].x, x.x, pv);
+      pv = fmaf(wv[k].y, x.y, pv);
+      pv = fmaf(wv[k].z, x.z, pv);
+      pv = fmaf(wv[k].w, x.w, pv);
+    }
+  }
+  const float tsum = wave_sum(pv);
+  if (lane == 0) part[wave] = tsum;
+  __syncthreads();
+  if (threadIdx.x == 0) a.logits[row] = ((part[0] + part[1]) + part[2]) + part[3];
+}
+
+// ------------------------------------------------------------------ routing of one row
+// moe_forward's routing (:1199-1239) as k_router computes it for a row: softmax (max, exp,
+// sum, divide), top-n_used by probability (ties to the lower expert index), pruning
+// (moe_prune >= 1: keep clamp(x, max(2, n/2), n); < 1: the mass rule), the weights' sum over
+// the kept choices in choice order. lv[k] = logit of expert lane + 64k. Lane i < n_used ends
+// with choice i (my_e, my_p); keep and wsum in every lane.
+__device__ __forceinline__ void route_row(const float (&lv)[4], int ne, int nu, float moe_prune, int &my_e, float &my_p, int &keep,
+                                          float &wsum) {
+  const int lane = threadIdx.x & 63;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 4; k++) mx = fmaxf(mx, lv[k]);
+  mx = wave_max(mx);
+  float pv[4], sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; k++) { const int e = lane + 64 * k; pv[k] = e < ne ? expf(lv[k] - mx) : 0.0f; sum += pv[k]; }
+  sum = wave_sum(sum);
+  unsigned long long key[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int e = lane + 64 * k;
+    if (e < ne) pv[k] = pv[k] / sum;
+    key[k] = e < ne ? ((unsigned long long)__float_as_uint(pv[k]) << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)e) : 0ull;
+  }
+  my_e = 0;
+  my_p = 0.0f;
+  for (int i = 0; i < nu; i++) {
+    unsigned long long bk = key[0];
+#pragma unroll
+    for (int k = 1; k < 4; k++) bk = key[k] > bk ? key[k] : bk;
+    bk = wave_max_u64(bk);
+    const int e = (int)(0xFFFFFFFFu - (unsigned)(bk & 0xFFFFFFFFull));
+    if (lane == i) { my_e = e; my_p = __uint_as_float((uint32_t)(bk >> 32)); }
+    if ((e & 63) == lane) key[e >> 6] = 0ull;
+  }
+  keep = nu;
+  if (moe_prune > 0.0f && nu > 2) {
+    const int min_keep = max(2, nu / 2);
+    if (moe_prune >= 1.0f) keep = min(max((int)moe_prune, min_keep), nu);
+    else {
+      float top = 0.0f;
+      for (int i = 0; i < nu; i++) top += __shfl(my_p, i);
+      const float target = top * (1.0f - moe_prune);
+      float cum = 0.0f;
+      int k = 0;
+      while (k < nu && (k < min_keep || cum < target)) { cum += __shfl(my_p, k); k++; }
+      keep = k;
+    }
+  }
+  wsum = 0.0f;
+  for (int i = 0; i < keep; i++) wsum += __shfl(my_p, i);
+}
+
+// ------------------------------------------------------------------ gate / up + SwiGLU
+// Grid (n_ff / 16, n_used): workgroup (x, s) computes rows 16x .. 16x+15 of h for chosen slot
+// s; in each wavefront row groups 0-3 take gate rows r..r+3 and 4-7 the same rows of up.
+// h[s][r] = silu(g) * u (silu :586-588). Every wavefront routes the row itself; workgroup
+// (0, 0) publishes the routing for kd_down (chosen experts, weights, kept count).
+template <int T, int NB>
+__global__ __launch_bounds__(256) void kd_gateup(const DecGateUpArgs a) {
+  constexpr int NW = 4, KB = DEC_MAXNB / NW;
+  __shared__ __align__(16) uint32_t lq_[DEC_MAXNB * 64];
+  __shared__ float ld_[DEC_MAXNB];
+  __shared__ __align__(16) int2 lbs_[DEC_MAXNB * 8];
+  __shared__ float bsum_[DEC_MAXNB];
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)lq_;
+  SPX_L float *ld = (SPX_L float *)ld_, *bsum = (SPX_L float *)bsum_;
+  SPX_L int2 *lbs = (SPX_L int2 *)lbs_;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int n_ff = a.n_ff, nb = a.in.cols >> 8;
+  const int r = blockIdx.x * 16 + wave * 4 + (slot & 3);
+  const bool valid = r < n_ff;
+  float lv[4];
+  if (a.logits) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int e = lane + 64 * k;
+      lv[k] = e < a.n_expert ? gld<float>(a.logits + e) : -INFINITY;
+    }
+  }
+  InRow<KB> in;
+  in_load<NW, KB>(a.in, in);
+  int expert = 0;
+  if (a.logits) {
+    int my_e, keep;
+    float my_p, wsum;
+    route_row(lv, a.n_expert, a.n_used, a.moe_prune, my_e, my_p, keep, wsum);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+      if (lane < keep) {
+        gst<int>(a.chosen + lane, my_e);
+        gst<float>(a.weights + lane, a.norm ? my_p / wsum : my_p);
+        if (a.expert_count) gst<int>(a.expert_count + my_e, gld<int>(a.expert_count + my_e) + 1);
+      }
+      if (lane == 0) { gst<int>(a.nkeep, keep); gst<int>(a.njobs, keep); }
+    }
+    if ((int)blockIdx.y >= keep) return;  // a pruned slot (the same in every wavefront)
+    expert = __builtin_amdgcn_readfirstlane(__shfl(my_e, blockIdx.y));
+  }
+  const int64_t grow = (int64_t)expert * a.gate.rows + (valid ? r : n_ff - 1);
+  DRaw raw[NB];
+  draw_row<T, NB>(raw, slot < 4 ? a.gate.pl : a.up.pl, grow, nb, l);
+  in_quant<NW, KB>(a.in, in, lq, ld, lbs, bsum, nullptr);
+  __syncthreads();
+  const float res = dot_row<T, NB>(raw, nb, l, lq, ld, lbs);
+  const float u = __shfl_down(res, 32);
+  if (slot < 4 && l == 0 && valid) {
+    const float x = res;
+    gst<float>(a.h + (int64_t)blockIdx.y * n_ff + r, x / (1.0f + expf(-x)) * u);
+  }
+}
+
+// ------------------------------------------------------------------ down + combine
+// Eight wavefronts per workgroup, one output row each; row group s of a wavefront takes the
+// row of chosen expert s (rounds of eight for more). Every workgroup quantizes the kept
+// slots' h rows into LDS (Q8_K, :420-424). out = sum over the kept choices, in choice order,
+// of w * y (non-fused multiply and add, ffns_fused :432-437); res_out = res_in + rscale * out.
+template <int T, int NB>
+__global__ __launch_bounds__(512) void kd_down(const DecDownArgs a) {
+  constexpr int NWD = 8, QB = DEC_DOWN_Q / 256, HB = QB / NWD;
+  __shared__ __align__(16) uint32_t lq_[DEC_DOWN_Q / 4];
+  __shared__ float ld_[QB];
+  __shared__ __align__(16) int2 lbs_[QB * 8];
+  __shared__ float ys[NWD][32];
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)lq_;
+  SPX_L float *ld = (SPX_L float *)ld_;
+  SPX_L int2 *lbs = (SPX_L int2 *)lbs_;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, nbh = n_ff >> 8;
+  const int64_t r = (int64_t)blockIdx.x * NWD + wave;
+  const int64_t rr = r < dim ? r : dim - 1;
+  // h blocks of every slot (wave w: blocks w, w + 8, ...) and the chosen experts' rows are
+  // requested before the kept count arrives (slots past it hold earlier, valid expert ids)
+  const int nqa = a.n_used * nbh;
+  float4 hv[HB];
+#pragma unroll
+  for (int k = 0; k < HB; k++) {
+    const int vb = wave + NWD * k;
+    hv[k] = vb < nqa ? gld<float4>(a.h + (int64_t)(vb / nbh) * n_ff + (vb % nbh) * 256 + 4 * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  DRaw raw[NB];
+  draw_row<T, NB>(raw, a.w.pl, (int64_t)gld<int>(a.chosen + min(slot, a.n_used - 1)) * dim + rr, nbh, l);
+  const int nk = gld<int>(a.nkeep), nqb = nk * nbh, s0max = (nk + 7) / 8;
+#pragma unroll
+  for (int k = 0; k < HB; k++) {
+    const int vb = wave + NWD * k;
+    if (vb < nqb) {
+      const float am = wave_max(amax4(hv[k]));
+      q8k_block_store(hv[k], am, lq + vb * 64, ld + vb, (SPX_L int *)(lbs + vb * 8));
+    }
+  }
+  __syncthreads();
+  for (int round = 0; round < s0max; round++) {
+    const int s = round * 8 + slot;
+    if (round > 0) draw_row<T, NB>(raw, a.w.pl, (int64_t)gld<int>(a.chosen + min(s, nk - 1)) * dim + rr, nbh, l);
+    const int sv = min(s, nk - 1);
+    const float y = dot_row<T, NB>(raw, nbh, l, lq + sv * nbh * 64, ld + sv * nbh, lbs + sv * nbh * 8);
+    if (l == 0 && s < nk) ys[wave][s] = y;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  if (lane == 0 && r < dim) {
+    float acc = 0.0f;
+    for (int i = 0; i < nk; i++) acc = acc + gld<float>(a.weights + i) * ys[wave][i];
+    gst<float>(a.res_out + r, gld<float>(a.res_in + r) + a.rscale * acc);
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+static int nb_bucket(int nb) { return nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 3 ? 3 : nb <= 4 ? 4 : nb <= 8 ? 8 : 16; }
+
+template <int TT>
+static hipError_t dec_mv_tt(const DecMVArgs &a, int grid, hipStream_t s) {
+  switch (nb_bucket(a.in.cols >> 8)) {
+  case 1: hipLaunchKernelGGL((kd_mv<TT, 1>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
+  case 2: hipLaunchKernelGGL((kd_mv<TT, 2>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
+  case 3: hipLaunchKernelGGL((kd_mv<TT, 3>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
+  case 4: hipLaunchKernelGGL((kd_mv<TT, 4>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
+  case 8: hipLaunchKernelGGL((kd_mv<TT, 8>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
+  default: hipLaunchKernelGGL((kd_mv<TT, 16>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_dec_mv(const DecMVArgs &a, int grid, hipStream_t s) {
+  const int nb = a.in.cols >> 8;
+  if (a.nseg < 1 || a.nseg > 3 || grid < 1 || nb < 1 || nb > DEC_MAXNB || a.in.cols % 256) return hipErrorInvalidValue;
+  bool all4 = true, all6 = true;
+  for (int i = 0; i < a.nseg; i++) {
+    if (a.w[i].dtype != T_Q4K && a.w[i].dtype != T_Q6K) return hipErrorInvalidValue;
+    if (a.w[i].nb != nb) return hipErrorInvalidValue;
+    all4 = all4 && a.w[i].dtype == T_Q4K;
+    all6 = all6 && a.w[i].dtype == T_Q6K;
+  }
+  if (all4) return dec_mv_tt<T_Q4K>(a, grid, s);
+  if (all6) return dec_mv_tt<T_Q6K>(a, grid, s);
+  return dec_mv_tt<0>(a, grid, s);
+}
+
+hipError_t launch_dec_merge(const DecMergeArgs &a, const StepRec *st, hipStream_t s) {
+  const int qd = a.n_heads * a.hd;
+  if (qd % 256) return hipErrorInvalidValue;
+  if (a.hd == 128) hipLaunchKernelGGL(kd_merge<128>, dim3(qd / 256), dim3(1024), 0, s, a, st);
+  else if (a.hd == 64) hipLaunchKernelGGL(kd_merge<64>, dim3(qd / 256), dim3(1024), 0, s, a, st);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_dec_router(const DecRouterArgs &a, hipStream_t s) {
+  if (a.in.cols % 256 || a.in.cols > 256 * DEC_MAXNB || !a.in.nw) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kd_router, dim3(a.n_expert), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int T>
+static hipError_t dec_gu_t(const DecGateUpArgs &a, dim3 grid, hipStream_t s) {
+  switch (nb_bucket(a.in.cols >> 8)) {
+  case 1: hipLaunchKernelGGL((kd_gateup<T, 1>), grid, dim3(256), 0, s, a); break;
+  case 2: hipLaunchKernelGGL((kd_gateup<T, 2>), grid, dim3(256), 0, s, a); break;
+  case 3: hipLaunchKernelGGL((kd_gateup<T, 3>), grid, dim3(256), 0, s, a); break;
+  case 4: hipLaunchKernelGGL((kd_gateup<T, 4>), grid, dim3(256), 0, s, a); break;
+  case 8: hipLaunchKernelGGL((kd_gateup<T, 8>), grid, dim3(256), 0, s, a); break;
+  default: hipLaunchKernelGGL((kd_gateup<T, 16>), grid, dim3(256), 0, s, a); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_dec_gateup(const DecGateUpArgs &a, hipStream_t s) {
+  const int nb = a.in.cols >> 8;
+  if (a.in.cols % 256 || nb > DEC_MAXNB || a.gate.nb != nb || a.up.nb != nb || a.gate.dtype != a.up.dtype || !a.in.nw) return hipErrorInvalidValue;
+  if (a.logits && (a.n_expert < 1 || a.n_expert > 256 || a.n_used < 1 || a.n_used > 32 || a.n_used > a.n_expert)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((a.n_ff + 15) / 16), a.logits ? (unsigned)a.n_used : 1u);
+  if (a.gate.dtype == T_Q4K) return dec_gu_t<T_Q4K>(a, grid, s);
+  if (a.gate.dtype == T_Q6K) return dec_gu_t<T_Q6K>(a, grid, s);
+  return hipErrorInvalidValue;
+}
+
+template <int T>
+static hipError_t dec_down_t(const DecDownArgs &a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.w.rows + 7) / 8));
+  switch (nb_bucket((int)a.w.nb)) {
+  case 1: hipLaunchKernelGGL((kd_down<T, 1>), grid, dim3(512), 0, s, a); break;
+  case 2: hipLaunchKernelGGL((kd_down<T, 2>), grid, dim3(512), 0, s, a); break;
+  case 3: hipLaunchKernelGGL((kd_down<T, 3>), grid, dim3(512), 0, s, a); break;
+  case 4: hipLaunchKernelGGL((kd_down<T, 4>), grid, dim3(512), 0, s, a); break;
+  case 8: hipLaunchKernelGGL((kd_down<T, 8>), grid, dim3(512), 0, s, a); break;
+  default: hipLaunchKernelGGL((kd_down<T, 16>), grid, dim3(512), 0, s, a); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_dec_down(const DecDownArgs &a, hipStream_t s) {
+  if (a.w.cols % 256 || a.w.nb > DEC_MAXNB || a.n_used < 1 || a.n_used > 32 || (int64_t)a.n_used * a.w.cols > DEC_DOWN_Q) return hipErrorInvalidValue;
+  if (a.w.dtype == T_Q4K) return dec_down_t<T_Q4K>(a, s);
+  if (a.w.dtype == T_Q6K) return dec_down_t<T_Q6K>(a, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace spx

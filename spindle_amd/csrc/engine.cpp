@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "../../include/spx.h"
+#include "decode.h"
 #include "fused.h"
 #include "internal.h"
 
@@ -65,6 +66,7 @@ struct spx_engine {
   spx_tensor *embed = nullptr, *lm_head = nullptr;
   const float *out_norm = nullptr;
   bool prepared = false, use_graphs = true;
+  bool dec_ok = false, dec_on = true;  // one-row passes on the decode pipeline (decode.hip)
   std::vector<void *> allocs;
   // device state
   __half *kc = nullptr, *vc = nullptr;
@@ -357,15 +359,121 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
   return 0;
 }
 
+// One-row pass on the decode pipeline (decode.hip): the same values as enqueue_forward(E, 1),
+// computed by kernels that meet only at kernel boundaries. Residual stream: the embedding
+// writes xA; attn_output writes xB = xA + rscale * proj; the FFN writes xA = xB + rscale * y.
+int enqueue_decode(spx_engine *E, bool advance) {
+  const auto &c = E->c;
+  hipStream_t s = E->ctx->stream;
+  const int dim = c.dim, hd = c.head_dim;
+  auto tiles = [](int64_t rows) { return (int)((rows + DEC_NW * 8 - 1) / (DEC_NW * 8)); };
+  {
+    ProfScope ps(E, PC_EMBED, 0);
+    NormTail t{};
+    t.x = E->xA;
+    t.dim = dim;
+    SPX_HIP(launch_embed(E->embed->v, E->st_dev, c.embedding_scale, t, 1, s));
+  }
+  for (int l = 0; l < c.n_layers; l++) {
+    const LayerW &ly = E->L[l];
+    {
+      ProfScope ps(E, PC_QKV, wbytes(ly.wq) + wbytes(ly.wk) + wbytes(ly.wv));
+      DecMVArgs a{};
+      const spx_tensor *w3[3] = {ly.wq, ly.wk, ly.wv};
+      float *o3[3] = {E->q, E->k, E->v};
+      int total = 0;
+      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.tiles[i] = tiles(w3[i]->v.rows); total += a.tiles[i]; }
+      a.nseg = 3;
+      a.in = DecIn{E->xA, ly.attn_norm, c.rms_eps, dim};
+      SPX_HIP(launch_dec_mv(a, total, s));
+    }
+    {
+      ProfScope ps(E, PC_ATTN, -1.0 - l);
+      AttnArgs aa{};
+      aa.q = E->q; aa.k = E->k; aa.v = E->v;
+      aa.q_bias = ly.q_bias; aa.k_bias = ly.k_bias; aa.v_bias = ly.v_bias; aa.q_norm = ly.q_norm; aa.k_norm = ly.k_norm;
+      aa.rope = E->rope; aa.kc = E->kc; aa.vc = E->vc; aa.part_ml = E->part_ml; aa.part_o = E->part_o; aa.counter = E->att_cnt; aa.att = E->att;
+      aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
+      aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
+      aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
+      SPX_HIP(launch_attention_partials(aa, E->st_dev, s));
+      DecMergeArgs ma{E->part_ml, E->part_o, E->att, aa.nslot, hd, c.n_heads, c.n_kv_heads};
+      SPX_HIP(launch_dec_merge(ma, E->st_dev, s));
+    }
+    {
+      ProfScope ps(E, PC_WO, wbytes(ly.wo));
+      DecMVArgs a{};
+      a.w[0] = ly.wo->v; a.out[0] = E->proj; a.tiles[0] = tiles(ly.wo->v.rows); a.nseg = 1;
+      a.in = DecIn{E->att, nullptr, 0.0f, E->q_dim};
+      a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
+      SPX_HIP(launch_dec_mv(a, a.tiles[0], s));
+    }
+    const int nff = (int)ly.gate->v.rows;
+    const DecIn fin{E->xB, ly.ffn_norm, c.rms_eps, dim};
+    DecGateUpArgs ga{};
+    ga.gate = ly.gate->v; ga.up = ly.up->v; ga.in = fin; ga.h = E->h; ga.n_ff = nff;
+    if (ly.moe) {  // moe_forward (:1176-1392)
+      {
+        ProfScope ps(E, PC_ROUTER, wbytes(ly.router));
+        DecRouterArgs ra{ly.router->v, fin, E->rlog, c.n_expert};
+        SPX_HIP(launch_dec_router(ra, s));
+      }
+      {
+        ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up), l, true);  // one expert's slabs
+        ga.logits = E->rlog; ga.n_expert = c.n_expert; ga.n_used = c.n_expert_used; ga.norm = c.expert_norm; ga.moe_prune = c.moe_prune;
+        ga.chosen = E->chosen; ga.weights = E->weights; ga.nkeep = E->nkeep; ga.njobs = ly.njobs;
+        ga.expert_count = E->expert_count + (size_t)l * c.n_expert;
+        SPX_HIP(launch_dec_gateup(ga, s));
+      }
+      {
+        ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
+        DecDownArgs da{ly.down->v, E->h, E->chosen, E->weights, E->nkeep, c.n_expert_used, E->xB, E->xA, c.residual_scale};
+        SPX_HIP(launch_dec_down(da, s));
+      }
+    } else {  // ffn_forward (:590-614)
+      {
+        ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
+        SPX_HIP(launch_dec_gateup(ga, s));
+      }
+      {
+        ProfScope ps(E, PC_DOWN, wbytes(ly.down));
+        DecMVArgs a{};
+        a.w[0] = ly.down->v; a.out[0] = E->ffn; a.tiles[0] = tiles(ly.down->v.rows); a.nseg = 1;
+        a.in = DecIn{E->h, nullptr, 0.0f, nff};
+        a.res_in = E->xB; a.res_out = E->xA; a.rscale = c.residual_scale;
+        SPX_HIP(launch_dec_mv(a, a.tiles[0], s));
+      }
+    }
+  }
+  int grid = 1;
+  {
+    ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
+    DecMVArgs a{};
+    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.tiles[0] = tiles(E->lm_head->v.rows); a.nseg = 1;
+    a.in = DecIn{E->xA, E->out_norm, c.rms_eps, dim};
+    a.best = E->best; a.lscale = c.logit_scale; a.xn_out = E->xn;
+    grid = std::min(a.tiles[0], E->lm_grid);
+    SPX_HIP(launch_dec_mv(a, grid, s));
+  }
+  E->nbest = grid;
+  {
+    ProfScope ps(E, PC_ARGMAX, 0);
+    SPX_HIP(launch_argmax_final(E->best, grid, E->amax, E->st_dev, advance ? E->hist : nullptr, 1, s));
+  }
+  return 0;
+}
+
 // Graph slot m (1..16): a pass of m rows; slot 0: a one-row decode pass that advances the
 // step record itself (back-to-back greedy decoding without host round trips).
 int run_forward(spx_engine *E, int m, bool advance = false) {
   hipStream_t s = E->ctx->stream;
-  if (!E->use_graphs || E->profiling) return enqueue_forward(E, m, advance);
+  const bool dec = m == 1 && E->dec_ok && E->dec_on;
+  auto enqueue = [&]() { return dec ? enqueue_decode(E, advance) : enqueue_forward(E, m, advance); };
+  if (!E->use_graphs || E->profiling) return enqueue();
   const int slot = advance ? 0 : m;
   if (!E->graph[slot]) {
     SPX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    int r = enqueue_forward(E, m, advance);
+    int r = enqueue();
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(s, &g);
     if (r) { if (g) (void)hipGraphDestroy(g); return r; }
@@ -554,6 +662,15 @@ int spx_engine_prepare(spx_engine *E) {
   SPX_HIP(hipMemcpy(E->rope, tab.data(), sizeof(float2) * tab.size(), hipMemcpyHostToDevice));
   SPX_HIP(hipDeviceSynchronize());
   E->n_used = nu;
+  // the decode pipeline takes models whose matrices are all K-quants (integer path)
+  bool dok = is_kq(E->lm_head) && c.dim % 256 == 0 && E->q_dim % 256 == 0 && c.dim <= 256 * DEC_MAXNB &&
+             E->q_dim <= 256 * DEC_MAXNB && E->n_ff <= 256 * DEC_MAXNB;
+  for (auto &ly : E->L) {
+    for (spx_tensor *t : {ly.wq, ly.wk, ly.wv, ly.wo, ly.gate, ly.up, ly.down}) dok = dok && is_kq(t);
+    if (ly.moe) dok = dok && (int64_t)nu * ly.gate->v.rows <= DEC_DOWN_Q;
+  }
+  E->dec_ok = dok;
+  if (const char *v = std::getenv("SPX_DECODE")) E->dec_on = atoi(v) != 0;
   E->prepared = true;
   return 0;
 }
@@ -561,6 +678,24 @@ int spx_engine_prepare(spx_engine *E) {
 int spx_engine_set_graphs(spx_engine *E, int on) {
   if (!E) return fail("null engine");
   E->use_graphs = on != 0;
+  return 0;
+}
+
+int spx_engine_set_decode(spx_engine *E, int on) {
+  if (!E) return fail("null engine");
+  if (E->dec_on != (on != 0)) {  // the one-row graphs hold the other pipeline: capture again
+    SPX_HIP(hipStreamSynchronize(E->ctx->stream));
+    for (int slot : {0, 1})
+      if (E->graph[slot]) { (void)hipGraphExecDestroy(E->graph[slot]); E->graph[slot] = nullptr; }
+  }
+  E->dec_on = on != 0;
+  return 0;
+}
+
+int spx_engine_decode_pipeline(spx_engine *E, int *active) {
+  if (!E || !active) return fail("null argument");
+  if (!E->prepared) return fail("spx_engine_decode_pipeline: call spx_engine_prepare first");
+  *active = E->dec_ok && E->dec_on ? 1 : 0;
   return 0;
 }
 

@@ -20,66 +20,10 @@
 #include <float.h>
 
 #include "fused.h"
+#include "decode.h"
+#include "dev.h"
 
 namespace spx {
-
-// ------------------------------------------------------------------ wave reductions
-#define SPX_DPPF(v, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), (ctrl), 0xF, 0xF, true))
-
-// Butterfly sum / max over the 64 lanes; every lane gets the same bits (each step combines
-// a value with its partner's, and fp add / max are commutative).
-__device__ __forceinline__ float wave_sum(float v) {
-  v = v + SPX_DPPF(v, 0xB1);
-  v = v + SPX_DPPF(v, 0x4E);
-  v = v + SPX_DPPF(v, 0x141);
-  v = v + SPX_DPPF(v, 0x140);
-  v = v + __shfl_xor(v, 16);
-  v = v + __shfl_xor(v, 32);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, SPX_DPPF(v, 0xB1));
-  v = fmaxf(v, SPX_DPPF(v, 0x4E));
-  v = fmaxf(v, SPX_DPPF(v, 0x141));
-  v = fmaxf(v, SPX_DPPF(v, 0x140));
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
-}
-#define SPX_DPP64(v, ctrl)                                                                                         \
-  (((unsigned long long)(uint32_t)__builtin_amdgcn_mov_dpp((int)((v) >> 32), (ctrl), 0xF, 0xF, true) << 32) | \
-   (unsigned long long)(uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v), (ctrl), 0xF, 0xF, true))
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-  unsigned long long w;
-  w = SPX_DPP64(v, 0xB1); v = w > v ? w : v;
-  w = SPX_DPP64(v, 0x4E); v = w > v ? w : v;
-  w = SPX_DPP64(v, 0x141); v = w > v ? w : v;
-  w = SPX_DPP64(v, 0x140); v = w > v ? w : v;
-  w = __shfl_xor(v, 16); v = w > v ? w : v;
-  w = __shfl_xor(v, 32); v = w > v ? w : v;
-  return v;
-}
-
-// ------------------------------------------------------------------ cross-workgroup hand-off
-// Values one workgroup leaves for the last workgroup of a launch go through agent-coherent
-// (sc1) stores and loads: relaxed agent-scope atomics for scalars, raw buffer operations with
-// the sc1 bit for vectors (these the compiler can batch). No workgroup writes back or
-// invalidates a whole L2. Before a workgroup counts itself in, all its stores have completed
-// (s_waitcnt 0) and its waves have met at a barrier.
-typedef float f4v __attribute__((ext_vector_type(4)));
-typedef float f2v __attribute__((ext_vector_type(2)));
-typedef int i4v __attribute__((ext_vector_type(4)));
-typedef int i2v __attribute__((ext_vector_type(2)));
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-__device__ __forceinline__ rsrc_t rsrc_of(const void *base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
-}
-__device__ __forceinline__ f4v ld_coh4(rsrc_t r, int off) { return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16)); }
-__device__ __forceinline__ f2v ld_coh2(rsrc_t r, int off) { return __builtin_bit_cast(f2v, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 16)); }
-__device__ __forceinline__ void st_coh4(rsrc_t r, int off, f4v v) { __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, v), r, off, 0, 16); }
-__device__ __forceinline__ void st_coh2(rsrc_t r, int off, f2v v) { __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2v, v), r, off, 0, 16); }
-__device__ __forceinline__ void st_dev(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ float ld_dev(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 // Single counter: returns the counter's previous value to every thread.
 __device__ __forceinline__ int arrive(int *counter) {
@@ -112,31 +56,6 @@ __device__ __forceinline__ bool arrive_last(int *cnt, int n) {
   __syncthreads();
   return last;
 }
-
-// ------------------------------------------------------------------ Q8_K of one block
-// quantize_avx2 (quant_q8k.rs:84-121) of 256 values, lane j holding values 4j..4j+3:
-// amax (exact), iscale = 127/amax and d = amax/127 correctly rounded, q = rint(x*iscale)
-// saturated to int8, bsums = sums of 16 codes; zero or non-finite amax -> zeros. Writes the
-// permuted layout (lane j's dword goes to [l = j % 8][k = j / 8]).
-__device__ __forceinline__ void q8k_block_store(float4 x, float amax, uint32_t *q, float *d, int *bs) {
-  const int lane = threadIdx.x & 63;
-  int qv[4] = {0, 0, 0, 0};
-  float dv = 0.0f;
-  if (amax > 0.0f && !isinf(amax)) {
-    const float iscale = __fdiv_rn(127.0f, amax);
-    dv = __fdiv_rn(amax, 127.0f);
-    const float xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-    for (int j = 0; j < 4; j++) qv[j] = (int)fminf(fmaxf(rintf(__fmul_rn(xs[j], iscale)), -128.0f), 127.0f);
-  }
-  q[(lane & 7) * 8 + (lane >> 3)] = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
-                                    ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
-  const int s = quad_sum(qv[0] + qv[1] + qv[2] + qv[3]);
-  if ((lane & 3) == 0) bs[lane >> 2] = s;
-  if (lane == 0) *d = dv;
-}
-
-__device__ __forceinline__ float amax4(float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); }
 
 // ------------------------------------------------------------------ norm tail
 // Rows [b0, b1) of a NormTail by all NW wavefronts of the workgroup. Wave w takes the
@@ -527,18 +446,6 @@ __device__ __forceinline__ void f32_walk(const Planes &pl, int64_t grow, int64_t
 template <int MT>
 constexpr int f_depth() { return MT <= 2 ? 4 : 2; }
 
-// ------------------------------------------------------------------ greedy-pick keys
-// ------------------------------------------------------------------ greedy-pick keys
-// logits / logit_scale, then the last maximum under f32 total order (max_by(total_cmp),
-// :3661-3671): key = total-order bits as unsigned, packed above the row index so that the
-// larger packed value is the larger logit and, on ties, the higher index.
-__device__ __forceinline__ unsigned long long pick_key(float v, float lscale, int64_t row) {
-  const float x = lscale != 1.0f ? v / lscale : v;
-  const int i = __float_as_int(x);
-  const int k = i ^ (int)(((unsigned)(i >> 31)) >> 1);
-  return ((unsigned long long)((unsigned)k ^ 0x80000000u) << 32) | (unsigned long long)(uint32_t)row;
-}
-
 template <int MT, int NW>
 __device__ __forceinline__ void best_flush(const MVArgs &a, unsigned long long (&bestv)[MT], int m) {
   __shared__ unsigned long long sb[NW][MT];
@@ -830,6 +737,7 @@ __global__ __launch_bounds__(256) void k_embed(TensorView e, const StepRec *st, 
     if (escale != 1.0f) v *= escale;
     out[j] = v;
   }
+  if (!t.nw) return;  // no norm tail: the consumers normalise the row themselves
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   norm_rows<4>(t, b, b + 1);
@@ -975,7 +883,7 @@ __host__ __device__ inline int attn_sub(int nq, int total) {
   return nq <= 16 ? 1 : (nsc + 15) / 16;
 }
 
-template <int HD>
+template <int HD, bool MERGE>
 __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
   using LY = AttnLds<HD>;
@@ -1143,6 +1051,7 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
       if (qi < NQ) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(acc[j][r]), r_o, ((c * ATT_QMAX + qi) * HD + (wave * TPW + j) * 16 + ar) * 4, 0, 16);
     }
   if (tid < 16 && qa + tid < NQ) st_coh2(r_ml, (c * ATT_QMAX + qa + tid) * 8, f2v{rm[tid], rl[tid]});
+  if (!MERGE) return;  // merged by a kernel of its own (one-row decode passes)
 
   // merges of this query tile: the last chunk of each group of ATT_GRP chunks merges the
   // group, the last group merger merges the groups (chunk / group order)
@@ -1724,8 +1633,22 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
 template <int HD>
 static void launch_attn_t(const AttnArgs &a, int nqt, const StepRec *st, hipStream_t s) {
   const size_t sm = AttnLds<HD>::BYTES;
-  SPX_LDS((k_attn<HD>), sm);
-  hipLaunchKernelGGL((k_attn<HD>), dim3(a.nch, a.n_kv, nqt), dim3(256), sm, s, a, st);
+  SPX_LDS((k_attn<HD, true>), sm);
+  hipLaunchKernelGGL((k_attn<HD, true>), dim3(a.nch, a.n_kv, nqt), dim3(256), sm, s, a, st);
+}
+
+hipError_t launch_attention_partials(const AttnArgs &a, const StepRec *st, hipStream_t s) {
+  if (a.n_heads / a.n_kv > 16) return hipErrorInvalidValue;
+  if (a.hd == 128) {
+    SPX_LDS((k_attn<128, false>), AttnLds<128>::BYTES);
+    hipLaunchKernelGGL((k_attn<128, false>), dim3(a.nch, a.n_kv, 1), dim3(256), AttnLds<128>::BYTES, s, a, st);
+  } else if (a.hd == 64) {
+    SPX_LDS((k_attn<64, false>), AttnLds<64>::BYTES);
+    hipLaunchKernelGGL((k_attn<64, false>), dim3(a.nch, a.n_kv, 1), dim3(256), AttnLds<64>::BYTES, s, a, st);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {

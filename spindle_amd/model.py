@@ -222,6 +222,16 @@ class Engine:
         check(lib.spx_engine_set_graphs(h, int(graphs)))
         ctx.adopt(self)
 
+    def set_decode(self, on):
+        """One-token passes on the decode pipeline (True, the default) or the fused pass kernels."""
+        check(lib.spx_engine_set_decode(self.h, int(on)))
+
+    def decode_pipeline(self):
+        """True when one-token passes run on the decode pipeline."""
+        v = C.c_int()
+        check(lib.spx_engine_decode_pipeline(self.h, C.byref(v)))
+        return bool(v.value)
+
     def forward(self, ids, start_pos, hidden=False, logits=False):
         """One pass; returns (argmax [m], hidden [m, dim] or None, logits [m, vocab] or None)."""
         ids = np.ascontiguousarray(ids, np.int32)

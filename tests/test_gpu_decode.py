@@ -1,0 +1,155 @@
+"""The one-row decode pipeline (decode.hip) against the fused pass kernels (fused.hip).
+
+Both compute forward_slice (smollm_chat.rs:3364-3552) with the same operations in the same
+order, so every one-token pass must give the same bits on both: final hidden state, logits,
+greedy pick, KV cache rows and MoE routing statistics. The fused kernels are themselves
+held to the CPU oracle by test_gpu_engine.py; the pipeline is also checked against the oracle
+directly here (teacher-forced, same bars as there)."""
+import numpy as np
+import pytest
+
+from spindle_amd import model as M
+from oracle.model import OracleModel
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+KQ = dict(t_embd=M.Q4K, t_q=M.Q4K, t_k=M.Q4K, t_v=M.Q6K, t_o=M.Q4K, t_gate=M.Q4K, t_up=M.Q4K, t_down=M.Q6K, t_out=M.Q6K)
+CASES = {
+    "moe": M.TINY["tiny-qwen3moe"].replace(sigma=0.05),
+    "moe-prune2": M.TINY["tiny-qwen3moe"].replace(sigma=0.05, moe_prune=2.0),
+    "moe-prune-mass": M.TINY["tiny-qwen3moe"].replace(sigma=0.05, moe_prune=0.3),
+    "dense-kquant": M.TINY["tiny-qwen3"].replace(sigma=0.05, **KQ),
+}
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from spindle_amd import ops
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    c = ops.Context(0)
+    yield c
+    c.close()
+
+
+def _same(a, b):
+    return np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+def test_pipeline_applies_to_kquant_models_only(ctx):
+    for name, want in (("tiny-qwen3moe", True), ("tiny-llama", False), ("tiny-qwen3", False), ("tiny-granite", False)):
+        cfg = M.TINY[name]
+        eng = M.Engine(ctx, cfg, M.synth_model(cfg, seed=3))
+        assert eng.decode_pipeline() == want, name
+        eng.set_decode(False)
+        assert not eng.decode_pipeline()
+        eng.close()
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_decode_pipeline_bitwise(ctx, case):
+    """One-token passes at contexts of one chunk, several 64-position chunks and (for the MoE
+    case) more than 16 chunks, where the merge runs in two levels."""
+    cfg = CASES[case]
+    long_ctx = case == "moe"
+    if long_ctx:
+        cfg = cfg.replace(max_seq=1280)
+    w = M.synth_model(cfg, seed=31)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    assert a.decode_pipeline()
+    b.set_decode(False)
+    assert not b.decode_pipeline()
+    rng = np.random.default_rng(5)
+    n_pre = 1100 if long_ctx else 150
+    ids = rng.integers(0, cfg.vocab, n_pre + 40)
+    checkpoints = [16, 70, 140] + ([1090] if long_ctx else [])
+    pos = 0
+    for cp in checkpoints:
+        while pos < cp:  # prefill (fused kernels in both) up to the checkpoint
+            m = min(16, cp - pos)
+            a.forward(ids[pos:pos + m], pos)
+            b.forward(ids[pos:pos + m], pos)
+            pos += m
+        for _ in range(3):
+            am0, h0, l0 = a.forward(ids[pos:pos + 1], pos, hidden=True, logits=True)
+            am1, h1, l1 = b.forward(ids[pos:pos + 1], pos, hidden=True, logits=True)
+            assert _same(h0, h1), (case, pos, "hidden")
+            assert _same(l0, l1), (case, pos, "logits")
+            assert np.array_equal(am0, am1), (case, pos)
+            pos += 1
+    ka, va = a.kv_cache()
+    kb, vb = b.kv_cache()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    if cfg.moe:
+        assert np.array_equal(a.last_experts(), b.last_experts())
+    a.close()
+    b.close()
+
+
+def test_back_to_back_decode_on_pipeline(ctx):
+    """spx_engine_decode's one-row graph (the pick advances the step record on the device)
+    on the pipeline picks what separate passes on the fused kernels pick."""
+    cfg = CASES["moe"]
+    w = M.synth_model(cfg, seed=32)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    b.set_decode(False)
+    ids = np.arange(20) * 13 % cfg.vocab
+    a.forward(ids[:16], 0)
+    b.forward(ids[:16], 0)
+    got = a.decode(int(ids[16]), 16, 40)
+    tok, want = int(ids[16]), []
+    for i in range(40):
+        am, _, _ = b.forward([tok], 16 + i)
+        tok = int(am[0])
+        want.append(tok)
+    assert got.tolist() == want
+    ka, va = a.kv_cache()
+    kb, vb = b.kv_cache()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    a.close()
+    b.close()
+
+
+def test_toggle_recaptures_graphs(ctx):
+    """Switching pipelines drops the captured one-row graphs; both directions keep the bits."""
+    cfg = CASES["moe"]
+    w = M.synth_model(cfg, seed=33)
+    eng = M.Engine(ctx, cfg, w)
+    ids = np.arange(24) * 3 % cfg.vocab
+    eng.forward(ids[:16], 0)
+    outs = []
+    for on in (True, False, True):
+        eng.set_decode(on)
+        _, h, l = eng.forward(ids[16:17], 16, hidden=True, logits=True)
+        outs.append((h, l))
+    assert all(_same(outs[0][0], o[0]) and _same(outs[0][1], o[1]) for o in outs[1:])
+    eng.close()
+
+
+@pytest.mark.parametrize("case", ["moe", "dense-kquant"])
+def test_decode_pipeline_matches_oracle(ctx, case):
+    """Teacher-forced: the oracle gets the GPU's KV cache before each one-token pass."""
+    cfg = CASES[case]
+    w = M.synth_model(cfg, seed=34)
+    eng = M.Engine(ctx, cfg, w)
+    assert eng.decode_pipeline()
+    om = OracleModel(cfg, w)
+    ids = np.random.default_rng(6).integers(0, cfg.vocab, 48)
+    eng.forward(ids[:16], 0)
+    errs, flips = [], 0
+    for pos in range(16, len(ids)):
+        k, v = eng.kv_cache()
+        om.k_cache[:] = k
+        om.v_cache[:] = v
+        _, _, lg = eng.forward(ids[pos:pos + 1], pos, logits=True)
+        want = om.logits(om.forward(ids[pos:pos + 1], pos))[0].astype(np.float64)
+        e = float(np.max(np.abs(lg[0] - want)) / max(1.0, float(np.max(np.abs(want)))))
+        errs.append(e)
+        if e > 1e-3:  # a Q8_K code moved by one step (see test_gpu_engine.py)
+            assert e <= 5e-2, (case, pos, e)
+            flips += 1
+    print(f"{case}: logits err median {np.median(errs):.1e} max {max(errs):.1e}, flip steps {flips}")
+    assert flips <= 0.15 * len(errs)
+    assert np.median(errs) <= 1e-5
+    eng.close()

@@ -38,8 +38,8 @@ struct DecMVArgs {
   float *xn_out;      // the normalised input row, written by workgroup 0 (null: not written)
 };
 
-// Merge of the attention partials of one pass row: one workgroup per 256 values of the
-// output (256 / head_dim query heads), written as fp32.
+// Merge of the attention partials of one pass row: one workgroup per query head, written as
+// fp32.
 struct DecMergeArgs {
   const float *part_ml, *part_o;  // as AttnArgs
   float *att;

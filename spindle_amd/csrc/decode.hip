@@ -270,22 +270,21 @@ __global__ __launch_bounds__(DEC_NW * 64) void kd_mv(const DecMVArgs a) {
 }
 
 // ------------------------------------------------------------------ attention merge
-// One workgroup per 256 output values (256 / HD query heads of the row). Thread (d, gs):
-// output value d, chunk groups gs, gs + 4, ...: each group of ATT_GRP chunks is merged as the
-// fused kernel's first level does (M = max m_c, w_c = exp(m_c - M), L = sum l_c w_c,
+// One workgroup per query head of the row, 1024 threads. Thread (d, gs): output value d of
+// the head, chunk groups gs, gs + 1024 / HD, ...: each group of ATT_GRP chunks is merged as
+// the fused kernel's first level does (M = max m_c, w_c = exp(m_c - M), L = sum l_c w_c,
 // O = sum w_c o_c in chunk order), then the groups in group order; O / L is the output.
 template <int HD>
 __global__ __launch_bounds__(1024) void kd_merge(const DecMergeArgs a, const StepRec *st) {
-  constexpr int QPB = 256 / HD;
-  __shared__ float sO[ATT_GMAX][256];
-  __shared__ float sM[ATT_GMAX][QPB], sL[ATT_GMAX][QPB];
+  constexpr int NGS = 1024 / HD;
+  __shared__ float sO[ATT_GMAX][HD];
+  __shared__ float sM[ATT_GMAX], sL[ATT_GMAX];
   const int total = st->start + 1, nch = (total + 63) >> 6, ngrp = (nch + ATT_GRP - 1) / ATT_GRP;
-  const int t = threadIdx.x, d = t & 255, gs = t >> 8;
-  const int hq = d / HD, dim = d % HD, head = blockIdx.x * QPB + hq;
+  const int t = threadIdx.x, d = t % HD, gs = t / HD, head = blockIdx.x;
   const int g = a.n_heads / a.n_kv, h = head / g, qi = head % g;
   const float2 *pml = reinterpret_cast<const float2 *>(a.part_ml) + ((int64_t)h * a.nslot) * ATT_QMAX + qi;
-  const float *po = a.part_o + ((int64_t)h * a.nslot * ATT_QMAX + qi) * HD + dim;
-  for (int gi = gs; gi < ngrp; gi += 4) {
+  const float *po = a.part_o + ((int64_t)h * a.nslot * ATT_QMAX + qi) * HD + d;
+  for (int gi = gs; gi < ngrp; gi += NGS) {
     const int s0 = gi * ATT_GRP, n = min(ATT_GRP, nch - s0);
     float2 ml[ATT_GRP];
     float ov[ATT_GRP];
@@ -309,17 +308,17 @@ __global__ __launch_bounds__(1024) void kd_merge(const DecMergeArgs a, const Ste
     for (int k = 0; k < ATT_GRP; k++)
       if (k < n) acc = fmaf(ov[k], w[k], acc);
     sO[gi][d] = acc;
-    if (dim == 0) { sM[gi][hq] = M; sL[gi][hq] = L; }
+    if (d == 0) { sM[gi] = M; sL[gi] = L; }
   }
   __syncthreads();
   if (gs != 0) return;
   float out;
   if (ngrp == 1) {
-    out = sO[0][d] * __fdiv_rn(1.0f, fmaxf(sL[0][hq], 1e-30f));
+    out = sO[0][d] * __fdiv_rn(1.0f, fmaxf(sL[0], 1e-30f));
   } else {
     float mg[ATT_GMAX];
 #pragma unroll
-    for (int k = 0; k < ATT_GMAX; k++) mg[k] = k < ngrp ? sM[k][hq] : -INFINITY;
+    for (int k = 0; k < ATT_GMAX; k++) mg[k] = k < ngrp ? sM[k] : -INFINITY;
     float M = -INFINITY;
 #pragma unroll
     for (int k = 0; k < ATT_GMAX; k++) M = fmaxf(M, mg[k]);
@@ -328,13 +327,13 @@ __global__ __launch_bounds__(1024) void kd_merge(const DecMergeArgs a, const Ste
     for (int k = 0; k < ATT_GMAX; k++) {
       const float w = mg[k] == -INFINITY ? 0.0f : expf(mg[k] - M);
       if (k < ngrp) {
-        L = fmaf(sL[k][hq], w, L);
+        L = fmaf(sL[k], w, L);
         acc = fmaf(sO[k][d], w, acc);
       }
     }
     out = acc * __fdiv_rn(1.0f, fmaxf(L, 1e-30f));
   }
-  a.att[(int64_t)head * HD + dim] = out;
+  a.att[(int64_t)head * HD + d] = out;
 }
 
 // ------------------------------------------------------------------ router
@@ -435,16 +434,16 @@ __device__ __forceinline__ void route_row(const float (&lv)[4], int ne, int nu, 
     if (moe_prune >= 1.0f) keep = min(max((int)moe_prune, min_keep), nu);
     else {
       float top = 0.0f;
-      for (int i = 0; i < nu; i++) top += __shfl(my_p, i);
+      for (int i = 0; i < nu; i++) top += lane_f(my_p, i);
       const float target = top * (1.0f - moe_prune);
       float cum = 0.0f;
       int k = 0;
-      while (k < nu && (k < min_keep || cum < target)) { cum += __shfl(my_p, k); k++; }
+      while (k < nu && (k < min_keep || cum < target)) { cum += lane_f(my_p, k); k++; }
       keep = k;
     }
   }
   wsum = 0.0f;
-  for (int i = 0; i < keep; i++) wsum += __shfl(my_p, i);
+  for (int i = 0; i < keep; i++) wsum += lane_f(my_p, i);
 }
 
 // ------------------------------------------------------------------ gate / up + SwiGLU
@@ -490,7 +489,7 @@ __global__ __launch_bounds__(256) void kd_gateup(const DecGateUpArgs a) {
       if (lane == 0) { gst<int>(a.nkeep, keep); gst<int>(a.njobs, keep); }
     }
     if ((int)blockIdx.y >= keep) return;  // a pruned slot (the same in every wavefront)
-    expert = __builtin_amdgcn_readfirstlane(__shfl(my_e, blockIdx.y));
+    expert = lane_i(my_e, blockIdx.y);
   }
   const int64_t grow = (int64_t)expert * a.gate.rows + (valid ? r : n_ff - 1);
   DRaw raw[NB];
@@ -498,7 +497,9 @@ __global__ __launch_bounds__(256) void kd_gateup(const DecGateUpArgs a) {
   in_quant<NW, KB>(a.in, in, lq, ld, lbs, bsum, nullptr);
   __syncthreads();
   const float res = dot_row<T, NB>(raw, nb, l, lq, ld, lbs);
-  const float u = __shfl_down(res, 32);
+  uint32_t r_lo, r_hi;  // lanes 0-31 get the up rows' results from lanes 32-63
+  xchg32(__float_as_uint(res), r_lo, r_hi);
+  const float u = __uint_as_float(r_hi);
   if (slot < 4 && l == 0 && valid) {
     const float x = res;
     gst<float>(a.h + (int64_t)blockIdx.y * n_ff + r, x / (1.0f + expf(-x)) * u);
@@ -593,10 +594,8 @@ hipError_t launch_dec_mv(const DecMVArgs &a, int grid, hipStream_t s) {
 }
 
 hipError_t launch_dec_merge(const DecMergeArgs &a, const StepRec *st, hipStream_t s) {
-  const int qd = a.n_heads * a.hd;
-  if (qd % 256) return hipErrorInvalidValue;
-  if (a.hd == 128) hipLaunchKernelGGL(kd_merge<128>, dim3(qd / 256), dim3(1024), 0, s, a, st);
-  else if (a.hd == 64) hipLaunchKernelGGL(kd_merge<64>, dim3(qd / 256), dim3(1024), 0, s, a, st);
+  if (a.hd == 128) hipLaunchKernelGGL(kd_merge<128>, dim3(a.n_heads), dim3(1024), 0, s, a, st);
+  else if (a.hd == 64) hipLaunchKernelGGL(kd_merge<64>, dim3(a.n_heads), dim3(1024), 0, s, a, st);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }

@@ -9,6 +9,25 @@ namespace spx {
 // ------------------------------------------------------------------ wave reductions
 #define SPX_DPPF(v, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), (ctrl), 0xF, 0xF, true))
 
+// Exchange across 16-lane rows / 32-lane halves with the gfx950 permlane swaps (VALU ops, no
+// LDS crossbar): with both operands v, lane i ends up holding {v_i, v_(i^16)} (resp. i^32) as
+// the pair (r0, r1), in one order or the other; combined with a commutative operation the
+// result is the butterfly step v_i (op) v_(i^k), bit for bit.
+__device__ __forceinline__ void xchg16(uint32_t v, uint32_t &a, uint32_t &b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  a = r[0];
+  b = r[1];
+}
+__device__ __forceinline__ void xchg32(uint32_t v, uint32_t &a, uint32_t &b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  a = r[0];
+  b = r[1];
+}
+__device__ __forceinline__ float add16(float v) { uint32_t a, b; xchg16(__float_as_uint(v), a, b); return __uint_as_float(a) + __uint_as_float(b); }
+__device__ __forceinline__ float add32(float v) { uint32_t a, b; xchg32(__float_as_uint(v), a, b); return __uint_as_float(a) + __uint_as_float(b); }
+__device__ __forceinline__ float max16(float v) { uint32_t a, b; xchg16(__float_as_uint(v), a, b); return fmaxf(__uint_as_float(a), __uint_as_float(b)); }
+__device__ __forceinline__ float max32(float v) { uint32_t a, b; xchg32(__float_as_uint(v), a, b); return fmaxf(__uint_as_float(a), __uint_as_float(b)); }
+
 // Butterfly sum / max over the 64 lanes; every lane gets the same bits (each step combines
 // a value with its partner's, and fp add / max are commutative).
 __device__ __forceinline__ float wave_sum(float v) {
@@ -16,32 +35,39 @@ __device__ __forceinline__ float wave_sum(float v) {
   v = v + SPX_DPPF(v, 0x4E);
   v = v + SPX_DPPF(v, 0x141);
   v = v + SPX_DPPF(v, 0x140);
-  v = v + __shfl_xor(v, 16);
-  v = v + __shfl_xor(v, 32);
-  return v;
+  v = add16(v);
+  return add32(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, SPX_DPPF(v, 0xB1));
   v = fmaxf(v, SPX_DPPF(v, 0x4E));
   v = fmaxf(v, SPX_DPPF(v, 0x141));
   v = fmaxf(v, SPX_DPPF(v, 0x140));
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  v = max16(v);
+  return max32(v);
 }
 #define SPX_DPP64(v, ctrl)                                                                                         \
   (((unsigned long long)(uint32_t)__builtin_amdgcn_mov_dpp((int)((v) >> 32), (ctrl), 0xF, 0xF, true) << 32) | \
    (unsigned long long)(uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v), (ctrl), 0xF, 0xF, true))
+__device__ __forceinline__ unsigned long long max_u64_x(unsigned long long v, bool x32) {
+  uint32_t la, lb, ha, hb;
+  if (x32) { xchg32((uint32_t)v, la, lb); xchg32((uint32_t)(v >> 32), ha, hb); }
+  else { xchg16((uint32_t)v, la, lb); xchg16((uint32_t)(v >> 32), ha, hb); }
+  const unsigned long long a = ((unsigned long long)ha << 32) | la, b = ((unsigned long long)hb << 32) | lb;
+  return a > b ? a : b;
+}
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
   unsigned long long w;
   w = SPX_DPP64(v, 0xB1); v = w > v ? w : v;
   w = SPX_DPP64(v, 0x4E); v = w > v ? w : v;
   w = SPX_DPP64(v, 0x141); v = w > v ? w : v;
   w = SPX_DPP64(v, 0x140); v = w > v ? w : v;
-  w = __shfl_xor(v, 16); v = w > v ? w : v;
-  w = __shfl_xor(v, 32); v = w > v ? w : v;
-  return v;
+  v = max_u64_x(v, false);
+  return max_u64_x(v, true);
 }
+// Lane i's value of lane src (src wave-uniform).
+__device__ __forceinline__ float lane_f(float v, int src) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src)); }
+__device__ __forceinline__ int lane_i(int v, int src) { return __builtin_amdgcn_readlane(v, src); }
 
 // ------------------------------------------------------------------ cross-workgroup hand-off
 // Values one workgroup leaves for the last workgroup of a launch go through agent-coherent

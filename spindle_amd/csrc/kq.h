@@ -43,10 +43,13 @@ __device__ __forceinline__ int sum8(int v) {
 }
 
 // hsum of quant_q8k.rs:151-158 over the row group's 8 lane accumulators; valid in lane 0.
+// DPP row shifts (lane j reads lane j + n of its 16-lane row; lanes 0-3 of a group read
+// inside their own group): x_l = a_l + a_(l+4), t = x_l + x_(l+2), result t_0 + t_1.
+#define SPX_SHLF(v, n) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x100 + (n), 0xF, 0xF, true))
 __device__ __forceinline__ float hsum_rows8(float a) {
-  const float x = a + __shfl_xor(a, 4);   // x_l = a_l + a_{l+4}
-  const float t = x + __shfl_xor(x, 2);   // lane 0: x0 + x2, lane 1: x1 + x3
-  return t + __shfl_xor(t, 1);            // (x0 + x2) + (x1 + x3)
+  const float x = a + SPX_SHLF(a, 4);   // x_l = a_l + a_{l+4}
+  const float t = x + SPX_SHLF(x, 2);   // lane 0: x0 + x2, lane 1: x1 + x3
+  return t + SPX_SHLF(t, 1);            // (x0 + x2) + (x1 + x3)
 }
 
 // Raw bytes of one block as lane l loads them.

@@ -21,12 +21,14 @@ struct DecIn {
   int cols;
 };
 
-// Integer matvec of one row over up to three tensors (segments) sharing the input.
+// Integer matvec of one row over up to three tensors (segments) sharing the input. Rows are
+// taken in tiles of DEC_MV_NW * R rows (G, R: rp_shape of the blocks per row).
 struct DecMVArgs {
   TensorView w[3];
   float *out[3];      // segment outputs (null: not written)
-  int tiles[3];       // row tiles (NW * 8 rows) of each segment
+  int tiles[3];       // row tiles (DEC_MV_NW * R rows) of each segment
   int nseg;
+  int G;              // row groups per row (rp_shape of the blocks per row)
   DecIn in;
   // residual epilogue (one segment): res_out[r] = res_in[r] + rscale * y[r]
   const float *res_in;
@@ -84,7 +86,7 @@ struct DecDownArgs {
   float rscale;
 };
 
-constexpr int DEC_NW = 4;       // wavefronts per matvec workgroup
+constexpr int DEC_MV_NW = 16;   // wavefronts per matvec workgroup
 constexpr int DEC_MAXNB = 16;   // blocks per row (cols <= 4096) of the decode kernels
 constexpr int DEC_DOWN_Q = 16384;  // n_used * n_ff values of h quantized in LDS by the down kernel
 

@@ -185,24 +185,69 @@ __device__ __forceinline__ void in_quant(const DecIn &in, InRow<KB> &r, SPX_L ui
   }
 }
 
+// ------------------------------------------------------------------ row-parallel block dots
+// A row's nb blocks are spread over the G row groups of its wavefront: group gi takes blocks
+// gi, gi + G, ... (BPG of them, raw bytes in registers) and leaves per block, in the chain
+// buffer cb (LDS), the 8 lane dots as floats, d * xd and the correction term. Then group 0
+// runs the reference's per-lane chain over the blocks in order (acc_l = fma(d * xd,
+// float(P_l), acc_l), corr += term) exactly as kq_walk_tile does: the same fp32 values.
+template <int T, int BPG>
+__device__ __forceinline__ void rp_dots(const DRaw (&raw)[BPG], int nb, int G, int gi, int l, const SPX_L uint32_t *lq, const SPX_L float *ld,
+                                        const SPX_L int2 *lbs, SPX_L float *cbr) {
+#pragma unroll
+  for (int j = 0; j < BPG; j++) {
+    const int i = gi + G * j;
+    if (i < nb) {
+      KQDec<T> dec;
+      dec.decode(draw_kq<T>(raw[j]), l);
+      const uint4 y0 = lld<uint4>(lq + i * 64 + 8 * l), y1 = lld<uint4>(lq + i * 64 + 8 * l + 4);
+      int P, s;
+      dec.dot(y0, y1, lld<int2>(lbs + i * 8 + l), P, s);
+      s = sum8(s);
+      const float xd = ld[i];
+      SPX_L float *e = cbr + i * 10;
+      e[l] = (float)P;
+      if (l == 0) { e[8] = dec.d * xd; e[9] = dec.corr_term(xd, s); }
+    }
+  }
+}
+// The chain over the row's blocks (group 0); the row result in lane 0 of the group.
+__device__ __forceinline__ float rp_chain(const SPX_L float *cbr, int nb, int l) {
+  float acc = 0.0f, cr = 0.0f;
+  for (int i = 0; i < nb; i++) {
+    const SPX_L float *e = cbr + i * 10;
+    acc = fmaf(e[8], e[l], acc);
+    cr = cr + e[9];
+  }
+  return hsum_rows8(acc) - cr;
+}
+
+template <int T, int BPG>
+__device__ __forceinline__ void rp_load(DRaw (&raw)[BPG], const Planes &pl, int64_t grow, int nb, int G, int gi, int l) {
+#pragma unroll
+  for (int j = 0; j < BPG; j++) draw_load<T>(raw[j], pl, grow * nb + min(gi + G * j, nb - 1), l);
+}
+
 // ------------------------------------------------------------------ integer matvec, one row
-// Four wavefronts per workgroup, eight rows per wavefront (row group = 8 lanes, lane l = the
-// reference's lane l), every block of a row in registers. Tiles of 32 rows stride over the
-// grid (the LM head runs on fewer workgroups than tiles). TT = the segments' format, or 0
-// when they differ (then per segment).
-template <int TT, int NB>
-__global__ __launch_bounds__(DEC_NW * 64) void kd_mv(const DecMVArgs a) {
-  constexpr int NW = DEC_NW, KB = DEC_MAXNB / NW;
+// DEC_MV_NW wavefronts per workgroup; a wavefront takes R rows with G row groups each
+// (G * R = 8, G = the power of two >= nb, at most 8), so tiles of DEC_MV_NW * R rows stride
+// over the grid (the LM head runs on fewer workgroups than tiles). TT = the segments' format,
+// or 0 when they differ (then per segment).
+template <int TT, int BPG, int PD>
+__global__ __launch_bounds__(DEC_MV_NW * 64) __attribute__((amdgpu_waves_per_eu(PD == 1 ? 8 : 4))) void kd_mv(const DecMVArgs a) {
+  constexpr int NW = DEC_MV_NW, KB = (DEC_MAXNB + NW - 1) / NW;
   __shared__ __align__(16) uint32_t lq_[DEC_MAXNB * 64];
   __shared__ float ld_[DEC_MAXNB];
   __shared__ __align__(16) int2 lbs_[DEC_MAXNB * 8];
   __shared__ float bsum_[DEC_MAXNB];
+  __shared__ float cb_[NW][8 * 10 * 2];  // per wavefront R * nb <= 16 blocks x 10 floats
   __shared__ unsigned long long sbest[NW];
   SPX_L uint32_t *lq = (SPX_L uint32_t *)lq_;
   SPX_L float *ld = (SPX_L float *)ld_, *bsum = (SPX_L float *)bsum_;
   SPX_L int2 *lbs = (SPX_L int2 *)lbs_;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
-  const int nb = a.in.cols >> 8;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 3, l = lane & 7;
+  const int nb = a.in.cols >> 8, G = a.G, R = 8 / G, r = grp / G, gi = grp - r * G;
+  SPX_L float *cbr = (SPX_L float *)cb_[wave] + r * nb * 10;
   const int t0 = a.tiles[0], t1 = a.nseg > 1 ? a.tiles[1] : 0, t2 = a.nseg > 2 ? a.tiles[2] : 0;
   const int total = t0 + t1 + t2;
   // segment and row of tile t; the segments' fields are all read from the kernel arguments
@@ -214,57 +259,90 @@ __global__ __launch_bounds__(DEC_NW * 64) void kd_mv(const DecMVArgs a) {
   float *const o0 = a.out[0], *const o1 = a.out[1], *const o2 = a.out[2];
   InRow<KB> in;
   in_load<NW, KB>(a.in, in);  // the input row's loads go first
-  DRaw raw[NB];
-  int t = min((int)blockIdx.x, total - 1), si, dt;
-  int64_t row, rows;
-  Planes pl;
-  float *out;
-#define SPX_LOCATE_ISSUE()                                                        \
-  do {                                                                            \
-    si = __builtin_amdgcn_readfirstlane(t >= t0 ? (t >= t0 + t1 ? 2 : 1) : 0);    \
-    const int tt = t - (si > 0 ? t0 : 0) - (si > 1 ? t1 : 0);                     \
-    row = ((int64_t)tt * NW + wave) * 8 + slot;                                   \
-    rows = si == 0 ? rw0 : si == 1 ? rw1 : rw2;                                   \
-    dt = si == 0 ? dt0 : si == 1 ? dt1 : dt2;                                     \
-    out = si == 0 ? o0 : si == 1 ? o1 : o2;                                       \
-    pl.p0 = si == 0 ? pl0.p0 : si == 1 ? pl1.p0 : pl2.p0;                         \
-    pl.p1 = si == 0 ? pl0.p1 : si == 1 ? pl1.p1 : pl2.p1;                         \
-    pl.p2 = si == 0 ? pl0.p2 : si == 1 ? pl1.p2 : pl2.p2;                         \
-    pl.p3 = si == 0 ? pl0.p3 : si == 1 ? pl1.p3 : pl2.p3;                         \
-    const int64_t grow = row < rows ? row : rows - 1;                             \
-    if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) draw_row<T_Q4K, NB>(raw, pl, grow, nb, l); \
-    else draw_row<T_Q6K, NB>(raw, pl, grow, nb, l);                               \
-  } while (0)
-  SPX_LOCATE_ISSUE();
-  in_quant<NW, KB>(a.in, in, lq, ld, lbs, bsum, blockIdx.x == 0 ? a.xn_out : nullptr);
-  __syncthreads();
   unsigned long long bestk = 0;
-  const bool live = (int)blockIdx.x < total;
-  while (live) {
-    float res;
-    if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) res = dot_row<T_Q4K, NB>(raw, nb, l, lq, ld, lbs);
-    else res = dot_row<T_Q6K, NB>(raw, nb, l, lq, ld, lbs);
-    if (l == 0 && row < rows) {
-      if (out) gst<float>(out + row, res);
-      if (a.res_out) gst<float>(a.res_out + row, gld<float>(a.res_in + row) + a.rscale * res);
-      if (a.best) {
-        const unsigned long long k = pick_key(res, a.lscale, row);
-        bestk = k > bestk ? k : bestk;
+  if constexpr (PD == 1) {
+    DRaw raw[BPG];
+    const int t = min((int)blockIdx.x, total - 1);
+    const int si = __builtin_amdgcn_readfirstlane(t >= t0 ? (t >= t0 + t1 ? 2 : 1) : 0);
+    const int tt = t - (si > 0 ? t0 : 0) - (si > 1 ? t1 : 0);
+    const int64_t row = ((int64_t)tt * NW + wave) * R + r;
+    const int64_t rows = si == 0 ? rw0 : si == 1 ? rw1 : rw2;
+    const int dt = si == 0 ? dt0 : si == 1 ? dt1 : dt2;
+    float *const out = si == 0 ? o0 : si == 1 ? o1 : o2;
+    Planes pl;
+    pl.p0 = si == 0 ? pl0.p0 : si == 1 ? pl1.p0 : pl2.p0;
+    pl.p1 = si == 0 ? pl0.p1 : si == 1 ? pl1.p1 : pl2.p1;
+    pl.p2 = si == 0 ? pl0.p2 : si == 1 ? pl1.p2 : pl2.p2;
+    pl.p3 = si == 0 ? pl0.p3 : si == 1 ? pl1.p3 : pl2.p3;
+    const int64_t grow = row < rows ? row : rows - 1;
+    if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) rp_load<T_Q4K, BPG>(raw, pl, grow, nb, G, gi, l);
+    else rp_load<T_Q6K, BPG>(raw, pl, grow, nb, G, gi, l);
+    in_quant<NW, KB>(a.in, in, lq, ld, lbs, bsum, blockIdx.x == 0 ? a.xn_out : nullptr);
+    __syncthreads();
+    if ((int)blockIdx.x < total) {
+      if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) rp_dots<T_Q4K, BPG>(raw, nb, G, gi, l, lq, ld, lbs, cbr);
+      else rp_dots<T_Q6K, BPG>(raw, nb, G, gi, l, lq, ld, lbs, cbr);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the chain buffer is written
+      __builtin_amdgcn_wave_barrier();
+      if (gi == 0) {
+        const float res = rp_chain(cbr, nb, l);
+        if (l == 0 && row < rows) {
+          if (out) gst<float>(out + row, res);
+          if (a.res_out) gst<float>(a.res_out + row, gld<float>(a.res_in + row) + a.rscale * res);
+          if (a.best) bestk = pick_key(res, a.lscale, row);
+        }
       }
     }
-    t += gridDim.x;
-    if (t >= total) break;
-    SPX_LOCATE_ISSUE();
+  } else {
+    // one segment (TT fixed), tiles blockIdx.x + k * gridDim.x; PD tiles' weights in flight
+    static_assert(TT == T_Q4K || TT == T_Q6K, "prefetched launches take one format");
+    DRaw raw[PD][BPG];
+    const int64_t rows = rw0;
+    const int g = gridDim.x;
+    auto row_of = [&](int t) { return ((int64_t)t * NW + wave) * R + r; };
+#pragma unroll
+    for (int k = 0; k < PD; k++) {
+      const int64_t row = row_of(min((int)blockIdx.x + k * g, total - 1));
+      rp_load<TT, BPG>(raw[k], pl0, row < rows ? row : rows - 1, nb, G, gi, l);
+    }
+    in_quant<NW, KB>(a.in, in, lq, ld, lbs, bsum, blockIdx.x == 0 ? a.xn_out : nullptr);
+    __syncthreads();
+    for (int t = blockIdx.x; t < total;) {
+#pragma unroll
+      for (int k = 0; k < PD; k++) {
+        if (t < total) {
+          rp_dots<TT, BPG>(raw[k], nb, G, gi, l, lq, ld, lbs, cbr);
+          const int64_t nrow = row_of(min(t + PD * g, total - 1));
+          rp_load<TT, BPG>(raw[k], pl0, nrow < rows ? nrow : rows - 1, nb, G, gi, l);  // tile t + PD * g
+          __builtin_amdgcn_s_waitcnt(0xc07f);
+          __builtin_amdgcn_wave_barrier();
+          const int64_t row = row_of(t);
+          if (gi == 0) {
+            const float res = rp_chain(cbr, nb, l);
+            if (l == 0 && row < rows) {
+              if (o0) gst<float>(o0 + row, res);
+              if (a.res_out) gst<float>(a.res_out + row, gld<float>(a.res_in + row) + a.rscale * res);
+              if (a.best) {
+                const unsigned long long key = pick_key(res, a.lscale, row);
+                bestk = key > bestk ? key : bestk;
+              }
+            }
+          }
+          __builtin_amdgcn_s_waitcnt(0xc07f);
+          __builtin_amdgcn_wave_barrier();  // the chain buffer is refilled by the next tile
+        }
+        t += g;
+      }
+    }
   }
-#undef SPX_LOCATE_ISSUE
   if (a.best) {
     const unsigned long long b = wave_max_u64(bestk);
     if (lane == 0) sbest[wave] = b;
     __syncthreads();
     if (threadIdx.x == 0) {
-      unsigned long long r = sbest[0];
-      for (int w = 1; w < NW; w++) r = sbest[w] > r ? sbest[w] : r;
-      gst<unsigned long long>(a.best + blockIdx.x, r);
+      unsigned long long rb = sbest[0];
+      for (int w = 1; w < NW; w++) rb = sbest[w] > rb ? sbest[w] : rb;
+      gst<unsigned long long>(a.best + blockIdx.x, rb);
     }
   }
 }
@@ -297,16 +375,15 @@ __global__ __launch_bounds__(1024) void kd_merge(const DecMergeArgs a, const Ste
     float M = -INFINITY;
 #pragma unroll
     for (int k = 0; k < ATT_GRP; k++) M = fmaxf(M, ml[k].x);
-    float w[ATT_GRP], L = 0.0f;
+    float L = 0.0f, acc = 0.0f;
 #pragma unroll
     for (int k = 0; k < ATT_GRP; k++) {
-      w[k] = ml[k].x == -INFINITY ? 0.0f : expf(ml[k].x - M);
-      if (k < n) L = fmaf(ml[k].y, w[k], L);
+      if (k < n) {  // chunks past n (padding: weight 0) are skipped
+        const float w = ml[k].x == -INFINITY ? 0.0f : expf(ml[k].x - M);
+        L = fmaf(ml[k].y, w, L);
+        acc = fmaf(ov[k], w, acc);
+      }
     }
-    float acc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < ATT_GRP; k++)
-      if (k < n) acc = fmaf(ov[k], w[k], acc);
     sO[gi][d] = acc;
     if (d == 0) { sM[gi] = M; sL[gi] = L; }
   }
@@ -316,20 +393,13 @@ __global__ __launch_bounds__(1024) void kd_merge(const DecMergeArgs a, const Ste
   if (ngrp == 1) {
     out = sO[0][d] * __fdiv_rn(1.0f, fmaxf(sL[0], 1e-30f));
   } else {
-    float mg[ATT_GMAX];
-#pragma unroll
-    for (int k = 0; k < ATT_GMAX; k++) mg[k] = k < ngrp ? sM[k] : -INFINITY;
     float M = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < ATT_GMAX; k++) M = fmaxf(M, mg[k]);
+    for (int k = 0; k < ngrp; k++) M = fmaxf(M, sM[k]);
     float L = 0.0f, acc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < ATT_GMAX; k++) {
-      const float w = mg[k] == -INFINITY ? 0.0f : expf(mg[k] - M);
-      if (k < ngrp) {
-        L = fmaf(sL[k], w, L);
-        acc = fmaf(sO[k][d], w, acc);
-      }
+    for (int k = 0; k < ngrp; k++) {
+      const float w = sM[k] == -INFINITY ? 0.0f : expf(sM[k] - M);
+      L = fmaf(sL[k], w, L);
+      acc = fmaf(sO[k][d], w, acc);
     }
     out = acc * __fdiv_rn(1.0f, fmaxf(L, 1e-30f));
   }
@@ -447,26 +517,31 @@ __device__ __forceinline__ void route_row(const float (&lv)[4], int ne, int nu, 
 }
 
 // ------------------------------------------------------------------ gate / up + SwiGLU
-// Grid (n_ff / 16, n_used): workgroup (x, s) computes rows 16x .. 16x+15 of h for chosen slot
-// s; in each wavefront row groups 0-3 take gate rows r..r+3 and 4-7 the same rows of up.
-// h[s][r] = silu(g) * u (silu :586-588). Every wavefront routes the row itself; workgroup
-// (0, 0) publishes the routing for kd_down (chosen experts, weights, kept count).
-template <int T, int NB>
-__global__ __launch_bounds__(256) void kd_gateup(const DecGateUpArgs a) {
-  constexpr int NW = 4, KB = DEC_MAXNB / NW;
+// Grid (n_ff / DEC_MV_NW, n_used): workgroup (x, s) computes rows DEC_MV_NW * x .. of h for
+// chosen slot s, one row per wavefront: lanes 0-31 take the gate row, 32-63 the up row, four
+// row groups each (blocks gi, gi + 4, ...), chains as rp_chain. h[s][r] = silu(g) * u (silu
+// :586-588). Wavefront 0 routes the row; workgroup (0, 0) publishes the routing for kd_down
+// (chosen experts, weights, kept count).
+template <int T, int BPG>
+__global__ __launch_bounds__(DEC_MV_NW * 64) void kd_gateup(const DecGateUpArgs a) {
+  constexpr int NW = DEC_MV_NW, KB = (DEC_MAXNB + NW - 1) / NW;
   __shared__ __align__(16) uint32_t lq_[DEC_MAXNB * 64];
   __shared__ float ld_[DEC_MAXNB];
   __shared__ __align__(16) int2 lbs_[DEC_MAXNB * 8];
   __shared__ float bsum_[DEC_MAXNB];
+  __shared__ float cb_[NW][2 * DEC_MAXNB * 10];
+  __shared__ int s_route[2];
   SPX_L uint32_t *lq = (SPX_L uint32_t *)lq_;
   SPX_L float *ld = (SPX_L float *)ld_, *bsum = (SPX_L float *)bsum_;
   SPX_L int2 *lbs = (SPX_L int2 *)lbs_;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 3, l = lane & 7;
+  const int half = grp >> 2, gi = grp & 3;  // half 0: gate row, 1: up row
   const int n_ff = a.n_ff, nb = a.in.cols >> 8;
-  const int r = blockIdx.x * 16 + wave * 4 + (slot & 3);
+  const int r = blockIdx.x * NW + wave;
   const bool valid = r < n_ff;
+  SPX_L float *cbr = (SPX_L float *)cb_[wave] + half * nb * 10;
   float lv[4];
-  if (a.logits) {
+  if (a.logits && wave == 0) {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int e = lane + 64 * k;
@@ -477,30 +552,37 @@ __global__ __launch_bounds__(256) void kd_gateup(const DecGateUpArgs a) {
   in_load<NW, KB>(a.in, in);
   int expert = 0;
   if (a.logits) {
-    int my_e, keep;
-    float my_p, wsum;
-    route_row(lv, a.n_expert, a.n_used, a.moe_prune, my_e, my_p, keep, wsum);
-    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
-      if (lane < keep) {
-        gst<int>(a.chosen + lane, my_e);
-        gst<float>(a.weights + lane, a.norm ? my_p / wsum : my_p);
-        if (a.expert_count) gst<int>(a.expert_count + my_e, gld<int>(a.expert_count + my_e) + 1);
+    if (wave == 0) {
+      int my_e, keep;
+      float my_p, wsum;
+      route_row(lv, a.n_expert, a.n_used, a.moe_prune, my_e, my_p, keep, wsum);
+      if (blockIdx.x == 0 && blockIdx.y == 0) {
+        if (lane < keep) {
+          gst<int>(a.chosen + lane, my_e);
+          gst<float>(a.weights + lane, a.norm ? my_p / wsum : my_p);
+          if (a.expert_count) gst<int>(a.expert_count + my_e, gld<int>(a.expert_count + my_e) + 1);
+        }
+        if (lane == 0) { gst<int>(a.nkeep, keep); gst<int>(a.njobs, keep); }
       }
-      if (lane == 0) { gst<int>(a.nkeep, keep); gst<int>(a.njobs, keep); }
+      if (lane == 0) { s_route[0] = lane_i(my_e, blockIdx.y); s_route[1] = keep; }
     }
-    if ((int)blockIdx.y >= keep) return;  // a pruned slot (the same in every wavefront)
-    expert = lane_i(my_e, blockIdx.y);
+    __syncthreads();
+    if ((int)blockIdx.y >= s_route[1]) return;  // a pruned slot (the whole workgroup)
+    expert = s_route[0];
   }
   const int64_t grow = (int64_t)expert * a.gate.rows + (valid ? r : n_ff - 1);
-  DRaw raw[NB];
-  draw_row<T, NB>(raw, slot < 4 ? a.gate.pl : a.up.pl, grow, nb, l);
+  DRaw raw[BPG];
+  rp_load<T, BPG>(raw, half ? a.up.pl : a.gate.pl, grow, nb, 4, gi, l);
   in_quant<NW, KB>(a.in, in, lq, ld, lbs, bsum, nullptr);
   __syncthreads();
-  const float res = dot_row<T, NB>(raw, nb, l, lq, ld, lbs);
-  uint32_t r_lo, r_hi;  // lanes 0-31 get the up rows' results from lanes 32-63
+  rp_dots<T, BPG>(raw, nb, 4, gi, l, lq, ld, lbs, cbr);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the chain buffer is written
+  __builtin_amdgcn_wave_barrier();
+  const float res = gi == 0 ? rp_chain(cbr, nb, l) : 0.0f;
+  uint32_t r_lo, r_hi;  // lanes 0-31 get the up row's result from lanes 32-63
   xchg32(__float_as_uint(res), r_lo, r_hi);
   const float u = __uint_as_float(r_hi);
-  if (slot < 4 && l == 0 && valid) {
+  if (lane == 0 && valid) {
     const float x = res;
     gst<float>(a.h + (int64_t)blockIdx.y * n_ff + r, x / (1.0f + expf(-x)) * u);
   }
@@ -567,20 +649,29 @@ static int nb_bucket(int nb) { return nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 3 ? 3 : 
 
 template <int TT>
 static hipError_t dec_mv_tt(const DecMVArgs &a, int grid, hipStream_t s) {
-  switch (nb_bucket(a.in.cols >> 8)) {
-  case 1: hipLaunchKernelGGL((kd_mv<TT, 1>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
-  case 2: hipLaunchKernelGGL((kd_mv<TT, 2>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
-  case 3: hipLaunchKernelGGL((kd_mv<TT, 3>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
-  case 4: hipLaunchKernelGGL((kd_mv<TT, 4>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
-  case 8: hipLaunchKernelGGL((kd_mv<TT, 8>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
-  default: hipLaunchKernelGGL((kd_mv<TT, 16>), dim3(grid), dim3(DEC_NW * 64), 0, s, a); break;
+  const int nb = a.in.cols >> 8, bpg = (nb + a.G - 1) / a.G;
+  const int total = a.tiles[0] + (a.nseg > 1 ? a.tiles[1] : 0) + (a.nseg > 2 ? a.tiles[2] : 0);
+  const dim3 b(DEC_MV_NW * 64);
+  if constexpr (TT != 0) {
+    if (grid < total) {  // tiles stride over the grid: four (two) tiles' weights in flight
+      if (a.nseg != 1) return hipErrorInvalidValue;
+      if (bpg == 1) hipLaunchKernelGGL((kd_mv<TT, 1, 4>), dim3(grid), b, 0, s, a);
+      else hipLaunchKernelGGL((kd_mv<TT, 2, 2>), dim3(grid), b, 0, s, a);
+      return hipGetLastError();
+    }
   }
+  if (grid != total) return hipErrorInvalidValue;
+  if (bpg == 1) hipLaunchKernelGGL((kd_mv<TT, 1, 1>), dim3(grid), b, 0, s, a);
+  else hipLaunchKernelGGL((kd_mv<TT, 2, 1>), dim3(grid), b, 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_dec_mv(const DecMVArgs &a, int grid, hipStream_t s) {
   const int nb = a.in.cols >> 8;
   if (a.nseg < 1 || a.nseg > 3 || grid < 1 || nb < 1 || nb > DEC_MAXNB || a.in.cols % 256) return hipErrorInvalidValue;
+  int G, R;
+  rp_shape(nb, G, R);
+  if (a.G != G) return hipErrorInvalidValue;
   bool all4 = true, all6 = true;
   for (int i = 0; i < a.nseg; i++) {
     if (a.w[i].dtype != T_Q4K && a.w[i].dtype != T_Q6K) return hipErrorInvalidValue;
@@ -608,14 +699,10 @@ hipError_t launch_dec_router(const DecRouterArgs &a, hipStream_t s) {
 
 template <int T>
 static hipError_t dec_gu_t(const DecGateUpArgs &a, dim3 grid, hipStream_t s) {
-  switch (nb_bucket(a.in.cols >> 8)) {
-  case 1: hipLaunchKernelGGL((kd_gateup<T, 1>), grid, dim3(256), 0, s, a); break;
-  case 2: hipLaunchKernelGGL((kd_gateup<T, 2>), grid, dim3(256), 0, s, a); break;
-  case 3: hipLaunchKernelGGL((kd_gateup<T, 3>), grid, dim3(256), 0, s, a); break;
-  case 4: hipLaunchKernelGGL((kd_gateup<T, 4>), grid, dim3(256), 0, s, a); break;
-  case 8: hipLaunchKernelGGL((kd_gateup<T, 8>), grid, dim3(256), 0, s, a); break;
-  default: hipLaunchKernelGGL((kd_gateup<T, 16>), grid, dim3(256), 0, s, a); break;
-  }
+  const int bpg = ((a.in.cols >> 8) + 3) / 4;
+  if (bpg == 1) hipLaunchKernelGGL((kd_gateup<T, 1>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
+  else if (bpg == 2) hipLaunchKernelGGL((kd_gateup<T, 2>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
+  else hipLaunchKernelGGL((kd_gateup<T, 4>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
@@ -623,7 +710,7 @@ hipError_t launch_dec_gateup(const DecGateUpArgs &a, hipStream_t s) {
   const int nb = a.in.cols >> 8;
   if (a.in.cols % 256 || nb > DEC_MAXNB || a.gate.nb != nb || a.up.nb != nb || a.gate.dtype != a.up.dtype || !a.in.nw) return hipErrorInvalidValue;
   if (a.logits && (a.n_expert < 1 || a.n_expert > 256 || a.n_used < 1 || a.n_used > 32 || a.n_used > a.n_expert)) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((a.n_ff + 15) / 16), a.logits ? (unsigned)a.n_used : 1u);
+  const dim3 grid((unsigned)((a.n_ff + DEC_MV_NW - 1) / DEC_MV_NW), a.logits ? (unsigned)a.n_used : 1u);
   if (a.gate.dtype == T_Q4K) return dec_gu_t<T_Q4K>(a, grid, s);
   if (a.gate.dtype == T_Q6K) return dec_gu_t<T_Q6K>(a, grid, s);
   return hipErrorInvalidValue;

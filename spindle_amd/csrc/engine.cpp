@@ -58,6 +58,7 @@ struct spx_engine {
   spx_ctx *ctx = nullptr;
   spx_model_config c{};
   int q_dim = 0, kv_dim = 0, n_ff = 0, nch = 1, lm_grid = 2048, nbest = 1;
+  int lm_dec_grid = 256;  // decode pipeline: LM head workgroups (SPX_LM_DEC_GRID), one per CU
   int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
@@ -366,7 +367,12 @@ int enqueue_decode(spx_engine *E, bool advance) {
   const auto &c = E->c;
   hipStream_t s = E->ctx->stream;
   const int dim = c.dim, hd = c.head_dim;
-  auto tiles = [](int64_t rows) { return (int)((rows + DEC_NW * 8 - 1) / (DEC_NW * 8)); };
+  auto tiles = [](const spx_tensor *t) {
+    int G, R;
+    rp_shape(t->v.nb, G, R);
+    return (int)((t->v.rows + DEC_MV_NW * R - 1) / (DEC_MV_NW * R));
+  };
+  auto gshape = [](const spx_tensor *t) { int G, R; rp_shape(t->v.nb, G, R); return G; };
   {
     ProfScope ps(E, PC_EMBED, 0);
     NormTail t{};
@@ -382,8 +388,9 @@ int enqueue_decode(spx_engine *E, bool advance) {
       const spx_tensor *w3[3] = {ly.wq, ly.wk, ly.wv};
       float *o3[3] = {E->q, E->k, E->v};
       int total = 0;
-      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.tiles[i] = tiles(w3[i]->v.rows); total += a.tiles[i]; }
+      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.tiles[i] = tiles(w3[i]); total += a.tiles[i]; }
       a.nseg = 3;
+      a.G = gshape(ly.wq);
       a.in = DecIn{E->xA, ly.attn_norm, c.rms_eps, dim};
       SPX_HIP(launch_dec_mv(a, total, s));
     }
@@ -403,7 +410,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
     {
       ProfScope ps(E, PC_WO, wbytes(ly.wo));
       DecMVArgs a{};
-      a.w[0] = ly.wo->v; a.out[0] = E->proj; a.tiles[0] = tiles(ly.wo->v.rows); a.nseg = 1;
+      a.w[0] = ly.wo->v; a.out[0] = E->proj; a.tiles[0] = tiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
       a.in = DecIn{E->att, nullptr, 0.0f, E->q_dim};
       a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
       SPX_HIP(launch_dec_mv(a, a.tiles[0], s));
@@ -438,7 +445,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down));
         DecMVArgs a{};
-        a.w[0] = ly.down->v; a.out[0] = E->ffn; a.tiles[0] = tiles(ly.down->v.rows); a.nseg = 1;
+        a.w[0] = ly.down->v; a.out[0] = E->ffn; a.tiles[0] = tiles(ly.down); a.nseg = 1; a.G = gshape(ly.down);
         a.in = DecIn{E->h, nullptr, 0.0f, nff};
         a.res_in = E->xB; a.res_out = E->xA; a.rscale = c.residual_scale;
         SPX_HIP(launch_dec_mv(a, a.tiles[0], s));
@@ -449,10 +456,10 @@ int enqueue_decode(spx_engine *E, bool advance) {
   {
     ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
     DecMVArgs a{};
-    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.tiles[0] = tiles(E->lm_head->v.rows); a.nseg = 1;
+    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.tiles[0] = tiles(E->lm_head); a.nseg = 1; a.G = gshape(E->lm_head);
     a.in = DecIn{E->xA, E->out_norm, c.rms_eps, dim};
     a.best = E->best; a.lscale = c.logit_scale; a.xn_out = E->xn;
-    grid = std::min(a.tiles[0], E->lm_grid);
+    grid = std::min(a.tiles[0], E->lm_dec_grid);
     SPX_HIP(launch_dec_mv(a, grid, s));
   }
   E->nbest = grid;
@@ -513,6 +520,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   E->L.resize(c.n_layers);
   E->nch = (c.max_seq + 63) / 64;
   if (const char *v = std::getenv("SPX_LM_GRID")) E->lm_grid = std::max(1, atoi(v));
+  if (const char *v = std::getenv("SPX_LM_DEC_GRID")) E->lm_dec_grid = std::max(1, std::min(atoi(v), 2048));
   if (const char *v = std::getenv("SPX_MV_MODE")) E->mv_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_LM_MODE")) E->lm_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_TAIL_MAX")) E->tail_max = std::max(0, std::min(MAX_M, atoi(v)));

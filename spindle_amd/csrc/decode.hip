@@ -357,20 +357,35 @@ __global__ __launch_bounds__(1024) void kd_merge(const DecMergeArgs a, const Ste
   constexpr int NGS = 1024 / HD;
   __shared__ float sO[ATT_GMAX][HD];
   __shared__ float sM[ATT_GMAX], sL[ATT_GMAX];
-  const int total = st->start + 1, nch = (total + 63) >> 6, ngrp = (nch + ATT_GRP - 1) / ATT_GRP;
   const int t = threadIdx.x, d = t % HD, gs = t / HD, head = blockIdx.x;
   const int g = a.n_heads / a.n_kv, h = head / g, qi = head % g;
   const float2 *pml = reinterpret_cast<const float2 *>(a.part_ml) + ((int64_t)h * a.nslot) * ATT_QMAX + qi;
   const float *po = a.part_o + ((int64_t)h * a.nslot * ATT_QMAX + qi) * HD + d;
+  // group gs's slots are requested before the step record arrives (slots past the pass's
+  // chunks hold earlier values, never used)
+  float2 ml0[ATT_GRP];
+  float ov0[ATT_GRP];
+#pragma unroll
+  for (int k = 0; k < ATT_GRP; k++) {
+    const int c = min(gs * ATT_GRP + k, a.nslot - 1);
+    ml0[k] = pml[(int64_t)c * ATT_QMAX];
+    ov0[k] = po[(int64_t)c * ATT_QMAX * HD];
+  }
+  const int total = st->start + 1, nch = (total + 63) >> 6, ngrp = (nch + ATT_GRP - 1) / ATT_GRP;
   for (int gi = gs; gi < ngrp; gi += NGS) {
     const int s0 = gi * ATT_GRP, n = min(ATT_GRP, nch - s0);
     float2 ml[ATT_GRP];
     float ov[ATT_GRP];
 #pragma unroll
     for (int k = 0; k < ATT_GRP; k++) {
-      const int c = s0 + min(k, n - 1);
-      ml[k] = k < n ? pml[(int64_t)c * ATT_QMAX] : make_float2(-INFINITY, 0.0f);
-      ov[k] = po[(int64_t)c * ATT_QMAX * HD];
+      if (gi == gs) {
+        ml[k] = k < n ? ml0[k] : make_float2(-INFINITY, 0.0f);
+        ov[k] = ov0[k];
+      } else {
+        const int c = s0 + min(k, n - 1);
+        ml[k] = k < n ? pml[(int64_t)c * ATT_QMAX] : make_float2(-INFINITY, 0.0f);
+        ov[k] = po[(int64_t)c * ATT_QMAX * HD];
+      }
     }
     float M = -INFINITY;
 #pragma unroll

@@ -911,22 +911,77 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
   const int da = a.neox ? lane : 2 * lane, db = a.neox ? lane + half : 2 * lane + 1;
   const int ar = lane & 15, kg = (lane >> 4) * 4;  // MFMA operand row / column, k offset
 
-  // K/V of the first sub-chunk in flight while the queries are prepared
+  // K/V of the first sub-chunk in flight while the queries are prepared (one-row passes: the
+  // chunk's rows, clamped to the cache, need not wait for the step record)
   const int lp = tid >> 2, lq = tid & 3;
   uint32_t kr[4 * NU], vr[4 * NU];
-  attn_kv_load<NU>(a, cache0 + (int64_t)min(p_lo + lp, p_hi - 1) * a.kv_dim + lq * DQ, kr, vr);
+  attn_kv_load<NU>(a, cache0 + (int64_t)min(p_lo + lp, MERGE ? p_hi - 1 : a.max_seq - 1) * a.kv_dim + lq * DQ, kr, vr);
   // queries of this tile -> LDS as hi / lo f16 (rows past NQ are zero)
-  for (int r = wave; r < 16; r += 4) {
-    const int qi = qa + r;
-    float e0 = 0.0f, e1 = 0.0f;
-    if (qi < NQ) {
-      const int b = qi / g, head = h * g + qi % g;
-      head_prep(a.q + (int64_t)b * a.n_heads * HD + head * HD, a.q_bias ? a.q_bias + head * HD : nullptr, a.q_norm,
-                a.rope + (int64_t)(start + b) * half, HD, a.neox, a.eps, e0, e1);
+  float nk_x[2] = {0.0f, 0.0f}, nv_x[2] = {0.0f, 0.0f}, nk_w[2] = {0.0f, 0.0f}, rc = 1.0f, rs = 0.0f;
+  if constexpr (!MERGE) {
+    // one-row pass: NQ = g <= 8 query rows, wavefront w takes rows w and w + 4; every load is
+    // issued before the first reduction (head_prep's arithmetic, operation for operation)
+    float x0[2], x1[2], n0 = 0.0f, n1 = 0.0f, c0[2], s0[2];
+    const bool act = lane < half;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int qi = min(wave + 4 * j, NQ - 1), head = h * g + qi;
+      const float *src = a.q + head * HD;
+      x0[j] = act ? src[da] : 0.0f;
+      x1[j] = act ? src[db] : 0.0f;
+      if (a.q_bias && act) { x0[j] += a.q_bias[head * HD + da]; x1[j] += a.q_bias[head * HD + db]; }
     }
-    if (lane < half) {
-      split_f16(e0, qh[r * QS + da], ql[r * QS + da]);
-      split_f16(e1, qh[r * QS + db], ql[r * QS + db]);
+    if (a.q_norm && act) { n0 = a.q_norm[da]; n1 = a.q_norm[db]; }
+    // the pass row's new K / V values (wavefront 0 normalises them if its chunk holds them)
+    if (wave == 0 && act) {
+      nk_x[0] = a.k[h * HD + da]; nk_x[1] = a.k[h * HD + db];
+      nv_x[0] = a.v[h * HD + da]; nv_x[1] = a.v[h * HD + db];
+      if (a.k_bias) { nk_x[0] += a.k_bias[h * HD + da]; nk_x[1] += a.k_bias[h * HD + db]; }
+      if (a.v_bias) { nv_x[0] += a.v_bias[h * HD + da]; nv_x[1] += a.v_bias[h * HD + db]; }
+      if (a.k_norm) { nk_w[0] = a.k_norm[da]; nk_w[1] = a.k_norm[db]; }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      c0[j] = 1.0f; s0[j] = 0.0f;
+      if (act) { const float2 cs = a.rope[(int64_t)start * half + lane]; c0[j] = cs.x; s0[j] = cs.y; }
+    }
+    rc = c0[0];
+    rs = s0[0];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int r = wave + 4 * j;
+      float e0 = x0[j], e1 = x1[j];
+      if (a.q_norm) {
+        const float ssq = wave_sum(fmaf(e0, e0, e1 * e1));
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ssq, (float)HD) + a.eps));
+        if (act) { e0 = e0 * inv * n0; e1 = e1 * inv * n1; }
+      }
+      if (act) {
+        const float r0 = e0 * c0[j] - e1 * s0[j], r1 = e0 * s0[j] + e1 * c0[j];
+        e0 = r0;
+        e1 = r1;
+      }
+      if (r >= NQ) { e0 = 0.0f; e1 = 0.0f; }
+      if (act) {
+        split_f16(e0, qh[r * QS + da], ql[r * QS + da]);
+        split_f16(e1, qh[r * QS + db], ql[r * QS + db]);
+        split_f16(0.0f, qh[(r + 8) * QS + da], ql[(r + 8) * QS + da]);
+        split_f16(0.0f, qh[(r + 8) * QS + db], ql[(r + 8) * QS + db]);
+      }
+    }
+  } else {
+    for (int r = wave; r < 16; r += 4) {
+      const int qi = qa + r;
+      float e0 = 0.0f, e1 = 0.0f;
+      if (qi < NQ) {
+        const int b = qi / g, head = h * g + qi % g;
+        head_prep(a.q + (int64_t)b * a.n_heads * HD + head * HD, a.q_bias ? a.q_bias + head * HD : nullptr, a.q_norm,
+                  a.rope + (int64_t)(start + b) * half, HD, a.neox, a.eps, e0, e1);
+      }
+      if (lane < half) {
+        split_f16(e0, qh[r * QS + da], ql[r * QS + da]);
+        split_f16(e1, qh[r * QS + db], ql[r * QS + db]);
+      }
     }
   }
   if (tid < 16) { rm[tid] = -INFINITY; rl[tid] = 0.0f; }
@@ -954,7 +1009,33 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
     }
     if (s0 + 64 < p_hi) attn_kv_load<NU>(a, cache0 + (int64_t)min(s0 + 64 + lp, p_hi - 1) * a.kv_dim + lq * DQ, kr, vr);
     // this pass's K/V rows in the sub-chunk: normed / rotated here, to the cache by tile 0
-    for (int b = wave; b < m; b += 4) {
+    if (!MERGE && wave == 0 && start >= s0 && start < s0 + 64 && start < p_hi) {
+      // one-row pass, values loaded at entry: head_prep's arithmetic (k: norm, RoPE; v: as is)
+      const int pos = start, pp = pos - s0;
+      const bool act = lane < half;
+      float e0 = nk_x[0], e1 = nk_x[1];
+      if (a.k_norm) {
+        const float ssq = wave_sum(fmaf(e0, e0, e1 * e1));
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ssq, (float)HD) + a.eps));
+        if (act) { e0 = e0 * inv * nk_w[0]; e1 = e1 * inv * nk_w[1]; }
+      }
+      if (act) {
+        const float r0 = e0 * rc - e1 * rs, r1 = e0 * rs + e1 * rc;
+        const __half k0 = __float2half_rn(r0), k1 = __float2half_rn(r1);
+        ks[pp * KS + da] = (_Float16)__half2float(k0);
+        ks[pp * KS + db] = (_Float16)__half2float(k1);
+        __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim;
+        kd[da] = k0;
+        kd[db] = k1;
+        const __half v0 = __float2half_rn(nv_x[0]), v1 = __float2half_rn(nv_x[1]);
+        vt[da * VS + pp] = (_Float16)__half2float(v0);
+        vt[db * VS + pp] = (_Float16)__half2float(v1);
+        __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim;
+        vd[da] = v0;
+        vd[db] = v1;
+      }
+    }
+    for (int b = wave; MERGE && b < m; b += 4) {
       const int pos = start + b, pp = pos - s0;
       if (pp < 0 || pp >= 64 || pos >= p_hi) continue;
       float e0, e1;
@@ -992,19 +1073,26 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
     __syncthreads();
     // online softmax, wavefront w: query rows w, w+4, w+8, w+12 (rows past the pass: their
     // probabilities are zero), lane = position; the rows' reductions are interleaved
+    if (!MERGE) {  // rows 8-15 hold no query in a one-row pass: their values as computed below
+      const int row = wave + 8 + 4 * (lane >> 5);
+      ph[row * PS + (lane & 31)] = (_Float16)0.0f; ph[row * PS + 32 + (lane & 31)] = (_Float16)0.0f;
+      pl[row * PS + (lane & 31)] = (_Float16)0.0f; pl[row * PS + 32 + (lane & 31)] = (_Float16)0.0f;
+      if ((lane & 31) == 0) { rm[row] = -INFINITY; rl[row] = rl[row] * 1.0f + 0.0f; sa[row] = 1.0f; }
+    }
     {
+      constexpr int NR4 = MERGE ? 4 : 2;
       float sv[4], mx[4];
 #pragma unroll
-      for (int r4 = 0; r4 < 4; r4++) {
+      for (int r4 = 0; r4 < NR4; r4++) {
         const int row = wave + 4 * r4, qi = qa + row, pos = s0 + lane;
         sv[r4] = qi < NQ && pos < p_hi && pos <= start + qi / g ? ss[row * SS + lane] * a.scale : -INFINITY;
         mx[r4] = sv[r4];
       }
 #pragma unroll
-      for (int r4 = 0; r4 < 4; r4++) mx[r4] = wave_max(mx[r4]);
+      for (int r4 = 0; r4 < NR4; r4++) mx[r4] = wave_max(mx[r4]);
       float pv[4], ls[4], mn[4], al[4];
 #pragma unroll
-      for (int r4 = 0; r4 < 4; r4++) {
+      for (int r4 = 0; r4 < NR4; r4++) {
         const int row = wave + 4 * r4;
         const float m_old = rm[row];
         mn[r4] = fmaxf(m_old, mx[r4]);
@@ -1013,9 +1101,9 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
         ls[r4] = pv[r4];
       }
 #pragma unroll
-      for (int r4 = 0; r4 < 4; r4++) ls[r4] = wave_sum(ls[r4]);
+      for (int r4 = 0; r4 < NR4; r4++) ls[r4] = wave_sum(ls[r4]);
 #pragma unroll
-      for (int r4 = 0; r4 < 4; r4++) {
+      for (int r4 = 0; r4 < NR4; r4++) {
         const int row = wave + 4 * r4;
         split_f16(pv[r4], ph[row * PS + lane], pl[row * PS + lane]);
         if (lane == 0) { rm[row] = mn[r4]; rl[row] = rl[row] * al[r4] + ls[r4]; sa[row] = al[r4]; }
@@ -1638,7 +1726,7 @@ static void launch_attn_t(const AttnArgs &a, int nqt, const StepRec *st, hipStre
 }
 
 hipError_t launch_attention_partials(const AttnArgs &a, const StepRec *st, hipStream_t s) {
-  if (a.n_heads / a.n_kv > 16) return hipErrorInvalidValue;
+  if (a.n_heads / a.n_kv > 8) return hipErrorInvalidValue;  // one 16-row query tile: rows 0-7 hold the queries
   if (a.hd == 128) {
     SPX_LDS((k_attn<128, false>), AttnLds<128>::BYTES);
     hipLaunchKernelGGL((k_attn<128, false>), dim3(a.nch, a.n_kv, 1), dim3(256), AttnLds<128>::BYTES, s, a, st);

@@ -87,10 +87,95 @@ struct DecDownArgs {
 };
 
 constexpr int DEC_MV_NW = 16;   // wavefronts per matvec workgroup
+constexpr int DEC_MM_NW = 8;    // wavefronts per workgroup of the multi-row kernels
 constexpr int DEC_MAXNB = 16;   // blocks per row (cols <= 4096) of the decode kernels
 constexpr int DEC_DOWN_Q = 16384;  // n_used * n_ff values of h quantized in LDS by the down kernel
 
 hipError_t launch_dec_mv(const DecMVArgs &a, int grid, hipStream_t s);
+
+// ---- passes of 2..16 rows (verify / prefill): the same arithmetic per row as the one-row
+// kernels; the activations are normalised once per layer (kd_norm) and read as Q8_K.
+
+// RMSNorm (+ the fp32 normalised rows and / or their Q8_K) of m rows, one workgroup per row.
+struct DecNormArgs {
+  const float *x;     // [m][dim]
+  const float *nw;
+  float eps;
+  int dim;
+  float *xn_out;      // [m][dim] (null: not written)
+  Q8KP q_out;         // [m] (q null: not written)
+};
+
+// Integer matvec of m vectors (Q8_K, global) over up to three segments.
+struct DecMMArgs {
+  TensorView w[3];
+  float *out[3];      // row r of vector v -> out[v * ld_out + r]
+  int64_t ld_out[3];
+  int tiles[3];       // row tiles (DEC_MM_NW * R rows)
+  int nseg;
+  int G;
+  Q8KP y;
+  int cols, m;
+  const float *res_in;  // residual epilogue (one segment): res_out[v][r] = res_in[v][r] + rscale * y
+  float *res_out;
+  float rscale;
+  unsigned long long *best;  // greedy keys: best[v * nbest + blockIdx.x]
+  int nbest;
+  float lscale;
+};
+
+// F32 router rows (one per workgroup) of m fp32 normalised rows.
+struct DecRouterMArgs {
+  TensorView w;
+  const float *x;     // [m][dim]
+  float *logits;      // [m][n_expert]
+  int n_expert, dim, m;
+};
+
+// Routing of m rows and the grouped job list: experts with at least one user, in expert order,
+// users in (row, slot) order; job j: vec[k] = the user's row, out[k] = row * n_used + slot.
+struct DecRouteArgs {
+  const float *logits;
+  int n_expert, n_used, norm, m;
+  float moe_prune;
+  int *chosen;        // [16][32]
+  float *weights;     // [16][32]
+  int *nkeep;         // [16]
+  Job *jobs;          // [<= 256]
+  int *njobs;         // [1]
+  int *expert_count;  // [n_expert] (null: none)
+};
+
+// Gate/up + SwiGLU over the jobs (jobs null: dense, users = rows 0..m-1).
+struct DecGateUpMArgs {
+  TensorView gate, up;
+  Q8KP y;             // normalised rows [m]
+  const Job *jobs;
+  const int *njobs;
+  float *h;           // [m * n_used][n_ff] (dense: [m][n_ff])
+  int n_ff, m;
+};
+
+// Down projection over the jobs, weighted combine per row, residual add.
+struct DecDownMArgs {
+  TensorView w;
+  Q8KP hq;            // Q8_K of h [m * n_used]
+  const Job *jobs;
+  const int *njobs;
+  const float *weights;
+  const int *nkeep;
+  int n_used, m;
+  const float *res_in;
+  float *res_out;
+  float rscale;
+};
+
+hipError_t launch_dec_norm(const DecNormArgs &a, int m, hipStream_t s);
+hipError_t launch_dec_mm(const DecMMArgs &a, int grid, hipStream_t s);
+hipError_t launch_dec_router_m(const DecRouterMArgs &a, hipStream_t s);
+hipError_t launch_dec_route(const DecRouteArgs &a, hipStream_t s);
+hipError_t launch_dec_gateup_m(const DecGateUpMArgs &a, int max_jobs, hipStream_t s);
+hipError_t launch_dec_down_m(const DecDownMArgs &a, hipStream_t s);
 hipError_t launch_dec_merge(const DecMergeArgs &a, const StepRec *st, hipStream_t s);
 hipError_t launch_dec_router(const DecRouterArgs &a, hipStream_t s);
 hipError_t launch_dec_gateup(const DecGateUpArgs &a, hipStream_t s);

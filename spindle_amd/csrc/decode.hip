@@ -42,6 +42,11 @@ __device__ __forceinline__ T lld(const SPX_L void *p) {
   return __builtin_bit_cast(T, *(const SPX_L W *)p);
 }
 template <class T>
+__device__ __forceinline__ void lst(SPX_L void *p, T v) {
+  typedef typename GWord<sizeof(T)>::type W;
+  *(SPX_L W *)p = __builtin_bit_cast(W, v);
+}
+template <class T>
 __device__ __forceinline__ void gst(void *p, T v) {
   typedef typename GWord<sizeof(T)>::type W;
   *(SPX_G W *)p = __builtin_bit_cast(W, v);
@@ -142,9 +147,8 @@ __device__ __forceinline__ void in_load(const DecIn &in, InRow<KB> &r) {
 // rmsnorm (:569-575) as the norm tails compute it (per 256 block a wavefront tree, then the
 // blocks in order; inv = 1 / sqrt(S / cols + eps) correctly rounded; x * inv * w), then
 // quantize_avx2 of each block into the LDS image (lq, ld, lbs). xn_out: the normalised row.
-template <int NW, int KB>
-__device__ __forceinline__ void in_quant(const DecIn &in, InRow<KB> &r, SPX_L uint32_t *lq, SPX_L float *ld, SPX_L int2 *lbs, SPX_L float *bsum,
-                                         float *xn_out) {
+template <int NW, int KB, class QP, class DP, class BP>
+__device__ __forceinline__ void in_quant(const DecIn &in, InRow<KB> &r, QP lq, DP ld, BP lbs, SPX_L float *bsum, float *xn_out) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nbq = in.cols >> 8;
   if (in.nw) {
 #pragma unroll
@@ -180,7 +184,7 @@ __device__ __forceinline__ void in_quant(const DecIn &in, InRow<KB> &r, SPX_L ui
     const int tb = wave + NW * k;
     if (tb < nbq) {
       const float am = wave_max(amax4(r.v[k]));
-      q8k_block_store(r.v[k], am, lq + tb * 64, ld + tb, (SPX_L int *)(lbs + tb * 8));
+      q8k_block_store(r.v[k], am, lq + tb * 64, ld + tb, lbs + tb * 16);  // lbs: the bsum pairs as ints
     }
   }
 }
@@ -277,7 +281,7 @@ __global__ __launch_bounds__(DEC_MV_NW * 64) __attribute__((amdgpu_waves_per_eu(
     const int64_t grow = row < rows ? row : rows - 1;
     if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) rp_load<T_Q4K, BPG>(raw, pl, grow, nb, G, gi, l);
     else rp_load<T_Q6K, BPG>(raw, pl, grow, nb, G, gi, l);
-    in_quant<NW, KB>(a.in, in, lq, ld, lbs, bsum, blockIdx.x == 0 ? a.xn_out : nullptr);
+    in_quant<NW, KB>(a.in, in, lq, ld, (SPX_L int *)lbs, bsum, blockIdx.x == 0 ? a.xn_out : nullptr);
     __syncthreads();
     if ((int)blockIdx.x < total) {
       if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) rp_dots<T_Q4K, BPG>(raw, nb, G, gi, l, lq, ld, lbs, cbr);
@@ -305,7 +309,7 @@ __global__ __launch_bounds__(DEC_MV_NW * 64) __attribute__((amdgpu_waves_per_eu(
       const int64_t row = row_of(min((int)blockIdx.x + k * g, total - 1));
       rp_load<TT, BPG>(raw[k], pl0, row < rows ? row : rows - 1, nb, G, gi, l);
     }
-    in_quant<NW, KB>(a.in, in, lq, ld, lbs, bsum, blockIdx.x == 0 ? a.xn_out : nullptr);
+    in_quant<NW, KB>(a.in, in, lq, ld, (SPX_L int *)lbs, bsum, blockIdx.x == 0 ? a.xn_out : nullptr);
     __syncthreads();
     for (int t = blockIdx.x; t < total;) {
 #pragma unroll
@@ -588,7 +592,7 @@ __global__ __launch_bounds__(DEC_MV_NW * 64) void kd_gateup(const DecGateUpArgs 
   const int64_t grow = (int64_t)expert * a.gate.rows + (valid ? r : n_ff - 1);
   DRaw raw[BPG];
   rp_load<T, BPG>(raw, half ? a.up.pl : a.gate.pl, grow, nb, 4, gi, l);
-  in_quant<NW, KB>(a.in, in, lq, ld, lbs, bsum, nullptr);
+  in_quant<NW, KB>(a.in, in, lq, ld, (SPX_L int *)lbs, bsum, nullptr);
   __syncthreads();
   rp_dots<T, BPG>(raw, nb, 4, gi, l, lq, ld, lbs, cbr);
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the chain buffer is written
@@ -656,6 +660,481 @@ __global__ __launch_bounds__(512) void kd_down(const DecDownArgs a) {
     float acc = 0.0f;
     for (int i = 0; i < nk; i++) acc = acc + gld<float>(a.weights + i) * ys[wave][i];
     gst<float>(a.res_out + r, gld<float>(a.res_in + r) + a.rscale * acc);
+  }
+}
+
+// ================================================================== passes of 2..16 rows
+// ------------------------------------------------------------------ norm of m rows
+// One workgroup per row: residual row -> rmsnorm (the norm tails' fixed-order sum) -> fp32
+// normalised row and / or its Q8_K, in global memory.
+__global__ __launch_bounds__(256) void kd_norm(const DecNormArgs a) {
+  constexpr int NW = 4, KB = DEC_MAXNB / NW;
+  __shared__ float bsum_[DEC_MAXNB];
+  const int b = blockIdx.x, nbq = a.dim >> 8;
+  const DecIn in{a.x + (int64_t)b * a.dim, a.nw, a.eps, a.dim};
+  InRow<KB> r;
+  in_load<NW, KB>(in, r);
+  float *xn = a.xn_out ? a.xn_out + (int64_t)b * a.dim : nullptr;
+  if (a.q_out.q) {
+    in_quant<NW, KB>(in, r, (SPX_G uint32_t *)(a.q_out.q + (int64_t)b * a.dim / 4), (SPX_G float *)(a.q_out.d + (int64_t)b * nbq),
+                     (SPX_G int *)(a.q_out.bs + (int64_t)b * nbq * 8), (SPX_L float *)bsum_, xn);
+  } else {  // fp32 only: quantize into a scratch image nobody reads
+    __shared__ uint32_t sq[DEC_MAXNB * 64];
+    __shared__ float sd[DEC_MAXNB];
+    __shared__ int sb[DEC_MAXNB * 16];
+    in_quant<NW, KB>(in, r, (SPX_L uint32_t *)sq, (SPX_L float *)sd, (SPX_L int *)sb, (SPX_L float *)bsum_, xn);
+  }
+}
+
+// ------------------------------------------------------------------ multi-vector matvec
+// DEC_MM_NW wavefronts per workgroup, R rows x G row groups per wavefront (rp_shape); the m
+// vectors' Q8_K rows are staged in LDS. Blocks are taken in rounds: in round j group gi
+// computes block gi + G * j for every vector into the chain buffer; then the group that owns
+// vector v (v mod G) advances v's chain over the round's blocks in order. The chain per
+// vector is the reference's, block by block (the same fp32 values as one vector alone).
+__host__ __device__ inline size_t mm_act_bytes(int m, int cols) {
+  const int nbq = cols >> 8;
+  return (((size_t)m * cols + 15) & ~(size_t)15) + (((size_t)m * nbq * 4 + 15) & ~(size_t)15) + (size_t)m * nbq * 64;
+}
+__host__ __device__ inline size_t mm_lds_bytes(int m, int cols) { return mm_act_bytes(m, cols) + (size_t)DEC_MM_NW * 80 * m * 4; }
+
+// Copies m permuted Q8_K vectors (global y, cols columns; vector v from y's vector vsrc[v],
+// or v) into LDS (lq, ld, lbs), all threads; each thread's loads go out before its stores.
+template <int NT>
+__device__ __forceinline__ void stage_q8(const Q8KP &y, const int *vsrc, int m, int cols, SPX_L uint32_t *lq, SPX_L float *ld, SPX_L int2 *lbs) {
+  const int nbq = cols >> 8, n16 = cols / 16, nb16 = nbq * 4, nq = m * n16, nb4 = m * nb16;
+  const int tid = threadIdx.x;
+  for (int i0 = tid; i0 < nq; i0 += 4 * NT) {  // loads of four rounds go out before their stores
+    uint4 t[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int i = i0 + k * NT;
+      if (i < nq) {
+        const int v = i / n16, kk = i - v * n16, sv = vsrc ? vsrc[v] : v;
+        t[k] = gld<uint4>(reinterpret_cast<const uint8_t *>(y.q) + (int64_t)sv * cols + 16 * kk);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int i = i0 + k * NT;
+      if (i < nq) lst<uint4>((SPX_L uint4 *)lq + i, t[k]);
+    }
+  }
+  for (int i0 = tid; i0 < nb4; i0 += 2 * NT) {
+    uint4 t[2];
+    float dv[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int i = i0 + k * NT;
+      if (i < nb4) {
+        const int v = i / nb16, kk = i - v * nb16, sv = vsrc ? vsrc[v] : v;
+        t[k] = gld<uint4>(reinterpret_cast<const uint8_t *>(y.bs) + ((int64_t)sv * nbq * 8) * 8 + 16 * kk);
+      }
+      if (i < m * nbq) {
+        const int v = i / nbq, kk = i - v * nbq, sv = vsrc ? vsrc[v] : v;
+        dv[k] = gld<float>(y.d + (int64_t)sv * nbq + kk);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int i = i0 + k * NT;
+      if (i < nb4) lst<uint4>((SPX_L uint4 *)lbs + i, t[k]);
+      if (i < m * nbq) ld[i] = dv[k];
+    }
+  }
+}
+
+// Round j of a row's blocks for vectors 0..m-1: group gi's block (raw[j]) against every
+// vector into cb [G][m][10].
+template <int T, int BPG>
+__device__ __forceinline__ void mm_round_dots(const DRaw (&raw)[BPG], int j, int nb, int G, int gi, int l, int m, int nbq,
+                                              const SPX_L uint32_t *lq, const SPX_L float *ld, const SPX_L int2 *lbs, SPX_L float *cbr) {
+  const int i = gi + G * j;
+  if (i >= nb) return;
+  KQDec<T> dec;
+  dec.decode(draw_kq<T>(raw[j]), l);
+#pragma unroll 2
+  for (int v = 0; v < m; v++) {
+    const int vb = v * nbq + i;
+    const uint4 y0 = lld<uint4>(lq + vb * 64 + 8 * l), y1 = lld<uint4>(lq + vb * 64 + 8 * l + 4);
+    int P, s;
+    dec.dot(y0, y1, lld<int2>(lbs + vb * 8 + l), P, s);
+    s = sum8(s);
+    const float xd = ld[vb];
+    SPX_L float *e = cbr + (gi * m + v) * 10;
+    e[l] = (float)P;
+    if (l == 0) { e[8] = dec.d * xd; e[9] = dec.corr_term(xd, s); }
+  }
+}
+
+// The chain owner's update over round j (blocks G*j .. G*j+G-1 in order) for its vectors
+// v = gi, gi + G, ... (slot q = v / G).
+template <int QN>
+__device__ __forceinline__ void mm_round_chain(int j, int nb, int G, int gi, int l, int m, const SPX_L float *cbr, float (&acc)[QN],
+                                               float (&cr)[QN]) {
+#pragma unroll
+  for (int q = 0; q < QN; q++) {
+    const int v = gi + G * q;
+    if (v < m) {
+      for (int k = 0; k < G && G * j + k < nb; k++) {
+        const SPX_L float *e = cbr + (k * m + v) * 10;
+        acc[q] = fmaf(e[8], e[l], acc[q]);
+        cr[q] = cr[q] + e[9];
+      }
+    }
+  }
+}
+
+template <int TT, int BPG, int QN>  // QN = MAX_M / G: vectors whose chains one row group owns
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void kd_mm(const DecMMArgs a) {
+  constexpr int NW = DEC_MM_NW;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ unsigned long long sbest[MAX_M];
+  const int m = a.m, cols = a.cols, nbq = cols >> 8, nb = nbq;
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
+  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)m * cols + 15) & ~(size_t)15));
+  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)m * cols + 15) & ~(size_t)15) + (((size_t)m * nbq * 4 + 15) & ~(size_t)15));
+  SPX_L float *cbw = (SPX_L float *)(smem + mm_act_bytes(m, cols));
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 3, l = lane & 7;
+  const int G = a.G, R = 8 / G, r = grp / G, gi = grp - r * G;
+  SPX_L float *cbr = cbw + (size_t)(wave * R + r) * G * m * 10;
+  const int t0 = a.tiles[0], t1 = a.nseg > 1 ? a.tiles[1] : 0, t2 = a.nseg > 2 ? a.tiles[2] : 0;
+  const int total = t0 + t1 + t2;
+  const Planes pl0 = a.w[0].pl, pl1 = a.w[1].pl, pl2 = a.w[2].pl;
+  const int64_t rw0 = a.w[0].rows, rw1 = a.w[1].rows, rw2 = a.w[2].rows;
+  const int dt0 = a.w[0].dtype, dt1 = a.w[1].dtype, dt2 = a.w[2].dtype;
+  if (threadIdx.x < MAX_M) sbest[threadIdx.x] = 0;
+  DRaw raw[BPG];
+  int t = blockIdx.x, si = 0, dt = dt0;
+  int64_t row = 0, rows = rw0;
+  Planes pl = pl0;
+#define SPX_MM_LOCATE()                                                                          \
+  do {                                                                                           \
+    si = __builtin_amdgcn_readfirstlane(t >= t0 ? (t >= t0 + t1 ? 2 : 1) : 0);                   \
+    const int tt = t - (si > 0 ? t0 : 0) - (si > 1 ? t1 : 0);                                    \
+    row = ((int64_t)tt * NW + wave) * R + r;                                                     \
+    rows = si == 0 ? rw0 : si == 1 ? rw1 : rw2;                                                  \
+    dt = si == 0 ? dt0 : si == 1 ? dt1 : dt2;                                                    \
+    pl.p0 = si == 0 ? pl0.p0 : si == 1 ? pl1.p0 : pl2.p0;                                        \
+    pl.p1 = si == 0 ? pl0.p1 : si == 1 ? pl1.p1 : pl2.p1;                                        \
+    pl.p2 = si == 0 ? pl0.p2 : si == 1 ? pl1.p2 : pl2.p2;                                        \
+    pl.p3 = si == 0 ? pl0.p3 : si == 1 ? pl1.p3 : pl2.p3;                                        \
+    const int64_t grow = row < rows ? row : rows - 1;                                            \
+    if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) rp_load<T_Q4K, BPG>(raw, pl, grow, nb, G, gi, l); \
+    else rp_load<T_Q6K, BPG>(raw, pl, grow, nb, G, gi, l);                                       \
+  } while (0)
+  if (t < total) SPX_MM_LOCATE();
+  stage_q8<DEC_MM_NW * 64>(a.y, nullptr, m, cols, lq, ld, lbs);
+  __syncthreads();
+  for (; t < total;) {
+    float acc[QN], cr[QN];
+#pragma unroll
+    for (int q = 0; q < QN; q++) { acc[q] = 0.0f; cr[q] = 0.0f; }
+#pragma unroll
+    for (int j = 0; j < BPG; j++) {
+      if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) mm_round_dots<T_Q4K, BPG>(raw, j, nb, G, gi, l, m, nbq, lq, ld, lbs, cbr);
+      else mm_round_dots<T_Q6K, BPG>(raw, j, nb, G, gi, l, m, nbq, lq, ld, lbs, cbr);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+      mm_round_chain<QN>(j, nb, G, gi, l, m, cbr, acc, cr);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+    }
+    const int64_t row_c = row, rows_c = rows;
+    float *const out = si == 0 ? a.out[0] : si == 1 ? a.out[1] : a.out[2];
+    const int64_t ldo = si == 0 ? a.ld_out[0] : si == 1 ? a.ld_out[1] : a.ld_out[2];
+    t += gridDim.x;
+    if (t < total) SPX_MM_LOCATE();  // the next tile's weights go out before the results
+#pragma unroll
+    for (int q = 0; q < QN; q++) {
+      const int v = gi + G * q;
+      if (v < m) {
+        const float res = hsum_rows8(acc[q]) - cr[q];
+        if (l == 0 && row_c < rows_c) {
+          if (out) gst<float>(out + (int64_t)v * ldo + row_c, res);
+          if (a.res_out) {
+            const int64_t o = (int64_t)v * rows_c + row_c;
+            gst<float>(a.res_out + o, gld<float>(a.res_in + o) + a.rscale * res);
+          }
+          if (a.best) atomicMax(&sbest[v], pick_key(res, a.lscale, row_c));
+        }
+      }
+    }
+  }
+#undef SPX_MM_LOCATE
+  if (a.best) {
+    __syncthreads();
+    if ((int)threadIdx.x < m) gst<unsigned long long>(a.best + (int64_t)threadIdx.x * a.nbest + blockIdx.x, sbest[threadIdx.x]);
+  }
+}
+
+// ------------------------------------------------------------------ router, m rows
+// k_router's arithmetic for each row: wavefront w, lane j hold float4s w*64 + j + 256k of the
+// router row; the lane's fma chain against the normalised row, the wave tree, the four
+// wavefronts in order.
+__global__ __launch_bounds__(256) void kd_router_m(const DecRouterMArgs a) {
+  constexpr int NK = DEC_MAXNB / 4;
+  __shared__ float part[4][MAX_M];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, row = blockIdx.x;
+  const int dim = a.dim, n4 = dim >> 2;
+  float4 wv[NK];
+#pragma unroll
+  for (int k = 0; k < NK; k++) {
+    const int f = wave * 64 + lane + 256 * k;
+    wv[k] = f < n4 ? gld<float4>(a.w.pl.p0 + ((int64_t)row * dim + 4 * f) * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int v0 = 0; v0 < MAX_M; v0 += 4) {
+    if (v0 < a.m) {
+      float4 x[4][NK];
+#pragma unroll
+      for (int vv = 0; vv < 4; vv++)
+#pragma unroll
+        for (int k = 0; k < NK; k++) {
+          const int f = wave * 64 + lane + 256 * k, v = min(v0 + vv, a.m - 1);
+          x[vv][k] = f < n4 ? gld<float4>(a.x + (int64_t)v * dim + 4 * f) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+      for (int vv = 0; vv < 4; vv++) {
+        float pv = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NK; k++) {
+          const int f = wave * 64 + lane + 256 * k;
+          if (f < n4) {
+            pv = fmaf(wv[k].x, x[vv][k].x, pv);
+            pv = fmaf(wv[k].y, x[vv][k].y, pv);
+            pv = fmaf(wv[k].z, x[vv][k].z, pv);
+            pv = fmaf(wv[k].w, x[vv][k].w, pv);
+          }
+        }
+        const float tsum = wave_sum(pv);
+        if (lane == 0 && v0 + vv < a.m) part[wave][v0 + vv] = tsum;
+      }
+    }
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < a.m) {
+    const int v = threadIdx.x;
+    gst<float>(a.logits + (int64_t)v * a.n_expert + row, ((part[0][v] + part[1][v]) + part[2][v]) + part[3][v]);
+  }
+}
+
+// ------------------------------------------------------------------ routing + jobs, m rows
+// One workgroup: wavefront b routes row b (route_row), then the job list (k_router's tail).
+__global__ __launch_bounds__(1024) void kd_route(const DecRouteArgs a) {
+  __shared__ signed char slot_of[MAX_M][256];
+  __shared__ int wcount[16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ne = a.n_expert, nu = a.n_used, m = a.m;
+  for (int i = threadIdx.x; i < MAX_M * 256; i += blockDim.x) (&slot_of[0][0])[i] = -1;
+  __syncthreads();
+  if (wave < m) {
+    const int b = wave;
+    float lv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int e = lane + 64 * k;
+      lv[k] = e < ne ? gld<float>(a.logits + (int64_t)b * ne + e) : -INFINITY;
+    }
+    int my_e, keep;
+    float my_p, wsum;
+    route_row(lv, ne, nu, a.moe_prune, my_e, my_p, keep, wsum);
+    if (lane < keep) {
+      gst<int>(a.chosen + b * 32 + lane, my_e);
+      gst<float>(a.weights + b * 32 + lane, a.norm ? my_p / wsum : my_p);
+      slot_of[b][my_e] = (signed char)lane;
+    }
+    if (lane == 0) gst<int>(a.nkeep + b, keep);
+  }
+  __syncthreads();
+  // jobs: experts with at least one user, in expert order (thread e = expert e); users in row
+  // order (a row chooses an expert at most once)
+  const int e = threadIdx.x;
+  int cnt = 0;
+  if (e < ne)
+    for (int b = 0; b < m; b++) cnt += slot_of[b][e] >= 0;
+  const unsigned long long bal = __ballot(cnt > 0);
+  if (lane == 0) wcount[wave] = __popcll(bal);
+  __syncthreads();
+  if (cnt > 0) {
+    int base = 0;
+    for (int w = 0; w < wave; w++) base += wcount[w];
+    const int j = base + __popcll(bal & ((1ull << lane) - 1ull));
+    Job J;
+    J.expert = e;
+    int k = 0;
+    for (int b = 0; b < m; b++) {
+      const int sl = slot_of[b][e];
+      if (sl >= 0) { J.vec[k] = b; J.out[k] = b * nu + sl; k++; }
+    }
+    J.nvec = k;
+    for (int q = k; q < MAX_M; q++) { J.vec[q] = 0; J.out[q] = 0; }
+    a.jobs[j] = J;
+    if (a.expert_count) a.expert_count[e] += 1;
+  }
+  if (threadIdx.x == 0) {
+    int n = 0;
+    for (int w = 0; w < 16; w++) n += wcount[w];
+    gst<int>(a.njobs, n);
+  }
+}
+
+// ------------------------------------------------------------------ gate / up, m rows
+// Grid (n_ff / DEC_MM_NW, jobs): workgroup (x, j) computes rows DEC_MM_NW * x .. of h for the
+// users of job j (dense: all rows), one row per wavefront: lanes 0-31 the gate row, 32-63 the
+// up row, four groups each; rounds of four blocks as kd_mm. h[out][r] = silu(g) * u.
+template <int T, int BPG>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void kd_gateup_m(const DecGateUpMArgs a) {
+  constexpr int NW = DEC_MM_NW;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int s_vec[MAX_M], s_out[MAX_M], s_hdr[2];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 3, l = lane & 7;
+  const int half = grp >> 2, gi = grp & 3;
+  const int n_ff = a.n_ff, cols = (int)a.gate.cols, nbq = cols >> 8, nb = nbq;
+  const int r = blockIdx.x * NW + wave;
+  const bool valid = r < n_ff;
+  if (threadIdx.x == 0) {
+    if (a.jobs) {
+      const int nj = gld<int>(a.njobs);
+      s_hdr[0] = (int)blockIdx.y < nj ? a.jobs[blockIdx.y].expert : -1;
+      s_hdr[1] = (int)blockIdx.y < nj ? a.jobs[blockIdx.y].nvec : 0;
+    } else {
+      s_hdr[0] = 0;
+      s_hdr[1] = a.m;
+    }
+  }
+  if (threadIdx.x < MAX_M) {
+    s_vec[threadIdx.x] = a.jobs ? a.jobs[blockIdx.y].vec[threadIdx.x] : threadIdx.x;
+    s_out[threadIdx.x] = a.jobs ? a.jobs[blockIdx.y].out[threadIdx.x] : threadIdx.x;
+  }
+  __syncthreads();
+  const int expert = s_hdr[0], nv = s_hdr[1];
+  if (expert < 0) return;  // past the job count (the whole workgroup)
+  const size_t act = mm_act_bytes(nv, cols);
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
+  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)nv * cols + 15) & ~(size_t)15));
+  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)nv * cols + 15) & ~(size_t)15) + (((size_t)nv * nbq * 4 + 15) & ~(size_t)15));
+  SPX_L float *cbr = (SPX_L float *)(smem + act) + (size_t)(wave * 2 + half) * 4 * nv * 10;
+  const int64_t grow = (int64_t)expert * a.gate.rows + (valid ? r : n_ff - 1);
+  DRaw raw[BPG];
+  rp_load<T, BPG>(raw, half ? a.up.pl : a.gate.pl, grow, nb, 4, gi, l);
+  stage_q8<DEC_MM_NW * 64>(a.y, s_vec, nv, cols, lq, ld, lbs);
+  __syncthreads();
+  float acc[MAX_M / 4], cr[MAX_M / 4];
+#pragma unroll
+  for (int q = 0; q < MAX_M / 4; q++) { acc[q] = 0.0f; cr[q] = 0.0f; }
+#pragma unroll
+  for (int j = 0; j < BPG; j++) {
+    mm_round_dots<T, BPG>(raw, j, nb, 4, gi, l, nv, nbq, lq, ld, lbs, cbr);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    mm_round_chain<MAX_M / 4>(j, nb, 4, gi, l, nv, cbr, acc, cr);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+  }
+#pragma unroll
+  for (int q = 0; q < MAX_M / 4; q++) {
+    const int v = gi + 4 * q;
+    if (v < nv) {  // wave-uniform per group pair: gate lanes and up lanes own the same v
+      const float res = hsum_rows8(acc[q]) - cr[q];
+      uint32_t r_lo, r_hi;
+      xchg32(__float_as_uint(res), r_lo, r_hi);
+      const float u = __uint_as_float(r_hi);
+      if (half == 0 && l == 0 && valid) {
+        const float x = res;
+        gst<float>(a.h + (int64_t)s_out[v] * n_ff + r, x / (1.0f + expf(-x)) * u);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ down + combine, m rows
+// Eight wavefronts, one output row each; row group s takes job j0 + s (rounds of eight), its
+// expert's row decoded once and dotted with each user's Q8_K h (read through the caches);
+// then row b's output = sum over its kept choices, in choice order, of w * y.
+template <int T, int NB>
+__global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_m(const DecDownMArgs a) {
+  constexpr int NW = DEC_MM_NW;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float yb[NW][MAX_M * 32];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
+  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, nbh = n_ff >> 8, nvh = a.m * a.n_used;
+  const int64_t r = (int64_t)blockIdx.x * NW + wave;
+  const int64_t rr = r < dim ? r : dim - 1;
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
+  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)nvh * n_ff + 15) & ~(size_t)15));
+  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)nvh * n_ff + 15) & ~(size_t)15) + (((size_t)nvh * nbh * 4 + 15) & ~(size_t)15));
+  const int nj = gld<int>(a.njobs);
+  // first round's expert rows in flight while the users' h rows are staged
+  int j = min(slot, nj - 1);
+  DRaw raw[NB];
+  draw_row<T, NB>(raw, a.w.pl, (int64_t)a.jobs[j].expert * dim + rr, nbh, l);
+  {  // loads of four rounds go out before their stores
+    const int nq = nvh * n_ff / 16, nb4 = nvh * nbh * 4;
+    for (int i0 = threadIdx.x; i0 < nq; i0 += 4 * blockDim.x) {
+      uint4 t[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int i = i0 + k * blockDim.x;
+        if (i < nq) t[k] = gld<uint4>(reinterpret_cast<const uint8_t *>(a.hq.q) + 16 * (int64_t)i);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int i = i0 + k * blockDim.x;
+        if (i < nq) lst<uint4>((SPX_L uint4 *)lq + i, t[k]);
+      }
+    }
+    for (int i0 = threadIdx.x; i0 < nb4; i0 += 4 * blockDim.x) {
+      uint4 t[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int i = i0 + k * blockDim.x;
+        if (i < nb4) t[k] = gld<uint4>(reinterpret_cast<const uint8_t *>(a.hq.bs) + 16 * (int64_t)i);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int i = i0 + k * blockDim.x;
+        if (i < nb4) lst<uint4>((SPX_L uint4 *)lbs + i, t[k]);
+      }
+    }
+    for (int i = threadIdx.x; i < nvh * nbh; i += blockDim.x) ld[i] = gld<float>(a.hq.d + i);
+  }
+  __syncthreads();
+  for (int j0 = 0; j0 < nj; j0 += 8) {
+    j = min(j0 + slot, nj - 1);
+    const int nvec = j0 + slot < nj ? a.jobs[j].nvec : 0;
+    if (j0 > 0) draw_row<T, NB>(raw, a.w.pl, (int64_t)a.jobs[j].expert * dim + rr, nbh, l);
+    KQDec<T> dec[NB];
+#pragma unroll
+    for (int i = 0; i < NB; i++)
+      if (i < nbh) dec[i].decode(draw_kq<T>(raw[i]), l);
+    for (int k = 0; k < nvec; k++) {
+      const int u = a.jobs[j].out[k];
+      float acc = 0.0f, corr = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NB; i++) {
+        if (i < nbh) {
+          const int vb = u * nbh + i;
+          const uint4 y0 = lld<uint4>(lq + vb * 64 + 8 * l), y1 = lld<uint4>(lq + vb * 64 + 8 * l + 4);
+          int P, s;
+          dec[i].dot(y0, y1, lld<int2>(lbs + vb * 8 + l), P, s);
+          s = sum8(s);
+          const float xd = ld[vb];
+          corr = corr + dec[i].corr_term(xd, s);
+          acc = fmaf(dec[i].d * xd, (float)P, acc);
+        }
+      }
+      const float y = hsum_rows8(acc) - corr;
+      if (l == 0) yb[wave][u] = y;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  if (lane < a.m && r < dim) {
+    const int b = lane, nk = gld<int>(a.nkeep + b);
+    float acc = 0.0f;
+    for (int i = 0; i < nk; i++) acc = acc + gld<float>(a.weights + b * 32 + i) * yb[wave][b * a.n_used + i];
+    const int64_t o = (int64_t)b * dim + r;
+    gst<float>(a.res_out + o, gld<float>(a.res_in + o) + a.rscale * acc);
   }
 }
 
@@ -749,6 +1228,109 @@ hipError_t launch_dec_down(const DecDownArgs &a, hipStream_t s) {
   if (a.w.cols % 256 || a.w.nb > DEC_MAXNB || a.n_used < 1 || a.n_used > 32 || (int64_t)a.n_used * a.w.cols > DEC_DOWN_Q) return hipErrorInvalidValue;
   if (a.w.dtype == T_Q4K) return dec_down_t<T_Q4K>(a, s);
   if (a.w.dtype == T_Q6K) return dec_down_t<T_Q6K>(a, s);
+  return hipErrorInvalidValue;
+}
+
+// ------------------------------------------------------------------ launchers, m rows
+hipError_t launch_dec_norm(const DecNormArgs &a, int m, hipStream_t s) {
+  if (a.dim % 256 || a.dim > 256 * DEC_MAXNB || !a.nw || m < 1 || m > MAX_M) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kd_norm, dim3(m), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+#define SPX_DLDS(kern, sm) \
+  if ((sm) > 65536) (void)hipFuncSetAttribute((const void *)(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)(sm))
+
+template <int TT, int QN>
+static hipError_t dec_mm_q(const DecMMArgs &a, int grid, int bpg, size_t sm, hipStream_t s) {
+  const dim3 b(DEC_MM_NW * 64);
+  if (bpg == 1) { SPX_DLDS((kd_mm<TT, 1, QN>), sm); hipLaunchKernelGGL((kd_mm<TT, 1, QN>), dim3(grid), b, sm, s, a); }
+  else { SPX_DLDS((kd_mm<TT, 2, QN>), sm); hipLaunchKernelGGL((kd_mm<TT, 2, QN>), dim3(grid), b, sm, s, a); }
+  return hipGetLastError();
+}
+
+template <int TT>
+static hipError_t dec_mm_tt(const DecMMArgs &a, int grid, hipStream_t s) {
+  const int nb = a.cols >> 8, bpg = (nb + a.G - 1) / a.G;
+  const size_t sm = mm_lds_bytes(a.m, a.cols);
+  switch (a.G) {
+  case 8: return dec_mm_q<TT, MAX_M / 8>(a, grid, bpg, sm, s);
+  case 4: return dec_mm_q<TT, MAX_M / 4>(a, grid, bpg, sm, s);
+  case 2: return dec_mm_q<TT, MAX_M / 2>(a, grid, bpg, sm, s);
+  default: return dec_mm_q<TT, MAX_M>(a, grid, bpg, sm, s);
+  }
+}
+
+hipError_t launch_dec_mm(const DecMMArgs &a, int grid, hipStream_t s) {
+  const int nb = a.cols >> 8;
+  if (a.nseg < 1 || a.nseg > 3 || grid < 1 || nb < 1 || nb > DEC_MAXNB || a.cols % 256 || a.m < 1 || a.m > MAX_M) return hipErrorInvalidValue;
+  int G, R;
+  rp_shape(nb, G, R);
+  if (a.G != G || mm_lds_bytes(a.m, a.cols) > 160 * 1024) return hipErrorInvalidValue;
+  bool all4 = true, all6 = true;
+  for (int i = 0; i < a.nseg; i++) {
+    if ((a.w[i].dtype != T_Q4K && a.w[i].dtype != T_Q6K) || a.w[i].nb != nb) return hipErrorInvalidValue;
+    all4 = all4 && a.w[i].dtype == T_Q4K;
+    all6 = all6 && a.w[i].dtype == T_Q6K;
+  }
+  if (a.res_out && a.nseg != 1) return hipErrorInvalidValue;
+  if (all4) return dec_mm_tt<T_Q4K>(a, grid, s);
+  if (all6) return dec_mm_tt<T_Q6K>(a, grid, s);
+  return dec_mm_tt<0>(a, grid, s);
+}
+
+hipError_t launch_dec_router_m(const DecRouterMArgs &a, hipStream_t s) {
+  if (a.dim % 256 || a.dim > 256 * DEC_MAXNB || a.m < 1 || a.m > MAX_M) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kd_router_m, dim3(a.n_expert), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_dec_route(const DecRouteArgs &a, hipStream_t s) {
+  if (a.n_expert < 1 || a.n_expert > 256 || a.n_used < 1 || a.n_used > 32 || a.n_used > a.n_expert || a.m < 1 || a.m > MAX_M) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kd_route, dim3(1), dim3(1024), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int T>
+static hipError_t dec_gum_t(const DecGateUpMArgs &a, int max_jobs, hipStream_t s) {
+  const int cols = (int)a.gate.cols, bpg = ((cols >> 8) + 3) / 4, nv = a.m;
+  const size_t sm = mm_act_bytes(nv, cols) + (size_t)DEC_MM_NW * 2 * 4 * nv * 10 * 4;
+  if (sm > 160 * 1024) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((a.n_ff + DEC_MM_NW - 1) / DEC_MM_NW), (unsigned)max_jobs), b(DEC_MM_NW * 64);
+  if (bpg == 1) { SPX_DLDS((kd_gateup_m<T, 1>), sm); hipLaunchKernelGGL((kd_gateup_m<T, 1>), grid, b, sm, s, a); }
+  else if (bpg == 2) { SPX_DLDS((kd_gateup_m<T, 2>), sm); hipLaunchKernelGGL((kd_gateup_m<T, 2>), grid, b, sm, s, a); }
+  else { SPX_DLDS((kd_gateup_m<T, 4>), sm); hipLaunchKernelGGL((kd_gateup_m<T, 4>), grid, b, sm, s, a); }
+  return hipGetLastError();
+}
+
+hipError_t launch_dec_gateup_m(const DecGateUpMArgs &a, int max_jobs, hipStream_t s) {
+  const int nb = (int)(a.gate.cols >> 8);
+  if (a.gate.cols % 256 || nb > DEC_MAXNB || a.gate.nb != nb || a.up.nb != nb || a.gate.dtype != a.up.dtype || a.m < 1 || a.m > MAX_M || max_jobs < 1)
+    return hipErrorInvalidValue;
+  if (a.gate.dtype == T_Q4K) return dec_gum_t<T_Q4K>(a, max_jobs, s);
+  if (a.gate.dtype == T_Q6K) return dec_gum_t<T_Q6K>(a, max_jobs, s);
+  return hipErrorInvalidValue;
+}
+
+template <int T>
+static hipError_t dec_downm_t(const DecDownMArgs &a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.w.rows + DEC_MM_NW - 1) / DEC_MM_NW)), b(DEC_MM_NW * 64);
+  const size_t sm = mm_act_bytes(a.m * a.n_used, (int)a.w.cols);
+  if (sm > 128 * 1024) return hipErrorInvalidValue;
+  switch (nb_bucket((int)a.w.nb)) {
+  case 1: SPX_DLDS((kd_down_m<T, 1>), sm); hipLaunchKernelGGL((kd_down_m<T, 1>), grid, b, sm, s, a); break;
+  case 2: SPX_DLDS((kd_down_m<T, 2>), sm); hipLaunchKernelGGL((kd_down_m<T, 2>), grid, b, sm, s, a); break;
+  case 3: SPX_DLDS((kd_down_m<T, 3>), sm); hipLaunchKernelGGL((kd_down_m<T, 3>), grid, b, sm, s, a); break;
+  case 4: SPX_DLDS((kd_down_m<T, 4>), sm); hipLaunchKernelGGL((kd_down_m<T, 4>), grid, b, sm, s, a); break;
+  default: return hipErrorInvalidValue;  // n_ff > 1024: the expert rows take the fused kernels
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_dec_down_m(const DecDownMArgs &a, hipStream_t s) {
+  if (a.w.cols % 256 || a.w.nb > 4 || a.n_used < 1 || a.n_used > 32 || a.m < 1 || a.m > MAX_M || (int64_t)a.m * a.n_used > MAX_M * 32) return hipErrorInvalidValue;
+  if (a.w.dtype == T_Q4K) return dec_downm_t<T_Q4K>(a, s);
+  if (a.w.dtype == T_Q6K) return dec_downm_t<T_Q6K>(a, s);
   return hipErrorInvalidValue;
 }
 

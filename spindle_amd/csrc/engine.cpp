@@ -470,12 +470,139 @@ int enqueue_decode(spx_engine *E, bool advance) {
   return 0;
 }
 
+// A pass of 2 <= m <= 16 rows on the decode pipeline's multi-row kernels: the same values as
+// enqueue_forward(E, m). Per layer: attn_norm (Q8_K of the rows), q/k/v, attention (the fused
+// multi-row kernel, its merge and the Q8_K of its output included), attn_output + residual,
+// ffn_norm, then router / routing + jobs / grouped gate-up / Q8_K of h / grouped down +
+// combine + residual (dense: gate-up / Q8_K of h / down + residual).
+int enqueue_pass_m(spx_engine *E, int m) {
+  const auto &c = E->c;
+  hipStream_t s = E->ctx->stream;
+  const int dim = c.dim, hd = c.head_dim, nu = E->n_used;
+  auto mtiles = [](const spx_tensor *t) {
+    int G, R;
+    rp_shape(t->v.nb, G, R);
+    return (int)((t->v.rows + DEC_MM_NW * R - 1) / (DEC_MM_NW * R));
+  };
+  auto gshape = [](const spx_tensor *t) { int G, R; rp_shape(t->v.nb, G, R); return G; };
+  auto norm = [&](const float *x, const float *nw, float *xn_out, Q8KP q) {
+    DecNormArgs na{x, nw, c.rms_eps, dim, xn_out, q};
+    return launch_dec_norm(na, m, s);
+  };
+  {
+    ProfScope ps(E, PC_EMBED, 0);
+    NormTail t{};
+    t.x = E->xA;
+    t.dim = dim;
+    SPX_HIP(launch_embed(E->embed->v, E->st_dev, c.embedding_scale, t, m, s));
+  }
+  for (int l = 0; l < c.n_layers; l++) {
+    const LayerW &ly = E->L[l];
+    {
+      ProfScope ps(E, PC_NORM, 0);
+      SPX_HIP(norm(E->xA, ly.attn_norm, nullptr, E->xq2));
+    }
+    {
+      ProfScope ps(E, PC_QKV, wbytes(ly.wq) + wbytes(ly.wk) + wbytes(ly.wv));
+      DecMMArgs a{};
+      const spx_tensor *w3[3] = {ly.wq, ly.wk, ly.wv};
+      float *o3[3] = {E->q, E->k, E->v};
+      const int64_t ld3[3] = {E->q_dim, E->kv_dim, E->kv_dim};
+      int total = 0;
+      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.ld_out[i] = ld3[i]; a.tiles[i] = mtiles(w3[i]); total += a.tiles[i]; }
+      a.nseg = 3; a.G = gshape(ly.wq); a.y = E->xq2; a.cols = dim; a.m = m;
+      SPX_HIP(launch_dec_mm(a, total, s));
+    }
+    const bool att_q_fused = ((c.n_heads / c.n_kv_heads) * hd) % 256 == 0;
+    {
+      ProfScope ps(E, PC_ATTN, -1.0 - l);
+      AttnArgs aa{};
+      aa.q = E->q; aa.k = E->k; aa.v = E->v;
+      aa.q_bias = ly.q_bias; aa.k_bias = ly.k_bias; aa.v_bias = ly.v_bias; aa.q_norm = ly.q_norm; aa.k_norm = ly.k_norm;
+      aa.rope = E->rope; aa.kc = E->kc; aa.vc = E->vc; aa.part_ml = E->part_ml; aa.part_o = E->part_o; aa.counter = E->att_cnt; aa.att = E->att;
+      if (att_q_fused) aa.aq = E->aq;
+      aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
+      aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
+      aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
+      SPX_HIP(launch_attention(aa, m, E->st_dev, s));
+    }
+    if (!att_q_fused) { ProfScope ps(E, PC_QUANT, 0); SPX_HIP(launch_q8kp_quantize(E->att, E->q_dim, E->q_dim, m, E->aq, s)); }
+    {
+      ProfScope ps(E, PC_WO, wbytes(ly.wo));
+      DecMMArgs a{};
+      a.w[0] = ly.wo->v; a.out[0] = E->proj; a.ld_out[0] = dim; a.tiles[0] = mtiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
+      a.y = E->aq; a.cols = E->q_dim; a.m = m;
+      a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
+      SPX_HIP(launch_dec_mm(a, a.tiles[0], s));
+    }
+    const int nff = (int)ly.gate->v.rows;
+    {
+      ProfScope ps(E, PC_NORM, 0);
+      SPX_HIP(norm(E->xB, ly.ffn_norm, ly.moe ? E->xn2 : nullptr, E->xq2));
+    }
+    DecGateUpMArgs ga{};
+    ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.h = E->h; ga.n_ff = nff; ga.m = m;
+    if (ly.moe) {  // moe_forward_batch (:925-1174)
+      {
+        ProfScope ps(E, PC_ROUTER, wbytes(ly.router));
+        DecRouterMArgs ra{ly.router->v, E->xn2, E->rlog, c.n_expert, dim, m};
+        SPX_HIP(launch_dec_router_m(ra, s));
+        DecRouteArgs rt{E->rlog, c.n_expert, c.n_expert_used, c.expert_norm, m, c.moe_prune, E->chosen, E->weights, E->nkeep,
+                        E->jobs, ly.njobs, E->expert_count + (size_t)l * c.n_expert};
+        SPX_HIP(launch_dec_route(rt, s));
+      }
+      {
+        ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up), l, true);
+        ga.jobs = E->jobs; ga.njobs = ly.njobs;
+        SPX_HIP(launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
+        SPX_HIP(launch_q8kp_quantize(E->h, nff, nff, m * nu, E->hq, s));
+      }
+      {
+        ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
+        DecDownMArgs da{ly.down->v, E->hq, E->jobs, ly.njobs, E->weights, E->nkeep, nu, m, E->xB, E->xA, c.residual_scale};
+        SPX_HIP(launch_dec_down_m(da, s));
+      }
+    } else {  // ffn_forward_multi (:616-646)
+      {
+        ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
+        SPX_HIP(launch_dec_gateup_m(ga, 1, s));
+        SPX_HIP(launch_q8kp_quantize(E->h, nff, nff, m, E->hq, s));
+      }
+      {
+        ProfScope ps(E, PC_DOWN, wbytes(ly.down));
+        DecMMArgs a{};
+        a.w[0] = ly.down->v; a.out[0] = E->ffn; a.ld_out[0] = dim; a.tiles[0] = mtiles(ly.down); a.nseg = 1; a.G = gshape(ly.down);
+        a.y = E->hq; a.cols = nff; a.m = m;
+        a.res_in = E->xB; a.res_out = E->xA; a.rscale = c.residual_scale;
+        SPX_HIP(launch_dec_mm(a, a.tiles[0], s));
+      }
+    }
+  }
+  int grid = 1;
+  {
+    ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
+    SPX_HIP(norm(E->xA, E->out_norm, E->xn, E->xq));
+    DecMMArgs a{};
+    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.ld_out[0] = c.vocab; a.tiles[0] = mtiles(E->lm_head); a.nseg = 1;
+    a.G = gshape(E->lm_head); a.y = E->xq; a.cols = dim; a.m = m;
+    grid = std::min(a.tiles[0], 512);
+    a.best = E->best; a.nbest = grid; a.lscale = c.logit_scale;
+    SPX_HIP(launch_dec_mm(a, grid, s));
+  }
+  E->nbest = grid;
+  {
+    ProfScope ps(E, PC_ARGMAX, 0);
+    SPX_HIP(launch_argmax_final(E->best, grid, E->amax, E->st_dev, nullptr, m, s));
+  }
+  return 0;
+}
+
 // Graph slot m (1..16): a pass of m rows; slot 0: a one-row decode pass that advances the
 // step record itself (back-to-back greedy decoding without host round trips).
 int run_forward(spx_engine *E, int m, bool advance = false) {
   hipStream_t s = E->ctx->stream;
-  const bool dec = m == 1 && E->dec_ok && E->dec_on;
-  auto enqueue = [&]() { return dec ? enqueue_decode(E, advance) : enqueue_forward(E, m, advance); };
+  const bool dec = E->dec_ok && E->dec_on;
+  auto enqueue = [&]() { return !dec ? enqueue_forward(E, m, advance) : m == 1 ? enqueue_decode(E, advance) : enqueue_pass_m(E, m); };
   if (!E->use_graphs || E->profiling) return enqueue();
   const int slot = advance ? 0 : m;
   if (!E->graph[slot]) {
@@ -678,6 +805,10 @@ int spx_engine_prepare(spx_engine *E) {
     if (ly.moe) dok = dok && (int64_t)nu * ly.gate->v.rows <= DEC_DOWN_Q;
   }
   E->dec_ok = dok;
+  // passes of 2..16 rows: expert down rows of at most 4 blocks (n_ff <= 1024)
+  // the down kernel stages every user's Q8_K h row in LDS: 16 rows x n_used users
+  for (auto &ly : E->L)
+    if (ly.moe && (ly.down->v.nb > 4 || (double)MAX_M * nu * ly.down->v.cols * (1.0 + 68.0 / 256.0) + 64 > 128.0 * 1024)) E->dec_ok = false;
   if (const char *v = std::getenv("SPX_DECODE")) E->dec_on = atoi(v) != 0;
   E->prepared = true;
   return 0;
@@ -691,9 +822,9 @@ int spx_engine_set_graphs(spx_engine *E, int on) {
 
 int spx_engine_set_decode(spx_engine *E, int on) {
   if (!E) return fail("null engine");
-  if (E->dec_on != (on != 0)) {  // the one-row graphs hold the other pipeline: capture again
+  if (E->dec_on != (on != 0)) {  // the captured graphs hold the other pipeline: capture again
     SPX_HIP(hipStreamSynchronize(E->ctx->stream));
-    for (int slot : {0, 1})
+    for (int slot = 0; slot <= MAX_M; slot++)
       if (E->graph[slot]) { (void)hipGraphExecDestroy(E->graph[slot]); E->graph[slot] = nullptr; }
   }
   E->dec_on = on != 0;

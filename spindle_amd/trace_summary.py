@@ -32,7 +32,7 @@ lines.append(f"kernels in trace: {len(rows)}; forward passes found: {len(passes)
 # classify by kernel count
 groups = collections.defaultdict(list)
 for p in passes:
-    sig = next((short(r[2]) for r in p if short(r[2]).startswith(("k_mvr", "k_mvt", "k_mv_f", "kd_mv"))), "none")
+    sig = next((short(r[2]) for r in p if short(r[2]).startswith(("k_mvr", "k_mvt", "k_mv_f", "kd_mv", "kd_mm"))), "none")
     groups[(len(p), sig)].append(p)
 for n, ps in sorted(groups.items()):
     spans = [(p[-1][1] - p[0][0]) / 1e3 for p in ps]

@@ -153,3 +153,29 @@ def test_decode_pipeline_matches_oracle(ctx, case):
     assert flips <= 0.15 * len(errs)
     assert np.median(errs) <= 1e-5
     eng.close()
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_multi_row_passes_bitwise(ctx, case):
+    """Passes of 2..16 rows on the pipeline's multi-row kernels (norm once per layer, grouped
+    expert jobs) against the fused pass kernels: the same bits for every row."""
+    cfg = CASES[case]
+    w = M.synth_model(cfg, seed=35)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    b.set_decode(False)
+    ids = np.random.default_rng(7).integers(0, cfg.vocab, 120)
+    pos = 0
+    for m in (16, 5, 2, 9, 16, 3, 1, 12, 16, 7):
+        am0, h0, l0 = a.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        am1, h1, l1 = b.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        assert _same(h0, h1), (case, m, pos, "hidden")
+        assert _same(l0, l1), (case, m, pos, "logits")
+        assert np.array_equal(am0, am1), (case, m, pos)
+        if cfg.moe:
+            assert np.array_equal(a.last_experts(), b.last_experts()), (case, m, pos)
+        pos += m
+    ka, va = a.kv_cache()
+    kb, vb = b.kv_cache()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    a.close()
+    b.close()

@@ -387,8 +387,49 @@ static void q5_0_codes(const uint8_t *blk, float q[32]) {
   }
 }
 
+/* Q5_K (quant.rs:1266-1313, dot_q5_k_row_avx2_presum with compute_subblock_sums_32 :167-178):
+ * per 32-value sub-block the activation sum act = hsum((x_l + x_{8+l}) + (x_{16+l} + x_{24+l}));
+ * per block min_term = sum_k mn_k * act_k (in k order), total_min += min_term * dmin; per
+ * sub-block j = 2c + h lane l: sqx_l = fma chain over elements l, 8+l, 16+l, 24+l (fma_u8x16
+ * :1163-1172), acc_l = fma(d * sc_j, sqx_l, acc_l); the row is hsum(acc) - total_min. */
+static float act_sum32(const float *p) {
+  float s[8];
+  for (int l = 0; l < 8; l++) s[l] = (p[l] + p[8 + l]) + (p[16 + l] + p[24 + l]);
+  return hsum_hadd(s);
+}
+static float dot_q5k_row(const uint8_t *row, size_t n, const float *x) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, total_min = 0.0f;
+  for (size_t b = 0; b < n / 256; b++) {
+    const uint8_t *blk = row + b * 176;
+    const float d = rd16(blk), dmin = rd16(blk + 2);
+    uint8_t sc[8], mn[8];
+    or_unpack_q4k_scales(blk + 4, sc, mn);
+    const uint8_t *qh = blk + 16, *qs = blk + 48;
+    const float *xb = x + b * 256;
+    float min_term = 0.0f;
+    for (int k = 0; k < 8; k++) min_term += (float)mn[k] * act_sum32(xb + 32 * k);
+    total_min += min_term * dmin;
+    for (int c = 0; c < 4; c++)
+      for (int h = 0; h < 2; h++) {
+        float q[32];
+        for (int t = 0; t < 32; t++) {
+          const uint32_t byte = qs[32 * c + t], nib = h ? byte >> 4 : byte & 0x0F;
+          q[t] = (float)(nib | (((uint32_t)(qh[t] >> (2 * c + h)) & 1u) << 4));
+        }
+        const float *xs = xb + 64 * c + 32 * h, dsc = d * (float)sc[2 * c + h];
+        for (int l = 0; l < 8; l++) {
+          float sq = 0.0f;
+          for (int k = 0; k < 4; k++) sq = fmaf(q[8 * k + l], xs[8 * k + l], sq);
+          acc[l] = fmaf(dsc, sq, acc[l]);
+        }
+      }
+  }
+  return hsum_hadd(acc) - total_min;
+}
+
 static float dot_float_row(const uint8_t *row, int dtype, size_t n, const float *x) {
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (dtype == OR_Q5K) return dot_q5k_row(row, n, x);
   if (dtype == OR_Q8_0 || dtype == OR_Q5_0) { /* quant.rs:48-161 */
     size_t bb = dtype == OR_Q8_0 ? 34 : 22;
     for (size_t b = 0; b < n / 32; b++) {
@@ -422,7 +463,7 @@ static void fjob_run(void *p, int t, int nt) {
 }
 
 int or_matvec_rows(const uint8_t *tensor, int dtype, size_t cols, const float *x, float *out, size_t r0, size_t nrows) {
-  if (!(dtype == OR_F32 || dtype == OR_F16 || dtype == OR_Q8_0 || dtype == OR_Q5_0)) return -1;
+  if (!(dtype == OR_F32 || dtype == OR_F16 || dtype == OR_Q8_0 || dtype == OR_Q5_0 || dtype == OR_Q5K)) return -1;
   if (!or_row_bytes(dtype, cols)) return -1;
   fjob j = {tensor, dtype, cols, x, out, r0, nrows};
   if (nrows * cols >= PAR_MIN_WEIGHTS) run_pool(fjob_run, &j); else fjob_run(&j, 0, 1);

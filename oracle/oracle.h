@@ -77,7 +77,7 @@ void or_q8k_block_sums(const uint8_t *row, int dtype, size_t cols, const int8_t 
                        const int16_t *xb, int32_t *sumi, int32_t *corr, int32_t *lanes);
 
 /* ---- float kernels ----
- * M=1 (quant.rs:937-1094): out[i] = row r0+i. Supported: F32, F16, Q8_0, Q5_0. */
+ * M=1 (quant.rs:937-1094): out[i] = row r0+i. Supported: F32, F16, Q8_0, Q5_0, Q5_K. */
 int or_matvec_rows(const uint8_t *tensor, int dtype, size_t cols, const float *x, float *out,
                    size_t r0, size_t nrows);
 /* M>1 shared-decode (quant_multi.rs:124-273): Q8_0, F32; others fall back per vector. */

@@ -25,7 +25,7 @@ int64_t block_elems(int dtype) {
   switch (dtype) {
   case T_F32: case T_F16: return 1;
   case T_Q5_0: case T_Q8_0: return 32;
-  case T_Q4K: case T_Q6K: return 256;
+  case T_Q4K: case T_Q5K: case T_Q6K: return 256;
   default: return 0;
   }
 }
@@ -38,6 +38,7 @@ int64_t row_bytes(int dtype, int64_t cols) {
   case T_Q5_0: bb = 22; break;
   case T_Q8_0: bb = 34; break;
   case T_Q4K: bb = 144; break;
+  case T_Q5K: bb = 176; break;
   case T_Q6K: bb = 210; break;
   default: return 0;
   }
@@ -64,11 +65,12 @@ static int fields_of(int dtype, Field *f) {
   case T_Q6K: f[0] = {0, 128, 0}; f[1] = {128, 64, 1}; f[2] = {192, 16, 2}; f[3] = {208, 2, 3}; return 4;
   case T_Q8_0: f[0] = {2, 32, 0}; f[1] = {0, 2, 3}; return 2;
   case T_Q5_0: f[0] = {6, 16, 0}; f[1] = {2, 4, 1}; f[2] = {0, 2, 3}; return 3;
+  case T_Q5K: f[0] = {48, 128, 0}; f[1] = {16, 32, 1}; f[2] = {0, 16, 2}; return 3;
   default: return 0;
   }
 }
 static int block_bytes(int dtype) {
-  switch (dtype) { case T_Q4K: return 144; case T_Q6K: return 210; case T_Q8_0: return 34; case T_Q5_0: return 22; default: return 0; }
+  switch (dtype) { case T_Q4K: return 144; case T_Q5K: return 176; case T_Q6K: return 210; case T_Q8_0: return 34; case T_Q5_0: return 22; default: return 0; }
 }
 
 // Byte order inside one plane record: device position of GGUF byte b of the field, so that
@@ -76,11 +78,15 @@ static int block_bytes(int dtype) {
 //   Q4_K codes  qs[32c + 4l + j]        -> 16l + 4c + j      (lane l: dword c, c = 0..3)
 //   Q6_K ql     ql[64h + 32mm + 4l + j] -> 16l + 8h + 4mm + j
 //   Q6_K qh     qh[32h + 4l + j]        -> 8l + 4h + j
+//   Q5_K codes  qs[32c + 8k + l]        -> 16l + 4c + k      (lane l: elements 8k + l of each 32)
+//   Q5_K qh     qh[8k + l]              -> 4l + k
 // Every other field keeps the GGUF order.
 static int perm_of(int dtype, int plane, int b) {
   if (dtype == T_Q4K && plane == 0) { const int c = b >> 5, l = (b >> 2) & 7, j = b & 3; return 16 * l + 4 * c + j; }
   if (dtype == T_Q6K && plane == 0) { const int h = b >> 6, mm = (b >> 5) & 1, l = (b >> 2) & 7, j = b & 3; return 16 * l + 8 * h + 4 * mm + j; }
   if (dtype == T_Q6K && plane == 1) { const int h = b >> 5, l = (b >> 2) & 7, j = b & 3; return 8 * l + 4 * h + j; }
+  if (dtype == T_Q5K && plane == 0) { const int c = b >> 5, k = (b >> 3) & 3, l = b & 7; return 16 * l + 4 * c + k; }
+  if (dtype == T_Q5K && plane == 1) { const int k = b >> 3, l = b & 7; return 4 * l + k; }
   return b;
 }
 
@@ -328,7 +334,8 @@ int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, in
     return mv_launch(ctx, w, expert, m, nullptr, 0, y, out, ld_out, 0, rows);
   }
   if (w->v.dtype == T_F32 && cols % 16) return fail("spx_matvec: F32 needs cols % 16 == 0");
-  if (w->v.dtype != T_Q8_0 && w->v.dtype != T_Q5_0 && w->v.dtype != T_F32) return fail("spx_matvec: unsupported dtype " + std::to_string(w->v.dtype));
+  if (w->v.dtype != T_Q8_0 && w->v.dtype != T_Q5_0 && w->v.dtype != T_Q5K && w->v.dtype != T_F32)
+    return fail("spx_matvec: unsupported dtype " + std::to_string(w->v.dtype));
   return mv_launch(ctx, w, expert, m, x, ld_x, Q8KP{}, out, ld_out, 0, rows);
 }
 

@@ -24,6 +24,8 @@ enum DType : int {
 //   Q6_K: p0 = ql (128, lane-permuted), p1 = qh (64, lane-permuted), p2 = scales (16), p3 = d (2)
 //   Q8_0: p0 = codes (32), p3 = d (2)
 //   Q5_0: p0 = low nibbles (16), p1 = high bits (4), p3 = d (2)
+//   Q5_K: p0 = codes (128, lane-permuted), p1 = high bits (32, lane-permuted), p2 = header (16 B:
+//         d, dmin, scales[12])
 //   F32 / F16: p0 = row-major values
 struct Planes {
   const uint8_t *p0, *p1, *p2, *p3;

@@ -45,7 +45,7 @@ struct LayerW {
 };
 
 bool is_kq(const spx_tensor *t) { return t && (t->v.dtype == T_Q4K || t->v.dtype == T_Q6K); }
-bool is_fq(const spx_tensor *t) { return t && (t->v.dtype == T_Q8_0 || t->v.dtype == T_Q5_0); }
+bool is_fq(const spx_tensor *t) { return t && (t->v.dtype == T_Q8_0 || t->v.dtype == T_Q5_0 || t->v.dtype == T_Q5K); }
 int bucket(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
 
 int64_t now_us() {
@@ -696,7 +696,7 @@ int spx_engine_prepare(spx_engine *E) {
     if (t->v.cols != cols || t->v.rows != rows || t->v.n_expert != ne)
       return fail(n + ": expected " + std::to_string(rows) + "x" + std::to_string(cols) + "x" + std::to_string(ne) + ", got " +
                   std::to_string(t->v.rows) + "x" + std::to_string(t->v.cols) + "x" + std::to_string(t->v.n_expert));
-    if (!is_kq(t) && !is_fq(t)) return fail(n + ": weight matrices must be Q4_K, Q6_K, Q8_0 or Q5_0 for the GPU kernels");
+    if (!is_kq(t) && !is_fq(t)) return fail(n + ": weight matrices must be Q4_K, Q6_K, Q8_0, Q5_0 or Q5_K for the GPU kernels");
     *dst = t;
     return 0;
   };
@@ -704,7 +704,7 @@ int spx_engine_prepare(spx_engine *E) {
   if (!E->embed || E->embed->v.cols != c.dim || E->embed->v.rows != c.vocab) return fail("missing or misshaped token_embd.weight");
   E->lm_head = mat("output.weight") ? mat("output.weight") : E->embed;  // tied embeddings (:1921)
   if (E->lm_head->v.cols != c.dim || E->lm_head->v.rows != c.vocab) return fail("misshaped output.weight");
-  if (!is_kq(E->lm_head) && !is_fq(E->lm_head)) return fail("the LM head must be Q4_K, Q6_K, Q8_0 or Q5_0");
+  if (!is_kq(E->lm_head) && !is_fq(E->lm_head)) return fail("the LM head must be Q4_K, Q6_K, Q8_0, Q5_0 or Q5_K");
   if (!(E->out_norm = vec("output_norm.weight", c.dim))) return fail("missing output_norm.weight");
   int nff_max = 0;
   for (int l = 0; l < c.n_layers; l++) {

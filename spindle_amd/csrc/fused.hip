@@ -371,9 +371,91 @@ template <> struct FRaw<T_Q5_0> {
   }
 };
 
+// Q5_K weights x fp32 activations: the reference's float kernel (dot_q5_k_row_avx2_presum,
+// quant.rs:1266-1313) lane for lane, lane l of the row group being its lane l: per 32-value
+// sub-block j = 2c + h the lane's chain sqx = fma over elements l, 8+l, 16+l, 24+l, then
+// acc = fma(d * sc_j, sqx, acc); per block the activation sums of the eight sub-blocks
+// (compute_subblock_sums_32 :167-178, the hadd tree over the lanes) give
+// total_min += (sum_k mn_k * act_k) * dmin; the row is hadd(acc) - total_min (lane 0).
+// Device layout: lane l's code bytes (qs[32c + 8k + l]) at 16l + 4c + k, its high-bit bytes
+// (qh[8k + l]) at 4l + k.
+__device__ __forceinline__ float hsum_hadd8(float a) {  // valid in lane 0 of the row group
+  const float x = a + SPX_SHLF(a, 4);  // x_l = a_l + a_{l+4}
+  const float t = x + SPX_SHLF(x, 1);  // lane 0: x0 + x1, lane 2: x2 + x3
+  return t + SPX_SHLF(t, 2);           // (x0 + x1) + (x2 + x3)
+}
+template <int MT>
+__device__ __forceinline__ void q5k_walk(const Planes &pl, int64_t grow, int nb, const float *x, int64_t ld_x, const int *vidx, int mv, int l,
+                                         float *res) {
+  float acc[MT], tmin[MT];
+#pragma unroll
+  for (int v = 0; v < MT; v++) { acc[v] = 0.0f; tmin[v] = 0.0f; }
+  for (int i = 0; i < nb; i++) {
+    const int64_t g = grow * nb + i;
+    const uint4 qs = ld16(pl.p0 + g * 128 + 16 * l);
+    const uint32_t qh = *reinterpret_cast<const uint32_t *>(pl.p1 + g * 32 + 4 * l);
+    const uint4 hd = ld16(pl.p2 + g * 16);
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    const uint32_t S0 = hd.y, S1 = hd.z, S2 = hd.w;  // unpack_q4k_scales (q4k_gemv.rs:70-85)
+    int sc[8], mn[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      sc[k] = (int)((S0 >> (8 * k)) & 63u);
+      mn[k] = (int)((S1 >> (8 * k)) & 63u);
+      sc[4 + k] = (int)(((S2 >> (8 * k)) & 15u) | (((S0 >> (8 * k + 6)) & 3u) << 4));
+      mn[4 + k] = (int)(((S2 >> (8 * k + 4)) & 15u) | (((S1 >> (8 * k + 6)) & 3u) << 4));
+    }
+    const uint32_t cw[4] = {qs.x, qs.y, qs.z, qs.w};  // word c: byte k = qs[32c + 8k + l]
+#pragma unroll
+    for (int v = 0; v < MT; v++) {
+      if (v < mv) {
+        const float *xb = x + (int64_t)vidx[v] * ld_x + (int64_t)i * 256 + l;
+        float xv[32];  // xv[8j + k] = value 32j + 8k + l of the block
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+#pragma unroll
+          for (int k = 0; k < 4; k++) xv[4 * j + k] = xb[32 * j + 8 * k];
+        float min_term = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float p = (xv[4 * j] + xv[4 * j + 1]) + (xv[4 * j + 2] + xv[4 * j + 3]);
+          min_term += (float)mn[j] * hsum_hadd8(p);
+        }
+        tmin[v] += min_term * dmin;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+          for (int h = 0; h < 2; h++) {
+            const int j = 2 * c + h;
+            float sq = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+              const uint32_t byte = (cw[c] >> (8 * k)) & 0xffu, nib = h ? byte >> 4 : byte & 15u;
+              const uint32_t q = nib | (((qh >> (8 * k + j)) & 1u) << 4);
+              sq = fmaf((float)q, xv[4 * j + k], sq);
+            }
+            acc[v] = fmaf(d * (float)sc[j], sq, acc[v]);
+          }
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < MT; v++) res[v] = hsum_hadd8(acc[v]) - tmin[v];
+}
+
+template <> struct FRaw<T_Q5K> {  // not used: Q5_K rows take q5k_walk
+  uint32_t d;
+  __device__ __forceinline__ void load(const Planes &, int64_t) {}
+  __device__ __forceinline__ void decode(float q[32]) const {}
+};
+
 template <int T, int MT, int D>
 __device__ __forceinline__ void f_walk(const Planes &pl, int64_t grow, int nb, const float *x, int64_t ld_x, const int *vidx, int mv, int l,
                                        float *res) {
+  if constexpr (T == T_Q5K) {
+    q5k_walk<MT>(pl, grow, nb, x, ld_x, vidx, mv, l, res);
+    return;
+  }
   float acc[MT];
 #pragma unroll
   for (int v = 0; v < MT; v++) acc[v] = 0.0f;
@@ -629,6 +711,7 @@ __global__ __launch_bounds__(256) void k_mv_f(const MVArgs a, const StepRec *st)
     const Seg &sg = a.seg[seg_index(a, t, wg)];
     if (sg.w.dtype == T_Q8_0) mv_f_task<T_Q8_0, MT>(a, sg, wg, m, coh, bestv);
     else if (sg.w.dtype == T_Q5_0) mv_f_task<T_Q5_0, MT>(a, sg, wg, m, coh, bestv);
+    else if (sg.w.dtype == T_Q5K) mv_f_task<T_Q5K, MT>(a, sg, wg, m, coh, bestv);
     else mv_f_task<T_F32, MT>(a, sg, wg, m, coh, bestv);
   }
   if (a.best) best_flush<MT, 4>(a, bestv, m);
@@ -722,6 +805,20 @@ __global__ __launch_bounds__(256) void k_embed(TensorView e, const StepRec *st, 
       else { sc = (s[jj + 4] & 0xF) | ((s[jj - 4] >> 6) << 4); mn = (s[jj + 4] >> 4) | ((s[jj] >> 6) << 4); }
       const int byte = e.pl.p0[g * 128 + 16 * (tt >> 2) + 4 * c + (tt & 3)];
       const int q = hi ? (byte >> 4) : (byte & 0xF);
+      v = dd * (float)sc * (float)q - dm * (float)mn;
+    } else if (e.dtype == T_Q5K) {  // element 64c + 32h + t: qs[32c + t] (device 16(t%8) + 4c + t/8), qh[t] bit 2c+h
+      const int64_t g = tok * e.nb + j / 256;
+      const int k = (int)(j % 256), c = k / 64, tt = k % 32, hi = (k % 64) >= 32;
+      const uint8_t *hd = e.pl.p2 + g * 16;
+      const float dd = h2f(hd[0] | (hd[1] << 8)), dm = h2f(hd[2] | (hd[3] << 8));
+      const uint8_t *s = hd + 4;
+      const int jj = 2 * c + hi;
+      int sc, mn;
+      if (jj < 4) { sc = s[jj] & 63; mn = s[jj + 4] & 63; }
+      else { sc = (s[jj + 4] & 0xF) | ((s[jj - 4] >> 6) << 4); mn = (s[jj + 4] >> 4) | ((s[jj] >> 6) << 4); }
+      const int byte = e.pl.p0[g * 128 + 16 * (tt & 7) + 4 * c + (tt >> 3)];
+      const int qhb = e.pl.p1[g * 32 + 4 * (tt & 7) + (tt >> 3)];
+      const int q = (hi ? (byte >> 4) : (byte & 0xF)) | (((qhb >> jj) & 1) << 4);
       v = dd * (float)sc * (float)q - dm * (float)mn;
     } else if (e.dtype == T_Q6K) {  // element 128h + 32mq + t
       const int64_t g = tok * e.nb + j / 256;
@@ -1798,6 +1895,7 @@ hipError_t launch_gateup(const GUArgs &a, int mt, int mode, const StepRec *st, i
   case T_Q6K: return launch_gu_dt<T_Q6K>(a, mt, mode, st, max_jobs, s);
   case T_Q8_0: return launch_gu_dt<T_Q8_0>(a, mt, mode, st, max_jobs, s);
   case T_Q5_0: return launch_gu_dt<T_Q5_0>(a, mt, mode, st, max_jobs, s);
+  case T_Q5K: return launch_gu_dt<T_Q5K>(a, mt, mode, st, max_jobs, s);
   default: return hipErrorInvalidValue;
   }
 }
@@ -1846,6 +1944,7 @@ hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, h
   case T_Q6K: return launch_down_dt<T_Q6K>(a, mt, mode, st, s);
   case T_Q8_0: return launch_down_dt<T_Q8_0>(a, mt, mode, st, s);
   case T_Q5_0: return launch_down_dt<T_Q5_0>(a, mt, mode, st, s);
+  case T_Q5K: return launch_down_dt<T_Q5K>(a, mt, mode, st, s);
   default: return hipErrorInvalidValue;
   }
 }

@@ -10,6 +10,7 @@
 //         converted with round-to-nearest-even).
 //   Q8_0: codes uniform in [-127, 127]; d = f16(sigma/73.6 * j).
 //   Q5_0: low nibbles and high bits uniform; d = f16(sigma/9.23 * j).
+//   Q5_K: scales/mins, high bits and codes uniform; d = f16(sigma/533 * j), dmin = f16(15.5 * d).
 //   F32:  kind 1: uniform with standard deviation sigma; kind 2: 1 + sigma * U(-1, 1).
 #include <string.h>
 
@@ -92,6 +93,14 @@ void gen_block(int dtype, uint8_t *blk, uint64_t seed, uint64_t g, float sigma) 
     memcpy(blk + 2, &dm, 2);
     break;
   }
+  case spx::T_Q5K: {
+    fill_bytes(blk + 4, 172, seed, base);
+    const uint16_t d = f2h(sigma / 533.0f * j);
+    const uint16_t dm = f2h(15.5f * h2f_host(d));
+    memcpy(blk, &d, 2);
+    memcpy(blk + 2, &dm, 2);
+    break;
+  }
   case spx::T_Q6K: {
     fill_bytes(blk, 208, seed, base);
     const uint16_t d = f2h(sigma / 1365.3f * j);
@@ -120,7 +129,7 @@ void gen_block(int dtype, uint8_t *blk, uint64_t seed, uint64_t g, float sigma) 
 extern "C" {
 
 // Fills `out` (GGUF layout, n_expert slabs of rows x cols) with seeded synthetic values.
-// kind 0: quantized weights (dtype Q4_K/Q6_K/Q8_0/Q5_0) with std sigma; kind 1: F32 uniform
+// kind 0: quantized weights (dtype Q4_K/Q5_K/Q6_K/Q8_0/Q5_0) with std sigma; kind 1: F32 uniform
 // with std sigma; kind 2: F32 1 + sigma*U(-1,1) (norm weights).
 int spx_synth_tensor(int dtype, int64_t cols, int64_t rows, int n_expert, uint64_t seed, float sigma, int kind, void *out) {
   const int64_t rb = spx::row_bytes(dtype, cols);

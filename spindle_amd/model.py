@@ -16,8 +16,8 @@ import numpy as np
 
 from ._lib import P, check, lib, load
 
-F32, F16, Q5_0, Q8_0, Q4K, Q6K = 0, 1, 6, 8, 12, 14
-BLOCK = {F32: (1, 4), F16: (1, 2), Q5_0: (32, 22), Q8_0: (32, 34), Q4K: (256, 144), Q6K: (256, 210)}
+F32, F16, Q5_0, Q8_0, Q4K, Q5K, Q6K = 0, 1, 6, 8, 12, 13, 14
+BLOCK = {F32: (1, 4), F16: (1, 2), Q5_0: (32, 22), Q8_0: (32, 34), Q4K: (256, 144), Q5K: (256, 176), Q6K: (256, 210)}
 
 
 def row_bytes(dtype, cols):
@@ -110,6 +110,9 @@ TINY = {
     "tiny-granite": ModelConfig("tiny-granite", "granitemoe", 256, 2, 4, 2, 64, 128, 777, max_seq=256, rms_eps=1e-6,
                                 n_expert=8, n_expert_used=4, embedding_scale=12.0, residual_scale=0.22,
                                 logit_scale=6.0, attn_scale=0.03),
+    "tiny-q5k": ModelConfig("tiny-q5k", "qwen3", 256, 2, 4, 2, 64, 768, 1000, max_seq=256, rope_theta=1e6, rms_eps=1e-6,
+                            qk_norm=True, t_embd=Q5K, t_q=Q5K, t_k=Q5K, t_v=Q5K, t_o=Q5K, t_gate=Q5K, t_up=Q5K, t_down=Q5K,
+                            t_out=Q5K),
     "tiny-qwen3moe": ModelConfig("tiny-qwen3moe", "qwen3moe", 512, 3, 8, 2, 64, 256, 1000, max_seq=320,
                                  rope_theta=1e6, rms_eps=1e-6, qk_norm=True, n_expert=16, n_expert_used=4,
                                  tied=False, t_embd=Q4K, t_q=Q4K, t_k=Q4K, t_v=Q6K, t_o=Q4K, t_gate=Q4K,

@@ -15,7 +15,7 @@ from oracle.model import OracleModel
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
-FAMILIES = ["tiny-llama", "tiny-qwen3", "tiny-granite", "tiny-qwen3moe"]
+FAMILIES = ["tiny-llama", "tiny-qwen3", "tiny-granite", "tiny-qwen3moe", "tiny-q5k"]
 
 
 @pytest.fixture(scope="module")

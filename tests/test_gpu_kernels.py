@@ -151,17 +151,21 @@ def test_int_matvec_real_shapes(ctx, dtype, n, rows, ne, mv_mode):
             assert np.array_equal(got[v].view(np.uint32), want.view(np.uint32)), (e, v)
 
 
-@pytest.mark.parametrize("dtype", [R.Q8_0, R.Q5_0, R.F32])
+@pytest.mark.parametrize("dtype", [R.Q8_0, R.Q5_0, R.Q5K, R.F32])
 def test_float_matvec(ctx, dtype):
     from spindle_amd import ops
     rng = np.random.default_rng(dtype)
     for n, rows in [(1024, 100), (576, 64), (3072, 65)]:
+        if dtype == R.Q5K and n % 256:
+            n = 768
         if dtype == R.F32:
             raw = rng.uniform(-1, 1, n * rows).astype(np.float32).view(np.uint8)
         else:
-            bb = 34 if dtype == R.Q8_0 else 22
+            bb = {R.Q8_0: 34, R.Q5_0: 22, R.Q5K: 176}[dtype]
             raw = rng.integers(0, 256, R.row_bytes(dtype, n) * rows, dtype=np.uint8)
             raw.reshape(-1, bb)[:, 0:2] = np.float16(rng.uniform(0.001, 0.05, raw.size // bb)).view(np.uint8).reshape(-1, 2)
+            if dtype == R.Q5K:  # dmin
+                raw.reshape(-1, bb)[:, 2:4] = np.float16(rng.uniform(0.001, 0.05, raw.size // bb)).view(np.uint8).reshape(-1, 2)
         w = ops.Tensor(ctx, dtype, n, rows, raw)
         x = rng.standard_normal((9, n)).astype(np.float32)
         got = ops.matvec(ctx, w, _cuda(x)).cpu().numpy()
@@ -170,13 +174,15 @@ def test_float_matvec(ctx, dtype):
         for v in range(9):
             want = ffi.matvec(m1, x[v])              # the reference's M=1 kernel
             assert _norm_err(got[v], want) <= 1e-4
+            if dtype == R.Q5K:  # the GPU walker follows the reference's lanes: the same bits
+                assert np.array_equal(got[v].view(np.uint32), want.view(np.uint32)), v
             scale = np.abs(wd * x[v].astype(np.float64)).sum(1)
             assert np.all(np.abs(got[v] - wd @ x[v].astype(np.float64)) <= 1e-4 * scale + 1e-6)
         one = ops.matvec(ctx, w, _cuda(x[4:5])).cpu().numpy()
         assert np.array_equal(one.view(np.uint32), got[4:5].view(np.uint32))
 
 
-@pytest.mark.parametrize("dtype,n", [(R.Q4K, 2048), (R.Q6K, 768), (R.Q8_0, 1024), (R.Q5_0, 576), (R.F32, 64)])
+@pytest.mark.parametrize("dtype,n", [(R.Q4K, 2048), (R.Q6K, 768), (R.Q8_0, 1024), (R.Q5_0, 576), (R.Q5K, 512), (R.F32, 64)])
 def test_tensor_round_trip(ctx, dtype, n):
     from spindle_amd import ops
     rng = np.random.default_rng(1)

@@ -105,3 +105,38 @@ def test_q8k_quantize_nonfinite_block_is_zero():
     d, qs, bs = ffi.q8k_quantize(x)
     assert d[1] == 0 and not qs[256:].any() and not bs[16:].any()
     assert d[0] == np.float32(1.0) / np.float32(127.0) and np.all(qs[:256] == 127)
+
+
+def test_q5k_dequant_pinned_by_q4k_and_the_high_bit_rule():
+    """Q5_K (quant.rs:1122-1137, dequant :1612-1640) shares Q4_K's header and code nibbles:
+    with every high bit clear a Q5_K block dequantizes exactly like the Q4_K block with the
+    same d, dmin, scales and codes (Q4_K is pinned by the known-answer blocks above); setting
+    bit 2c+h of qh[t] raises exactly element 64c + 32h + t, by 16 * d * sc_(2c+h) in code units
+    (the value is recomputed from the code, so compare through the dequant of code + 16)."""
+    rng = np.random.default_rng(3)
+    hdr = bytearray(rng.integers(0, 256, 16, dtype=np.uint8).tobytes())
+    hdr[0:2] = np.float16(0.03).tobytes()
+    hdr[2:4] = np.float16(0.01).tobytes()
+    qs = rng.integers(0, 256, 128, dtype=np.uint8).tobytes()
+    q4 = np.frombuffer(bytes(hdr) + qs, np.uint8).copy()
+    q5 = np.frombuffer(bytes(hdr) + bytes(32) + qs, np.uint8).copy()
+    base = ffi.dequant_row(ffi.Q4K, q4, 256)
+    assert np.array_equal(ffi.dequant_row(ffi.Q5K, q5, 256), base)
+    d = float(np.frombuffer(bytes(hdr[0:2]), np.float16)[0])
+    dmin = float(np.frombuffer(bytes(hdr[2:4]), np.float16)[0])
+    s12 = hdr[4:16]
+    def scale_min(j):  # unpack_q4k_scales (q4k_gemv.rs:70-85)
+        if j < 4:
+            return s12[j] & 63, s12[j + 4] & 63
+        return (s12[j + 4] & 0xF) | ((s12[j - 4] >> 6) << 4), (s12[j + 4] >> 4) | ((s12[j] >> 6) << 4)
+    for t, c, h in [(0, 0, 0), (5, 1, 1), (31, 3, 0), (17, 2, 1), (8, 3, 1)]:
+        blk = bytearray(q5.tobytes())
+        blk[16 + t] |= 1 << (2 * c + h)
+        y = ffi.dequant_row(ffi.Q5K, np.frombuffer(bytes(blk), np.uint8).copy(), 256)
+        e = 64 * c + 32 * h + t
+        changed = np.nonzero(y != base)[0]
+        assert changed.tolist() == [e], (t, c, h, changed)
+        sc, mn = scale_min(2 * c + h)
+        code = (qs[32 * c + t] >> 4) if h else (qs[32 * c + t] & 0xF)
+        want = np.float32(np.float32(d * sc) * np.float32(code + 16)) - np.float32(np.float32(dmin) * np.float32(mn))
+        assert y[e] == want, (t, c, h, y[e], want)

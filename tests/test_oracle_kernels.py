@@ -99,12 +99,12 @@ def test_int_lane_partition():
 
 
 SIMD_TYPES = [R.F32, R.F16, R.BF16, R.Q4_0, R.Q4_1, R.Q5_0, R.Q5_1, R.Q8_0, R.Q4K, R.Q5K, R.Q6K]
-ORACLE_FLOAT = {R.F32, R.F16, R.Q5_0, R.Q8_0}
+ORACLE_FLOAT = {R.F32, R.F16, R.Q5_0, R.Q8_0, R.Q5K}
 
 
 def test_float_kernels_match_scalar_reference():
     """quant.rs:1727-1771 with the same seed; the oracle restates the float kernels the
-    decode path uses (F32, F16, Q5_0, Q8_0), the other types only consume the stream."""
+    decode path uses (F32, F16, Q5_0, Q8_0, Q5_K), the other types only consume the stream."""
     rng = R.Rng(0x2545F4914F6CDD1D)
     for dtype in SIMD_TYPES:
         for n in (256, 768, 2048):

@@ -28,12 +28,13 @@ HBM_PEAK_GBS = 8000.0
 
 # HBM bytes per M=1 decode launch at context ~4.1K, measured with rocprofv3 hardware counters
 # (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, factors from a 512 MiB copy measured the same way) by
-# spindle_amd.traffic_probe; profiles/decode_qwen3_30b_a3b_hbm_traffic.txt holds the runs.
-# Counters cannot be read inside a timed run, so the bench reports this measurement.
+# spindle_amd.traffic_probe; profiles/decode_qwen3_30b_a3b_hbm_traffic.txt holds the runs. The
+# attention class is the split-K kernel plus its merge. Counters cannot be read inside a timed
+# run, so the bench reports this measurement.
 MEASURED_TRAFFIC = {
-    "attention": 11_235_328, "qkv_matvec": 6_455_296, "attn_output_matvec": 5_064_499,
-    "router_route": 1_191_629, "gate_up_swiglu": 14_630_502, "down_combine": 11_404_902,
-    "lm_head_matvec": 256_084_480,
+    "attention": 11_698_381, "qkv_matvec": 6_425_600, "attn_output_matvec": 4_982_784,
+    "router_route": 1_234_944, "gate_up_swiglu": 14_438_298, "down_combine": 10_976_256,
+    "lm_head_matvec": 256_884_122,
 }
 
 

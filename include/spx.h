@@ -106,13 +106,15 @@ int spx_engine_set_tensor(spx_engine *e, const char *name, int dtype, int64_t co
 int spx_engine_prepare(spx_engine *e);
 /* 1 (default): each pass length m is captured once into a HIP graph and replayed. */
 int spx_engine_set_graphs(spx_engine *e, int on);
-/* 1 (default): one-token passes (forward_slice :3364-3552, the decode step of generate_reply
- * :4205-4348) run on the decode pipeline, a launch chain whose kernels meet only at kernel
- * boundaries; 0: on the fused pass kernels that m > 1 passes use. Both give the same values.
- * The pipeline takes models whose matrices are all Q4_K / Q6_K (others always use the fused
- * kernels); spx_engine_decode_pipeline reports whether one-token passes use it. */
+/* 1 (default): passes (forward_slice :3364-3552 for one token, forward_batch_slice :3142-3362
+ * for 2..16 rows, as in the decode and verify steps of generate_reply :4205-4348) run on the
+ * decode pipeline, launch chains whose kernels meet only at kernel boundaries; 0: on the fused
+ * pass kernels. Both give the same values, bit for bit. The pipeline takes models whose
+ * matrices are all Q4_K / Q6_K (others always use the fused kernels);
+ * spx_engine_decode_pipeline reports whether passes use it. No counterpart in the reference
+ * (a choice between two implementations of its passes). */
 int spx_engine_set_decode(spx_engine *e, int on);
-int spx_engine_decode_pipeline(spx_engine *e, int *active);
+int spx_engine_decode_pipeline(spx_engine *e, int *active);  /* *active = 1: the pipeline runs */
 
 /* One pass of m <= 16 tokens at positions start_pos.. (forward_slice :3364-3552 for m == 1,
  * forward_batch_slice :3142-3362 for m > 1, then compute_logits_batch :3588-3602 and the

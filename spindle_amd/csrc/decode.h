@@ -104,6 +104,16 @@ struct DecNormArgs {
   int dim;
   float *xn_out;      // [m][dim] (null: not written)
   Q8KP q_out;         // [m] (q null: not written)
+  // MoE combine ahead of the norm (yd null: none): row b is
+  // res_in[b] + rscale * sum_i cw[b][i] * yd[b * n_used + i] over its kept choices in choice
+  // order (unfused multiply and add, ffns_fused :432-437), written to x_out, then normalised
+  const float *yd;    // [m * n_used][dim]
+  const float *cw;    // [16][32] choice weights
+  const int *nkeep;   // [16]
+  const float *res_in;
+  float *x_out;
+  int n_used;
+  float rscale;
 };
 
 // Integer matvec of m vectors (Q8_K, global) over up to three segments.
@@ -146,34 +156,45 @@ struct DecRouteArgs {
   int *expert_count;  // [n_expert] (null: none)
 };
 
-// Gate/up + SwiGLU over the jobs (jobs null: dense, users = rows 0..m-1).
+// Routing of the m rows, then gate/up + SwiGLU over the jobs (rt.logits null: dense, one job
+// of users 0..m-1). Every workgroup routes the rows and builds the job list itself; workgroup 0
+// publishes the routing results, the job list and the selection counts (rt's outputs).
 struct DecGateUpMArgs {
   TensorView gate, up;
   Q8KP y;             // normalised rows [m]
-  const Job *jobs;
-  const int *njobs;
+  DecRouteArgs rt;
   float *h;           // [m * n_used][n_ff] (dense: [m][n_ff])
   int n_ff, m;
+  int max_jobs;       // bound of the job count (set by the launcher)
 };
 
-// Down projection over the jobs, weighted combine per row, residual add.
+// Down projection of the jobs' users (y per (user, row), combined by the next kd_norm).
 struct DecDownMArgs {
   TensorView w;
-  Q8KP hq;            // Q8_K of h [m * n_used]
+  const float *h;     // [m * n_used][n_ff] fp32 (quantized to Q8_K by the kernel)
   const Job *jobs;
   const int *njobs;
-  const float *weights;
-  const int *nkeep;
-  int n_used, m;
-  const float *res_in;
-  float *res_out;
-  float rscale;
+  float *yd;          // [m * n_used][dim]: y of each (row, choice), combined by the next kd_norm
+  int max_jobs;       // bound of the job count
 };
+
+// LDS image of m Q8_K vectors of cols columns (codes, scales, bsum pairs), as kd_mm and the
+// grouped expert kernels stage them.
+__host__ __device__ inline size_t mm_act_bytes(int m, int cols) {
+  const int nbq = cols >> 8;
+  return (((size_t)m * cols + 15) & ~(size_t)15) + (((size_t)m * nbq * 4 + 15) & ~(size_t)15) + (size_t)m * nbq * 64;
+}
+// kd_down_m's LDS: one job's users' Q8_K h
+__host__ __device__ inline size_t downm_lds_bytes(int n_ff) { return mm_act_bytes(MAX_M, n_ff); }
+
+// kd_gateup_m's LDS: one job's users' Q8_K rows, the chain buffers, the job table
+__host__ __device__ inline size_t gum_lds_bytes(int m, int cols, int max_jobs) {
+  return mm_act_bytes(m, cols) + (size_t)DEC_MM_NW * 2 * 4 * m * 10 * 4 + (size_t)max_jobs * (2 + 2 * MAX_M) * 4;
+}
 
 hipError_t launch_dec_norm(const DecNormArgs &a, int m, hipStream_t s);
 hipError_t launch_dec_mm(const DecMMArgs &a, int grid, hipStream_t s);
 hipError_t launch_dec_router_m(const DecRouterMArgs &a, hipStream_t s);
-hipError_t launch_dec_route(const DecRouteArgs &a, hipStream_t s);
 hipError_t launch_dec_gateup_m(const DecGateUpMArgs &a, int max_jobs, hipStream_t s);
 hipError_t launch_dec_down_m(const DecDownMArgs &a, hipStream_t s);
 hipError_t launch_dec_merge(const DecMergeArgs &a, const StepRec *st, hipStream_t s);

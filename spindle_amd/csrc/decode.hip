@@ -499,23 +499,31 @@ __device__ __forceinline__ void route_row(const float (&lv)[4], int ne, int nu, 
 #pragma unroll
   for (int k = 0; k < 4; k++) { const int e = lane + 64 * k; pv[k] = e < ne ? expf(lv[k] - mx) : 0.0f; sum += pv[k]; }
   sum = wave_sum(sum);
-  unsigned long long key[4];
+  // key = probability bits + 1 (non-negative floats order as their bits); 0: no expert or
+  // taken. Each round: the wave's largest key, then the lowest expert index holding it
+  // (experts lane + 64k, k ascending, by ballots).
+  uint32_t key[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     const int e = lane + 64 * k;
     if (e < ne) pv[k] = pv[k] / sum;
-    key[k] = e < ne ? ((unsigned long long)__float_as_uint(pv[k]) << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)e) : 0ull;
+    key[k] = e < ne ? __float_as_uint(pv[k]) + 1u : 0u;
   }
   my_e = 0;
   my_p = 0.0f;
   for (int i = 0; i < nu; i++) {
-    unsigned long long bk = key[0];
+    const uint32_t bk = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+    int e = 0;
 #pragma unroll
-    for (int k = 1; k < 4; k++) bk = key[k] > bk ? key[k] : bk;
-    bk = wave_max_u64(bk);
-    const int e = (int)(0xFFFFFFFFu - (unsigned)(bk & 0xFFFFFFFFull));
-    if (lane == i) { my_e = e; my_p = __uint_as_float((uint32_t)(bk >> 32)); }
-    if ((e & 63) == lane) key[e >> 6] = 0ull;
+    for (int k = 3; k >= 0; k--) {
+      const unsigned long long bal = __ballot(key[k] == bk);
+      if (bal) e = 64 * k + (int)__builtin_ctzll(bal);
+    }
+    if (lane == i) { my_e = e; my_p = __uint_as_float(bk - 1u); }
+    if ((e & 63) == lane) {
+      const int k = e >> 6;
+      if (k == 0) key[0] = 0u; else if (k == 1) key[1] = 0u; else if (k == 2) key[2] = 0u; else key[3] = 0u;
+    }
   }
   keep = nu;
   if (moe_prune > 0.0f && nu > 2) {
@@ -671,9 +679,48 @@ __global__ __launch_bounds__(256) void kd_norm(const DecNormArgs a) {
   constexpr int NW = 4, KB = DEC_MAXNB / NW;
   __shared__ float bsum_[DEC_MAXNB];
   const int b = blockIdx.x, nbq = a.dim >> 8;
-  const DecIn in{a.x + (int64_t)b * a.dim, a.nw, a.eps, a.dim};
+  const DecIn in{(a.yd ? a.res_in : a.x) + (int64_t)b * a.dim, a.nw, a.eps, a.dim};
   InRow<KB> r;
   in_load<NW, KB>(in, r);
+  if (a.yd) {  // the MoE combine of row b: kept choices in choice order, then the residual add
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nk = gld<int>(a.nkeep + b);
+    const float *yr = a.yd + (int64_t)b * a.n_used * a.dim;
+    float4 acc[KB];
+#pragma unroll
+    for (int k = 0; k < KB; k++) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i0 = 0; i0 < nk; i0 += 4) {  // four choices' loads in flight, then their sums in order
+      float wv[4];
+      float4 yv[4][KB];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int i = min(i0 + t, nk - 1);
+        wv[t] = gld<float>(a.cw + b * 32 + i);
+#pragma unroll
+        for (int k = 0; k < KB; k++) {
+          const int tb = wave + NW * k;
+          yv[t][k] = tb < nbq ? gld<float4>(yr + (int64_t)i * a.dim + 4 * (tb * 64 + lane)) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+        if (i0 + t < nk)
+#pragma unroll
+          for (int k = 0; k < KB; k++) {
+            acc[k].x = acc[k].x + wv[t] * yv[t][k].x; acc[k].y = acc[k].y + wv[t] * yv[t][k].y;
+            acc[k].z = acc[k].z + wv[t] * yv[t][k].z; acc[k].w = acc[k].w + wv[t] * yv[t][k].w;
+          }
+    }
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+      const int tb = wave + NW * k;
+      if (tb < nbq) {
+        float4 x = r.v[k];
+        x.x = x.x + a.rscale * acc[k].x; x.y = x.y + a.rscale * acc[k].y; x.z = x.z + a.rscale * acc[k].z; x.w = x.w + a.rscale * acc[k].w;
+        r.v[k] = x;
+        gst<float4>(a.x_out + (int64_t)b * a.dim + 4 * (tb * 64 + lane), x);
+      }
+    }
+  }
   float *xn = a.xn_out ? a.xn_out + (int64_t)b * a.dim : nullptr;
   if (a.q_out.q) {
     in_quant<NW, KB>(in, r, (SPX_G uint32_t *)(a.q_out.q + (int64_t)b * a.dim / 4), (SPX_G float *)(a.q_out.d + (int64_t)b * nbq),
@@ -692,16 +739,12 @@ __global__ __launch_bounds__(256) void kd_norm(const DecNormArgs a) {
 // computes block gi + G * j for every vector into the chain buffer; then the group that owns
 // vector v (v mod G) advances v's chain over the round's blocks in order. The chain per
 // vector is the reference's, block by block (the same fp32 values as one vector alone).
-__host__ __device__ inline size_t mm_act_bytes(int m, int cols) {
-  const int nbq = cols >> 8;
-  return (((size_t)m * cols + 15) & ~(size_t)15) + (((size_t)m * nbq * 4 + 15) & ~(size_t)15) + (size_t)m * nbq * 64;
-}
 __host__ __device__ inline size_t mm_lds_bytes(int m, int cols) { return mm_act_bytes(m, cols) + (size_t)DEC_MM_NW * 80 * m * 4; }
 
 // Copies m permuted Q8_K vectors (global y, cols columns; vector v from y's vector vsrc[v],
 // or v) into LDS (lq, ld, lbs), all threads; each thread's loads go out before its stores.
-template <int NT>
-__device__ __forceinline__ void stage_q8(const Q8KP &y, const int *vsrc, int m, int cols, SPX_L uint32_t *lq, SPX_L float *ld, SPX_L int2 *lbs) {
+template <int NT, class VP = const int *>
+__device__ __forceinline__ void stage_q8(const Q8KP &y, VP vsrc, int m, int cols, SPX_L uint32_t *lq, SPX_L float *ld, SPX_L int2 *lbs) {
   const int nbq = cols >> 8, n16 = cols / 16, nb16 = nbq * 4, nq = m * n16, nb4 = m * nb16;
   const int tid = threadIdx.x;
   for (int i0 = tid; i0 < nq; i0 += 4 * NT) {  // loads of four rounds go out before their stores
@@ -824,7 +867,7 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
     else rp_load<T_Q6K, BPG>(raw, pl, grow, nb, G, gi, l);                                       \
   } while (0)
   if (t < total) SPX_MM_LOCATE();
-  stage_q8<DEC_MM_NW * 64>(a.y, nullptr, m, cols, lq, ld, lbs);
+  stage_q8<DEC_MM_NW * 64>(a.y, (const int *)nullptr, m, cols, lq, ld, lbs);
   __syncthreads();
   for (; t < total;) {
     float acc[QN], cr[QN];
@@ -920,221 +963,326 @@ __global__ __launch_bounds__(256) void kd_router_m(const DecRouterMArgs a) {
 }
 
 // ------------------------------------------------------------------ routing + jobs, m rows
-// One workgroup: wavefront b routes row b (route_row), then the job list (k_router's tail).
-__global__ __launch_bounds__(1024) void kd_route(const DecRouteArgs a) {
-  __shared__ signed char slot_of[MAX_M][256];
-  __shared__ int wcount[16];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ne = a.n_expert, nu = a.n_used, m = a.m;
-  for (int i = threadIdx.x; i < MAX_M * 256; i += blockDim.x) (&slot_of[0][0])[i] = -1;
-  __syncthreads();
-  if (wave < m) {
-    const int b = wave;
-    float lv[4];
+// Every workgroup of kd_gateup_m (NW wavefronts, NW * 64 >= n_expert threads): wavefront w
+// routes rows w and w + NW (route_row; route_load brings their logits), then thread e builds
+// expert e's job if it has users:
+// jobs in expert order, users in row order (a row chooses an expert at most once), into the
+// LDS table sj (JR ints a job: expert, nvec, vec[MAX_M], out[MAX_M]), the job list of
+// k_router's tail. publish: the routing results, the job list and the selection counts also go
+// to global memory. Returns the job count.
+template <int NW>
+__device__ __forceinline__ void route_load(const DecRouteArgs &a, float (&lv)[2][4]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const int b = wave + NW * r;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int e = lane + 64 * k;
-      lv[k] = e < ne ? gld<float>(a.logits + (int64_t)b * ne + e) : -INFINITY;
+      lv[r][k] = b < a.m && e < a.n_expert ? gld<float>(a.logits + (int64_t)b * a.n_expert + e) : -INFINITY;
     }
-    int my_e, keep;
-    float my_p, wsum;
-    route_row(lv, ne, nu, a.moe_prune, my_e, my_p, keep, wsum);
-    if (lane < keep) {
-      gst<int>(a.chosen + b * 32 + lane, my_e);
-      gst<float>(a.weights + b * 32 + lane, a.norm ? my_p / wsum : my_p);
-      slot_of[b][my_e] = (signed char)lane;
+  }
+}
+
+template <int NW>
+__device__ int route_jobs(const DecRouteArgs &a, const float (&lv)[2][4], SPX_L int *sj, SPX_L signed char *slot_of, SPX_L int *wcount,
+                          bool publish) {
+  constexpr int JR = 2 + 2 * MAX_M;
+  static_assert(2 * NW >= MAX_M, "two rows a wavefront");
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ne = a.n_expert, nu = a.n_used, m = a.m;
+  for (int i = threadIdx.x; i < MAX_M * 256; i += NW * 64) slot_of[i] = -1;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const int b = wave + NW * r;
+    if (b < m) {
+      int my_e, keep;
+      float my_p, wsum;
+      route_row(lv[r], ne, nu, a.moe_prune, my_e, my_p, keep, wsum);
+      if (lane < keep) {
+        slot_of[b * 256 + my_e] = (signed char)lane;
+        if (publish) {
+          gst<int>(a.chosen + b * 32 + lane, my_e);
+          gst<float>(a.weights + b * 32 + lane, a.norm ? my_p / wsum : my_p);
+        }
+      }
+      if (publish && lane == 0) gst<int>(a.nkeep + b, keep);
     }
-    if (lane == 0) gst<int>(a.nkeep + b, keep);
   }
   __syncthreads();
-  // jobs: experts with at least one user, in expert order (thread e = expert e); users in row
-  // order (a row chooses an expert at most once)
   const int e = threadIdx.x;
   int cnt = 0;
   if (e < ne)
-    for (int b = 0; b < m; b++) cnt += slot_of[b][e] >= 0;
+    for (int b = 0; b < m; b++) cnt += slot_of[b * 256 + e] >= 0;
   const unsigned long long bal = __ballot(cnt > 0);
   if (lane == 0) wcount[wave] = __popcll(bal);
   __syncthreads();
+  int nj = 0, base = 0;
+  for (int w = 0; w < NW; w++) {
+    base += w < wave ? wcount[w] : 0;
+    nj += wcount[w];
+  }
   if (cnt > 0) {
-    int base = 0;
-    for (int w = 0; w < wave; w++) base += wcount[w];
     const int j = base + __popcll(bal & ((1ull << lane) - 1ull));
-    Job J;
-    J.expert = e;
+    SPX_L int *J = sj + j * JR;
     int k = 0;
     for (int b = 0; b < m; b++) {
-      const int sl = slot_of[b][e];
-      if (sl >= 0) { J.vec[k] = b; J.out[k] = b * nu + sl; k++; }
+      const int sl = slot_of[b * 256 + e];
+      if (sl >= 0) { J[2 + k] = b; J[2 + MAX_M + k] = b * nu + sl; k++; }
     }
-    J.nvec = k;
-    for (int q = k; q < MAX_M; q++) { J.vec[q] = 0; J.out[q] = 0; }
-    a.jobs[j] = J;
-    if (a.expert_count) a.expert_count[e] += 1;
+    for (int q = k; q < MAX_M; q++) { J[2 + q] = 0; J[2 + MAX_M + q] = 0; }
+    J[0] = e;
+    J[1] = k;
+    if (publish) {
+      int *G = reinterpret_cast<int *>(a.jobs + j);
+      for (int f = 0; f < JR; f++) gst<int>(G + f, J[f]);
+      if (a.expert_count) atomicAdd(a.expert_count + e, 1);
+    }
   }
-  if (threadIdx.x == 0) {
-    int n = 0;
-    for (int w = 0; w < 16; w++) n += wcount[w];
-    gst<int>(a.njobs, n);
-  }
+  if (publish && threadIdx.x == 0) gst<int>(a.njobs, nj);
+  __syncthreads();
+  return nj;
 }
 
 // ------------------------------------------------------------------ gate / up, m rows
-// Grid (n_ff / DEC_MM_NW, jobs): workgroup (x, j) computes rows DEC_MM_NW * x .. of h for the
-// users of job j (dense: all rows), one row per wavefront: lanes 0-31 the gate row, 32-63 the
-// up row, four groups each; rounds of four blocks as kd_mm. h[out][r] = silu(g) * u.
+// Items (job j, tile x) with TX = ceil(n_ff / DEC_MM_NW) tiles per job; workgroup b of the
+// grid (at most two per CU) takes items [b n / G, (b + 1) n / G), consecutive tiles of one or
+// two jobs, so a job's users are staged once and no workgroup is launched past the job count.
+// Tile x: rows DEC_MM_NW * x .. of h, one row per wavefront: lanes 0-31 the gate row, 32-63 the
+// up row, four groups each; rounds of four blocks as kd_mm. h[out][r] = silu(g) * u. The m
+// rows' Q8_K image is staged once (its loads overlap the routing); the next item's weights are
+// requested before the current item's dots.
 template <int T, int BPG>
-__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void kd_gateup_m(const DecGateUpMArgs a) {
-  constexpr int NW = DEC_MM_NW;
-  extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ int s_vec[MAX_M], s_out[MAX_M], s_hdr[2];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 3, l = lane & 7;
-  const int half = grp >> 2, gi = grp & 3;
-  const int n_ff = a.n_ff, cols = (int)a.gate.cols, nbq = cols >> 8, nb = nbq;
-  const int r = blockIdx.x * NW + wave;
-  const bool valid = r < n_ff;
-  if (threadIdx.x == 0) {
-    if (a.jobs) {
-      const int nj = gld<int>(a.njobs);
-      s_hdr[0] = (int)blockIdx.y < nj ? a.jobs[blockIdx.y].expert : -1;
-      s_hdr[1] = (int)blockIdx.y < nj ? a.jobs[blockIdx.y].nvec : 0;
-    } else {
-      s_hdr[0] = 0;
-      s_hdr[1] = a.m;
-    }
-  }
-  if (threadIdx.x < MAX_M) {
-    s_vec[threadIdx.x] = a.jobs ? a.jobs[blockIdx.y].vec[threadIdx.x] : threadIdx.x;
-    s_out[threadIdx.x] = a.jobs ? a.jobs[blockIdx.y].out[threadIdx.x] : threadIdx.x;
-  }
-  __syncthreads();
-  const int expert = s_hdr[0], nv = s_hdr[1];
-  if (expert < 0) return;  // past the job count (the whole workgroup)
-  const size_t act = mm_act_bytes(nv, cols);
-  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
-  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)nv * cols + 15) & ~(size_t)15));
-  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)nv * cols + 15) & ~(size_t)15) + (((size_t)nv * nbq * 4 + 15) & ~(size_t)15));
-  SPX_L float *cbr = (SPX_L float *)(smem + act) + (size_t)(wave * 2 + half) * 4 * nv * 10;
-  const int64_t grow = (int64_t)expert * a.gate.rows + (valid ? r : n_ff - 1);
-  DRaw raw[BPG];
+__device__ __forceinline__ void gum_load(DRaw (&raw)[BPG], const DecGateUpMArgs &a, const SPX_L int *sj, int j, int x, int half, int gi,
+                                         int l, int nb) {
+  constexpr int JR = 2 + 2 * MAX_M;
+  const int r = x * DEC_MM_NW + (int)(threadIdx.x >> 6);
+  const int e = min(max(sj[j * JR], 0), a.gate.n_expert - 1);
+  const int64_t grow = (int64_t)e * a.gate.rows + (r < a.n_ff ? r : a.n_ff - 1);
   rp_load<T, BPG>(raw, half ? a.up.pl : a.gate.pl, grow, nb, 4, gi, l);
-  stage_q8<DEC_MM_NW * 64>(a.y, s_vec, nv, cols, lq, ld, lbs);
-  __syncthreads();
-  float acc[MAX_M / 4], cr[MAX_M / 4];
+}
+
+// The m rows' Q8_K image (global y -> LDS, row b at slot b) in two steps: the loads go out
+// (get), other work runs, then the LDS stores (put). NT threads; at most MAX_M rows of
+// DEC_MAXNB blocks.
+template <int NT>
+struct StageQ8 {
+  static constexpr int NQ = (MAX_M * DEC_MAXNB * 16 + NT - 1) / NT, NS = (MAX_M * DEC_MAXNB * 4 + NT - 1) / NT,
+                       ND = (MAX_M * DEC_MAXNB + NT - 1) / NT;
+  uint4 q[NQ], bs[NS];
+  float d[ND];
+  __device__ __forceinline__ void get(const Q8KP &y, int m, int cols) {
+    const int nbq = cols >> 8, nq = m * (cols / 16), nb4 = m * nbq * 4, nd = m * nbq, t = threadIdx.x;
 #pragma unroll
-  for (int q = 0; q < MAX_M / 4; q++) { acc[q] = 0.0f; cr[q] = 0.0f; }
+    for (int k = 0; k < NQ; k++)
+      if (t + k * NT < nq) q[k] = gld<uint4>(reinterpret_cast<const uint8_t *>(y.q) + 16 * (int64_t)(t + k * NT));
 #pragma unroll
-  for (int j = 0; j < BPG; j++) {
-    mm_round_dots<T, BPG>(raw, j, nb, 4, gi, l, nv, nbq, lq, ld, lbs, cbr);
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    mm_round_chain<MAX_M / 4>(j, nb, 4, gi, l, nv, cbr, acc, cr);
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
+    for (int k = 0; k < NS; k++)
+      if (t + k * NT < nb4) bs[k] = gld<uint4>(reinterpret_cast<const uint8_t *>(y.bs) + 16 * (int64_t)(t + k * NT));
+#pragma unroll
+    for (int k = 0; k < ND; k++)
+      if (t + k * NT < nd) d[k] = gld<float>(y.d + t + k * NT);
   }
+  __device__ __forceinline__ void put(int m, int cols, SPX_L uint32_t *lq, SPX_L float *ld, SPX_L int2 *lbs) const {
+    const int nbq = cols >> 8, nq = m * (cols / 16), nb4 = m * nbq * 4, nd = m * nbq, t = threadIdx.x;
 #pragma unroll
-  for (int q = 0; q < MAX_M / 4; q++) {
-    const int v = gi + 4 * q;
-    if (v < nv) {  // wave-uniform per group pair: gate lanes and up lanes own the same v
-      const float res = hsum_rows8(acc[q]) - cr[q];
-      uint32_t r_lo, r_hi;
-      xchg32(__float_as_uint(res), r_lo, r_hi);
-      const float u = __uint_as_float(r_hi);
-      if (half == 0 && l == 0 && valid) {
-        const float x = res;
-        gst<float>(a.h + (int64_t)s_out[v] * n_ff + r, x / (1.0f + expf(-x)) * u);
-      }
-    }
+    for (int k = 0; k < NQ; k++)
+      if (t + k * NT < nq) lst<uint4>((SPX_L uint4 *)lq + t + k * NT, q[k]);
+#pragma unroll
+    for (int k = 0; k < NS; k++)
+      if (t + k * NT < nb4) lst<uint4>((SPX_L uint4 *)lbs + t + k * NT, bs[k]);
+#pragma unroll
+    for (int k = 0; k < ND; k++)
+      if (t + k * NT < nd) ld[t + k * NT] = d[k];
+  }
+};
+
+// Round k of a row's blocks for the users of a job (user v = row rows[v] of the image): group
+// gi's block against every user into cb [G][nv][10], as mm_round_dots.
+template <int T, int BPG>
+__device__ __forceinline__ void gum_round_dots(const DRaw (&raw)[BPG], int k, int nb, int gi, int l, int nv, int nbq,
+                                               const SPX_L int *rows, const SPX_L uint32_t *lq, const SPX_L float *ld, const SPX_L int2 *lbs,
+                                               SPX_L float *cbr) {
+  const int i = gi + 4 * k;
+  if (i >= nb) return;
+  KQDec<T> dec;
+  dec.decode(draw_kq<T>(raw[k]), l);
+#pragma unroll 2
+  for (int v = 0; v < nv; v++) {
+    const int vb = rows[v] * nbq + i;
+    const uint4 y0 = lld<uint4>(lq + vb * 64 + 8 * l), y1 = lld<uint4>(lq + vb * 64 + 8 * l + 4);
+    int P, s;
+    dec.dot(y0, y1, lld<int2>(lbs + vb * 8 + l), P, s);
+    s = sum8(s);
+    const float xd = ld[vb];
+    SPX_L float *e = cbr + (gi * nv + v) * 10;  // the layout mm_round_chain reads (m = nv)
+    e[l] = (float)P;
+    if (l == 0) { e[8] = dec.d * xd; e[9] = dec.corr_term(xd, s); }
   }
 }
 
-// ------------------------------------------------------------------ down + combine, m rows
-// Eight wavefronts, one output row each; row group s takes job j0 + s (rounds of eight), its
-// expert's row decoded once and dotted with each user's Q8_K h (read through the caches);
-// then row b's output = sum over its kept choices, in choice order, of w * y.
-template <int T, int NB>
-__global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_m(const DecDownMArgs a) {
-  constexpr int NW = DEC_MM_NW;
+template <int T, int BPG>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(BPG > 2 ? 2 : 4))) void kd_gateup_m(const DecGateUpMArgs a) {
+  constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M;  // a Job record in ints: expert, nvec, vec[], out[]
   extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ float yb[NW][MAX_M * 32];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
-  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, nbh = n_ff >> 8, nvh = a.m * a.n_used;
-  const int64_t r = (int64_t)blockIdx.x * NW + wave;
-  const int64_t rr = r < dim ? r : dim - 1;
+  __shared__ signed char slot_of[MAX_M * 256];
+  __shared__ int wcount[NW];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 3, l = lane & 7;
+  const int half = grp >> 2, gi = grp & 3;
+  const int n_ff = a.n_ff, cols = (int)a.gate.cols, nbq = cols >> 8, nb = nbq, m = a.m;
+  const int TX = (n_ff + NW - 1) / NW;
+  const size_t act = mm_act_bytes(m, cols);
   SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
-  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)nvh * n_ff + 15) & ~(size_t)15));
-  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)nvh * n_ff + 15) & ~(size_t)15) + (((size_t)nvh * nbh * 4 + 15) & ~(size_t)15));
-  const int nj = gld<int>(a.njobs);
-  // first round's expert rows in flight while the users' h rows are staged
-  int j = min(slot, nj - 1);
-  DRaw raw[NB];
-  draw_row<T, NB>(raw, a.w.pl, (int64_t)a.jobs[j].expert * dim + rr, nbh, l);
-  {  // loads of four rounds go out before their stores
-    const int nq = nvh * n_ff / 16, nb4 = nvh * nbh * 4;
-    for (int i0 = threadIdx.x; i0 < nq; i0 += 4 * blockDim.x) {
-      uint4 t[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int i = i0 + k * blockDim.x;
-        if (i < nq) t[k] = gld<uint4>(reinterpret_cast<const uint8_t *>(a.hq.q) + 16 * (int64_t)i);
-      }
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int i = i0 + k * blockDim.x;
-        if (i < nq) lst<uint4>((SPX_L uint4 *)lq + i, t[k]);
-      }
+  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)m * cols + 15) & ~(size_t)15));
+  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)m * cols + 15) & ~(size_t)15) + (((size_t)m * nbq * 4 + 15) & ~(size_t)15));
+  SPX_L float *cbr = (SPX_L float *)(smem + act) + (size_t)(wave * 2 + half) * 4 * m * 10;
+  SPX_L int *sj = (SPX_L int *)(smem + act + (size_t)NW * 2 * 4 * m * 10 * 4);  // [max jobs][JR]
+  int nj = 1;
+  {
+    StageQ8<NW * 64> st;
+    if (a.rt.logits) {
+      float lv[2][4];
+      route_load<NW>(a.rt, lv);
+      st.get(a.y, m, cols);  // the image's loads overlap the routing
+      nj = route_jobs<NW>(a.rt, lv, sj, (SPX_L signed char *)slot_of, (SPX_L int *)wcount, blockIdx.x == 0);
+    } else {  // dense: one job, expert 0, users = rows 0..m-1
+      st.get(a.y, m, cols);
+      for (int i = threadIdx.x; i < JR; i += blockDim.x) sj[i] = i == 0 ? 0 : i == 1 ? m : i < 2 + MAX_M ? i - 2 : i - 2 - MAX_M;
+      __syncthreads();  // the job record (gum_load reads it)
     }
-    for (int i0 = threadIdx.x; i0 < nb4; i0 += 4 * blockDim.x) {
-      uint4 t[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int i = i0 + k * blockDim.x;
-        if (i < nb4) t[k] = gld<uint4>(reinterpret_cast<const uint8_t *>(a.hq.bs) + 16 * (int64_t)i);
-      }
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int i = i0 + k * blockDim.x;
-        if (i < nb4) lst<uint4>((SPX_L uint4 *)lbs + i, t[k]);
-      }
-    }
-    for (int i = threadIdx.x; i < nvh * nbh; i += blockDim.x) ld[i] = gld<float>(a.hq.d + i);
+    st.put(m, cols, lq, ld, lbs);
   }
-  __syncthreads();
-  for (int j0 = 0; j0 < nj; j0 += 8) {
-    j = min(j0 + slot, nj - 1);
-    const int nvec = j0 + slot < nj ? a.jobs[j].nvec : 0;
-    if (j0 > 0) draw_row<T, NB>(raw, a.w.pl, (int64_t)a.jobs[j].expert * dim + rr, nbh, l);
-    KQDec<T> dec[NB];
+  const int n = TX * nj, G = gridDim.x;
+  const int i0 = (int)((int64_t)blockIdx.x * n / G), i1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
+  if (i0 >= i1) return;  // the whole workgroup
+  int i = i0, j = i0 / TX, x = i0 - (i0 / TX) * TX;
+  DRaw raw[BPG];
+  gum_load<T, BPG>(raw, a, sj, j, x, half, gi, l, nb);
+  __syncthreads();  // the image and the job table
+  for (;;) {
+    const int nv = sj[j * JR + 1];
+    int jn = j, xn = x + 1;
+    if (xn == TX) { jn++; xn = 0; }
+    DRaw nraw[BPG];
+    if (i + 1 < i1) gum_load<T, BPG>(nraw, a, sj, jn, xn, half, gi, l, nb);
+    float acc[MAX_M / 4], cr[MAX_M / 4];
 #pragma unroll
-    for (int i = 0; i < NB; i++)
-      if (i < nbh) dec[i].decode(draw_kq<T>(raw[i]), l);
-    for (int k = 0; k < nvec; k++) {
-      const int u = a.jobs[j].out[k];
-      float acc = 0.0f, corr = 0.0f;
+    for (int q = 0; q < MAX_M / 4; q++) { acc[q] = 0.0f; cr[q] = 0.0f; }
 #pragma unroll
-      for (int i = 0; i < NB; i++) {
-        if (i < nbh) {
-          const int vb = u * nbh + i;
-          const uint4 y0 = lld<uint4>(lq + vb * 64 + 8 * l), y1 = lld<uint4>(lq + vb * 64 + 8 * l + 4);
-          int P, s;
-          dec[i].dot(y0, y1, lld<int2>(lbs + vb * 8 + l), P, s);
-          s = sum8(s);
-          const float xd = ld[vb];
-          corr = corr + dec[i].corr_term(xd, s);
-          acc = fmaf(dec[i].d * xd, (float)P, acc);
+    for (int k = 0; k < BPG; k++) {
+      gum_round_dots<T, BPG>(raw, k, nb, gi, l, nv, nbq, sj + j * JR + 2, lq, ld, lbs, cbr);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+      mm_round_chain<MAX_M / 4>(k, nb, 4, gi, l, nv, cbr, acc, cr);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+    }
+    const int r = x * NW + wave;
+#pragma unroll
+    for (int q = 0; q < MAX_M / 4; q++) {
+      const int v = gi + 4 * q;
+      if (v < nv) {  // wave-uniform per group pair: gate lanes and up lanes own the same v
+        const float res = hsum_rows8(acc[q]) - cr[q];
+        uint32_t r_lo, r_hi;
+        xchg32(__float_as_uint(res), r_lo, r_hi);
+        const float u = __uint_as_float(r_hi);
+        if (half == 0 && l == 0 && r < n_ff) {
+          const float xg = res;
+          gst<float>(a.h + (int64_t)sj[j * JR + 2 + MAX_M + v] * n_ff + r, xg / (1.0f + expf(-xg)) * u);
         }
       }
-      const float y = hsum_rows8(acc) - corr;
-      if (l == 0) yb[wave][u] = y;
     }
+    if (++i >= i1) break;
+#pragma unroll
+    for (int k = 0; k < BPG; k++) raw[k] = nraw[k];
+    j = jn;
+    x = xn;
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  if (lane < a.m && r < dim) {
-    const int b = lane, nk = gld<int>(a.nkeep + b);
-    float acc = 0.0f;
-    for (int i = 0; i < nk; i++) acc = acc + gld<float>(a.weights + b * 32 + i) * yb[wave][b * a.n_used + i];
-    const int64_t o = (int64_t)b * dim + r;
-    gst<float>(a.res_out + o, gld<float>(a.res_in + o) + a.rscale * acc);
+}
+
+// ------------------------------------------------------------------ down, m rows
+// Items (job j, tile x of 64 rows of the expert's down matrix): a workgroup of eight
+// wavefronts; row group g of wavefront w takes row 64x + 8w + g, all its blocks in order (the
+// reference's chain in registers, as kq_walk_tile), against each of the job's users' h, which
+// the workgroup quantizes into LDS from the fp32 h rows (quantize_avx2 per 256 block).
+// y[out][r] for every (user, row); the weighted combine and the residual add are kd_norm's.
+template <int T, int NB>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void kd_down_m(const DecDownMArgs a) {
+  constexpr int NW = DEC_MM_NW, RW = NW * 8, JF = 2 + MAX_M;  // rows per item; job fields: expert, nvec, out[]
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int s_job[JF];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, l = lane & 7;
+  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, nbh = n_ff >> 8, TX = (dim + RW - 1) / RW;
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
+  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)MAX_M * n_ff + 15) & ~(size_t)15));
+  SPX_L int *lbs = (SPX_L int *)(smem + (((size_t)MAX_M * n_ff + 15) & ~(size_t)15) + (((size_t)MAX_M * nbh * 4 + 15) & ~(size_t)15));
+  const int n = TX * gld<int>(a.njobs);
+  for (int it = blockIdx.x; it < n; it += gridDim.x) {
+    const int j = it / TX, x = it - j * TX;
+    if ((int)threadIdx.x < JF) {
+      const int f = threadIdx.x;
+      s_job[f] = gld<int>(reinterpret_cast<const int *>(a.jobs + j) + (f < 2 ? f : 2 + MAX_M + (f - 2)));
+    }
+    __syncthreads();
+    const int e = min(max(s_job[0], 0), a.w.n_expert - 1), nv = min(max(s_job[1], 0), MAX_M);
+    const int64_t r = (int64_t)x * RW + wave * 8 + g;
+    const int64_t rr = r < dim ? r : dim - 1;
+    DRaw raw[NB];
+    draw_row<T, NB>(raw, a.w.pl, (int64_t)e * dim + rr, nbh, l);
+    // users' h blocks q = k * nbh + i (user k, block i); wavefront w takes q = w, w + NW, ...
+    const int nq = nv * nbh;
+    for (int q0 = wave; q0 < nq; q0 += 4 * NW) {
+      float4 hv[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int q = q0 + NW * t;
+        if (q < nq) {
+          const int k = q / nbh, i = q - k * nbh;
+          hv[t] = gld<float4>(a.h + (int64_t)s_job[2 + k] * n_ff + i * 256 + 4 * lane);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int q = q0 + NW * t;
+        if (q < nq) {
+          const float am = wave_max(amax4(hv[t]));
+          q8k_block_store(hv[t], am, lq + q * 64, ld + q, lbs + q * 16);
+        }
+      }
+    }
+    __syncthreads();
+    // blocks in order, each decoded once; every user's chain advances block by block
+    float acc[MAX_M], corr[MAX_M];
+#pragma unroll
+    for (int k = 0; k < MAX_M; k++) { acc[k] = 0.0f; corr[k] = 0.0f; }
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+      if (i < nbh) {
+        KQDec<T> dec;
+        dec.decode(draw_kq<T>(raw[i]), l);
+#pragma unroll
+        for (int k = 0; k < MAX_M; k++) {
+          if (k < nv) {
+            const int vb = k * nbh + i;
+            const uint4 y0 = lld<uint4>(lq + vb * 64 + 8 * l), y1 = lld<uint4>(lq + vb * 64 + 8 * l + 4);
+            int P, sm;
+            dec.dot(y0, y1, lld<int2>(lbs + vb * 16 + 2 * l), P, sm);
+            sm = sum8(sm);
+            const float xd = ld[vb];
+            corr[k] = corr[k] + dec.corr_term(xd, sm);
+            acc[k] = fmaf(dec.d * xd, (float)P, acc[k]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < MAX_M; k++) {
+      if (k < nv) {
+        const float y = hsum_rows8(acc[k]) - corr[k];
+        if (l == 0 && r < dim) gst<float>(a.yd + (int64_t)s_job[2 + k] * dim + r, y);
+      }
+    }
+    __syncthreads();  // s_job and the LDS image are refilled by the next item
   }
 }
 
@@ -1285,50 +1433,58 @@ hipError_t launch_dec_router_m(const DecRouterMArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_dec_route(const DecRouteArgs &a, hipStream_t s) {
-  if (a.n_expert < 1 || a.n_expert > 256 || a.n_used < 1 || a.n_used > 32 || a.n_used > a.n_expert || a.m < 1 || a.m > MAX_M) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kd_route, dim3(1), dim3(1024), 0, s, a);
-  return hipGetLastError();
+static int cu_count() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+  }
+  return n;
 }
 
 template <int T>
-static hipError_t dec_gum_t(const DecGateUpMArgs &a, int max_jobs, hipStream_t s) {
-  const int cols = (int)a.gate.cols, bpg = ((cols >> 8) + 3) / 4, nv = a.m;
-  const size_t sm = mm_act_bytes(nv, cols) + (size_t)DEC_MM_NW * 2 * 4 * nv * 10 * 4;
+static hipError_t dec_gum_t(const DecGateUpMArgs &a, hipStream_t s) {
+  const int cols = (int)a.gate.cols, bpg = ((cols >> 8) + 3) / 4;
+  const size_t sm = gum_lds_bytes(a.m, cols, a.rt.logits ? a.max_jobs : 1);
   if (sm > 160 * 1024) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((a.n_ff + DEC_MM_NW - 1) / DEC_MM_NW), (unsigned)max_jobs), b(DEC_MM_NW * 64);
+  const int tx = (a.n_ff + DEC_MM_NW - 1) / DEC_MM_NW, items = tx * (a.rt.logits ? a.max_jobs : 1);
+  const dim3 grid((unsigned)std::min(items, 2 * cu_count())), b(DEC_MM_NW * 64);
   if (bpg == 1) { SPX_DLDS((kd_gateup_m<T, 1>), sm); hipLaunchKernelGGL((kd_gateup_m<T, 1>), grid, b, sm, s, a); }
   else if (bpg == 2) { SPX_DLDS((kd_gateup_m<T, 2>), sm); hipLaunchKernelGGL((kd_gateup_m<T, 2>), grid, b, sm, s, a); }
   else { SPX_DLDS((kd_gateup_m<T, 4>), sm); hipLaunchKernelGGL((kd_gateup_m<T, 4>), grid, b, sm, s, a); }
   return hipGetLastError();
 }
 
-hipError_t launch_dec_gateup_m(const DecGateUpMArgs &a, int max_jobs, hipStream_t s) {
+hipError_t launch_dec_gateup_m(const DecGateUpMArgs &args, int max_jobs, hipStream_t s) {
+  DecGateUpMArgs a = args;
+  a.max_jobs = max_jobs;
   const int nb = (int)(a.gate.cols >> 8);
-  if (a.gate.cols % 256 || nb > DEC_MAXNB || a.gate.nb != nb || a.up.nb != nb || a.gate.dtype != a.up.dtype || a.m < 1 || a.m > MAX_M || max_jobs < 1)
+  if (a.gate.cols % 256 || nb > DEC_MAXNB || a.gate.nb != nb || a.up.nb != nb || a.gate.dtype != a.up.dtype || a.m < 1 || a.m > MAX_M || max_jobs < 1 ||
+      max_jobs > 512 || (a.rt.logits && (max_jobs > a.gate.n_expert || a.rt.m != a.m || a.rt.n_expert < 1 || a.rt.n_expert > DEC_MM_NW * 64 ||
+                                         a.rt.n_expert > 256 || a.rt.n_used < 1 || a.rt.n_used > 32 || a.rt.n_used > a.rt.n_expert)))
     return hipErrorInvalidValue;
-  if (a.gate.dtype == T_Q4K) return dec_gum_t<T_Q4K>(a, max_jobs, s);
-  if (a.gate.dtype == T_Q6K) return dec_gum_t<T_Q6K>(a, max_jobs, s);
+  if (a.gate.dtype == T_Q4K) return dec_gum_t<T_Q4K>(a, s);
+  if (a.gate.dtype == T_Q6K) return dec_gum_t<T_Q6K>(a, s);
   return hipErrorInvalidValue;
 }
 
 template <int T>
 static hipError_t dec_downm_t(const DecDownMArgs &a, hipStream_t s) {
-  const dim3 grid((unsigned)((a.w.rows + DEC_MM_NW - 1) / DEC_MM_NW)), b(DEC_MM_NW * 64);
-  const size_t sm = mm_act_bytes(a.m * a.n_used, (int)a.w.cols);
-  if (sm > 128 * 1024) return hipErrorInvalidValue;
+  const int tx = (int)((a.w.rows + DEC_MM_NW * 8 - 1) / (DEC_MM_NW * 8));
+  const dim3 grid((unsigned)std::min(tx * a.max_jobs, 2 * cu_count())), b(DEC_MM_NW * 64);
+  const size_t sm = downm_lds_bytes((int)a.w.cols);
   switch (nb_bucket((int)a.w.nb)) {
-  case 1: SPX_DLDS((kd_down_m<T, 1>), sm); hipLaunchKernelGGL((kd_down_m<T, 1>), grid, b, sm, s, a); break;
-  case 2: SPX_DLDS((kd_down_m<T, 2>), sm); hipLaunchKernelGGL((kd_down_m<T, 2>), grid, b, sm, s, a); break;
-  case 3: SPX_DLDS((kd_down_m<T, 3>), sm); hipLaunchKernelGGL((kd_down_m<T, 3>), grid, b, sm, s, a); break;
-  case 4: SPX_DLDS((kd_down_m<T, 4>), sm); hipLaunchKernelGGL((kd_down_m<T, 4>), grid, b, sm, s, a); break;
+  case 1: hipLaunchKernelGGL((kd_down_m<T, 1>), grid, b, sm, s, a); break;
+  case 2: hipLaunchKernelGGL((kd_down_m<T, 2>), grid, b, sm, s, a); break;
+  case 3: hipLaunchKernelGGL((kd_down_m<T, 3>), grid, b, sm, s, a); break;
+  case 4: hipLaunchKernelGGL((kd_down_m<T, 4>), grid, b, sm, s, a); break;
   default: return hipErrorInvalidValue;  // n_ff > 1024: the expert rows take the fused kernels
   }
   return hipGetLastError();
 }
 
 hipError_t launch_dec_down_m(const DecDownMArgs &a, hipStream_t s) {
-  if (a.w.cols % 256 || a.w.nb > 4 || a.n_used < 1 || a.n_used > 32 || a.m < 1 || a.m > MAX_M || (int64_t)a.m * a.n_used > MAX_M * 32) return hipErrorInvalidValue;
+  if (a.w.cols % 256 || a.w.nb > 4 || a.max_jobs < 1 || a.max_jobs > 512 || a.max_jobs > a.w.n_expert || !a.h || !a.yd) return hipErrorInvalidValue;
   if (a.w.dtype == T_Q4K) return dec_downm_t<T_Q4K>(a, s);
   if (a.w.dtype == T_Q6K) return dec_downm_t<T_Q6K>(a, s);
   return hipErrorInvalidValue;

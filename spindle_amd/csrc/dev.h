@@ -56,6 +56,17 @@ __device__ __forceinline__ unsigned long long max_u64_x(unsigned long long v, bo
   const unsigned long long a = ((unsigned long long)ha << 32) | la, b = ((unsigned long long)hb << 32) | lb;
   return a > b ? a : b;
 }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, true));
+  uint32_t a, b;
+  xchg16(v, a, b);
+  v = max(a, b);
+  xchg32(v, a, b);
+  return max(a, b);
+}
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
   unsigned long long w;
   w = SPX_DPP64(v, 0xB1); v = w > v ? w : v;

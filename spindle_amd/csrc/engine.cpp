@@ -82,6 +82,7 @@ struct spx_engine {
   int *chosen = nullptr, *nkeep = nullptr, *expert_count = nullptr;
   float *weights = nullptr;
   Job *jobs = nullptr;
+  float *yd = nullptr;  // [16 * n_used][dim]: expert outputs of a multi-row pass, combined by the next norm
   hipGraphExec_t graph[MAX_M + 1] = {};
   int n_used = 0;
   // kernel-class timing (eager passes only): event pairs recorded around each launch
@@ -485,8 +486,15 @@ int enqueue_pass_m(spx_engine *E, int m) {
     return (int)((t->v.rows + DEC_MM_NW * R - 1) / (DEC_MM_NW * R));
   };
   auto gshape = [](const spx_tensor *t) { int G, R; rp_shape(t->v.nb, G, R); return G; };
+  bool combine = false;  // the last MoE layer's expert outputs wait in yd for the next norm
   auto norm = [&](const float *x, const float *nw, float *xn_out, Q8KP q) {
-    DecNormArgs na{x, nw, c.rms_eps, dim, xn_out, q};
+    DecNormArgs na{};
+    na.x = x; na.nw = nw; na.eps = c.rms_eps; na.dim = dim; na.xn_out = xn_out; na.q_out = q;
+    if (combine) {  // x = xB + combine, written back to xA (= x)
+      na.yd = E->yd; na.cw = E->weights; na.nkeep = E->nkeep; na.res_in = E->xB; na.x_out = E->xA;
+      na.n_used = nu; na.rscale = c.residual_scale;
+      combine = false;
+    }
     return launch_dec_norm(na, m, s);
   };
   {
@@ -547,20 +555,18 @@ int enqueue_pass_m(spx_engine *E, int m) {
         ProfScope ps(E, PC_ROUTER, wbytes(ly.router));
         DecRouterMArgs ra{ly.router->v, E->xn2, E->rlog, c.n_expert, dim, m};
         SPX_HIP(launch_dec_router_m(ra, s));
-        DecRouteArgs rt{E->rlog, c.n_expert, c.n_expert_used, c.expert_norm, m, c.moe_prune, E->chosen, E->weights, E->nkeep,
-                        E->jobs, ly.njobs, E->expert_count + (size_t)l * c.n_expert};
-        SPX_HIP(launch_dec_route(rt, s));
       }
-      {
+      {  // routing + jobs (every workgroup) and the grouped gate/up
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up), l, true);
-        ga.jobs = E->jobs; ga.njobs = ly.njobs;
+        ga.rt = DecRouteArgs{E->rlog, c.n_expert, c.n_expert_used, c.expert_norm, m, c.moe_prune, E->chosen, E->weights, E->nkeep,
+                             E->jobs, ly.njobs, E->expert_count + (size_t)l * c.n_expert};
         SPX_HIP(launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
-        SPX_HIP(launch_q8kp_quantize(E->h, nff, nff, m * nu, E->hq, s));
       }
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
-        DecDownMArgs da{ly.down->v, E->hq, E->jobs, ly.njobs, E->weights, E->nkeep, nu, m, E->xB, E->xA, c.residual_scale};
+        DecDownMArgs da{ly.down->v, E->h, E->jobs, ly.njobs, E->yd, std::min(m * nu, c.n_expert)};
         SPX_HIP(launch_dec_down_m(da, s));
+        combine = true;  // + weighted combine + residual in the next norm (xB -> xA)
       }
     } else {  // ffn_forward_multi (:616-646)
       {
@@ -768,7 +774,7 @@ int spx_engine_prepare(spx_engine *E) {
             (E->v = E->dalloc<float>((size_t)M * E->kv_dim)) && (E->att = E->dalloc<float>((size_t)M * E->q_dim)) &&
             (E->proj = E->dalloc<float>((size_t)M * c.dim)) && (E->ffn = E->dalloc<float>((size_t)M * c.dim)) &&
             (E->xn2 = E->dalloc<float>((size_t)M * qmax)) && (E->xn = E->dalloc<float>((size_t)M * c.dim)) &&
-            (E->h = E->dalloc<float>((size_t)nv * nff)) && (E->rlog = E->dalloc<float>((size_t)M * std::max(1, c.n_expert))) &&
+            (E->h = E->dalloc<float>((size_t)nv * nff)) && (E->yd = E->dalloc<float>((size_t)nv * c.dim)) && (E->rlog = E->dalloc<float>((size_t)M * std::max(1, c.n_expert))) &&
             (E->logits = E->dalloc<float>((size_t)M * c.vocab)) && (E->amax = E->dalloc<int>(M)) &&
             (E->best = E->dalloc<unsigned long long>((size_t)M * std::max<int64_t>(E->lm_grid, c.vocab / 4 + 1))) &&
             (E->tail_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) && (E->hist = E->dalloc<int>((size_t)c.max_seq)) &&
@@ -807,8 +813,10 @@ int spx_engine_prepare(spx_engine *E) {
   E->dec_ok = dok;
   // passes of 2..16 rows: expert down rows of at most 4 blocks (n_ff <= 1024)
   // the down kernel stages every user's Q8_K h row in LDS: 16 rows x n_used users
-  for (auto &ly : E->L)
-    if (ly.moe && (ly.down->v.nb > 4 || (double)MAX_M * nu * ly.down->v.cols * (1.0 + 68.0 / 256.0) + 64 > 128.0 * 1024)) E->dec_ok = false;
+  for (auto &ly : E->L) {
+    if (ly.moe && (ly.down->v.nb > 4 || downm_lds_bytes((int)ly.down->v.cols) > 64 * 1024)) E->dec_ok = false;
+    if (gum_lds_bytes(MAX_M, (int)ly.gate->v.cols, ly.moe ? std::min(MAX_M * nu, c.n_expert) : 1) > 160 * 1024) E->dec_ok = false;
+  }
   if (const char *v = std::getenv("SPX_DECODE")) E->dec_on = atoi(v) != 0;
   E->prepared = true;
   return 0;

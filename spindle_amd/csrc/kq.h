@@ -74,6 +74,10 @@ template <> struct KQRaw<T_Q6K> {
 };
 
 // A block decoded for lane l (shared by all activation vectors).
+// Scale products use 24-bit multiplies (v_mul_i32_i24, full rate; a 32-bit multiply is
+// quarter rate): every operand fits 24 bits signed. Q4_K: scales and mins 0..63, a 4-code dot
+// |.| <= 4 * 15 * 128, a bsum pair |.| <= 32 * 128; Q6_K: scales int8, a 4-code dot
+// |.| <= 4 * 63 * 128, a bsum |.| <= 16 * 128. The products and their sums stay exact int32.
 template <int T> struct KQDec;
 template <> struct KQDec<T_Q4K> {
   uint32_t lo[4], hi[4];
@@ -104,11 +108,11 @@ template <> struct KQDec<T_Q4K> {
     int p = 0;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      p += sc[2 * c] * sdot4((int)lo[c], (int)Y[2 * c], 0);
-      p += sc[2 * c + 1] * sdot4((int)hi[c], (int)Y[2 * c + 1], 0);
+      p += __mul24(sc[2 * c], sdot4((int)lo[c], (int)Y[2 * c], 0));
+      p += __mul24(sc[2 * c + 1], sdot4((int)hi[c], (int)Y[2 * c + 1], 0));
     }
     P = p;
-    s = mn * (bs.x + bs.y);
+    s = __mul24(mn, bs.x + bs.y);
   }
   // corr += (dmin*xd) * float(s); the caller applies acc = fma(d*xd, float(P), acc)
   __device__ __forceinline__ float corr_term(float xd, int s) const { return (dm * xd) * (float)s; }
@@ -144,9 +148,9 @@ template <> struct KQDec<T_Q6K> {
     const uint32_t Y[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
     int p = 0;
 #pragma unroll
-    for (int k = 0; k < 8; k++) p += sc[k] * sdot4((int)q[k], (int)Y[k], 0);
+    for (int k = 0; k < 8; k++) p += __mul24(sc[k], sdot4((int)q[k], (int)Y[k], 0));
     P = p;
-    s = sa * bs.x + sb * bs.y;
+    s = __mul24(sa, bs.x) + __mul24(sb, bs.y);
   }
   __device__ __forceinline__ float corr_term(float xd, int s) const { return (dm * xd) * (float)(32 * s); }
 };

@@ -194,6 +194,9 @@ __host__ __device__ inline size_t gum_lds_bytes(int m, int cols, int max_jobs) {
 
 hipError_t launch_dec_norm(const DecNormArgs &a, int m, hipStream_t s);
 hipError_t launch_dec_mm(const DecMMArgs &a, int grid, hipStream_t s);
+// kd_mm grid for a number of tiles: at most two workgroups a CU, the same number of tiles each
+// (tiles stride over the grid; the next tile's weights are requested before the results)
+int dec_mm_grid(int tiles);
 hipError_t launch_dec_router_m(const DecRouterMArgs &a, hipStream_t s);
 hipError_t launch_dec_gateup_m(const DecGateUpMArgs &a, int max_jobs, hipStream_t s);
 hipError_t launch_dec_down_m(const DecDownMArgs &a, hipStream_t s);

@@ -1442,6 +1442,11 @@ static int cu_count() {
   return n;
 }
 
+int dec_mm_grid(int tiles) {
+  const int slots = 2 * cu_count(), per = (tiles + slots - 1) / slots;
+  return (tiles + per - 1) / per;
+}
+
 template <int T>
 static hipError_t dec_gum_t(const DecGateUpMArgs &a, hipStream_t s) {
   const int cols = (int)a.gate.cols, bpg = ((cols >> 8) + 3) / 4;

@@ -519,7 +519,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
       int total = 0;
       for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.ld_out[i] = ld3[i]; a.tiles[i] = mtiles(w3[i]); total += a.tiles[i]; }
       a.nseg = 3; a.G = gshape(ly.wq); a.y = E->xq2; a.cols = dim; a.m = m;
-      SPX_HIP(launch_dec_mm(a, total, s));
+      SPX_HIP(launch_dec_mm(a, dec_mm_grid(total), s));
     }
     const bool att_q_fused = ((c.n_heads / c.n_kv_heads) * hd) % 256 == 0;
     {
@@ -541,7 +541,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
       a.w[0] = ly.wo->v; a.out[0] = E->proj; a.ld_out[0] = dim; a.tiles[0] = mtiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
       a.y = E->aq; a.cols = E->q_dim; a.m = m;
       a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
-      SPX_HIP(launch_dec_mm(a, a.tiles[0], s));
+      SPX_HIP(launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
     }
     const int nff = (int)ly.gate->v.rows;
     {
@@ -580,7 +580,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
         a.w[0] = ly.down->v; a.out[0] = E->ffn; a.ld_out[0] = dim; a.tiles[0] = mtiles(ly.down); a.nseg = 1; a.G = gshape(ly.down);
         a.y = E->hq; a.cols = nff; a.m = m;
         a.res_in = E->xB; a.res_out = E->xA; a.rscale = c.residual_scale;
-        SPX_HIP(launch_dec_mm(a, a.tiles[0], s));
+        SPX_HIP(launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
       }
     }
   }

@@ -977,7 +977,7 @@ template <int HD> struct AttnLds {
 // parallelism); otherwise enough that a kv head has at most 16 chunks (one merge level).
 __host__ __device__ inline int attn_sub(int nq, int total) {
   const int nsc = (total + 63) >> 6;
-  return nq <= 16 ? 1 : (nsc + 15) / 16;
+  return nq <= 16 ? 1 : (nsc + ATT_GRP - 1) / ATT_GRP;
 }
 
 template <int HD, bool MERGE>
@@ -1819,7 +1819,10 @@ template <int HD>
 static void launch_attn_t(const AttnArgs &a, int nqt, const StepRec *st, hipStream_t s) {
   const size_t sm = AttnLds<HD>::BYTES;
   SPX_LDS((k_attn<HD, true>), sm);
-  hipLaunchKernelGGL((k_attn<HD, true>), dim3(a.nch, a.n_kv, nqt), dim3(256), sm, s, a, st);
+  // more than one query tile: at most ATT_GRP chunks a kv head (attn_sub), so no workgroups
+  // past them are launched
+  const int nc = nqt > 1 ? std::min(a.nch, ATT_GRP) : a.nch;
+  hipLaunchKernelGGL((k_attn<HD, true>), dim3(nc, a.n_kv, nqt), dim3(256), sm, s, a, st);
 }
 
 hipError_t launch_attention_partials(const AttnArgs &a, const StepRec *st, hipStream_t s) {

@@ -74,29 +74,51 @@ template <> struct KQRaw<T_Q6K> {
 };
 
 // A block decoded for lane l (shared by all activation vectors).
-// Scale products use 24-bit multiplies (v_mul_i32_i24, full rate; a 32-bit multiply is
-// quarter rate): every operand fits 24 bits signed. Q4_K: scales and mins 0..63, a 4-code dot
-// |.| <= 4 * 15 * 128, a bsum pair |.| <= 32 * 128; Q6_K: scales int8, a 4-code dot
-// |.| <= 4 * 63 * 128, a bsum |.| <= 16 * 128. The products and their sums stay exact int32.
+// The lane's scaled dot P = sum_k sc_k d_k (d_k the 4-code dot of sub-block k) is taken in
+// Abel form: t_k = d_0 + .. + d_k accumulates in the dot instruction itself (v_dot4c, no
+// zeroing), and P = sum_{k<7} (sc_k - sc_{k+1}) t_k + sc_7 t_7 with the differences computed
+// once per block at decode. Same integer, every term exact: |t_k| <= 8 * 4 * 63 * 128 < 2^23
+// and |sc_k - sc_{k+1}| <= 255, so the 24-bit multiplies (v_mad_i32_i24, full rate; a 32-bit
+// multiply is quarter rate) see in-range operands and the sums stay far inside int32. The min
+// correction's operands (mins 0..63 or int8 scales, bsums |.| <= 32 * 128) also fit 24 bits.
 template <int T> struct KQDec;
+
+// sum_k cf_k t_k over the running dots t_k of W_k . Y_k (cf: the Abel coefficients)
+__device__ __forceinline__ int abel_dot8(const uint32_t (&W)[8], const uint32_t (&Y)[8], const int (&cf)[8]) {
+  int t = sdot4((int)W[0], (int)Y[0], 0);
+  int p = __mul24(cf[0], t);
+#pragma unroll
+  for (int k = 1; k < 8; k++) {
+    t = sdot4((int)W[k], (int)Y[k], t);
+    p += __mul24(cf[k], t);
+  }
+  return p;
+}
+__device__ __forceinline__ void abel_coef(int (&cf)[8], const int (&sc)[8]) {
+#pragma unroll
+  for (int k = 0; k < 7; k++) cf[k] = sc[k] - sc[k + 1];
+  cf[7] = sc[7];
+}
 template <> struct KQDec<T_Q4K> {
-  uint32_t lo[4], hi[4];
-  int sc[8], mn;
+  uint32_t w[8];  // sub-block k: lo nibbles of code word k / 2 (k even), hi nibbles (k odd)
+  int cf[8], mn;  // Abel coefficients of the sub-block scales
   float d, dm;  // d and dmin
   __device__ __forceinline__ void decode(const KQRaw<T_Q4K> &r, int l) {
     const uint32_t cw[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      lo[c] = cw[c] & 0x0F0F0F0Fu;         // sub-block 2c
-      hi[c] = (cw[c] >> 4) & 0x0F0F0F0Fu;  // sub-block 2c+1
+      w[2 * c] = cw[c] & 0x0F0F0F0Fu;             // sub-block 2c
+      w[2 * c + 1] = (cw[c] >> 4) & 0x0F0F0F0Fu;  // sub-block 2c+1
     }
     // unpack_q4k_scales (q4k_gemv.rs:70-85): bytes 0-3 = S0, 4-7 = S1, 8-11 = S2
     const uint32_t S0 = r.h.y, S1 = r.h.z, S2 = r.h.w;
+    int sc[8];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       sc[k] = (int)((S0 >> (8 * k)) & 63u);
       sc[4 + k] = (int)(((S2 >> (8 * k)) & 15u) | (((S0 >> (8 * k + 6)) & 3u) << 4));
     }
+    abel_coef(cf, sc);
     const int k = l & 3;
     mn = l < 4 ? (int)((S1 >> (8 * k)) & 63u) : (int)(((S2 >> (8 * k + 4)) & 15u) | (((S1 >> (8 * k + 6)) & 3u) << 4));
     d = h2f(r.h.x);
@@ -105,13 +127,7 @@ template <> struct KQDec<T_Q4K> {
   // P = this lane's scaled dot (lane l of sumi), s = its part of the min correction.
   __device__ __forceinline__ void dot(const uint4 &y0, const uint4 &y1, const int2 &bs, int &P, int &s) const {
     const uint32_t Y[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
-    int p = 0;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      p += __mul24(sc[2 * c], sdot4((int)lo[c], (int)Y[2 * c], 0));
-      p += __mul24(sc[2 * c + 1], sdot4((int)hi[c], (int)Y[2 * c + 1], 0));
-    }
-    P = p;
+    P = abel_dot8(w, Y, cf);
     s = __mul24(mn, bs.x + bs.y);
   }
   // corr += (dmin*xd) * float(s); the caller applies acc = fma(d*xd, float(P), acc)
@@ -119,13 +135,14 @@ template <> struct KQDec<T_Q4K> {
 };
 template <> struct KQDec<T_Q6K> {
   uint32_t q[8];  // k = 4h + m: codes of elements 32k + 4l .. +3 (0..63)
-  int sc[8], sa, sb;
+  int cf[8], sa, sb;  // Abel coefficients of the lane's eight scales
   float d, dm;
   __device__ __forceinline__ void decode(const KQRaw<T_Q6K> &r, int l) {
     const uint32_t QL[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};  // [h][mm]
     const uint32_t QH[2] = {r.qh.x, r.qh.y};
     const uint32_t SC[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
     const int hb = (l >> 2) * 8;  // scale of elements 16..31 of each 32 for lanes 4..7
+    int sc[8];
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
@@ -136,6 +153,7 @@ template <> struct KQDec<T_Q6K> {
         // scale index 8h + 2m + (l >> 2): word 2h + (m >> 1), byte 2(m & 1) + (l >> 2)
         sc[4 * h + m] = (int)(int8_t)(SC[2 * h + (m >> 1)] >> (16 * (m & 1) + hb));
       }
+    abel_coef(cf, sc);
     // scales 2l and 2l+1 for this lane's share of 32 * sum_g sc_g * bsum_g
     const uint32_t w = l < 4 ? (l < 2 ? SC[0] : SC[1]) : (l < 6 ? SC[2] : SC[3]);
     const int sh = 16 * (l & 1);
@@ -146,10 +164,7 @@ template <> struct KQDec<T_Q6K> {
   }
   __device__ __forceinline__ void dot(const uint4 &y0, const uint4 &y1, const int2 &bs, int &P, int &s) const {
     const uint32_t Y[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
-    int p = 0;
-#pragma unroll
-    for (int k = 0; k < 8; k++) p += __mul24(sc[k], sdot4((int)q[k], (int)Y[k], 0));
-    P = p;
+    P = abel_dot8(q, Y, cf);
     s = __mul24(sa, bs.x) + __mul24(sb, bs.y);
   }
   __device__ __forceinline__ float corr_term(float xd, int s) const { return (dm * xd) * (float)(32 * s); }

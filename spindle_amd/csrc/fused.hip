@@ -967,7 +967,10 @@ __device__ __forceinline__ void attn_kv_load(const AttnArgs &a, int64_t off, uin
 
 // LDS of k_attn (strides in halves / floats, padded against bank conflicts)
 template <int HD> struct AttnLds {
-  static constexpr int QS = HD + 16, KS = HD + 16, VS = 64 + 16, PS = 64 + 16, SS = 64 + 4;
+  // row strides (f16 elements) of the MFMA operands: rows 4 dwords apart modulo 64 banks, so
+  // the sixteen rows an 8-byte operand load touches fall on distinct banks (and K rows stay
+  // 16-byte aligned for the row stores)
+  static constexpr int QS = HD + 8, KS = HD + 8, VS = 64 + 8, PS = 64 + 8, SS = 64 + 4;
   static constexpr size_t QB = (size_t)2 * 16 * QS * 2;  // qh, ql; later the merged output [16][HD] f32
   static constexpr size_t BYTES = QB + (size_t)64 * KS * 2 + (size_t)HD * VS * 2 + (size_t)16 * SS * 4 + (size_t)2 * 16 * PS * 2 + 3 * 16 * 4;
   static_assert(QB >= (size_t)16 * HD * 4, "merged output fits over the queries");

@@ -1313,7 +1313,8 @@ hipError_t launch_dec_mv(const DecMVArgs &a, int grid, hipStream_t s) {
   if (a.nseg < 1 || a.nseg > 3 || grid < 1 || nb < 1 || nb > DEC_MAXNB || a.in.cols % 256) return hipErrorInvalidValue;
   int G, R;
   rp_shape(nb, G, R);
-  if (a.G != G) return hipErrorInvalidValue;
+  // row groups: rp_shape's, or half as many (two blocks a group, twice the rows a workgroup)
+  if (a.G != G && !(a.G == G / 2 && (nb + a.G - 1) / a.G <= 2)) return hipErrorInvalidValue;
   bool all4 = true, all6 = true;
   for (int i = 0; i < a.nseg; i++) {
     if (a.w[i].dtype != T_Q4K && a.w[i].dtype != T_Q6K) return hipErrorInvalidValue;

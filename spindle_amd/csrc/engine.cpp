@@ -59,6 +59,7 @@ struct spx_engine {
   spx_model_config c{};
   int q_dim = 0, kv_dim = 0, n_ff = 0, nch = 1, lm_grid = 2048, nbest = 1;
   int lm_dec_grid = 256;  // decode pipeline: LM head workgroups (SPX_LM_DEC_GRID), one per CU
+  int n_cu = 256;         // compute units of the device
   int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
@@ -368,12 +369,9 @@ int enqueue_decode(spx_engine *E, bool advance) {
   const auto &c = E->c;
   hipStream_t s = E->ctx->stream;
   const int dim = c.dim, hd = c.head_dim;
-  auto tiles = [](const spx_tensor *t) {
-    int G, R;
-    rp_shape(t->v.nb, G, R);
-    return (int)((t->v.rows + DEC_MV_NW * R - 1) / (DEC_MV_NW * R));
-  };
+  auto tiles_g = [](const spx_tensor *t, int G) { return (int)((t->v.rows + DEC_MV_NW * (8 / G) - 1) / (DEC_MV_NW * (8 / G))); };
   auto gshape = [](const spx_tensor *t) { int G, R; rp_shape(t->v.nb, G, R); return G; };
+  auto tiles = [&](const spx_tensor *t) { return tiles_g(t, gshape(t)); };
   {
     ProfScope ps(E, PC_EMBED, 0);
     NormTail t{};
@@ -388,10 +386,15 @@ int enqueue_decode(spx_engine *E, bool advance) {
       DecMVArgs a{};
       const spx_tensor *w3[3] = {ly.wq, ly.wk, ly.wv};
       float *o3[3] = {E->q, E->k, E->v};
-      int total = 0;
-      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.tiles[i] = tiles(w3[i]); total += a.tiles[i]; }
+      // row groups: rp_shape's unless twice the rows a workgroup (G / 2, two blocks a group)
+      // keeps the launch within one workgroup a CU (a second one on a CU doubles its prologue)
+      int G = gshape(ly.wq), total = 0;
+      if (G >= 2 && (ly.wq->v.nb + G / 2 - 1) / (G / 2) <= 2 && tiles_g(ly.wq, G) + tiles_g(ly.wk, G) + tiles_g(ly.wv, G) > E->n_cu &&
+          tiles_g(ly.wq, G / 2) + tiles_g(ly.wk, G / 2) + tiles_g(ly.wv, G / 2) <= E->n_cu)
+        G /= 2;
+      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.tiles[i] = tiles_g(w3[i], G); total += a.tiles[i]; }
       a.nseg = 3;
-      a.G = gshape(ly.wq);
+      a.G = G;
       a.in = DecIn{E->xA, ly.attn_norm, c.rms_eps, dim};
       SPX_HIP(launch_dec_mv(a, total, s));
     }
@@ -652,6 +655,10 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   E->kv_dim = c.n_kv_heads * c.head_dim;
   E->L.resize(c.n_layers);
   E->nch = (c.max_seq + 63) / 64;
+  {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) E->n_cu = n;
+  }
   if (const char *v = std::getenv("SPX_LM_GRID")) E->lm_grid = std::max(1, atoi(v));
   if (const char *v = std::getenv("SPX_LM_DEC_GRID")) E->lm_dec_grid = std::max(1, std::min(atoi(v), 2048));
   if (const char *v = std::getenv("SPX_MV_MODE")) E->mv_mode = std::max(0, std::min(1, atoi(v)));

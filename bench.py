@@ -32,9 +32,9 @@ HBM_PEAK_GBS = 8000.0
 # attention class is the split-K kernel plus its merge. Counters cannot be read inside a timed
 # run, so the bench reports this measurement.
 MEASURED_TRAFFIC = {
-    "attention": 11_698_381, "qkv_matvec": 6_425_600, "attn_output_matvec": 4_982_784,
-    "router_route": 1_234_944, "gate_up_swiglu": 14_438_298, "down_combine": 10_976_256,
-    "lm_head_matvec": 256_884_122,
+    "attention": 11_692_237, "qkv_matvec": 6_446_080, "attn_output_matvec": 4_982_784,
+    "router_route": 1_236_992, "gate_up_swiglu": 14_435_021, "down_combine": 10_970_112,
+    "lm_head_matvec": 256_769_434,
 }
 
 

@@ -191,6 +191,10 @@ int spx_tensor_upload(spx_ctx *ctx, int dtype, int64_t cols, int64_t rows, int n
       t->plane_off[f[k].plane] = bytes;
       bytes += (((size_t)nblk * f[k].len + 255) & ~(size_t)255) + 256;  // slack: 16-byte loads may run past a plane's end
     }
+    if (dtype == T_Q4K) {  // derived plane 2: scales and mins unpacked to bytes (below)
+      t->plane_off[2] = bytes;
+      bytes += (((size_t)nblk * 16 + 255) & ~(size_t)255) + 256;
+    }
   }
   hipError_t e = hipMalloc(&t->dev, std::max<size_t>(bytes, 256));
   if (e != hipSuccess) { delete t; return hip_fail(e, "hipMalloc(tensor)"); }
@@ -201,6 +205,22 @@ int spx_tensor_upload(spx_ctx *ctx, int dtype, int64_t cols, int64_t rows, int n
   } else {
     img.resize(bytes);
     parallel_blocks(nblk, [&](int64_t a, int64_t b) { relayout(dtype, src, img.data(), t->plane_off, a, b, true); });
+    if (dtype == T_Q4K) {
+      // sc[0..7], mn[0..7] of each block as bytes (unpack_q4k_scales, q4k_gemv.rs:70-85), read
+      // by the multi-row MFMA kernels; a copy of the header's information, so download ignores it
+      parallel_blocks(nblk, [&](int64_t a0, int64_t a1) {
+        for (int64_t g = a0; g < a1; g++) {
+          const uint8_t *sc = src + (size_t)g * 144 + 4;
+          uint8_t *o = img.data() + t->plane_off[2] + (size_t)g * 16;
+          for (int k = 0; k < 4; k++) {
+            o[k] = sc[k] & 63;
+            o[4 + k] = (uint8_t)((sc[8 + k] & 15) | ((sc[k] >> 6) << 4));
+            o[8 + k] = sc[4 + k] & 63;
+            o[12 + k] = (uint8_t)((sc[8 + k] >> 4) | ((sc[4 + k] >> 6) << 4));
+          }
+        }
+      });
+    }
     e = hipMemcpy(t->dev, img.data(), bytes, hipMemcpyHostToDevice);
   }
   if (e != hipSuccess) { (void)hipFree(t->dev); delete t; return hip_fail(e, "hipMemcpy(tensor)"); }

@@ -20,7 +20,7 @@ enum DType : int {
 
 // Device view of one uploaded tensor (all experts). Plane pointers by dtype:
 //   Q4_K: p0 = codes (128 B/blk, lane-permuted, see kq.h), p1 = header (16 B/blk: d, dmin,
-//         scales[12])
+//         scales[12]), p2 = the scales and mins unpacked to bytes (16 B/blk: sc[0..7], mn[0..7])
 //   Q6_K: p0 = ql (128, lane-permuted), p1 = qh (64, lane-permuted), p2 = scales (16), p3 = d (2)
 //   Q8_0: p0 = codes (32), p3 = d (2)
 //   Q5_0: p0 = low nibbles (16), p1 = high bits (4), p3 = d (2)

@@ -194,12 +194,18 @@ __host__ __device__ inline size_t gum_lds_bytes(int m, int cols, int max_jobs) {
 
 hipError_t launch_dec_norm(const DecNormArgs &a, int m, hipStream_t s);
 hipError_t launch_dec_mm(const DecMMArgs &a, int grid, hipStream_t s);
+// The same matvec on the int8 matrix cores (16-row tiles; block totals exact, fp32 sums to
+// rounding): tiles[i] counts 16-row tiles; tiles stride over the grid.
+hipError_t launch_dec_mq(const DecMMArgs &a, int grid, hipStream_t s);
 // kd_mm grid for a number of tiles: at most two workgroups a CU, the same number of tiles each
 // (tiles stride over the grid; the next tile's weights are requested before the results)
 int dec_mm_grid(int tiles);
 hipError_t launch_dec_router_m(const DecRouterMArgs &a, hipStream_t s);
 hipError_t launch_dec_gateup_m(const DecGateUpMArgs &a, int max_jobs, hipStream_t s);
 hipError_t launch_dec_down_m(const DecDownMArgs &a, hipStream_t s);
+// The grouped expert kernels on the int8 matrix cores (16-row tiles)
+hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &a, int max_jobs, hipStream_t s);
+hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s);
 hipError_t launch_dec_merge(const DecMergeArgs &a, const StepRec *st, hipStream_t s);
 hipError_t launch_dec_router(const DecRouterArgs &a, hipStream_t s);
 hipError_t launch_dec_gateup(const DecGateUpArgs &a, hipStream_t s);

@@ -1286,7 +1286,395 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
   }
 }
 
+// ================================================================== int8 MFMA, 2..16 rows
+// The multi-row kernels' alternative to the per-lane dot chains (the verify pass of the
+// speculative loop): per 256-block the exact integer P = sum_s sc_s S_s, S_s the sub-block's
+// (group's) code x activation dot from v_mfma_i32_16x16x32_i8 (16 vectors x 16 matrix rows),
+// and the exact correction integer C of the reference's block; then per block in order
+// acc = fma(d xd, float(P), acc), corr += (dmin xd) float(C) (Q6_K: (d xd) float(32 C)),
+// out = acc - corr. The integers are the reference's block totals; the fp32 sums take the block
+// total where the reference converts eight lane partials, so the outputs agree to rounding
+// (not bit for bit). Operand layouts of 16x16x32 i8: A[i][k] in lane i + 16 (k / 8), byte k % 8;
+// B[k][j] in lane j + 16 (k / 8); D[i][j] in lane j + 16 (i / 4), element i % 4. A holds the
+// activations (i = vector), B the weight codes (j = matrix row), so lane c16 + 16 k4 owns matrix
+// row c16 for vectors 4 k4 + t: one row's scales and d a lane.
+typedef int mq_v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ mq_v4i mq_mfma(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1) {
+  const long a = (long)(((unsigned long long)a1 << 32) | a0), b = (long)(((unsigned long long)b1 << 32) | b0);
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, mq_v4i{0, 0, 0, 0}, 0, 0, 0);
+}
+__device__ __forceinline__ int mq_byte(uint4 v, int i) {  // byte i (0..15, constant after unrolling)
+  const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
+  return (int)((w >> (8 * (i & 3))) & 0xffu);
+}
+__device__ __forceinline__ int mq_sbyte(uint4 v, int i) { return (int)(int8_t)mq_byte(v, i); }
+
+// Raw bytes of one 256-block of a 16-row tile as a lane loads them: the code words of matrix
+// row lane & 15 for K = 32 (lane >> 4) .. +31 of each sub-block's MFMA, and that row's scales
+// and d. Q4_K: a, b = codes, s = unpacked scales (plane 2), d = d | dmin << 16. Q6_K: a, b = ql,
+// h = qh, s = int8 scales, d = fp16 d.
+struct MqRaw {
+  uint4 a, b, h, s;
+  uint32_t d;
+};
+template <int T>
+__device__ __forceinline__ void mq_load(MqRaw &r, const Planes &pl, int64_t row0, int nrows, int nb, int b) {
+  const int lane = threadIdx.x & 63, c16 = lane & 15, k4 = lane >> 4;
+  const int64_t ra = (row0 + min(c16, nrows - 1)) * nb + b;
+  const uint8_t *cp = pl.p0 + ra * 128 + 32 * k4;
+  r.a = gld<uint4>(cp);
+  r.b = gld<uint4>(cp + 16);
+  r.s = gld<uint4>(pl.p2 + ra * 16);
+  if constexpr (T == T_Q6K) {
+    r.h = gld<uint4>(pl.p1 + ra * 64 + 16 * k4);
+    r.d = gld<uint16_t>(pl.p3 + ra * 2);
+  } else {
+    r.d = gld<uint32_t>(pl.p1 + ra * 16);
+  }
+}
+struct MqIdentity {
+  __device__ __forceinline__ int operator()(int v) const { return v; }
+};
+struct MqRows {
+  const SPX_L int *r;
+  __device__ __forceinline__ int operator()(int v) const { return r[v]; }
+};
+
+// The tile's vectors: the A operand's vector (lane & 15) and the D elements' vectors
+// 4 (lane >> 4) + t, as rows of the LDS Q8_K image (row 0 stands in past the last vector).
+struct MqVec {
+  bool ain;
+  int a, d[4];
+};
+template <class VR>
+__device__ __forceinline__ MqVec mq_vecs(int nv, VR vrow) {
+  const int lane = threadIdx.x & 63, c16 = lane & 15, k4 = lane >> 4;
+  MqVec v;
+  v.ain = c16 < nv;
+  v.a = v.ain ? vrow(c16) : 0;
+#pragma unroll
+  for (int t = 0; t < 4; t++) v.d[t] = 4 * k4 + t < nv ? vrow(4 * k4 + t) : 0;
+  return v;
+}
+// Block b of the tile: acc / cr of matrix row lane & 15, vectors 4 (lane >> 4) + t.
+template <int T>
+__device__ __forceinline__ void mq_block(const MqRaw &r, const MqVec &vv, int nb, int b, const SPX_L uint32_t *lq,
+                                         const SPX_L float *ld, const SPX_L int2 *lbs, float (&acc)[4], float (&cr)[4]) {
+  const int k4 = (threadIdx.x & 63) >> 4;
+  const SPX_L uint32_t *yp = lq + (vv.a * nb + b) * 64 + 16 * k4;
+  auto Yw = [&](int i) { return vv.ain ? yp[i] : 0u; };
+  int P[4] = {0, 0, 0, 0}, C[4] = {0, 0, 0, 0};
+  if constexpr (T == T_Q4K) {
+    const uint32_t CA[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, CB[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+      const int c = s >> 1, h = s & 1;
+      const mq_v4i S = mq_mfma(Yw(s), Yw(8 + s), (CA[c] >> (4 * h)) & 0x0F0F0F0Fu, (CB[c] >> (4 * h)) & 0x0F0F0F0Fu);
+      const int sc = mq_byte(r.s, s);
+#pragma unroll
+      for (int t = 0; t < 4; t++) P[t] += __mul24(S[t], sc);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {  // C = sum_s mn_s (bsum_2s + bsum_2s+1) of vector 4 k4 + t
+      const SPX_L int4 *bq = (const SPX_L int4 *)(lbs + (vv.d[t] * nb + b) * 8);
+      const int4 q0 = lld<int4>(bq), q1 = lld<int4>(bq + 1), q2 = lld<int4>(bq + 2), q3 = lld<int4>(bq + 3);
+      C[t] = __mul24(q0.x + q0.y, mq_byte(r.s, 8)) + __mul24(q0.z + q0.w, mq_byte(r.s, 9)) + __mul24(q1.x + q1.y, mq_byte(r.s, 10)) +
+             __mul24(q1.z + q1.w, mq_byte(r.s, 11)) + __mul24(q2.x + q2.y, mq_byte(r.s, 12)) + __mul24(q2.z + q2.w, mq_byte(r.s, 13)) +
+             __mul24(q3.x + q3.y, mq_byte(r.s, 14)) + __mul24(q3.z + q3.w, mq_byte(r.s, 15));
+    }
+    const float d = h2f(r.d), dm = h2f(r.d >> 16);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const float xd = ld[vv.d[t] * nb + b];
+      acc[t] = fmaf(d * xd, (float)P[t], acc[t]);
+      cr[t] = cr[t] + (dm * xd) * (float)C[t];
+    }
+  } else {  // T_Q6K: 16 groups of 16 (two MFMAs a sub-block, the other half's codes zero)
+    const uint32_t QA[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, QB[4] = {r.b.x, r.b.y, r.b.z, r.b.w}, QH[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int h = k >> 2, m = k & 3;
+      const uint32_t c0 = ((QA[2 * h + (m & 1)] >> (4 * (m >> 1))) & 0x0F0F0F0Fu) | (((QH[h] >> (2 * m)) & 0x03030303u) << 4);
+      const uint32_t c1 = ((QB[2 * h + (m & 1)] >> (4 * (m >> 1))) & 0x0F0F0F0Fu) | (((QH[2 + h] >> (2 * m)) & 0x03030303u) << 4);
+      const bool lo = k4 < 2;
+      const uint32_t ya = Yw(k), yb = Yw(8 + k);
+      const mq_v4i S0 = mq_mfma(ya, yb, lo ? c0 : 0u, lo ? c1 : 0u);   // group 2k
+      const mq_v4i S1 = mq_mfma(ya, yb, lo ? 0u : c0, lo ? 0u : c1);   // group 2k + 1
+      const int s0 = mq_sbyte(r.s, 2 * k), s1 = mq_sbyte(r.s, 2 * k + 1);
+#pragma unroll
+      for (int t = 0; t < 4; t++) P[t] += __mul24(S0[t], s0) + __mul24(S1[t], s1);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {  // C = sum_g sc_g bsum_g of vector 4 k4 + t
+      const SPX_L int4 *bq = (const SPX_L int4 *)(lbs + (vv.d[t] * nb + b) * 8);
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int4 q = lld<int4>(bq + i);
+        c += __mul24(q.x, mq_sbyte(r.s, 4 * i)) + __mul24(q.y, mq_sbyte(r.s, 4 * i + 1)) + __mul24(q.z, mq_sbyte(r.s, 4 * i + 2)) +
+             __mul24(q.w, mq_sbyte(r.s, 4 * i + 3));
+      }
+      C[t] = c;
+    }
+    const float d = h2f(r.d);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const float xd = ld[vv.d[t] * nb + b];
+      acc[t] = fmaf(d * xd, (float)P[t], acc[t]);
+      cr[t] = cr[t] + (d * xd) * (float)(32 * C[t]);
+    }
+  }
+}
+// Blocks b0, b0 + bstep, ... of a 16-row tile (matrix rows row0 .. row0 + nrows - 1, clamped).
+template <int T>
+__device__ __forceinline__ void mq_tile(const Planes &pl, int64_t row0, int nrows, int nb, int b0, int bstep, const MqVec &vv,
+                                        const SPX_L uint32_t *lq, const SPX_L float *ld, const SPX_L int2 *lbs, float (&acc)[4],
+                                        float (&cr)[4]) {
+  for (int b = b0; b < nb; b += bstep) {
+    MqRaw r;
+    mq_load<T>(r, pl, row0, nrows, nb, b);
+    mq_block<T>(r, vv, nb, b, lq, ld, lbs, acc, cr);
+  }
+}
+
+// A unit of kd_mq: tile t (segment si, rows row0 .. row0 + nrows - 1), block wave + NW u. The
+// bookkeeping is wave-uniform and kept scalar (readfirstlane), so the segment's fields are read
+// from the arguments with scalar loads: a vector load between a block's loads and their use
+// would wait for every load in flight.
+struct MqPos {
+  int t, u, si, nrows;
+  int64_t row0;
+};
+__device__ __forceinline__ void mq_locate(const DecMMArgs &a, int total, MqPos &p) {
+  const int t0 = a.tiles[0], t1 = a.nseg > 1 ? a.tiles[1] : 0, tt = min(p.t, total - 1);
+  p.si = __builtin_amdgcn_readfirstlane(tt >= t0 ? (tt >= t0 + t1 ? 2 : 1) : 0);
+  p.row0 = (int64_t)(tt - (p.si > 0 ? t0 : 0) - (p.si > 1 ? t1 : 0)) * 16;
+  p.nrows = (int)min((int64_t)16, a.w[p.si].rows - p.row0);
+}
+// Multi-vector matvec on the matrix cores: tiles of 16 rows over up to three segments (the
+// formats may differ by segment), the m vectors' Q8_K staged in LDS; wavefront w of the
+// DEC_MM_NW takes blocks w, w + DEC_MM_NW, ... of each tile. The wavefronts' partials
+// (acc - corr) meet in LDS, two tiles' worth so one barrier a tile suffices, and wavefront
+// q < 4 adds row group q in wavefront order and runs the epilogue (residual, greedy keys) as
+// kd_mm does.
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void kd_mq(const DecMMArgs a) {
+  constexpr int NW = DEC_MM_NW;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float red[2][NW][4][64];
+  __shared__ unsigned long long sbest[MAX_M];
+  const int m = a.m, cols = a.cols, nbq = cols >> 8, nb = nbq;
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
+  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)m * cols + 15) & ~(size_t)15));
+  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)m * cols + 15) & ~(size_t)15) + (((size_t)m * nbq * 4 + 15) & ~(size_t)15));
+  const int total = a.tiles[0] + (a.nseg > 1 ? a.tiles[1] : 0) + (a.nseg > 2 ? a.tiles[2] : 0);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, c16 = lane & 15;
+  if (threadIdx.x < MAX_M) sbest[threadIdx.x] = 0;
+  stage_q8<NW * 64>(a.y, (const int *)nullptr, m, cols, lq, ld, lbs);
+  __syncthreads();
+  int buf = 0;
+  const MqVec vv = mq_vecs(m, MqIdentity{});
+  for (int t = blockIdx.x; t < total; t += gridDim.x) {
+    MqPos p;
+    p.t = t;
+    p.u = 0;
+    mq_locate(a, total, p);
+    const TensorView &w = a.w[p.si];
+    float acc[4] = {0.f, 0.f, 0.f, 0.f}, cr[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int b = wave; b < nb; b += NW) {
+      MqRaw r;
+      if (w.dtype == T_Q4K) {
+        mq_load<T_Q4K>(r, w.pl, p.row0, p.nrows, nb, b);
+        mq_block<T_Q4K>(r, vv, nb, b, lq, ld, lbs, acc, cr);
+      } else {
+        mq_load<T_Q6K>(r, w.pl, p.row0, p.nrows, nb, b);
+        mq_block<T_Q6K>(r, vv, nb, b, lq, ld, lbs, acc, cr);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) red[buf][wave][q][lane] = acc[q] - cr[q];
+    __syncthreads();
+    if (wave < 4) {
+      const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
+      float res = red[buf][0][q][lane];
+      for (int w2 = 1; w2 < NW; w2++) res = res + red[buf][w2][q][lane];
+      if (v < m && r < p.nrows) {
+        float *const out = a.out[p.si];
+        const int64_t row = p.row0 + r;
+        if (out) gst<float>(out + (int64_t)v * a.ld_out[p.si] + row, res);
+        if (a.res_out) {
+          const int64_t o = (int64_t)v * w.rows + row;
+          gst<float>(a.res_out + o, gld<float>(a.res_in + o) + a.rscale * res);
+        }
+        if (a.best) atomicMax(&sbest[v], pick_key(res, a.lscale, row));
+      }
+    }
+    buf ^= 1;
+  }
+  if (a.best) {
+    __syncthreads();
+    if ((int)threadIdx.x < m) gst<unsigned long long>(a.best + (int64_t)threadIdx.x * a.nbest + blockIdx.x, sbest[threadIdx.x]);
+  }
+}
+
+// Routing + gate/up + SwiGLU over the jobs on the matrix cores (kd_gateup_m's prologue, job
+// list and item split; items are (job, 16 h rows)): wavefront w takes blocks w, w + 8, ... of
+// the item's gate and up tiles, the partial sums meet in LDS in wavefront order.
+template <int T>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(T == T_Q4K ? 4 : 2))) void kd_gateup_mq(const DecGateUpMArgs a) {
+  constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ signed char slot_of[MAX_M * 256];
+  __shared__ int wcount[NW];
+  __shared__ float red[2][NW][2][4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n_ff = a.n_ff, cols = (int)a.gate.cols, nbq = cols >> 8, nb = nbq, m = a.m;
+  const int TX = (n_ff + 15) / 16;
+  const size_t act = mm_act_bytes(m, cols);
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
+  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)m * cols + 15) & ~(size_t)15));
+  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)m * cols + 15) & ~(size_t)15) + (((size_t)m * nbq * 4 + 15) & ~(size_t)15));
+  SPX_L int *sj = (SPX_L int *)(smem + act);  // [max jobs][JR]
+  int nj = 1;
+  {
+    StageQ8<NW * 64> st;
+    if (a.rt.logits) {
+      float lv[2][4];
+      route_load<NW>(a.rt, lv);
+      st.get(a.y, m, cols);
+      nj = route_jobs<NW>(a.rt, lv, sj, (SPX_L signed char *)slot_of, (SPX_L int *)wcount, blockIdx.x == 0);
+    } else {
+      st.get(a.y, m, cols);
+      for (int i = threadIdx.x; i < JR; i += blockDim.x) sj[i] = i == 0 ? 0 : i == 1 ? m : i < 2 + MAX_M ? i - 2 : i - 2 - MAX_M;
+    }
+    st.put(m, cols, lq, ld, lbs);
+  }
+  __syncthreads();
+  const int n = TX * nj, G = gridDim.x;
+  const int i0 = (int)((int64_t)blockIdx.x * n / G), i1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
+  // units of an item: (block wave + NW (u >> 1), gate if u even else up), u < 2 U; each unit's
+  // bytes are loaded while the previous unit is multiplied
+  const int nbw = wave < nb ? (nb - wave + NW - 1) / NW : 0, U2 = 2 * max(nbw, 1);
+  const int c16 = lane & 15;
+  auto item_rows = [&](int i, int64_t &row0, int &nrows) {
+    const int j = i / TX, x = i - j * TX;
+    const int e = min(max(sj[j * JR], 0), a.gate.n_expert - 1);
+    row0 = (int64_t)e * a.gate.rows + (int64_t)x * 16;
+    nrows = min(16, n_ff - x * 16);
+  };
+  int i = i0, u = 0, buf = 0;
+  int64_t crow0 = 0;
+  int cnrows = 1;
+  if (i < i1) item_rows(i, crow0, cnrows);
+  MqRaw cur, nxt;
+  if (i < i1 && nbw > 0) mq_load<T>(cur, a.gate.pl, crow0, cnrows, nb, wave);
+  float ag[4] = {0.f, 0.f, 0.f, 0.f}, cg[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f}, cu[4] = {0.f, 0.f, 0.f, 0.f};
+  while (i < i1) {
+    int in = i, un = u + 1;
+    if (un >= U2) { un = 0; in++; }
+    int64_t nrow0 = crow0;
+    int nnrows = cnrows;
+    if (un == 0 && in < i1) item_rows(in, nrow0, nnrows);
+    if (in < i1 && nbw > 0) mq_load<T>(nxt, (un & 1) ? a.up.pl : a.gate.pl, nrow0, nnrows, nb, wave + NW * (un >> 1));
+    const int j = i / TX, nv = sj[j * JR + 1];
+    if (nbw > 0) {
+      const MqVec vv = mq_vecs(nv, MqRows{sj + j * JR + 2});
+      if (u & 1) mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lbs, au, cu);
+      else mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lbs, ag, cg);
+    }
+    if (un == 0) {  // item i complete
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        red[buf][wave][0][q][lane] = ag[q] - cg[q];
+        red[buf][wave][1][q][lane] = au[q] - cu[q];
+        ag[q] = cg[q] = au[q] = cu[q] = 0.f;
+      }
+      __syncthreads();
+      if (wave < 4) {
+        const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
+        float g = red[buf][0][0][q][lane], up = red[buf][0][1][q][lane];
+        for (int w2 = 1; w2 < NW; w2++) { g = g + red[buf][w2][0][q][lane]; up = up + red[buf][w2][1][q][lane]; }
+        const int x = i - j * TX;
+        if (v < nv && r < cnrows) gst<float>(a.h + (int64_t)sj[j * JR + 2 + MAX_M + v] * n_ff + x * 16 + r, g / (1.0f + expf(-g)) * up);
+      }
+      buf ^= 1;
+      crow0 = nrow0;
+      cnrows = nnrows;
+    }
+    cur = nxt;
+    i = in;
+    u = un;
+  }
+}
+
+// Down projection of the jobs' users on the matrix cores: items (job, 128 rows), wavefront w
+// takes the 16-row tile w, all its blocks in order; the job's users' h rows are quantized into
+// LDS (quantize_avx2 per 256 block) as kd_down_m does; y per (row, choice) to yd.
+template <int T>
+__global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_mq(const DecDownMArgs a) {
+  constexpr int NW = DEC_MM_NW, RW = NW * 16, JF = 2 + MAX_M;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int s_job[JF];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, nbh = n_ff >> 8, TX = (dim + RW - 1) / RW;
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
+  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)MAX_M * n_ff + 15) & ~(size_t)15));
+  SPX_L int *lbs = (SPX_L int *)(smem + (((size_t)MAX_M * n_ff + 15) & ~(size_t)15) + (((size_t)MAX_M * nbh * 4 + 15) & ~(size_t)15));
+  const int n = TX * gld<int>(a.njobs);
+  for (int it = blockIdx.x; it < n; it += gridDim.x) {
+    const int j = it / TX, x = it - j * TX;
+    if ((int)threadIdx.x < JF) {
+      const int f = threadIdx.x;
+      s_job[f] = gld<int>(reinterpret_cast<const int *>(a.jobs + j) + (f < 2 ? f : 2 + MAX_M + (f - 2)));
+    }
+    __syncthreads();
+    const int e = min(max(s_job[0], 0), a.w.n_expert - 1), nv = min(max(s_job[1], 0), MAX_M);
+    const int nq = nv * nbh;
+    for (int q0 = wave; q0 < nq; q0 += 4 * NW) {
+      float4 hv[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int q = q0 + NW * t;
+        if (q < nq) {
+          const int k = q / nbh, i = q - k * nbh;
+          hv[t] = gld<float4>(a.h + (int64_t)s_job[2 + k] * n_ff + i * 256 + 4 * lane);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int q = q0 + NW * t;
+        if (q < nq) {
+          const float am = wave_max(amax4(hv[t]));
+          q8k_block_store(hv[t], am, lq + q * 64, ld + q, lbs + q * 16);
+        }
+      }
+    }
+    __syncthreads();
+    const int64_t r0 = (int64_t)x * RW + wave * 16;
+    if (r0 < dim) {
+      const int nrows = (int)min((int64_t)16, dim - r0);
+      float acc[4] = {0.f, 0.f, 0.f, 0.f}, cr[4] = {0.f, 0.f, 0.f, 0.f};
+      mq_tile<T>(a.w.pl, (int64_t)e * dim + r0, nrows, nbh, 0, 1, mq_vecs(nv, MqIdentity{}), lq, ld, (const SPX_L int2 *)lbs, acc, cr);
+      const int r = lane & 15;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int v = 4 * (lane >> 4) + q;
+        if (v < nv && r < nrows) gst<float>(a.yd + (int64_t)s_job[2 + v] * dim + r0 + r, acc[q] - cr[q]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // ------------------------------------------------------------------ launchers
+static int cu_count() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+  }
+  return n;
+}
+
 static int nb_bucket(int nb) { return nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 3 ? 3 : nb <= 4 ? 4 : nb <= 8 ? 8 : 16; }
 
 template <int TT>
@@ -1428,19 +1816,53 @@ hipError_t launch_dec_mm(const DecMMArgs &a, int grid, hipStream_t s) {
   return dec_mm_tt<0>(a, grid, s);
 }
 
+hipError_t launch_dec_mq(const DecMMArgs &a, int grid, hipStream_t s) {
+  const int nb = a.cols >> 8;
+  if (a.nseg < 1 || a.nseg > 3 || grid < 1 || nb < 1 || nb > DEC_MAXNB || a.cols % 256 || a.m < 1 || a.m > MAX_M) return hipErrorInvalidValue;
+  for (int i = 0; i < a.nseg; i++)
+    if ((a.w[i].dtype != T_Q4K && a.w[i].dtype != T_Q6K) || a.w[i].nb != nb) return hipErrorInvalidValue;
+  if (a.res_out && a.nseg != 1) return hipErrorInvalidValue;
+  const size_t sm = mm_act_bytes(a.m, a.cols);
+  SPX_DLDS(kd_mq, sm);
+  hipLaunchKernelGGL(kd_mq, dim3(grid), dim3(DEC_MM_NW * 64), sm, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &args, int max_jobs, hipStream_t s) {
+  DecGateUpMArgs a = args;
+  a.max_jobs = max_jobs;
+  const int nb = (int)(a.gate.cols >> 8), cols = (int)a.gate.cols;
+  if (a.gate.cols % 256 || nb > DEC_MAXNB || a.gate.nb != nb || a.up.nb != nb || a.gate.dtype != a.up.dtype || a.m < 1 || a.m > MAX_M || max_jobs < 1 ||
+      max_jobs > 512 || (a.rt.logits && (max_jobs > a.gate.n_expert || a.rt.m != a.m || a.rt.n_expert < 1 || a.rt.n_expert > 256 || a.rt.n_used < 1 ||
+                                         a.rt.n_used > 32 || a.rt.n_used > a.rt.n_expert)))
+    return hipErrorInvalidValue;
+  const size_t sm = mm_act_bytes(a.m, cols) + (size_t)(a.rt.logits ? max_jobs : 1) * (2 + 2 * MAX_M) * 4;
+  if (sm > 100 * 1024) return hipErrorInvalidValue;
+  // two workgroups a CU (Q4_K: at most 128 registers a lane), all resident, so each routes once
+  // and takes its items in turn
+  const int items = ((a.n_ff + 15) / 16) * (a.rt.logits ? max_jobs : 1);
+  const dim3 grid((unsigned)std::min(items, (a.gate.dtype == T_Q4K ? 2 : 1) * cu_count())), b(DEC_MM_NW * 64);
+  if (a.gate.dtype == T_Q4K) { SPX_DLDS((kd_gateup_mq<T_Q4K>), sm); hipLaunchKernelGGL((kd_gateup_mq<T_Q4K>), grid, b, sm, s, a); }
+  else if (a.gate.dtype == T_Q6K) { SPX_DLDS((kd_gateup_mq<T_Q6K>), sm); hipLaunchKernelGGL((kd_gateup_mq<T_Q6K>), grid, b, sm, s, a); }
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s) {
+  if (a.w.cols % 256 || a.w.nb > 4 || a.max_jobs < 1 || a.max_jobs > 512 || a.max_jobs > a.w.n_expert || !a.h || !a.yd) return hipErrorInvalidValue;
+  const int tx = (int)((a.w.rows + DEC_MM_NW * 16 - 1) / (DEC_MM_NW * 16));
+  const dim3 grid((unsigned)std::min(tx * a.max_jobs, 2 * cu_count())), b(DEC_MM_NW * 64);
+  const size_t sm = downm_lds_bytes((int)a.w.cols);
+  if (a.w.dtype == T_Q4K) hipLaunchKernelGGL((kd_down_mq<T_Q4K>), grid, b, sm, s, a);
+  else if (a.w.dtype == T_Q6K) hipLaunchKernelGGL((kd_down_mq<T_Q6K>), grid, b, sm, s, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 hipError_t launch_dec_router_m(const DecRouterMArgs &a, hipStream_t s) {
   if (a.dim % 256 || a.dim > 256 * DEC_MAXNB || a.m < 1 || a.m > MAX_M) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kd_router_m, dim3(a.n_expert), dim3(256), 0, s, a);
   return hipGetLastError();
-}
-
-static int cu_count() {
-  static int n = 0;
-  if (!n) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
-  }
-  return n;
 }
 
 int dec_mm_grid(int tiles) {

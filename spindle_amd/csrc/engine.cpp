@@ -60,6 +60,10 @@ struct spx_engine {
   int q_dim = 0, kv_dim = 0, n_ff = 0, nch = 1, lm_grid = 2048, nbest = 1;
   int lm_dec_grid = 256;  // decode pipeline: LM head workgroups (SPX_LM_DEC_GRID), one per CU
   int n_cu = 256;         // compute units of the device
+  bool mq = true;          // passes of 2..16 rows on the int8 matrix cores (SPX_MQ, spx_engine_set_mfma)
+  bool mq_down = false;    // also the routed experts' down projection (SPX_MQ_DOWN): about one row an expert,
+                           // so the MFMA's 16 columns idle and the per-lane dot kernel is faster
+  bool mq_gateup = true;   // the gate/up projections (SPX_MQ_GATEUP)
   int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
@@ -489,6 +493,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
     return (int)((t->v.rows + DEC_MM_NW * R - 1) / (DEC_MM_NW * R));
   };
   auto gshape = [](const spx_tensor *t) { int G, R; rp_shape(t->v.nb, G, R); return G; };
+  auto qtiles = [](const spx_tensor *t) { return (int)((t->v.rows + 15) / 16); };
   bool combine = false;  // the last MoE layer's expert outputs wait in yd for the next norm
   auto norm = [&](const float *x, const float *nw, float *xn_out, Q8KP q) {
     DecNormArgs na{};
@@ -520,9 +525,9 @@ int enqueue_pass_m(spx_engine *E, int m) {
       float *o3[3] = {E->q, E->k, E->v};
       const int64_t ld3[3] = {E->q_dim, E->kv_dim, E->kv_dim};
       int total = 0;
-      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.ld_out[i] = ld3[i]; a.tiles[i] = mtiles(w3[i]); total += a.tiles[i]; }
+      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.ld_out[i] = ld3[i]; a.tiles[i] = E->mq ? qtiles(w3[i]) : mtiles(w3[i]); total += a.tiles[i]; }
       a.nseg = 3; a.G = gshape(ly.wq); a.y = E->xq2; a.cols = dim; a.m = m;
-      SPX_HIP(launch_dec_mm(a, dec_mm_grid(total), s));
+      SPX_HIP(E->mq ? launch_dec_mq(a, std::min(total, 2 * E->n_cu), s) : launch_dec_mm(a, dec_mm_grid(total), s));
     }
     const bool att_q_fused = ((c.n_heads / c.n_kv_heads) * hd) % 256 == 0;
     {
@@ -541,10 +546,10 @@ int enqueue_pass_m(spx_engine *E, int m) {
     {
       ProfScope ps(E, PC_WO, wbytes(ly.wo));
       DecMMArgs a{};
-      a.w[0] = ly.wo->v; a.out[0] = E->proj; a.ld_out[0] = dim; a.tiles[0] = mtiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
+      a.w[0] = ly.wo->v; a.out[0] = E->proj; a.ld_out[0] = dim; a.tiles[0] = E->mq ? qtiles(ly.wo) : mtiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
       a.y = E->aq; a.cols = E->q_dim; a.m = m;
       a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
-      SPX_HIP(launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
+      SPX_HIP(E->mq ? launch_dec_mq(a, std::min(a.tiles[0], 2 * E->n_cu), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
     }
     const int nff = (int)ly.gate->v.rows;
     {
@@ -563,27 +568,27 @@ int enqueue_pass_m(spx_engine *E, int m) {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up), l, true);
         ga.rt = DecRouteArgs{E->rlog, c.n_expert, c.n_expert_used, c.expert_norm, m, c.moe_prune, E->chosen, E->weights, E->nkeep,
                              E->jobs, ly.njobs, E->expert_count + (size_t)l * c.n_expert};
-        SPX_HIP(launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
+        SPX_HIP(E->mq && E->mq_gateup ? launch_dec_gateup_mq(ga, std::min(m * nu, c.n_expert), s) : launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
       }
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
         DecDownMArgs da{ly.down->v, E->h, E->jobs, ly.njobs, E->yd, std::min(m * nu, c.n_expert)};
-        SPX_HIP(launch_dec_down_m(da, s));
+        SPX_HIP(E->mq && E->mq_down ? launch_dec_down_mq(da, s) : launch_dec_down_m(da, s));
         combine = true;  // + weighted combine + residual in the next norm (xB -> xA)
       }
     } else {  // ffn_forward_multi (:616-646)
       {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
-        SPX_HIP(launch_dec_gateup_m(ga, 1, s));
+        SPX_HIP(E->mq && E->mq_gateup ? launch_dec_gateup_mq(ga, 1, s) : launch_dec_gateup_m(ga, 1, s));
         SPX_HIP(launch_q8kp_quantize(E->h, nff, nff, m, E->hq, s));
       }
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down));
         DecMMArgs a{};
-        a.w[0] = ly.down->v; a.out[0] = E->ffn; a.ld_out[0] = dim; a.tiles[0] = mtiles(ly.down); a.nseg = 1; a.G = gshape(ly.down);
-        a.y = E->hq; a.cols = nff; a.m = m;
+        a.w[0] = ly.down->v; a.out[0] = E->ffn; a.ld_out[0] = dim; a.tiles[0] = E->mq ? qtiles(ly.down) : mtiles(ly.down); a.nseg = 1;
+        a.G = gshape(ly.down); a.y = E->hq; a.cols = nff; a.m = m;
         a.res_in = E->xB; a.res_out = E->xA; a.rscale = c.residual_scale;
-        SPX_HIP(launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
+        SPX_HIP(E->mq ? launch_dec_mq(a, std::min(a.tiles[0], 2 * E->n_cu), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
       }
     }
   }
@@ -592,11 +597,11 @@ int enqueue_pass_m(spx_engine *E, int m) {
     ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
     SPX_HIP(norm(E->xA, E->out_norm, E->xn, E->xq));
     DecMMArgs a{};
-    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.ld_out[0] = c.vocab; a.tiles[0] = mtiles(E->lm_head); a.nseg = 1;
+    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.ld_out[0] = c.vocab; a.tiles[0] = E->mq ? qtiles(E->lm_head) : mtiles(E->lm_head); a.nseg = 1;
     a.G = gshape(E->lm_head); a.y = E->xq; a.cols = dim; a.m = m;
-    grid = std::min(a.tiles[0], 512);
+    grid = std::min(a.tiles[0], E->mq ? 2 * E->n_cu : 512);
     a.best = E->best; a.nbest = grid; a.lscale = c.logit_scale;
-    SPX_HIP(launch_dec_mm(a, grid, s));
+    SPX_HIP(E->mq ? launch_dec_mq(a, grid, s) : launch_dec_mm(a, grid, s));
   }
   E->nbest = grid;
   {
@@ -825,6 +830,9 @@ int spx_engine_prepare(spx_engine *E) {
     if (gum_lds_bytes(MAX_M, (int)ly.gate->v.cols, ly.moe ? std::min(MAX_M * nu, c.n_expert) : 1) > 160 * 1024) E->dec_ok = false;
   }
   if (const char *v = std::getenv("SPX_DECODE")) E->dec_on = atoi(v) != 0;
+  if (const char *v = std::getenv("SPX_MQ")) E->mq = atoi(v) != 0;
+  if (const char *v = std::getenv("SPX_MQ_DOWN")) E->mq_down = atoi(v) != 0;
+  if (const char *v = std::getenv("SPX_MQ_GATEUP")) E->mq_gateup = atoi(v) != 0;
   E->prepared = true;
   return 0;
 }
@@ -843,6 +851,17 @@ int spx_engine_set_decode(spx_engine *E, int on) {
       if (E->graph[slot]) { (void)hipGraphExecDestroy(E->graph[slot]); E->graph[slot] = nullptr; }
   }
   E->dec_on = on != 0;
+  return 0;
+}
+
+int spx_engine_set_mfma(spx_engine *E, int on) {
+  if (!E) return fail("null engine");
+  if (E->mq != (on != 0)) {  // the captured multi-row graphs hold the other kernels: capture again
+    SPX_HIP(hipStreamSynchronize(E->ctx->stream));
+    for (int slot = 0; slot <= MAX_M; slot++)
+      if (E->graph[slot]) { (void)hipGraphExecDestroy(E->graph[slot]); E->graph[slot] = nullptr; }
+  }
+  E->mq = on != 0;
   return 0;
 }
 

@@ -229,6 +229,12 @@ class Engine:
         """One-token passes on the decode pipeline (True, the default) or the fused pass kernels."""
         check(lib.spx_engine_set_decode(self.h, int(on)))
 
+    def set_mfma(self, on):
+        """Passes of 2..16 rows on the int8 matrix cores (True, the default; block totals exact,
+        fp32 sums to rounding) or on the lane-exact dot chains (False: the same bits as one-row
+        passes)."""
+        check(lib.spx_engine_set_mfma(self.h, int(on)))
+
     def decode_pipeline(self):
         """True when one-token passes run on the decode pipeline."""
         v = C.c_int()

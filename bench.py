@@ -181,7 +181,8 @@ def main():
     ver_us = st["verify_us"] / max(1, st["verifies"])
     acc = st["accepted"] / max(1, st["verifies"])
     spec_tok_s = len(toks) / ((st["verify_us"] + st["step_us"]) / 1e6)
-    log(f"verify: {st['verifies']} passes of M<=9, {ver_us:.0f} us/pass, {acc:.2f} accepted/pass, "
+    rows = 1 + st["drafted"] / max(1, st["verifies"])  # a random-init model falls into short loops: short drafts
+    log(f"verify: {st['verifies']} passes of M<=9 (mean {rows:.2f} rows), {ver_us:.0f} us/pass, {acc:.2f} accepted/pass, "
         f"{st['steps']} plain steps, {spec_tok_s:.1f} tok/s end to end")
     # one M=9 pass timed alone (fixed draft of 8 copied tokens)
     ids = prompt[100:109]
@@ -193,6 +194,17 @@ def main():
     m9_us = (time.perf_counter() - t0) / 10 * 1e6
     ver_experts = eng.last_experts()
     ver_bytes = decode_bytes(cfg, specs, 1008, ver_experts)
+    # the same pass on the lane-exact kernels (the same bits as one-row passes)
+    eng.set_mfma(False)
+    for _ in range(3):
+        eng.forward(ids, 1000)
+    t0 = time.perf_counter()
+    for _ in range(10):
+        eng.forward(ids, 1000)
+    m9_exact_us = (time.perf_counter() - t0) / 10 * 1e6
+    eng.set_mfma(True)
+    log(f"M=9 pass: {m9_us:.0f} us on the matrix cores ({ver_bytes / m9_us / 1e3:.0f} GB/s), "
+        f"{m9_exact_us:.0f} us lane-exact")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -212,7 +224,8 @@ def main():
                    "prompt_tokens": args.prompt_len, "weights_gib": round(gib, 2)},
         "decode_gb_per_pass": round(dec_bytes / 1e9, 4), "decode_hbm_gbs": round(dec_bytes * tok_s / 1e9, 1),
         "decode_roofline_frac": round(dec_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
-        "verify_pass_us": round(ver_us, 1), "verify_m9_pass_us": round(m9_us, 1),
+        "verify_pass_us": round(ver_us, 1), "verify_mean_rows": round(rows, 2), "verify_m9_pass_us": round(m9_us, 1),
+        "verify_m9_pass_us_lane_exact": round(m9_exact_us, 1), "verify_m9_hbm_gbs": round(ver_bytes / m9_us / 1e3, 1),
         "verify_gb_per_pass": round(ver_bytes / 1e9, 4), "verify_unique_experts_per_layer": round(float(np.mean(ver_experts)), 1),
         "accepted_per_pass": round(acc, 3), "spec_tok_s": round(spec_tok_s, 2), "prefill_tok_s": round(len(prompt) / prefill_s, 1),
         "roofline": roof, "cpu_baseline": cpu,

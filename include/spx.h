@@ -118,9 +118,11 @@ int spx_engine_decode_pipeline(spx_engine *e, int *active);  /* *active = 1: the
 /* 1 (default): the pipeline's passes of 2..16 rows (the verify step of generate_reply
  * :4251-4348, and prefill) take their integer matvecs on the int8 matrix cores: per block the
  * exact integer totals of the reference's kernel (rows<B,T>, quant_q8k.rs:163-245), their fp32
- * sums to rounding (within 1e-4 of the lane-exact result; logits within 1e-3). 0: the lane-exact
- * dot chains, the same bits as one-row passes. No counterpart in the reference (a choice
- * between two implementations of its batched kernel). */
+ * sums to rounding (a matvec within ~1e-6 relative of the lane-exact result; a whole pass can
+ * differ more where that moves a downstream Q8_K code or a near-tied expert choice, and greedy
+ * picks only at near-ties). 0: the lane-exact dot chains, the same bits as one-row passes, so
+ * speculation reproduces plain greedy decoding bit for bit. No counterpart in the reference (a
+ * choice between two implementations of its batched kernel). */
 int spx_engine_set_mfma(spx_engine *e, int on);
 
 /* One pass of m <= 16 tokens at positions start_pos.. (forward_slice :3364-3552 for m == 1,

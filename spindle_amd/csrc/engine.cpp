@@ -61,8 +61,9 @@ struct spx_engine {
   int lm_dec_grid = 256;  // decode pipeline: LM head workgroups (SPX_LM_DEC_GRID), one per CU
   int n_cu = 256;         // compute units of the device
   bool mq = true;          // passes of 2..16 rows on the int8 matrix cores (SPX_MQ, spx_engine_set_mfma)
-  bool mq_down = false;    // also the routed experts' down projection (SPX_MQ_DOWN): about one row an expert,
-                           // so the MFMA's 16 columns idle and the per-lane dot kernel is faster
+  int mq_down_rows = 4;    // the routed experts' down projection on MFMA from this many rows (SPX_MQ_DOWN_ROWS):
+                           // a pass of fewer rows gives an expert about one row, the MFMA's 16 columns idle
+                           // and the per-lane dot kernel is faster
   bool mq_gateup = true;   // the gate/up projections (SPX_MQ_GATEUP)
   int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   std::map<std::string, spx_tensor *> mats;
@@ -573,7 +574,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
         DecDownMArgs da{ly.down->v, E->h, E->jobs, ly.njobs, E->yd, std::min(m * nu, c.n_expert)};
-        SPX_HIP(E->mq && E->mq_down ? launch_dec_down_mq(da, s) : launch_dec_down_m(da, s));
+        SPX_HIP(E->mq && m >= E->mq_down_rows ? launch_dec_down_mq(da, s) : launch_dec_down_m(da, s));
         combine = true;  // + weighted combine + residual in the next norm (xB -> xA)
       }
     } else {  // ffn_forward_multi (:616-646)
@@ -831,7 +832,7 @@ int spx_engine_prepare(spx_engine *E) {
   }
   if (const char *v = std::getenv("SPX_DECODE")) E->dec_on = atoi(v) != 0;
   if (const char *v = std::getenv("SPX_MQ")) E->mq = atoi(v) != 0;
-  if (const char *v = std::getenv("SPX_MQ_DOWN")) E->mq_down = atoi(v) != 0;
+  if (const char *v = std::getenv("SPX_MQ_DOWN_ROWS")) E->mq_down_rows = atoi(v);
   if (const char *v = std::getenv("SPX_MQ_GATEUP")) E->mq_gateup = atoi(v) != 0;
   E->prepared = true;
   return 0;

@@ -1340,6 +1340,41 @@ struct MqRows {
   __device__ __forceinline__ int operator()(int v) const { return r[v]; }
 };
 
+// The correction operands of the MFMA path, per (vector, 256-block) 12 words next to the Q8_K
+// image: the sixteen 16-element bsums split as bs = 64 hi + lo (lo = bs & 63, hi = bs >> 6:
+// |bs| <= 2032 keeps hi in int8), lo[16] then hi[16] (words 0-7, Q6_K groups), then the eight
+// 32-element sums (|.| <= 4064) split the same way, lo[8] then hi[8] (words 8-11, Q4_K
+// sub-blocks). The correction C = sum sc bs is then two MFMAs: D1 over lo and hi, D2 over hi
+// alone, C = D1 + 63 D2 (exact).
+constexpr int MQ_CW = 12;  // words a (vector, block)
+__host__ __device__ inline size_t mq_corr_bytes(int m, int cols) { return (size_t)m * (cols >> 8) * MQ_CW * 4; }
+__device__ __forceinline__ uint32_t mq_pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)(d & 255) << 24);
+}
+__device__ __forceinline__ void mq_corr_stage(int nq, const SPX_L int2 *lbs, SPX_L uint32_t *lc) {
+  for (int q = threadIdx.x; q < nq; q += blockDim.x) {
+    int bs[16];
+#pragma unroll
+    for (int i = 0; i < 8; i++) { const int2 v = lld<int2>(lbs + q * 8 + i); bs[2 * i] = v.x; bs[2 * i + 1] = v.y; }
+    uint32_t w[MQ_CW];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      w[i] = mq_pack4(bs[4 * i] & 63, bs[4 * i + 1] & 63, bs[4 * i + 2] & 63, bs[4 * i + 3] & 63);
+      w[4 + i] = mq_pack4(bs[4 * i] >> 6, bs[4 * i + 1] >> 6, bs[4 * i + 2] >> 6, bs[4 * i + 3] >> 6);
+    }
+    int s32[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) s32[i] = bs[2 * i] + bs[2 * i + 1];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      w[8 + i] = mq_pack4(s32[4 * i] & 63, s32[4 * i + 1] & 63, s32[4 * i + 2] & 63, s32[4 * i + 3] & 63);
+      w[10 + i] = mq_pack4(s32[4 * i] >> 6, s32[4 * i + 1] >> 6, s32[4 * i + 2] >> 6, s32[4 * i + 3] >> 6);
+    }
+#pragma unroll
+    for (int i = 0; i < MQ_CW; i += 4) lst<uint4>((SPX_L uint4 *)(lc + q * MQ_CW + i), make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]));
+  }
+}
+
 // The tile's vectors: the A operand's vector (lane & 15) and the D elements' vectors
 // 4 (lane >> 4) + t, as rows of the LDS Q8_K image (row 0 stands in past the last vector).
 struct MqVec {
@@ -1359,29 +1394,33 @@ __device__ __forceinline__ MqVec mq_vecs(int nv, VR vrow) {
 // Block b of the tile: acc / cr of matrix row lane & 15, vectors 4 (lane >> 4) + t.
 template <int T>
 __device__ __forceinline__ void mq_block(const MqRaw &r, const MqVec &vv, int nb, int b, const SPX_L uint32_t *lq,
-                                         const SPX_L float *ld, const SPX_L int2 *lbs, float (&acc)[4], float (&cr)[4]) {
+                                         const SPX_L float *ld, const SPX_L uint32_t *lc, float (&acc)[4], float (&cr)[4]) {
   const int k4 = (threadIdx.x & 63) >> 4;
-  const SPX_L uint32_t *yp = lq + (vv.a * nb + b) * 64 + 16 * k4;
-  auto Yw = [&](int i) { return vv.ain ? yp[i] : 0u; };
-  int P[4] = {0, 0, 0, 0}, C[4] = {0, 0, 0, 0};
+  // A rows past the vectors read vector 0's words: a row of A only reaches the same row of D,
+  // and those rows are never stored
+  const int va = vv.a * nb + b;
+  const SPX_L uint32_t *yp = lq + va * 64 + 16 * k4;
+  const uint4 y0 = lld<uint4>(yp), y1 = lld<uint4>(yp + 4), y2 = lld<uint4>(yp + 8), y3 = lld<uint4>(yp + 12);
+  const uint32_t Y[16] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w, y2.x, y2.y, y2.z, y2.w, y3.x, y3.y, y3.z, y3.w};
+  int P[4] = {0, 0, 0, 0};
+  mq_v4i C;
   if constexpr (T == T_Q4K) {
     const uint32_t CA[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, CB[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
     for (int s = 0; s < 8; s++) {
       const int c = s >> 1, h = s & 1;
-      const mq_v4i S = mq_mfma(Yw(s), Yw(8 + s), (CA[c] >> (4 * h)) & 0x0F0F0F0Fu, (CB[c] >> (4 * h)) & 0x0F0F0F0Fu);
+      const mq_v4i S = mq_mfma(Y[s], Y[8 + s], (CA[c] >> (4 * h)) & 0x0F0F0F0Fu, (CB[c] >> (4 * h)) & 0x0F0F0F0Fu);
       const int sc = mq_byte(r.s, s);
 #pragma unroll
       for (int t = 0; t < 4; t++) P[t] += __mul24(S[t], sc);
     }
+    // C = sum_s mn_s (bsum_2s + bsum_2s+1): K 0-7 the sums' lo, 8-15 their hi, against the mins
+    const uint2 cw = lld<uint2>(lc + va * MQ_CW + 8 + 2 * (k4 & 1));
+    const uint32_t a0 = k4 < 2 ? cw.x : 0u, a1 = k4 < 2 ? cw.y : 0u;
+    const mq_v4i D1 = mq_mfma(a0, a1, r.s.z, r.s.w);
+    const mq_v4i D2 = mq_mfma(k4 == 1 ? a0 : 0u, k4 == 1 ? a1 : 0u, r.s.z, r.s.w);
 #pragma unroll
-    for (int t = 0; t < 4; t++) {  // C = sum_s mn_s (bsum_2s + bsum_2s+1) of vector 4 k4 + t
-      const SPX_L int4 *bq = (const SPX_L int4 *)(lbs + (vv.d[t] * nb + b) * 8);
-      const int4 q0 = lld<int4>(bq), q1 = lld<int4>(bq + 1), q2 = lld<int4>(bq + 2), q3 = lld<int4>(bq + 3);
-      C[t] = __mul24(q0.x + q0.y, mq_byte(r.s, 8)) + __mul24(q0.z + q0.w, mq_byte(r.s, 9)) + __mul24(q1.x + q1.y, mq_byte(r.s, 10)) +
-             __mul24(q1.z + q1.w, mq_byte(r.s, 11)) + __mul24(q2.x + q2.y, mq_byte(r.s, 12)) + __mul24(q2.z + q2.w, mq_byte(r.s, 13)) +
-             __mul24(q3.x + q3.y, mq_byte(r.s, 14)) + __mul24(q3.z + q3.w, mq_byte(r.s, 15));
-    }
+    for (int t = 0; t < 4; t++) C[t] = D1[t] + 63 * D2[t];
     const float d = h2f(r.d), dm = h2f(r.d >> 16);
 #pragma unroll
     for (int t = 0; t < 4; t++) {
@@ -1389,33 +1428,28 @@ __device__ __forceinline__ void mq_block(const MqRaw &r, const MqVec &vv, int nb
       acc[t] = fmaf(d * xd, (float)P[t], acc[t]);
       cr[t] = cr[t] + (dm * xd) * (float)C[t];
     }
-  } else {  // T_Q6K: 16 groups of 16 (two MFMAs a sub-block, the other half's codes zero)
+  } else {  // T_Q6K: 16 groups of 16: per sub-block the group 2k alone (the other half's codes
+            // zero) and the whole sub-block, P += (s0 - s1) S0 + s1 S
     const uint32_t QA[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, QB[4] = {r.b.x, r.b.y, r.b.z, r.b.w}, QH[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+    const bool lo = k4 < 2;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
       const int h = k >> 2, m = k & 3;
       const uint32_t c0 = ((QA[2 * h + (m & 1)] >> (4 * (m >> 1))) & 0x0F0F0F0Fu) | (((QH[h] >> (2 * m)) & 0x03030303u) << 4);
       const uint32_t c1 = ((QB[2 * h + (m & 1)] >> (4 * (m >> 1))) & 0x0F0F0F0Fu) | (((QH[2 + h] >> (2 * m)) & 0x03030303u) << 4);
-      const bool lo = k4 < 2;
-      const uint32_t ya = Yw(k), yb = Yw(8 + k);
-      const mq_v4i S0 = mq_mfma(ya, yb, lo ? c0 : 0u, lo ? c1 : 0u);   // group 2k
-      const mq_v4i S1 = mq_mfma(ya, yb, lo ? 0u : c0, lo ? 0u : c1);   // group 2k + 1
-      const int s0 = mq_sbyte(r.s, 2 * k), s1 = mq_sbyte(r.s, 2 * k + 1);
+      const mq_v4i S0 = mq_mfma(Y[k], Y[8 + k], lo ? c0 : 0u, lo ? c1 : 0u);  // group 2k
+      const mq_v4i S = mq_mfma(Y[k], Y[8 + k], c0, c1);                       // groups 2k and 2k + 1
+      const int s0 = mq_sbyte(r.s, 2 * k), s1 = mq_sbyte(r.s, 2 * k + 1), ds = s0 - s1;
 #pragma unroll
-      for (int t = 0; t < 4; t++) P[t] += __mul24(S0[t], s0) + __mul24(S1[t], s1);
+      for (int t = 0; t < 4; t++) P[t] += __mul24(S0[t], ds) + __mul24(S[t], s1);
     }
+    // C = sum_g sc_g bsum_g: K 0-15 the bsums' lo, 16-31 their hi, against the scales
+    const uint2 cw = lld<uint2>(lc + va * MQ_CW + 2 * k4);
+    const uint32_t b0 = (k4 & 1) ? r.s.z : r.s.x, b1 = (k4 & 1) ? r.s.w : r.s.y;
+    const mq_v4i D1 = mq_mfma(cw.x, cw.y, b0, b1);
+    const mq_v4i D2 = mq_mfma(lo ? 0u : cw.x, lo ? 0u : cw.y, b0, b1);
 #pragma unroll
-    for (int t = 0; t < 4; t++) {  // C = sum_g sc_g bsum_g of vector 4 k4 + t
-      const SPX_L int4 *bq = (const SPX_L int4 *)(lbs + (vv.d[t] * nb + b) * 8);
-      int c = 0;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int4 q = lld<int4>(bq + i);
-        c += __mul24(q.x, mq_sbyte(r.s, 4 * i)) + __mul24(q.y, mq_sbyte(r.s, 4 * i + 1)) + __mul24(q.z, mq_sbyte(r.s, 4 * i + 2)) +
-             __mul24(q.w, mq_sbyte(r.s, 4 * i + 3));
-      }
-      C[t] = c;
-    }
+    for (int t = 0; t < 4; t++) C[t] = D1[t] + 63 * D2[t];
     const float d = h2f(r.d);
 #pragma unroll
     for (int t = 0; t < 4; t++) {
@@ -1428,12 +1462,12 @@ __device__ __forceinline__ void mq_block(const MqRaw &r, const MqVec &vv, int nb
 // Blocks b0, b0 + bstep, ... of a 16-row tile (matrix rows row0 .. row0 + nrows - 1, clamped).
 template <int T>
 __device__ __forceinline__ void mq_tile(const Planes &pl, int64_t row0, int nrows, int nb, int b0, int bstep, const MqVec &vv,
-                                        const SPX_L uint32_t *lq, const SPX_L float *ld, const SPX_L int2 *lbs, float (&acc)[4],
+                                        const SPX_L uint32_t *lq, const SPX_L float *ld, const SPX_L uint32_t *lc, float (&acc)[4],
                                         float (&cr)[4]) {
   for (int b = b0; b < nb; b += bstep) {
     MqRaw r;
     mq_load<T>(r, pl, row0, nrows, nb, b);
-    mq_block<T>(r, vv, nb, b, lq, ld, lbs, acc, cr);
+    mq_block<T>(r, vv, nb, b, lq, ld, lc, acc, cr);
   }
 }
 
@@ -1470,6 +1504,9 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, c16 = lane & 15;
   if (threadIdx.x < MAX_M) sbest[threadIdx.x] = 0;
   stage_q8<NW * 64>(a.y, (const int *)nullptr, m, cols, lq, ld, lbs);
+  SPX_L uint32_t *lc = (SPX_L uint32_t *)(smem + mm_act_bytes(m, cols));
+  __syncthreads();
+  mq_corr_stage(m * nb, lbs, lc);
   __syncthreads();
   int buf = 0;
   const MqVec vv = mq_vecs(m, MqIdentity{});
@@ -1484,10 +1521,10 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
       MqRaw r;
       if (w.dtype == T_Q4K) {
         mq_load<T_Q4K>(r, w.pl, p.row0, p.nrows, nb, b);
-        mq_block<T_Q4K>(r, vv, nb, b, lq, ld, lbs, acc, cr);
+        mq_block<T_Q4K>(r, vv, nb, b, lq, ld, lc, acc, cr);
       } else {
         mq_load<T_Q6K>(r, w.pl, p.row0, p.nrows, nb, b);
-        mq_block<T_Q6K>(r, vv, nb, b, lq, ld, lbs, acc, cr);
+        mq_block<T_Q6K>(r, vv, nb, b, lq, ld, lc, acc, cr);
       }
     }
 #pragma unroll
@@ -1548,6 +1585,10 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
     }
     st.put(m, cols, lq, ld, lbs);
   }
+  // the correction operands after the job table
+  SPX_L uint32_t *lc = (SPX_L uint32_t *)(smem + act + (((size_t)(a.rt.logits ? a.max_jobs : 1) * JR * 4 + 15) & ~(size_t)15));
+  __syncthreads();
+  mq_corr_stage(m * nb, lbs, lc);
   __syncthreads();
   const int n = TX * nj, G = gridDim.x;
   const int i0 = (int)((int64_t)blockIdx.x * n / G), i1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
@@ -1578,8 +1619,8 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
     const int j = i / TX, nv = sj[j * JR + 1];
     if (nbw > 0) {
       const MqVec vv = mq_vecs(nv, MqRows{sj + j * JR + 2});
-      if (u & 1) mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lbs, au, cu);
-      else mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lbs, ag, cg);
+      if (u & 1) mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lc, au, cu);
+      else mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lc, ag, cg);
     }
     if (un == 0) {  // item i complete
 #pragma unroll
@@ -1619,6 +1660,7 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_mq(const DecDownMArgs 
   SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
   SPX_L float *ld = (SPX_L float *)(smem + (((size_t)MAX_M * n_ff + 15) & ~(size_t)15));
   SPX_L int *lbs = (SPX_L int *)(smem + (((size_t)MAX_M * n_ff + 15) & ~(size_t)15) + (((size_t)MAX_M * nbh * 4 + 15) & ~(size_t)15));
+  SPX_L uint32_t *lc = (SPX_L uint32_t *)(smem + downm_lds_bytes(n_ff));
   const int n = TX * gld<int>(a.njobs);
   for (int it = blockIdx.x; it < n; it += gridDim.x) {
     const int j = it / TX, x = it - j * TX;
@@ -1649,11 +1691,13 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_mq(const DecDownMArgs 
       }
     }
     __syncthreads();
+    mq_corr_stage(nq, (const SPX_L int2 *)lbs, lc);
+    __syncthreads();
     const int64_t r0 = (int64_t)x * RW + wave * 16;
     if (r0 < dim) {
       const int nrows = (int)min((int64_t)16, dim - r0);
       float acc[4] = {0.f, 0.f, 0.f, 0.f}, cr[4] = {0.f, 0.f, 0.f, 0.f};
-      mq_tile<T>(a.w.pl, (int64_t)e * dim + r0, nrows, nbh, 0, 1, mq_vecs(nv, MqIdentity{}), lq, ld, (const SPX_L int2 *)lbs, acc, cr);
+      mq_tile<T>(a.w.pl, (int64_t)e * dim + r0, nrows, nbh, 0, 1, mq_vecs(nv, MqIdentity{}), lq, ld, lc, acc, cr);
       const int r = lane & 15;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
@@ -1822,7 +1866,7 @@ hipError_t launch_dec_mq(const DecMMArgs &a, int grid, hipStream_t s) {
   for (int i = 0; i < a.nseg; i++)
     if ((a.w[i].dtype != T_Q4K && a.w[i].dtype != T_Q6K) || a.w[i].nb != nb) return hipErrorInvalidValue;
   if (a.res_out && a.nseg != 1) return hipErrorInvalidValue;
-  const size_t sm = mm_act_bytes(a.m, a.cols);
+  const size_t sm = mm_act_bytes(a.m, a.cols) + mq_corr_bytes(a.m, a.cols);
   SPX_DLDS(kd_mq, sm);
   hipLaunchKernelGGL(kd_mq, dim3(grid), dim3(DEC_MM_NW * 64), sm, s, a);
   return hipGetLastError();
@@ -1836,7 +1880,8 @@ hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &args, int max_jobs, hipStr
       max_jobs > 512 || (a.rt.logits && (max_jobs > a.gate.n_expert || a.rt.m != a.m || a.rt.n_expert < 1 || a.rt.n_expert > 256 || a.rt.n_used < 1 ||
                                          a.rt.n_used > 32 || a.rt.n_used > a.rt.n_expert)))
     return hipErrorInvalidValue;
-  const size_t sm = mm_act_bytes(a.m, cols) + (size_t)(a.rt.logits ? max_jobs : 1) * (2 + 2 * MAX_M) * 4;
+  const size_t sm = mm_act_bytes(a.m, cols) + (((size_t)(a.rt.logits ? max_jobs : 1) * (2 + 2 * MAX_M) * 4 + 15) & ~(size_t)15) +
+                    mq_corr_bytes(a.m, cols);
   if (sm > 100 * 1024) return hipErrorInvalidValue;
   // two workgroups a CU (Q4_K: at most 128 registers a lane), all resident, so each routes once
   // and takes its items in turn
@@ -1852,7 +1897,7 @@ hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s) {
   if (a.w.cols % 256 || a.w.nb > 4 || a.max_jobs < 1 || a.max_jobs > 512 || a.max_jobs > a.w.n_expert || !a.h || !a.yd) return hipErrorInvalidValue;
   const int tx = (int)((a.w.rows + DEC_MM_NW * 16 - 1) / (DEC_MM_NW * 16));
   const dim3 grid((unsigned)std::min(tx * a.max_jobs, 2 * cu_count())), b(DEC_MM_NW * 64);
-  const size_t sm = downm_lds_bytes((int)a.w.cols);
+  const size_t sm = downm_lds_bytes((int)a.w.cols) + mq_corr_bytes(MAX_M, (int)a.w.cols);
   if (a.w.dtype == T_Q4K) hipLaunchKernelGGL((kd_down_mq<T_Q4K>), grid, b, sm, s, a);
   else if (a.w.dtype == T_Q6K) hipLaunchKernelGGL((kd_down_mq<T_Q6K>), grid, b, sm, s, a);
   else return hipErrorInvalidValue;

@@ -1883,10 +1883,14 @@ hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &args, int max_jobs, hipStr
   const size_t sm = mm_act_bytes(a.m, cols) + (((size_t)(a.rt.logits ? max_jobs : 1) * (2 + 2 * MAX_M) * 4 + 15) & ~(size_t)15) +
                     mq_corr_bytes(a.m, cols);
   if (sm > 100 * 1024) return hipErrorInvalidValue;
-  // two workgroups a CU (Q4_K: at most 128 registers a lane), all resident, so each routes once
-  // and takes its items in turn
+  // all workgroups resident (Q4_K: at most 128 registers a lane, two fit a CU), so each routes
+  // once and takes its items in turn. Every workgroup routes the pass, so a second one a CU
+  // pays off only while the items per workgroup are few: two a CU up to 12 rows, one above
+  // (Qwen3-30B-A3B, measured: M = 9 pass 3.78 vs 3.87 ms with one; 16-row prefill 3.5k vs
+  // 3.1k tok/s with one)
   const int items = ((a.n_ff + 15) / 16) * (a.rt.logits ? max_jobs : 1);
-  const dim3 grid((unsigned)std::min(items, (a.gate.dtype == T_Q4K ? 2 : 1) * cu_count())), b(DEC_MM_NW * 64);
+  const int gmax = (a.gate.dtype == T_Q4K && a.m <= 12 ? 2 : 1) * cu_count();
+  const dim3 grid((unsigned)std::min(items, gmax)), b(DEC_MM_NW * 64);
   if (a.gate.dtype == T_Q4K) { SPX_DLDS((kd_gateup_mq<T_Q4K>), sm); hipLaunchKernelGGL((kd_gateup_mq<T_Q4K>), grid, b, sm, s, a); }
   else if (a.gate.dtype == T_Q6K) { SPX_DLDS((kd_gateup_mq<T_Q6K>), sm); hipLaunchKernelGGL((kd_gateup_mq<T_Q6K>), grid, b, sm, s, a); }
   else return hipErrorInvalidValue;

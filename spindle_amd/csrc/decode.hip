@@ -1489,8 +1489,9 @@ __device__ __forceinline__ void mq_locate(const DecMMArgs &a, int total, MqPos &
 // formats may differ by segment), the m vectors' Q8_K staged in LDS; wavefront w of the
 // DEC_MM_NW takes blocks w, w + DEC_MM_NW, ... of each tile. The wavefronts' partials
 // (acc - corr) meet in LDS, two tiles' worth so one barrier a tile suffices, and wavefront
-// q < 4 adds row group q in wavefront order and runs the epilogue (residual, greedy keys) as
-// kd_mm does.
+// q < 4 adds accumulator q (matrix row lane & 15, vector 4 (lane >> 4) + q) in wavefront order
+// and runs the epilogue (residual, greedy keys) as kd_mm does. The correction operands are
+// staged next to the Q8_K image once.
 __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void kd_mq(const DecMMArgs a) {
   constexpr int NW = DEC_MM_NW;
   extern __shared__ __align__(16) uint8_t smem[];
@@ -1555,7 +1556,9 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
 
 // Routing + gate/up + SwiGLU over the jobs on the matrix cores (kd_gateup_m's prologue, job
 // list and item split; items are (job, 16 h rows)): wavefront w takes blocks w, w + 8, ... of
-// the item's gate and up tiles, the partial sums meet in LDS in wavefront order.
+// the item's gate and up tiles, alternating gate and up blocks with the next one's bytes
+// requested before the current one is multiplied; the partials (acc - corr) meet in LDS in
+// wavefront order, two items' worth, and wavefront q < 4 applies SwiGLU to accumulator q.
 template <int T>
 __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(T == T_Q4K ? 4 : 2))) void kd_gateup_mq(const DecGateUpMArgs a) {
   constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M;

@@ -75,6 +75,30 @@ def decode_bytes(cfg, specs, pos, experts_per_layer):
     return by
 
 
+def cpu_info(threads):
+    """Model name, sockets, physical cores of the host (and of the cores this process may use),
+    from /proc/cpuinfo and the sysfs topology."""
+    info = {"model": None, "sockets": None, "physical_cores": None, "threads_used": threads}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    info["model"] = line.split(":", 1)[1].strip()
+                    break
+        pkgs, cores = set(), set()
+        for c in sorted(os.sched_getaffinity(0)):
+            base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+            pk = open(base + "physical_package_id").read().strip()
+            co = open(base + "core_id").read().strip()
+            pkgs.add(pk)
+            cores.add((pk, co))
+        info["sockets"] = len(pkgs)
+        info["physical_cores"] = len(cores)
+    except OSError:
+        pass
+    return info
+
+
 def cpu_baseline(cfg, w, eng, tok, pos, seconds, threads):
     from oracle import ffi
     from oracle.model import OracleModel
@@ -94,6 +118,63 @@ def cpu_baseline(cfg, w, eng, tok, pos, seconds, threads):
     return n / el, n, el
 
 
+def time_pass(eng, ids, pos, reps=10):
+    """Mean wall time (us) of one pass of len(ids) rows at pos (graph replay, synchronised)."""
+    for _ in range(3):
+        eng.forward(ids, pos)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        eng.forward(ids, pos)
+    return (time.perf_counter() - t0) / reps * 1e6
+
+
+def prefill(eng, prompt, verbose=False):
+    t0 = time.perf_counter()
+    for s in range(0, len(prompt), 16):
+        am, _, _ = eng.forward(prompt[s:s + 16], s)
+        if verbose and s % 1024 == 0:
+            log(f"prefill {s + len(prompt[s:s + 16])}/{len(prompt)}")
+    return int(am[-1]), time.perf_counter() - t0
+
+
+def timed_decode(ctx, eng, tok, pos, warmup, steps):
+    out = eng.decode(tok, pos, warmup)
+    tok, pos = int(out[-1]), pos + warmup
+    ctx.sync()
+    t0 = time.perf_counter()
+    out = eng.decode(tok, pos, steps)
+    ctx.sync()
+    return steps / (time.perf_counter() - t0), int(out[-1]), pos + steps
+
+
+def small_config_leg(ctx, name, seed, prompt_len, spans, steps):
+    """decode tok/s at the config's context, one M=9 pass, and for the
+    repeated-span prompts the speculative generation (n-gram 3, k=8, fixed)."""
+    from spindle_amd import model as M
+    cfg = M.CONFIGS[name]
+    w = M.synth_model(cfg, seed)
+    eng = M.Engine(ctx, cfg, w)
+    prompt = spec_prompt(cfg.vocab, prompt_len, seed) if spans else \
+        np.random.default_rng(seed).integers(0, cfg.vocab, prompt_len).astype(np.int32)
+    tok, _ = prefill(eng, prompt)
+    tok_s, tok, pos = timed_decode(ctx, eng, tok, len(prompt), 4, steps)
+    by = decode_bytes(cfg, M.tensor_specs(cfg), pos - steps // 2,
+                      eng.last_experts() if cfg.moe else [0] * cfg.n_layers)
+    r = {"decode_tok_s": round(tok_s, 1), "decode_gb_per_pass": round(by / 1e9, 4),
+         "decode_roofline_frac": round(by * tok_s / 1e9 / HBM_PEAK_GBS, 4), "context": pos}
+    m9 = time_pass(eng, prompt[-9:], pos)
+    r["verify_m9_pass_us"] = round(m9, 1)
+    if spans:
+        toks, st = eng.generate(prompt, 128, draft_len=8, min_ngram=3, max_ngram=3, fixed=True,
+                                adaptive_k=False, n_cached=len(prompt) - 1)
+        r["spec_tok_s"] = round(len(toks) / ((st["verify_us"] + st["step_us"]) / 1e6), 1)
+        r["verify_pass_us"] = round(st["verify_us"] / max(1, st["verifies"]), 1)
+        r["accepted_per_pass"] = round(st["accepted"] / max(1, st["verifies"]), 3)
+    log(f"config {name}: {r}")
+    eng.close()
+    return r
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -106,6 +187,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-legs", action="store_true", help="skip the prune / diverse-routing / configs 1-4 legs")
     ap.add_argument("--seed", type=int, default=1)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -117,7 +199,7 @@ def main():
     from spindle_amd import ops
 
     cfg = M.get_config(args.config)
-    need = args.prompt_len + args.warmup + args.steps + args.profile_passes + 32
+    need = args.prompt_len + args.warmup + args.steps + args.profile_passes + 64
     if cfg.max_seq < need:
         cfg = cfg.replace(max_seq=need)
     specs = M.tensor_specs(cfg)
@@ -131,31 +213,28 @@ def main():
     log(f"uploaded in {time.perf_counter() - t0:.1f}s")
 
     prompt = spec_prompt(cfg.vocab, args.prompt_len, args.seed)
-    t0 = time.perf_counter()
-    pos = 0
-    for s in range(0, len(prompt), 16):
-        am, _, _ = eng.forward(prompt[s:s + 16], s)
-        pos = s + len(prompt[s:s + 16])
-        if s % 1024 == 0:
-            log(f"prefill {pos}/{len(prompt)}")
-    prefill_s = time.perf_counter() - t0
-    tok = int(am[-1])
+    tok, prefill_s = prefill(eng, prompt, verbose=True)
+    pos = len(prompt)
     log(f"prefill {len(prompt)} tokens in {prefill_s:.2f}s ({len(prompt) / prefill_s:.0f} tok/s, 16-row passes)")
 
-    # warmup, then the timed decode passes (each pass synchronises: the next token is its argmax)
-    out = eng.decode(tok, pos, args.warmup)
-    tok, pos = int(out[-1]), pos + args.warmup
-    ctx.sync()
-    t0 = time.perf_counter()
-    out = eng.decode(tok, pos, args.steps)
-    ctx.sync()
-    dt = time.perf_counter() - t0
-    tok_s = args.steps / dt
+    # CPU baseline from the KV state the GPU's timed decode starts from (read-only on the GPU)
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = min(args.cpu_threads, len(os.sched_getaffinity(0)))
+        cpu_tok_s, n_cpu, el = cpu_baseline(cfg, w, eng, tok, pos, args.cpu_seconds, threads)
+        ci = cpu_info(threads)
+        log(f"cpu baseline (oracle, {threads} threads on {ci}): {n_cpu} tokens in {el:.1f}s = {cpu_tok_s:.3f} tok/s")
+        cpu = {"value": round(cpu_tok_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"{n_cpu} greedy decode passes at positions {pos}..{pos + n_cpu - 1} from the KV state the GPU "
+                         f"decode starts from (same weights, C restatement of the reference's AVX2 kernels, {threads} threads)",
+               "cpu": ci}
+
+    # warmup, then the timed decode passes (back-to-back graph replays, picks fed forward on the device)
+    tok_s, tok, pos = timed_decode(ctx, eng, tok, pos, args.warmup, args.steps)
     experts = eng.last_experts()
-    dec_bytes = decode_bytes(cfg, specs, pos + args.steps // 2, experts)
-    log(f"decode: {args.steps} passes in {dt * 1e3:.1f} ms = {tok_s:.1f} tok/s, "
+    dec_bytes = decode_bytes(cfg, specs, pos - args.steps // 2, experts)
+    log(f"decode: {args.steps} passes = {tok_s:.1f} tok/s, "
         f"{dec_bytes / 1e9:.3f} GB/pass -> {dec_bytes * tok_s / 1e9:.0f} GB/s end to end")
-    tok, pos = int(out[-1]), pos + args.steps
 
     # per-kernel profile of eager decode passes (HIP events on the engine's stream)
     eng.profile(True)
@@ -175,45 +254,62 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(dom), "kernel": dom,
             "bytes_per_launch": round(by / n), "avg_launch_us": round(us / n, 3)}
 
-    # verify: prompt-lookup speculation, benchmark mode (n-gram 3, k = 8, fixed length)
+    # one M=9 verify pass at the decode context (past every position written so far): the
+    # prompt-lookup draft of the generated stream, on the int8 matrix cores and lane-exact
+    ids = np.concatenate([[tok], out[-8:]]).astype(np.int32) if len(out) >= 8 else prompt[-9:]
+    m9_pos = pos
+    m9_us = time_pass(eng, ids, m9_pos)
+    ver_experts = eng.last_experts()
+    ver_bytes = decode_bytes(cfg, specs, m9_pos + 8, ver_experts)
+    eng.set_mfma(False)
+    m9_exact_us = time_pass(eng, ids, m9_pos)
+    eng.set_mfma(True)
+    log(f"M=9 pass at position {m9_pos}: {m9_us:.0f} us on the matrix cores ({ver_bytes / m9_us / 1e3:.0f} GB/s, "
+        f"{np.mean(ver_experts):.1f} unique experts a layer), {m9_exact_us:.0f} us lane-exact")
+
+    # speculative generation, benchmark mode (n-gram 3, k = 8, fixed length), from the prefilled prompt
     toks, st = eng.generate(prompt, args.spec_tokens, draft_len=8, min_ngram=3, max_ngram=3, fixed=True,
-                            adaptive_k=False, prefill_chunk=16)
+                            adaptive_k=False, prefill_chunk=16, n_cached=len(prompt) - 1)
     ver_us = st["verify_us"] / max(1, st["verifies"])
     acc = st["accepted"] / max(1, st["verifies"])
     spec_tok_s = len(toks) / ((st["verify_us"] + st["step_us"]) / 1e6)
     rows = 1 + st["drafted"] / max(1, st["verifies"])  # a random-init model falls into short loops: short drafts
     log(f"verify: {st['verifies']} passes of M<=9 (mean {rows:.2f} rows), {ver_us:.0f} us/pass, {acc:.2f} accepted/pass, "
         f"{st['steps']} plain steps, {spec_tok_s:.1f} tok/s end to end")
-    # one M=9 pass timed alone (fixed draft of 8 copied tokens)
-    ids = prompt[100:109]
-    for _ in range(3):
-        eng.forward(ids, 1000)
-    t0 = time.perf_counter()
-    for _ in range(10):
-        eng.forward(ids, 1000)
-    m9_us = (time.perf_counter() - t0) / 10 * 1e6
-    ver_experts = eng.last_experts()
-    ver_bytes = decode_bytes(cfg, specs, 1008, ver_experts)
-    # the same pass on the lane-exact kernels (the same bits as one-row passes)
-    eng.set_mfma(False)
-    for _ in range(3):
-        eng.forward(ids, 1000)
-    t0 = time.perf_counter()
-    for _ in range(10):
-        eng.forward(ids, 1000)
-    m9_exact_us = (time.perf_counter() - t0) / 10 * 1e6
-    eng.set_mfma(True)
-    log(f"M=9 pass: {m9_us:.0f} us on the matrix cores ({ver_bytes / m9_us / 1e3:.0f} GB/s), "
-        f"{m9_exact_us:.0f} us lane-exact")
+    eng.close()
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        threads = min(args.cpu_threads, os.cpu_count() or 1)
-        cpu_tok_s, n_cpu, el = cpu_baseline(cfg, w, eng, tok, pos, args.cpu_seconds, threads)
-        log(f"cpu baseline (oracle, {threads} threads): {n_cpu} tokens in {el:.1f}s = {cpu_tok_s:.3f} tok/s")
-        cpu = {"value": round(cpu_tok_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": f"{n_cpu} greedy decode passes at positions {pos}..{pos + n_cpu - 1} from the GPU's KV cache "
-                         f"(same weights, C restatement of the reference's AVX2 kernels, {threads} threads)"}
+    legs = {}
+    if not args.no_legs and args.config == "qwen3-30b-a3b":
+        # moe_prune top-4 (the reference's optional variant, smollm_chat.rs:1221-1237)
+        e4 = M.Engine(ctx, cfg.replace(moe_prune=4.0), w)
+        tk, _ = prefill(e4, prompt)
+        p4_tok_s, tk, p4 = timed_decode(ctx, e4, tk, len(prompt), 4, 64)
+        b4 = decode_bytes(cfg, specs, p4 - 32, e4.last_experts())
+        m9p = time_pass(e4, prompt[-9:], p4)
+        legs["moe_prune_top4"] = {"decode_tok_s": round(p4_tok_s, 1), "decode_gb_per_pass": round(b4 / 1e9, 4),
+                                  "decode_roofline_frac": round(b4 * p4_tok_s / 1e9 / HBM_PEAK_GBS, 4),
+                                  "verify_m9_pass_us": round(m9p, 1)}
+        log(f"moe_prune top-4: {legs['moe_prune_top4']}")
+        e4.close()
+        # diverse routing: token embeddings scaled up so that each row's residual stream is its
+        # own and the 9 rows of a pass choose experts nearly independently (a random-init model
+        # otherwise drifts to a common hidden direction over a long context)
+        ed = M.Engine(ctx, cfg.replace(embedding_scale=40.0), w)
+        tk, _ = prefill(ed, prompt[:1024])
+        ids9 = np.random.default_rng(args.seed).integers(0, cfg.vocab, 9).astype(np.int32)
+        dv_us = time_pass(ed, ids9, 1024)
+        dv_exp = ed.last_experts()
+        dv_bytes = decode_bytes(cfg, specs, 1032, dv_exp)
+        legs["verify_m9_diverse_routing"] = {"pass_us": round(dv_us, 1), "unique_experts_per_layer": round(float(np.mean(dv_exp)), 1),
+                                             "gb_per_pass": round(dv_bytes / 1e9, 4), "hbm_gbs": round(dv_bytes / dv_us / 1e3, 1),
+                                             "context": 1033}
+        log(f"M=9 diverse routing: {legs['verify_m9_diverse_routing']}")
+        ed.close()
+        del w
+        for name, plen, spans in (("smollm2-135m", 32, False), ("qwen3-0.6b", 512, False),
+                                  ("granite-1b-a400m", 256, False)):
+            legs[name] = small_config_leg(ctx, name, args.seed, plen, spans, 64)
+        legs["qwen3-0.6b-spec"] = small_config_leg(ctx, "qwen3-0.6b", args.seed, 2048, True, 32)
 
     res = {
         "metric": "decode tok/s (Qwen3-30B-A3B Q4_K_M-shaped, 1 GPU); k=8 verify-pass us; HBM GB/s",
@@ -224,14 +320,14 @@ def main():
                    "prompt_tokens": args.prompt_len, "weights_gib": round(gib, 2)},
         "decode_gb_per_pass": round(dec_bytes / 1e9, 4), "decode_hbm_gbs": round(dec_bytes * tok_s / 1e9, 1),
         "decode_roofline_frac": round(dec_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
-        "verify_pass_us": round(ver_us, 1), "verify_mean_rows": round(rows, 2), "verify_m9_pass_us": round(m9_us, 1),
+        "verify_m9_pass_us": round(m9_us, 1), "verify_m9_position": m9_pos,
         "verify_m9_pass_us_lane_exact": round(m9_exact_us, 1), "verify_m9_hbm_gbs": round(ver_bytes / m9_us / 1e3, 1),
         "verify_gb_per_pass": round(ver_bytes / 1e9, 4), "verify_unique_experts_per_layer": round(float(np.mean(ver_experts)), 1),
+        "spec_verify_pass_us": round(ver_us, 1), "spec_verify_mean_rows": round(rows, 2),
         "accepted_per_pass": round(acc, 3), "spec_tok_s": round(spec_tok_s, 2), "prefill_tok_s": round(len(prompt) / prefill_s, 1),
-        "roofline": roof, "cpu_baseline": cpu,
+        "legs": legs, "roofline": roof, "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
-    eng.close()
     ctx.close()
 
 

@@ -166,6 +166,9 @@ typedef struct {
   int speculate;     /* 0: plain one-token decoding */
   int adaptive_k;    /* grow k after a fully accepted draft (:4343) */
   int prefill_chunk; /* prompt rows per pass, <= 16 */
+  int n_cached;      /* prompt tokens already in the KV cache at positions 0..n_cached-1 (a
+                        session's earlier turns, generate_reply's cur_pos): only the rest of the
+                        prompt is fed; 0 <= n_cached < n_prompt */
 } spx_gen_params;
 
 typedef struct {
@@ -174,7 +177,7 @@ typedef struct {
 } spx_gen_stats;
 
 /* Greedy generation with prompt-lookup speculation (generate_reply's loop :4205-4348 minus
- * chat framing, stop tokens ignored, repeat penalty 1): feeds the prompt from position 0,
+ * chat framing, stop tokens ignored, repeat penalty 1): feeds the prompt from position n_cached,
  * writes up to max_new tokens to out and returns how many. */
 int spx_engine_generate(spx_engine *e, const int32_t *prompt, int n_prompt, int max_new,
                         const spx_gen_params *params, int32_t *out, spx_gen_stats *stats);

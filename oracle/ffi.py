@@ -65,7 +65,7 @@ class SpecModel(C.Structure):
 
 
 class GenParams(C.Structure):
-    _fields_ = [(n, C.c_int) for n in ("draft_len", "min_ngram", "max_ngram", "fixed", "speculate", "adaptive_k", "prefill_chunk")]
+    _fields_ = [(n, C.c_int) for n in ("draft_len", "min_ngram", "max_ngram", "fixed", "speculate", "adaptive_k", "prefill_chunk", "n_cached")]
 
 
 class GenStats(C.Structure):
@@ -114,6 +114,7 @@ _sig("or_spec_record_step", None, C.POINTER(SpecModel), C.c_uint64)
 _sig("or_spec_record_verify", None, C.POINTER(SpecModel), C.c_int, C.c_uint64)
 _sig("or_generate", C.c_int, C.POINTER(Model), P, C.c_int, C.c_int, C.POINTER(GenParams), P, C.POINTER(GenStats))
 _sig("or_set_threads", None, C.c_int)
+_sig("or_set_norm_order", None, C.c_int)
 _sig("or_get_threads", C.c_int)
 
 
@@ -200,3 +201,8 @@ def matvec_multi(m, xs):
 
 def set_threads(n):
     lib.or_set_threads(n)
+
+
+def set_norm_order(gpu_order):
+    """Test knob: RMSNorm sums in the GPU kernels' order (True) or the reference's (False)."""
+    lib.or_set_norm_order(int(bool(gpu_order)))

@@ -35,6 +35,7 @@ static void *worker_main(void *arg) {
       if (++spins > 2000) sched_yield();
     }
     seen = atomic_load_explicit(&g_gen, memory_order_acquire);
+    if (t >= g_threads) continue; /* started by an earlier, larger or_set_threads: idle */
     g_job(g_ctx, t, g_threads);
     atomic_fetch_sub_explicit(&g_remaining, 1, memory_order_acq_rel);
   }
@@ -565,16 +566,66 @@ int or_matvec_multi(const or_mat *m, int nvec, const float *const *xs, float *co
 }
 
 /* ------------------------------------------------------------------ small ops */
+/* Test knob (never on by default): g_norm_order = 1 sums the RMSNorm squares in the order the
+ * GPU kernels use instead of the reference's sequential order, to measure how far a last-bit
+ * difference in one norm carries through a whole model (tests/test_gpu_configs.py). Per
+ * 256-value block, value group j = x[4j..4j+3] gives fma(x3,x3,fma(x2,x2,fma(x1,x1,x0*x0))),
+ * the 64 groups are added in a pairwise tree in index order, the blocks in order; a head of
+ * hd <= 128 values gives fma(a,a,b*b) per pair (a, b) = the RoPE pair, then the same tree. */
+static int g_norm_order = 0;
+void or_set_norm_order(int gpu_order) { g_norm_order = gpu_order; }
+static float tree64(float p[64]) {
+  for (int w = 1; w < 64; w *= 2)
+    for (int i = 0; i < 64; i += 2 * w) p[i] = p[i] + p[i + w];
+  return p[0];
+}
+static float sumsq_blocks(const float *x, size_t n) {
+  float S = 0.0f;
+  for (size_t b = 0; b < n / 256; b++) {
+    float p[64];
+    for (int j = 0; j < 64; j++) {
+      const float *v = x + 256 * b + 4 * j;
+      float t = v[0] * v[0];
+      t = fmaf(v[1], v[1], t);
+      t = fmaf(v[2], v[2], t);
+      t = fmaf(v[3], v[3], t);
+      p[j] = t;
+    }
+    S = S + tree64(p);
+  }
+  return S;
+}
+static float sumsq_head(const float *x, size_t hd, int neox) {
+  float p[64];
+  size_t half = hd / 2;
+  for (int j = 0; j < 64; j++) {
+    if ((size_t)j < half) {
+      float a = x[neox ? (size_t)j : 2 * (size_t)j], b = x[neox ? j + half : 2 * (size_t)j + 1];
+      p[j] = fmaf(a, a, b * b);
+    } else p[j] = 0.0f;
+  }
+  return tree64(p);
+}
 void or_rmsnorm(const float *x, const float *w, float *out, size_t n, float eps) { /* :569-575 */
   float ss = 0.0f;
-  for (size_t i = 0; i < n; i++) ss += x[i] * x[i];
+  if (g_norm_order && n % 256 == 0) ss = sumsq_blocks(x, n);
+  else for (size_t i = 0; i < n; i++) ss += x[i] * x[i];
   float inv = 1.0f / sqrtf(ss / (float)n + eps);
   for (size_t i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
 }
-void or_rmsnorm_heads(float *v, const float *w, size_t len, size_t hd, float eps) { /* :577-584 */
+static void rmsnorm_heads_neox(float *v, const float *w, size_t len, size_t hd, float eps, int neox) {
   float *tmp = malloc(sizeof(float) * hd);
-  for (size_t h = 0; h + hd <= len; h += hd) { or_rmsnorm(v + h, w, tmp, hd, eps); memcpy(v + h, tmp, hd * 4); }
+  for (size_t h = 0; h + hd <= len; h += hd) {
+    if (g_norm_order && hd <= 128) {
+      float inv = 1.0f / sqrtf(sumsq_head(v + h, hd, neox) / (float)hd + eps);
+      for (size_t i = 0; i < hd; i++) tmp[i] = v[h + i] * inv * w[i];
+    } else or_rmsnorm(v + h, w, tmp, hd, eps);
+    memcpy(v + h, tmp, hd * 4);
+  }
   free(tmp);
+}
+void or_rmsnorm_heads(float *v, const float *w, size_t len, size_t hd, float eps) { /* :577-584 */
+  rmsnorm_heads_neox(v, w, len, hd, eps, 1);
 }
 float or_silu(float x) { return x / (1.0f + expf(-x)); } /* :586-588 */
 
@@ -782,8 +833,8 @@ static void qkv_post(or_model *m, const or_layer *ly, int layer, int pos, float 
   const or_config *c = &m->c;
   int q_dim = c->n_heads * c->head_dim, kv_dim = c->n_kv_heads * c->head_dim;
   add_bias(q, ly->q_bias, q_dim); add_bias(k, ly->k_bias, kv_dim); add_bias(v, ly->v_bias, kv_dim);
-  if (ly->q_norm) { int nn = ly->qk_norm_full ? q_dim : c->head_dim; or_rmsnorm_heads(q, ly->q_norm, q_dim, nn, c->rms_eps); }
-  if (ly->k_norm) { int nn = ly->qk_norm_full ? kv_dim : c->head_dim; or_rmsnorm_heads(k, ly->k_norm, kv_dim, nn, c->rms_eps); }
+  if (ly->q_norm) { int nn = ly->qk_norm_full ? q_dim : c->head_dim; rmsnorm_heads_neox(q, ly->q_norm, q_dim, nn, c->rms_eps, c->rope_neox); }
+  if (ly->k_norm) { int nn = ly->qk_norm_full ? kv_dim : c->head_dim; rmsnorm_heads_neox(k, ly->k_norm, kv_dim, nn, c->rms_eps, c->rope_neox); }
   or_rope_rotate(m->inv_freq, c->rope_neox, q, q_dim, c->head_dim, (float)pos);
   or_rope_rotate(m->inv_freq, c->rope_neox, k, kv_dim, c->head_dim, (float)pos);
   size_t off = ((size_t)layer * c->max_seq + pos) * kv_dim;
@@ -982,12 +1033,12 @@ int or_generate(or_model *m, const int *prompt, int n_prompt, int max_new, const
   int *corpus = malloc(sizeof(int) * (CORPUS_MAX + n_prompt + 64)), nc = 0;
   float *hid = malloc(sizeof(float) * dim * 17), *logits = malloc(sizeof(float) * (size_t)vocab * 17);
   memset(st, 0, sizeof *st);
-  if (n_prompt + max_new + 16 > c->max_seq) return -1;
+  if (n_prompt + max_new + 16 > c->max_seq || p->n_cached < 0 || p->n_cached >= n_prompt) return -1;
   remember(corpus, &nc, prompt, n_prompt);
-  int pos = 0;
+  int pos = p->n_cached;
   /* feed :3041-3104 (chunks; a chunk of one token goes through forward_slice) */
   float *hbuf = malloc(sizeof(float) * (size_t)dim * chunk);
-  for (int s = 0; s < n_prompt; s += chunk) {
+  for (int s = p->n_cached; s < n_prompt; s += chunk) {
     int cnt = n_prompt - s < chunk ? n_prompt - s : chunk;
     if (or_forward_batch(m, prompt + s, cnt, pos, hbuf)) return -1;
     memcpy(hid, hbuf + (size_t)(cnt - 1) * dim, 4 * dim);

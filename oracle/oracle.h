@@ -171,6 +171,7 @@ typedef struct {
   int speculate;   /* 0: plain decode */
   int adaptive_k;  /* k_dyn growth after full accepts (:4343) */
   int prefill_chunk;
+  int n_cached;    /* prompt tokens already in the KV cache (positions 0..n_cached-1) */
 } or_gen_params;
 
 typedef struct { int accepted, drafted, verifies, steps; } or_gen_stats;
@@ -181,6 +182,8 @@ int or_generate(or_model *m, const int *prompt, int n_prompt, int max_new,
                 const or_gen_params *p, int *out, or_gen_stats *st);
 
 void or_set_threads(int n);
+/* Test knob, off by default: 1 = RMSNorm sums in the GPU kernels' order (sensitivity tests). */
+void or_set_norm_order(int gpu_order);
 int or_get_threads(void);
 
 #ifdef __cplusplus

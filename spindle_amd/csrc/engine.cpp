@@ -1092,20 +1092,21 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
   if (n_prompt < 1 || max_new < 1) return fail("spx_engine_generate: empty prompt or max_new < 1");
   if (n_prompt + max_new + MAX_M > E->c.max_seq) return fail("spx_engine_generate: prompt + max_new exceeds max_seq");
   if (p->speculate && (p->draft_len < 1 || p->draft_len > MAX_M - 1)) return fail("spx_engine_generate: draft_len must be in 1..15");
+  if (p->n_cached < 0 || p->n_cached >= n_prompt) return fail("spx_engine_generate: n_cached must be in 0..n_prompt-1");
   memset(st, 0, sizeof(*st));
   std::vector<int32_t> corpus;
   remember(corpus, prompt, n_prompt);
   const int chunk = std::min(MAX_M, p->prefill_chunk > 0 ? p->prefill_chunk : MAX_M);
-  int pos = 0;
+  int pos = p->n_cached;
   int32_t am[MAX_M];
   int64_t t0 = now_us();
-  for (int s = 0; s < n_prompt; s += chunk) {  // feed (:3041-3104)
+  for (int s = p->n_cached; s < n_prompt; s += chunk) {  // feed (:3041-3104)
     const int cnt = std::min(chunk, n_prompt - s);
     if (int r = spx_engine_forward(E, prompt + s, cnt, pos, nullptr, nullptr, am)) return r;
     pos += cnt;
   }
   st->prefill_us = (double)(now_us() - t0);
-  const int last_rows = n_prompt - ((n_prompt - 1) / chunk) * chunk;  // rows in the last chunk
+  const int last_rows = n_prompt - p->n_cached - ((n_prompt - p->n_cached - 1) / chunk) * chunk;  // rows in the last chunk
   int tok = am[last_rows - 1];
   int gen = 0, backoff = 0, skip = 0, k_dyn = p->draft_len;
   SpecModel sm;

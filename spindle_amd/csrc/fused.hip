@@ -976,12 +976,9 @@ template <int HD> struct AttnLds {
   static_assert(QB >= (size_t)16 * HD * 4, "merged output fits over the queries");
 };
 
-// Sub-chunks per chunk: one when one query tile covers the pass (decode: most chunks, most
-// parallelism); otherwise enough that a kv head has at most 16 chunks (one merge level).
-__host__ __device__ inline int attn_sub(int nq, int total) {
-  const int nsc = (total + 63) >> 6;
-  return nq <= 16 ? 1 : (nsc + ATT_GRP - 1) / ATT_GRP;
-}
+// Chunks are 64 positions for every pass size and query tile, merged in chunk order in the
+// same two levels (groups of ATT_GRP chunks, then the groups) as a one-row pass's kd_merge:
+// a query's partials, and so its output bits, do not depend on how many rows the pass has.
 
 template <int HD, bool MERGE>
 __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *st) {
@@ -994,7 +991,8 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
   const int m = st->m, start = st->start, total = start + m;
   const int g = a.n_heads / a.n_kv, NQ = m * g, qa = qt * 16;
   if (qa >= NQ) return;
-  const int SUB = attn_sub(NQ, total), CS = 64 * SUB, nch = (total + CS - 1) / CS;
+  constexpr int CS = 64;
+  const int nch = (total + CS - 1) / CS;
   if (c >= nch) return;
   const int p_lo = c * CS, p_hi = min(p_lo + CS, total);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -1827,10 +1825,7 @@ template <int HD>
 static void launch_attn_t(const AttnArgs &a, int nqt, const StepRec *st, hipStream_t s) {
   const size_t sm = AttnLds<HD>::BYTES;
   SPX_LDS((k_attn<HD, true>), sm);
-  // more than one query tile: at most ATT_GRP chunks a kv head (attn_sub), so no workgroups
-  // past them are launched
-  const int nc = nqt > 1 ? std::min(a.nch, ATT_GRP) : a.nch;
-  hipLaunchKernelGGL((k_attn<HD, true>), dim3(nc, a.n_kv, nqt), dim3(256), sm, s, a, st);
+  hipLaunchKernelGGL((k_attn<HD, true>), dim3(a.nch, a.n_kv, nqt), dim3(256), sm, s, a, st);
 }
 
 hipError_t launch_attention_partials(const AttnArgs &a, const StepRec *st, hipStream_t s) {

@@ -117,6 +117,12 @@ TINY = {
                                  rope_theta=1e6, rms_eps=1e-6, qk_norm=True, n_expert=16, n_expert_used=4,
                                  tied=False, t_embd=Q4K, t_q=Q4K, t_k=Q4K, t_v=Q6K, t_o=Q4K, t_gate=Q4K,
                                  t_up=Q4K, t_down=Q6K, t_out=Q6K),
+    # the headline kernels' shapes at small width: head_dim 128, 8 query heads a kv head, 128
+    # experts top-8 (Qwen3-30B-A3B's attention tiles and routing), a context past 16 chunks
+    "tiny-a3b": ModelConfig("tiny-a3b", "qwen3moe", 512, 2, 16, 2, 128, 256, 1000, max_seq=1280,
+                            rope_theta=1e6, rms_eps=1e-6, qk_norm=True, n_expert=128, n_expert_used=8,
+                            tied=False, t_embd=Q4K, t_q=Q4K, t_k=Q4K, t_v=Q6K, t_o=Q4K, t_gate=Q4K,
+                            t_up=Q4K, t_down=Q6K, t_out=Q6K),
 }
 
 
@@ -194,7 +200,7 @@ class ModelConfigC(C.Structure):
 
 
 class GenParams(C.Structure):
-    _fields_ = [(n, C.c_int) for n in ("draft_len", "min_ngram", "max_ngram", "fixed", "speculate", "adaptive_k", "prefill_chunk")]
+    _fields_ = [(n, C.c_int) for n in ("draft_len", "min_ngram", "max_ngram", "fixed", "speculate", "adaptive_k", "prefill_chunk", "n_cached")]
 
 
 class GenStats(C.Structure):
@@ -260,10 +266,10 @@ class Engine:
         return self.forward(ids, start_pos, hidden=True)[1]
 
     def generate(self, prompt, max_new, draft_len=8, min_ngram=2, max_ngram=4, fixed=False, speculate=True,
-                 adaptive_k=True, prefill_chunk=16):
+                 adaptive_k=True, prefill_chunk=16, n_cached=0):
         prompt = np.ascontiguousarray(prompt, np.int32)
         out = np.empty(max_new, np.int32)
-        gp = GenParams(draft_len, min_ngram, max_ngram, int(fixed), int(speculate), int(adaptive_k), prefill_chunk)
+        gp = GenParams(draft_len, min_ngram, max_ngram, int(fixed), int(speculate), int(adaptive_k), prefill_chunk, n_cached)
         st = GenStats()
         n = lib.spx_engine_generate(self.h, prompt.ctypes.data_as(P), prompt.size, max_new, C.byref(gp),
                                     out.ctypes.data_as(P), C.byref(st))

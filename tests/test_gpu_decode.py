@@ -20,7 +20,12 @@ CASES = {
     "moe-prune2": M.TINY["tiny-qwen3moe"].replace(sigma=0.05, moe_prune=2.0),
     "moe-prune-mass": M.TINY["tiny-qwen3moe"].replace(sigma=0.05, moe_prune=0.3),
     "dense-kquant": M.TINY["tiny-qwen3"].replace(sigma=0.05, **KQ),
+    # Qwen3-30B-A3B's kernel shapes: head_dim 128, hpk 8, 128 experts top-8, moe_prune off / top-4 / mass
+    "a3b": M.TINY["tiny-a3b"].replace(sigma=0.05),
+    "a3b-prune4": M.TINY["tiny-a3b"].replace(sigma=0.05, moe_prune=4.0),
+    "a3b-prune-mass": M.TINY["tiny-a3b"].replace(sigma=0.05, moe_prune=0.1),
 }
+LONG = ("moe", "a3b")  # contexts past 16 chunks (two-level merge) and past position 1024
 
 
 @pytest.fixture(scope="module")
@@ -52,7 +57,7 @@ def test_decode_pipeline_bitwise(ctx, case):
     """One-token passes at contexts of one chunk, several 64-position chunks and (for the MoE
     case) more than 16 chunks, where the merge runs in two levels."""
     cfg = CASES[case]
-    long_ctx = case == "moe"
+    long_ctx = case in LONG
     if long_ctx:
         cfg = cfg.replace(max_seq=1280)
     w = M.synth_model(cfg, seed=31)
@@ -129,18 +134,21 @@ def test_toggle_recaptures_graphs(ctx):
     eng.close()
 
 
-@pytest.mark.parametrize("case", ["moe", "dense-kquant"])
+@pytest.mark.parametrize("case", list(CASES))
 def test_decode_pipeline_matches_oracle(ctx, case):
-    """Teacher-forced: the oracle gets the GPU's KV cache before each one-token pass."""
+    """Teacher-forced: the oracle gets the GPU's KV cache before each one-token pass (for the
+    headline-shaped family also at positions past 1024, 17+ attention chunks)."""
     cfg = CASES[case]
     w = M.synth_model(cfg, seed=34)
     eng = M.Engine(ctx, cfg, w)
     assert eng.decode_pipeline()
     om = OracleModel(cfg, w)
-    ids = np.random.default_rng(6).integers(0, cfg.vocab, 48)
-    eng.forward(ids[:16], 0)
+    n_pre = 1100 if case in LONG and cfg.max_seq >= 1280 else 16
+    ids = np.random.default_rng(6).integers(0, cfg.vocab, n_pre + 32)
+    for s0 in range(0, n_pre, 16):
+        eng.forward(ids[s0:min(s0 + 16, n_pre)], s0)
     errs, flips = [], 0
-    for pos in range(16, len(ids)):
+    for pos in range(n_pre, len(ids)):
         k, v = eng.kv_cache()
         om.k_cache[:] = k
         om.v_cache[:] = v
@@ -193,7 +201,7 @@ def _margin(logits):
     return top[1] - top[0]
 
 
-@pytest.mark.parametrize("case", list(CASES))
+@pytest.mark.parametrize("case", [c for c in CASES if CASES[c].n_expert <= 64])
 def test_multi_row_passes_mfma(ctx, case):
     """Passes of 2..16 rows on the int8 matrix cores against the lane-exact kernels, pass by pass
     on one engine (each pass is run both ways over the same KV cache, the lane-exact run last).

@@ -15,7 +15,7 @@ from oracle.model import OracleModel
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
-FAMILIES = ["tiny-llama", "tiny-qwen3", "tiny-granite", "tiny-qwen3moe", "tiny-q5k"]
+FAMILIES = ["tiny-llama", "tiny-qwen3", "tiny-granite", "tiny-qwen3moe", "tiny-q5k", "tiny-a3b"]
 
 
 @pytest.fixture(scope="module")
@@ -93,6 +93,29 @@ def test_batch_equals_sequential_bitwise(ctx, name):
         _, hs, ls = b.forward(ids[4 + i:5 + i], 4 + i, hidden=True, logits=True)
         assert np.array_equal(hs[0].view(np.uint32), hb[i].view(np.uint32)), (name, i)
         assert np.array_equal(ls[0].view(np.uint32), lb[i].view(np.uint32)), (name, i)
+
+
+@pytest.mark.parametrize("name", ["tiny-a3b", "tiny-qwen3", "tiny-qwen3moe"])
+def test_batch_equals_sequential_long_context(ctx, name):
+    """Past 1024 positions (17+ attention chunks, two merge levels) a verify pass of 9 rows,
+    whose queries span several 16-query tiles, still gives each row the bits of its one-row
+    pass: the chunking and merge order do not depend on the pass size."""
+    cfg = M.TINY[name].replace(sigma=0.05, max_seq=1280)
+    w = M.synth_model(cfg, seed=16)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    a.set_mfma(False)
+    b.set_mfma(False)
+    ids = np.random.default_rng(3).integers(0, cfg.vocab, 1120)
+    for s0 in range(0, 1100, 16):
+        a.forward(ids[s0:min(s0 + 16, 1100)], s0)
+        b.forward(ids[s0:min(s0 + 16, 1100)], s0)
+    _, hb, lb = a.forward(ids[1100:1109], 1100, hidden=True, logits=True)
+    for i in range(9):
+        _, hs, ls = b.forward(ids[1100 + i:1101 + i], 1100 + i, hidden=True, logits=True)
+        assert np.array_equal(hs[0].view(np.uint32), hb[i].view(np.uint32)), (name, i)
+        assert np.array_equal(ls[0].view(np.uint32), lb[i].view(np.uint32)), (name, i)
+    a.close()
+    b.close()
 
 
 SHAPES = {"tiles at decode": {"SPX_MV_MODE": "0"}, "standalone norms": {"SPX_TAIL_MAX": "0"},

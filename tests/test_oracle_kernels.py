@@ -172,3 +172,18 @@ def test_q8_0_single_and_multi_orders_differ_but_agree():
     for o in (one, multi):
         assert np.all(np.abs(o - want) <= 1e-4 * scale)
     assert not np.array_equal(one, multi)
+
+
+def test_pool_shrink_keeps_results():
+    """Lowering the oracle's thread count after a larger one leaves the extra workers idle: the
+    row split changes, the results (rows are independent) do not."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(1024).astype(np.float32)
+    raw = rng.integers(0, 256, 34 * 32 * 300).astype(np.uint8)
+    raw.reshape(-1, 34)[:, 1] = 0x1C  # finite f16 scales
+    m = ffi.mat(ffi.Q8_0, raw, 300, 1024)
+    outs = []
+    for t in (8, 2, 5, 1):
+        ffi.set_threads(t)
+        outs.append(ffi.matvec(m, x))
+    assert all(np.array_equal(outs[0].view(np.uint32), o.view(np.uint32)) for o in outs[1:])

@@ -85,6 +85,63 @@ def test_rmsnorm_matches_float64():
         assert np.max(np.abs(out - want)) <= 1e-5 * np.max(np.abs(want))
 
 
+def test_rmsnorm_sums_in_sequence():
+    """rmsnorm (smollm_chat.rs:569-575) sums x*x with Iterator::sum, one f32 add at a time in
+    index order: the oracle's result equals that sequence bit for bit."""
+    rng = np.random.default_rng(4)
+    for n in (576, 2048):
+        x = (rng.standard_normal(n) * np.exp(rng.uniform(-3, 3, n))).astype(np.float32)
+        w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        ss = np.float32(0.0)
+        for v in x:
+            ss = np.float32(ss + np.float32(v * v))
+        inv = np.float32(1.0) / np.sqrt(np.float32(ss / np.float32(n) + np.float32(1e-5)))
+        want = (x * inv).astype(np.float32) * w
+        out = np.zeros(n, np.float32)
+        rmsnorm(_p(x), _p(w), _p(out), n, 1e-5)
+        assert np.array_equal(out.view(np.uint32), want.astype(np.float32).view(np.uint32)), n
+
+
+def _fma32(a, b, c):
+    from fractions import Fraction
+    return np.float32(float(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))))
+
+
+def test_norm_order_knob_is_the_gpu_tree():
+    """The sensitivity knob (ffi.set_norm_order): per 256-value block the four-value fma chain
+    of each group, a pairwise tree over the 64 groups in index order, the blocks in order; off
+    again, the reference's sequence."""
+    from oracle import ffi
+    rng = np.random.default_rng(5)
+    n = 512
+    x = (rng.standard_normal(n) * np.exp(rng.uniform(-4, 4, n))).astype(np.float32)
+    w = np.ones(n, np.float32)
+    S = np.float32(0.0)
+    for b in range(n // 256):
+        p = []
+        for j in range(64):
+            v = x[256 * b + 4 * j: 256 * b + 4 * j + 4]
+            t = np.float32(v[0] * v[0])
+            for k in (1, 2, 3):
+                t = _fma32(v[k], v[k], t)
+            p.append(t)
+        while len(p) > 1:
+            p = [np.float32(p[i] + p[i + 1]) for i in range(0, len(p), 2)]
+        S = np.float32(S + p[0])
+    inv = np.float32(1.0) / np.sqrt(np.float32(S / np.float32(n) + np.float32(1e-5)))
+    want = ((x * inv).astype(np.float32) * w).astype(np.float32)
+    out = np.zeros(n, np.float32)
+    ffi.set_norm_order(True)
+    try:
+        rmsnorm(_p(x), _p(w), _p(out), n, 1e-5)
+    finally:
+        ffi.set_norm_order(False)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
+    seq = np.zeros(n, np.float32)
+    rmsnorm(_p(x), _p(w), _p(seq), n, 1e-5)
+    assert np.max(np.abs(seq - out)) <= 1e-5 * np.max(np.abs(out))  # the two orders: last bits only
+
+
 def _xorshift_floats(seed, n):
     """The reference tests' generator (smollm_chat.rs:4894-4903): xorshift64, (s>>40)/2^24 - 0.5."""
     out = np.empty(n, np.float32)

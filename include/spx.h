@@ -124,6 +124,14 @@ int spx_engine_decode_pipeline(spx_engine *e, int *active);  /* *active = 1: the
  * speculation reproduces plain greedy decoding bit for bit. No counterpart in the reference (a
  * choice between two implementations of its batched kernel). */
 int spx_engine_set_mfma(spx_engine *e, int on);
+/* One-row passes (decode) with each layer as one cooperative launch of co-resident workgroups
+ * whose phases meet at device-wide barriers (the persistent pass, for Q4_K_M-format models with
+ * head_dim 64 or 128): the same bits as the decode pipeline's kernels. Off by default (slower
+ * than the pipeline as measured); set_persist(1) selects it where the model fits.
+ * persist_active reports whether one-row passes take it. No counterpart in the reference,
+ * whose passes are CPU loops (forward_slice smollm_chat.rs:3364-3552). */
+int spx_engine_set_persist(spx_engine *e, int on);
+int spx_engine_persist_active(spx_engine *e, int *active);
 
 /* One pass of m <= 16 tokens at positions start_pos.. (forward_slice :3364-3552 for m == 1,
  * forward_batch_slice :3142-3362 for m > 1, then compute_logits_batch :3588-3602 and the

@@ -36,6 +36,8 @@ SIGNATURES = {
     "spx_engine_set_decode": (C.c_int, [P, C.c_int]),
     "spx_engine_decode_pipeline": (C.c_int, [P, C.POINTER(C.c_int)]),
     "spx_engine_set_mfma": (C.c_int, [P, C.c_int]),
+    "spx_engine_set_persist": (C.c_int, [P, C.c_int]),
+    "spx_engine_persist_active": (C.c_int, [P, C.POINTER(C.c_int)]),
     "spx_engine_forward": (C.c_int, [P, P, C.c_int, C.c_int, P, P, P]),
     "spx_engine_last_experts": (C.c_int, [P, P]),
     "spx_engine_debug_read": (C.c_int, [P, C.c_char_p, P, I64]),

@@ -95,6 +95,8 @@ __device__ __forceinline__ rsrc_t rsrc_of(const void *base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
 }
 __device__ __forceinline__ f4v ld_coh4(rsrc_t r, int off) { return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16)); }
+__device__ __forceinline__ float ld_coh1(rsrc_t r, int off) { return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 16)); }
+__device__ __forceinline__ void st_coh1(rsrc_t r, int off, float v) { __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(v), r, off, 0, 16); }
 __device__ __forceinline__ f2v ld_coh2(rsrc_t r, int off) { return __builtin_bit_cast(f2v, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 16)); }
 __device__ __forceinline__ void st_coh4(rsrc_t r, int off, f4v v) { __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, v), r, off, 0, 16); }
 __device__ __forceinline__ void st_coh2(rsrc_t r, int off, f2v v) { __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2v, v), r, off, 0, 16); }

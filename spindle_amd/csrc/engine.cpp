@@ -23,6 +23,7 @@
 #include "decode.h"
 #include "fused.h"
 #include "internal.h"
+#include "persist.h"
 
 using namespace spx;
 
@@ -74,6 +75,14 @@ struct spx_engine {
   const float *out_norm = nullptr;
   bool prepared = false, use_graphs = true;
   bool dec_ok = false, dec_on = true;  // one-row passes on the decode pipeline (decode.hip)
+  // one-row passes with their layers as cooperative launches (persist.hip), where the model
+  // fits its tiles; off by default: measured slower than the pipeline (SPX_PERSIST=1 or
+  // spx_engine_set_persist turns it on)
+  bool persist_ok = false, persist_on = false;
+  int persist_grid_n = 0;
+  PersistArgs pa{};
+  std::vector<PLayer> players;  // the layers' tensors, passed to each layer's launch
+  int *perr_host = nullptr;  // pinned: the launch's error word, copied back with the pick
   std::vector<void *> allocs;
   // device state
   __half *kc = nullptr, *vc = nullptr;
@@ -612,11 +621,66 @@ int enqueue_pass_m(spx_engine *E, int m) {
   return 0;
 }
 
+// A one-row pass with its layers as cooperative launches of the persistent kernel (barrier
+// counters zeroed first) between the decode pipeline's embedding and its LM head and pick.
+int enqueue_persist(spx_engine *E, bool advance) {
+  const auto &c = E->c;
+  hipStream_t s = E->ctx->stream;
+  {
+    ProfScope ps(E, PC_EMBED, 0);
+    NormTail t{};
+    t.x = E->xA;
+    t.dim = c.dim;
+    SPX_HIP(launch_embed(E->embed->v, E->st_dev, c.embedding_scale, t, 1, s));
+  }
+  SPX_HIP(hipMemsetAsync(E->pa.bar, 0, PERSIST_BAR_WORDS * sizeof(unsigned), s));
+  unsigned epoch = 0;
+  for (int l = 0; l < c.n_layers; l++) {
+    SPX_HIP(launch_persist_layer(E->pa, E->players[l], l, epoch, E->persist_grid_n, s));
+    epoch += persist_layer_barriers(E->L[l].moe);
+  }
+  int grid = 1;
+  {
+    ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
+    auto tiles = [](const spx_tensor *t) { int G, R; rp_shape(t->v.nb, G, R); return (int)((t->v.rows + DEC_MV_NW * R - 1) / (DEC_MV_NW * R)); };
+    DecMVArgs a{};
+    int G, R;
+    rp_shape(E->lm_head->v.nb, G, R);
+    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.tiles[0] = tiles(E->lm_head); a.nseg = 1; a.G = G;
+    a.in = DecIn{E->xA, E->out_norm, c.rms_eps, c.dim};
+    a.best = E->best; a.lscale = c.logit_scale; a.xn_out = E->xn;
+    grid = std::min(a.tiles[0], E->lm_dec_grid);
+    SPX_HIP(launch_dec_mv(a, grid, s));
+  }
+  E->nbest = grid;
+  {
+    ProfScope ps(E, PC_ARGMAX, 0);
+    SPX_HIP(launch_argmax_final(E->best, grid, E->amax, E->st_dev, advance ? E->hist : nullptr, 1, s));
+  }
+  return 0;
+}
+
+bool persist_used(const spx_engine *E, int m) {
+  return m == 1 && E->dec_ok && E->dec_on && E->persist_ok && E->persist_on && !E->profiling;
+}
+
+// After a synchronised pass on the persistent kernel: a barrier that timed out voids the pass;
+// the engine then falls back to the decode pipeline for good.
+int persist_check(spx_engine *E) {
+  if (*E->perr_host == 0) return 0;
+  *E->perr_host = 0;
+  (void)hipMemset(E->pa.err, 0, sizeof(int));
+  E->persist_ok = false;
+  return fail("persistent decode pass: a device-wide barrier timed out, the pass is void; one-row passes run on the decode "
+              "pipeline from now on");
+}
+
 // Graph slot m (1..16): a pass of m rows; slot 0: a one-row decode pass that advances the
 // step record itself (back-to-back greedy decoding without host round trips).
 int run_forward(spx_engine *E, int m, bool advance = false) {
   hipStream_t s = E->ctx->stream;
   const bool dec = E->dec_ok && E->dec_on;
+  if (persist_used(E, m)) return enqueue_persist(E, advance);
   auto enqueue = [&]() { return !dec ? enqueue_forward(E, m, advance) : m == 1 ? enqueue_decode(E, advance) : enqueue_pass_m(E, m); };
   if (!E->use_graphs || E->profiling) return enqueue();
   const int slot = advance ? 0 : m;
@@ -830,6 +894,44 @@ int spx_engine_prepare(spx_engine *E) {
     if (ly.moe && (ly.down->v.nb > 4 || downm_lds_bytes((int)ly.down->v.cols) > 64 * 1024)) E->dec_ok = false;
     if (gum_lds_bytes(MAX_M, (int)ly.gate->v.cols, ly.moe ? std::min(MAX_M * nu, c.n_expert) : 1) > 160 * 1024) E->dec_ok = false;
   }
+  if (E->dec_ok) {  // the persistent decode pass: per-layer tensor table, barrier words
+    std::vector<PLayer> pl(c.n_layers);
+    for (int l = 0; l < c.n_layers; l++) {
+      const LayerW &ly = E->L[l];
+      PLayer &d = pl[l];
+      d.wq = ly.wq->v; d.wk = ly.wk->v; d.wv = ly.wv->v; d.wo = ly.wo->v;
+      d.gate = ly.gate->v; d.up = ly.up->v; d.down = ly.down->v;
+      if (ly.router) d.router = ly.router->v;
+      d.attn_norm = ly.attn_norm; d.ffn_norm = ly.ffn_norm; d.q_norm = ly.q_norm; d.k_norm = ly.k_norm;
+      d.q_bias = ly.q_bias; d.k_bias = ly.k_bias; d.v_bias = ly.v_bias;
+      d.moe = ly.moe ? 1 : 0;
+      d.njobs = ly.njobs;
+      d.expert_count = ly.moe ? E->expert_count + (size_t)l * c.n_expert : nullptr;
+    }
+    E->players = pl;
+    unsigned *bar = E->dalloc<unsigned>(PERSIST_BAR_WORDS);
+    int *err = E->dalloc<int>(1);
+    if (!bar || !err) return fail("out of device memory");
+    SPX_HIP(hipHostMalloc(&E->perr_host, sizeof(int)));
+    *E->perr_host = 0;
+    PersistArgs &a = E->pa;
+    a.n_layers = c.n_layers; a.lm_head = E->lm_head->v; a.out_norm = E->out_norm;
+    a.dim = c.dim; a.q_dim = E->q_dim; a.kv_dim = E->kv_dim; a.hd = c.head_dim; a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads;
+    a.n_ff = E->n_ff; a.n_expert = c.n_expert; a.n_used = nu; a.expert_norm = c.expert_norm; a.moe_prune = c.moe_prune;
+    a.eps = c.rms_eps; a.rscale = c.residual_scale; a.lscale = c.logit_scale;
+    a.attn_scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)c.head_dim);
+    a.neox = c.rope_neox; a.max_seq = c.max_seq; a.nch = E->nch; a.nslot = E->nch + ATT_GMAX;
+    a.xa = E->xA; a.xb = E->xB; a.q = E->q; a.k = E->k; a.v = E->v; a.att = E->att; a.h = E->h; a.rlog = E->rlog;
+    a.logits = E->logits; a.xn = E->xn; a.part_ml = E->part_ml; a.part_o = E->part_o; a.kc = E->kc; a.vc = E->vc; a.rope = E->rope;
+    a.best = E->best; a.chosen = E->chosen; a.nkeep = E->nkeep; a.weights = E->weights; a.st = E->st_dev; a.hist = E->hist;
+    a.amax = E->amax; a.bar = bar; a.err = err;
+    E->persist_grid_n = persist_grid(c.head_dim, E->n_cu);
+    bool uniform = true;  // one feed-forward width for every layer
+    for (auto &ly : E->L) uniform = uniform && ly.gate->v.rows == E->n_ff;
+    E->persist_ok = uniform && E->persist_grid_n > 0 && persist_fits(a, E->persist_grid_n);
+  }
+  if (const char *v = std::getenv("SPX_PERSIST")) E->persist_on = atoi(v) != 0;
+  if (std::getenv("SPX_PERSIST_TSTAMP") && E->dec_ok) E->pa.tstamp = E->dalloc<uint64_t>(4096);
   if (const char *v = std::getenv("SPX_DECODE")) E->dec_on = atoi(v) != 0;
   if (const char *v = std::getenv("SPX_MQ")) E->mq = atoi(v) != 0;
   if (const char *v = std::getenv("SPX_MQ_DOWN_ROWS")) E->mq_down_rows = atoi(v);
@@ -873,6 +975,18 @@ int spx_engine_decode_pipeline(spx_engine *E, int *active) {
   return 0;
 }
 
+int spx_engine_set_persist(spx_engine *E, int on) {
+  if (!E) return fail("null engine");
+  E->persist_on = on != 0;
+  return 0;
+}
+
+int spx_engine_persist_active(spx_engine *E, int *active) {
+  if (!E || !active) return fail("null argument");
+  *active = E->dec_ok && E->dec_on && E->persist_ok && E->persist_on ? 1 : 0;
+  return 0;
+}
+
 int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, float *hidden, float *logits, int32_t *argmax) {
   if (!E || !ids) return fail("spx_engine_forward: null argument");
   if (!E->prepared) return fail("spx_engine_forward: call spx_engine_prepare first");
@@ -892,7 +1006,11 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
   if (hidden) SPX_HIP(hipMemcpyAsync(hidden, E->xn, sizeof(float) * m * E->c.dim, hipMemcpyDeviceToHost, s));
   if (logits) SPX_HIP(hipMemcpyAsync(logits, E->logits, sizeof(float) * m * E->c.vocab, hipMemcpyDeviceToHost, s));
   if (argmax) SPX_HIP(hipMemcpyAsync(argmax, E->amax, sizeof(int) * m, hipMemcpyDeviceToHost, s));
+  const bool pers = persist_used(E, m);
+  if (pers) SPX_HIP(hipMemcpyAsync(E->perr_host, E->pa.err, sizeof(int), hipMemcpyDeviceToHost, s));
   SPX_HIP(hipStreamSynchronize(s));
+  if (pers)
+    if (int r = persist_check(E)) return r;
   if (E->profiling && !E->prof.empty()) {
     std::vector<int32_t> nj(E->c.n_layers, 0);
     for (int l = 0; l < E->c.n_layers; l++)
@@ -956,17 +1074,21 @@ int spx_engine_decode(spx_engine *E, int32_t token, int start_pos, int n, int32_
   E->st_host->ids[0] = token;
   E->st_host->step = 0;
   SPX_HIP(hipMemcpyAsync(E->st_dev, E->st_host, sizeof(StepRec), hipMemcpyHostToDevice, s));
+  const bool pers = persist_used(E, 1);
   for (int i = 0; i < n; i++)
     if (int r = run_forward(E, 1, true)) return r;
   SPX_HIP(hipMemcpyAsync(out, E->hist, sizeof(int32_t) * n, hipMemcpyDeviceToHost, s));
+  if (pers) SPX_HIP(hipMemcpyAsync(E->perr_host, E->pa.err, sizeof(int), hipMemcpyDeviceToHost, s));
   SPX_HIP(hipStreamSynchronize(s));
+  if (pers)
+    if (int r = persist_check(E)) return r;
   return 0;
 }
 
 int spx_engine_debug_read(spx_engine *E, const char *what, void *host, int64_t bytes) {
   if (!E || !what || !host) return fail("null argument");
   const std::string w(what);
-  const void *src = w == "x" ? (const void *)E->xA : w == "xn" ? (const void *)E->xn : w == "q" ? (const void *)E->q : w == "k" ? (const void *)E->k : w == "v" ? (const void *)E->v
+  const void *src = w == "tstamp" ? (const void *)E->pa.tstamp : w == "x" ? (const void *)E->xA : w == "xn" ? (const void *)E->xn : w == "q" ? (const void *)E->q : w == "k" ? (const void *)E->k : w == "v" ? (const void *)E->v
                   : w == "att" ? (const void *)E->att : w == "proj" ? (const void *)E->proj : w == "rlog" ? (const void *)E->rlog
                   : w == "chosen" ? (const void *)E->chosen : w == "weights" ? (const void *)E->weights
                   : w == "nkeep" ? (const void *)E->nkeep : w == "h" ? (const void *)E->h : w == "y" ? (const void *)E->ffn : nullptr;
@@ -1180,6 +1302,7 @@ int spx_engine_destroy(spx_engine *E) {
   for (auto &kv : E->mats) spx_tensor_free(E->ctx, kv.second);
   for (void *p : E->allocs) (void)hipFree(p);
   if (E->st_host) (void)hipHostFree(E->st_host);
+  if (E->perr_host) (void)hipHostFree(E->perr_host);
   delete E;
   return 0;
 }

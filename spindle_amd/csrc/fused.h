@@ -157,7 +157,7 @@ int mv_wgs(int64_t rows, int mt, int mode, int dtype, int R);
 
 // Row-parallel shape for rows of nb blocks: G lane groups per row (the smallest power of two
 // >= nb, at most 8), R = 8 / G rows per wavefront.
-inline void rp_shape(int64_t nb, int &G, int &R) {
+__host__ __device__ inline void rp_shape(int64_t nb, int &G, int &R) {
   G = 1;
   while (G < nb && G < 8) G *= 2;
   R = 8 / G;

@@ -241,6 +241,17 @@ class Engine:
         passes)."""
         check(lib.spx_engine_set_mfma(self.h, int(on)))
 
+    def set_persist(self, on):
+        """One-row passes with each layer as one cooperative launch (True; where the model fits
+        it) or as the decode pipeline's kernel sequence (False, the default); the same bits."""
+        check(lib.spx_engine_set_persist(self.h, int(on)))
+
+    def persist_active(self):
+        """True when one-row passes run as the persistent pass."""
+        v = C.c_int()
+        check(lib.spx_engine_persist_active(self.h, C.byref(v)))
+        return bool(v.value)
+
     def decode_pipeline(self):
         """True when one-token passes run on the decode pipeline."""
         v = C.c_int()

@@ -234,3 +234,51 @@ def test_multi_row_passes_mfma(ctx, case):
     assert np.median(errs) <= 1e-5
     assert big <= len(errs) // 2
     e.close()
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_persistent_pass_bitwise(ctx, case):
+    """One-row passes with their layers as cooperative launches (persist.hip) against the decode
+    pipeline's kernel sequence: the same bits for hidden state, logits, pick, KV cache rows and
+    routing statistics, at contexts of one chunk, several, and (long cases) past 16 chunks."""
+    cfg = CASES[case]
+    long_ctx = case in LONG
+    if long_ctx:
+        cfg = cfg.replace(max_seq=1280)
+    w = M.synth_model(cfg, seed=36)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    a.set_mfma(False)
+    b.set_mfma(False)
+    a.set_persist(True)
+    assert a.persist_active(), case
+    b.set_persist(False)
+    assert not b.persist_active() and b.decode_pipeline()
+    rng = np.random.default_rng(8)
+    n_pre = 1100 if long_ctx else 150
+    ids = rng.integers(0, cfg.vocab, n_pre + 40)
+    checkpoints = [16, 70, 140] + ([1090] if long_ctx else [])
+    pos = 0
+    for cp in checkpoints:
+        while pos < cp:
+            m = min(16, cp - pos)
+            a.forward(ids[pos:pos + m], pos)
+            b.forward(ids[pos:pos + m], pos)
+            pos += m
+        for _ in range(3):
+            am0, h0, l0 = a.forward(ids[pos:pos + 1], pos, hidden=True, logits=True)
+            am1, h1, l1 = b.forward(ids[pos:pos + 1], pos, hidden=True, logits=True)
+            assert _same(h0, h1), (case, pos, "hidden")
+            assert _same(l0, l1), (case, pos, "logits")
+            assert np.array_equal(am0, am1), (case, pos)
+            if cfg.moe:
+                assert np.array_equal(a.last_experts(), b.last_experts()), (case, pos)
+            pos += 1
+    # back-to-back decoding (the pick feeds the next pass on the device)
+    got = a.decode(int(ids[pos]), pos, 12)
+    want = b.decode(int(ids[pos]), pos, 12)
+    assert got.tolist() == want.tolist(), case
+    ka, va = a.kv_cache()
+    kb, vb = b.kv_cache()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    a.close()
+    b.close()

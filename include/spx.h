@@ -72,6 +72,17 @@ int spx_block_sums_q8k(spx_ctx *ctx, const spx_tensor *w, int expert, int64_t ro
 int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, int64_t ld_x, int m,
                float *out, int64_t ld_out);
 
+/* spx_matvec without any allocation: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference. The Q8_K staging of K-quant activations lives in a fixed device array of
+ * SPX_NOALLOC_SCRATCH_BYTES per device (m * cols up to 786432 codes, e.g. 16 vectors of 49152
+ * columns); larger requests are rejected with an error. Float formats need no staging. The array
+ * is shared by every call on a device and fully rewritten by each call before use, so calls on
+ * one device must not overlap (concurrent calls race). Same results, bit for bit, as spx_matvec. */
+#define SPX_NOALLOC_SCRATCH_BYTES (1u << 20)
+int spx_matvec_noalloc(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, int64_t ld_x,
+                       int m, float *out, int64_t ld_out);
+
 /* ------------------------------------------------------------------ synthetic weights */
 /* Seeded synthetic tensor in GGUF block layout (n_expert slabs of rows x cols). kind 0:
  * quantized weights (Q4_K/Q6_K/Q8_0/Q5_0) whose dequantised values have std sigma; kind 1:

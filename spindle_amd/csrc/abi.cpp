@@ -57,6 +57,24 @@ void *ws_get(spx_ctx *ctx, size_t bytes) {
   return ctx->ws;
 }
 
+// Fixed scratch for spx_matvec_noalloc: the permuted Q8_K image of its activations. Each device
+// the library runs on holds one copy until the process ends; every call on that device shares
+// it (calls that overlap on one device race).
+static __device__ __align__(256) uint8_t g_noalloc_scratch[SPX_NOALLOC_SCRATCH_BYTES];
+
+// Layout of m permuted Q8_K vectors of n columns in one buffer (codes, d, bsum pairs; each
+// region 256-byte aligned); total bytes in *bytes.
+static Q8KP q8kp_layout(uint8_t *base, int m, int64_t n, size_t *bytes) {
+  const int64_t nb = n / 256;
+  const size_t qb = ((size_t)m * n + 255) & ~(size_t)255, db = ((size_t)m * nb * 4 + 255) & ~(size_t)255;
+  *bytes = qb + db + (size_t)m * nb * 64;
+  Q8KP r{};
+  r.q = reinterpret_cast<uint32_t *>(base);
+  r.d = reinterpret_cast<float *>(base + qb);
+  r.bs = reinterpret_cast<int2 *>(base + qb + db);
+  return r;
+}
+
 // Field records of one GGUF block: (offset in block, length, plane).
 struct Field { int off, len, plane; };
 static int fields_of(int dtype, Field *f) {
@@ -143,6 +161,13 @@ int spx_create(int device, spx_ctx **out) {
   c->device = device;
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) { delete c; return hip_fail(e, "hipStreamCreate"); }
+  // this device's address of the fixed scratch array (the host-side name is not a device address)
+  e = hipGetSymbolAddress(reinterpret_cast<void **>(&c->scratch), HIP_SYMBOL(g_noalloc_scratch));
+  if (e != hipSuccess) {
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return hip_fail(e, "hipGetSymbolAddress(scratch)");
+  }
   *out = c;
   return 0;
 }
@@ -274,16 +299,12 @@ static int check_kq(const spx_tensor *w, int expert, int m) {
 
 // Workspace image of m permuted Q8_K vectors of n columns.
 static Q8KP ws_q8kp(spx_ctx *ctx, int m, int64_t n, bool *ok) {
-  const int64_t nb = n / 256;
-  const size_t qb = ((size_t)m * n + 255) & ~(size_t)255, db = ((size_t)m * nb * 4 + 255) & ~(size_t)255;
-  uint8_t *w = static_cast<uint8_t *>(ws_get(ctx, qb + db + (size_t)m * nb * 64));
-  Q8KP r{};
+  size_t bytes = 0;
+  (void)q8kp_layout(nullptr, m, n, &bytes);
+  uint8_t *w = static_cast<uint8_t *>(ws_get(ctx, bytes));
   *ok = w != nullptr;
-  if (!w) return r;
-  r.q = reinterpret_cast<uint32_t *>(w);
-  r.d = reinterpret_cast<float *>(w + qb);
-  r.bs = reinterpret_cast<int2 *>(w + qb + db);
-  return r;
+  if (!w) return Q8KP{};
+  return q8kp_layout(w, m, n, &bytes);
 }
 
 // Launch mode: row-parallel for integer weights, eight rows per wavefront for the float
@@ -356,6 +377,29 @@ int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, in
   if (w->v.dtype == T_F32 && cols % 16) return fail("spx_matvec: F32 needs cols % 16 == 0");
   if (w->v.dtype != T_Q8_0 && w->v.dtype != T_Q5_0 && w->v.dtype != T_Q5K && w->v.dtype != T_F32)
     return fail("spx_matvec: unsupported dtype " + std::to_string(w->v.dtype));
+  return mv_launch(ctx, w, expert, m, x, ld_x, Q8KP{}, out, ld_out, 0, rows);
+}
+
+int spx_matvec_noalloc(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, int64_t ld_x, int m, float *out, int64_t ld_out) {
+  if (!ctx || !w || !x || !out) return fail("spx_matvec_noalloc: null argument");
+  if (m < 1 || m > 16) return fail("spx_matvec_noalloc: m must be in 1..16");
+  if (expert < 0 || expert >= w->v.n_expert) return fail("spx_matvec_noalloc: expert index out of range");
+  const int64_t cols = w->v.cols, rows = w->v.rows;
+  if (ld_x < cols || (m > 1 && ld_out < rows)) return fail("spx_matvec_noalloc: leading dimension too small");
+  if (ld_x % 4) return fail("spx_matvec_noalloc: ld_x must be a multiple of 4 (16-byte rows)");
+  if (w->v.dtype == T_Q4K || w->v.dtype == T_Q6K) {
+    if (!ctx->scratch) return fail("spx_matvec_noalloc: the scratch array has no device address in this context");
+    size_t bytes = 0;
+    const Q8KP y = q8kp_layout(ctx->scratch, m, cols, &bytes);
+    if (bytes > SPX_NOALLOC_SCRATCH_BYTES)
+      return fail("spx_matvec_noalloc: m x cols needs " + std::to_string(bytes) + " bytes of Q8_K staging, above the fixed scratch of " +
+                  std::to_string(SPX_NOALLOC_SCRATCH_BYTES) + " (use spx_matvec)");
+    SPX_HIP(launch_q8kp_quantize(x, cols, ld_x, m, y, ctx->stream));
+    return mv_launch(ctx, w, expert, m, nullptr, 0, y, out, ld_out, 0, rows);
+  }
+  if (w->v.dtype == T_F32 && cols % 16) return fail("spx_matvec_noalloc: F32 needs cols % 16 == 0");
+  if (w->v.dtype != T_Q8_0 && w->v.dtype != T_Q5_0 && w->v.dtype != T_Q5K && w->v.dtype != T_F32)
+    return fail("spx_matvec_noalloc: unsupported dtype " + std::to_string(w->v.dtype));
   return mv_launch(ctx, w, expert, m, x, ld_x, Q8KP{}, out, ld_out, 0, rows);
 }
 

@@ -19,6 +19,7 @@ struct spx_ctx {
   hipStream_t stream = nullptr;
   void *ws = nullptr;      // grow-only workspace for internal Q8_K staging
   size_t ws_bytes = 0;
+  uint8_t *scratch = nullptr;  // this device's copy of the fixed scratch array (spx_matvec_noalloc)
 };
 
 namespace spx {

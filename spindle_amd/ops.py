@@ -132,4 +132,16 @@ def matvec(ctx, w, x, expert=0):
     return out
 
 
+def matvec_noalloc(ctx, w, x, expert=0):
+    """matvec through spx_matvec_noalloc: the K-quant activations' Q8_K staged in the library's
+    fixed per-device scratch array instead of an allocated workspace (same results)."""
+    x = x.contiguous()
+    m = x.shape[0]
+    out = torch.empty((m, w.rows), dtype=torch.float32, device=x.device)
+    torch.cuda.synchronize()
+    check(lib.spx_matvec_noalloc(ctx.h, w.h, expert, _p(x), x.shape[1], m, _p(out), w.rows))
+    ctx.sync()
+    return out
+
+
 matvec_multi = matvec

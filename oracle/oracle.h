@@ -30,9 +30,14 @@
  *   or_moe_* ........................... loop reference smollm_chat.rs:4936-4973 (1e-4)
  *   or_lookup_draft / or_spec_* ........ hand-built corpora / the reference test
  *                                         smollm_chat.rs:4667-4694
- *   or_forward_* ....................... batched == sequential on all-K-quant models
- *                                         (bitwise, the reference's qwen3_moe_batch_is_bitwise
- *                                         property) and a float64 numpy forward (tolerance)
+ *   or_forward_* ....................... a float64 numpy forward restated from the formulas
+ *                                         (tests/test_oracle_forward.py: GQA hpk 1/3/8, hd 64/128,
+ *                                         both RoPE layouts, QK-norm, Granite scales, pruning;
+ *                                         a planted head-mapping mistake must fail), and batched
+ *                                         == sequential on all-K-quant models (bitwise)
+ *   MoE routing / pruning .............. hand-derived choice lists for both pruning rules and
+ *                                         for exact ties (tests/test_oracle_ops.py)
+ *   or_argmax .......................... last maximum under total order, -0/+0, NaN, scale
  * Parity unpinned at the bit level (no reference build exists here: no Rust toolchain):
  *   the exact fp32 bits of expf/sinf/cosf/powf (Rust's libm vs glibc), and the order of
  *   exactly tied router probabilities (select_nth_unstable_by is implementation-defined).

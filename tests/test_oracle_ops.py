@@ -27,6 +27,7 @@ rope_rotate = _f("or_rope_rotate", None, fp, C.c_int, fp, C.c_size_t, C.c_size_t
 rmsnorm = _f("or_rmsnorm", None, fp, fp, fp, C.c_size_t, C.c_float)
 moe_forward = _f("or_moe_forward", C.c_int, C.POINTER(ffi.Config), C.POINTER(ffi.Layer), C.c_int,
                  C.POINTER(fp), C.POINTER(fp), ip, ip)
+argmax = _f("or_argmax", C.c_int, fp, C.c_int, C.c_float)
 lookup_draft = _f("or_lookup_draft", C.c_int, ip, C.c_int, C.c_int, ip, C.c_int, C.c_int, C.c_int, ip, ip)
 spec_init = _f("or_spec_init", None, C.POINTER(ffi.SpecModel), C.c_int)
 spec_best_len = _f("or_spec_best_len", C.c_int, C.POINTER(ffi.SpecModel), C.c_int, C.c_int)
@@ -244,3 +245,82 @@ def test_spec_model_reference_case():
     f = ffi.SpecModel()
     spec_init(C.byref(f), 1)
     assert spec_best_len(C.byref(f), 0, 4) == 4
+
+
+def _route_case(logits, n_used, prune, norm=1):
+    """or_moe_forward on x = e_0 against an F32 router whose column 0 holds `logits` (so the
+    router's output is exactly `logits`) and small F32 experts; returns the kept experts in
+    choice order."""
+    ne, dim, ff = len(logits), 32, 16
+    router = np.zeros((ne, dim), np.float32)
+    router[:, 0] = logits
+    rng = np.random.default_rng(1)
+    gate = (rng.standard_normal((ne, ff, dim)) * 0.1).astype(np.float32)
+    up = (rng.standard_normal((ne, ff, dim)) * 0.1).astype(np.float32)
+    down = (rng.standard_normal((ne, dim, ff)) * 0.1).astype(np.float32)
+    x = np.zeros(dim, np.float32)
+    x[0] = 1.0
+    cfg = ffi.Config(dim=dim, n_expert=ne, n_expert_used=n_used, expert_norm=norm, moe_prune=prune)
+    ly = ffi.Layer()
+    ly.is_moe = 1
+    keep = [np.ascontiguousarray(a) for a in (router, gate, up, down)]
+    ly.router = ffi.Mat(ffi.F32, dim, ne, keep[0].ctypes.data)
+    ly.gate = ffi.Mat(ffi.F32, dim, ff, keep[1].ctypes.data)
+    ly.up = ffi.Mat(ffi.F32, dim, ff, keep[2].ctypes.data)
+    ly.down = ffi.Mat(ffi.F32, ff, dim, keep[3].ctypes.data)
+    out = np.zeros(dim, np.float32)
+    chosen = np.zeros(32, np.int32)
+    nkeep = np.zeros(1, np.int32)
+    assert moe_forward(C.byref(cfg), C.byref(ly), 1, (fp * 1)(_p(x)), (fp * 1)(_p(out)), _p(chosen, ip), _p(nkeep, ip)) == 0
+    return chosen[:nkeep[0]].tolist()
+
+
+# probabilities of ten experts, assigned to a shuffled expert order so that choice order matters
+_PROBS = [0.40, 0.20, 0.15, 0.10, 0.05, 0.04, 0.03, 0.02, 0.005, 0.005]
+_PERM = [7, 2, 9, 0, 4, 8, 1, 5, 3, 6]  # expert holding the i-th largest probability
+
+
+def _prune_logits():
+    lg = np.zeros(10, np.float32)
+    for i, e in enumerate(_PERM):
+        lg[e] = np.log(_PROBS[i])
+    return lg
+
+
+@pytest.mark.parametrize("prune,keep", [(0.0, 8), (4.0, 4), (2.0, 4), (6.0, 6), (9.0, 8)])
+def test_prune_count_rule_by_hand(prune, keep):
+    """moe_prune >= 1 (smollm_chat.rs:1224-1226): keep clamp(prune, max(2, n_used/2), n_used) of
+    the top n_used = 8 by probability; here min_keep = 4. Expected counts worked out by hand."""
+    assert _route_case(_prune_logits(), 8, prune) == _PERM[:keep]
+
+
+@pytest.mark.parametrize("prune,keep", [(0.5, 4), (0.1, 5), (0.03, 7)])
+def test_prune_mass_rule_by_hand(prune, keep):
+    """moe_prune < 1 (:1227-1235): keep the fewest top choices (at least min_keep = 4) whose mass
+    reaches (1 - prune) of the top-8 mass 0.99. 0.5: target 0.495, the first four already hold
+    0.85, so the cut falls exactly at min_keep; 0.1: target 0.891, 0.85 + 0.05 reaches it at 5;
+    0.03: target 0.9603, the cumulative 0.94 (6) then 0.97 (7)."""
+    assert _route_case(_prune_logits(), 8, prune) == _PERM[:keep]
+
+
+def test_route_ties_go_to_the_lower_index():
+    """Exactly equal probabilities: the lower expert index is chosen first (the reference's
+    select_nth_unstable_by leaves tie order unspecified; this build fixes it)."""
+    lg = np.array([0.0, 1.0, 0.0, 2.0, 0.0, 0.0, 1.0, 0.0], np.float32)
+    assert _route_case(lg, 4, 0.0) == [3, 1, 6, 0]
+
+
+def test_argmax_total_order_last_max():
+    """sample_from_logits' greedy pick (:3661-3671): logits / logit_scale, then
+    max_by(total_cmp) over the logits in index order, which keeps the last of equal maxima;
+    -0.0 orders below +0.0 and a positive NaN above +inf."""
+    def am(v, scale=1.0):
+        a = np.array(v, np.float32)
+        return argmax(_p(a), a.size, scale)
+    assert am([1.0, 3.0, 3.0, 2.0]) == 2
+    assert am([1.0, 3.0, 3.0, 2.0], 6.0) == 2
+    assert am([5.0, 5.0, 5.0]) == 2
+    assert am([-0.0, 0.0]) == 1 and am([0.0, -0.0]) == 0
+    assert am([1.0, np.nan, np.inf, 2.0]) == 1
+    assert am([-np.inf, -np.inf]) == 1
+    assert am([-3.0, -1.0, -2.0]) == 1

@@ -493,7 +493,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
     for (int j = wave; j < nrow / qpb; j += 4) {
       const int q0 = qa + j * qpb, b = q0 / g, head = h * g + q0 % g;
       const float4 xv = reinterpret_cast<const float4 *>(ol + j * 256)[lane];
-      const float am = wave_max(amax4(xv));
+      const float am = q8k_amax(xv);
       const int64_t vb = (int64_t)b * nbr + head * HD / 256;
       q8k_block_store(xv, am, a.aq.q + vb * 64, a.aq.d + vb, reinterpret_cast<int *>(a.aq.bs + vb * 8));
     }

@@ -378,7 +378,7 @@ __global__ __launch_bounds__(512) void kd_down(const DecDownArgs a) {
   for (int k = 0; k < HB; k++) {
     const int vb = wave + NWD * k;
     if (vb < nqb) {
-      const float am = wave_max(amax4(hv[k]));
+      const float am = q8k_amax(hv[k]);
       q8k_block_store(hv[k], am, lq + vb * 64, ld + vb, (SPX_L int *)(lbs + vb * 8));
     }
   }
@@ -973,7 +973,7 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
       for (int t = 0; t < 4; t++) {
         const int q = q0 + NW * t;
         if (q < nq) {
-          const float am = wave_max(amax4(hv[t]));
+          const float am = q8k_amax(hv[t]);
           q8k_block_store(hv[t], am, lq + q * 64, ld + q, lbs + q * 16);
         }
       }
@@ -1416,7 +1416,7 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_mq(const DecDownMArgs 
       for (int t = 0; t < 4; t++) {
         const int q = q0 + NW * t;
         if (q < nq) {
-          const float am = wave_max(amax4(hv[t]));
+          const float am = q8k_amax(hv[t]);
           q8k_block_store(hv[t], am, lq + q * 64, ld + q, lbs + q * 16);
         }
       }

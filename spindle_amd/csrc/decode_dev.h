@@ -172,7 +172,7 @@ __device__ __forceinline__ void in_quant(const DecIn &in, InRow<KB> &r, QP lq, D
   for (int k = 0; k < KB; k++) {
     const int tb = wave + NW * k;
     if (tb < nbq) {
-      const float am = wave_max(amax4(r.v[k]));
+      const float am = q8k_amax(r.v[k]);
       q8k_block_store(r.v[k], am, lq + tb * 64, ld + tb, lbs + tb * 16);  // lbs: the bsum pairs as ints
     }
   }

@@ -104,30 +104,87 @@ __device__ __forceinline__ void st_dev(float *p, float v) { __hip_atomic_store(p
 __device__ __forceinline__ float ld_dev(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 // ------------------------------------------------------------------ Q8_K of one block
-// quantize_avx2 (quant_q8k.rs:84-121) of 256 values, lane j holding values 4j..4j+3:
-// amax (exact), iscale = 127/amax and d = amax/127 correctly rounded, q = rint(x*iscale)
-// saturated to int8, bsums = sums of 16 codes; zero or non-finite amax -> zeros. Writes the
-// permuted layout (lane j's dword goes to [l = j % 8][k = j / 8]).
+// quantize_avx2 (quant_q8k.rs:84-121) of 256 values, lane j holding values 4j..4j+3.
+__device__ __forceinline__ float amax4(float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); }
+
+// maxps: the first operand when it compares greater, else the second (so the second when
+// either is NaN).
+__device__ __forceinline__ float max_ps(float a, float b) { return a > b ? a : b; }
+
+// The reference's amax (:89-98): eight running maxima, lane l over the values 8i + l in
+// order i = 0..31, then max_ps(l, l + 4), max_ps of (0, 2) and (1, 3), max_ps of the two.
+// A NaN resets its lane's running maximum to the next value of that lane, so a running
+// maximum is the plain maximum of the values after the lane's last NaN, or NaN when that
+// NaN is in the last group (i = 31); the tree keeps a NaN only as a second operand.
+// Value 8i + l sits in wave lane 2i + l / 4, component l % 4: running lane c < 4 is
+// component c of the even wave lanes, running lane 4 + c that of the odd ones. Every lane
+// returns the result.
+__device__ __forceinline__ float q8k_amax_nan(float4 v) {
+  const int lane = threadIdx.x & 63;
+  const float xs[4] = {v.x, v.y, v.z, v.w};
+  float a[8];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const unsigned long long nm = __builtin_amdgcn_ballot_w64(isnan(xs[c]));
+    const unsigned long long ne = nm & 0x5555555555555555ull, no = nm & 0xAAAAAAAAAAAAAAAAull;
+    const int he = ne ? 63 - __builtin_clzll(ne) : -1, ho = no ? 63 - __builtin_clzll(no) : -1;  // last NaN lanes
+    float r = lane > ((lane & 1) ? ho : he) ? fabsf(xs[c]) : 0.0f;
+    // maximum over the lanes of one parity: xor 2, rotations by 4 and 8 in rows of 16, xor 16, xor 32
+    r = fmaxf(r, SPX_DPPF(r, 0x4E));
+    r = fmaxf(r, SPX_DPPF(r, 0x124));
+    r = fmaxf(r, SPX_DPPF(r, 0x128));
+    r = max16(r);
+    r = max32(r);
+    a[c] = he == 62 ? __builtin_nanf("") : lane_f(r, 0);
+    a[4 + c] = ho == 63 ? __builtin_nanf("") : lane_f(r, 1);
+  }
+  const float v0 = max_ps(max_ps(a[0], a[4]), max_ps(a[2], a[6]));
+  const float v1 = max_ps(max_ps(a[1], a[5]), max_ps(a[3], a[7]));
+  return max_ps(v0, v1);
+}
+
+// amax of the wave's block: without a NaN the reference's result is the exact maximum, which
+// the butterfly gives in any order; a block with a NaN (rare) takes the literal order.
+__device__ __forceinline__ float q8k_amax(float4 v) {
+  const bool nan = isnan(v.x) || isnan(v.y) || isnan(v.z) || isnan(v.w);
+  if (__builtin_expect(__builtin_amdgcn_ballot_w64(nan) != 0, 0)) return q8k_amax_nan(v);
+  return wave_max(amax4(v));
+}
+
+// The code of x * iscale: cvtps_epi32 (round half to even; NaN or out of int32 range gives
+// INT_MIN) then the int8 saturation of packs. A value outside [-amax, amax] (possible only
+// when a NaN reset the maximum) saturates as there, +inf included (-128).
+__device__ __forceinline__ int q8k_code(float x, float iscale) {
+  const float r = rintf(__fmul_rn(x, iscale));
+  return (r >= -2147483648.0f && r < 2147483648.0f) ? (int)fminf(fmaxf(r, -128.0f), 127.0f) : -128;
+}
+
+// The codes of lane j's four values and the block scale: iscale = 127/amax and d = amax/127
+// correctly rounded; zero, NaN or infinite amax gives zero codes and d = 0.
+__device__ __forceinline__ float q8k_codes(float4 x, float amax, int qv[4]) {
+  qv[0] = qv[1] = qv[2] = qv[3] = 0;
+  if (!(amax > 0.0f) || isinf(amax)) return 0.0f;
+  const float iscale = __fdiv_rn(127.0f, amax);
+  qv[0] = q8k_code(x.x, iscale);
+  qv[1] = q8k_code(x.y, iscale);
+  qv[2] = q8k_code(x.z, iscale);
+  qv[3] = q8k_code(x.w, iscale);
+  return __fdiv_rn(amax, 127.0f);
+}
+
+// The block quantized (amax from q8k_amax), bsums = sums of 16 codes, written in the permuted
+// layout (lane j's dword goes to [l = j % 8][k = j / 8]).
 template <class QP, class DP, class BP>  // pointers (global or LDS) to uint32_t, float, int
 __device__ __forceinline__ void q8k_block_store(float4 x, float amax, QP q, DP d, BP bs) {
   const int lane = threadIdx.x & 63;
-  int qv[4] = {0, 0, 0, 0};
-  float dv = 0.0f;
-  if (amax > 0.0f && !isinf(amax)) {
-    const float iscale = __fdiv_rn(127.0f, amax);
-    dv = __fdiv_rn(amax, 127.0f);
-    const float xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-    for (int j = 0; j < 4; j++) qv[j] = (int)fminf(fmaxf(rintf(__fmul_rn(xs[j], iscale)), -128.0f), 127.0f);
-  }
+  int qv[4];
+  const float dv = q8k_codes(x, amax, qv);
   q[(lane & 7) * 8 + (lane >> 3)] = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
                                     ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
   const int s = quad_sum(qv[0] + qv[1] + qv[2] + qv[3]);
   if ((lane & 3) == 0) bs[lane >> 2] = s;
   if (lane == 0) *d = dv;
 }
-
-__device__ __forceinline__ float amax4(float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); }
 
 // ------------------------------------------------------------------ greedy-pick keys
 // logits / logit_scale, then the last maximum under f32 total order (max_by(total_cmp),

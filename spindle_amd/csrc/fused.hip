@@ -82,7 +82,7 @@ __device__ __forceinline__ void norm_rows(const NormTail &t, int b0, int b1) {
           if (t.xn_out) reinterpret_cast<float4 *>(t.xn_out)[(int64_t)b * n4 + f] = v;
         }
         if (t.q_out.q) {
-          const float am = wave_max(amax4(v));
+          const float am = q8k_amax(v);
           const int64_t vb = (int64_t)b * nbq + tb;
           q8k_block_store(v, am, t.q_out.q + vb * 64, t.q_out.d + vb, reinterpret_cast<int *>(t.q_out.bs + vb * 8));
         }
@@ -700,7 +700,7 @@ __global__ __launch_bounds__(256) void k_q8kp_quantize(const float *x, int64_t n
   if (gb >= nb * m) return;
   const int64_t v = gb / nb, b = gb % nb;
   const float4 xv = reinterpret_cast<const float4 *>(x + v * ld_x + b * 256)[lane];
-  const float am = wave_max(amax4(xv));
+  const float am = q8k_amax(xv);
   const int64_t vb = v * nb + b;
   q8k_block_store(xv, am, out.q + vb * 64, out.d + vb, reinterpret_cast<int *>(out.bs + vb * 8));
 }
@@ -1026,7 +1026,7 @@ __device__ __forceinline__ void gateup_quant_tail(const GUArgs &a, int nvec, con
     const int vo = jo ? jo[u] : u;
     const float *hp = a.h + (int64_t)vo * n_ff + blk * 256 + 4 * lane;
     const float4 xv = make_float4(ld_dev(hp), ld_dev(hp + 1), ld_dev(hp + 2), ld_dev(hp + 3));
-    const float am = wave_max(amax4(xv));
+    const float am = q8k_amax(xv);
     const int64_t vb = (int64_t)vo * nbh + blk;
     q8k_block_store(xv, am, a.hq.q + vb * 64, a.hq.d + vb, reinterpret_cast<int *>(a.hq.bs + vb * 8));
   }

@@ -543,7 +543,7 @@ __global__ __launch_bounds__(PERSIST_NT) __attribute__((amdgpu_waves_per_eu(2, 2
       for (int k = 0; k < DN_HB; k++) {
         const int vb = wave + NW * k;
         if (vb < nqb) {
-          const float am = wave_max(amax4(hv[k]));
+          const float am = q8k_amax(hv[k]);
           q8k_block_store(hv[k], am, lqh + vb * 64, ldh + vb, (SPX_L int *)(lbsh + vb * 8));
         }
       }

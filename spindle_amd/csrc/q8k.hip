@@ -1,9 +1,8 @@
 // Q8_K activation quantization on gfx950 (quantize_avx2, quant_q8k.rs:84-121).
-// One wavefront per 256-value block: lane l holds x[4l..4l+3]. amax is an exact max;
-// iscale = 127/amax and d = amax/127 use correctly rounded division, q = rint(x*iscale)
-// (round half to even, like cvtps_epi32) saturated to int8, bsums = sums of 16 codes.
-// An all-zero or non-finite block gives d = 0, zero codes and zero sums, as the reference.
-#include "common.h"
+// One wavefront per 256-value block: lane l holds x[4l..4l+3]; amax and the codes as
+// q8k_amax / q8k_codes state (the reference's max order, NaN included), bsums = sums of 16
+// codes, in the reference's plain layout.
+#include "dev.h"
 
 namespace spx {
 
@@ -15,22 +14,9 @@ __global__ __launch_bounds__(256) void k_q8k_quantize(const float *x, int64_t n,
   if (gb >= nblk * m) return;
   const int64_t v = gb / nblk, b = gb % nblk;
   const float4 xv = reinterpret_cast<const float4 *>(x + v * ld_x + b * 256)[lane];
-  float am = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
-  float dv = 0.0f;
-  int q[4] = {0, 0, 0, 0};
-  if (!(!(am > 0.0f) || isinf(am))) {
-    const float iscale = __fdiv_rn(127.0f, am);
-    dv = __fdiv_rn(am, 127.0f);
-    const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float r = rintf(__fmul_rn(xs[j], iscale));
-      r = fminf(fmaxf(r, -128.0f), 127.0f);
-      q[j] = (int)r;
-    }
-  }
+  const float am = q8k_amax(xv);
+  int q[4];
+  const float dv = q8k_codes(xv, am, q);
   const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
                           ((uint32_t)(q[3] & 0xff) << 24);
   reinterpret_cast<uint32_t *>(qs + v * n + b * 256)[lane] = packed;

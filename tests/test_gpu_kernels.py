@@ -74,6 +74,50 @@ def test_q8k_quantize_bitwise(ctx):
         assert np.array_equal(bs[v].cpu().numpy(), ob), v
 
 
+def _nan_rows(rng, rows, n):
+    """Blocks with NaN at random places, often in the last group of eight (where the
+    reference's max order lets one survive or drops it by lane), and some +-inf."""
+    x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    for r in range(rows):
+        for b in range(n // 256):
+            pos = rng.integers(0, 256, rng.integers(0, 4))
+            if rng.random() < 0.5:
+                pos = np.append(pos, 248 + rng.integers(0, 8))
+            x[r, b * 256 + pos] = np.nan
+            if rng.random() < 0.25:
+                x[r, b * 256 + rng.integers(0, 256)] = np.inf * rng.choice([-1.0, 1.0])
+    return x
+
+
+def test_q8k_quantize_nan_bitwise(ctx):
+    """NaN/inf blocks: the block maximum in quantize_avx2's max_ps order, bit for bit, through
+    the plain quantizer and through the matvec's own (permuted) one."""
+    from spindle_amd import ops
+    rng = np.random.default_rng(5)
+    n = 2048
+    x = _nan_rows(rng, 24, n)
+    for lane in range(8):  # one NaN in each lane of the last group, alone in its block
+        x[lane, 248 + lane] = np.nan
+        x[lane, 256:512] = rng.standard_normal(256)
+        x[lane, 256 + 248 + lane] = np.nan
+    d, qs, bs = ops.q8k_quantize(ctx, _cuda(x))
+    zeroed = 0
+    for v in range(x.shape[0]):
+        od, oq, ob = ffi.q8k_quantize(x[v])
+        zeroed += int((od == 0).sum())
+        assert np.array_equal(d[v].cpu().numpy().view(np.uint32), od.view(np.uint32)), v
+        assert np.array_equal(qs[v].cpu().numpy(), oq), v
+        assert np.array_equal(bs[v].cpu().numpy(), ob), v
+    assert zeroed > 0  # some NaN survived to zero its block, as x[255] does
+    raw = _rand_kquant(R.Q4K, n, 96, rng)
+    w = ops.Tensor(ctx, R.Q4K, n, 96, raw)
+    got = ops.matvec(ctx, w, _cuda(x[:6])).cpu().numpy()
+    m = ffi.mat(R.Q4K, raw, 96, n)
+    for v in range(6):
+        want = ffi.matvec(m, x[v])
+        assert np.array_equal(got[v].view(np.uint32), want.view(np.uint32)), v
+
+
 @pytest.mark.parametrize("dtype", [R.Q4K, R.Q6K])
 @pytest.mark.parametrize("n", [256, 768, 2048, 4096])
 def test_block_sums_bitwise(ctx, dtype, n):

@@ -107,6 +107,58 @@ def test_q8k_quantize_nonfinite_block_is_zero():
     assert d[0] == np.float32(1.0) / np.float32(127.0) and np.all(qs[:256] == 127)
 
 
+def _nan_block(big=100.0):
+    """Lane l of quantize_avx2's running max sees x[8i + l]; values chosen so that each lane's
+    maximum names the lane: |x| = l + 1 everywhere, one big value in lane 0 at group 0."""
+    x = np.tile(np.arange(1, 9, dtype=np.float32), 32) * np.float32(0.5)
+    x[0] = big
+    return x
+
+
+@pytest.mark.parametrize("case", ["reset", "last_lane7", "last_lane6", "last_lane3", "inf_after_reset"])
+def test_q8k_quantize_nan_follows_maxps_order(case):
+    """_mm256_max_ps / _mm_max_ps / _mm_max_ss return the second operand when either is NaN
+    (quant_q8k.rs:89-98), so the block maximum depends on where the NaN sits; derived by hand:
+    - reset: NaN at x[8] (lane 0, group 1) makes lane 0 restart, dropping x[0] = 100 -> amax 4.0
+    - last_lane7: NaN at x[255] survives max_ps(am3, am7), (v1, v3) and (v0, v1) -> zero block
+    - last_lane6: NaN at x[254] makes v2 and then v0 NaN, which max_ss drops -> amax = v1 =
+      the odd lanes' maximum 4.0 (lane 0's 100 is lost with v0)
+    - last_lane3: NaN at x[251] is max_ps's first operand against lane 7 -> dropped, amax 100
+    - inf_after_reset: +inf at x[0] then NaN at x[8]: amax 4.0 and the inf codes as cvtps'
+      out-of-range INT_MIN saturated to -128; a NaN element codes as -128 too."""
+    x = _nan_block()
+    if case == "reset":
+        x[8] = np.nan
+        want = 4.0
+    elif case == "last_lane7":
+        x[255] = np.nan
+        want = None
+    elif case == "last_lane6":
+        x[254] = np.nan
+        want = 4.0
+    elif case == "last_lane3":
+        x[251] = np.nan
+        want = 100.0
+    else:
+        x[0] = np.inf
+        x[8] = np.nan
+        want = 4.0
+    d, qs, bs = ffi.q8k_quantize(x)
+    if want is None:
+        assert d[0] == 0 and not qs.any() and not bs.any()
+        return
+    want = np.float32(want)
+    assert d[0] == want / np.float32(127.0)
+    iscale = np.float32(127.0) / want
+    nan = np.isnan(x)
+    ok = ~nan & np.isfinite(x)
+    assert np.array_equal(qs[ok], np.clip(np.rint(x[ok] * iscale), -128, 127).astype(np.int8))
+    assert np.all(qs[nan] == -128) and np.all(qs[np.isinf(x)] == -128)
+    if case == "reset":
+        assert qs[0] == 127  # 100 * 127/4 saturates
+    assert np.array_equal(bs.astype(np.int32), qs.astype(np.int32).reshape(-1, 16).sum(1))
+
+
 def test_q5k_dequant_pinned_by_q4k_and_the_high_bit_rule():
     """Q5_K (quant.rs:1122-1137, dequant :1612-1640) shares Q4_K's header and code nibbles:
     with every high bit clear a Q5_K block dequantizes exactly like the Q4_K block with the

@@ -178,6 +178,24 @@ int spx_engine_destroy(spx_engine *e);
 int spx_lookup_draft(const int32_t *corpus, int n, int k, const int32_t *stop_ids, int n_stop,
                      int min_ngram, int max_ngram, int32_t *draft, int *ngram);
 
+/* The speculative loop's draft-length model (SpecModel, smollm_chat.rs:1670-1809), the object
+ * spx_engine_generate drives: accept rates per draft class decayed by 0.97 (floor 0.5), the
+ * one-token step cost and the per-extra-row verify cost, which choose how many drafted tokens
+ * a verify takes. For a host that runs its own loop over spx_engine_forward. Classes: 0 =
+ * 1-2-gram lookup, 1 = 3-gram, 2 = 4+-gram, 3 = draft model; times in whole microseconds.
+ * Entry points returning int give -1 on a null model or an argument out of range. */
+typedef struct spx_spec_model spx_spec_model;
+spx_spec_model *spx_spec_create(int fixed);            /* SpecModel::default, fixed = SPINDLE_SPEC_FIXED (:1693-1706) */
+spx_spec_model *spx_spec_clone(const spx_spec_model *m); /* Clone */
+void spx_spec_destroy(spx_spec_model *m);
+int spx_spec_class(int ngram);                                      /* SpecModel::class (:1710) */
+double spx_spec_accept_rate(const spx_spec_model *m, int cls);      /* :1719 */
+int spx_spec_best_len(spx_spec_model *m, int cls, int avail);       /* :1728 */
+void spx_spec_reset_rates(spx_spec_model *m);                       /* :1756 */
+int spx_spec_record_draft(spx_spec_model *m, int cls, int drafted, int accepted); /* :1763 */
+void spx_spec_record_step(spx_spec_model *m, uint64_t us);          /* :1777 */
+void spx_spec_record_verify(spx_spec_model *m, int rows, uint64_t us); /* :1788 */
+
 typedef struct {
   int draft_len;     /* k: tokens proposed per verify (draft_len, :1952) */
   int min_ngram, max_ngram;

@@ -47,6 +47,16 @@ SIGNATURES = {
     "spx_engine_destroy": (C.c_int, [P]),
     "spx_lookup_draft": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int, C.c_int, C.c_int, P, P]),
     "spx_engine_generate": (C.c_int, [P, P, C.c_int, C.c_int, P, P, P]),
+    "spx_spec_create": (P, [C.c_int]),
+    "spx_spec_clone": (P, [P]),
+    "spx_spec_destroy": (None, [P]),
+    "spx_spec_class": (C.c_int, [C.c_int]),
+    "spx_spec_accept_rate": (C.c_double, [P, C.c_int]),
+    "spx_spec_best_len": (C.c_int, [P, C.c_int, C.c_int]),
+    "spx_spec_reset_rates": (None, [P]),
+    "spx_spec_record_draft": (C.c_int, [P, C.c_int, C.c_int, C.c_int]),
+    "spx_spec_record_step": (None, [P, C.c_uint64]),
+    "spx_spec_record_verify": (None, [P, C.c_int, C.c_uint64]),
     "spx_engine_decode": (C.c_int, [P, C.c_int32, C.c_int, C.c_int, P]),
     "spx_engine_profile": (C.c_int, [P, C.c_int]),
     "spx_engine_profile_read": (C.c_int, [P, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_int64), C.POINTER(C.c_double), C.POINTER(C.c_double)]),

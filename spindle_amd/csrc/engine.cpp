@@ -24,6 +24,7 @@
 #include "fused.h"
 #include "internal.h"
 #include "persist.h"
+#include "spec.h"
 
 using namespace spx;
 
@@ -1153,46 +1154,6 @@ int spx_lookup_draft(const int32_t *c, int n, int k, const int32_t *stop, int n_
 
 namespace {
 
-// SpecModel (:1670-1809): measured accept rates and pass costs choose each draft's length.
-struct SpecModel {
-  double acc[4] = {1, 1, 1, 1}, fail_[4] = {1, 1, 1, 1}, t1_us = 100000.0, extra_us = 30000.0;
-  bool have_t1 = false, have_extra = false, fixed = false;
-  int since_try = 0;
-  static int cls(int ng) { return ng == 0 ? 3 : ng <= 2 ? 0 : ng == 3 ? 1 : 2; }
-  double rate(int c) const { return acc[c] / (acc[c] + fail_[c]); }
-  double cost(int b) const { return t1_us + extra_us * (double)(b > 1 ? b - 1 : 0); }
-  int best_len(int c, int avail) {
-    if (fixed || avail == 0) return avail;
-    const double p = rate(c);
-    double best_rate = 1.0 / cost(1), gain = 1.0, pk = 1.0;
-    int best = 0;
-    for (int k = 1; k <= avail; k++) {
-      pk *= p;
-      gain += pk;
-      const double r = gain / cost(k + 1);
-      if (r > best_rate) { best_rate = r; best = k; }
-    }
-    if (best == 0 && ++since_try >= 24) { since_try = 0; return std::min(avail, 2); }
-    return best;
-  }
-  void record_draft(int c, int drafted, int accepted) {
-    for (int i = 0; i < 4; i++) { acc[i] = std::max(acc[i] * 0.97, 0.5); fail_[i] = std::max(fail_[i] * 0.97, 0.5); }
-    acc[c] += accepted;
-    if (accepted < drafted) fail_[c] += 1.0;
-  }
-  void record_step(double us) {
-    t1_us = have_t1 ? 0.9 * t1_us + 0.1 * us : us;
-    if (!have_extra) extra_us = 0.3 * t1_us;
-    have_t1 = true;
-  }
-  void record_verify(int b, double us) {
-    if (b < 2 || !have_t1) return;
-    const double m = std::min(std::max((us - t1_us) / (double)(b - 1), 0.0), 1.5 * t1_us);
-    extra_us = have_extra ? 0.85 * extra_us + 0.15 * m : m;
-    have_extra = true;
-  }
-};
-
 constexpr int CORPUS_MAX = 16 * 1024;  // LOOKUP_CORPUS_MAX (:28)
 
 void remember(std::vector<int32_t> &corpus, const int32_t *ids, int n) {
@@ -1231,7 +1192,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
   const int last_rows = n_prompt - p->n_cached - ((n_prompt - p->n_cached - 1) / chunk) * chunk;  // rows in the last chunk
   int tok = am[last_rows - 1];
   int gen = 0, backoff = 0, skip = 0, k_dyn = p->draft_len;
-  SpecModel sm;
+  spx::SpecModel sm;
   sm.fixed = p->fixed != 0;
   for (;;) {
     out[gen++] = tok;  // emit!
@@ -1244,7 +1205,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
       int32_t d[MAX_M];
       int ng = 0;
       const int len = spx_lookup_draft(corpus.data(), (int)corpus.size(), std::min(k, MAX_M - 1), nullptr, 0, p->min_ngram, p->max_ngram, d, &ng);
-      if (skip == 0 || ng > 2) { memcpy(draft, d, sizeof(int32_t) * len); nd = len; cls = SpecModel::cls(ng); }
+      if (skip == 0 || ng > 2) { memcpy(draft, d, sizeof(int32_t) * len); nd = len; cls = spx::SpecModel::cls(ng); }
     }
     nd = sm.best_len(cls, nd);
     if (skip > 0) skip--;
@@ -1254,7 +1215,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
       const double us = (double)(now_us() - ts);
       pos++;
       tok = am[0];
-      sm.record_step(us);
+      sm.record_step((uint64_t)us);
       st->steps++;
       st->step_us += us;
       continue;
@@ -1266,7 +1227,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     const int64_t tv = now_us();
     if (int r = spx_engine_forward(E, batch, nd + 1, start, nullptr, nullptr, am)) return r;
     const double us = (double)(now_us() - tv);
-    sm.record_verify(nd + 1, us);
+    sm.record_verify(nd + 1, (uint64_t)us);
     st->verify_us += us;
     st->drafted += nd;
     st->verifies++;

@@ -10,7 +10,9 @@ import pytest
 
 from oracle import ffi
 
-lib = ffi.lib
+# a handle of its own: the typed signatures below must not change ffi.lib's, which other
+# modules call with void pointers
+lib = C.CDLL(ffi.LIB_PATH)
 P = C.c_void_p
 fp = C.POINTER(C.c_float)
 ip = C.POINTER(C.c_int)

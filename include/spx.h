@@ -213,9 +213,50 @@ typedef struct {
   double prefill_us, step_us, verify_us;  /* host wall time of the passes */
 } spx_gen_stats;
 
-/* Greedy generation with prompt-lookup speculation (generate_reply's loop :4205-4348 minus
- * chat framing, stop tokens ignored, repeat penalty 1): feeds the prompt from position n_cached,
- * writes up to max_new tokens to out and returns how many. */
+/* Token sampling (SamplerConfig :1523-1555, sample_from_logits :3624-3726, SplitMix64
+ * :1557-1572) over device logits: logits / logit_scale; the repeat penalty on each distinct
+ * token of the window (positive / p, others * p); stop ids to -inf while forbid_stop, the
+ * think-open id while forbid_think; then temperature <= 0: the last maximum under f32 total
+ * order; else top-k (0: every finite logit) by logit, softmax with temperature (the C
+ * library's expf, sequential sums), min-p, top-p, one SplitMix64 draw. Candidates with equal
+ * logits rank by ascending id (the reference's unstable sorts leave that order unspecified).
+ * The per-vocabulary work runs on the GPU (top_k up to 1024 selected there; top_k 0 or above
+ * 1024 copies the processed rows to the host and sorts them there); the O(k) tail on the host. */
+typedef struct {
+  float temperature;       /* 0.6 in the reference's default */
+  int top_k;               /* 40 */
+  float top_p, min_p;      /* 0.9, 0.05 */
+  float repeat_penalty;    /* 1.1 */
+  uint64_t seed;           /* SplitMix64 state at creation */
+  const int32_t *stop_ids; /* copied at creation */
+  int n_stop;
+  int think_open;          /* -1: none */
+} spx_sampler_params;
+typedef struct spx_sampler spx_sampler;
+int spx_sampler_create(spx_ctx *ctx, const spx_sampler_params *p, int vocab, spx_sampler **out);
+int spx_sampler_destroy(spx_sampler *s);
+int spx_sampler_reseed(spx_sampler *s, uint64_t seed);  /* set_sampler's SplitMix64(seed) (:2238) */
+/* sample_from_logits for one row of vocab device logits. */
+int spx_sample(spx_sampler *s, const float *logits, float logit_scale, const int32_t *recent, int n_recent,
+               int forbid_stop, int forbid_think, int32_t *token);
+/* The verify loop's sampling (:4305-4331): rows 0..n_draft of a pass (row i at logits + i*ld)
+ * sampled in order, row i over the window recent + draft[0..i) with stop ids forbidden while
+ * generated + i < 2, until a sample differs from draft[i] (the correction) or row n_draft (the
+ * bonus token). tokens gets the accepted drafts then that token (*n_out = accepted + 1); when
+ * accepted reaches max_accept first (the reply is full), no further row is drawn and
+ * *n_out = accepted. */
+int spx_sample_verify(spx_sampler *s, const float *logits, int64_t ld, int n_draft, float logit_scale,
+                      const int32_t *recent, int n_recent, const int32_t *draft, int generated, int max_accept,
+                      int forbid_think, int32_t *tokens, int *n_out);
+/* The engine's sampler for spx_engine_generate (a copy of p, its SplitMix64 state kept across
+ * calls like the reference's engine); NULL: plain greedy, no penalty, no stop ids. */
+int spx_engine_set_sampler(spx_engine *e, const spx_sampler_params *p);
+
+/* Generation with prompt-lookup speculation (generate_reply's loop :4205-4348 minus chat
+ * framing): feeds the prompt from position n_cached, writes up to max_new tokens to out and
+ * returns how many. Tokens come from the engine's sampler (spx_engine_set_sampler) over the
+ * tokens of this call so far, stop ids forbidden while fewer than 2 are out and ending the
+ * reply before one is emitted; without a sampler, plain greedy picks. */
 int spx_engine_generate(spx_engine *e, const int32_t *prompt, int n_prompt, int max_new,
                         const spx_gen_params *params, int32_t *out, spx_gen_stats *stats);
 

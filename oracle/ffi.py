@@ -68,6 +68,16 @@ class GenParams(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("draft_len", "min_ngram", "max_ngram", "fixed", "speculate", "adaptive_k", "prefill_chunk", "n_cached")]
 
 
+class SamplerParams(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("seed", C.c_uint64), ("stop_ids", C.POINTER(C.c_int)),
+                ("n_stop", C.c_int), ("think_open", C.c_int)]
+
+
+class Sampler(C.Structure):
+    _fields_ = [("p", SamplerParams), ("rng", C.c_uint64)]
+
+
 class GenStats(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("accepted", "drafted", "verifies", "steps")]
 
@@ -113,6 +123,11 @@ _sig("or_spec_record_draft", None, C.POINTER(SpecModel), C.c_int, C.c_int, C.c_i
 _sig("or_spec_record_step", None, C.POINTER(SpecModel), C.c_uint64)
 _sig("or_spec_record_verify", None, C.POINTER(SpecModel), C.c_int, C.c_uint64)
 _sig("or_generate", C.c_int, C.POINTER(Model), P, C.c_int, C.c_int, C.POINTER(GenParams), P, C.POINTER(GenStats))
+_sig("or_generate_sampled", C.c_int, C.POINTER(Model), P, C.c_int, C.c_int, C.POINTER(GenParams), C.POINTER(Sampler), P, C.POINTER(GenStats))
+_sig("or_sampler_init", None, C.POINTER(Sampler), C.POINTER(SamplerParams))
+_sig("or_splitmix_next", C.c_uint64, C.POINTER(C.c_uint64))
+_sig("or_splitmix_f32", C.c_float, C.POINTER(C.c_uint64))
+_sig("or_sample", C.c_int, C.POINTER(Sampler), P, C.c_int, C.c_float, P, C.c_int, C.c_int, C.c_int)
 _sig("or_set_threads", None, C.c_int)
 _sig("or_set_norm_order", None, C.c_int)
 _sig("or_get_threads", C.c_int)
@@ -197,6 +212,24 @@ def matvec_multi(m, xs):
     outs = [np.empty(m.rows, np.float32) for _ in xs]
     assert lib.or_matvec_multi(C.byref(m), len(xs), _parr(xs), _parr(outs)) == 0
     return outs
+
+
+class OracleSampler:
+    """sample_from_logits with its SplitMix64 state (or_sample); keeps the stop-id array alive."""
+
+    def __init__(self, temperature=0.6, top_k=40, top_p=0.9, min_p=0.05, repeat_penalty=1.1, seed=1,
+                 stop_ids=(), think_open=-1):
+        self._stop = (C.c_int * max(1, len(stop_ids)))(*stop_ids)
+        self.params = SamplerParams(temperature, top_k, top_p, min_p, repeat_penalty, seed,
+                                    C.cast(self._stop, C.POINTER(C.c_int)), len(stop_ids), think_open)
+        self.s = Sampler()
+        lib.or_sampler_init(C.byref(self.s), C.byref(self.params))
+
+    def sample(self, logits, recent=(), forbid_stop=False, forbid_think=False, logit_scale=1.0):
+        lg = np.ascontiguousarray(logits, np.float32)
+        rc = np.ascontiguousarray(np.asarray(recent, np.int32).reshape(-1))
+        return lib.or_sample(C.byref(self.s), ptr(lg), lg.size, logit_scale, ptr(rc) if rc.size else None, rc.size,
+                             int(forbid_stop), int(forbid_think))
 
 
 def set_threads(n):

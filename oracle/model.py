@@ -77,12 +77,17 @@ class OracleModel:
         return ffi.lib.or_argmax(lg.ctypes.data_as(C.c_void_p), lg.size, self.cfg.logit_scale)
 
     def generate(self, prompt, max_new, draft_len=8, min_ngram=2, max_ngram=4, fixed=False, speculate=True,
-                 adaptive_k=True, prefill_chunk=16, n_cached=0):
+                 adaptive_k=True, prefill_chunk=16, n_cached=0, sampler=None):
+        """sampler: an ffi.OracleSampler (its SplitMix64 state advances), or None for greedy."""
         prompt = np.ascontiguousarray(prompt, np.int32)
         out = np.empty(max_new, np.int32)
         gp = ffi.GenParams(draft_len, min_ngram, max_ngram, int(fixed), int(speculate), int(adaptive_k), prefill_chunk, n_cached)
         st = ffi.GenStats()
-        n = ffi.lib.or_generate(C.byref(self.m), prompt.ctypes.data_as(C.c_void_p), prompt.size, max_new, C.byref(gp),
-                                out.ctypes.data_as(C.c_void_p), C.byref(st))
+        if sampler is not None:
+            n = ffi.lib.or_generate_sampled(C.byref(self.m), prompt.ctypes.data_as(C.c_void_p), prompt.size, max_new,
+                                            C.byref(gp), C.byref(sampler.s), out.ctypes.data_as(C.c_void_p), C.byref(st))
+        else:
+            n = ffi.lib.or_generate(C.byref(self.m), prompt.ctypes.data_as(C.c_void_p), prompt.size, max_new, C.byref(gp),
+                                    out.ctypes.data_as(C.c_void_p), C.byref(st))
         assert n >= 0
         return out[:n], {k: getattr(st, k) for k, _ in ffi.GenStats._fields_}

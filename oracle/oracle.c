@@ -946,6 +946,79 @@ int or_argmax(const float *logits, int n, float logit_scale) {
   return best;
 }
 
+/* ------------------------------------------------------------------ sampling */
+uint64_t or_splitmix_next(uint64_t *x) { /* SplitMix64::next_u64 :1560-1566 */
+  uint64_t z = (*x += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+float or_splitmix_f32(uint64_t *x) { /* next_f32 :1569-1571: top 24 bits / 2^24 */
+  return (float)(or_splitmix_next(x) >> 40) / (float)(1u << 24);
+}
+
+void or_sampler_init(or_sampler *s, const or_sampler_params *p) { s->p = *p; s->rng = p->seed; }
+
+static int argmax_total(const float *l, int n) { /* max_by(total_cmp): the last maximum */
+  int best = 0; int32_t bk = 0;
+  for (int i = 0; i < n; i++) { int32_t k = total_key(l[i]); if (i == 0 || k >= bk) { bk = k; best = i; } }
+  return best;
+}
+
+static const float *g_sort_l;
+static int cand_cmp(const void *a, const void *b) { /* total_cmp descending, then index ascending */
+  int i = *(const int *)a, j = *(const int *)b;
+  int32_t ki = total_key(g_sort_l[i]), kj = total_key(g_sort_l[j]);
+  if (ki != kj) return ki > kj ? -1 : 1;
+  return i < j ? -1 : i > j;
+}
+
+int or_sample(or_sampler *S, const float *in, int V, float lscale, const int *recent, int nr, int forbid_stop, int forbid_think) {
+  const or_sampler_params *sc = &S->p;
+  float *l = malloc(sizeof(float) * V);
+  for (int i = 0; i < V; i++) l[i] = lscale != 1.0f ? in[i] / lscale : in[i];  /* :3626-3628 */
+  if (sc->repeat_penalty != 1.0f) {  /* :3631-3646, each distinct recent token once */
+    unsigned char *seen = calloc(V, 1);
+    for (int i = 0; i < nr; i++) {
+      int t = recent[i];
+      if (t < 0 || t >= V || seen[t]) continue;
+      seen[t] = 1;
+      l[t] = l[t] > 0.0f ? l[t] / sc->repeat_penalty : l[t] * sc->repeat_penalty;
+    }
+    free(seen);
+  }
+  if (forbid_stop)
+    for (int i = 0; i < sc->n_stop; i++)
+      if (sc->stop_ids[i] >= 0 && sc->stop_ids[i] < V) l[sc->stop_ids[i]] = -INFINITY;
+  if (forbid_think && sc->think_open >= 0 && sc->think_open < V) l[sc->think_open] = -INFINITY;
+  int tok;
+  if (sc->temperature <= 0.0f) { tok = argmax_total(l, V); free(l); return tok; }
+  int *cand = malloc(sizeof(int) * V), n = 0;  /* finite candidates :3671 */
+  for (int i = 0; i < V; i++) if (isfinite(l[i])) cand[n++] = i;
+  int k = sc->top_k == 0 ? n : (sc->top_k < n ? sc->top_k : n);
+  if (k == 0) { tok = argmax_total(l, V); free(cand); free(l); return tok; }
+  g_sort_l = l;
+  qsort(cand, n, sizeof(int), cand_cmp);  /* select_nth_unstable + sort_unstable :3677-3681 */
+  float *pr = malloc(sizeof(float) * k), mx = l[cand[0]], sum = 0.0f;
+  for (int i = 0; i < k; i++) pr[i] = expf((l[cand[i]] - mx) / sc->temperature);  /* :3684-3699 */
+  for (int i = 0; i < k; i++) sum += pr[i];
+  for (int i = 0; i < k; i++) pr[i] /= sum;
+  float floor_ = sc->min_p * pr[0];  /* min-p, then top-p :3702-3711 */
+  int keep = 0;
+  while (keep < k && pr[keep] >= floor_) keep++;
+  if (keep < 1) keep = 1;
+  float cum = 0.0f;
+  for (int i = 0; i < keep; i++) { cum += pr[i]; if (cum >= sc->top_p) { keep = i + 1; break; } }
+  float total = 0.0f;  /* :3714-3725 */
+  for (int i = 0; i < keep; i++) total += pr[i];
+  float r = or_splitmix_f32(&S->rng) * total;
+  tok = cand[keep - 1];
+  for (int i = 0; i < keep; i++) { r -= pr[i]; if (r <= 0.0f) { tok = cand[i]; break; } }
+  free(pr); free(cand); free(l);
+  return tok;
+}
+
 /* ------------------------------------------------------------------ speculation */
 int or_lookup_draft(const int *c, int n, int k, const int *stop, int n_stop, int min_ng, int max_ng, int *draft, int *ngram) {
   /* lookup_draft smollm_chat.rs:2982-3015 */
@@ -1027,13 +1100,32 @@ static void remember(int *corpus, int *n, const int *ids, int cnt) { /* :2973-29
   if (*n > CORPUS_MAX) { int drop = *n - CORPUS_MAX / 2; memmove(corpus, corpus + drop, sizeof(int) * (*n - drop)); *n -= drop; }
 }
 
+/* One token for row `row` of the pass's logits: the sampler's, or greedy (argmax after
+ * logit_scale) without one. */
+static int gen_pick(or_model *m, or_sampler *sp, const float *logits, const int *out, int gen) {
+  if (!sp) return or_argmax(logits, m->c.vocab, m->c.logit_scale);
+  return or_sample(sp, logits, m->c.vocab, m->c.logit_scale, out, gen, gen < 2, 0);  /* :4220, 4292, 4311 */
+}
+
+static int is_stop(const or_sampler *sp, int t) {
+  if (!sp) return 0;
+  for (int i = 0; i < sp->p.n_stop; i++) if (sp->p.stop_ids[i] == t) return 1;
+  return 0;
+}
+
 int or_generate(or_model *m, const int *prompt, int n_prompt, int max_new, const or_gen_params *p, int *out, or_gen_stats *st) {
+  return or_generate_sampled(m, prompt, n_prompt, max_new, p, NULL, out, st);
+}
+
+int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_new, const or_gen_params *p,
+                        or_sampler *sp, int *out, or_gen_stats *st) {
   const or_config *c = &m->c;
   int dim = c->dim, vocab = c->vocab, chunk = p->prefill_chunk > 0 ? p->prefill_chunk : 128;
-  int *corpus = malloc(sizeof(int) * (CORPUS_MAX + n_prompt + 64)), nc = 0;
-  float *hid = malloc(sizeof(float) * dim * 17), *logits = malloc(sizeof(float) * (size_t)vocab * 17);
+  const int *stop = sp ? sp->p.stop_ids : NULL, n_stop = sp ? sp->p.n_stop : 0;
   memset(st, 0, sizeof *st);
   if (n_prompt + max_new + 16 > c->max_seq || p->n_cached < 0 || p->n_cached >= n_prompt) return -1;
+  int *corpus = malloc(sizeof(int) * (CORPUS_MAX + n_prompt + 64)), nc = 0;
+  float *hid = malloc(sizeof(float) * dim * 17), *logits = malloc(sizeof(float) * (size_t)vocab * 17);
   remember(corpus, &nc, prompt, n_prompt);
   int pos = p->n_cached;
   /* feed :3041-3104 (chunks; a chunk of one token goes through forward_slice) */
@@ -1046,16 +1138,17 @@ int or_generate(or_model *m, const int *prompt, int n_prompt, int max_new, const
   }
   free(hbuf);
   or_logits(m, hid, 1, logits);
-  int tok = or_argmax(logits, vocab, c->logit_scale), gen = 0;
+  int gen = 0, tok = gen_pick(m, sp, logits, out, gen);
   or_spec_model sm; or_spec_init(&sm, p->fixed);
   int backoff = 0, skip = 0, k_dyn = p->draft_len;
   for (;;) {
+    if (is_stop(sp, tok)) break;                                  /* :4226 */
     out[gen++] = tok; remember(corpus, &nc, &tok, 1);           /* emit! */
     if (gen >= max_new) break;
     int budget = max_new - gen, k = k_dyn < budget - 1 ? k_dyn : budget - 1;
     int draft[64], nd = 0, cls = 3;
     if (p->speculate && k > 0) {
-      int d[64], ng = 0, len = or_lookup_draft(corpus, nc, k, NULL, 0, p->min_ngram, p->max_ngram, d, &ng);
+      int d[64], ng = 0, len = or_lookup_draft(corpus, nc, k, stop, n_stop, p->min_ngram, p->max_ngram, d, &ng);
       if (skip == 0 || ng > 2) /* weak = 2-gram (:4274) */ { memcpy(draft, d, sizeof(int) * len); nd = len; cls = or_spec_class(ng); }
     }
     nd = or_spec_best_len(&sm, cls, nd);
@@ -1065,7 +1158,7 @@ int or_generate(or_model *m, const int *prompt, int n_prompt, int max_new, const
       if (or_forward_slice(m, tok, pos, hid)) return -1;
       pos++;
       or_logits(m, hid, 1, logits);
-      tok = or_argmax(logits, vocab, c->logit_scale);
+      tok = gen_pick(m, sp, logits, out, gen);
       or_spec_record_step(&sm, now_us() - t0);
       st->steps++;
       continue;
@@ -1078,7 +1171,7 @@ int or_generate(or_model *m, const int *prompt, int n_prompt, int max_new, const
     st->drafted += nd; st->verifies++;
     int accepted = 0, correction = -1, done = 0;
     for (int i = 0; i < nd; i++) {
-      int s = or_argmax(logits + (size_t)i * vocab, vocab, c->logit_scale);
+      int s = gen_pick(m, sp, logits + (size_t)i * vocab, out, gen);
       if (s != draft[i]) { correction = s; break; }
       accepted++;
       out[gen++] = s; remember(corpus, &nc, &s, 1);
@@ -1094,7 +1187,7 @@ int or_generate(or_model *m, const int *prompt, int n_prompt, int max_new, const
       if (accepted == nd) { int kk = k_dyn + 2 < 7 ? k_dyn + 2 : 7; k_dyn = kk > p->draft_len ? kk : p->draft_len; }
       else k_dyn = p->draft_len;
     }
-    tok = correction >= 0 ? correction : or_argmax(logits + (size_t)nd * vocab, vocab, c->logit_scale);
+    tok = correction >= 0 ? correction : gen_pick(m, sp, logits + (size_t)nd * vocab, out, gen);
   }
   free(corpus); free(hid); free(logits);
   return gen;

@@ -181,10 +181,33 @@ typedef struct {
 
 typedef struct { int accepted, drafted, verifies, steps; } or_gen_stats;
 
-/* Greedy generation with prompt-lookup speculation (generate_reply minus chat framing).
- * Writes up to max_new tokens; returns the count. */
+/* ---- sampling (SamplerConfig :1523-1555, SplitMix64 :1557-1572, sample_from_logits :3624-3726) */
+typedef struct {
+  float temperature;   /* <= 0: greedy */
+  int top_k;           /* 0: every finite logit */
+  float top_p, min_p, repeat_penalty;
+  uint64_t seed;
+  const int *stop_ids; /* -inf while forbid_stop; generation ends on one */
+  int n_stop;
+  int think_open;      /* -1: none; -inf while forbid_think */
+} or_sampler_params;
+typedef struct { or_sampler_params p; uint64_t rng; } or_sampler;
+void or_sampler_init(or_sampler *s, const or_sampler_params *p);
+uint64_t or_splitmix_next(uint64_t *state);
+float or_splitmix_f32(uint64_t *state);
+/* One token from one row of logits; recent = the penalty window (ids outside 0..vocab-1 are
+ * skipped, repeats count once). Candidates equal under total order are ordered by index. */
+int or_sample(or_sampler *s, const float *logits, int vocab, float logit_scale, const int *recent, int n_recent,
+              int forbid_stop, int forbid_think);
+
+/* Generation with prompt-lookup speculation (generate_reply minus chat framing). Writes up to
+ * max_new tokens; returns the count. Greedy, no penalty, no stop ids: */
 int or_generate(or_model *m, const int *prompt, int n_prompt, int max_new,
                 const or_gen_params *p, int *out, or_gen_stats *st);
+/* ... and with a sampler: every token drawn by or_sample over the reply's tokens so far, stop
+ * ids forbidden while fewer than 2 are out, generation ending before a stop id. */
+int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_new, const or_gen_params *p,
+                        or_sampler *s, int *out, or_gen_stats *st);
 
 void or_set_threads(int n);
 /* Test knob, off by default: 1 = RMSNorm sums in the GPU kernels' order (sensitivity tests). */

@@ -47,6 +47,12 @@ SIGNATURES = {
     "spx_engine_destroy": (C.c_int, [P]),
     "spx_lookup_draft": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int, C.c_int, C.c_int, P, P]),
     "spx_engine_generate": (C.c_int, [P, P, C.c_int, C.c_int, P, P, P]),
+    "spx_sampler_create": (C.c_int, [P, P, C.c_int, C.POINTER(P)]),
+    "spx_sampler_destroy": (C.c_int, [P]),
+    "spx_sampler_reseed": (C.c_int, [P, C.c_uint64]),
+    "spx_sample": (C.c_int, [P, P, C.c_float, P, C.c_int, C.c_int, C.c_int, P]),
+    "spx_sample_verify": (C.c_int, [P, P, I64, C.c_int, C.c_float, P, C.c_int, P, C.c_int, C.c_int, C.c_int, P, P]),
+    "spx_engine_set_sampler": (C.c_int, [P, P]),
     "spx_spec_create": (P, [C.c_int]),
     "spx_spec_clone": (P, [P]),
     "spx_spec_destroy": (None, [P]),

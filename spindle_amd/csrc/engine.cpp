@@ -16,6 +16,7 @@
 #include <cstdlib>
 #include <map>
 #include <memory>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -24,6 +25,7 @@
 #include "fused.h"
 #include "internal.h"
 #include "persist.h"
+#include "sample.h"
 #include "spec.h"
 
 using namespace spx;
@@ -84,6 +86,7 @@ struct spx_engine {
   PersistArgs pa{};
   std::vector<PLayer> players;  // the layers' tensors, passed to each layer's launch
   int *perr_host = nullptr;  // pinned: the launch's error word, copied back with the pick
+  std::unique_ptr<spx::Sampler> smp;  // spx_engine_generate's sampler (none: plain greedy)
   std::vector<void *> allocs;
   // device state
   __half *kc = nullptr, *vc = nullptr;
@@ -1089,6 +1092,11 @@ int spx_engine_decode(spx_engine *E, int32_t token, int start_pos, int n, int32_
 int spx_engine_debug_read(spx_engine *E, const char *what, void *host, int64_t bytes) {
   if (!E || !what || !host) return fail("null argument");
   const std::string w(what);
+  if (w == "sampler_rng") {  // the engine sampler's SplitMix64 state (host memory)
+    if (!E->smp || bytes != 8) return fail("spx_engine_debug_read: no sampler, or bytes != 8");
+    memcpy(host, &E->smp->rng, 8);
+    return 0;
+  }
   const void *src = w == "tstamp" ? (const void *)E->pa.tstamp : w == "x" ? (const void *)E->xA : w == "xn" ? (const void *)E->xn : w == "q" ? (const void *)E->q : w == "k" ? (const void *)E->k : w == "v" ? (const void *)E->v
                   : w == "att" ? (const void *)E->att : w == "proj" ? (const void *)E->proj : w == "rlog" ? (const void *)E->rlog
                   : w == "chosen" ? (const void *)E->chosen : w == "weights" ? (const void *)E->weights
@@ -1165,6 +1173,19 @@ void remember(std::vector<int32_t> &corpus, const int32_t *ids, int n) {
 
 extern "C" {
 
+int spx_engine_set_sampler(spx_engine *E, const spx_sampler_params *p) {
+  if (!E) return fail("spx_engine_set_sampler: null engine");
+  if (!p) {
+    E->smp.reset();
+    return 0;
+  }
+  std::unique_ptr<spx::Sampler> s(new (std::nothrow) spx::Sampler());
+  if (!s) return fail("spx_engine_set_sampler: out of memory");
+  if (int r = s->init(p, E->c.vocab, E->ctx->device, E->ctx->stream)) return r;
+  E->smp = std::move(s);
+  return 0;
+}
+
 // generate_reply's speculative loop (:4205-4348) without chat framing: greedy decoding of up
 // to max_new tokens after the prompt. Invariant at the top of the loop: `tok` is sampled but
 // not yet in the KV cache; a verify pass feeds [tok, drafts...], the longest matching prefix
@@ -1190,11 +1211,26 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
   }
   st->prefill_us = (double)(now_us() - t0);
   const int last_rows = n_prompt - p->n_cached - ((n_prompt - p->n_cached - 1) / chunk) * chunk;  // rows in the last chunk
+  // the sampler (sample_next_token / sample_from_batch :3574-3621) over the tokens of this
+  // reply, stop ids forbidden while fewer than 2 are out (:4220); without one, the greedy picks
+  spx::Sampler *smp = E->smp && !E->smp->greedy_plain() ? E->smp.get() : nullptr;
+  const int32_t *stop = smp ? smp->stop.data() : nullptr;
+  const int n_stop = smp ? (int)smp->stop.size() : 0;
+  const int V = E->c.vocab;
+  const float lsc = E->c.logit_scale;
+  int gen = 0;
   int tok = am[last_rows - 1];
-  int gen = 0, backoff = 0, skip = 0, k_dyn = p->draft_len;
+  if (smp) {
+    if (int r = smp->prepare(E->logits + (size_t)(last_rows - 1) * V, V, 1, lsc, out, 0, 1u, false)) return r;
+    tok = smp->pick(0);
+  }
+  int backoff = 0, skip = 0, k_dyn = p->draft_len;
   spx::SpecModel sm;
   sm.fixed = p->fixed != 0;
   for (;;) {
+    bool is_stop = false;
+    for (int i = 0; i < n_stop; i++) is_stop |= stop[i] == tok;
+    if (is_stop) break;  // :4226
     out[gen++] = tok;  // emit!
     remember(corpus, &tok, 1);
     if (gen >= max_new) break;
@@ -1204,7 +1240,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     if (p->speculate && k > 0) {
       int32_t d[MAX_M];
       int ng = 0;
-      const int len = spx_lookup_draft(corpus.data(), (int)corpus.size(), std::min(k, MAX_M - 1), nullptr, 0, p->min_ngram, p->max_ngram, d, &ng);
+      const int len = spx_lookup_draft(corpus.data(), (int)corpus.size(), std::min(k, MAX_M - 1), stop, n_stop, p->min_ngram, p->max_ngram, d, &ng);
       if (skip == 0 || ng > 2) { memcpy(draft, d, sizeof(int32_t) * len); nd = len; cls = spx::SpecModel::cls(ng); }
     }
     nd = sm.best_len(cls, nd);
@@ -1215,6 +1251,10 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
       const double us = (double)(now_us() - ts);
       pos++;
       tok = am[0];
+      if (smp) {
+        if (int r = smp->prepare(E->logits, V, 1, lsc, out, gen, gen < 2 ? 1u : 0u, false)) return r;
+        tok = smp->pick(0);
+      }
       sm.record_step((uint64_t)us);
       st->steps++;
       st->step_us += us;
@@ -1231,10 +1271,18 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     st->verify_us += us;
     st->drafted += nd;
     st->verifies++;
+    if (smp) {  // rows 0..nd over the reply + draft[0..i) (sample_from_batch :4311)
+      std::vector<int32_t> win(out, out + gen);
+      win.insert(win.end(), draft, draft + nd);
+      uint32_t fs = 0;
+      for (int i = 0; i <= nd; i++)
+        if (gen + i < 2) fs |= 1u << i;
+      if (int r = smp->prepare(E->logits, V, nd + 1, lsc, win.data(), gen, fs, false)) return r;
+    }
     int accepted = 0, correction = -1;
     bool done = false;
     for (int i = 0; i < nd; i++) {
-      const int s = am[i];
+      const int s = smp ? smp->pick(i) : am[i];
       if (s != draft[i]) { correction = s; break; }
       accepted++;
       out[gen++] = s;
@@ -1248,7 +1296,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     if (accepted == 0) { backoff = std::min(std::max(backoff * 2, 1), 16); skip = backoff; }
     else backoff = 0;
     if (p->adaptive_k) k_dyn = accepted == nd ? std::max(std::min(k_dyn + 2, 7), p->draft_len) : p->draft_len;
-    tok = correction >= 0 ? correction : am[nd];
+    tok = correction >= 0 ? correction : smp ? smp->pick(nd) : am[nd];
   }
   return gen;
 }

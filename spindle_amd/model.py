@@ -288,6 +288,16 @@ class Engine:
             check(n)
         return out[:n], {k: getattr(st, k) for k, _ in GenStats._fields_}
 
+    def set_sampler(self, **kw):
+        """The sampler generate() draws with (ops.sampler_params keywords: temperature, top_k,
+        top_p, min_p, repeat_penalty, seed, stop_ids, think_open); no keywords: plain greedy."""
+        from .ops import sampler_params
+        if not kw:
+            check(lib.spx_engine_set_sampler(self.h, None))
+            return
+        params, keep = sampler_params(**kw)
+        check(lib.spx_engine_set_sampler(self.h, C.byref(params)))
+
     def decode(self, token, start_pos, n):
         """n greedy one-token passes starting with `token` at start_pos; returns the n picks."""
         out = np.empty(n, np.int32)

@@ -145,3 +145,66 @@ def matvec_noalloc(ctx, w, x, expert=0):
 
 
 matvec_multi = matvec
+
+
+class SamplerParams(C.Structure):
+    """spx_sampler_params (SamplerConfig, smollm_chat.rs:1523-1555)."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("seed", C.c_uint64), ("stop_ids", C.POINTER(C.c_int32)),
+                ("n_stop", C.c_int), ("think_open", C.c_int)]
+
+
+def sampler_params(temperature=0.6, top_k=40, top_p=0.9, min_p=0.05, repeat_penalty=1.1, seed=1, stop_ids=(),
+                   think_open=-1):
+    """The reference's defaults (a fixed seed instead of the clock); returns (params, keep-alive)."""
+    stop = (C.c_int32 * max(1, len(stop_ids)))(*stop_ids)
+    return SamplerParams(temperature, top_k, top_p, min_p, repeat_penalty, seed,
+                         C.cast(stop, C.POINTER(C.c_int32)), len(stop_ids), think_open), stop
+
+
+class Sampler:
+    """sample_from_logits over device logits with its own SplitMix64 state (spx_sampler)."""
+
+    def __init__(self, ctx, vocab, **kw):
+        self.ctx, self.vocab = ctx, vocab
+        params, keep = sampler_params(**kw)
+        h = P()
+        check(lib.spx_sampler_create(ctx.h, C.byref(params), vocab, C.byref(h)))
+        self.h = h
+        ctx.adopt(self)
+
+    def reseed(self, seed):
+        check(lib.spx_sampler_reseed(self.h, seed))
+
+    def sample(self, logits, recent=(), forbid_stop=False, forbid_think=False, logit_scale=1.0):
+        """One token from one row of device logits [vocab] (a float32 cuda tensor)."""
+        assert logits.is_cuda and logits.dtype == torch.float32 and logits.numel() == self.vocab and logits.is_contiguous()
+        rc = np.ascontiguousarray(np.asarray(recent, np.int32).reshape(-1))
+        tok = C.c_int32()
+        check(lib.spx_sample(self.h, _p(logits), logit_scale, rc.ctypes.data_as(P) if rc.size else None, rc.size,
+                             int(forbid_stop), int(forbid_think), C.byref(tok)))
+        return tok.value
+
+    def sample_verify(self, logits, recent, draft, generated, max_accept, forbid_think=False, logit_scale=1.0):
+        """The verify loop's sampling over rows 0..len(draft) of logits [>= len(draft)+1, vocab]."""
+        assert logits.is_cuda and logits.dtype == torch.float32 and logits.shape[-1] == self.vocab
+        rc = np.ascontiguousarray(np.asarray(recent, np.int32).reshape(-1))
+        dr = np.ascontiguousarray(np.asarray(draft, np.int32).reshape(-1))
+        toks = np.empty(dr.size + 1, np.int32)
+        n = C.c_int()
+        check(lib.spx_sample_verify(self.h, _p(logits), logits.stride(0), dr.size, logit_scale,
+                                    rc.ctypes.data_as(P) if rc.size else None, rc.size,
+                                    dr.ctypes.data_as(P) if dr.size else None, generated, max_accept,
+                                    int(forbid_think), toks.ctypes.data_as(P), C.byref(n)))
+        return toks[:n.value]
+
+    def close(self):
+        if self.h:
+            lib.spx_sampler_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

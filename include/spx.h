@@ -173,6 +173,57 @@ int spx_engine_expert_counts(spx_engine *e, int32_t *counts);
 int spx_engine_kv_download(spx_engine *e, void *k_host, void *v_host);
 int spx_engine_destroy(spx_engine *e);
 
+/* ------------------------------------------------------------------ GGUF files */
+/* A GGUF v2/v3 file opened read-only and mapped (GgufModelIndex::parse_file,
+ * gguf_loader.rs:142-247): the metadata table, the tensor table, general.alignment (U32/U64,
+ * at least 32, default 32) and the data section at the header's end rounded up to it; tensor
+ * offsets are absolute file offsets. Strings over 16 MiB, unknown value types and nested
+ * arrays are errors, as there. Host only, no GPU needed. */
+typedef struct spx_gguf spx_gguf;
+int spx_gguf_open(const char *path, spx_gguf **out);
+int spx_gguf_close(spx_gguf *g);
+int spx_gguf_info(const spx_gguf *g, uint32_t *version, uint64_t *alignment, uint64_t *data_offset,
+                  int64_t *n_tensors, int64_t *n_meta);
+/* Tensor i: name (valid until close), ggml type, dims (GGUF order: dims[0] = columns; unused
+ * dims are 1) and absolute file offset. */
+int spx_gguf_tensor(const spx_gguf *g, int64_t i, const char **name, int *dtype, int *n_dims, uint64_t *dims,
+                    uint64_t *abs_offset);
+int64_t spx_gguf_find(const spx_gguf *g, const char *name); /* index, -1 when absent */
+/* Metadata: the GGUF value type of key (-1 absent); a non-negative integer of any integer
+ * type (GgufValue::as_usize :88-101); a number as f32 (as_f32 :104-110); bool; string (valid
+ * until close); an array's element type and count. Each fails when the key has no such value. */
+int spx_gguf_meta_type(const spx_gguf *g, const char *key);
+int spx_gguf_meta_index(const spx_gguf *g, const char *key, uint64_t *out);
+int spx_gguf_meta_f32(const spx_gguf *g, const char *key, float *out);
+int spx_gguf_meta_bool(const spx_gguf *g, const char *key, int *out);
+int spx_gguf_meta_str(const spx_gguf *g, const char *key, const char **out);
+int spx_gguf_meta_array(const spx_gguf *g, const char *key, int *elem_type, uint64_t *count);
+/* tokenizer.ggml.tokens: count (0 when absent) and token strings (NULL out of range). */
+int64_t spx_gguf_vocab_size(const spx_gguf *g);
+const char *spx_gguf_token(const spx_gguf *g, int64_t id);
+/* ModelConfig::from_gguf (smollm_chat.rs:69-120): architecture llama / granite / granitemoe
+ * (rope pairs) or qwen2 / qwen2moe / qwen3 / qwen3moe / olmoe (NeoX halves); softmax gating
+ * only; required embedding_length, attention.head_count, block_count; head_count_kv,
+ * key_length, context_length (-> max_seq, default 2048), rope.freq_base (10000),
+ * layer_norm_rms_epsilon (1e-5), expert counts, expert_weights_norm (default: true except
+ * qwen2moe / olmoe), Granite's embedding / residual / logit scales and attention.scale;
+ * head_dim a multiple of 8 and n_heads a multiple of n_kv_heads. vocab = the tokenizer
+ * table's length (without one: token_embd's rows). */
+int spx_gguf_config(const spx_gguf *g, spx_model_config *cfg);
+/* The stop ids of load_with_index_sharded (:1925-1936): eos_token_id, then <|endoftext|>,
+ * <|im_end|>, <|end_of_text|> where the vocabulary has them, without repeats (*n = how many;
+ * the first cap are written); <think> / </think> ids (:1937) or -1 / -1. */
+int spx_gguf_stop_ids(const spx_gguf *g, int32_t *ids, int cap, int *n);
+int spx_gguf_think_ids(const spx_gguf *g, int32_t *open_id, int32_t *close_id);
+/* Fails when a tensor's rows end past the file's end (a cut-off download, :1944-1963). */
+int spx_gguf_check(const spx_gguf *g);
+/* SmolLm2Engine::load (:1887-2154) onto the GPU: the config from the file (max_seq > 0
+ * overrides context_length; moe_prune as set_moe_prune :2401), resolve_layers' tensors
+ * (:214-284) uploaded from the mapping, prepared. Refused like there: old per-expert Mixtral
+ * tensors, MoE tensors without expert counts; and what this engine does not run: shared
+ * experts, whole-projection Q/K norms (OLMoE). */
+int spx_engine_load_gguf(spx_ctx *ctx, const spx_gguf *g, int max_seq, float moe_prune, spx_engine **out);
+
 /* Prompt-lookup drafting (lookup_draft, smollm_chat.rs:2982-3015) with the n-gram range as a
  * parameter: the reference uses min_ngram 2, max_ngram 4. Returns the draft length. */
 int spx_lookup_draft(const int32_t *corpus, int n, int k, const int32_t *stop_ids, int n_stop,

@@ -53,6 +53,24 @@ SIGNATURES = {
     "spx_sample": (C.c_int, [P, P, C.c_float, P, C.c_int, C.c_int, C.c_int, P]),
     "spx_sample_verify": (C.c_int, [P, P, I64, C.c_int, C.c_float, P, C.c_int, P, C.c_int, C.c_int, C.c_int, P, P]),
     "spx_engine_set_sampler": (C.c_int, [P, P]),
+    "spx_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+    "spx_gguf_close": (C.c_int, [P]),
+    "spx_gguf_info": (C.c_int, [P, P, P, P, P, P]),
+    "spx_gguf_tensor": (C.c_int, [P, I64, P, P, P, P, P]),
+    "spx_gguf_find": (I64, [P, C.c_char_p]),
+    "spx_gguf_meta_type": (C.c_int, [P, C.c_char_p]),
+    "spx_gguf_meta_index": (C.c_int, [P, C.c_char_p, P]),
+    "spx_gguf_meta_f32": (C.c_int, [P, C.c_char_p, P]),
+    "spx_gguf_meta_bool": (C.c_int, [P, C.c_char_p, P]),
+    "spx_gguf_meta_str": (C.c_int, [P, C.c_char_p, P]),
+    "spx_gguf_meta_array": (C.c_int, [P, C.c_char_p, P, P]),
+    "spx_gguf_vocab_size": (I64, [P]),
+    "spx_gguf_token": (C.c_char_p, [P, I64]),
+    "spx_gguf_config": (C.c_int, [P, P]),
+    "spx_gguf_stop_ids": (C.c_int, [P, P, C.c_int, P]),
+    "spx_gguf_think_ids": (C.c_int, [P, P, P]),
+    "spx_gguf_check": (C.c_int, [P]),
+    "spx_engine_load_gguf": (C.c_int, [P, P, C.c_int, C.c_float, C.POINTER(P)]),
     "spx_spec_create": (P, [C.c_int]),
     "spx_spec_clone": (P, [P]),
     "spx_spec_destroy": (None, [P]),

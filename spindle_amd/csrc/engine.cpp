@@ -69,7 +69,8 @@ struct spx_engine {
                            // a pass of fewer rows gives an expert about one row, the MFMA's 16 columns idle
                            // and the per-lane dot kernel is faster
   bool mq_gateup = true;   // the gate/up projections (SPX_MQ_GATEUP)
-  int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
+  int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;
+  bool att_merge = false;  // one-row passes: attention chunks merged inside the attention launch (SPX_ATT_MERGE)  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
   std::map<std::string, int64_t> vec_len;
@@ -425,9 +426,13 @@ int enqueue_decode(spx_engine *E, bool advance) {
       aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
       aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
       aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
-      SPX_HIP(launch_attention_partials(aa, E->st_dev, s));
-      DecMergeArgs ma{E->part_ml, E->part_o, E->att, aa.nslot, hd, c.n_heads, c.n_kv_heads};
-      SPX_HIP(launch_dec_merge(ma, E->st_dev, s));
+      if (E->att_merge) {
+        SPX_HIP(launch_attention(aa, 1, E->st_dev, s));
+      } else {
+        SPX_HIP(launch_attention_partials(aa, E->st_dev, s));
+        DecMergeArgs ma{E->part_ml, E->part_o, E->att, aa.nslot, hd, c.n_heads, c.n_kv_heads};
+        SPX_HIP(launch_dec_merge(ma, E->st_dev, s));
+      }
     }
     {
       ProfScope ps(E, PC_WO, wbytes(ly.wo));
@@ -739,6 +744,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   if (const char *v = std::getenv("SPX_LM_MODE")) E->lm_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_TAIL_MAX")) E->tail_max = std::max(0, std::min(MAX_M, atoi(v)));
   if (const char *v = std::getenv("SPX_DOWN_MODE")) E->down_mode = std::max(0, std::min(1, atoi(v)));
+  if (const char *v = std::getenv("SPX_ATT_MERGE")) E->att_merge = atoi(v) != 0;
   *out = E;
   return 0;
 }

@@ -199,16 +199,16 @@ Sampler::~Sampler() {
     (void)hipSetDevice(device);
     (void)hipStreamSynchronize(stream);
   }
-  hipFree(d_scratch);
-  hipFree(d_cidx);
-  hipFree(d_cval);
-  hipFree(d_meta);
-  hipFree(d_ids);
-  hipHostFree(h_cidx);
-  hipHostFree(h_cval);
-  hipHostFree(h_meta);
-  hipHostFree(h_ids);
-  hipHostFree(h_row);
+  (void)hipFree(d_scratch);
+  (void)hipFree(d_cidx);
+  (void)hipFree(d_cval);
+  (void)hipFree(d_meta);
+  (void)hipFree(d_ids);
+  (void)hipHostFree(h_cidx);
+  (void)hipHostFree(h_cval);
+  (void)hipHostFree(h_meta);
+  (void)hipHostFree(h_ids);
+  (void)hipHostFree(h_row);
 }
 
 int Sampler::init(const spx_sampler_params *pp, int V, int dev, hipStream_t s) {
@@ -258,8 +258,8 @@ int Sampler::prepare(const float *logits, int64_t ld, int m, float lscale, const
   if (n_ids > ids_cap) {
     const int cap = std::max(n_ids, 4096);
     SPX_HIP(hipStreamSynchronize(stream));
-    hipFree(d_ids);
-    hipHostFree(h_ids);
+    (void)hipFree(d_ids);
+    (void)hipHostFree(h_ids);
     d_ids = nullptr;
     h_ids = nullptr;
     SPX_HIP(hipMalloc(&d_ids, sizeof(int32_t) * cap));

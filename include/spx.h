@@ -169,6 +169,13 @@ int spx_engine_debug_read(spx_engine *e, const char *what, void *host, int64_t b
 int spx_engine_last_experts(spx_engine *e, int32_t *njobs_per_layer);
 /* Per layer and expert: passes that selected the expert since prepare ([n_layers][n_expert]). */
 int spx_engine_expert_counts(spx_engine *e, int32_t *counts);
+/* The KV window (shift_kv :2944-2971, ensure_kv_room :2924-2940): shift_kv drops n_discard
+ * positions (at most cur_pos - n_keep) after the n_keep pinned ones, moves the rest down and
+ * re-rotates their keys by -n_discard (f16 -> f32 -> RoPE -> f16 RNE; values move as they are);
+ * ensure_kv_room slides by max(overflow, half the unpinned context) when cur_pos + needed >
+ * max_seq, and fails when the pinned positions leave no room. *new_pos = the next position. */
+int spx_engine_shift_kv(spx_engine *e, int n_keep, int n_discard, int cur_pos, int *new_pos);
+int spx_engine_ensure_kv_room(spx_engine *e, int n_keep, int cur_pos, int needed, int *new_pos);
 /* Copies the f16 K and V caches ([n_layers][max_seq][kv_dim] each) to host memory. */
 int spx_engine_kv_download(spx_engine *e, void *k_host, void *v_host);
 int spx_engine_destroy(spx_engine *e);
@@ -257,6 +264,8 @@ typedef struct {
   int n_cached;      /* prompt tokens already in the KV cache at positions 0..n_cached-1 (a
                         session's earlier turns, generate_reply's cur_pos): only the rest of the
                         prompt is fed; 0 <= n_cached < n_prompt */
+  int kv_keep;       /* n_keep: positions the sliding window never evicts (the system prompt);
+                        before each pass the window slides as ensure_kv_room does */
 } spx_gen_params;
 
 typedef struct {

@@ -65,7 +65,8 @@ class SpecModel(C.Structure):
 
 
 class GenParams(C.Structure):
-    _fields_ = [(n, C.c_int) for n in ("draft_len", "min_ngram", "max_ngram", "fixed", "speculate", "adaptive_k", "prefill_chunk", "n_cached")]
+    _fields_ = [(n, C.c_int) for n in ("draft_len", "min_ngram", "max_ngram", "fixed", "speculate", "adaptive_k", "prefill_chunk", "n_cached",
+                                       "kv_keep")]
 
 
 class SamplerParams(C.Structure):
@@ -128,6 +129,8 @@ _sig("or_sampler_init", None, C.POINTER(Sampler), C.POINTER(SamplerParams))
 _sig("or_splitmix_next", C.c_uint64, C.POINTER(C.c_uint64))
 _sig("or_splitmix_f32", C.c_float, C.POINTER(C.c_uint64))
 _sig("or_sample", C.c_int, C.POINTER(Sampler), P, C.c_int, C.c_float, P, C.c_int, C.c_int, C.c_int)
+_sig("or_shift_kv", C.c_int, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P, C.c_int, C.c_int, C.c_int)
+_sig("or_ensure_kv_room", C.c_int, C.POINTER(Model), C.c_int, C.c_int, C.c_int)
 _sig("or_set_threads", None, C.c_int)
 _sig("or_set_norm_order", None, C.c_int)
 _sig("or_get_threads", C.c_int)
@@ -230,6 +233,13 @@ class OracleSampler:
         rc = np.ascontiguousarray(np.asarray(recent, np.int32).reshape(-1))
         return lib.or_sample(C.byref(self.s), ptr(lg), lg.size, logit_scale, ptr(rc) if rc.size else None, rc.size,
                              int(forbid_stop), int(forbid_think))
+
+
+def shift_kv(k16, v16, n_layers, max_seq, kv_dim, head_dim, neox, theta, n_keep, n_discard, cur_pos):
+    """shift_kv on uint16 (f16-bit) caches [n_layers][max_seq][kv_dim], in place; returns the new cur_pos."""
+    inv = np.empty(head_dim // 2 + 1, np.float32)
+    lib.or_rope_inv_freq(head_dim, theta, ptr(inv))
+    return lib.or_shift_kv(ptr(k16), ptr(v16), n_layers, max_seq, kv_dim, head_dim, int(neox), ptr(inv), n_keep, n_discard, cur_pos)
 
 
 def set_threads(n):

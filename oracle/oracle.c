@@ -841,6 +841,36 @@ static void qkv_post(or_model *m, const or_layer *ly, int layer, int pos, float 
   for (int i = 0; i < kv_dim; i++) { m->k_cache[off + i] = or_f32_to_f16(k[i]); m->v_cache[off + i] = or_f32_to_f16(v[i]); }
 }
 
+int or_shift_kv(uint16_t *kc, uint16_t *vc, int n_layers, int max_seq, int kv_dim, int hd, int neox, const float *inv_freq,
+                int n_keep, int n_discard, int cur_pos) {
+  int n_ctx = cur_pos > n_keep ? cur_pos - n_keep : 0; /* :2944-2971 */
+  if (n_discard > n_ctx) n_discard = n_ctx;
+  if (n_discard <= 0) return cur_pos;
+  int n_move = n_ctx - n_discard;
+  float *tmp = malloc(sizeof(float) * kv_dim);
+  for (int l = 0; l < n_layers; l++)
+    for (int i = 0; i < n_move; i++) {
+      size_t src = ((size_t)l * max_seq + n_keep + n_discard + i) * kv_dim, dst = ((size_t)l * max_seq + n_keep + i) * kv_dim;
+      for (int j = 0; j < kv_dim; j++) tmp[j] = or_f16_to_f32(kc[src + j]);
+      or_rope_rotate(inv_freq, neox, tmp, kv_dim, hd, -(float)n_discard);
+      for (int j = 0; j < kv_dim; j++) kc[dst + j] = or_f32_to_f16(tmp[j]);
+      memmove(vc + dst, vc + src, sizeof(uint16_t) * kv_dim);
+    }
+  free(tmp);
+  return cur_pos - n_discard;
+}
+
+int or_ensure_kv_room(or_model *m, int n_keep, int cur_pos, int needed) {
+  const or_config *c = &m->c;
+  if (cur_pos + needed <= c->max_seq) return cur_pos; /* :2924-2940 */
+  int n_ctx = cur_pos - n_keep, want = cur_pos + needed - c->max_seq;
+  if (want < n_ctx / 2) want = n_ctx / 2;
+  int n_discard = want < n_ctx ? want : n_ctx;
+  if (!m->inv_freq) { m->inv_freq = malloc(sizeof(float) * (c->head_dim / 2 + 1)); or_rope_inv_freq(c->head_dim, c->rope_theta, m->inv_freq); }
+  return or_shift_kv(m->k_cache, m->v_cache, c->n_layers, c->max_seq, c->n_kv_heads * c->head_dim, c->head_dim, c->rope_neox,
+                     m->inv_freq, n_keep, n_discard, cur_pos);
+}
+
 int or_forward_slice(or_model *m, int token, int pos, float *hidden) {
   const or_config *c = &m->c;
   int dim = c->dim, q_dim = c->n_heads * c->head_dim, kv_dim = c->n_kv_heads * c->head_dim;
@@ -1123,7 +1153,7 @@ int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_ne
   int dim = c->dim, vocab = c->vocab, chunk = p->prefill_chunk > 0 ? p->prefill_chunk : 128;
   const int *stop = sp ? sp->p.stop_ids : NULL, n_stop = sp ? sp->p.n_stop : 0;
   memset(st, 0, sizeof *st);
-  if (n_prompt + max_new + 16 > c->max_seq || p->n_cached < 0 || p->n_cached >= n_prompt) return -1;
+  if (p->n_cached < 0 || p->n_cached >= n_prompt || p->kv_keep < 0 || p->kv_keep + chunk + 16 > c->max_seq) return -1;
   int *corpus = malloc(sizeof(int) * (CORPUS_MAX + n_prompt + 64)), nc = 0;
   float *hid = malloc(sizeof(float) * dim * 17), *logits = malloc(sizeof(float) * (size_t)vocab * 17);
   remember(corpus, &nc, prompt, n_prompt);
@@ -1132,6 +1162,7 @@ int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_ne
   float *hbuf = malloc(sizeof(float) * (size_t)dim * chunk);
   for (int s = p->n_cached; s < n_prompt; s += chunk) {
     int cnt = n_prompt - s < chunk ? n_prompt - s : chunk;
+    pos = or_ensure_kv_room(m, p->kv_keep, pos, cnt); /* feed :3089-3090 */
     if (or_forward_batch(m, prompt + s, cnt, pos, hbuf)) return -1;
     memcpy(hid, hbuf + (size_t)(cnt - 1) * dim, 4 * dim);
     pos += cnt;
@@ -1154,6 +1185,7 @@ int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_ne
     nd = or_spec_best_len(&sm, cls, nd);
     if (skip > 0) skip--;
     if (nd == 0) {
+      pos = or_ensure_kv_room(m, p->kv_keep, pos, 1); /* :4283 */
       uint64_t t0 = now_us();
       if (or_forward_slice(m, tok, pos, hid)) return -1;
       pos++;
@@ -1164,6 +1196,7 @@ int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_ne
       continue;
     }
     int batch[65]; batch[0] = tok; memcpy(batch + 1, draft, sizeof(int) * nd);
+    pos = or_ensure_kv_room(m, p->kv_keep, pos, nd + 1); /* :4298 */
     int start = pos; uint64_t t0 = now_us();
     if (or_forward_batch(m, batch, nd + 1, start, hid)) return -1;
     or_logits(m, hid, nd + 1, logits);

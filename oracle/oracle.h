@@ -138,6 +138,15 @@ typedef struct {
 void or_model_init(or_model *m);
 /* forward_slice: one token at pos -> output-normed hidden (smollm_chat.rs:3364-3552) */
 int or_forward_slice(or_model *m, int token, int pos, float *hidden);
+/* shift_kv (smollm_chat.rs:2944-2971) on f16 caches [n_layers][max_seq][kv_dim]: drops n_discard
+ * positions after the n_keep pinned ones (clamped to cur_pos - n_keep), moves the rest down and
+ * re-rotates each moved K by -n_discard (f16 -> f32, Rope::rotate, f32 -> f16 RNE); V moves as
+ * is. Returns the new cur_pos. */
+int or_shift_kv(uint16_t *k_cache, uint16_t *v_cache, int n_layers, int max_seq, int kv_dim, int head_dim, int neox,
+                const float *inv_freq, int n_keep, int n_discard, int cur_pos);
+/* ensure_kv_room (:2924-2940): when cur_pos + needed > max_seq, discards max(overflow, half of
+ * the unpinned context), at most all of it; returns the new cur_pos. */
+int or_ensure_kv_room(or_model *m, int n_keep, int cur_pos, int needed);
 /* forward_batch_slice: m tokens at start_pos (m==1 delegates to forward_slice) */
 int or_forward_batch(or_model *m, const int *ids, int n, int start_pos, float *hidden);
 /* LM head: matvec (n==1) or matvec_multi (smollm_chat.rs:3560-3602) */
@@ -177,6 +186,7 @@ typedef struct {
   int adaptive_k;  /* k_dyn growth after full accepts (:4343) */
   int prefill_chunk;
   int n_cached;    /* prompt tokens already in the KV cache (positions 0..n_cached-1) */
+  int kv_keep;     /* n_keep: positions the sliding window never evicts */
 } or_gen_params;
 
 typedef struct { int accepted, drafted, verifies, steps; } or_gen_stats;

@@ -44,6 +44,8 @@ SIGNATURES = {
     "spx_engine_debug_read": (C.c_int, [P, C.c_char_p, P, I64]),
     "spx_engine_expert_counts": (C.c_int, [P, P]),
     "spx_engine_kv_download": (C.c_int, [P, P, P]),
+    "spx_engine_shift_kv": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int)]),
+    "spx_engine_ensure_kv_room": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int)]),
     "spx_engine_destroy": (C.c_int, [P]),
     "spx_lookup_draft": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int, C.c_int, C.c_int, P, P]),
     "spx_engine_generate": (C.c_int, [P, P, C.c_int, C.c_int, P, P, P]),

@@ -25,6 +25,7 @@
 #include "fused.h"
 #include "internal.h"
 #include "persist.h"
+#include "kv.h"
 #include "sample.h"
 #include "spec.h"
 
@@ -88,6 +89,9 @@ struct spx_engine {
   std::vector<PLayer> players;  // the layers' tensors, passed to each layer's launch
   int *perr_host = nullptr;  // pinned: the launch's error word, copied back with the pick
   std::unique_ptr<spx::Sampler> smp;  // spx_engine_generate's sampler (none: plain greedy)
+  std::vector<float> inv_freq;        // RoPE inverse frequencies (host), for the window's slide
+  __half *kv_stage = nullptr;         // the slide's staging rows (allocated at the first slide)
+  float2 *kv_cs = nullptr;
   std::vector<void *> allocs;
   // device state
   __half *kc = nullptr, *vc = nullptr;
@@ -882,6 +886,7 @@ int spx_engine_prepare(spx_engine *E) {
   std::vector<float2> tab((size_t)c.max_seq * half);
   std::vector<float> inv(half);
   for (int i = 0; i < half; i++) inv[i] = 1.0f / powf(c.rope_theta, 2.0f * (float)i / (float)c.head_dim);
+  E->inv_freq = inv;
   for (int p = 0; p < c.max_seq; p++)
     for (int i = 0; i < half; i++) {
       const float ang = (float)p * inv[i];
@@ -1179,6 +1184,58 @@ void remember(std::vector<int32_t> &corpus, const int32_t *ids, int n) {
 
 extern "C" {
 
+// shift_kv (:2944-2971): n_discard (at most cur_pos - n_keep) positions after the n_keep pinned
+// ones leave the window; the rest move down with their keys re-rotated by -n_discard.
+int spx_engine_shift_kv(spx_engine *E, int n_keep, int n_discard, int cur_pos, int *new_pos) {
+  if (!E || !new_pos) return fail("spx_engine_shift_kv: null argument");
+  if (!E->prepared) return fail("spx_engine_shift_kv: call spx_engine_prepare first");
+  if (n_keep < 0 || cur_pos < 0 || cur_pos > E->c.max_seq || n_discard < 0) return fail("spx_engine_shift_kv: bad positions");
+  const int n_ctx = cur_pos > n_keep ? cur_pos - n_keep : 0;
+  n_discard = std::min(n_discard, n_ctx);
+  *new_pos = cur_pos;
+  if (n_discard == 0) return 0;
+  const auto &c = E->c;
+  SPX_HIP(hipSetDevice(E->ctx->device));
+  if (!E->kv_stage) {
+    if (!(E->kv_stage = E->dalloc<__half>((size_t)2 * c.n_layers * c.max_seq * E->kv_dim)) ||
+        !(E->kv_cs = E->dalloc<float2>((size_t)c.head_dim / 2)))
+      return fail("out of device memory for the KV window's slide");
+  }
+  // Rope::rotate's angle (pos * inv_freq, f32) at pos = -n_discard, sin / cos in f32
+  const int half = c.head_dim / 2;
+  std::vector<float2> cs(half);
+  for (int i = 0; i < half; i++) {
+    const float ang = -(float)n_discard * E->inv_freq[i];
+    cs[i] = make_float2(cosf(ang), sinf(ang));
+  }
+  hipStream_t s = E->ctx->stream;
+  SPX_HIP(hipMemcpyAsync(E->kv_cs, cs.data(), sizeof(float2) * half, hipMemcpyHostToDevice, s));
+  KVShiftArgs a{};
+  a.kc = E->kc; a.vc = E->vc;
+  a.kt = E->kv_stage; a.vt = E->kv_stage + (size_t)c.n_layers * c.max_seq * E->kv_dim;
+  a.cs = E->kv_cs;
+  a.n_layers = c.n_layers; a.max_seq = c.max_seq; a.kv_dim = E->kv_dim; a.head_dim = c.head_dim; a.neox = c.rope_neox;
+  a.n_keep = n_keep; a.n_discard = n_discard; a.n_move = n_ctx - n_discard;
+  SPX_HIP(launch_kv_shift(a, s));
+  SPX_HIP(hipStreamSynchronize(s));  // the host copy of cs goes out of scope
+  *new_pos = cur_pos - n_discard;
+  return 0;
+}
+
+// ensure_kv_room (:2924-2940): when cur_pos + needed passes max_seq, slides the window by the
+// overflow or half the unpinned context, whichever is more (at most all of it).
+int spx_engine_ensure_kv_room(spx_engine *E, int n_keep, int cur_pos, int needed, int *new_pos) {
+  if (!E || !new_pos) return fail("spx_engine_ensure_kv_room: null argument");
+  if (needed < 0 || cur_pos < 0) return fail("spx_engine_ensure_kv_room: bad positions");
+  *new_pos = cur_pos;
+  if (cur_pos + needed <= E->c.max_seq) return 0;
+  const int n_ctx = cur_pos - n_keep;
+  const int want = std::max(cur_pos + needed - E->c.max_seq, n_ctx / 2);
+  if (int r = spx_engine_shift_kv(E, n_keep, std::min(want, std::max(n_ctx, 0)), cur_pos, new_pos)) return r;
+  if (*new_pos + needed > E->c.max_seq) return fail("spx_engine_ensure_kv_room: the pinned positions leave no room");
+  return 0;
+}
+
 int spx_engine_set_sampler(spx_engine *E, const spx_sampler_params *p) {
   if (!E) return fail("spx_engine_set_sampler: null engine");
   if (!p) {
@@ -1200,7 +1257,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
                         spx_gen_stats *st) {
   if (!E || !prompt || !p || !out || !st) return fail("spx_engine_generate: null argument");
   if (n_prompt < 1 || max_new < 1) return fail("spx_engine_generate: empty prompt or max_new < 1");
-  if (n_prompt + max_new + MAX_M > E->c.max_seq) return fail("spx_engine_generate: prompt + max_new exceeds max_seq");
+  if (p->kv_keep < 0 || p->kv_keep + 2 * MAX_M > E->c.max_seq) return fail("spx_engine_generate: kv_keep must leave room for a pass");
   if (p->speculate && (p->draft_len < 1 || p->draft_len > MAX_M - 1)) return fail("spx_engine_generate: draft_len must be in 1..15");
   if (p->n_cached < 0 || p->n_cached >= n_prompt) return fail("spx_engine_generate: n_cached must be in 0..n_prompt-1");
   memset(st, 0, sizeof(*st));
@@ -1212,6 +1269,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
   int64_t t0 = now_us();
   for (int s = p->n_cached; s < n_prompt; s += chunk) {  // feed (:3041-3104)
     const int cnt = std::min(chunk, n_prompt - s);
+    if (int r = spx_engine_ensure_kv_room(E, p->kv_keep, pos, cnt, &pos)) return r;  // feed (:3089-3090)
     if (int r = spx_engine_forward(E, prompt + s, cnt, pos, nullptr, nullptr, am)) return r;
     pos += cnt;
   }
@@ -1252,6 +1310,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     nd = sm.best_len(cls, nd);
     if (skip > 0) skip--;
     if (nd == 0) {
+      if (int r = spx_engine_ensure_kv_room(E, p->kv_keep, pos, 1, &pos)) return r;  // (:4283)
       const int64_t ts = now_us();
       if (int r = spx_engine_forward(E, &tok, 1, pos, nullptr, nullptr, am)) return r;
       const double us = (double)(now_us() - ts);
@@ -1269,6 +1328,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     int32_t batch[MAX_M];
     batch[0] = tok;
     memcpy(batch + 1, draft, sizeof(int32_t) * nd);
+    if (int r = spx_engine_ensure_kv_room(E, p->kv_keep, pos, nd + 1, &pos)) return r;  // (:4298)
     const int start = pos;
     const int64_t tv = now_us();
     if (int r = spx_engine_forward(E, batch, nd + 1, start, nullptr, nullptr, am)) return r;

@@ -200,7 +200,8 @@ class ModelConfigC(C.Structure):
 
 
 class GenParams(C.Structure):
-    _fields_ = [(n, C.c_int) for n in ("draft_len", "min_ngram", "max_ngram", "fixed", "speculate", "adaptive_k", "prefill_chunk", "n_cached")]
+    _fields_ = [(n, C.c_int) for n in ("draft_len", "min_ngram", "max_ngram", "fixed", "speculate", "adaptive_k", "prefill_chunk", "n_cached",
+                                       "kv_keep")]
 
 
 class GenStats(C.Structure):
@@ -277,16 +278,37 @@ class Engine:
         return self.forward(ids, start_pos, hidden=True)[1]
 
     def generate(self, prompt, max_new, draft_len=8, min_ngram=2, max_ngram=4, fixed=False, speculate=True,
-                 adaptive_k=True, prefill_chunk=16, n_cached=0):
+                 adaptive_k=True, prefill_chunk=16, n_cached=0, kv_keep=0):
         prompt = np.ascontiguousarray(prompt, np.int32)
         out = np.empty(max_new, np.int32)
-        gp = GenParams(draft_len, min_ngram, max_ngram, int(fixed), int(speculate), int(adaptive_k), prefill_chunk, n_cached)
+        gp = GenParams(draft_len, min_ngram, max_ngram, int(fixed), int(speculate), int(adaptive_k), prefill_chunk, n_cached,
+                       kv_keep)
         st = GenStats()
         n = lib.spx_engine_generate(self.h, prompt.ctypes.data_as(P), prompt.size, max_new, C.byref(gp),
                                     out.ctypes.data_as(P), C.byref(st))
         if n < 0:
             check(n)
         return out[:n], {k: getattr(st, k) for k, _ in GenStats._fields_}
+
+    def shift_kv(self, n_keep, n_discard, cur_pos):
+        """shift_kv: returns the next position."""
+        v = C.c_int()
+        check(lib.spx_engine_shift_kv(self.h, n_keep, n_discard, cur_pos, C.byref(v)))
+        return v.value
+
+    def ensure_kv_room(self, n_keep, cur_pos, needed):
+        """ensure_kv_room: returns the next position."""
+        v = C.c_int()
+        check(lib.spx_engine_ensure_kv_room(self.h, n_keep, cur_pos, needed, C.byref(v)))
+        return v.value
+
+    def kv_download(self):
+        """The f16 K and V caches as uint16 arrays [n_layers][max_seq][kv_dim]."""
+        c = self.cfg
+        k = np.empty((c.n_layers, c.max_seq, c.kv_dim), np.uint16)
+        v = np.empty_like(k)
+        check(lib.spx_engine_kv_download(self.h, k.ctypes.data_as(P), v.ctypes.data_as(P)))
+        return k, v
 
     def set_sampler(self, **kw):
         """The sampler generate() draws with (ops.sampler_params keywords: temperature, top_k,

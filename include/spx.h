@@ -83,6 +83,17 @@ int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, in
 int spx_matvec_noalloc(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, int64_t ld_x,
                        int m, float *out, int64_t ld_out);
 
+/* The routed experts of a MoE layer with the routing given (ffns_fused smollm_chat.rs:379-442
+ * for m == 1; moe_batch_fused :650-760 with moe_forward_batch's combine :1133-1140 for m <= 16):
+ * y[b] = sum over j < k, in j order, of weights[b*k + j] * FFN_e(x_b), e = chosen[b*k + j]
+ * (each row's experts distinct), FFN_e = down_e(silu(gate_e x) * up_e x), each product and sum
+ * rounded separately from 0. gate / up: [n_expert][n_ff][dim] (one format), down:
+ * [n_expert][dim][n_ff]; K-quant matrices take Q8_K activations (x, then h), the others fp32.
+ * x, y: device rows at x + b*ld_x, y + b*ld_y; chosen / weights: host arrays, read before the
+ * call returns. m * k <= 256, k <= 32. Each row's result does not depend on the others. */
+int spx_moe(spx_ctx *ctx, const spx_tensor *gate, const spx_tensor *up, const spx_tensor *down, const float *x,
+            int64_t ld_x, int m, int k, const int32_t *chosen, const float *weights, float *y, int64_t ld_y);
+
 /* ------------------------------------------------------------------ synthetic weights */
 /* Seeded synthetic tensor in GGUF block layout (n_expert slabs of rows x cols). kind 0:
  * quantized weights (Q4_K/Q6_K/Q8_0/Q5_0) whose dequantised values have std sigma; kind 1:
@@ -169,6 +180,14 @@ int spx_engine_debug_read(spx_engine *e, const char *what, void *host, int64_t b
 int spx_engine_last_experts(spx_engine *e, int32_t *njobs_per_layer);
 /* Per layer and expert: passes that selected the expert since prepare ([n_layers][n_expert]). */
 int spx_engine_expert_counts(spx_engine *e, int32_t *counts);
+/* The attention block of a pass (forward_batch_slice :3226-3300; forward_slice :3432-3470) for
+ * m <= 16 rows at positions start_pos.. of one layer, on the engine's KV cache: q [m][q_dim],
+ * k / v [m][kv_dim] are the projections' outputs (device); biases, per-head Q/K RMSNorm and
+ * RoPE are applied, the rows' K / V written to the cache (f16 RNE), then row b attends to
+ * positions <= start_pos + b; att [m][q_dim] (device) gets the heads' outputs. The same
+ * kernels and bits as inside spx_engine_forward. */
+int spx_engine_attention(spx_engine *e, int layer, const float *q, const float *k, const float *v, int m,
+                         int start_pos, float *att);
 /* The KV window (shift_kv :2944-2971, ensure_kv_room :2924-2940): shift_kv drops n_discard
  * positions (at most cur_pos - n_keep) after the n_keep pinned ones, moves the rest down and
  * re-rotates their keys by -n_discard (f16 -> f32 -> RoPE -> f16 RNE; values move as they are);

@@ -29,6 +29,7 @@ SIGNATURES = {
     "spx_block_sums_q8k": (C.c_int, [P, P, C.c_int, I64, P, P, P]),
     "spx_matvec": (C.c_int, [P, P, C.c_int, P, I64, C.c_int, P, I64]),
     "spx_matvec_noalloc": (C.c_int, [P, P, C.c_int, P, I64, C.c_int, P, I64]),
+    "spx_moe": (C.c_int, [P, P, P, P, P, I64, C.c_int, C.c_int, P, P, P, I64]),
     "spx_synth_tensor": (C.c_int, [C.c_int, I64, I64, C.c_int, C.c_uint64, C.c_float, C.c_int, P]),
     "spx_engine_create": (C.c_int, [P, P, C.POINTER(P)]),
     "spx_engine_set_tensor": (C.c_int, [P, C.c_char_p, C.c_int, I64, I64, C.c_int, P]),
@@ -44,6 +45,7 @@ SIGNATURES = {
     "spx_engine_debug_read": (C.c_int, [P, C.c_char_p, P, I64]),
     "spx_engine_expert_counts": (C.c_int, [P, P]),
     "spx_engine_kv_download": (C.c_int, [P, P, P]),
+    "spx_engine_attention": (C.c_int, [P, C.c_int, P, P, P, C.c_int, C.c_int, P]),
     "spx_engine_shift_kv": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int)]),
     "spx_engine_ensure_kv_room": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int)]),
     "spx_engine_destroy": (C.c_int, [P]),

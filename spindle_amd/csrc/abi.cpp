@@ -404,3 +404,106 @@ int spx_matvec_noalloc(spx_ctx *ctx, const spx_tensor *w, int expert, const floa
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------------ routed experts
+// ffns_fused (smollm_chat.rs:379-442) for one row and moe_batch_fused (:650-760) plus
+// moe_forward_batch's combine (:1133-1140) for 2..16 rows, with the routing given: the pass
+// kernels' gate/up + SwiGLU (+ Q8_K of h) and down + combine over jobs built here the way the
+// router kernel builds them (experts in index order, users in row order, gate/up jobs of at
+// most GU_USERS users).
+namespace {
+struct MoeHost {  // copied to the device in one piece
+  Job jobs[512];
+  int njobs[2];
+  int nkeep[MAX_M];
+  float weights[MAX_M * 32];
+  StepRec st;
+};
+size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+}  // namespace
+
+extern "C" int spx_moe(spx_ctx *ctx, const spx_tensor *gate, const spx_tensor *up, const spx_tensor *down, const float *x,
+                       int64_t ld_x, int m, int k, const int32_t *chosen, const float *weights, float *y, int64_t ld_y) {
+  if (!ctx || !gate || !up || !down || !x || !chosen || !weights || !y) return fail("spx_moe: null argument");
+  if (m < 1 || m > MAX_M || k < 1 || k > 32 || m * k > 256) return fail("spx_moe: m must be in 1..16, k in 1..32, m * k <= 256");
+  const int64_t dim = gate->v.cols, n_ff = gate->v.rows;
+  const int ne = gate->v.n_expert;
+  if (up->v.cols != dim || up->v.rows != n_ff || up->v.n_expert != ne || down->v.cols != n_ff || down->v.rows != dim ||
+      down->v.n_expert != ne)
+    return fail("spx_moe: gate/up must be [n_expert][n_ff][dim] and down [n_expert][dim][n_ff]");
+  if (gate->v.dtype != up->v.dtype) return fail("spx_moe: gate and up must share a format");
+  const bool g_int = gate->v.dtype == T_Q4K || gate->v.dtype == T_Q6K, d_int = down->v.dtype == T_Q4K || down->v.dtype == T_Q6K;
+  if (n_ff % 16 || (d_int && n_ff % 256) || (g_int && dim % 256) || dim % 4) return fail("spx_moe: unsupported widths");
+  if (ld_x < dim || ld_y < dim || ld_x % 4) return fail("spx_moe: leading dimension too small (or ld_x not a multiple of 4)");
+  MoeHost hb;
+  memset(&hb, 0, sizeof hb);
+  std::vector<std::vector<int>> slot_of(m, std::vector<int>(ne, -1));
+  for (int b = 0; b < m; b++)
+    for (int s = 0; s < k; s++) {
+      const int e = chosen[b * k + s];
+      if (e < 0 || e >= ne) return fail("spx_moe: expert id out of range");
+      if (slot_of[b][e] >= 0) return fail("spx_moe: a row chooses an expert twice");
+      slot_of[b][e] = s;
+      hb.weights[b * 32 + s] = weights[b * k + s];
+    }
+  int nd = 0, ng = 0;
+  for (int e = 0; e < ne; e++) {
+    Job &Jd = hb.jobs[256 + nd];
+    int kk = 0, ks = 0;
+    for (int b = 0; b < m; b++) {
+      const int s = slot_of[b][e];
+      if (s < 0) continue;
+      Jd.vec[kk] = Jd.out[kk] = b * k + s;
+      kk++;
+      Job &J = hb.jobs[ng];
+      J.vec[ks] = b;
+      J.out[ks] = b * k + s;
+      if (++ks == GU_USERS) { J.expert = e; J.nvec = ks; ng++; ks = 0; }
+    }
+    if (ks > 0) { hb.jobs[ng].expert = e; hb.jobs[ng].nvec = ks; ng++; }
+    if (kk > 0) { Jd.expert = e; Jd.nvec = kk; nd++; }
+  }
+  hb.njobs[0] = nd;
+  hb.njobs[1] = ng;
+  for (int b = 0; b < m; b++) hb.nkeep[b] = k;
+  hb.st.m = m;
+  // workspace: host block, x (packed), y (Q8_K), h, hq, gate/up counters, output rows
+  const int nv = m * k, nbh = (int)(n_ff / 256);
+  size_t yq_b = 0, hq_b = 0;
+  (void)q8kp_layout(nullptr, m, dim, &yq_b);
+  (void)q8kp_layout(nullptr, nv, n_ff, &hq_b);
+  const size_t cnt_b = sizeof(int) * (size_t)nv * std::max(nbh, 1) * (1 + GU_SUB) * CNT_STRIDE;
+  const size_t sz[7] = {al256(sizeof hb), al256(sizeof(float) * m * dim), al256(g_int ? yq_b : 0), al256(sizeof(float) * nv * n_ff),
+                        al256(d_int ? hq_b : 0), al256(cnt_b), al256(sizeof(float) * m * dim)};
+  size_t tot = 0;
+  for (size_t v : sz) tot += v;
+  uint8_t *w = static_cast<uint8_t *>(ws_get(ctx, tot));
+  if (!w) return fail("spx_moe: workspace allocation failed");
+  uint8_t *p[7];
+  for (int i = 0, o = 0; i < 7; o += (int)sz[i], i++) p[i] = w + o;
+  hipStream_t s = ctx->stream;
+  SPX_HIP(hipMemcpyAsync(p[0], &hb, sizeof hb, hipMemcpyHostToDevice, s));
+  SPX_HIP(hipStreamSynchronize(s));  // chosen / weights consumed before return
+  const MoeHost *dh = reinterpret_cast<const MoeHost *>(p[0]);
+  float *xp = reinterpret_cast<float *>(p[1]), *h = reinterpret_cast<float *>(p[3]), *out = reinterpret_cast<float *>(p[6]);
+  int *cnt = reinterpret_cast<int *>(p[5]);
+  SPX_HIP(hipMemcpy2DAsync(xp, sizeof(float) * dim, x, sizeof(float) * ld_x, sizeof(float) * dim, m, hipMemcpyDeviceToDevice, s));
+  SPX_HIP(hipMemsetAsync(cnt, 0, cnt_b, s));
+  Q8KP yq{}, hq{};
+  if (g_int) {
+    yq = q8kp_layout(p[2], m, dim, &yq_b);
+    SPX_HIP(launch_q8kp_quantize(xp, dim, dim, m, yq, s));
+  }
+  if (d_int) hq = q8kp_layout(p[4], nv, n_ff, &hq_b);
+  GUArgs ga{};
+  ga.gate = gate->v; ga.up = up->v; ga.y = yq; ga.x = xp; ga.jobs = dh->jobs; ga.njobs = dh->njobs + 1; ga.h = h;
+  ga.counter = cnt; ga.n_ff = (int)n_ff;
+  if (d_int) ga.hq = hq;
+  SPX_HIP(launch_gateup(ga, std::min(m, GU_USERS), g_int ? 1 : 0, &dh->st, std::min(256, nv), s));
+  DownArgs da{};
+  da.w = down->v; da.y = hq; da.x = h; da.jobs = dh->jobs + 256; da.njobs = dh->njobs; da.weights = dh->weights;
+  da.nkeep = dh->nkeep; da.n_used = k; da.out = out;
+  SPX_HIP(launch_down(da, m, 0, &dh->st, s));
+  SPX_HIP(hipMemcpy2DAsync(y, sizeof(float) * ld_y, out, sizeof(float) * dim, sizeof(float) * dim, m, hipMemcpyDeviceToDevice, s));
+  return 0;
+}

@@ -1184,6 +1184,37 @@ void remember(std::vector<int32_t> &corpus, const int32_t *ids, int n) {
 
 extern "C" {
 
+// The attention block of a pass (forward_batch_slice :3226-3300, forward_slice :3432-3470) for
+// m rows at start_pos..start_pos+m-1 of layer `layer`: q / k / v are the projections' outputs
+// (device [m][q_dim], [m][kv_dim], [m][kv_dim]); biases, Q/K RMSNorm and RoPE are applied here,
+// the rows' K / V written to the cache, and each row attends causally to positions <= its own.
+int spx_engine_attention(spx_engine *E, int layer, const float *q, const float *k, const float *v, int m, int start_pos, float *att) {
+  if (!E || !q || !k || !v || !att) return fail("spx_engine_attention: null argument");
+  if (!E->prepared) return fail("spx_engine_attention: call spx_engine_prepare first");
+  if (layer < 0 || layer >= E->c.n_layers) return fail("spx_engine_attention: layer out of range");
+  if (m < 1 || m > MAX_M || start_pos < 0 || start_pos + m > E->c.max_seq) return fail("spx_engine_attention: rows / positions out of range");
+  const auto &c = E->c;
+  const LayerW &ly = E->L[layer];
+  const int hd = c.head_dim;
+  hipStream_t s = E->ctx->stream;
+  SPX_HIP(hipSetDevice(E->ctx->device));
+  SPX_HIP(hipStreamSynchronize(s));
+  E->st_host->m = m;
+  E->st_host->start = start_pos;
+  E->st_host->step = 0;
+  SPX_HIP(hipMemcpyAsync(E->st_dev, E->st_host, sizeof(StepRec), hipMemcpyHostToDevice, s));
+  AttnArgs aa{};
+  aa.q = q; aa.k = k; aa.v = v;
+  aa.q_bias = ly.q_bias; aa.k_bias = ly.k_bias; aa.v_bias = ly.v_bias; aa.q_norm = ly.q_norm; aa.k_norm = ly.k_norm;
+  aa.rope = E->rope; aa.kc = E->kc; aa.vc = E->vc; aa.part_ml = E->part_ml; aa.part_o = E->part_o; aa.counter = E->att_cnt; aa.att = att;
+  aa.layer = layer; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
+  aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
+  aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
+  SPX_HIP(launch_attention(aa, m, E->st_dev, s));
+  SPX_HIP(hipStreamSynchronize(s));  // the step record is the engine's
+  return 0;
+}
+
 // shift_kv (:2944-2971): n_discard (at most cur_pos - n_keep) positions after the n_keep pinned
 // ones leave the window; the rest move down with their keys re-rotated by -n_discard.
 int spx_engine_shift_kv(spx_engine *E, int n_keep, int n_discard, int cur_pos, int *new_pos) {

@@ -290,6 +290,19 @@ class Engine:
             check(n)
         return out[:n], {k: getattr(st, k) for k, _ in GenStats._fields_}
 
+    def attention(self, layer, q, k, v, start_pos):
+        """The attention block for rows of projections q [m, q_dim], k / v [m, kv_dim] (float32
+        cuda tensors) at start_pos..; writes their K / V to the cache; returns att [m, q_dim]."""
+        import torch
+        m = q.shape[0]
+        att = torch.empty((m, self.cfg.q_dim), dtype=torch.float32, device=q.device)
+        for t in (q, k, v):
+            assert t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()
+        torch.cuda.synchronize()  # inputs written on torch's stream; the engine runs on its context's
+        check(lib.spx_engine_attention(self.h, layer, P(q.data_ptr()), P(k.data_ptr()), P(v.data_ptr()), m, start_pos,
+                                       P(att.data_ptr())))
+        return att
+
     def shift_kv(self, n_keep, n_discard, cur_pos):
         """shift_kv: returns the next position."""
         v = C.c_int()

@@ -147,6 +147,21 @@ def matvec_noalloc(ctx, w, x, expert=0):
 matvec_multi = matvec
 
 
+def moe(ctx, gate, up, down, x, chosen, weights):
+    """ffns_fused / moe_batch_fused with the combine: x [m, dim] float32 cuda; chosen, weights
+    [m, k] host arrays (each row's experts distinct). Returns y [m, dim]."""
+    assert x.is_cuda and x.dtype == torch.float32 and x.dim() == 2
+    ch = np.ascontiguousarray(chosen, np.int32)
+    wt = np.ascontiguousarray(weights, np.float32)
+    m, k = ch.shape
+    y = torch.empty((m, down.rows), dtype=torch.float32, device=x.device)
+    torch.cuda.synchronize()  # x is written on torch's stream, the library runs on the context's
+    check(lib.spx_moe(ctx.h, gate.h, up.h, down.h, _p(x), x.stride(0), m, k, ch.ctypes.data_as(P), wt.ctypes.data_as(P),
+                      _p(y), y.stride(0)))
+    ctx.sync()
+    return y
+
+
 class SamplerParams(C.Structure):
     """spx_sampler_params (SamplerConfig, smollm_chat.rs:1523-1555)."""
     _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("min_p", C.c_float),
@@ -181,6 +196,7 @@ class Sampler:
         assert logits.is_cuda and logits.dtype == torch.float32 and logits.numel() == self.vocab and logits.is_contiguous()
         rc = np.ascontiguousarray(np.asarray(recent, np.int32).reshape(-1))
         tok = C.c_int32()
+        torch.cuda.synchronize()
         check(lib.spx_sample(self.h, _p(logits), logit_scale, rc.ctypes.data_as(P) if rc.size else None, rc.size,
                              int(forbid_stop), int(forbid_think), C.byref(tok)))
         return tok.value
@@ -192,6 +208,7 @@ class Sampler:
         dr = np.ascontiguousarray(np.asarray(draft, np.int32).reshape(-1))
         toks = np.empty(dr.size + 1, np.int32)
         n = C.c_int()
+        torch.cuda.synchronize()
         check(lib.spx_sample_verify(self.h, _p(logits), logits.stride(0), dr.size, logit_scale,
                                     rc.ctypes.data_as(P) if rc.size else None, rc.size,
                                     dr.ctypes.data_as(P) if dr.size else None, generated, max_accept,

@@ -331,6 +331,14 @@ int spx_sample_verify(spx_sampler *s, const float *logits, int64_t ld, int n_dra
  * calls like the reference's engine); NULL: plain greedy, no penalty, no stop ids. */
 int spx_engine_set_sampler(spx_engine *e, const spx_sampler_params *p);
 
+/* A draft model for spx_engine_generate (draft_engine, generate_reply :4244-4269; NULL: prompt
+ * lookup). The draft engine is fed the same prompt; before each verify it catches up on the
+ * committed tokens it has not seen, one pass each, then proposes up to k tokens with its own
+ * pick (greedy, or its sampler with no penalty window), stopping at its stop ids; after the
+ * verify its position falls back to the committed tokens. Drafting stops for the rest of a
+ * reply once either window slides. The engine must outlive its use here. */
+int spx_engine_set_draft(spx_engine *e, spx_engine *draft);
+
 /* Generation with prompt-lookup speculation (generate_reply's loop :4205-4348 minus chat
  * framing): feeds the prompt from position n_cached, writes up to max_new tokens to out and
  * returns how many. Tokens come from the engine's sampler (spx_engine_set_sampler) over the

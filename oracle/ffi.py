@@ -125,6 +125,8 @@ _sig("or_spec_record_step", None, C.POINTER(SpecModel), C.c_uint64)
 _sig("or_spec_record_verify", None, C.POINTER(SpecModel), C.c_int, C.c_uint64)
 _sig("or_generate", C.c_int, C.POINTER(Model), P, C.c_int, C.c_int, C.POINTER(GenParams), P, C.POINTER(GenStats))
 _sig("or_generate_sampled", C.c_int, C.POINTER(Model), P, C.c_int, C.c_int, C.POINTER(GenParams), C.POINTER(Sampler), P, C.POINTER(GenStats))
+_sig("or_generate_full", C.c_int, C.POINTER(Model), C.POINTER(Model), P, C.c_int, C.c_int, C.POINTER(GenParams), C.POINTER(Sampler), P,
+     C.POINTER(GenStats))
 _sig("or_sampler_init", None, C.POINTER(Sampler), C.POINTER(SamplerParams))
 _sig("or_splitmix_next", C.c_uint64, C.POINTER(C.c_uint64))
 _sig("or_splitmix_f32", C.c_float, C.POINTER(C.c_uint64))

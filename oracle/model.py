@@ -77,14 +77,19 @@ class OracleModel:
         return ffi.lib.or_argmax(lg.ctypes.data_as(C.c_void_p), lg.size, self.cfg.logit_scale)
 
     def generate(self, prompt, max_new, draft_len=8, min_ngram=2, max_ngram=4, fixed=False, speculate=True,
-                 adaptive_k=True, prefill_chunk=16, n_cached=0, sampler=None, kv_keep=0):
-        """sampler: an ffi.OracleSampler (its SplitMix64 state advances), or None for greedy."""
+                 adaptive_k=True, prefill_chunk=16, n_cached=0, sampler=None, kv_keep=0, draft=None):
+        """sampler: an ffi.OracleSampler (its SplitMix64 state advances), or None for greedy;
+        draft: an OracleModel drafting instead of the prompt lookup."""
         prompt = np.ascontiguousarray(prompt, np.int32)
         out = np.empty(max_new, np.int32)
         gp = ffi.GenParams(draft_len, min_ngram, max_ngram, int(fixed), int(speculate), int(adaptive_k), prefill_chunk, n_cached,
                            kv_keep)
         st = ffi.GenStats()
-        if sampler is not None:
+        if draft is not None:
+            n = ffi.lib.or_generate_full(C.byref(self.m), C.byref(draft.m), prompt.ctypes.data_as(C.c_void_p), prompt.size, max_new,
+                                         C.byref(gp), C.byref(sampler.s) if sampler is not None else None,
+                                         out.ctypes.data_as(C.c_void_p), C.byref(st))
+        elif sampler is not None:
             n = ffi.lib.or_generate_sampled(C.byref(self.m), prompt.ctypes.data_as(C.c_void_p), prompt.size, max_new,
                                             C.byref(gp), C.byref(sampler.s), out.ctypes.data_as(C.c_void_p), C.byref(st))
         else:

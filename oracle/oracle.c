@@ -1149,6 +1149,11 @@ int or_generate(or_model *m, const int *prompt, int n_prompt, int max_new, const
 
 int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_new, const or_gen_params *p,
                         or_sampler *sp, int *out, or_gen_stats *st) {
+  return or_generate_full(m, NULL, prompt, n_prompt, max_new, p, sp, out, st);
+}
+
+int or_generate_full(or_model *m, or_model *dm, const int *prompt, int n_prompt, int max_new, const or_gen_params *p,
+                     or_sampler *sp, int *out, or_gen_stats *st) {
   const or_config *c = &m->c;
   int dim = c->dim, vocab = c->vocab, chunk = p->prefill_chunk > 0 ? p->prefill_chunk : 128;
   const int *stop = sp ? sp->p.stop_ids : NULL, n_stop = sp ? sp->p.n_stop : 0;
@@ -1167,7 +1172,19 @@ int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_ne
     memcpy(hid, hbuf + (size_t)(cnt - 1) * dim, 4 * dim);
     pos += cnt;
   }
+  /* the draft model is fed the same turn (:4141-4143) */
+  int d_pos = p->n_cached, shifted = 0;
+  float *dhid = dm ? malloc(sizeof(float) * dm->c.dim * 17) : NULL, *dlog = dm ? malloc(sizeof(float) * (size_t)dm->c.vocab) : NULL;
+  if (dm) {
+    for (int s = p->n_cached; s < n_prompt; s += chunk) {
+      int cnt = n_prompt - s < chunk ? n_prompt - s : chunk;
+      d_pos = or_ensure_kv_room(dm, p->kv_keep, d_pos, cnt);
+      if (or_forward_batch(dm, prompt + s, cnt, d_pos, hbuf)) return -1;
+      d_pos += cnt;
+    }
+  }
   free(hbuf);
+  int reply_start = pos;
   or_logits(m, hid, 1, logits);
   int gen = 0, tok = gen_pick(m, sp, logits, out, gen);
   or_spec_model sm; or_spec_init(&sm, p->fixed);
@@ -1177,15 +1194,41 @@ int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_ne
     out[gen++] = tok; remember(corpus, &nc, &tok, 1);           /* emit! */
     if (gen >= max_new) break;
     int budget = max_new - gen, k = k_dyn < budget - 1 ? k_dyn : budget - 1;
-    int draft[64], nd = 0, cls = 3;
-    if (p->speculate && k > 0) {
-      int d[64], ng = 0, len = or_lookup_draft(corpus, nc, k, stop, n_stop, p->min_ngram, p->max_ngram, d, &ng);
-      if (skip == 0 || ng > 2) /* weak = 2-gram (:4274) */ { memcpy(draft, d, sizeof(int) * len); nd = len; cls = or_spec_class(ng); }
+    int draft[64], nd = 0, cls = 3, use_lookup = p->speculate && !dm;
+    if (k > 0 && (skip == 0 || use_lookup)) {
+      if (dm) { /* draft_engine :4244-4269, greedy draft picks */
+        if (!shifted && d_pos >= reply_start) {
+          int have = 0, dshift = 0, from = d_pos - reply_start < gen ? d_pos - reply_start : gen;
+          for (int i = from; i < gen; i++) {
+            int np = or_ensure_kv_room(dm, p->kv_keep, d_pos, 1);
+            if (np < d_pos) dshift = 1;
+            d_pos = np;
+            if (or_forward_slice(dm, out[i], d_pos, dhid)) return -1;
+            d_pos++; have = 1;
+          }
+          for (int j = 0; have && !dshift && j < k; j++) {
+            or_logits(dm, dhid, 1, dlog);
+            int x = or_argmax(dlog, dm->c.vocab, dm->c.logit_scale);
+            draft[nd++] = x;
+            if (j + 1 < k) {
+              int np = or_ensure_kv_room(dm, p->kv_keep, d_pos, 1);
+              if (np < d_pos) dshift = 1;
+              d_pos = np;
+              if (or_forward_slice(dm, x, d_pos, dhid)) return -1;
+              d_pos++;
+            }
+          }
+          if (dshift) { nd = 0; shifted = 1; }
+        }
+      } else if (use_lookup) {
+        int d[64], ng = 0, len = or_lookup_draft(corpus, nc, k, stop, n_stop, p->min_ngram, p->max_ngram, d, &ng);
+        if (skip == 0 || ng > 2) /* weak = 2-gram (:4274) */ { memcpy(draft, d, sizeof(int) * len); nd = len; cls = or_spec_class(ng); }
+      }
     }
     nd = or_spec_best_len(&sm, cls, nd);
     if (skip > 0) skip--;
     if (nd == 0) {
-      pos = or_ensure_kv_room(m, p->kv_keep, pos, 1); /* :4283 */
+      { int np = or_ensure_kv_room(m, p->kv_keep, pos, 1); if (np < pos) shifted = 1; pos = np; } /* :4283 */
       uint64_t t0 = now_us();
       if (or_forward_slice(m, tok, pos, hid)) return -1;
       pos++;
@@ -1196,7 +1239,7 @@ int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_ne
       continue;
     }
     int batch[65]; batch[0] = tok; memcpy(batch + 1, draft, sizeof(int) * nd);
-    pos = or_ensure_kv_room(m, p->kv_keep, pos, nd + 1); /* :4298 */
+    { int np = or_ensure_kv_room(m, p->kv_keep, pos, nd + 1); if (np < pos) shifted = 1; pos = np; } /* :4298 */
     int start = pos; uint64_t t0 = now_us();
     if (or_forward_batch(m, batch, nd + 1, start, hid)) return -1;
     or_logits(m, hid, nd + 1, logits);
@@ -1213,6 +1256,7 @@ int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_ne
     st->accepted += accepted;
     or_spec_record_draft(&sm, cls, nd, accepted);
     pos = start + 1 + accepted;
+    if (dm && d_pos > reply_start + gen) d_pos = reply_start + gen; /* :4334-4336 */
     if (done) break;
     if (accepted == 0) { backoff = backoff * 2; if (backoff < 1) backoff = 1; if (backoff > 16) backoff = 16; skip = backoff; }
     else backoff = 0;
@@ -1222,6 +1266,6 @@ int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_ne
     }
     tok = correction >= 0 ? correction : gen_pick(m, sp, logits + (size_t)nd * vocab, out, gen);
   }
-  free(corpus); free(hid); free(logits);
+  free(corpus); free(hid); free(logits); free(dhid); free(dlog);
   return gen;
 }

@@ -218,6 +218,10 @@ int or_generate(or_model *m, const int *prompt, int n_prompt, int max_new,
  * ids forbidden while fewer than 2 are out, generation ending before a stop id. */
 int or_generate_sampled(or_model *m, const int *prompt, int n_prompt, int max_new, const or_gen_params *p,
                         or_sampler *s, int *out, or_gen_stats *st);
+/* ... and with a draft model (draft_engine :4244-4269, greedy draft picks) instead of prompt
+ * lookup when draft is not NULL. */
+int or_generate_full(or_model *m, or_model *draft, const int *prompt, int n_prompt, int max_new, const or_gen_params *p,
+                     or_sampler *s, int *out, or_gen_stats *st);
 
 void or_set_threads(int n);
 /* Test knob, off by default: 1 = RMSNorm sums in the GPU kernels' order (sensitivity tests). */

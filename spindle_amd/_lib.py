@@ -57,6 +57,7 @@ SIGNATURES = {
     "spx_sample": (C.c_int, [P, P, C.c_float, P, C.c_int, C.c_int, C.c_int, P]),
     "spx_sample_verify": (C.c_int, [P, P, I64, C.c_int, C.c_float, P, C.c_int, P, C.c_int, C.c_int, C.c_int, P, P]),
     "spx_engine_set_sampler": (C.c_int, [P, P]),
+    "spx_engine_set_draft": (C.c_int, [P, P]),
     "spx_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
     "spx_gguf_close": (C.c_int, [P]),
     "spx_gguf_info": (C.c_int, [P, P, P, P, P, P]),

@@ -89,6 +89,7 @@ struct spx_engine {
   std::vector<PLayer> players;  // the layers' tensors, passed to each layer's launch
   int *perr_host = nullptr;  // pinned: the launch's error word, copied back with the pick
   std::unique_ptr<spx::Sampler> smp;  // spx_engine_generate's sampler (none: plain greedy)
+  spx_engine *draft = nullptr;        // draft model for spx_engine_generate (none: prompt lookup)
   std::vector<float> inv_freq;        // RoPE inverse frequencies (host), for the window's slide
   __half *kv_stage = nullptr;         // the slide's staging rows (allocated at the first slide)
   float2 *kv_cs = nullptr;
@@ -1267,6 +1268,14 @@ int spx_engine_ensure_kv_room(spx_engine *E, int n_keep, int cur_pos, int needed
   return 0;
 }
 
+int spx_engine_set_draft(spx_engine *E, spx_engine *D) {
+  if (!E) return fail("spx_engine_set_draft: null engine");
+  if (D == E) return fail("spx_engine_set_draft: an engine cannot draft for itself");
+  if (D && D->c.vocab != E->c.vocab) return fail("spx_engine_set_draft: the draft model needs the same vocabulary");
+  E->draft = D;
+  return 0;
+}
+
 int spx_engine_set_sampler(spx_engine *E, const spx_sampler_params *p) {
   if (!E) return fail("spx_engine_set_sampler: null engine");
   if (!p) {
@@ -1304,8 +1313,31 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     if (int r = spx_engine_forward(E, prompt + s, cnt, pos, nullptr, nullptr, am)) return r;
     pos += cnt;
   }
-  st->prefill_us = (double)(now_us() - t0);
   const int last_rows = n_prompt - p->n_cached - ((n_prompt - p->n_cached - 1) / chunk) * chunk;  // rows in the last chunk
+  // a draft model is fed the same turn (:4141-4143); drafting stops for the reply once either
+  // engine's window slides after this point (kv_shifts checks :4245, :4255)
+  spx_engine *D = E->draft;
+  int d_pos = p->n_cached;
+  bool shifted = false;
+  if (D) {
+    int32_t dam[MAX_M];
+    for (int s = p->n_cached; s < n_prompt; s += chunk) {
+      const int cnt = std::min(chunk, n_prompt - s);
+      if (int r = spx_engine_ensure_kv_room(D, p->kv_keep, d_pos, cnt, &d_pos)) return r;
+      if (int r = spx_engine_forward(D, prompt + s, cnt, d_pos, nullptr, nullptr, dam)) return r;
+      d_pos += cnt;
+    }
+  }
+  st->prefill_us = (double)(now_us() - t0);
+  const int reply_start = pos;
+  // pos = ensure_kv_room(pos, need), noting a slide of the target's window
+  auto room = [&](int need) -> int {
+    const int before = pos;
+    if (int r = spx_engine_ensure_kv_room(E, p->kv_keep, pos, need, &pos)) return r;
+    if (pos < before) shifted = true;
+    return 0;
+  };
+  spx::Sampler *dsmp = D && D->smp && !D->smp->greedy_plain() ? D->smp.get() : nullptr;
   // the sampler (sample_next_token / sample_from_batch :3574-3621) over the tokens of this
   // reply, stop ids forbidden while fewer than 2 are out (:4220); without one, the greedy picks
   spx::Sampler *smp = E->smp && !E->smp->greedy_plain() ? E->smp.get() : nullptr;
@@ -1332,16 +1364,54 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     const int budget = max_new - gen, k = std::min(k_dyn, budget - 1);
     int32_t draft[MAX_M];
     int nd = 0, cls = 3;
-    if (p->speculate && k > 0) {
-      int32_t d[MAX_M];
-      int ng = 0;
-      const int len = spx_lookup_draft(corpus.data(), (int)corpus.size(), std::min(k, MAX_M - 1), stop, n_stop, p->min_ngram, p->max_ngram, d, &ng);
-      if (skip == 0 || ng > 2) { memcpy(draft, d, sizeof(int32_t) * len); nd = len; cls = spx::SpecModel::cls(ng); }
+    const bool use_lookup = p->speculate && !D;
+    if (k > 0 && (skip == 0 || use_lookup)) {
+      if (D) {  // draft_engine (:4244-4269)
+        if (!shifted && d_pos >= reply_start) {
+          // catch the draft model up on the committed tokens it has not seen (tok at least),
+          // then let it autoregress k proposals (its own greedy pick or sampler, no penalty)
+          bool have = false, dshift = false;
+          int32_t dam[MAX_M];
+          auto dstep = [&](int32_t t) -> int {
+            const int before = d_pos;
+            if (int r = spx_engine_ensure_kv_room(D, p->kv_keep, d_pos, 1, &d_pos)) return r;
+            if (d_pos < before) dshift = true;
+            if (int r = spx_engine_forward(D, &t, 1, d_pos, nullptr, nullptr, dam)) return r;
+            d_pos++;
+            return 0;
+          };
+          for (int i = std::min(d_pos - reply_start, gen); i < gen; i++) {
+            if (int r = dstep(out[i])) return r;
+            have = true;
+          }
+          const int32_t *dstop = dsmp ? dsmp->stop.data() : nullptr;
+          const int n_dstop = dsmp ? (int)dsmp->stop.size() : 0;
+          for (int j = 0; have && !dshift && j < std::min(k, MAX_M - 1); j++) {
+            int32_t x = dam[0];
+            if (dsmp) {
+              if (int r = dsmp->prepare(D->logits, D->c.vocab, 1, D->c.logit_scale, nullptr, 0, 0u, false)) return r;
+              x = dsmp->pick(0);
+            }
+            bool ds = false;
+            for (int q = 0; q < n_dstop; q++) ds |= dstop[q] == x;
+            if (ds) break;
+            draft[nd++] = x;
+            if (j + 1 < k)
+              if (int r = dstep(x)) return r;
+          }
+          if (dshift) nd = 0, shifted = true;  // the draft's window slid: no drafts from here on
+        }
+      } else if (use_lookup) {
+        int32_t d[MAX_M];
+        int ng = 0;
+        const int len = spx_lookup_draft(corpus.data(), (int)corpus.size(), std::min(k, MAX_M - 1), stop, n_stop, p->min_ngram, p->max_ngram, d, &ng);
+        if (skip == 0 || ng > 2) { memcpy(draft, d, sizeof(int32_t) * len); nd = len; cls = spx::SpecModel::cls(ng); }
+      }
     }
     nd = sm.best_len(cls, nd);
     if (skip > 0) skip--;
     if (nd == 0) {
-      if (int r = spx_engine_ensure_kv_room(E, p->kv_keep, pos, 1, &pos)) return r;  // (:4283)
+      if (int r = room(1)) return r;  // (:4283)
       const int64_t ts = now_us();
       if (int r = spx_engine_forward(E, &tok, 1, pos, nullptr, nullptr, am)) return r;
       const double us = (double)(now_us() - ts);
@@ -1359,7 +1429,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     int32_t batch[MAX_M];
     batch[0] = tok;
     memcpy(batch + 1, draft, sizeof(int32_t) * nd);
-    if (int r = spx_engine_ensure_kv_room(E, p->kv_keep, pos, nd + 1, &pos)) return r;  // (:4298)
+    if (int r = room(nd + 1)) return r;  // (:4298)
     const int start = pos;
     const int64_t tv = now_us();
     if (int r = spx_engine_forward(E, batch, nd + 1, start, nullptr, nullptr, am)) return r;
@@ -1389,6 +1459,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     st->accepted += accepted;
     sm.record_draft(cls, nd, accepted);
     pos = start + 1 + accepted;
+    if (D) d_pos = std::min(d_pos, reply_start + gen);  // (:4334-4336)
     if (done) break;
     if (accepted == 0) { backoff = std::min(std::max(backoff * 2, 1), 16); skip = backoff; }
     else backoff = 0;

@@ -323,6 +323,11 @@ class Engine:
         check(lib.spx_engine_kv_download(self.h, k.ctypes.data_as(P), v.ctypes.data_as(P)))
         return k, v
 
+    def set_draft(self, draft):
+        """A draft-model Engine for generate() (None: prompt lookup)."""
+        self._draft = draft  # kept alive while in use
+        check(lib.spx_engine_set_draft(self.h, draft.h if draft is not None else None))
+
     def set_sampler(self, **kw):
         """The sampler generate() draws with (ops.sampler_params keywords: temperature, top_k,
         top_p, min_p, repeat_penalty, seed, stop_ids, think_open); no keywords: plain greedy."""

@@ -8,9 +8,13 @@ import ctypes as C
 import weakref
 
 import numpy as np
-import torch
 
 from ._lib import P, check, lib
+
+try:  # device buffers of the operator functions below are torch tensors; a context needs no torch
+    import torch
+except ImportError:  # pragma: no cover - torch is part of this image
+    torch = None
 
 F32, F16, Q5_0, Q8_0, Q4K, Q6K = 0, 1, 6, 8, 12, 14
 
@@ -19,12 +23,11 @@ class Context:
     """A device + HIP stream (replaces the reference's WorkerPool as the execution resource)."""
 
     def __init__(self, device=0):
-        if not torch.cuda.is_available():
-            raise RuntimeError("spindle_amd needs a visible AMD GPU (torch.cuda.is_available() is False)")
         self.device = device
-        torch.cuda.set_device(device)
+        if torch is not None and torch.cuda.is_available():
+            torch.cuda.set_device(device)  # torch's buffers on the same device
         h = P()
-        check(lib.spx_create(device, C.byref(h)))
+        check(lib.spx_create(device, C.byref(h)))  # fails (SpxError) without a visible GPU
         self.h = h
         self._children = weakref.WeakSet()   # engines / tensors to release before the context
 

@@ -268,3 +268,37 @@ def test_speculation_on_matrix_cores(ctx, name):
             assert mg < 1e-4, (name, lo, hi, k, i, mg)
             print(f"{name}: streams diverge at {i} on a near-tie (margin {mg:.2e})")
     eng.close()
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-qwen3moe"])
+def test_draft_model_speculation(ctx, name):
+    """spx_engine_set_draft (draft_engine, generate_reply :4244-4269): with lane-exact verify
+    passes the stream is the target's plain greedy stream whatever the draft proposes; a draft
+    identical to the target has every proposal accepted; accept counts and stream equal the
+    oracle's draft-model generation (float family; the MoE family's 1e-2 logit noise can move
+    a near-tie, reported)."""
+    cfg = M.TINY[name].replace(sigma=0.06)
+    w, w2 = M.synth_model(cfg, seed=21), M.synth_model(cfg, seed=22)
+    rng = np.random.default_rng(2)
+    base = rng.integers(0, cfg.vocab, 20)
+    prompt = np.concatenate([base, base]).astype(np.int32)
+    eng, same, other = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w2)
+    for e in (eng, same, other):
+        e.set_mfma(False)
+    plain, _ = eng.generate(prompt, 40, speculate=False)
+    eng.set_draft(same)
+    g, st = eng.generate(prompt, 40, draft_len=4)
+    assert np.array_equal(g, plain) and st["drafted"] > 0 and st["accepted"] == st["drafted"], st
+    eng.set_draft(other)
+    g2, st2 = eng.generate(prompt, 40, draft_len=4, fixed=True)  # fixed: draft lengths independent of timings
+    assert np.array_equal(g2, plain) and st2["accepted"] < st2["drafted"], st2
+    o, ost = OracleModel(cfg, w).generate(prompt, 40, draft_len=4, fixed=True, draft=OracleModel(cfg, w2))
+    if np.array_equal(g2, o):
+        for k in ("accepted", "drafted", "verifies", "steps"):
+            assert st2[k] == ost[k], (k, st2, ost)
+    else:
+        assert name == "tiny-qwen3moe", (g2, o)
+        print(f"{name}: draft-model stream differs from the oracle's at {int(np.argmax(g2 != o))}")
+    eng.set_draft(None)
+    for e in (eng, same, other):
+        e.close()

@@ -51,3 +51,20 @@ def test_speculation_is_exact(name):
     assert st["verifies"] > 0
     if name == "tiny-qwen3moe":   # integer kernels: verify rows are bitwise decode rows
         assert np.array_equal(off, on)
+
+
+def test_draft_model_speculation():
+    """generate_reply with a draft engine (:4244-4269): verification keeps the target's own
+    greedy stream whatever the draft proposes; a draft identical to the target has every
+    proposal accepted; a different draft model fewer."""
+    cfg = M.TINY["tiny-qwen3"].replace(sigma=0.06)
+    w = M.synth_model(cfg, seed=21)
+    rng = np.random.default_rng(2)
+    base = rng.integers(0, cfg.vocab, 20)
+    prompt = np.concatenate([base, base]).astype(np.int32)
+    plain, _ = OracleModel(cfg, w).generate(prompt, 40, speculate=False)
+    same, st = OracleModel(cfg, w).generate(prompt, 40, draft_len=4, draft=OracleModel(cfg, w))
+    assert np.array_equal(plain, same) and st["drafted"] > 0 and st["accepted"] == st["drafted"] and st["steps"] == 0
+    other = OracleModel(cfg, M.synth_model(cfg, seed=22))
+    diff, st2 = OracleModel(cfg, w).generate(prompt, 40, draft_len=4, draft=other)
+    assert np.array_equal(plain, diff) and st2["accepted"] < st2["drafted"]

@@ -134,6 +134,7 @@ _sig("or_sample", C.c_int, C.POINTER(Sampler), P, C.c_int, C.c_float, P, C.c_int
 _sig("or_shift_kv", C.c_int, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P, C.c_int, C.c_int, C.c_int)
 _sig("or_ensure_kv_room", C.c_int, C.POINTER(Model), C.c_int, C.c_int, C.c_int)
 _sig("or_set_threads", None, C.c_int)
+_sig("or_set_simd", None, C.c_int)
 _sig("or_set_norm_order", None, C.c_int)
 _sig("or_get_threads", C.c_int)
 
@@ -242,6 +243,11 @@ def shift_kv(k16, v16, n_layers, max_seq, kv_dim, head_dim, neox, theta, n_keep,
     inv = np.empty(head_dim // 2 + 1, np.float32)
     lib.or_rope_inv_freq(head_dim, theta, ptr(inv))
     return lib.or_shift_kv(ptr(k16), ptr(v16), n_layers, max_seq, kv_dim, head_dim, int(neox), ptr(inv), n_keep, n_discard, cur_pos)
+
+
+def set_simd(on):
+    """The AVX2 kernels (True, default) or the scalar restatement (False): the same bits."""
+    lib.or_set_simd(int(bool(on)))
 
 
 def set_threads(n):

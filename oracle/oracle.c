@@ -7,6 +7,7 @@
 #define _GNU_SOURCE
 #include "oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
 #include <sched.h>
@@ -343,6 +344,91 @@ static float q8k_row_dot(const uint8_t *row, int dtype, size_t nb, const float *
   return hsum_int(acc) - corr;                               /* :247 */
 }
 
+/* The same kernel with the reference's AVX2 instructions (rows<B,T> quant_q8k.rs:163-245):
+ * each block's codes unpacked once into eight 32-byte chunks (chunk k = elements 32k..32k+31)
+ * and applied to every vector: maddubs (u8 x i8 pairs -> i16), madd with the chunk's i16
+ * scales (Q6_K: one per 16 elements), eight int32 lanes; the fp32 chain per lane. Lane l's
+ * integer and every rounding are those of q8k_block_lanes / q8k_row_dot (checked bit for bit). */
+static int g_simd = 1;
+void or_set_simd(int on) { g_simd = on; }
+
+static inline void q8k_block_decode_avx2(const uint8_t *blk, int dtype, __m256i w[8], __m256i scv[8], int8_t sc6[16],
+                                         uint8_t mn4[8], float *d, float *dmin) {
+  const __m256i m4 = _mm256_set1_epi8(0x0F), m3 = _mm256_set1_epi8(3);
+  if (dtype == OR_Q4K) {
+    uint8_t sc[8];
+    or_unpack_q4k_scales(blk + 4, sc, mn4);
+    for (int c = 0; c < 4; c++) {
+      __m256i q = _mm256_loadu_si256((const __m256i *)(blk + 16 + 32 * c));
+      w[2 * c] = _mm256_and_si256(q, m4);
+      w[2 * c + 1] = _mm256_and_si256(_mm256_srli_epi16(q, 4), m4);
+      scv[2 * c] = _mm256_set1_epi16(sc[2 * c]);
+      scv[2 * c + 1] = _mm256_set1_epi16(sc[2 * c + 1]);
+    }
+    *d = rd16(blk); *dmin = rd16(blk + 2);
+  } else {
+    const int8_t *sc = (const int8_t *)(blk + 192);
+    for (int h = 0; h < 2; h++) {
+      __m256i l0 = _mm256_loadu_si256((const __m256i *)(blk + 64 * h)), l1 = _mm256_loadu_si256((const __m256i *)(blk + 64 * h + 32));
+      __m256i qh = _mm256_loadu_si256((const __m256i *)(blk + 128 + 32 * h));
+      w[4 * h + 0] = _mm256_or_si256(_mm256_and_si256(l0, m4), _mm256_slli_epi16(_mm256_and_si256(qh, m3), 4));
+      w[4 * h + 1] = _mm256_or_si256(_mm256_and_si256(l1, m4), _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(qh, 2), m3), 4));
+      w[4 * h + 2] = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(l0, 4), m4), _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(qh, 4), m3), 4));
+      w[4 * h + 3] = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(l1, 4), m4), _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(qh, 6), m3), 4));
+    }
+    for (int k = 0; k < 8; k++) {
+      __m128i lo = _mm_set1_epi16(sc[2 * k]), hi = _mm_set1_epi16(sc[2 * k + 1]);
+      scv[k] = _mm256_set_m128i(hi, lo);
+    }
+    memcpy(sc6, sc, 16);
+    *d = rd16(blk + 208); *dmin = 0.0f;
+  }
+}
+
+static void q8k_rows_avx2(const uint8_t *tensor, int dtype, size_t cols, int nvec, const float *const *xd, const int8_t *const *xs,
+                          const int16_t *const *xb, float *const *outs, size_t r0, size_t r1) {
+  size_t nb = cols / 256, rb = or_row_bytes(dtype, cols);
+  __m256 acc[16];
+  float corr[16];
+  for (size_t r = r0; r < r1; r++) {
+    const uint8_t *row = tensor + r * rb;
+    for (int v0 = 0; v0 < nvec; v0 += 16) {
+      int nv = nvec - v0 < 16 ? nvec - v0 : 16;
+      for (int v = 0; v < nv; v++) { acc[v] = _mm256_setzero_ps(); corr[v] = 0.0f; }
+      for (size_t i = 0; i < nb; i++) {
+        __m256i w[8], scv[8];
+        int8_t sc6[16];
+        uint8_t mn[8];
+        float d, dmin;
+        q8k_block_decode_avx2(row + i * (dtype == OR_Q4K ? 144 : 210), dtype, w, scv, sc6, mn, &d, &dmin);
+        for (int v = 0; v < nv; v++) {
+          const int8_t *y = xs[v0 + v] + i * 256;
+          const int16_t *bs = xb[v0 + v] + i * 16;
+          __m256i l8 = _mm256_setzero_si256();
+          for (int k = 0; k < 8; k++) {
+            __m256i p = _mm256_maddubs_epi16(w[k], _mm256_loadu_si256((const __m256i *)(y + 32 * k)));
+            l8 = _mm256_add_epi32(l8, _mm256_madd_epi16(p, scv[k]));
+          }
+          int ci = 0;
+          if (dtype == OR_Q4K) {
+            for (int j = 0; j < 8; j++) ci += mn[j] * ((int)bs[2 * j] + (int)bs[2 * j + 1]);
+            corr[v] += dmin * xd[v0 + v][i] * (float)ci;
+          } else {
+            for (int g = 0; g < 16; g++) ci += (int)sc6[g] * (int)bs[g];
+            corr[v] += d * xd[v0 + v][i] * (float)(32 * ci);
+          }
+          acc[v] = _mm256_fmadd_ps(_mm256_set1_ps(d * xd[v0 + v][i]), _mm256_cvtepi32_ps(l8), acc[v]);
+        }
+      }
+      for (int v = 0; v < nv; v++) {
+        float a[8];
+        _mm256_storeu_ps(a, acc[v]);
+        outs[v0 + v][r] = hsum_int(a) - corr[v];
+      }
+    }
+  }
+}
+
 typedef struct {
   const uint8_t *tensor; int dtype; size_t cols; int nvec;
   const float *const *xd; const int8_t *const *xs; const int16_t *const *xb; float *const *outs;
@@ -352,6 +438,7 @@ typedef struct {
 static void q8k_job_run(void *p, int t, int n) {
   q8k_job *j = (q8k_job *)p;
   size_t rows = j->r1 - j->r0, a = j->r0 + rows * t / n, b = j->r0 + rows * (t + 1) / n;
+  if (g_simd) { q8k_rows_avx2(j->tensor, j->dtype, j->cols, j->nvec, j->xd, j->xs, j->xb, j->outs, a, b); return; }
   size_t nb = j->cols / 256, rb = or_row_bytes(j->dtype, j->cols);
   for (size_t r = a; r < b; r++)
     for (int v = 0; v < j->nvec; v++)
@@ -791,14 +878,27 @@ static void attn_head(const attn_job *j, int h) { /* :3456-3495 */
     size_t off = ((size_t)j->layer * c->max_seq + t) * kv_dim + (size_t)kvh * hd;
     const uint16_t *kh = j->m->k_cache + off, *vh = j->m->v_cache + off;
     float a8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int i = 0; i < hd; i += 8)
-      for (int l = 0; l < 8; l++) a8[l] = fmaf(or_f16_to_f32(kh[i + l]), qh[i + l], a8[l]);
+    if (g_simd) { /* dot_f16_row_avx2: cvtph, fmadd over 8 lanes */
+      __m256 av = _mm256_setzero_ps();
+      for (int i = 0; i < hd; i += 8)
+        av = _mm256_fmadd_ps(_mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(kh + i))), _mm256_loadu_ps(qh + i), av);
+      _mm256_storeu_ps(a8, av);
+    } else {
+      for (int i = 0; i < hd; i += 8)
+        for (int l = 0; l < 8; l++) a8[l] = fmaf(or_f16_to_f32(kh[i + l]), qh[i + l], a8[l]);
+    }
     float score = (hsum_hadd(a8) + 0.0f) * j->scale;
     float mnew = fmaxf(mprev, score);
     float alpha = expf(mprev - mnew), p = expf(score - mnew);
     lprev = lprev * alpha + p;
     mprev = mnew;
-    for (int d = 0; d < hd; d++) acc[d] = fmaf(p, or_f16_to_f32(vh[d]), acc[d] * alpha);
+    if (g_simd) { /* acc = fmadd(p, v, acc * alpha) per 8 dims */
+      __m256 va = _mm256_set1_ps(alpha), vp = _mm256_set1_ps(p);
+      for (int d = 0; d < hd; d += 8)
+        _mm256_storeu_ps(acc + d, _mm256_fmadd_ps(vp, _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(vh + d))), _mm256_mul_ps(_mm256_loadu_ps(acc + d), va)));
+    } else {
+      for (int d = 0; d < hd; d++) acc[d] = fmaf(p, or_f16_to_f32(vh[d]), acc[d] * alpha);
+    }
   }
   float invl = 1.0f / fmaxf(lprev, 1e-9f);
   for (int d = 0; d < hd; d++) oh[d] = acc[d] * invl;

@@ -224,6 +224,9 @@ int or_generate_full(or_model *m, or_model *draft, const int *prompt, int n_prom
                      or_sampler *s, int *out, or_gen_stats *st);
 
 void or_set_threads(int n);
+/* 1 (default): the integer rows kernel and attention with the reference's AVX2 instructions;
+ * 0: the scalar restatement (the same bits; the tests compare the two). */
+void or_set_simd(int on);
 /* Test knob, off by default: 1 = RMSNorm sums in the GPU kernels' order (sensitivity tests). */
 void or_set_norm_order(int gpu_order);
 int or_get_threads(void);

@@ -187,3 +187,43 @@ def test_pool_shrink_keeps_results():
         ffi.set_threads(t)
         outs.append(ffi.matvec(m, x))
     assert all(np.array_equal(outs[0].view(np.uint32), o.view(np.uint32)) for o in outs[1:])
+
+
+@pytest.mark.parametrize("dtype", [R.Q4K, R.Q6K])
+def test_avx2_rows_kernel_equals_scalar(dtype):
+    """The oracle's AVX2 rows kernel (the reference's maddubs / madd lanes, each block decoded
+    once for all vectors) gives the scalar restatement's bits for every vector count."""
+    rng = R.Rng(7 + dtype)
+    n, rows = 1024, 23
+    mat = R.random_matrix(dtype, n, rows, rng)
+    xs = [rng.floats(n, -2.0, 2.0) for _ in range(20)]
+    qs = [ffi.q8k_quantize(x) for x in xs]
+    try:
+        for nv in (1, 3, 16, 20):
+            ffi.set_simd(False)
+            a = ffi.q8k_matmul_rows(mat, dtype, n, qs[:nv], rows)
+            ffi.set_simd(True)
+            b = ffi.q8k_matmul_rows(mat, dtype, n, qs[:nv], rows)
+            for v in range(nv):
+                assert np.array_equal(a[v].view(np.uint32), b[v].view(np.uint32)), (nv, v)
+    finally:
+        ffi.set_simd(True)
+
+
+def test_avx2_attention_equals_scalar():
+    """A whole forward (attention included) with the AVX2 kernels equals the scalar one bit for bit."""
+    from oracle.model import OracleModel
+    from spindle_amd import model as M
+    cfg = M.TINY["tiny-qwen3moe"]
+    w = M.synth_model(cfg, seed=5)
+    ids = np.random.default_rng(2).integers(0, cfg.vocab, 40).astype(np.int32)
+    out = []
+    try:
+        for simd in (False, True):
+            ffi.set_simd(simd)
+            om = OracleModel(cfg, w)
+            h = np.concatenate([om.forward(ids[s:s + 8], s) for s in range(0, 40, 8)])
+            out.append(h)
+    finally:
+        ffi.set_simd(True)
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))

@@ -193,13 +193,89 @@ __device__ __forceinline__ void attn_kv_first(const AttnArgs &a, int total, int 
   attn_kv_load<NU>(a, cache0 + (int64_t)min(p_lo + lp, MERGE ? p_hi - 1 : a.max_seq - 1) * a.kv_dim + lq * DQ, kr, vr);
 }
 
+// Raw inputs of a multi-row item's head_prep rows (wavefront w: query rows w + 4j of the tile,
+// new pass rows b = w + 4j when their position falls in the item's chunk), loaded before the
+// chunk's K/V rows: memory returns in issue order, so a row loaded after the K/V would wait
+// for all of it, and each row's norm reduction would wait for the next row's load.
+struct AttnPre {
+  float q0[4], q1[4], qb0[4], qb1[4], qc[4], qs[4];
+  float k0[4], k1[4], kb0[4], kb1[4], v0[4], v1[4], vb0[4], vb1[4], kc[4], ks[4];
+  float qn0, qn1, kn0, kn1;
+};
+
+template <int HD>
+__device__ __forceinline__ void attn_pre_load(const AttnArgs &a, int m, int start, int c, int h, int qt, AttnPre &p) {
+  const int tid = threadIdx.x & 255, wave = tid >> 6, lane = tid & 63, half = HD / 2;
+  const bool act = lane < half;
+  const int da = a.neox ? lane : 2 * lane, db = a.neox ? lane + half : 2 * lane + 1;
+  const int g = a.n_heads / a.n_kv, NQ = m * g, qa = qt * 16, total = start + m;
+  const int p_lo = c * 64, p_hi = min(p_lo + 64, total);
+  p.qn0 = p.qn1 = p.kn0 = p.kn1 = 0.0f;
+  if (a.q_norm && act) { p.qn0 = a.q_norm[da]; p.qn1 = a.q_norm[db]; }
+  if (a.k_norm && act) { p.kn0 = a.k_norm[da]; p.kn1 = a.k_norm[db]; }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int qi = qa + wave + 4 * j;
+    p.q0[j] = p.q1[j] = p.qb0[j] = p.qb1[j] = 0.0f;
+    p.qc[j] = 1.0f;
+    p.qs[j] = 0.0f;
+    if (qi < NQ && act) {
+      const int b = qi / g, head = h * g + qi % g;
+      const float *src = a.q + (int64_t)b * a.n_heads * HD + head * HD;
+      p.q0[j] = src[da];
+      p.q1[j] = src[db];
+      if (a.q_bias) { p.qb0[j] = a.q_bias[head * HD + da]; p.qb1[j] = a.q_bias[head * HD + db]; }
+      const float2 cs = a.rope[(int64_t)(start + b) * half + lane];
+      p.qc[j] = cs.x;
+      p.qs[j] = cs.y;
+    }
+    const int b = wave + 4 * j, pos = start + b;
+    p.k0[j] = p.k1[j] = p.kb0[j] = p.kb1[j] = p.v0[j] = p.v1[j] = p.vb0[j] = p.vb1[j] = 0.0f;
+    p.kc[j] = 1.0f;
+    p.ks[j] = 0.0f;
+    if (b < m && pos >= p_lo && pos < p_hi && act) {
+      const float *ks = a.k + (int64_t)b * a.kv_dim + h * HD, *vs = a.v + (int64_t)b * a.kv_dim + h * HD;
+      p.k0[j] = ks[da];
+      p.k1[j] = ks[db];
+      p.v0[j] = vs[da];
+      p.v1[j] = vs[db];
+      if (a.k_bias) { p.kb0[j] = a.k_bias[h * HD + da]; p.kb1[j] = a.k_bias[h * HD + db]; }
+      if (a.v_bias) { p.vb0[j] = a.v_bias[h * HD + da]; p.vb1[j] = a.v_bias[h * HD + db]; }
+      const float2 cs = a.rope[(int64_t)pos * half + lane];
+      p.kc[j] = cs.x;
+      p.ks[j] = cs.y;
+    }
+  }
+}
+
+// head_prep's arithmetic on preloaded values (x: the row, xb: its bias, nw0 / nw1: the norm
+// weights, c / s: the rotation), operation for operation
+__device__ __forceinline__ void head_prep_pre(float x0, float x1, float xb0, float xb1, bool bias, bool norm, float nw0, float nw1,
+                                              bool rope, float c, float s, int hd, float eps, float &e0, float &e1) {
+  const bool act = (int)(threadIdx.x & 63) < (hd >> 1);
+  if (bias && act) { x0 += xb0; x1 += xb1; }
+  if (norm) {
+    const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)hd) + eps));
+    if (act) { x0 = x0 * inv * nw0; x1 = x1 * inv * nw1; }
+  }
+  if (rope && act) {
+    const float r0 = x0 * c - x1 * s, r1 = x0 * s + x1 * c;
+    x0 = r0;
+    x1 = r1;
+  }
+  e0 = x0;
+  e1 = x1;
+}
+
 // One attention item: chunk c (64 positions) of kv head h for query tile qt of a pass of m rows
 // at start, with 256 threads, LDS at smem (AttnLds<HD>::BYTES) and the chunk's first K/V rows
 // already in kr / vr (attn_kv_first). COH: the q / k / v rows and the partials are handed
-// between workgroups of one launch (the persistent pass): read and written coherently.
+// between workgroups of one launch (the persistent pass): read and written coherently. MERGE
+// items take their query and new rows from pre (attn_pre_load, issued before attn_kv_first).
 template <int HD, bool MERGE, bool COH>
 __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const int start, const int c, const int h, const int qt,
-                                          uint8_t *smem, uint32_t (&kr)[HD / 8], uint32_t (&vr)[HD / 8]) {
+                                          uint8_t *smem, uint32_t (&kr)[HD / 8], uint32_t (&vr)[HD / 8], const AttnPre *pre = nullptr) {
   using LY = AttnLds<HD>;
   constexpr int QS = LY::QS, KS = LY::KS, VS = LY::VS, PS = LY::PS, SS = LY::SS;
   constexpr int DT = HD / 16, TPW = DT / 4;  // 16-dim output tiles, per wavefront
@@ -290,14 +366,13 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
       }
     }
   } else {
-    for (int r = wave; r < 16; r += 4) {
-      const int qi = qa + r;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int r = wave + 4 * j, qi = qa + r;
       float e0 = 0.0f, e1 = 0.0f;
-      if (qi < NQ) {
-        const int b = qi / g, head = h * g + qi % g;
-        head_prep(a.q + (int64_t)b * a.n_heads * HD + head * HD, a.q_bias ? a.q_bias + head * HD : nullptr, a.q_norm,
-                  a.rope + (int64_t)(start + b) * half, HD, a.neox, a.eps, e0, e1);
-      }
+      if (qi < NQ)
+        head_prep_pre(pre->q0[j], pre->q1[j], pre->qb0[j], pre->qb1[j], a.q_bias != nullptr, a.q_norm != nullptr, pre->qn0, pre->qn1,
+                      true, pre->qc[j], pre->qs[j], HD, a.eps, e0, e1);
       if (lane < half) {
         split_f16(e0, qh[r * QS + da], ql[r * QS + da]);
         split_f16(e1, qh[r * QS + db], ql[r * QS + db]);
@@ -355,7 +430,29 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
         vd[db] = v1;
       }
     }
-    for (int b = wave; MERGE && b < m; b += 4) {
+#pragma unroll
+    for (int j = 0; MERGE && j < 4; j++) {  // rows b = wave + 4j, preloaded
+      const int b = wave + 4 * j, pos = start + b, pp = pos - s0;
+      if (b >= m || pp < 0 || pp >= 64 || pos >= p_hi) continue;
+      float e0, e1;
+      head_prep_pre(pre->k0[j], pre->k1[j], pre->kb0[j], pre->kb1[j], a.k_bias != nullptr, a.k_norm != nullptr, pre->kn0, pre->kn1,
+                    true, pre->kc[j], pre->ks[j], HD, a.eps, e0, e1);
+      if (lane < half) {
+        const __half k0 = __float2half_rn(e0), k1 = __float2half_rn(e1);
+        ks[pp * KS + da] = (_Float16)__half2float(k0);
+        ks[pp * KS + db] = (_Float16)__half2float(k1);
+        if (qt == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
+      }
+      head_prep_pre(pre->v0[j], pre->v1[j], pre->vb0[j], pre->vb1[j], a.v_bias != nullptr, false, 0.0f, 0.0f, false, 1.0f, 0.0f, HD,
+                    a.eps, e0, e1);
+      if (lane < half) {
+        const __half v0 = __float2half_rn(e0), v1 = __float2half_rn(e1);
+        vt[da * VS + pp] = (_Float16)__half2float(v0);
+        vt[db * VS + pp] = (_Float16)__half2float(v1);
+        if (qt == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
+      }
+    }
+    for (int b = wave + 16; MERGE && b < m; b += 4) {  // rows past the preloaded ones
       const int pos = start + b, pp = pos - s0;
       if (pp < 0 || pp >= 64 || pos >= p_hi) continue;
       float e0, e1;

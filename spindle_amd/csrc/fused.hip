@@ -817,8 +817,10 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
   const int m = st->m, start = st->start, total = start + m;
   if (qt * 16 >= m * (a.n_heads / a.n_kv) || c >= (total + 63) / 64) return;
   uint32_t kr[HD / 8], vr[HD / 8];
+  AttnPre pre;
+  if constexpr (MERGE) attn_pre_load<HD>(a, m, start, c, h, qt, pre);
   attn_kv_first<HD, MERGE>(a, total, c, h, kr, vr);
-  attn_item<HD, MERGE, false>(a, m, start, c, h, qt, smem, kr, vr);
+  attn_item<HD, MERGE, false>(a, m, start, c, h, qt, smem, kr, vr, &pre);
 }
 
 // ------------------------------------------------------------------ MoE router + routing

@@ -128,12 +128,15 @@ def time_pass(eng, ids, pos, reps=10):
     return (time.perf_counter() - t0) / reps * 1e6
 
 
+PREFILL_CHUNK = 128  # feed's prompt chunks (smollm_chat.rs:3090)
+
+
 def prefill(eng, prompt, verbose=False):
     t0 = time.perf_counter()
-    for s in range(0, len(prompt), 16):
-        am, _, _ = eng.forward(prompt[s:s + 16], s)
+    for s in range(0, len(prompt), PREFILL_CHUNK):
+        am, _, _ = eng.forward(prompt[s:s + PREFILL_CHUNK], s)
         if verbose and s % 1024 == 0:
-            log(f"prefill {s + len(prompt[s:s + 16])}/{len(prompt)}")
+            log(f"prefill {s + len(prompt[s:s + PREFILL_CHUNK])}/{len(prompt)}")
     return int(am[-1]), time.perf_counter() - t0
 
 
@@ -215,7 +218,7 @@ def main():
     prompt = spec_prompt(cfg.vocab, args.prompt_len, args.seed)
     tok, prefill_s = prefill(eng, prompt, verbose=True)
     pos = len(prompt)
-    log(f"prefill {len(prompt)} tokens in {prefill_s:.2f}s ({len(prompt) / prefill_s:.0f} tok/s, 16-row passes)")
+    log(f"prefill {len(prompt)} tokens in {prefill_s:.2f}s ({len(prompt) / prefill_s:.0f} tok/s, {PREFILL_CHUNK}-row passes)")
 
     # CPU baseline from the KV state the GPU's timed decode starts from (read-only on the GPU)
     cpu = None

@@ -224,16 +224,18 @@ __device__ __forceinline__ void attn_pre_load(const AttnArgs &a, int m, int star
       const float *src = a.q + (int64_t)b * a.n_heads * HD + head * HD;
       p.q0[j] = src[da];
       p.q1[j] = src[db];
-      if (a.q_bias) { p.qb0[j] = a.q_bias[head * HD + da]; p.qb1[j] = a.q_bias[head * HD + db]; }
-      const float2 cs = a.rope[(int64_t)(start + b) * half + lane];
-      p.qc[j] = cs.x;
-      p.qs[j] = cs.y;
+      if (!a.prepped) {
+        if (a.q_bias) { p.qb0[j] = a.q_bias[head * HD + da]; p.qb1[j] = a.q_bias[head * HD + db]; }
+        const float2 cs = a.rope[(int64_t)(start + b) * half + lane];
+        p.qc[j] = cs.x;
+        p.qs[j] = cs.y;
+      }
     }
     const int b = wave + 4 * j, pos = start + b;
     p.k0[j] = p.k1[j] = p.kb0[j] = p.kb1[j] = p.v0[j] = p.v1[j] = p.vb0[j] = p.vb1[j] = 0.0f;
     p.kc[j] = 1.0f;
     p.ks[j] = 0.0f;
-    if (b < m && pos >= p_lo && pos < p_hi && act) {
+    if (!a.prepped && b < m && pos >= p_lo && pos < p_hi && act) {
       const float *ks = a.k + (int64_t)b * a.kv_dim + h * HD, *vs = a.v + (int64_t)b * a.kv_dim + h * HD;
       p.k0[j] = ks[da];
       p.k1[j] = ks[db];
@@ -370,9 +372,9 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
     for (int j = 0; j < 4; j++) {
       const int r = wave + 4 * j, qi = qa + r;
       float e0 = 0.0f, e1 = 0.0f;
-      if (qi < NQ)
-        head_prep_pre(pre->q0[j], pre->q1[j], pre->qb0[j], pre->qb1[j], a.q_bias != nullptr, a.q_norm != nullptr, pre->qn0, pre->qn1,
-                      true, pre->qc[j], pre->qs[j], HD, a.eps, e0, e1);
+      if (qi < NQ)  // prepared queries (a.prepped) are taken as they are
+        head_prep_pre(pre->q0[j], pre->q1[j], pre->qb0[j], pre->qb1[j], a.q_bias && !a.prepped, a.q_norm && !a.prepped, pre->qn0,
+                      pre->qn1, !a.prepped, pre->qc[j], pre->qs[j], HD, a.eps, e0, e1);
       if (lane < half) {
         split_f16(e0, qh[r * QS + da], ql[r * QS + da]);
         split_f16(e1, qh[r * QS + db], ql[r * QS + db]);
@@ -384,6 +386,8 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
 #pragma unroll
   for (int j = 0; j < TPW; j++) acc[j] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // first position whose K / V row this item makes itself (prepared passes: none)
+  const int new0 = MERGE && a.prepped ? total : start;
   for (int s0 = p_lo; s0 < p_hi; s0 += 64) {
     __syncthreads();  // the previous sub-chunk is done with ks / vt / ph / pl
     // cached rows -> LDS (K row-major, V transposed); rows of this pass come from below; rows
@@ -392,7 +396,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
 #pragma unroll
       for (int t = 0; t < 4 * NU; t++) { kr[t] = 0u; vr[t] = 0u; }
     }
-    if (s0 + lp < start || s0 + lp >= total) {
+    if (s0 + lp < new0 || s0 + lp >= total) {
       uint16_t *vt16 = reinterpret_cast<uint16_t *>(vt);
 #pragma unroll
       for (int u = 0; u < NU; u++) reinterpret_cast<uint4 *>(ks + lp * KS + lq * DQ)[u] = make_uint4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
@@ -431,7 +435,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
       }
     }
 #pragma unroll
-    for (int j = 0; MERGE && j < 4; j++) {  // rows b = wave + 4j, preloaded
+    for (int j = 0; MERGE && !a.prepped && j < 4; j++) {  // rows b = wave + 4j, preloaded
       const int b = wave + 4 * j, pos = start + b, pp = pos - s0;
       if (b >= m || pp < 0 || pp >= 64 || pos >= p_hi) continue;
       float e0, e1;
@@ -452,7 +456,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
         if (qt == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
       }
     }
-    for (int b = wave + 16; MERGE && b < m; b += 4) {  // rows past the preloaded ones
+    for (int b = wave + 16; MERGE && !a.prepped && b < m; b += 4) {  // rows past the preloaded ones
       const int pos = start + b, pp = pos - s0;
       if (pp < 0 || pp >= 64 || pos >= p_hi) continue;
       float e0, e1;

@@ -108,8 +108,8 @@ struct DecNormArgs {
   // res_in[b] + rscale * sum_i cw[b][i] * yd[b * n_used + i] over its kept choices in choice
   // order (unfused multiply and add, ffns_fused :432-437), written to x_out, then normalised
   const float *yd;    // [m * n_used][dim]
-  const float *cw;    // [16][32] choice weights
-  const int *nkeep;   // [16]
+  const float *cw;    // [m][32] choice weights
+  const int *nkeep;   // [m]
   const float *res_in;
   float *x_out;
   int n_used;
@@ -148,11 +148,11 @@ struct DecRouteArgs {
   const float *logits;
   int n_expert, n_used, norm, m;
   float moe_prune;
-  int *chosen;        // [16][32]
-  float *weights;     // [16][32]
-  int *nkeep;         // [16]
-  Job *jobs;          // [<= 256]
-  int *njobs;         // [1]
+  int *chosen;        // [m][32]
+  float *weights;     // [m][32]
+  int *nkeep;         // [m]
+  Job *jobs;          // [<= 512]
+  int *njobs;         // [0]: jobs; [2]: experts with users (kp_route)
   int *expert_count;  // [n_expert] (null: none)
 };
 
@@ -197,6 +197,10 @@ hipError_t launch_dec_mm(const DecMMArgs &a, int grid, hipStream_t s);
 // The same matvec on the int8 matrix cores (16-row tiles; block totals exact, fp32 sums to
 // rounding): tiles[i] counts 16-row tiles; tiles stride over the grid.
 hipError_t launch_dec_mq(const DecMMArgs &a, int grid, hipStream_t s);
+// kd_mq's grid argument for a number of tiles and m vectors: up to 16 vectors, workgroups (at
+// most two a CU); more (prefill), tile ranges, a multiple of eight (the launch holds
+// ceil(m / 16) workgroups per range). With greedy keys, nbest = this value.
+int dec_mq_grid(int tiles, int m);
 // kd_mm grid for a number of tiles: at most two workgroups a CU, the same number of tiles each
 // (tiles stride over the grid; the next tile's weights are requested before the results)
 int dec_mm_grid(int tiles);
@@ -206,6 +210,10 @@ hipError_t launch_dec_down_m(const DecDownMArgs &a, hipStream_t s);
 // The grouped expert kernels on the int8 matrix cores (16-row tiles)
 hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &a, int max_jobs, hipStream_t s);
 hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s);
+// Prefill passes (17..PMAX rows): routing + the job list (at most 16 users a job) in global
+// memory; gate/up over such a list (jobs null: dense, rows in sixteens), max_jobs bounds it
+hipError_t launch_kp_route(const DecRouteArgs &a, hipStream_t s);
+hipError_t launch_kp_gateup_mq(const DecGateUpMArgs &a, const Job *jobs, const int *njobs, int max_jobs, hipStream_t s);
 hipError_t launch_dec_merge(const DecMergeArgs &a, const StepRec *st, hipStream_t s);
 hipError_t launch_dec_router(const DecRouterArgs &a, hipStream_t s);
 hipError_t launch_dec_gateup(const DecGateUpArgs &a, hipStream_t s);

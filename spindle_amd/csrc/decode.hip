@@ -642,12 +642,14 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
 // ------------------------------------------------------------------ router, m rows
 // k_router's arithmetic for each row: wavefront w, lane j hold float4s w*64 + j + 256k of the
 // router row; the lane's fma chain against the normalised row, the wave tree, the four
-// wavefronts in order.
+// wavefronts in order. Workgroup (e, g): router row e against rows 16g .. 16g + 15.
 __global__ __launch_bounds__(256) void kd_router_m(const DecRouterMArgs a) {
   constexpr int NK = DEC_MAXNB / 4;
   __shared__ float part[4][MAX_M];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, row = blockIdx.x;
-  const int dim = a.dim, n4 = dim >> 2;
+  const int dim = a.dim, n4 = dim >> 2, vb = blockIdx.y * MAX_M, mg = min(MAX_M, a.m - vb);
+  const float *xg = a.x + (int64_t)vb * dim;
+  float *lg = a.logits + (int64_t)vb * a.n_expert;
   float4 wv[NK];
 #pragma unroll
   for (int k = 0; k < NK; k++) {
@@ -656,14 +658,14 @@ __global__ __launch_bounds__(256) void kd_router_m(const DecRouterMArgs a) {
   }
 #pragma unroll
   for (int v0 = 0; v0 < MAX_M; v0 += 4) {
-    if (v0 < a.m) {
+    if (v0 < mg) {
       float4 x[4][NK];
 #pragma unroll
       for (int vv = 0; vv < 4; vv++)
 #pragma unroll
         for (int k = 0; k < NK; k++) {
-          const int f = wave * 64 + lane + 256 * k, v = min(v0 + vv, a.m - 1);
-          x[vv][k] = f < n4 ? gld<float4>(a.x + (int64_t)v * dim + 4 * f) : make_float4(0.f, 0.f, 0.f, 0.f);
+          const int f = wave * 64 + lane + 256 * k, v = min(v0 + vv, mg - 1);
+          x[vv][k] = f < n4 ? gld<float4>(xg + (int64_t)v * dim + 4 * f) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
       for (int vv = 0; vv < 4; vv++) {
@@ -679,14 +681,14 @@ __global__ __launch_bounds__(256) void kd_router_m(const DecRouterMArgs a) {
           }
         }
         const float tsum = wave_sum(pv);
-        if (lane == 0 && v0 + vv < a.m) part[wave][v0 + vv] = tsum;
+        if (lane == 0 && v0 + vv < mg) part[wave][v0 + vv] = tsum;
       }
     }
   }
   __syncthreads();
-  if ((int)threadIdx.x < a.m) {
+  if ((int)threadIdx.x < mg) {
     const int v = threadIdx.x;
-    gst<float>(a.logits + (int64_t)v * a.n_expert + row, ((part[0][v] + part[1][v]) + part[2][v]) + part[3][v]);
+    gst<float>(lg + (int64_t)v * a.n_expert + row, ((part[0][v] + part[1][v]) + part[2][v]) + part[3][v]);
   }
 }
 
@@ -1220,26 +1222,43 @@ __device__ __forceinline__ void mq_locate(const DecMMArgs &a, int total, MqPos &
 // q < 4 adds accumulator q (matrix row lane & 15, vector 4 (lane >> 4) + q) in wavefront order
 // and runs the epilogue (residual, greedy keys) as kd_mm does. The correction operands are
 // staged next to the Q8_K image once.
+//
+// Passes of more than 16 rows (prefill) take the vectors in groups of 16: the launch holds
+// R x groups workgroups; workgroup i = 8k + x (x: its XCD) takes group k mod groups and tile
+// range r = 8 (k / groups) + x (tiles r, r + R, ...), so the groups' workgroups of one tile
+// range share an XCD and its L2: the weights come from HBM about once.
 __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void kd_mq(const DecMMArgs a) {
   constexpr int NW = DEC_MM_NW;
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[2][NW][4][64];
   __shared__ unsigned long long sbest[MAX_M];
-  const int m = a.m, cols = a.cols, nbq = cols >> 8, nb = nbq;
+  const int nvg = (a.m + 15) >> 4;
+  int vg = 0, r0 = blockIdx.x, R = gridDim.x;
+  if (nvg > 1) {
+    const int k = blockIdx.x >> 3;
+    vg = k % nvg;
+    r0 = (k / nvg) * 8 + (blockIdx.x & 7);
+    R = gridDim.x / nvg;
+  }
+  const int v0 = vg * 16, m = min(16, a.m - v0), cols = a.cols, nbq = cols >> 8, nb = nbq;
+  Q8KP y = a.y;
+  y.q += (int64_t)v0 * (cols >> 2);
+  y.d += (int64_t)v0 * nbq;
+  y.bs += (int64_t)v0 * nbq * 8;
   SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
   SPX_L float *ld = (SPX_L float *)(smem + (((size_t)m * cols + 15) & ~(size_t)15));
   SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)m * cols + 15) & ~(size_t)15) + (((size_t)m * nbq * 4 + 15) & ~(size_t)15));
   const int total = a.tiles[0] + (a.nseg > 1 ? a.tiles[1] : 0) + (a.nseg > 2 ? a.tiles[2] : 0);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, c16 = lane & 15;
   if (threadIdx.x < MAX_M) sbest[threadIdx.x] = 0;
-  stage_q8<NW * 64>(a.y, (const int *)nullptr, m, cols, lq, ld, lbs);
+  stage_q8<NW * 64>(y, (const int *)nullptr, m, cols, lq, ld, lbs);
   SPX_L uint32_t *lc = (SPX_L uint32_t *)(smem + mm_act_bytes(m, cols));
   __syncthreads();
   mq_corr_stage(m * nb, lbs, lc);
   __syncthreads();
   int buf = 0;
   const MqVec vv = mq_vecs(m, MqIdentity{});
-  for (int t = blockIdx.x; t < total; t += gridDim.x) {
+  for (int t = r0; t < total; t += R) {
     MqPos p;
     p.t = t;
     p.u = 0;
@@ -1265,10 +1284,10 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
       for (int w2 = 1; w2 < NW; w2++) res = res + red[buf][w2][q][lane];
       if (v < m && r < p.nrows) {
         float *const out = a.out[p.si];
-        const int64_t row = p.row0 + r;
-        if (out) gst<float>(out + (int64_t)v * a.ld_out[p.si] + row, res);
+        const int64_t row = p.row0 + r, gv = v0 + v;
+        if (out) gst<float>(out + gv * a.ld_out[p.si] + row, res);
         if (a.res_out) {
-          const int64_t o = (int64_t)v * w.rows + row;
+          const int64_t o = gv * w.rows + row;
           gst<float>(a.res_out + o, gld<float>(a.res_in + o) + a.rscale * res);
         }
         if (a.best) atomicMax(&sbest[v], pick_key(res, a.lscale, row));
@@ -1276,9 +1295,9 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
     }
     buf ^= 1;
   }
-  if (a.best) {
+  if (a.best) {  // per vector, the best key of each tile range
     __syncthreads();
-    if ((int)threadIdx.x < m) gst<unsigned long long>(a.best + (int64_t)threadIdx.x * a.nbest + blockIdx.x, sbest[threadIdx.x]);
+    if ((int)threadIdx.x < m) gst<unsigned long long>(a.best + (int64_t)(v0 + threadIdx.x) * a.nbest + r0, sbest[threadIdx.x]);
   }
 }
 
@@ -1440,6 +1459,167 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_mq(const DecDownMArgs 
   }
 }
 
+// ------------------------------------------------------------------ prefill passes (17..128 rows)
+// Routing of m <= PMAX rows and the job list in global memory, one workgroup of 16 wavefronts:
+// wavefront w routes rows w, w + 16, ... (route_row, the rows' results to chosen / weights /
+// nkeep), then thread e lists expert e's users in row order, sixteen a job (jobs in expert
+// order). njobs[0] = the job count, njobs[2] = the experts with users; expert_count counts
+// each of them once.
+__global__ __launch_bounds__(1024) void kp_route(const DecRouteArgs a) {
+  constexpr int NW = 16;
+  __shared__ signed char slot_of[PMAX * 256];
+  __shared__ int nje[256];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ne = a.n_expert, nu = a.n_used, m = a.m;
+  for (int i = threadIdx.x; i < m * 256; i += NW * 64) slot_of[i] = -1;
+  __syncthreads();
+  for (int b = wave; b < m; b += NW) {
+    float lv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int e = lane + 64 * k;
+      lv[k] = e < ne ? gld<float>(a.logits + (int64_t)b * ne + e) : -INFINITY;
+    }
+    int my_e, keep;
+    float my_p, wsum;
+    route_row(lv, ne, nu, a.moe_prune, my_e, my_p, keep, wsum);
+    if (lane < keep) {
+      slot_of[b * 256 + my_e] = (signed char)lane;
+      gst<int>(a.chosen + b * 32 + lane, my_e);
+      gst<float>(a.weights + b * 32 + lane, a.norm ? my_p / wsum : my_p);
+    }
+    if (lane == 0) gst<int>(a.nkeep + b, keep);
+  }
+  __syncthreads();
+  const int e = threadIdx.x;
+  int cnt = 0;
+  if (e < ne)
+    for (int b = 0; b < m; b++) cnt += slot_of[b * 256 + e] >= 0;
+  if (e < 256) nje[e] = (cnt + MAX_M - 1) / MAX_M;
+  __syncthreads();
+  if (e < ne && cnt > 0) {
+    int j = 0;
+    for (int i = 0; i < e; i++) j += nje[i];
+    int *J = nullptr;
+    int k = 0;
+    for (int b = 0; b < m; b++) {
+      const int sl = slot_of[b * 256 + e];
+      if (sl < 0) continue;
+      if (k == 0) J = reinterpret_cast<int *>(a.jobs + j);
+      gst<int>(J + 2 + k, b);
+      gst<int>(J + 2 + MAX_M + k, b * nu + sl);
+      if (++k == MAX_M) {
+        gst<int>(J, e);
+        gst<int>(J + 1, k);
+        j++;
+        k = 0;
+      }
+    }
+    if (k > 0) {
+      for (int q = k; q < MAX_M; q++) { gst<int>(J + 2 + q, 0); gst<int>(J + 2 + MAX_M + q, 0); }
+      gst<int>(J, e);
+      gst<int>(J + 1, k);
+    }
+    if (a.expert_count) atomicAdd(a.expert_count + e, 1);
+  }
+  if (threadIdx.x == 0) {
+    int nj = 0, nx = 0;
+    for (int i = 0; i < 256; i++) { nj += nje[i]; nx += nje[i] > 0; }
+    gst<int>(a.njobs, nj);
+    gst<int>(a.njobs + 2, nx);
+  }
+}
+
+// Gate / up + SwiGLU of a prefill pass on the matrix cores over a job list of at most sixteen
+// users a job (MoE: kp_route's, in global memory; dense, jobs null: rows 16j .. 16j + 15 as
+// job j): items (job, 16 h rows) as kd_gateup_mq takes them, workgroup b the items
+// [b n / G, (b + 1) n / G); at each job the users' Q8_K rows are staged in LDS (slot = the
+// user's place in the job). An item's arithmetic, and so each h value, is kd_gateup_mq's.
+template <int T>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(T == T_Q4K ? 4 : 2))) void kp_gateup_mq(const DecGateUpMArgs a,
+                                                                                                                     const Job *jobs,
+                                                                                                                     const int *njobs) {
+  constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int sj[JR];
+  __shared__ float red[2][NW][2][4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n_ff = a.n_ff, cols = (int)a.gate.cols, nb = cols >> 8, m = a.m;
+  const int TX = (n_ff + 15) / 16;
+  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
+  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)MAX_M * cols + 15) & ~(size_t)15));
+  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)MAX_M * cols + 15) & ~(size_t)15) + (((size_t)MAX_M * nb * 4 + 15) & ~(size_t)15));
+  SPX_L uint32_t *lc = (SPX_L uint32_t *)(smem + mm_act_bytes(MAX_M, cols));
+  const int nj = jobs ? gld<int>(njobs) : (m + MAX_M - 1) / MAX_M;
+  const int n = TX * nj, G = gridDim.x;
+  const int i0 = (int)((int64_t)blockIdx.x * n / G), i1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
+  auto stage_job = [&](int j) {
+    __syncthreads();  // the previous job's users are done with
+    if ((int)threadIdx.x < JR) {
+      const int f = threadIdx.x;
+      sj[f] = jobs ? gld<int>(reinterpret_cast<const int *>(jobs + j) + f)
+                   : f == 0 ? 0 : f == 1 ? min(MAX_M, m - MAX_M * j) : MAX_M * j + (f - 2) % MAX_M;
+    }
+    __syncthreads();
+    stage_q8<NW * 64>(a.y, (const SPX_L int *)(sj + 2), sj[1], cols, lq, ld, lbs);
+    __syncthreads();
+    mq_corr_stage(sj[1] * nb, lbs, lc);
+    __syncthreads();
+  };
+  const int nbw = wave < nb ? (nb - wave + NW - 1) / NW : 0, U2 = 2 * max(nbw, 1);
+  const int c16 = lane & 15;
+  auto item_rows = [&](int i, int64_t &row0, int &nrows) {
+    const int j = i / TX, x = i - j * TX;
+    const int e = jobs ? min(max(gld<int>(reinterpret_cast<const int *>(jobs + j)), 0), a.gate.n_expert - 1) : 0;
+    row0 = (int64_t)e * a.gate.rows + (int64_t)x * 16;
+    nrows = min(16, n_ff - x * 16);
+  };
+  int i = i0, u = 0, buf = 0;
+  int64_t crow0 = 0;
+  int cnrows = 1;
+  if (i < i1) item_rows(i, crow0, cnrows);
+  MqRaw cur, nxt;
+  if (i < i1 && nbw > 0) mq_load<T>(cur, a.gate.pl, crow0, cnrows, nb, wave);
+  if (i < i1) stage_job(i / TX);
+  float ag[4] = {0.f, 0.f, 0.f, 0.f}, cg[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f}, cu[4] = {0.f, 0.f, 0.f, 0.f};
+  while (i < i1) {
+    int in = i, un = u + 1;
+    if (un >= U2) { un = 0; in++; }
+    int64_t nrow0 = crow0;
+    int nnrows = cnrows;
+    if (un == 0 && in < i1) item_rows(in, nrow0, nnrows);
+    if (in < i1 && nbw > 0) mq_load<T>(nxt, (un & 1) ? a.up.pl : a.gate.pl, nrow0, nnrows, nb, wave + NW * (un >> 1));
+    const int j = i / TX, nv = sj[1];
+    if (nbw > 0) {
+      const MqVec vv = mq_vecs(nv, MqIdentity{});
+      if (u & 1) mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lc, au, cu);
+      else mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lc, ag, cg);
+    }
+    if (un == 0) {  // item i complete
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        red[buf][wave][0][q][lane] = ag[q] - cg[q];
+        red[buf][wave][1][q][lane] = au[q] - cu[q];
+        ag[q] = cg[q] = au[q] = cu[q] = 0.f;
+      }
+      __syncthreads();
+      if (wave < 4) {
+        const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
+        float g = red[buf][0][0][q][lane], up = red[buf][0][1][q][lane];
+        for (int w2 = 1; w2 < NW; w2++) { g = g + red[buf][w2][0][q][lane]; up = up + red[buf][w2][1][q][lane]; }
+        const int x = i - j * TX;
+        if (v < nv && r < cnrows) gst<float>(a.h + (int64_t)sj[2 + MAX_M + v] * n_ff + x * 16 + r, g / (1.0f + expf(-g)) * up);
+      }
+      buf ^= 1;
+      crow0 = nrow0;
+      cnrows = nnrows;
+      if (in < i1 && in / TX != j) stage_job(in / TX);
+    }
+    cur = nxt;
+    i = in;
+    u = un;
+  }
+}
+
 // ------------------------------------------------------------------ launchers
 static int cu_count() {
   static int n = 0;
@@ -1545,7 +1725,7 @@ hipError_t launch_dec_down(const DecDownArgs &a, hipStream_t s) {
 
 // ------------------------------------------------------------------ launchers, m rows
 hipError_t launch_dec_norm(const DecNormArgs &a, int m, hipStream_t s) {
-  if (a.dim % 256 || a.dim > 256 * DEC_MAXNB || !a.nw || m < 1 || m > MAX_M) return hipErrorInvalidValue;
+  if (a.dim % 256 || a.dim > 256 * DEC_MAXNB || !a.nw || m < 1 || m > PMAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kd_norm, dim3(m), dim3(256), 0, s, a);
   return hipGetLastError();
 }
@@ -1592,15 +1772,25 @@ hipError_t launch_dec_mm(const DecMMArgs &a, int grid, hipStream_t s) {
 }
 
 hipError_t launch_dec_mq(const DecMMArgs &a, int grid, hipStream_t s) {
-  const int nb = a.cols >> 8;
-  if (a.nseg < 1 || a.nseg > 3 || grid < 1 || nb < 1 || nb > DEC_MAXNB || a.cols % 256 || a.m < 1 || a.m > MAX_M) return hipErrorInvalidValue;
+  const int nb = a.cols >> 8, nvg = (a.m + 15) / 16;
+  if (a.nseg < 1 || a.nseg > 3 || grid < 1 || nb < 1 || nb > DEC_MAXNB || a.cols % 256 || a.m < 1 || a.m > PMAX) return hipErrorInvalidValue;
+  if (nvg > 1 && grid % 8) return hipErrorInvalidValue;  // tile ranges come in eights (one per XCD)
   for (int i = 0; i < a.nseg; i++)
     if ((a.w[i].dtype != T_Q4K && a.w[i].dtype != T_Q6K) || a.w[i].nb != nb) return hipErrorInvalidValue;
   if (a.res_out && a.nseg != 1) return hipErrorInvalidValue;
-  const size_t sm = mm_act_bytes(a.m, a.cols) + mq_corr_bytes(a.m, a.cols);
+  if (a.best && a.nbest != grid) return hipErrorInvalidValue;
+  const int mv = std::min(a.m, MAX_M);
+  const size_t sm = mm_act_bytes(mv, a.cols) + mq_corr_bytes(mv, a.cols);
   SPX_DLDS(kd_mq, sm);
-  hipLaunchKernelGGL(kd_mq, dim3(grid), dim3(DEC_MM_NW * 64), sm, s, a);
+  hipLaunchKernelGGL(kd_mq, dim3(grid * nvg), dim3(DEC_MM_NW * 64), sm, s, a);
   return hipGetLastError();
+}
+
+int dec_mq_grid(int tiles, int m) {
+  const int slots = 2 * cu_count();
+  if (m <= MAX_M) return std::min(tiles, slots);
+  const int nvg = (m + 15) / 16, per = (slots / nvg + 7) / 8 * 8;
+  return std::max(8, std::min((tiles + 7) / 8 * 8, per));
 }
 
 hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &args, int max_jobs, hipStream_t s) {
@@ -1628,8 +1818,30 @@ hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &args, int max_jobs, hipStr
   return hipGetLastError();
 }
 
+hipError_t launch_kp_route(const DecRouteArgs &a, hipStream_t s) {
+  if (a.m < 1 || a.m > PMAX || a.n_expert < 1 || a.n_expert > 256 || a.n_used < 1 || a.n_used > 32 || a.n_used > a.n_expert || !a.jobs ||
+      !a.njobs)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kp_route, dim3(1), dim3(1024), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_kp_gateup_mq(const DecGateUpMArgs &a, const Job *jobs, const int *njobs, int max_jobs, hipStream_t s) {
+  const int nb = (int)(a.gate.cols >> 8), cols = (int)a.gate.cols;
+  if (a.gate.cols % 256 || nb > DEC_MAXNB || a.gate.nb != nb || a.up.nb != nb || a.gate.dtype != a.up.dtype || a.m < 1 || a.m > PMAX ||
+      max_jobs < 1 || max_jobs > 512 || (jobs && !njobs))
+    return hipErrorInvalidValue;
+  const size_t sm = mm_act_bytes(MAX_M, cols) + mq_corr_bytes(MAX_M, cols);
+  const int items = ((a.n_ff + 15) / 16) * (jobs ? max_jobs : (a.m + MAX_M - 1) / MAX_M);
+  const dim3 grid((unsigned)std::min(items, (a.gate.dtype == T_Q4K ? 2 : 1) * cu_count())), b(DEC_MM_NW * 64);
+  if (a.gate.dtype == T_Q4K) { SPX_DLDS((kp_gateup_mq<T_Q4K>), sm); hipLaunchKernelGGL((kp_gateup_mq<T_Q4K>), grid, b, sm, s, a, jobs, njobs); }
+  else if (a.gate.dtype == T_Q6K) { SPX_DLDS((kp_gateup_mq<T_Q6K>), sm); hipLaunchKernelGGL((kp_gateup_mq<T_Q6K>), grid, b, sm, s, a, jobs, njobs); }
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s) {
-  if (a.w.cols % 256 || a.w.nb > 4 || a.max_jobs < 1 || a.max_jobs > 512 || a.max_jobs > a.w.n_expert || !a.h || !a.yd) return hipErrorInvalidValue;
+  if (a.w.cols % 256 || a.w.nb > 4 || a.max_jobs < 1 || a.max_jobs > 512 || !a.h || !a.yd) return hipErrorInvalidValue;
   const int tx = (int)((a.w.rows + DEC_MM_NW * 16 - 1) / (DEC_MM_NW * 16));
   const dim3 grid((unsigned)std::min(tx * a.max_jobs, 2 * cu_count())), b(DEC_MM_NW * 64);
   const size_t sm = downm_lds_bytes((int)a.w.cols) + mq_corr_bytes(MAX_M, (int)a.w.cols);
@@ -1640,8 +1852,8 @@ hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_dec_router_m(const DecRouterMArgs &a, hipStream_t s) {
-  if (a.dim % 256 || a.dim > 256 * DEC_MAXNB || a.m < 1 || a.m > MAX_M) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kd_router_m, dim3(a.n_expert), dim3(256), 0, s, a);
+  if (a.dim % 256 || a.dim > 256 * DEC_MAXNB || a.m < 1 || a.m > PMAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kd_router_m, dim3(a.n_expert, (a.m + MAX_M - 1) / MAX_M), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

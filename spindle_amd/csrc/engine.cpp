@@ -46,7 +46,7 @@ struct LayerW {
   spx_tensor *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
   bool moe = false;
   spx_tensor *gate = nullptr, *up = nullptr, *down = nullptr, *router = nullptr;
-  int *njobs = nullptr;  // device: jobs of this layer's last pass (union of chosen experts)
+  int *njobs = nullptr;  // device: [0] jobs of this layer's last pass, [2] experts with users (passes of > 16 rows)
 };
 
 bool is_kq(const spx_tensor *t) { return t && (t->v.dtype == T_Q4K || t->v.dtype == T_Q6K); }
@@ -107,8 +107,10 @@ struct spx_engine {
   int *chosen = nullptr, *nkeep = nullptr, *expert_count = nullptr;
   float *weights = nullptr;
   Job *jobs = nullptr;
-  float *yd = nullptr;  // [16 * n_used][dim]: expert outputs of a multi-row pass, combined by the next norm
-  hipGraphExec_t graph[MAX_M + 1] = {};
+  float *yd = nullptr;  // [PMAX * n_used][dim]: expert outputs of a multi-row pass, combined by the next norm
+  float *qp = nullptr;  // [PMAX][q_dim]: prepared queries of a prefill pass
+  int last_m = 0;       // rows of the last pass
+  hipGraphExec_t graph[PMAX + 1] = {};
   int n_used = 0;
   // kernel-class timing (eager passes only): event pairs recorded around each launch
   struct ProfRec { int cls, layer; double bytes; bool per_expert; hipEvent_t a, b; };
@@ -123,8 +125,10 @@ struct spx_engine {
   T *dalloc(size_t n) {
     void *p = nullptr;
     if (hipMalloc(&p, std::max<size_t>(n * sizeof(T), 16)) != hipSuccess) return nullptr;
-    (void)hipMemset(p, 0, std::max<size_t>(n * sizeof(T), 16));
     allocs.push_back(p);
+    // the context's stream does not wait for the null stream: finish the clear before any
+    // launch on it can touch the buffer
+    if (hipMemset(p, 0, std::max<size_t>(n * sizeof(T), 16)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return nullptr;
     return static_cast<T *>(p);
   }
   // permuted Q8_K buffer for nv vectors of cols columns
@@ -518,6 +522,13 @@ int enqueue_pass_m(spx_engine *E, int m) {
   };
   auto gshape = [](const spx_tensor *t) { int G, R; rp_shape(t->v.nb, G, R); return G; };
   auto qtiles = [](const spx_tensor *t) { return (int)((t->v.rows + 15) / 16); };
+  // passes of more than 16 rows (prefill; matrix cores only): the matvecs take the rows in
+  // groups of 16 per workgroup, the attention rows are prepared once (launch_rows_prep), the
+  // MoE jobs hold at most 16 users (kp_route) and are staged job by job (kp_gateup_mq)
+  const bool big = m > MAX_M;
+  if (big && !E->mq) return fail("passes of more than 16 rows run on the matrix cores only");
+  auto mq_grid = [&](int tiles) { return big ? dec_mq_grid(tiles, m) : std::min(tiles, 2 * E->n_cu); };
+  const int maxj = std::min(512, std::min(c.n_expert, m * nu) + (m * nu) / MAX_M);  // jobs of <= 16 users
   bool combine = false;  // the last MoE layer's expert outputs wait in yd for the next norm
   auto norm = [&](const float *x, const float *nw, float *xn_out, Q8KP q) {
     DecNormArgs na{};
@@ -551,7 +562,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
       int total = 0;
       for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.ld_out[i] = ld3[i]; a.tiles[i] = E->mq ? qtiles(w3[i]) : mtiles(w3[i]); total += a.tiles[i]; }
       a.nseg = 3; a.G = gshape(ly.wq); a.y = E->xq2; a.cols = dim; a.m = m;
-      SPX_HIP(E->mq ? launch_dec_mq(a, std::min(total, 2 * E->n_cu), s) : launch_dec_mm(a, dec_mm_grid(total), s));
+      SPX_HIP(E->mq ? launch_dec_mq(a, mq_grid(total), s) : launch_dec_mm(a, dec_mm_grid(total), s));
     }
     const bool att_q_fused = ((c.n_heads / c.n_kv_heads) * hd) % 256 == 0;
     {
@@ -564,6 +575,11 @@ int enqueue_pass_m(spx_engine *E, int m) {
       aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
       aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
       aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
+      if (big) {
+        SPX_HIP(launch_rows_prep(aa, E->qp, m, E->st_dev, s));
+        aa.q = E->qp;
+        aa.prepped = 1;
+      }
       SPX_HIP(launch_attention(aa, m, E->st_dev, s));
     }
     if (!att_q_fused) { ProfScope ps(E, PC_QUANT, 0); SPX_HIP(launch_q8kp_quantize(E->att, E->q_dim, E->q_dim, m, E->aq, s)); }
@@ -573,7 +589,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
       a.w[0] = ly.wo->v; a.out[0] = E->proj; a.ld_out[0] = dim; a.tiles[0] = E->mq ? qtiles(ly.wo) : mtiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
       a.y = E->aq; a.cols = E->q_dim; a.m = m;
       a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
-      SPX_HIP(E->mq ? launch_dec_mq(a, std::min(a.tiles[0], 2 * E->n_cu), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
+      SPX_HIP(E->mq ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
     }
     const int nff = (int)ly.gate->v.rows;
     {
@@ -592,18 +608,24 @@ int enqueue_pass_m(spx_engine *E, int m) {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up), l, true);
         ga.rt = DecRouteArgs{E->rlog, c.n_expert, c.n_expert_used, c.expert_norm, m, c.moe_prune, E->chosen, E->weights, E->nkeep,
                              E->jobs, ly.njobs, E->expert_count + (size_t)l * c.n_expert};
-        SPX_HIP(E->mq && E->mq_gateup ? launch_dec_gateup_mq(ga, std::min(m * nu, c.n_expert), s) : launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
+        if (big) {
+          SPX_HIP(launch_kp_route(ga.rt, s));
+          SPX_HIP(launch_kp_gateup_mq(ga, E->jobs, ly.njobs, maxj, s));
+        } else {
+          SPX_HIP(E->mq && E->mq_gateup ? launch_dec_gateup_mq(ga, std::min(m * nu, c.n_expert), s) : launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
+        }
       }
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
-        DecDownMArgs da{ly.down->v, E->h, E->jobs, ly.njobs, E->yd, std::min(m * nu, c.n_expert)};
-        SPX_HIP(E->mq && m >= E->mq_down_rows ? launch_dec_down_mq(da, s) : launch_dec_down_m(da, s));
+        DecDownMArgs da{ly.down->v, E->h, E->jobs, ly.njobs, E->yd, big ? maxj : std::min(m * nu, c.n_expert)};
+        SPX_HIP(E->mq && (big || m >= E->mq_down_rows) ? launch_dec_down_mq(da, s) : launch_dec_down_m(da, s));
         combine = true;  // + weighted combine + residual in the next norm (xB -> xA)
       }
     } else {  // ffn_forward_multi (:616-646)
       {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
-        SPX_HIP(E->mq && E->mq_gateup ? launch_dec_gateup_mq(ga, 1, s) : launch_dec_gateup_m(ga, 1, s));
+        if (big) SPX_HIP(launch_kp_gateup_mq(ga, nullptr, nullptr, 1, s));
+        else SPX_HIP(E->mq && E->mq_gateup ? launch_dec_gateup_mq(ga, 1, s) : launch_dec_gateup_m(ga, 1, s));
         SPX_HIP(launch_q8kp_quantize(E->h, nff, nff, m, E->hq, s));
       }
       {
@@ -612,7 +634,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
         a.w[0] = ly.down->v; a.out[0] = E->ffn; a.ld_out[0] = dim; a.tiles[0] = E->mq ? qtiles(ly.down) : mtiles(ly.down); a.nseg = 1;
         a.G = gshape(ly.down); a.y = E->hq; a.cols = nff; a.m = m;
         a.res_in = E->xB; a.res_out = E->xA; a.rscale = c.residual_scale;
-        SPX_HIP(E->mq ? launch_dec_mq(a, std::min(a.tiles[0], 2 * E->n_cu), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
+        SPX_HIP(E->mq ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
       }
     }
   }
@@ -623,7 +645,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
     DecMMArgs a{};
     a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.ld_out[0] = c.vocab; a.tiles[0] = E->mq ? qtiles(E->lm_head) : mtiles(E->lm_head); a.nseg = 1;
     a.G = gshape(E->lm_head); a.y = E->xq; a.cols = dim; a.m = m;
-    grid = std::min(a.tiles[0], E->mq ? 2 * E->n_cu : 512);
+    grid = E->mq ? mq_grid(a.tiles[0]) : std::min(a.tiles[0], 512);
     a.best = E->best; a.nbest = grid; a.lscale = c.logit_scale;
     SPX_HIP(E->mq ? launch_dec_mq(a, grid, s) : launch_dec_mm(a, grid, s));
   }
@@ -683,7 +705,7 @@ bool persist_used(const spx_engine *E, int m) {
 int persist_check(spx_engine *E) {
   if (*E->perr_host == 0) return 0;
   *E->perr_host = 0;
-  (void)hipMemset(E->pa.err, 0, sizeof(int));
+  (void)hipMemsetAsync(E->pa.err, 0, sizeof(int), E->ctx->stream);
   E->persist_ok = false;
   return fail("persistent decode pass: a device-wide barrier timed out, the pass is void; one-row passes run on the decode "
               "pipeline from now on");
@@ -855,7 +877,7 @@ int spx_engine_prepare(spx_engine *E) {
     for (spx_tensor *t : {ly.wq, ly.wk, ly.wv, ly.wo, ly.gate, ly.up, ly.down, E->lm_head})
       if (t && is_kq(t) && t->v.cols % 256) return fail("K-quant tensors need cols % 256 == 0");
   // device buffers
-  const int M = MAX_M, nu = std::max(1, c.n_expert_used), nv = M * nu;
+  const int M = PMAX, nu = std::max(1, c.n_expert_used), nv = M * nu;
   const int64_t kvn = (int64_t)c.n_layers * c.max_seq * E->kv_dim;
   const int qmax = std::max({c.dim, E->q_dim});
   const int nff = std::max(256, E->n_ff);
@@ -866,6 +888,7 @@ int spx_engine_prepare(spx_engine *E) {
             (E->v = E->dalloc<float>((size_t)M * E->kv_dim)) && (E->att = E->dalloc<float>((size_t)M * E->q_dim)) &&
             (E->proj = E->dalloc<float>((size_t)M * c.dim)) && (E->ffn = E->dalloc<float>((size_t)M * c.dim)) &&
             (E->xn2 = E->dalloc<float>((size_t)M * qmax)) && (E->xn = E->dalloc<float>((size_t)M * c.dim)) &&
+            (E->qp = E->dalloc<float>((size_t)M * E->q_dim)) &&
             (E->h = E->dalloc<float>((size_t)nv * nff)) && (E->yd = E->dalloc<float>((size_t)nv * c.dim)) && (E->rlog = E->dalloc<float>((size_t)M * std::max(1, c.n_expert))) &&
             (E->logits = E->dalloc<float>((size_t)M * c.vocab)) && (E->amax = E->dalloc<int>(M)) &&
             (E->best = E->dalloc<unsigned long long>((size_t)M * std::max<int64_t>(E->lm_grid, c.vocab / 4 + 1))) &&
@@ -873,14 +896,14 @@ int spx_engine_prepare(spx_engine *E) {
             (E->part_ml = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * 2)) &&
             (E->part_o = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * c.head_dim)) &&
             (E->att_cnt = E->dalloc<int>((size_t)c.n_kv_heads * ATT_QT * (1 + ATT_GMAX) * CNT_STRIDE)) && (E->rt_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) &&
-            (E->gu_cnt = E->dalloc<int>((size_t)nv * (nff / 256 + 1) * (1 + GU_SUB) * CNT_STRIDE)) && (E->chosen = E->dalloc<int>(16 * 32)) &&
-            (E->nkeep = E->dalloc<int>(16)) && (E->weights = E->dalloc<float>(16 * 32)) && (E->jobs = E->dalloc<Job>(512)) &&
+            (E->gu_cnt = E->dalloc<int>((size_t)MAX_M * nu * (nff / 256 + 1) * (1 + GU_SUB) * CNT_STRIDE)) && (E->chosen = E->dalloc<int>(M * 32)) &&
+            (E->nkeep = E->dalloc<int>(M)) && (E->weights = E->dalloc<float>(M * 32)) && (E->jobs = E->dalloc<Job>(512)) &&
             (E->expert_count = E->dalloc<int>((size_t)c.n_layers * std::max(1, c.n_expert))) &&
             E->q8alloc(E->aq, M, ((E->q_dim + 255) / 256) * 256) && E->q8alloc(E->xq2, M, ((c.dim + 255) / 256) * 256) &&
             E->q8alloc(E->xq, M, ((c.dim + 255) / 256) * 256) && E->q8alloc(E->hq, nv, nff);
   if (!ok) return fail("spx_engine_prepare: out of device memory");
   for (auto &ly : E->L)
-    if (ly.moe && !(ly.njobs = E->dalloc<int>(2))) return fail("out of device memory");
+    if (ly.moe && !(ly.njobs = E->dalloc<int>(3))) return fail("out of device memory");
   SPX_HIP(hipHostMalloc(&E->st_host, sizeof(StepRec)));
   // RoPE table: inv_freq = 1/theta^(2i/hd) (Rope::new :1399-1402); angle = pos * inv_freq.
   const int half = c.head_dim / 2;
@@ -966,7 +989,7 @@ int spx_engine_set_decode(spx_engine *E, int on) {
   if (!E) return fail("null engine");
   if (E->dec_on != (on != 0)) {  // the captured graphs hold the other pipeline: capture again
     SPX_HIP(hipStreamSynchronize(E->ctx->stream));
-    for (int slot = 0; slot <= MAX_M; slot++)
+    for (int slot = 0; slot <= PMAX; slot++)
       if (E->graph[slot]) { (void)hipGraphExecDestroy(E->graph[slot]); E->graph[slot] = nullptr; }
   }
   E->dec_on = on != 0;
@@ -977,7 +1000,7 @@ int spx_engine_set_mfma(spx_engine *E, int on) {
   if (!E) return fail("null engine");
   if (E->mq != (on != 0)) {  // the captured multi-row graphs hold the other kernels: capture again
     SPX_HIP(hipStreamSynchronize(E->ctx->stream));
-    for (int slot = 0; slot <= MAX_M; slot++)
+    for (int slot = 0; slot <= PMAX; slot++)
       if (E->graph[slot]) { (void)hipGraphExecDestroy(E->graph[slot]); E->graph[slot] = nullptr; }
   }
   E->mq = on != 0;
@@ -1006,10 +1029,21 @@ int spx_engine_persist_active(spx_engine *E, int *active) {
 int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, float *hidden, float *logits, int32_t *argmax) {
   if (!E || !ids) return fail("spx_engine_forward: null argument");
   if (!E->prepared) return fail("spx_engine_forward: call spx_engine_prepare first");
-  if (m < 1 || m > MAX_M) return fail("spx_engine_forward: m must be in 1..16");
+  if (m < 1 || m > PMAX) return fail("spx_engine_forward: m must be in 1.." + std::to_string(PMAX));
   if (start_pos < 0 || start_pos + m > E->c.max_seq) return fail("spx_engine_forward: positions beyond max_seq (the KV window is full)");
   for (int i = 0; i < m; i++)
     if (ids[i] < 0 || ids[i] >= E->c.vocab) return fail("spx_engine_forward: token id out of range");
+  if (m > MAX_M && !(E->dec_ok && E->dec_on && E->mq)) {
+    // no prefill kernels for this model / setting: passes of at most 16 rows, one after the
+    // other (a row's results do not depend on the rows that share its pass)
+    for (int r0 = 0; r0 < m; r0 += MAX_M) {
+      const int n = std::min(MAX_M, m - r0);
+      if (int r = spx_engine_forward(E, ids + r0, n, start_pos + r0, hidden ? hidden + (int64_t)r0 * E->c.dim : nullptr,
+                                     logits ? logits + (int64_t)r0 * E->c.vocab : nullptr, argmax ? argmax + r0 : nullptr))
+        return r;
+    }
+    return 0;
+  }
   hipStream_t s = E->ctx->stream;
   SPX_HIP(hipSetDevice(E->ctx->device));
   SPX_HIP(hipStreamSynchronize(s));
@@ -1017,6 +1051,7 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
   E->st_host->start = start_pos;
   E->st_host->step = 0;
   for (int i = 0; i < m; i++) E->st_host->ids[i] = ids[i];
+  E->last_m = m;
   SPX_HIP(hipMemcpyAsync(E->st_dev, E->st_host, sizeof(StepRec), hipMemcpyHostToDevice, s));
   if (int r = run_forward(E, m)) return r;
   if (hidden) SPX_HIP(hipMemcpyAsync(hidden, E->xn, sizeof(float) * m * E->c.dim, hipMemcpyDeviceToHost, s));
@@ -1028,9 +1063,9 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
   if (pers)
     if (int r = persist_check(E)) return r;
   if (E->profiling && !E->prof.empty()) {
-    std::vector<int32_t> nj(E->c.n_layers, 0);
+    std::vector<int32_t> nj(E->c.n_layers, 0);  // experts run per layer (their slabs' bytes)
     for (int l = 0; l < E->c.n_layers; l++)
-      if (E->L[l].moe) SPX_HIP(hipMemcpy(&nj[l], E->L[l].njobs, sizeof(int), hipMemcpyDeviceToHost));
+      if (E->L[l].moe) SPX_HIP(hipMemcpy(&nj[l], E->L[l].njobs + (m > MAX_M ? 2 : 0), sizeof(int), hipMemcpyDeviceToHost));
     const int64_t kv_pos_bytes = (int64_t)E->kv_dim * 2 * 2;  // K and V, f16
     for (auto &r : E->prof) {
       float ms = 0.0f;
@@ -1089,6 +1124,7 @@ int spx_engine_decode(spx_engine *E, int32_t token, int start_pos, int n, int32_
   E->st_host->start = start_pos;
   E->st_host->ids[0] = token;
   E->st_host->step = 0;
+  E->last_m = 1;
   SPX_HIP(hipMemcpyAsync(E->st_dev, E->st_host, sizeof(StepRec), hipMemcpyHostToDevice, s));
   const bool pers = persist_used(E, 1);
   for (int i = 0; i < n; i++)
@@ -1124,7 +1160,7 @@ int spx_engine_last_experts(spx_engine *E, int32_t *njobs_per_layer) {
   SPX_HIP(hipStreamSynchronize(E->ctx->stream));
   for (int l = 0; l < E->c.n_layers; l++) {
     njobs_per_layer[l] = 0;
-    if (E->L[l].moe) SPX_HIP(hipMemcpy(&njobs_per_layer[l], E->L[l].njobs, sizeof(int), hipMemcpyDeviceToHost));
+    if (E->L[l].moe) SPX_HIP(hipMemcpy(&njobs_per_layer[l], E->L[l].njobs + (E->last_m > MAX_M ? 2 : 0), sizeof(int), hipMemcpyDeviceToHost));
   }
   return 0;
 }
@@ -1297,15 +1333,17 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
                         spx_gen_stats *st) {
   if (!E || !prompt || !p || !out || !st) return fail("spx_engine_generate: null argument");
   if (n_prompt < 1 || max_new < 1) return fail("spx_engine_generate: empty prompt or max_new < 1");
-  if (p->kv_keep < 0 || p->kv_keep + 2 * MAX_M > E->c.max_seq) return fail("spx_engine_generate: kv_keep must leave room for a pass");
+  const int chunk = p->prefill_chunk > 0 ? p->prefill_chunk : PMAX;  // feed's chunks of 128 (:3090)
+  if (chunk > PMAX) return fail("spx_engine_generate: prefill_chunk must be at most " + std::to_string(PMAX));
+  if (p->kv_keep < 0 || p->kv_keep + std::max(chunk, MAX_M) + MAX_M > E->c.max_seq)
+    return fail("spx_engine_generate: kv_keep must leave room for a prompt chunk and a pass");
   if (p->speculate && (p->draft_len < 1 || p->draft_len > MAX_M - 1)) return fail("spx_engine_generate: draft_len must be in 1..15");
   if (p->n_cached < 0 || p->n_cached >= n_prompt) return fail("spx_engine_generate: n_cached must be in 0..n_prompt-1");
   memset(st, 0, sizeof(*st));
   std::vector<int32_t> corpus;
   remember(corpus, prompt, n_prompt);
-  const int chunk = std::min(MAX_M, p->prefill_chunk > 0 ? p->prefill_chunk : MAX_M);
   int pos = p->n_cached;
-  int32_t am[MAX_M];
+  int32_t am[PMAX];
   int64_t t0 = now_us();
   for (int s = p->n_cached; s < n_prompt; s += chunk) {  // feed (:3041-3104)
     const int cnt = std::min(chunk, n_prompt - s);
@@ -1320,7 +1358,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
   int d_pos = p->n_cached;
   bool shifted = false;
   if (D) {
-    int32_t dam[MAX_M];
+    int32_t dam[PMAX];
     for (int s = p->n_cached; s < n_prompt; s += chunk) {
       const int cnt = std::min(chunk, n_prompt - s);
       if (int r = spx_engine_ensure_kv_room(D, p->kv_keep, d_pos, cnt, &d_pos)) return r;

@@ -5,8 +5,9 @@
 
 namespace spx {
 
-constexpr int MAX_M = 16;       // rows per verify / prefill pass
-constexpr int ATT_QMAX = 128;   // query heads x rows per kv head in one pass (16 rows x 8)
+constexpr int MAX_M = 16;       // rows per verify pass (and per pass of the fused kernels)
+constexpr int PMAX = 128;       // rows per prefill pass (forward_batch_slice's prompt chunks)
+constexpr int ATT_QMAX = PMAX * 8;  // query heads x rows per kv head in one pass (128 rows x 8)
 constexpr int ATT_QT = ATT_QMAX / 16;  // attention: 16-query tiles per kv head
 constexpr int ATT_GRP = 16;     // attention: chunks merged per group
 constexpr int ATT_GMAX = 16;    // attention: groups per kv head (max_seq <= 64 * 16 * 16)
@@ -20,7 +21,7 @@ constexpr int GU_USERS = 2;     // users per gate/up job (an expert's users spli
 struct StepRec {
   int m;
   int start;
-  int ids[MAX_M];
+  int ids[PMAX];
   int step;           // back-to-back decode: passes done (index into the token history)
 };
 
@@ -83,6 +84,9 @@ struct AttnArgs {
   int layer, max_seq, kv_dim, hd, n_heads, n_kv, neox;
   int nch;                            // chunks launched per kv head (>= max_seq / 64)
   int nslot;                          // partial slots per kv head: nch chunks, then group partials
+  // 1: q holds the prepared queries (bias, norm, RoPE applied) and the pass's K / V rows are in
+  // the cache already (launch_rows_prep); multi-row passes only
+  int prepped;
   float eps, scale;
 };
 
@@ -142,6 +146,10 @@ hipError_t launch_embed(const TensorView &e, const StepRec *st, float escale, co
 // mode 0: eight rows per wavefront (tiles); 1: row-parallel (integer only)
 hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int grid, hipStream_t s);
 hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);
+// The attention block's row preparation of the step record's pass of m rows (bias, per-head RMSNorm and RoPE of
+// q and k, as the attention kernel does it): prepared queries to qp [m][q_dim], K / V rows to
+// the cache (f16 RNE); then launch_attention with a.prepped = 1 reads them from there
+hipError_t launch_rows_prep(const AttnArgs &a, float *qp, int m, const StepRec *st, hipStream_t s);
 hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStream_t s);
 hipError_t launch_gateup(const GUArgs &a, int mt, int mode, const StepRec *st, int max_jobs, hipStream_t s);
 hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, hipStream_t s);

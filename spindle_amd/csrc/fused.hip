@@ -823,6 +823,38 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
   attn_item<HD, MERGE, false>(a, m, start, c, h, qt, smem, kr, vr, &pre);
 }
 
+// Row preparation of a prefill pass: one wavefront per (row b, head j); heads 0 .. n_heads-1
+// are the queries (head_prep -> qp), then the n_kv keys (head_prep -> f16 RNE -> K cache) and
+// the n_kv values (bias -> f16 -> V cache), the same operations as attn_item makes on them.
+__global__ __launch_bounds__(64) void k_rows_prep(const AttnArgs a, float *qp, const StepRec *st) {
+  const int b = blockIdx.x, j = blockIdx.y, lane = threadIdx.x & 63, hd = a.hd, half = hd >> 1;
+  if (b >= st->m) return;
+  const int pos = st->start + b;
+  const int da = a.neox ? lane : 2 * lane, db = a.neox ? lane + half : 2 * lane + 1;
+  const float2 *rope = a.rope + (int64_t)pos * half;
+  float e0, e1;
+  if (j < a.n_heads) {
+    head_prep(a.q + ((int64_t)b * a.n_heads + j) * hd, a.q_bias ? a.q_bias + j * hd : nullptr, a.q_norm, rope, hd, a.neox, a.eps, e0, e1);
+    if (lane < half) {
+      float *o = qp + ((int64_t)b * a.n_heads + j) * hd;
+      o[da] = e0;
+      o[db] = e1;
+    }
+    return;
+  }
+  const int jj = j - a.n_heads, h = jj % a.n_kv;
+  const bool is_k = jj < a.n_kv;
+  if (is_k)
+    head_prep(a.k + (int64_t)b * a.kv_dim + h * hd, a.k_bias ? a.k_bias + h * hd : nullptr, a.k_norm, rope, hd, a.neox, a.eps, e0, e1);
+  else
+    head_prep(a.v + (int64_t)b * a.kv_dim + h * hd, a.v_bias ? a.v_bias + h * hd : nullptr, nullptr, nullptr, hd, a.neox, a.eps, e0, e1);
+  if (lane < half) {
+    __half *d = (is_k ? a.kc : a.vc) + ((int64_t)a.layer * a.max_seq + pos) * a.kv_dim + h * hd;
+    d[da] = __float2half_rn(e0);
+    d[db] = __float2half_rn(e1);
+  }
+}
+
 // ------------------------------------------------------------------ MoE router + routing
 // F32 router rows (one per workgroup; wavefront w, lane j hold float4s w*64 + j + 256k of the
 // row in registers; each vector's dot is the lane's fma chain, the wave tree, then the four
@@ -1390,10 +1422,16 @@ hipError_t launch_attention_partials(const AttnArgs &a, const StepRec *st, hipSt
 
 hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
   const int nqt = (m * (a.n_heads / a.n_kv) + 15) / 16;
-  if (nqt > ATT_QT) return hipErrorInvalidValue;
+  if (nqt > ATT_QT || (m > MAX_M && !a.prepped)) return hipErrorInvalidValue;
   if (a.hd == 128) launch_attn_t<128>(a, nqt, st, s);
   else if (a.hd == 64) launch_attn_t<64>(a, nqt, st, s);
   else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_rows_prep(const AttnArgs &a, float *qp, int m, const StepRec *st, hipStream_t s) {
+  if (m < 1 || m > PMAX || (a.hd != 64 && a.hd != 128) || !qp) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rows_prep, dim3(m, a.n_heads + 2 * a.n_kv), dim3(64), 0, s, a, qp, st);
   return hipGetLastError();
 }
 

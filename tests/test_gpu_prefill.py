@@ -1,0 +1,185 @@
+"""Prefill passes of 17..128 rows (forward_batch_slice at M up to 128, the prompt chunks of feed,
+smollm_chat.rs:3090-3101) on the prefill kernels: the matvecs in 16-vector groups, the
+attention rows prepared once, MoE jobs of at most 16 users staged job by job.
+
+A row's arithmetic in these kernels is the same as in a pass of at most 16 rows on the int8
+matrix cores (the same block split, the same fp32 sums in the same order), so the bar is
+bitwise: hidden states, logits, greedy picks and the KV cache of a 128-row pass equal those of
+the same tokens in 16-row passes. The 16-row passes are held to the oracle by
+test_gpu_decode.py / test_gpu_engine.py; the prefill pass is also checked against the oracle
+directly with the bars of those tests."""
+import numpy as np
+import pytest
+
+from spindle_amd import model as M
+from oracle.model import OracleModel
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+KQ = dict(t_embd=M.Q4K, t_q=M.Q4K, t_k=M.Q4K, t_v=M.Q6K, t_o=M.Q4K, t_gate=M.Q4K, t_up=M.Q4K, t_down=M.Q6K, t_out=M.Q6K)
+CASES = {
+    "moe": M.TINY["tiny-qwen3moe"].replace(sigma=0.05),
+    "moe-prune-mass": M.TINY["tiny-qwen3moe"].replace(sigma=0.05, moe_prune=0.3),
+    "dense-kquant": M.TINY["tiny-qwen3"].replace(sigma=0.05, **KQ),
+    "a3b": M.TINY["tiny-a3b"].replace(sigma=0.05),
+    "a3b-prune4": M.TINY["tiny-a3b"].replace(sigma=0.05, moe_prune=4.0),
+}
+# pass sizes: a full chunk and ragged ones (a last vector group of 1, 8 and 2 rows), 252 positions
+SIZES = (128, 17, 40, 1, 50, 16)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from spindle_amd import ops
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    c = ops.Context(0)
+    yield c
+    c.close()
+
+
+def _same(a, b):
+    return np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+def _split16(n):
+    """Pass sizes of at most 16 rows for n rows, none below 4 unless n is: passes of 1 row run
+    on the one-row pipeline and passes of 2-3 rows take the per-lane down kernel, whose fp32
+    sums round differently from the matrix cores'."""
+    sizes = [16] * (n // 16) + ([n % 16] if n % 16 else [])
+    if len(sizes) > 1 and sizes[-1] < 4:
+        sizes[-2] -= 4 - sizes[-1]
+        sizes[-1] = 4
+    return sizes
+
+
+def _in16(eng, ids, pos):
+    """The same rows in passes of at most 16 rows: (argmax, hidden, logits) concatenated."""
+    outs, s = [], 0
+    for n in _split16(len(ids)):
+        outs.append(eng.forward(ids[s:s + n], pos + s, hidden=True, logits=True))
+        s += n
+    return tuple(np.concatenate([o[i] for o in outs]) for i in range(3))
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_prefill_pass_equals_16_row_passes(ctx, case):
+    cfg = CASES[case]
+    w = M.synth_model(cfg, seed=41)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    assert a.decode_pipeline()
+    ids = np.random.default_rng(9).integers(0, cfg.vocab, sum(SIZES))
+    pos = 0
+    for m in SIZES:
+        print(f"{case}: pass of {m} rows at {pos}", flush=True)
+        am0, h0, l0 = a.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        am1, h1, l1 = _in16(b, ids[pos:pos + m], pos)
+        assert _same(h0, h1), (case, m, pos, "hidden")
+        assert _same(l0, l1), (case, m, pos, "logits")
+        assert np.array_equal(am0, am1), (case, m, pos)
+        pos += m
+    ka, va = a.kv_cache()
+    kb, vb = b.kv_cache()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    if cfg.moe:  # the last pass's experts with users per layer (distinct experts, not jobs)
+        assert all(0 < n <= cfg.n_expert for n in a.last_experts())
+    a.close()
+    b.close()
+
+
+@pytest.mark.parametrize("case", ["a3b", "moe"])
+def test_prefill_long_context(ctx, case):
+    """128-row passes past 1024 positions (17+ attention chunks, two merge levels; 128 rows x 8
+    query heads = 64 query tiles a kv head) against 16-row passes, bitwise."""
+    cfg = CASES[case].replace(max_seq=1280)
+    w = M.synth_model(cfg, seed=42)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    ids = np.random.default_rng(10).integers(0, cfg.vocab, 1240)
+    for s0 in range(0, 1240, 128):
+        n = min(128, 1240 - s0)
+        print(f"{case}: pass of {n} rows at {s0}", flush=True)
+        am0, h0, l0 = a.forward(ids[s0:s0 + n], s0, hidden=True, logits=True)
+        am1, h1, l1 = _in16(b, ids[s0:s0 + n], s0)
+        assert _same(h0, h1) and _same(l0, l1) and np.array_equal(am0, am1), (case, s0)
+    ka, va = a.kv_cache()
+    kb, vb = b.kv_cache()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    a.close()
+    b.close()
+
+
+def _norm_err(x, y):
+    return float(np.max(np.abs(x.astype(np.float64) - y.astype(np.float64))) / max(1.0, float(np.max(np.abs(y)))))
+
+
+@pytest.mark.parametrize("case", ["moe", "dense-kquant", "a3b"])
+def test_prefill_matches_oracle(ctx, case):
+    """A 128-row pass against the oracle, row by row on the pass's own context: after the GPU
+    pass the oracle gets the GPU's KV cache and computes row p alone at position p (positions
+    below p from the GPU's cache), so a Q8_K rounding flip in one row does not carry into the
+    rows after it through attention. Bars of the integer-path tests: logits median <= 1e-5;
+    rows above 1e-3 are such flips, at most 15% of rows and 5e-2 each."""
+    cfg = CASES[case]
+    w = M.synth_model(cfg, seed=43)
+    eng = M.Engine(ctx, cfg, w)
+    om = OracleModel(cfg, w)
+    ids = np.random.default_rng(11).integers(0, cfg.vocab, 128)
+    _, _, lg = eng.forward(ids, 0, logits=True)
+    k, v = eng.kv_cache()
+    errs = []
+    for p in range(128):
+        om.k_cache[:] = k
+        om.v_cache[:] = v
+        lo = om.logits(om.forward(ids[p:p + 1], p))[0]
+        errs.append(_norm_err(lg[p], lo))
+    errs = np.array(errs)
+    print(f"{case}: logits err median {np.median(errs):.1e} max {errs.max():.1e}, rows above 1e-3: {(errs > 1e-3).sum()}")
+    assert np.median(errs) <= 1e-5
+    assert errs.max() <= 5e-2
+    assert (errs > 1e-3).sum() <= 0.15 * len(errs)
+    eng.close()
+
+
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-granite"])
+def test_prefill_without_prefill_kernels(ctx, name):
+    """Models outside the K-quant pipeline (and K-quant models with the matrix cores off) run a
+    pass of more than 16 rows as passes of at most 16: the same bits."""
+    cfg = M.TINY[name].replace(sigma=0.05)
+    w = M.synth_model(cfg, seed=44)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    ids = np.random.default_rng(12).integers(0, cfg.vocab, 60)
+    am0, h0, l0 = a.forward(ids, 0, hidden=True, logits=True)
+    am1, h1, l1 = _in16(b, ids, 0)
+    assert _same(h0, h1) and _same(l0, l1) and np.array_equal(am0, am1)
+    a.close()
+    b.close()
+    cfg = CASES["moe"]
+    w = M.synth_model(cfg, seed=45)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    a.set_mfma(False)
+    b.set_mfma(False)
+    am0, h0, l0 = a.forward(ids[:40], 0, hidden=True, logits=True)
+    am1, h1, l1 = _in16(b, ids[:40], 0)
+    assert _same(h0, h1) and _same(l0, l1) and np.array_equal(am0, am1)
+    a.close()
+    b.close()
+
+
+@pytest.mark.parametrize("case", ["moe", "a3b"])
+def test_generate_with_128_row_prompt_chunks(ctx, case):
+    """generate with feed's 128-row prompt chunks gives the stream and counts of 16-row chunks
+    (the prompt's KV cache is the same bits), and the default chunk is 128."""
+    cfg = CASES[case]
+    w = M.synth_model(cfg, seed=46)
+    rng = np.random.default_rng(13)
+    head = rng.integers(0, cfg.vocab, 150)
+    prompt = np.concatenate([head, head[40:110]]).astype(np.int32)
+    eng = M.Engine(ctx, cfg, w)
+    t16, s16 = eng.generate(prompt, 24, draft_len=8, min_ngram=2, max_ngram=4, fixed=True, prefill_chunk=16)
+    t128, s128 = eng.generate(prompt, 24, draft_len=8, min_ngram=2, max_ngram=4, fixed=True, prefill_chunk=128)
+    t0, s0 = eng.generate(prompt, 24, draft_len=8, min_ngram=2, max_ngram=4, fixed=True, prefill_chunk=0)
+    assert np.array_equal(t16, t128) and np.array_equal(t16, t0)
+    for k in ("accepted", "drafted", "verifies", "steps"):
+        assert s16[k] == s128[k] == s0[k], k
+    eng.close()

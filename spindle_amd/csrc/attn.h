@@ -193,6 +193,28 @@ __device__ __forceinline__ void attn_kv_first(const AttnArgs &a, int total, int 
   attn_kv_load<NU>(a, cache0 + (int64_t)min(p_lo + lp, MERGE ? p_hi - 1 : a.max_seq - 1) * a.kv_dim + lq * DQ, kr, vr);
 }
 
+// The merged outputs of query tile qa .. qa + 15 of kv head h (ol: [16][HD] in LDS, 256 threads)
+// to the att rows, and their Q8_K when a.aq is set.
+template <int HD>
+__device__ __forceinline__ void attn_tile_out(const AttnArgs &a, int h, int qa, int NQ, const float *ol) {
+  const int tid = threadIdx.x & 255, wave = tid >> 6, lane = tid & 63, g = a.n_heads / a.n_kv;
+  const int nrow = min(16, NQ - qa);
+  for (int i = tid; i < nrow * HD; i += 256) {
+    const int qi = qa + i / HD, d = i % HD, b = qi / g, head = h * g + qi % g;
+    a.att[(int64_t)b * a.n_heads * HD + head * HD + d] = ol[i];
+  }
+  if (a.aq.q) {  // 256-value blocks of att rows: (256 / HD) consecutive queries of the tile
+    const int qpb = 256 / HD, nbr = a.n_heads * HD / 256;
+    for (int j = wave; j < nrow / qpb; j += 4) {
+      const int q0 = qa + j * qpb, b = q0 / g, head = h * g + q0 % g;
+      const float4 xv = reinterpret_cast<const float4 *>(ol + j * 256)[lane];
+      const float am = q8k_amax(xv);
+      const int64_t vb = (int64_t)b * nbr + head * HD / 256;
+      q8k_block_store(xv, am, a.aq.q + vb * 64, a.aq.d + vb, reinterpret_cast<int *>(a.aq.bs + vb * 8));
+    }
+  }
+}
+
 // Raw inputs of a multi-row item's head_prep rows (wavefront w: query rows w + 4j of the tile,
 // new pass rows b = w + 4j when their position falls in the item's chunk), loaded before the
 // chunk's K/V rows: memory returns in issue order, so a row loaded after the K/V would wait
@@ -584,21 +606,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
     attn_merge16<HD>(r_ml, r_o, a.nch, ngrp, qa, NQ, ol, nullptr, nullptr, 0);
   }
   __syncthreads();
-  const int nrow = min(16, NQ - qa);
-  for (int i = tid; i < nrow * HD; i += 256) {
-    const int qi = qa + i / HD, d = i % HD, b = qi / g, head = h * g + qi % g;
-    a.att[(int64_t)b * a.n_heads * HD + head * HD + d] = ol[i];
-  }
-  if (a.aq.q) {  // 256-value blocks of att rows: (256 / HD) consecutive queries of the tile
-    const int qpb = 256 / HD, nbr = a.n_heads * HD / 256;
-    for (int j = wave; j < nrow / qpb; j += 4) {
-      const int q0 = qa + j * qpb, b = q0 / g, head = h * g + q0 % g;
-      const float4 xv = reinterpret_cast<const float4 *>(ol + j * 256)[lane];
-      const float am = q8k_amax(xv);
-      const int64_t vb = (int64_t)b * nbr + head * HD / 256;
-      q8k_block_store(xv, am, a.aq.q + vb * 64, a.aq.d + vb, reinterpret_cast<int *>(a.aq.bs + vb * 8));
-    }
-  }
+  attn_tile_out<HD>(a, h, qa, NQ, ol);
 }
 
 }  // namespace spx

@@ -71,6 +71,7 @@ struct spx_engine {
                            // and the per-lane dot kernel is faster
   bool mq_gateup = true;   // the gate/up projections (SPX_MQ_GATEUP)
   int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;
+  bool pf_attn = true;      // prefill passes: attention on k_attn_pf + its merge launch (SPX_PF_ATTN)
   bool att_merge = false;  // one-row passes: attention chunks merged inside the attention launch (SPX_ATT_MERGE)  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
@@ -579,8 +580,10 @@ int enqueue_pass_m(spx_engine *E, int m) {
         SPX_HIP(launch_rows_prep(aa, E->qp, m, E->st_dev, s));
         aa.q = E->qp;
         aa.prepped = 1;
+        SPX_HIP(E->pf_attn ? launch_attention_pf(aa, m, E->st_dev, s) : launch_attention(aa, m, E->st_dev, s));
+      } else {
+        SPX_HIP(launch_attention(aa, m, E->st_dev, s));
       }
-      SPX_HIP(launch_attention(aa, m, E->st_dev, s));
     }
     if (!att_q_fused) { ProfScope ps(E, PC_QUANT, 0); SPX_HIP(launch_q8kp_quantize(E->att, E->q_dim, E->q_dim, m, E->aq, s)); }
     {
@@ -772,6 +775,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   if (const char *v = std::getenv("SPX_TAIL_MAX")) E->tail_max = std::max(0, std::min(MAX_M, atoi(v)));
   if (const char *v = std::getenv("SPX_DOWN_MODE")) E->down_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_ATT_MERGE")) E->att_merge = atoi(v) != 0;
+  if (const char *v = std::getenv("SPX_PF_ATTN")) E->pf_attn = atoi(v) != 0;
   *out = E;
   return 0;
 }

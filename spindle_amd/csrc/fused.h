@@ -150,6 +150,9 @@ hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStre
 // q and k, as the attention kernel does it): prepared queries to qp [m][q_dim], K / V rows to
 // the cache (f16 RNE); then launch_attention with a.prepped = 1 reads them from there
 hipError_t launch_rows_prep(const AttnArgs &a, float *qp, int m, const StepRec *st, hipStream_t s);
+// The same attention for prepared rows as partials (a workgroup per chunk, kv head and four
+// query tiles, a wavefront per tile) and a merge launch: each output has launch_attention's bits
+hipError_t launch_attention_pf(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);
 hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStream_t s);
 hipError_t launch_gateup(const GUArgs &a, int mt, int mode, const StepRec *st, int max_jobs, hipStream_t s);
 hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, hipStream_t s);

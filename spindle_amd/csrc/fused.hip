@@ -823,6 +823,175 @@ __global__ __launch_bounds__(256) void k_attn(const AttnArgs a, const StepRec *s
   attn_item<HD, MERGE, false>(a, m, start, c, h, qt, smem, kr, vr, &pre);
 }
 
+// Attention partials of a prefill pass (rows prepared by k_rows_prep, so every K / V row is in
+// the cache): one workgroup per (64-position chunk, kv head, four 16-query tiles). The chunk's
+// K / V go to LDS once; then wavefront w takes tile 4 blockIdx.z + w on its own (its LDS
+// regions private, no workgroup barrier): the query operand straight from the prepared rows
+// (hi + lo f16 in registers), S = Q K^T for the four 16-position blocks, the online softmax of
+// each query row over the chunk (lane = position, the chunk's only sub-chunk), O = P V for
+// every 16-dim tile. Per element the operations and their order are attn_item's, so each
+// (chunk, query) partial has its bits; k_attn_pf_merge merges them as attn_item's mergers do.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_pf(const AttnArgs a, const StepRec *st) {
+  using LY = AttnLds<HD>;
+  constexpr int KS = LY::KS, VS = LY::VS, PS = LY::PS, SS = LY::SS;
+  constexpr int DT = HD / 16, DQ = HD / 4, NU = DQ / 8;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int h = blockIdx.y, c = blockIdx.x;
+  const int m = st->m, start = st->start, total = start + m;
+  const int g = a.n_heads / a.n_kv, NQ = m * g;
+  if (blockIdx.z * 64 >= NQ || c >= (total + 63) / 64) return;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lp = tid >> 2, lq = tid & 3;
+  const int ar = lane & 15, kg = (lane >> 4) * 4;
+  const int qt = blockIdx.z * 4 + wave, qa = qt * 16;
+  const bool act = qa < NQ;
+  const int p_lo = c * 64, p_hi = min(p_lo + 64, total);
+  _Float16 *ks = reinterpret_cast<_Float16 *>(smem);  // [64][KS]
+  _Float16 *vt = ks + 64 * KS;                         // [HD][VS]
+  uint8_t *wp = reinterpret_cast<uint8_t *>(vt + HD * VS) + (size_t)wave * (16 * SS * 4 + 2 * 16 * PS * 2 + 16 * 4);
+  float *ss = reinterpret_cast<float *>(wp);             // [16][SS]
+  _Float16 *ph = reinterpret_cast<_Float16 *>(ss + 16 * SS), *pl = ph + 16 * PS;  // [16][PS]
+  float *sa = reinterpret_cast<float *>(pl + 16 * PS);  // [16]
+  uint32_t kr[HD / 8], vr[HD / 8];
+  attn_kv_first<HD, true>(a, total, c, h, kr, vr);
+  // the query operand: row ar of the tile, dims 16 kt + kg .. + 3, as hi + lo f16
+  h4v qhi[DT], qlo[DT];
+  {
+    const int qi = qa + ar;
+    const float *src = qi < NQ ? a.q + (int64_t)(qi / g) * a.n_heads * HD + (h * g + qi % g) * HD : nullptr;
+    float4 x[DT];
+#pragma unroll
+    for (int kt = 0; kt < DT; kt++) x[kt] = src ? *reinterpret_cast<const float4 *>(src + kt * 16 + kg) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int kt = 0; kt < DT; kt++) {
+      _Float16 hh, ll;
+      split_f16(x[kt].x, hh, ll); qhi[kt][0] = hh; qlo[kt][0] = ll;
+      split_f16(x[kt].y, hh, ll); qhi[kt][1] = hh; qlo[kt][1] = ll;
+      split_f16(x[kt].z, hh, ll); qhi[kt][2] = hh; qlo[kt][2] = ll;
+      split_f16(x[kt].w, hh, ll); qhi[kt][3] = hh; qlo[kt][3] = ll;
+    }
+  }
+  // cached rows -> LDS (K row-major, V transposed); rows past the pass are zero
+  if (p_lo + lp >= total) {
+#pragma unroll
+    for (int t = 0; t < 4 * NU; t++) { kr[t] = 0u; vr[t] = 0u; }
+  }
+  {
+    uint16_t *vt16 = reinterpret_cast<uint16_t *>(vt);
+#pragma unroll
+    for (int u = 0; u < NU; u++) reinterpret_cast<uint4 *>(ks + lp * KS + lq * DQ)[u] = make_uint4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
+#pragma unroll
+    for (int t = 0; t < 4 * NU; t++) {
+      vt16[(lq * DQ + 2 * t) * VS + lp] = (uint16_t)(vr[t] & 0xffffu);
+      vt16[(lq * DQ + 2 * t + 1) * VS + lp] = (uint16_t)(vr[t] >> 16);
+    }
+  }
+  __syncthreads();
+  if (!act) return;
+  // scores S = Q K^T, position blocks pb = 0..3
+#pragma unroll
+  for (int pb = 0; pb < 4; pb++) {
+    f4v sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kt = 0; kt < DT; kt++) {
+      const h4v bk = *reinterpret_cast<const h4v *>(ks + (pb * 16 + ar) * KS + kt * 16 + kg);
+      sacc = mfma16(qhi[kt], bk, sacc);
+      sacc = mfma16(qlo[kt], bk, sacc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) ss[(kg + r) * SS + pb * 16 + ar] = sacc[r];
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the scores are in LDS
+  __builtin_amdgcn_wave_barrier();
+  // online softmax of rows r4 * 4 .. r4 * 4 + 3 (lane = position) from the running state
+  // (max -inf, sum 0) of a chunk's first sub-chunk
+  float rm = -INFINITY, rl = 0.0f;  // lane r: row r's results
+#pragma unroll
+  for (int r0 = 0; r0 < 16; r0 += 4) {
+    float sv[4], mx[4], pv[4], ls[4], mn[4], al[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = r0 + i, qi = qa + row, pos = p_lo + lane;
+      sv[i] = qi < NQ && pos < p_hi && pos <= start + qi / g ? ss[row * SS + lane] * a.scale : -INFINITY;
+      mx[i] = sv[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) mx[i] = wave_max(mx[i]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float m_old = -INFINITY;
+      mn[i] = fmaxf(m_old, mx[i]);
+      pv[i] = (sv[i] == -INFINITY || mn[i] == -INFINITY) ? 0.0f : expf(sv[i] - mn[i]);
+      al[i] = mn[i] == -INFINITY ? 1.0f : (m_old == -INFINITY ? 0.0f : expf(m_old - mn[i]));
+      ls[i] = pv[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) ls[i] = wave_sum(ls[i]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = r0 + i;
+      split_f16(pv[i], ph[row * PS + lane], pl[row * PS + lane]);
+      if (lane == row) { rm = mn[i]; rl = 0.0f * al[i] + ls[i]; }
+      if (lane == 0) sa[row] = al[i];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // probabilities and rescales in LDS
+  __builtin_amdgcn_wave_barrier();
+  const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nslot) * ATT_QMAX * 2);
+  const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nslot) * ATT_QMAX * HD);
+  float sar[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) sar[r] = sa[kg + r];
+  // O = O * alpha + P V for every 16-dim tile (O starts at zero), then to the partial slot
+#pragma unroll
+  for (int j = 0; j < DT; j++) {
+    f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[r] *= sar[r];
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+      const h4v bv = *reinterpret_cast<const h4v *>(vt + (j * 16 + ar) * VS + kt * 16 + kg);
+      const h4v ahi = *reinterpret_cast<const h4v *>(ph + ar * PS + kt * 16 + kg);
+      const h4v alo = *reinterpret_cast<const h4v *>(pl + ar * PS + kt * 16 + kg);
+      acc = mfma16(ahi, bv, acc);
+      acc = mfma16(alo, bv, acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int qi = qa + kg + r;
+      if (qi < NQ) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(acc[r]), r_o, ((c * ATT_QMAX + qi) * HD + j * 16 + ar) * 4, 0, 0);
+    }
+  }
+  if (lane < 16 && qa + lane < NQ)
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2v, f2v{rm, rl}), r_ml, (c * ATT_QMAX + qa + lane) * 8, 0, 0);
+}
+
+// The merges of a prefill pass's partials, one workgroup per (kv head, query tile): the chunks
+// of each group of ATT_GRP in chunk order (to slot nch + group when there are several groups),
+// then the groups, as attn_item's last arrivals merge them; then the tile's att rows (+ Q8_K).
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_pf_merge(const AttnArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int h = blockIdx.x, qt = blockIdx.y;
+  const int m = st->m, total = st->start + m, g = a.n_heads / a.n_kv, NQ = m * g, qa = qt * 16;
+  if (qa >= NQ) return;
+  const int nch = (total + 63) / 64, ngrp = (nch + ATT_GRP - 1) / ATT_GRP;
+  const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nslot) * ATT_QMAX * 2);
+  const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nslot) * ATT_QMAX * HD);
+  float *ol = reinterpret_cast<float *>(smem);  // [16][HD]
+  if (ngrp == 1) {
+    attn_merge16<HD>(r_ml, r_o, 0, nch, qa, NQ, ol, nullptr, nullptr, 0);
+  } else {
+    for (int grp = 0; grp < ngrp; grp++)
+      attn_merge16<HD>(r_ml, r_o, grp * ATT_GRP, min(ATT_GRP, nch - grp * ATT_GRP), qa, NQ, nullptr, &r_ml, &r_o, a.nch + grp);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    attn_merge16<HD>(r_ml, r_o, a.nch, ngrp, qa, NQ, ol, nullptr, nullptr, 0);
+  }
+  __syncthreads();
+  attn_tile_out<HD>(a, h, qa, NQ, ol);
+}
+
 // Row preparation of a prefill pass: one wavefront per (row b, head j); heads 0 .. n_heads-1
 // are the queries (head_prep -> qp), then the n_kv keys (head_prep -> f16 RNE -> K cache) and
 // the n_kv values (bias -> f16 -> V cache), the same operations as attn_item makes on them.
@@ -1425,6 +1594,24 @@ hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStre
   if (nqt > ATT_QT || (m > MAX_M && !a.prepped)) return hipErrorInvalidValue;
   if (a.hd == 128) launch_attn_t<128>(a, nqt, st, s);
   else if (a.hd == 64) launch_attn_t<64>(a, nqt, st, s);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+template <int HD>
+static void launch_attn_pf_t(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
+  using LY = AttnLds<HD>;
+  const size_t sm = (size_t)64 * LY::KS * 2 + (size_t)HD * LY::VS * 2 + 4 * ((size_t)16 * LY::SS * 4 + (size_t)2 * 16 * LY::PS * 2 + 16 * 4);
+  const int nq = m * (a.n_heads / a.n_kv);
+  SPX_LDS((k_attn_pf<HD>), sm);
+  hipLaunchKernelGGL((k_attn_pf<HD>), dim3(a.nch, a.n_kv, (nq + 63) / 64), dim3(256), sm, s, a, st);
+  hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, (nq + 15) / 16), dim3(256), (size_t)16 * HD * 4, s, a, st);
+}
+
+hipError_t launch_attention_pf(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
+  if (!a.prepped || m < 1 || m > PMAX || (m * (a.n_heads / a.n_kv) + 15) / 16 > ATT_QT) return hipErrorInvalidValue;
+  if (a.hd == 128) launch_attn_pf_t<128>(a, m, st, s);
+  else if (a.hd == 64) launch_attn_pf_t<64>(a, m, st, s);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }

@@ -1460,72 +1460,101 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_mq(const DecDownMArgs 
 }
 
 // ------------------------------------------------------------------ prefill passes (17..128 rows)
-// Routing of m <= PMAX rows and the job list in global memory, one workgroup of 16 wavefronts:
-// wavefront w routes rows w, w + 16, ... (route_row, the rows' results to chosen / weights /
-// nkeep), then thread e lists expert e's users in row order, sixteen a job (jobs in expert
-// order). njobs[0] = the job count, njobs[2] = the experts with users; expert_count counts
-// each of them once.
-__global__ __launch_bounds__(1024) void kp_route(const DecRouteArgs a) {
-  constexpr int NW = 16;
-  __shared__ signed char slot_of[PMAX * 256];
-  __shared__ int nje[256];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ne = a.n_expert, nu = a.n_used, m = a.m;
-  for (int i = threadIdx.x; i < m * 256; i += NW * 64) slot_of[i] = -1;
-  __syncthreads();
-  for (int b = wave; b < m; b += NW) {
-    float lv[4];
+// Routing of m <= PMAX rows, a wavefront per row (route_row; the rows' results to chosen /
+// weights / nkeep), four rows a workgroup.
+__global__ __launch_bounds__(256) void kp_route_rows(const DecRouteArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ne = a.n_expert, b = blockIdx.x * 4 + wave;
+  if (b >= a.m) return;
+  float lv[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int e = lane + 64 * k;
-      lv[k] = e < ne ? gld<float>(a.logits + (int64_t)b * ne + e) : -INFINITY;
+  for (int k = 0; k < 4; k++) {
+    const int e = lane + 64 * k;
+    lv[k] = e < ne ? gld<float>(a.logits + (int64_t)b * ne + e) : -INFINITY;
+  }
+  int my_e, keep;
+  float my_p, wsum;
+  route_row(lv, ne, a.n_used, a.moe_prune, my_e, my_p, keep, wsum);
+  if (lane < keep) {
+    gst<int>(a.chosen + b * 32 + lane, my_e);
+    gst<float>(a.weights + b * 32 + lane, a.norm ? my_p / wsum : my_p);
+  }
+  if (lane == 0) gst<int>(a.nkeep + b, keep);
+}
+
+// The job list of the routed rows in global memory: expert e's users in row order, sixteen a
+// job, jobs in expert order (user (b, slot): vec = b, out = b * n_used + slot). A bit mask of
+// the rows per expert gives each user its rank, so every user is placed by its own thread.
+// njobs[0] = the job count, njobs[2] = the experts with users; expert_count counts each once.
+__global__ __launch_bounds__(256) void kp_jobs(const DecRouteArgs a) {
+  __shared__ unsigned long long mask[256][PMAX / 64];
+  __shared__ int jbase[257];
+  __shared__ int sch[PMAX * 32], snk[PMAX];  // the rows' choices (-1: none)
+  const int tid = threadIdx.x, m = a.m, nu = a.n_used;
+  for (int i = tid; i < 256 * (PMAX / 64); i += 256) (&mask[0][0])[i] = 0ull;
+  if (tid < m) snk[tid] = gld<int>(a.nkeep + tid);
+  {
+    constexpr int NL = PMAX * 32 / 256;  // every load in flight at once
+    int v[NL];
+#pragma unroll
+    for (int k = 0; k < NL; k++) v[k] = tid + 256 * k < m * 32 ? gld<int>(a.chosen + tid + 256 * k) : 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < NL; k++) {
+      const int i = tid + 256 * k;
+      if (i < m * 32) sch[i] = (i & 31) < snk[i >> 5] ? v[k] : -1;
     }
-    int my_e, keep;
-    float my_p, wsum;
-    route_row(lv, ne, nu, a.moe_prune, my_e, my_p, keep, wsum);
-    if (lane < keep) {
-      slot_of[b * 256 + my_e] = (signed char)lane;
-      gst<int>(a.chosen + b * 32 + lane, my_e);
-      gst<float>(a.weights + b * 32 + lane, a.norm ? my_p / wsum : my_p);
-    }
-    if (lane == 0) gst<int>(a.nkeep + b, keep);
   }
   __syncthreads();
-  const int e = threadIdx.x;
+  for (int i = tid; i < m * 32; i += 256)
+    if (sch[i] >= 0) atomicOr(&mask[sch[i]][i >> 11], 1ull << ((i >> 5) & 63));  // row i >> 5
+  __syncthreads();
   int cnt = 0;
-  if (e < ne)
-    for (int b = 0; b < m; b++) cnt += slot_of[b * 256 + e] >= 0;
-  if (e < 256) nje[e] = (cnt + MAX_M - 1) / MAX_M;
-  __syncthreads();
-  if (e < ne && cnt > 0) {
-    int j = 0;
-    for (int i = 0; i < e; i++) j += nje[i];
-    int *J = nullptr;
-    int k = 0;
-    for (int b = 0; b < m; b++) {
-      const int sl = slot_of[b * 256 + e];
-      if (sl < 0) continue;
-      if (k == 0) J = reinterpret_cast<int *>(a.jobs + j);
-      gst<int>(J + 2 + k, b);
-      gst<int>(J + 2 + MAX_M + k, b * nu + sl);
-      if (++k == MAX_M) {
-        gst<int>(J, e);
-        gst<int>(J + 1, k);
-        j++;
-        k = 0;
-      }
-    }
-    if (k > 0) {
-      for (int q = k; q < MAX_M; q++) { gst<int>(J + 2 + q, 0); gst<int>(J + 2 + MAX_M + q, 0); }
-      gst<int>(J, e);
-      gst<int>(J + 1, k);
-    }
-    if (a.expert_count) atomicAdd(a.expert_count + e, 1);
+#pragma unroll
+  for (int w = 0; w < PMAX / 64; w++) cnt += __popcll(mask[tid][w]);
+  const int nje = (cnt + MAX_M - 1) / MAX_M;
+  // exclusive scan of the experts' job counts (four wavefronts, then their totals)
+  const int wave = tid >> 6, lane = tid & 63;
+  int incl = nje;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += t;
   }
-  if (threadIdx.x == 0) {
-    int nj = 0, nx = 0;
-    for (int i = 0; i < 256; i++) { nj += nje[i]; nx += nje[i] > 0; }
-    gst<int>(a.njobs, nj);
-    gst<int>(a.njobs + 2, nx);
+  __shared__ int wsum[4], wnx[4];
+  const unsigned long long used = __ballot(cnt > 0);
+  if (lane == 63) wsum[wave] = incl;
+  if (lane == 0) wnx[wave] = __popcll(used);
+  __syncthreads();
+  int off = 0;
+  for (int w = 0; w < wave; w++) off += wsum[w];
+  jbase[tid] = off + incl - nje;
+  if (tid == 255) {
+    gst<int>(a.njobs, off + incl);
+    gst<int>(a.njobs + 2, wnx[0] + wnx[1] + wnx[2] + wnx[3]);
+  }
+  __syncthreads();
+  for (int i = tid; i < m * 32; i += 256) {  // each user at its rank
+    const int b = i >> 5, sl = i & 31, e = sch[i];
+    if (e < 0) continue;
+    int rank = 0;
+#pragma unroll
+    for (int w = 0; w < PMAX / 64; w++) {
+      const unsigned long long mw = mask[e][w];
+      rank += w < (b >> 6) ? __popcll(mw) : w == (b >> 6) ? __popcll(mw & ((1ull << (b & 63)) - 1ull)) : 0;
+    }
+    int *J = reinterpret_cast<int *>(a.jobs + jbase[e] + rank / MAX_M);
+    gst<int>(J + 2 + rank % MAX_M, b);
+    gst<int>(J + 2 + MAX_M + rank % MAX_M, b * nu + sl);
+  }
+  if (tid < a.n_expert && cnt > 0) {  // each job's expert, user count and unused entries
+    for (int j = 0; j < nje; j++) {
+      int *J = reinterpret_cast<int *>(a.jobs + jbase[tid] + j);
+      const int k = min(MAX_M, cnt - j * MAX_M);
+      gst<int>(J, tid);
+      gst<int>(J + 1, k);
+      for (int q = k; q < MAX_M; q++) { gst<int>(J + 2 + q, 0); gst<int>(J + 2 + MAX_M + q, 0); }
+    }
+    if (a.expert_count) atomicAdd(a.expert_count + tid, 1);
   }
 }
 
@@ -1822,7 +1851,8 @@ hipError_t launch_kp_route(const DecRouteArgs &a, hipStream_t s) {
   if (a.m < 1 || a.m > PMAX || a.n_expert < 1 || a.n_expert > 256 || a.n_used < 1 || a.n_used > 32 || a.n_used > a.n_expert || !a.jobs ||
       !a.njobs)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kp_route, dim3(1), dim3(1024), 0, s, a);
+  hipLaunchKernelGGL(kp_route_rows, dim3((a.m + 3) / 4), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(kp_jobs, dim3(1), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

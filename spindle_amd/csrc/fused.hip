@@ -966,26 +966,28 @@ __global__ __launch_bounds__(256) void k_attn_pf(const AttnArgs a, const StepRec
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2v, f2v{rm, rl}), r_ml, (c * ATT_QMAX + qa + lane) * 8, 0, 0);
 }
 
-// The merges of a prefill pass's partials, one workgroup per (kv head, query tile): the chunks
-// of each group of ATT_GRP in chunk order (to slot nch + group when there are several groups),
-// then the groups, as attn_item's last arrivals merge them; then the tile's att rows (+ Q8_K).
+// The merges of a prefill pass's partials, one workgroup per (kv head, query tile, chunk group):
+// the group's chunks in chunk order (with one group: straight to the tile's att rows + Q8_K;
+// else to slot nch + group), then the last of the tile's group mergers merges the groups in
+// group order: attn_item's merges, operation for operation.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_pf_merge(const AttnArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];
-  const int h = blockIdx.x, qt = blockIdx.y;
+  const int h = blockIdx.x, qt = blockIdx.y, grp = blockIdx.z;
   const int m = st->m, total = st->start + m, g = a.n_heads / a.n_kv, NQ = m * g, qa = qt * 16;
-  if (qa >= NQ) return;
   const int nch = (total + 63) / 64, ngrp = (nch + ATT_GRP - 1) / ATT_GRP;
+  if (qa >= NQ || grp >= ngrp) return;
+  const int gcnt = min(ATT_GRP, nch - grp * ATT_GRP);
   const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nslot) * ATT_QMAX * 2);
   const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nslot) * ATT_QMAX * HD);
   float *ol = reinterpret_cast<float *>(smem);  // [16][HD]
   if (ngrp == 1) {
-    attn_merge16<HD>(r_ml, r_o, 0, nch, qa, NQ, ol, nullptr, nullptr, 0);
+    attn_merge16<HD>(r_ml, r_o, 0, gcnt, qa, NQ, ol, nullptr, nullptr, 0);
   } else {
-    for (int grp = 0; grp < ngrp; grp++)
-      attn_merge16<HD>(r_ml, r_o, grp * ATT_GRP, min(ATT_GRP, nch - grp * ATT_GRP), qa, NQ, nullptr, &r_ml, &r_o, a.nch + grp);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    attn_merge16<HD>(r_ml, r_o, grp * ATT_GRP, gcnt, qa, NQ, nullptr, &r_ml, &r_o, a.nch + grp);
+    int *cnt = a.counter + ((int64_t)h * ATT_QT + qt) * (1 + ATT_GMAX) * CNT_STRIDE;
+    if (arrive(cnt) != ngrp - 1) return;
+    if (threadIdx.x == 0) *cnt = 0;
     attn_merge16<HD>(r_ml, r_o, a.nch, ngrp, qa, NQ, ol, nullptr, nullptr, 0);
   }
   __syncthreads();
@@ -1605,7 +1607,7 @@ static void launch_attn_pf_t(const AttnArgs &a, int m, const StepRec *st, hipStr
   const int nq = m * (a.n_heads / a.n_kv);
   SPX_LDS((k_attn_pf<HD>), sm);
   hipLaunchKernelGGL((k_attn_pf<HD>), dim3(a.nch, a.n_kv, (nq + 63) / 64), dim3(256), sm, s, a, st);
-  hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, (nq + 15) / 16), dim3(256), (size_t)16 * HD * 4, s, a, st);
+  hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, (nq + 15) / 16, (a.nch + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
 }
 
 hipError_t launch_attention_pf(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {

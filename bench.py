@@ -192,6 +192,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-legs", action="store_true", help="skip the prune / diverse-routing / configs 1-4 legs")
     ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="build the model, prefill the prompt in 128-row passes, report prompt tok/s and exit (no JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the whole model fits in one MI355X's HBM and this build "
@@ -219,6 +221,8 @@ def main():
     tok, prefill_s = prefill(eng, prompt, verbose=True)
     pos = len(prompt)
     log(f"prefill {len(prompt)} tokens in {prefill_s:.2f}s ({len(prompt) / prefill_s:.0f} tok/s, {PREFILL_CHUNK}-row passes)")
+    if args.prefill_only:
+        return
 
     # CPU baseline from the KV state the GPU's timed decode starts from (read-only on the GPU)
     cpu = None

@@ -155,11 +155,14 @@ int spx_engine_set_mfma(spx_engine *e, int on);
 int spx_engine_set_persist(spx_engine *e, int on);
 int spx_engine_persist_active(spx_engine *e, int *active);
 
-/* One pass of m <= 16 tokens at positions start_pos.. (forward_slice :3364-3552 for m == 1,
- * forward_batch_slice :3142-3362 for m > 1, then compute_logits_batch :3588-3602 and the
- * greedy pick of sample_from_logits :3624-3671). K/V of every row are written before any
- * row attends, row b sees positions <= start_pos + b. Optional host outputs: hidden [m][dim]
- * (after output_norm), logits [m][vocab], argmax [m]. Synchronous. */
+/* One pass of m <= 128 tokens at positions start_pos.. (forward_slice :3364-3552 for m == 1,
+ * forward_batch_slice :3142-3362 for m > 1 — verify passes of k+1 rows and feed's prompt
+ * chunks of up to 128 rows :3090-3101 — then compute_logits_batch :3588-3602 and the greedy
+ * pick of sample_from_logits :3624-3671). K/V of every row are written before any row
+ * attends, row b sees positions <= start_pos + b. A pass of more than 16 rows runs on the
+ * prefill kernels (K-quant models, matrix cores on), else as consecutive passes of at most
+ * 16 rows; either way each row gets the bits it would get in a pass of 16. Optional host
+ * outputs: hidden [m][dim] (after output_norm), logits [m][vocab], argmax [m]. Synchronous. */
 int spx_engine_forward(spx_engine *e, const int32_t *ids, int m, int start_pos, float *hidden,
                        float *logits, int32_t *argmax);
 /* Greedy decoding of n tokens, one pass each (step_token :3106-3132 + the greedy pick):
@@ -279,7 +282,7 @@ typedef struct {
   int fixed;         /* SPINDLE_SPEC_FIXED: always verify the whole draft (:1703) */
   int speculate;     /* 0: plain one-token decoding */
   int adaptive_k;    /* grow k after a fully accepted draft (:4343) */
-  int prefill_chunk; /* prompt rows per pass, <= 16 */
+  int prefill_chunk; /* prompt rows per pass, <= 128; 0: 128 (feed's chunks :3090) */
   int n_cached;      /* prompt tokens already in the KV cache at positions 0..n_cached-1 (a
                         session's earlier turns, generate_reply's cur_pos): only the rest of the
                         prompt is fed; 0 <= n_cached < n_prompt */

@@ -236,6 +236,7 @@ int mv_run(spx_engine *E, MVArgs &a, int m, int mode, int grid_cap = 0) {
   if (grid_cap > 0 && grid > grid_cap) grid = grid_cap;
   a.m = m;
   a.nbest = grid;
+  a.fq = E->mq ? 1 : 0;
   SPX_HIP(launch_mv(a, m, mode, E->st_dev, grid, E->ctx->stream));
   return 0;
 }

@@ -69,7 +69,11 @@ struct MVArgs {
   int nbest;
   float lscale;
   NormTail tail;
+  // float path, passes of FQ_MIN_ROWS..16 rows: Q8_0 segments on the fp32 matrix cores
+  // (k_mv_fq) instead of the per-lane walk (the same products, summed in another order)
+  int fq;
 };
+constexpr int FQ_MIN_ROWS = 4;  // below, a 16-vector tile idles most of its columns (measured slower)
 
 struct AttnArgs {
   const float *q, *k, *v;             // raw projections [m][q_dim], [m][kv_dim]

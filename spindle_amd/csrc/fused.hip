@@ -687,6 +687,94 @@ __global__ __launch_bounds__(256) void k_mv_f(const MVArgs a, const StepRec *st)
   if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
 }
 
+// Float matvec of 4..16 vectors on the fp32 matrix cores (Q8_0 weights): four wavefronts per
+// workgroup on one task of 32 rows (tasks stride over the grid as k_mv_f's): wavefront w takes
+// the 16-row tile w & 1 and the batches of eight blocks with index = w >> 1 mod 2. Per
+// 32-column block eight v_mfma_f32_16x16x4f32: lane (j, kq) = (lane & 15, lane >> 4) gives
+// A[vector j][k = kq] = x[j][32b + 8kq + s] and B[k = kq][row j] = code[32b + 8kq + s] * d
+// (an int8 times an f16 scale: exact in fp32) at step s; D holds row lane & 15 of vectors
+// 4 (lane >> 4) .. + 3. Every product is the per-lane walk's; the sums run in a fixed order of
+// their own (four chains, block b in chain b mod 4, (0 + 1) + (2 + 3), then the first half's
+// batches + the second's): a row's result does not depend on the pass's other rows.
+__global__ __launch_bounds__(256) void k_mv_fq(const MVArgs a, const StepRec *st) {
+  const int m = st ? st->m : a.m;
+  const bool coh = a.tail.nw != nullptr;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15, kq = lane >> 4;
+  const int tile = wave & 1, kh = wave >> 1;
+  __shared__ unsigned long long sbest[16];
+  __shared__ float part[2][4][64];
+  if (threadIdx.x < 16) sbest[threadIdx.x] = 0;
+  __syncthreads();
+  const int total = a.seg[0].wgs + (a.nseg > 1 ? a.seg[1].wgs : 0) + (a.nseg > 2 ? a.seg[2].wgs : 0);
+  const bool vin = j < m;
+  for (int t = blockIdx.x; t < total; t += gridDim.x) {
+    int wg;
+    const Seg &sg = a.seg[seg_index(a, t, wg)];
+    const int64_t r0 = sg.r0 + ((int64_t)wg * 2 + tile) * 16;
+    float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (r0 < sg.r1) {
+      const int64_t grow = (int64_t)sg.expert * sg.w.rows + min(r0 + j, sg.r1 - 1);
+      const int nb = (int)sg.w.nb;
+      const uint8_t *cp = sg.w.pl.p0 + grow * nb * 32 + 8 * kq;
+      const uint16_t *dp = reinterpret_cast<const uint16_t *>(sg.w.pl.p3) + grow * nb;
+      const float *xr = a.x + (int64_t)(vin ? j : 0) * a.ld_x + 8 * kq;
+      f4v acc[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) acc[u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int b0 = 8 * kh; b0 < nb; b0 += 16) {
+        uint2 c[8];
+        uint32_t dh[8];
+        float4 x0[8], x1[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          const int b = min(b0 + u, nb - 1);
+          c[u] = *reinterpret_cast<const uint2 *>(cp + (int64_t)b * 32);
+          dh[u] = dp[b];
+          x0[u] = *reinterpret_cast<const float4 *>(xr + (int64_t)b * 32);
+          x1[u] = *reinterpret_cast<const float4 *>(xr + (int64_t)b * 32 + 4);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          if (b0 + u < nb) {
+            const float d = h2f(dh[u]);
+            const float xs[8] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w, x1[u].x, x1[u].y, x1[u].z, x1[u].w};
+#pragma unroll
+            for (int s2 = 0; s2 < 8; s2++) {
+              const float w = (float)(int8_t)((s2 < 4 ? c[u].x : c[u].y) >> (8 * (s2 & 3))) * d;
+              acc[u & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vin ? xs[s2] : 0.0f, w, acc[u & 3], 0, 0, 0);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; q++) r[q] = (acc[0][q] + acc[1][q]) + (acc[2][q] + acc[3][q]);
+    }
+    if (kh == 1) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) part[tile][q][lane] = r[q];
+    }
+    __syncthreads();
+    if (kh == 0 && r0 < sg.r1) {
+      const int64_t row = r0 + j;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int v = 4 * kq + q;
+        const float res = r[q] + part[tile][q][lane];
+        if (v < m && row < sg.r1) {
+          out_store(sg.out + (int64_t)v * sg.ld_out + row, res, coh);
+          if (a.best) atomicMax(&sbest[v], pick_key(res, a.lscale, row));
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (a.best) {
+    __syncthreads();
+    if ((int)threadIdx.x < m) a.best[(int64_t)threadIdx.x * a.nbest + blockIdx.x] = sbest[threadIdx.x];
+  }
+  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
+}
+
 // ------------------------------------------------------------------ standalone kernels
 // Standalone norm: one workgroup per row.
 __global__ __launch_bounds__(256) void k_norm(const NormTail t, const StepRec *st) {
@@ -1531,6 +1619,12 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
   const int dt = a.seg[0].w.dtype, cols = (int)a.seg[0].w.cols, nb = cols / 256;
   if (grid < 1) return hipErrorInvalidValue;
   if (!kq_type(dt)) {
+    bool fq = a.fq && a.m >= FQ_MIN_ROWS;
+    for (int i = 0; i < a.nseg; i++) fq = fq && a.seg[i].w.dtype == T_Q8_0;
+    if (fq) {
+      hipLaunchKernelGGL(k_mv_fq, dim3(grid), dim3(256), 0, s, a, st);
+      return hipGetLastError();
+    }
 #define SPX_MVF(MTV) hipLaunchKernelGGL(k_mv_f<MTV>, dim3(grid), dim3(256), 0, s, a, st)
     switch (mt) {
     case 1: SPX_MVF(1); break;

@@ -359,6 +359,7 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
         GUArgs ga{};
         ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.x = E->xn2; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
+        ga.fq = E->mq && m >= FQ_MIN_ROWS ? 1 : 0;
         if (d_int) ga.hq = E->hq;
         SPX_HIP(launch_gateup(ga, m, gmode, E->st_dev, 1, s));
       }

@@ -130,6 +130,7 @@ struct GUArgs {
   int *counter;                       // [vectors][n_ff/256][1 + GU_SUB][CNT_STRIDE], zero between passes
   int n_ff;
   int G;                              // row-parallel launch: lane groups per row
+  int fq;                             // dense Q8_0, 4..16 rows: on the fp32 matrix cores (k_gateup_fq)
 };
 
 struct DownArgs {

@@ -687,6 +687,46 @@ __global__ __launch_bounds__(256) void k_mv_f(const MVArgs a, const StepRec *st)
   if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
 }
 
+// One wavefront's half of a Q8_0 16-row tile against up to 16 vectors on the fp32 matrix cores:
+// the batches of eight 32-column blocks with index = kh mod 2 (all of a batch's loads in flight),
+// eight v_mfma_f32_16x16x4f32 per block with A[vector j][kq] = x[j][32b + 8kq + s] and
+// B[kq][row j] = code[32b + 8kq + s] * d (an int8 times an f16 scale: exact in fp32), four
+// accumulator chains (block b in chain b mod 4) summed (0 + 1) + (2 + 3). cp / dp: row
+// lane & 15's codes (+ 8 (lane >> 4)) and scales; xr: vector lane & 15's values (+ 8 (lane >> 4)).
+// r[q]: row lane & 15 of vector 4 (lane >> 4) + q.
+__device__ __forceinline__ void fq_half(const uint8_t *cp, const uint16_t *dp, const float *xr, bool vin, int nb, int kh, float (&r)[4]) {
+  f4v acc[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) acc[u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int b0 = 8 * kh; b0 < nb; b0 += 16) {
+    uint2 c[8];
+    uint32_t dh[8];
+    float4 x0[8], x1[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int b = min(b0 + u, nb - 1);
+      c[u] = *reinterpret_cast<const uint2 *>(cp + (int64_t)b * 32);
+      dh[u] = dp[b];
+      x0[u] = *reinterpret_cast<const float4 *>(xr + (int64_t)b * 32);
+      x1[u] = *reinterpret_cast<const float4 *>(xr + (int64_t)b * 32 + 4);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      if (b0 + u < nb) {
+        const float d = h2f(dh[u]);
+        const float xs[8] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w, x1[u].x, x1[u].y, x1[u].z, x1[u].w};
+#pragma unroll
+        for (int s2 = 0; s2 < 8; s2++) {
+          const float w = (float)(int8_t)((s2 < 4 ? c[u].x : c[u].y) >> (8 * (s2 & 3))) * d;
+          acc[u & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vin ? xs[s2] : 0.0f, w, acc[u & 3], 0, 0, 0);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; q++) r[q] = (acc[0][q] + acc[1][q]) + (acc[2][q] + acc[3][q]);
+}
+
 // Float matvec of 4..16 vectors on the fp32 matrix cores (Q8_0 weights): four wavefronts per
 // workgroup on one task of 32 rows (tasks stride over the grid as k_mv_f's): wavefront w takes
 // the 16-row tile w & 1 and the batches of eight blocks with index = w >> 1 mod 2. Per
@@ -717,37 +757,7 @@ __global__ __launch_bounds__(256) void k_mv_fq(const MVArgs a, const StepRec *st
       const int nb = (int)sg.w.nb;
       const uint8_t *cp = sg.w.pl.p0 + grow * nb * 32 + 8 * kq;
       const uint16_t *dp = reinterpret_cast<const uint16_t *>(sg.w.pl.p3) + grow * nb;
-      const float *xr = a.x + (int64_t)(vin ? j : 0) * a.ld_x + 8 * kq;
-      f4v acc[4];
-#pragma unroll
-      for (int u = 0; u < 4; u++) acc[u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-      for (int b0 = 8 * kh; b0 < nb; b0 += 16) {
-        uint2 c[8];
-        uint32_t dh[8];
-        float4 x0[8], x1[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-          const int b = min(b0 + u, nb - 1);
-          c[u] = *reinterpret_cast<const uint2 *>(cp + (int64_t)b * 32);
-          dh[u] = dp[b];
-          x0[u] = *reinterpret_cast<const float4 *>(xr + (int64_t)b * 32);
-          x1[u] = *reinterpret_cast<const float4 *>(xr + (int64_t)b * 32 + 4);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-          if (b0 + u < nb) {
-            const float d = h2f(dh[u]);
-            const float xs[8] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w, x1[u].x, x1[u].y, x1[u].z, x1[u].w};
-#pragma unroll
-            for (int s2 = 0; s2 < 8; s2++) {
-              const float w = (float)(int8_t)((s2 < 4 ? c[u].x : c[u].y) >> (8 * (s2 & 3))) * d;
-              acc[u & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vin ? xs[s2] : 0.0f, w, acc[u & 3], 0, 0, 0);
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; q++) r[q] = (acc[0][q] + acc[1][q]) + (acc[2][q] + acc[3][q]);
+      fq_half(cp, dp, a.x + (int64_t)(vin ? j : 0) * a.ld_x + 8 * kq, vin, nb, kh, r);
     }
     if (kh == 1) {
 #pragma unroll
@@ -1436,6 +1446,39 @@ __global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec 
   if (a.hq.q) gateup_quant_tail(a, J.nvec, J.jo, 16);
 }
 
+// Dense gate / up + SwiGLU of 4..16 rows on the fp32 matrix cores (Q8_0): 16 rows of h per
+// workgroup, wavefronts 0-1 the gate tile's two halves (fq_half), 2-3 the up tile's; the
+// halves meet in LDS (first + second), h = silu(g) * u as k_gateup_f writes it.
+__global__ __launch_bounds__(256) void k_gateup_fq(const GUArgs a, const StepRec *st) {
+  GUJob J;
+  if (!gu_job(a, st->m, J)) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15, kq = lane >> 4, kh = wave & 1;
+  __shared__ float part[4][4][64];
+  const TensorView &w = wave < 2 ? a.gate : a.up;
+  const int nb = (int)w.nb, n_ff = a.n_ff;
+  const int64_t r0 = (int64_t)blockIdx.x * 16, grow = (int64_t)J.expert * w.rows + min(r0 + j, (int64_t)n_ff - 1);
+  const bool vin = j < J.nvec;
+  const int xv = vin ? (J.jv ? J.jv[j] : j) : 0;
+  float r[4];
+  fq_half(w.pl.p0 + grow * nb * 32 + 8 * kq, reinterpret_cast<const uint16_t *>(w.pl.p3) + grow * nb, a.x + (int64_t)xv * w.cols + 8 * kq,
+          vin, nb, kh, r);
+#pragma unroll
+  for (int q = 0; q < 4; q++) part[wave][q][lane] = r[q];
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int v = 4 * kq + q;
+      const int64_t row = r0 + j;
+      if (v < J.nvec && row < n_ff) {
+        const float g = part[0][q][lane] + part[1][q][lane], u = part[2][q][lane] + part[3][q][lane];
+        st_dev(a.h + (int64_t)(J.jo ? J.jo[v] : v) * n_ff + row, g / (1.0f + expf(-g)) * u);
+      }
+    }
+  }
+  if (a.hq.q) gateup_quant_tail(a, J.nvec, J.jo, 16);
+}
+
 // ------------------------------------------------------------------ down + combine
 // One output row per wavefront; row slots take jobs eight at a time; each job's users get
 // y_e[r] in LDS, then out[b][r] = sum over b's chosen slots, in chosen order, of w * y
@@ -1744,6 +1787,8 @@ static hipError_t launch_gu_t(const GUArgs &a, int mode, const StepRec *st, int 
     const size_t sm = (MT <= 2 ? ldsq_bytes(MT, dim) : 0) + (size_t)4 * 8 * nb * tile_bpb();
     SPX_LDS((k_gateup_kq<T, MT>), sm);
     hipLaunchKernelGGL((k_gateup_kq<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), sm, s, a, st);
+  } else if (T == T_Q8_0 && MT >= 4 && a.fq) {
+    hipLaunchKernelGGL(k_gateup_fq, dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), 0, s, a, st);
   } else {
     hipLaunchKernelGGL((k_gateup_f<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), 0, s, a, st);
   }

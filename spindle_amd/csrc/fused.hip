@@ -687,23 +687,25 @@ __global__ __launch_bounds__(256) void k_mv_f(const MVArgs a, const StepRec *st)
   if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
 }
 
-// One wavefront's half of a Q8_0 16-row tile against up to 16 vectors on the fp32 matrix cores:
-// the batches of eight 32-column blocks with index = kh mod 2 (all of a batch's loads in flight),
+// One wavefront's part of a Q8_0 16-row tile against up to 16 vectors on the fp32 matrix cores:
+// the batches of FQ_B 32-column blocks with index = kp mod FQ_KP (all of a batch's loads in flight),
 // eight v_mfma_f32_16x16x4f32 per block with A[vector j][kq] = x[j][32b + 8kq + s] and
 // B[kq][row j] = code[32b + 8kq + s] * d (an int8 times an f16 scale: exact in fp32), four
 // accumulator chains (block b in chain b mod 4) summed (0 + 1) + (2 + 3). cp / dp: row
 // lane & 15's codes (+ 8 (lane >> 4)) and scales; xr: vector lane & 15's values (+ 8 (lane >> 4)).
 // r[q]: row lane & 15 of vector 4 (lane >> 4) + q.
-__device__ __forceinline__ void fq_half(const uint8_t *cp, const uint16_t *dp, const float *xr, bool vin, int nb, int kh, float (&r)[4]) {
+constexpr int FQ_KP = 8;  // parts a tile's blocks are split into (wavefronts per tile)
+constexpr int FQ_B = 4;   // blocks a part loads at once
+__device__ __forceinline__ void fq_part(const uint8_t *cp, const uint16_t *dp, const float *xr, bool vin, int nb, int kp, float (&r)[4]) {
   f4v acc[4];
 #pragma unroll
   for (int u = 0; u < 4; u++) acc[u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int b0 = 8 * kh; b0 < nb; b0 += 16) {
-    uint2 c[8];
-    uint32_t dh[8];
-    float4 x0[8], x1[8];
+  for (int b0 = FQ_B * kp; b0 < nb; b0 += FQ_B * FQ_KP) {
+    uint2 c[FQ_B];
+    uint32_t dh[FQ_B];
+    float4 x0[FQ_B], x1[FQ_B];
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
+    for (int u = 0; u < FQ_B; u++) {
       const int b = min(b0 + u, nb - 1);
       c[u] = *reinterpret_cast<const uint2 *>(cp + (int64_t)b * 32);
       dh[u] = dp[b];
@@ -711,7 +713,7 @@ __device__ __forceinline__ void fq_half(const uint8_t *cp, const uint16_t *dp, c
       x1[u] = *reinterpret_cast<const float4 *>(xr + (int64_t)b * 32 + 4);
     }
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
+    for (int u = 0; u < FQ_B; u++) {
       if (b0 + u < nb) {
         const float d = h2f(dh[u]);
         const float xs[8] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w, x1[u].x, x1[u].y, x1[u].z, x1[u].w};
@@ -727,22 +729,18 @@ __device__ __forceinline__ void fq_half(const uint8_t *cp, const uint16_t *dp, c
   for (int q = 0; q < 4; q++) r[q] = (acc[0][q] + acc[1][q]) + (acc[2][q] + acc[3][q]);
 }
 
-// Float matvec of 4..16 vectors on the fp32 matrix cores (Q8_0 weights): four wavefronts per
-// workgroup on one task of 32 rows (tasks stride over the grid as k_mv_f's): wavefront w takes
-// the 16-row tile w & 1 and the batches of eight blocks with index = w >> 1 mod 2. Per
-// 32-column block eight v_mfma_f32_16x16x4f32: lane (j, kq) = (lane & 15, lane >> 4) gives
-// A[vector j][k = kq] = x[j][32b + 8kq + s] and B[k = kq][row j] = code[32b + 8kq + s] * d
-// (an int8 times an f16 scale: exact in fp32) at step s; D holds row lane & 15 of vectors
-// 4 (lane >> 4) .. + 3. Every product is the per-lane walk's; the sums run in a fixed order of
-// their own (four chains, block b in chain b mod 4, (0 + 1) + (2 + 3), then the first half's
-// batches + the second's): a row's result does not depend on the pass's other rows.
-__global__ __launch_bounds__(256) void k_mv_fq(const MVArgs a, const StepRec *st) {
+// Float matvec of 4..16 vectors on the fp32 matrix cores (Q8_0 weights): sixteen wavefronts
+// per workgroup on one task of 32 rows (tasks stride over the grid as k_mv_f's): wavefront w
+// takes the 16-row tile w & 1 and part w >> 1 of its blocks (fq_part); the parts meet in LDS
+// and are summed in part order. Every product is the per-lane walk's; the sums run in a fixed
+// order of their own, so a row's result does not depend on the pass's other rows.
+__global__ __launch_bounds__(1024) void k_mv_fq(const MVArgs a, const StepRec *st) {
   const int m = st ? st->m : a.m;
   const bool coh = a.tail.nw != nullptr;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15, kq = lane >> 4;
-  const int tile = wave & 1, kh = wave >> 1;
+  const int tile = wave & 1, kp = wave >> 1;
   __shared__ unsigned long long sbest[16];
-  __shared__ float part[2][4][64];
+  __shared__ float part[FQ_KP][2][4][64];
   if (threadIdx.x < 16) sbest[threadIdx.x] = 0;
   __syncthreads();
   const int total = a.seg[0].wgs + (a.nseg > 1 ? a.seg[1].wgs : 0) + (a.nseg > 2 ? a.seg[2].wgs : 0);
@@ -755,24 +753,32 @@ __global__ __launch_bounds__(256) void k_mv_fq(const MVArgs a, const StepRec *st
     if (r0 < sg.r1) {
       const int64_t grow = (int64_t)sg.expert * sg.w.rows + min(r0 + j, sg.r1 - 1);
       const int nb = (int)sg.w.nb;
-      const uint8_t *cp = sg.w.pl.p0 + grow * nb * 32 + 8 * kq;
-      const uint16_t *dp = reinterpret_cast<const uint16_t *>(sg.w.pl.p3) + grow * nb;
-      fq_half(cp, dp, a.x + (int64_t)(vin ? j : 0) * a.ld_x + 8 * kq, vin, nb, kh, r);
+      fq_part(sg.w.pl.p0 + grow * nb * 32 + 8 * kq, reinterpret_cast<const uint16_t *>(sg.w.pl.p3) + grow * nb,
+              a.x + (int64_t)(vin ? j : 0) * a.ld_x + 8 * kq, vin, nb, kp, r);
     }
-    if (kh == 1) {
 #pragma unroll
-      for (int q = 0; q < 4; q++) part[tile][q][lane] = r[q];
-    }
+    for (int q = 0; q < 4; q++) part[kp][tile][q][lane] = r[q];
     __syncthreads();
-    if (kh == 0 && r0 < sg.r1) {
+    if (kp == 0 && r0 < sg.r1) {
       const int64_t row = r0 + j;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const int v = 4 * kq + q;
-        const float res = r[q] + part[tile][q][lane];
+        float res = part[0][tile][q][lane];
+#pragma unroll
+        for (int p2 = 1; p2 < FQ_KP; p2++) res = res + part[p2][tile][q][lane];
+        unsigned long long key = 0;
         if (v < m && row < sg.r1) {
           out_store(sg.out + (int64_t)v * sg.ld_out + row, res, coh);
-          if (a.best) atomicMax(&sbest[v], pick_key(res, a.lscale, row));
+          key = pick_key(res, a.lscale, row);
+        }
+        if (a.best) {  // the 16 rows' best key of vector v, then one atomic per vector
+#pragma unroll
+          for (int o = 1; o < 16; o <<= 1) {
+            const unsigned long long k2 = __shfl_xor(key, o, 64);
+            key = k2 > key ? k2 : key;
+          }
+          if (j == 0 && v < m) atomicMax(&sbest[v], key);
         }
       }
     }
@@ -782,7 +788,7 @@ __global__ __launch_bounds__(256) void k_mv_fq(const MVArgs a, const StepRec *st
     __syncthreads();
     if ((int)threadIdx.x < m) a.best[(int64_t)threadIdx.x * a.nbest + blockIdx.x] = sbest[threadIdx.x];
   }
-  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
+  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<16>(a.tail, 0, m);
 }
 
 // ------------------------------------------------------------------ standalone kernels
@@ -1324,7 +1330,7 @@ __device__ __forceinline__ void gateup_quant_tail(const GUArgs &a, int nvec, con
     quant_u[threadIdx.x] = last;
   }
   __syncthreads();
-  for (int u = wave; u < nvec; u += 4) {
+  for (int u = wave; u < nvec; u += (int)(blockDim.x >> 6)) {
     if (!quant_u[u]) continue;
     const int vo = jo ? jo[u] : u;
     const float *hp = a.h + (int64_t)vo * n_ff + blk * 256 + 4 * lane;
@@ -1447,23 +1453,24 @@ __global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec 
 }
 
 // Dense gate / up + SwiGLU of 4..16 rows on the fp32 matrix cores (Q8_0): 16 rows of h per
-// workgroup, wavefronts 0-1 the gate tile's two halves (fq_half), 2-3 the up tile's; the
-// halves meet in LDS (first + second), h = silu(g) * u as k_gateup_f writes it.
-__global__ __launch_bounds__(256) void k_gateup_fq(const GUArgs a, const StepRec *st) {
+// workgroup of sixteen wavefronts: wavefront w takes part w >> 1 (fq_part) of the gate tile
+// (w even) or the up tile (w odd); the parts meet in LDS (summed in part order) and
+// h = silu(g) * u as k_gateup_f writes it.
+__global__ __launch_bounds__(1024) void k_gateup_fq(const GUArgs a, const StepRec *st) {
   GUJob J;
   if (!gu_job(a, st->m, J)) return;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15, kq = lane >> 4, kh = wave & 1;
-  __shared__ float part[4][4][64];
-  const TensorView &w = wave < 2 ? a.gate : a.up;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15, kq = lane >> 4, mat = wave & 1, kp = wave >> 1;
+  __shared__ float part[FQ_KP][2][4][64];
+  const TensorView &w = mat ? a.up : a.gate;
   const int nb = (int)w.nb, n_ff = a.n_ff;
   const int64_t r0 = (int64_t)blockIdx.x * 16, grow = (int64_t)J.expert * w.rows + min(r0 + j, (int64_t)n_ff - 1);
   const bool vin = j < J.nvec;
   const int xv = vin ? (J.jv ? J.jv[j] : j) : 0;
   float r[4];
-  fq_half(w.pl.p0 + grow * nb * 32 + 8 * kq, reinterpret_cast<const uint16_t *>(w.pl.p3) + grow * nb, a.x + (int64_t)xv * w.cols + 8 * kq,
-          vin, nb, kh, r);
+  fq_part(w.pl.p0 + grow * nb * 32 + 8 * kq, reinterpret_cast<const uint16_t *>(w.pl.p3) + grow * nb, a.x + (int64_t)xv * w.cols + 8 * kq,
+          vin, nb, kp, r);
 #pragma unroll
-  for (int q = 0; q < 4; q++) part[wave][q][lane] = r[q];
+  for (int q = 0; q < 4; q++) part[kp][mat][q][lane] = r[q];
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
@@ -1471,7 +1478,9 @@ __global__ __launch_bounds__(256) void k_gateup_fq(const GUArgs a, const StepRec
       const int v = 4 * kq + q;
       const int64_t row = r0 + j;
       if (v < J.nvec && row < n_ff) {
-        const float g = part[0][q][lane] + part[1][q][lane], u = part[2][q][lane] + part[3][q][lane];
+        float g = part[0][0][q][lane], u = part[0][1][q][lane];
+#pragma unroll
+        for (int p2 = 1; p2 < FQ_KP; p2++) { g = g + part[p2][0][q][lane]; u = u + part[p2][1][q][lane]; }
         st_dev(a.h + (int64_t)(J.jo ? J.jo[v] : v) * n_ff + row, g / (1.0f + expf(-g)) * u);
       }
     }
@@ -1665,7 +1674,7 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
     bool fq = a.fq && a.m >= FQ_MIN_ROWS;
     for (int i = 0; i < a.nseg; i++) fq = fq && a.seg[i].w.dtype == T_Q8_0;
     if (fq) {
-      hipLaunchKernelGGL(k_mv_fq, dim3(grid), dim3(256), 0, s, a, st);
+      hipLaunchKernelGGL(k_mv_fq, dim3(grid), dim3(1024), 0, s, a, st);
       return hipGetLastError();
     }
 #define SPX_MVF(MTV) hipLaunchKernelGGL(k_mv_f<MTV>, dim3(grid), dim3(256), 0, s, a, st)
@@ -1788,7 +1797,7 @@ static hipError_t launch_gu_t(const GUArgs &a, int mode, const StepRec *st, int 
     SPX_LDS((k_gateup_kq<T, MT>), sm);
     hipLaunchKernelGGL((k_gateup_kq<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), sm, s, a, st);
   } else if (T == T_Q8_0 && MT >= 4 && a.fq) {
-    hipLaunchKernelGGL(k_gateup_fq, dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), 0, s, a, st);
+    hipLaunchKernelGGL(k_gateup_fq, dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(1024), 0, s, a, st);
   } else {
     hipLaunchKernelGGL((k_gateup_f<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), 0, s, a, st);
   }

@@ -73,7 +73,8 @@ struct spx_engine {
   int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;
   bool pf_attn = true;      // prefill passes: attention on k_attn_pf + its merge launch (SPX_PF_ATTN)
   int pf_min_rows = MAX_M + 1;  // passes of this many rows or more prepare their attention rows once (SPX_PF_MIN)
-  bool att_merge = false;  // one-row passes: attention chunks merged inside the attention launch (SPX_ATT_MERGE)  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
+  bool att_merge = false;  // one-row passes: attention chunks merged inside the attention launch (SPX_ATT_MERGE)
+  int att_mt_min = 2;      // unprepared passes of this many rows (up to 16) take the multi-tile attention (SPX_ATT_MT; 0: never)  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
   std::map<std::string, int64_t> vec_len;
@@ -271,6 +272,14 @@ int mv_one(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld
 // LM head and the greedy pick (forward_slice / forward_batch_slice + compute_logits_batch).
 // Residual stream: the embedding writes xA; attn_output's norm tail adds its output to xA
 // and writes xB; the FFN's tail adds its output to xB and writes xA.
+// Attention of a pass of m unprepared rows: the multi-tile kernels (launch_attention_mt) from
+// att_mt_min rows, else the tile-per-workgroup kernel; both give the same bits.
+hipError_t attn_launch(spx_engine *E, const AttnArgs &aa, int m, hipStream_t s) {
+  if (E->att_mt_min > 0 && m >= E->att_mt_min && m <= MAX_M && !aa.prepped && (aa.hd == 64 || aa.hd == 128))
+    return launch_attention_mt(aa, m, E->st_dev, s);
+  return launch_attention(aa, m, E->st_dev, s);
+}
+
 int enqueue_forward(spx_engine *E, int m, bool advance = false) {
   const auto &c = E->c;
   hipStream_t s = E->ctx->stream;
@@ -313,7 +322,7 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
       aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
       aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
       aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
-      SPX_HIP(launch_attention(aa, m, E->st_dev, s));
+      SPX_HIP(attn_launch(E, aa, m, s));
     }
     if (wo_int && !att_q_fused) { ProfScope ps(E, PC_QUANT, 0); SPX_HIP(launch_q8kp_quantize(E->att, E->q_dim, E->q_dim, m, E->aq, s)); }
     {  // attn_output + residual + ffn_norm
@@ -583,9 +592,9 @@ int enqueue_pass_m(spx_engine *E, int m) {
         SPX_HIP(launch_rows_prep(aa, E->qp, m, E->st_dev, s));
         aa.q = E->qp;
         aa.prepped = 1;
-        SPX_HIP(E->pf_attn ? launch_attention_pf(aa, m, E->st_dev, s) : launch_attention(aa, m, E->st_dev, s));
+        SPX_HIP(E->pf_attn ? launch_attention_pf(aa, m, E->st_dev, s) : attn_launch(E, aa, m, s));
       } else {
-        SPX_HIP(launch_attention(aa, m, E->st_dev, s));
+        SPX_HIP(attn_launch(E, aa, m, s));
       }
     }
     if (!att_q_fused) { ProfScope ps(E, PC_QUANT, 0); SPX_HIP(launch_q8kp_quantize(E->att, E->q_dim, E->q_dim, m, E->aq, s)); }
@@ -779,6 +788,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   if (const char *v = std::getenv("SPX_DOWN_MODE")) E->down_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_ATT_MERGE")) E->att_merge = atoi(v) != 0;
   if (const char *v = std::getenv("SPX_PF_ATTN")) E->pf_attn = atoi(v) != 0;
+  if (const char *v = std::getenv("SPX_ATT_MT")) E->att_mt_min = std::max(0, std::min(MAX_M + 1, atoi(v)));
   if (const char *v = std::getenv("SPX_PF_MIN")) E->pf_min_rows = std::max(2, std::min(MAX_M + 1, atoi(v)));
   *out = E;
   return 0;
@@ -1255,7 +1265,7 @@ int spx_engine_attention(spx_engine *E, int layer, const float *q, const float *
   aa.layer = layer; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
   aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
   aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
-  SPX_HIP(launch_attention(aa, m, E->st_dev, s));
+  SPX_HIP(attn_launch(E, aa, m, s));
   SPX_HIP(hipStreamSynchronize(s));  // the step record is the engine's
   return 0;
 }

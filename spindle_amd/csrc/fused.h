@@ -158,6 +158,10 @@ hipError_t launch_rows_prep(const AttnArgs &a, float *qp, int m, const StepRec *
 // The same attention for prepared rows as partials (a workgroup per chunk, kv head and four
 // query tiles, a wavefront per tile) and a merge launch: each output has launch_attention's bits
 hipError_t launch_attention_pf(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);
+// Passes of up to 16 rows, unprepared: the same outputs (att rows, Q8_K, the pass's K / V rows in
+// the cache) as launch_attention, bit for bit, from a workgroup per (chunk, kv head) whose
+// wavefronts take a query tile each, then a merge launch a workgroup per 256 att values and row
+hipError_t launch_attention_mt(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);
 hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStream_t s);
 hipError_t launch_gateup(const GUArgs &a, int mt, int mode, const StepRec *st, int max_jobs, hipStream_t s);
 hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, hipStream_t s);

@@ -1063,11 +1063,11 @@ __global__ __launch_bounds__(256) void k_attn_pf(const AttnArgs a, const StepRec
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int qi = qa + kg + r;
-      if (qi < NQ) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(acc[r]), r_o, ((c * ATT_QMAX + qi) * HD + j * 16 + ar) * 4, 0, 0);
+      if (qi < NQ) st_coh1(r_o, ((c * ATT_QMAX + qi) * HD + j * 16 + ar) * 4, acc[r]);  // through the L2 (see k_attn_mt)
     }
   }
   if (lane < 16 && qa + lane < NQ)
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2v, f2v{rm, rl}), r_ml, (c * ATT_QMAX + qa + lane) * 8, 0, 0);
+    st_coh2(r_ml, (c * ATT_QMAX + qa + lane) * 8, f2v{rm, rl});
 }
 
 // The merges of a prefill pass's partials, one workgroup per (kv head, query tile, chunk group):
@@ -1096,6 +1096,391 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(const AttnArgs a, const S
   }
   __syncthreads();
   attn_tile_out<HD>(a, h, qa, NQ, ol);
+}
+
+// ------------------------------------------------------------------ multi-tile attention
+// Passes of up to 16 rows: one workgroup of eight wavefronts per (64-position chunk, kv head,
+// eight 16-query tiles). The chunk's K / V rows go to LDS once (the pass's own rows normed and
+// rotated on the way, and written to the cache); then wavefront w computes query tile
+// 8 blockIdx.z + w alone, in registers, with no further barrier:
+//   * its queries prepared in the matrix cores' operand layout (lane: query lane & 15, dims
+//     16 kt + 4 (lane >> 4) .. + 3), head_prep's operations with its norm reduction tree
+//     restated over that layout (every butterfly node pairs the same two values);
+//   * the scores as S^T = K Q^T: a lane then holds positions 16 pb + 4 (lane >> 4) + r of its
+//     query, which is the layout P V takes its probabilities in, so they never go to LDS;
+//     the products are the ones of Q K^T (f16 x f16, exact in fp32) summed in the same order;
+//   * the chunk's max and sum as the 64-lane butterflies of wave_max / wave_sum restated over
+//     the positions a lane holds (in-lane for position bits 0, 1, 4, 5; lane ^ 16, lane ^ 32 for
+//     bits 2, 3), then P V as attn_item does it.
+// Each (chunk, query) partial therefore has attn_item's bits; k_attn_mrg merges them.
+template <int HD>
+struct MtLds {
+  static constexpr int KS = HD + 8, VS = 64 + 8;
+  // K [64][KS], V^T [HD][VS] (f16); rotations of the pass's rows [MAX_M][HD/2] (float2), the
+  // query norm weights [HD]; then, with a query bias, the kv group's biases [g][HD]
+  static constexpr size_t OFF_ROT = (size_t)64 * KS * 2 + (size_t)HD * VS * 2, OFF_QN = OFF_ROT + (size_t)MAX_M * HD * 4,
+                          OFF_QB = OFF_QN + (size_t)HD * 4;
+  static size_t bytes(int g, bool bias) { return OFF_QB + (bias ? (size_t)g * HD * 4 : 0); }
+};
+
+template <int HD>
+__global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec *st) {
+  using LY = MtLds<HD>;
+  constexpr int KS = LY::KS, VS = LY::VS;
+  constexpr int DT = HD / 16;              // 16-dim tiles: k steps of K Q^T, output tiles of P V
+  constexpr int DQ = HD / 8, NU = DQ / 8;  // K / V loader: 8 threads a position, DQ dims each
+  constexpr int half = HD / 2;
+  extern __shared__ __align__(16) uint8_t smem[];
+  _Float16 *ks = reinterpret_cast<_Float16 *>(smem);  // [64][KS]
+  _Float16 *vt = ks + 64 * KS;                        // [HD][VS] (V transposed)
+  float *rot_s = reinterpret_cast<float *>(smem + LY::OFF_ROT), *qn_s = reinterpret_cast<float *>(smem + LY::OFF_QN);
+  float *qb_s = reinterpret_cast<float *>(smem + LY::OFF_QB);
+  const int h = blockIdx.y, c = blockIdx.x;
+  const int m = st->m, start = st->start, total = start + m;
+  const int g = a.n_heads / a.n_kv, NQ = m * g;
+  if (blockIdx.z * 128 >= NQ || c >= (total + 63) / 64) return;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int ar = lane & 15, kq = lane >> 4, kg = 4 * kq;
+  const int qa = (blockIdx.z * 8 + wave) * 16, qi = qa + ar;
+  const bool qact = qi < NQ;
+  const int p_lo = c * 64, p_hi = min(p_lo + 64, total);
+  const int64_t cache0 = (int64_t)a.layer * a.max_seq * a.kv_dim + (int64_t)h * HD;
+
+  // (1) loads in the order their values are needed (they return in issue order): the values
+  // every wavefront shares (rotations of the pass's rows, norm weights, biases) for LDS, then
+  // this lane's raw query values
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 sh_rot = z4, sh_qn = z4, sh_qb = z4;
+  const bool ld_rot = tid < m * (half / 2), ld_qn = a.q_norm && tid < HD / 4, ld_qb = a.q_bias && tid < g * HD / 4;
+  if (ld_rot) sh_rot = reinterpret_cast<const float4 *>(a.rope + (int64_t)start * half)[tid];
+  if (ld_qn) sh_qn = reinterpret_cast<const float4 *>(a.q_norm)[tid];
+  if (ld_qb) sh_qb = reinterpret_cast<const float4 *>(a.q_bias + (int64_t)h * g * HD)[tid];
+  float4 xq[DT];
+  const int qb_row = qact ? qi / g : 0, qhead = qact ? qi % g : 0;  // a lane past the pass reads row 0 and drops it
+  {
+    const float *src = a.q + (int64_t)qb_row * a.n_heads * HD + (h * g + qhead) * HD + kg;
+#pragma unroll
+    for (int kt = 0; kt < DT; kt++) xq[kt] = *reinterpret_cast<const float4 *>(src + kt * 16);
+  }
+  // (2) the pass's new K / V rows in this chunk: rows b = wave, wave + 8 (head_prep's layout)
+  const bool act = lane < half;
+  const int da = a.neox ? lane : 2 * lane, db = a.neox ? lane + half : 2 * lane + 1;
+  float nk0[2], nk1[2], nkb0[2], nkb1[2], nv0[2], nv1[2], nvb0[2], nvb1[2], nkc[2], nks[2], kn0 = 0.0f, kn1 = 0.0f;
+  if (a.k_norm && act) { kn0 = a.k_norm[da]; kn1 = a.k_norm[db]; }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int b = wave + 8 * j, pos = start + b;
+    nk0[j] = nk1[j] = nkb0[j] = nkb1[j] = nv0[j] = nv1[j] = nvb0[j] = nvb1[j] = 0.0f;
+    nkc[j] = 1.0f;
+    nks[j] = 0.0f;
+    if (b < m && pos >= p_lo && pos < p_hi && act) {
+      const float *kp = a.k + (int64_t)b * a.kv_dim + h * HD, *vp = a.v + (int64_t)b * a.kv_dim + h * HD;
+      nk0[j] = kp[da]; nk1[j] = kp[db];
+      nv0[j] = vp[da]; nv1[j] = vp[db];
+      if (a.k_bias) { nkb0[j] = a.k_bias[h * HD + da]; nkb1[j] = a.k_bias[h * HD + db]; }
+      if (a.v_bias) { nvb0[j] = a.v_bias[h * HD + da]; nvb1[j] = a.v_bias[h * HD + db]; }
+      const float2 cs = a.rope[(int64_t)pos * half + lane];
+      nkc[j] = cs.x;
+      nks[j] = cs.y;
+    }
+  }
+  // (3) the chunk's cached rows
+  const int lp = tid >> 3, lq = tid & 7;
+  uint32_t kr[4 * NU], vr[4 * NU];
+  attn_kv_load<NU>(a, cache0 + (int64_t)min(p_lo + lp, p_hi - 1) * a.kv_dim + lq * DQ, kr, vr);
+
+  // the shared values to LDS (waits for them only)
+  if (ld_rot) reinterpret_cast<float4 *>(rot_s)[tid] = sh_rot;
+  if (ld_qn) reinterpret_cast<float4 *>(qn_s)[tid] = sh_qn;
+  if (ld_qb) reinterpret_cast<float4 *>(qb_s)[tid] = sh_qb;
+  __syncthreads();
+  // (4) the queries: bias, RMSNorm, rotation (head_prep's operations), as hi + lo f16 operands
+  // (waits for (1) only; a wavefront without a tile prepares zeros)
+  float x[DT][4];
+#pragma unroll
+  for (int kt = 0; kt < DT; kt++) {
+    x[kt][0] = xq[kt].x; x[kt][1] = xq[kt].y; x[kt][2] = xq[kt].z; x[kt][3] = xq[kt].w;
+    if (a.q_bias) {
+      const float4 xb = *reinterpret_cast<const float4 *>(qb_s + qhead * HD + kt * 16 + kg);
+      x[kt][0] += xb.x; x[kt][1] += xb.y; x[kt][2] += xb.z; x[kt][3] += xb.w;
+    }
+  }
+  if (a.q_norm) {
+    // head_prep: wave_sum over lanes L < HD/2 of fmaf(x[da(L)], x[da(L)], x[db(L)]^2) (lanes
+    // past HD/2 add zeros); node L ^ 2^i of that butterfly, over the values this lane holds
+    float ssq;
+    if (a.neox) {  // L = 16kt + 4kq + s (kt < DT/2): bits 0-1 s, 2-3 kq, 4.. kt
+      float t4[DT / 2];
+#pragma unroll
+      for (int kt = 0; kt < DT / 2; kt++) {
+        float tt[4];
+#pragma unroll
+        for (int s = 0; s < 4; s++) tt[s] = fmaf(x[kt][s], x[kt][s], x[kt + DT / 2][s] * x[kt + DT / 2][s]);
+        t4[kt] = (tt[0] + tt[1]) + (tt[2] + tt[3]);
+        t4[kt] = add16(t4[kt]);
+        t4[kt] = add32(t4[kt]);
+      }
+      if constexpr (DT / 2 == 4) ssq = (t4[0] + t4[1]) + (t4[2] + t4[3]);
+      else ssq = t4[0] + t4[1];
+    } else {  // L = 8kt + 2kq + s/2: bit 0 s/2, bits 1-2 kq, 3.. kt
+      float t2[DT];
+#pragma unroll
+      for (int kt = 0; kt < DT; kt++) {
+        t2[kt] = fmaf(x[kt][0], x[kt][0], x[kt][1] * x[kt][1]) + fmaf(x[kt][2], x[kt][2], x[kt][3] * x[kt][3]);
+        t2[kt] = add16(t2[kt]);
+        t2[kt] = add32(t2[kt]);
+      }
+      if constexpr (DT == 8) ssq = ((t2[0] + t2[1]) + (t2[2] + t2[3])) + ((t2[4] + t2[5]) + (t2[6] + t2[7]));
+      else ssq = (t2[0] + t2[1]) + (t2[2] + t2[3]);
+    }
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ssq, (float)HD) + a.eps));
+#pragma unroll
+    for (int kt = 0; kt < DT; kt++) {
+      const float4 nq = *reinterpret_cast<const float4 *>(qn_s + kt * 16 + kg);
+      x[kt][0] = x[kt][0] * inv * nq.x; x[kt][1] = x[kt][1] * inv * nq.y;
+      x[kt][2] = x[kt][2] * inv * nq.z; x[kt][3] = x[kt][3] * inv * nq.w;
+    }
+  }
+  if (a.neox) {
+#pragma unroll
+    for (int kt = 0; kt < DT / 2; kt++) {
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const float4 r4 = *reinterpret_cast<const float4 *>(rot_s + qb_row * HD + 2 * (kt * 16 + kg) + 4 * (s >> 1));
+        const float cv = (s & 1) ? r4.z : r4.x, sn = (s & 1) ? r4.w : r4.y;
+        const float x0 = x[kt][s], x1 = x[kt + DT / 2][s];
+        x[kt][s] = x0 * cv - x1 * sn;
+        x[kt + DT / 2][s] = x0 * sn + x1 * cv;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int kt = 0; kt < DT; kt++) {
+      const float4 r4 = *reinterpret_cast<const float4 *>(rot_s + qb_row * HD + 2 * (kt * 8 + 2 * kq));
+#pragma unroll
+      for (int p = 0; p < 2; p++) {
+        const float cv = p ? r4.z : r4.x, sv = p ? r4.w : r4.y;
+        const float x0 = x[kt][2 * p], x1 = x[kt][2 * p + 1];
+        x[kt][2 * p] = x0 * cv - x1 * sv;
+        x[kt][2 * p + 1] = x0 * sv + x1 * cv;
+      }
+    }
+  }
+  h4v qhi[DT], qlo[DT];
+#pragma unroll
+  for (int kt = 0; kt < DT; kt++)
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      _Float16 hh, ll;
+      split_f16(qact ? x[kt][s] : 0.0f, hh, ll);
+      qhi[kt][s] = hh;
+      qlo[kt][s] = ll;
+    }
+  // (5) LDS
+  // cached rows -> LDS (K row-major, V transposed); rows past the pass are zero, the pass's
+  // rows come from (2)
+  if (p_lo + lp >= total) {
+#pragma unroll
+    for (int t = 0; t < 4 * NU; t++) { kr[t] = 0u; vr[t] = 0u; }
+  }
+  if (p_lo + lp < start || p_lo + lp >= total) {
+    uint16_t *vt16 = reinterpret_cast<uint16_t *>(vt);
+#pragma unroll
+    for (int u = 0; u < NU; u++) reinterpret_cast<uint4 *>(ks + lp * KS + lq * DQ)[u] = make_uint4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]);
+#pragma unroll
+    for (int t = 0; t < 4 * NU; t++) {
+      vt16[(lq * DQ + 2 * t) * VS + lp] = (uint16_t)(vr[t] & 0xffffu);
+      vt16[(lq * DQ + 2 * t + 1) * VS + lp] = (uint16_t)(vr[t] >> 16);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int b = wave + 8 * j, pos = start + b, pp = pos - p_lo;
+    if (b < m && pos >= p_lo && pos < p_hi) {
+      float e0, e1;
+      head_prep_pre(nk0[j], nk1[j], nkb0[j], nkb1[j], a.k_bias != nullptr, a.k_norm != nullptr, kn0, kn1, true, nkc[j], nks[j], HD, a.eps,
+                    e0, e1);
+      if (act) {
+        const __half k0 = __float2half_rn(e0), k1 = __float2half_rn(e1);
+        ks[pp * KS + da] = (_Float16)__half2float(k0);
+        ks[pp * KS + db] = (_Float16)__half2float(k1);
+        if (blockIdx.z == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
+      }
+      head_prep_pre(nv0[j], nv1[j], nvb0[j], nvb1[j], a.v_bias != nullptr, false, 0.0f, 0.0f, false, 1.0f, 0.0f, HD, a.eps, e0, e1);
+      if (act) {
+        const __half v0 = __float2half_rn(e0), v1 = __float2half_rn(e1);
+        vt[da * VS + pp] = (_Float16)__half2float(v0);
+        vt[db * VS + pp] = (_Float16)__half2float(v1);
+        if (blockIdx.z == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
+      }
+    }
+  }
+
+  __syncthreads();
+  if (qa >= NQ) return;  // no tile (no barrier follows)
+
+  // (6) scores S^T = K Q^T: sacc[pb] holds S[query ar][position 16 pb + kg + r]
+  f4v sacc[4];
+#pragma unroll
+  for (int pb = 0; pb < 4; pb++) {
+    sacc[pb] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kt = 0; kt < DT; kt++) {
+      const h4v bk = *reinterpret_cast<const h4v *>(ks + (pb * 16 + ar) * KS + kt * 16 + kg);
+      sacc[pb] = mfma16(bk, qhi[kt], sacc[pb]);
+      sacc[pb] = mfma16(bk, qlo[kt], sacc[pb]);
+    }
+  }
+  // (7) softmax of the chunk (the item's only sub-chunk: running max -inf, sum 0 before it)
+  const int lim = qact ? min(p_hi, start + qi / g + 1) : p_lo;  // positions < lim are visible
+  float sv[4][4], mx = -INFINITY;
+#pragma unroll
+  for (int pb = 0; pb < 4; pb++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int pos = p_lo + pb * 16 + kg + r;
+      sv[pb][r] = pos < lim ? sacc[pb][r] * a.scale : -INFINITY;
+      mx = fmaxf(mx, sv[pb][r]);
+    }
+  mx = max16(mx);
+  mx = max32(mx);
+  const float mn = fmaxf(-INFINITY, mx);
+  float pv[4][4], ls4[4];
+#pragma unroll
+  for (int pb = 0; pb < 4; pb++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) pv[pb][r] = (sv[pb][r] == -INFINITY || mn == -INFINITY) ? 0.0f : expf(sv[pb][r] - mn);
+    // wave_sum over positions (lane = position): bits 0, 1 in-lane, 2 lane ^ 16, 3 lane ^ 32
+    ls4[pb] = (pv[pb][0] + pv[pb][1]) + (pv[pb][2] + pv[pb][3]);
+    ls4[pb] = add16(ls4[pb]);
+    ls4[pb] = add32(ls4[pb]);
+  }
+  const float ls = (ls4[0] + ls4[1]) + (ls4[2] + ls4[3]);  // position bits 4, 5
+  const float al = mn == -INFINITY ? 1.0f : 0.0f;
+  const float rl = 0.0f * al + ls;
+  // (8) O = P V for every 16-dim tile (O starts at zero: attn_item's O * alpha is 0 here)
+  h4v phv[4], plv[4];
+#pragma unroll
+  for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      _Float16 hh, ll;
+      split_f16(pv[kt][r], hh, ll);
+      phv[kt][r] = hh;
+      plv[kt][r] = ll;
+    }
+  // partials written through the L2 (sc1): ~10 MB of them at M = 9 would otherwise sit dirty in
+  // the eight L2s and be written back at the end of the launch, on the merge's critical path
+  const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nslot) * ATT_QMAX * 2);
+  const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nslot) * ATT_QMAX * HD);
+#pragma unroll
+  for (int dt = 0; dt < DT; dt++) {
+    f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+      const h4v bv = *reinterpret_cast<const h4v *>(vt + (dt * 16 + ar) * VS + kt * 16 + kg);
+      acc = mfma16(phv[kt], bv, acc);
+      acc = mfma16(plv[kt], bv, acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int q = qa + kg + r;
+      if (q < NQ) st_coh1(r_o, ((c * ATT_QMAX + q) * HD + dt * 16 + ar) * 4, acc[r]);
+    }
+  }
+  if (kq == 0 && qact) st_coh2(r_ml, (c * ATT_QMAX + qi) * 8, f2v{mn, rl});
+}
+
+// The merge of k_attn_mt's partials: one workgroup per (256 values of an att row, row); four
+// slices of 256 threads (a value each) merge chunk groups gs, gs + 4, .. (kd_merge's and
+// attn_merge_q's operations: M = max, w = exp(m - M), L and O as fma chains in chunk order),
+// then slice 0 merges the groups in group order, writes the att row and, when a.aq is set, the
+// 256 values' Q8_K block (attn_tile_out's quantization).
+template <int HD>
+__global__ __launch_bounds__(1024) void k_attn_mrg(const AttnArgs a, const StepRec *st) {
+  constexpr int NGS = 4, QPB = 256 / HD;
+  __shared__ float sO[ATT_GMAX][256];
+  __shared__ float sM[ATT_GMAX][QPB], sL[ATT_GMAX][QPB];
+  __shared__ __align__(16) float sout[256];
+  const int t = threadIdx.x, v = t & 255, gs = t >> 8, b = blockIdx.y;
+  const int qd = a.n_heads * HD, e = min(blockIdx.x * 256 + v, qd - 1);
+  const int head = e / HD, d = e % HD, g = a.n_heads / a.n_kv, h = head / g, qi = b * g + head % g;
+  const float2 *pml = reinterpret_cast<const float2 *>(a.part_ml) + (int64_t)h * a.nslot * ATT_QMAX + qi;
+  const float *po = a.part_o + ((int64_t)h * a.nslot * ATT_QMAX + qi) * HD + d;
+  // the slots of groups gs and gs + 4 are requested before the step record arrives (slots past
+  // the pass's chunks hold earlier values, never used)
+  float2 ml0[ATT_GRP], ml1[ATT_GRP];
+  float ov0[ATT_GRP], ov1[ATT_GRP];
+#pragma unroll
+  for (int k = 0; k < ATT_GRP; k++) {
+    const int c = min(gs * ATT_GRP + k, a.nslot - 1), c1 = min((gs + NGS) * ATT_GRP + k, a.nslot - 1);
+    ml0[k] = pml[(int64_t)c * ATT_QMAX];
+    ov0[k] = po[(int64_t)c * ATT_QMAX * HD];
+    ml1[k] = pml[(int64_t)c1 * ATT_QMAX];
+    ov1[k] = po[(int64_t)c1 * ATT_QMAX * HD];
+  }
+  const int total = st->start + st->m, nch = (total + 63) >> 6, ngrp = (nch + ATT_GRP - 1) / ATT_GRP;
+  for (int gi = gs; gi < ngrp; gi += NGS) {
+    const int s0 = gi * ATT_GRP, n = min(ATT_GRP, nch - s0);
+    float2 ml[ATT_GRP];
+    float ov[ATT_GRP];
+#pragma unroll
+    for (int k = 0; k < ATT_GRP; k++) {
+      if (gi == gs) {
+        ml[k] = k < n ? ml0[k] : make_float2(-INFINITY, 0.0f);
+        ov[k] = ov0[k];
+      } else if (gi == gs + NGS) {
+        ml[k] = k < n ? ml1[k] : make_float2(-INFINITY, 0.0f);
+        ov[k] = ov1[k];
+      } else {
+        const int c = s0 + min(k, n - 1);
+        ml[k] = k < n ? pml[(int64_t)c * ATT_QMAX] : make_float2(-INFINITY, 0.0f);
+        ov[k] = po[(int64_t)c * ATT_QMAX * HD];
+      }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < ATT_GRP; k++) M = fmaxf(M, ml[k].x);
+    float L = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < ATT_GRP; k++) {
+      if (k < n) {
+        const float w = ml[k].x == -INFINITY ? 0.0f : expf(ml[k].x - M);
+        L = fmaf(ml[k].y, w, L);
+        acc = fmaf(ov[k], w, acc);
+      }
+    }
+    sO[gi][v] = acc;
+    if (d == 0) { sM[gi][v / HD] = M; sL[gi][v / HD] = L; }
+  }
+  __syncthreads();
+  if (gs == 0) {
+    const int hq = v / HD;
+    float out;
+    if (ngrp == 1) {
+      out = sO[0][v] * __fdiv_rn(1.0f, fmaxf(sL[0][hq], 1e-30f));
+    } else {
+      float M = -INFINITY;
+      for (int k = 0; k < ngrp; k++) M = fmaxf(M, sM[k][hq]);
+      float L = 0.0f, acc = 0.0f;
+      for (int k = 0; k < ngrp; k++) {
+        const float w = sM[k][hq] == -INFINITY ? 0.0f : expf(sM[k][hq] - M);
+        L = fmaf(sL[k][hq], w, L);
+        acc = fmaf(sO[k][v], w, acc);
+      }
+      out = acc * __fdiv_rn(1.0f, fmaxf(L, 1e-30f));
+    }
+    if (blockIdx.x * 256 + v < qd) a.att[(int64_t)b * qd + blockIdx.x * 256 + v] = out;
+    sout[v] = out;
+  }
+  if (!a.aq.q) return;
+  __syncthreads();
+  if (t < 64) {  // the block's Q8_K (a.aq is set only when the att row is whole 256-blocks)
+    const float4 xv = reinterpret_cast<const float4 *>(sout)[t];
+    const float am = q8k_amax(xv);
+    const int64_t vb = (int64_t)b * (qd / 256) + blockIdx.x;
+    q8k_block_store(xv, am, a.aq.q + vb * 64, a.aq.d + vb, reinterpret_cast<int *>(a.aq.bs + vb * 8));
+  }
 }
 
 // Row preparation of a prefill pass: one wavefront per (row b, head j); heads 0 .. n_heads-1
@@ -1754,6 +2139,23 @@ static void launch_attn_pf_t(const AttnArgs &a, int m, const StepRec *st, hipStr
   SPX_LDS((k_attn_pf<HD>), sm);
   hipLaunchKernelGGL((k_attn_pf<HD>), dim3(a.nch, a.n_kv, (nq + 63) / 64), dim3(256), sm, s, a, st);
   hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, (nq + 15) / 16, (a.nch + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
+}
+
+template <int HD>
+static void launch_attn_mt_t(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
+  const int nqt = (m * (a.n_heads / a.n_kv) + 15) / 16;
+  const size_t sm = MtLds<HD>::bytes(a.n_heads / a.n_kv, a.q_bias != nullptr);
+  SPX_LDS((k_attn_mt<HD>), sm);
+  hipLaunchKernelGGL((k_attn_mt<HD>), dim3(a.nch, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
+  hipLaunchKernelGGL((k_attn_mrg<HD>), dim3((a.n_heads * HD + 255) / 256, m), dim3(1024), 0, s, a, st);
+}
+
+hipError_t launch_attention_mt(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
+  if (a.prepped || m < 1 || m > MAX_M || a.n_heads % a.n_kv || (a.aq.q && (a.n_heads * a.hd) % 256)) return hipErrorInvalidValue;
+  if (a.hd == 128) launch_attn_mt_t<128>(a, m, st, s);
+  else if (a.hd == 64) launch_attn_mt_t<64>(a, m, st, s);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_attention_pf(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {

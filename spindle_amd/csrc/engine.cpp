@@ -104,7 +104,7 @@ struct spx_engine {
   float *xA = nullptr, *xB = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *proj = nullptr, *ffn = nullptr;
   float *xn2 = nullptr, *h = nullptr, *rlog = nullptr, *logits = nullptr, *xn = nullptr, *part_ml = nullptr, *part_o = nullptr;
   Q8KP aq{}, xq2{}, hq{}, xq{};
-  int *amax = nullptr, *att_cnt = nullptr, *rt_cnt = nullptr, *gu_cnt = nullptr, *tail_cnt = nullptr;
+  int *amax = nullptr, *att_cnt = nullptr, *rt_cnt = nullptr, *gu_cnt = nullptr, *tail_cnt = nullptr, *dn_cnt = nullptr;
   unsigned long long *best = nullptr;
   int *hist = nullptr;  // token history of back-to-back decode passes [max_seq]
   int *chosen = nullptr, *nkeep = nullptr, *expert_count = nullptr;
@@ -346,13 +346,22 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
         SPX_HIP(launch_router(ra, m, E->st_dev, s));
       }
       const int max_gu_jobs = std::min(256, m * nu);  // jobs of at most GU_USERS users
+      // Q8_0 experts, 4..16 rows: gate/up and down on the fp32 matrix cores, a job per expert
+      const bool fq = E->mq && m >= FQ_MIN_ROWS && m <= MAX_M && ly.gate->v.dtype == T_Q8_0 && ly.up->v.dtype == T_Q8_0 &&
+                      ly.down->v.dtype == T_Q8_0;
+      const int max_dn_jobs = std::min(ne, m * nu);
       {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up), l, true);  // one expert's slabs
         GUArgs ga{};
         ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.x = E->xn2;
         ga.jobs = E->jobs; ga.njobs = ly.njobs + 1; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
         if (d_int) ga.hq = E->hq;
-        SPX_HIP(launch_gateup(ga, std::min(m, GU_USERS), mode_of(E, ly.gate, m), E->st_dev, max_gu_jobs, s));
+        if (fq) {
+          ga.jobs = E->jobs + 256; ga.njobs = ly.njobs; ga.vdiv = nu; ga.fq = 1;
+          SPX_HIP(launch_gateup(ga, m, 0, E->st_dev, max_dn_jobs, s));
+        } else {
+          SPX_HIP(launch_gateup(ga, std::min(m, GU_USERS), mode_of(E, ly.gate, m), E->st_dev, max_gu_jobs, s));
+        }
       }
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
@@ -360,7 +369,12 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
         da.w = ly.down->v; da.y = E->hq; da.x = E->h; da.jobs = E->jobs + 256; da.njobs = ly.njobs; da.weights = E->weights;
         da.nkeep = E->nkeep; da.n_used = nu; da.out = E->ffn;
         if (tails) da.tail = tn;
-        SPX_HIP(launch_down(da, m, m > 2 && d_int && E->down_mode == 1 ? 1 : 0, E->st_dev, s));
+        if (fq) {
+          da.yd = E->yd; da.counter = E->dn_cnt;
+          SPX_HIP(launch_down_fq(da, max_dn_jobs, E->st_dev, s));
+        } else {
+          SPX_HIP(launch_down(da, m, m > 2 && d_int && E->down_mode == 1 ? 1 : 0, E->st_dev, s));
+        }
       }
       if (!tails) { ProfScope ps(E, PC_NORM, 0); SPX_HIP(launch_norm(tn, E->st_dev, m, s)); }
     } else {  // ffn_forward / ffn_forward_multi (:590-646): k = 1, w = 1
@@ -910,7 +924,7 @@ int spx_engine_prepare(spx_engine *E) {
             (E->h = E->dalloc<float>((size_t)nv * nff)) && (E->yd = E->dalloc<float>((size_t)nv * c.dim)) && (E->rlog = E->dalloc<float>((size_t)M * std::max(1, c.n_expert))) &&
             (E->logits = E->dalloc<float>((size_t)M * c.vocab)) && (E->amax = E->dalloc<int>(M)) &&
             (E->best = E->dalloc<unsigned long long>((size_t)M * std::max<int64_t>(E->lm_grid, c.vocab / 4 + 1))) &&
-            (E->tail_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) && (E->hist = E->dalloc<int>((size_t)c.max_seq)) &&
+            (E->tail_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) && (E->dn_cnt = E->dalloc<int>((size_t)(2 + c.dim / 32) * CNT_STRIDE)) && (E->hist = E->dalloc<int>((size_t)c.max_seq)) &&
             (E->part_ml = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * 2)) &&
             (E->part_o = E->dalloc<float>((size_t)c.n_kv_heads * (E->nch + ATT_GMAX) * ATT_QMAX * c.head_dim)) &&
             (E->att_cnt = E->dalloc<int>((size_t)c.n_kv_heads * ATT_QT * (1 + ATT_GMAX) * CNT_STRIDE)) && (E->rt_cnt = E->dalloc<int>((size_t)(1 + CNT_SUB) * CNT_STRIDE)) &&

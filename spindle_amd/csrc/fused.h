@@ -130,7 +130,8 @@ struct GUArgs {
   int *counter;                       // [vectors][n_ff/256][1 + GU_SUB][CNT_STRIDE], zero between passes
   int n_ff;
   int G;                              // row-parallel launch: lane groups per row
-  int fq;                             // dense Q8_0, 4..16 rows: on the fp32 matrix cores (k_gateup_fq)
+  int fq;                             // Q8_0, 4..16 rows: on the fp32 matrix cores (k_gateup_fq)
+  int vdiv;                           // > 1: a job's vec entries are h indices (row * vdiv + slot), the input row their quotient
 };
 
 struct DownArgs {
@@ -145,6 +146,8 @@ struct DownArgs {
   float *out;                         // [m][dim]
   int G;                              // row-parallel launch: lane groups per row
   NormTail tail;
+  float *yd;                          // launch_down_fq: y per (row, slot) [m * n_used][dim]
+  int *counter;                       // launch_down_fq: arrivals per 32 output rows [dim / 32][CNT_STRIDE] (+ one), zero between passes
 };
 
 hipError_t launch_embed(const TensorView &e, const StepRec *st, float escale, const NormTail &t, int m, hipStream_t s);
@@ -165,6 +168,10 @@ hipError_t launch_attention_mt(const AttnArgs &a, int m, const StepRec *st, hipS
 hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStream_t s);
 hipError_t launch_gateup(const GUArgs &a, int mt, int mode, const StepRec *st, int max_jobs, hipStream_t s);
 hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, hipStream_t s);
+// Routed experts' down projection of 4..16 rows, Q8_0 weights, on the fp32 matrix cores: a
+// workgroup per (32 output rows, down job), then per 32 rows the combine in choice order, then
+// the norm tail (a.tail.nw set) in the last of them
+hipError_t launch_down_fq(const DownArgs &a, int max_jobs, const StepRec *st, hipStream_t s);
 hipError_t launch_norm(const NormTail &t, const StepRec *st, int m, hipStream_t s);
 // hist non-null (m == 1): the pick advances the step record (next token and position) and is
 // appended to hist[step]

@@ -1837,8 +1837,9 @@ __global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec 
   if (a.hq.q) gateup_quant_tail(a, J.nvec, J.jo, 16);
 }
 
-// Dense gate / up + SwiGLU of 4..16 rows on the fp32 matrix cores (Q8_0): 16 rows of h per
-// workgroup of sixteen wavefronts: wavefront w takes part w >> 1 (fq_part) of the gate tile
+// Gate / up + SwiGLU of 4..16 rows on the fp32 matrix cores (Q8_0), dense or one routed expert's
+// users a job (vdiv: the down jobs, whose entries are h indices): 16 rows of h per workgroup of
+// sixteen wavefronts: wavefront w takes part w >> 1 (fq_part) of the gate tile
 // (w even) or the up tile (w odd); the parts meet in LDS (summed in part order) and
 // h = silu(g) * u as k_gateup_f writes it.
 __global__ __launch_bounds__(1024) void k_gateup_fq(const GUArgs a, const StepRec *st) {
@@ -1850,7 +1851,7 @@ __global__ __launch_bounds__(1024) void k_gateup_fq(const GUArgs a, const StepRe
   const int nb = (int)w.nb, n_ff = a.n_ff;
   const int64_t r0 = (int64_t)blockIdx.x * 16, grow = (int64_t)J.expert * w.rows + min(r0 + j, (int64_t)n_ff - 1);
   const bool vin = j < J.nvec;
-  const int xv = vin ? (J.jv ? J.jv[j] : j) : 0;
+  const int xv = vin ? (J.jv ? (a.vdiv > 1 ? J.jv[j] / a.vdiv : J.jv[j]) : j) : 0;
   float r[4];
   fq_part(w.pl.p0 + grow * nb * 32 + 8 * kq, reinterpret_cast<const uint16_t *>(w.pl.p3) + grow * nb, a.x + (int64_t)xv * w.cols + 8 * kq,
           vin, nb, kp, r);
@@ -2009,6 +2010,64 @@ __global__ __launch_bounds__(256) void k_down_f(const DownArgs a, const StepRec 
   __syncthreads();
   down_combine(a, m, yb, r, dim, coh);
   if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
+}
+
+// Routed experts' down projection of 4..16 rows on the fp32 matrix cores (Q8_0): workgroup
+// (32 output rows, down job) of sixteen wavefronts as k_mv_fq's (tile w & 1, part w >> 1, the
+// parts summed in part order), the job's users' h rows as the vectors; y of (user, row) goes to
+// yd through the L2. The last of a row block's job workgroups combines its 32 rows for every
+// pass row in choice order (down_combine's arithmetic), and the last row block runs the norm
+// tail.
+__global__ __launch_bounds__(1024) void k_down_fq(const DownArgs a, const StepRec *st) {
+  const int m = st->m, nj = *a.njobs;
+  if ((int)blockIdx.y >= nj) return;
+  const Job &J = a.jobs[blockIdx.y];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15, kq = lane >> 4;
+  const int tile = wave & 1, kp = wave >> 1;
+  __shared__ float part[FQ_KP][2][4][64];
+  const int dim = (int)a.w.rows, nb = (int)a.w.nb, n_ff = (int)a.w.cols;
+  const bool coh = a.tail.nw != nullptr;
+  const int nvec = J.nvec;
+  const bool vin = j < nvec;
+  const int xv = vin ? J.vec[j] : 0;
+  const int64_t r0 = (int64_t)blockIdx.x * 32 + tile * 16;
+  float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (r0 < dim) {
+    const int64_t grow = (int64_t)J.expert * dim + min(r0 + j, (int64_t)dim - 1);
+    fq_part(a.w.pl.p0 + grow * nb * 32 + 8 * kq, reinterpret_cast<const uint16_t *>(a.w.pl.p3) + grow * nb, a.x + (int64_t)xv * n_ff + 8 * kq,
+            vin, nb, kp, r);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; q++) part[kp][tile][q][lane] = r[q];
+  __syncthreads();
+  const rsrc_t ry = rsrc_of(a.yd);
+  if (kp == 0 && r0 < dim) {
+    const int64_t row = r0 + j;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int v = 4 * kq + q;
+      float res = part[0][tile][q][lane];
+#pragma unroll
+      for (int p2 = 1; p2 < FQ_KP; p2++) res = res + part[p2][tile][q][lane];
+      if (v < nvec && row < dim) st_coh1(ry, (int)(((int64_t)J.out[v] * dim + row) * 4), res);
+    }
+  }
+  int *tc = a.counter + (int64_t)(1 + blockIdx.x) * CNT_STRIDE;
+  if (arrive(tc) != nj - 1) return;
+  if (threadIdx.x == 0) *tc = 0;
+  for (int i = threadIdx.x; i < m * 32; i += 1024) {
+    const int b = i >> 5, row = blockIdx.x * 32 + (i & 31);
+    if (row < dim) {
+      const int nk = a.nkeep[b];
+      float acc = 0.0f;
+      for (int s2 = 0; s2 < nk; s2++) acc = acc + a.weights[b * 32 + s2] * ld_coh1(ry, (int)(((int64_t)(b * a.n_used + s2) * dim + row) * 4));
+      out_store(a.out + (int64_t)b * dim + row, acc, coh);
+    }
+  }
+  if (!coh) return;
+  if (arrive(a.counter) != (int)gridDim.x - 1) return;
+  if (threadIdx.x == 0) *a.counter = 0;
+  norm_rows<16>(a.tail, 0, m);
 }
 
 // ------------------------------------------------------------------ final greedy pick
@@ -2276,6 +2335,12 @@ hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, h
   case T_Q5K: return launch_down_dt<T_Q5K>(a, mt, mode, st, s);
   default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_down_fq(const DownArgs &a, int max_jobs, const StepRec *st, hipStream_t s) {
+  if (a.w.dtype != T_Q8_0 || !a.yd || !a.counter || max_jobs < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_down_fq, dim3((unsigned)((a.w.rows + 31) / 32), (unsigned)max_jobs), dim3(1024), 0, s, a, st);
+  return hipGetLastError();
 }
 
 hipError_t launch_embed(const TensorView &e, const StepRec *st, float escale, const NormTail &t, int m, hipStream_t s) {

@@ -1407,17 +1407,15 @@ __global__ __launch_bounds__(1024) void k_attn_mrg(const AttnArgs a, const StepR
   const int head = e / HD, d = e % HD, g = a.n_heads / a.n_kv, h = head / g, qi = b * g + head % g;
   const float2 *pml = reinterpret_cast<const float2 *>(a.part_ml) + (int64_t)h * a.nslot * ATT_QMAX + qi;
   const float *po = a.part_o + ((int64_t)h * a.nslot * ATT_QMAX + qi) * HD + d;
-  // the slots of groups gs and gs + 4 are requested before the step record arrives (slots past
-  // the pass's chunks hold earlier values, never used)
-  float2 ml0[ATT_GRP], ml1[ATT_GRP];
-  float ov0[ATT_GRP], ov1[ATT_GRP];
+  // group gs's slots are requested before the step record arrives (slots past the pass's
+  // chunks hold earlier values, never used)
+  float2 ml0[ATT_GRP];
+  float ov0[ATT_GRP];
 #pragma unroll
   for (int k = 0; k < ATT_GRP; k++) {
-    const int c = min(gs * ATT_GRP + k, a.nslot - 1), c1 = min((gs + NGS) * ATT_GRP + k, a.nslot - 1);
+    const int c = min(gs * ATT_GRP + k, a.nslot - 1);
     ml0[k] = pml[(int64_t)c * ATT_QMAX];
     ov0[k] = po[(int64_t)c * ATT_QMAX * HD];
-    ml1[k] = pml[(int64_t)c1 * ATT_QMAX];
-    ov1[k] = po[(int64_t)c1 * ATT_QMAX * HD];
   }
   const int total = st->start + st->m, nch = (total + 63) >> 6, ngrp = (nch + ATT_GRP - 1) / ATT_GRP;
   for (int gi = gs; gi < ngrp; gi += NGS) {
@@ -1429,9 +1427,6 @@ __global__ __launch_bounds__(1024) void k_attn_mrg(const AttnArgs a, const StepR
       if (gi == gs) {
         ml[k] = k < n ? ml0[k] : make_float2(-INFINITY, 0.0f);
         ov[k] = ov0[k];
-      } else if (gi == gs + NGS) {
-        ml[k] = k < n ? ml1[k] : make_float2(-INFINITY, 0.0f);
-        ov[k] = ov1[k];
       } else {
         const int c = s0 + min(k, n - 1);
         ml[k] = k < n ? pml[(int64_t)c * ATT_QMAX] : make_float2(-INFINITY, 0.0f);

@@ -197,8 +197,9 @@ def test_teacher_forced_decode(ctx, key):
 
 @pytest.mark.parametrize("key", list(RUNS))
 def test_verify_pass_at_context(ctx, key):
-    """M=9 at the config's context: lane-exact == nine one-row passes bitwise; the int8
-    matrix-core pass (K-quant models) within 1e-2 of it, picks equal except near-ties."""
+    """M=9 at the config's context: lane-exact == nine one-row passes bitwise; the matrix-core
+    pass (int8 for K-quant models, fp32 for Q8_0 ones) within the bars below of it, picks equal
+    except near-ties."""
     S = setup(ctx, key)
     cfg, eng = S.cfg, S.eng
     pos = S.n0 + 64  # past the teacher-forced rows, inside the config's context
@@ -216,8 +217,10 @@ def test_verify_pass_at_context(ctx, key):
     print(f"[{key}] M=9 at position {pos}: lane-exact == one-row bitwise; matrix cores vs lane-exact logits err {e:.1e}")
     # the int8 matrix-core pass rounds its fp32 block sums once per block instead of per lane;
     # on the 48-layer K-quant model that last-bit change carries as far as the norm-order change
-    # does in the oracle (test_teacher_forced_decode): the same <= 5e-2 bar
-    assert e <= 5e-2
+    # does in the oracle (test_teacher_forced_decode): the same <= 5e-2 bar. Float models (Q8_0
+    # on the fp32 matrix cores: the same products summed in another fixed order) keep the
+    # logits bar, 1e-3.
+    assert e <= (5e-2 if _integer(cfg) else 1e-3)
     for r in np.nonzero(am_q != am9)[0]:
         assert _margin(l9[r] / cfg.logit_scale) < max(1e-4, 2 * e * float(np.max(np.abs(l9[r])))), (key, r)
     eng.set_mfma(True)

@@ -71,7 +71,8 @@ struct spx_engine {
                            // and the per-lane dot kernel is faster
   bool mq_gateup = true;   // the gate/up projections (SPX_MQ_GATEUP)
   int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;
-  bool pf_attn = true;      // prefill passes: attention on k_attn_pf + its merge launch (SPX_PF_ATTN)
+  int pf_attn = 2;          // prefill passes: 2 the multi-tile kernels (at least 2 query heads a kv head), 1 k_rows_prep +
+                            // k_attn_pf + merge, 0 k_rows_prep + k_attn (SPX_PF_ATTN)
   int pf_min_rows = MAX_M + 1;  // passes of this many rows or more prepare their attention rows once (SPX_PF_MIN)
   bool att_merge = false;  // one-row passes: attention chunks merged inside the attention launch (SPX_ATT_MERGE)
   int att_mt_min = 2;      // unprepared passes of this many rows (up to 16) take the multi-tile attention (SPX_ATT_MT; 0: never)  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
@@ -602,7 +603,9 @@ int enqueue_pass_m(spx_engine *E, int m) {
       aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
       aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
       aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
-      if (m >= E->pf_min_rows) {  // rows prepared once (for 2..16 rows the fused kernel is faster: M = 9 4.46 vs 4.69 ms a pass)
+      if (m >= E->pf_min_rows && E->pf_attn == 2 && m > MAX_M && c.n_heads / c.n_kv_heads >= 2) {
+        SPX_HIP(launch_attention_mt(aa, m, E->st_dev, s));
+      } else if (m >= E->pf_min_rows) {  // rows prepared once (for 2..16 rows the fused kernel is faster: M = 9 4.46 vs 4.69 ms a pass)
         SPX_HIP(launch_rows_prep(aa, E->qp, m, E->st_dev, s));
         aa.q = E->qp;
         aa.prepped = 1;
@@ -801,7 +804,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   if (const char *v = std::getenv("SPX_TAIL_MAX")) E->tail_max = std::max(0, std::min(MAX_M, atoi(v)));
   if (const char *v = std::getenv("SPX_DOWN_MODE")) E->down_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_ATT_MERGE")) E->att_merge = atoi(v) != 0;
-  if (const char *v = std::getenv("SPX_PF_ATTN")) E->pf_attn = atoi(v) != 0;
+  if (const char *v = std::getenv("SPX_PF_ATTN")) E->pf_attn = std::max(0, std::min(2, atoi(v)));
   if (const char *v = std::getenv("SPX_ATT_MT")) E->att_mt_min = std::max(0, std::min(MAX_M + 1, atoi(v)));
   if (const char *v = std::getenv("SPX_PF_MIN")) E->pf_min_rows = std::max(2, std::min(MAX_M + 1, atoi(v)));
   *out = E;

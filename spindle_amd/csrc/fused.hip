@@ -1122,14 +1122,19 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(const AttnArgs a, const S
 template <int HD>
 struct MtLds {
   static constexpr int KS = HD + 8, VS = 64 + 8;
-  // K [64][KS], V^T [HD][VS] (f16); rotations of the pass's rows [MAX_M][HD/2] (float2), the
-  // query norm weights [HD]; then, with a query bias, the kv group's biases [g][HD]
-  static constexpr size_t OFF_ROT = (size_t)64 * KS * 2 + (size_t)HD * VS * 2, OFF_QN = OFF_ROT + (size_t)MAX_M * HD * 4,
-                          OFF_QB = OFF_QN + (size_t)HD * 4;
-  static size_t bytes(int g, bool bias) { return OFF_QB + (bias ? (size_t)g * HD * 4 : 0); }
+  // K [64][KS], V^T [HD][VS] (f16); the query norm weights [HD]; with a query bias the kv
+  // group's biases [g][HD]; the rotations of the pass rows the workgroup's queries belong to
+  // [rows][HD/2] (float2) at off_rot
+  static constexpr size_t OFF_QN = (size_t)64 * KS * 2 + (size_t)HD * VS * 2, OFF_QB = OFF_QN + (size_t)HD * 4;
+  __host__ __device__ static size_t off_rot(int g, bool bias) { return OFF_QB + (bias ? (size_t)g * HD * 4 : 0); }
+  // pass rows the 128 queries of a workgroup span (g queries a row)
+  __host__ __device__ static int rot_rows(int g, int m) { return min(m, (128 + g - 1) / g + 1); }
+  static size_t bytes(int g, bool bias, int m) { return off_rot(g, bias) + (size_t)rot_rows(g, m) * HD * 4; }
 };
 
-template <int HD>
+// BIG: prefill passes (up to 128 rows, a workgroup per 128 queries of a (chunk, kv head)); the
+// pass's new K / V rows in the chunk (up to 64) are prepared from memory in a loop
+template <int HD, bool BIG>
 __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec *st) {
   using LY = MtLds<HD>;
   constexpr int KS = LY::KS, VS = LY::VS;
@@ -1139,11 +1144,11 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
   extern __shared__ __align__(16) uint8_t smem[];
   _Float16 *ks = reinterpret_cast<_Float16 *>(smem);  // [64][KS]
   _Float16 *vt = ks + 64 * KS;                        // [HD][VS] (V transposed)
-  float *rot_s = reinterpret_cast<float *>(smem + LY::OFF_ROT), *qn_s = reinterpret_cast<float *>(smem + LY::OFF_QN);
-  float *qb_s = reinterpret_cast<float *>(smem + LY::OFF_QB);
   const int h = blockIdx.y, c = blockIdx.x;
   const int m = st->m, start = st->start, total = start + m;
   const int g = a.n_heads / a.n_kv, NQ = m * g;
+  float *qn_s = reinterpret_cast<float *>(smem + LY::OFF_QN), *qb_s = reinterpret_cast<float *>(smem + LY::OFF_QB);
+  float *rot_s = reinterpret_cast<float *>(smem + LY::off_rot(g, a.q_bias != nullptr));
   if (blockIdx.z * 128 >= NQ || c >= (total + 63) / 64) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ar = lane & 15, kq = lane >> 4, kg = 4 * kq;
@@ -1156,9 +1161,13 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
   // every wavefront shares (rotations of the pass's rows, norm weights, biases) for LDS, then
   // this lane's raw query values
   const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  float4 sh_rot = z4, sh_qn = z4, sh_qb = z4;
-  const bool ld_rot = tid < m * (half / 2), ld_qn = a.q_norm && tid < HD / 4, ld_qb = a.q_bias && tid < g * HD / 4;
-  if (ld_rot) sh_rot = reinterpret_cast<const float4 *>(a.rope + (int64_t)start * half)[tid];
+  constexpr int RPT = BIG ? 5 : 1;  // rotation float4s a thread stages (rows <= 65 at g >= 2 for BIG)
+  const int rb0 = blockIdx.z * 128 / g, nrot = min(m - rb0, LY::rot_rows(g, m)), nrv = nrot * (half / 2);
+  float4 sh_rot[RPT], sh_qn = z4, sh_qb = z4;
+  const bool ld_qn = a.q_norm && tid < HD / 4, ld_qb = a.q_bias && tid < g * HD / 4;
+#pragma unroll
+  for (int i = 0; i < RPT; i++)
+    sh_rot[i] = reinterpret_cast<const float4 *>(a.rope + (int64_t)(start + rb0) * half)[min(tid + 512 * i, nrv - 1)];  // (valid index)
   if (ld_qn) sh_qn = reinterpret_cast<const float4 *>(a.q_norm)[tid];
   if (ld_qb) sh_qb = reinterpret_cast<const float4 *>(a.q_bias + (int64_t)h * g * HD)[tid];
   float4 xq[DT];
@@ -1168,13 +1177,14 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
 #pragma unroll
     for (int kt = 0; kt < DT; kt++) xq[kt] = *reinterpret_cast<const float4 *>(src + kt * 16);
   }
-  // (2) the pass's new K / V rows in this chunk: rows b = wave, wave + 8 (head_prep's layout)
+  // (2) the pass's new K / V rows in this chunk: rows b = wave, wave + 8 (head_prep's layout;
+  // BIG: prepared from memory below)
   const bool act = lane < half;
   const int da = a.neox ? lane : 2 * lane, db = a.neox ? lane + half : 2 * lane + 1;
   float nk0[2], nk1[2], nkb0[2], nkb1[2], nv0[2], nv1[2], nvb0[2], nvb1[2], nkc[2], nks[2], kn0 = 0.0f, kn1 = 0.0f;
   if (a.k_norm && act) { kn0 = a.k_norm[da]; kn1 = a.k_norm[db]; }
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
+  for (int j = 0; j < 2 && !BIG; j++) {
     const int b = wave + 8 * j, pos = start + b;
     nk0[j] = nk1[j] = nkb0[j] = nkb1[j] = nv0[j] = nv1[j] = nvb0[j] = nvb1[j] = 0.0f;
     nkc[j] = 1.0f;
@@ -1196,7 +1206,9 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
   attn_kv_load<NU>(a, cache0 + (int64_t)min(p_lo + lp, p_hi - 1) * a.kv_dim + lq * DQ, kr, vr);
 
   // the shared values to LDS (waits for them only)
-  if (ld_rot) reinterpret_cast<float4 *>(rot_s)[tid] = sh_rot;
+#pragma unroll
+  for (int i = 0; i < RPT; i++)
+    if (tid + 512 * i < nrv) reinterpret_cast<float4 *>(rot_s)[tid + 512 * i] = sh_rot[i];
   if (ld_qn) reinterpret_cast<float4 *>(qn_s)[tid] = sh_qn;
   if (ld_qb) reinterpret_cast<float4 *>(qb_s)[tid] = sh_qb;
   __syncthreads();
@@ -1252,7 +1264,7 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
     for (int kt = 0; kt < DT / 2; kt++) {
 #pragma unroll
       for (int s = 0; s < 4; s++) {
-        const float4 r4 = *reinterpret_cast<const float4 *>(rot_s + qb_row * HD + 2 * (kt * 16 + kg) + 4 * (s >> 1));
+        const float4 r4 = *reinterpret_cast<const float4 *>(rot_s + (qb_row - rb0) * HD + 2 * (kt * 16 + kg) + 4 * (s >> 1));
         const float cv = (s & 1) ? r4.z : r4.x, sn = (s & 1) ? r4.w : r4.y;
         const float x0 = x[kt][s], x1 = x[kt + DT / 2][s];
         x[kt][s] = x0 * cv - x1 * sn;
@@ -1262,7 +1274,7 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
   } else {
 #pragma unroll
     for (int kt = 0; kt < DT; kt++) {
-      const float4 r4 = *reinterpret_cast<const float4 *>(rot_s + qb_row * HD + 2 * (kt * 8 + 2 * kq));
+      const float4 r4 = *reinterpret_cast<const float4 *>(rot_s + (qb_row - rb0) * HD + 2 * (kt * 8 + 2 * kq));
 #pragma unroll
       for (int p = 0; p < 2; p++) {
         const float cv = p ? r4.z : r4.x, sv = p ? r4.w : r4.y;
@@ -1300,7 +1312,7 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
     }
   }
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
+  for (int j = 0; j < 2 && !BIG; j++) {
     const int b = wave + 8 * j, pos = start + b, pp = pos - p_lo;
     if (b < m && pos >= p_lo && pos < p_hi) {
       float e0, e1;
@@ -1313,6 +1325,27 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
         if (blockIdx.z == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
       }
       head_prep_pre(nv0[j], nv1[j], nvb0[j], nvb1[j], a.v_bias != nullptr, false, 0.0f, 0.0f, false, 1.0f, 0.0f, HD, a.eps, e0, e1);
+      if (act) {
+        const __half v0 = __float2half_rn(e0), v1 = __float2half_rn(e1);
+        vt[da * VS + pp] = (_Float16)__half2float(v0);
+        vt[db * VS + pp] = (_Float16)__half2float(v1);
+        if (blockIdx.z == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
+      }
+    }
+  }
+  if constexpr (BIG) {  // rows b in [p_lo - start, p_hi - start): wavefront w takes every eighth
+    for (int b = max(0, p_lo - start) + wave; b < min(m, p_hi - start); b += 8) {
+      const int pos = start + b, pp = pos - p_lo;
+      float e0, e1;
+      head_prep(a.k + (int64_t)b * a.kv_dim + h * HD, a.k_bias ? a.k_bias + h * HD : nullptr, a.k_norm, a.rope + (int64_t)pos * half, HD,
+                a.neox, a.eps, e0, e1);
+      if (act) {
+        const __half k0 = __float2half_rn(e0), k1 = __float2half_rn(e1);
+        ks[pp * KS + da] = (_Float16)__half2float(k0);
+        ks[pp * KS + db] = (_Float16)__half2float(k1);
+        if (blockIdx.z == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
+      }
+      head_prep(a.v + (int64_t)b * a.kv_dim + h * HD, a.v_bias ? a.v_bias + h * HD : nullptr, nullptr, nullptr, HD, a.neox, a.eps, e0, e1);
       if (act) {
         const __half v0 = __float2half_rn(e0), v1 = __float2half_rn(e1);
         vt[da * VS + pp] = (_Float16)__half2float(v0);
@@ -2212,15 +2245,24 @@ static void launch_attn_pf_t(const AttnArgs &a, int m, const StepRec *st, hipStr
 
 template <int HD>
 static void launch_attn_mt_t(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
-  const int nqt = (m * (a.n_heads / a.n_kv) + 15) / 16;
-  const size_t sm = MtLds<HD>::bytes(a.n_heads / a.n_kv, a.q_bias != nullptr);
-  SPX_LDS((k_attn_mt<HD>), sm);
-  hipLaunchKernelGGL((k_attn_mt<HD>), dim3(a.nch, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
-  hipLaunchKernelGGL((k_attn_mrg<HD>), dim3((a.n_heads * HD + 255) / 256, m), dim3(1024), 0, s, a, st);
+  const int g = a.n_heads / a.n_kv, nqt = (m * g + 15) / 16;
+  const size_t sm = MtLds<HD>::bytes(g, a.q_bias != nullptr, m);
+  if (m > MAX_M) {  // merged per (query tile, chunk group): k_attn_pf_merge (41 vs 24 us a layer at 128 rows)
+    SPX_LDS((k_attn_mt<HD, true>), sm);
+    hipLaunchKernelGGL((k_attn_mt<HD, true>), dim3(a.nch, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
+    hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, nqt, (a.nch + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
+  } else {
+    SPX_LDS((k_attn_mt<HD, false>), sm);
+    hipLaunchKernelGGL((k_attn_mt<HD, false>), dim3(a.nch, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
+    hipLaunchKernelGGL((k_attn_mrg<HD>), dim3((a.n_heads * HD + 255) / 256, m), dim3(1024), 0, s, a, st);
+  }
 }
 
 hipError_t launch_attention_mt(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
-  if (a.prepped || m < 1 || m > MAX_M || a.n_heads % a.n_kv || (a.aq.q && (a.n_heads * a.hd) % 256)) return hipErrorInvalidValue;
+  // (prefill passes: at least two queries a pass row, so a workgroup's rotations fit RPT = 5)
+  if (a.prepped || m < 1 || m > PMAX || a.n_heads % a.n_kv || (m > MAX_M && a.n_heads / a.n_kv < 2) ||
+      (m * (a.n_heads / a.n_kv) + 15) / 16 > ATT_QT || (a.aq.q && (a.n_heads * a.hd) % 256))
+    return hipErrorInvalidValue;
   if (a.hd == 128) launch_attn_mt_t<128>(a, m, st, s);
   else if (a.hd == 64) launch_attn_mt_t<64>(a, m, st, s);
   else return hipErrorInvalidValue;

@@ -4,7 +4,9 @@ tile-per-workgroup kernel with its in-kernel merges (SPX_ATT_MT=0). Per (chunk, 
 operations and their order are the same (the scores computed as K Q^T, the reductions as the
 same butterflies), so the bar is bitwise: hidden states, logits, picks and the KV cache of
 passes of 1..16 rows, on head_dim 64 and 128, NEOX and pairwise rotation, with and without
-QK-norm, one and two merge levels (contexts past 16 chunks)."""
+QK-norm, one and two merge levels (contexts past 16 chunks); and prefill passes of 17..128 rows
+(SPX_PF_ATTN=2: the same kernels, a workgroup per 128 queries of a (chunk, kv head)) against
+the prepared-rows prefill kernels (k_rows_prep + k_attn_pf)."""
 import os
 
 import numpy as np
@@ -35,16 +37,20 @@ def ctx():
     c.close()
 
 
-def _engine(ctx, cfg, w, mt):
-    old = os.environ.get("SPX_ATT_MT")
-    os.environ["SPX_ATT_MT"] = "1" if mt else "0"  # read when the engine is created
+def _engine(ctx, cfg, w, mt, pf=None):
+    env = {"SPX_ATT_MT": "1" if mt else "0"}  # read when the engine is created
+    if pf is not None:
+        env["SPX_PF_ATTN"] = str(pf)
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
     try:
         return M.Engine(ctx, cfg, w)
     finally:
-        if old is None:
-            del os.environ["SPX_ATT_MT"]
-        else:
-            os.environ["SPX_ATT_MT"] = old
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
 
 
 def _same(a, b):
@@ -109,5 +115,35 @@ def test_multi_tile_attention_lane_exact_verify(ctx):
         hs.append(h)
         ls.append(l)
     assert _same(h0, np.concatenate(hs)) and _same(l0, np.concatenate(ls))
+    a.close()
+    b.close()
+
+
+PF_CASES = ["a3b", "qwen3moe", "qwen3", "granite"]
+
+
+@pytest.mark.parametrize("case", PF_CASES)
+def test_multi_tile_prefill_bitwise(ctx, case):
+    """Prefill passes on the multi-tile kernels against the prepared-rows prefill kernels (the
+    K-quant pipelines) or 16-row passes (the fused path), bitwise, past 16 chunks."""
+    cfg = CASES[case].replace(max_seq=1280)
+    w = M.synth_model(cfg, seed=65)
+    a, b = _engine(ctx, cfg, w, True, pf=2), _engine(ctx, cfg, w, True, pf=1)
+    rng = np.random.default_rng(66)
+    ids = rng.integers(0, cfg.vocab, 1200)
+    pos = 0
+    for m in (128, 17, 40, 128, 100, 128, 33, 128, 64, 128, 128, 90, 128):
+        if pos + m > 1200:
+            break
+        print(f"{case}: prefill pass of {m} rows at {pos}", flush=True)
+        am0, h0, l0 = a.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        am1, h1, l1 = b.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        assert _same(h0, h1), (case, m, pos, "hidden")
+        assert _same(l0, l1), (case, m, pos, "logits")
+        assert np.array_equal(am0, am1), (case, m, pos)
+        pos += m
+    ka, va = a.kv_cache()
+    kb, vb = b.kv_cache()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
     a.close()
     b.close()

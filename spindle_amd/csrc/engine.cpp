@@ -347,7 +347,7 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
         SPX_HIP(launch_router(ra, m, E->st_dev, s));
       }
       const int max_gu_jobs = std::min(256, m * nu);  // jobs of at most GU_USERS users
-      // Q8_0 experts, 4..16 rows: gate/up and down on the fp32 matrix cores, a job per expert
+      // Q8_0 experts, 2..16 rows: gate/up and down on the fp32 matrix cores, a job per expert
       const bool fq = E->mq && m >= FQ_MIN_ROWS && m <= MAX_M && ly.gate->v.dtype == T_Q8_0 && ly.up->v.dtype == T_Q8_0 &&
                       ly.down->v.dtype == T_Q8_0;
       const int max_dn_jobs = std::min(ne, m * nu);

@@ -73,7 +73,7 @@ struct MVArgs {
   // (k_mv_fq) instead of the per-lane walk (the same products, summed in another order)
   int fq;
 };
-constexpr int FQ_MIN_ROWS = 4;  // below, a 16-vector tile idles most of its columns (measured slower)
+constexpr int FQ_MIN_ROWS = 2;  // one-row passes keep the per-lane walk (a 16-vector tile would idle 15 columns)
 
 struct AttnArgs {
   const float *q, *k, *v;             // raw projections [m][q_dim], [m][kv_dim]
@@ -130,7 +130,7 @@ struct GUArgs {
   int *counter;                       // [vectors][n_ff/256][1 + GU_SUB][CNT_STRIDE], zero between passes
   int n_ff;
   int G;                              // row-parallel launch: lane groups per row
-  int fq;                             // Q8_0, 4..16 rows: on the fp32 matrix cores (k_gateup_fq)
+  int fq;                             // Q8_0, 2..16 rows: on the fp32 matrix cores (k_gateup_fq)
   int vdiv;                           // > 1: a job's vec entries are h indices (row * vdiv + slot), the input row their quotient
 };
 
@@ -168,7 +168,7 @@ hipError_t launch_attention_mt(const AttnArgs &a, int m, const StepRec *st, hipS
 hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStream_t s);
 hipError_t launch_gateup(const GUArgs &a, int mt, int mode, const StepRec *st, int max_jobs, hipStream_t s);
 hipError_t launch_down(const DownArgs &a, int mt, int mode, const StepRec *st, hipStream_t s);
-// Routed experts' down projection of 4..16 rows, Q8_0 weights, on the fp32 matrix cores: a
+// Routed experts' down projection of 2..16 rows, Q8_0 weights, on the fp32 matrix cores: a
 // workgroup per (32 output rows, down job), then per 32 rows the combine in choice order, then
 // the norm tail (a.tail.nw set) in the last of them
 hipError_t launch_down_fq(const DownArgs &a, int max_jobs, const StepRec *st, hipStream_t s);

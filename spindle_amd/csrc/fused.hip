@@ -729,7 +729,7 @@ __device__ __forceinline__ void fq_part(const uint8_t *cp, const uint16_t *dp, c
   for (int q = 0; q < 4; q++) r[q] = (acc[0][q] + acc[1][q]) + (acc[2][q] + acc[3][q]);
 }
 
-// Float matvec of 4..16 vectors on the fp32 matrix cores (Q8_0 weights): TPW 16-row tiles per
+// Float matvec of 2..16 vectors on the fp32 matrix cores (Q8_0 weights): TPW 16-row tiles per
 // workgroup, eight wavefronts per tile (tasks stride over the grid as k_mv_f's): wavefront w
 // takes tile w / 8 and part w % 8 of its blocks (fq_part); the parts meet in LDS and are summed
 // in part order. Every product is the per-lane walk's; the sums run in a fixed order of their
@@ -1871,7 +1871,7 @@ __global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec 
   if (a.hq.q) gateup_quant_tail(a, J.nvec, J.jo, 16);
 }
 
-// Gate / up + SwiGLU of 4..16 rows on the fp32 matrix cores (Q8_0), dense or one routed expert's
+// Gate / up + SwiGLU of 2..16 rows on the fp32 matrix cores (Q8_0), dense or one routed expert's
 // users a job (vdiv: the down jobs, whose entries are h indices): 16 rows of h per workgroup of
 // sixteen wavefronts: wavefront w takes part w >> 1 (fq_part) of the gate tile
 // (w even) or the up tile (w odd); the parts meet in LDS (summed in part order) and
@@ -2046,7 +2046,7 @@ __global__ __launch_bounds__(256) void k_down_f(const DownArgs a, const StepRec 
   if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
 }
 
-// Routed experts' down projection of 4..16 rows on the fp32 matrix cores (Q8_0): workgroup
+// Routed experts' down projection of 2..16 rows on the fp32 matrix cores (Q8_0): workgroup
 // (32 output rows, down job) of sixteen wavefronts as k_mv_fq's (tile w & 1, part w >> 1, the
 // parts summed in part order), the job's users' h rows as the vectors; y of (user, row) goes to
 // yd through the L2. The last of a row block's job workgroups combines its 32 rows for every

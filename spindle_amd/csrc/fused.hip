@@ -1430,37 +1430,35 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
   if (kq == 0 && qact) st_coh2(r_ml, (c * ATT_QMAX + qi) * 8, f2v{mn, rl});
 }
 
-// The merge of k_attn_mt's partials: one workgroup per (256 values of an att row, row); four
-// slices of 256 threads (a value each) merge chunk groups gs, gs + 4, .. (kd_merge's and
-// attn_merge_q's operations: M = max, w = exp(m - M), L and O as fma chains in chunk order),
-// then slice 0 merges the groups in group order, writes the att row and, when a.aq is set, the
-// 256 values' Q8_K block (attn_tile_out's quantization).
+// The merge of k_attn_mt's partials: one workgroup per (256 values of an att row, row); eight
+// slices of 128 threads (two adjacent values each) merge chunk groups gs, gs + 8, .. (kd_merge's
+// and attn_merge_q's operations per value: M = max, w = exp(m - M), L and O as fma chains in
+// chunk order), then slice 0 merges the groups in group order, writes the att row and, when
+// a.aq is set, the 256 values' Q8_K block (attn_tile_out's quantization).
 template <int HD>
 __global__ __launch_bounds__(1024) void k_attn_mrg(const AttnArgs a, const StepRec *st) {
-  constexpr int NGS = 4, QPB = 256 / HD;
+  constexpr int NGS = 8, QPB = 256 / HD;
   __shared__ float sO[ATT_GMAX][256];
   __shared__ float sM[ATT_GMAX][QPB], sL[ATT_GMAX][QPB];
   __shared__ __align__(16) float sout[256];
-  const int t = threadIdx.x, v = t & 255, gs = t >> 8, b = blockIdx.y;
-  const int qd = a.n_heads * HD, e = min(blockIdx.x * 256 + v, qd - 1);
+  const int t = threadIdx.x, v = 2 * (t & 127), gs = t >> 7, b = blockIdx.y;
+  const int qd = a.n_heads * HD, e = min(blockIdx.x * 256 + v, qd - 2);
   const int head = e / HD, d = e % HD, g = a.n_heads / a.n_kv, h = head / g, qi = b * g + head % g;
   const float2 *pml = reinterpret_cast<const float2 *>(a.part_ml) + (int64_t)h * a.nslot * ATT_QMAX + qi;
-  const float *po = a.part_o + ((int64_t)h * a.nslot * ATT_QMAX + qi) * HD + d;
+  const float2 *po = reinterpret_cast<const float2 *>(a.part_o + ((int64_t)h * a.nslot * ATT_QMAX + qi) * HD + d);
   // group gs's slots are requested before the step record arrives (slots past the pass's
   // chunks hold earlier values, never used)
-  float2 ml0[ATT_GRP];
-  float ov0[ATT_GRP];
+  float2 ml0[ATT_GRP], ov0[ATT_GRP];
 #pragma unroll
   for (int k = 0; k < ATT_GRP; k++) {
     const int c = min(gs * ATT_GRP + k, a.nslot - 1);
     ml0[k] = pml[(int64_t)c * ATT_QMAX];
-    ov0[k] = po[(int64_t)c * ATT_QMAX * HD];
+    ov0[k] = po[(int64_t)c * ATT_QMAX * HD / 2];
   }
   const int total = st->start + st->m, nch = (total + 63) >> 6, ngrp = (nch + ATT_GRP - 1) / ATT_GRP;
   for (int gi = gs; gi < ngrp; gi += NGS) {
     const int s0 = gi * ATT_GRP, n = min(ATT_GRP, nch - s0);
-    float2 ml[ATT_GRP];
-    float ov[ATT_GRP];
+    float2 ml[ATT_GRP], ov[ATT_GRP];
 #pragma unroll
     for (int k = 0; k < ATT_GRP; k++) {
       if (gi == gs) {
@@ -1469,43 +1467,53 @@ __global__ __launch_bounds__(1024) void k_attn_mrg(const AttnArgs a, const StepR
       } else {
         const int c = s0 + min(k, n - 1);
         ml[k] = k < n ? pml[(int64_t)c * ATT_QMAX] : make_float2(-INFINITY, 0.0f);
-        ov[k] = po[(int64_t)c * ATT_QMAX * HD];
+        ov[k] = po[(int64_t)c * ATT_QMAX * HD / 2];
       }
     }
     float M = -INFINITY;
 #pragma unroll
     for (int k = 0; k < ATT_GRP; k++) M = fmaxf(M, ml[k].x);
-    float L = 0.0f, acc = 0.0f;
+    float L = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
     for (int k = 0; k < ATT_GRP; k++) {
       if (k < n) {
         const float w = ml[k].x == -INFINITY ? 0.0f : expf(ml[k].x - M);
         L = fmaf(ml[k].y, w, L);
-        acc = fmaf(ov[k], w, acc);
+        acc0 = fmaf(ov[k].x, w, acc0);
+        acc1 = fmaf(ov[k].y, w, acc1);
       }
     }
-    sO[gi][v] = acc;
+    sO[gi][v] = acc0;
+    sO[gi][v + 1] = acc1;
     if (d == 0) { sM[gi][v / HD] = M; sL[gi][v / HD] = L; }
   }
   __syncthreads();
   if (gs == 0) {
     const int hq = v / HD;
-    float out;
+    float out[2];
     if (ngrp == 1) {
-      out = sO[0][v] * __fdiv_rn(1.0f, fmaxf(sL[0][hq], 1e-30f));
+      const float il = __fdiv_rn(1.0f, fmaxf(sL[0][hq], 1e-30f));
+      out[0] = sO[0][v] * il;
+      out[1] = sO[0][v + 1] * il;
     } else {
       float M = -INFINITY;
       for (int k = 0; k < ngrp; k++) M = fmaxf(M, sM[k][hq]);
-      float L = 0.0f, acc = 0.0f;
+      float L = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
       for (int k = 0; k < ngrp; k++) {
         const float w = sM[k][hq] == -INFINITY ? 0.0f : expf(sM[k][hq] - M);
         L = fmaf(sL[k][hq], w, L);
-        acc = fmaf(sO[k][v], w, acc);
+        acc0 = fmaf(sO[k][v], w, acc0);
+        acc1 = fmaf(sO[k][v + 1], w, acc1);
       }
-      out = acc * __fdiv_rn(1.0f, fmaxf(L, 1e-30f));
+      const float il = __fdiv_rn(1.0f, fmaxf(L, 1e-30f));
+      out[0] = acc0 * il;
+      out[1] = acc1 * il;
     }
-    if (blockIdx.x * 256 + v < qd) a.att[(int64_t)b * qd + blockIdx.x * 256 + v] = out;
-    sout[v] = out;
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      if (blockIdx.x * 256 + v + u < qd) a.att[(int64_t)b * qd + blockIdx.x * 256 + v + u] = out[u];
+      sout[v + u] = out[u];
+    }
   }
   if (!a.aq.q) return;
   __syncthreads();

@@ -118,14 +118,17 @@ def cpu_baseline(cfg, w, eng, tok, pos, seconds, threads):
     return n / el, n, el
 
 
-def time_pass(eng, ids, pos, reps=10):
-    """Mean wall time (us) of one pass of len(ids) rows at pos (graph replay, synchronised)."""
+def time_pass(eng, ids, pos, reps=20):
+    """Median wall time (us) of one pass of len(ids) rows at pos (graph replay, ids in and picks
+    out, synchronised), over reps passes after three warm ones."""
     for _ in range(3):
         eng.forward(ids, pos)
-    t0 = time.perf_counter()
+    ts = []
     for _ in range(reps):
+        t0 = time.perf_counter()
         eng.forward(ids, pos)
-    return (time.perf_counter() - t0) / reps * 1e6
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)) * 1e6
 
 
 PREFILL_CHUNK = 128  # feed's prompt chunks (smollm_chat.rs:3090)

@@ -571,8 +571,9 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
   }
   __syncthreads();
 
-  // partials (coherent stores when merged in this kernel): O from the accumulators, (max, sum)
-  // per query
+  // partials, written through the L2 (sc1: the merge reads them in this launch or the next,
+  // and they need no write-back at the launch's end): O from the accumulators, (max, sum) per
+  // query
   const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nslot) * ATT_QMAX * 2);
   const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nslot) * ATT_QMAX * HD);
 #pragma unroll
@@ -580,14 +581,9 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int qi = qa + kg + r;
-      if (qi < NQ) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(acc[j][r]), r_o, ((c * ATT_QMAX + qi) * HD + (wave * TPW + j) * 16 + ar) * 4, 0, MERGE || COH ? 16 : 0);
+      if (qi < NQ) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(acc[j][r]), r_o, ((c * ATT_QMAX + qi) * HD + (wave * TPW + j) * 16 + ar) * 4, 0, 16);
     }
-  // (a one-row pass's partials are merged by the next kernel: plain stores, unless merged in
-  // the same launch)
-  if (tid < 16 && qa + tid < NQ) {
-    if (MERGE || COH) st_coh2(r_ml, (c * ATT_QMAX + qa + tid) * 8, f2v{rm[tid], rl[tid]});
-    else __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2v, f2v{rm[tid], rl[tid]}), r_ml, (c * ATT_QMAX + qa + tid) * 8, 0, 0);
-  }
+  if (tid < 16 && qa + tid < NQ) st_coh2(r_ml, (c * ATT_QMAX + qa + tid) * 8, f2v{rm[tid], rl[tid]});
   if (!MERGE) return;  // merged by a kernel of its own (one-row decode passes)
 
   // merges of this query tile: the last chunk of each group of ATT_GRP chunks merges the

@@ -2166,10 +2166,9 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
     bool fq = a.fq && a.m >= FQ_MIN_ROWS;
     for (int i = 0; i < a.nseg; i++) fq = fq && a.seg[i].w.dtype == T_Q8_0;
     if (fq) {
-      // up to 8192 rows (and no greedy keys, whose slots follow the grid): one tile a workgroup,
-      // twice the workgroups (Qwen3-0.6B M = 9: 2.82 -> 2.27 ms a pass)
-      if (!a.best && grid == mv_total(a) && grid < 256) hipLaunchKernelGGL(k_mv_fq<1>, dim3(2 * grid), dim3(512), 0, s, a, st);
-      else hipLaunchKernelGGL(k_mv_fq<2>, dim3(grid), dim3(1024), 0, s, a, st);
+      // one tile a workgroup (two tiles: Qwen3-0.6B M = 9 2.82 vs 2.26 ms a pass): twice the
+      // workgroups when the grid covers the tasks, else the same grid (greedy-key slots follow it)
+      hipLaunchKernelGGL(k_mv_fq<1>, dim3(!a.best && grid == mv_total(a) ? 2 * grid : grid), dim3(512), 0, s, a, st);
       return hipGetLastError();
     }
 #define SPX_MVF(MTV) hipLaunchKernelGGL(k_mv_f<MTV>, dim3(grid), dim3(256), 0, s, a, st)

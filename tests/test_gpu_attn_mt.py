@@ -147,3 +147,25 @@ def test_multi_tile_prefill_bitwise(ctx, case):
     assert np.array_equal(ka, kb) and np.array_equal(va, vb)
     a.close()
     b.close()
+
+
+def test_multi_tile_attention_nine_groups(ctx):
+    """Past 8192 positions (129+ chunks, nine chunk groups: the merge's slices take a second
+    group each): verify passes and prefill passes against the earlier kernels, bitwise."""
+    cfg = CASES["a3b"].replace(max_seq=8448)
+    w = M.synth_model(cfg, seed=67)
+    a, b = _engine(ctx, cfg, w, True, pf=2), _engine(ctx, cfg, w, False, pf=1)
+    rng = np.random.default_rng(68)
+    ids = rng.integers(0, cfg.vocab, 8300)
+    for s0 in range(0, 8192, 128):
+        a.forward(ids[s0:s0 + 128], s0)
+        b.forward(ids[s0:s0 + 128], s0)
+    pos = 8192
+    for m in (9, 16, 2, 1, 128):
+        print(f"pass of {m} rows at {pos}", flush=True)
+        am0, h0, l0 = a.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        am1, h1, l1 = b.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        assert _same(h0, h1) and _same(l0, l1) and np.array_equal(am0, am1), (m, pos)
+        pos += m
+    a.close()
+    b.close()

@@ -118,6 +118,42 @@ def cpu_baseline(cfg, w, eng, tok, pos, seconds, threads):
     return n / el, n, el
 
 
+# the reference's one-thread kernel bench shapes (bench_int_vs_float, src/quant_q8k.rs:450-455)
+BENCH_INT_SHAPES = (("Q4_K expert gate/up (2048 cols)", "Q4K", 2048, 768 * 16),
+                    ("Q6_K expert down (768 cols)", "Q6K", 768, 2048 * 16),
+                    ("Q4_K expert down (768 cols)", "Q4K", 768, 2048 * 16),
+                    ("Q6_K LM-head slice (2048 cols)", "Q6K", 2048, 16384))
+
+
+def cpu_microbench(seed, seconds=0.3):
+    """One thread: the C oracle's AVX2 integer rows kernel (the reference's rows<B, T> and its
+    Q8_K activations) on the reference's bench_int_vs_float shapes, 1 and 8 vectors: us per call
+    and GB/s of weight bytes, comparable with the reference's own single-thread figures."""
+    from oracle import ffi
+    from spindle_amd import model as M
+    ffi.set_threads(1)
+    rng = np.random.default_rng(seed)
+    res = []
+    for name, dt, cols, rows in BENCH_INT_SHAPES:
+        dtype = getattr(M, dt)
+        data = M.synth_tensor(M.TensorSpec(name, dtype, cols, rows), seed)
+        for b in (1, 8):
+            qs = [ffi.q8k_quantize(rng.uniform(-1.0, 1.0, cols).astype(np.float32)) for _ in range(b)]
+            outs = [np.empty(rows, np.float32) for _ in range(b)]
+            ffi.q8k_matmul_rows(data, dtype, cols, qs, rows, outs=outs)
+            n, t0 = 0, time.perf_counter()
+            while True:
+                ffi.q8k_matmul_rows(data, dtype, cols, qs, rows, outs=outs)
+                n += 1
+                el = time.perf_counter() - t0
+                if el >= seconds:
+                    break
+            us = el / n * 1e6
+            res.append({"shape": name, "rows": rows, "cols": cols, "vectors": b, "us": round(us, 1),
+                        "weight_gb_s": round(data.size / us / 1e3, 2)})
+    return res
+
+
 def time_pass(eng, ids, pos, reps=20):
     """Median wall time (us) of one pass of len(ids) rows at pos (graph replay, ids in and picks
     out, synchronised), over reps passes after three warm ones."""
@@ -238,6 +274,9 @@ def main():
                "sample": f"{n_cpu} greedy decode passes at positions {pos}..{pos + n_cpu - 1} from the KV state the GPU "
                          f"decode starts from (same weights, C restatement of the reference's AVX2 kernels, {threads} threads)",
                "cpu": ci}
+        cpu["microbench_1thread"] = cpu_microbench(args.seed)
+        for r in cpu["microbench_1thread"]:
+            log(f"cpu 1-thread {r['shape']}, {r['vectors']} vector(s): {r['us']:.0f} us, {r['weight_gb_s']:.2f} GB/s")
 
     # warmup, then the timed decode passes (back-to-back graph replays, picks fed forward on the device)
     tok_s, tok, pos = timed_decode(ctx, eng, tok, pos, args.warmup, args.steps)

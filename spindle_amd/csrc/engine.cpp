@@ -70,12 +70,12 @@ struct spx_engine {
                            // a pass of fewer rows gives an expert about one row, the MFMA's 16 columns idle
                            // and the per-lane dot kernel is faster
   bool mq_gateup = true;   // the gate/up projections (SPX_MQ_GATEUP)
-  int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;
+  int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   int pf_attn = 2;          // prefill passes: 2 the multi-tile kernels (at least 2 query heads a kv head), 1 k_rows_prep +
                             // k_attn_pf + merge, 0 k_rows_prep + k_attn (SPX_PF_ATTN)
   int pf_min_rows = MAX_M + 1;  // passes of this many rows or more prepare their attention rows once (SPX_PF_MIN)
   bool att_merge = false;  // one-row passes: attention chunks merged inside the attention launch (SPX_ATT_MERGE)
-  int att_mt_min = 2;      // unprepared passes of this many rows (up to 16) take the multi-tile attention (SPX_ATT_MT; 0: never)  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
+  int att_mt_min = 2;      // unprepared passes of this many rows (up to 16) take the multi-tile attention (SPX_ATT_MT; 0: never)
   std::map<std::string, spx_tensor *> mats;
   std::map<std::string, float *> vecs;
   std::map<std::string, int64_t> vec_len;

@@ -276,7 +276,8 @@ int mv_one(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld
 // Attention of a pass of m unprepared rows: the multi-tile kernels (launch_attention_mt) from
 // att_mt_min rows, else the tile-per-workgroup kernel; both give the same bits.
 hipError_t attn_launch(spx_engine *E, const AttnArgs &aa, int m, hipStream_t s) {
-  if (E->att_mt_min > 0 && m >= E->att_mt_min && m <= MAX_M && !aa.prepped && (aa.hd == 64 || aa.hd == 128))
+  if (E->att_mt_min > 0 && m >= E->att_mt_min && m <= MAX_M && !aa.prepped && (aa.hd == 64 || aa.hd == 128) &&
+      (!aa.q_bias || (aa.n_heads / aa.n_kv) * aa.hd <= 2048))
     return launch_attention_mt(aa, m, E->st_dev, s);
   return launch_attention(aa, m, E->st_dev, s);
 }
@@ -603,7 +604,8 @@ int enqueue_pass_m(spx_engine *E, int m) {
       aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
       aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
       aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
-      if (m >= E->pf_min_rows && E->pf_attn == 2 && m > MAX_M && c.n_heads / c.n_kv_heads >= 2) {
+      if (m >= E->pf_min_rows && E->pf_attn == 2 && m > MAX_M && c.n_heads / c.n_kv_heads >= 2 &&
+          (!ly.q_bias || (c.n_heads / c.n_kv_heads) * hd <= 2048)) {
         SPX_HIP(launch_attention_mt(aa, m, E->st_dev, s));
       } else if (m >= E->pf_min_rows) {  // rows prepared once (for 2..16 rows the fused kernel is faster: M = 9 4.46 vs 4.69 ms a pass)
         SPX_HIP(launch_rows_prep(aa, E->qp, m, E->st_dev, s));

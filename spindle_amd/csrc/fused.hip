@@ -2267,8 +2267,10 @@ static void launch_attn_mt_t(const AttnArgs &a, int m, const StepRec *st, hipStr
 
 hipError_t launch_attention_mt(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
   // (prefill passes: at least two queries a pass row, so a workgroup's rotations fit RPT = 5)
+  // (the kv group's query biases are staged a float4 a thread: at most 512 of them)
   if (a.prepped || m < 1 || m > PMAX || a.n_heads % a.n_kv || (m > MAX_M && a.n_heads / a.n_kv < 2) ||
-      (m * (a.n_heads / a.n_kv) + 15) / 16 > ATT_QT || (a.aq.q && (a.n_heads * a.hd) % 256))
+      (m * (a.n_heads / a.n_kv) + 15) / 16 > ATT_QT || (a.aq.q && (a.n_heads * a.hd) % 256) ||
+      (a.q_bias && (a.n_heads / a.n_kv) * a.hd > 2048))
     return hipErrorInvalidValue;
   if (a.hd == 128) launch_attn_mt_t<128>(a, m, st, s);
   else if (a.hd == 64) launch_attn_mt_t<64>(a, m, st, s);

@@ -1333,24 +1333,48 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
       }
     }
   }
-  if constexpr (BIG) {  // rows b in [p_lo - start, p_hi - start): wavefront w takes every eighth
-    for (int b = max(0, p_lo - start) + wave; b < min(m, p_hi - start); b += 8) {
-      const int pos = start + b, pp = pos - p_lo;
-      float e0, e1;
-      head_prep(a.k + (int64_t)b * a.kv_dim + h * HD, a.k_bias ? a.k_bias + h * HD : nullptr, a.k_norm, a.rope + (int64_t)pos * half, HD,
-                a.neox, a.eps, e0, e1);
-      if (act) {
-        const __half k0 = __float2half_rn(e0), k1 = __float2half_rn(e1);
-        ks[pp * KS + da] = (_Float16)__half2float(k0);
-        ks[pp * KS + db] = (_Float16)__half2float(k1);
-        if (blockIdx.z == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
+  if constexpr (BIG) {
+    // rows b in [b_lo, b_hi): wavefront w takes b_lo + w + 8 j, in batches of NB rows whose
+    // loads (row values, rotation) are all issued before the first row's arithmetic; then
+    // head_prep_pre, head_prep's operations on the loaded values (inactive lanes hold zeros)
+    constexpr int NB = 8;
+    const int b_lo = max(0, p_lo - start), b_hi = min(m, p_hi - start);
+    const int dA = act ? da : 0, dB = act ? db : 0, ln = act ? lane : 0;
+    float kb0 = 0.0f, kb1 = 0.0f, vb0 = 0.0f, vb1 = 0.0f;
+    if (a.k_bias) { kb0 = a.k_bias[h * HD + dA]; kb1 = a.k_bias[h * HD + dB]; }
+    if (a.v_bias) { vb0 = a.v_bias[h * HD + dA]; vb1 = a.v_bias[h * HD + dB]; }
+    for (int b0 = b_lo + wave; b0 < b_hi; b0 += 8 * NB) {
+      float rk0[NB], rk1[NB], rv0[NB], rv1[NB];
+      float2 rcs[NB];
+#pragma unroll
+      for (int j = 0; j < NB; j++) {  // clamped rows: every load valid
+        const int b = min(b0 + 8 * j, b_hi - 1);
+        const float *kp = a.k + (int64_t)b * a.kv_dim + h * HD, *vp = a.v + (int64_t)b * a.kv_dim + h * HD;
+        rk0[j] = kp[dA]; rk1[j] = kp[dB];
+        rv0[j] = vp[dA]; rv1[j] = vp[dB];
+        rcs[j] = a.rope[(int64_t)(start + b) * half + ln];
       }
-      head_prep(a.v + (int64_t)b * a.kv_dim + h * HD, a.v_bias ? a.v_bias + h * HD : nullptr, nullptr, nullptr, HD, a.neox, a.eps, e0, e1);
-      if (act) {
-        const __half v0 = __float2half_rn(e0), v1 = __float2half_rn(e1);
-        vt[da * VS + pp] = (_Float16)__half2float(v0);
-        vt[db * VS + pp] = (_Float16)__half2float(v1);
-        if (blockIdx.z == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        const int b = b0 + 8 * j, pos = start + b, pp = pos - p_lo;
+        if (b >= b_hi) break;  // (uniform across the wavefront)
+        float e0, e1;
+        head_prep_pre(act ? rk0[j] : 0.0f, act ? rk1[j] : 0.0f, kb0, kb1, a.k_bias != nullptr, a.k_norm != nullptr, kn0, kn1, true, rcs[j].x,
+                      rcs[j].y, HD, a.eps, e0, e1);
+        if (act) {
+          const __half k0 = __float2half_rn(e0), k1 = __float2half_rn(e1);
+          ks[pp * KS + da] = (_Float16)__half2float(k0);
+          ks[pp * KS + db] = (_Float16)__half2float(k1);
+          if (blockIdx.z == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
+        }
+        head_prep_pre(act ? rv0[j] : 0.0f, act ? rv1[j] : 0.0f, vb0, vb1, a.v_bias != nullptr, false, 0.0f, 0.0f, false, 1.0f, 0.0f, HD, a.eps,
+                      e0, e1);
+        if (act) {
+          const __half v0 = __float2half_rn(e0), v1 = __float2half_rn(e1);
+          vt[da * VS + pp] = (_Float16)__half2float(v0);
+          vt[db * VS + pp] = (_Float16)__half2float(v1);
+          if (blockIdx.z == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
+        }
       }
     }
   }
@@ -2240,27 +2264,31 @@ hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStre
   return hipGetLastError();
 }
 
+// Chunks a launch covers: the pass's own when the host knows them, else every slot (the
+// workgroups past the pass's end return at once)
+static int launch_nch(const AttnArgs &a) { return a.grid_nch > 0 ? min(a.grid_nch, a.nch) : a.nch; }
+
 template <int HD>
 static void launch_attn_pf_t(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
   using LY = AttnLds<HD>;
   const size_t sm = (size_t)64 * LY::KS * 2 + (size_t)HD * LY::VS * 2 + 4 * ((size_t)16 * LY::SS * 4 + (size_t)2 * 16 * LY::PS * 2 + 16 * 4);
-  const int nq = m * (a.n_heads / a.n_kv);
+  const int nq = m * (a.n_heads / a.n_kv), gx = launch_nch(a);
   SPX_LDS((k_attn_pf<HD>), sm);
-  hipLaunchKernelGGL((k_attn_pf<HD>), dim3(a.nch, a.n_kv, (nq + 63) / 64), dim3(256), sm, s, a, st);
-  hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, (nq + 15) / 16, (a.nch + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
+  hipLaunchKernelGGL((k_attn_pf<HD>), dim3(gx, a.n_kv, (nq + 63) / 64), dim3(256), sm, s, a, st);
+  hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, (nq + 15) / 16, (gx + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
 }
 
 template <int HD>
 static void launch_attn_mt_t(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
-  const int g = a.n_heads / a.n_kv, nqt = (m * g + 15) / 16;
+  const int g = a.n_heads / a.n_kv, nqt = (m * g + 15) / 16, gx = launch_nch(a);
   const size_t sm = MtLds<HD>::bytes(g, a.q_bias != nullptr, m);
   if (m > MAX_M) {  // merged per (query tile, chunk group): k_attn_pf_merge (41 vs 24 us a layer at 128 rows)
     SPX_LDS((k_attn_mt<HD, true>), sm);
-    hipLaunchKernelGGL((k_attn_mt<HD, true>), dim3(a.nch, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
-    hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, nqt, (a.nch + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
+    hipLaunchKernelGGL((k_attn_mt<HD, true>), dim3(gx, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
+    hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, nqt, (gx + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
   } else {
     SPX_LDS((k_attn_mt<HD, false>), sm);
-    hipLaunchKernelGGL((k_attn_mt<HD, false>), dim3(a.nch, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
+    hipLaunchKernelGGL((k_attn_mt<HD, false>), dim3(gx, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
     hipLaunchKernelGGL((k_attn_mrg<HD>), dim3((a.n_heads * HD + 255) / 256, m), dim3(1024), 0, s, a, st);
   }
 }

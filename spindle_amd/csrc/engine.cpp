@@ -604,7 +604,6 @@ int enqueue_pass_m(spx_engine *E, int m) {
       aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
       aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
       aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
-      if (big) aa.grid_nch = (E->st_host->start + m + 63) / 64;  // uncaptured (run_forward)
       if (m >= E->pf_min_rows && E->pf_attn == 2 && m > MAX_M && c.n_heads / c.n_kv_heads >= 2 &&
           (!ly.q_bias || (c.n_heads / c.n_kv_heads) * hd <= 2048)) {
         SPX_HIP(launch_attention_mt(aa, m, E->st_dev, s));
@@ -753,9 +752,7 @@ int run_forward(spx_engine *E, int m, bool advance = false) {
   const bool dec = E->dec_ok && E->dec_on;
   if (persist_used(E, m)) return enqueue_persist(E, advance);
   auto enqueue = [&]() { return !dec ? enqueue_forward(E, m, advance) : m == 1 ? enqueue_decode(E, advance) : enqueue_pass_m(E, m); };
-  // passes of more than 16 rows (prefill) run uncaptured: their attention launches cover only
-  // the pass's chunks (start is known on the host), where a replayed graph must cover max_seq
-  if (!E->use_graphs || E->profiling || m > MAX_M) return enqueue();
+  if (!E->use_graphs || E->profiling) return enqueue();
   const int slot = advance ? 0 : m;
   if (!E->graph[slot]) {
     SPX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));

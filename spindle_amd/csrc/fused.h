@@ -86,11 +86,8 @@ struct AttnArgs {
   float *att;                         // [m][q_dim]
   Q8KP aq;                            // permuted Q8_K of att (q null: not produced)
   int layer, max_seq, kv_dim, hd, n_heads, n_kv, neox;
-  int nch;                            // chunk slots per kv head (>= max_seq / 64)
+  int nch;                            // chunks launched per kv head (>= max_seq / 64)
   int nslot;                          // partial slots per kv head: nch chunks, then group partials
-  // chunks to launch per kv head when the pass's end is known on the host (an uncaptured
-  // pass: ceil((start + m) / 64)); 0: nch (graph replays, whose start is read on the device)
-  int grid_nch;
   // 1: q holds the prepared queries (bias, norm, RoPE applied) and the pass's K / V rows are in
   // the cache already (launch_rows_prep); multi-row passes only
   int prepped;

@@ -2264,31 +2264,27 @@ hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStre
   return hipGetLastError();
 }
 
-// Chunks a launch covers: the pass's own when the host knows them, else every slot (the
-// workgroups past the pass's end return at once)
-static int launch_nch(const AttnArgs &a) { return a.grid_nch > 0 ? min(a.grid_nch, a.nch) : a.nch; }
-
 template <int HD>
 static void launch_attn_pf_t(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
   using LY = AttnLds<HD>;
   const size_t sm = (size_t)64 * LY::KS * 2 + (size_t)HD * LY::VS * 2 + 4 * ((size_t)16 * LY::SS * 4 + (size_t)2 * 16 * LY::PS * 2 + 16 * 4);
-  const int nq = m * (a.n_heads / a.n_kv), gx = launch_nch(a);
+  const int nq = m * (a.n_heads / a.n_kv);
   SPX_LDS((k_attn_pf<HD>), sm);
-  hipLaunchKernelGGL((k_attn_pf<HD>), dim3(gx, a.n_kv, (nq + 63) / 64), dim3(256), sm, s, a, st);
-  hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, (nq + 15) / 16, (gx + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
+  hipLaunchKernelGGL((k_attn_pf<HD>), dim3(a.nch, a.n_kv, (nq + 63) / 64), dim3(256), sm, s, a, st);
+  hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, (nq + 15) / 16, (a.nch + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
 }
 
 template <int HD>
 static void launch_attn_mt_t(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
-  const int g = a.n_heads / a.n_kv, nqt = (m * g + 15) / 16, gx = launch_nch(a);
+  const int g = a.n_heads / a.n_kv, nqt = (m * g + 15) / 16;
   const size_t sm = MtLds<HD>::bytes(g, a.q_bias != nullptr, m);
   if (m > MAX_M) {  // merged per (query tile, chunk group): k_attn_pf_merge (41 vs 24 us a layer at 128 rows)
     SPX_LDS((k_attn_mt<HD, true>), sm);
-    hipLaunchKernelGGL((k_attn_mt<HD, true>), dim3(gx, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
-    hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, nqt, (gx + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
+    hipLaunchKernelGGL((k_attn_mt<HD, true>), dim3(a.nch, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
+    hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, nqt, (a.nch + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
   } else {
     SPX_LDS((k_attn_mt<HD, false>), sm);
-    hipLaunchKernelGGL((k_attn_mt<HD, false>), dim3(gx, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
+    hipLaunchKernelGGL((k_attn_mt<HD, false>), dim3(a.nch, a.n_kv, (nqt + 7) / 8), dim3(512), sm, s, a, st);
     hipLaunchKernelGGL((k_attn_mrg<HD>), dim3((a.n_heads * HD + 255) / 256, m), dim3(1024), 0, s, a, st);
   }
 }

@@ -1144,15 +1144,26 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
   extern __shared__ __align__(16) uint8_t smem[];
   _Float16 *ks = reinterpret_cast<_Float16 *>(smem);  // [64][KS]
   _Float16 *vt = ks + 64 * KS;                        // [HD][VS] (V transposed)
-  const int h = blockIdx.y, c = blockIdx.x;
+  // BIG: workgroups placed by XCD (workgroup i runs on XCD i mod 8): XCD x takes the
+  // (kv head, query block) pairs x P/8 .. x P/8 + P/8 - 1 (P = n_kv x query blocks, kv head
+  // major) over all chunks, so a query block's raw rows are fetched by one L2, not eight, and a
+  // kv head's chunks by P/8 query blocks' XCDs; the same (chunk, head, block) items as the grid
+  int c = blockIdx.x, h = blockIdx.y, zb = blockIdx.z;
+  if (BIG && ((gridDim.y * gridDim.z) & 7) == 0) {
+    const int L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), sl = L >> 3;
+    const int pr = (L & 7) * ((gridDim.y * gridDim.z) >> 3) + sl / gridDim.x;
+    c = sl % gridDim.x;
+    h = pr / gridDim.z;
+    zb = pr % gridDim.z;
+  }
   const int m = st->m, start = st->start, total = start + m;
   const int g = a.n_heads / a.n_kv, NQ = m * g;
   float *qn_s = reinterpret_cast<float *>(smem + LY::OFF_QN), *qb_s = reinterpret_cast<float *>(smem + LY::OFF_QB);
   float *rot_s = reinterpret_cast<float *>(smem + LY::off_rot(g, a.q_bias != nullptr));
-  if (blockIdx.z * 128 >= NQ || c >= (total + 63) / 64) return;
+  if (zb * 128 >= NQ || c >= (total + 63) / 64) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ar = lane & 15, kq = lane >> 4, kg = 4 * kq;
-  const int qa = (blockIdx.z * 8 + wave) * 16, qi = qa + ar;
+  const int qa = (zb * 8 + wave) * 16, qi = qa + ar;
   const bool qact = qi < NQ;
   const int p_lo = c * 64, p_hi = min(p_lo + 64, total);
   const int64_t cache0 = (int64_t)a.layer * a.max_seq * a.kv_dim + (int64_t)h * HD;
@@ -1162,7 +1173,7 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
   // this lane's raw query values
   const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
   constexpr int RPT = BIG ? 5 : 1;  // rotation float4s a thread stages (rows <= 65 at g >= 2 for BIG)
-  const int rb0 = blockIdx.z * 128 / g, nrot = min(m - rb0, LY::rot_rows(g, m)), nrv = nrot * (half / 2);
+  const int rb0 = zb * 128 / g, nrot = min(m - rb0, LY::rot_rows(g, m)), nrv = nrot * (half / 2);
   float4 sh_rot[RPT], sh_qn = z4, sh_qb = z4;
   const bool ld_qn = a.q_norm && tid < HD / 4, ld_qb = a.q_bias && tid < g * HD / 4;
 #pragma unroll
@@ -1322,14 +1333,14 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
         const __half k0 = __float2half_rn(e0), k1 = __float2half_rn(e1);
         ks[pp * KS + da] = (_Float16)__half2float(k0);
         ks[pp * KS + db] = (_Float16)__half2float(k1);
-        if (blockIdx.z == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
+        if (zb == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
       }
       head_prep_pre(nv0[j], nv1[j], nvb0[j], nvb1[j], a.v_bias != nullptr, false, 0.0f, 0.0f, false, 1.0f, 0.0f, HD, a.eps, e0, e1);
       if (act) {
         const __half v0 = __float2half_rn(e0), v1 = __float2half_rn(e1);
         vt[da * VS + pp] = (_Float16)__half2float(v0);
         vt[db * VS + pp] = (_Float16)__half2float(v1);
-        if (blockIdx.z == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
+        if (zb == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
       }
     }
   }
@@ -1365,7 +1376,7 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
           const __half k0 = __float2half_rn(e0), k1 = __float2half_rn(e1);
           ks[pp * KS + da] = (_Float16)__half2float(k0);
           ks[pp * KS + db] = (_Float16)__half2float(k1);
-          if (blockIdx.z == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
+          if (zb == 0) { __half *kd = a.kc + cache0 + (int64_t)pos * a.kv_dim; kd[da] = k0; kd[db] = k1; }
         }
         head_prep_pre(act ? rv0[j] : 0.0f, act ? rv1[j] : 0.0f, vb0, vb1, a.v_bias != nullptr, false, 0.0f, 0.0f, false, 1.0f, 0.0f, HD, a.eps,
                       e0, e1);
@@ -1373,7 +1384,7 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
           const __half v0 = __float2half_rn(e0), v1 = __float2half_rn(e1);
           vt[da * VS + pp] = (_Float16)__half2float(v0);
           vt[db * VS + pp] = (_Float16)__half2float(v1);
-          if (blockIdx.z == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
+          if (zb == 0) { __half *vd = a.vc + cache0 + (int64_t)pos * a.kv_dim; vd[da] = v0; vd[db] = v1; }
         }
       }
     }

@@ -77,8 +77,10 @@ int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, in
  * the reference. The Q8_K staging of K-quant activations lives in a fixed device array of
  * SPX_NOALLOC_SCRATCH_BYTES per device (m * cols up to 786432 codes, e.g. 16 vectors of 49152
  * columns); larger requests are rejected with an error. Float formats need no staging. The array
- * is shared by every call on a device and fully rewritten by each call before use, so calls on
- * one device must not overlap (concurrent calls race). Same results, bit for bit, as spx_matvec. */
+ * is shared by every call on a device and fully rewritten by each call before use; calls from
+ * different contexts (streams) take turns on it through a per-device event (each call's stream
+ * waits for the previous call's kernels). Under graph capture that wait is skipped: captured
+ * calls whose replays overlap on one device race. Same results, bit for bit, as spx_matvec. */
 #define SPX_NOALLOC_SCRATCH_BYTES (1u << 20)
 int spx_matvec_noalloc(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, int64_t ld_x,
                        int m, float *out, int64_t ld_out);

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <functional>
+#include <mutex>
 #include <thread>
 
 #include "../../include/spx.h"
@@ -61,6 +62,14 @@ void *ws_get(spx_ctx *ctx, size_t bytes) {
 // the library runs on holds one copy until the process ends; every call on that device shares
 // it (calls that overlap on one device race).
 static __device__ __align__(256) uint8_t g_noalloc_scratch[SPX_NOALLOC_SCRATCH_BYTES];
+// Per device, the event recorded after the last call's kernels: the next call, from any context
+// (each has its own stream), waits for it before it writes the array, so calls from different
+// streams take turns instead of overwriting each other's staging. Created once per device (an
+// event holds no device memory) and kept until the process ends.
+constexpr int NOALLOC_MAX_DEV = 64;
+static std::mutex g_noalloc_mu;
+static hipEvent_t g_noalloc_ev[NOALLOC_MAX_DEV];
+static bool g_noalloc_used[NOALLOC_MAX_DEV];
 
 // Layout of m permuted Q8_K vectors of n columns in one buffer (codes, d, bsum pairs; each
 // region 256-byte aligned); total bytes in *bytes.
@@ -167,6 +176,18 @@ int spx_create(int device, spx_ctx **out) {
     (void)hipStreamDestroy(c->stream);
     delete c;
     return hip_fail(e, "hipGetSymbolAddress(scratch)");
+  }
+  if (device < NOALLOC_MAX_DEV) {
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ev[device]) {
+      e = hipEventCreateWithFlags(&g_noalloc_ev[device], hipEventDisableTiming);
+      if (e != hipSuccess) {
+        g_noalloc_ev[device] = nullptr;
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return hip_fail(e, "hipEventCreate(scratch turn)");
+      }
+    }
   }
   *out = c;
   return 0;
@@ -371,8 +392,25 @@ int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, in
     bool ok = false;
     Q8KP y = ws_q8kp(ctx, m, cols, &ok);
     if (!ok) return fail("spx_matvec: workspace allocation failed");
+    if (ctx->device >= NOALLOC_MAX_DEV) return fail("spx_matvec_noalloc: device index above 63");
+    // take this device's turn on the array: wait for the previous call's kernels (any stream),
+    // then mark this call's end. A stream under graph capture skips both: the replay order of
+    // the captured graph is the caller's to arrange.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    SPX_HIP(hipStreamIsCapturing(ctx->stream, &cap));
+    const bool turn = cap == hipStreamCaptureStatusNone;
+    std::unique_lock<std::mutex> lk(g_noalloc_mu, std::defer_lock);
+    if (turn) {
+      lk.lock();
+      if (g_noalloc_used[ctx->device]) SPX_HIP(hipStreamWaitEvent(ctx->stream, g_noalloc_ev[ctx->device], 0));
+    }
     SPX_HIP(launch_q8kp_quantize(x, cols, ld_x, m, y, ctx->stream));
-    return mv_launch(ctx, w, expert, m, nullptr, 0, y, out, ld_out, 0, rows);
+    if (int r = mv_launch(ctx, w, expert, m, nullptr, 0, y, out, ld_out, 0, rows)) return r;
+    if (turn) {
+      SPX_HIP(hipEventRecord(g_noalloc_ev[ctx->device], ctx->stream));
+      g_noalloc_used[ctx->device] = true;
+    }
+    return 0;
   }
   if (w->v.dtype == T_F32 && cols % 16) return fail("spx_matvec: F32 needs cols % 16 == 0");
   if (w->v.dtype != T_Q8_0 && w->v.dtype != T_Q5_0 && w->v.dtype != T_Q5K && w->v.dtype != T_F32)
@@ -394,8 +432,25 @@ int spx_matvec_noalloc(spx_ctx *ctx, const spx_tensor *w, int expert, const floa
     if (bytes > SPX_NOALLOC_SCRATCH_BYTES)
       return fail("spx_matvec_noalloc: m x cols needs " + std::to_string(bytes) + " bytes of Q8_K staging, above the fixed scratch of " +
                   std::to_string(SPX_NOALLOC_SCRATCH_BYTES) + " (use spx_matvec)");
+    if (ctx->device >= NOALLOC_MAX_DEV) return fail("spx_matvec_noalloc: device index above 63");
+    // take this device's turn on the array: wait for the previous call's kernels (any stream),
+    // then mark this call's end. A stream under graph capture skips both: the replay order of
+    // the captured graph is the caller's to arrange.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    SPX_HIP(hipStreamIsCapturing(ctx->stream, &cap));
+    const bool turn = cap == hipStreamCaptureStatusNone;
+    std::unique_lock<std::mutex> lk(g_noalloc_mu, std::defer_lock);
+    if (turn) {
+      lk.lock();
+      if (g_noalloc_used[ctx->device]) SPX_HIP(hipStreamWaitEvent(ctx->stream, g_noalloc_ev[ctx->device], 0));
+    }
     SPX_HIP(launch_q8kp_quantize(x, cols, ld_x, m, y, ctx->stream));
-    return mv_launch(ctx, w, expert, m, nullptr, 0, y, out, ld_out, 0, rows);
+    if (int r = mv_launch(ctx, w, expert, m, nullptr, 0, y, out, ld_out, 0, rows)) return r;
+    if (turn) {
+      SPX_HIP(hipEventRecord(g_noalloc_ev[ctx->device], ctx->stream));
+      g_noalloc_used[ctx->device] = true;
+    }
+    return 0;
   }
   if (w->v.dtype == T_F32 && cols % 16) return fail("spx_matvec_noalloc: F32 needs cols % 16 == 0");
   if (w->v.dtype != T_Q8_0 && w->v.dtype != T_Q5_0 && w->v.dtype != T_Q5K && w->v.dtype != T_F32)

@@ -95,7 +95,7 @@ struct spx_engine {
   std::unique_ptr<spx::Sampler> smp;  // spx_engine_generate's sampler (none: plain greedy)
   spx_engine *draft = nullptr;        // draft model for spx_engine_generate (none: prompt lookup)
   std::vector<float> inv_freq;        // RoPE inverse frequencies (host), for the window's slide
-  __half *kv_stage = nullptr;         // the slide's staging rows (allocated at the first slide)
+  __half *kv_stage = nullptr;         // the slide's staging rows: one layer's K and V [2][max_seq][kv_dim]
   float2 *kv_cs = nullptr;
   std::vector<void *> allocs;
   // device state
@@ -937,7 +937,8 @@ int spx_engine_prepare(spx_engine *E) {
             (E->nkeep = E->dalloc<int>(M)) && (E->weights = E->dalloc<float>(M * 32)) && (E->jobs = E->dalloc<Job>(512)) &&
             (E->expert_count = E->dalloc<int>((size_t)c.n_layers * std::max(1, c.n_expert))) &&
             E->q8alloc(E->aq, M, ((E->q_dim + 255) / 256) * 256) && E->q8alloc(E->xq2, M, ((c.dim + 255) / 256) * 256) &&
-            E->q8alloc(E->xq, M, ((c.dim + 255) / 256) * 256) && E->q8alloc(E->hq, nv, nff);
+            E->q8alloc(E->xq, M, ((c.dim + 255) / 256) * 256) && E->q8alloc(E->hq, nv, nff) &&
+            (E->kv_stage = E->dalloc<__half>((size_t)2 * c.max_seq * E->kv_dim)) && (E->kv_cs = E->dalloc<float2>((size_t)c.head_dim / 2));
   if (!ok) return fail("spx_engine_prepare: out of device memory");
   for (auto &ly : E->L)
     if (ly.moe && !(ly.njobs = E->dalloc<int>(3))) return fail("out of device memory");
@@ -1301,11 +1302,7 @@ int spx_engine_shift_kv(spx_engine *E, int n_keep, int n_discard, int cur_pos, i
   if (n_discard == 0) return 0;
   const auto &c = E->c;
   SPX_HIP(hipSetDevice(E->ctx->device));
-  if (!E->kv_stage) {
-    if (!(E->kv_stage = E->dalloc<__half>((size_t)2 * c.n_layers * c.max_seq * E->kv_dim)) ||
-        !(E->kv_cs = E->dalloc<float2>((size_t)c.head_dim / 2)))
-      return fail("out of device memory for the KV window's slide");
-  }
+  if (!E->kv_stage || !E->kv_cs) return fail("spx_engine_shift_kv: no staging rows (engine not prepared)");
   // Rope::rotate's angle (pos * inv_freq, f32) at pos = -n_discard, sin / cos in f32
   const int half = c.head_dim / 2;
   std::vector<float2> cs(half);
@@ -1315,13 +1312,17 @@ int spx_engine_shift_kv(spx_engine *E, int n_keep, int n_discard, int cur_pos, i
   }
   hipStream_t s = E->ctx->stream;
   SPX_HIP(hipMemcpyAsync(E->kv_cs, cs.data(), sizeof(float2) * half, hipMemcpyHostToDevice, s));
-  KVShiftArgs a{};
-  a.kc = E->kc; a.vc = E->vc;
-  a.kt = E->kv_stage; a.vt = E->kv_stage + (size_t)c.n_layers * c.max_seq * E->kv_dim;
-  a.cs = E->kv_cs;
-  a.n_layers = c.n_layers; a.max_seq = c.max_seq; a.kv_dim = E->kv_dim; a.head_dim = c.head_dim; a.neox = c.rope_neox;
-  a.n_keep = n_keep; a.n_discard = n_discard; a.n_move = n_ctx - n_discard;
-  SPX_HIP(launch_kv_shift(a, s));
+  // one layer at a time through one layer's staging rows (allocated by spx_engine_prepare: a
+  // slide in the middle of a generation allocates nothing)
+  for (int l = 0; l < c.n_layers; l++) {
+    KVShiftArgs a{};
+    a.kc = E->kc + (size_t)l * c.max_seq * E->kv_dim; a.vc = E->vc + (size_t)l * c.max_seq * E->kv_dim;
+    a.kt = E->kv_stage; a.vt = E->kv_stage + (size_t)c.max_seq * E->kv_dim;
+    a.cs = E->kv_cs;
+    a.n_layers = 1; a.max_seq = c.max_seq; a.kv_dim = E->kv_dim; a.head_dim = c.head_dim; a.neox = c.rope_neox;
+    a.n_keep = n_keep; a.n_discard = n_discard; a.n_move = n_ctx - n_discard;
+    SPX_HIP(launch_kv_shift(a, s));
+  }
   SPX_HIP(hipStreamSynchronize(s));  // the host copy of cs goes out of scope
   *new_pos = cur_pos - n_discard;
   return 0;

@@ -182,7 +182,12 @@ int parse(spx_gguf *g) {
     g->meta[key] = std::move(v);
   }
   if (const Value *a = g->get("general.alignment")) {  // (:186-190) U32 or U64, at least 32
-    if (a->type == GV_U32 || a->type == GV_U64) g->alignment = std::max<uint64_t>(a->u, 32);
+    if (a->type == GV_U32 || a->type == GV_U64) {
+      // a power of two of at most 1 GiB (ggml's rule): the padding below cannot wrap
+      if (a->u == 0 || (a->u & (a->u - 1)) != 0 || a->u > (1ull << 30))
+        return spx::fail("general.alignment " + std::to_string(a->u) + " is not a power of two of at most 1 GiB");
+      g->alignment = std::max<uint64_t>(a->u, 32);
+    }
   }
   const Value *ar = g->get("general.architecture");
   g->arch = ar && ar->type == GV_STR ? ar->s : "";
@@ -202,13 +207,17 @@ int parse(spx_gguf *g) {
   }
   const uint64_t header_end = (uint64_t)(r.p - g->base);
   g->data_off = (header_end + g->alignment - 1) / g->alignment * g->alignment;  // (:219-221)
-  for (auto &t : g->tensors) t.abs = g->data_off + t.rel;
+  for (auto &t : g->tensors)
+    if (__builtin_add_overflow(g->data_off, t.rel, &t.abs))
+      return spx::fail("tensor " + t.name + ": data offset " + std::to_string(t.rel) + " overflows");
   return 0;
 }
 
+// rows = dims[1] * dims[2] * dims[3]; -1 when a dimension or the product leaves int64
 int64_t tensor_rows(const Tensor &t) {
   int64_t n = 1;
-  for (size_t k = 1; k < t.dims.size(); k++) n *= (int64_t)t.dims[k];
+  for (size_t k = 1; k < t.dims.size(); k++)
+    if (t.dims[k] > (uint64_t)INT64_MAX || __builtin_mul_overflow(n, (int64_t)t.dims[k], &n)) return -1;
   return n;
 }
 
@@ -408,8 +417,13 @@ int spx_gguf_check(const spx_gguf *g) {
   if (!g) return spx::fail("spx_gguf_check: null file");
   uint64_t needed = 0;
   for (const auto &t : g->tensors) {
-    const int64_t rb = spx::row_bytes((int)t.dtype, (int64_t)t.dims[0]);
-    if (rb > 0) needed = std::max(needed, t.abs + (uint64_t)rb * (uint64_t)tensor_rows(t));
+    if (t.dims[0] > (uint64_t)INT64_MAX) return spx::fail("tensor " + t.name + ": dims[0] out of range");
+    const int64_t rb = spx::row_bytes((int)t.dtype, (int64_t)t.dims[0]), rows = tensor_rows(t);
+    if (rb <= 0) continue;
+    uint64_t bytes = 0;
+    if (rows < 0 || __builtin_mul_overflow((uint64_t)rb, (uint64_t)rows, &bytes) || t.abs > g->size || bytes > g->size - t.abs)
+      return spx::fail("the file is incomplete: tensor " + t.name + " does not fit in its " + std::to_string(g->size >> 20) + " MiB");
+    needed = std::max(needed, t.abs + bytes);
   }
   if (needed > g->size)
     return spx::fail("the file is incomplete: it is " + std::to_string(g->size >> 20) + " MiB but its tensors need " +

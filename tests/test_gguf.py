@@ -172,3 +172,46 @@ def test_written_model_round_trip_and_cut_off_file(path):
     with G.GgufFile(path) as g:
         with pytest.raises(SpxError, match="incomplete"):
             g.check()
+
+
+def _one_tensor_file(path, dims, rel=0, dtype=0, alignment=None):
+    """A GGUF v3 file by hand: optional general.alignment (U64), one tensor with the given dims and
+    data offset, then 64 data bytes."""
+    meta = b""
+    n_kv = 0
+    if alignment is not None:
+        meta = struct.pack("<Q", 17) + b"general.alignment" + struct.pack("<IQ", G.U64, alignment)
+        n_kv = 1
+    t = struct.pack("<Q", 1) + b"w" + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+    t += struct.pack("<IQ", dtype, rel)
+    body = struct.pack("<IIQQ", G.MAGIC, 3, 1, n_kv) + meta + t
+    body += b"\0" * ((-len(body)) % 32) + bytes(64)
+    with open(path, "wb") as f:
+        f.write(body)
+
+
+@pytest.mark.parametrize("case", ["rows_wrap", "bytes_wrap", "offset_wrap", "offset_past_end", "cols_huge"])
+def test_sizes_that_wrap_are_refused(path, case):
+    """Dims whose product, byte count or offset wraps 64 bits (and offsets past the end) fail the
+    completeness check instead of passing it with a wrapped sum: the bounds the reference's slice
+    indexing enforces (gguf_loader.rs, :1944-1963)."""
+    dims, rel = {"rows_wrap": ([32, 1 << 40, 1 << 40], 0),          # rows overflow int64
+                 "bytes_wrap": ([32, (1 << 62) // 4], 0),            # F32: 128 B a row x 2^60 rows
+                 "offset_wrap": ([8], (1 << 64) - 16),               # data_offset + rel wraps
+                 "offset_past_end": ([8], 1 << 40),
+                 "cols_huge": ([1 << 63, 1], 0)}[case]
+    _one_tensor_file(path, dims, rel)
+    if case == "offset_wrap":
+        with pytest.raises(SpxError, match="overflows"):
+            G.GgufFile(path)
+        return
+    with G.GgufFile(path) as g:
+        with pytest.raises(SpxError, match="incomplete|out of range"):
+            g.check()
+
+
+@pytest.mark.parametrize("align", [0, 48, 1 << 31])
+def test_alignment_not_a_power_of_two_is_refused(path, align):
+    _one_tensor_file(path, [8], alignment=align)
+    with pytest.raises(SpxError, match="power of two"):
+        G.GgufFile(path)

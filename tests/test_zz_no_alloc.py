@@ -50,3 +50,30 @@ def test_noalloc_refuses_beyond_scratch(ctx):
     with pytest.raises(SpxError, match="fixed scratch"):
         ops.matvec_noalloc(ctx, w, x)
     w.close()
+
+
+def test_noalloc_two_contexts_take_turns(ctx):
+    """Two contexts (two streams) call spx_matvec_noalloc back to back with no synchronisation in
+    between, several rounds: the second call waits for the first call's kernels through the
+    per-device event, so neither overwrites the other's staging (both equal spx_matvec)."""
+    from spindle_amd import ops
+    from spindle_amd._lib import check, lib
+    from spindle_amd.ops import _p
+    ctx2 = ops.Context(0)
+    try:
+        rng = np.random.default_rng(11)
+        w = _tensor(ctx, M.Q4K, 8192, 2048, 21)
+        xs = [torch.from_numpy(rng.standard_normal((16, 8192)).astype(np.float32)).cuda() for _ in range(2)]
+        want = [ops.matvec(ctx, w, x).cpu().numpy() for x in xs]
+        for _ in range(4):
+            outs = [torch.empty((16, w.rows), dtype=torch.float32, device="cuda") for _ in range(2)]
+            torch.cuda.synchronize()
+            for c, x, o in zip((ctx, ctx2), xs, outs):
+                check(lib.spx_matvec_noalloc(c.h, w.h, 0, _p(x), 8192, 16, _p(o), w.rows))
+            ctx.sync()
+            ctx2.sync()
+            for o, wv in zip(outs, want):
+                assert np.array_equal(o.cpu().numpy().view(np.uint32), wv.view(np.uint32))
+        w.close()
+    finally:
+        ctx2.close()

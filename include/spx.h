@@ -181,6 +181,18 @@ int spx_engine_profile_read(spx_engine *e, int cls, const char **name, int64_t *
 /* Copies `bytes` of an internal buffer of the last pass (x, xn, q, k, v, att, proj, rlog,
  * chosen, weights, nkeep, h, y: the last layer's values) to host memory; for tests. */
 int spx_engine_debug_read(spx_engine *e, const char *what, void *host, int64_t bytes);
+/* Layer snapshots for the layer-by-layer parity tests (no reference counterpart; the oracle's
+ * stages are fed the GPU's own inputs). While on, passes run eagerly on the decode pipelines
+ * (K-quant models; refused otherwise) and each layer l copies, for each row b < m of the pass,
+ * its values into a device record read back with spx_engine_debug_read(e, "layers", ...):
+ * record (l * 16 + b) * R + off[f] holds field f, f = 0 x_in (the residual entering layer l;
+ * l = n_layers: the final residual), 1 q, 2 k, 3 v (raw projections), 4 att (attention output),
+ * 5 proj (attn_output projection), 6 x_mid (x_in + residual_scale * proj), 7 router logits,
+ * 8 h (the SwiGLU rows of the chosen experts in chosen order, n_used x n_ff; dense: n_ff),
+ * 9 chosen (int32, 32 slots), 10 weights (32), 11 nkeep (int32); off[12] = R (floats a row).
+ * spx_engine_debug_layout fills off[0..12]. */
+int spx_engine_debug_layers(spx_engine *e, int on);
+int spx_engine_debug_layout(spx_engine *e, int64_t *off);
 /* Number of distinct experts each MoE layer ran in the last pass (0 for dense layers). */
 int spx_engine_last_experts(spx_engine *e, int32_t *njobs_per_layer);
 /* Per layer and expert: passes that selected the expert since prepare ([n_layers][n_expert]). */

@@ -110,6 +110,10 @@ _sig("or_rope_rotate", None, P, C.c_int, P, C.c_size_t, C.c_size_t, C.c_float)
 _sig("or_model_init", None, C.POINTER(Model))
 _sig("or_forward_slice", C.c_int, C.POINTER(Model), C.c_int, C.c_int, P)
 _sig("or_forward_batch", C.c_int, C.POINTER(Model), P, C.c_int, C.c_int, P)
+_sig("or_attn_rows", C.c_int, C.POINTER(Model), C.c_int, C.c_int, C.c_int, P, P, P, P)
+_sig("or_layer_forward", C.c_int, C.POINTER(Model), C.c_int, C.c_int, C.c_int, P)
+_sig("or_down_combine", C.c_int, C.POINTER(Mat), C.c_int, P, P, P, P)
+_sig("or_set_dbg_h", None, P)
 _sig("or_logits", C.c_int, C.POINTER(Model), P, C.c_int, P)
 _sig("or_argmax", C.c_int, P, C.c_int, C.c_float)
 _sig("or_moe_forward", C.c_int, C.POINTER(Config), C.POINTER(Layer), C.c_int, P, P, P, P)

@@ -97,3 +97,64 @@ class OracleModel:
                                     out.ctypes.data_as(C.c_void_p), C.byref(st))
         assert n >= 0
         return out[:n], {k: getattr(st, k) for k, _ in ffi.GenStats._fields_}
+
+    # ---- per-layer stages (the layer-by-layer parity tests feed these the GPU's own inputs)
+    def layer_forward(self, layer, x, start):
+        """One layer on x [n, dim] (a copy) at positions start..start+n-1: forward_slice's layer
+        for n == 1, forward_batch_slice's for n > 1; writes the rows' K/V into the oracle's cache."""
+        x = np.array(x, np.float32, copy=True, order="C")
+        assert ffi.lib.or_layer_forward(C.byref(self.m), layer, x.shape[0], start, ffi.ptr(x)) == 0
+        return x
+
+    def attn_rows(self, layer, q, k, v, start):
+        """qkv_post + attention of n rows from the raw projections (copies); returns att [n, q_dim]."""
+        q, k, v = (np.array(a, np.float32, copy=True, order="C") for a in (q, k, v))
+        att = np.empty_like(q)
+        assert ffi.lib.or_attn_rows(C.byref(self.m), layer, q.shape[0], start, ffi.ptr(q), ffi.ptr(k), ffi.ptr(v), ffi.ptr(att)) == 0
+        return att
+
+    def norm(self, layer, which, x):
+        """attn_norm ('attn') or ffn_norm ('ffn') of layer on one row x."""
+        ly = self.layers[layer]
+        w = ly.attn_norm if which == "attn" else ly.ffn_norm
+        out = np.empty(self.cfg.dim, np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        ffi.lib.or_rmsnorm(ffi.ptr(x), w, ffi.ptr(out), self.cfg.dim, self.cfg.rms_eps)
+        return out
+
+    def mat(self, layer, name):
+        """The layer's matrix descriptor: wq, wk, wv, wo, gate, up, down, router."""
+        return getattr(self.layers[layer], name)
+
+    def moe_row(self, layer, xn):
+        """moe_forward of one ffn-normed row (router, routing, ffns_fused): (out, chosen, h) with
+        h the chosen experts' SwiGLU rows [keep, n_ff] in chosen order."""
+        cfg = self.cfg
+        ly = self.layers[layer]
+        nff = ly.gate.rows
+        h = np.full((cfg.n_expert_used, nff), np.nan, np.float32)
+        out = np.empty(cfg.dim, np.float32)
+        chosen = np.full(32, -1, np.int32)
+        nkeep = np.zeros(1, np.int32)
+        xn = np.ascontiguousarray(xn, np.float32)
+        xs = (C.c_void_p * 1)(xn.ctypes.data)
+        os_ = (C.c_void_p * 1)(out.ctypes.data)
+        ffi.lib.or_set_dbg_h(ffi.ptr(h))
+        try:
+            assert ffi.lib.or_moe_forward(C.byref(self.m.c), C.byref(ly), 1, xs, os_, ffi.ptr(chosen), ffi.ptr(nkeep)) == 0
+        finally:
+            ffi.lib.or_set_dbg_h(None)
+        k = int(nkeep[0])
+        return out, chosen[:k].copy(), h[:k].copy()
+
+    def down_combine(self, layer, chosen, weights, h):
+        """The routed experts' down projections of the given SwiGLU rows h [k, n_ff] (Q8_K-quantized
+        for an integer down) combined with the weights in chosen order, from zero."""
+        ly = self.layers[layer]
+        k = len(chosen)
+        chosen = np.ascontiguousarray(chosen, np.int32)
+        weights = np.ascontiguousarray(weights, np.float32)
+        h = np.ascontiguousarray(h, np.float32)
+        out = np.zeros(self.cfg.dim, np.float32)
+        assert ffi.lib.or_down_combine(C.byref(ly.down), k, ffi.ptr(chosen), ffi.ptr(weights), ffi.ptr(h), ffi.ptr(out)) == 0
+        return out

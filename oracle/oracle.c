@@ -661,6 +661,9 @@ int or_matvec_multi(const or_mat *m, int nvec, const float *const *xs, float *co
  * hd <= 128 values gives fma(a,a,b*b) per pair (a, b) = the RoPE pair, then the same tree. */
 static int g_norm_order = 0;
 void or_set_norm_order(int gpu_order) { g_norm_order = gpu_order; }
+/* Test capture (never set by default): or_ffns_fused copies its k x n_ff SwiGLU rows here. */
+static float *g_dbg_h = NULL;
+void or_set_dbg_h(float *h) { g_dbg_h = h; }
 static float tree64(float p[64]) {
   for (int w = 1; w < 64; w *= 2)
     for (int i = 0; i < 64; i += 2 * w) p[i] = p[i] + p[i + w];
@@ -739,18 +742,14 @@ static void swiglu_rows(const or_mat *g, const or_mat *u, const float *x, const 
   for (size_t r = 0; r < g->rows; r++) h[r] = or_silu(h[r]) * t[r];
 }
 
-int or_ffns_fused(const or_mat *gate, const or_mat *up, const or_mat *down, int k,
-                  const int *experts, const float *weights, const float *x, float *out) {
+/* ffns_fused's second pass and combine (:410-437): y_e = down_e(h_e) (h_e re-quantized to Q8_K
+ * for an integer down), then out[r] += w_e y_e[r] in chosen order, each product and sum rounded
+ * separately. h: k rows of down->cols. */
+int or_down_combine(const or_mat *down, int k, const int *experts, const float *weights, const float *h, float *out) {
   if (k <= 0) return 0;
-  size_t nff = gate->rows, dim = down->rows;
-  int use_int = q8k_supports(gate) || q8k_supports(up), int_down = q8k_supports(down);
-  float *h = malloc(sizeof(float) * k * nff), *t = malloc(sizeof(float) * nff), *y = malloc(sizeof(float) * k * dim);
-  q8k_buf xq = q8k_alloc(gate->cols);
-  if (use_int) or_q8k_quantize(x, gate->cols, xq.d, xq.qs, xq.bs);
-  for (int e = 0; e < k; e++) {
-    or_mat g = or_expert(*gate, experts[e]), u = or_expert(*up, experts[e]);
-    swiglu_rows(&g, &u, x, use_int ? &xq : NULL, h + e * nff, t);
-  }
+  size_t nff = down->cols, dim = down->rows;
+  int int_down = q8k_supports(down);
+  float *y = malloc(sizeof(float) * k * dim);
   for (int e = 0; e < k; e++) {
     or_mat d = or_expert(*down, experts[e]);
     if (int_down) {
@@ -765,7 +764,25 @@ int or_ffns_fused(const or_mat *gate, const or_mat *up, const or_mat *down, int 
     for (int e = 0; e < k; e++) acc += weights[e] * y[e * dim + r];
     out[r] = acc;
   }
-  q8k_free(xq); free(h); free(t); free(y);
+  free(y);
+  return 0;
+}
+
+int or_ffns_fused(const or_mat *gate, const or_mat *up, const or_mat *down, int k,
+                  const int *experts, const float *weights, const float *x, float *out) {
+  if (k <= 0) return 0;
+  size_t nff = gate->rows;
+  int use_int = q8k_supports(gate) || q8k_supports(up);
+  float *h = malloc(sizeof(float) * k * nff), *t = malloc(sizeof(float) * nff);
+  q8k_buf xq = q8k_alloc(gate->cols);
+  if (use_int) or_q8k_quantize(x, gate->cols, xq.d, xq.qs, xq.bs);
+  for (int e = 0; e < k; e++) {
+    or_mat g = or_expert(*gate, experts[e]), u = or_expert(*up, experts[e]);
+    swiglu_rows(&g, &u, x, use_int ? &xq : NULL, h + e * nff, t);
+  }
+  if (g_dbg_h) memcpy(g_dbg_h, h, sizeof(float) * k * nff);
+  or_down_combine(down, k, experts, weights, h, out);
+  q8k_free(xq); free(h); free(t);
   return 0;
 }
 
@@ -971,88 +988,103 @@ int or_ensure_kv_room(or_model *m, int n_keep, int cur_pos, int needed) {
                      m->inv_freq, n_keep, n_discard, cur_pos);
 }
 
-int or_forward_slice(or_model *m, int token, int pos, float *hidden) {
+/* qkv_post + attention for n rows at positions start..start+n-1 (forward_slice :3401-3495,
+ * forward_batch_slice :3235-3319): bias, q/k norms and RoPE applied to q, k, v in place, the n
+ * K/V rows written first, then row b attends over positions 0..start+b. */
+int or_attn_rows(or_model *m, int layer, int n, int start, float *q, float *k, float *v, float *att) {
+  const or_config *c = &m->c;
+  const or_layer *ly = &m->layers[layer];
+  int q_dim = c->n_heads * c->head_dim, kv_dim = c->n_kv_heads * c->head_dim;
+  if (layer < 0 || layer >= c->n_layers || n < 1 || start < 0 || start + n > c->max_seq) return -1;
+  for (int b = 0; b < n; b++) qkv_post(m, ly, layer, start + b, q + (size_t)b * q_dim, k + (size_t)b * kv_dim, v + (size_t)b * kv_dim);
+  for (int b = 0; b < n; b++) attention(m, layer, start + b, q + (size_t)b * q_dim, att + (size_t)b * q_dim);
+  return 0;
+}
+
+/* One layer on x [n][dim] in place: forward_slice's layer body for n == 1 (:3389-3548: matvec,
+ * moe_forward / the fused dense FFN), forward_batch_slice's for n > 1 (:3190-3356:
+ * matvec_multi, moe_forward_batch / ffn_forward_multi). */
+int or_layer_forward(or_model *m, int l, int n, int start, float *x) {
   const or_config *c = &m->c;
   int dim = c->dim, q_dim = c->n_heads * c->head_dim, kv_dim = c->n_kv_heads * c->head_dim;
-  if (pos < 0 || pos >= c->max_seq || token < 0 || token >= c->vocab) return -1;
-  float *x = malloc(4 * dim), *xn = malloc(4 * dim), *q = malloc(4 * q_dim), *k = malloc(4 * kv_dim),
-        *v = malloc(4 * kv_dim), *ao = malloc(4 * q_dim), *proj = malloc(4 * dim);
-  embed_row(m, token, x);
-  for (int l = 0; l < c->n_layers; l++) {
-    const or_layer *ly = &m->layers[l];
-    or_rmsnorm(x, ly->attn_norm, xn, dim, c->rms_eps);
-    or_matvec(&ly->wq, xn, q); or_matvec(&ly->wk, xn, k); or_matvec(&ly->wv, xn, v);
-    qkv_post(m, ly, l, pos, q, k, v);
-    attention(m, l, pos, q, ao);
-    or_matvec(&ly->wo, ao, proj);
-    if (m->dbg_q) { memcpy(m->dbg_q, q, 4 * q_dim); memcpy(m->dbg_att, ao, 4 * q_dim); memcpy(m->dbg_proj, proj, 4 * dim); }
-    for (int i = 0; i < dim; i++) x[i] += c->residual_scale * proj[i];
-    or_rmsnorm(x, ly->ffn_norm, xn, dim, c->rms_eps);
-    if (ly->is_moe) {
-      const float *xs[1] = {xn}; float *os[1] = {proj};
-      if (or_moe_forward(c, ly, 1, xs, os, m->last_chosen, NULL)) return -1;
-    } else {
-      int e0 = 0; float w1 = 1.0f;
-      memset(proj, 0, 4 * dim);
-      or_ffns_fused(&ly->gate, &ly->up, &ly->down, 1, &e0, &w1, xn, proj);
-    }
-    if (m->dbg_ffn) memcpy(m->dbg_ffn, proj, 4 * dim);
-    for (int i = 0; i < dim; i++) x[i] += c->residual_scale * proj[i];
+  if (l < 0 || l >= c->n_layers || n < 1 || n > 128 || start < 0 || start + n > c->max_seq) return -1;
+  const or_layer *ly = &m->layers[l];
+  float *xn = malloc(4 * (size_t)dim * n), *q = malloc(4 * (size_t)q_dim * n), *k = malloc(4 * (size_t)kv_dim * n),
+        *v = malloc(4 * (size_t)kv_dim * n), *ao = malloc(4 * (size_t)q_dim * n), *proj = malloc(4 * (size_t)dim * n);
+  const float *xr[128]; float *qr[128], *kr[128], *vr[128], *pr[128]; const float *ar[128];
+  for (int b = 0; b < n; b++) {
+    xr[b] = xn + (size_t)b * dim; qr[b] = q + (size_t)b * q_dim; kr[b] = k + (size_t)b * kv_dim;
+    vr[b] = v + (size_t)b * kv_dim; pr[b] = proj + (size_t)b * dim; ar[b] = ao + (size_t)b * q_dim;
   }
-  or_rmsnorm(x, m->output_norm, hidden, dim, c->rms_eps);
-  free(x); free(xn); free(q); free(k); free(v); free(ao); free(proj);
-  return 0;
+  int rc = 0;
+  for (int b = 0; b < n; b++) or_rmsnorm(x + (size_t)b * dim, ly->attn_norm, xn + (size_t)b * dim, dim, c->rms_eps);
+  if (n == 1) { or_matvec(&ly->wq, xn, q); or_matvec(&ly->wk, xn, k); or_matvec(&ly->wv, xn, v); }
+  else { or_matvec_multi(&ly->wq, n, xr, qr); or_matvec_multi(&ly->wk, n, xr, kr); or_matvec_multi(&ly->wv, n, xr, vr); }
+  or_attn_rows(m, l, n, start, q, k, v, ao);
+  if (n == 1) or_matvec(&ly->wo, ao, proj); else or_matvec_multi(&ly->wo, n, ar, pr);
+  if (m->dbg_q) { memcpy(m->dbg_q, q, 4 * q_dim); memcpy(m->dbg_att, ao, 4 * q_dim); memcpy(m->dbg_proj, proj, 4 * dim); }
+  for (int b = 0; b < n; b++) {
+    float *xb = x + (size_t)b * dim;
+    for (int i = 0; i < dim; i++) xb[i] += c->residual_scale * pr[b][i];
+    or_rmsnorm(xb, ly->ffn_norm, xn + (size_t)b * dim, dim, c->rms_eps);
+  }
+  if (ly->is_moe) {
+    if (n == 1) {
+      const float *xs[1] = {xn}; float *os[1] = {proj};
+      rc = or_moe_forward(c, ly, 1, xs, os, m->last_chosen, NULL);
+    } else if (n > 16) { /* MoE batches above 16 rows: split (per-row results do not depend on it) */
+      for (int s0 = 0; s0 < n && !rc; s0 += 16) { int cnt = n - s0 < 16 ? n - s0 : 16; rc = or_moe_forward(c, ly, cnt, xr + s0, pr + s0, NULL, NULL); }
+    } else rc = or_moe_forward(c, ly, n, xr, pr, m->last_chosen, NULL);
+  } else if (n == 1) { /* ffn_forward :590-614: the fused job with k = 1, w = 1 */
+    int e0 = 0; float w1 = 1.0f;
+    memset(proj, 0, 4 * dim);
+    or_ffns_fused(&ly->gate, &ly->up, &ly->down, 1, &e0, &w1, xn, proj);
+  } else { /* ffn_forward_multi :616-646 */
+    int nff = (int)ly->gate.rows;
+    float *g = malloc(4 * (size_t)nff * n), *u = malloc(4 * (size_t)nff * n);
+    float *gr[128], *ur[128]; const float *gc[128];
+    for (int b = 0; b < n; b++) { gr[b] = g + (size_t)b * nff; ur[b] = u + (size_t)b * nff; gc[b] = gr[b]; }
+    or_matvec_multi(&ly->gate, n, xr, gr); or_matvec_multi(&ly->up, n, xr, ur);
+    for (size_t i = 0; i < (size_t)nff * n; i++) g[i] = or_silu(g[i]) * u[i];
+    or_matvec_multi(&ly->down, n, gc, pr);
+    free(g); free(u);
+  }
+  if (m->dbg_ffn) memcpy(m->dbg_ffn, proj, 4 * dim);
+  for (int b = 0; b < n; b++) {
+    float *xb = x + (size_t)b * dim;
+    for (int i = 0; i < dim; i++) xb[i] += c->residual_scale * pr[b][i];
+  }
+  free(xn); free(q); free(k); free(v); free(ao); free(proj);
+  return rc;
+}
+
+int or_forward_slice(or_model *m, int token, int pos, float *hidden) {
+  const or_config *c = &m->c;
+  if (pos < 0 || pos >= c->max_seq || token < 0 || token >= c->vocab) return -1;
+  float *x = malloc(4 * (size_t)c->dim);
+  embed_row(m, token, x);
+  int rc = 0;
+  for (int l = 0; l < c->n_layers && !rc; l++) rc = or_layer_forward(m, l, 1, pos, x);
+  if (!rc) or_rmsnorm(x, m->output_norm, hidden, c->dim, c->rms_eps);
+  free(x);
+  return rc;
 }
 
 int or_forward_batch(or_model *m, const int *ids, int n, int start, float *hidden) {
   if (n == 1) return or_forward_slice(m, ids[0], start, hidden);
   const or_config *c = &m->c;
-  int dim = c->dim, q_dim = c->n_heads * c->head_dim, kv_dim = c->n_kv_heads * c->head_dim;
+  int dim = c->dim;
   if (n < 1 || n > 128 || start < 0 || start + n > c->max_seq) return -1;
-  float *x = malloc(4 * (size_t)dim * n), *xn = malloc(4 * (size_t)dim * n), *q = malloc(4 * (size_t)q_dim * n),
-        *k = malloc(4 * (size_t)kv_dim * n), *v = malloc(4 * (size_t)kv_dim * n), *ao = malloc(4 * (size_t)q_dim * n),
-        *proj = malloc(4 * (size_t)dim * n);
-  const float *xr[128]; float *qr[128], *kr[128], *vr[128], *pr[128]; const float *ar[128];
-  for (int b = 0; b < n; b++) {
+  for (int b = 0; b < n; b++)
     if (ids[b] < 0 || ids[b] >= c->vocab) return -1;
-    embed_row(m, ids[b], x + (size_t)b * dim);
-    xr[b] = xn + (size_t)b * dim; qr[b] = q + (size_t)b * q_dim; kr[b] = k + (size_t)b * kv_dim;
-    vr[b] = v + (size_t)b * kv_dim; pr[b] = proj + (size_t)b * dim; ar[b] = ao + (size_t)b * q_dim;
-  }
-  for (int l = 0; l < c->n_layers; l++) {
-    const or_layer *ly = &m->layers[l];
-    for (int b = 0; b < n; b++) or_rmsnorm(x + (size_t)b * dim, ly->attn_norm, xn + (size_t)b * dim, dim, c->rms_eps);
-    or_matvec_multi(&ly->wq, n, xr, qr); or_matvec_multi(&ly->wk, n, xr, kr); or_matvec_multi(&ly->wv, n, xr, vr);
-    for (int b = 0; b < n; b++) qkv_post(m, ly, l, start + b, qr[b], kr[b], vr[b]);
-    for (int b = 0; b < n; b++) attention(m, l, start + b, qr[b], ao + (size_t)b * q_dim);
-    or_matvec_multi(&ly->wo, n, ar, pr);
-    for (int b = 0; b < n; b++) {
-      float *xb = x + (size_t)b * dim;
-      for (int i = 0; i < dim; i++) xb[i] += c->residual_scale * pr[b][i];
-      or_rmsnorm(xb, ly->ffn_norm, xn + (size_t)b * dim, dim, c->rms_eps);
-    }
-    if (ly->is_moe) {
-      if (n > 16) { /* MoE batches above 16 rows: split (per-row results do not depend on it) */
-        for (int s = 0; s < n; s += 16) { int cnt = n - s < 16 ? n - s : 16; or_moe_forward(c, ly, cnt, xr + s, pr + s, NULL, NULL); }
-      } else if (or_moe_forward(c, ly, n, xr, pr, m->last_chosen, NULL)) return -1;
-    } else { /* ffn_forward_multi :616-646 */
-      int nff = (int)ly->gate.rows;
-      float *g = malloc(4 * (size_t)nff * n), *u = malloc(4 * (size_t)nff * n);
-      float *gr[128], *ur[128]; const float *gc[128];
-      for (int b = 0; b < n; b++) { gr[b] = g + (size_t)b * nff; ur[b] = u + (size_t)b * nff; gc[b] = gr[b]; }
-      or_matvec_multi(&ly->gate, n, xr, gr); or_matvec_multi(&ly->up, n, xr, ur);
-      for (size_t i = 0; i < (size_t)nff * n; i++) g[i] = or_silu(g[i]) * u[i];
-      or_matvec_multi(&ly->down, n, gc, pr);
-      free(g); free(u);
-    }
-    for (int b = 0; b < n; b++) {
-      float *xb = x + (size_t)b * dim;
-      for (int i = 0; i < dim; i++) xb[i] += c->residual_scale * pr[b][i];
-    }
-  }
-  for (int b = 0; b < n; b++) or_rmsnorm(x + (size_t)b * dim, m->output_norm, hidden + (size_t)b * dim, dim, c->rms_eps);
-  free(x); free(xn); free(q); free(k); free(v); free(ao); free(proj);
-  return 0;
+  float *x = malloc(4 * (size_t)dim * n);
+  for (int b = 0; b < n; b++) embed_row(m, ids[b], x + (size_t)b * dim);
+  int rc = 0;
+  for (int l = 0; l < c->n_layers && !rc; l++) rc = or_layer_forward(m, l, n, start, x);
+  if (!rc)
+    for (int b = 0; b < n; b++) or_rmsnorm(x + (size_t)b * dim, m->output_norm, hidden + (size_t)b * dim, dim, c->rms_eps);
+  free(x);
+  return rc;
 }
 
 int or_logits(or_model *m, const float *hidden, int n, float *logits) {

@@ -147,6 +147,13 @@ int or_shift_kv(uint16_t *k_cache, uint16_t *v_cache, int n_layers, int max_seq,
 /* ensure_kv_room (:2924-2940): when cur_pos + needed > max_seq, discards max(overflow, half of
  * the unpinned context), at most all of it; returns the new cur_pos. */
 int or_ensure_kv_room(or_model *m, int n_keep, int cur_pos, int needed);
+/* qkv_post + attention for n rows at start..start+n-1: q [n][q_dim], k, v [n][kv_dim] are the raw
+ * projections (bias, q/k norms, RoPE applied in place), their K/V rows written to the cache
+ * first; att [n][q_dim] (forward_slice :3401-3495, forward_batch_slice :3235-3319). */
+int or_attn_rows(or_model *m, int layer, int n, int start, float *q, float *k, float *v, float *att);
+/* One layer on x [n][dim] in place (forward_slice's layer for n == 1, forward_batch_slice's for
+ * n > 1); the rows' K/V written at start..start+n-1. */
+int or_layer_forward(or_model *m, int layer, int n, int start, float *x);
 /* forward_batch_slice: m tokens at start_pos (m==1 delegates to forward_slice) */
 int or_forward_batch(or_model *m, const int *ids, int n, int start_pos, float *hidden);
 /* LM head: matvec (n==1) or matvec_multi (smollm_chat.rs:3560-3602) */
@@ -157,6 +164,9 @@ int or_argmax(const float *logits, int n, float logit_scale);
 /* MoE layer on its own (moe_forward / moe_forward_batch, :925-1392) */
 int or_moe_forward(const or_config *c, const or_layer *ly, int n, const float *const *xs,
                    float *const *outs, int *chosen_out, int *nkeep_out);
+/* ffns_fused's down pass and combine (:410-437): out += sum_e w_e down_e(h_e), h: k rows of
+ * down->cols (Q8_K-quantized for an integer down), adds in chosen order */
+int or_down_combine(const or_mat *down, int k, const int *experts, const float *weights, const float *h, float *out);
 /* fused SwiGLU job, M=1 (ffns_fused :379-442): out += sum_e w_e FFN_e(x) */
 int or_ffns_fused(const or_mat *gate, const or_mat *up, const or_mat *down, int k,
                   const int *experts, const float *weights, const float *x, float *out);
@@ -229,6 +239,8 @@ void or_set_threads(int n);
 void or_set_simd(int on);
 /* Test knob, off by default: 1 = RMSNorm sums in the GPU kernels' order (sensitivity tests). */
 void or_set_norm_order(int gpu_order);
+/* Test capture, off by default: or_ffns_fused copies its k x n_ff SwiGLU rows to h (NULL: off). */
+void or_set_dbg_h(float *h);
 int or_get_threads(void);
 
 #ifdef __cplusplus

@@ -43,6 +43,8 @@ SIGNATURES = {
     "spx_engine_forward": (C.c_int, [P, P, C.c_int, C.c_int, P, P, P]),
     "spx_engine_last_experts": (C.c_int, [P, P]),
     "spx_engine_debug_read": (C.c_int, [P, C.c_char_p, P, I64]),
+    "spx_engine_debug_layers": (C.c_int, [P, C.c_int]),
+    "spx_engine_debug_layout": (C.c_int, [P, P]),
     "spx_engine_expert_counts": (C.c_int, [P, P]),
     "spx_engine_kv_download": (C.c_int, [P, P, P]),
     "spx_engine_attention": (C.c_int, [P, C.c_int, P, P, P, C.c_int, C.c_int, P]),

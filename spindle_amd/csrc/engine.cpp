@@ -114,6 +114,10 @@ struct spx_engine {
   float *yd = nullptr;  // [PMAX * n_used][dim]: expert outputs of a multi-row pass, combined by the next norm
   float *qp = nullptr;  // [PMAX][q_dim]: prepared queries of a prefill pass
   int last_m = 0;       // rows of the last pass
+  // layer snapshots (spx_engine_debug_layers): [n_layers + 1][MAX_M][dbg_off[DBG_NF]] floats
+  bool dbg_on = false;
+  float *dbg = nullptr;
+  int64_t dbg_off[13] = {};
   hipGraphExec_t graph[PMAX + 1] = {};
   int n_used = 0;
   // kernel-class timing (eager passes only): event pairs recorded around each launch
@@ -282,6 +286,32 @@ hipError_t attn_launch(spx_engine *E, const AttnArgs &aa, int m, hipStream_t s) 
   return launch_attention(aa, m, E->st_dev, s);
 }
 
+// layer snapshot fields (spx_engine_debug_layers)
+enum { DBG_XIN, DBG_Q, DBG_K, DBG_V, DBG_ATT, DBG_PROJ, DBG_XMID, DBG_RLOG, DBG_H, DBG_CHOSEN, DBG_WEIGHTS, DBG_NKEEP, DBG_NF };
+
+// Copies m rows of len words (source rows len words apart, or ld) into field f of layer l's
+// snapshot record.
+int snap(spx_engine *E, int l, int f, const void *src, int64_t len, int m, int64_t ld = 0) {
+  if (!E->dbg_on) return 0;
+  const int64_t R = E->dbg_off[DBG_NF];
+  SPX_HIP(hipMemcpy2DAsync(E->dbg + (int64_t)l * MAX_M * R + E->dbg_off[f], (size_t)R * 4, src, (size_t)(ld ? ld : len) * 4,
+                           (size_t)len * 4, (size_t)m, hipMemcpyDeviceToDevice, E->ctx->stream));
+  return 0;
+}
+
+// The routed experts' (or the dense FFN's) snapshot fields of layer l after its gate/up.
+int snap_ffn(spx_engine *E, int l, int m) {
+  if (!E->dbg_on) return 0;
+  const LayerW &ly = E->L[l];
+  const int64_t nff = ly.gate->v.rows;
+  if (int r = snap(E, l, DBG_H, E->h, (ly.moe ? E->n_used : 1) * nff, m)) return r;
+  if (!ly.moe) return 0;
+  if (int r = snap(E, l, DBG_RLOG, E->rlog, E->c.n_expert, m)) return r;
+  if (int r = snap(E, l, DBG_CHOSEN, E->chosen, 32, m)) return r;
+  if (int r = snap(E, l, DBG_WEIGHTS, E->weights, 32, m)) return r;
+  return snap(E, l, DBG_NKEEP, E->nkeep, 1, m);
+}
+
 int enqueue_forward(spx_engine *E, int m, bool advance = false) {
   const auto &c = E->c;
   hipStream_t s = E->ctx->stream;
@@ -438,6 +468,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
   }
   for (int l = 0; l < c.n_layers; l++) {
     const LayerW &ly = E->L[l];
+    if (int r = snap(E, l, DBG_XIN, E->xA, dim, 1)) return r;
     {
       ProfScope ps(E, PC_QKV, wbytes(ly.wq) + wbytes(ly.wk) + wbytes(ly.wv));
       DecMVArgs a{};
@@ -455,6 +486,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
       a.in = DecIn{E->xA, ly.attn_norm, c.rms_eps, dim};
       SPX_HIP(launch_dec_mv(a, total, s));
     }
+    if (int r = snap(E, l, DBG_Q, E->q, E->q_dim, 1) || snap(E, l, DBG_K, E->k, E->kv_dim, 1) || snap(E, l, DBG_V, E->v, E->kv_dim, 1)) return r;
     {
       ProfScope ps(E, PC_ATTN, -1.0 - l);
       AttnArgs aa{};
@@ -472,6 +504,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
         SPX_HIP(launch_dec_merge(ma, E->st_dev, s));
       }
     }
+    if (int r = snap(E, l, DBG_ATT, E->att, E->q_dim, 1)) return r;
     {
       ProfScope ps(E, PC_WO, wbytes(ly.wo));
       DecMVArgs a{};
@@ -480,6 +513,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
       a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
       SPX_HIP(launch_dec_mv(a, a.tiles[0], s));
     }
+    if (int r = snap(E, l, DBG_PROJ, E->proj, dim, 1) || snap(E, l, DBG_XMID, E->xB, dim, 1)) return r;
     const int nff = (int)ly.gate->v.rows;
     const DecIn fin{E->xB, ly.ffn_norm, c.rms_eps, dim};
     DecGateUpArgs ga{};
@@ -497,6 +531,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
         ga.expert_count = E->expert_count + (size_t)l * c.n_expert;
         SPX_HIP(launch_dec_gateup(ga, s));
       }
+      if (int r = snap_ffn(E, l, 1)) return r;
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
         DecDownArgs da{ly.down->v, E->h, E->chosen, E->weights, E->nkeep, c.n_expert_used, E->xB, E->xA, c.residual_scale};
@@ -507,6 +542,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
         SPX_HIP(launch_dec_gateup(ga, s));
       }
+      if (int r = snap_ffn(E, l, 1)) return r;
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down));
         DecMVArgs a{};
@@ -517,6 +553,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
       }
     }
   }
+  if (int r = snap(E, c.n_layers, DBG_XIN, E->xA, dim, 1)) return r;
   int grid = 1;
   {
     ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
@@ -582,6 +619,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
       ProfScope ps(E, PC_NORM, 0);
       SPX_HIP(norm(E->xA, ly.attn_norm, nullptr, E->xq2));
     }
+    if (int r = snap(E, l, DBG_XIN, E->xA, dim, m)) return r;
     {
       ProfScope ps(E, PC_QKV, wbytes(ly.wq) + wbytes(ly.wk) + wbytes(ly.wv));
       DecMMArgs a{};
@@ -593,6 +631,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
       a.nseg = 3; a.G = gshape(ly.wq); a.y = E->xq2; a.cols = dim; a.m = m;
       SPX_HIP(E->mq ? launch_dec_mq(a, mq_grid(total), s) : launch_dec_mm(a, dec_mm_grid(total), s));
     }
+    if (int r = snap(E, l, DBG_Q, E->q, E->q_dim, m) || snap(E, l, DBG_K, E->k, E->kv_dim, m) || snap(E, l, DBG_V, E->v, E->kv_dim, m)) return r;
     const bool att_q_fused = ((c.n_heads / c.n_kv_heads) * hd) % 256 == 0;
     {
       ProfScope ps(E, PC_ATTN, -1.0 - l);
@@ -617,6 +656,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
       }
     }
     if (!att_q_fused) { ProfScope ps(E, PC_QUANT, 0); SPX_HIP(launch_q8kp_quantize(E->att, E->q_dim, E->q_dim, m, E->aq, s)); }
+    if (int r = snap(E, l, DBG_ATT, E->att, E->q_dim, m)) return r;
     {
       ProfScope ps(E, PC_WO, wbytes(ly.wo));
       DecMMArgs a{};
@@ -625,6 +665,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
       a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
       SPX_HIP(E->mq ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
     }
+    if (int r = snap(E, l, DBG_PROJ, E->proj, dim, m) || snap(E, l, DBG_XMID, E->xB, dim, m)) return r;
     const int nff = (int)ly.gate->v.rows;
     {
       ProfScope ps(E, PC_NORM, 0);
@@ -649,6 +690,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
           SPX_HIP(E->mq && E->mq_gateup ? launch_dec_gateup_mq(ga, std::min(m * nu, c.n_expert), s) : launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
         }
       }
+      if (int r = snap_ffn(E, l, m)) return r;
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
         DecDownMArgs da{ly.down->v, E->h, E->jobs, ly.njobs, E->yd, big ? maxj : std::min(m * nu, c.n_expert)};
@@ -662,6 +704,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
         else SPX_HIP(E->mq && E->mq_gateup ? launch_dec_gateup_mq(ga, 1, s) : launch_dec_gateup_m(ga, 1, s));
         SPX_HIP(launch_q8kp_quantize(E->h, nff, nff, m, E->hq, s));
       }
+      if (int r = snap_ffn(E, l, m)) return r;
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down));
         DecMMArgs a{};
@@ -676,6 +719,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
   {
     ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
     SPX_HIP(norm(E->xA, E->out_norm, E->xn, E->xq));
+    if (int r = snap(E, c.n_layers, DBG_XIN, E->xA, dim, m)) return r;
     DecMMArgs a{};
     a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.ld_out[0] = c.vocab; a.tiles[0] = E->mq ? qtiles(E->lm_head) : mtiles(E->lm_head); a.nseg = 1;
     a.G = gshape(E->lm_head); a.y = E->xq; a.cols = dim; a.m = m;
@@ -731,7 +775,7 @@ int enqueue_persist(spx_engine *E, bool advance) {
 }
 
 bool persist_used(const spx_engine *E, int m) {
-  return m == 1 && E->dec_ok && E->dec_on && E->persist_ok && E->persist_on && !E->profiling;
+  return m == 1 && E->dec_ok && E->dec_on && E->persist_ok && E->persist_on && !E->profiling && !E->dbg_on;
 }
 
 // After a synchronised pass on the persistent kernel: a barrier that timed out voids the pass;
@@ -752,7 +796,7 @@ int run_forward(spx_engine *E, int m, bool advance = false) {
   const bool dec = E->dec_ok && E->dec_on;
   if (persist_used(E, m)) return enqueue_persist(E, advance);
   auto enqueue = [&]() { return !dec ? enqueue_forward(E, m, advance) : m == 1 ? enqueue_decode(E, advance) : enqueue_pass_m(E, m); };
-  if (!E->use_graphs || E->profiling) return enqueue();
+  if (!E->use_graphs || E->profiling || E->dbg_on) return enqueue();
   const int slot = advance ? 0 : m;
   if (!E->graph[slot]) {
     SPX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
@@ -1139,7 +1183,7 @@ int spx_engine_profile_read(spx_engine *E, int cls, const char **name, int64_t *
 
 int spx_engine_decode(spx_engine *E, int32_t token, int start_pos, int n, int32_t *out) {
   if (!E || !out || n < 0) return fail("spx_engine_decode: bad argument");
-  if (!E->use_graphs || E->profiling) {
+  if (!E->use_graphs || E->profiling || E->dbg_on) {
     int32_t tok = token;
     for (int i = 0; i < n; i++) {  // step_token (:3106-3132) + greedy sample, one token per pass
       int32_t am = 0;
@@ -1183,6 +1227,14 @@ int spx_engine_debug_read(spx_engine *E, const char *what, void *host, int64_t b
     memcpy(host, &E->smp->rng, 8);
     return 0;
   }
+  if (w == "layers") {
+    if (!E->dbg) return fail("spx_engine_debug_read: layer snapshots are off (spx_engine_debug_layers)");
+    const int64_t have = (int64_t)(E->c.n_layers + 1) * MAX_M * E->dbg_off[DBG_NF] * 4;
+    if (bytes > have) return fail("spx_engine_debug_read: the layer record holds " + std::to_string(have) + " bytes");
+    SPX_HIP(hipStreamSynchronize(E->ctx->stream));
+    SPX_HIP(hipMemcpy(host, E->dbg, (size_t)bytes, hipMemcpyDeviceToHost));
+    return 0;
+  }
   const void *src = w == "tstamp" ? (const void *)E->pa.tstamp : w == "x" ? (const void *)E->xA : w == "xn" ? (const void *)E->xn : w == "q" ? (const void *)E->q : w == "k" ? (const void *)E->k : w == "v" ? (const void *)E->v
                   : w == "att" ? (const void *)E->att : w == "proj" ? (const void *)E->proj : w == "rlog" ? (const void *)E->rlog
                   : w == "chosen" ? (const void *)E->chosen : w == "weights" ? (const void *)E->weights
@@ -1190,6 +1242,32 @@ int spx_engine_debug_read(spx_engine *E, const char *what, void *host, int64_t b
   if (!src) return fail("spx_engine_debug_read: unknown buffer " + w);
   SPX_HIP(hipStreamSynchronize(E->ctx->stream));
   SPX_HIP(hipMemcpy(host, src, (size_t)bytes, hipMemcpyDeviceToHost));
+  return 0;
+}
+
+int spx_engine_debug_layout(spx_engine *E, int64_t *off) {
+  if (!E || !off) return fail("null argument");
+  if (!E->prepared) return fail("spx_engine_debug_layout: call spx_engine_prepare first");
+  const auto &c = E->c;
+  int64_t nff = 0;
+  for (const auto &ly : E->L) nff = std::max<int64_t>(nff, ly.gate->v.rows);
+  const int64_t len[DBG_NF] = {c.dim, E->q_dim, E->kv_dim, E->kv_dim, E->q_dim, c.dim, c.dim, std::max(1, c.n_expert),
+                               std::max(1, E->n_used) * nff, 32, 32, 1};
+  int64_t o = 0;
+  for (int f = 0; f < DBG_NF; f++) { off[f] = o; o += len[f]; }
+  off[DBG_NF] = o;
+  return 0;
+}
+
+int spx_engine_debug_layers(spx_engine *E, int on) {
+  if (!E) return fail("null engine");
+  if (!on) { E->dbg_on = false; return 0; }
+  if (!E->prepared) return fail("spx_engine_debug_layers: call spx_engine_prepare first");
+  if (!(E->dec_ok && E->dec_on)) return fail("spx_engine_debug_layers: layer snapshots need the decode pipelines (a K-quant model)");
+  if (int r = spx_engine_debug_layout(E, E->dbg_off)) return r;
+  if (!E->dbg && !(E->dbg = E->dalloc<float>((size_t)(E->c.n_layers + 1) * MAX_M * E->dbg_off[DBG_NF])))
+    return fail("spx_engine_debug_layers: out of device memory");
+  E->dbg_on = true;
   return 0;
 }
 

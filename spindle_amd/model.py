@@ -360,6 +360,27 @@ class Engine:
             res[name.value.decode()] = (n.value, us.value, by.value)
         return res
 
+    LAYER_FIELDS = ("x_in", "q", "k", "v", "att", "proj", "x_mid", "rlog", "h", "chosen", "weights", "nkeep")
+
+    def debug_layers(self, on):
+        """Layer snapshots on (passes run eagerly and record each layer's values) or off."""
+        check(lib.spx_engine_debug_layers(self.h, int(on)))
+
+    def read_layers(self, m):
+        """The last pass's layer snapshots (m rows): {field: array [n_layers + 1, m, len]}; x_in of
+        layer n_layers is the final residual; chosen / nkeep as int32."""
+        off = np.zeros(13, np.int64)
+        check(lib.spx_engine_debug_layout(self.h, off.ctypes.data_as(P)))
+        R, L = int(off[12]), self.cfg.n_layers + 1
+        buf = np.empty(L * 16 * R, np.float32)
+        check(lib.spx_engine_debug_read(self.h, b"layers", buf.ctypes.data_as(P), buf.nbytes))
+        buf = buf.reshape(L, 16, R)[:, :m]
+        out = {}
+        for f, name in enumerate(self.LAYER_FIELDS):
+            a = buf[:, :, off[f]:off[f + 1]]
+            out[name] = a.view(np.int32).copy() if name in ("chosen", "nkeep") else a.copy()
+        return out
+
     def last_experts(self):
         out = np.empty(self.cfg.n_layers, np.int32)
         check(lib.spx_engine_last_experts(self.h, out.ctypes.data_as(P)))

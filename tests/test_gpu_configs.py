@@ -299,3 +299,139 @@ def test_qwen3_30b_a3b_moe_prune(ctx, prune):
     smollm_chat.rs:1221-1237): teacher-forced decode against the oracle."""
     S = setup(ctx, "qwen3-30b-a3b", moe_prune=prune)
     _kquant_bar(*_teacher_forced(S, 6, sensitivity=True))
+
+
+# ---------------------------------------------------------------- layer by layer (K-quant models)
+def _nerr(a, b):
+    """max |a - b| over max(1e-30, max |b|) (max-abs normalised)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(1e-30, float(np.max(np.abs(b)))))
+
+
+def _codes(x):
+    """Q8_K codes of one row (the reference's quantize_avx2, via the oracle)."""
+    return ffi.q8k_quantize(np.ascontiguousarray(x, np.float32))[1].astype(np.int16)
+
+
+def _bitwise(a, b):
+    return np.array_equal(np.ascontiguousarray(a, np.float32).view(np.uint32), np.ascontiguousarray(b, np.float32).view(np.uint32))
+
+
+def _layer_pins(S, ids, pos):
+    """One pass of len(ids) rows at pos with layer snapshots on; for every layer and row, the
+    oracle's stages fed the GPU's own stage inputs:
+      q|k|v    from the GPU's x_in, norm in the GPU's sum order: bitwise (the same Q8_K codes and
+               the exact integer path); in the reference's order: the Q8_K codes differ by at most
+               one step where they differ, the projections within 1e-2 of each other
+      attention from the GPU's raw q / k / v and KV cache: within 1e-4
+      attn_output from the GPU's attention output: bitwise, and so x_mid
+      router   from the GPU's x_mid (GPU norm order): within 1e-4, the same experts and weights
+      experts  SwiGLU rows within 1e-4 (Q8_K codes at most one step apart); the down projections
+               and combine from the GPU's own h and weights: bitwise, and so the layer output
+      layer    the whole layer in the oracle (reference order) from the GPU's x_in: within 1e-3
+    Returns the per-layer statistics."""
+    cfg, eng, om = S.cfg, S.eng, S.om
+    m = len(ids)
+    eng.debug_layers(True)
+    try:
+        eng.forward(ids, pos)
+        sn = eng.read_layers(m)
+    finally:
+        eng.debug_layers(False)
+    S.sync_kv()
+    nu, rs = cfg.n_expert_used, np.float32(cfg.residual_scale)
+    stats = dict(att=[], rlog=[], h=[], layer=[], qkv_ref=[], flips_xn=0, flips_h=0, kv_f16_diff=0)
+    for l in range(cfg.n_layers):
+        x_in, x_out = sn["x_in"][l], sn["x_in"][l + 1]
+        # q|k|v
+        for b in range(m):
+            ffi.set_norm_order(True)
+            try:
+                xn = om.norm(l, "attn", x_in[b])
+            finally:
+                ffi.set_norm_order(False)
+            xr = om.norm(l, "attn", x_in[b])
+            for name, f in (("wq", "q"), ("wk", "k"), ("wv", "v")):
+                mt = om.mat(l, name)
+                got = sn[f][l, b]
+                assert _bitwise(ffi.matvec(mt, xn), got), (S.key, l, b, name, "projection of the same Q8_K input")
+                e = _nerr(ffi.matvec(mt, xr), got)
+                assert e <= 1e-2, (S.key, l, b, name, "projection of the reference-order norm", e)
+                stats["qkv_ref"].append(e)
+            dc = np.abs(_codes(xr) - _codes(xn))
+            assert dc.max() <= 1, (S.key, l, b, "a Q8_K code moved by more than one step")
+            stats["flips_xn"] += int(np.count_nonzero(dc))
+        # attention (the oracle writes its own K/V rows of these positions from the GPU's raw k, v)
+        k_gpu = om.k_cache.reshape(cfg.n_layers, cfg.max_seq, cfg.kv_dim)[l, pos:pos + m].copy()  # the GPU's rows (sync_kv)
+        att = om.attn_rows(l, sn["q"][l], sn["k"][l], sn["v"][l], pos)
+        e = _nerr(att, sn["att"][l])
+        assert e <= 1e-4, (S.key, l, "attention", e)
+        stats["att"].append(e)
+        k_or = om.k_cache.reshape(cfg.n_layers, cfg.max_seq, cfg.kv_dim)[l, pos:pos + m]
+        stats["kv_f16_diff"] += int(np.count_nonzero(k_or != k_gpu))
+        for b in range(m):
+            # attn_output + residual
+            proj = ffi.matvec(om.mat(l, "wo"), sn["att"][l, b])
+            assert _bitwise(proj, sn["proj"][l, b]), (S.key, l, b, "attn_output of the same Q8_K input")
+            assert _bitwise(x_in[b] + rs * proj, sn["x_mid"][l, b]), (S.key, l, b, "x_mid")
+            # router, routing, experts
+            ffi.set_norm_order(True)
+            try:
+                xn2 = om.norm(l, "ffn", sn["x_mid"][l, b])
+            finally:
+                ffi.set_norm_order(False)
+            rl = ffi.matvec(om.mat(l, "router"), xn2)
+            e = _nerr(sn["rlog"][l, b], rl)
+            assert e <= 1e-4, (S.key, l, b, "router logits", e)
+            stats["rlog"].append(e)
+            y_or, ch_or, h_or = om.moe_row(l, xn2)
+            k = int(sn["nkeep"][l, b, 0])
+            ch = sn["chosen"][l, b, :k]
+            assert np.array_equal(ch, ch_or), (S.key, l, b, "chosen experts", ch, ch_or)
+            h = sn["h"][l, b].reshape(nu, -1)[:k]
+            e = _nerr(h, h_or)
+            assert e <= 1e-4, (S.key, l, b, "SwiGLU rows", e)
+            stats["h"].append(e)
+            for j in range(k):
+                dc = np.abs(_codes(h[j]) - _codes(h_or[j]))
+                assert dc.max() <= 1, (S.key, l, b, j, "a Q8_K code of h moved by more than one step")
+                stats["flips_h"] += int(np.count_nonzero(dc))
+            y = om.down_combine(l, ch, sn["weights"][l, b, :k], h)
+            assert _bitwise(sn["x_mid"][l, b] + rs * y, x_out[b]), (S.key, l, b, "down + combine of the same h")
+        # the whole layer in the oracle, reference order, from the GPU's layer input
+        xo = om.layer_forward(l, x_in, pos)
+        e = _nerr(xo, x_out)
+        assert e <= 1e-3, (S.key, l, "layer output", e)
+        stats["layer"].append(e)
+    S.sync_kv()  # the oracle's cache back to the GPU's rows
+    return stats
+
+
+def _report(key, what, st):
+    f = lambda v: f"median {np.median(v):.1e} max {max(v):.1e}"
+    print(f"[{key}] {what}: q|k|v from the reference-order norm {f(st['qkv_ref'])}; attention {f(st['att'])}; "
+          f"router {f(st['rlog'])}; SwiGLU rows {f(st['h'])}; layer output {f(st['layer'])}; one-step Q8_K moves: "
+          f"{st['flips_xn']} in normed inputs, {st['flips_h']} in h; K rows with an f16 bit apart {st['kv_f16_diff']}")
+
+
+def test_layer_by_layer_decode(ctx):
+    """Config 5 (Qwen3-30B-A3B-shaped Q4_K_M) at full shape, every one of the 48 layers of a
+    one-row decode pass at the config's context, each stage against the oracle fed the GPU's own
+    inputs (_layer_pins: bitwise where the arithmetic is integer or shared, 1e-4 for attention,
+    router and SwiGLU, 1e-3 for the layer)."""
+    S = setup(ctx, "qwen3-30b-a3b")
+    tok = int(np.random.default_rng(SEED + 3).integers(0, S.cfg.vocab))
+    _report(S.key, "decode, 48 layers", _layer_pins(S, [tok], S.n0 + 40))
+
+
+def test_layer_by_layer_verify(ctx):
+    """The same pins for a lane-exact verify pass of 9 rows (each row's values are the one-row
+    pass's, test_verify_pass_at_context)."""
+    S = setup(ctx, "qwen3-30b-a3b")
+    ids = np.random.default_rng(SEED + 4).integers(0, S.cfg.vocab, 9).astype(np.int32)
+    S.eng.set_mfma(False)
+    try:
+        _report(S.key, "verify M=9, 48 layers", _layer_pins(S, ids, S.n0 + 48))
+    finally:
+        S.eng.set_mfma(True)

@@ -68,3 +68,38 @@ def test_draft_model_speculation():
     other = OracleModel(cfg, M.synth_model(cfg, seed=22))
     diff, st2 = OracleModel(cfg, w).generate(prompt, 40, draft_len=4, draft=other)
     assert np.array_equal(plain, diff) and st2["accepted"] < st2["drafted"]
+
+
+def test_layer_stages_compose_to_the_forward():
+    """The per-layer entry points the layer-by-layer GPU tests feed with the GPU's own values:
+    embedding + layer_forward over the layers + output_norm gives forward()'s hidden state bit for
+    bit, and writes forward()'s KV rows (a 5-row batch); moe_row's SwiGLU rows through
+    down_combine give moe_row's output (within 1e-5: the routing weights are recomputed here in
+    numpy, not by the oracle's route())."""
+    from oracle import ffi
+    cfg = M.TINY["tiny-qwen3moe"]
+    w = M.synth_model(cfg, seed=8)
+    a, b = OracleModel(cfg, w), OracleModel(cfg, w)
+    ids = np.array([5, 77, 400, 12, 999], np.int32)
+    want = a.forward(ids, 3)
+    emb, _ = w["token_embd.weight"]
+    x = np.stack([ffi.dequant_row(emb.dtype, w["token_embd.weight"][1][t * ffi.row_bytes(emb.dtype, cfg.dim):(t + 1) * ffi.row_bytes(emb.dtype, cfg.dim)], cfg.dim)
+                  for t in ids]) * np.float32(cfg.embedding_scale)
+    for l in range(cfg.n_layers):
+        x = b.layer_forward(l, x, 3)
+    assert np.array_equal(a.k_cache, b.k_cache) and np.array_equal(a.v_cache, b.v_cache)
+    onorm = w["output_norm.weight"][1]
+    for r in range(len(ids)):
+        h = np.empty(cfg.dim, np.float32)
+        ffi.lib.or_rmsnorm(ffi.ptr(np.ascontiguousarray(x[r])), onorm.ctypes.data, ffi.ptr(h), cfg.dim, cfg.rms_eps)
+        assert np.array_equal(h.view(np.uint32), want[r].view(np.uint32)), r
+    xn = b.norm(0, "ffn", x[0])
+    y, ch, hr = b.moe_row(0, xn)
+    assert len(ch) == cfg.n_expert_used and np.isfinite(hr).all()
+    # the routing weights as route() forms them: softmax over the router logits, renormalised
+    rl = ffi.matvec(b.mat(0, "router"), xn).astype(np.float32)
+    p = np.exp(rl - rl.max()).astype(np.float32)
+    p = p / p.sum(dtype=np.float32)
+    wts = (p[ch] / p[ch].sum(dtype=np.float32)) if cfg.expert_norm else p[ch]
+    y2 = b.down_combine(0, ch, wts.astype(np.float32), hr)
+    assert np.allclose(y2, y, rtol=1e-5, atol=1e-6 * float(np.abs(y).max()))

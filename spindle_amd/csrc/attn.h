@@ -62,7 +62,7 @@ __device__ __forceinline__ void head_prep(const float *src, const float *bias, c
   if (bias && act) { x0 += bias[da]; x1 += bias[db]; }
   if (nw) {
     const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)hd) + eps));
+    const float inv = inv_rms(ss, (float)hd, eps);
     if (act) { x0 = x0 * inv * nw[da]; x1 = x1 * inv * nw[db]; }
   }
   if (rope_row && act) {  // Rope::rotate (:1404-1419)
@@ -280,7 +280,7 @@ __device__ __forceinline__ void head_prep_pre(float x0, float x1, float xb0, flo
   if (bias && act) { x0 += xb0; x1 += xb1; }
   if (norm) {
     const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)hd) + eps));
+    const float inv = inv_rms(ss, (float)hd, eps);
     if (act) { x0 = x0 * inv * nw0; x1 = x1 * inv * nw1; }
   }
   if (rope && act) {
@@ -373,7 +373,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
       float e0 = x0[j], e1 = x1[j];
       if (a.q_norm) {
         const float ssq = wave_sum(fmaf(e0, e0, e1 * e1));
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ssq, (float)HD) + a.eps));
+        const float inv = inv_rms(ssq, (float)HD, a.eps);
         if (act) { e0 = e0 * inv * n0; e1 = e1 * inv * n1; }
       }
       if (act) {
@@ -437,7 +437,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, const int m, const 
       float e0 = nk_x[0], e1 = nk_x[1];
       if (a.k_norm) {
         const float ssq = wave_sum(fmaf(e0, e0, e1 * e1));
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ssq, (float)HD) + a.eps));
+        const float inv = inv_rms(ssq, (float)HD, a.eps);
         if (act) { e0 = e0 * inv * nk_w[0]; e1 = e1 * inv * nk_w[1]; }
       }
       if (act) {

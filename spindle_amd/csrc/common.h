@@ -44,6 +44,13 @@ __device__ __forceinline__ float h2f(uint32_t h) {
 }
 
 // Intra-quad reductions (lanes 4k..4k+3) through DPP quad permutes.
+// RMSNorm's 1 / sqrt(S / n + eps) with the reference's IEEE rounding (f32::sqrt and the division
+// both correctly rounded). HIP's __fsqrt_rn is the native v_sqrt_f32 (up to 1 ulp off) unless
+// OCML_BASIC_ROUNDED_OPERATIONS is defined, while sqrtf lowers to v_sqrt_f32 plus the +-1 ulp
+// fma correction (correctly rounded; the build also passes -fhip-fp32-correctly-rounded-divide-
+// sqrt); the division is the full div_scale / div_fmas / div_fixup sequence.
+__device__ __forceinline__ float inv_rms(float sumsq, float n, float eps) { return 1.0f / sqrtf(sumsq / n + eps); }
+
 __device__ __forceinline__ int quad_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true); }
 __device__ __forceinline__ int quad_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true); }
 __device__ __forceinline__ int quad_sum(int v) { v += quad_xor1(v); v += quad_xor2(v); return v; }

@@ -250,7 +250,7 @@ __global__ __launch_bounds__(256) void kd_router(const DecRouterArgs a) {
   __syncthreads();
   float S = 0.0f;
   for (int k = 0; k < nbq; k++) S = S + bsum[k];
-  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(S, (float)dim) + a.in.eps));
+  const float inv = inv_rms(S, (float)dim, a.in.eps);
   float pv = 0.0f;
 #pragma unroll
   for (int k = 0; k < NK; k++) {

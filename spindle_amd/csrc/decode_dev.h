@@ -155,7 +155,7 @@ __device__ __forceinline__ void in_quant(const DecIn &in, InRow<KB> &r, QP lq, D
     __syncthreads();
     float S = 0.0f;
     for (int k = 0; k < nbq; k++) S = S + bsum[k];
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(S, (float)in.cols) + in.eps));
+    const float inv = inv_rms(S, (float)in.cols, in.eps);
 #pragma unroll
     for (int k = 0; k < KB; k++) {
       const int tb = wave + NW * k;

@@ -69,7 +69,7 @@ __device__ __forceinline__ void norm_rows(const NormTail &t, int b0, int b1) {
     __syncthreads();
     float S = 0.0f;
     for (int k = 0; k < nblk; k++) S = S + bsum[k];
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(S, (float)dim) + t.eps));
+    const float inv = inv_rms(S, (float)dim, t.eps);
 #pragma unroll
     for (int k = 0; k < NORM_NT / NW; k++) {
       const int tb = wave + NW * k, f = tb * 64 + lane;
@@ -1262,7 +1262,7 @@ __global__ __launch_bounds__(512) void k_attn_mt(const AttnArgs a, const StepRec
       if constexpr (DT == 8) ssq = ((t2[0] + t2[1]) + (t2[2] + t2[3])) + ((t2[4] + t2[5]) + (t2[6] + t2[7]));
       else ssq = (t2[0] + t2[1]) + (t2[2] + t2[3]);
     }
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ssq, (float)HD) + a.eps));
+    const float inv = inv_rms(ssq, (float)HD, a.eps);
 #pragma unroll
     for (int kt = 0; kt < DT; kt++) {
       const float4 nq = *reinterpret_cast<const float4 *>(qn_s + kt * 16 + kg);

@@ -415,7 +415,7 @@ __global__ __launch_bounds__(PERSIST_NT) __attribute__((amdgpu_waves_per_eu(2, 2
         __syncthreads();
         float S = 0.0f;
         for (int k = 0; k < nbq; k++) S = S + L.bsum[k];
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(S, (float)dim) + a.eps));
+        const float inv = inv_rms(S, (float)dim, a.eps);
         float pv = 0.0f;
 #pragma unroll
         for (int k = 0; k < KB; k++) {

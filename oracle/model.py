@@ -114,9 +114,12 @@ class OracleModel:
         return att
 
     def norm(self, layer, which, x):
-        """attn_norm ('attn') or ffn_norm ('ffn') of layer on one row x."""
-        ly = self.layers[layer]
-        w = ly.attn_norm if which == "attn" else ly.ffn_norm
+        """attn_norm ('attn') or ffn_norm ('ffn') of layer on one row x; 'out': output_norm."""
+        if which == "out":
+            w = self.m.output_norm
+        else:
+            ly = self.layers[layer]
+            w = ly.attn_norm if which == "attn" else ly.ffn_norm
         out = np.empty(self.cfg.dim, np.float32)
         x = np.ascontiguousarray(x, np.float32)
         ffi.lib.or_rmsnorm(ffi.ptr(x), w, ffi.ptr(out), self.cfg.dim, self.cfg.rms_eps)
@@ -158,3 +161,20 @@ class OracleModel:
         out = np.zeros(self.cfg.dim, np.float32)
         assert ffi.lib.or_down_combine(C.byref(ly.down), k, ffi.ptr(chosen), ffi.ptr(weights), ffi.ptr(h), ffi.ptr(out)) == 0
         return out
+
+    def dense_row(self, layer, xn):
+        """ffn_forward of one ffn-normed row (the fused job with k = 1, w = 1): (out, h) with h the
+        SwiGLU row [1, n_ff]."""
+        ly = self.layers[layer]
+        h = np.full((1, ly.gate.rows), np.nan, np.float32)
+        out = np.zeros(self.cfg.dim, np.float32)
+        e0 = np.zeros(1, np.int32)
+        w1 = np.ones(1, np.float32)
+        xn = np.ascontiguousarray(xn, np.float32)
+        ffi.lib.or_set_dbg_h(ffi.ptr(h))
+        try:
+            assert ffi.lib.or_ffns_fused(C.byref(ly.gate), C.byref(ly.up), C.byref(ly.down), 1, ffi.ptr(e0), ffi.ptr(w1),
+                                         ffi.ptr(xn), ffi.ptr(out)) == 0
+        finally:
+            ffi.lib.or_set_dbg_h(None)
+        return out, h

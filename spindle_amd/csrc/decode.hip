@@ -1017,17 +1017,11 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
 }
 
 // ================================================================== int8 MFMA, 2..16 rows
-// The multi-row kernels' alternative to the per-lane dot chains (the verify pass of the
-// speculative loop): per 256-block the exact integer P = sum_s sc_s S_s, S_s the sub-block's
-// (group's) code x activation dot from v_mfma_i32_16x16x32_i8 (16 vectors x 16 matrix rows),
-// and the exact correction integer C of the reference's block; then per block in order
-// acc = fma(d xd, float(P), acc), corr += (dmin xd) float(C) (Q6_K: (d xd) float(32 C)),
-// out = acc - corr. The integers are the reference's block totals; the fp32 sums take the block
-// total where the reference converts eight lane partials, so the outputs agree to rounding
-// (not bit for bit). Operand layouts of 16x16x32 i8: A[i][k] in lane i + 16 (k / 8), byte k % 8;
-// B[k][j] in lane j + 16 (k / 8); D[i][j] in lane j + 16 (i / 4), element i % 4. A holds the
-// activations (i = vector), B the weight codes (j = matrix row), so lane c16 + 16 k4 owns matrix
-// row c16 for vectors 4 k4 + t: one row's scales and d a lane.
+// The multi-row kernels on the int8 matrix cores (v_mfma_i32_16x16x32_i8; the verify pass of the
+// speculative loop, prefill passes), bit for bit the per-lane dot chains. Operand layouts of
+// 16x16x32 i8: A[i][k] in lane i + 16 (k / 8), byte k % 8; B[k][j] in lane j + 16 (k / 8); D[i][j]
+// in lane j + 16 (i / 4), element i % 4. A holds the activations (i = vector), B the weights
+// (j = matrix row), so lane c16 + 16 k4 owns matrix row c16 for vectors 4 k4 + t.
 typedef int mq_v4i __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ mq_v4i mq_mfma(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1) {
   const long a = (long)(((unsigned long long)a1 << 32) | a0), b = (long)(((unsigned long long)b1 << 32) | b0);
@@ -1039,29 +1033,6 @@ __device__ __forceinline__ int mq_byte(uint4 v, int i) {  // byte i (0..15, cons
 }
 __device__ __forceinline__ int mq_sbyte(uint4 v, int i) { return (int)(int8_t)mq_byte(v, i); }
 
-// Raw bytes of one 256-block of a 16-row tile as a lane loads them: the code words of matrix
-// row lane & 15 for K = 32 (lane >> 4) .. +31 of each sub-block's MFMA, and that row's scales
-// and d. Q4_K: a, b = codes, s = unpacked scales (plane 2), d = d | dmin << 16. Q6_K: a, b = ql,
-// h = qh, s = int8 scales, d = fp16 d.
-struct MqRaw {
-  uint4 a, b, h, s;
-  uint32_t d;
-};
-template <int T>
-__device__ __forceinline__ void mq_load(MqRaw &r, const Planes &pl, int64_t row0, int nrows, int nb, int b) {
-  const int lane = threadIdx.x & 63, c16 = lane & 15, k4 = lane >> 4;
-  const int64_t ra = (row0 + min(c16, nrows - 1)) * nb + b;
-  const uint8_t *cp = pl.p0 + ra * 128 + 32 * k4;
-  r.a = gld<uint4>(cp);
-  r.b = gld<uint4>(cp + 16);
-  r.s = gld<uint4>(pl.p2 + ra * 16);
-  if constexpr (T == T_Q6K) {
-    r.h = gld<uint4>(pl.p1 + ra * 64 + 16 * k4);
-    r.d = gld<uint16_t>(pl.p3 + ra * 2);
-  } else {
-    r.d = gld<uint32_t>(pl.p1 + ra * 16);
-  }
-}
 struct MqIdentity {
   __device__ __forceinline__ int operator()(int v) const { return v; }
 };
@@ -1121,29 +1092,114 @@ __device__ __forceinline__ MqVec mq_vecs(int nv, VR vrow) {
   for (int t = 0; t < 4; t++) v.d[t] = 4 * k4 + t < nv ? vrow(4 * k4 + t) : 0;
   return v;
 }
-// Block b of the tile: acc / cr of matrix row lane & 15, vectors 4 (lane >> 4) + t.
+// ---- the reference's lane classes on the matrix cores
+// The reference's result bits are fixed by eight int32 partials per (row, vector, block),
+// P_l = sum_s sc_s sum_{j<4} q[32s + 4l + j] y[32s + 4l + j] (rows<B,T>, quant_q8k.rs:229-243:
+// maddubs pairs, madd with the sub-block scale), each converted to fp32 and chained per lane
+// class l over the blocks in order (acc_l = fma(d xd, float(P_l), acc_l)) before the 8 -> 1 hsum.
+// Here wavefront l of a workgroup's eight owns lane class l of a 16-row tile and runs its chain.
+// Per block one contraction over the class's 32 codes, K = 4 s + j (lane c16 + 16 k4 holds
+// K = 8 k4 .. 8 k4 + 7: sub-blocks 2 k4 and 2 k4 + 1), with the sub-block scales folded into the
+// weight operand so that D is P_l itself, exactly:
+//   Q4_K: sc (0..63) = 8 sh + sl (3 bits each); operands q sl and q sh (<= 105);
+//         P_l = D(q sl) + 8 D(q sh)
+//   Q6_K: q (0..63) = 8 qh + ql, sc (int8) = 16 sh + sl (sl = sc & 15, sh = sc >> 4 in -8..7);
+//         operands ql sl, qh sl (<= 105) and ql sh, qh sh (-56..49);
+//         P_l = D(ql sl) + 8 D(qh sl) + 16 D(ql sh) + 128 D(qh sh)
+// (|P_l| < 2^25: exact in int32). A 64-code contraction (the x64 MFMA) would add two classes' or
+// two scale digits' sums that the reference keeps apart, so each class takes x32 contractions.
+// The block's correction integer C (mins / -32 term, the reference's per block) stays a block
+// total; wavefront 0 chains it. Then out = ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)) - corr.
+typedef unsigned short mx_u16x2 __attribute__((ext_vector_type(2)));
+// Per byte of v (each <= 15) times s (<= 15) with both products of a 16-bit half <= 105: no
+// carry leaves a byte (v_pk_mul_lo_u16).
+__device__ __forceinline__ uint32_t mx_pmul(uint32_t v, uint32_t s) {
+  const mx_u16x2 a = __builtin_bit_cast(mx_u16x2, v), b = {(unsigned short)s, (unsigned short)s};
+  return __builtin_bit_cast(uint32_t, a * b);
+}
+// Per byte q (0..7) times sh (-8..7) as int8: q (sh + 8) - 8 q, the subtraction kept inside each
+// byte by a bias of 128 (q (sh + 8) <= 105, 8 q <= 56: no borrow leaves a byte).
+__device__ __forceinline__ uint32_t mx_pmul_s(uint32_t q, int sh) {
+  return ((mx_pmul(q, (uint32_t)(sh + 8)) | 0x80808080u) - (q << 3)) ^ 0x80808080u;
+}
+
+// One block's bytes of lane class l as lane c16 + 16 k4 loads them (row ra = row * nb + block):
+// Q4_K a.x = the code word of class l, dword k4 (low nibbles sub-block 2 k4, high 2 k4 + 1),
+// s = the unpacked scales 2 k4, 2 k4 + 1; Q6_K a = the ql words (h = k4 >> 1, m = 0, 1), b = the
+// qh word (h), s = the int8 scales of groups 4 k4 .. 4 k4 + 3; d = fp16 d.
+struct MxRaw {
+  uint2 a;
+  uint32_t b, s, d;
+};
 template <int T>
-__device__ __forceinline__ void mq_block(const MqRaw &r, const MqVec &vv, int nb, int b, const SPX_L uint32_t *lq,
-                                         const SPX_L float *ld, const SPX_L uint32_t *lc, float (&acc)[4], float (&cr)[4]) {
+__device__ __forceinline__ void mx_load(MxRaw &r, const Planes &pl, int64_t ra, int l) {
   const int k4 = (threadIdx.x & 63) >> 4;
-  // A rows past the vectors read vector 0's words: a row of A only reaches the same row of D,
-  // and those rows are never stored
-  const int va = vv.a * nb + b;
-  const SPX_L uint32_t *yp = lq + va * 64 + 16 * k4;
-  const uint4 y0 = lld<uint4>(yp), y1 = lld<uint4>(yp + 4), y2 = lld<uint4>(yp + 8), y3 = lld<uint4>(yp + 12);
-  const uint32_t Y[16] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w, y2.x, y2.y, y2.z, y2.w, y3.x, y3.y, y3.z, y3.w};
-  int P[4] = {0, 0, 0, 0};
+  if constexpr (T == T_Q4K) {
+    r.a.x = gld<uint32_t>(pl.p0 + ra * 128 + 16 * l + 4 * k4);
+    r.s = gld<uint16_t>(pl.p2 + ra * 16 + 2 * k4);
+    r.d = gld<uint16_t>(pl.p1 + ra * 16);
+  } else {
+    r.a = gld<uint2>(pl.p0 + ra * 128 + 16 * l + 8 * (k4 >> 1));
+    r.b = gld<uint32_t>(pl.p1 + ra * 64 + 8 * l + 4 * (k4 >> 1));
+    r.s = gld<uint32_t>(pl.p2 + ra * 16 + 4 * k4);
+    r.d = gld<uint16_t>(pl.p3 + ra * 2);
+  }
+}
+// The correction's operands of a block: the row's whole scale line and Q4_K d | dmin << 16 (Q6_K d).
+struct MxCorr {
+  uint4 s;
+  uint32_t d;
+};
+template <int T>
+__device__ __forceinline__ void mx_load_corr(MxCorr &r, const Planes &pl, int64_t ra) {
+  r.s = gld<uint4>(pl.p2 + ra * 16);
+  r.d = T == T_Q4K ? gld<uint32_t>(pl.p1 + ra * 16) : (uint32_t)gld<uint16_t>(pl.p3 + ra * 2);
+}
+
+// Block b, lane class l: acc[t] of matrix row lane & 15, vector 4 (lane >> 4) + t.
+template <int T>
+__device__ __forceinline__ void mx_block(const MxRaw &r, const MqVec &vv, int nb, int b, int l, const SPX_L uint32_t *lq,
+                                         const SPX_L float *ld, float (&acc)[4]) {
+  const int k4 = (threadIdx.x & 63) >> 4;
+  // A: vector lane & 15's class-l codes of sub-blocks 2 k4, 2 k4 + 1 (rows past the vectors read
+  // vector 0's: a row of A reaches only the same row of D, never stored)
+  const uint2 y = lld<uint2>(lq + (vv.a * nb + b) * 64 + 8 * l + 2 * k4);
+  int P[4];
+  if constexpr (T == T_Q4K) {
+    const uint32_t c0 = r.a.x & 0x0F0F0F0Fu, c1 = (r.a.x >> 4) & 0x0F0F0F0Fu;
+    const uint32_t s0 = r.s & 0xFFu, s1 = (r.s >> 8) & 0xFFu;
+    const mq_v4i Dl = mq_mfma(y.x, y.y, mx_pmul(c0, s0 & 7u), mx_pmul(c1, s1 & 7u));
+    const mq_v4i Dh = mq_mfma(y.x, y.y, mx_pmul(c0, s0 >> 3), mx_pmul(c1, s1 >> 3));
+#pragma unroll
+    for (int t = 0; t < 4; t++) P[t] = Dl[t] + 8 * Dh[t];
+  } else {
+    const int sh = 4 * (k4 & 1), hb = l >= 4 ? 8 : 0;
+    const uint32_t c0 = ((r.a.x >> sh) & 0x0F0F0F0Fu) | (((r.b >> sh) & 0x03030303u) << 4);
+    const uint32_t c1 = ((r.a.y >> sh) & 0x0F0F0F0Fu) | (((r.b >> (sh + 2)) & 0x03030303u) << 4);
+    const int sc0 = (int)(int8_t)(r.s >> hb), sc1 = (int)(int8_t)(r.s >> (16 + hb));
+    const uint32_t l0 = c0 & 0x07070707u, h0 = (c0 >> 3) & 0x07070707u, l1 = c1 & 0x07070707u, h1 = (c1 >> 3) & 0x07070707u;
+    const uint32_t sl0 = (uint32_t)(sc0 & 15), sl1 = (uint32_t)(sc1 & 15);
+    const int sh0 = sc0 >> 4, sh1 = sc1 >> 4;
+    const mq_v4i Dll = mq_mfma(y.x, y.y, mx_pmul(l0, sl0), mx_pmul(l1, sl1));
+    const mq_v4i Dhl = mq_mfma(y.x, y.y, mx_pmul(h0, sl0), mx_pmul(h1, sl1));
+    const mq_v4i Dlh = mq_mfma(y.x, y.y, mx_pmul_s(l0, sh0), mx_pmul_s(l1, sh1));
+    const mq_v4i Dhh = mq_mfma(y.x, y.y, mx_pmul_s(h0, sh0), mx_pmul_s(h1, sh1));
+#pragma unroll
+    for (int t = 0; t < 4; t++) P[t] = Dll[t] + 8 * Dhl[t] + 16 * Dlh[t] + 128 * Dhh[t];
+  }
+  const float d = h2f(r.d);
+#pragma unroll
+  for (int t = 0; t < 4; t++) acc[t] = fmaf(d * ld[vv.d[t] * nb + b], (float)P[t], acc[t]);
+}
+
+// Block b's correction: cr[t] = cr[t] + (dmin xd) float(C) (Q6_K: (d xd) float(32 C)), C the
+// block's exact correction integer from two MFMAs over the staged bsum words (mq_corr_stage).
+template <int T>
+__device__ __forceinline__ void mx_corr(const MxCorr &r, const MqVec &vv, int nb, int b, const SPX_L uint32_t *lc,
+                                        const SPX_L float *ld, float (&cr)[4]) {
+  const int k4 = (threadIdx.x & 63) >> 4, va = vv.a * nb + b;
   mq_v4i C;
   if constexpr (T == T_Q4K) {
-    const uint32_t CA[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, CB[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-#pragma unroll
-    for (int s = 0; s < 8; s++) {
-      const int c = s >> 1, h = s & 1;
-      const mq_v4i S = mq_mfma(Y[s], Y[8 + s], (CA[c] >> (4 * h)) & 0x0F0F0F0Fu, (CB[c] >> (4 * h)) & 0x0F0F0F0Fu);
-      const int sc = mq_byte(r.s, s);
-#pragma unroll
-      for (int t = 0; t < 4; t++) P[t] += __mul24(S[t], sc);
-    }
     // C = sum_s mn_s (bsum_2s + bsum_2s+1): K 0-7 the sums' lo, 8-15 their hi, against the mins
     const uint2 cw = lld<uint2>(lc + va * MQ_CW + 8 + 2 * (k4 & 1));
     const uint32_t a0 = k4 < 2 ? cw.x : 0u, a1 = k4 < 2 ? cw.y : 0u;
@@ -1151,54 +1207,56 @@ __device__ __forceinline__ void mq_block(const MqRaw &r, const MqVec &vv, int nb
     const mq_v4i D2 = mq_mfma(k4 == 1 ? a0 : 0u, k4 == 1 ? a1 : 0u, r.s.z, r.s.w);
 #pragma unroll
     for (int t = 0; t < 4; t++) C[t] = D1[t] + 63 * D2[t];
-    const float d = h2f(r.d), dm = h2f(r.d >> 16);
+    const float dm = h2f(r.d >> 16);
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const float xd = ld[vv.d[t] * nb + b];
-      acc[t] = fmaf(d * xd, (float)P[t], acc[t]);
-      cr[t] = cr[t] + (dm * xd) * (float)C[t];
-    }
-  } else {  // T_Q6K: 16 groups of 16: per sub-block the group 2k alone (the other half's codes
-            // zero) and the whole sub-block, P += (s0 - s1) S0 + s1 S
-    const uint32_t QA[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, QB[4] = {r.b.x, r.b.y, r.b.z, r.b.w}, QH[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
-    const bool lo = k4 < 2;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int h = k >> 2, m = k & 3;
-      const uint32_t c0 = ((QA[2 * h + (m & 1)] >> (4 * (m >> 1))) & 0x0F0F0F0Fu) | (((QH[h] >> (2 * m)) & 0x03030303u) << 4);
-      const uint32_t c1 = ((QB[2 * h + (m & 1)] >> (4 * (m >> 1))) & 0x0F0F0F0Fu) | (((QH[2 + h] >> (2 * m)) & 0x03030303u) << 4);
-      const mq_v4i S0 = mq_mfma(Y[k], Y[8 + k], lo ? c0 : 0u, lo ? c1 : 0u);  // group 2k
-      const mq_v4i S = mq_mfma(Y[k], Y[8 + k], c0, c1);                       // groups 2k and 2k + 1
-      const int s0 = mq_sbyte(r.s, 2 * k), s1 = mq_sbyte(r.s, 2 * k + 1), ds = s0 - s1;
-#pragma unroll
-      for (int t = 0; t < 4; t++) P[t] += __mul24(S0[t], ds) + __mul24(S[t], s1);
-    }
+    for (int t = 0; t < 4; t++) cr[t] = cr[t] + (dm * ld[vv.d[t] * nb + b]) * (float)C[t];
+  } else {
     // C = sum_g sc_g bsum_g: K 0-15 the bsums' lo, 16-31 their hi, against the scales
     const uint2 cw = lld<uint2>(lc + va * MQ_CW + 2 * k4);
     const uint32_t b0 = (k4 & 1) ? r.s.z : r.s.x, b1 = (k4 & 1) ? r.s.w : r.s.y;
+    const bool lo = k4 < 2;
     const mq_v4i D1 = mq_mfma(cw.x, cw.y, b0, b1);
     const mq_v4i D2 = mq_mfma(lo ? 0u : cw.x, lo ? 0u : cw.y, b0, b1);
 #pragma unroll
     for (int t = 0; t < 4; t++) C[t] = D1[t] + 63 * D2[t];
     const float d = h2f(r.d);
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const float xd = ld[vv.d[t] * nb + b];
-      acc[t] = fmaf(d * xd, (float)P[t], acc[t]);
-      cr[t] = cr[t] + (d * xd) * (float)(32 * C[t]);
-    }
+    for (int t = 0; t < 4; t++) cr[t] = cr[t] + (d * ld[vv.d[t] * nb + b]) * (float)(32 * C[t]);
   }
 }
-// Blocks b0, b0 + bstep, ... of a 16-row tile (matrix rows row0 .. row0 + nrows - 1, clamped).
-template <int T>
-__device__ __forceinline__ void mq_tile(const Planes &pl, int64_t row0, int nrows, int nb, int b0, int bstep, const MqVec &vv,
+
+// Lane class l's chain over the blocks of a 16-row tile (matrix rows row0 .. row0 + nrows - 1,
+// clamped), CH blocks' bytes in flight at a time; corr: this wavefront then chains the
+// correction (cr) too.
+template <int T, int CH>
+__device__ __forceinline__ void mx_tile(const Planes &pl, int64_t row0, int nrows, int nb, int l, bool corr, const MqVec &vv,
                                         const SPX_L uint32_t *lq, const SPX_L float *ld, const SPX_L uint32_t *lc, float (&acc)[4],
                                         float (&cr)[4]) {
-  for (int b = b0; b < nb; b += bstep) {
-    MqRaw r;
-    mq_load<T>(r, pl, row0, nrows, nb, b);
-    mq_block<T>(r, vv, nb, b, lq, ld, lc, acc, cr);
+  const int64_t rr = (row0 + min(threadIdx.x & 15, nrows - 1)) * nb;
+  for (int b0 = 0; b0 < nb; b0 += CH) {
+    MxRaw r[CH];
+#pragma unroll
+    for (int k = 0; k < CH; k++) mx_load<T>(r[k], pl, rr + min(b0 + k, nb - 1), l);
+#pragma unroll
+    for (int k = 0; k < CH; k++)
+      if (b0 + k < nb) mx_block<T>(r[k], vv, nb, b0 + k, l, lq, ld, acc);
   }
+  if (!corr) return;
+  for (int b0 = 0; b0 < nb; b0 += CH) {
+    MxCorr r[CH];
+#pragma unroll
+    for (int k = 0; k < CH; k++) mx_load_corr<T>(r[k], pl, rr + min(b0 + k, nb - 1));
+#pragma unroll
+    for (int k = 0; k < CH; k++)
+      if (b0 + k < nb) mx_corr<T>(r[k], vv, nb, b0 + k, lc, ld, cr);
+  }
+}
+
+// The tile's result for vectors 4 (lane >> 4) + q: the eight classes' chains (red[class][q][lane])
+// in the reference's hsum order, minus the correction.
+__device__ __forceinline__ float mx_hsum(const SPX_L float *red, int q, int lane, float corr) {
+  auto a = [&](int c) { return red[(c * 4 + q) * 64 + lane]; };
+  return (((a(0) + a(4)) + (a(2) + a(6))) + ((a(1) + a(5)) + (a(3) + a(7)))) - corr;
 }
 
 // A unit of kd_mq: tile t (segment si, rows row0 .. row0 + nrows - 1), block wave + NW u. The
@@ -1216,12 +1274,12 @@ __device__ __forceinline__ void mq_locate(const DecMMArgs &a, int total, MqPos &
   p.nrows = (int)min((int64_t)16, a.w[p.si].rows - p.row0);
 }
 // Multi-vector matvec on the matrix cores: tiles of 16 rows over up to three segments (the
-// formats may differ by segment), the m vectors' Q8_K staged in LDS; wavefront w of the
-// DEC_MM_NW takes blocks w, w + DEC_MM_NW, ... of each tile. The wavefronts' partials
-// (acc - corr) meet in LDS, two tiles' worth so one barrier a tile suffices, and wavefront
-// q < 4 adds accumulator q (matrix row lane & 15, vector 4 (lane >> 4) + q) in wavefront order
-// and runs the epilogue (residual, greedy keys) as kd_mm does. The correction operands are
-// staged next to the Q8_K image once.
+// formats may differ by segment), the m vectors' Q8_K staged in LDS; wavefront l of the
+// DEC_MM_NW runs lane class l's chain over all blocks of each tile (mx_tile), wavefront 0 also
+// the correction's. The classes' chains meet in LDS, two tiles' worth so one barrier a tile
+// suffices, and wavefront q < 4 forms the reference's hsum for vectors 4 (lane >> 4) + q
+// (matrix row lane & 15) and runs the epilogue (residual, greedy keys) as kd_mm does. The
+// correction operands are staged next to the Q8_K image once.
 //
 // Passes of more than 16 rows (prefill) take the vectors in groups of 16: the launch holds
 // R x groups workgroups; workgroup i = 8k + x (x: its XCD) takes group k mod groups and tile
@@ -1231,6 +1289,7 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
   constexpr int NW = DEC_MM_NW;
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[2][NW][4][64];
+  __shared__ float redc[2][4][64];
   __shared__ unsigned long long sbest[MAX_M];
   const int nvg = (a.m + 15) >> 4;
   int vg = 0, r0 = blockIdx.x, R = gridDim.x;
@@ -1265,23 +1324,17 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
     mq_locate(a, total, p);
     const TensorView &w = a.w[p.si];
     float acc[4] = {0.f, 0.f, 0.f, 0.f}, cr[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int b = wave; b < nb; b += NW) {
-      MqRaw r;
-      if (w.dtype == T_Q4K) {
-        mq_load<T_Q4K>(r, w.pl, p.row0, p.nrows, nb, b);
-        mq_block<T_Q4K>(r, vv, nb, b, lq, ld, lc, acc, cr);
-      } else {
-        mq_load<T_Q6K>(r, w.pl, p.row0, p.nrows, nb, b);
-        mq_block<T_Q6K>(r, vv, nb, b, lq, ld, lc, acc, cr);
-      }
-    }
+    if (w.dtype == T_Q4K) mx_tile<T_Q4K, 8>(w.pl, p.row0, p.nrows, nb, wave, wave == 0, vv, lq, ld, lc, acc, cr);
+    else mx_tile<T_Q6K, 8>(w.pl, p.row0, p.nrows, nb, wave, wave == 0, vv, lq, ld, lc, acc, cr);
 #pragma unroll
-    for (int q = 0; q < 4; q++) red[buf][wave][q][lane] = acc[q] - cr[q];
+    for (int q = 0; q < 4; q++) {
+      red[buf][wave][q][lane] = acc[q];
+      if (wave == 0) redc[buf][q][lane] = cr[q];
+    }
     __syncthreads();
     if (wave < 4) {
       const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
-      float res = red[buf][0][q][lane];
-      for (int w2 = 1; w2 < NW; w2++) res = res + red[buf][w2][q][lane];
+      const float res = mx_hsum((const SPX_L float *)&red[buf][0][0][0], q, lane, redc[buf][q][lane]);
       if (v < m && r < p.nrows) {
         float *const out = a.out[p.si];
         const int64_t row = p.row0 + r, gv = v0 + v;
@@ -1302,17 +1355,18 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
 }
 
 // Routing + gate/up + SwiGLU over the jobs on the matrix cores (kd_gateup_m's prologue, job
-// list and item split; items are (job, 16 h rows)): wavefront w takes blocks w, w + 8, ... of
-// the item's gate and up tiles, alternating gate and up blocks with the next one's bytes
-// requested before the current one is multiplied; the partials (acc - corr) meet in LDS in
-// wavefront order, two items' worth, and wavefront q < 4 applies SwiGLU to accumulator q.
+// list and item split; items are (job, 16 h rows)): wavefront l runs lane class l's chains over
+// all blocks of the item's gate and up tiles (mx_tile; wavefront 0 also the corrections); the
+// chains meet in LDS, two items' worth, and wavefront q < 4 forms the reference's hsum of gate
+// and up for vectors 4 (lane >> 4) + q and applies SwiGLU.
 template <int T>
 __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(T == T_Q4K ? 4 : 2))) void kd_gateup_mq(const DecGateUpMArgs a) {
   constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M;
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ signed char slot_of[MAX_M * 256];
   __shared__ int wcount[NW];
-  __shared__ float red[2][NW][2][4][64];
+  __shared__ float red[2][2][NW][4][64];
+  __shared__ float redc[2][2][4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n_ff = a.n_ff, cols = (int)a.gate.cols, nbq = cols >> 8, nb = nbq, m = a.m;
   const int TX = (n_ff + 15) / 16;
@@ -1342,71 +1396,51 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
   __syncthreads();
   const int n = TX * nj, G = gridDim.x;
   const int i0 = (int)((int64_t)blockIdx.x * n / G), i1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
-  // units of an item: (block wave + NW (u >> 1), gate if u even else up), u < 2 U; each unit's
-  // bytes are loaded while the previous unit is multiplied
-  const int nbw = wave < nb ? (nb - wave + NW - 1) / NW : 0, U2 = 2 * max(nbw, 1);
   const int c16 = lane & 15;
-  auto item_rows = [&](int i, int64_t &row0, int &nrows) {
+  int buf = 0;
+  for (int i = i0; i < i1; i++) {
     const int j = i / TX, x = i - j * TX;
-    const int e = min(max(sj[j * JR], 0), a.gate.n_expert - 1);
-    row0 = (int64_t)e * a.gate.rows + (int64_t)x * 16;
-    nrows = min(16, n_ff - x * 16);
-  };
-  int i = i0, u = 0, buf = 0;
-  int64_t crow0 = 0;
-  int cnrows = 1;
-  if (i < i1) item_rows(i, crow0, cnrows);
-  MqRaw cur, nxt;
-  if (i < i1 && nbw > 0) mq_load<T>(cur, a.gate.pl, crow0, cnrows, nb, wave);
-  float ag[4] = {0.f, 0.f, 0.f, 0.f}, cg[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f}, cu[4] = {0.f, 0.f, 0.f, 0.f};
-  while (i < i1) {
-    int in = i, un = u + 1;
-    if (un >= U2) { un = 0; in++; }
-    int64_t nrow0 = crow0;
-    int nnrows = cnrows;
-    if (un == 0 && in < i1) item_rows(in, nrow0, nnrows);
-    if (in < i1 && nbw > 0) mq_load<T>(nxt, (un & 1) ? a.up.pl : a.gate.pl, nrow0, nnrows, nb, wave + NW * (un >> 1));
-    const int j = i / TX, nv = sj[j * JR + 1];
-    if (nbw > 0) {
-      const MqVec vv = mq_vecs(nv, MqRows{sj + j * JR + 2});
-      if (u & 1) mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lc, au, cu);
-      else mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lc, ag, cg);
-    }
-    if (un == 0) {  // item i complete
+    const int e = min(max(sj[j * JR], 0), a.gate.n_expert - 1), nv = sj[j * JR + 1];
+    const int64_t row0 = (int64_t)e * a.gate.rows + (int64_t)x * 16;
+    const int nrows = min(16, n_ff - x * 16);
+    const MqVec vv = mq_vecs(nv, MqRows{sj + j * JR + 2});
+    float ag[4] = {0.f, 0.f, 0.f, 0.f}, cg[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f}, cu[4] = {0.f, 0.f, 0.f, 0.f};
+    mx_tile<T, 8>(a.gate.pl, row0, nrows, nb, wave, wave == 0, vv, lq, ld, lc, ag, cg);
+    mx_tile<T, 8>(a.up.pl, row0, nrows, nb, wave, wave == 0, vv, lq, ld, lc, au, cu);
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        red[buf][wave][0][q][lane] = ag[q] - cg[q];
-        red[buf][wave][1][q][lane] = au[q] - cu[q];
-        ag[q] = cg[q] = au[q] = cu[q] = 0.f;
-      }
-      __syncthreads();
-      if (wave < 4) {
-        const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
-        float g = red[buf][0][0][q][lane], up = red[buf][0][1][q][lane];
-        for (int w2 = 1; w2 < NW; w2++) { g = g + red[buf][w2][0][q][lane]; up = up + red[buf][w2][1][q][lane]; }
-        const int x = i - j * TX;
-        if (v < nv && r < cnrows) gst<float>(a.h + (int64_t)sj[j * JR + 2 + MAX_M + v] * n_ff + x * 16 + r, g / (1.0f + expf(-g)) * up);
-      }
-      buf ^= 1;
-      crow0 = nrow0;
-      cnrows = nnrows;
+    for (int q = 0; q < 4; q++) {
+      red[buf][0][wave][q][lane] = ag[q];
+      red[buf][1][wave][q][lane] = au[q];
+      if (wave == 0) { redc[buf][0][q][lane] = cg[q]; redc[buf][1][q][lane] = cu[q]; }
     }
-    cur = nxt;
-    i = in;
-    u = un;
+    __syncthreads();
+    if (wave < 4) {
+      const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
+      const float g = mx_hsum((const SPX_L float *)&red[buf][0][0][0][0], q, lane, redc[buf][0][q][lane]);
+      const float up = mx_hsum((const SPX_L float *)&red[buf][1][0][0][0], q, lane, redc[buf][1][q][lane]);
+      if (v < nv && r < nrows) gst<float>(a.h + (int64_t)sj[j * JR + 2 + MAX_M + v] * n_ff + x * 16 + r, g / (1.0f + expf(-g)) * up);
+    }
+    buf ^= 1;
   }
 }
 
-// Down projection of the jobs' users on the matrix cores: items (job, 128 rows), wavefront w
-// takes the 16-row tile w, all its blocks in order; the job's users' h rows are quantized into
-// LDS (quantize_avx2 per 256 block) as kd_down_m does; y per (row, choice) to yd.
+// Down projection of the jobs' users on the matrix cores: items (job, DOWN_MQ_ROWS = 64 rows);
+// the job's users' h rows are quantized into LDS (quantize_avx2 per 256 block) as kd_down_m does;
+// then for each of the item's four 16-row tiles wavefront l runs lane class l's chain over the
+// blocks (mx_tile; wavefront 0 also the corrections), the chains of all four tiles meet in LDS at
+// once, and each wavefront forms the reference's hsum for two (tile, vector group) pairs; y per
+// (row, choice) to yd.
+constexpr int DOWN_MQ_TILES = 4, DOWN_MQ_ROWS = 16 * DOWN_MQ_TILES;
 template <int T>
 __global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_mq(const DecDownMArgs a) {
-  constexpr int NW = DEC_MM_NW, RW = NW * 16, JF = 2 + MAX_M;
+  constexpr int NW = DEC_MM_NW, JF = 2 + MAX_M, NT = DOWN_MQ_TILES;
+  static_assert(NT * 4 == 2 * NW, "two (tile, vector group) pairs a wavefront");
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int s_job[JF];
+  __shared__ float red[NT][NW][4][64];
+  __shared__ float redc[NT][4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, nbh = n_ff >> 8, TX = (dim + RW - 1) / RW;
+  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, nbh = n_ff >> 8, TX = (dim + DOWN_MQ_ROWS - 1) / DOWN_MQ_ROWS;
   SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
   SPX_L float *ld = (SPX_L float *)(smem + (((size_t)MAX_M * n_ff + 15) & ~(size_t)15));
   SPX_L int *lbs = (SPX_L int *)(smem + (((size_t)MAX_M * n_ff + 15) & ~(size_t)15) + (((size_t)MAX_M * nbh * 4 + 15) & ~(size_t)15));
@@ -1443,17 +1477,26 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_mq(const DecDownMArgs 
     __syncthreads();
     mq_corr_stage(nq, (const SPX_L int2 *)lbs, lc);
     __syncthreads();
-    const int64_t r0 = (int64_t)x * RW + wave * 16;
-    if (r0 < dim) {
-      const int nrows = (int)min((int64_t)16, dim - r0);
+    const MqVec vv = mq_vecs(nv, MqIdentity{});
+    const int64_t rx = (int64_t)x * DOWN_MQ_ROWS;
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) {
+      const int64_t r0 = rx + 16 * tt;
       float acc[4] = {0.f, 0.f, 0.f, 0.f}, cr[4] = {0.f, 0.f, 0.f, 0.f};
-      mq_tile<T>(a.w.pl, (int64_t)e * dim + r0, nrows, nbh, 0, 1, mq_vecs(nv, MqIdentity{}), lq, ld, lc, acc, cr);
-      const int r = lane & 15;
+      if (r0 < dim) mx_tile<T, 4>(a.w.pl, (int64_t)e * dim + r0, (int)min((int64_t)16, dim - r0), nbh, wave, wave == 0, vv, lq, ld, lc, acc, cr);
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const int v = 4 * (lane >> 4) + q;
-        if (v < nv && r < nrows) gst<float>(a.yd + (int64_t)s_job[2 + v] * dim + r0 + r, acc[q] - cr[q]);
+        red[tt][wave][q][lane] = acc[q];
+        if (wave == 0) redc[tt][q][lane] = cr[q];
       }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int pi = 2 * wave + k, tt = pi >> 2, q = pi & 3, r = lane & 15, v = 4 * (lane >> 4) + q;
+      const int64_t r0 = rx + 16 * tt;
+      const float y = mx_hsum((const SPX_L float *)&red[tt][0][0][0], q, lane, redc[tt][q][lane]);
+      if (v < nv && r0 + r < dim) gst<float>(a.yd + (int64_t)s_job[2 + v] * dim + r0 + r, y);
     }
     __syncthreads();
   }
@@ -1570,7 +1613,8 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
   constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M;
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int sj[JR];
-  __shared__ float red[2][NW][2][4][64];
+  __shared__ float red[2][2][NW][4][64];
+  __shared__ float redc[2][2][4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n_ff = a.n_ff, cols = (int)a.gate.cols, nb = cols >> 8, m = a.m;
   const int TX = (n_ff + 15) / 16;
@@ -1594,58 +1638,32 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
     mq_corr_stage(sj[1] * nb, lbs, lc);
     __syncthreads();
   };
-  const int nbw = wave < nb ? (nb - wave + NW - 1) / NW : 0, U2 = 2 * max(nbw, 1);
   const int c16 = lane & 15;
-  auto item_rows = [&](int i, int64_t &row0, int &nrows) {
+  int buf = 0;
+  for (int i = i0; i < i1; i++) {
     const int j = i / TX, x = i - j * TX;
-    const int e = jobs ? min(max(gld<int>(reinterpret_cast<const int *>(jobs + j)), 0), a.gate.n_expert - 1) : 0;
-    row0 = (int64_t)e * a.gate.rows + (int64_t)x * 16;
-    nrows = min(16, n_ff - x * 16);
-  };
-  int i = i0, u = 0, buf = 0;
-  int64_t crow0 = 0;
-  int cnrows = 1;
-  if (i < i1) item_rows(i, crow0, cnrows);
-  MqRaw cur, nxt;
-  if (i < i1 && nbw > 0) mq_load<T>(cur, a.gate.pl, crow0, cnrows, nb, wave);
-  if (i < i1) stage_job(i / TX);
-  float ag[4] = {0.f, 0.f, 0.f, 0.f}, cg[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f}, cu[4] = {0.f, 0.f, 0.f, 0.f};
-  while (i < i1) {
-    int in = i, un = u + 1;
-    if (un >= U2) { un = 0; in++; }
-    int64_t nrow0 = crow0;
-    int nnrows = cnrows;
-    if (un == 0 && in < i1) item_rows(in, nrow0, nnrows);
-    if (in < i1 && nbw > 0) mq_load<T>(nxt, (un & 1) ? a.up.pl : a.gate.pl, nrow0, nnrows, nb, wave + NW * (un >> 1));
-    const int j = i / TX, nv = sj[1];
-    if (nbw > 0) {
-      const MqVec vv = mq_vecs(nv, MqIdentity{});
-      if (u & 1) mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lc, au, cu);
-      else mq_block<T>(cur, vv, nb, wave + NW * (u >> 1), lq, ld, lc, ag, cg);
-    }
-    if (un == 0) {  // item i complete
+    if (i == i0 || x == 0) stage_job(j);
+    const int e = jobs ? min(max(sj[0], 0), a.gate.n_expert - 1) : 0, nv = sj[1];
+    const int64_t row0 = (int64_t)e * a.gate.rows + (int64_t)x * 16;
+    const int nrows = min(16, n_ff - x * 16);
+    const MqVec vv = mq_vecs(nv, MqIdentity{});
+    float ag[4] = {0.f, 0.f, 0.f, 0.f}, cg[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f}, cu[4] = {0.f, 0.f, 0.f, 0.f};
+    mx_tile<T, 8>(a.gate.pl, row0, nrows, nb, wave, wave == 0, vv, lq, ld, lc, ag, cg);
+    mx_tile<T, 8>(a.up.pl, row0, nrows, nb, wave, wave == 0, vv, lq, ld, lc, au, cu);
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        red[buf][wave][0][q][lane] = ag[q] - cg[q];
-        red[buf][wave][1][q][lane] = au[q] - cu[q];
-        ag[q] = cg[q] = au[q] = cu[q] = 0.f;
-      }
-      __syncthreads();
-      if (wave < 4) {
-        const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
-        float g = red[buf][0][0][q][lane], up = red[buf][0][1][q][lane];
-        for (int w2 = 1; w2 < NW; w2++) { g = g + red[buf][w2][0][q][lane]; up = up + red[buf][w2][1][q][lane]; }
-        const int x = i - j * TX;
-        if (v < nv && r < cnrows) gst<float>(a.h + (int64_t)sj[2 + MAX_M + v] * n_ff + x * 16 + r, g / (1.0f + expf(-g)) * up);
-      }
-      buf ^= 1;
-      crow0 = nrow0;
-      cnrows = nnrows;
-      if (in < i1 && in / TX != j) stage_job(in / TX);
+    for (int q = 0; q < 4; q++) {
+      red[buf][0][wave][q][lane] = ag[q];
+      red[buf][1][wave][q][lane] = au[q];
+      if (wave == 0) { redc[buf][0][q][lane] = cg[q]; redc[buf][1][q][lane] = cu[q]; }
     }
-    cur = nxt;
-    i = in;
-    u = un;
+    __syncthreads();
+    if (wave < 4) {
+      const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
+      const float g = mx_hsum((const SPX_L float *)&red[buf][0][0][0][0], q, lane, redc[buf][0][q][lane]);
+      const float up = mx_hsum((const SPX_L float *)&red[buf][1][0][0][0], q, lane, redc[buf][1][q][lane]);
+      if (v < nv && r < nrows) gst<float>(a.h + (int64_t)sj[2 + MAX_M + v] * n_ff + x * 16 + r, g / (1.0f + expf(-g)) * up);
+    }
+    buf ^= 1;
   }
 }
 
@@ -1872,7 +1890,7 @@ hipError_t launch_kp_gateup_mq(const DecGateUpMArgs &a, const Job *jobs, const i
 
 hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s) {
   if (a.w.cols % 256 || a.w.nb > 4 || a.max_jobs < 1 || a.max_jobs > 512 || !a.h || !a.yd) return hipErrorInvalidValue;
-  const int tx = (int)((a.w.rows + DEC_MM_NW * 16 - 1) / (DEC_MM_NW * 16));
+  const int tx = (int)((a.w.rows + DOWN_MQ_ROWS - 1) / DOWN_MQ_ROWS);
   const dim3 grid((unsigned)std::min(tx * a.max_jobs, 2 * cu_count())), b(DEC_MM_NW * 64);
   const size_t sm = downm_lds_bytes((int)a.w.cols) + mq_corr_bytes(MAX_M, (int)a.w.cols);
   if (a.w.dtype == T_Q4K) hipLaunchKernelGGL((kd_down_mq<T_Q4K>), grid, b, sm, s, a);

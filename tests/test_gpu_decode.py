@@ -10,6 +10,7 @@ import pytest
 
 from spindle_amd import model as M
 from oracle.model import OracleModel
+from tests import layer_pins as LP
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -156,13 +157,18 @@ def test_decode_pipeline_matches_oracle(ctx, case):
         want = om.logits(om.forward(ids[pos:pos + 1], pos))[0].astype(np.float64)
         e = float(np.max(np.abs(lg[0] - want)) / max(1.0, float(np.max(np.abs(want)))))
         errs.append(e)
-        if e > 1e-3:  # a Q8_K code moved by one step (see test_gpu_engine.py)
-            assert e <= 5e-2, (case, pos, e)
+        if e > 1e-3:  # traced layer by layer: every stage pinned, every moved Q8_K code one step
+            LP.report(case, f"step at {pos} ({e:.1e})", LP.layer_pins(eng, om, cfg, ids[pos:pos + 1], pos, lambda: _sync(eng, om), case))
             flips += 1
-    print(f"{case}: logits err median {np.median(errs):.1e} max {max(errs):.1e}, flip steps {flips}")
-    assert flips <= 0.15 * len(errs)
+    print(f"{case}: logits err median {np.median(errs):.1e} max {max(errs):.1e}, steps traced to Q8_K steps {flips}")
     assert np.median(errs) <= 1e-5
     eng.close()
+
+
+def _sync(eng, om):
+    k, v = eng.kv_cache()
+    om.k_cache[:] = k
+    om.v_cache[:] = v
 
 
 @pytest.mark.parametrize("case", list(CASES))
@@ -201,39 +207,34 @@ def _margin(logits):
     return top[1] - top[0]
 
 
-@pytest.mark.parametrize("case", [c for c in CASES if CASES[c].n_expert <= 64])
+@pytest.mark.parametrize("case", list(CASES))
 def test_multi_row_passes_mfma(ctx, case):
-    """Passes of 2..16 rows on the int8 matrix cores against the lane-exact kernels, pass by pass
-    on one engine (each pass is run both ways over the same KV cache, the lane-exact run last).
-    The block integers are exact and only the fp32 sums round differently, so a pass agrees to
-    ~1e-7 relative; that last-bit difference can move a downstream Q8_K code (or, in a MoE pass,
-    a near-tied expert choice), a larger but bounded step (the same allowance as the oracle tests
-    give re-quantized passes; it shows with the gate/up projections on the lane-exact kernels
-    too, so it is the amplification, not one kernel). Greedy picks agree except at near-ties."""
+    """Passes of 2..16 rows on the int8 matrix cores (the default: each wavefront contracts one of
+    the reference's eight lane classes and runs its fp32 chain) against the lane-exact kernels:
+    the same bits for every row (hidden state, logits, picks, routing statistics, KV cache),
+    128-expert cases included; and so the same bits as one-row passes (the reference's batch
+    invariance, quant_q8k.rs:413-442)."""
     cfg = CASES[case]
     w = M.synth_model(cfg, seed=35)
-    e = M.Engine(ctx, cfg, w)
+    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    a.set_mfma(True)
+    b.set_mfma(False)
     ids = np.random.default_rng(7).integers(0, cfg.vocab, 120)
     pos = 0
-    errs = []
     for m in (16, 5, 2, 9, 16, 3, 12, 16, 7, 4, 11):
-        e.set_mfma(True)
-        am1, h1, l1 = e.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
-        e.set_mfma(False)
-        am0, h0, l0 = e.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
-        el = _rel(l1, l0)
-        errs.append(el)
-        assert el <= 5e-2 and _rel(h1, h0) <= 5e-2, (case, m, pos, el)
-        for r in np.nonzero(am0 != am1)[0]:
-            mg = _margin(l0[r] / cfg.logit_scale)
-            assert mg < max(1e-4, 2 * el * float(np.max(np.abs(l0[r])))), (case, m, pos, r, mg)
-            print(f"{case}: pick differs at pos {pos + r} on a near-tie (margin {mg:.2e})")
+        am0, h0, l0 = a.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        am1, h1, l1 = b.forward(ids[pos:pos + m], pos, hidden=True, logits=True)
+        assert _same(h0, h1), (case, m, pos, "hidden", _rel(h0, h1))
+        assert _same(l0, l1), (case, m, pos, "logits", _rel(l0, l1))
+        assert np.array_equal(am0, am1), (case, m, pos)
+        if cfg.moe:
+            assert np.array_equal(a.last_experts(), b.last_experts()), (case, m, pos)
         pos += m
-    big = sum(x > 1e-5 for x in errs)
-    print(f"{case}: logits rel median {np.median(errs):.1e} max {max(errs):.1e}, passes above 1e-5: {big}")
-    assert np.median(errs) <= 1e-5
-    assert big <= len(errs) // 2
-    e.close()
+    ka, va = a.kv_cache()
+    kb, vb = b.kv_cache()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    a.close()
+    b.close()
 
 
 @pytest.mark.parametrize("case", list(CASES))

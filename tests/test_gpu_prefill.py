@@ -2,10 +2,11 @@
 smollm_chat.rs:3090-3101) on the prefill kernels: the matvecs in 16-vector groups, the
 attention rows prepared once, MoE jobs of at most 16 users staged job by job.
 
-A row's arithmetic in these kernels is the same as in a pass of at most 16 rows on the int8
-matrix cores (the same block split, the same fp32 sums in the same order), so the bar is
-bitwise: hidden states, logits, greedy picks and the KV cache of a 128-row pass equal those of
-the same tokens in 16-row passes. The 16-row passes are held to the oracle by
+A row's arithmetic in these kernels is the reference's: each wavefront of a matvec contracts one
+of its eight lane classes on the int8 matrix cores and runs that class's fp32 chain (the same
+bits as the per-lane dot kernels and as one-row passes). So the bar is bitwise: hidden states,
+logits, greedy picks and the KV cache of a 128-row pass equal those of the same tokens in
+passes of at most 16 rows on the lane-exact kernels. Those are held to the oracle by
 test_gpu_decode.py / test_gpu_engine.py; the prefill pass is also checked against the oracle
 directly with the bars of those tests."""
 import numpy as np
@@ -13,6 +14,7 @@ import pytest
 
 from spindle_amd import model as M
 from oracle.model import OracleModel
+from tests import layer_pins as LP
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -44,14 +46,8 @@ def _same(a, b):
 
 
 def _split16(n):
-    """Pass sizes of at most 16 rows for n rows, none below 4 unless n is: passes of 1 row run
-    on the one-row pipeline and passes of 2-3 rows take the per-lane down kernel, whose fp32
-    sums round differently from the matrix cores'."""
-    sizes = [16] * (n // 16) + ([n % 16] if n % 16 else [])
-    if len(sizes) > 1 and sizes[-1] < 4:
-        sizes[-2] -= 4 - sizes[-1]
-        sizes[-1] = 4
-    return sizes
+    """Pass sizes of at most 16 rows for n rows (a ragged last pass of 1..15 rows included)."""
+    return [16] * (n // 16) + ([n % 16] if n % 16 else [])
 
 
 def _in16(eng, ids, pos):
@@ -69,6 +65,7 @@ def test_prefill_pass_equals_16_row_passes(ctx, case):
     w = M.synth_model(cfg, seed=41)
     a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
     assert a.decode_pipeline()
+    b.set_mfma(False)  # the reference: passes of at most 16 rows on the lane-exact kernels
     ids = np.random.default_rng(9).integers(0, cfg.vocab, sum(SIZES))
     pos = 0
     for m in SIZES:
@@ -91,10 +88,11 @@ def test_prefill_pass_equals_16_row_passes(ctx, case):
 @pytest.mark.parametrize("case", ["a3b", "moe"])
 def test_prefill_long_context(ctx, case):
     """128-row passes past 1024 positions (17+ attention chunks, two merge levels; 128 rows x 8
-    query heads = 64 query tiles a kv head) against 16-row passes, bitwise."""
+    query heads = 64 query tiles a kv head) against lane-exact 16-row passes, bitwise."""
     cfg = CASES[case].replace(max_seq=1280)
     w = M.synth_model(cfg, seed=42)
     a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    b.set_mfma(False)
     ids = np.random.default_rng(10).integers(0, cfg.vocab, 1240)
     for s0 in range(0, 1240, 128):
         n = min(128, 1240 - s0)
@@ -117,9 +115,10 @@ def _norm_err(x, y):
 def test_prefill_matches_oracle(ctx, case):
     """A 128-row pass against the oracle, row by row on the pass's own context: after the GPU
     pass the oracle gets the GPU's KV cache and computes row p alone at position p (positions
-    below p from the GPU's cache), so a Q8_K rounding flip in one row does not carry into the
-    rows after it through attention. Bars of the integer-path tests: logits median <= 1e-5;
-    rows above 1e-3 are such flips, at most 15% of rows and 5e-2 each."""
+    below p from the GPU's cache), so a Q8_K rounding step in one row does not carry into the
+    rows after it through attention. Logits median <= 1e-5; a row above 1e-3 is traced layer by
+    layer (the pass's rows are one-row passes' bits): every stage pinned, every moved Q8_K code
+    a single step."""
     cfg = CASES[case]
     w = M.synth_model(cfg, seed=43)
     eng = M.Engine(ctx, cfg, w)
@@ -136,8 +135,13 @@ def test_prefill_matches_oracle(ctx, case):
     errs = np.array(errs)
     print(f"{case}: logits err median {np.median(errs):.1e} max {errs.max():.1e}, rows above 1e-3: {(errs > 1e-3).sum()}")
     assert np.median(errs) <= 1e-5
-    assert errs.max() <= 5e-2
-    assert (errs > 1e-3).sum() <= 0.15 * len(errs)
+
+    def sync():
+        kk, vv = eng.kv_cache()
+        om.k_cache[:] = kk
+        om.v_cache[:] = vv
+    for p in np.nonzero(errs > 1e-3)[0]:
+        LP.report(case, f"row {p} ({errs[p]:.1e})", LP.layer_pins(eng, om, cfg, ids[p:p + 1], int(p), sync, case))
     eng.close()
 
 

@@ -343,15 +343,17 @@ def main():
         # diverse routing: token embeddings scaled up so that each row's residual stream is its
         # own and the 9 rows of a pass choose experts nearly independently (a random-init model
         # otherwise drifts to a common hidden direction over a long context)
+        # (at the headline context: the whole prompt prefilled first)
         ed = M.Engine(ctx, cfg.replace(embedding_scale=40.0), w)
-        tk, _ = prefill(ed, prompt[:1024])
+        tk, _ = prefill(ed, prompt)
         ids9 = np.random.default_rng(args.seed).integers(0, cfg.vocab, 9).astype(np.int32)
-        dv_us = time_pass(ed, ids9, 1024)
+        dv_us = time_pass(ed, ids9, len(prompt))
         dv_exp = ed.last_experts()
-        dv_bytes = decode_bytes(cfg, specs, 1032, dv_exp)
+        dv_bytes = decode_bytes(cfg, specs, len(prompt) + 8, dv_exp)
         legs["verify_m9_diverse_routing"] = {"pass_us": round(dv_us, 1), "unique_experts_per_layer": round(float(np.mean(dv_exp)), 1),
                                              "gb_per_pass": round(dv_bytes / 1e9, 4), "hbm_gbs": round(dv_bytes / dv_us / 1e3, 1),
-                                             "context": 1033}
+                                             "roofline_frac": round(dv_bytes / dv_us / 1e3 / HBM_PEAK_GBS, 4),
+                                             "context": len(prompt) + 9}
         log(f"M=9 diverse routing: {legs['verify_m9_diverse_routing']}")
         ed.close()
         del w

@@ -194,9 +194,12 @@ __host__ __device__ inline size_t gum_lds_bytes(int m, int cols, int max_jobs) {
 
 hipError_t launch_dec_norm(const DecNormArgs &a, int m, hipStream_t s);
 hipError_t launch_dec_mm(const DecMMArgs &a, int grid, hipStream_t s);
-// The same matvec on the int8 matrix cores (16-row tiles; block totals exact, fp32 sums to
-// rounding): tiles[i] counts 16-row tiles; tiles stride over the grid.
+// The same matvec on the int8 matrix cores (16-row tiles, a wavefront per tile; the reference's
+// per-lane-class int32 partials and fp32 chains, so the results are kd_mm's bit for bit):
+// tiles[i] counts 16-row tiles; tiles stride over the grid's wavefronts.
 hipError_t launch_dec_mq(const DecMMArgs &a, int grid, hipStream_t s);
+// The blocks-per-row counts (cols / 256) the matrix-core kernels take: 1, 2, 3, 4, 8, 16.
+bool dec_mq_nb_ok(int nb);
 // kd_mq's grid argument for a number of tiles and m vectors: up to 16 vectors, workgroups (at
 // most two a CU); more (prefill), tile ranges, a multiple of eight (the launch holds
 // ceil(m / 16) workgroups per range). With greedy keys, nbest = this value.

@@ -15,6 +15,7 @@
 // for bit, as the fused pipeline's (same operations in the same order: the norm's fixed-order
 // sum, quantize_avx2, the reference's per-lane integer-dot chain, the router's lane chains
 // and wave tree, the combine's chosen-order sum); only where the work is done changes.
+#include <type_traits>
 #include "decode.h"
 #include "decode_dev.h"
 #include "dev.h"
@@ -471,8 +472,10 @@ __host__ __device__ inline size_t mm_lds_bytes(int m, int cols) { return mm_act_
 
 // Copies m permuted Q8_K vectors (global y, cols columns; vector v from y's vector vsrc[v],
 // or v) into LDS (lq, ld, lbs), all threads; each thread's loads go out before its stores.
+// vs4: 16-byte words a vector row of lq (0: cols / 16, rows back to back).
 template <int NT, class VP = const int *>
-__device__ __forceinline__ void stage_q8(const Q8KP &y, VP vsrc, int m, int cols, SPX_L uint32_t *lq, SPX_L float *ld, SPX_L int2 *lbs) {
+__device__ __forceinline__ void stage_q8(const Q8KP &y, VP vsrc, int m, int cols, SPX_L uint32_t *lq, SPX_L float *ld, SPX_L int2 *lbs,
+                                         int vs4 = 0) {
   const int nbq = cols >> 8, n16 = cols / 16, nb16 = nbq * 4, nq = m * n16, nb4 = m * nb16;
   const int tid = threadIdx.x;
   for (int i0 = tid; i0 < nq; i0 += 4 * NT) {  // loads of four rounds go out before their stores
@@ -488,7 +491,10 @@ __device__ __forceinline__ void stage_q8(const Q8KP &y, VP vsrc, int m, int cols
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int i = i0 + k * NT;
-      if (i < nq) lst<uint4>((SPX_L uint4 *)lq + i, t[k]);
+      if (i < nq) {
+        const int v = i / n16;
+        lst<uint4>((SPX_L uint4 *)lq + (vs4 ? v * vs4 + (i - v * n16) : i), t[k]);
+      }
     }
   }
   for (int i0 = tid; i0 < nb4; i0 += 2 * NT) {
@@ -813,11 +819,14 @@ struct StageQ8 {
     for (int k = 0; k < ND; k++)
       if (t + k * NT < nd) d[k] = gld<float>(y.d + t + k * NT);
   }
-  __device__ __forceinline__ void put(int m, int cols, SPX_L uint32_t *lq, SPX_L float *ld, SPX_L int2 *lbs) const {
-    const int nbq = cols >> 8, nq = m * (cols / 16), nb4 = m * nbq * 4, nd = m * nbq, t = threadIdx.x;
+  // vs4: 16-byte words a vector row of lq (0: cols / 16, rows back to back)
+  __device__ __forceinline__ void put(int m, int cols, SPX_L uint32_t *lq, SPX_L float *ld, SPX_L int2 *lbs, int vs4 = 0) const {
+    const int nbq = cols >> 8, n16 = cols / 16, nq = m * n16, nb4 = m * nbq * 4, nd = m * nbq, t = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < NQ; k++)
-      if (t + k * NT < nq) lst<uint4>((SPX_L uint4 *)lq + t + k * NT, q[k]);
+    for (int k = 0; k < NQ; k++) {
+      const int i = t + k * NT, v = i / n16;
+      if (i < nq) lst<uint4>((SPX_L uint4 *)lq + (vs4 ? v * vs4 + (i - v * n16) : i), q[k]);
+    }
 #pragma unroll
     for (int k = 0; k < NS; k++)
       if (t + k * NT < nb4) lst<uint4>((SPX_L uint4 *)lbs + t + k * NT, bs[k]);
@@ -1027,6 +1036,10 @@ __device__ __forceinline__ mq_v4i mq_mfma(uint32_t a0, uint32_t a1, uint32_t b0,
   const long a = (long)(((unsigned long long)a1 << 32) | a0), b = (long)(((unsigned long long)b1 << 32) | b0);
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, mq_v4i{0, 0, 0, 0}, 0, 0, 0);
 }
+__device__ __forceinline__ mq_v4i mq_mfma_c(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, mq_v4i c) {
+  const long a = (long)(((unsigned long long)a1 << 32) | a0), b = (long)(((unsigned long long)b1 << 32) | b0);
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ int mq_byte(uint4 v, int i) {  // byte i (0..15, constant after unrolling)
   const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
   return (int)((w >> (8 * (i & 3))) & 0xffu);
@@ -1048,34 +1061,9 @@ struct MqRows {
 // sub-blocks). The correction C = sum sc bs is then two MFMAs: D1 over lo and hi, D2 over hi
 // alone, C = D1 + 63 D2 (exact).
 constexpr int MQ_CW = 12;  // words a (vector, block)
-__host__ __device__ inline size_t mq_corr_bytes(int m, int cols) { return (size_t)m * (cols >> 8) * MQ_CW * 4; }
 __device__ __forceinline__ uint32_t mq_pack4(int a, int b, int c, int d) {
   return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)(d & 255) << 24);
 }
-__device__ __forceinline__ void mq_corr_stage(int nq, const SPX_L int2 *lbs, SPX_L uint32_t *lc) {
-  for (int q = threadIdx.x; q < nq; q += blockDim.x) {
-    int bs[16];
-#pragma unroll
-    for (int i = 0; i < 8; i++) { const int2 v = lld<int2>(lbs + q * 8 + i); bs[2 * i] = v.x; bs[2 * i + 1] = v.y; }
-    uint32_t w[MQ_CW];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      w[i] = mq_pack4(bs[4 * i] & 63, bs[4 * i + 1] & 63, bs[4 * i + 2] & 63, bs[4 * i + 3] & 63);
-      w[4 + i] = mq_pack4(bs[4 * i] >> 6, bs[4 * i + 1] >> 6, bs[4 * i + 2] >> 6, bs[4 * i + 3] >> 6);
-    }
-    int s32[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) s32[i] = bs[2 * i] + bs[2 * i + 1];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      w[8 + i] = mq_pack4(s32[4 * i] & 63, s32[4 * i + 1] & 63, s32[4 * i + 2] & 63, s32[4 * i + 3] & 63);
-      w[10 + i] = mq_pack4(s32[4 * i] >> 6, s32[4 * i + 1] >> 6, s32[4 * i + 2] >> 6, s32[4 * i + 3] >> 6);
-    }
-#pragma unroll
-    for (int i = 0; i < MQ_CW; i += 4) lst<uint4>((SPX_L uint4 *)(lc + q * MQ_CW + i), make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]));
-  }
-}
-
 // The tile's vectors: the A operand's vector (lane & 15) and the D elements' vectors
 // 4 (lane >> 4) + t, as rows of the LDS Q8_K image (row 0 stands in past the last vector).
 struct MqVec {
@@ -1097,10 +1085,10 @@ __device__ __forceinline__ MqVec mq_vecs(int nv, VR vrow) {
 // P_l = sum_s sc_s sum_{j<4} q[32s + 4l + j] y[32s + 4l + j] (rows<B,T>, quant_q8k.rs:229-243:
 // maddubs pairs, madd with the sub-block scale), each converted to fp32 and chained per lane
 // class l over the blocks in order (acc_l = fma(d xd, float(P_l), acc_l)) before the 8 -> 1 hsum.
-// Here wavefront l of a workgroup's eight owns lane class l of a 16-row tile and runs its chain.
-// Per block one contraction over the class's 32 codes, K = 4 s + j (lane c16 + 16 k4 holds
-// K = 8 k4 .. 8 k4 + 7: sub-blocks 2 k4 and 2 k4 + 1), with the sub-block scales folded into the
-// weight operand so that D is P_l itself, exactly:
+// Here one wavefront owns a tile of 16 matrix rows x 16 vectors and all eight classes: per block
+// and class one contraction over the class's 32 codes, K = 4 s + j (lane c16 + 16 k4 holds
+// K = 8 k4 .. 8 k4 + 7: sub-blocks 2 k4 and 2 k4 + 1), with the sub-block scales folded into
+// the weight operand so that D is P_l itself, exactly:
 //   Q4_K: sc (0..63) = 8 sh + sl (3 bits each); operands q sl and q sh (<= 105);
 //         P_l = D(q sl) + 8 D(q sh)
 //   Q6_K: q (0..63) = 8 qh + ql, sc (int8) = 16 sh + sl (sl = sc & 15, sh = sc >> 4 in -8..7);
@@ -1108,9 +1096,14 @@ __device__ __forceinline__ MqVec mq_vecs(int nv, VR vrow) {
 //         P_l = D(ql sl) + 8 D(qh sl) + 16 D(ql sh) + 128 D(qh sh)
 // (|P_l| < 2^25: exact in int32). A 64-code contraction (the x64 MFMA) would add two classes' or
 // two scale digits' sums that the reference keeps apart, so each class takes x32 contractions.
-// The block's correction integer C (mins / -32 term, the reference's per block) stays a block
-// total; wavefront 0 chains it. Then out = ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)) - corr.
+// The eight chains stay in the lane's registers (acc[l][t]: matrix row lane & 15, vector
+// 4 (lane >> 4) + t), the block's correction integer C (mins / -32 term, the reference's per
+// block) is chained beside them, and out = ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)) - corr
+// needs no other wavefront.
 typedef unsigned short mx_u16x2 __attribute__((ext_vector_type(2)));
+// Lambdas of the matrix-core walks are inlined: a lambda left out of line would take its
+// array arguments (the block ring, a tile's results) through scratch memory.
+#define SPX_AI __attribute__((always_inline))
 // Per byte of v (each <= 15) times s (<= 15) with both products of a 16-bit half <= 105: no
 // carry leaves a byte (v_pk_mul_lo_u16).
 __device__ __forceinline__ uint32_t mx_pmul(uint32_t v, uint32_t s) {
@@ -1123,148 +1116,429 @@ __device__ __forceinline__ uint32_t mx_pmul_s(uint32_t q, int sh) {
   return ((mx_pmul(q, (uint32_t)(sh + 8)) | 0x80808080u) - (q << 3)) ^ 0x80808080u;
 }
 
-// One block's bytes of lane class l as lane c16 + 16 k4 loads them (row ra = row * nb + block):
-// Q4_K a.x = the code word of class l, dword k4 (low nibbles sub-block 2 k4, high 2 k4 + 1),
-// s = the unpacked scales 2 k4, 2 k4 + 1; Q6_K a = the ql words (h = k4 >> 1, m = 0, 1), b = the
-// qh word (h), s = the int8 scales of groups 4 k4 .. 4 k4 + 3; d = fp16 d.
-struct MxRaw {
-  uint2 a;
-  uint32_t b, s, d;
+// 4 x 4 transpose over the wavefront's four 16-lane rows: row g of r[c] holds M[g][c] on entry
+// and M[c][g] on return (v_permlane32_swap: rows 2, 3 of the first operand <-> rows 0, 1 of the
+// second; v_permlane16_swap: rows 1, 3 of the first <-> rows 0, 2 of the second).
+__device__ __forceinline__ void mw_t4(uint32_t (&r)[4]) {
+  const auto p = __builtin_amdgcn_permlane32_swap(r[0], r[2], false, false);
+  const auto q = __builtin_amdgcn_permlane32_swap(r[1], r[3], false, false);
+  const auto u = __builtin_amdgcn_permlane16_swap(p[0], q[0], false, false);
+  const auto v = __builtin_amdgcn_permlane16_swap(p[1], q[1], false, false);
+  r[0] = u[0];
+  r[1] = u[1];
+  r[2] = v[0];
+  r[3] = v[1];
+}
+// The same for rows (a, a, b, b): three swaps.
+__device__ __forceinline__ void mw_t4d(uint32_t a, uint32_t b, uint32_t (&r)[4]) {
+  const auto p = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  const auto u = __builtin_amdgcn_permlane16_swap(p[0], p[0], false, false);
+  const auto v = __builtin_amdgcn_permlane16_swap(p[1], p[1], false, false);
+  r[0] = u[0];
+  r[1] = u[1];
+  r[2] = v[0];
+  r[3] = v[1];
+}
+
+// The LDS image of a tile's vectors (at most 16): codes lq (vector v's block b at dword
+// v mw_vs + 64 b; eight pad dwords a vector put the sixteen vectors' reads of one class word in
+// different banks), block scales ld [v nb + b], bsum pairs lbs [v nb + b][8], and the
+// correction words lc (vector v's block b at v mw_cs + MQ_CW b, padded likewise).
+__host__ __device__ inline int mw_vs(int nb) { return nb * 64 + 8; }
+__host__ __device__ inline int mw_cs(int nb) { return nb * MQ_CW + ((8 - nb * MQ_CW) % 64 + 64) % 64; }
+__host__ __device__ inline size_t mw_act_bytes(int m, int nb) {
+  return (size_t)m * mw_vs(nb) * 4 + (((size_t)m * nb * 4 + 15) & ~(size_t)15) + (size_t)m * nb * 64 + (size_t)m * mw_cs(nb) * 4;
+}
+struct MwLds {
+  SPX_L uint32_t *lq;
+  SPX_L float *ld;
+  SPX_L int2 *lbs;
+  SPX_L uint32_t *lc;
 };
-template <int T>
-__device__ __forceinline__ void mx_load(MxRaw &r, const Planes &pl, int64_t ra, int l) {
-  const int k4 = (threadIdx.x & 63) >> 4;
-  if constexpr (T == T_Q4K) {
-    r.a.x = gld<uint32_t>(pl.p0 + ra * 128 + 16 * l + 4 * k4);
-    r.s = gld<uint16_t>(pl.p2 + ra * 16 + 2 * k4);
-    r.d = gld<uint16_t>(pl.p1 + ra * 16);
-  } else {
-    r.a = gld<uint2>(pl.p0 + ra * 128 + 16 * l + 8 * (k4 >> 1));
-    r.b = gld<uint32_t>(pl.p1 + ra * 64 + 8 * l + 4 * (k4 >> 1));
-    r.s = gld<uint32_t>(pl.p2 + ra * 16 + 4 * k4);
-    r.d = gld<uint16_t>(pl.p3 + ra * 2);
+__device__ __forceinline__ MwLds mw_lds(uint8_t *base, int m, int nb) {
+  MwLds L;
+  size_t o = (size_t)m * mw_vs(nb) * 4;
+  L.lq = (SPX_L uint32_t *)base;
+  L.ld = (SPX_L float *)(base + o);
+  o += ((size_t)m * nb * 4 + 15) & ~(size_t)15;
+  L.lbs = (SPX_L int2 *)(base + o);
+  o += (size_t)m * nb * 64;
+  L.lc = (SPX_L uint32_t *)(base + o);
+  return L;
+}
+// The correction words of the image's m vectors (from the staged bsum pairs).
+__device__ __forceinline__ void mq_corr_stage(int m, int nb, const SPX_L int2 *lbs, SPX_L uint32_t *lc) {
+  const int cs = mw_cs(nb);
+  for (int q = threadIdx.x; q < m * nb; q += blockDim.x) {
+    int bs[16];
+#pragma unroll
+    for (int i = 0; i < 8; i++) { const int2 v = lld<int2>(lbs + q * 8 + i); bs[2 * i] = v.x; bs[2 * i + 1] = v.y; }
+    uint32_t w[MQ_CW];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      w[i] = mq_pack4(bs[4 * i] & 63, bs[4 * i + 1] & 63, bs[4 * i + 2] & 63, bs[4 * i + 3] & 63);
+      w[4 + i] = mq_pack4(bs[4 * i] >> 6, bs[4 * i + 1] >> 6, bs[4 * i + 2] >> 6, bs[4 * i + 3] >> 6);
+    }
+    int s32[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) s32[i] = bs[2 * i] + bs[2 * i + 1];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      w[8 + i] = mq_pack4(s32[4 * i] & 63, s32[4 * i + 1] & 63, s32[4 * i + 2] & 63, s32[4 * i + 3] & 63);
+      w[10 + i] = mq_pack4(s32[4 * i] >> 6, s32[4 * i + 1] >> 6, s32[4 * i + 2] >> 6, s32[4 * i + 3] >> 6);
+    }
+    const int v = q / nb, b = q - v * nb;
+    SPX_L uint32_t *o = lc + v * cs + b * MQ_CW;
+#pragma unroll
+    for (int i = 0; i < MQ_CW; i += 4) lst<uint4>((SPX_L uint4 *)(o + i), make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]));
   }
 }
-// The correction's operands of a block: the row's whole scale line and Q4_K d | dmin << 16 (Q6_K d).
-struct MxCorr {
-  uint4 s;
+
+// One block of a tile as lane c16 + 16 k4 loads it, from matrix row c16's bytes in 16-byte
+// pieces (the row's four lanes read its 128 code bytes as two 64-byte halves): Q4_K c[e] = code
+// dwords 16 e + 4 k4 .. + 3; Q6_K c[e] = ql dwords 16 e + 4 k4 .. + 3 and h[e] = qh dwords
+// 8 e + 2 k4, + 1; s = the row's scale line (Q4_K: 8 scales, 8 mins; Q6_K: 16 int8 scales);
+// d = Q4_K d | dmin << 16, Q6_K d.
+struct MwRaw {
+  uint4 c[2], s;
+  uint2 h[2];
   uint32_t d;
 };
-template <int T>
-__device__ __forceinline__ void mx_load_corr(MxCorr &r, const Planes &pl, int64_t ra) {
-  r.s = gld<uint4>(pl.p2 + ra * 16);
-  r.d = T == T_Q4K ? gld<uint32_t>(pl.p1 + ra * 16) : (uint32_t)gld<uint16_t>(pl.p3 + ra * 2);
+// A tile's planes at its first row (wave-uniform: scalar registers) and this lane's row as a
+// block offset from there, so the loads take a scalar base and a 32-bit lane offset.
+struct MwSrc {
+  const uint8_t *p0, *p1, *p2, *p3;
+  int rb;  // (row c16, clamped to the tile) x nb
+  int dt;
+};
+__device__ __forceinline__ int64_t mw_uni64(int64_t v) {
+  const uint64_t u = (uint64_t)v;
+  return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(u >> 32)) << 32) | (uint32_t)__builtin_amdgcn_readfirstlane((int)u));
 }
-
-// Block b, lane class l: acc[t] of matrix row lane & 15, vector 4 (lane >> 4) + t.
-template <int T>
-__device__ __forceinline__ void mx_block(const MxRaw &r, const MqVec &vv, int nb, int b, int l, const SPX_L uint32_t *lq,
-                                         const SPX_L float *ld, float (&acc)[4]) {
+__device__ __forceinline__ MwSrc mw_src(const Planes &pl, int dt, int64_t row0, int nrows, int nb) {
+  const int64_t r0 = mw_uni64(row0) * nb;
+  MwSrc s;
+  s.dt = __builtin_amdgcn_readfirstlane(dt);
+  s.p0 = pl.p0 + r0 * 128;
+  s.p2 = pl.p2 + r0 * 16;
+  if (s.dt == T_Q4K) {
+    s.p1 = pl.p1 + r0 * 16;
+    s.p3 = s.p1;
+  } else {
+    s.p1 = pl.p1 + r0 * 64;
+    s.p3 = pl.p3 + r0 * 2;
+  }
+  s.rb = min((int)(threadIdx.x & 15), __builtin_amdgcn_readfirstlane(nrows) - 1) * nb;
+  return s;
+}
+template <int TT>  // TT: the tile's format when fixed for the launch, 0: s.dt at run time
+__device__ __forceinline__ void mw_fetch(MwRaw &r, const MwSrc &s, int b) {
+  const uint32_t k4 = (threadIdx.x & 63) >> 4, ob = (uint32_t)(s.rb + b);
+  r.c[0] = gld<uint4>(s.p0 + (ob * 128u + 16u * k4));
+  r.c[1] = gld<uint4>(s.p0 + (ob * 128u + 16u * k4 + 64u));
+  r.s = gld<uint4>(s.p2 + ob * 16u);
+  if (TT == T_Q4K || (TT == 0 && s.dt == T_Q4K)) {
+    r.d = gld<uint32_t>(s.p1 + ob * 16u);
+  } else {
+    r.h[0] = gld<uint2>(s.p1 + (ob * 64u + 8u * k4));
+    r.h[1] = gld<uint2>(s.p1 + (ob * 64u + 8u * k4 + 32u));
+    r.d = gld<uint16_t>(s.p3 + ob * 2u);
+  }
+}
+// The tile's LDS operands for this lane: A (vector lane & 15's class words, dword 2 k4 of each),
+// its correction words, the block scales of vectors 4 (lane >> 4) + t. Rows of A past the
+// vectors read vector 0's: a row of A reaches only the same row of D, never stored.
+struct MwDst {
+  const SPX_L uint32_t *py, *pw;
+  const SPX_L float *px[4];
+  int dt;
+};
+__device__ __forceinline__ MwDst mw_dst(const MwLds &L, const MqVec &vv, int nb, int dt) {
   const int k4 = (threadIdx.x & 63) >> 4;
-  // A: vector lane & 15's class-l codes of sub-blocks 2 k4, 2 k4 + 1 (rows past the vectors read
-  // vector 0's: a row of A reaches only the same row of D, never stored)
-  const uint2 y = lld<uint2>(lq + (vv.a * nb + b) * 64 + 8 * l + 2 * k4);
-  int P[4];
+  MwDst d;
+  d.dt = dt;
+  d.py = L.lq + vv.a * mw_vs(nb) + 2 * k4;
+  d.pw = L.lc + vv.a * mw_cs(nb);
+#pragma unroll
+  for (int t = 0; t < 4; t++) d.px[t] = L.ld + vv.d[t] * nb;
+  return d;
+}
+
+// The lane classes a wavefront takes: part C of WPT (WPT 1: all eight; 2: C, C + 2, C + 4, C + 6;
+// 4: p and p + 4 with p = 0, 2, 1, 3 for C = 0 .. 3); slot j of its chains holds class
+// mw_cls<WPT, C>(j). The parts' partial sums then meet in the reference's hsum order
+// ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)): WPT 2: A0 + A1 with
+// A_C = (a_C + a_C+4) + (a_C+2 + a_C+6); WPT 4: (P0 + P1) + (P2 + P3) with P_C = a_p + a_p+4.
+// Part 0 also chains the correction.
+template <int WPT, int C>
+__host__ __device__ constexpr int mw_cls(int j) {
+  return WPT == 1 ? j : WPT == 2 ? C + 2 * j : (C == 0 ? 0 : C == 1 ? 2 : C == 2 ? 1 : 3) + 4 * j;
+}
+template <int WPT, int C>
+__host__ __device__ constexpr int mw_slot(int l) {  // the slot of class l, -1: another part's
+  for (int j = 0; j < 8 / WPT; j++)
+    if (mw_cls<WPT, C>(j) == l) return j;
+  return -1;
+}
+
+// One block's integers and scale factors for part C: P[j] = P_l of class slot j (D rows: vectors
+// 4 (lane >> 4) + t, columns: matrix rows), Cc the correction integer (part 0; Q6_K 32 C), dx[t] =
+// d xd and cf[t] = dmin xd (Q6_K d xd). The arithmetic of several blocks is issued before their
+// fp32 chains advance (mw_chain), so the matrix-core latencies overlap.
+template <int WPT>
+struct MwProd {
+  mq_v4i P[8 / WPT], Cc;
+  float dx[4], cf[4];
+};
+
+// Q6_K classes 4 E .. 4 E + 3 of a block (those of part C) from its ql words c (dwords
+// 16 E + 4 k4 ..) and qh words h (dwords 8 E + 2 k4, + 1); sw = the lane's four int8 scales
+// (groups 4 k4 .. 4 k4 + 3). P = D(ql sl) + 8 (D(qh sl) + 2 (D(ql sh) + 8 D(qh sh))), the
+// digits accumulated on the matrix core (exact in int32).
+template <int E, int WPT, int C>
+__device__ __forceinline__ void mw_q6_half(const uint4 &c, const uint2 &h, uint32_t sw, const SPX_L uint32_t *py, mq_v4i (&P)[8 / WPT]) {
+  const int sh = 4 * ((threadIdx.x >> 4) & 1);
+  uint32_t q0[4], q1[4], qh[4];
+  mw_t4d(c.x, c.z, q0);
+  mw_t4d(c.y, c.w, q1);
+  mw_t4d(h.x, h.y, qh);
+  const int sc0 = (int)(int8_t)(sw >> (8 * E)), sc1 = (int)(int8_t)(sw >> (16 + 8 * E));
+  const uint32_t sl0 = (uint32_t)(sc0 & 15), sl1 = (uint32_t)(sc1 & 15);
+  const int sh0 = sc0 >> 4, sh1 = sc1 >> 4;
+  uint32_t l0[4], h0[4], l1[4], h1[4];
+  uint2 y[4];
+#pragma unroll
+  for (int a = 0; a < 4; a++) {
+    if (mw_slot<WPT, C>(4 * E + a) < 0) continue;
+    const uint32_t c0 = ((q0[a] >> sh) & 0x0F0F0F0Fu) | (((qh[a] >> sh) & 0x03030303u) << 4);
+    const uint32_t c1 = ((q1[a] >> sh) & 0x0F0F0F0Fu) | (((qh[a] >> (sh + 2)) & 0x03030303u) << 4);
+    l0[a] = c0 & 0x07070707u;
+    h0[a] = (c0 >> 3) & 0x07070707u;
+    l1[a] = c1 & 0x07070707u;
+    h1[a] = (c1 >> 3) & 0x07070707u;
+    y[a] = lld<uint2>(py + 8 * (4 * E + a));
+  }
+  // the classes' digit contractions interleaved, one dependent step at a time
+#pragma unroll
+  for (int a = 0; a < 4; a++) {
+    const int j = mw_slot<WPT, C>(4 * E + a);
+    if (j >= 0) P[j] = mq_mfma(y[a].x, y[a].y, mx_pmul_s(h0[a], sh0), mx_pmul_s(h1[a], sh1)) * 8;
+  }
+#pragma unroll
+  for (int a = 0; a < 4; a++) {
+    const int j = mw_slot<WPT, C>(4 * E + a);
+    if (j >= 0) P[j] = mq_mfma_c(y[a].x, y[a].y, mx_pmul_s(l0[a], sh0), mx_pmul_s(l1[a], sh1), P[j]) * 2;
+  }
+#pragma unroll
+  for (int a = 0; a < 4; a++) {
+    const int j = mw_slot<WPT, C>(4 * E + a);
+    if (j >= 0) P[j] = mq_mfma_c(y[a].x, y[a].y, mx_pmul(h0[a], sl0), mx_pmul(h1[a], sl1), P[j]) * 8;
+  }
+#pragma unroll
+  for (int a = 0; a < 4; a++) {
+    const int j = mw_slot<WPT, C>(4 * E + a);
+    if (j >= 0) P[j] = mq_mfma_c(y[a].x, y[a].y, mx_pmul(l0[a], sl0), mx_pmul(l1[a], sl1), P[j]);
+  }
+}
+
+// Block b of a tile, part C: its integers (mw_prod). The class words are regrouped across the
+// four 16-lane rows (mw_t4): lane row k4 then holds, for class l, the code word of sub-blocks
+// 2 k4, 2 k4 + 1 (Q4_K dword 4 l + k4; Q6_K ql dwords 4 l + 2 (k4 >> 1) + 0, 1 and qh dword
+// 2 l + (k4 >> 1)).
+template <int T, int WPT, int C>
+__device__ __forceinline__ void mw_prod(const MwRaw &r, const MwDst &d, int b, MwProd<WPT> &o) {
+  const int k4 = (threadIdx.x & 63) >> 4;
+  const SPX_L uint32_t *py = d.py + b * 64, *pw = d.pw + b * MQ_CW;
+  float xd[4];
+  const float dd = h2f(r.d);
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    xd[t] = d.px[t][b];
+    o.dx[t] = dd * xd[t];
+  }
   if constexpr (T == T_Q4K) {
-    const uint32_t c0 = r.a.x & 0x0F0F0F0Fu, c1 = (r.a.x >> 4) & 0x0F0F0F0Fu;
-    const uint32_t s0 = r.s & 0xFFu, s1 = (r.s >> 8) & 0xFFu;
-    const mq_v4i Dl = mq_mfma(y.x, y.y, mx_pmul(c0, s0 & 7u), mx_pmul(c1, s1 & 7u));
-    const mq_v4i Dh = mq_mfma(y.x, y.y, mx_pmul(c0, s0 >> 3), mx_pmul(c1, s1 >> 3));
+    uint32_t w[2][4] = {{r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w}, {r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w}};
+    mw_t4(w[0]);
+    mw_t4(w[1]);
+    const uint32_t sw = k4 < 2 ? r.s.x : r.s.y, sp = (k4 & 1) ? sw >> 16 : sw;
+    const uint32_t s0 = sp & 0xFFu, s1 = (sp >> 8) & 0xFFu;
+    const uint32_t lo0 = s0 & 7u, hi0 = s0 >> 3, lo1 = s1 & 7u, hi1 = s1 >> 3;
+    // P = D(q sl) + 8 D(q sh), the digits accumulated on the matrix core (exact in int32); the
+    // classes interleaved four at a time
+    constexpr int CG = 8 / WPT < 4 ? 8 / WPT : 4;
 #pragma unroll
-    for (int t = 0; t < 4; t++) P[t] = Dl[t] + 8 * Dh[t];
+    for (int j0 = 0; j0 < 8 / WPT; j0 += CG) {
+      uint32_t c0[CG], c1[CG];
+      uint2 y[CG];
+#pragma unroll
+      for (int q = 0; q < CG; q++) {
+        const int l = mw_cls<WPT, C>(j0 + q);
+        const uint32_t wl = w[l >> 2][l & 3];
+        c0[q] = wl & 0x0F0F0F0Fu;
+        c1[q] = (wl >> 4) & 0x0F0F0F0Fu;
+        y[q] = lld<uint2>(py + 8 * l);
+      }
+#pragma unroll
+      for (int q = 0; q < CG; q++) o.P[j0 + q] = mq_mfma(y[q].x, y[q].y, mx_pmul(c0[q], hi0), mx_pmul(c1[q], hi1)) * 8;
+#pragma unroll
+      for (int q = 0; q < CG; q++) o.P[j0 + q] = mq_mfma_c(y[q].x, y[q].y, mx_pmul(c0[q], lo0), mx_pmul(c1[q], lo1), o.P[j0 + q]);
+    }
+    if (C == 0) {
+      // C = sum_s mn_s (bsum_2s + bsum_2s+1): K 0-7 the sums' lo, 8-15 their hi, against the mins
+      const uint2 cw = lld<uint2>(pw + 8 + 2 * (k4 & 1));
+      const uint32_t a0 = k4 < 2 ? cw.x : 0u, a1 = k4 < 2 ? cw.y : 0u;
+      o.Cc = mq_mfma_c(a0, a1, r.s.z, r.s.w, mq_mfma(k4 == 1 ? a0 : 0u, k4 == 1 ? a1 : 0u, r.s.z, r.s.w) * 63);
+      const float dm = h2f(r.d >> 16);
+#pragma unroll
+      for (int t = 0; t < 4; t++) o.cf[t] = dm * xd[t];
+    }
   } else {
-    const int sh = 4 * (k4 & 1), hb = l >= 4 ? 8 : 0;
-    const uint32_t c0 = ((r.a.x >> sh) & 0x0F0F0F0Fu) | (((r.b >> sh) & 0x03030303u) << 4);
-    const uint32_t c1 = ((r.a.y >> sh) & 0x0F0F0F0Fu) | (((r.b >> (sh + 2)) & 0x03030303u) << 4);
-    const int sc0 = (int)(int8_t)(r.s >> hb), sc1 = (int)(int8_t)(r.s >> (16 + hb));
-    const uint32_t l0 = c0 & 0x07070707u, h0 = (c0 >> 3) & 0x07070707u, l1 = c1 & 0x07070707u, h1 = (c1 >> 3) & 0x07070707u;
-    const uint32_t sl0 = (uint32_t)(sc0 & 15), sl1 = (uint32_t)(sc1 & 15);
-    const int sh0 = sc0 >> 4, sh1 = sc1 >> 4;
-    const mq_v4i Dll = mq_mfma(y.x, y.y, mx_pmul(l0, sl0), mx_pmul(l1, sl1));
-    const mq_v4i Dhl = mq_mfma(y.x, y.y, mx_pmul(h0, sl0), mx_pmul(h1, sl1));
-    const mq_v4i Dlh = mq_mfma(y.x, y.y, mx_pmul_s(l0, sh0), mx_pmul_s(l1, sh1));
-    const mq_v4i Dhh = mq_mfma(y.x, y.y, mx_pmul_s(h0, sh0), mx_pmul_s(h1, sh1));
+    // the lane's scale dword k4, by shifts of the line (a select among the raw fields would have
+    // the compiler index the block buffer in scratch memory)
+    const uint64_t s01 = ((uint64_t)r.s.y << 32) | r.s.x, s23 = ((uint64_t)r.s.w << 32) | r.s.z;
+    const uint32_t sw = (uint32_t)(((k4 & 2) ? s23 : s01) >> (32 * (k4 & 1)));
+    mw_q6_half<0, WPT, C>(r.c[0], r.h[0], sw, py, o.P);
+    mw_q6_half<1, WPT, C>(r.c[1], r.h[1], sw, py, o.P);
+    if (C == 0) {
+      // C = sum_g sc_g bsum_g: K 0-15 the bsums' lo, 16-31 their hi, against the scales
+      const uint2 cw = lld<uint2>(pw + 2 * k4);
+      const uint32_t b0 = (k4 & 1) ? r.s.z : r.s.x, b1 = (k4 & 1) ? r.s.w : r.s.y;
+      const bool lo = k4 < 2;
+      o.Cc = mq_mfma_c(cw.x, cw.y, b0, b1, mq_mfma(lo ? 0u : cw.x, lo ? 0u : cw.y, b0, b1) * 63) * 32;
 #pragma unroll
-    for (int t = 0; t < 4; t++) P[t] = Dll[t] + 8 * Dhl[t] + 16 * Dlh[t] + 128 * Dhh[t];
+      for (int t = 0; t < 4; t++) o.cf[t] = dd * xd[t];
+    }
   }
-  const float d = h2f(r.d);
+}
+// The chains advance by one block: acc_l = fma(d xd, float(P_l), acc_l) and, part 0,
+// corr = corr + (dmin xd) float(C) (Q6_K (d xd) float(32 C)).
+template <int WPT, int C>
+__device__ __forceinline__ void mw_chain(const MwProd<WPT> &o, float (&acc)[8 / WPT][4], float (&cr)[4]) {
 #pragma unroll
-  for (int t = 0; t < 4; t++) acc[t] = fmaf(d * ld[vv.d[t] * nb + b], (float)P[t], acc[t]);
+  for (int j = 0; j < 8 / WPT; j++)
+#pragma unroll
+    for (int t = 0; t < 4; t++) acc[j][t] = fmaf(o.dx[t], (float)o.P[j][t], acc[j][t]);
+  if (C == 0)
+#pragma unroll
+    for (int t = 0; t < 4; t++) cr[t] = cr[t] + o.cf[t] * (float)o.Cc[t];
 }
 
-// Block b's correction: cr[t] = cr[t] + (dmin xd) float(C) (Q6_K: (d xd) float(32 C)), C the
-// block's exact correction integer from two MFMAs over the staged bsum words (mq_corr_stage).
-template <int T>
-__device__ __forceinline__ void mx_corr(const MxCorr &r, const MqVec &vv, int nb, int b, const SPX_L uint32_t *lc,
-                                        const SPX_L float *ld, float (&cr)[4]) {
-  const int k4 = (threadIdx.x & 63) >> 4, va = vv.a * nb + b;
-  mq_v4i C;
-  if constexpr (T == T_Q4K) {
-    // C = sum_s mn_s (bsum_2s + bsum_2s+1): K 0-7 the sums' lo, 8-15 their hi, against the mins
-    const uint2 cw = lld<uint2>(lc + va * MQ_CW + 8 + 2 * (k4 & 1));
-    const uint32_t a0 = k4 < 2 ? cw.x : 0u, a1 = k4 < 2 ? cw.y : 0u;
-    const mq_v4i D1 = mq_mfma(a0, a1, r.s.z, r.s.w);
-    const mq_v4i D2 = mq_mfma(k4 == 1 ? a0 : 0u, k4 == 1 ? a1 : 0u, r.s.z, r.s.w);
+// The walk of one wavefront (part C of WPT) over its tiles 0 .. ntiles - 1: tile i's bytes from
+// src(i), its LDS operands from dst(i). A tile's blocks are taken in stages of PD (mw_pd: NB up
+// to three blocks a row, two at four, else four); each block's bytes are requested one stage
+// ahead of its arithmetic into a ring of PD buffers (the next tile's first stage during the last
+// one, the last tile's first stage again at the end), the same loads on every path, so the
+// compiler's wait for a block leaves the PD later blocks in flight. done(i, part, cr) takes
+// tile i's partial sums part[t] (WPT 1: the whole hsum less the correction; matrix row lane & 15,
+// vector 4 (lane >> 4) + t) and, part 0, the correction chain cr; a done() with barriers is met
+// by every wavefront of the workgroup as long as they walk the same number of tiles.
+template <int NB>
+constexpr int mw_pd() { return NB <= 3 ? NB : NB == 4 ? 2 : 4; }
+template <int NB, int TT, int WPT, int C, class Src, class Dst, class Done>
+__device__ __forceinline__ void mw_walk(int ntiles, Src src, Dst dst, Done done) {
+  constexpr int PD = mw_pd<NB>(), NS = NB / PD, CPW = 8 / WPT;
+  constexpr int BB = WPT == 4 ? PD : WPT == 2 && PD % 2 == 0 ? 2 : 1;  // blocks whose integers are issued together
+  static_assert(NB % PD == 0, "whole stages");
+  if (ntiles <= 0) return;
+  MwRaw r[PD];
+  MwSrc sc = src(0);
 #pragma unroll
-    for (int t = 0; t < 4; t++) C[t] = D1[t] + 63 * D2[t];
-    const float dm = h2f(r.d >> 16);
+  for (int p = 0; p < PD; p++) mw_fetch<TT>(r[p], sc, p);
+  for (int i = 0; i < ntiles; i++) {
+    const MwDst dc = dst(i);
+    const MwSrc sn = i + 1 < ntiles ? src(i + 1) : sc;
+    float acc[CPW][4], cr[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) cr[t] = cr[t] + (dm * ld[vv.d[t] * nb + b]) * (float)C[t];
+    for (int t = 0; t < 4; t++) {
+      cr[t] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPW; j++) acc[j][t] = 0.0f;
+    }
+    for (int st = 0; st < NS; st++) {
+      const bool last = st == NS - 1;
+      // the stage's integers in groups of BB blocks, then their chains in block order
+#pragma unroll
+      for (int p0 = 0; p0 < PD; p0 += BB) {
+        MwProd<WPT> pr[BB];
+#pragma unroll
+        for (int q = 0; q < BB; q++) {
+          if (TT == T_Q4K || (TT == 0 && dc.dt == T_Q4K)) mw_prod<T_Q4K, WPT, C>(r[p0 + q], dc, st * PD + p0 + q, pr[q]);
+          else mw_prod<T_Q6K, WPT, C>(r[p0 + q], dc, st * PD + p0 + q, pr[q]);
+        }
+#pragma unroll
+        for (int q = 0; q < BB; q++) mw_chain<WPT, C>(pr[q], acc, cr);
+      }
+#pragma unroll
+      for (int p = 0; p < PD; p++) {
+        const int b = st * PD + p;
+        MwSrc fs;
+        fs.p0 = last ? sn.p0 : sc.p0;
+        fs.p1 = last ? sn.p1 : sc.p1;
+        fs.p2 = last ? sn.p2 : sc.p2;
+        fs.p3 = last ? sn.p3 : sc.p3;
+        fs.rb = last ? sn.rb : sc.rb;
+        fs.dt = last ? sn.dt : sc.dt;
+        mw_fetch<TT>(r[p], fs, last ? p : b + PD);
+      }
+    }
+    float part[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      if constexpr (WPT == 1)
+        part[t] = (((acc[0][t] + acc[4][t]) + (acc[2][t] + acc[6][t])) + ((acc[1][t] + acc[5][t]) + (acc[3][t] + acc[7][t]))) - cr[t];
+      else if constexpr (WPT == 2)
+        part[t] = (acc[0][t] + acc[2][t]) + (acc[1][t] + acc[3][t]);
+      else
+        part[t] = acc[0][t] + acc[1][t];
+    }
+    done(i, part, cr);
+    sc = sn;
+  }
+}
+// The walk of part c (wave-uniform) of WPT: one instance per part.
+template <int NB, int TT, int WPT, class Src, class Dst, class Done>
+__device__ __forceinline__ void mw_walk_part(int c, int ntiles, Src src, Dst dst, Done done) {
+  if constexpr (WPT == 1) {
+    mw_walk<NB, TT, 1, 0>(ntiles, src, dst, done);
+  } else if constexpr (WPT == 2) {
+    if (c == 0) mw_walk<NB, TT, 2, 0>(ntiles, src, dst, done);
+    else mw_walk<NB, TT, 2, 1>(ntiles, src, dst, done);
   } else {
-    // C = sum_g sc_g bsum_g: K 0-15 the bsums' lo, 16-31 their hi, against the scales
-    const uint2 cw = lld<uint2>(lc + va * MQ_CW + 2 * k4);
-    const uint32_t b0 = (k4 & 1) ? r.s.z : r.s.x, b1 = (k4 & 1) ? r.s.w : r.s.y;
-    const bool lo = k4 < 2;
-    const mq_v4i D1 = mq_mfma(cw.x, cw.y, b0, b1);
-    const mq_v4i D2 = mq_mfma(lo ? 0u : cw.x, lo ? 0u : cw.y, b0, b1);
+    switch (c) {
+    case 0: mw_walk<NB, TT, 4, 0>(ntiles, src, dst, done); break;
+    case 1: mw_walk<NB, TT, 4, 1>(ntiles, src, dst, done); break;
+    case 2: mw_walk<NB, TT, 4, 2>(ntiles, src, dst, done); break;
+    default: mw_walk<NB, TT, 4, 3>(ntiles, src, dst, done); break;
+    }
+  }
+}
+// The parts' partial sums of a tile meet in LDS (xch: [WPT][4][64] floats of the tile's parts, one
+// barrier; the caller alternates two such areas between tiles): part 0 returns the tile's
+// results (hsum order as at mw_cls, less the correction), other parts return zeros.
+template <int WPT>
+__device__ __forceinline__ void mw_meet(SPX_L float *xch, int c, const float (&part)[4], const float (&cr)[4], float (&out)[4]) {
+  const int lane = threadIdx.x & 63;
+  if constexpr (WPT == 1) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) C[t] = D1[t] + 63 * D2[t];
-    const float d = h2f(r.d);
+    for (int t = 0; t < 4; t++) out[t] = part[t];
+  } else {
 #pragma unroll
-    for (int t = 0; t < 4; t++) cr[t] = cr[t] + (d * ld[vv.d[t] * nb + b]) * (float)(32 * C[t]);
+    for (int t = 0; t < 4; t++) xch[(c * 4 + t) * 64 + lane] = part[t];
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      auto P = [&](int q) { return xch[(q * 4 + t) * 64 + lane]; };
+      if constexpr (WPT == 2) out[t] = c == 0 ? (part[t] + P(1)) - cr[t] : 0.0f;
+      else out[t] = c == 0 ? ((part[t] + P(1)) + (P(2) + P(3))) - cr[t] : 0.0f;
+    }
   }
 }
 
-// Lane class l's chain over the blocks of a 16-row tile (matrix rows row0 .. row0 + nrows - 1,
-// clamped), CH blocks' bytes in flight at a time; corr: this wavefront then chains the
-// correction (cr) too.
-template <int T, int CH>
-__device__ __forceinline__ void mx_tile(const Planes &pl, int64_t row0, int nrows, int nb, int l, bool corr, const MqVec &vv,
-                                        const SPX_L uint32_t *lq, const SPX_L float *ld, const SPX_L uint32_t *lc, float (&acc)[4],
-                                        float (&cr)[4]) {
-  const int64_t rr = (row0 + min(threadIdx.x & 15, nrows - 1)) * nb;
-  for (int b0 = 0; b0 < nb; b0 += CH) {
-    MxRaw r[CH];
-#pragma unroll
-    for (int k = 0; k < CH; k++) mx_load<T>(r[k], pl, rr + min(b0 + k, nb - 1), l);
-#pragma unroll
-    for (int k = 0; k < CH; k++)
-      if (b0 + k < nb) mx_block<T>(r[k], vv, nb, b0 + k, l, lq, ld, acc);
-  }
-  if (!corr) return;
-  for (int b0 = 0; b0 < nb; b0 += CH) {
-    MxCorr r[CH];
-#pragma unroll
-    for (int k = 0; k < CH; k++) mx_load_corr<T>(r[k], pl, rr + min(b0 + k, nb - 1));
-#pragma unroll
-    for (int k = 0; k < CH; k++)
-      if (b0 + k < nb) mx_corr<T>(r[k], vv, nb, b0 + k, lc, ld, cr);
-  }
-}
-
-// The tile's result for vectors 4 (lane >> 4) + q: the eight classes' chains (red[class][q][lane])
-// in the reference's hsum order, minus the correction.
-__device__ __forceinline__ float mx_hsum(const SPX_L float *red, int q, int lane, float corr) {
-  auto a = [&](int c) { return red[(c * 4 + q) * 64 + lane]; };
-  return (((a(0) + a(4)) + (a(2) + a(6))) + ((a(1) + a(5)) + (a(3) + a(7)))) - corr;
-}
-
-// A unit of kd_mq: tile t (segment si, rows row0 .. row0 + nrows - 1), block wave + NW u. The
-// bookkeeping is wave-uniform and kept scalar (readfirstlane), so the segment's fields are read
-// from the arguments with scalar loads: a vector load between a block's loads and their use
-// would wait for every load in flight.
+// A unit of kd_mq: tile t (segment si, rows row0 .. row0 + nrows - 1). The bookkeeping is
+// wave-uniform and kept scalar (readfirstlane), so the segment's fields are read from the
+// arguments with scalar loads.
 struct MqPos {
-  int t, u, si, nrows;
+  int t, si, nrows;
   int64_t row0;
 };
 __device__ __forceinline__ void mq_locate(const DecMMArgs &a, int total, MqPos &p) {
@@ -1274,23 +1548,24 @@ __device__ __forceinline__ void mq_locate(const DecMMArgs &a, int total, MqPos &
   p.nrows = (int)min((int64_t)16, a.w[p.si].rows - p.row0);
 }
 // Multi-vector matvec on the matrix cores: tiles of 16 rows over up to three segments (the
-// formats may differ by segment), the m vectors' Q8_K staged in LDS; wavefront l of the
-// DEC_MM_NW runs lane class l's chain over all blocks of each tile (mx_tile), wavefront 0 also
-// the correction's. The classes' chains meet in LDS, two tiles' worth so one barrier a tile
-// suffices, and wavefront q < 4 forms the reference's hsum for vectors 4 (lane >> 4) + q
-// (matrix row lane & 15) and runs the epilogue (residual, greedy keys) as kd_mm does. The
-// correction operands are staged next to the Q8_K image once.
+// formats may differ by segment), the m vectors' Q8_K staged in LDS with their correction
+// words. A tile is walked by WPT wavefronts (mw_walk, each a part of the lane classes; their
+// partial sums meet in LDS), so a workgroup of MW_NW walks TP = MW_NW / WPT tiles at a time:
+// round i of workgroup r takes tiles (r + R i) TP .. + TP - 1. Part 0 runs the epilogue
+// (residual, greedy keys). Few tiles (q|k|v, the attention output) take WPT 4: a quarter of the
+// classes' arithmetic on each wavefront's path; many (the LM head) WPT 1 (mq_wpt).
 //
 // Passes of more than 16 rows (prefill) take the vectors in groups of 16: the launch holds
 // R x groups workgroups; workgroup i = 8k + x (x: its XCD) takes group k mod groups and tile
-// range r = 8 (k / groups) + x (tiles r, r + R, ...), so the groups' workgroups of one tile
-// range share an XCD and its L2: the weights come from HBM about once.
-__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void kd_mq(const DecMMArgs a) {
-  constexpr int NW = DEC_MM_NW;
+// range r = 8 (k / groups) + x, so the groups' workgroups of one tile range share an XCD and its
+// L2: the weights come from HBM about once.
+constexpr int MW_NW = 4;  // wavefronts a workgroup of kd_mq
+template <int NB, int TT, int WPT>  // TT: the segments' one format, or 0 when they differ
+__global__ __launch_bounds__(MW_NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void kd_mq(const DecMMArgs a) {
+  constexpr int TP = MW_NW / WPT;
   extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ float red[2][NW][4][64];
-  __shared__ float redc[2][4][64];
   __shared__ unsigned long long sbest[MAX_M];
+  __shared__ float xch[WPT > 1 ? 2 : 1][MW_NW][4][64];
   const int nvg = (a.m + 15) >> 4;
   int vg = 0, r0 = blockIdx.x, R = gridDim.x;
   if (nvg > 1) {
@@ -1299,82 +1574,79 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
     r0 = (k / nvg) * 8 + (blockIdx.x & 7);
     R = gridDim.x / nvg;
   }
-  const int v0 = vg * 16, m = min(16, a.m - v0), cols = a.cols, nbq = cols >> 8, nb = nbq;
+  const int v0 = vg * 16, m = min(16, a.m - v0), cols = a.cols, nb = cols >> 8;
   Q8KP y = a.y;
   y.q += (int64_t)v0 * (cols >> 2);
-  y.d += (int64_t)v0 * nbq;
-  y.bs += (int64_t)v0 * nbq * 8;
-  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
-  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)m * cols + 15) & ~(size_t)15));
-  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)m * cols + 15) & ~(size_t)15) + (((size_t)m * nbq * 4 + 15) & ~(size_t)15));
+  y.d += (int64_t)v0 * nb;
+  y.bs += (int64_t)v0 * nb * 8;
+  const MwLds L = mw_lds(smem, m, nb);
   const int total = a.tiles[0] + (a.nseg > 1 ? a.tiles[1] : 0) + (a.nseg > 2 ? a.tiles[2] : 0);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, c16 = lane & 15;
+  const int g = wave / WPT, c = wave - g * WPT;
   if (threadIdx.x < MAX_M) sbest[threadIdx.x] = 0;
-  stage_q8<NW * 64>(y, (const int *)nullptr, m, cols, lq, ld, lbs);
-  SPX_L uint32_t *lc = (SPX_L uint32_t *)(smem + mm_act_bytes(m, cols));
+  stage_q8<MW_NW * 64>(y, (const int *)nullptr, m, cols, L.lq, L.ld, L.lbs, mw_vs(nb) / 4);
   __syncthreads();
-  mq_corr_stage(m * nb, lbs, lc);
+  mq_corr_stage(m, nb, L.lbs, L.lc);
   __syncthreads();
-  int buf = 0;
   const MqVec vv = mq_vecs(m, MqIdentity{});
-  for (int t = r0; t < total; t += R) {
+  const int base = r0 * TP, S = R * TP, nr = base < total ? (total - base + S - 1) / S : 0;
+  auto pos_of = [&](int i) SPX_AI {
     MqPos p;
-    p.t = t;
-    p.u = 0;
+    p.t = base + i * S + g;  // (past the last tile: mq_locate's clamp, results not stored)
     mq_locate(a, total, p);
+    return p;
+  };
+  auto src = [&](int i) SPX_AI {
+    const MqPos p = pos_of(i);
     const TensorView &w = a.w[p.si];
-    float acc[4] = {0.f, 0.f, 0.f, 0.f}, cr[4] = {0.f, 0.f, 0.f, 0.f};
-    if (w.dtype == T_Q4K) mx_tile<T_Q4K, 8>(w.pl, p.row0, p.nrows, nb, wave, wave == 0, vv, lq, ld, lc, acc, cr);
-    else mx_tile<T_Q6K, 8>(w.pl, p.row0, p.nrows, nb, wave, wave == 0, vv, lq, ld, lc, acc, cr);
+    return mw_src(w.pl, w.dtype, p.row0, p.nrows, NB);
+  };
+  auto dst = [&](int i) SPX_AI { return mw_dst(L, vv, NB, a.w[pos_of(i).si].dtype); };
+  auto done = [&](int i, const float(&part)[4], const float(&cr)[4]) SPX_AI {
+    float out[4];
+    mw_meet<WPT>((SPX_L float *)&xch[WPT > 1 ? (i & 1) : 0][g * WPT][0][0], c, part, cr, out);
+    if (c != 0 || base + i * S + g >= total) return;
+    const MqPos p = pos_of(i);
+    float *const o = a.out[p.si];
+    const int64_t wrows = a.w[p.si].rows, ldo = a.ld_out[p.si];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      red[buf][wave][q][lane] = acc[q];
-      if (wave == 0) redc[buf][q][lane] = cr[q];
-    }
-    __syncthreads();
-    if (wave < 4) {
-      const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
-      const float res = mx_hsum((const SPX_L float *)&red[buf][0][0][0], q, lane, redc[buf][q][lane]);
-      if (v < m && r < p.nrows) {
-        float *const out = a.out[p.si];
-        const int64_t row = p.row0 + r, gv = v0 + v;
-        if (out) gst<float>(out + gv * a.ld_out[p.si] + row, res);
+    for (int t = 0; t < 4; t++) {
+      const int v = 4 * (lane >> 4) + t;
+      if (v < m && c16 < p.nrows) {
+        const int64_t row = p.row0 + c16, gv = v0 + v;
+        if (o) gst<float>(o + gv * ldo + row, out[t]);
         if (a.res_out) {
-          const int64_t o = gv * w.rows + row;
-          gst<float>(a.res_out + o, gld<float>(a.res_in + o) + a.rscale * res);
+          const int64_t q = gv * wrows + row;
+          gst<float>(a.res_out + q, gld<float>(a.res_in + q) + a.rscale * out[t]);
         }
-        if (a.best) atomicMax(&sbest[v], pick_key(res, a.lscale, row));
+        if (a.best) atomicMax(&sbest[v], pick_key(out[t], a.lscale, row));
       }
     }
-    buf ^= 1;
-  }
+  };
+  mw_walk_part<NB, TT, WPT>(c, nr, src, dst, done);
   if (a.best) {  // per vector, the best key of each tile range
     __syncthreads();
     if ((int)threadIdx.x < m) gst<unsigned long long>(a.best + (int64_t)(v0 + threadIdx.x) * a.nbest + r0, sbest[threadIdx.x]);
   }
 }
 
-// Routing + gate/up + SwiGLU over the jobs on the matrix cores (kd_gateup_m's prologue, job
-// list and item split; items are (job, 16 h rows)): wavefront l runs lane class l's chains over
-// all blocks of the item's gate and up tiles (mx_tile; wavefront 0 also the corrections); the
-// chains meet in LDS, two items' worth, and wavefront q < 4 forms the reference's hsum of gate
-// and up for vectors 4 (lane >> 4) + q and applies SwiGLU.
-template <int T>
-__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(T == T_Q4K ? 4 : 2))) void kd_gateup_mq(const DecGateUpMArgs a) {
-  constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M;
+// Routing + gate/up + SwiGLU over the jobs on the matrix cores (kd_gateup_m's prologue and job
+// list): items (job, 16 h rows), TP = NW / WPT of them a round: round i of workgroup b takes
+// items (b + G i) TP .. + TP - 1, each walked (gate tile, then up tile) by WPT wavefronts whose
+// partial sums meet in LDS; part 0 applies SwiGLU.
+template <int T, int NB, int WPT>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void kd_gateup_mq(const DecGateUpMArgs a) {
+  constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M, TP = NW / WPT;
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ signed char slot_of[MAX_M * 256];
   __shared__ int wcount[NW];
-  __shared__ float red[2][2][NW][4][64];
-  __shared__ float redc[2][2][4][64];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n_ff = a.n_ff, cols = (int)a.gate.cols, nbq = cols >> 8, nb = nbq, m = a.m;
+  __shared__ float xch[WPT > 1 ? 2 : 1][NW][4][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int g = wave / WPT, c = wave - g * WPT;
+  const int n_ff = a.n_ff, cols = (int)a.gate.cols, nb = cols >> 8, m = a.m;
   const int TX = (n_ff + 15) / 16;
-  const size_t act = mm_act_bytes(m, cols);
-  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
-  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)m * cols + 15) & ~(size_t)15));
-  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)m * cols + 15) & ~(size_t)15) + (((size_t)m * nbq * 4 + 15) & ~(size_t)15));
-  SPX_L int *sj = (SPX_L int *)(smem + act);  // [max jobs][JR]
+  const MwLds L = mw_lds(smem, m, nb);
+  SPX_L int *sj = (SPX_L int *)(smem + mw_act_bytes(m, nb));  // [max jobs][JR]
   int nj = 1;
   {
     StageQ8<NW * 64> st;
@@ -1387,119 +1659,124 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
       st.get(a.y, m, cols);
       for (int i = threadIdx.x; i < JR; i += blockDim.x) sj[i] = i == 0 ? 0 : i == 1 ? m : i < 2 + MAX_M ? i - 2 : i - 2 - MAX_M;
     }
-    st.put(m, cols, lq, ld, lbs);
+    st.put(m, cols, L.lq, L.ld, L.lbs, mw_vs(nb) / 4);
   }
-  // the correction operands after the job table
-  SPX_L uint32_t *lc = (SPX_L uint32_t *)(smem + act + (((size_t)(a.rt.logits ? a.max_jobs : 1) * JR * 4 + 15) & ~(size_t)15));
   __syncthreads();
-  mq_corr_stage(m * nb, lbs, lc);
+  mq_corr_stage(m, nb, L.lbs, L.lc);
   __syncthreads();
-  const int n = TX * nj, G = gridDim.x;
-  const int i0 = (int)((int64_t)blockIdx.x * n / G), i1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
-  const int c16 = lane & 15;
-  int buf = 0;
-  for (int i = i0; i < i1; i++) {
-    const int j = i / TX, x = i - j * TX;
-    const int e = min(max(sj[j * JR], 0), a.gate.n_expert - 1), nv = sj[j * JR + 1];
-    const int64_t row0 = (int64_t)e * a.gate.rows + (int64_t)x * 16;
-    const int nrows = min(16, n_ff - x * 16);
-    const MqVec vv = mq_vecs(nv, MqRows{sj + j * JR + 2});
-    float ag[4] = {0.f, 0.f, 0.f, 0.f}, cg[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f}, cu[4] = {0.f, 0.f, 0.f, 0.f};
-    mx_tile<T, 8>(a.gate.pl, row0, nrows, nb, wave, wave == 0, vv, lq, ld, lc, ag, cg);
-    mx_tile<T, 8>(a.up.pl, row0, nrows, nb, wave, wave == 0, vv, lq, ld, lc, au, cu);
+  const int n = TX * nj, base = blockIdx.x * TP, S = gridDim.x * TP, nr = base < n ? (n - base + S - 1) / S : 0;
+  auto item = [&](int k) SPX_AI { return min(base + S * (k >> 1) + g, n - 1); };  // tile k: gate (k even) or up
+  float gv[4];
+  auto src = [&](int k) SPX_AI {
+    const int i = item(k), j = i / TX, x = i - j * TX;
+    const int e = min(max(sj[j * JR], 0), a.gate.n_expert - 1);
+    return mw_src((k & 1) ? a.up.pl : a.gate.pl, T, (int64_t)e * a.gate.rows + (int64_t)x * 16, min(16, n_ff - x * 16), NB);
+  };
+  auto dst = [&](int k) SPX_AI {
+    const int j = item(k) / TX;
+    return mw_dst(L, mq_vecs(sj[j * JR + 1], MqRows{sj + j * JR + 2}), NB, T);
+  };
+  auto done = [&](int k, const float(&part)[4], const float(&cr)[4]) SPX_AI {
+    float out[4];
+    mw_meet<WPT>((SPX_L float *)&xch[WPT > 1 ? (k & 1) : 0][g * WPT][0][0], c, part, cr, out);
+    if (c != 0) return;
+    if (!(k & 1)) {
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      red[buf][0][wave][q][lane] = ag[q];
-      red[buf][1][wave][q][lane] = au[q];
-      if (wave == 0) { redc[buf][0][q][lane] = cg[q]; redc[buf][1][q][lane] = cu[q]; }
+      for (int t = 0; t < 4; t++) gv[t] = out[t];
+      return;
     }
-    __syncthreads();
-    if (wave < 4) {
-      const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
-      const float g = mx_hsum((const SPX_L float *)&red[buf][0][0][0][0], q, lane, redc[buf][0][q][lane]);
-      const float up = mx_hsum((const SPX_L float *)&red[buf][1][0][0][0], q, lane, redc[buf][1][q][lane]);
-      if (v < nv && r < nrows) gst<float>(a.h + (int64_t)sj[j * JR + 2 + MAX_M + v] * n_ff + x * 16 + r, g / (1.0f + expf(-g)) * up);
+    if (base + S * (k >> 1) + g >= n) return;
+    const int i = item(k), j = i / TX, x = i - j * TX, nv = sj[j * JR + 1], r = lane & 15;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const int v = 4 * (lane >> 4) + t;
+      if (v < nv && x * 16 + r < n_ff)
+        gst<float>(a.h + (int64_t)sj[j * JR + 2 + MAX_M + v] * n_ff + x * 16 + r, gv[t] / (1.0f + expf(-gv[t])) * out[t]);
     }
-    buf ^= 1;
-  }
+  };
+  mw_walk_part<NB, T, WPT>(c, 2 * nr, src, dst, done);
 }
 
-// Down projection of the jobs' users on the matrix cores: items (job, DOWN_MQ_ROWS = 64 rows);
-// the job's users' h rows are quantized into LDS (quantize_avx2 per 256 block) as kd_down_m does;
-// then for each of the item's four 16-row tiles wavefront l runs lane class l's chain over the
-// blocks (mx_tile; wavefront 0 also the corrections), the chains of all four tiles meet in LDS at
-// once, and each wavefront forms the reference's hsum for two (tile, vector group) pairs; y per
-// (row, choice) to yd.
-constexpr int DOWN_MQ_TILES = 4, DOWN_MQ_ROWS = 16 * DOWN_MQ_TILES;
-template <int T>
-__global__ __launch_bounds__(DEC_MM_NW * 64) void kd_down_mq(const DecDownMArgs a) {
-  constexpr int NW = DEC_MM_NW, JF = 2 + MAX_M, NT = DOWN_MQ_TILES;
-  static_assert(NT * 4 == 2 * NW, "two (tile, vector group) pairs a wavefront");
+// Down projection of the jobs' users on the matrix cores: items (job, DOWN_MQ_ROWS = 8 tiles),
+// workgroup b the items b, b + G, ...; at each item the job's users' h rows are quantized into
+// LDS (quantize_avx2 per 256 block) as kd_down_m does, and the item's tiles are walked TP =
+// NW / WPT at a time (WPT wavefronts a tile, their partial sums meeting in LDS; mw_walk: the
+// next item's bytes are requested before its staging); y per (row, choice) to yd.
+constexpr int DOWN_MQ_ROWS = 16 * DEC_MM_NW, DOWN_MQ_ITEMS = 64;
+template <int T, int NB, int WPT>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void kd_down_mq(const DecDownMArgs a) {
+  constexpr int NW = DEC_MM_NW, JF = 2 + MAX_M, TP = NW / WPT, RI = NW / TP;  // RI: rounds an item
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int s_job[JF];
-  __shared__ float red[NT][NW][4][64];
-  __shared__ float redc[NT][4][64];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, nbh = n_ff >> 8, TX = (dim + DOWN_MQ_ROWS - 1) / DOWN_MQ_ROWS;
-  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
-  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)MAX_M * n_ff + 15) & ~(size_t)15));
-  SPX_L int *lbs = (SPX_L int *)(smem + (((size_t)MAX_M * n_ff + 15) & ~(size_t)15) + (((size_t)MAX_M * nbh * 4 + 15) & ~(size_t)15));
-  SPX_L uint32_t *lc = (SPX_L uint32_t *)(smem + downm_lds_bytes(n_ff));
-  const int n = TX * gld<int>(a.njobs);
-  for (int it = blockIdx.x; it < n; it += gridDim.x) {
-    const int j = it / TX, x = it - j * TX;
+  __shared__ int ihead[DOWN_MQ_ITEMS][2];  // expert, users of the workgroup's items
+  __shared__ float xch[WPT > 1 ? 2 : 1][NW][4][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int g = wave / WPT, c = wave - g * WPT;
+  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, TX = (dim + DOWN_MQ_ROWS - 1) / DOWN_MQ_ROWS, G = gridDim.x;
+  const MwLds L = mw_lds(smem, MAX_M, NB);
+  const int n = TX * gld<int>(a.njobs), nit = (int)blockIdx.x < n ? (n - (int)blockIdx.x + G - 1) / G : 0;
+  for (int k = threadIdx.x; k < min(nit, DOWN_MQ_ITEMS); k += blockDim.x) {
+    const int j = ((int)blockIdx.x + G * k) / TX;
+    ihead[k][0] = min(max(gld<int>(reinterpret_cast<const int *>(a.jobs + j)), 0), a.w.n_expert - 1);
+    ihead[k][1] = min(max(gld<int>(reinterpret_cast<const int *>(a.jobs + j) + 1), 0), MAX_M);
+  }
+  auto stage = [&](int k) SPX_AI {  // item k's users' h rows, quantized
+    __syncthreads();
+    const int j = ((int)blockIdx.x + G * k) / TX;
     if ((int)threadIdx.x < JF) {
       const int f = threadIdx.x;
       s_job[f] = gld<int>(reinterpret_cast<const int *>(a.jobs + j) + (f < 2 ? f : 2 + MAX_M + (f - 2)));
     }
     __syncthreads();
-    const int e = min(max(s_job[0], 0), a.w.n_expert - 1), nv = min(max(s_job[1], 0), MAX_M);
-    const int nq = nv * nbh;
+    const int nv = min(max(s_job[1], 0), MAX_M), nq = nv * NB;
     for (int q0 = wave; q0 < nq; q0 += 4 * NW) {
       float4 hv[4];
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const int q = q0 + NW * t;
         if (q < nq) {
-          const int k = q / nbh, i = q - k * nbh;
-          hv[t] = gld<float4>(a.h + (int64_t)s_job[2 + k] * n_ff + i * 256 + 4 * lane);
+          const int u = q / NB, i = q - u * NB;
+          hv[t] = gld<float4>(a.h + (int64_t)s_job[2 + u] * n_ff + i * 256 + 4 * lane);
         }
       }
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const int q = q0 + NW * t;
         if (q < nq) {
+          const int u = q / NB, i = q - u * NB;
           const float am = q8k_amax(hv[t]);
-          q8k_block_store(hv[t], am, lq + q * 64, ld + q, lbs + q * 16);
+          q8k_block_store(hv[t], am, L.lq + u * mw_vs(NB) + i * 64, L.ld + q, (SPX_L int *)L.lbs + q * 16);
         }
       }
     }
     __syncthreads();
-    mq_corr_stage(nq, (const SPX_L int2 *)lbs, lc);
+    mq_corr_stage(nv, NB, L.lbs, L.lc);
     __syncthreads();
-    const MqVec vv = mq_vecs(nv, MqIdentity{});
-    const int64_t rx = (int64_t)x * DOWN_MQ_ROWS;
+  };
+  auto row0 = [&](int k) SPX_AI {  // tile k: item k / RI, its tile (k % RI) TP + g
+    const int it = (int)blockIdx.x + G * (k / RI);
+    return (it - (it / TX) * TX) * DOWN_MQ_ROWS + 16 * ((k % RI) * TP + g);
+  };
+  auto src = [&](int k) SPX_AI {
+    const int r0 = row0(k);
+    return mw_src(a.w.pl, T, (int64_t)ihead[k / RI][0] * dim + min(r0, dim - 1), max(1, min(16, dim - r0)), NB);
+  };
+  auto dst = [&](int k) SPX_AI { return mw_dst(L, mq_vecs(ihead[k / RI][1], MqIdentity{}), NB, T); };
+  auto done = [&](int k, const float(&part)[4], const float(&cr)[4]) SPX_AI {
+    float out[4];
+    mw_meet<WPT>((SPX_L float *)&xch[WPT > 1 ? (k & 1) : 0][g * WPT][0][0], c, part, cr, out);
+    if (c == 0) {
+      const int r0 = row0(k), nv = ihead[k / RI][1], r = lane & 15;
 #pragma unroll
-    for (int tt = 0; tt < NT; tt++) {
-      const int64_t r0 = rx + 16 * tt;
-      float acc[4] = {0.f, 0.f, 0.f, 0.f}, cr[4] = {0.f, 0.f, 0.f, 0.f};
-      if (r0 < dim) mx_tile<T, 4>(a.w.pl, (int64_t)e * dim + r0, (int)min((int64_t)16, dim - r0), nbh, wave, wave == 0, vv, lq, ld, lc, acc, cr);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        red[tt][wave][q][lane] = acc[q];
-        if (wave == 0) redc[tt][q][lane] = cr[q];
+      for (int t = 0; t < 4; t++) {
+        const int v = 4 * (lane >> 4) + t;
+        if (v < nv && r0 + r < dim) gst<float>(a.yd + (int64_t)s_job[2 + v] * dim + r0 + r, out[t]);
       }
     }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const int pi = 2 * wave + k, tt = pi >> 2, q = pi & 3, r = lane & 15, v = 4 * (lane >> 4) + q;
-      const int64_t r0 = rx + 16 * tt;
-      const float y = mx_hsum((const SPX_L float *)&red[tt][0][0][0], q, lane, redc[tt][q][lane]);
-      if (v < nv && r0 + r < dim) gst<float>(a.yd + (int64_t)s_job[2 + v] * dim + r0 + r, y);
-    }
-    __syncthreads();
-  }
+    if (k % RI == RI - 1 && k / RI + 1 < nit) stage(k / RI + 1);  // (its first barrier: every reader of s_job is done)
+  };
+  if (nit > 0) stage(0);
+  mw_walk_part<NB, T, WPT>(c, nit * RI, src, dst, done);
 }
 
 // ------------------------------------------------------------------ prefill passes (17..128 rows)
@@ -1604,28 +1881,25 @@ __global__ __launch_bounds__(256) void kp_jobs(const DecRouteArgs a) {
 // Gate / up + SwiGLU of a prefill pass on the matrix cores over a job list of at most sixteen
 // users a job (MoE: kp_route's, in global memory; dense, jobs null: rows 16j .. 16j + 15 as
 // job j): items (job, 16 h rows) as kd_gateup_mq takes them, workgroup b the items
-// [b n / G, (b + 1) n / G); at each job the users' Q8_K rows are staged in LDS (slot = the
-// user's place in the job). An item's arithmetic, and so each h value, is kd_gateup_mq's.
-template <int T>
-__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(T == T_Q4K ? 4 : 2))) void kp_gateup_mq(const DecGateUpMArgs a,
-                                                                                                                     const Job *jobs,
-                                                                                                                     const int *njobs) {
+// [b n / G, (b + 1) n / G), job by job: the job's users' Q8_K rows are staged in LDS (slot =
+// the user's place in the job), then wavefront w walks the job's items w, w + NW, ... of the
+// range. An item's arithmetic, and so each h value, is kd_gateup_mq's.
+template <int T, int NB>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void kp_gateup_mq(const DecGateUpMArgs a,
+                                                                                                     const Job *jobs,
+                                                                                                     const int *njobs) {
   constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M;
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int sj[JR];
-  __shared__ float red[2][2][NW][4][64];
-  __shared__ float redc[2][2][4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n_ff = a.n_ff, cols = (int)a.gate.cols, nb = cols >> 8, m = a.m;
   const int TX = (n_ff + 15) / 16;
-  SPX_L uint32_t *lq = (SPX_L uint32_t *)smem;
-  SPX_L float *ld = (SPX_L float *)(smem + (((size_t)MAX_M * cols + 15) & ~(size_t)15));
-  SPX_L int2 *lbs = (SPX_L int2 *)(smem + (((size_t)MAX_M * cols + 15) & ~(size_t)15) + (((size_t)MAX_M * nb * 4 + 15) & ~(size_t)15));
-  SPX_L uint32_t *lc = (SPX_L uint32_t *)(smem + mm_act_bytes(MAX_M, cols));
+  const MwLds L = mw_lds(smem, MAX_M, nb);
   const int nj = jobs ? gld<int>(njobs) : (m + MAX_M - 1) / MAX_M;
   const int n = TX * nj, G = gridDim.x;
   const int i0 = (int)((int64_t)blockIdx.x * n / G), i1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
-  auto stage_job = [&](int j) {
+  for (int s0 = i0; s0 < i1;) {
+    const int j = s0 / TX, s1 = min(i1, (j + 1) * TX);
     __syncthreads();  // the previous job's users are done with
     if ((int)threadIdx.x < JR) {
       const int f = threadIdx.x;
@@ -1633,37 +1907,33 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
                    : f == 0 ? 0 : f == 1 ? min(MAX_M, m - MAX_M * j) : MAX_M * j + (f - 2) % MAX_M;
     }
     __syncthreads();
-    stage_q8<NW * 64>(a.y, (const SPX_L int *)(sj + 2), sj[1], cols, lq, ld, lbs);
+    const int nv = min(max(sj[1], 0), MAX_M), e = min(max(sj[0], 0), a.gate.n_expert - 1);
+    stage_q8<NW * 64>(a.y, (const SPX_L int *)(sj + 2), nv, cols, L.lq, L.ld, L.lbs, mw_vs(nb) / 4);
     __syncthreads();
-    mq_corr_stage(sj[1] * nb, lbs, lc);
+    mq_corr_stage(nv, nb, L.lbs, L.lc);
     __syncthreads();
-  };
-  const int c16 = lane & 15;
-  int buf = 0;
-  for (int i = i0; i < i1; i++) {
-    const int j = i / TX, x = i - j * TX;
-    if (i == i0 || x == 0) stage_job(j);
-    const int e = jobs ? min(max(sj[0], 0), a.gate.n_expert - 1) : 0, nv = sj[1];
-    const int64_t row0 = (int64_t)e * a.gate.rows + (int64_t)x * 16;
-    const int nrows = min(16, n_ff - x * 16);
+    const int cnt = s1 - s0, nit = wave < cnt ? (cnt - wave + NW - 1) / NW : 0;
     const MqVec vv = mq_vecs(nv, MqIdentity{});
-    float ag[4] = {0.f, 0.f, 0.f, 0.f}, cg[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f}, cu[4] = {0.f, 0.f, 0.f, 0.f};
-    mx_tile<T, 8>(a.gate.pl, row0, nrows, nb, wave, wave == 0, vv, lq, ld, lc, ag, cg);
-    mx_tile<T, 8>(a.up.pl, row0, nrows, nb, wave, wave == 0, vv, lq, ld, lc, au, cu);
+    float g[4];
+    auto src = [&](int k) SPX_AI {  // tile k: item s0 + wave + NW (k / 2), gate (k even) or up
+      const int x = s0 + wave + NW * (k >> 1) - j * TX;
+      return mw_src((k & 1) ? a.up.pl : a.gate.pl, T, (int64_t)e * a.gate.rows + (int64_t)x * 16, min(16, n_ff - x * 16), NB);
+    };
+    auto dst = [&](int) SPX_AI { return mw_dst(L, vv, NB, T); };
+    auto done = [&](int k, const float (&out)[4], const float (&)[4]) SPX_AI {
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      red[buf][0][wave][q][lane] = ag[q];
-      red[buf][1][wave][q][lane] = au[q];
-      if (wave == 0) { redc[buf][0][q][lane] = cg[q]; redc[buf][1][q][lane] = cu[q]; }
-    }
-    __syncthreads();
-    if (wave < 4) {
-      const int q = wave, v = 4 * (lane >> 4) + q, r = c16;
-      const float g = mx_hsum((const SPX_L float *)&red[buf][0][0][0][0], q, lane, redc[buf][0][q][lane]);
-      const float up = mx_hsum((const SPX_L float *)&red[buf][1][0][0][0], q, lane, redc[buf][1][q][lane]);
-      if (v < nv && r < nrows) gst<float>(a.h + (int64_t)sj[2 + MAX_M + v] * n_ff + x * 16 + r, g / (1.0f + expf(-g)) * up);
-    }
-    buf ^= 1;
+      for (int t = 0; t < 4; t++)
+        if (!(k & 1)) g[t] = out[t];
+      if (!(k & 1)) return;
+      const int x = s0 + wave + NW * (k >> 1) - j * TX, r = lane & 15;
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int v = 4 * (lane >> 4) + t;
+        if (v < nv && x * 16 + r < n_ff) gst<float>(a.h + (int64_t)sj[2 + MAX_M + v] * n_ff + x * 16 + r, g[t] / (1.0f + expf(-g[t])) * out[t]);
+      }
+    };
+    mw_walk<NB, T, 1, 0>(2 * nit, src, dst, done);
+    s0 = s1;
   }
 }
 
@@ -1818,6 +2088,25 @@ hipError_t launch_dec_mm(const DecMMArgs &a, int grid, hipStream_t s) {
   return dec_mm_tt<0>(a, grid, s);
 }
 
+// Calls f(std::integral_constant<int, NB>) with the compile-time block count of nb, for the counts
+// the matrix-core kernels take (mq_nb_ok: 1, 2, 3, 4, 8, 16); other counts are refused.
+template <class F>
+static hipError_t with_nb(int nb, F &&f) {
+  switch (nb) {
+  case 1: return f(std::integral_constant<int, 1>{});
+  case 2: return f(std::integral_constant<int, 2>{});
+  case 3: return f(std::integral_constant<int, 3>{});
+  case 4: return f(std::integral_constant<int, 4>{});
+  case 8: return f(std::integral_constant<int, 8>{});
+  case 16: return f(std::integral_constant<int, 16>{});
+  default: return hipErrorInvalidValue;
+  }
+}
+
+// Wavefronts a tile of kd_mq (the class split): few tiles 4 (a quarter of the classes' path
+// each), many 1 (throughput; the LM head), prefill 1.
+static int mq_wpt(int tiles, int m) { return m > MAX_M ? 1 : tiles <= 2 * cu_count() ? 4 : tiles <= 4 * cu_count() ? 2 : 1; }
+
 hipError_t launch_dec_mq(const DecMMArgs &a, int grid, hipStream_t s) {
   const int nb = a.cols >> 8, nvg = (a.m + 15) / 16;
   if (a.nseg < 1 || a.nseg > 3 || grid < 1 || nb < 1 || nb > DEC_MAXNB || a.cols % 256 || a.m < 1 || a.m > PMAX) return hipErrorInvalidValue;
@@ -1826,43 +2115,63 @@ hipError_t launch_dec_mq(const DecMMArgs &a, int grid, hipStream_t s) {
     if ((a.w[i].dtype != T_Q4K && a.w[i].dtype != T_Q6K) || a.w[i].nb != nb) return hipErrorInvalidValue;
   if (a.res_out && a.nseg != 1) return hipErrorInvalidValue;
   if (a.best && a.nbest != grid) return hipErrorInvalidValue;
-  const int mv = std::min(a.m, MAX_M);
-  const size_t sm = mm_act_bytes(mv, a.cols) + mq_corr_bytes(mv, a.cols);
-  SPX_DLDS(kd_mq, sm);
-  hipLaunchKernelGGL(kd_mq, dim3(grid * nvg), dim3(DEC_MM_NW * 64), sm, s, a);
-  return hipGetLastError();
+  const size_t sm = mw_act_bytes(std::min(a.m, MAX_M), nb);
+  const int total = a.tiles[0] + (a.nseg > 1 ? a.tiles[1] : 0) + (a.nseg > 2 ? a.tiles[2] : 0), wpt = mq_wpt(total, a.m);
+  int tt = a.w[0].dtype;
+  for (int i = 1; i < a.nseg; i++)
+    if (a.w[i].dtype != tt) tt = 0;
+  const dim3 g(grid * nvg), b(MW_NW * 64);
+  auto go = [&](auto kern) {
+    SPX_DLDS(kern, sm);
+    hipLaunchKernelGGL(kern, g, b, sm, s, a);
+    return hipGetLastError();
+  };
+  return with_nb(nb, [&](auto NBc) {
+    constexpr int NB = decltype(NBc)::value;
+    auto by_wpt = [&](auto TTc) {
+      constexpr int TT = decltype(TTc)::value;
+      return wpt == 4 ? go(kd_mq<NB, TT, 4>) : wpt == 2 ? go(kd_mq<NB, TT, 2>) : go(kd_mq<NB, TT, 1>);
+    };
+    if (tt == T_Q4K) return by_wpt(std::integral_constant<int, T_Q4K>{});
+    if (tt == T_Q6K) return by_wpt(std::integral_constant<int, T_Q6K>{});
+    return by_wpt(std::integral_constant<int, 0>{});
+  });
 }
 
+bool dec_mq_nb_ok(int nb) { return nb == 1 || nb == 2 || nb == 3 || nb == 4 || nb == 8 || nb == 16; }
+
+// kd_mq's workgroups: MW_NW wavefronts, MW_NW / mq_wpt tiles at a time, two workgroups a CU.
 int dec_mq_grid(int tiles, int m) {
-  const int slots = 2 * cu_count();
-  if (m <= MAX_M) return std::min(tiles, slots);
+  const int slots = 2 * cu_count(), tp = MW_NW / mq_wpt(tiles, m), need = (tiles + tp - 1) / tp;
+  if (m <= MAX_M) return std::max(1, std::min(need, slots));
   const int nvg = (m + 15) / 16, per = (slots / nvg + 7) / 8 * 8;
-  return std::max(8, std::min((tiles + 7) / 8 * 8, per));
+  return std::max(8, std::min((need + 7) / 8 * 8, per));
 }
 
 hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &args, int max_jobs, hipStream_t s) {
   DecGateUpMArgs a = args;
   a.max_jobs = max_jobs;
-  const int nb = (int)(a.gate.cols >> 8), cols = (int)a.gate.cols;
+  const int nb = (int)(a.gate.cols >> 8);
   if (a.gate.cols % 256 || nb > DEC_MAXNB || a.gate.nb != nb || a.up.nb != nb || a.gate.dtype != a.up.dtype || a.m < 1 || a.m > MAX_M || max_jobs < 1 ||
       max_jobs > 512 || (a.rt.logits && (max_jobs > a.gate.n_expert || a.rt.m != a.m || a.rt.n_expert < 1 || a.rt.n_expert > 256 || a.rt.n_used < 1 ||
                                          a.rt.n_used > 32 || a.rt.n_used > a.rt.n_expert)))
     return hipErrorInvalidValue;
-  const size_t sm = mm_act_bytes(a.m, cols) + (((size_t)(a.rt.logits ? max_jobs : 1) * (2 + 2 * MAX_M) * 4 + 15) & ~(size_t)15) +
-                    mq_corr_bytes(a.m, cols);
-  if (sm > 100 * 1024) return hipErrorInvalidValue;
-  // all workgroups resident (Q4_K: at most 128 registers a lane, two fit a CU), so each routes
-  // once and takes its items in turn. Every workgroup routes the pass, so a second one a CU
-  // pays off only while the items per workgroup are few: two a CU up to 12 rows, one above
-  // (Qwen3-30B-A3B, measured: M = 9 pass 3.78 vs 3.87 ms with one; 16-row prefill 3.5k vs
-  // 3.1k tok/s with one)
-  const int items = ((a.n_ff + 15) / 16) * (a.rt.logits ? max_jobs : 1);
-  const int gmax = (a.gate.dtype == T_Q4K && a.m <= 12 ? 2 : 1) * cu_count();
-  const dim3 grid((unsigned)std::min(items, gmax)), b(DEC_MM_NW * 64);
-  if (a.gate.dtype == T_Q4K) { SPX_DLDS((kd_gateup_mq<T_Q4K>), sm); hipLaunchKernelGGL((kd_gateup_mq<T_Q4K>), grid, b, sm, s, a); }
-  else if (a.gate.dtype == T_Q6K) { SPX_DLDS((kd_gateup_mq<T_Q6K>), sm); hipLaunchKernelGGL((kd_gateup_mq<T_Q6K>), grid, b, sm, s, a); }
-  else return hipErrorInvalidValue;
-  return hipGetLastError();
+  const size_t sm = mw_act_bytes(a.m, nb) + (size_t)(a.rt.logits ? max_jobs : 1) * (2 + 2 * MAX_M) * 4;
+  if (sm > 120 * 1024) return hipErrorInvalidValue;
+  // four wavefronts an item (two items a round), one workgroup a CU: every workgroup routes the
+  // pass (the items beyond the job count end at once)
+  const int items = ((a.n_ff + 15) / 16) * (a.rt.logits ? max_jobs : 1), tp = DEC_MM_NW / 4;
+  const dim3 grid((unsigned)std::max(1, std::min((items + tp - 1) / tp, cu_count()))), b(DEC_MM_NW * 64);
+  if (a.gate.dtype != T_Q4K && a.gate.dtype != T_Q6K) return hipErrorInvalidValue;
+  auto go = [&](auto kern) {
+    SPX_DLDS(kern, sm);
+    hipLaunchKernelGGL(kern, grid, b, sm, s, a);
+    return hipGetLastError();
+  };
+  return with_nb(nb, [&](auto NBc) {
+    constexpr int NB = decltype(NBc)::value;
+    return a.gate.dtype == T_Q4K ? go(kd_gateup_mq<T_Q4K, NB, 4>) : go(kd_gateup_mq<T_Q6K, NB, 4>);
+  });
 }
 
 hipError_t launch_kp_route(const DecRouteArgs &a, hipStream_t s) {
@@ -1875,28 +2184,41 @@ hipError_t launch_kp_route(const DecRouteArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_kp_gateup_mq(const DecGateUpMArgs &a, const Job *jobs, const int *njobs, int max_jobs, hipStream_t s) {
-  const int nb = (int)(a.gate.cols >> 8), cols = (int)a.gate.cols;
+  const int nb = (int)(a.gate.cols >> 8);
   if (a.gate.cols % 256 || nb > DEC_MAXNB || a.gate.nb != nb || a.up.nb != nb || a.gate.dtype != a.up.dtype || a.m < 1 || a.m > PMAX ||
       max_jobs < 1 || max_jobs > 512 || (jobs && !njobs))
     return hipErrorInvalidValue;
-  const size_t sm = mm_act_bytes(MAX_M, cols) + mq_corr_bytes(MAX_M, cols);
-  const int items = ((a.n_ff + 15) / 16) * (jobs ? max_jobs : (a.m + MAX_M - 1) / MAX_M);
-  const dim3 grid((unsigned)std::min(items, (a.gate.dtype == T_Q4K ? 2 : 1) * cu_count())), b(DEC_MM_NW * 64);
-  if (a.gate.dtype == T_Q4K) { SPX_DLDS((kp_gateup_mq<T_Q4K>), sm); hipLaunchKernelGGL((kp_gateup_mq<T_Q4K>), grid, b, sm, s, a, jobs, njobs); }
-  else if (a.gate.dtype == T_Q6K) { SPX_DLDS((kp_gateup_mq<T_Q6K>), sm); hipLaunchKernelGGL((kp_gateup_mq<T_Q6K>), grid, b, sm, s, a, jobs, njobs); }
-  else return hipErrorInvalidValue;
-  return hipGetLastError();
+  const size_t sm = mw_act_bytes(MAX_M, nb);
+  const int njob = jobs ? max_jobs : (a.m + MAX_M - 1) / MAX_M, items = ((a.n_ff + 15) / 16) * njob;
+  const dim3 grid((unsigned)std::max(1, std::min((items + DEC_MM_NW - 1) / DEC_MM_NW, cu_count()))), b(DEC_MM_NW * 64);
+  if (a.gate.dtype != T_Q4K && a.gate.dtype != T_Q6K) return hipErrorInvalidValue;
+  return with_nb(nb, [&](auto NBc) {
+    constexpr int NB = decltype(NBc)::value;
+    if (a.gate.dtype == T_Q4K) { SPX_DLDS((kp_gateup_mq<T_Q4K, NB>), sm); hipLaunchKernelGGL((kp_gateup_mq<T_Q4K, NB>), grid, b, sm, s, a, jobs, njobs); }
+    else { SPX_DLDS((kp_gateup_mq<T_Q6K, NB>), sm); hipLaunchKernelGGL((kp_gateup_mq<T_Q6K, NB>), grid, b, sm, s, a, jobs, njobs); }
+    return hipGetLastError();
+  });
 }
 
 hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s) {
   if (a.w.cols % 256 || a.w.nb > 4 || a.max_jobs < 1 || a.max_jobs > 512 || !a.h || !a.yd) return hipErrorInvalidValue;
-  const int tx = (int)((a.w.rows + DOWN_MQ_ROWS - 1) / DOWN_MQ_ROWS);
-  const dim3 grid((unsigned)std::min(tx * a.max_jobs, 2 * cu_count())), b(DEC_MM_NW * 64);
-  const size_t sm = downm_lds_bytes((int)a.w.cols) + mq_corr_bytes(MAX_M, (int)a.w.cols);
-  if (a.w.dtype == T_Q4K) hipLaunchKernelGGL((kd_down_mq<T_Q4K>), grid, b, sm, s, a);
-  else if (a.w.dtype == T_Q6K) hipLaunchKernelGGL((kd_down_mq<T_Q6K>), grid, b, sm, s, a);
-  else return hipErrorInvalidValue;
-  return hipGetLastError();
+  const int tx = (int)((a.w.rows + DOWN_MQ_ROWS - 1) / DOWN_MQ_ROWS), G = std::min(tx * a.max_jobs, cu_count());
+  if ((tx * a.max_jobs + G - 1) / G > DOWN_MQ_ITEMS) return hipErrorInvalidValue;  // items a workgroup, cached in LDS
+  const dim3 grid((unsigned)G), b(DEC_MM_NW * 64);
+  const size_t sm = mw_act_bytes(MAX_M, (int)a.w.nb);
+  if (a.w.dtype != T_Q4K && a.w.dtype != T_Q6K) return hipErrorInvalidValue;
+  auto go = [&](auto kern) {
+    SPX_DLDS(kern, sm);
+    hipLaunchKernelGGL(kern, grid, b, sm, s, a);
+    return hipGetLastError();
+  };
+  // a pass of up to 16 rows (at most 128 jobs): four wavefronts a tile; prefill: one
+  const bool split = a.max_jobs <= 128;
+  return with_nb((int)a.w.nb, [&](auto NBc) {
+    constexpr int NB = decltype(NBc)::value;
+    if (a.w.dtype == T_Q4K) return split ? go(kd_down_mq<T_Q4K, NB, 4>) : go(kd_down_mq<T_Q4K, NB, 1>);
+    return split ? go(kd_down_mq<T_Q6K, NB, 4>) : go(kd_down_mq<T_Q6K, NB, 1>);
+  });
 }
 
 hipError_t launch_dec_router_m(const DecRouterMArgs &a, hipStream_t s) {

@@ -70,6 +70,7 @@ struct spx_engine {
                            // a pass of fewer rows gives an expert about one row, the MFMA's 16 columns idle
                            // and the per-lane dot kernel is faster
   bool mq_gateup = true;   // the gate/up projections (SPX_MQ_GATEUP)
+  bool mq_shapes = true;   // every K-quant matrix's blocks-a-row count is one the matrix-core kernels take (dec_mq_nb_ok)
   int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   int pf_attn = 2;          // prefill passes: 2 the multi-tile kernels (at least 2 query heads a kv head), 1 k_rows_prep +
                             // k_attn_pf + merge, 0 k_rows_prep + k_attn (SPX_PF_ATTN)
@@ -592,8 +593,9 @@ int enqueue_pass_m(spx_engine *E, int m) {
   // groups of 16 per workgroup, the attention rows are prepared once (launch_rows_prep), the
   // MoE jobs hold at most 16 users (kp_route) and are staged job by job (kp_gateup_mq)
   const bool big = m > MAX_M;
-  if (big && !E->mq) return fail("passes of more than 16 rows run on the matrix cores only");
-  auto mq_grid = [&](int tiles) { return big ? dec_mq_grid(tiles, m) : std::min(tiles, 2 * E->n_cu); };
+  const bool mq = E->mq && E->mq_shapes;  // (the lane-exact kernels where a matrix's shape has no matrix-core kernel)
+  if (big && !mq) return fail("passes of more than 16 rows run on the matrix cores only (blocks-a-row counts 1, 2, 3, 4, 8, 16)");
+  auto mq_grid = [&](int tiles) { return dec_mq_grid(tiles, m); };
   const int maxj = std::min(512, std::min(c.n_expert, m * nu) + (m * nu) / MAX_M);  // jobs of <= 16 users
   bool combine = false;  // the last MoE layer's expert outputs wait in yd for the next norm
   auto norm = [&](const float *x, const float *nw, float *xn_out, Q8KP q) {
@@ -627,9 +629,9 @@ int enqueue_pass_m(spx_engine *E, int m) {
       float *o3[3] = {E->q, E->k, E->v};
       const int64_t ld3[3] = {E->q_dim, E->kv_dim, E->kv_dim};
       int total = 0;
-      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.ld_out[i] = ld3[i]; a.tiles[i] = E->mq ? qtiles(w3[i]) : mtiles(w3[i]); total += a.tiles[i]; }
+      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.ld_out[i] = ld3[i]; a.tiles[i] = mq ? qtiles(w3[i]) : mtiles(w3[i]); total += a.tiles[i]; }
       a.nseg = 3; a.G = gshape(ly.wq); a.y = E->xq2; a.cols = dim; a.m = m;
-      SPX_HIP(E->mq ? launch_dec_mq(a, mq_grid(total), s) : launch_dec_mm(a, dec_mm_grid(total), s));
+      SPX_HIP(mq ? launch_dec_mq(a, mq_grid(total), s) : launch_dec_mm(a, dec_mm_grid(total), s));
     }
     if (int r = snap(E, l, DBG_Q, E->q, E->q_dim, m) || snap(E, l, DBG_K, E->k, E->kv_dim, m) || snap(E, l, DBG_V, E->v, E->kv_dim, m)) return r;
     const bool att_q_fused = ((c.n_heads / c.n_kv_heads) * hd) % 256 == 0;
@@ -660,10 +662,10 @@ int enqueue_pass_m(spx_engine *E, int m) {
     {
       ProfScope ps(E, PC_WO, wbytes(ly.wo));
       DecMMArgs a{};
-      a.w[0] = ly.wo->v; a.out[0] = E->proj; a.ld_out[0] = dim; a.tiles[0] = E->mq ? qtiles(ly.wo) : mtiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
+      a.w[0] = ly.wo->v; a.out[0] = E->proj; a.ld_out[0] = dim; a.tiles[0] = mq ? qtiles(ly.wo) : mtiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
       a.y = E->aq; a.cols = E->q_dim; a.m = m;
       a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
-      SPX_HIP(E->mq ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
+      SPX_HIP(mq ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
     }
     if (int r = snap(E, l, DBG_PROJ, E->proj, dim, m) || snap(E, l, DBG_XMID, E->xB, dim, m)) return r;
     const int nff = (int)ly.gate->v.rows;
@@ -687,31 +689,31 @@ int enqueue_pass_m(spx_engine *E, int m) {
           SPX_HIP(launch_kp_route(ga.rt, s));
           SPX_HIP(launch_kp_gateup_mq(ga, E->jobs, ly.njobs, maxj, s));
         } else {
-          SPX_HIP(E->mq && E->mq_gateup ? launch_dec_gateup_mq(ga, std::min(m * nu, c.n_expert), s) : launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
+          SPX_HIP(mq && E->mq_gateup ? launch_dec_gateup_mq(ga, std::min(m * nu, c.n_expert), s) : launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
         }
       }
       if (int r = snap_ffn(E, l, m)) return r;
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
         DecDownMArgs da{ly.down->v, E->h, E->jobs, ly.njobs, E->yd, big ? maxj : std::min(m * nu, c.n_expert)};
-        SPX_HIP(E->mq && (big || m >= E->mq_down_rows) ? launch_dec_down_mq(da, s) : launch_dec_down_m(da, s));
+        SPX_HIP(mq && (big || m >= E->mq_down_rows) ? launch_dec_down_mq(da, s) : launch_dec_down_m(da, s));
         combine = true;  // + weighted combine + residual in the next norm (xB -> xA)
       }
     } else {  // ffn_forward_multi (:616-646)
       {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
         if (big) SPX_HIP(launch_kp_gateup_mq(ga, nullptr, nullptr, 1, s));
-        else SPX_HIP(E->mq && E->mq_gateup ? launch_dec_gateup_mq(ga, 1, s) : launch_dec_gateup_m(ga, 1, s));
+        else SPX_HIP(mq && E->mq_gateup ? launch_dec_gateup_mq(ga, 1, s) : launch_dec_gateup_m(ga, 1, s));
         SPX_HIP(launch_q8kp_quantize(E->h, nff, nff, m, E->hq, s));
       }
       if (int r = snap_ffn(E, l, m)) return r;
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down));
         DecMMArgs a{};
-        a.w[0] = ly.down->v; a.out[0] = E->ffn; a.ld_out[0] = dim; a.tiles[0] = E->mq ? qtiles(ly.down) : mtiles(ly.down); a.nseg = 1;
+        a.w[0] = ly.down->v; a.out[0] = E->ffn; a.ld_out[0] = dim; a.tiles[0] = mq ? qtiles(ly.down) : mtiles(ly.down); a.nseg = 1;
         a.G = gshape(ly.down); a.y = E->hq; a.cols = nff; a.m = m;
         a.res_in = E->xB; a.res_out = E->xA; a.rscale = c.residual_scale;
-        SPX_HIP(E->mq ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
+        SPX_HIP(mq ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
       }
     }
   }
@@ -721,11 +723,11 @@ int enqueue_pass_m(spx_engine *E, int m) {
     SPX_HIP(norm(E->xA, E->out_norm, E->xn, E->xq));
     if (int r = snap(E, c.n_layers, DBG_XIN, E->xA, dim, m)) return r;
     DecMMArgs a{};
-    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.ld_out[0] = c.vocab; a.tiles[0] = E->mq ? qtiles(E->lm_head) : mtiles(E->lm_head); a.nseg = 1;
+    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.ld_out[0] = c.vocab; a.tiles[0] = mq ? qtiles(E->lm_head) : mtiles(E->lm_head); a.nseg = 1;
     a.G = gshape(E->lm_head); a.y = E->xq; a.cols = dim; a.m = m;
-    grid = E->mq ? mq_grid(a.tiles[0]) : std::min(a.tiles[0], 512);
+    grid = mq ? mq_grid(a.tiles[0]) : std::min(a.tiles[0], 512);
     a.best = E->best; a.nbest = grid; a.lscale = c.logit_scale;
-    SPX_HIP(E->mq ? launch_dec_mq(a, grid, s) : launch_dec_mm(a, grid, s));
+    SPX_HIP(mq ? launch_dec_mq(a, grid, s) : launch_dec_mm(a, grid, s));
   }
   E->nbest = grid;
   {
@@ -1051,6 +1053,10 @@ int spx_engine_prepare(spx_engine *E) {
     for (auto &ly : E->L) uniform = uniform && ly.gate->v.rows == E->n_ff;
     E->persist_ok = uniform && E->persist_grid_n > 0 && persist_fits(a, E->persist_grid_n);
   }
+  for (const auto &kv : E->mats) {
+    const TensorView &v = kv.second->v;
+    if ((v.dtype == T_Q4K || v.dtype == T_Q6K) && !dec_mq_nb_ok((int)v.nb)) E->mq_shapes = false;
+  }
   if (const char *v = std::getenv("SPX_PERSIST")) E->persist_on = atoi(v) != 0;
   if (std::getenv("SPX_PERSIST_TSTAMP") && E->dec_ok) E->pa.tstamp = E->dalloc<uint64_t>(4096);
   if (const char *v = std::getenv("SPX_DECODE")) E->dec_on = atoi(v) != 0;
@@ -1115,7 +1121,7 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
   if (start_pos < 0 || start_pos + m > E->c.max_seq) return fail("spx_engine_forward: positions beyond max_seq (the KV window is full)");
   for (int i = 0; i < m; i++)
     if (ids[i] < 0 || ids[i] >= E->c.vocab) return fail("spx_engine_forward: token id out of range");
-  if (m > MAX_M && !(E->dec_ok && E->dec_on && E->mq)) {
+  if (m > MAX_M && !(E->dec_ok && E->dec_on && E->mq && E->mq_shapes)) {
     // no prefill kernels for this model / setting: passes of at most 16 rows, one after the
     // other (a row's results do not depend on the rows that share its pass)
     for (int r0 = 0; r0 < m; r0 += MAX_M) {

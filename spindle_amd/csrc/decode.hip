@@ -1142,13 +1142,15 @@ __device__ __forceinline__ void mw_t4d(uint32_t a, uint32_t b, uint32_t (&r)[4])
 
 // The LDS image of a tile's vectors (at most 16): codes lq (vector v's block b at dword
 // v mw_vs + 64 b; eight pad dwords a vector put the sixteen vectors' reads of one class word in
-// different banks), block scales ld [v nb + b], bsum pairs lbs [v nb + b][8], and the
-// correction words lc (vector v's block b at v mw_cs + MQ_CW b, padded likewise).
+// different banks), block scales ld [v nb + b], the correction words lc (vector v's block b at
+// v mw_cs + MQ_CW b, padded likewise), and last the bsum pairs lbs [v nb + b][8], needed only to
+// build lc (mw_tail_off: where lbs starts; a kernel may reuse the space from there on).
 __host__ __device__ inline int mw_vs(int nb) { return nb * 64 + 8; }
 __host__ __device__ inline int mw_cs(int nb) { return nb * MQ_CW + ((8 - nb * MQ_CW) % 64 + 64) % 64; }
-__host__ __device__ inline size_t mw_act_bytes(int m, int nb) {
-  return (size_t)m * mw_vs(nb) * 4 + (((size_t)m * nb * 4 + 15) & ~(size_t)15) + (size_t)m * nb * 64 + (size_t)m * mw_cs(nb) * 4;
+__host__ __device__ inline size_t mw_tail_off(int m, int nb) {
+  return (size_t)m * mw_vs(nb) * 4 + (((size_t)m * nb * 4 + 15) & ~(size_t)15) + (size_t)m * mw_cs(nb) * 4;
 }
+__host__ __device__ inline size_t mw_act_bytes(int m, int nb) { return mw_tail_off(m, nb) + (size_t)m * nb * 64; }
 struct MwLds {
   SPX_L uint32_t *lq;
   SPX_L float *ld;
@@ -1161,9 +1163,8 @@ __device__ __forceinline__ MwLds mw_lds(uint8_t *base, int m, int nb) {
   L.lq = (SPX_L uint32_t *)base;
   L.ld = (SPX_L float *)(base + o);
   o += ((size_t)m * nb * 4 + 15) & ~(size_t)15;
-  L.lbs = (SPX_L int2 *)(base + o);
-  o += (size_t)m * nb * 64;
   L.lc = (SPX_L uint32_t *)(base + o);
+  L.lbs = (SPX_L int2 *)(base + mw_tail_off(m, nb));
   return L;
 }
 // The correction words of the image's m vectors (from the staged bsum pairs).
@@ -1534,6 +1535,252 @@ __device__ __forceinline__ void mw_meet(SPX_L float *xch, int c, const float (&p
   }
 }
 
+// ---- staged tiles: a workgroup brings a tile's bytes into LDS once (16-byte coalesced loads)
+// and its wavefronts read their classes' words from there (no lane swaps, one memory round a
+// tile). Layout of one tile (16 rows, NB blocks a row, row r's block b):
+//   codes  r MS_CR + 128 b   (MS_CR = 128 NB + 16: the 16 rows' words of one class in different banks)
+//   qh     r MS_HR + 64 b    (Q6_K; MS_HR = 64 NB + 16)
+//   scales r MS_SR + 16 b    (MS_SR = 16 NB + 8)
+//   d      (r NB + b) 4      (Q4_K d | dmin << 16; Q6_K d in the low half)
+template <int NB, bool Q6 = true>  // Q6: room for Q6_K tiles (qh)
+struct MsGeo {
+  static constexpr int CR = 128 * NB + 16, HR = 64 * NB + 16, SR = 16 * NB + 8;
+  static constexpr int OC = 0, OH = OC + 16 * CR, OS = OH + (Q6 ? 16 * HR : 0), OD = OS + 16 * SR, BYTES = OD + 16 * NB * 4;
+  // 16-byte chunks of a tile: codes, qh (Q6_K), scale lines
+  static constexpr int NCC = 128 * NB, NCH = Q6 ? 64 * NB : 0, NCS = 16 * NB, NC = NCC + NCH + NCS, ND = 16 * NB;
+};
+// TP (1 or 2) tiles' bytes in registers on their way to LDS: NT threads, chunk i = tid + NT k
+// over the tiles' chunks in turn; tile u's image at tl + u MsGeo::BYTES.
+struct MsSrc {
+  Planes pl;
+  int64_t row0;
+  int nrows;  // rows past nrows repeat the last
+};
+template <int NB, int NT, bool Q6, int TP = 1>
+struct MsLoad {
+  static_assert(TP == 1 || TP == 2, "one or two tiles");
+  using G = MsGeo<NB, Q6>;
+  static constexpr int KC = (TP * G::NC + NT - 1) / NT, KD = (TP * G::ND + NT - 1) / NT;
+  uint4 v[KC];
+  uint32_t d[KD];
+  __device__ __forceinline__ void get(int dt, const MsSrc &s0, const MsSrc &s1) {
+    const int t = threadIdx.x;
+    const bool q6 = dt == T_Q6K;
+#pragma unroll
+    for (int k = 0; k < KC; k++) {
+      const int i0 = t + NT * k, u = i0 >= G::NC ? 1 : 0, i = i0 - u * G::NC;
+      if (i0 >= TP * G::NC) continue;  // (past the last tile's chunks)
+      const MsSrc &sr = u ? s1 : s0;
+      const uint8_t *src;
+      if (i < G::NCC) {
+        const int r = i / (8 * NB), o = i - r * 8 * NB;
+        src = sr.pl.p0 + ((sr.row0 + min(r, sr.nrows - 1)) * NB) * 128 + 16 * o;
+      } else if (i < G::NCC + G::NCH) {
+        const int j = i - G::NCC, r = j / (4 * NB), o = j - r * 4 * NB;
+        if (!q6) continue;
+        src = sr.pl.p1 + ((sr.row0 + min(r, sr.nrows - 1)) * NB) * 64 + 16 * o;
+      } else {
+        const int r = (i - G::NCC - G::NCH) / NB, b = (i - G::NCC - G::NCH) - r * NB;
+        src = sr.pl.p2 + ((sr.row0 + min(r, sr.nrows - 1)) * NB + b) * 16;
+      }
+      v[k] = gld<uint4>(src);
+    }
+#pragma unroll
+    for (int k = 0; k < KD; k++) {
+      const int i0 = t + NT * k, u = i0 >= G::ND ? 1 : 0, i = i0 - u * G::ND;
+      if (i0 >= TP * G::ND) continue;
+      const MsSrc &sr = u ? s1 : s0;
+      const int r = i / NB, b = i - r * NB;
+      const int64_t ra = (sr.row0 + min(r, sr.nrows - 1)) * NB + b;
+      d[k] = q6 ? (uint32_t)gld<uint16_t>(sr.pl.p3 + ra * 2) : gld<uint32_t>(sr.pl.p1 + ra * 16);
+    }
+  }
+  __device__ __forceinline__ void get(int dt, const MsSrc &s0) { get(dt, s0, s0); }
+  __device__ __forceinline__ void put(SPX_L uint8_t *tl, int dt) const {
+    const int t = threadIdx.x;
+    const bool q6 = dt == T_Q6K;
+#pragma unroll
+    for (int k = 0; k < KC; k++) {
+      const int i0 = t + NT * k, u = i0 >= G::NC ? 1 : 0, i = i0 - u * G::NC;
+      if (i0 >= TP * G::NC) continue;  // (past the last tile's chunks)
+      SPX_L uint8_t *tu = tl + u * G::BYTES;
+      int o;
+      if (i < G::NCC) {
+        const int r = i / (8 * NB);
+        o = G::OC + r * G::CR + 16 * (i - r * 8 * NB);
+      } else if (i < G::NCC + G::NCH) {
+        if (!q6) continue;
+        const int j = i - G::NCC, r = j / (4 * NB);
+        o = G::OH + r * G::HR + 16 * (j - r * 4 * NB);
+      } else {
+        const int j = i - G::NCC - G::NCH, r = j / NB;
+        o = G::OS + r * G::SR + 16 * (j - r * NB);
+      }
+      // scale lines sit 8-byte aligned: two 8-byte stores
+      if (i >= G::NCC + G::NCH) {
+        lst<uint2>((SPX_L uint2 *)(tu + o), make_uint2(v[k].x, v[k].y));
+        lst<uint2>((SPX_L uint2 *)(tu + o + 8), make_uint2(v[k].z, v[k].w));
+      } else {
+        lst<uint4>((SPX_L uint4 *)(tu + o), v[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < KD; k++) {
+      const int i0 = t + NT * k, u = i0 >= G::ND ? 1 : 0, i = i0 - u * G::ND;
+      if (i0 < TP * G::ND) lst<uint32_t>((SPX_L uint32_t *)(tl + u * G::BYTES + G::OD + 4 * i), d[k]);
+    }
+  }
+};
+// Block b of a staged tile, part C: its integers (MwProd), as mw_prod from the LDS image.
+template <int T, int NB, bool Q6, int WPT, int C>
+__device__ __forceinline__ void ms_prod(const SPX_L uint8_t *tl, const MwDst &d, int b, MwProd<WPT> &o) {
+  using G = MsGeo<NB, Q6>;
+  const int lane = threadIdx.x & 63, k4 = lane >> 4, c16 = lane & 15;
+  const SPX_L uint32_t *py = d.py + b * 64, *pw = d.pw + b * MQ_CW;
+  const SPX_L uint8_t *rc = tl + G::OC + c16 * G::CR + 128 * b, *rs = tl + G::OS + c16 * G::SR + 16 * b;
+  const uint32_t dw = lld<uint32_t>((const SPX_L uint32_t *)(tl + G::OD + 4 * (c16 * NB + b)));
+  float xd[4];
+  const float dd = h2f(dw);
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    xd[t] = d.px[t][b];
+    o.dx[t] = dd * xd[t];
+  }
+  if constexpr (T == T_Q4K) {
+    const uint32_t sp = lld<uint16_t>((const SPX_L uint16_t *)(rs + 2 * k4));
+    const uint32_t s0 = sp & 0xFFu, s1 = (sp >> 8) & 0xFFu;
+    const uint32_t lo0 = s0 & 7u, hi0 = s0 >> 3, lo1 = s1 & 7u, hi1 = s1 >> 3;
+    constexpr int CG = 8 / WPT < 4 ? 8 / WPT : 4;
+#pragma unroll
+    for (int j0 = 0; j0 < 8 / WPT; j0 += CG) {
+      uint32_t c0[CG], c1[CG];
+      uint2 y[CG];
+#pragma unroll
+      for (int q = 0; q < CG; q++) {
+        const int l = mw_cls<WPT, C>(j0 + q);
+        const uint32_t wl = lld<uint32_t>((const SPX_L uint32_t *)(rc + 16 * l + 4 * k4));
+        c0[q] = wl & 0x0F0F0F0Fu;
+        c1[q] = (wl >> 4) & 0x0F0F0F0Fu;
+        y[q] = lld<uint2>(py + 8 * l);
+      }
+      // P = D(q sl) + 8 D(q sh), the digits accumulated on the matrix core (exact in int32)
+#pragma unroll
+      for (int q = 0; q < CG; q++) o.P[j0 + q] = mq_mfma(y[q].x, y[q].y, mx_pmul(c0[q], hi0), mx_pmul(c1[q], hi1)) * 8;
+#pragma unroll
+      for (int q = 0; q < CG; q++) o.P[j0 + q] = mq_mfma_c(y[q].x, y[q].y, mx_pmul(c0[q], lo0), mx_pmul(c1[q], lo1), o.P[j0 + q]);
+    }
+    if (C == 0) {
+      // C = sum_s mn_s (bsum_2s + bsum_2s+1): K 0-7 the sums' lo, 8-15 their hi, against the mins
+      const uint2 mn = lld<uint2>((const SPX_L uint2 *)(rs + 8));
+      const uint2 cw = lld<uint2>(pw + 8 + 2 * (k4 & 1));
+      const uint32_t a0 = k4 < 2 ? cw.x : 0u, a1 = k4 < 2 ? cw.y : 0u;
+      o.Cc = mq_mfma_c(a0, a1, mn.x, mn.y, mq_mfma(k4 == 1 ? a0 : 0u, k4 == 1 ? a1 : 0u, mn.x, mn.y) * 63);
+      const float dm = h2f(dw >> 16);
+#pragma unroll
+      for (int t = 0; t < 4; t++) o.cf[t] = dm * xd[t];
+    }
+  } else {
+    const SPX_L uint8_t *rh = tl + G::OH + c16 * G::HR + 64 * b;
+    const int h = k4 >> 1, sh = 4 * (k4 & 1);
+    const uint32_t sw = lld<uint32_t>((const SPX_L uint32_t *)(rs + 4 * k4));
+    uint32_t l0[8 / WPT], h0[8 / WPT], l1[8 / WPT], h1[8 / WPT];
+    uint2 y[8 / WPT];
+#pragma unroll
+    for (int j = 0; j < 8 / WPT; j++) {
+      const int l = mw_cls<WPT, C>(j);
+      const uint2 ql = lld<uint2>((const SPX_L uint2 *)(rc + 16 * l + 8 * h));
+      const uint32_t qh = lld<uint32_t>((const SPX_L uint32_t *)(rh + 8 * l + 4 * h));
+      const uint32_t c0 = ((ql.x >> sh) & 0x0F0F0F0Fu) | (((qh >> sh) & 0x03030303u) << 4);
+      const uint32_t c1 = ((ql.y >> sh) & 0x0F0F0F0Fu) | (((qh >> (sh + 2)) & 0x03030303u) << 4);
+      l0[j] = c0 & 0x07070707u;
+      h0[j] = (c0 >> 3) & 0x07070707u;
+      l1[j] = c1 & 0x07070707u;
+      h1[j] = (c1 >> 3) & 0x07070707u;
+      y[j] = lld<uint2>(py + 8 * l);
+    }
+    // P = D(ql sl) + 8 (D(qh sl) + 2 (D(ql sh) + 8 D(qh sh))), accumulated on the matrix core;
+    // a class's scales: groups 2 s + (l >= 4) of its sub-blocks s = 2 k4, 2 k4 + 1
+#pragma unroll
+    for (int j = 0; j < 8 / WPT; j++) {
+      const int l = mw_cls<WPT, C>(j), hb = l >= 4 ? 8 : 0;
+      const int sh1 = (int)(int8_t)(sw >> (16 + hb)) >> 4, sh0 = (int)(int8_t)(sw >> hb) >> 4;
+      o.P[j] = mq_mfma(y[j].x, y[j].y, mx_pmul_s(h0[j], sh0), mx_pmul_s(h1[j], sh1)) * 8;
+    }
+#pragma unroll
+    for (int j = 0; j < 8 / WPT; j++) {
+      const int l = mw_cls<WPT, C>(j), hb = l >= 4 ? 8 : 0;
+      const int sh1 = (int)(int8_t)(sw >> (16 + hb)) >> 4, sh0 = (int)(int8_t)(sw >> hb) >> 4;
+      o.P[j] = mq_mfma_c(y[j].x, y[j].y, mx_pmul_s(l0[j], sh0), mx_pmul_s(l1[j], sh1), o.P[j]) * 2;
+    }
+#pragma unroll
+    for (int j = 0; j < 8 / WPT; j++) {
+      const int l = mw_cls<WPT, C>(j), hb = l >= 4 ? 8 : 0;
+      const uint32_t sl0 = (uint32_t)((int)(int8_t)(sw >> hb) & 15), sl1 = (uint32_t)((int)(int8_t)(sw >> (16 + hb)) & 15);
+      o.P[j] = mq_mfma_c(y[j].x, y[j].y, mx_pmul(h0[j], sl0), mx_pmul(h1[j], sl1), o.P[j]) * 8;
+    }
+#pragma unroll
+    for (int j = 0; j < 8 / WPT; j++) {
+      const int l = mw_cls<WPT, C>(j), hb = l >= 4 ? 8 : 0;
+      const uint32_t sl0 = (uint32_t)((int)(int8_t)(sw >> hb) & 15), sl1 = (uint32_t)((int)(int8_t)(sw >> (16 + hb)) & 15);
+      o.P[j] = mq_mfma_c(y[j].x, y[j].y, mx_pmul(l0[j], sl0), mx_pmul(l1[j], sl1), o.P[j]);
+    }
+    if (C == 0) {
+      // C = sum_g sc_g bsum_g: K 0-15 the bsums' lo, 16-31 their hi, against the scales
+      const uint2 bb = lld<uint2>((const SPX_L uint2 *)(rs + 8 * (k4 & 1)));
+      const uint2 cw = lld<uint2>(pw + 2 * k4);
+      const bool lo = k4 < 2;
+      o.Cc = mq_mfma_c(cw.x, cw.y, bb.x, bb.y, mq_mfma(lo ? 0u : cw.x, lo ? 0u : cw.y, bb.x, bb.y) * 63) * 32;
+#pragma unroll
+      for (int t = 0; t < 4; t++) o.cf[t] = dd * xd[t];
+    }
+  }
+}
+// Part C's chains over a staged tile's NB blocks (integers of BB blocks issued together).
+template <int NB, int TT, int WPT, int C>
+__device__ __forceinline__ void ms_tile(const SPX_L uint8_t *tl, int dt, const MwDst &d, float (&part)[4], float (&cr)[4]) {
+  constexpr int BB = NB % 4 == 0 ? 4 : NB % 2 == 0 ? 2 : 1;
+  float acc[8 / WPT][4];
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    cr[t] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8 / WPT; j++) acc[j][t] = 0.0f;
+  }
+  for (int b0 = 0; b0 < NB; b0 += BB) {
+    MwProd<WPT> pr[BB];
+#pragma unroll
+    for (int q = 0; q < BB; q++) {
+      if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) ms_prod<T_Q4K, NB, TT != T_Q4K, WPT, C>(tl, d, b0 + q, pr[q]);
+      else ms_prod<T_Q6K, NB, true, WPT, C>(tl, d, b0 + q, pr[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < BB; q++) mw_chain<WPT, C>(pr[q], acc, cr);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    if constexpr (WPT == 1)
+      part[t] = (((acc[0][t] + acc[4][t]) + (acc[2][t] + acc[6][t])) + ((acc[1][t] + acc[5][t]) + (acc[3][t] + acc[7][t]))) - cr[t];
+    else if constexpr (WPT == 2)
+      part[t] = (acc[0][t] + acc[2][t]) + (acc[1][t] + acc[3][t]);
+    else
+      part[t] = acc[0][t] + acc[1][t];
+  }
+}
+template <int NB, int TT, int WPT>
+__device__ __forceinline__ void ms_tile_part(int c, const SPX_L uint8_t *tl, int dt, const MwDst &d, float (&part)[4], float (&cr)[4]) {
+  if constexpr (WPT == 2) {
+    if (c == 0) ms_tile<NB, TT, 2, 0>(tl, dt, d, part, cr);
+    else ms_tile<NB, TT, 2, 1>(tl, dt, d, part, cr);
+  } else {
+    switch (c) {
+    case 0: ms_tile<NB, TT, 4, 0>(tl, dt, d, part, cr); break;
+    case 1: ms_tile<NB, TT, 4, 1>(tl, dt, d, part, cr); break;
+    case 2: ms_tile<NB, TT, 4, 2>(tl, dt, d, part, cr); break;
+    default: ms_tile<NB, TT, 4, 3>(tl, dt, d, part, cr); break;
+    }
+  }
+}
+
 // A unit of kd_mq: tile t (segment si, rows row0 .. row0 + nrows - 1). The bookkeeping is
 // wave-uniform and kept scalar (readfirstlane), so the segment's fields are read from the
 // arguments with scalar loads.
@@ -1630,6 +1877,75 @@ __global__ __launch_bounds__(MW_NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
   }
 }
 
+// kd_mq for up to 16 vectors on staged tiles (few tiles: q|k|v, the attention output): workgroup
+// r takes tiles r, r + R, ...; the tile's bytes come into LDS in one round (MsLoad: the next
+// tile's loads fly while this one is multiplied), its four wavefronts each take a quarter of the
+// lane classes (mw_cls, WPT 4) and their partial sums meet in LDS; part 0 runs the epilogue.
+template <int NB, int TT>
+__global__ __launch_bounds__(MW_NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void kd_mqs(const DecMMArgs a) {
+  static_assert(MW_NW == 4, "a wavefront per part of four");
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ unsigned long long sbest[MAX_M];
+  __shared__ float xch[2][MW_NW][4][64];
+  const int m = a.m, cols = a.cols;
+  const MwLds L = mw_lds(smem, m, NB);
+  SPX_L uint8_t *tl = (SPX_L uint8_t *)(smem + mw_tail_off(m, NB));  // (over lbs, once lc is built)
+  const int total = a.tiles[0] + (a.nseg > 1 ? a.tiles[1] : 0) + (a.nseg > 2 ? a.tiles[2] : 0);
+  const int c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, c16 = lane & 15;
+  const int R = gridDim.x, nr = (int)blockIdx.x < total ? (total - (int)blockIdx.x + R - 1) / R : 0;
+  auto pos_of = [&](int i) SPX_AI {
+    MqPos p;
+    p.t = blockIdx.x + i * R;
+    mq_locate(a, total, p);
+    return p;
+  };
+  MsLoad<NB, MW_NW * 64, TT != T_Q4K> ld;
+  auto msrc = [&](const MqPos &p) SPX_AI { return MsSrc{a.w[p.si].pl, p.row0, p.nrows}; };
+  if (nr > 0) {
+    const MqPos p = pos_of(0);
+    ld.get(a.w[p.si].dtype, msrc(p));
+  }
+  if (threadIdx.x < MAX_M) sbest[threadIdx.x] = 0;
+  stage_q8<MW_NW * 64>(a.y, (const int *)nullptr, m, cols, L.lq, L.ld, L.lbs, mw_vs(NB) / 4);
+  __syncthreads();
+  mq_corr_stage(m, NB, L.lbs, L.lc);
+  __syncthreads();  // lbs read: the tile may take its place
+  const MqVec vv = mq_vecs(m, MqIdentity{});
+  for (int i = 0; i < nr; i++) {
+    const MqPos p = pos_of(i);
+    const int dt = __builtin_amdgcn_readfirstlane(a.w[p.si].dtype);
+    ld.put(tl, dt);
+    __syncthreads();
+    if (i + 1 < nr) {  // the next tile's bytes requested before this one's arithmetic
+      const MqPos q = pos_of(i + 1);
+      ld.get(a.w[q.si].dtype, msrc(q));
+    }
+    float part[4], cr[4], out[4];
+    ms_tile_part<NB, TT, 4>(c, tl, dt, mw_dst(L, vv, NB, dt), part, cr);
+    mw_meet<4>((SPX_L float *)&xch[i & 1][0][0][0], c, part, cr, out);  // (its barrier: the tile is read)
+    if (c != 0) continue;
+    float *const o = a.out[p.si];
+    const int64_t wrows = a.w[p.si].rows, ldo = a.ld_out[p.si];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const int v = 4 * (lane >> 4) + t;
+      if (v < m && c16 < p.nrows) {
+        const int64_t row = p.row0 + c16;
+        if (o) gst<float>(o + v * ldo + row, out[t]);
+        if (a.res_out) {
+          const int64_t q = v * wrows + row;
+          gst<float>(a.res_out + q, gld<float>(a.res_in + q) + a.rscale * out[t]);
+        }
+        if (a.best) atomicMax(&sbest[v], pick_key(out[t], a.lscale, row));
+      }
+    }
+  }
+  if (a.best) {
+    __syncthreads();
+    if ((int)threadIdx.x < m) gst<unsigned long long>(a.best + (int64_t)threadIdx.x * a.nbest + blockIdx.x, sbest[threadIdx.x]);
+  }
+}
+
 // Routing + gate/up + SwiGLU over the jobs on the matrix cores (kd_gateup_m's prologue and job
 // list): items (job, 16 h rows), TP = NW / WPT of them a round: round i of workgroup b takes
 // items (b + G i) TP .. + TP - 1, each walked (gate tile, then up tile) by WPT wavefronts whose
@@ -1695,6 +2011,78 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
     }
   };
   mw_walk_part<NB, T, WPT>(c, 2 * nr, src, dst, done);
+}
+
+// kd_gateup_mq on staged tiles: rounds of two items' gate tiles, then their up tiles (MsLoad: a
+// round's bytes come into LDS at once, the next round's loads fly during this one); wavefronts
+// 0-3 take the first item's tile, 4-7 the second's, a quarter of the lane classes each, their
+// partial sums meeting in LDS; part 0 applies SwiGLU. Workgroup b takes item pairs b, b + G, ...
+template <int T, int NB>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void kd_gateup_mqs(const DecGateUpMArgs a) {
+  constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M;
+  static_assert(NW == 8, "two items of four wavefronts");
+  using G = MsGeo<NB, T == T_Q6K>;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ signed char slot_of[MAX_M * 256];
+  __shared__ int wcount[NW];
+  __shared__ float xch[2][NW][4][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int g = wave >> 2, c = wave & 3;
+  const int n_ff = a.n_ff, cols = (int)a.gate.cols, m = a.m;
+  const int TX = (n_ff + 15) / 16;
+  const MwLds L = mw_lds(smem, m, NB);
+  SPX_L uint8_t *tl = (SPX_L uint8_t *)(smem + mw_tail_off(m, NB));  // (over lbs, once lc is built)
+  SPX_L int *sj = (SPX_L int *)(smem + mw_tail_off(m, NB) + (((size_t)std::max(m * NB * 64, 2 * G::BYTES) + 15) & ~(size_t)15));
+  int nj = 1;
+  StageQ8<NW * 64> st;
+  if (a.rt.logits) {
+    float lv[2][4];
+    route_load<NW>(a.rt, lv);
+    st.get(a.y, m, cols);
+    nj = route_jobs<NW>(a.rt, lv, sj, (SPX_L signed char *)slot_of, (SPX_L int *)wcount, blockIdx.x == 0);
+  } else {
+    st.get(a.y, m, cols);
+    for (int i = threadIdx.x; i < JR; i += blockDim.x) sj[i] = i == 0 ? 0 : i == 1 ? m : i < 2 + MAX_M ? i - 2 : i - 2 - MAX_M;
+    __syncthreads();
+  }
+  const int n = TX * nj, R = gridDim.x, np = (n + 1) / 2, nr = (int)blockIdx.x < np ? (np - (int)blockIdx.x + R - 1) / R : 0;
+  // round k: item pair blockIdx.x + R (k / 2), gate (k even) or up tiles
+  auto item = [&](int k, int u) SPX_AI { return min(2 * ((int)blockIdx.x + R * (k >> 1)) + u, n - 1); };
+  auto msrc = [&](int k, int u) SPX_AI {
+    const int i = item(k, u), j = i / TX, x = i - j * TX;
+    const int e = __builtin_amdgcn_readfirstlane(min(max(sj[j * JR], 0), a.gate.n_expert - 1));
+    return MsSrc{(k & 1) ? a.up.pl : a.gate.pl, (int64_t)e * a.gate.rows + (int64_t)x * 16, min(16, n_ff - x * 16)};
+  };
+  MsLoad<NB, NW * 64, T == T_Q6K, 2> ld;
+  if (nr > 0) ld.get(T, msrc(0, 0), msrc(0, 1));
+  st.put(m, cols, L.lq, L.ld, L.lbs, mw_vs(NB) / 4);
+  __syncthreads();
+  mq_corr_stage(m, NB, L.lbs, L.lc);
+  __syncthreads();  // lbs read: the tiles may take its place
+  float gv[4];
+  for (int k = 0; k < 2 * nr; k++) {
+    ld.put(tl, T);
+    __syncthreads();
+    if (k + 1 < 2 * nr) ld.get(T, msrc(k + 1, 0), msrc(k + 1, 1));
+    const int i = item(k, g), j = i / TX, x = i - j * TX;
+    float part[4], cr[4], out[4];
+    ms_tile_part<NB, T, 4>(c, tl + g * G::BYTES, T, mw_dst(L, mq_vecs(sj[j * JR + 1], MqRows{sj + j * JR + 2}), NB, T), part, cr);
+    mw_meet<4>((SPX_L float *)&xch[k & 1][4 * g][0][0], c, part, cr, out);  // (its barrier: the tiles are read)
+    if (c != 0) continue;
+    if (!(k & 1)) {
+#pragma unroll
+      for (int t = 0; t < 4; t++) gv[t] = out[t];
+      continue;
+    }
+    if (2 * ((int)blockIdx.x + R * (k >> 1)) + g >= n) continue;
+    const int nv = sj[j * JR + 1], r = lane & 15;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const int v = 4 * (lane >> 4) + t;
+      if (v < nv && x * 16 + r < n_ff)
+        gst<float>(a.h + (int64_t)sj[j * JR + 2 + MAX_M + v] * n_ff + x * 16 + r, gv[t] / (1.0f + expf(-gv[t])) * out[t]);
+    }
+  }
 }
 
 // Down projection of the jobs' users on the matrix cores: items (job, DOWN_MQ_ROWS = 8 tiles),
@@ -1777,6 +2165,92 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
   };
   if (nit > 0) stage(0);
   mw_walk_part<NB, T, WPT>(c, nit * RI, src, dst, done);
+}
+
+// kd_down_mq for passes of up to 16 rows on staged tiles: an item's eight tiles in four rounds
+// of two (MsLoad; the next round's loads, the next item's included, fly during this one),
+// wavefronts 0-3 on the first tile, 4-7 on the second, a quarter of the lane classes each.
+template <int T, int NB>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void kd_down_mqs(const DecDownMArgs a) {
+  constexpr int NW = DEC_MM_NW, JF = 2 + MAX_M, RI = 4;  // RI: rounds an item
+  static_assert(DOWN_MQ_ROWS == 16 * 2 * RI, "eight tiles an item");
+  using G = MsGeo<NB, T == T_Q6K>;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int s_job[JF];
+  __shared__ int ihead[DOWN_MQ_ITEMS][2];  // expert, users of the workgroup's items
+  __shared__ float xch[2][NW][4][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int g = wave >> 2, c = wave & 3;
+  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, TX = (dim + DOWN_MQ_ROWS - 1) / DOWN_MQ_ROWS, R = gridDim.x;
+  const MwLds L = mw_lds(smem, MAX_M, NB);
+  SPX_L uint8_t *tl = (SPX_L uint8_t *)(smem + mw_tail_off(MAX_M, NB));  // (over lbs between the items' stagings)
+  const int n = TX * gld<int>(a.njobs), nit = (int)blockIdx.x < n ? (n - (int)blockIdx.x + R - 1) / R : 0;
+  for (int k = threadIdx.x; k < min(nit, DOWN_MQ_ITEMS); k += blockDim.x) {
+    const int j = ((int)blockIdx.x + R * k) / TX;
+    ihead[k][0] = min(max(gld<int>(reinterpret_cast<const int *>(a.jobs + j)), 0), a.w.n_expert - 1);
+    ihead[k][1] = min(max(gld<int>(reinterpret_cast<const int *>(a.jobs + j) + 1), 0), MAX_M);
+  }
+  __syncthreads();
+  // round k: item k / RI, its tiles 2 (k % RI) + u
+  auto row0 = [&](int k, int u) SPX_AI {
+    const int it = (int)blockIdx.x + R * (k / RI);
+    return (it - (it / TX) * TX) * DOWN_MQ_ROWS + 16 * (2 * (k % RI) + u);
+  };
+  auto msrc = [&](int k, int u) SPX_AI {
+    const int r0 = row0(k, u);
+    return MsSrc{a.w.pl, (int64_t)ihead[k / RI][0] * dim + min(r0, dim - 1), max(1, min(16, dim - r0))};
+  };
+  MsLoad<NB, NW * 64, T == T_Q6K, 2> ld;
+  if (nit > 0) ld.get(T, msrc(0, 0), msrc(0, 1));
+  for (int k = 0; k < nit * RI; k++) {
+    if (k % RI == 0) {  // item k / RI: its users' h rows, quantized (quantize_avx2 per 256 block)
+      const int j = ((int)blockIdx.x + R * (k / RI)) / TX;
+      if ((int)threadIdx.x < JF) {
+        const int f = threadIdx.x;
+        s_job[f] = gld<int>(reinterpret_cast<const int *>(a.jobs + j) + (f < 2 ? f : 2 + MAX_M + (f - 2)));
+      }
+      __syncthreads();
+      const int nv = min(max(s_job[1], 0), MAX_M), nq = nv * NB;
+      for (int q0 = wave; q0 < nq; q0 += 4 * NW) {
+        float4 hv[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const int q = q0 + NW * t;
+          if (q < nq) {
+            const int u = q / NB, i = q - u * NB;
+            hv[t] = gld<float4>(a.h + (int64_t)s_job[2 + u] * n_ff + i * 256 + 4 * lane);
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const int q = q0 + NW * t;
+          if (q < nq) {
+            const int u = q / NB, i = q - u * NB;
+            const float am = q8k_amax(hv[t]);
+            q8k_block_store(hv[t], am, L.lq + u * mw_vs(NB) + i * 64, L.ld + q, (SPX_L int *)L.lbs + q * 16);
+          }
+        }
+      }
+      __syncthreads();
+      mq_corr_stage(nv, NB, L.lbs, L.lc);
+      __syncthreads();  // lbs read: the tiles may take its place
+    }
+    ld.put(tl, T);
+    __syncthreads();
+    if (k + 1 < nit * RI) ld.get(T, msrc(k + 1, 0), msrc(k + 1, 1));
+    float part[4], cr[4], out[4];
+    ms_tile_part<NB, T, 4>(c, tl + g * G::BYTES, T, mw_dst(L, mq_vecs(ihead[k / RI][1], MqIdentity{}), NB, T), part, cr);
+    mw_meet<4>((SPX_L float *)&xch[k & 1][4 * g][0][0], c, part, cr, out);  // (its barrier: the tiles are read)
+    if (c == 0) {
+      const int r0 = row0(k, g), nv = ihead[k / RI][1], r = lane & 15;
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int v = 4 * (lane >> 4) + t;
+        if (v < nv && r0 + r < dim) gst<float>(a.yd + (int64_t)s_job[2 + v] * dim + r0 + r, out[t]);
+      }
+    }
+    if (k % RI == RI - 1) __syncthreads();  // every reader of s_job and the staged h is done
+  }
 }
 
 // ------------------------------------------------------------------ prefill passes (17..128 rows)
@@ -2103,9 +2577,21 @@ static hipError_t with_nb(int nb, F &&f) {
   }
 }
 
-// Wavefronts a tile of kd_mq (the class split): few tiles 4 (a quarter of the classes' path
-// each), many 1 (throughput; the LM head), prefill 1.
-static int mq_wpt(int tiles, int m) { return m > MAX_M ? 1 : tiles <= 2 * cu_count() ? 4 : tiles <= 4 * cu_count() ? 2 : 1; }
+static size_t ms_tile_bytes(int nb, bool q6) {
+  switch (nb) {
+  case 1: return q6 ? MsGeo<1, true>::BYTES : MsGeo<1, false>::BYTES;
+  case 2: return q6 ? MsGeo<2, true>::BYTES : MsGeo<2, false>::BYTES;
+  case 3: return q6 ? MsGeo<3, true>::BYTES : MsGeo<3, false>::BYTES;
+  case 4: return q6 ? MsGeo<4, true>::BYTES : MsGeo<4, false>::BYTES;
+  case 8: return q6 ? MsGeo<8, true>::BYTES : MsGeo<8, false>::BYTES;
+  default: return q6 ? MsGeo<16, true>::BYTES : MsGeo<16, false>::BYTES;
+  }
+}
+// kd_mq's form: up to 16 vectors and up to four tiles a CU, the staged tiles (kd_mqs: four
+// wavefronts a tile); taller matrices (the LM head), one wavefront a tile (kd_mq's walk, WPT 1);
+// prefill, two (WPT 2: the walk's eight chains and block ring exceed the registers of one
+// wavefront when the formats are mixed).
+static int mq_wpt(int tiles, int m) { return m > MAX_M ? 2 : tiles > 4 * cu_count() ? 1 : 4; }
 
 hipError_t launch_dec_mq(const DecMMArgs &a, int grid, hipStream_t s) {
   const int nb = a.cols >> 8, nvg = (a.m + 15) / 16;
@@ -2126,11 +2612,18 @@ hipError_t launch_dec_mq(const DecMMArgs &a, int grid, hipStream_t s) {
     hipLaunchKernelGGL(kern, g, b, sm, s, a);
     return hipGetLastError();
   };
+  const int mv = std::min(a.m, MAX_M);
+  const size_t sms = mw_tail_off(mv, nb) + std::max((size_t)mv * nb * 64, ms_tile_bytes(nb, tt != T_Q4K));
+  auto gos = [&](auto kern) {
+    SPX_DLDS(kern, sms);
+    hipLaunchKernelGGL(kern, g, b, sms, s, a);
+    return hipGetLastError();
+  };
   return with_nb(nb, [&](auto NBc) {
     constexpr int NB = decltype(NBc)::value;
     auto by_wpt = [&](auto TTc) {
       constexpr int TT = decltype(TTc)::value;
-      return wpt == 4 ? go(kd_mq<NB, TT, 4>) : wpt == 2 ? go(kd_mq<NB, TT, 2>) : go(kd_mq<NB, TT, 1>);
+      return wpt == 4 ? gos(kd_mqs<NB, TT>) : wpt == 2 ? go(kd_mq<NB, TT, 2>) : go(kd_mq<NB, TT, 1>);
     };
     if (tt == T_Q4K) return by_wpt(std::integral_constant<int, T_Q4K>{});
     if (tt == T_Q6K) return by_wpt(std::integral_constant<int, T_Q6K>{});
@@ -2156,13 +2649,14 @@ hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &args, int max_jobs, hipStr
       max_jobs > 512 || (a.rt.logits && (max_jobs > a.gate.n_expert || a.rt.m != a.m || a.rt.n_expert < 1 || a.rt.n_expert > 256 || a.rt.n_used < 1 ||
                                          a.rt.n_used > 32 || a.rt.n_used > a.rt.n_expert)))
     return hipErrorInvalidValue;
-  const size_t sm = mw_act_bytes(a.m, nb) + (size_t)(a.rt.logits ? max_jobs : 1) * (2 + 2 * MAX_M) * 4;
-  if (sm > 120 * 1024) return hipErrorInvalidValue;
-  // four wavefronts an item (two items a round), one workgroup a CU: every workgroup routes the
-  // pass (the items beyond the job count end at once)
-  const int items = ((a.n_ff + 15) / 16) * (a.rt.logits ? max_jobs : 1), tp = DEC_MM_NW / 4;
-  const dim3 grid((unsigned)std::max(1, std::min((items + tp - 1) / tp, cu_count()))), b(DEC_MM_NW * 64);
   if (a.gate.dtype != T_Q4K && a.gate.dtype != T_Q6K) return hipErrorInvalidValue;
+  // staged tiles: two items a round, one workgroup a CU; every workgroup routes the pass (the
+  // items beyond the job count end at once)
+  const size_t jb = (size_t)(a.rt.logits ? max_jobs : 1) * (2 + 2 * MAX_M) * 4;
+  const size_t sm = mw_tail_off(a.m, nb) + ((std::max((size_t)a.m * nb * 64, 2 * ms_tile_bytes(nb, a.gate.dtype == T_Q6K)) + 15) & ~(size_t)15) + jb;
+  if (sm > 136 * 1024) return hipErrorInvalidValue;
+  const int items = ((a.n_ff + 15) / 16) * (a.rt.logits ? max_jobs : 1);
+  const dim3 grid((unsigned)std::max(1, std::min((items + 1) / 2, cu_count()))), b(DEC_MM_NW * 64);
   auto go = [&](auto kern) {
     SPX_DLDS(kern, sm);
     hipLaunchKernelGGL(kern, grid, b, sm, s, a);
@@ -2170,7 +2664,7 @@ hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &args, int max_jobs, hipStr
   };
   return with_nb(nb, [&](auto NBc) {
     constexpr int NB = decltype(NBc)::value;
-    return a.gate.dtype == T_Q4K ? go(kd_gateup_mq<T_Q4K, NB, 4>) : go(kd_gateup_mq<T_Q6K, NB, 4>);
+    return a.gate.dtype == T_Q4K ? go(kd_gateup_mqs<T_Q4K, NB>) : go(kd_gateup_mqs<T_Q6K, NB>);
   });
 }
 
@@ -2212,12 +2706,19 @@ hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(kern, grid, b, sm, s, a);
     return hipGetLastError();
   };
-  // a pass of up to 16 rows (at most 128 jobs): four wavefronts a tile; prefill: one
-  const bool split = a.max_jobs <= 128;
+  // a pass of up to 16 rows (at most 128 jobs): staged tiles, four wavefronts a tile; prefill:
+  // one wavefront a tile
+  const size_t sms = mw_tail_off(MAX_M, (int)a.w.nb) + std::max((size_t)MAX_M * a.w.nb * 64, 2 * ms_tile_bytes((int)a.w.nb, a.w.dtype == T_Q6K));
+  auto gos = [&](auto kern) {
+    SPX_DLDS(kern, sms);
+    hipLaunchKernelGGL(kern, grid, b, sms, s, a);
+    return hipGetLastError();
+  };
+  const bool staged = a.max_jobs <= 128;
   return with_nb((int)a.w.nb, [&](auto NBc) {
     constexpr int NB = decltype(NBc)::value;
-    if (a.w.dtype == T_Q4K) return split ? go(kd_down_mq<T_Q4K, NB, 4>) : go(kd_down_mq<T_Q4K, NB, 1>);
-    return split ? go(kd_down_mq<T_Q6K, NB, 4>) : go(kd_down_mq<T_Q6K, NB, 1>);
+    if (a.w.dtype == T_Q4K) return staged ? gos(kd_down_mqs<T_Q4K, NB>) : go(kd_down_mq<T_Q4K, NB, 1>);
+    return staged ? gos(kd_down_mqs<T_Q6K, NB>) : go(kd_down_mq<T_Q6K, NB, 1>);
   });
 }
 

@@ -66,10 +66,14 @@ struct spx_engine {
   int lm_dec_grid = 256;  // decode pipeline: LM head workgroups (SPX_LM_DEC_GRID), one per CU
   int n_cu = 256;         // compute units of the device
   bool mq = true;          // passes of 2..16 rows on the int8 matrix cores (SPX_MQ, spx_engine_set_mfma)
-  int mq_down_rows = 4;    // the routed experts' down projection on MFMA from this many rows (SPX_MQ_DOWN_ROWS):
-                           // a pass of fewer rows gives an expert about one row, the MFMA's 16 columns idle
-                           // and the per-lane dot kernel is faster
-  bool mq_gateup = true;   // the gate/up projections (SPX_MQ_GATEUP)
+  // passes of 2..16 rows: the matrix-core kernels from this many rows, per projection (q|k|v,
+  // attention output, gate/up, routed down, LM head; SPX_MQ_ROWS "a,b,c,d,e"); below, the
+  // lane-exact kernels (the same bits). Qwen3-30B-A3B shapes, us per launch (matrix cores vs
+  // lane-exact): rows 2: 11.2/8.2, 9.9/6.4, 17.4/14.9, 9.4 (lane), 114/93; rows 9: 12.0/13.5,
+  // 12.6/11.3, 23.0/31.5, 19.8/16.8, 117/191; rows 16: 12.4/27.7, 13.9/15.1, 26.2/72.8,
+  // 22.0/25.4, 119/420.
+  enum { MQ_QKV, MQ_WO, MQ_GATEUP, MQ_DOWN, MQ_LM, MQ_KINDS };
+  int mq_rows[MQ_KINDS] = {6, 12, 5, 12, 4};
   bool mq_shapes = true;   // every K-quant matrix's blocks-a-row count is one the matrix-core kernels take (dec_mq_nb_ok)
   int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
   int pf_attn = 2;          // prefill passes: 2 the multi-tile kernels (at least 2 query heads a kv head), 1 k_rows_prep +
@@ -595,6 +599,7 @@ int enqueue_pass_m(spx_engine *E, int m) {
   const bool big = m > MAX_M;
   const bool mq = E->mq && E->mq_shapes;  // (the lane-exact kernels where a matrix's shape has no matrix-core kernel)
   if (big && !mq) return fail("passes of more than 16 rows run on the matrix cores only (blocks-a-row counts 1, 2, 3, 4, 8, 16)");
+  auto mqk = [&](int kind) { return mq && (big || m >= E->mq_rows[kind]); };
   auto mq_grid = [&](int tiles) { return dec_mq_grid(tiles, m); };
   const int maxj = std::min(512, std::min(c.n_expert, m * nu) + (m * nu) / MAX_M);  // jobs of <= 16 users
   bool combine = false;  // the last MoE layer's expert outputs wait in yd for the next norm
@@ -629,9 +634,9 @@ int enqueue_pass_m(spx_engine *E, int m) {
       float *o3[3] = {E->q, E->k, E->v};
       const int64_t ld3[3] = {E->q_dim, E->kv_dim, E->kv_dim};
       int total = 0;
-      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.ld_out[i] = ld3[i]; a.tiles[i] = mq ? qtiles(w3[i]) : mtiles(w3[i]); total += a.tiles[i]; }
+      for (int i = 0; i < 3; i++) { a.w[i] = w3[i]->v; a.out[i] = o3[i]; a.ld_out[i] = ld3[i]; a.tiles[i] = mqk(spx_engine::MQ_QKV) ? qtiles(w3[i]) : mtiles(w3[i]); total += a.tiles[i]; }
       a.nseg = 3; a.G = gshape(ly.wq); a.y = E->xq2; a.cols = dim; a.m = m;
-      SPX_HIP(mq ? launch_dec_mq(a, mq_grid(total), s) : launch_dec_mm(a, dec_mm_grid(total), s));
+      SPX_HIP(mqk(spx_engine::MQ_QKV) ? launch_dec_mq(a, mq_grid(total), s) : launch_dec_mm(a, dec_mm_grid(total), s));
     }
     if (int r = snap(E, l, DBG_Q, E->q, E->q_dim, m) || snap(E, l, DBG_K, E->k, E->kv_dim, m) || snap(E, l, DBG_V, E->v, E->kv_dim, m)) return r;
     const bool att_q_fused = ((c.n_heads / c.n_kv_heads) * hd) % 256 == 0;
@@ -662,10 +667,10 @@ int enqueue_pass_m(spx_engine *E, int m) {
     {
       ProfScope ps(E, PC_WO, wbytes(ly.wo));
       DecMMArgs a{};
-      a.w[0] = ly.wo->v; a.out[0] = E->proj; a.ld_out[0] = dim; a.tiles[0] = mq ? qtiles(ly.wo) : mtiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
+      a.w[0] = ly.wo->v; a.out[0] = E->proj; a.ld_out[0] = dim; a.tiles[0] = mqk(spx_engine::MQ_WO) ? qtiles(ly.wo) : mtiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
       a.y = E->aq; a.cols = E->q_dim; a.m = m;
       a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
-      SPX_HIP(mq ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
+      SPX_HIP(mqk(spx_engine::MQ_WO) ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
     }
     if (int r = snap(E, l, DBG_PROJ, E->proj, dim, m) || snap(E, l, DBG_XMID, E->xB, dim, m)) return r;
     const int nff = (int)ly.gate->v.rows;
@@ -689,31 +694,31 @@ int enqueue_pass_m(spx_engine *E, int m) {
           SPX_HIP(launch_kp_route(ga.rt, s));
           SPX_HIP(launch_kp_gateup_mq(ga, E->jobs, ly.njobs, maxj, s));
         } else {
-          SPX_HIP(mq && E->mq_gateup ? launch_dec_gateup_mq(ga, std::min(m * nu, c.n_expert), s) : launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
+          SPX_HIP(mqk(spx_engine::MQ_GATEUP) ? launch_dec_gateup_mq(ga, std::min(m * nu, c.n_expert), s) : launch_dec_gateup_m(ga, std::min(m * nu, c.n_expert), s));
         }
       }
       if (int r = snap_ffn(E, l, m)) return r;
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
         DecDownMArgs da{ly.down->v, E->h, E->jobs, ly.njobs, E->yd, big ? maxj : std::min(m * nu, c.n_expert)};
-        SPX_HIP(mq && (big || m >= E->mq_down_rows) ? launch_dec_down_mq(da, s) : launch_dec_down_m(da, s));
+        SPX_HIP(mqk(spx_engine::MQ_DOWN) ? launch_dec_down_mq(da, s) : launch_dec_down_m(da, s));
         combine = true;  // + weighted combine + residual in the next norm (xB -> xA)
       }
     } else {  // ffn_forward_multi (:616-646)
       {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
         if (big) SPX_HIP(launch_kp_gateup_mq(ga, nullptr, nullptr, 1, s));
-        else SPX_HIP(mq && E->mq_gateup ? launch_dec_gateup_mq(ga, 1, s) : launch_dec_gateup_m(ga, 1, s));
+        else SPX_HIP(mqk(spx_engine::MQ_GATEUP) ? launch_dec_gateup_mq(ga, 1, s) : launch_dec_gateup_m(ga, 1, s));
         SPX_HIP(launch_q8kp_quantize(E->h, nff, nff, m, E->hq, s));
       }
       if (int r = snap_ffn(E, l, m)) return r;
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down));
         DecMMArgs a{};
-        a.w[0] = ly.down->v; a.out[0] = E->ffn; a.ld_out[0] = dim; a.tiles[0] = mq ? qtiles(ly.down) : mtiles(ly.down); a.nseg = 1;
+        a.w[0] = ly.down->v; a.out[0] = E->ffn; a.ld_out[0] = dim; a.tiles[0] = mqk(spx_engine::MQ_DOWN) ? qtiles(ly.down) : mtiles(ly.down); a.nseg = 1;
         a.G = gshape(ly.down); a.y = E->hq; a.cols = nff; a.m = m;
         a.res_in = E->xB; a.res_out = E->xA; a.rscale = c.residual_scale;
-        SPX_HIP(mq ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
+        SPX_HIP(mqk(spx_engine::MQ_DOWN) ? launch_dec_mq(a, mq_grid(a.tiles[0]), s) : launch_dec_mm(a, dec_mm_grid(a.tiles[0]), s));
       }
     }
   }
@@ -723,11 +728,11 @@ int enqueue_pass_m(spx_engine *E, int m) {
     SPX_HIP(norm(E->xA, E->out_norm, E->xn, E->xq));
     if (int r = snap(E, c.n_layers, DBG_XIN, E->xA, dim, m)) return r;
     DecMMArgs a{};
-    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.ld_out[0] = c.vocab; a.tiles[0] = mq ? qtiles(E->lm_head) : mtiles(E->lm_head); a.nseg = 1;
+    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.ld_out[0] = c.vocab; a.tiles[0] = mqk(spx_engine::MQ_LM) ? qtiles(E->lm_head) : mtiles(E->lm_head); a.nseg = 1;
     a.G = gshape(E->lm_head); a.y = E->xq; a.cols = dim; a.m = m;
-    grid = mq ? mq_grid(a.tiles[0]) : std::min(a.tiles[0], 512);
+    grid = mqk(spx_engine::MQ_LM) ? mq_grid(a.tiles[0]) : std::min(a.tiles[0], 512);
     a.best = E->best; a.nbest = grid; a.lscale = c.logit_scale;
-    SPX_HIP(mq ? launch_dec_mq(a, grid, s) : launch_dec_mm(a, grid, s));
+    SPX_HIP(mqk(spx_engine::MQ_LM) ? launch_dec_mq(a, grid, s) : launch_dec_mm(a, grid, s));
   }
   E->nbest = grid;
   {
@@ -1061,8 +1066,14 @@ int spx_engine_prepare(spx_engine *E) {
   if (std::getenv("SPX_PERSIST_TSTAMP") && E->dec_ok) E->pa.tstamp = E->dalloc<uint64_t>(4096);
   if (const char *v = std::getenv("SPX_DECODE")) E->dec_on = atoi(v) != 0;
   if (const char *v = std::getenv("SPX_MQ")) E->mq = atoi(v) != 0;
-  if (const char *v = std::getenv("SPX_MQ_DOWN_ROWS")) E->mq_down_rows = atoi(v);
-  if (const char *v = std::getenv("SPX_MQ_GATEUP")) E->mq_gateup = atoi(v) != 0;
+  if (const char *v = std::getenv("SPX_MQ_ROWS")) {
+    int k = 0;
+    for (const char *p = v; *p && k < spx_engine::MQ_KINDS; k++) {
+      E->mq_rows[k] = std::max(2, atoi(p));
+      while (*p && *p != ',') p++;
+      if (*p == ',') p++;
+    }
+  }
   E->prepared = true;
   return 0;
 }

@@ -208,15 +208,19 @@ def _margin(logits):
 
 
 @pytest.mark.parametrize("case", list(CASES))
-def test_multi_row_passes_mfma(ctx, case):
-    """Passes of 2..16 rows on the int8 matrix cores (the default: each wavefront contracts one of
-    the reference's eight lane classes and runs its fp32 chain) against the lane-exact kernels:
-    the same bits for every row (hidden state, logits, picks, routing statistics, KV cache),
+def test_multi_row_passes_mfma(ctx, case, monkeypatch):
+    """Passes of 2..16 rows on the int8 matrix cores (the reference's eight lane classes kept apart,
+    each with its fp32 chain; SPX_MQ_ROWS=2,...: every projection on the matrix cores from two
+    rows, where the default takes them from a few rows more) against the lane-exact kernels: the
+    same bits for every row (hidden state, logits, picks, routing statistics, KV cache),
     128-expert cases included; and so the same bits as one-row passes (the reference's batch
     invariance, quant_q8k.rs:413-442)."""
     cfg = CASES[case]
     w = M.synth_model(cfg, seed=35)
-    a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+    monkeypatch.setenv("SPX_MQ_ROWS", "2,2,2,2,2")
+    a = M.Engine(ctx, cfg, w)
+    monkeypatch.delenv("SPX_MQ_ROWS")
+    b = M.Engine(ctx, cfg, w)
     a.set_mfma(True)
     b.set_mfma(False)
     ids = np.random.default_rng(7).integers(0, cfg.vocab, 120)

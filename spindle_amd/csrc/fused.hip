@@ -19,6 +19,7 @@
 // replays at any position. References are to smollm_chat.rs unless a file is named.
 #include <float.h>
 
+#include <type_traits>
 #include "fused.h"
 #include "decode.h"
 #include "dev.h"
@@ -685,6 +686,92 @@ __global__ __launch_bounds__(256) void k_mv_f(const MVArgs a, const StepRec *st)
   }
   if (a.best) best_flush<MT, 4>(a, bestv, m);
   if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<4>(a.tail, 0, m);
+}
+
+// One-row float matvec over Q8_0 segments (the one-row pass of a Q8_0 model), f_walk's
+// arithmetic spread over the wavefront. A task's 32 rows (k_mv_f's tasks) go to S = 8 / RW
+// workgroups of four wavefronts, RW rows a wavefront (few tasks: more workgroups); a
+// wavefront's RW nb (row, block) items go to its lanes in turn (item i: row i / nb, block
+// i % nb; all their loads in flight), each lane forms its blocks' dots as f_walk does (four
+// chains over the block's eight float4 of x, (s0 + s1) + (s2 + s3)) and parks (d, dot) in LDS;
+// then lane 8 r + l runs row r's chain l over blocks l, l + 8, ... (acc = fma(d, dot, acc)) and
+// the 8-lane tree hsum_rows8 forms the row: the bits of k_mv_f<1>. x is staged in LDS once.
+// NI = items a lane takes (ceil(RW nb / 64)).
+constexpr int MVF1_NW = 4;
+template <int NI, int RW>
+__global__ __launch_bounds__(MVF1_NW * 64) void k_mv_f1(const MVArgs a, const StepRec *st) {
+  constexpr int S = 8 / RW;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const bool coh = a.tail.nw != nullptr;
+  const int nb = (int)a.seg[0].w.nb, cols = 32 * nb, ni = RW * nb;
+  float *lx = reinterpret_cast<float *>(smem);
+  float2 *ldd = reinterpret_cast<float2 *>(smem + (size_t)cols * 4) + (size_t)wave * ni;  // (d, dot) [row][block]
+  unsigned long long bestv[1] = {0};
+  const int total = a.seg[0].wgs + (a.nseg > 1 ? a.seg[1].wgs : 0) + (a.nseg > 2 ? a.seg[2].wgs : 0);
+  const int sub = (int)blockIdx.x % S;
+  uint4 c0[NI], c1[NI];
+  uint32_t dh[NI];
+  auto fetch = [&](int t) {  // task t's items (the first task's before x is staged)
+    int wg;
+    const Seg &sg = a.seg[seg_index(a, min(t, total - 1), wg)];
+    const int64_t rbase = sg.r0 + (int64_t)wg * 32 + (sub * MVF1_NW + wave) * RW, ebase = (int64_t)sg.expert * sg.w.rows;
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+      const int i = min(lane + 64 * k, ni - 1), r = i / nb, b = i - r * nb;
+      const int64_t g = (ebase + min(rbase + r, sg.r1 - 1)) * nb + b;
+      c0[k] = ld16(sg.w.pl.p0 + g * 32);
+      c1[k] = ld16(sg.w.pl.p0 + g * 32 + 16);
+      dh[k] = *reinterpret_cast<const uint16_t *>(sg.w.pl.p3 + g * 2);
+    }
+  };
+  fetch((int)blockIdx.x / S);
+  for (int i = threadIdx.x; i < cols / 4; i += MVF1_NW * 64) reinterpret_cast<float4 *>(lx)[i] = reinterpret_cast<const float4 *>(a.x)[i];
+  __syncthreads();
+  for (int t = (int)blockIdx.x / S; t < total; t += (int)gridDim.x / S) {
+    int wg;
+    const Seg &sg = a.seg[seg_index(a, t, wg)];
+    const int64_t rbase = sg.r0 + (int64_t)wg * 32 + (sub * MVF1_NW + wave) * RW;
+    if (t != (int)blockIdx.x / S) fetch(t);
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+      const int i = lane + 64 * k;
+      if (i < ni) {
+        const int b = i % nb;
+        const float4 *xv = reinterpret_cast<const float4 *>(lx + 32 * b);
+        const uint32_t cw[8] = {c0[k].x, c0[k].y, c0[k].z, c0[k].w, c1[k].x, c1[k].y, c1[k].z, c1[k].w};
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+          const float4 xx = xv[kk];
+          s0 = fmaf((float)(int8_t)(cw[kk]), xx.x, s0);
+          s1 = fmaf((float)(int8_t)(cw[kk] >> 8), xx.y, s1);
+          s2 = fmaf((float)(int8_t)(cw[kk] >> 16), xx.z, s2);
+          s3 = fmaf((float)(int8_t)(cw[kk] >> 24), xx.w, s3);
+        }
+        ldd[i] = make_float2(h2f(dh[k]), (s0 + s1) + (s2 + s3));
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the items are parked
+    __builtin_amdgcn_wave_barrier();
+    const int r = lane >> 3, l = lane & 7;
+    float acc = 0.0f;
+    if (r < RW)
+      for (int b = l; b < nb; b += 8) {
+        const float2 e = ldd[r * nb + b];
+        acc = fmaf(e.x, e.y, acc);
+      }
+    const float res = hsum_rows8(acc);
+    const int64_t row = rbase + r;
+    if (r < RW && l == 0 && row < sg.r1) {
+      out_store(sg.out + row, res, coh);
+      if (a.best) { const unsigned long long key = pick_key(res, a.lscale, row); bestv[0] = key > bestv[0] ? key : bestv[0]; }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();  // the items' LDS is refilled by the next task
+  }
+  if (a.best) best_flush<1, MVF1_NW>(a, bestv, 1);
+  if (coh && arrive_last(a.tail.counter, gridDim.x)) norm_rows<MVF1_NW>(a.tail, 0, 1);
 }
 
 // One wavefront's part of a Q8_0 16-row tile against up to 16 vectors on the fp32 matrix cores:
@@ -2193,6 +2280,15 @@ static int mv_total(const MVArgs &a) {
 #define SPX_LDS(kern, sm) \
   if ((sm) > 65536) (void)hipFuncSetAttribute((const void *)(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)(sm))
 
+static int cu_count_f() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+  }
+  return n;
+}
+
 hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int grid, hipStream_t s) {
   mt = bucket(mt);
   const int dt = a.seg[0].w.dtype, cols = (int)a.seg[0].w.cols, nb = cols / 256;
@@ -2205,6 +2301,31 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
       // workgroups when the grid covers the tasks, else the same grid (greedy-key slots follow it)
       hipLaunchKernelGGL(k_mv_fq<1>, dim3(!a.best && grid == mv_total(a) ? 2 * grid : grid), dim3(512), 0, s, a, st);
       return hipGetLastError();
+    }
+    if (mt == 1) {  // one row over Q8_0 segments: k_mv_f1
+      bool q8 = true;
+      for (int i = 0; i < a.nseg; i++) q8 = q8 && a.seg[i].w.dtype == T_Q8_0 && a.seg[i].w.cols == a.seg[0].w.cols;
+      // rows a wavefront: 8 with greedy keys (a slot per task) or tasks for the whole GPU, else
+      // fewer, so that the launch has about 2 x CUs workgroups
+      int rw = 8;
+      while (!a.best && rw > 1 && grid * (8 / rw) < 2 * cu_count_f()) rw >>= 1;
+      const int nb = (int)a.seg[0].w.nb, ni = (rw * nb + 63) / 64;
+      const size_t sm = (size_t)32 * nb * 4 + (size_t)MVF1_NW * rw * nb * 8;
+      if (q8 && ni <= 16 && sm <= 64 * 1024) {
+        const dim3 g((unsigned)(grid * (8 / rw))), b(MVF1_NW * 64);
+        auto go = [&](auto kern) {
+          hipLaunchKernelGGL(kern, g, b, sm, s, a, st);
+          return hipGetLastError();
+        };
+        auto by_ni = [&](auto RWc) {
+          constexpr int RW = decltype(RWc)::value;
+          return ni <= 2 ? go(k_mv_f1<2, RW>) : ni <= 4 ? go(k_mv_f1<4, RW>) : ni <= 8 ? go(k_mv_f1<8, RW>) : ni <= 12 ? go(k_mv_f1<12, RW>) : go(k_mv_f1<16, RW>);
+        };
+        if (rw == 8) return by_ni(std::integral_constant<int, 8>{});
+        if (rw == 4) return by_ni(std::integral_constant<int, 4>{});
+        if (rw == 2) return by_ni(std::integral_constant<int, 2>{});
+        return by_ni(std::integral_constant<int, 1>{});
+      }
     }
 #define SPX_MVF(MTV) hipLaunchKernelGGL(k_mv_f<MTV>, dim3(grid), dim3(256), 0, s, a, st)
     switch (mt) {

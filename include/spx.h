@@ -92,9 +92,20 @@ int spx_matvec_noalloc(spx_ctx *ctx, const spx_tensor *w, int expert, const floa
  * rounded separately from 0. gate / up: [n_expert][n_ff][dim] (one format), down:
  * [n_expert][dim][n_ff]; K-quant matrices take Q8_K activations (x, then h), the others fp32.
  * x, y: device rows at x + b*ld_x, y + b*ld_y; chosen / weights: host arrays, read before the
- * call returns. m * k <= 256, k <= 32. Each row's result does not depend on the others. */
+ * call returns (the job list goes to the device with the launches; the call does not wait for
+ * them). m * k <= 256, k <= 32. Each row's result does not depend on the others. */
 int spx_moe(spx_ctx *ctx, const spx_tensor *gate, const spx_tensor *up, const spx_tensor *down, const float *x,
             int64_t ld_x, int m, int k, const int32_t *chosen, const float *weights, float *y, int64_t ld_y);
+
+/* spx_moe with the routing in device memory (chosen / weights: device arrays [m][k], as a router
+ * on the GPU leaves them; moe_batch_fused :650-760 with the combine :1133-1140): nothing waits
+ * on the host, so the call can follow a device-side router in one stream or a captured graph.
+ * K-quant experts only (gate / up Q4_K or Q6_K in one format, down Q4_K or Q6_K; dim and n_ff
+ * multiples of 256 with 1, 2, 3, 4, 8 or 16 blocks a row, n_ff <= 1024, n_expert <= 256), on the
+ * int8 matrix cores; m <= 128, k <= 32. A row whose ids are out of range or repeated gets NaN.
+ * The same bits as spx_moe for the same routing. */
+int spx_moe_dev(spx_ctx *ctx, const spx_tensor *gate, const spx_tensor *up, const spx_tensor *down, const float *x,
+                int64_t ld_x, int m, int k, const int32_t *chosen, const float *weights, float *y, int64_t ld_y);
 
 /* ------------------------------------------------------------------ synthetic weights */
 /* Seeded synthetic tensor in GGUF block layout (n_expert slabs of rows x cols). kind 0:

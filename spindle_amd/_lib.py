@@ -30,6 +30,7 @@ SIGNATURES = {
     "spx_matvec": (C.c_int, [P, P, C.c_int, P, I64, C.c_int, P, I64]),
     "spx_matvec_noalloc": (C.c_int, [P, P, C.c_int, P, I64, C.c_int, P, I64]),
     "spx_moe": (C.c_int, [P, P, P, P, P, I64, C.c_int, C.c_int, P, P, P, I64]),
+    "spx_moe_dev": (C.c_int, [P, P, P, P, P, I64, C.c_int, C.c_int, P, P, P, I64]),
     "spx_synth_tensor": (C.c_int, [C.c_int, I64, I64, C.c_int, C.c_uint64, C.c_float, C.c_int, P]),
     "spx_engine_create": (C.c_int, [P, P, C.POINTER(P)]),
     "spx_engine_set_tensor": (C.c_int, [P, C.c_char_p, C.c_int, I64, I64, C.c_int, P]),

@@ -8,6 +8,7 @@
 #include <thread>
 
 #include "../../include/spx.h"
+#include "decode.h"
 #include "fused.h"
 #include "internal.h"
 
@@ -198,6 +199,8 @@ int spx_destroy(spx_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->moe_pin) (void)hipHostFree(ctx->moe_pin);
+  if (ctx->moe_ev) (void)hipEventDestroy(ctx->moe_ev);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return 0;
@@ -328,13 +331,51 @@ static Q8KP ws_q8kp(spx_ctx *ctx, int m, int64_t n, bool *ok) {
   return q8kp_layout(w, m, n, &bytes);
 }
 
-// Launch mode: row-parallel for integer weights, eight rows per wavefront for the float
-// formats; SPX_MV_MODE=0 forces the eight-row tiles for integer weights too (tests cover both).
+// Expert e's rows r0.. of a K-quant tensor as a view of its own (n_expert 1): each plane's
+// bytes per 256-value block are fixed (codes 128, scales 16, Q4_K header 16 / Q6_K high bits
+// 64, Q6_K d 2), so the planes start (e rows + r0) nb blocks further on.
+static TensorView kq_rows_view(const TensorView &v, int expert, int64_t r0, int64_t r1) {
+  TensorView o = v;
+  const int64_t blk = ((int64_t)expert * v.rows + r0) * v.nb;
+  o.pl.p0 = v.pl.p0 + blk * 128;
+  o.pl.p2 = v.pl.p2 + blk * 16;
+  if (v.dtype == T_Q4K) {
+    o.pl.p1 = v.pl.p1 + blk * 16;
+  } else {
+    o.pl.p1 = v.pl.p1 + blk * 64;
+    o.pl.p3 = v.pl.p3 + blk * 2;
+  }
+  o.rows = r1 - r0;
+  o.n_expert = 1;
+  return o;
+}
+
+// Launch choice. Integer weights: one row, row-parallel lanes; two or more, the int8 matrix
+// cores (kd_mq: 16-row tiles, the reference's lane classes and fp32 chains) where the row width
+// is one they take, else the eight-row lane tiles. Every choice gives the reference's bits;
+// SPX_MV_MODE forces one (0: lane tiles, 1: row-parallel, 2: matrix cores where they apply).
+// Float formats: eight rows a wavefront (the reference's M = 1 order); Q8_0 with two or more
+// rows on the fp32 matrix cores (k_mv_fq, the multi-row order of quant_multi.rs's kernel,
+// within 1e-4 of it; a row's bits do not depend on the other rows of the batch).
 static int mv_launch(spx_ctx *ctx, const spx_tensor *w, int expert, int m, const float *x, int64_t ld_x, Q8KP y, float *out,
                      int64_t ld_out, int64_t r0, int64_t r1) {
   const bool kq = w->v.dtype == T_Q4K || w->v.dtype == T_Q6K;
-  int mode = kq ? 1 : 0;
-  if (const char *v = std::getenv("SPX_MV_MODE")) mode = kq && atoi(v) == 1 ? 1 : 0;
+  int mode = kq ? (m >= 2 ? 2 : 1) : 0;
+  if (const char *v = std::getenv("SPX_MV_MODE")) mode = kq ? std::min(std::max(atoi(v), 0), 2) : 0;
+  if (mode == 2 && !dec_mq_nb_ok((int)w->v.nb)) mode = m >= 2 ? 0 : 1;
+  if (mode == 2) {
+    DecMMArgs a{};
+    a.w[0] = kq_rows_view(w->v, expert, r0, r1);
+    a.out[0] = out + r0;
+    a.ld_out[0] = ld_out;
+    a.tiles[0] = (int)((r1 - r0 + 15) / 16);
+    a.nseg = 1;
+    a.y = y;
+    a.cols = (int)w->v.cols;
+    a.m = m;
+    SPX_HIP(launch_dec_mq(a, dec_mq_grid(a.tiles[0], m), ctx->stream));
+    return 0;
+  }
   int G = 8, R = 1;
   rp_shape(w->v.nb, G, R);
   MVArgs a{};
@@ -352,6 +393,7 @@ static int mv_launch(spx_ctx *ctx, const spx_tensor *w, int expert, int m, const
   a.m = m;
   a.G = G;
   a.R = R;
+  a.fq = !kq && m >= FQ_MIN_ROWS ? 1 : 0;
   SPX_HIP(launch_mv(a, m, mode, nullptr, a.seg[0].wgs, ctx->stream));
   return 0;
 }
@@ -392,25 +434,8 @@ int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, in
     bool ok = false;
     Q8KP y = ws_q8kp(ctx, m, cols, &ok);
     if (!ok) return fail("spx_matvec: workspace allocation failed");
-    if (ctx->device >= NOALLOC_MAX_DEV) return fail("spx_matvec_noalloc: device index above 63");
-    // take this device's turn on the array: wait for the previous call's kernels (any stream),
-    // then mark this call's end. A stream under graph capture skips both: the replay order of
-    // the captured graph is the caller's to arrange.
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    SPX_HIP(hipStreamIsCapturing(ctx->stream, &cap));
-    const bool turn = cap == hipStreamCaptureStatusNone;
-    std::unique_lock<std::mutex> lk(g_noalloc_mu, std::defer_lock);
-    if (turn) {
-      lk.lock();
-      if (g_noalloc_used[ctx->device]) SPX_HIP(hipStreamWaitEvent(ctx->stream, g_noalloc_ev[ctx->device], 0));
-    }
     SPX_HIP(launch_q8kp_quantize(x, cols, ld_x, m, y, ctx->stream));
-    if (int r = mv_launch(ctx, w, expert, m, nullptr, 0, y, out, ld_out, 0, rows)) return r;
-    if (turn) {
-      SPX_HIP(hipEventRecord(g_noalloc_ev[ctx->device], ctx->stream));
-      g_noalloc_used[ctx->device] = true;
-    }
-    return 0;
+    return mv_launch(ctx, w, expert, m, nullptr, 0, y, out, ld_out, 0, rows);
   }
   if (w->v.dtype == T_F32 && cols % 16) return fail("spx_matvec: F32 needs cols % 16 == 0");
   if (w->v.dtype != T_Q8_0 && w->v.dtype != T_Q5_0 && w->v.dtype != T_Q5K && w->v.dtype != T_F32)
@@ -490,7 +515,16 @@ extern "C" int spx_moe(spx_ctx *ctx, const spx_tensor *gate, const spx_tensor *u
   const bool g_int = gate->v.dtype == T_Q4K || gate->v.dtype == T_Q6K, d_int = down->v.dtype == T_Q4K || down->v.dtype == T_Q6K;
   if (n_ff % 16 || (d_int && n_ff % 256) || (g_int && dim % 256) || dim % 4) return fail("spx_moe: unsupported widths");
   if (ld_x < dim || ld_y < dim || ld_x % 4) return fail("spx_moe: leading dimension too small (or ld_x not a multiple of 4)");
-  MoeHost hb;
+  // the job list is built in the context's pinned staging block and copied with the other
+  // launches (no wait on the stream: only a previous call's copy out of the block, if still
+  // pending, is waited for before the block is rewritten)
+  if (!ctx->moe_pin) {
+    SPX_HIP(hipHostMalloc(&ctx->moe_pin, sizeof(MoeHost), hipHostMallocDefault));
+    SPX_HIP(hipEventCreateWithFlags(&ctx->moe_ev, hipEventDisableTiming));
+  } else {
+    SPX_HIP(hipEventSynchronize(ctx->moe_ev));
+  }
+  MoeHost &hb = *static_cast<MoeHost *>(ctx->moe_pin);
   memset(&hb, 0, sizeof hb);
   std::vector<std::vector<int>> slot_of(m, std::vector<int>(ne, -1));
   for (int b = 0; b < m; b++)
@@ -538,7 +572,7 @@ extern "C" int spx_moe(spx_ctx *ctx, const spx_tensor *gate, const spx_tensor *u
   for (int i = 0, o = 0; i < 7; o += (int)sz[i], i++) p[i] = w + o;
   hipStream_t s = ctx->stream;
   SPX_HIP(hipMemcpyAsync(p[0], &hb, sizeof hb, hipMemcpyHostToDevice, s));
-  SPX_HIP(hipStreamSynchronize(s));  // chosen / weights consumed before return
+  SPX_HIP(hipEventRecord(ctx->moe_ev, s));
   const MoeHost *dh = reinterpret_cast<const MoeHost *>(p[0]);
   float *xp = reinterpret_cast<float *>(p[1]), *h = reinterpret_cast<float *>(p[3]), *out = reinterpret_cast<float *>(p[6]);
   int *cnt = reinterpret_cast<int *>(p[5]);
@@ -560,5 +594,54 @@ extern "C" int spx_moe(spx_ctx *ctx, const spx_tensor *gate, const spx_tensor *u
   da.nkeep = dh->nkeep; da.n_used = k; da.out = out;
   SPX_HIP(launch_down(da, m, 0, &dh->st, s));
   SPX_HIP(hipMemcpy2DAsync(y, sizeof(float) * ld_y, out, sizeof(float) * dim, sizeof(float) * dim, m, hipMemcpyDeviceToDevice, s));
+  return 0;
+}
+
+// The routed experts with the routing in device memory: nothing waits on the host. The routing
+// goes into the pipeline's layout (kp_moe_in), the job list is built on the device (kp_jobs: at
+// most 16 users a job), x is quantized to Q8_K, and the prefill pass's grouped kernels run on
+// the int8 matrix cores (kp_gateup_mq, kd_down_mq: the reference's per-lane integer dots and fp32
+// chains); kp_moe_combine sums each row's choices in order.
+extern "C" int spx_moe_dev(spx_ctx *ctx, const spx_tensor *gate, const spx_tensor *up, const spx_tensor *down, const float *x,
+                           int64_t ld_x, int m, int k, const int32_t *chosen, const float *weights, float *y, int64_t ld_y) {
+  if (!ctx || !gate || !up || !down || !x || !chosen || !weights || !y) return fail("spx_moe_dev: null argument");
+  if (m < 1 || m > PMAX || k < 1 || k > 32) return fail("spx_moe_dev: m must be in 1..128, k in 1..32");
+  const int64_t dim = gate->v.cols, n_ff = gate->v.rows;
+  const int ne = gate->v.n_expert;
+  if (up->v.cols != dim || up->v.rows != n_ff || up->v.n_expert != ne || down->v.cols != n_ff || down->v.rows != dim ||
+      down->v.n_expert != ne)
+    return fail("spx_moe_dev: gate/up must be [n_expert][n_ff][dim] and down [n_expert][dim][n_ff]");
+  auto kq = [](const spx_tensor *t) { return t->v.dtype == T_Q4K || t->v.dtype == T_Q6K; };
+  if (!kq(gate) || !kq(down) || gate->v.dtype != up->v.dtype) return fail("spx_moe_dev: gate / up (one format) and down must be Q4_K or Q6_K");
+  if (ne > 256 || dim % 256 || n_ff % 256 || n_ff > 1024 || !dec_mq_nb_ok((int)(dim / 256)) || !dec_mq_nb_ok((int)(n_ff / 256)))
+    return fail("spx_moe_dev: unsupported widths (dim and n_ff multiples of 256, n_ff <= 1024, blocks a row 1, 2, 3, 4, 8 or 16; n_expert <= 256)");
+  if (ld_x < dim || ld_y < dim) return fail("spx_moe_dev: leading dimension too small");
+  const int nv = m * k, max_jobs = std::min(512, std::min(ne, nv) + nv / MAX_M);
+  size_t yq_b = 0;
+  (void)q8kp_layout(nullptr, m, dim, &yq_b);
+  const size_t sz[8] = {al256(sizeof(int) * m * 32), al256(sizeof(float) * m * 32), al256(sizeof(int) * m), al256(sizeof(Job) * max_jobs),
+                        al256(sizeof(int) * 4), al256(yq_b), al256(sizeof(float) * nv * n_ff), al256(sizeof(float) * nv * dim)};
+  size_t tot = 0;
+  for (size_t v : sz) tot += v;
+  uint8_t *w = static_cast<uint8_t *>(ws_get(ctx, tot));
+  if (!w) return fail("spx_moe_dev: workspace allocation failed");
+  uint8_t *p[8];
+  for (int i = 0, o = 0; i < 8; o += (int)sz[i], i++) p[i] = w + o;
+  int *ch32 = reinterpret_cast<int *>(p[0]), *nkeep = reinterpret_cast<int *>(p[2]), *njobs = reinterpret_cast<int *>(p[4]);
+  float *w32 = reinterpret_cast<float *>(p[1]), *h = reinterpret_cast<float *>(p[6]), *yd = reinterpret_cast<float *>(p[7]);
+  Job *jobs = reinterpret_cast<Job *>(p[3]);
+  hipStream_t s = ctx->stream;
+  SPX_HIP(launch_kp_moe_in(chosen, weights, m, k, ne, ch32, w32, nkeep, s));
+  DecRouteArgs rt{};
+  rt.n_expert = ne; rt.n_used = k; rt.m = m; rt.chosen = ch32; rt.weights = w32; rt.nkeep = nkeep; rt.jobs = jobs; rt.njobs = njobs;
+  SPX_HIP(launch_kp_jobs(rt, s));
+  const Q8KP yq = q8kp_layout(p[5], m, dim, &yq_b);
+  SPX_HIP(launch_q8kp_quantize(x, dim, ld_x, m, yq, s));
+  DecGateUpMArgs ga{};
+  ga.gate = gate->v; ga.up = up->v; ga.y = yq; ga.h = h; ga.n_ff = (int)n_ff; ga.m = m;
+  SPX_HIP(launch_kp_gateup_mq(ga, jobs, njobs, max_jobs, s));
+  DecDownMArgs da{down->v, h, jobs, njobs, yd, max_jobs};
+  SPX_HIP(launch_dec_down_mq(da, s));
+  SPX_HIP(launch_kp_moe_combine(yd, w32, nkeep, m, k, (int)dim, y, ld_y, s));
   return 0;
 }

@@ -217,6 +217,12 @@ hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s);
 // memory; gate/up over such a list (jobs null: dense, rows in sixteens), max_jobs bounds it
 hipError_t launch_kp_route(const DecRouteArgs &a, hipStream_t s);
 hipError_t launch_kp_gateup_mq(const DecGateUpMArgs &a, const Job *jobs, const int *njobs, int max_jobs, hipStream_t s);
+// Routing given in device memory (spx_moe_dev): chosen / weights [m][k] into the [m][32] layout
+// with nkeep (rows with bad ids: nkeep 0); the job list from it (kp_jobs); the weighted combine
+// of the expert rows yd [m k][dim] into y (NaN rows for nkeep 0).
+hipError_t launch_kp_moe_in(const int *chosen, const float *weights, int m, int k, int ne, int *ch32, float *w32, int *nkeep, hipStream_t s);
+hipError_t launch_kp_jobs(const DecRouteArgs &a, hipStream_t s);
+hipError_t launch_kp_moe_combine(const float *yd, const float *w32, const int *nkeep, int m, int k, int dim, float *y, int64_t ld_y, hipStream_t s);
 hipError_t launch_dec_merge(const DecMergeArgs &a, const StepRec *st, hipStream_t s);
 hipError_t launch_dec_router(const DecRouterArgs &a, hipStream_t s);
 hipError_t launch_dec_gateup(const DecGateUpArgs &a, hipStream_t s);

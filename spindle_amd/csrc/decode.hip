@@ -2352,6 +2352,36 @@ __global__ __launch_bounds__(256) void kp_jobs(const DecRouteArgs a) {
   }
 }
 
+// spx_moe_dev's routing in device memory: row b's k choices (chosen / weights [m][k]) into the
+// pipeline's layout (ch32 / w32 [m][32], nkeep [m] = k), a row with an expert id out of range
+// or chosen twice kept with no choices (nkeep 0: its output is NaN); one thread a row.
+__global__ __launch_bounds__(256) void kp_moe_in(const int *chosen, const float *weights, int m, int k, int ne, int *ch32, float *w32,
+                                                 int *nkeep) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= m) return;
+  bool ok = true;
+  for (int j = 0; j < k; j++) {
+    const int e = gld<int>(chosen + (int64_t)b * k + j);
+    ok = ok && e >= 0 && e < ne;
+    for (int i = 0; i < j; i++) ok = ok && gld<int>(chosen + (int64_t)b * k + i) != e;
+    gst<int>(ch32 + b * 32 + j, ok ? e : 0);
+    gst<float>(w32 + b * 32 + j, gld<float>(weights + (int64_t)b * k + j));
+  }
+  gst<int>(nkeep + b, ok ? k : 0);
+}
+// y[b] = sum over j < nkeep[b], in j order, of w32[b][j] * yd[b k + j] (each product and sum
+// rounded, from 0: the combine of moe_forward_batch :1133-1140); NaN for a row kept with no
+// choices. A thread per output value.
+__global__ __launch_bounds__(256) void kp_moe_combine(const float *yd, const float *w32, const int *nkeep, int k, int dim, float *y,
+                                                      int64_t ld_y) {
+  const int b = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= dim) return;
+  const int nk = gld<int>(nkeep + b);
+  float acc = 0.0f;
+  for (int j = 0; j < nk; j++) acc = acc + gld<float>(w32 + b * 32 + j) * gld<float>(yd + ((int64_t)b * k + j) * dim + i);
+  gst<float>(y + (int64_t)b * ld_y + i, nk > 0 ? acc : __int_as_float(0x7fc00000));
+}
+
 // Gate / up + SwiGLU of a prefill pass on the matrix cores over a job list of at most sixteen
 // users a job (MoE: kp_route's, in global memory; dense, jobs null: rows 16j .. 16j + 15 as
 // job j): items (job, 16 h rows) as kd_gateup_mq takes them, workgroup b the items
@@ -2674,6 +2704,26 @@ hipError_t launch_kp_route(const DecRouteArgs &a, hipStream_t s) {
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(kp_route_rows, dim3((a.m + 3) / 4), dim3(256), 0, s, a);
   hipLaunchKernelGGL(kp_jobs, dim3(1), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_kp_moe_in(const int *chosen, const float *weights, int m, int k, int ne, int *ch32, float *w32, int *nkeep, hipStream_t s) {
+  if (m < 1 || m > PMAX || k < 1 || k > 32 || ne < 1 || ne > 256) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kp_moe_in, dim3((m + 255) / 256), dim3(256), 0, s, chosen, weights, m, k, ne, ch32, w32, nkeep);
+  return hipGetLastError();
+}
+
+hipError_t launch_kp_jobs(const DecRouteArgs &a, hipStream_t s) {
+  if (a.m < 1 || a.m > PMAX || a.n_expert < 1 || a.n_expert > 256 || a.n_used < 1 || a.n_used > 32 || !a.jobs || !a.njobs || !a.chosen ||
+      !a.nkeep)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kp_jobs, dim3(1), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_kp_moe_combine(const float *yd, const float *w32, const int *nkeep, int m, int k, int dim, float *y, int64_t ld_y, hipStream_t s) {
+  if (m < 1 || m > PMAX || k < 1 || k > 32 || dim < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kp_moe_combine, dim3((dim + 255) / 256, m), dim3(256), 0, s, yd, w32, nkeep, k, dim, y, ld_y);
   return hipGetLastError();
 }
 

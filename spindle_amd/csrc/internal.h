@@ -20,6 +20,8 @@ struct spx_ctx {
   void *ws = nullptr;      // grow-only workspace for internal Q8_K staging
   size_t ws_bytes = 0;
   uint8_t *scratch = nullptr;  // this device's copy of the fixed scratch array (spx_matvec_noalloc)
+  void *moe_pin = nullptr;     // spx_moe's pinned staging block for its job list
+  hipEvent_t moe_ev = nullptr; // recorded after the block's copy to the device
 };
 
 namespace spx {

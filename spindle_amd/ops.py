@@ -165,6 +165,21 @@ def moe(ctx, gate, up, down, x, chosen, weights):
     return y
 
 
+def moe_dev(ctx, gate, up, down, x, chosen, weights):
+    """moe with the routing in device memory (spx_moe_dev): chosen [m, k] int32 and weights
+    [m, k] float32 cuda tensors, as a router on the GPU leaves them; K-quant experts. A row whose
+    ids are out of range or repeated comes back NaN. Returns y [m, dim]."""
+    assert x.is_cuda and x.dtype == torch.float32 and x.dim() == 2
+    assert chosen.is_cuda and chosen.dtype == torch.int32 and weights.is_cuda and weights.dtype == torch.float32
+    chosen, weights = chosen.contiguous(), weights.contiguous()
+    m, k = chosen.shape
+    y = torch.empty((m, down.rows), dtype=torch.float32, device=x.device)
+    torch.cuda.synchronize()  # inputs written on torch's stream, the library runs on the context's
+    check(lib.spx_moe_dev(ctx.h, gate.h, up.h, down.h, _p(x), x.stride(0), m, k, _p(chosen), _p(weights), _p(y), y.stride(0)))
+    ctx.sync()
+    return y
+
+
 class SamplerParams(C.Structure):
     """spx_sampler_params (SamplerConfig, smollm_chat.rs:1523-1555)."""
     _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("min_p", C.c_float),

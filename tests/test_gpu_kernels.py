@@ -26,14 +26,15 @@ def ctx():
     c.close()
 
 
-@pytest.fixture(params=["auto", "tiles"])
+@pytest.fixture(params=["auto", "tiles", "rows"])
 def mv_mode(request, monkeypatch):
-    """Integer matvec launch shape: the default (row-parallel at m <= 2) or forced
-    eight-rows-per-wavefront tiles; both must give the reference's bits."""
-    if request.param == "tiles":
-        monkeypatch.setenv("SPX_MV_MODE", "0")
-    else:
+    """Integer matvec launch shape: the default (row-parallel lanes at one row, the int8 matrix
+    cores from two), or forced eight-row lane tiles, or forced row-parallel lanes; every shape
+    must give the reference's bits."""
+    if request.param == "auto":
         monkeypatch.delenv("SPX_MV_MODE", raising=False)
+    else:
+        monkeypatch.setenv("SPX_MV_MODE", "0" if request.param == "tiles" else "1")
     return request.param
 
 
@@ -180,19 +181,47 @@ def test_int_kernel_batch_bitwise(ctx, dtype, mv_mode):
 @pytest.mark.parametrize("dtype,n,rows,ne", [(R.Q4K, 2048, 768, 8), (R.Q6K, 768, 2048, 8), (R.Q4K, 4096, 2048, 1),
                                               (R.Q6K, 2048, 151936, 1)])
 def test_int_matvec_real_shapes(ctx, dtype, n, rows, ne, mv_mode):
-    """Qwen3-30B-A3B shapes: expert gate/up, expert down, attn_output, LM head."""
+    """Qwen3-30B-A3B shapes: expert gate/up, expert down, attn_output, LM head, at 1, 2 and 9
+    vectors (the default launch: row-parallel lanes, then the int8 matrix cores)."""
     from spindle_amd import ops
     rng = np.random.default_rng(rows)
     raw = _rand_kquant(dtype, n, rows, rng, ne)
     w = ops.Tensor(ctx, dtype, n, rows, raw, ne)
     ffi.set_threads(8)
     for e in sorted({0, ne - 1}):
-        x = rng.standard_normal((2, n)).astype(np.float32)
-        got = ops.matvec(ctx, w, _cuda(x), expert=e).cpu().numpy()
         m = ffi.mat(dtype, raw[e * rows * R.row_bytes(dtype, n):], rows, n)
-        for v in range(2):
-            want = ffi.matvec(m, x[v])
-            assert np.array_equal(got[v].view(np.uint32), want.view(np.uint32)), (e, v)
+        for nv in (1, 2, 9):
+            x = rng.standard_normal((nv, n)).astype(np.float32)
+            got = ops.matvec(ctx, w, _cuda(x), expert=e).cpu().numpy()
+            for v in range(nv):
+                want = ffi.matvec(m, x[v])
+                assert np.array_equal(got[v].view(np.uint32), want.view(np.uint32)), (e, nv, v)
+
+
+@pytest.mark.parametrize("n,rows", [(1024, 2048), (2048, 1024), (1024, 3072), (3072, 1024)])
+def test_q8_0_multi_config2_shapes(ctx, n, rows):
+    """Qwen3-0.6B's Q8_0 projections (q, attn_output, gate/up, down) at 2, 9 and 16 vectors:
+    the fp32 matrix-core kernel (k_mv_fq) against the reference's multi-row kernel
+    (quant_multi.rs, the oracle's or_matmul_rows_multi) within 1e-4 of the largest output, and
+    within the reference's per-row tolerance 1e-4 * sum|w x| + 1e-6 of the f64 dot; a vector's
+    bits the same in any batch of two or more."""
+    from spindle_amd import ops
+    rng = np.random.default_rng(n + rows)
+    raw = rng.integers(0, 256, R.row_bytes(R.Q8_0, n) * rows, dtype=np.uint8)
+    raw.reshape(-1, 34)[:, 0:2] = np.float16(rng.uniform(0.001, 0.05, raw.size // 34)).view(np.uint8).reshape(-1, 2)
+    w = ops.Tensor(ctx, R.Q8_0, n, rows, raw)
+    wd = ffi.dequant(R.Q8_0, raw, rows, n).astype(np.float64)
+    ffi.set_threads(8)
+    x = rng.standard_normal((16, n)).astype(np.float32)
+    full = ops.matvec(ctx, w, _cuda(x)).cpu().numpy()
+    want = ffi.matmul_rows_multi(raw, R.Q8_0, n, list(x), rows)
+    for v in range(16):
+        assert _norm_err(full[v], want[v]) <= 1e-4, v
+        scale = np.abs(wd * x[v].astype(np.float64)).sum(1)
+        assert np.all(np.abs(full[v] - wd @ x[v].astype(np.float64)) <= 1e-4 * scale + 1e-6), v
+    for nv, v0 in ((2, 5), (9, 7)):
+        part = ops.matvec(ctx, w, _cuda(x[v0:v0 + nv])).cpu().numpy()
+        assert np.array_equal(part.view(np.uint32), full[v0:v0 + nv].view(np.uint32)), nv
 
 
 @pytest.mark.parametrize("dtype", [R.Q8_0, R.Q5_0, R.Q5K, R.F32])
@@ -215,15 +244,21 @@ def test_float_matvec(ctx, dtype):
         got = ops.matvec(ctx, w, _cuda(x)).cpu().numpy()
         wd = ffi.dequant(dtype, raw, rows, n).astype(np.float64)
         m1 = ffi.mat(dtype, raw, rows, n)
+        multi = ffi.matmul_rows_multi(raw, dtype, n, list(x), rows)  # the reference's multi-row kernel
         for v in range(9):
             want = ffi.matvec(m1, x[v])              # the reference's M=1 kernel
             assert _norm_err(got[v], want) <= 1e-4
+            assert _norm_err(got[v], multi[v]) <= 1e-4
             if dtype == R.Q5K:  # the GPU walker follows the reference's lanes: the same bits
                 assert np.array_equal(got[v].view(np.uint32), want.view(np.uint32)), v
             scale = np.abs(wd * x[v].astype(np.float64)).sum(1)
             assert np.all(np.abs(got[v] - wd @ x[v].astype(np.float64)) <= 1e-4 * scale + 1e-6)
         one = ops.matvec(ctx, w, _cuda(x[4:5])).cpu().numpy()
-        assert np.array_equal(one.view(np.uint32), got[4:5].view(np.uint32))
+        assert _norm_err(one[0], got[4]) <= 1e-4
+        if dtype != R.Q8_0:  # the same walk at any batch size (Q8_0 takes the matrix cores from two rows)
+            assert np.array_equal(one.view(np.uint32), got[4:5].view(np.uint32))
+        pair = ops.matvec(ctx, w, _cuda(x[4:6])).cpu().numpy()
+        assert np.array_equal(pair.view(np.uint32), got[4:6].view(np.uint32))
 
 
 @pytest.mark.parametrize("dtype,n", [(R.Q4K, 2048), (R.Q6K, 768), (R.Q8_0, 1024), (R.Q5_0, 576), (R.Q5K, 512), (R.F32, 64)])

@@ -78,3 +78,46 @@ def test_moe_refuses_bad_routing(ctx):
         ops.moe(ctx, ex["gate"][1], ex["up"][1], ex["down"][1], x, [[3, 3]], [[0.5, 0.5]])
     with pytest.raises(SpxError, match="out of range"):
         ops.moe(ctx, ex["gate"][1], ex["up"][1], ex["down"][1], x, [[3, 16]], [[0.5, 0.5]])
+
+
+@pytest.mark.parametrize("fmt", [(R.Q4K, R.Q6K), (R.Q6K, R.Q4K)], ids=["q4k-q6k", "q6k-q4k"])
+@pytest.mark.parametrize("m,k", [(1, 8), (9, 8), (16, 8), (64, 8)])
+def test_moe_dev_matches_oracle(ctx, fmt, m, k):
+    """spx_moe_dev (routing in device memory, the prefill pass's matrix-core kernels): each row
+    within the integer path's 1e-5 bar of the oracle, and the same bits as spx_moe (host
+    routing, the lane-exact kernels) wherever spx_moe takes the batch (m * k <= 256)."""
+    from spindle_amd import ops
+    dim, nff, ne = 512, 256, 16
+    ex = _experts(ctx, fmt[0], fmt[1], dim, nff, ne, seed=m * 7 + k)
+    rng = np.random.default_rng(100 + m)
+    x = rng.standard_normal((m, dim)).astype(np.float32)
+    chosen = np.stack([rng.permutation(ne)[:k] for _ in range(m)]).astype(np.int32)
+    weights = rng.dirichlet(np.ones(k), m).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    y = ops.moe_dev(ctx, ex["gate"][1], ex["up"][1], ex["down"][1], xd, torch.from_numpy(chosen).cuda(),
+                    torch.from_numpy(weights).cuda()).cpu().numpy()
+    rows = range(m) if m <= 16 else [0, 1, m // 2, m - 1]
+    for b in rows:
+        want = _oracle_row(ex, x[b], chosen[b], weights[b])
+        assert np.abs(y[b] - want).max() <= 1e-5 * np.abs(want).max(), b
+    if m * k <= 256:
+        host = ops.moe(ctx, ex["gate"][1], ex["up"][1], ex["down"][1], xd, chosen, weights).cpu().numpy()
+        assert np.array_equal(host.view(np.uint32), y.view(np.uint32))
+
+
+def test_moe_dev_bad_rows_nan(ctx):
+    """A row whose ids repeat or leave the expert range comes back NaN; the other rows keep
+    their bits (spx_moe refuses such a call on the host; on the device no error can be raised
+    without a wait)."""
+    from spindle_amd import ops
+    ex = _experts(ctx, R.Q4K, R.Q6K, 512, 256, 16, seed=3)
+    rng = np.random.default_rng(5)
+    x = torch.from_numpy(rng.standard_normal((4, 512)).astype(np.float32)).cuda()
+    chosen = np.array([[1, 2], [3, 3], [4, 16], [5, 6]], np.int32)
+    weights = np.full((4, 2), 0.5, np.float32)
+    y = ops.moe_dev(ctx, ex["gate"][1], ex["up"][1], ex["down"][1], x, torch.from_numpy(chosen).cuda(),
+                    torch.from_numpy(weights).cuda()).cpu().numpy()
+    assert np.isnan(y[1]).all() and np.isnan(y[2]).all()
+    good = ops.moe_dev(ctx, ex["gate"][1], ex["up"][1], ex["down"][1], x[[0, 3]], torch.from_numpy(chosen[[0, 3]]).cuda(),
+                       torch.from_numpy(weights[[0, 3]]).cuda()).cpu().numpy()
+    assert np.array_equal(good.view(np.uint32), y[[0, 3]].view(np.uint32))

@@ -171,12 +171,12 @@ PREFILL_CHUNK = 128  # feed's prompt chunks (smollm_chat.rs:3090)
 
 
 def prefill(eng, prompt, verbose=False):
+    """feed (spx_engine_feed): 128-row passes, logits for the last prompt row only."""
     t0 = time.perf_counter()
-    for s in range(0, len(prompt), PREFILL_CHUNK):
-        am, _, _ = eng.forward(prompt[s:s + PREFILL_CHUNK], s)
-        if verbose and s % 1024 == 0:
-            log(f"prefill {s + len(prompt[s:s + PREFILL_CHUNK])}/{len(prompt)}")
-    return int(am[-1]), time.perf_counter() - t0
+    am, _, _ = eng.feed(prompt, 0)
+    if verbose:
+        log(f"prefill {len(prompt)} rows")
+    return int(am), time.perf_counter() - t0
 
 
 def timed_decode(ctx, eng, tok, pos, warmup, steps):

@@ -178,6 +178,13 @@ int spx_engine_persist_active(spx_engine *e, int *active);
  * outputs: hidden [m][dim] (after output_norm), logits [m][vocab], argmax [m]. Synchronous. */
 int spx_engine_forward(spx_engine *e, const int32_t *ids, int m, int start_pos, float *hidden,
                        float *logits, int32_t *argmax);
+/* feed (smollm_chat.rs:3044-3104): the prompt ids[0..n) at positions start_pos.. in passes of
+ * up to 128 rows (spx_engine_forward's passes, the same K/V bits), keeping only what feed keeps:
+ * the last row's hidden state (after output_norm) and, as the reference computes them from it
+ * afterwards, its logits and greedy pick. No LM head runs for the other rows. Optional host
+ * outputs: hidden_last [dim], logits_last [vocab], argmax_last [1]. Synchronous. */
+int spx_engine_feed(spx_engine *e, const int32_t *ids, int n, int start_pos, float *hidden_last,
+                    float *logits_last, int32_t *argmax_last);
 /* Greedy decoding of n tokens, one pass each (step_token :3106-3132 + the greedy pick):
  * feeds `token` at start_pos, then each pass's argmax at the next position; out[i] is the
  * token chosen by pass i. */

@@ -42,6 +42,7 @@ SIGNATURES = {
     "spx_engine_set_persist": (C.c_int, [P, C.c_int]),
     "spx_engine_persist_active": (C.c_int, [P, C.POINTER(C.c_int)]),
     "spx_engine_forward": (C.c_int, [P, P, C.c_int, C.c_int, P, P, P]),
+    "spx_engine_feed": (C.c_int, [P, P, C.c_int, C.c_int, P, P, P]),
     "spx_engine_last_experts": (C.c_int, [P, P]),
     "spx_engine_debug_read": (C.c_int, [P, C.c_char_p, P, I64]),
     "spx_engine_debug_layers": (C.c_int, [P, C.c_int]),

@@ -123,7 +123,10 @@ struct spx_engine {
   bool dbg_on = false;
   float *dbg = nullptr;
   int64_t dbg_off[13] = {};
-  hipGraphExec_t graph[PMAX + 1] = {};
+  // captured passes by LM-head selection and rows: [0] every row's logits and pick, [1] the
+  // last row's only, [2] none (spx_engine_feed's chunks)
+  hipGraphExec_t graph[3][PMAX + 1] = {};
+  int lm_sel = 0;       // LM-head selection of the pass being enqueued (as graph's first index)
   int n_used = 0;
   // kernel-class timing (eager passes only): event pairs recorded around each launch
   struct ProfRec { int cls, layer; double bytes; bool per_expert; hipEvent_t a, b; };
@@ -178,6 +181,14 @@ struct ProfScope {
 };
 
 double wbytes(const spx_tensor *t) { return (double)row_bytes(t->v.dtype, t->v.cols) * (double)t->v.rows; }
+
+// Row r of an m-row Q8_K image of cols values a row.
+Q8KP q8kp_row(Q8KP y, int r, int64_t cols) {
+  y.q += (int64_t)r * (cols >> 2);
+  y.d += (int64_t)r * (cols >> 8);
+  y.bs += (int64_t)r * (cols >> 8) * 8;
+  return y;
+}
 
 Seg seg_of(const spx_tensor *t, float *out, int64_t ld_out, int m, int mode, int R) {
   Seg s{};
@@ -429,27 +440,41 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
       }
     }
   }
+  if (E->lm_sel == 2) return 0;  // feed's earlier chunks: no logits
+  // feed's last chunk: the last row's logits and pick only (row 0 of logits / amax; its
+  // normalised row stays at row m - 1 of xn)
+  const bool last = E->lm_sel == 1 && m > 1;
+  const int lm = last ? 1 : m;
   {
     ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
     const int mode = E->lm_mode >= 0 && is_kq(E->lm_head) ? E->lm_mode : 0;
     int G = 8, R = 1;
     rp_shape(E->lm_head->v.nb, G, R);
     MVArgs a{};
-    a.seg[0] = seg_of(E->lm_head, E->logits, c.vocab, m, mode, R);
+    a.seg[0] = seg_of(E->lm_head, E->logits, c.vocab, lm, mode, R);
     a.nseg = 1;
-    a.x = E->xn;
+    a.x = E->xn + (int64_t)(m - lm) * dim;
     a.ld_x = dim;
-    a.y = E->xq;
+    a.y = q8kp_row(E->xq, m - lm, dim);
     a.G = G;
     a.R = R;
     a.best = E->best;
     a.lscale = c.logit_scale;
-    if (int r = mv_run(E, a, m, mode, mode == 0 ? E->lm_grid : 0)) return r;
-    E->nbest = a.nbest;
+    if (last) {  // one vector: no step record (its m is the pass's)
+      int grid = a.seg[0].wgs;
+      if (mode == 0 && E->lm_grid > 0 && grid > E->lm_grid) grid = E->lm_grid;
+      a.m = 1;
+      a.nbest = grid;
+      SPX_HIP(launch_mv(a, 1, mode, nullptr, grid, s));
+      E->nbest = grid;
+    } else {
+      if (int r = mv_run(E, a, m, mode, mode == 0 ? E->lm_grid : 0)) return r;
+      E->nbest = a.nbest;
+    }
   }
   {
     ProfScope ps(E, PC_ARGMAX, 0);
-    SPX_HIP(launch_argmax_final(E->best, E->nbest, E->amax, E->st_dev, advance ? E->hist : nullptr, m, s));
+    SPX_HIP(launch_argmax_final(E->best, E->nbest, E->amax, last ? nullptr : E->st_dev, advance ? E->hist : nullptr, lm, s));
   }
   return 0;
 }
@@ -722,7 +747,24 @@ int enqueue_pass_m(spx_engine *E, int m) {
       }
     }
   }
+  if (E->lm_sel == 2) return 0;  // feed's earlier chunks: no logits
   int grid = 1;
+  if (E->lm_sel == 1) {  // feed's last chunk: the last row's output_norm, logits and pick (row 0 of xn / logits / amax)
+    ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
+    SPX_HIP(norm(E->xA, E->out_norm, E->xn, E->xq));  // (also the last layer's expert combine into xA)
+    const int G = gshape(E->lm_head), R = 8 / G;
+    DecMVArgs a{};
+    a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.tiles[0] = (int)((E->lm_head->v.rows + DEC_MV_NW * R - 1) / (DEC_MV_NW * R));
+    a.nseg = 1; a.G = G;
+    a.in = DecIn{E->xA + (int64_t)(m - 1) * dim, E->out_norm, c.rms_eps, dim};
+    a.best = E->best; a.lscale = c.logit_scale; a.xn_out = E->xn;
+    grid = std::min(a.tiles[0], E->lm_dec_grid);
+    SPX_HIP(launch_dec_mv(a, grid, s));
+    E->nbest = grid;
+    ProfScope pa(E, PC_ARGMAX, 0);
+    SPX_HIP(launch_argmax_final(E->best, grid, E->amax, nullptr, nullptr, 1, s));
+    return 0;
+  }
   {
     ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
     SPX_HIP(norm(E->xA, E->out_norm, E->xn, E->xq));
@@ -798,6 +840,12 @@ int persist_check(spx_engine *E) {
 
 // Graph slot m (1..16): a pass of m rows; slot 0: a one-row decode pass that advances the
 // step record itself (back-to-back greedy decoding without host round trips).
+void drop_graphs(spx_engine *E) {
+  for (auto &row : E->graph)
+    for (auto &g : row)
+      if (g) { (void)hipGraphExecDestroy(g); g = nullptr; }
+}
+
 int run_forward(spx_engine *E, int m, bool advance = false) {
   hipStream_t s = E->ctx->stream;
   const bool dec = E->dec_ok && E->dec_on;
@@ -805,18 +853,19 @@ int run_forward(spx_engine *E, int m, bool advance = false) {
   auto enqueue = [&]() { return !dec ? enqueue_forward(E, m, advance) : m == 1 ? enqueue_decode(E, advance) : enqueue_pass_m(E, m); };
   if (!E->use_graphs || E->profiling || E->dbg_on) return enqueue();
   const int slot = advance ? 0 : m;
-  if (!E->graph[slot]) {
+  hipGraphExec_t &gx = E->graph[advance ? 0 : E->lm_sel][slot];
+  if (!gx) {
     SPX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     int r = enqueue();
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(s, &g);
     if (r) { if (g) (void)hipGraphDestroy(g); return r; }
     if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
-    e = hipGraphInstantiate(&E->graph[slot], g, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(&gx, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
-    if (e != hipSuccess) { E->graph[slot] = nullptr; return hip_fail(e, "hipGraphInstantiate"); }
+    if (e != hipSuccess) { gx = nullptr; return hip_fail(e, "hipGraphInstantiate"); }
   }
-  SPX_HIP(hipGraphLaunch(E->graph[slot], s));
+  SPX_HIP(hipGraphLaunch(gx, s));
   return 0;
 }
 
@@ -1088,8 +1137,7 @@ int spx_engine_set_decode(spx_engine *E, int on) {
   if (!E) return fail("null engine");
   if (E->dec_on != (on != 0)) {  // the captured graphs hold the other pipeline: capture again
     SPX_HIP(hipStreamSynchronize(E->ctx->stream));
-    for (int slot = 0; slot <= PMAX; slot++)
-      if (E->graph[slot]) { (void)hipGraphExecDestroy(E->graph[slot]); E->graph[slot] = nullptr; }
+    drop_graphs(E);
   }
   E->dec_on = on != 0;
   return 0;
@@ -1099,8 +1147,7 @@ int spx_engine_set_mfma(spx_engine *E, int on) {
   if (!E) return fail("null engine");
   if (E->mq != (on != 0)) {  // the captured multi-row graphs hold the other kernels: capture again
     SPX_HIP(hipStreamSynchronize(E->ctx->stream));
-    for (int slot = 0; slot <= PMAX; slot++)
-      if (E->graph[slot]) { (void)hipGraphExecDestroy(E->graph[slot]); E->graph[slot] = nullptr; }
+    drop_graphs(E);
   }
   E->mq = on != 0;
   return 0;
@@ -1125,8 +1172,14 @@ int spx_engine_persist_active(spx_engine *E, int *active) {
   return 0;
 }
 
-int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, float *hidden, float *logits, int32_t *argmax) {
+}  // extern "C"
+
+namespace {
+// One pass of m rows (spx_engine_forward) with LM-head selection sel (0: every row, 1: the last
+// row's logits / pick / normalised row into row 0 of logits / argmax / hidden, 2: none).
+int forward_sel(spx_engine *E, const int32_t *ids, int m, int start_pos, float *hidden, float *logits, int32_t *argmax, int sel) {
   if (!E || !ids) return fail("spx_engine_forward: null argument");
+  if (m == 1) sel = sel == 2 ? 2 : 0;
   if (!E->prepared) return fail("spx_engine_forward: call spx_engine_prepare first");
   if (m < 1 || m > PMAX) return fail("spx_engine_forward: m must be in 1.." + std::to_string(PMAX));
   if (start_pos < 0 || start_pos + m > E->c.max_seq) return fail("spx_engine_forward: positions beyond max_seq (the KV window is full)");
@@ -1137,8 +1190,15 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
     // other (a row's results do not depend on the rows that share its pass)
     for (int r0 = 0; r0 < m; r0 += MAX_M) {
       const int n = std::min(MAX_M, m - r0);
-      if (int r = spx_engine_forward(E, ids + r0, n, start_pos + r0, hidden ? hidden + (int64_t)r0 * E->c.dim : nullptr,
-                                     logits ? logits + (int64_t)r0 * E->c.vocab : nullptr, argmax ? argmax + r0 : nullptr))
+      if (sel) {  // feed: only the last pass's last row
+        const bool fin = r0 + n == m;
+        if (int r = forward_sel(E, ids + r0, n, start_pos + r0, fin ? hidden : nullptr, fin ? logits : nullptr, fin ? argmax : nullptr,
+                                fin ? sel : 2))
+          return r;
+        continue;
+      }
+      if (int r = forward_sel(E, ids + r0, n, start_pos + r0, hidden ? hidden + (int64_t)r0 * E->c.dim : nullptr,
+                              logits ? logits + (int64_t)r0 * E->c.vocab : nullptr, argmax ? argmax + r0 : nullptr, 0))
         return r;
     }
     return 0;
@@ -1152,10 +1212,17 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
   for (int i = 0; i < m; i++) E->st_host->ids[i] = ids[i];
   E->last_m = m;
   SPX_HIP(hipMemcpyAsync(E->st_dev, E->st_host, sizeof(StepRec), hipMemcpyHostToDevice, s));
-  if (int r = run_forward(E, m)) return r;
-  if (hidden) SPX_HIP(hipMemcpyAsync(hidden, E->xn, sizeof(float) * m * E->c.dim, hipMemcpyDeviceToHost, s));
-  if (logits) SPX_HIP(hipMemcpyAsync(logits, E->logits, sizeof(float) * m * E->c.vocab, hipMemcpyDeviceToHost, s));
-  if (argmax) SPX_HIP(hipMemcpyAsync(argmax, E->amax, sizeof(int) * m, hipMemcpyDeviceToHost, s));
+  E->lm_sel = sel;
+  const int rf = run_forward(E, m);
+  E->lm_sel = 0;
+  if (rf) return rf;
+  const int nr = sel ? 1 : m;  // rows copied out (sel 1: the last row's, at row 0; the decode pipeline's norm writes row 0)
+  const int64_t hrow = sel && !(E->dec_ok && E->dec_on) ? m - 1 : 0;
+  if (sel != 2) {
+    if (hidden) SPX_HIP(hipMemcpyAsync(hidden, E->xn + hrow * E->c.dim, sizeof(float) * nr * E->c.dim, hipMemcpyDeviceToHost, s));
+    if (logits) SPX_HIP(hipMemcpyAsync(logits, E->logits, sizeof(float) * nr * E->c.vocab, hipMemcpyDeviceToHost, s));
+    if (argmax) SPX_HIP(hipMemcpyAsync(argmax, E->amax, sizeof(int) * nr, hipMemcpyDeviceToHost, s));
+  }
   const bool pers = persist_used(E, m);
   if (pers) SPX_HIP(hipMemcpyAsync(E->perr_host, E->pa.err, sizeof(int), hipMemcpyDeviceToHost, s));
   SPX_HIP(hipStreamSynchronize(s));
@@ -1178,6 +1245,27 @@ int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, 
     }
     E->prof.clear();
     E->ev_next = 0;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int spx_engine_forward(spx_engine *E, const int32_t *ids, int m, int start_pos, float *hidden, float *logits, int32_t *argmax) {
+  return forward_sel(E, ids, m, start_pos, hidden, logits, argmax, 0);
+}
+
+int spx_engine_feed(spx_engine *E, const int32_t *ids, int n, int start_pos, float *hidden_last, float *logits_last, int32_t *argmax_last) {
+  if (!E || !ids) return fail("spx_engine_feed: null argument");
+  if (n < 1) return fail("spx_engine_feed: n must be at least 1");
+  for (int s0 = 0; s0 < n; s0 += PMAX) {
+    const int cnt = std::min(PMAX, n - s0);
+    const bool fin = s0 + cnt == n;
+    if (int r = forward_sel(E, ids + s0, cnt, start_pos + s0, fin ? hidden_last : nullptr, fin ? logits_last : nullptr,
+                            fin ? argmax_last : nullptr, fin ? 1 : 2))
+      return r;
   }
   return 0;
 }
@@ -1478,13 +1566,12 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
   int pos = p->n_cached;
   int32_t am[PMAX];
   int64_t t0 = now_us();
-  for (int s = p->n_cached; s < n_prompt; s += chunk) {  // feed (:3041-3104)
+  for (int s = p->n_cached; s < n_prompt; s += chunk) {  // feed (:3041-3104): the last row's logits only
     const int cnt = std::min(chunk, n_prompt - s);
     if (int r = spx_engine_ensure_kv_room(E, p->kv_keep, pos, cnt, &pos)) return r;  // feed (:3089-3090)
-    if (int r = spx_engine_forward(E, prompt + s, cnt, pos, nullptr, nullptr, am)) return r;
+    if (int r = forward_sel(E, prompt + s, cnt, pos, nullptr, nullptr, am, s + cnt == n_prompt ? 1 : 2)) return r;
     pos += cnt;
   }
-  const int last_rows = n_prompt - p->n_cached - ((n_prompt - p->n_cached - 1) / chunk) * chunk;  // rows in the last chunk
   // a draft model is fed the same turn (:4141-4143); drafting stops for the reply once either
   // engine's window slides after this point (kv_shifts checks :4245, :4255)
   spx_engine *D = E->draft;
@@ -1495,7 +1582,7 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
     for (int s = p->n_cached; s < n_prompt; s += chunk) {
       const int cnt = std::min(chunk, n_prompt - s);
       if (int r = spx_engine_ensure_kv_room(D, p->kv_keep, d_pos, cnt, &d_pos)) return r;
-      if (int r = spx_engine_forward(D, prompt + s, cnt, d_pos, nullptr, nullptr, dam)) return r;
+      if (int r = forward_sel(D, prompt + s, cnt, d_pos, nullptr, nullptr, dam, 2)) return r;
       d_pos += cnt;
     }
   }
@@ -1517,9 +1604,9 @@ int spx_engine_generate(spx_engine *E, const int32_t *prompt, int n_prompt, int 
   const int V = E->c.vocab;
   const float lsc = E->c.logit_scale;
   int gen = 0;
-  int tok = am[last_rows - 1];
+  int tok = am[0];  // (the last prompt row's pick; its logits are row 0)
   if (smp) {
-    if (int r = smp->prepare(E->logits + (size_t)(last_rows - 1) * V, V, 1, lsc, out, 0, 1u, false)) return r;
+    if (int r = smp->prepare(E->logits, V, 1, lsc, out, 0, 1u, false)) return r;
     tok = smp->pick(0);
   }
   int backoff = 0, skip = 0, k_dyn = p->draft_len;
@@ -1644,8 +1731,7 @@ int spx_engine_destroy(spx_engine *E) {
   if (!E) return 0;
   (void)hipSetDevice(E->ctx->device);
   (void)hipStreamSynchronize(E->ctx->stream);
-  for (auto &g : E->graph)
-    if (g) (void)hipGraphExecDestroy(g);
+  drop_graphs(E);
   for (auto ev : E->ev_pool) (void)hipEventDestroy(ev);
   for (auto &kv : E->mats) spx_tensor_free(E->ctx, kv.second);
   for (void *p : E->allocs) (void)hipFree(p);

@@ -271,6 +271,18 @@ class Engine:
                                      lg.ctypes.data_as(P) if logits else None, am.ctypes.data_as(P)))
         return am, hid, lg
 
+    def feed(self, ids, start_pos, hidden=False, logits=False):
+        """feed (spx_engine_feed): the prompt in passes of up to 128 rows, logits for the last
+        row only; returns (argmax of the last row, hidden [dim] or None, logits [vocab] or None)."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        am = np.empty(1, np.int32)
+        hid = np.empty(self.cfg.dim, np.float32) if hidden else None
+        lg = np.empty(self.cfg.vocab, np.float32) if logits else None
+        check(lib.spx_engine_feed(self.h, ids.ctypes.data_as(P), ids.size, start_pos,
+                                  hid.ctypes.data_as(P) if hidden else None,
+                                  lg.ctypes.data_as(P) if logits else None, am.ctypes.data_as(P)))
+        return int(am[0]), hid, lg
+
     def forward_slice(self, token, pos):
         return self.forward([token], pos, hidden=True)[1][0]
 

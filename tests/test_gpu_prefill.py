@@ -187,3 +187,37 @@ def test_generate_with_128_row_prompt_chunks(ctx, case):
     for k in ("accepted", "drafted", "verifies", "steps"):
         assert s16[k] == s128[k] == s0[k], k
     eng.close()
+
+
+@pytest.mark.parametrize("case", ["a3b", "dense-kquant", "tiny-llama", "tiny-granite"])
+def test_feed_equals_forward_last_row(ctx, case):
+    """spx_engine_feed (feed :3044-3104: prompt chunks of up to 128 rows, the LM head for the last
+    row only) gives the last row's hidden state of spx_engine_forward over the same chunks and
+    the same KV cache, bitwise; prompts ending in a 44-row, a one-row and a full chunk. Its
+    logits come from the one-row LM head, as the reference computes them from feed's last
+    hidden: for K-quant models the bits of the multi-row pass's last row; for the float formats
+    (whose 2..16-row LM head sums in its own order) within the matvec bar 1e-4 of it, and the
+    same pick unless the top two logits are within that bar."""
+    cfg = (CASES[case] if case in CASES else M.TINY[case].replace(sigma=0.05)).replace(max_seq=320)
+    w = M.synth_model(cfg, seed=47)
+    rng = np.random.default_rng(14)
+    for n in (300, 257, 128):
+        a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
+        ids = rng.integers(0, cfg.vocab, n)
+        print(f"{case}: feed of {n} rows", flush=True)
+        am0, h0, l0 = a.feed(ids, 0, hidden=True, logits=True)
+        for s0 in range(0, n, 128):
+            am1, h1, l1 = b.forward(ids[s0:s0 + 128], s0, hidden=True, logits=True)
+        assert _same(h0, h1[-1]), (case, n)
+        if case in CASES:
+            assert _same(l0, l1[-1]) and am0 == am1[-1], (case, n)
+        else:
+            bar = 1e-4 * np.abs(l1[-1]).max()
+            assert np.abs(l0 - l1[-1]).max() <= bar, (case, n)
+            top2 = np.sort(l1[-1])[-2:]
+            assert am0 == am1[-1] or top2[1] - top2[0] <= 2 * bar, (case, n)
+        ka, va = a.kv_cache()
+        kb, vb = b.kv_cache()
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb), (case, n)
+        a.close()
+        b.close()

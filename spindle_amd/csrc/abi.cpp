@@ -398,6 +398,25 @@ static int mv_launch(spx_ctx *ctx, const spx_tensor *w, int expert, int m, const
   return 0;
 }
 
+// One vector against a K-quant matrix on the one-row decode kernel (kd_mv: the row's Q8_K made
+// in each workgroup's prologue, row-parallel lanes, the reference's bits; no workspace): a
+// workgroup a tile up to 512 tiles, else one a CU striding over them (as for an LM head).
+static int mv_one_row(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, float *out) {
+  int G = 8, R = 1;
+  rp_shape(w->v.nb, G, R);
+  DecMVArgs a{};
+  a.w[0] = kq_rows_view(w->v, expert, 0, w->v.rows);
+  a.out[0] = out;
+  a.tiles[0] = (int)((w->v.rows + DEC_MV_NW * R - 1) / (DEC_MV_NW * R));
+  a.nseg = 1;
+  a.G = G;
+  a.in = DecIn{x, nullptr, 0.0f, (int)w->v.cols};
+  int cus = 0;
+  SPX_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
+  SPX_HIP(launch_dec_mv(a, a.tiles[0] <= 512 ? a.tiles[0] : std::max(cus, 1), ctx->stream));
+  return 0;
+}
+
 int spx_matmul_rows_q8k(spx_ctx *ctx, const spx_tensor *w, int expert, const float *xd, const int8_t *xs, const int16_t *xb, int m, float *out, int64_t ld_out, int64_t r0, int64_t r1) {
   if (!ctx || !xd || !xs || !xb || !out) return fail("spx_matmul_rows_q8k: null argument");
   if (int r = check_kq(w, expert, m)) return r;
@@ -431,6 +450,7 @@ int spx_matvec(spx_ctx *ctx, const spx_tensor *w, int expert, const float *x, in
   if (ld_x < cols || (m > 1 && ld_out < rows)) return fail("spx_matvec: leading dimension too small");
   if (ld_x % 4) return fail("spx_matvec: ld_x must be a multiple of 4 (16-byte rows)");
   if (w->v.dtype == T_Q4K || w->v.dtype == T_Q6K) {
+    if (m == 1 && w->v.nb <= DEC_MAXNB && !std::getenv("SPX_MV_MODE")) return mv_one_row(ctx, w, expert, x, out);
     bool ok = false;
     Q8KP y = ws_q8kp(ctx, m, cols, &ok);
     if (!ok) return fail("spx_matvec: workspace allocation failed");

@@ -1,6 +1,7 @@
 """Summarises a rocprofv3 kernel trace of the engine per forward pass.
 
-A pass is the kernels from k_embed to k_argmax_final; passes are grouped by kernel count, their
+A pass is the kernels from k_embed to k_argmax_final (or to the next k_embed: a prompt chunk of
+spx_engine_feed runs no LM head); passes are grouped by kernel count, their
 first matrix kernel (k_mvr<M> / k_mvt<M> / k_mv_f<M>: M = the pass's row bucket; kd_mv / kd_mm /
 kd_mq: the decode, lane-exact multi-row and int8-MFMA multi-row kernels) and their row count
 (k_embed's grid: 256 threads a row). For each group: pass span vs busy time, and (groups of at
@@ -24,6 +25,8 @@ passes, cur = [], None
 for r in rows:
     nm = short(r[2])
     if nm.startswith("k_embed"):
+        if cur is not None:
+            passes.append(cur)
         cur = [r]
     elif cur is not None:
         cur.append(r)

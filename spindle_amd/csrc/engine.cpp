@@ -89,6 +89,10 @@ struct spx_engine {
   const float *out_norm = nullptr;
   bool prepared = false, use_graphs = true;
   bool dec_ok = false, dec_on = true;  // one-row passes on the decode pipeline (decode.hip)
+  // one-row passes of a Q8_0 model on the fused kernels with the norms in the consumers'
+  // prologues and the residual adds in the producers' epilogues instead of last-workgroup
+  // tails (the same bits; SPX_FPRO=0 keeps the tails)
+  bool fpro = false;
   // one-row passes with their layers as cooperative launches (persist.hip), where the model
   // fits its tiles; off by default: measured slower than the pipeline (SPX_PERSIST=1 or
   // spx_engine_set_persist turns it on)
@@ -289,6 +293,21 @@ int mv_one(spx_engine *E, const spx_tensor *w, int m, const float *x, int64_t ld
   return 0;
 }
 
+// One-row Q8_0 matvec with the residual epilogue res_out = res_in + rscale * y (k_mv_f1):
+// the producer's half of a pass without norm tails.
+int mv_res(spx_engine *E, const spx_tensor *w, const float *x, int64_t ld_x, float *out, const float *res_in, float *res_out) {
+  MVArgs a{};
+  a.seg[0] = seg_of(w, out, w->v.rows, 1, 0, 1);
+  a.nseg = 1;
+  a.x = x;
+  a.ld_x = ld_x;
+  a.lscale = E->c.logit_scale;
+  a.res_in = res_in;
+  a.res_out = res_out;
+  a.rscale = E->c.residual_scale;
+  return mv_run(E, a, 1, 0);
+}
+
 // One forward pass of m rows at the step record's start position: embeddings through the
 // LM head and the greedy pick (forward_slice / forward_batch_slice + compute_logits_batch).
 // Residual stream: the embedding writes xA; attn_output's norm tail adds its output to xA
@@ -333,9 +352,18 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
   hipStream_t s = E->ctx->stream;
   const int dim = c.dim, hd = c.head_dim;
   const bool tails = m <= E->tail_max;
+  // one-row passes of a Q8_0 model: each consumer normalises its input row itself (pro), each
+  // producer adds its residual itself (res): no tails, no norm launches
+  const bool pro = E->fpro && m == 1;
+  auto pro_of = [&](const float *x, const float *nw, float *xn_out) {
+    NormTail t{};
+    t.x = x; t.nw = nw; t.eps = c.rms_eps; t.dim = dim; t.xn_out = xn_out;
+    return t;
+  };
   {
     ProfScope ps(E, PC_EMBED, 0);
     NormTail t = norm_next(E, 0, E->xA, nullptr, nullptr);
+    if (pro) t.nw = nullptr;  // the embedding row only
     SPX_HIP(launch_embed(E->embed->v, E->st_dev, c.embedding_scale, t, m, s));
   }
   for (int l = 0; l < c.n_layers; l++) {
@@ -355,6 +383,7 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
       a.ld_x = dim;
       a.G = G;
       a.R = R;
+      if (pro) a.pro = pro_of(E->xA, ly.attn_norm, nullptr);
       if (int r = mv_run(E, a, m, mode)) return r;
     }
     // attention (+ Q8_K of its output for an integer attn_output)
@@ -376,7 +405,11 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
     {  // attn_output + residual + ffn_norm
       ProfScope ps(E, PC_WO, wbytes(ly.wo));
       const NormTail t = norm_ffn(E, l, E->xA, E->proj, E->xB);
-      if (int r = mv_one(E, ly.wo, m, E->att, E->q_dim, E->aq, E->proj, dim, &t, tails, PC_NORM)) return r;
+      if (pro) {
+        if (int r = mv_res(E, ly.wo, E->att, E->q_dim, E->proj, E->xA, E->xB)) return r;
+      } else {
+        if (int r = mv_one(E, ly.wo, m, E->att, E->q_dim, E->aq, E->proj, dim, &t, tails, PC_NORM)) return r;
+      }
     }
     const int nff = (int)ly.gate->v.rows;
     const bool d_int = is_kq(ly.down);
@@ -391,6 +424,7 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
         ra.n_expert = ne; ra.n_used = nu; ra.norm = c.expert_norm; ra.moe_prune = c.moe_prune; ra.counter = E->rt_cnt;
         ra.chosen = E->chosen; ra.weights = E->weights; ra.nkeep = E->nkeep; ra.jobs = E->jobs; ra.njobs = ly.njobs;
         ra.expert_count = E->expert_count + (size_t)l * ne;
+        if (pro) ra.pro = pro_of(E->xB, ly.ffn_norm, nullptr);
         SPX_HIP(launch_router(ra, m, E->st_dev, s));
       }
       const int max_gu_jobs = std::min(256, m * nu);  // jobs of at most GU_USERS users
@@ -404,6 +438,7 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
         ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.x = E->xn2;
         ga.jobs = E->jobs; ga.njobs = ly.njobs + 1; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
         if (d_int) ga.hq = E->hq;
+        if (pro) ga.pro = pro_of(E->xB, ly.ffn_norm, nullptr);
         if (fq) {
           ga.jobs = E->jobs + 256; ga.njobs = ly.njobs; ga.vdiv = nu; ga.fq = 1;
           SPX_HIP(launch_gateup(ga, m, 0, E->st_dev, max_dn_jobs, s));
@@ -416,7 +451,8 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
         DownArgs da{};
         da.w = ly.down->v; da.y = E->hq; da.x = E->h; da.jobs = E->jobs + 256; da.njobs = ly.njobs; da.weights = E->weights;
         da.nkeep = E->nkeep; da.n_used = nu; da.out = E->ffn;
-        if (tails) da.tail = tn;
+        if (pro) { da.res_in = E->xB; da.res_out = E->xA; da.rscale = c.residual_scale; }
+        else if (tails) da.tail = tn;
         if (fq) {
           da.yd = E->yd; da.counter = E->dn_cnt;
           SPX_HIP(launch_down_fq(da, max_dn_jobs, E->st_dev, s));
@@ -424,7 +460,7 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
           SPX_HIP(launch_down(da, m, m > 2 && d_int && E->down_mode == 1 ? 1 : 0, E->st_dev, s));
         }
       }
-      if (!tails) { ProfScope ps(E, PC_NORM, 0); SPX_HIP(launch_norm(tn, E->st_dev, m, s)); }
+      if (!tails && !pro) { ProfScope ps(E, PC_NORM, 0); SPX_HIP(launch_norm(tn, E->st_dev, m, s)); }
     } else {  // ffn_forward / ffn_forward_multi (:590-646): k = 1, w = 1
       {
         ProfScope ps(E, PC_GATEUP, wbytes(ly.gate) + wbytes(ly.up));
@@ -432,11 +468,16 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
         ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.x = E->xn2; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
         ga.fq = E->mq && m >= FQ_MIN_ROWS ? 1 : 0;
         if (d_int) ga.hq = E->hq;
+        if (pro) ga.pro = pro_of(E->xB, ly.ffn_norm, nullptr);
         SPX_HIP(launch_gateup(ga, m, gmode, E->st_dev, 1, s));
       }
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down));
-        if (int r = mv_one(E, ly.down, m, E->h, nff, E->hq, E->ffn, dim, &tn, tails, PC_NORM)) return r;
+        if (pro) {
+          if (int r = mv_res(E, ly.down, E->h, nff, E->ffn, E->xB, E->xA)) return r;
+        } else {
+          if (int r = mv_one(E, ly.down, m, E->h, nff, E->hq, E->ffn, dim, &tn, tails, PC_NORM)) return r;
+        }
       }
     }
   }
@@ -456,6 +497,7 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
     a.x = E->xn + (int64_t)(m - lm) * dim;
     a.ld_x = dim;
     a.y = q8kp_row(E->xq, m - lm, dim);
+    if (pro) a.pro = pro_of(E->xA, E->out_norm, E->xn);  // (one row: xn written by workgroup 0)
     a.G = G;
     a.R = R;
     a.best = E->best;
@@ -1065,6 +1107,17 @@ int spx_engine_prepare(spx_engine *E) {
     if (ly.moe) dok = dok && (int64_t)nu * ly.gate->v.rows <= DEC_DOWN_Q;
   }
   E->dec_ok = dok;
+  {  // every one-row consumer of a normalised row must be a kernel with the prologue
+    auto q8 = [](const spx_tensor *t) { return t->v.dtype == T_Q8_0 && t->v.cols <= 4096; };
+    bool fp = !dok && q8(E->lm_head) && c.dim <= 256 * NORM_NT;
+    for (auto &ly : E->L) {
+      fp = fp && q8(ly.wq) && q8(ly.wk) && q8(ly.wv) && q8(ly.wo) && ly.wk->v.cols == ly.wq->v.cols && ly.wv->v.cols == ly.wq->v.cols;
+      fp = fp && !is_kq(ly.gate) && !is_kq(ly.up);
+      fp = fp && (ly.moe ? ly.router->v.dtype == T_F32 && !is_kq(ly.down) : q8(ly.down));
+    }
+    if (const char *v = std::getenv("SPX_FPRO")) fp = fp && atoi(v) != 0;
+    E->fpro = fp;
+  }
   // passes of 2..16 rows: expert down rows of at most 4 blocks (n_ff <= 1024)
   // the down kernel stages every user's Q8_K h row in LDS: 16 rows x n_used users
   for (auto &ly : E->L) {

@@ -72,6 +72,13 @@ struct MVArgs {
   // float path, passes of FQ_MIN_ROWS..16 rows: Q8_0 segments on the fp32 matrix cores
   // (k_mv_fq) instead of the per-lane walk (the same products, summed in another order)
   int fq;
+  // one-row Q8_0 passes (k_mv_f1 only): pro.nw set: the input row is pro.x, normalised by every
+  // workgroup as norm_rows would (workgroup 0 also writes pro.xn_out); res_out set: residual
+  // epilogue res_out[r] = res_in[r] + rscale * y[r] (one segment)
+  NormTail pro;
+  const float *res_in;
+  float *res_out;
+  float rscale;
 };
 constexpr int FQ_MIN_ROWS = 2;  // one-row passes keep the per-lane walk (a 16-vector tile would idle 15 columns)
 
@@ -115,6 +122,7 @@ struct RouterArgs {
   Job *jobs;                          // gate/up jobs [256] (<= GU_USERS users), then down jobs [256]
   int *njobs;                         // [2]: down jobs (= distinct experts), gate/up jobs
   int *expert_count;                  // optional [n_expert] selection counter
+  NormTail pro;                       // one-row passes: pro.nw set: x is pro.x, normalised in every workgroup
 };
 
 // Gate/up + SwiGLU (+ Q8_K of h by the last workgroup covering each 256-row block) over
@@ -132,6 +140,7 @@ struct GUArgs {
   int G;                              // row-parallel launch: lane groups per row
   int fq;                             // Q8_0, 2..16 rows: on the fp32 matrix cores (k_gateup_fq)
   int vdiv;                           // > 1: a job's vec entries are h indices (row * vdiv + slot), the input row their quotient
+  NormTail pro;                       // one-row float passes (k_gateup_f): pro.nw set: x is pro.x, normalised in every workgroup
 };
 
 struct DownArgs {
@@ -148,6 +157,9 @@ struct DownArgs {
   NormTail tail;
   float *yd;                          // launch_down_fq: y per (row, slot) [m * n_used][dim]
   int *counter;                       // launch_down_fq: arrivals per 32 output rows [dim / 32][CNT_STRIDE] (+ one), zero between passes
+  const float *res_in;                // k_down_f: residual epilogue res_out = res_in + rscale * out (instead of a tail)
+  float *res_out;
+  float rscale;
 };
 
 hipError_t launch_embed(const TensorView &e, const StepRec *st, float escale, const NormTail &t, int m, hipStream_t s);

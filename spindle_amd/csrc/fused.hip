@@ -93,6 +93,59 @@ __device__ __forceinline__ void norm_rows(const NormTail &t, int b0, int b1) {
   }
 }
 
+// The same RMSNorm of one row (t.x, no residual add) computed by a consumer's workgroup for
+// itself: the row and its weights loaded (load), then norm_rows's per-block fma chains and
+// wavefront trees, the blocks in order, x * inv * w (finish) into LDS lx (and memory, xn_out).
+// The bits are norm_rows's: a producer's residual epilogue plus this prologue replace its tail.
+template <int NW>
+struct NormRow {
+  float4 r[NORM_NT / NW], w[NORM_NT / NW];
+  __device__ __forceinline__ void load(const NormTail &t) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n4 = t.dim >> 2, nblk = (n4 + 63) >> 6;
+#pragma unroll
+    for (int k = 0; k < NORM_NT / NW; k++) {
+      const int tb = wave + NW * k, f = tb * 64 + lane;
+      r[k] = w[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (tb < nblk && f < n4) {
+        r[k] = reinterpret_cast<const float4 *>(t.x)[f];
+        w[k] = reinterpret_cast<const float4 *>(t.nw)[f];
+      }
+    }
+  }
+  __device__ __forceinline__ void finish(const NormTail &t, float *lx, float *xn_out) {
+    __shared__ float bsum[NORM_NT];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n4 = t.dim >> 2, nblk = (n4 + 63) >> 6;
+#pragma unroll
+    for (int k = 0; k < NORM_NT / NW; k++) {
+      const int tb = wave + NW * k;
+      if (tb < nblk) {
+        float p = r[k].x * r[k].x;
+        p = fmaf(r[k].y, r[k].y, p);
+        p = fmaf(r[k].z, r[k].z, p);
+        p = fmaf(r[k].w, r[k].w, p);
+        p = wave_sum(p);
+        if (lane == 0) bsum[tb] = p;
+      }
+    }
+    __syncthreads();
+    float S = 0.0f;
+    for (int k = 0; k < nblk; k++) S = S + bsum[k];
+    const float inv = inv_rms(S, (float)t.dim, t.eps);
+#pragma unroll
+    for (int k = 0; k < NORM_NT / NW; k++) {
+      const int tb = wave + NW * k, f = tb * 64 + lane;
+      if (tb < nblk && f < n4) {
+        float4 v = r[k];
+        const float4 ww = w[k];
+        v.x = v.x * inv * ww.x; v.y = v.y * inv * ww.y; v.z = v.z * inv * ww.z; v.w = v.w * inv * ww.w;
+        reinterpret_cast<float4 *>(lx)[f] = v;
+        if (xn_out) reinterpret_cast<float4 *>(xn_out)[f] = v;
+      }
+    }
+    __syncthreads();
+  }
+};
+
 // ------------------------------------------------------------------ activations in LDS
 __host__ __device__ inline size_t ldsq_dbytes(int mt, int dim) { return ((size_t)mt * (dim / 256) * 4 + 15) & ~(size_t)15; }
 __host__ __device__ inline size_t ldsq_bytes(int mt, int dim) {
@@ -419,10 +472,16 @@ template <> struct FRaw<T_Q5K> {  // not used: Q5_K rows take q5k_walk
   __device__ __forceinline__ void decode(float q[32]) const {}
 };
 
-template <int T, int MT, int D>
+struct NoPre {
+  __device__ __forceinline__ void operator()() const {}
+};
+// pre() runs once the first blocks' loads are issued, before x is read (every thread of the
+// workgroup reaches it: it may synchronise the workgroup).
+template <int T, int MT, int D, class Pre = NoPre>
 __device__ __forceinline__ void f_walk(const Planes &pl, int64_t grow, int nb, const float *x, int64_t ld_x, const int *vidx, int mv, int l,
-                                       float *res) {
+                                       float *res, Pre pre = Pre{}) {
   if constexpr (T == T_Q5K) {
+    pre();
     q5k_walk<MT>(pl, grow, nb, x, ld_x, vidx, mv, l, res);
     return;
   }
@@ -435,6 +494,7 @@ __device__ __forceinline__ void f_walk(const Planes &pl, int64_t grow, int nb, c
 #pragma unroll
   for (int j = 0; j < D; j++)
     if (j < nmine) buf[j].load(pl, g0 + l + 8 * j);
+  pre();
   for (int k0 = 0; k0 < nmine; k0 += D) {
 #pragma unroll
     for (int j = 0; j < D; j++) {
@@ -725,9 +785,16 @@ __global__ __launch_bounds__(MVF1_NW * 64) void k_mv_f1(const MVArgs a, const St
       dh[k] = *reinterpret_cast<const uint16_t *>(sg.w.pl.p3 + g * 2);
     }
   };
-  fetch((int)blockIdx.x / S);
-  for (int i = threadIdx.x; i < cols / 4; i += MVF1_NW * 64) reinterpret_cast<float4 *>(lx)[i] = reinterpret_cast<const float4 *>(a.x)[i];
-  __syncthreads();
+  if (a.pro.nw) {  // the input row normalised here (a producer's tail otherwise)
+    NormRow<MVF1_NW> nr;
+    nr.load(a.pro);
+    fetch((int)blockIdx.x / S);
+    nr.finish(a.pro, lx, blockIdx.x == 0 ? a.pro.xn_out : nullptr);
+  } else {
+    fetch((int)blockIdx.x / S);
+    for (int i = threadIdx.x; i < cols / 4; i += MVF1_NW * 64) reinterpret_cast<float4 *>(lx)[i] = reinterpret_cast<const float4 *>(a.x)[i];
+    __syncthreads();
+  }
   for (int t = (int)blockIdx.x / S; t < total; t += (int)gridDim.x / S) {
     int wg;
     const Seg &sg = a.seg[seg_index(a, t, wg)];
@@ -765,6 +832,7 @@ __global__ __launch_bounds__(MVF1_NW * 64) void k_mv_f1(const MVArgs a, const St
     const int64_t row = rbase + r;
     if (r < RW && l == 0 && row < sg.r1) {
       out_store(sg.out + row, res, coh);
+      if (a.res_out) a.res_out[row] = a.res_in[row] + a.rscale * res;
       if (a.best) { const unsigned long long key = pick_key(res, a.lscale, row); bestv[0] = key > bestv[0] ? key : bestv[0]; }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -1690,6 +1758,7 @@ __global__ __launch_bounds__(64) void k_rows_prep(const AttnArgs a, float *qp, c
 // expert order, users in (row, slot) order (:982-986).
 template <int MT>
 __global__ __launch_bounds__(256) void k_router(const RouterArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];  // one-row passes with pro.nw: the normalised row
   __shared__ float part[4][MAX_M];
   const int m = st->m, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int dim = a.dim, n4 = dim >> 2, row = blockIdx.x;
@@ -1697,10 +1766,16 @@ __global__ __launch_bounds__(256) void k_router(const RouterArgs a, const StepRe
   const float4 *wr = reinterpret_cast<const float4 *>(a.w.pl.p0 + (int64_t)row * dim * 4);
   const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
   float4 wv[NK];
+  NormRow<4> nr;
+  if (MT == 1 && a.pro.nw) nr.load(a.pro);  // one-row passes: the input row normalised here
 #pragma unroll
   for (int k = 0; k < NK; k++) {
     const int f = wave * 64 + lane + 256 * k;
     wv[k] = f < n4 ? wr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (MT == 1 && a.pro.nw) {
+    nr.finish(a.pro, reinterpret_cast<float *>(smem), nullptr);
+    x4 = reinterpret_cast<const float4 *>(smem);
   }
   for (int v0 = 0; v0 < m; v0 += MT) {
     float pv[MT];
@@ -1975,6 +2050,7 @@ __global__ __launch_bounds__(256) void k_gateup_rp(const GUArgs a, const StepRec
 // Float weights (Q8_0 / Q5_0) x fp32 activations: 16 rows of h per workgroup.
 template <int T, int MT>
 __global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];  // one-row passes with pro.nw: the normalised row
   GUJob J;
   if (!gu_job(a, st->m, J)) return;
   constexpr int D = f_depth<MT>();
@@ -1989,7 +2065,14 @@ __global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec 
 #pragma unroll
   for (int v = 0; v < MT; v++) vidx[v] = J.jv && v < J.nvec ? J.jv[v] : v;
   float res[MT];
-  f_walk<T, MT, D>(pl, grow, nb, a.x, w.cols, vidx, J.nvec, l, res);
+  if (MT == 1 && a.pro.nw) {  // the input row normalised here, once the first weights are requested
+    float *lx = reinterpret_cast<float *>(smem);
+    NormRow<4> nr;
+    nr.load(a.pro);
+    f_walk<T, MT, D>(pl, grow, nb, lx, w.cols, vidx, J.nvec, l, res, [&]() { nr.finish(a.pro, lx, nullptr); });
+  } else {
+    f_walk<T, MT, D>(pl, grow, nb, a.x, w.cols, vidx, J.nvec, l, res);
+  }
 #pragma unroll
   for (int v = 0; v < MT; v++) {
     const float u = __shfl_down(res[v], 32);
@@ -2050,6 +2133,7 @@ __device__ __forceinline__ void down_combine(const DownArgs &a, int m, float (*y
     float acc = 0.0f;
     for (int i = 0; i < nk; i++) acc = acc + a.weights[b * 32 + i] * yb[wave][b * a.n_used + i];
     out_store(a.out + (int64_t)b * dim + r, acc, coh);
+    if (a.res_out) a.res_out[(int64_t)b * dim + r] = a.res_in[(int64_t)b * dim + r] + a.rscale * acc;
   }
 }
 
@@ -2293,6 +2377,8 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
   mt = bucket(mt);
   const int dt = a.seg[0].w.dtype, cols = (int)a.seg[0].w.cols, nb = cols / 256;
   if (grid < 1) return hipErrorInvalidValue;
+  const bool f1_only = a.pro.nw || a.res_out;  // prologue norm / residual epilogue: k_mv_f1 only
+  if (f1_only && (kq_type(dt) || mt != 1 || (a.res_out && a.nseg != 1))) return hipErrorInvalidValue;
   if (!kq_type(dt)) {
     bool fq = a.fq && a.m >= FQ_MIN_ROWS;
     for (int i = 0; i < a.nseg; i++) fq = fq && a.seg[i].w.dtype == T_Q8_0;
@@ -2302,7 +2388,7 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
       hipLaunchKernelGGL(k_mv_fq<1>, dim3(!a.best && grid == mv_total(a) ? 2 * grid : grid), dim3(512), 0, s, a, st);
       return hipGetLastError();
     }
-    if (mt == 1) {  // one row over Q8_0 segments: k_mv_f1
+    if (mt == 1) {  // one row over Q8_0 segments: k_mv_f1 (the only kernel that takes pro / res_out)
       bool q8 = true;
       for (int i = 0; i < a.nseg; i++) q8 = q8 && a.seg[i].w.dtype == T_Q8_0 && a.seg[i].w.cols == a.seg[0].w.cols;
       // rows a wavefront: 8 with greedy keys (a slot per task) or tasks for the whole GPU, else
@@ -2327,6 +2413,7 @@ hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int g
         return by_ni(std::integral_constant<int, 1>{});
       }
     }
+    if (f1_only) return hipErrorInvalidValue;
 #define SPX_MVF(MTV) hipLaunchKernelGGL(k_mv_f<MTV>, dim3(grid), dim3(256), 0, s, a, st)
     switch (mt) {
     case 1: SPX_MVF(1); break;
@@ -2452,7 +2539,7 @@ hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStre
   mt = bucket(mt);
   const int grid = a.n_expert;
   switch (mt) {
-  case 1: hipLaunchKernelGGL(k_router<1>, dim3(grid), dim3(256), 0, s, a, st); break;
+  case 1: hipLaunchKernelGGL(k_router<1>, dim3(grid), dim3(256), a.pro.nw ? (size_t)a.dim * 4 : 0, s, a, st); break;
   case 2: hipLaunchKernelGGL(k_router<2>, dim3(grid), dim3(256), 0, s, a, st); break;
   case 4: hipLaunchKernelGGL(k_router<4>, dim3(grid), dim3(256), 0, s, a, st); break;
   default: hipLaunchKernelGGL(k_router<8>, dim3(grid), dim3(256), 0, s, a, st); break;
@@ -2477,7 +2564,8 @@ static hipError_t launch_gu_t(const GUArgs &a, int mode, const StepRec *st, int 
   } else if (T == T_Q8_0 && MT >= 4 && a.fq) {
     hipLaunchKernelGGL(k_gateup_fq, dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(1024), 0, s, a, st);
   } else {
-    hipLaunchKernelGGL((k_gateup_f<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), 0, s, a, st);
+    hipLaunchKernelGGL((k_gateup_f<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256),
+                       MT == 1 && a.pro.nw ? (size_t)a.gate.cols * 4 : 0, s, a, st);
   }
   return hipGetLastError();
 }

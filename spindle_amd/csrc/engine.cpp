@@ -424,7 +424,7 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
         ra.n_expert = ne; ra.n_used = nu; ra.norm = c.expert_norm; ra.moe_prune = c.moe_prune; ra.counter = E->rt_cnt;
         ra.chosen = E->chosen; ra.weights = E->weights; ra.nkeep = E->nkeep; ra.jobs = E->jobs; ra.njobs = ly.njobs;
         ra.expert_count = E->expert_count + (size_t)l * ne;
-        if (pro) ra.pro = pro_of(E->xB, ly.ffn_norm, nullptr);
+        if (pro) { ra.pro = pro_of(E->xB, ly.ffn_norm, nullptr); ra.logits_only = 1; }
         SPX_HIP(launch_router(ra, m, E->st_dev, s));
       }
       const int max_gu_jobs = std::min(256, m * nu);  // jobs of at most GU_USERS users
@@ -438,7 +438,13 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
         ga.gate = ly.gate->v; ga.up = ly.up->v; ga.y = E->xq2; ga.x = E->xn2;
         ga.jobs = E->jobs; ga.njobs = ly.njobs + 1; ga.h = E->h; ga.counter = E->gu_cnt; ga.n_ff = nff;
         if (d_int) ga.hq = E->hq;
-        if (pro) ga.pro = pro_of(E->xB, ly.ffn_norm, nullptr);
+        if (pro) {  // the routing in the gate/up prologue (one job per kept choice)
+          ga.pro = pro_of(E->xB, ly.ffn_norm, nullptr);
+          F1Route &rt = ga.rt;
+          rt.logits = E->rlog; rt.n_expert = ne; rt.n_used = nu; rt.norm = c.expert_norm; rt.moe_prune = c.moe_prune;
+          rt.chosen = E->chosen; rt.weights = E->weights; rt.nkeep = E->nkeep; rt.jobs = E->jobs + 256; rt.njobs = ly.njobs;
+          rt.expert_count = E->expert_count + (size_t)l * ne;
+        }
         if (fq) {
           ga.jobs = E->jobs + 256; ga.njobs = ly.njobs; ga.vdiv = nu; ga.fq = 1;
           SPX_HIP(launch_gateup(ga, m, 0, E->st_dev, max_dn_jobs, s));

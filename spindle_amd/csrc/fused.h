@@ -123,6 +123,23 @@ struct RouterArgs {
   int *njobs;                         // [2]: down jobs (= distinct experts), gate/up jobs
   int *expert_count;                  // optional [n_expert] selection counter
   NormTail pro;                       // one-row passes: pro.nw set: x is pro.x, normalised in every workgroup
+  int logits_only;                    // the logits only (the routing runs in the gate/up prologue)
+};
+
+// One-row passes of a float MoE: the routing in every gate/up workgroup from the router's
+// logits (route_row), workgroup b.y taking the job of rank b.y among the kept choices in expert
+// order; workgroup (0, 0) writes the choices, weights, keep count, the down jobs (one user each),
+// the job counts and the selection counts, as the router's last workgroup would.
+struct F1Route {
+  const float *logits;                // [n_expert]; null: jobs come from the router
+  int n_expert, n_used, norm;
+  float moe_prune;
+  int *chosen;                        // [32]
+  float *weights;                     // [32]
+  int *nkeep;                         // [1]
+  Job *jobs;                          // down jobs
+  int *njobs;                         // [2]: down jobs, gate/up jobs
+  int *expert_count;                  // optional [n_expert]
 };
 
 // Gate/up + SwiGLU (+ Q8_K of h by the last workgroup covering each 256-row block) over
@@ -141,6 +158,7 @@ struct GUArgs {
   int fq;                             // Q8_0, 2..16 rows: on the fp32 matrix cores (k_gateup_fq)
   int vdiv;                           // > 1: a job's vec entries are h indices (row * vdiv + slot), the input row their quotient
   NormTail pro;                       // one-row float passes (k_gateup_f): pro.nw set: x is pro.x, normalised in every workgroup
+  F1Route rt;                         // one-row float passes (k_gateup_f): routing in the prologue
 };
 
 struct DownArgs {

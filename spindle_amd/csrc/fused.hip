@@ -24,6 +24,7 @@
 #include "decode.h"
 #include "dev.h"
 #include "attn.h"
+#include "decode_dev.h"
 
 namespace spx {
 
@@ -1807,6 +1808,7 @@ __global__ __launch_bounds__(256) void k_router(const RouterArgs a, const StepRe
     const int v = threadIdx.x;
     st_dev(a.logits + (int64_t)v * a.n_expert + row, ((part[0][v] + part[1][v]) + part[2][v]) + part[3][v]);
   }
+  if (a.logits_only) return;
   if (!arrive_last(a.counter, gridDim.x)) return;
   // routing: wave w takes rows w, w+4, ...; lane i < n_used ends up holding the row's i-th
   // choice (expert, probability)
@@ -2052,7 +2054,47 @@ template <int T, int MT>
 __global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec *st) {
   extern __shared__ __align__(16) uint8_t smem[];  // one-row passes with pro.nw: the normalised row
   GUJob J;
-  if (!gu_job(a, st->m, J)) return;
+  __shared__ int s_route[2];  // this workgroup's job: expert (-1: none), slot
+  NormRow<4> nr;
+  if (MT == 1 && a.pro.nw) nr.load(a.pro);  // (in flight during the routing)
+  if (MT == 1 && a.rt.logits) {
+    const F1Route &rt = a.rt;
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      float lv[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) lv[k] = lane + 64 * k < rt.n_expert ? rt.logits[lane + 64 * k] : -INFINITY;
+      int my_e, keep;
+      float my_p, wsum;
+      route_row(lv, rt.n_expert, rt.n_used, rt.moe_prune, my_e, my_p, keep, wsum);
+      int rank = 0;  // among the kept choices by expert index: the job order
+      for (int i = 0; i < keep; i++) rank += __shfl(my_e, i) < my_e ? 1 : 0;
+      if (lane == 0) s_route[0] = -1;
+      __builtin_amdgcn_wave_barrier();
+      if (lane < keep && rank == (int)blockIdx.y) { s_route[0] = my_e; s_route[1] = lane; }
+      if (blockIdx.x == 0 && blockIdx.y == 0) {
+        if (lane < keep) {
+          rt.chosen[lane] = my_e;
+          rt.weights[lane] = rt.norm ? my_p / wsum : my_p;
+          Job &Jd = rt.jobs[rank];
+          Jd.expert = my_e;
+          Jd.nvec = 1;
+          Jd.vec[0] = lane;
+          Jd.out[0] = lane;
+          if (rt.expert_count) rt.expert_count[my_e] += 1;
+        }
+        if (lane == 0) { rt.nkeep[0] = keep; rt.njobs[0] = keep; rt.njobs[1] = keep; }
+      }
+    }
+    __syncthreads();
+    if (s_route[0] < 0) return;
+    J.expert = s_route[0];
+    J.nvec = 1;
+    J.jv = nullptr;
+    J.jo = &s_route[1];
+  } else if (!gu_job(a, st->m, J)) {
+    return;
+  }
   constexpr int D = f_depth<MT>();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
   const TensorView &w = slot < 4 ? a.gate : a.up;
@@ -2067,8 +2109,6 @@ __global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec 
   float res[MT];
   if (MT == 1 && a.pro.nw) {  // the input row normalised here, once the first weights are requested
     float *lx = reinterpret_cast<float *>(smem);
-    NormRow<4> nr;
-    nr.load(a.pro);
     f_walk<T, MT, D>(pl, grow, nb, lx, w.cols, vidx, J.nvec, l, res, [&]() { nr.finish(a.pro, lx, nullptr); });
   } else {
     f_walk<T, MT, D>(pl, grow, nb, a.x, w.cols, vidx, J.nvec, l, res);

@@ -188,6 +188,10 @@ hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStre
 // q and k, as the attention kernel does it): prepared queries to qp [m][q_dim], K / V rows to
 // the cache (f16 RNE); then launch_attention with a.prepped = 1 reads them from there
 hipError_t launch_rows_prep(const AttnArgs &a, float *qp, int m, const StepRec *st, hipStream_t s);
+// Prefill attention with bits of its own (rows prepared by launch_rows_prep, a.prepped = 1): a
+// chunk loop per (kv head, 64 queries, one of four splits of the chunks) with an online softmax,
+// then the splits merged in order into the att rows (and their Q8_K when a.aq is set).
+hipError_t launch_attention_fl(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);
 // The same attention for prepared rows as partials (a workgroup per chunk, kv head and four
 // query tiles, a wavefront per tile) and a merge launch: each output has launch_attention's bits
 hipError_t launch_attention_pf(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);

@@ -1260,6 +1260,206 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(const AttnArgs a, const S
   attn_tile_out<HD>(a, h, qa, NQ, ol);
 }
 
+// ------------------------------------------------------------------ prefill attention, chunk loop
+// Prefill passes (rows prepared by k_rows_prep: queries in qp, every K / V row in the cache) with
+// attention bits of their own: a workgroup of eight wavefronts per (kv head, block of 64 queries,
+// split sp of FL_SPLITS over the pass's 64-position chunks). Its two halves (wavefronts 0-3 and
+// 4-7, 16 queries a wavefront) walk the split's even and odd chunks with an online softmax: per
+// chunk S^T = K Q^T on the matrix cores (queries as hi + lo f16, as the chunk items take them),
+// the chunk's max, M' = max(M, m_c), p = exp(s - M'), O = O exp(M - M') + P V,
+// L = L exp(M - M') + sum p; then the halves' states meet in LDS (half 0 then half 1) and one
+// (M, L, O) partial per query and split goes to memory, which k_attn_fl_merge merges in split
+// order (attn_merge16: the chunk merges' arithmetic). The queries are prepared once per
+// workgroup, not once per chunk, and the partials are FL_SPLITS a query, not one a chunk. The
+// workgroups of one (kv head, split) run on one XCD (workgroup i on XCD i mod 8), so its
+// chunks' K / V come from HBM about once for all its query blocks.
+constexpr int FL_SPLITS = 4;
+template <int HD>
+__global__ __launch_bounds__(512) void k_attn_fl(const AttnArgs a, const StepRec *st) {
+  constexpr int KS = HD + 8, VS = 64 + 8, DT = HD / 16, DQ = HD / 4, NU = DQ / 8;
+  constexpr int HALF_E = 64 * KS + HD * VS;  // f16 elements of one half's K / V tiles
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int m = st->m, start = st->start, total = start + m;
+  const int g = a.n_heads / a.n_kv, NQ = m * g, nqb = (gridDim.x >> 3) / ((a.n_kv * FL_SPLITS + 7) >> 3);
+  const int L = blockIdx.x, xcd = L & 7, j = L >> 3, qb = j % nqb, pr = (j / nqb) * 8 + xcd;
+  if (pr >= a.n_kv * FL_SPLITS || qb * 64 >= NQ) return;
+  const int h = pr / FL_SPLITS, sp = pr - h * FL_SPLITS;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ar = lane & 15, kq = lane >> 4, kg = 4 * kq;
+  const int hf = wave >> 2, t256 = tid & 255;  // half (stream) and the thread's place in it
+  _Float16 *ks = reinterpret_cast<_Float16 *>(smem) + hf * HALF_E;  // [64][KS]
+  _Float16 *vt = ks + 64 * KS;                                       // [HD][VS] (V transposed)
+  const int qa = qb * 64 + (wave & 3) * 16, qi = qa + ar;
+  const bool qact = qi < NQ;
+  // chunks of this split, up to the last position the workgroup's queries see; half hf takes
+  // c0 + hf, c0 + hf + 2, ... (both halves walk the same number of steps: the barriers)
+  const int nch = (total + 63) >> 6, b_last = min(NQ, qb * 64 + 64) - 1;
+  const int c0 = sp * nch / FL_SPLITS, c1 = min((sp + 1) * nch / FL_SPLITS, (start + b_last / g) / 64 + 1);
+  const int nstep = c1 > c0 ? (c1 - c0 + 1) >> 1 : 0;
+  const int64_t cache0 = (int64_t)a.layer * a.max_seq * a.kv_dim + (int64_t)h * HD;
+  const int lp = t256 >> 2, lq = t256 & 3;  // K / V loader: position lp, dims lq DQ ..
+  uint32_t kr[4 * NU], vr[4 * NU];
+  auto kv_load = [&](int c) {  // (a step past the split's chunks loads a valid row, never used)
+    attn_kv_load<NU>(a, cache0 + (int64_t)min(min(c, nch - 1) * 64 + lp, total - 1) * a.kv_dim + lq * DQ, kr, vr);
+  };
+  if (nstep > 0) kv_load(c0 + hf);
+  // the queries (prepared rows), hi + lo f16 operands: lane holds query ar, dims 16 kt + kg ..
+  h4v qhi[DT], qlo[DT];
+  {
+    const int qb_row = qact ? qi / g : 0, qhead = qact ? qi % g : 0;
+    const float *src = a.q + (int64_t)qb_row * a.n_heads * HD + (h * g + qhead) * HD + kg;
+#pragma unroll
+    for (int kt = 0; kt < DT; kt++) {
+      const float4 x = *reinterpret_cast<const float4 *>(src + kt * 16);
+      const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; s4++) {
+        _Float16 hh, ll;
+        split_f16(qact ? xs[s4] : 0.0f, hh, ll);
+        qhi[kt][s4] = hh;
+        qlo[kt][s4] = ll;
+      }
+    }
+  }
+  const int lim = qact ? start + qi / g + 1 : 0;  // positions < lim are visible to query ar
+  float Mq = -INFINITY, Lq = 0.0f;                // running max and sum of query ar
+  f4v acc[DT];                                    // O: query kg + r, dim 16 dt + ar
+#pragma unroll
+  for (int dt = 0; dt < DT; dt++) acc[dt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int step = 0; step < nstep; step++) {
+    const int c = c0 + hf + 2 * step, p_lo = c * 64;
+    const bool mine = c < c1;
+    __syncthreads();  // the previous chunks' K / V are read
+    {  // chunk c's rows to LDS (rows past the pass: zero), then the next chunk's loads in flight
+      uint16_t *vt16 = reinterpret_cast<uint16_t *>(vt);
+      const bool live = mine && p_lo + lp < total;
+#pragma unroll
+      for (int u = 0; u < NU; u++)
+        reinterpret_cast<uint4 *>(ks + lp * KS + lq * DQ)[u] =
+            live ? make_uint4(kr[4 * u], kr[4 * u + 1], kr[4 * u + 2], kr[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int t = 0; t < 4 * NU; t++) {
+        const uint32_t w = live ? vr[t] : 0u;
+        vt16[(lq * DQ + 2 * t) * VS + lp] = (uint16_t)(w & 0xffffu);
+        vt16[(lq * DQ + 2 * t + 1) * VS + lp] = (uint16_t)(w >> 16);
+      }
+    }
+    if (step + 1 < nstep) kv_load(c + 2);
+    __syncthreads();
+    if (qa >= NQ || !mine) continue;  // (such wavefronts still meet the barriers)
+    // scores: sacc[pb][r] = S[query ar][position p_lo + 16 pb + kg + r]
+    f4v sacc[4];
+#pragma unroll
+    for (int pb = 0; pb < 4; pb++) {
+      sacc[pb] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kt = 0; kt < DT; kt++) {
+        const h4v bk = *reinterpret_cast<const h4v *>(ks + (pb * 16 + ar) * KS + kt * 16 + kg);
+        sacc[pb] = mfma16(bk, qhi[kt], sacc[pb]);
+        sacc[pb] = mfma16(bk, qlo[kt], sacc[pb]);
+      }
+    }
+    float sv[4][4], mx = -INFINITY;
+#pragma unroll
+    for (int pb = 0; pb < 4; pb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int pos = p_lo + pb * 16 + kg + r;
+        sv[pb][r] = pos < lim ? sacc[pb][r] * a.scale : -INFINITY;
+        mx = fmaxf(mx, sv[pb][r]);
+      }
+    mx = max16(mx);
+    mx = max32(mx);
+    const float Mn = fmaxf(Mq, mx);
+    const float al = Mq == -INFINITY ? 0.0f : expf(Mq - Mn);  // (nothing accumulated yet: O, L are 0)
+    float pv[4][4], ls4[4];
+#pragma unroll
+    for (int pb = 0; pb < 4; pb++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) pv[pb][r] = sv[pb][r] == -INFINITY ? 0.0f : expf(sv[pb][r] - Mn);
+      ls4[pb] = (pv[pb][0] + pv[pb][1]) + (pv[pb][2] + pv[pb][3]);
+      ls4[pb] = add16(ls4[pb]);
+      ls4[pb] = add32(ls4[pb]);
+    }
+    Lq = fmaf(Lq, al, (ls4[0] + ls4[1]) + (ls4[2] + ls4[3]));
+    Mq = Mn;
+    // O rows are queries kg + r: their factors from lanes kg + r (query ar = kg + r)
+    float alr[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) alr[r] = __shfl(al, kg + r, 64);
+    h4v phv[4], plv[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        _Float16 hh, ll;
+        split_f16(pv[kt][r], hh, ll);
+        phv[kt][r] = hh;
+        plv[kt][r] = ll;
+      }
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) {
+      f4v o = acc[dt];
+#pragma unroll
+      for (int r = 0; r < 4; r++) o[r] = o[r] * alr[r];
+#pragma unroll
+      for (int kt = 0; kt < 4; kt++) {
+        const h4v bv = *reinterpret_cast<const h4v *>(vt + (dt * 16 + ar) * VS + kt * 16 + kg);
+        o = mfma16(phv[kt], bv, o);
+        o = mfma16(plv[kt], bv, o);
+      }
+      acc[dt] = o;
+    }
+  }
+  // the halves meet: half 1's states to LDS (over the K / V tiles), half 0 combines (half 0's
+  // weight first) and writes the split's partial
+  __syncthreads();
+  float *xo = reinterpret_cast<float *>(smem);            // [4 waves][DT][4][64]
+  float *xm = xo + 4 * DT * 4 * 64;                       // [4 waves][16][2]
+  const int w4 = wave & 3;
+  if (hf == 1) {
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) xo[((w4 * DT + dt) * 4 + r) * 64 + lane] = acc[dt][r];
+    if (kq == 0) { xm[(w4 * 16 + ar) * 2] = Mq; xm[(w4 * 16 + ar) * 2 + 1] = Lq; }
+  }
+  __syncthreads();
+  if (hf == 1 || qa >= NQ) return;
+  const float M1 = xm[(w4 * 16 + ar) * 2], L1 = xm[(w4 * 16 + ar) * 2 + 1];
+  const float Mt = fmaxf(Mq, M1);
+  const float w0 = Mq == -INFINITY ? 0.0f : expf(Mq - Mt), w1 = M1 == -INFINITY ? 0.0f : expf(M1 - Mt);
+  const float Lt = fmaf(L1, w1, Lq * w0);
+  float w0r[4], w1r[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) { w0r[r] = __shfl(w0, kg + r, 64); w1r[r] = __shfl(w1, kg + r, 64); }
+  const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nslot) * ATT_QMAX * 2);
+  const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nslot) * ATT_QMAX * HD);
+  if (kq == 0 && qact) st_coh2(r_ml, (sp * ATT_QMAX + qi) * 8, f2v{Mt, Lt});
+#pragma unroll
+  for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int q = qa + kg + r;
+      const float o = fmaf(xo[((w4 * DT + dt) * 4 + r) * 64 + lane], w1r[r], acc[dt][r] * w0r[r]);
+      if (q < NQ) st_coh1(r_o, ((sp * ATT_QMAX + q) * HD + dt * 16 + ar) * 4, o);
+    }
+}
+
+// The splits' partials of 16 queries merged in split order (attn_merge16), then the att rows
+// and their Q8_K (attn_tile_out): a workgroup per (kv head, 16-query tile).
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_fl_merge(const AttnArgs a, const StepRec *st) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int h = blockIdx.x, qa = blockIdx.y * 16, NQ = st->m * (a.n_heads / a.n_kv);
+  if (qa >= NQ) return;
+  const rsrc_t r_ml = rsrc_of(a.part_ml + ((int64_t)h * a.nslot) * ATT_QMAX * 2);
+  const rsrc_t r_o = rsrc_of(a.part_o + ((int64_t)h * a.nslot) * ATT_QMAX * HD);
+  float *ol = reinterpret_cast<float *>(smem);  // [16][HD]
+  attn_merge16<HD>(r_ml, r_o, 0, FL_SPLITS, qa, NQ, ol, nullptr, nullptr, 0);
+  __syncthreads();
+  attn_tile_out<HD>(a, h, qa, NQ, ol);
+}
+
 // ------------------------------------------------------------------ multi-tile attention
 // Passes of up to 16 rows: one workgroup of eight wavefronts per (64-position chunk, kv head,
 // eight 16-query tiles). The chunk's K / V rows go to LDS once (the pass's own rows normed and
@@ -2531,6 +2731,27 @@ static void launch_attn_pf_t(const AttnArgs &a, int m, const StepRec *st, hipStr
   SPX_LDS((k_attn_pf<HD>), sm);
   hipLaunchKernelGGL((k_attn_pf<HD>), dim3(a.nch, a.n_kv, (nq + 63) / 64), dim3(256), sm, s, a, st);
   hipLaunchKernelGGL((k_attn_pf_merge<HD>), dim3(a.n_kv, (nq + 15) / 16, (a.nch + ATT_GRP - 1) / ATT_GRP), dim3(256), (size_t)16 * HD * 4, s, a, st);
+}
+
+template <int HD>
+static void launch_attn_fl_t(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
+  const int nq = m * (a.n_heads / a.n_kv), nqb = (nq + 63) / 64, per = (a.n_kv * FL_SPLITS + 7) / 8;
+  // two halves' K / V tiles; after the walk, half 1's states (O [4][DT][4][64] + (M, L) [4][16])
+  const size_t sm = std::max((size_t)2 * ((size_t)64 * (HD + 8) + (size_t)HD * (64 + 8)) * 2, (size_t)(4 * (HD / 16) * 4 * 64 + 4 * 16 * 2) * 4);
+  SPX_LDS((k_attn_fl<HD>), sm);
+  hipLaunchKernelGGL((k_attn_fl<HD>), dim3((unsigned)(8 * nqb * per)), dim3(512), sm, s, a, st);
+  hipLaunchKernelGGL((k_attn_fl_merge<HD>), dim3(a.n_kv, (nq + 15) / 16), dim3(256), (size_t)16 * HD * 4, s, a, st);
+}
+
+hipError_t launch_attention_fl(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
+  // prepared rows only; the splits' partial slots must exist (nslot), queries fit ATT_QMAX
+  if (!a.prepped || m < 1 || m > PMAX || a.n_heads % a.n_kv || m * (a.n_heads / a.n_kv) > ATT_QMAX || a.nslot < FL_SPLITS ||
+      (a.aq.q && (a.n_heads * a.hd) % 256))
+    return hipErrorInvalidValue;
+  if (a.hd == 128) launch_attn_fl_t<128>(a, m, st, s);
+  else if (a.hd == 64) launch_attn_fl_t<64>(a, m, st, s);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 template <int HD>

@@ -2,13 +2,16 @@
 smollm_chat.rs:3090-3101) on the prefill kernels: the matvecs in 16-vector groups, the
 attention rows prepared once, MoE jobs of at most 16 users staged job by job.
 
-A row's arithmetic in these kernels is the reference's: each wavefront of a matvec contracts one
-of its eight lane classes on the int8 matrix cores and runs that class's fp32 chain (the same
-bits as the per-lane dot kernels and as one-row passes). So the bar is bitwise: hidden states,
+A row's matvec arithmetic in these kernels is the reference's: each wavefront contracts the
+reference's lane classes on the int8 matrix cores and runs their fp32 chains (the same bits as
+the per-lane dot kernels and as one-row passes). Attention is the one stage with two forms: by
+default a chunk loop with an online softmax and bits of its own (k_attn_fl, SPX_PF_ATTN=3), or
+the multi-tile kernels whose per-chunk partials and merges give a row the bits it gets in a
+verify or decode pass (SPX_PF_ATTN=2). With the latter the bar is bitwise: hidden states,
 logits, greedy picks and the KV cache of a 128-row pass equal those of the same tokens in
-passes of at most 16 rows on the lane-exact kernels. Those are held to the oracle by
-test_gpu_decode.py / test_gpu_engine.py; the prefill pass is also checked against the oracle
-directly with the bars of those tests."""
+passes of at most 16 rows on the lane kernels. The default is held to the oracle row by row on
+the GPU's own KV cache (the bars of test_gpu_engine.py), at contexts where its splits hold
+several chunks."""
 import numpy as np
 import pytest
 
@@ -59,8 +62,14 @@ def _in16(eng, ids, pos):
     return tuple(np.concatenate([o[i] for o in outs]) for i in range(3))
 
 
+@pytest.fixture
+def shared_bits(monkeypatch):
+    """Prefill attention on the multi-tile kernels: a prefill row gets its verify row's bits."""
+    monkeypatch.setenv("SPX_PF_ATTN", "2")
+
+
 @pytest.mark.parametrize("case", list(CASES))
-def test_prefill_pass_equals_16_row_passes(ctx, case):
+def test_prefill_pass_equals_16_row_passes(ctx, case, shared_bits):
     cfg = CASES[case]
     w = M.synth_model(cfg, seed=41)
     a, b = M.Engine(ctx, cfg, w), M.Engine(ctx, cfg, w)
@@ -86,7 +95,7 @@ def test_prefill_pass_equals_16_row_passes(ctx, case):
 
 
 @pytest.mark.parametrize("case", ["a3b", "moe"])
-def test_prefill_long_context(ctx, case):
+def test_prefill_long_context(ctx, case, shared_bits):
     """128-row passes past 1024 positions (17+ attention chunks, two merge levels; 128 rows x 8
     query heads = 64 query tiles a kv head) against lane-exact 16-row passes, bitwise."""
     cfg = CASES[case].replace(max_seq=1280)
@@ -109,6 +118,34 @@ def test_prefill_long_context(ctx, case):
 
 def _norm_err(x, y):
     return float(np.max(np.abs(x.astype(np.float64) - y.astype(np.float64))) / max(1.0, float(np.max(np.abs(y)))))
+
+
+@pytest.mark.parametrize("case", ["moe", "dense-kquant", "a3b"])
+@pytest.mark.parametrize("attn", ["loop", "shared"])
+def test_prefill_pass_at_context_matches_oracle(ctx, case, attn, monkeypatch):
+    """A 128-row pass at positions 256..383 (each of the chunk loop's four splits holds one or two
+    of its six chunks) against the oracle row by row on the GPU's own KV cache, as below:
+    logits median <= 1e-5, in both attention forms."""
+    monkeypatch.setenv("SPX_PF_ATTN", "3" if attn == "loop" else "2")
+    cfg = CASES[case].replace(max_seq=512)
+    w = M.synth_model(cfg, seed=43)
+    eng = M.Engine(ctx, cfg, w)
+    om = OracleModel(cfg, w)
+    ids = np.random.default_rng(11).integers(0, cfg.vocab, 384)
+    for s0 in (0, 128):
+        eng.forward(ids[s0:s0 + 128], s0)
+    _, _, lg = eng.forward(ids[256:384], 256, logits=True)
+    k, v = eng.kv_cache()
+    errs = []
+    for p in range(256, 384, 4):
+        om.k_cache[:] = k
+        om.v_cache[:] = v
+        lo = om.logits(om.forward(ids[p:p + 1], p))[0]
+        errs.append(_norm_err(lg[p - 256], lo))
+    errs = np.array(errs)
+    print(f"{case} ({attn}): logits err median {np.median(errs):.1e} max {errs.max():.1e}, rows above 1e-3: {(errs > 1e-3).sum()}")
+    assert np.median(errs) <= 1e-5
+    eng.close()
 
 
 @pytest.mark.parametrize("case", ["moe", "dense-kquant", "a3b"])
@@ -171,7 +208,7 @@ def test_prefill_without_prefill_kernels(ctx, name):
 
 
 @pytest.mark.parametrize("case", ["moe", "a3b"])
-def test_generate_with_128_row_prompt_chunks(ctx, case):
+def test_generate_with_128_row_prompt_chunks(ctx, case, shared_bits):
     """generate with feed's 128-row prompt chunks gives the stream and counts of 16-row chunks
     (the prompt's KV cache is the same bits), and the default chunk is 128."""
     cfg = CASES[case]

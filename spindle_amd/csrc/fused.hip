@@ -2179,6 +2179,50 @@ __device__ __forceinline__ bool gu_job(const GUArgs &a, int m, GUJob &j) {
   return (int)blockIdx.y < *a.njobs;
 }
 
+// The job of a gate / up workgroup: from the router's job list (gu_job), or, for one-row float
+// passes with a.rt.logits, routed here (route_row in wavefront 0; the workgroup takes the job of
+// rank blockIdx.y among the kept choices in expert order; workgroup (0, 0) publishes the
+// choices, weights, keep count, down jobs and selection counts). s_route: two LDS ints.
+// False: the workgroup has no job (every thread returns).
+__device__ __forceinline__ bool gu_job_one(const GUArgs &a, int m, bool one_row, GUJob &J, int *s_route) {
+  if (!(one_row && a.rt.logits)) return gu_job(a, m, J);
+  const F1Route &rt = a.rt;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    float lv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) lv[k] = lane + 64 * k < rt.n_expert ? rt.logits[lane + 64 * k] : -INFINITY;
+    int my_e, keep;
+    float my_p, wsum;
+    route_row(lv, rt.n_expert, rt.n_used, rt.moe_prune, my_e, my_p, keep, wsum);
+    int rank = 0;  // among the kept choices by expert index: the job order
+    for (int i = 0; i < keep; i++) rank += __shfl(my_e, i) < my_e ? 1 : 0;
+    if (lane == 0) s_route[0] = -1;
+    __builtin_amdgcn_wave_barrier();
+    if (lane < keep && rank == (int)blockIdx.y) { s_route[0] = my_e; s_route[1] = lane; }
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      if (lane < keep) {
+        rt.chosen[lane] = my_e;
+        rt.weights[lane] = rt.norm ? my_p / wsum : my_p;
+        Job &Jd = rt.jobs[rank];
+        Jd.expert = my_e;
+        Jd.nvec = 1;
+        Jd.vec[0] = lane;
+        Jd.out[0] = lane;
+        if (rt.expert_count) rt.expert_count[my_e] += 1;
+      }
+      if (lane == 0) { rt.nkeep[0] = keep; rt.njobs[0] = keep; rt.njobs[1] = keep; }
+    }
+  }
+  __syncthreads();
+  if (s_route[0] < 0) return false;
+  J.expert = s_route[0];
+  J.nvec = 1;
+  J.jv = nullptr;
+  J.jo = s_route + 1;
+  return true;
+}
+
 // Integer, eight rows per wavefront: 16 rows of h per workgroup; in each wavefront slots 0-3
 // are gate rows r..r+3 and slots 4-7 the same rows of up.
 template <int T, int MT>
@@ -2257,44 +2301,7 @@ __global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec 
   __shared__ int s_route[2];  // this workgroup's job: expert (-1: none), slot
   NormRow<4> nr;
   if (MT == 1 && a.pro.nw) nr.load(a.pro);  // (in flight during the routing)
-  if (MT == 1 && a.rt.logits) {
-    const F1Route &rt = a.rt;
-    if (threadIdx.x < 64) {
-      const int lane = threadIdx.x;
-      float lv[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) lv[k] = lane + 64 * k < rt.n_expert ? rt.logits[lane + 64 * k] : -INFINITY;
-      int my_e, keep;
-      float my_p, wsum;
-      route_row(lv, rt.n_expert, rt.n_used, rt.moe_prune, my_e, my_p, keep, wsum);
-      int rank = 0;  // among the kept choices by expert index: the job order
-      for (int i = 0; i < keep; i++) rank += __shfl(my_e, i) < my_e ? 1 : 0;
-      if (lane == 0) s_route[0] = -1;
-      __builtin_amdgcn_wave_barrier();
-      if (lane < keep && rank == (int)blockIdx.y) { s_route[0] = my_e; s_route[1] = lane; }
-      if (blockIdx.x == 0 && blockIdx.y == 0) {
-        if (lane < keep) {
-          rt.chosen[lane] = my_e;
-          rt.weights[lane] = rt.norm ? my_p / wsum : my_p;
-          Job &Jd = rt.jobs[rank];
-          Jd.expert = my_e;
-          Jd.nvec = 1;
-          Jd.vec[0] = lane;
-          Jd.out[0] = lane;
-          if (rt.expert_count) rt.expert_count[my_e] += 1;
-        }
-        if (lane == 0) { rt.nkeep[0] = keep; rt.njobs[0] = keep; rt.njobs[1] = keep; }
-      }
-    }
-    __syncthreads();
-    if (s_route[0] < 0) return;
-    J.expert = s_route[0];
-    J.nvec = 1;
-    J.jv = nullptr;
-    J.jo = &s_route[1];
-  } else if (!gu_job(a, st->m, J)) {
-    return;
-  }
+  if (!gu_job_one(a, st->m, MT == 1, J, s_route)) return;
   constexpr int D = f_depth<MT>();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
   const TensorView &w = slot < 4 ? a.gate : a.up;
@@ -2322,6 +2329,84 @@ __global__ __launch_bounds__(256) void k_gateup_f(const GUArgs a, const StepRec 
     }
   }
   if (a.hq.q) gateup_quant_tail(a, J.nvec, J.jo, 16);
+}
+
+// Gate / up + SwiGLU of one row over Q8_0 weights with k_mv_f1's arithmetic spread over the
+// wavefront (the bits of k_gateup_f's f_walk): a workgroup takes H = 16 / S h rows of one job
+// (S = 8 / RW workgroups a 16-row block), wavefronts 0-1 their gate rows, 2-3 the same up rows,
+// RW rows a wavefront, each wavefront's (row, block) items spread over its lanes with (d, dot)
+// parked in LDS, then each row's eight block chains and the 8-lane tree; the 2H results meet in
+// LDS and H lanes write silu(g) u. The job and the input row as in k_gateup_f.
+template <int NI, int RW>
+__global__ __launch_bounds__(MVF1_NW * 64) void k_gateup_f1(const GUArgs a, const StepRec *st) {
+  constexpr int S = 8 / RW, H = 2 * RW;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int s_route[2];
+  __shared__ float sgu[2][H];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nb = (int)a.gate.nb, cols = 32 * nb, ni = RW * nb, n_ff = a.n_ff;
+  float *lx = reinterpret_cast<float *>(smem);
+  float2 *ldd = reinterpret_cast<float2 *>(smem + (size_t)cols * 4) + (size_t)wave * ni;  // (d, dot) [row][block]
+  NormRow<MVF1_NW> nr;
+  if (a.pro.nw) nr.load(a.pro);  // (in flight during the routing)
+  GUJob J;
+  if (!gu_job_one(a, st->m, true, J, s_route)) return;
+  const int half = wave >> 1, sub = (int)blockIdx.x % S, blk = (int)blockIdx.x / S;
+  const int64_t hr0 = (int64_t)blk * 16 + sub * H + (wave & 1) * RW;  // this wavefront's first h row
+  const TensorView &w = half ? a.up : a.gate;
+  const int64_t ebase = (int64_t)J.expert * w.rows;
+  uint4 c0[NI], c1[NI];
+  uint32_t dh[NI];
+#pragma unroll
+  for (int k = 0; k < NI; k++) {
+    const int i = min(lane + 64 * k, ni - 1), r = i / nb, b = i - r * nb;
+    const int64_t g = (ebase + min(hr0 + r, (int64_t)n_ff - 1)) * nb + b;
+    c0[k] = ld16(w.pl.p0 + g * 32);
+    c1[k] = ld16(w.pl.p0 + g * 32 + 16);
+    dh[k] = *reinterpret_cast<const uint16_t *>(w.pl.p3 + g * 2);
+  }
+  if (a.pro.nw) {
+    nr.finish(a.pro, lx, nullptr);
+  } else {
+    for (int i = threadIdx.x; i < cols / 4; i += MVF1_NW * 64) reinterpret_cast<float4 *>(lx)[i] = reinterpret_cast<const float4 *>(a.x)[i];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < NI; k++) {
+    const int i = lane + 64 * k;
+    if (i < ni) {
+      const int b = i % nb;
+      const float4 *xv = reinterpret_cast<const float4 *>(lx + 32 * b);
+      const uint32_t cw[8] = {c0[k].x, c0[k].y, c0[k].z, c0[k].w, c1[k].x, c1[k].y, c1[k].z, c1[k].w};
+      float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+      for (int kk = 0; kk < 8; kk++) {
+        const float4 xx = xv[kk];
+        s0 = fmaf((float)(int8_t)(cw[kk]), xx.x, s0);
+        s1 = fmaf((float)(int8_t)(cw[kk] >> 8), xx.y, s1);
+        s2 = fmaf((float)(int8_t)(cw[kk] >> 16), xx.z, s2);
+        s3 = fmaf((float)(int8_t)(cw[kk] >> 24), xx.w, s3);
+      }
+      ldd[i] = make_float2(h2f(dh[k]), (s0 + s1) + (s2 + s3));
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the items are parked
+  __builtin_amdgcn_wave_barrier();
+  const int r = lane >> 3, l = lane & 7;
+  float acc = 0.0f;
+  if (r < RW)
+    for (int b = l; b < nb; b += 8) {
+      const float2 e = ldd[r * nb + b];
+      acc = fmaf(e.x, e.y, acc);
+    }
+  const float res = hsum_rows8(acc);
+  if (r < RW && l == 0) sgu[half][(wave & 1) * RW + r] = res;
+  __syncthreads();
+  if ((int)threadIdx.x < H) {
+    const int64_t row = (int64_t)blk * 16 + sub * H + threadIdx.x;
+    const float x = sgu[0][threadIdx.x], u = sgu[1][threadIdx.x];
+    if (row < n_ff) st_dev(a.h + (int64_t)(J.jo ? J.jo[0] : 0) * n_ff + row, x / (1.0f + expf(-x)) * u);
+  }
 }
 
 // Gate / up + SwiGLU of 2..16 rows on the fp32 matrix cores (Q8_0), dense or one routed expert's
@@ -2808,6 +2893,15 @@ hipError_t launch_router(const RouterArgs &a, int mt, const StepRec *st, hipStre
   return hipGetLastError();
 }
 
+// one-row Q8_0 gate / up on k_gateup_f1 (SPX_GU_F1=0: k_gateup_f, the same bits)
+static bool gu_f1_on() {
+  static const bool on = [] {
+    const char *v = std::getenv("SPX_GU_F1");
+    return !v || atoi(v) != 0;
+  }();
+  return on;
+}
+
 template <int T, int MT>
 static hipError_t launch_gu_t(const GUArgs &a, int mode, const StepRec *st, int max_jobs, hipStream_t s) {
   const unsigned jobs = (unsigned)std::max(1, max_jobs);
@@ -2824,6 +2918,27 @@ static hipError_t launch_gu_t(const GUArgs &a, int mode, const StepRec *st, int 
     hipLaunchKernelGGL((k_gateup_kq<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256), sm, s, a, st);
   } else if (T == T_Q8_0 && MT >= 4 && a.fq) {
     hipLaunchKernelGGL(k_gateup_fq, dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(1024), 0, s, a, st);
+  } else if (T == T_Q8_0 && MT == 1 && !a.hq.q && a.gate.nb <= 128 && gu_f1_on()) {
+    // one row: k_gateup_f1, RW rows a wavefront (fewer for more workgroups, up to 2 a CU)
+    const int blocks = (a.n_ff + 15) / 16, nb = (int)a.gate.nb;
+    int rw = 8;
+    while (rw > 1 && (int64_t)blocks * jobs * (8 / rw) < 2 * cu_count_f()) rw >>= 1;
+    const int ni = (rw * nb + 63) / 64;
+    const size_t sm = (size_t)32 * nb * 4 + (size_t)MVF1_NW * rw * nb * 8;
+    const dim3 g((unsigned)(blocks * (8 / rw)), jobs), b(MVF1_NW * 64);
+    auto go = [&](auto kern) {
+      SPX_LDS(kern, sm);
+      hipLaunchKernelGGL(kern, g, b, sm, s, a, st);
+      return hipGetLastError();
+    };
+    auto by_ni = [&](auto RWc) {
+      constexpr int RW = decltype(RWc)::value;
+      return ni <= 2 ? go(k_gateup_f1<2, RW>) : ni <= 4 ? go(k_gateup_f1<4, RW>) : ni <= 8 ? go(k_gateup_f1<8, RW>) : go(k_gateup_f1<16, RW>);
+    };
+    if (rw == 8) return by_ni(std::integral_constant<int, 8>{});
+    if (rw == 4) return by_ni(std::integral_constant<int, 4>{});
+    if (rw == 2) return by_ni(std::integral_constant<int, 2>{});
+    return by_ni(std::integral_constant<int, 1>{});
   } else {
     hipLaunchKernelGGL((k_gateup_f<T, MT>), dim3((unsigned)((a.n_ff + 15) / 16), jobs), dim3(256),
                        MT == 1 && a.pro.nw ? (size_t)a.gate.cols * 4 : 0, s, a, st);

@@ -76,7 +76,7 @@ struct spx_engine {
   int mq_rows[MQ_KINDS] = {6, 12, 5, 12, 4};
   bool mq_shapes = true;   // every K-quant matrix's blocks-a-row count is one the matrix-core kernels take (dec_mq_nb_ok)
   int mv_mode = -1, lm_mode = -1, tail_max = 2, down_mode = 0;  // launch-shape overrides (SPX_MV_MODE, SPX_LM_MODE, SPX_TAIL_MAX, SPX_DOWN_MODE)
-  int pf_attn = 3;          // prefill passes: 3 k_rows_prep + the chunk loop (k_attn_fl: bits of its own), 2 the multi-tile
+  int pf_attn = 4;          // prefill passes: 4 K / V rows prepared + the position slices (k_attn_fs: bits of its own, no partials), 3 the chunk loop (k_attn_fl), 2 the multi-tile
                             // kernels (the bits verify and decode rows get; at least 2 query heads a kv head), 1 k_rows_prep +
                             // k_attn_pf + merge, 0 k_rows_prep + k_attn (SPX_PF_ATTN)
   int pf_min_rows = MAX_M + 1;  // passes of this many rows or more prepare their attention rows once (SPX_PF_MIN)
@@ -724,13 +724,19 @@ int enqueue_pass_m(spx_engine *E, int m) {
       aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
       aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
       aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
-      if (m >= E->pf_min_rows && E->pf_attn == 3 && m > MAX_M && (hd == 64 || hd == 128)) {
-        // rows prepared once, then the chunk loop with bits of its own (prefill rows share no
+      if (m >= E->pf_min_rows && E->pf_attn >= 3 && m > MAX_M && (hd == 64 || hd == 128)) {
+        // rows prepared once, then a chunk loop with bits of its own (prefill rows share no
         // bits with verify rows: a row's attention differs from its 16-row pass's in the last bits)
-        SPX_HIP(launch_rows_prep(aa, E->qp, m, E->st_dev, s));
-        aa.q = E->qp;
-        aa.prepped = 1;
-        SPX_HIP(launch_attention_fl(aa, m, E->st_dev, s));
+        if (E->pf_attn == 4) {  // K / V rows prepared, the queries in the attention kernel
+          SPX_HIP(launch_rows_prep(aa, nullptr, m, E->st_dev, s));
+          aa.prepped = 2;
+          SPX_HIP(launch_attention_fs(aa, m, E->st_dev, s));
+        } else {
+          SPX_HIP(launch_rows_prep(aa, E->qp, m, E->st_dev, s));
+          aa.q = E->qp;
+          aa.prepped = 1;
+          SPX_HIP(launch_attention_fl(aa, m, E->st_dev, s));
+        }
       } else if (m >= E->pf_min_rows && E->pf_attn >= 2 && m > MAX_M && c.n_heads / c.n_kv_heads >= 2 &&
           (!ly.q_bias || (c.n_heads / c.n_kv_heads) * hd <= 2048)) {
         SPX_HIP(launch_attention_mt(aa, m, E->st_dev, s));
@@ -962,7 +968,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   if (const char *v = std::getenv("SPX_TAIL_MAX")) E->tail_max = std::max(0, std::min(MAX_M, atoi(v)));
   if (const char *v = std::getenv("SPX_DOWN_MODE")) E->down_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_ATT_MERGE")) E->att_merge = atoi(v) != 0;
-  if (const char *v = std::getenv("SPX_PF_ATTN")) E->pf_attn = std::max(0, std::min(3, atoi(v)));
+  if (const char *v = std::getenv("SPX_PF_ATTN")) E->pf_attn = std::max(0, std::min(4, atoi(v)));
   if (const char *v = std::getenv("SPX_ATT_MT")) E->att_mt_min = std::max(0, std::min(MAX_M + 1, atoi(v)));
   if (const char *v = std::getenv("SPX_PF_MIN")) E->pf_min_rows = std::max(2, std::min(MAX_M + 1, atoi(v)));
   *out = E;

@@ -96,7 +96,8 @@ struct AttnArgs {
   int nch;                            // chunks launched per kv head (>= max_seq / 64)
   int nslot;                          // partial slots per kv head: nch chunks, then group partials
   // 1: q holds the prepared queries (bias, norm, RoPE applied) and the pass's K / V rows are in
-  // the cache already (launch_rows_prep); multi-row passes only
+  // the cache already (launch_rows_prep); 2: the K / V rows are in the cache, q holds the raw
+  // projections (launch_attention_fs only); multi-row passes only
   int prepped;
   float eps, scale;
 };
@@ -185,13 +186,19 @@ hipError_t launch_embed(const TensorView &e, const StepRec *st, float escale, co
 hipError_t launch_mv(const MVArgs &a, int mt, int mode, const StepRec *st, int grid, hipStream_t s);
 hipError_t launch_attention(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);
 // The attention block's row preparation of the step record's pass of m rows (bias, per-head RMSNorm and RoPE of
-// q and k, as the attention kernel does it): prepared queries to qp [m][q_dim], K / V rows to
-// the cache (f16 RNE); then launch_attention with a.prepped = 1 reads them from there
+// q and k, as the attention kernel does it): prepared queries to qp [m][q_dim] (qp null: none),
+// K / V rows to the cache (f16 RNE); then launch_attention with a.prepped = 1 reads them from there
 hipError_t launch_rows_prep(const AttnArgs &a, float *qp, int m, const StepRec *st, hipStream_t s);
 // Prefill attention with bits of its own (rows prepared by launch_rows_prep, a.prepped = 1): a
 // chunk loop per (kv head, 64 queries, one of four splits of the chunks) with an online softmax,
 // then the splits merged in order into the att rows (and their Q8_K when a.aq is set).
 hipError_t launch_attention_fl(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);
+// Prefill attention with bits of its own and no partials in memory (the pass's K / V rows put in
+// the cache by launch_rows_prep; a.prepped 1: prepared queries in q, 2: raw projections, prepared
+// here): a workgroup per (kv head, 16 queries), each wavefront an online softmax over every
+// eighth 32-position slice of the positions they see, the eight states merged in LDS into the
+// att rows (and their Q8_K when a.aq is set).
+hipError_t launch_attention_fs(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);
 // The same attention for prepared rows as partials (a workgroup per chunk, kv head and four
 // query tiles, a wavefront per tile) and a merge launch: each output has launch_attention's bits
 hipError_t launch_attention_pf(const AttnArgs &a, int m, const StepRec *st, hipStream_t s);

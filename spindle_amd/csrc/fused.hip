@@ -1274,6 +1274,25 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(const AttnArgs a, const S
 // workgroups of one (kv head, split) run on one XCD (workgroup i on XCD i mod 8), so its
 // chunks' K / V come from HBM about once for all its query blocks.
 constexpr int FL_SPLITS = 4;
+// Prepared query qi of kv head h (g queries a row) as hi + lo f16 matrix-core operands: dims
+// 16 kt + kg .. + 3 (a query past the pass: zeros)
+template <int HD>
+__device__ __forceinline__ void fl_queries(const AttnArgs &a, int h, int g, int qi, bool qact, int kg, h4v (&qhi)[HD / 16], h4v (&qlo)[HD / 16]) {
+  const int qb_row = qact ? qi / g : 0, qhead = qact ? qi % g : 0;
+  const float *src = a.q + (int64_t)qb_row * a.n_heads * HD + (h * g + qhead) * HD + kg;
+#pragma unroll
+  for (int kt = 0; kt < HD / 16; kt++) {
+    const float4 x = *reinterpret_cast<const float4 *>(src + kt * 16);
+    const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++) {
+      _Float16 hh, ll;
+      split_f16(qact ? xs[s4] : 0.0f, hh, ll);
+      qhi[kt][s4] = hh;
+      qlo[kt][s4] = ll;
+    }
+  }
+}
 template <int HD>
 __global__ __launch_bounds__(512) void k_attn_fl(const AttnArgs a, const StepRec *st) {
   constexpr int KS = HD + 8, VS = 64 + 8, DT = HD / 16, DQ = HD / 4, NU = DQ / 8;
@@ -1304,22 +1323,7 @@ __global__ __launch_bounds__(512) void k_attn_fl(const AttnArgs a, const StepRec
   if (nstep > 0) kv_load(c0 + hf);
   // the queries (prepared rows), hi + lo f16 operands: lane holds query ar, dims 16 kt + kg ..
   h4v qhi[DT], qlo[DT];
-  {
-    const int qb_row = qact ? qi / g : 0, qhead = qact ? qi % g : 0;
-    const float *src = a.q + (int64_t)qb_row * a.n_heads * HD + (h * g + qhead) * HD + kg;
-#pragma unroll
-    for (int kt = 0; kt < DT; kt++) {
-      const float4 x = *reinterpret_cast<const float4 *>(src + kt * 16);
-      const float xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-      for (int s4 = 0; s4 < 4; s4++) {
-        _Float16 hh, ll;
-        split_f16(qact ? xs[s4] : 0.0f, hh, ll);
-        qhi[kt][s4] = hh;
-        qlo[kt][s4] = ll;
-      }
-    }
-  }
+  fl_queries<HD>(a, h, g, qi, qact, kg, qhi, qlo);
   const int lim = qact ? start + qi / g + 1 : 0;  // positions < lim are visible to query ar
   float Mq = -INFINITY, Lq = 0.0f;                // running max and sum of query ar
   f4v acc[DT];                                    // O: query kg + r, dim 16 dt + ar
@@ -1458,6 +1462,252 @@ __global__ __launch_bounds__(256) void k_attn_fl_merge(const AttnArgs a, const S
   attn_merge16<HD>(r_ml, r_o, 0, FL_SPLITS, qa, NQ, ol, nullptr, nullptr, 0);
   __syncthreads();
   attn_tile_out<HD>(a, h, qa, NQ, ol);
+}
+
+// ------------------------------------------------------------------ prefill attention, position slices
+// Prefill passes (rows prepared by k_rows_prep) with attention bits of their own and no partials
+// in memory: a workgroup of eight wavefronts per (kv head, block of 16 queries). Wavefront w
+// takes the 32-position slices w, w + 8, w + 16, ... of the positions its queries see (each
+// workgroup starting at its own place in that list) and keeps
+// an online softmax over them in registers, with no LDS and no barrier until the end: per slice
+// S^T = K Q^T as two 16-position tiles and P V over the 32 positions, on the K = 32 f16 matrix
+// cores (v_mfma_f32_16x16x32_f16; queries and probabilities as hi + lo f16, products exact in
+// fp32), the slice's max, M' = max(M, m_s), p = exp(s - M'), O = O exp(M - M') + P V,
+// L = L exp(M - M') + sum p. The slice's K rows and V columns go from memory straight into the
+// operand layouts (the next slice's loads in flight during the softmax and P V): the contraction
+// dims are permuted alike in K and Q (lane group kq holds dims 32 u + 8 kq .. + 7 of step u: a
+// 16-byte piece of a K row per load), the positions alike in P and V (lane group kq holds
+// positions 16 t + 4 kq + r, r < 4, of tile t: the rows of S^T it holds), and P V's output
+// columns are dims DT x + t (lane x holds DT consecutive dims of each of its eight V rows: four
+// whole 256-byte rows per load). The eight states then meet in LDS (M = max M_w,
+// w_w = exp(M_w - M), L = sum L_w w_w, O = sum w_w O_w, wavefronts in order) and O / L goes to
+// the att rows (and their Q8_K). Workgroup i runs on XCD i mod 8, and XCD x takes the
+// (kv head, block) units x P .. x P + P - 1 (kv head major): a kv head's blocks share one or two
+// L2s.
+__device__ __forceinline__ uint32_t word_of(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+__device__ __forceinline__ uint32_t word_of(const uint2 &v, int i) { return i == 0 ? v.x : v.y; }
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f4v mfma32h(h8v a, h8v b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+template <int HD>
+__global__ __launch_bounds__(512) void k_attn_fs(const AttnArgs a, const StepRec *st) {
+  constexpr int DT = HD / 16, NPC = HD / 32;  // output tiles (dims a lane's column holds), K pieces a lane
+  using VRow = typename std::conditional<DT == 8, uint4, uint2>::type;  // DT f16 of one V row
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int m = st->m, start = st->start, total = start + m;
+  const int g = a.n_heads / a.n_kv, NQ = m * g, nqb = (NQ + 15) >> 4;
+  const int u = (int)(blockIdx.x & 7) * (int)(gridDim.x >> 3) + (int)(blockIdx.x >> 3);
+  if (u >= a.n_kv * nqb) return;
+  const int h = u / nqb, qa = (u - h * nqb) * 16;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ar = lane & 15, kq = lane >> 4, kg = 4 * kq;
+  const int qi = qa + ar;
+  const bool qact = qi < NQ;
+  const int p_end = start + (min(NQ, qa + 16) - 1) / g + 1;  // positions any of the block's queries sees
+  const int nsl = (p_end + 31) >> 5, nstep = wave < nsl ? (nsl - wave + 7) >> 3 : 0;
+  const __half *kc = a.kc + (int64_t)a.layer * a.max_seq * a.kv_dim + (int64_t)h * HD;
+  const __half *vc = a.vc + (int64_t)a.layer * a.max_seq * a.kv_dim + (int64_t)h * HD;
+  // slice i's rows as this lane takes them (rows past the pass: the last row, masked)
+  uint4 kr[2][NPC];
+  VRow vr[2][4];
+  auto kv_load = [&](int i) {
+    const int p0 = min(i, nsl - 1) * 32;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const __half *kp = kc + (int64_t)min(p0 + 16 * t + ar, total - 1) * a.kv_dim + 8 * kq;
+#pragma unroll
+      for (int uu = 0; uu < NPC; uu++) kr[t][uu] = *reinterpret_cast<const uint4 *>(kp + 32 * uu);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        vr[t][r] = *reinterpret_cast<const VRow *>(vc + (int64_t)min(p0 + 16 * t + kg + r, total - 1) * a.kv_dim + DT * ar);
+  };
+  // the workgroups of a kv head start their walks at different slices (rot), so the CUs of an
+  // XCD read different lines of its K / V at a time
+  const int rot = nstep > 0 ? (u - h * nqb) % nstep : 0;
+  if (nstep > 0) kv_load(wave + 8 * rot);
+  // the queries as hi + lo f16 operands, dims permuted as K's: step uu takes dims 32 uu + 8 kq ..
+  // + 7. a.prepped 2: from the raw projections, with head_prep's operations here (bias; RMSNorm,
+  // the sum of squares over the lane's 32 dims then the query's four lanes; RoPE, whose pairs
+  // (d, d + HD / 2) or (2 i, 2 i + 1) a lane holds both halves of); 1: prepared rows
+  h8v qhi[NPC], qlo[NPC];
+  {
+    const int qb_row = qact ? qi / g : 0, qhead = h * g + (qact ? qi % g : 0);
+    const float *src = a.q + (int64_t)qb_row * a.n_heads * HD + qhead * HD + 8 * kq;
+    float x[NPC][8];
+#pragma unroll
+    for (int uu = 0; uu < NPC; uu++) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(src + 32 * uu), x1 = *reinterpret_cast<const float4 *>(src + 32 * uu + 4);
+      x[uu][0] = x0.x; x[uu][1] = x0.y; x[uu][2] = x0.z; x[uu][3] = x0.w;
+      x[uu][4] = x1.x; x[uu][5] = x1.y; x[uu][6] = x1.z; x[uu][7] = x1.w;
+    }
+    if (a.prepped == 2) {
+      if (a.q_bias) {
+        const float *bp = a.q_bias + qhead * HD + 8 * kq;
+#pragma unroll
+        for (int uu = 0; uu < NPC; uu++)
+#pragma unroll
+          for (int j = 0; j < 8; j++) x[uu][j] += bp[32 * uu + j];
+      }
+      if (a.q_norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int uu = 0; uu < NPC; uu++)
+#pragma unroll
+          for (int j = 0; j < 8; j++) ss = fmaf(x[uu][j], x[uu][j], ss);
+        ss = add16(ss);
+        ss = add32(ss);
+        const float inv = inv_rms(ss, (float)HD, a.eps);
+        const float *nw = a.q_norm + 8 * kq;
+#pragma unroll
+        for (int uu = 0; uu < NPC; uu++)
+#pragma unroll
+          for (int j = 0; j < 8; j++) x[uu][j] = x[uu][j] * inv * nw[32 * uu + j];
+      }
+      const float2 *rp = a.rope + (int64_t)(start + qb_row) * (HD / 2);
+      if (a.neox) {
+#pragma unroll
+        for (int uu = 0; uu < NPC / 2; uu++)
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const float2 cs = rp[32 * uu + 8 * kq + j];
+            const float x0 = x[uu][j], x1 = x[uu + NPC / 2][j];
+            x[uu][j] = x0 * cs.x - x1 * cs.y;
+            x[uu + NPC / 2][j] = x0 * cs.y + x1 * cs.x;
+          }
+      } else {
+#pragma unroll
+        for (int uu = 0; uu < NPC; uu++)
+#pragma unroll
+          for (int j = 0; j < 8; j += 2) {
+            const float2 cs = rp[16 * uu + 4 * kq + j / 2];
+            const float x0 = x[uu][j], x1 = x[uu][j + 1];
+            x[uu][j] = x0 * cs.x - x1 * cs.y;
+            x[uu][j + 1] = x0 * cs.y + x1 * cs.x;
+          }
+      }
+    }
+#pragma unroll
+    for (int uu = 0; uu < NPC; uu++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        _Float16 hh, ll;
+        split_f16(qact ? x[uu][j] : 0.0f, hh, ll);
+        qhi[uu][j] = hh;
+        qlo[uu][j] = ll;
+      }
+  }
+  const int lim = qact ? start + qi / g + 1 : 0;  // positions < lim are visible to query ar
+  float Mq = -INFINITY, Lq = 0.0f;                // running max and sum of query ar over the slices
+  f4v acc[DT];                                    // O: query kg + r, dim DT ar + dt
+#pragma unroll
+  for (int dt = 0; dt < DT; dt++) acc[dt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int step = 0, sr = rot; step < nstep; step++, sr = sr + 1 == nstep ? 0 : sr + 1) {
+    const int i = wave + 8 * sr, p0 = 32 * i;
+    // scores: sacc[t][r] = S[query ar][position p0 + 16 t + kg + r]
+    f4v sacc[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      sacc[t] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int uu = 0; uu < NPC; uu++) {
+        const h8v bk = __builtin_bit_cast(h8v, kr[t][uu]);
+        sacc[t] = mfma32h(bk, qhi[uu], sacc[t]);
+        sacc[t] = mfma32h(bk, qlo[uu], sacc[t]);
+      }
+    }
+    // V columns of this lane: vv[dt] element 4 t + r = V[p0 + 16 t + kg + r][DT ar + dt]
+    h8v vv[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) {
+      // (v_perm_b32: the low or high halves of two rows' words side by side)
+      const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
+      uint32_t e[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        e[j] = __builtin_amdgcn_perm(word_of(vr[j >> 1][2 * (j & 1) + 1], dt >> 1), word_of(vr[j >> 1][2 * (j & 1)], dt >> 1), sel);
+      vv[dt] = __builtin_bit_cast(h8v, make_uint4(e[0], e[1], e[2], e[3]));
+    }
+    if (step + 1 < nstep) kv_load(wave + 8 * (sr + 1 == nstep ? 0 : sr + 1));
+    float sv[2][4], mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        sv[t][r] = p0 + 16 * t + kg + r < lim ? sacc[t][r] * a.scale : -INFINITY;
+        mx = fmaxf(mx, sv[t][r]);
+      }
+    mx = max16(mx);
+    mx = max32(mx);
+    const float Mn = fmaxf(Mq, mx);
+    const float al = Mq == -INFINITY ? 0.0f : expf(Mq - Mn);  // (nothing accumulated yet: O, L are 0)
+    float pv[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) pv[t][r] = sv[t][r] == -INFINITY ? 0.0f : expf(sv[t][r] - Mn);
+    float ls = ((pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3])) + ((pv[1][0] + pv[1][1]) + (pv[1][2] + pv[1][3]));
+    ls = add16(ls);
+    ls = add32(ls);
+    Lq = fmaf(Lq, al, ls);
+    Mq = Mn;
+    // O rows are queries kg + r: their factors from lanes kg + r (query ar = kg + r)
+    float alr[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) alr[r] = __shfl(al, kg + r, 64);
+    h8v phv, plv;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        _Float16 hh, ll;
+        split_f16(pv[t][r], hh, ll);
+        phv[4 * t + r] = hh;
+        plv[4 * t + r] = ll;
+      }
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) {
+      f4v o = acc[dt];
+#pragma unroll
+      for (int r = 0; r < 4; r++) o[r] = o[r] * alr[r];
+      o = mfma32h(phv, vv[dt], o);
+      o = mfma32h(plv, vv[dt], o);
+      acc[dt] = o;
+    }
+  }
+  // the eight states to LDS, merged per (query, dim) in wavefront order
+  float *xo = reinterpret_cast<float *>(smem);  // [8 waves][DT][4][64]
+  float *xm = xo + 8 * DT * 4 * 64;             // [8 waves][16][2]
+  float *ol = xm + 8 * 16 * 2;                  // [16][HD]
+#pragma unroll
+  for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) xo[((wave * DT + dt) * 4 + r) * 64 + lane] = acc[dt][r];
+  if (kq == 0) { xm[(wave * 16 + ar) * 2] = Mq; xm[(wave * 16 + ar) * 2 + 1] = Lq; }
+  __syncthreads();
+  {
+    constexpr int DW = HD / 32;  // 32 threads a query, DW dims each
+    const int qq = tid >> 5, d0 = (tid & 31) * DW, src_lane = 16 * (qq >> 2), r = qq & 3;
+    float mw[8], ww[8], M = -INFINITY, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 8; w++) { mw[w] = xm[(w * 16 + qq) * 2]; M = fmaxf(M, mw[w]); }
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+      ww[w] = mw[w] == -INFINITY ? 0.0f : expf(mw[w] - M);
+      L = fmaf(xm[(w * 16 + qq) * 2 + 1], ww[w], L);
+    }
+    const float il = __fdiv_rn(1.0f, fmaxf(L, 1e-30f));
+#pragma unroll
+    for (int j = 0; j < DW; j++) {
+      const int d = d0 + j, dt = d % DT, x = d / DT;  // dim d = DT x + dt: tile dt, column x
+      float o = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 8; w++) o = fmaf(xo[((w * DT + dt) * 4 + r) * 64 + src_lane + x], ww[w], o);
+      ol[qq * HD + d] = o * il;
+    }
+  }
+  __syncthreads();
+  if (tid < 256) attn_tile_out<HD>(a, h, qa, NQ, ol);
 }
 
 // ------------------------------------------------------------------ multi-tile attention
@@ -1920,7 +2170,7 @@ __global__ __launch_bounds__(1024) void k_attn_mrg(const AttnArgs a, const StepR
 // are the queries (head_prep -> qp), then the n_kv keys (head_prep -> f16 RNE -> K cache) and
 // the n_kv values (bias -> f16 -> V cache), the same operations as attn_item makes on them.
 __global__ __launch_bounds__(64) void k_rows_prep(const AttnArgs a, float *qp, const StepRec *st) {
-  const int b = blockIdx.x, j = blockIdx.y, lane = threadIdx.x & 63, hd = a.hd, half = hd >> 1;
+  const int b = blockIdx.x, j = blockIdx.y + (qp ? 0 : a.n_heads), lane = threadIdx.x & 63, hd = a.hd, half = hd >> 1;
   if (b >= st->m) return;
   const int pos = st->start + b;
   const int da = a.neox ? lane : 2 * lane, db = a.neox ? lane + half : 2 * lane + 1;
@@ -2840,6 +3090,27 @@ hipError_t launch_attention_fl(const AttnArgs &a, int m, const StepRec *st, hipS
 }
 
 template <int HD>
+static void launch_attn_fs_t(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
+  const int nqb = (m * (a.n_heads / a.n_kv) + 15) / 16, per = (a.n_kv * nqb + 7) / 8;
+  // the eight states (O [8][DT][4][64] + (M, L) [8][16]) and the merged outputs [16][HD]
+  const size_t sm = (size_t)(8 * (HD / 16) * 4 * 64 + 8 * 16 * 2 + 16 * HD) * 4;
+  SPX_LDS((k_attn_fs<HD>), sm);
+  hipLaunchKernelGGL((k_attn_fs<HD>), dim3((unsigned)(8 * per)), dim3(512), sm, s, a, st);
+}
+
+hipError_t launch_attention_fs(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
+  // the pass's K / V rows in the cache (prepped 1: prepared queries, 2: raw); a 256-value block of
+  // the att rows' Q8_K holds 256 / hd queries of one row
+  if (a.prepped < 1 || a.prepped > 2 || m < 1 || m > PMAX || a.n_heads % a.n_kv ||
+      (a.aq.q && ((a.n_heads * a.hd) % 256 || (a.n_heads / a.n_kv) % (256 / a.hd))))
+    return hipErrorInvalidValue;
+  if (a.hd == 128) launch_attn_fs_t<128>(a, m, st, s);
+  else if (a.hd == 64) launch_attn_fs_t<64>(a, m, st, s);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+template <int HD>
 static void launch_attn_mt_t(const AttnArgs &a, int m, const StepRec *st, hipStream_t s) {
   const int g = a.n_heads / a.n_kv, nqt = (m * g + 15) / 16;
   const size_t sm = MtLds<HD>::bytes(g, a.q_bias != nullptr, m);
@@ -2876,8 +3147,8 @@ hipError_t launch_attention_pf(const AttnArgs &a, int m, const StepRec *st, hipS
 }
 
 hipError_t launch_rows_prep(const AttnArgs &a, float *qp, int m, const StepRec *st, hipStream_t s) {
-  if (m < 1 || m > PMAX || (a.hd != 64 && a.hd != 128) || !qp) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_rows_prep, dim3(m, a.n_heads + 2 * a.n_kv), dim3(64), 0, s, a, qp, st);
+  if (m < 1 || m > PMAX || (a.hd != 64 && a.hd != 128)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rows_prep, dim3(m, (qp ? a.n_heads : 0) + 2 * a.n_kv), dim3(64), 0, s, a, qp, st);
   return hipGetLastError();
 }
 

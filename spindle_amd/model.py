@@ -393,6 +393,14 @@ class Engine:
             out[name] = a.view(np.int32).copy() if name in ("chosen", "nkeep") else a.copy()
         return out
 
+    def debug_buf(self, name, n):
+        """n float32 values of an engine work buffer after the last pass (synchronised): 'q', 'k',
+        'v' (the last layer's raw projections [m, q_dim | kv_dim]), 'att' (its attention rows),
+        'x', 'xn', 'proj', ..."""
+        buf = np.empty(n, np.float32)
+        check(lib.spx_engine_debug_read(self.h, name.encode(), buf.ctypes.data_as(P), buf.nbytes))
+        return buf
+
     def last_experts(self):
         out = np.empty(self.cfg.n_layers, np.int32)
         check(lib.spx_engine_last_experts(self.h, out.ctypes.data_as(P)))

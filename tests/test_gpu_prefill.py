@@ -4,14 +4,15 @@ attention rows prepared once, MoE jobs of at most 16 users staged job by job.
 
 A row's matvec arithmetic in these kernels is the reference's: each wavefront contracts the
 reference's lane classes on the int8 matrix cores and runs their fp32 chains (the same bits as
-the per-lane dot kernels and as one-row passes). Attention is the one stage with two forms: by
-default a chunk loop with an online softmax and bits of its own (k_attn_fl, SPX_PF_ATTN=3), or
-the multi-tile kernels whose per-chunk partials and merges give a row the bits it gets in a
-verify or decode pass (SPX_PF_ATTN=2). With the latter the bar is bitwise: hidden states,
-logits, greedy picks and the KV cache of a 128-row pass equal those of the same tokens in
-passes of at most 16 rows on the lane kernels. The default is held to the oracle row by row on
-the GPU's own KV cache (the bars of test_gpu_engine.py), at contexts where its splits hold
-several chunks."""
+the per-lane dot kernels and as one-row passes). Attention is the one stage with several forms:
+by default position slices with online softmaxes merged in LDS and bits of their own (k_attn_fs,
+SPX_PF_ATTN=4), the chunk loop with split partials (k_attn_fl, 3), or the multi-tile kernels
+whose per-chunk partials and merges give a row the bits it gets in a verify or decode pass
+(SPX_PF_ATTN=2). With the latter the bar is bitwise: hidden states, logits, greedy picks and the
+KV cache of a 128-row pass equal those of the same tokens in passes of at most 16 rows on the
+lane kernels. The others are held to the oracle row by row on the GPU's own KV cache (the bars
+of test_gpu_engine.py), at contexts of several chunks, and their attention stage directly
+against the oracle's attention of the same raw rows."""
 import numpy as np
 import pytest
 
@@ -120,13 +121,16 @@ def _norm_err(x, y):
     return float(np.max(np.abs(x.astype(np.float64) - y.astype(np.float64))) / max(1.0, float(np.max(np.abs(y)))))
 
 
+PF_ATTN = {"slices": "4", "loop": "3", "shared": "2"}
+
+
 @pytest.mark.parametrize("case", ["moe", "dense-kquant", "a3b"])
-@pytest.mark.parametrize("attn", ["loop", "shared"])
+@pytest.mark.parametrize("attn", list(PF_ATTN))
 def test_prefill_pass_at_context_matches_oracle(ctx, case, attn, monkeypatch):
     """A 128-row pass at positions 256..383 (each of the chunk loop's four splits holds one or two
     of its six chunks) against the oracle row by row on the GPU's own KV cache, as below:
-    logits median <= 1e-5, in both attention forms."""
-    monkeypatch.setenv("SPX_PF_ATTN", "3" if attn == "loop" else "2")
+    logits median <= 1e-5, in every attention form."""
+    monkeypatch.setenv("SPX_PF_ATTN", PF_ATTN[attn])
     cfg = CASES[case].replace(max_seq=512)
     w = M.synth_model(cfg, seed=43)
     eng = M.Engine(ctx, cfg, w)
@@ -145,6 +149,37 @@ def test_prefill_pass_at_context_matches_oracle(ctx, case, attn, monkeypatch):
     errs = np.array(errs)
     print(f"{case} ({attn}): logits err median {np.median(errs):.1e} max {errs.max():.1e}, rows above 1e-3: {(errs > 1e-3).sum()}")
     assert np.median(errs) <= 1e-5
+    eng.close()
+
+
+@pytest.mark.parametrize("case", ["a3b", "dense-kquant"])
+@pytest.mark.parametrize("attn", list(PF_ATTN))
+def test_prefill_attention_matches_oracle(ctx, case, attn, monkeypatch):
+    """The attention stage of a 128-row pass at positions 384..511 (eight chunks: four steps of
+    each half's walk, two chunks of each split) against the oracle's attention of the same raw
+    q / k / v rows on the GPU's own KV cache (the last layer's buffers after the pass): every
+    row within 1e-4 (max-abs normalised, the layer pins' attention bar), in every attention form."""
+    monkeypatch.setenv("SPX_PF_ATTN", PF_ATTN[attn])
+    cfg = CASES[case].replace(max_seq=512)
+    w = M.synth_model(cfg, seed=47)
+    eng = M.Engine(ctx, cfg, w)
+    om = OracleModel(cfg, w)
+    ids = np.random.default_rng(13).integers(0, cfg.vocab, 512)
+    for s0 in (0, 128, 256, 384):
+        eng.forward(ids[s0:s0 + 128], s0)
+    m, L = 128, cfg.n_layers - 1
+    q = eng.debug_buf("q", m * cfg.q_dim).reshape(m, cfg.q_dim)
+    k = eng.debug_buf("k", m * cfg.kv_dim).reshape(m, cfg.kv_dim)
+    v = eng.debug_buf("v", m * cfg.kv_dim).reshape(m, cfg.kv_dim)
+    att = eng.debug_buf("att", m * cfg.q_dim).reshape(m, cfg.q_dim)
+    kc, vc = eng.kv_cache()
+    om.k_cache[:] = kc
+    om.v_cache[:] = vc
+    ref = om.attn_rows(L, q, k, v, 384)
+    errs = np.array([LP._nerr(att[b], ref[b]) for b in range(m)])
+    print(f"{case} ({attn}): attention err median {np.median(errs):.1e} max {errs.max():.1e}")
+    assert np.isfinite(att).all()
+    assert errs.max() <= 1e-4
     eng.close()
 
 

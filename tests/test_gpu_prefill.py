@@ -30,6 +30,8 @@ CASES = {
     "dense-kquant": M.TINY["tiny-qwen3"].replace(sigma=0.05, **KQ),
     "a3b": M.TINY["tiny-a3b"].replace(sigma=0.05),
     "a3b-prune4": M.TINY["tiny-a3b"].replace(sigma=0.05, moe_prune=4.0),
+    # interleaved RoPE pairs (2i, 2i + 1), no q/k norms, Granite's scales
+    "granite-kquant": M.TINY["tiny-granite"].replace(sigma=0.05, n_ff=256, **KQ),
 }
 # pass sizes: a full chunk and ragged ones (a last vector group of 1, 8 and 2 rows), 252 positions
 SIZES = (128, 17, 40, 1, 50, 16)
@@ -124,7 +126,7 @@ def _norm_err(x, y):
 PF_ATTN = {"slices": "4", "loop": "3", "shared": "2"}
 
 
-@pytest.mark.parametrize("case", ["moe", "dense-kquant", "a3b"])
+@pytest.mark.parametrize("case", ["moe", "dense-kquant", "a3b", "granite-kquant"])
 @pytest.mark.parametrize("attn", list(PF_ATTN))
 def test_prefill_pass_at_context_matches_oracle(ctx, case, attn, monkeypatch):
     """A 128-row pass at positions 256..383 (each of the chunk loop's four splits holds one or two
@@ -152,7 +154,7 @@ def test_prefill_pass_at_context_matches_oracle(ctx, case, attn, monkeypatch):
     eng.close()
 
 
-@pytest.mark.parametrize("case", ["a3b", "dense-kquant"])
+@pytest.mark.parametrize("case", ["a3b", "dense-kquant", "moe", "granite-kquant"])
 @pytest.mark.parametrize("attn", list(PF_ATTN))
 def test_prefill_attention_matches_oracle(ctx, case, attn, monkeypatch):
     """The attention stage of a 128-row pass at positions 384..511 (eight chunks: four steps of

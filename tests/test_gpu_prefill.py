@@ -154,11 +154,12 @@ def test_prefill_pass_at_context_matches_oracle(ctx, case, attn, monkeypatch):
     eng.close()
 
 
-@pytest.mark.parametrize("case", ["a3b", "dense-kquant", "moe", "granite-kquant"])
-@pytest.mark.parametrize("attn", list(PF_ATTN))
-def test_prefill_attention_matches_oracle(ctx, case, attn, monkeypatch):
-    """The attention stage of a 128-row pass at positions 384..511 (eight chunks: four steps of
-    each half's walk, two chunks of each split) against the oracle's attention of the same raw
+@pytest.mark.parametrize("case,attn,m", [(c, a, 128) for c in ("a3b", "dense-kquant", "moe", "granite-kquant") for a in PF_ATTN]
+                         + [(c, "slices", r) for c in ("a3b", "moe") for r in (17, 50, 97)])
+def test_prefill_attention_matches_oracle(ctx, case, attn, m, monkeypatch):
+    """The attention stage of an m-row pass at positions 384.. (eight chunks at 128 rows: four
+    steps of each half's walk, two chunks of each split, sixteen 32-position slices; ragged
+    passes leave a part-filled last query block) against the oracle's attention of the same raw
     q / k / v rows on the GPU's own KV cache (the last layer's buffers after the pass): every
     row within 1e-4 (max-abs normalised, the layer pins' attention bar), in every attention form."""
     monkeypatch.setenv("SPX_PF_ATTN", PF_ATTN[attn])
@@ -167,9 +168,10 @@ def test_prefill_attention_matches_oracle(ctx, case, attn, monkeypatch):
     eng = M.Engine(ctx, cfg, w)
     om = OracleModel(cfg, w)
     ids = np.random.default_rng(13).integers(0, cfg.vocab, 512)
-    for s0 in (0, 128, 256, 384):
+    for s0 in (0, 128, 256):
         eng.forward(ids[s0:s0 + 128], s0)
-    m, L = 128, cfg.n_layers - 1
+    eng.forward(ids[384:384 + m], 384)
+    L = cfg.n_layers - 1
     q = eng.debug_buf("q", m * cfg.q_dim).reshape(m, cfg.q_dim)
     k = eng.debug_buf("k", m * cfg.kv_dim).reshape(m, cfg.kv_dim)
     v = eng.debug_buf("v", m * cfg.kv_dim).reshape(m, cfg.kv_dim)
@@ -179,7 +181,7 @@ def test_prefill_attention_matches_oracle(ctx, case, attn, monkeypatch):
     om.v_cache[:] = vc
     ref = om.attn_rows(L, q, k, v, 384)
     errs = np.array([LP._nerr(att[b], ref[b]) for b in range(m)])
-    print(f"{case} ({attn}): attention err median {np.median(errs):.1e} max {errs.max():.1e}")
+    print(f"{case} ({attn}, {m} rows): attention err median {np.median(errs):.1e} max {errs.max():.1e}")
     assert np.isfinite(att).all()
     assert errs.max() <= 1e-4
     eng.close()

@@ -38,6 +38,7 @@ struct DecMVArgs {
   unsigned long long *best;
   float lscale;
   float *xn_out;      // the normalised input row, written by workgroup 0 (null: not written)
+  int nv;             // rows of the pass: 0 or 1, or 2 (a two-row pass: rows v of in.x / out / res / xn_out, best [v][grid])
 };
 
 // Merge of the attention partials of one pass row: one workgroup per query head, written as
@@ -52,8 +53,9 @@ struct DecMergeArgs {
 struct DecRouterArgs {
   TensorView w;
   DecIn in;
-  float *logits;
+  float *logits;      // [nv][n_expert]
   int n_expert;
+  int nv;             // rows: 0 or 1, or 2 (rows v of in.x)
 };
 
 // Routing (MoE) and gate/up + SwiGLU of the chosen experts; a dense FFN is expert 0 with no
@@ -71,6 +73,7 @@ struct DecGateUpArgs {
   int *njobs;           // [1]: distinct experts of the pass (kept choices)
   int *expert_count;    // [n_expert] selection counter (null: none)
   int n_ff;
+  int nv;               // rows: 0 or 1, or 2 (h [v n_used + s], chosen / weights [v][n_used], nkeep [v])
 };
 
 // Down projection of the chosen experts + weighted combine + residual add.
@@ -84,6 +87,7 @@ struct DecDownArgs {
   const float *res_in;
   float *res_out;
   float rscale;
+  int nv;               // rows: 0 or 1, or 2 (slots v n_used + i; res rows v)
 };
 
 constexpr int DEC_MV_NW = 16;   // wavefronts per matvec workgroup

@@ -22,6 +22,10 @@
 
 namespace spx {
 
+// Lambdas of the matrix-core walks are inlined: a lambda left out of line would take its
+// array arguments (the block ring, a tile's results) through scratch memory.
+#define SPX_AI __attribute__((always_inline))
+
 // ------------------------------------------------------------------ integer matvec, one row
 // DEC_MV_NW wavefronts per workgroup; a wavefront takes R rows with G row groups each
 // (G * R = 8, G = the power of two >= nb, at most 8), so tiles of DEC_MV_NW * R rows stride
@@ -141,6 +145,149 @@ __global__ __launch_bounds__(DEC_MV_NW * 64) __attribute__((amdgpu_waves_per_eu(
   }
 }
 
+// ------------------------------------------------------------------ integer matvec, two rows
+// kd_mv for the NV rows of a two-row pass (input rows x + v cols, outputs out + v rows,
+// greedy keys best + v gridDim.x): each row with its own prologue, chains and epilogue, the
+// weights loaded once, so each row gets its one-row pass's bits.
+template <int TT, int BPG, int PD, int NV>
+__global__ __launch_bounds__(DEC_MV_NW * 64) __attribute__((amdgpu_waves_per_eu(PD == 1 ? 4 : 2))) void kd_mv2(const DecMVArgs a) {
+  constexpr int NW = DEC_MV_NW, KB = (DEC_MAXNB + NW - 1) / NW;
+  __shared__ __align__(16) uint32_t lq_[NV][DEC_MAXNB * 64];
+  __shared__ float ld_[NV][DEC_MAXNB];
+  __shared__ __align__(16) int2 lbs_[NV][DEC_MAXNB * 8];
+  __shared__ float bsum_[NV][DEC_MAXNB];
+  __shared__ float cb_[NV][NW][8 * 10 * 2];  // per wavefront R * nb <= 16 blocks x 10 floats
+  __shared__ unsigned long long sbest[NV][NW];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 3, l = lane & 7;
+  const int nb = a.in.cols >> 8, G = a.G, R = 8 / G, r = grp / G, gi = grp - r * G;
+  const int t0 = a.tiles[0], t1 = a.nseg > 1 ? a.tiles[1] : 0, t2 = a.nseg > 2 ? a.tiles[2] : 0;
+  const int total = t0 + t1 + t2;
+  // segment and row of tile t; the segments' fields are all read from the kernel arguments
+  // up front and picked with wave-uniform selects (an indexed argument access would chain
+  // dependent scalar loads ahead of the weight loads)
+  const Planes pl0 = a.w[0].pl, pl1 = a.w[1].pl, pl2 = a.w[2].pl;
+  const int64_t rw0 = a.w[0].rows, rw1 = a.w[1].rows, rw2 = a.w[2].rows;
+  const int dt0 = a.w[0].dtype, dt1 = a.w[1].dtype, dt2 = a.w[2].dtype;
+  float *const o0 = a.out[0], *const o1 = a.out[1], *const o2 = a.out[2];
+  auto in_of = [&](int v) SPX_AI { return DecIn{a.in.x + (int64_t)v * a.in.cols, a.in.nw, a.in.eps, a.in.cols}; };
+  auto xn_of = [&](int v) SPX_AI { return blockIdx.x == 0 && a.xn_out ? a.xn_out + (int64_t)v * a.in.cols : nullptr; };
+  InRow<KB> in[NV];
+#pragma unroll
+  for (int v = 0; v < NV; v++) in_load<NW, KB>(in_of(v), in[v]);  // the input rows' loads go first
+  unsigned long long bestk[NV];
+#pragma unroll
+  for (int v = 0; v < NV; v++) bestk[v] = 0;
+  if constexpr (PD == 1) {
+    DRaw raw[BPG];
+    const int t = min((int)blockIdx.x, total - 1);
+    const int si = __builtin_amdgcn_readfirstlane(t >= t0 ? (t >= t0 + t1 ? 2 : 1) : 0);
+    const int tt = t - (si > 0 ? t0 : 0) - (si > 1 ? t1 : 0);
+    const int64_t row = ((int64_t)tt * NW + wave) * R + r;
+    const int64_t rows = si == 0 ? rw0 : si == 1 ? rw1 : rw2;
+    const int dt = si == 0 ? dt0 : si == 1 ? dt1 : dt2;
+    float *const out = si == 0 ? o0 : si == 1 ? o1 : o2;
+    Planes pl;
+    pl.p0 = si == 0 ? pl0.p0 : si == 1 ? pl1.p0 : pl2.p0;
+    pl.p1 = si == 0 ? pl0.p1 : si == 1 ? pl1.p1 : pl2.p1;
+    pl.p2 = si == 0 ? pl0.p2 : si == 1 ? pl1.p2 : pl2.p2;
+    pl.p3 = si == 0 ? pl0.p3 : si == 1 ? pl1.p3 : pl2.p3;
+    const int64_t grow = row < rows ? row : rows - 1;
+    if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) rp_load<T_Q4K, BPG>(raw, pl, grow, nb, G, gi, l);
+    else rp_load<T_Q6K, BPG>(raw, pl, grow, nb, G, gi, l);
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+      in_quant<NW, KB>(in_of(v), in[v], (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int *)lbs_[v], (SPX_L float *)bsum_[v], xn_of(v));
+    __syncthreads();
+    if ((int)blockIdx.x < total) {
+#pragma unroll
+      for (int v = 0; v < NV; v++) {
+        SPX_L float *cbr = (SPX_L float *)cb_[v][wave] + r * nb * 10;
+        if (TT == T_Q4K || (TT == 0 && dt == T_Q4K))
+          rp_dots<T_Q4K, BPG>(raw, nb, G, gi, l, (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int2 *)lbs_[v], cbr);
+        else rp_dots<T_Q6K, BPG>(raw, nb, G, gi, l, (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int2 *)lbs_[v], cbr);
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the chain buffer is written
+      __builtin_amdgcn_wave_barrier();
+      if (gi == 0) {
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+          const float res = rp_chain((SPX_L float *)cb_[v][wave] + r * nb * 10, nb, l);
+          if (l == 0 && row < rows) {
+            const int64_t ro = (int64_t)v * rows + row;
+            if (out) gst<float>(out + ro, res);
+            if (a.res_out) gst<float>(a.res_out + ro, gld<float>(a.res_in + ro) + a.rscale * res);
+            if (a.best) bestk[v] = pick_key(res, a.lscale, row);
+          }
+        }
+      }
+    }
+  } else {
+    // one segment (TT fixed), tiles blockIdx.x + k * gridDim.x; PD tiles' weights in flight
+    static_assert(TT == T_Q4K || TT == T_Q6K, "prefetched launches take one format");
+    DRaw raw[PD][BPG];
+    const int64_t rows = rw0;
+    const int g = gridDim.x;
+    auto row_of = [&](int t) { return ((int64_t)t * NW + wave) * R + r; };
+#pragma unroll
+    for (int k = 0; k < PD; k++) {
+      const int64_t row = row_of(min((int)blockIdx.x + k * g, total - 1));
+      rp_load<TT, BPG>(raw[k], pl0, row < rows ? row : rows - 1, nb, G, gi, l);
+    }
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+      in_quant<NW, KB>(in_of(v), in[v], (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int *)lbs_[v], (SPX_L float *)bsum_[v], xn_of(v));
+    __syncthreads();
+    for (int t = blockIdx.x; t < total;) {
+#pragma unroll
+      for (int k = 0; k < PD; k++) {
+        if (t < total) {
+#pragma unroll
+          for (int v = 0; v < NV; v++)
+            rp_dots<TT, BPG>(raw[k], nb, G, gi, l, (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int2 *)lbs_[v],
+                             (SPX_L float *)cb_[v][wave] + r * nb * 10);
+          const int64_t nrow = row_of(min(t + PD * g, total - 1));
+          rp_load<TT, BPG>(raw[k], pl0, nrow < rows ? nrow : rows - 1, nb, G, gi, l);  // tile t + PD * g
+          __builtin_amdgcn_s_waitcnt(0xc07f);
+          __builtin_amdgcn_wave_barrier();
+          const int64_t row = row_of(t);
+          if (gi == 0) {
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+              const float res = rp_chain((SPX_L float *)cb_[v][wave] + r * nb * 10, nb, l);
+              if (l == 0 && row < rows) {
+                const int64_t ro = (int64_t)v * rows + row;
+                if (o0) gst<float>(o0 + ro, res);
+                if (a.res_out) gst<float>(a.res_out + ro, gld<float>(a.res_in + ro) + a.rscale * res);
+                if (a.best) {
+                  const unsigned long long key = pick_key(res, a.lscale, row);
+                  bestk[v] = key > bestk[v] ? key : bestk[v];
+                }
+              }
+            }
+          }
+          __builtin_amdgcn_s_waitcnt(0xc07f);
+          __builtin_amdgcn_wave_barrier();  // the chain buffer is refilled by the next tile
+        }
+        t += g;
+      }
+    }
+  }
+  if (a.best) {
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      const unsigned long long b = wave_max_u64(bestk[v]);
+      if (lane == 0) sbest[v][wave] = b;
+    }
+    __syncthreads();
+    if (threadIdx.x < NV) {
+      const int v = threadIdx.x;
+      unsigned long long rb = sbest[v][0];
+      for (int w = 1; w < NW; w++) rb = sbest[v][w] > rb ? sbest[v][w] : rb;
+      gst<unsigned long long>(a.best + (int64_t)v * gridDim.x + blockIdx.x, rb);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ attention merge
 // One workgroup per query head of the row, 1024 threads. Thread (d, gs): output value d of
 // the head, chunk groups gs, gs + 1024 / HD, ...: each group of ATT_GRP chunks is merged as
@@ -218,15 +365,18 @@ __global__ __launch_bounds__(1024) void kd_merge(const DecMergeArgs a, const Ste
 // ------------------------------------------------------------------ router
 // One F32 router row per workgroup (k_router's arithmetic: wavefront w, lane j hold float4s
 // w*64 + j + 256k; the lane's fma chain, the wave tree, the four wavefronts in order) against
-// the ffn_norm'd row, which every workgroup computes for itself.
+// the ffn_norm'd row, which every workgroup computes for itself. NV = 2: both rows of a
+// two-row pass against the row's weights, logits [v][n_expert].
+template <int NV = 1>
 __global__ __launch_bounds__(256) void kd_router(const DecRouterArgs a) {
   constexpr int NK = DEC_MAXNB / 4;
-  __shared__ float bsum[DEC_MAXNB];
-  __shared__ float part[4];
+  __shared__ float bsum[NV][DEC_MAXNB];
+  __shared__ float part[NV][4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, row = blockIdx.x;
   const int dim = a.in.cols, n4 = dim >> 2;
-  InRow<NK> in;
-  in_load<4, NK>(a.in, in);
+  InRow<NK> in[NV];
+#pragma unroll
+  for (int v = 0; v < NV; v++) in_load<4, NK>(DecIn{a.in.x + (int64_t)v * dim, a.in.nw, a.in.eps, dim}, in[v]);
   const float4 *wr = reinterpret_cast<const float4 *>(a.w.pl.p0 + (int64_t)row * dim * 4);
   float4 wv[NK];
 #pragma unroll
@@ -237,39 +387,47 @@ __global__ __launch_bounds__(256) void kd_router(const DecRouterArgs a) {
   // normalise in registers (block tb = wave + 4k holds float4 f = tb * 64 + lane)
   const int nbq = dim >> 8;
 #pragma unroll
-  for (int k = 0; k < NK; k++) {
-    const int tb = wave + 4 * k;
-    if (tb < nbq) {
-      float p = in.v[k].x * in.v[k].x;
-      p = fmaf(in.v[k].y, in.v[k].y, p);
-      p = fmaf(in.v[k].z, in.v[k].z, p);
-      p = fmaf(in.v[k].w, in.v[k].w, p);
-      p = wave_sum(p);
-      if (lane == 0) bsum[tb] = p;
-    }
-  }
-  __syncthreads();
-  float S = 0.0f;
-  for (int k = 0; k < nbq; k++) S = S + bsum[k];
-  const float inv = inv_rms(S, (float)dim, a.in.eps);
-  float pv = 0.0f;
+  for (int v = 0; v < NV; v++)
 #pragma unroll
-  for (int k = 0; k < NK; k++) {
-    const int f = wave * 64 + lane + 256 * k;
-    if (f < n4) {
-      float4 x = in.v[k];
-      const float4 w = in.w[k];
-      x.x = x.x * inv * w.x; x.y = x.y * inv * w.y; x.z = x.z * inv * w.z; x.w = x.w * inv * w.w;
-      pv = fmaf(wv[k].x, x.x, pv);
-      pv = fmaf(wv[k].y, x.y, pv);
-      pv = fmaf(wv[k].z, x.z, pv);
-      pv = fmaf(wv[k].w, x.w, pv);
+    for (int k = 0; k < NK; k++) {
+      const int tb = wave + 4 * k;
+      if (tb < nbq) {
+        float p = in[v].v[k].x * in[v].v[k].x;
+        p = fmaf(in[v].v[k].y, in[v].v[k].y, p);
+        p = fmaf(in[v].v[k].z, in[v].v[k].z, p);
+        p = fmaf(in[v].v[k].w, in[v].v[k].w, p);
+        p = wave_sum(p);
+        if (lane == 0) bsum[v][tb] = p;
+      }
     }
-  }
-  const float tsum = wave_sum(pv);
-  if (lane == 0) part[wave] = tsum;
   __syncthreads();
-  if (threadIdx.x == 0) a.logits[row] = ((part[0] + part[1]) + part[2]) + part[3];
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    float S = 0.0f;
+    for (int k = 0; k < nbq; k++) S = S + bsum[v][k];
+    const float inv = inv_rms(S, (float)dim, a.in.eps);
+    float pv = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NK; k++) {
+      const int f = wave * 64 + lane + 256 * k;
+      if (f < n4) {
+        float4 x = in[v].v[k];
+        const float4 w = in[v].w[k];
+        x.x = x.x * inv * w.x; x.y = x.y * inv * w.y; x.z = x.z * inv * w.z; x.w = x.w * inv * w.w;
+        pv = fmaf(wv[k].x, x.x, pv);
+        pv = fmaf(wv[k].y, x.y, pv);
+        pv = fmaf(wv[k].z, x.z, pv);
+        pv = fmaf(wv[k].w, x.w, pv);
+      }
+    }
+    const float tsum = wave_sum(pv);
+    if (lane == 0) part[v][wave] = tsum;
+  }
+  __syncthreads();
+  if (threadIdx.x < NV) {
+    const int v = threadIdx.x;
+    a.logits[(int64_t)v * a.n_expert + row] = ((part[v][0] + part[v][1]) + part[v][2]) + part[v][3];
+  }
 }
 
 // ------------------------------------------------------------------ gate / up + SwiGLU
@@ -277,71 +435,128 @@ __global__ __launch_bounds__(256) void kd_router(const DecRouterArgs a) {
 // chosen slot s, one row per wavefront: lanes 0-31 take the gate row, 32-63 the up row, four
 // row groups each (blocks gi, gi + 4, ...), chains as rp_chain. h[s][r] = silu(g) * u (silu
 // :586-588). Wavefront 0 routes the row; workgroup (0, 0) publishes the routing for kd_down
-// (chosen experts, weights, kept count).
-template <int T, int BPG>
-__global__ __launch_bounds__(DEC_MV_NW * 64) void kd_gateup(const DecGateUpArgs a) {
+// (chosen experts, weights, kept count). NV = 2: the two rows of a two-row pass, wavefront v
+// routing row v; workgroup (x, s) takes slot s of both rows (each its own expert's gate / up
+// rows and its own Q8_K input), h[v n_used + s], chosen / weights [v][n_used], nkeep [v].
+template <int T, int BPG, int NV = 1>
+__device__ __forceinline__ void gateup_body(const DecGateUpArgs &a) {
   constexpr int NW = DEC_MV_NW, KB = (DEC_MAXNB + NW - 1) / NW;
-  __shared__ __align__(16) uint32_t lq_[DEC_MAXNB * 64];
-  __shared__ float ld_[DEC_MAXNB];
-  __shared__ __align__(16) int2 lbs_[DEC_MAXNB * 8];
-  __shared__ float bsum_[DEC_MAXNB];
-  __shared__ float cb_[NW][2 * DEC_MAXNB * 10];
-  __shared__ int s_route[2];
-  SPX_L uint32_t *lq = (SPX_L uint32_t *)lq_;
-  SPX_L float *ld = (SPX_L float *)ld_, *bsum = (SPX_L float *)bsum_;
-  SPX_L int2 *lbs = (SPX_L int2 *)lbs_;
+  __shared__ __align__(16) uint32_t lq_[NV][DEC_MAXNB * 64];
+  __shared__ float ld_[NV][DEC_MAXNB];
+  __shared__ __align__(16) int2 lbs_[NV][DEC_MAXNB * 8];
+  __shared__ float bsum_[NV][DEC_MAXNB];
+  __shared__ float cb_[NV][NW][2 * DEC_MAXNB * 10];
+  __shared__ int s_route[NV][2];
+  __shared__ int s_ch[NV > 1 ? NV : 1][32];  // NV = 2: each row's kept experts (the pass's union)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 3, l = lane & 7;
   const int half = grp >> 2, gi = grp & 3;  // half 0: gate row, 1: up row
   const int n_ff = a.n_ff, nb = a.in.cols >> 8;
   const int r = blockIdx.x * NW + wave;
   const bool valid = r < n_ff;
-  SPX_L float *cbr = (SPX_L float *)cb_[wave] + half * nb * 10;
   float lv[4];
-  if (a.logits && wave == 0) {
+  if (a.logits && wave < NV) {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int e = lane + 64 * k;
-      lv[k] = e < a.n_expert ? gld<float>(a.logits + e) : -INFINITY;
+      lv[k] = e < a.n_expert ? gld<float>(a.logits + (int64_t)wave * a.n_expert + e) : -INFINITY;
     }
   }
-  InRow<KB> in;
-  in_load<NW, KB>(a.in, in);
-  int expert = 0;
+  auto in_of = [&](int v) SPX_AI { return DecIn{a.in.x + (int64_t)v * a.in.cols, a.in.nw, a.in.eps, a.in.cols}; };
+  InRow<KB> in[NV];
+#pragma unroll
+  for (int v = 0; v < NV; v++) in_load<NW, KB>(in_of(v), in[v]);
+  int expert[NV];
+  bool live[NV];
+#pragma unroll
+  for (int v = 0; v < NV; v++) { expert[v] = 0; live[v] = true; }
   if (a.logits) {
-    if (wave == 0) {
+    if (wave < NV) {
+      const int v = wave;
       int my_e, keep;
       float my_p, wsum;
       route_row(lv, a.n_expert, a.n_used, a.moe_prune, my_e, my_p, keep, wsum);
       if (blockIdx.x == 0 && blockIdx.y == 0) {
         if (lane < keep) {
-          gst<int>(a.chosen + lane, my_e);
-          gst<float>(a.weights + lane, a.norm ? my_p / wsum : my_p);
-          if (a.expert_count) gst<int>(a.expert_count + my_e, gld<int>(a.expert_count + my_e) + 1);
+          gst<int>(a.chosen + v * a.n_used + lane, my_e);
+          gst<float>(a.weights + v * a.n_used + lane, a.norm ? my_p / wsum : my_p);
+          if constexpr (NV == 1) {
+            if (a.expert_count) gst<int>(a.expert_count + my_e, gld<int>(a.expert_count + my_e) + 1);
+          } else {
+            s_ch[v][lane] = my_e;
+          }
         }
-        if (lane == 0) { gst<int>(a.nkeep, keep); gst<int>(a.njobs, keep); }
+        if (lane == 0) {
+          gst<int>(a.nkeep + v, keep);
+          if constexpr (NV == 1) gst<int>(a.njobs, keep);
+        }
       }
-      if (lane == 0) { s_route[0] = lane_i(my_e, blockIdx.y); s_route[1] = keep; }
+      if (lane == 0) { s_route[v][0] = lane_i(my_e, blockIdx.y); s_route[v][1] = keep; }
     }
     __syncthreads();
-    if ((int)blockIdx.y >= s_route[1]) return;  // a pruned slot (the whole workgroup)
-    expert = s_route[0];
+    bool any = false;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      live[v] = (int)blockIdx.y < s_route[v][1];
+      any = any || live[v];
+      expert[v] = s_route[v][0];
+    }
+    if constexpr (NV > 1) {
+      // the pass's distinct experts (row 0's kept choices, then row 1's not among them): the
+      // job count and one selection count each, as the multi-row passes count them
+      if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+        const int k0 = s_route[0][1], k1 = s_route[1][1];
+        bool fresh = false;
+        int e1 = 0;
+        if (lane < k1) {
+          e1 = s_ch[1][lane];
+          fresh = true;
+          for (int j = 0; j < k0; j++) fresh = fresh && s_ch[0][j] != e1;
+        }
+        if (a.expert_count) {
+          if (lane < k0) gst<int>(a.expert_count + s_ch[0][lane], gld<int>(a.expert_count + s_ch[0][lane]) + 1);
+          if (fresh) gst<int>(a.expert_count + e1, gld<int>(a.expert_count + e1) + 1);
+        }
+        const int nfresh = __popcll(__ballot(fresh));
+        if (lane == 0) gst<int>(a.njobs, k0 + nfresh);
+      }
+    }
+    if (!any) return;  // a pruned slot of every row (the whole workgroup)
   }
-  const int64_t grow = (int64_t)expert * a.gate.rows + (valid ? r : n_ff - 1);
-  DRaw raw[BPG];
-  rp_load<T, BPG>(raw, half ? a.up.pl : a.gate.pl, grow, nb, 4, gi, l);
-  in_quant<NW, KB>(a.in, in, lq, ld, (SPX_L int *)lbs, bsum, nullptr);
+  DRaw raw[NV][BPG];
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const int64_t grow = (int64_t)expert[v] * a.gate.rows + (valid ? r : n_ff - 1);
+    rp_load<T, BPG>(raw[v], half ? a.up.pl : a.gate.pl, grow, nb, 4, gi, l);
+  }
+#pragma unroll
+  for (int v = 0; v < NV; v++)
+    in_quant<NW, KB>(in_of(v), in[v], (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int *)lbs_[v], (SPX_L float *)bsum_[v], nullptr);
   __syncthreads();
-  rp_dots<T, BPG>(raw, nb, 4, gi, l, lq, ld, lbs, cbr);
+#pragma unroll
+  for (int v = 0; v < NV; v++)
+    rp_dots<T, BPG>(raw[v], nb, 4, gi, l, (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int2 *)lbs_[v],
+                    (SPX_L float *)cb_[v][wave] + half * nb * 10);
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the chain buffer is written
   __builtin_amdgcn_wave_barrier();
-  const float res = gi == 0 ? rp_chain(cbr, nb, l) : 0.0f;
-  uint32_t r_lo, r_hi;  // lanes 0-31 get the up row's result from lanes 32-63
-  xchg32(__float_as_uint(res), r_lo, r_hi);
-  const float u = __uint_as_float(r_hi);
-  if (lane == 0 && valid) {
-    const float x = res;
-    gst<float>(a.h + (int64_t)blockIdx.y * n_ff + r, x / (1.0f + expf(-x)) * u);
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const float res = gi == 0 ? rp_chain((SPX_L float *)cb_[v][wave] + half * nb * 10, nb, l) : 0.0f;
+    uint32_t r_lo, r_hi;  // lanes 0-31 get the up row's result from lanes 32-63
+    xchg32(__float_as_uint(res), r_lo, r_hi);
+    const float u = __uint_as_float(r_hi);
+    if (lane == 0 && valid && live[v]) {
+      const float x = res;
+      gst<float>(a.h + ((int64_t)v * gridDim.y + blockIdx.y) * n_ff + r, x / (1.0f + expf(-x)) * u);
+    }
   }
+}
+
+template <int T, int BPG>
+__global__ __launch_bounds__(DEC_MV_NW * 64) void kd_gateup(const DecGateUpArgs a) { gateup_body<T, BPG, 1>(a); }
+// two rows: two workgroups a CU (the grid's 384 workgroups of Qwen3-30B-A3B in one round)
+template <int T, int BPG>
+__global__ __launch_bounds__(DEC_MV_NW * 64) __attribute__((amdgpu_waves_per_eu(8))) void kd_gateup2(const DecGateUpArgs a) {
+  gateup_body<T, BPG, 2>(a);
 }
 
 // ------------------------------------------------------------------ down + combine
@@ -349,7 +564,9 @@ __global__ __launch_bounds__(DEC_MV_NW * 64) void kd_gateup(const DecGateUpArgs 
 // row of chosen expert s (rounds of eight for more). Every workgroup quantizes the kept
 // slots' h rows into LDS (Q8_K, :420-424). out = sum over the kept choices, in choice order,
 // of w * y (non-fused multiply and add, ffns_fused :432-437); res_out = res_in + rscale * out.
-template <int T, int NB>
+// NV = 2: the slots of both rows of a two-row pass (slot v n_used + i: row v's choice i, h and
+// chosen / weights as kd_gateup leaves them), each row's combine and residual add on its own.
+template <int T, int NB, int NV = 1>
 __global__ __launch_bounds__(512) void kd_down(const DecDownArgs a) {
   constexpr int NWD = 8, QB = DEC_DOWN_Q / 256, HB = QB / NWD;
   __shared__ __align__(16) uint32_t lq_[DEC_DOWN_Q / 4];
@@ -360,25 +577,34 @@ __global__ __launch_bounds__(512) void kd_down(const DecDownArgs a) {
   SPX_L float *ld = (SPX_L float *)ld_;
   SPX_L int2 *lbs = (SPX_L int2 *)lbs_;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 3, l = lane & 7;
-  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, nbh = n_ff >> 8;
+  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, nbh = n_ff >> 8, nu = a.n_used, ns = NV * nu;
   const int64_t r = (int64_t)blockIdx.x * NWD + wave;
   const int64_t rr = r < dim ? r : dim - 1;
   // h blocks of every slot (wave w: blocks w, w + 8, ...) and the chosen experts' rows are
   // requested before the kept count arrives (slots past it hold earlier, valid expert ids)
-  const int nqa = a.n_used * nbh;
+  const int nqa = ns * nbh;
   float4 hv[HB];
 #pragma unroll
   for (int k = 0; k < HB; k++) {
     const int vb = wave + NWD * k;
     hv[k] = vb < nqa ? gld<float4>(a.h + (int64_t)(vb / nbh) * n_ff + (vb % nbh) * 256 + 4 * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  auto expert_of = [&](int sv) SPX_AI {  // (clamped: a slot never written holds a zero)
+    return min(max(gld<int>(a.chosen + sv), 0), a.w.n_expert - 1);
+  };
   DRaw raw[NB];
-  draw_row<T, NB>(raw, a.w.pl, (int64_t)gld<int>(a.chosen + min(slot, a.n_used - 1)) * dim + rr, nbh, l);
-  const int nk = gld<int>(a.nkeep), nqb = nk * nbh, s0max = (nk + 7) / 8;
+  draw_row<T, NB>(raw, a.w.pl, (int64_t)expert_of(min(slot, ns - 1)) * dim + rr, nbh, l);
+  int nk[NV];
+#pragma unroll
+  for (int v = 0; v < NV; v++) nk[v] = gld<int>(a.nkeep + v);
+  // a slot sv = v nu + i is kept when i < nk[v]; rows past the kept slots are quantized too
+  // only for NV = 1 (its kept slots are a prefix)
+  auto kept = [&](int sv) SPX_AI { return NV == 1 ? sv < nk[0] : (sv % nu) < nk[min(sv / nu, NV - 1)]; };
+  const int nqb = NV == 1 ? nk[0] * nbh : nqa, s0max = NV == 1 ? (nk[0] + 7) / 8 : (ns + 7) / 8;
 #pragma unroll
   for (int k = 0; k < HB; k++) {
     const int vb = wave + NWD * k;
-    if (vb < nqb) {
+    if (vb < nqb && kept(vb / nbh)) {
       const float am = q8k_amax(hv[k]);
       q8k_block_store(hv[k], am, lq + vb * 64, ld + vb, (SPX_L int *)(lbs + vb * 8));
     }
@@ -386,17 +612,27 @@ __global__ __launch_bounds__(512) void kd_down(const DecDownArgs a) {
   __syncthreads();
   for (int round = 0; round < s0max; round++) {
     const int s = round * 8 + slot;
-    if (round > 0) draw_row<T, NB>(raw, a.w.pl, (int64_t)gld<int>(a.chosen + min(s, nk - 1)) * dim + rr, nbh, l);
-    const int sv = min(s, nk - 1);
-    const float y = dot_row<T, NB>(raw, nbh, l, lq + sv * nbh * 64, ld + sv * nbh, lbs + sv * nbh * 8);
-    if (l == 0 && s < nk) ys[wave][s] = y;
+    if constexpr (NV == 1) {
+      if (round > 0) draw_row<T, NB>(raw, a.w.pl, (int64_t)gld<int>(a.chosen + min(s, nk[0] - 1)) * dim + rr, nbh, l);
+      const int sv = min(s, nk[0] - 1);
+      const float y = dot_row<T, NB>(raw, nbh, l, lq + sv * nbh * 64, ld + sv * nbh, lbs + sv * nbh * 8);
+      if (l == 0 && s < nk[0]) ys[wave][s] = y;
+    } else {
+      if (round > 0) draw_row<T, NB>(raw, a.w.pl, (int64_t)expert_of(min(s, ns - 1)) * dim + rr, nbh, l);
+      const int sv = min(s, ns - 1);  // (a slot not kept reads an image nobody wrote; its y is dropped)
+      const float y = dot_row<T, NB>(raw, nbh, l, lq + sv * nbh * 64, ld + sv * nbh, lbs + sv * nbh * 8);
+      if (l == 0 && s < ns && kept(s)) ys[wave][s] = y;
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
   if (lane == 0 && r < dim) {
-    float acc = 0.0f;
-    for (int i = 0; i < nk; i++) acc = acc + gld<float>(a.weights + i) * ys[wave][i];
-    gst<float>(a.res_out + r, gld<float>(a.res_in + r) + a.rscale * acc);
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      float acc = 0.0f;
+      for (int i = 0; i < nk[v]; i++) acc = acc + gld<float>(a.weights + v * nu + i) * ys[wave][v * nu + i];
+      gst<float>(a.res_out + (int64_t)v * dim + r, gld<float>(a.res_in + (int64_t)v * dim + r) + a.rscale * acc);
+    }
   }
 }
 
@@ -1101,9 +1337,6 @@ __device__ __forceinline__ MqVec mq_vecs(int nv, VR vrow) {
 // block) is chained beside them, and out = ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)) - corr
 // needs no other wavefront.
 typedef unsigned short mx_u16x2 __attribute__((ext_vector_type(2)));
-// Lambdas of the matrix-core walks are inlined: a lambda left out of line would take its
-// array arguments (the block ring, a tile's results) through scratch memory.
-#define SPX_AI __attribute__((always_inline))
 // Per byte of v (each <= 15) times s (<= 15) with both products of a 16-bit half <= 105: no
 // carry leaves a byte (v_pk_mul_lo_u16).
 __device__ __forceinline__ uint32_t mx_pmul(uint32_t v, uint32_t s) {
@@ -2453,7 +2686,14 @@ static int cu_count() {
 
 static int nb_bucket(int nb) { return nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 3 ? 3 : nb <= 4 ? 4 : nb <= 8 ? 8 : 16; }
 
-template <int TT>
+// kd_mv for one row, kd_mv2 for the two rows of a two-row pass
+template <int TT, int BPG, int PD, int NV>
+constexpr auto kd_mvn() {
+  if constexpr (NV == 1) return kd_mv<TT, BPG, PD>;
+  else return kd_mv2<TT, BPG, PD, NV>;
+}
+
+template <int TT, int NV>
 static hipError_t dec_mv_tt(const DecMVArgs &a, int grid, hipStream_t s) {
   const int nb = a.in.cols >> 8, bpg = (nb + a.G - 1) / a.G;
   const int total = a.tiles[0] + (a.nseg > 1 ? a.tiles[1] : 0) + (a.nseg > 2 ? a.tiles[2] : 0);
@@ -2461,14 +2701,14 @@ static hipError_t dec_mv_tt(const DecMVArgs &a, int grid, hipStream_t s) {
   if constexpr (TT != 0) {
     if (grid < total) {  // tiles stride over the grid: four (two) tiles' weights in flight
       if (a.nseg != 1) return hipErrorInvalidValue;
-      if (bpg == 1) hipLaunchKernelGGL((kd_mv<TT, 1, 4>), dim3(grid), b, 0, s, a);
-      else hipLaunchKernelGGL((kd_mv<TT, 2, 2>), dim3(grid), b, 0, s, a);
+      if (bpg == 1) hipLaunchKernelGGL((kd_mvn<TT, 1, 4, NV>()), dim3(grid), b, 0, s, a);
+      else hipLaunchKernelGGL((kd_mvn<TT, 2, 2, NV>()), dim3(grid), b, 0, s, a);
       return hipGetLastError();
     }
   }
   if (grid != total) return hipErrorInvalidValue;
-  if (bpg == 1) hipLaunchKernelGGL((kd_mv<TT, 1, 1>), dim3(grid), b, 0, s, a);
-  else hipLaunchKernelGGL((kd_mv<TT, 2, 1>), dim3(grid), b, 0, s, a);
+  if (bpg == 1) hipLaunchKernelGGL((kd_mvn<TT, 1, 1, NV>()), dim3(grid), b, 0, s, a);
+  else hipLaunchKernelGGL((kd_mvn<TT, 2, 1, NV>()), dim3(grid), b, 0, s, a);
   return hipGetLastError();
 }
 
@@ -2486,9 +2726,15 @@ hipError_t launch_dec_mv(const DecMVArgs &a, int grid, hipStream_t s) {
     all4 = all4 && a.w[i].dtype == T_Q4K;
     all6 = all6 && a.w[i].dtype == T_Q6K;
   }
-  if (all4) return dec_mv_tt<T_Q4K>(a, grid, s);
-  if (all6) return dec_mv_tt<T_Q6K>(a, grid, s);
-  return dec_mv_tt<0>(a, grid, s);
+  if (a.nv < 0 || a.nv > 2) return hipErrorInvalidValue;
+  if (a.nv == 2) {
+    if (all4) return dec_mv_tt<T_Q4K, 2>(a, grid, s);
+    if (all6) return dec_mv_tt<T_Q6K, 2>(a, grid, s);
+    return dec_mv_tt<0, 2>(a, grid, s);
+  }
+  if (all4) return dec_mv_tt<T_Q4K, 1>(a, grid, s);
+  if (all6) return dec_mv_tt<T_Q6K, 1>(a, grid, s);
+  return dec_mv_tt<0, 1>(a, grid, s);
 }
 
 hipError_t launch_dec_merge(const DecMergeArgs &a, const StepRec *st, hipStream_t s) {
@@ -2499,17 +2745,24 @@ hipError_t launch_dec_merge(const DecMergeArgs &a, const StepRec *st, hipStream_
 }
 
 hipError_t launch_dec_router(const DecRouterArgs &a, hipStream_t s) {
-  if (a.in.cols % 256 || a.in.cols > 256 * DEC_MAXNB || !a.in.nw) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kd_router, dim3(a.n_expert), dim3(256), 0, s, a);
+  if (a.in.cols % 256 || a.in.cols > 256 * DEC_MAXNB || !a.in.nw || a.nv < 0 || a.nv > 2) return hipErrorInvalidValue;
+  if (a.nv == 2) hipLaunchKernelGGL(kd_router<2>, dim3(a.n_expert), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(kd_router<1>, dim3(a.n_expert), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
-template <int T>
+template <int T, int NV>
 static hipError_t dec_gu_t(const DecGateUpArgs &a, dim3 grid, hipStream_t s) {
   const int bpg = ((a.in.cols >> 8) + 3) / 4;
-  if (bpg == 1) hipLaunchKernelGGL((kd_gateup<T, 1>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
-  else if (bpg == 2) hipLaunchKernelGGL((kd_gateup<T, 2>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
-  else hipLaunchKernelGGL((kd_gateup<T, 4>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
+  if constexpr (NV == 2) {
+    if (bpg == 1) hipLaunchKernelGGL((kd_gateup2<T, 1>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
+    else if (bpg == 2) hipLaunchKernelGGL((kd_gateup2<T, 2>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
+    else hipLaunchKernelGGL((kd_gateup2<T, 4>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
+  } else {
+    if (bpg == 1) hipLaunchKernelGGL((kd_gateup<T, 1>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
+    else if (bpg == 2) hipLaunchKernelGGL((kd_gateup<T, 2>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
+    else hipLaunchKernelGGL((kd_gateup<T, 4>), grid, dim3(DEC_MV_NW * 64), 0, s, a);
+  }
   return hipGetLastError();
 }
 
@@ -2517,30 +2770,44 @@ hipError_t launch_dec_gateup(const DecGateUpArgs &a, hipStream_t s) {
   const int nb = a.in.cols >> 8;
   if (a.in.cols % 256 || nb > DEC_MAXNB || a.gate.nb != nb || a.up.nb != nb || a.gate.dtype != a.up.dtype || !a.in.nw) return hipErrorInvalidValue;
   if (a.logits && (a.n_expert < 1 || a.n_expert > 256 || a.n_used < 1 || a.n_used > 32 || a.n_used > a.n_expert)) return hipErrorInvalidValue;
+  if (a.nv < 0 || a.nv > 2) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((a.n_ff + DEC_MV_NW - 1) / DEC_MV_NW), a.logits ? (unsigned)a.n_used : 1u);
-  if (a.gate.dtype == T_Q4K) return dec_gu_t<T_Q4K>(a, grid, s);
-  if (a.gate.dtype == T_Q6K) return dec_gu_t<T_Q6K>(a, grid, s);
+  if (a.nv == 2) {
+    if (a.gate.dtype == T_Q4K) return dec_gu_t<T_Q4K, 2>(a, grid, s);
+    if (a.gate.dtype == T_Q6K) return dec_gu_t<T_Q6K, 2>(a, grid, s);
+    return hipErrorInvalidValue;
+  }
+  if (a.gate.dtype == T_Q4K) return dec_gu_t<T_Q4K, 1>(a, grid, s);
+  if (a.gate.dtype == T_Q6K) return dec_gu_t<T_Q6K, 1>(a, grid, s);
   return hipErrorInvalidValue;
 }
 
-template <int T>
+template <int T, int NV>
 static hipError_t dec_down_t(const DecDownArgs &a, hipStream_t s) {
   const dim3 grid((unsigned)((a.w.rows + 7) / 8));
   switch (nb_bucket((int)a.w.nb)) {
-  case 1: hipLaunchKernelGGL((kd_down<T, 1>), grid, dim3(512), 0, s, a); break;
-  case 2: hipLaunchKernelGGL((kd_down<T, 2>), grid, dim3(512), 0, s, a); break;
-  case 3: hipLaunchKernelGGL((kd_down<T, 3>), grid, dim3(512), 0, s, a); break;
-  case 4: hipLaunchKernelGGL((kd_down<T, 4>), grid, dim3(512), 0, s, a); break;
-  case 8: hipLaunchKernelGGL((kd_down<T, 8>), grid, dim3(512), 0, s, a); break;
-  default: hipLaunchKernelGGL((kd_down<T, 16>), grid, dim3(512), 0, s, a); break;
+  case 1: hipLaunchKernelGGL((kd_down<T, 1, NV>), grid, dim3(512), 0, s, a); break;
+  case 2: hipLaunchKernelGGL((kd_down<T, 2, NV>), grid, dim3(512), 0, s, a); break;
+  case 3: hipLaunchKernelGGL((kd_down<T, 3, NV>), grid, dim3(512), 0, s, a); break;
+  case 4: hipLaunchKernelGGL((kd_down<T, 4, NV>), grid, dim3(512), 0, s, a); break;
+  case 8: hipLaunchKernelGGL((kd_down<T, 8, NV>), grid, dim3(512), 0, s, a); break;
+  default: hipLaunchKernelGGL((kd_down<T, 16, NV>), grid, dim3(512), 0, s, a); break;
   }
   return hipGetLastError();
 }
 
 hipError_t launch_dec_down(const DecDownArgs &a, hipStream_t s) {
-  if (a.w.cols % 256 || a.w.nb > DEC_MAXNB || a.n_used < 1 || a.n_used > 32 || (int64_t)a.n_used * a.w.cols > DEC_DOWN_Q) return hipErrorInvalidValue;
-  if (a.w.dtype == T_Q4K) return dec_down_t<T_Q4K>(a, s);
-  if (a.w.dtype == T_Q6K) return dec_down_t<T_Q6K>(a, s);
+  const int nv = a.nv == 2 ? 2 : 1;
+  if (a.w.cols % 256 || a.w.nb > DEC_MAXNB || a.n_used < 1 || a.nv < 0 || a.nv > 2 || nv * a.n_used > 32 ||
+      (int64_t)nv * a.n_used * a.w.cols > DEC_DOWN_Q)
+    return hipErrorInvalidValue;
+  if (nv == 2) {
+    if (a.w.dtype == T_Q4K) return dec_down_t<T_Q4K, 2>(a, s);
+    if (a.w.dtype == T_Q6K) return dec_down_t<T_Q6K, 2>(a, s);
+    return hipErrorInvalidValue;
+  }
+  if (a.w.dtype == T_Q4K) return dec_down_t<T_Q4K, 1>(a, s);
+  if (a.w.dtype == T_Q6K) return dec_down_t<T_Q6K, 1>(a, s);
   return hipErrorInvalidValue;
 }
 

@@ -90,6 +90,7 @@ struct spx_engine {
   const float *out_norm = nullptr;
   bool prepared = false, use_graphs = true;
   bool dec_ok = false, dec_on = true;  // one-row passes on the decode pipeline (decode.hip)
+  bool dec2 = true;                    // two-row passes on it too (SPX_DEC2; enqueue_decode with nv = 2)
   // one-row passes of a Q8_0 model on the fused kernels with the norms in the consumers'
   // prologues and the residual adds in the producers' epilogues instead of last-workgroup
   // tails (the same bits; SPX_FPRO=0 keeps the tails)
@@ -531,7 +532,11 @@ int enqueue_forward(spx_engine *E, int m, bool advance = false) {
 // One-row pass on the decode pipeline (decode.hip): the same values as enqueue_forward(E, 1),
 // computed by kernels that meet only at kernel boundaries. Residual stream: the embedding
 // writes xA; attn_output writes xB = xA + rscale * proj; the FFN writes xA = xB + rscale * y.
-int enqueue_decode(spx_engine *E, bool advance) {
+// nv = 2: a two-row pass (verify of a one-token draft) on the same kernels, each taking both
+// rows (kd_mv2, kd_router<2>, kd_gateup<.., 2>, kd_down<.., 2>: every row the bits of its
+// one-row pass, the weights read once), attention on the multi-row kernels; no step-record
+// advance, no layer snapshots (those passes take enqueue_pass_m).
+int enqueue_decode(spx_engine *E, bool advance, int nv = 1) {
   const auto &c = E->c;
   hipStream_t s = E->ctx->stream;
   const int dim = c.dim, hd = c.head_dim;
@@ -543,7 +548,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
     NormTail t{};
     t.x = E->xA;
     t.dim = dim;
-    SPX_HIP(launch_embed(E->embed->v, E->st_dev, c.embedding_scale, t, 1, s));
+    SPX_HIP(launch_embed(E->embed->v, E->st_dev, c.embedding_scale, t, nv, s));
   }
   for (int l = 0; l < c.n_layers; l++) {
     const LayerW &ly = E->L[l];
@@ -563,6 +568,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
       a.nseg = 3;
       a.G = G;
       a.in = DecIn{E->xA, ly.attn_norm, c.rms_eps, dim};
+      a.nv = nv;
       SPX_HIP(launch_dec_mv(a, total, s));
     }
     if (int r = snap(E, l, DBG_Q, E->q, E->q_dim, 1) || snap(E, l, DBG_K, E->k, E->kv_dim, 1) || snap(E, l, DBG_V, E->v, E->kv_dim, 1)) return r;
@@ -575,7 +581,9 @@ int enqueue_decode(spx_engine *E, bool advance) {
       aa.layer = l; aa.max_seq = c.max_seq; aa.kv_dim = E->kv_dim; aa.hd = hd; aa.n_heads = c.n_heads; aa.n_kv = c.n_kv_heads;
       aa.neox = c.rope_neox; aa.nch = E->nch; aa.nslot = E->nch + ATT_GMAX; aa.eps = c.rms_eps;
       aa.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt((float)hd);
-      if (E->att_merge) {
+      if (nv > 1) {
+        SPX_HIP(attn_launch(E, aa, nv, s));
+      } else if (E->att_merge) {
         SPX_HIP(launch_attention(aa, 1, E->st_dev, s));
       } else {
         SPX_HIP(launch_attention_partials(aa, E->st_dev, s));
@@ -590,17 +598,18 @@ int enqueue_decode(spx_engine *E, bool advance) {
       a.w[0] = ly.wo->v; a.out[0] = E->proj; a.tiles[0] = tiles(ly.wo); a.nseg = 1; a.G = gshape(ly.wo);
       a.in = DecIn{E->att, nullptr, 0.0f, E->q_dim};
       a.res_in = E->xA; a.res_out = E->xB; a.rscale = c.residual_scale;
+      a.nv = nv;
       SPX_HIP(launch_dec_mv(a, a.tiles[0], s));
     }
     if (int r = snap(E, l, DBG_PROJ, E->proj, dim, 1) || snap(E, l, DBG_XMID, E->xB, dim, 1)) return r;
     const int nff = (int)ly.gate->v.rows;
     const DecIn fin{E->xB, ly.ffn_norm, c.rms_eps, dim};
     DecGateUpArgs ga{};
-    ga.gate = ly.gate->v; ga.up = ly.up->v; ga.in = fin; ga.h = E->h; ga.n_ff = nff;
+    ga.gate = ly.gate->v; ga.up = ly.up->v; ga.in = fin; ga.h = E->h; ga.n_ff = nff; ga.nv = nv;
     if (ly.moe) {  // moe_forward (:1176-1392)
       {
         ProfScope ps(E, PC_ROUTER, wbytes(ly.router));
-        DecRouterArgs ra{ly.router->v, fin, E->rlog, c.n_expert};
+        DecRouterArgs ra{ly.router->v, fin, E->rlog, c.n_expert, nv};
         SPX_HIP(launch_dec_router(ra, s));
       }
       {
@@ -613,7 +622,7 @@ int enqueue_decode(spx_engine *E, bool advance) {
       if (int r = snap_ffn(E, l, 1)) return r;
       {
         ProfScope ps(E, PC_DOWN, wbytes(ly.down), l, true);
-        DecDownArgs da{ly.down->v, E->h, E->chosen, E->weights, E->nkeep, c.n_expert_used, E->xB, E->xA, c.residual_scale};
+        DecDownArgs da{ly.down->v, E->h, E->chosen, E->weights, E->nkeep, c.n_expert_used, E->xB, E->xA, c.residual_scale, nv};
         SPX_HIP(launch_dec_down(da, s));
       }
     } else {  // ffn_forward (:590-614)
@@ -628,25 +637,30 @@ int enqueue_decode(spx_engine *E, bool advance) {
         a.w[0] = ly.down->v; a.out[0] = E->ffn; a.tiles[0] = tiles(ly.down); a.nseg = 1; a.G = gshape(ly.down);
         a.in = DecIn{E->h, nullptr, 0.0f, nff};
         a.res_in = E->xB; a.res_out = E->xA; a.rscale = c.residual_scale;
+        a.nv = nv;
         SPX_HIP(launch_dec_mv(a, a.tiles[0], s));
       }
     }
   }
   if (int r = snap(E, c.n_layers, DBG_XIN, E->xA, dim, 1)) return r;
+  if (nv > 1 && E->lm_sel == 2) return 0;  // feed's earlier chunks: no logits
+  const bool last = nv > 1 && E->lm_sel == 1;  // the last row only (row 0 of xn / logits / amax)
+  const int nl = last ? 1 : nv;
   int grid = 1;
   {
     ProfScope ps(E, PC_LMHEAD, wbytes(E->lm_head));
     DecMVArgs a{};
     a.w[0] = E->lm_head->v; a.out[0] = E->logits; a.tiles[0] = tiles(E->lm_head); a.nseg = 1; a.G = gshape(E->lm_head);
-    a.in = DecIn{E->xA, E->out_norm, c.rms_eps, dim};
+    a.in = DecIn{E->xA + (int64_t)(nv - nl) * dim, E->out_norm, c.rms_eps, dim};
     a.best = E->best; a.lscale = c.logit_scale; a.xn_out = E->xn;
+    a.nv = nl;
     grid = std::min(a.tiles[0], E->lm_dec_grid);
     SPX_HIP(launch_dec_mv(a, grid, s));
   }
   E->nbest = grid;
   {
     ProfScope ps(E, PC_ARGMAX, 0);
-    SPX_HIP(launch_argmax_final(E->best, grid, E->amax, E->st_dev, advance ? E->hist : nullptr, 1, s));
+    SPX_HIP(launch_argmax_final(E->best, grid, E->amax, last ? nullptr : E->st_dev, advance ? E->hist : nullptr, nl, s));
   }
   return 0;
 }
@@ -912,7 +926,11 @@ int run_forward(spx_engine *E, int m, bool advance = false) {
   hipStream_t s = E->ctx->stream;
   const bool dec = E->dec_ok && E->dec_on;
   if (persist_used(E, m)) return enqueue_persist(E, advance);
-  auto enqueue = [&]() { return !dec ? enqueue_forward(E, m, advance) : m == 1 ? enqueue_decode(E, advance) : enqueue_pass_m(E, m); };
+  auto enqueue = [&]() {
+    if (!dec) return enqueue_forward(E, m, advance);
+    if (m == 1) return enqueue_decode(E, advance);
+    return m == 2 && E->dec2 && !E->dbg_on ? enqueue_decode(E, false, 2) : enqueue_pass_m(E, m);
+  };
   if (!E->use_graphs || E->profiling || E->dbg_on) return enqueue();
   const int slot = advance ? 0 : m;
   hipGraphExec_t &gx = E->graph[advance ? 0 : E->lm_sel][slot];
@@ -969,6 +987,7 @@ int spx_engine_create(spx_ctx *ctx, const spx_model_config *cfg, spx_engine **ou
   if (const char *v = std::getenv("SPX_DOWN_MODE")) E->down_mode = std::max(0, std::min(1, atoi(v)));
   if (const char *v = std::getenv("SPX_ATT_MERGE")) E->att_merge = atoi(v) != 0;
   if (const char *v = std::getenv("SPX_PF_ATTN")) E->pf_attn = std::max(0, std::min(4, atoi(v)));
+  if (const char *v = std::getenv("SPX_DEC2")) E->dec2 = atoi(v) != 0;
   if (const char *v = std::getenv("SPX_ATT_MT")) E->att_mt_min = std::max(0, std::min(MAX_M + 1, atoi(v)));
   if (const char *v = std::getenv("SPX_PF_MIN")) E->pf_min_rows = std::max(2, std::min(MAX_M + 1, atoi(v)));
   *out = E;
@@ -1127,6 +1146,9 @@ int spx_engine_prepare(spx_engine *E) {
     if (ly.moe) dok = dok && (int64_t)nu * ly.gate->v.rows <= DEC_DOWN_Q;
   }
   E->dec_ok = dok;
+  // two-row passes on it: both rows' kept slots in the down kernel's LDS image and row groups
+  for (auto &ly : E->L)
+    if (ly.moe && (2 * nu > 32 || (int64_t)2 * nu * ly.gate->v.rows > DEC_DOWN_Q)) E->dec2 = false;
   {  // every one-row consumer of a normalised row must be a kernel with the prologue
     auto q8 = [](const spx_tensor *t) { return t->v.dtype == T_Q8_0 && t->v.cols <= 4096; };
     bool fp = !dok && q8(E->lm_head) && c.dim <= 256 * NORM_NT;

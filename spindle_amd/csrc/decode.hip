@@ -174,6 +174,17 @@ __global__ __launch_bounds__(DEC_MV_NW * 64) __attribute__((amdgpu_waves_per_eu(
   InRow<KB> in[NV];
 #pragma unroll
   for (int v = 0; v < NV; v++) in_load<NW, KB>(in_of(v), in[v]);  // the input rows' loads go first
+  const SPX_L uint32_t *lqv[NV];
+  const SPX_L float *ldv[NV];
+  const SPX_L int2 *lbsv[NV];
+  SPX_L float *cbrv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    lqv[v] = (SPX_L uint32_t *)lq_[v];
+    ldv[v] = (SPX_L float *)ld_[v];
+    lbsv[v] = (SPX_L int2 *)lbs_[v];
+    cbrv[v] = (SPX_L float *)cb_[v][wave] + r * nb * 10;
+  }
   unsigned long long bestk[NV];
 #pragma unroll
   for (int v = 0; v < NV; v++) bestk[v] = 0;
@@ -199,13 +210,8 @@ __global__ __launch_bounds__(DEC_MV_NW * 64) __attribute__((amdgpu_waves_per_eu(
       in_quant<NW, KB>(in_of(v), in[v], (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int *)lbs_[v], (SPX_L float *)bsum_[v], xn_of(v));
     __syncthreads();
     if ((int)blockIdx.x < total) {
-#pragma unroll
-      for (int v = 0; v < NV; v++) {
-        SPX_L float *cbr = (SPX_L float *)cb_[v][wave] + r * nb * 10;
-        if (TT == T_Q4K || (TT == 0 && dt == T_Q4K))
-          rp_dots<T_Q4K, BPG>(raw, nb, G, gi, l, (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int2 *)lbs_[v], cbr);
-        else rp_dots<T_Q6K, BPG>(raw, nb, G, gi, l, (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int2 *)lbs_[v], cbr);
-      }
+      if (TT == T_Q4K || (TT == 0 && dt == T_Q4K)) rp_dots_nv<T_Q4K, BPG, NV>(raw, nb, G, gi, l, lqv, ldv, lbsv, cbrv);
+      else rp_dots_nv<T_Q6K, BPG, NV>(raw, nb, G, gi, l, lqv, ldv, lbsv, cbrv);
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the chain buffer is written
       __builtin_amdgcn_wave_barrier();
       if (gi == 0) {
@@ -241,10 +247,7 @@ __global__ __launch_bounds__(DEC_MV_NW * 64) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int k = 0; k < PD; k++) {
         if (t < total) {
-#pragma unroll
-          for (int v = 0; v < NV; v++)
-            rp_dots<TT, BPG>(raw[k], nb, G, gi, l, (SPX_L uint32_t *)lq_[v], (SPX_L float *)ld_[v], (SPX_L int2 *)lbs_[v],
-                             (SPX_L float *)cb_[v][wave] + r * nb * 10);
+          rp_dots_nv<TT, BPG, NV>(raw[k], nb, G, gi, l, lqv, ldv, lbsv, cbrv);
           const int64_t nrow = row_of(min(t + PD * g, total - 1));
           rp_load<TT, BPG>(raw[k], pl0, nrow < rows ? nrow : rows - 1, nb, G, gi, l);  // tile t + PD * g
           __builtin_amdgcn_s_waitcnt(0xc07f);

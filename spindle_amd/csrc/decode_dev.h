@@ -204,6 +204,31 @@ __device__ __forceinline__ void rp_dots(const DRaw (&raw)[BPG], int nb, int G, i
     }
   }
 }
+// rp_dots for NV input rows against the same weights: each block decoded once, its dot with
+// every row as rp_dots forms it (the same values), each row's results to its chain buffer.
+template <int T, int BPG, int NV>
+__device__ __forceinline__ void rp_dots_nv(const DRaw (&raw)[BPG], int nb, int G, int gi, int l, const SPX_L uint32_t *const (&lq)[NV],
+                                           const SPX_L float *const (&ld)[NV], const SPX_L int2 *const (&lbs)[NV], SPX_L float *const (&cbr)[NV]) {
+#pragma unroll
+  for (int j = 0; j < BPG; j++) {
+    const int i = gi + G * j;
+    if (i < nb) {
+      KQDec<T> dec;
+      dec.decode(draw_kq<T>(raw[j]), l);
+#pragma unroll
+      for (int v = 0; v < NV; v++) {
+        const uint4 y0 = lld<uint4>(lq[v] + i * 64 + 8 * l), y1 = lld<uint4>(lq[v] + i * 64 + 8 * l + 4);
+        int P, s;
+        dec.dot(y0, y1, lld<int2>(lbs[v] + i * 8 + l), P, s);
+        s = sum8(s);
+        const float xd = ld[v][i];
+        SPX_L float *e = cbr[v] + i * 10;
+        e[l] = (float)P;
+        if (l == 0) { e[8] = dec.d * xd; e[9] = dec.corr_term(xd, s); }
+      }
+    }
+  }
+}
 // The chain over the row's blocks (group 0); the row result in lane 0 of the group.
 __device__ __forceinline__ float rp_chain(const SPX_L float *cbr, int nb, int l) {
   float acc = 0.0f, cr = 0.0f;

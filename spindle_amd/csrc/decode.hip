@@ -1671,9 +1671,9 @@ __device__ __forceinline__ void mw_chain(const MwProd<WPT> &o, float (&acc)[8 / 
 // by every wavefront of the workgroup as long as they walk the same number of tiles.
 template <int NB>
 constexpr int mw_pd() { return NB <= 3 ? NB : NB == 4 ? 2 : 4; }
-template <int NB, int TT, int WPT, int C, class Src, class Dst, class Done>
+template <int NB, int TT, int WPT, int C, int PD = mw_pd<NB>(), class Src, class Dst, class Done>
 __device__ __forceinline__ void mw_walk(int ntiles, Src src, Dst dst, Done done) {
-  constexpr int PD = mw_pd<NB>(), NS = NB / PD, CPW = 8 / WPT;
+  constexpr int NS = NB / PD, CPW = 8 / WPT;
   constexpr int BB = WPT == 4 ? PD : WPT == 2 && PD % 2 == 0 ? 2 : 1;  // blocks whose integers are issued together
   static_assert(NB % PD == 0, "whole stages");
   if (ntiles <= 0) return;
@@ -2624,6 +2624,8 @@ __global__ __launch_bounds__(256) void kp_moe_combine(const float *yd, const flo
 // [b n / G, (b + 1) n / G), job by job: the job's users' Q8_K rows are staged in LDS (slot =
 // the user's place in the job), then wavefront w walks the job's items w, w + NW, ... of the
 // range. An item's arithmetic, and so each h value, is kd_gateup_mq's.
+template <int NB>
+constexpr int KP_PD() { return NB >= 8 ? 2 : mw_pd<NB>(); }
 template <int T, int NB>
 __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void kp_gateup_mq(const DecGateUpMArgs a,
                                                                                                      const Job *jobs,
@@ -2672,7 +2674,7 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
         if (v < nv && x * 16 + r < n_ff) gst<float>(a.h + (int64_t)sj[2 + MAX_M + v] * n_ff + x * 16 + r, g[t] / (1.0f + expf(-g[t])) * out[t]);
       }
     };
-    mw_walk<NB, T, 1, 0>(2 * nit, src, dst, done);
+    mw_walk<NB, T, 1, 0, KP_PD<NB>()>(2 * nit, src, dst, done);
     s0 = s1;
   }
 }

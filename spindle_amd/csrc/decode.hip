@@ -2679,6 +2679,76 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
   }
 }
 
+// Down projection of a prefill pass over its job list: tiles (job, 16 rows of the expert's down
+// matrix), workgroup b the tiles [b n / G, (b + 1) n / G), job by job as kp_gateup_mq takes its
+// items: the job's users' h rows are quantized into LDS once (kd_down_mq's staging, quantize_avx2
+// per 256 block), then wavefront w walks the job's tiles w, w + NW, ... of the range with no
+// barrier between tiles. A tile's arithmetic is kd_down_mq's one-wavefront tile, so each y value
+// has its bits; y per (row, choice) to yd.
+template <int T, int NB>
+__global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void kp_down_mq(const DecDownMArgs a) {
+  constexpr int NW = DEC_MM_NW, JF = 2 + MAX_M;  // job fields: expert, nvec, out[]
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int s_job[JF];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int dim = (int)a.w.rows, n_ff = (int)a.w.cols, TX = (dim + 15) / 16, G = gridDim.x;
+  const MwLds L = mw_lds(smem, MAX_M, NB);
+  const int n = TX * gld<int>(a.njobs);
+  const int i0 = (int)((int64_t)blockIdx.x * n / G), i1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
+  for (int s0 = i0; s0 < i1;) {
+    const int j = s0 / TX, s1 = min(i1, (j + 1) * TX);
+    __syncthreads();  // the previous job's users are done with
+    if ((int)threadIdx.x < JF) {
+      const int f = threadIdx.x;
+      s_job[f] = gld<int>(reinterpret_cast<const int *>(a.jobs + j) + (f < 2 ? f : 2 + MAX_M + (f - 2)));
+    }
+    __syncthreads();
+    const int nv = __builtin_amdgcn_readfirstlane(min(max(s_job[1], 0), MAX_M));
+    const int e = __builtin_amdgcn_readfirstlane(min(max(s_job[0], 0), a.w.n_expert - 1)), nq = nv * NB;
+    for (int q0 = wave; q0 < nq; q0 += 4 * NW) {
+      float4 hv[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int q = q0 + NW * t;
+        if (q < nq) {
+          const int u = q / NB, i = q - u * NB;
+          hv[t] = gld<float4>(a.h + (int64_t)s_job[2 + u] * n_ff + i * 256 + 4 * lane);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int q = q0 + NW * t;
+        if (q < nq) {
+          const int u = q / NB, i = q - u * NB;
+          const float am = q8k_amax(hv[t]);
+          q8k_block_store(hv[t], am, L.lq + u * mw_vs(NB) + i * 64, L.ld + q, (SPX_L int *)L.lbs + q * 16);
+        }
+      }
+    }
+    __syncthreads();
+    mq_corr_stage(nv, NB, L.lbs, L.lc);
+    __syncthreads();
+    const int cnt = s1 - s0, nit = wave < cnt ? (cnt - wave + NW - 1) / NW : 0;
+    const MqVec vv = mq_vecs(nv, MqIdentity{});
+    auto row0 = [&](int k) SPX_AI { return (s0 + wave + NW * k - j * TX) * 16; };
+    auto src = [&](int k) SPX_AI {
+      const int r0 = row0(k);
+      return mw_src(a.w.pl, T, (int64_t)e * dim + r0, min(16, dim - r0), NB);
+    };
+    auto dst = [&](int) SPX_AI { return mw_dst(L, vv, NB, T); };
+    auto done = [&](int k, const float (&out)[4], const float (&)[4]) SPX_AI {
+      const int r0 = row0(k), r = lane & 15;
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int v = 4 * (lane >> 4) + t;
+        if (v < nv && r0 + r < dim) gst<float>(a.yd + (int64_t)s_job[2 + v] * dim + r0 + r, out[t]);
+      }
+    };
+    mw_walk<NB, T, 1, 0, 1>(nit, src, dst, done);
+    s0 = s1;
+  }
+}
+
 // ------------------------------------------------------------------ launchers
 static int cu_count() {
   static int n = 0;
@@ -3016,6 +3086,15 @@ hipError_t launch_kp_gateup_mq(const DecGateUpMArgs &a, const Job *jobs, const i
   });
 }
 
+// passes of more than 128 jobs on kp_down_mq (SPX_PF_DOWN=0: kd_down_mq, the same bits)
+static bool pf_down_on() {
+  static const bool on = [] {
+    const char *v = std::getenv("SPX_PF_DOWN");
+    return !v || atoi(v) != 0;
+  }();
+  return on;
+}
+
 hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s) {
   if (a.w.cols % 256 || a.w.nb > 4 || a.max_jobs < 1 || a.max_jobs > 512 || !a.h || !a.yd) return hipErrorInvalidValue;
   const int tx = (int)((a.w.rows + DOWN_MQ_ROWS - 1) / DOWN_MQ_ROWS), G = std::min(tx * a.max_jobs, cu_count());
@@ -3037,6 +3116,17 @@ hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s) {
     return hipGetLastError();
   };
   const bool staged = a.max_jobs <= 128;
+  if (!staged && pf_down_on()) {  // prefill: contiguous tile ranges, job by job (kp_down_mq)
+    const int items = (int)((a.w.rows + 15) / 16) * a.max_jobs;
+    const dim3 gp((unsigned)std::max(1, std::min((items + DEC_MM_NW - 1) / DEC_MM_NW, cu_count())));
+    return with_nb((int)a.w.nb, [&](auto NBc) {
+      constexpr int NB = decltype(NBc)::value;
+      auto kern = a.w.dtype == T_Q4K ? kp_down_mq<T_Q4K, NB> : kp_down_mq<T_Q6K, NB>;
+      SPX_DLDS(kern, sm);
+      hipLaunchKernelGGL(kern, gp, b, sm, s, a);
+      return hipGetLastError();
+    });
+  }
   return with_nb((int)a.w.nb, [&](auto NBc) {
     constexpr int NB = decltype(NBc)::value;
     if (a.w.dtype == T_Q4K) return staged ? gos(kd_down_mqs<T_Q4K, NB>) : go(kd_down_mq<T_Q4K, NB, 1>);

@@ -2633,7 +2633,7 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
   constexpr int NW = DEC_MM_NW, JR = 2 + 2 * MAX_M;
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int sj[JR];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n_ff = a.n_ff, cols = (int)a.gate.cols, nb = cols >> 8, m = a.m;
   const int TX = (n_ff + 15) / 16;
   const MwLds L = mw_lds(smem, MAX_M, nb);
@@ -2649,7 +2649,8 @@ __global__ __launch_bounds__(DEC_MM_NW * 64) __attribute__((amdgpu_waves_per_eu(
                    : f == 0 ? 0 : f == 1 ? min(MAX_M, m - MAX_M * j) : MAX_M * j + (f - 2) % MAX_M;
     }
     __syncthreads();
-    const int nv = min(max(sj[1], 0), MAX_M), e = min(max(sj[0], 0), a.gate.n_expert - 1);
+    const int nv = __builtin_amdgcn_readfirstlane(min(max(sj[1], 0), MAX_M));
+    const int e = __builtin_amdgcn_readfirstlane(min(max(sj[0], 0), a.gate.n_expert - 1));
     stage_q8<NW * 64>(a.y, (const SPX_L int *)(sj + 2), nv, cols, L.lq, L.ld, L.lbs, mw_vs(nb) / 4);
     __syncthreads();
     mq_corr_stage(nv, nb, L.lbs, L.lc);

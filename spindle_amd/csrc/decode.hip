@@ -2515,6 +2515,8 @@ __global__ __launch_bounds__(256) void kp_route_rows(const DecRouteArgs a) {
 // job, jobs in expert order (user (b, slot): vec = b, out = b * n_used + slot). A bit mask of
 // the rows per expert gives each user its rank, so every user is placed by its own thread.
 // njobs[0] = the job count, njobs[2] = the experts with users; expert_count counts each once.
+// Every workgroup of the grid (kp_jobs_grid) builds the masks and the job offsets; workgroup g
+// places the users of slots 256 (g + G k) + thread and writes the jobs of experts e = g mod G.
 __global__ __launch_bounds__(256) void kp_jobs(const DecRouteArgs a) {
   __shared__ unsigned long long mask[256][PMAX / 64];
   __shared__ int jbase[257];
@@ -2558,12 +2560,13 @@ __global__ __launch_bounds__(256) void kp_jobs(const DecRouteArgs a) {
   int off = 0;
   for (int w = 0; w < wave; w++) off += wsum[w];
   jbase[tid] = off + incl - nje;
-  if (tid == 255) {
+  const int G = gridDim.x, g = blockIdx.x;
+  if (tid == 255 && g == 0) {
     gst<int>(a.njobs, off + incl);
     gst<int>(a.njobs + 2, wnx[0] + wnx[1] + wnx[2] + wnx[3]);
   }
   __syncthreads();
-  for (int i = tid; i < m * 32; i += 256) {  // each user at its rank
+  for (int i = tid + 256 * g; i < m * 32; i += 256 * G) {  // each user at its rank
     const int b = i >> 5, sl = i & 31, e = sch[i];
     if (e < 0) continue;
     int rank = 0;
@@ -2576,7 +2579,7 @@ __global__ __launch_bounds__(256) void kp_jobs(const DecRouteArgs a) {
     gst<int>(J + 2 + rank % MAX_M, b);
     gst<int>(J + 2 + MAX_M + rank % MAX_M, b * nu + sl);
   }
-  if (tid < a.n_expert && cnt > 0) {  // each job's expert, user count and unused entries
+  if (tid < a.n_expert && cnt > 0 && tid % G == g) {  // each job's expert, user count and unused entries
     for (int j = 0; j < nje; j++) {
       int *J = reinterpret_cast<int *>(a.jobs + jbase[tid] + j);
       const int k = min(MAX_M, cnt - j * MAX_M);
@@ -3041,12 +3044,14 @@ hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &args, int max_jobs, hipStr
   });
 }
 
+static unsigned kp_jobs_grid(int m) { return (unsigned)std::min(16, (m * 32 + 255) / 256); }  // a slot a thread
+
 hipError_t launch_kp_route(const DecRouteArgs &a, hipStream_t s) {
   if (a.m < 1 || a.m > PMAX || a.n_expert < 1 || a.n_expert > 256 || a.n_used < 1 || a.n_used > 32 || a.n_used > a.n_expert || !a.jobs ||
       !a.njobs)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(kp_route_rows, dim3((a.m + 3) / 4), dim3(256), 0, s, a);
-  hipLaunchKernelGGL(kp_jobs, dim3(1), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(kp_jobs, dim3(kp_jobs_grid(a.m)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -3060,7 +3065,7 @@ hipError_t launch_kp_jobs(const DecRouteArgs &a, hipStream_t s) {
   if (a.m < 1 || a.m > PMAX || a.n_expert < 1 || a.n_expert > 256 || a.n_used < 1 || a.n_used > 32 || !a.jobs || !a.njobs || !a.chosen ||
       !a.nkeep)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kp_jobs, dim3(1), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(kp_jobs, dim3(kp_jobs_grid(a.m)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

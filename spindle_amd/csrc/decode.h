@@ -217,6 +217,7 @@ hipError_t launch_dec_down_m(const DecDownMArgs &a, hipStream_t s);
 // The grouped expert kernels on the int8 matrix cores (16-row tiles)
 hipError_t launch_dec_gateup_mq(const DecGateUpMArgs &a, int max_jobs, hipStream_t s);
 hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s);
+hipError_t launch_kp_down_mq(const DecDownMArgs &a, hipStream_t s);
 // Prefill passes (17..PMAX rows): routing + the job list (at most 16 users a job) in global
 // memory; gate/up over such a list (jobs null: dense, rows in sixteens), max_jobs bounds it
 hipError_t launch_kp_route(const DecRouteArgs &a, hipStream_t s);

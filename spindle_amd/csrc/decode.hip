@@ -3092,6 +3092,21 @@ hipError_t launch_kp_gateup_mq(const DecGateUpMArgs &a, const Job *jobs, const i
   });
 }
 
+hipError_t launch_kp_down_mq(const DecDownMArgs &a, hipStream_t s) {
+  if (a.w.cols % 256 || a.w.nb > 4 || a.max_jobs < 1 || a.max_jobs > 512 || !a.h || !a.yd) return hipErrorInvalidValue;
+  if (a.w.dtype != T_Q4K && a.w.dtype != T_Q6K) return hipErrorInvalidValue;
+  const int items = (int)((a.w.rows + 15) / 16) * a.max_jobs;
+  const dim3 grid((unsigned)std::max(1, std::min((items + DEC_MM_NW - 1) / DEC_MM_NW, cu_count()))), b(DEC_MM_NW * 64);
+  const size_t sm = mw_act_bytes(MAX_M, (int)a.w.nb);
+  return with_nb((int)a.w.nb, [&](auto NBc) {
+    constexpr int NB = decltype(NBc)::value;
+    auto kern = a.w.dtype == T_Q4K ? kp_down_mq<T_Q4K, NB> : kp_down_mq<T_Q6K, NB>;
+    SPX_DLDS(kern, sm);
+    hipLaunchKernelGGL(kern, grid, b, sm, s, a);
+    return hipGetLastError();
+  });
+}
+
 // passes of more than 128 jobs on kp_down_mq (SPX_PF_DOWN=0: kd_down_mq, the same bits)
 static bool pf_down_on() {
   static const bool on = [] {
@@ -3122,17 +3137,7 @@ hipError_t launch_dec_down_mq(const DecDownMArgs &a, hipStream_t s) {
     return hipGetLastError();
   };
   const bool staged = a.max_jobs <= 128;
-  if (!staged && pf_down_on()) {  // prefill: contiguous tile ranges, job by job (kp_down_mq)
-    const int items = (int)((a.w.rows + 15) / 16) * a.max_jobs;
-    const dim3 gp((unsigned)std::max(1, std::min((items + DEC_MM_NW - 1) / DEC_MM_NW, cu_count())));
-    return with_nb((int)a.w.nb, [&](auto NBc) {
-      constexpr int NB = decltype(NBc)::value;
-      auto kern = a.w.dtype == T_Q4K ? kp_down_mq<T_Q4K, NB> : kp_down_mq<T_Q6K, NB>;
-      SPX_DLDS(kern, sm);
-      hipLaunchKernelGGL(kern, gp, b, sm, s, a);
-      return hipGetLastError();
-    });
-  }
+  if (!staged && pf_down_on()) return launch_kp_down_mq(a, s);  // prefill: contiguous tile ranges, job by job
   return with_nb((int)a.w.nb, [&](auto NBc) {
     constexpr int NB = decltype(NBc)::value;
     if (a.w.dtype == T_Q4K) return staged ? gos(kd_down_mqs<T_Q4K, NB>) : go(kd_down_mq<T_Q4K, NB, 1>);

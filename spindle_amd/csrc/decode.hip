@@ -1346,10 +1346,17 @@ __device__ __forceinline__ uint32_t mx_pmul(uint32_t v, uint32_t s) {
   const mx_u16x2 a = __builtin_bit_cast(mx_u16x2, v), b = {(unsigned short)s, (unsigned short)s};
   return __builtin_bit_cast(uint32_t, a * b);
 }
-// Per byte q (0..7) times sh (-8..7) as int8: q (sh + 8) - 8 q, the subtraction kept inside each
-// byte by a bias of 128 (q (sh + 8) <= 105, 8 q <= 56: no borrow leaves a byte).
-__device__ __forceinline__ uint32_t mx_pmul_s(uint32_t q, int sh) {
-  return ((mx_pmul(q, (uint32_t)(sh + 8)) | 0x80808080u) - (q << 3)) ^ 0x80808080u;
+typedef short mx_i16x2 __attribute__((ext_vector_type(2)));
+// Per byte c (0..63) of q times the int8 scale s16 (sign-extended to a 16-bit lane): W = c s =
+// 128 hi + lo with lo = W & 127 (0..127) and hi = W >> 7 (-63..62), each packed back into the
+// byte's place (bytes 0, 2 and 1, 3 multiplied as 16-bit lanes, exact modulo 2^16).
+__device__ __forceinline__ void q6_wsplit(uint32_t q, uint32_t s16, uint32_t &hi, uint32_t &lo) {
+  const mx_u16x2 sv = {(unsigned short)s16, (unsigned short)s16};
+  const mx_u16x2 we = __builtin_bit_cast(mx_u16x2, __builtin_amdgcn_perm(0u, q, 0x0C020C00u)) * sv;
+  const mx_u16x2 wo = __builtin_bit_cast(mx_u16x2, __builtin_amdgcn_perm(0u, q, 0x0C030C01u)) * sv;
+  lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, wo), __builtin_bit_cast(uint32_t, we), 0x06020400u) & 0x7F7F7F7Fu;
+  const mx_i16x2 he = __builtin_bit_cast(mx_i16x2, we) >> (short)7, ho = __builtin_bit_cast(mx_i16x2, wo) >> (short)7;
+  hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, ho), __builtin_bit_cast(uint32_t, he), 0x06020400u);
 }
 
 // 4 x 4 transpose over the wavefront's four 16-lane rows: row g of r[c] holds M[g][c] on entry
@@ -1530,8 +1537,9 @@ struct MwProd {
 
 // Q6_K classes 4 E .. 4 E + 3 of a block (those of part C) from its ql words c (dwords
 // 16 E + 4 k4 ..) and qh words h (dwords 8 E + 2 k4, + 1); sw = the lane's four int8 scales
-// (groups 4 k4 .. 4 k4 + 3). P = D(ql sl) + 8 (D(qh sl) + 2 (D(ql sh) + 8 D(qh sh))), the
-// digits accumulated on the matrix core (exact in int32).
+// (groups 4 k4 .. 4 k4 + 3). Each 6-bit code c times its group's scale sc, W = c sc = 128 hi +
+// lo (q6_wsplit: lo 0..127, hi -63..62, both int8): P = 128 D(hi) + D(lo), accumulated on the
+// matrix core (exact in int32, the same integer as the digit products of c and sc).
 template <int E, int WPT, int C>
 __device__ __forceinline__ void mw_q6_half(const uint4 &c, const uint2 &h, uint32_t sw, const SPX_L uint32_t *py, mq_v4i (&P)[8 / WPT]) {
   const int sh = 4 * ((threadIdx.x >> 4) & 1);
@@ -1539,42 +1547,28 @@ __device__ __forceinline__ void mw_q6_half(const uint4 &c, const uint2 &h, uint3
   mw_t4d(c.x, c.z, q0);
   mw_t4d(c.y, c.w, q1);
   mw_t4d(h.x, h.y, qh);
-  const int sc0 = (int)(int8_t)(sw >> (8 * E)), sc1 = (int)(int8_t)(sw >> (16 + 8 * E));
-  const uint32_t sl0 = (uint32_t)(sc0 & 15), sl1 = (uint32_t)(sc1 & 15);
-  const int sh0 = sc0 >> 4, sh1 = sc1 >> 4;
-  uint32_t l0[4], h0[4], l1[4], h1[4];
+  const uint32_t s0 = (uint32_t)(uint16_t)(int16_t)(int8_t)(sw >> (8 * E)), s1 = (uint32_t)(uint16_t)(int16_t)(int8_t)(sw >> (16 + 8 * E));
+  uint32_t wh0[4], wl0[4], wh1[4], wl1[4];
   uint2 y[4];
 #pragma unroll
   for (int a = 0; a < 4; a++) {
     if (mw_slot<WPT, C>(4 * E + a) < 0) continue;
     const uint32_t c0 = ((q0[a] >> sh) & 0x0F0F0F0Fu) | (((qh[a] >> sh) & 0x03030303u) << 4);
     const uint32_t c1 = ((q1[a] >> sh) & 0x0F0F0F0Fu) | (((qh[a] >> (sh + 2)) & 0x03030303u) << 4);
-    l0[a] = c0 & 0x07070707u;
-    h0[a] = (c0 >> 3) & 0x07070707u;
-    l1[a] = c1 & 0x07070707u;
-    h1[a] = (c1 >> 3) & 0x07070707u;
+    q6_wsplit(c0, s0, wh0[a], wl0[a]);
+    q6_wsplit(c1, s1, wh1[a], wl1[a]);
     y[a] = lld<uint2>(py + 8 * (4 * E + a));
   }
-  // the classes' digit contractions interleaved, one dependent step at a time
+  // the classes' contractions interleaved, one dependent step at a time
 #pragma unroll
   for (int a = 0; a < 4; a++) {
     const int j = mw_slot<WPT, C>(4 * E + a);
-    if (j >= 0) P[j] = mq_mfma(y[a].x, y[a].y, mx_pmul_s(h0[a], sh0), mx_pmul_s(h1[a], sh1)) * 8;
+    if (j >= 0) P[j] = mq_mfma(y[a].x, y[a].y, wh0[a], wh1[a]) * 128;
   }
 #pragma unroll
   for (int a = 0; a < 4; a++) {
     const int j = mw_slot<WPT, C>(4 * E + a);
-    if (j >= 0) P[j] = mq_mfma_c(y[a].x, y[a].y, mx_pmul_s(l0[a], sh0), mx_pmul_s(l1[a], sh1), P[j]) * 2;
-  }
-#pragma unroll
-  for (int a = 0; a < 4; a++) {
-    const int j = mw_slot<WPT, C>(4 * E + a);
-    if (j >= 0) P[j] = mq_mfma_c(y[a].x, y[a].y, mx_pmul(h0[a], sl0), mx_pmul(h1[a], sl1), P[j]) * 8;
-  }
-#pragma unroll
-  for (int a = 0; a < 4; a++) {
-    const int j = mw_slot<WPT, C>(4 * E + a);
-    if (j >= 0) P[j] = mq_mfma_c(y[a].x, y[a].y, mx_pmul(l0[a], sl0), mx_pmul(l1[a], sl1), P[j]);
+    if (j >= 0) P[j] = mq_mfma_c(y[a].x, y[a].y, wl0[a], wl1[a], P[j]);
   }
 }
 
@@ -1919,47 +1913,25 @@ __device__ __forceinline__ void ms_prod(const SPX_L uint8_t *tl, const MwDst &d,
     const SPX_L uint8_t *rh = tl + G::OH + c16 * G::HR + 64 * b;
     const int h = k4 >> 1, sh = 4 * (k4 & 1);
     const uint32_t sw = lld<uint32_t>((const SPX_L uint32_t *)(rs + 4 * k4));
-    uint32_t l0[8 / WPT], h0[8 / WPT], l1[8 / WPT], h1[8 / WPT];
+    uint32_t wh0[8 / WPT], wl0[8 / WPT], wh1[8 / WPT], wl1[8 / WPT];
     uint2 y[8 / WPT];
+    // W = c sc = 128 hi + lo per code (q6_wsplit), P = 128 D(hi) + D(lo) on the matrix core; a
+    // class's scales: groups 2 s + (l >= 4) of its sub-blocks s = 2 k4, 2 k4 + 1
 #pragma unroll
     for (int j = 0; j < 8 / WPT; j++) {
-      const int l = mw_cls<WPT, C>(j);
+      const int l = mw_cls<WPT, C>(j), hb = l >= 4 ? 8 : 0;
       const uint2 ql = lld<uint2>((const SPX_L uint2 *)(rc + 16 * l + 8 * h));
       const uint32_t qh = lld<uint32_t>((const SPX_L uint32_t *)(rh + 8 * l + 4 * h));
       const uint32_t c0 = ((ql.x >> sh) & 0x0F0F0F0Fu) | (((qh >> sh) & 0x03030303u) << 4);
       const uint32_t c1 = ((ql.y >> sh) & 0x0F0F0F0Fu) | (((qh >> (sh + 2)) & 0x03030303u) << 4);
-      l0[j] = c0 & 0x07070707u;
-      h0[j] = (c0 >> 3) & 0x07070707u;
-      l1[j] = c1 & 0x07070707u;
-      h1[j] = (c1 >> 3) & 0x07070707u;
+      q6_wsplit(c0, (uint32_t)(uint16_t)(int16_t)(int8_t)(sw >> hb), wh0[j], wl0[j]);
+      q6_wsplit(c1, (uint32_t)(uint16_t)(int16_t)(int8_t)(sw >> (16 + hb)), wh1[j], wl1[j]);
       y[j] = lld<uint2>(py + 8 * l);
     }
-    // P = D(ql sl) + 8 (D(qh sl) + 2 (D(ql sh) + 8 D(qh sh))), accumulated on the matrix core;
-    // a class's scales: groups 2 s + (l >= 4) of its sub-blocks s = 2 k4, 2 k4 + 1
 #pragma unroll
-    for (int j = 0; j < 8 / WPT; j++) {
-      const int l = mw_cls<WPT, C>(j), hb = l >= 4 ? 8 : 0;
-      const int sh1 = (int)(int8_t)(sw >> (16 + hb)) >> 4, sh0 = (int)(int8_t)(sw >> hb) >> 4;
-      o.P[j] = mq_mfma(y[j].x, y[j].y, mx_pmul_s(h0[j], sh0), mx_pmul_s(h1[j], sh1)) * 8;
-    }
+    for (int j = 0; j < 8 / WPT; j++) o.P[j] = mq_mfma(y[j].x, y[j].y, wh0[j], wh1[j]) * 128;
 #pragma unroll
-    for (int j = 0; j < 8 / WPT; j++) {
-      const int l = mw_cls<WPT, C>(j), hb = l >= 4 ? 8 : 0;
-      const int sh1 = (int)(int8_t)(sw >> (16 + hb)) >> 4, sh0 = (int)(int8_t)(sw >> hb) >> 4;
-      o.P[j] = mq_mfma_c(y[j].x, y[j].y, mx_pmul_s(l0[j], sh0), mx_pmul_s(l1[j], sh1), o.P[j]) * 2;
-    }
-#pragma unroll
-    for (int j = 0; j < 8 / WPT; j++) {
-      const int l = mw_cls<WPT, C>(j), hb = l >= 4 ? 8 : 0;
-      const uint32_t sl0 = (uint32_t)((int)(int8_t)(sw >> hb) & 15), sl1 = (uint32_t)((int)(int8_t)(sw >> (16 + hb)) & 15);
-      o.P[j] = mq_mfma_c(y[j].x, y[j].y, mx_pmul(h0[j], sl0), mx_pmul(h1[j], sl1), o.P[j]) * 8;
-    }
-#pragma unroll
-    for (int j = 0; j < 8 / WPT; j++) {
-      const int l = mw_cls<WPT, C>(j), hb = l >= 4 ? 8 : 0;
-      const uint32_t sl0 = (uint32_t)((int)(int8_t)(sw >> hb) & 15), sl1 = (uint32_t)((int)(int8_t)(sw >> (16 + hb)) & 15);
-      o.P[j] = mq_mfma_c(y[j].x, y[j].y, mx_pmul(l0[j], sl0), mx_pmul(l1[j], sl1), o.P[j]);
-    }
+    for (int j = 0; j < 8 / WPT; j++) o.P[j] = mq_mfma_c(y[j].x, y[j].y, wl0[j], wl1[j], o.P[j]);
     if (C == 0) {
       // C = sum_g sc_g bsum_g: K 0-15 the bsums' lo, 16-31 their hi, against the scales
       const uint2 bb = lld<uint2>((const SPX_L uint2 *)(rs + 8 * (k4 & 1)));

@@ -236,7 +236,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the whole model fits in one MI355X's HBM and this build "
-              "has no multi-GPU path (see DESIGN.md, 'How the path would shard'). Use --gpus 1.", file=sys.stderr)
+              "has no multi-GPU path (the expert slabs would shard by expert over the GPUs, with one "
+              "all-to-all of the routed rows each way a layer). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     from spindle_amd import model as M
